@@ -1,0 +1,7 @@
+"""MI355X-native MoE block of c0ven's qwen4exp model: HIP kernels for gfx950 behind a C ABI (include/c0ven_moe.h).
+
+The compute lives in libc0ven_moe.so (c0ven_amd/csrc); this package is its ctypes binding. Importing it without the
+built library raises ImportError: there is no CPU fallback.
+"""
+from ._lib import (BLOCK, EXPORTS, QT_IQ3_S, QT_Q4_K, QT_Q8_0, QT_Q8_K, TYPE_NAMES, MoeBlock, MoeError,  # noqa: F401
+                   abi_layout, lib, quantize, row_bytes, synth_matrix, synth_normal, zipf_bias)

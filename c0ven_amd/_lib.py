@@ -1,0 +1,221 @@
+"""ctypes bindings of include/c0ven_moe.h (libc0ven_moe.so, built in-tree by __graft_entry__.build()).
+
+There is no fallback: importing this module without the built library raises, and every compute call goes to the
+HIP library.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libc0ven_moe.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError("c0ven_amd: %s is not built; run __graft_entry__.build()" % LIB_PATH)
+lib = C.CDLL(LIB_PATH)
+
+QT_Q8_0, QT_Q4_K, QT_Q8_K, QT_IQ3_S = 8, 12, 15, 21
+TYPE_NAMES = {QT_Q8_0: "Q8_0", QT_Q4_K: "Q4_K", QT_IQ3_S: "IQ3_S"}
+BLOCK = {QT_Q8_0: (32, 34), QT_Q4_K: (256, 144), QT_IQ3_S: (256, 110)}
+
+MOE_OK, MOE_ERROR, MOE_BAD_ARGUMENT, MOE_BUSY, MOE_TIMEOUT = 0, 1, 2, 3, 4
+
+
+class MoeConfig(C.Structure):
+    _fields_ = [
+        ("n_embd", C.c_uint32), ("n_ff", C.c_uint32), ("n_expert", C.c_uint32), ("n_used", C.c_uint32),
+        ("n_layer", C.c_uint32), ("gate_type", C.c_uint32), ("down_type", C.c_uint32), ("has_shared", C.c_uint32),
+        ("sh_gate_type", C.c_uint32), ("sh_down_type", C.c_uint32), ("max_tokens", C.c_uint32),
+        ("swiglu_limit", C.c_float), ("device", C.c_int32), ("reserved", C.c_uint32 * 4),
+    ]
+
+
+class MoeRouteOut(C.Structure):
+    _fields_ = [("ids", C.POINTER(C.c_int32)), ("w", C.POINTER(C.c_float))]
+
+
+class MoeJob(C.Structure):
+    _fields_ = [("layer", C.c_uint32), ("expert", C.c_uint32), ("tok", C.c_uint32), ("w", C.c_float)]
+
+
+class MoeAbiRow(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("offset", C.c_uint32), ("size", C.c_uint32)]
+
+
+class MoeTile(C.Structure):
+    _fields_ = [("expert", C.c_uint32), ("slot", C.c_uint32), ("start", C.c_uint32), ("count", C.c_uint32)]
+
+
+class MoeGroup(C.Structure):
+    _fields_ = [("slot", C.c_int32), ("n", C.c_uint32), ("asg", C.c_uint32 * 8)]
+
+
+_P = C.c_void_p
+_u32, _u64, _i32, _f32 = C.c_uint32, C.c_uint64, C.c_int32, C.c_float
+_SIGS = {
+    "moe_open": (_i32, [C.POINTER(MoeConfig), C.POINTER(_P)]),
+    "moe_close": (None, [_P]),
+    "moe_last_error": (C.c_char_p, [_P]),
+    "moe_load_router": (_i32, [_P, _u32, _P, _P]),
+    "moe_load_expert": (_i32, [_P, _u32, _u32, _P, _P, _P]),
+    "moe_forward": (_i32, [_P, _u32, _P, _u32, _u64, _P, _u64, C.POINTER(MoeRouteOut)]),
+    "moe_forward_async": (_i32, [_P, _u32, _P, _u32, _P, _P, _P, _P]),
+    "moe_forward_experts": (_i32, [_P, C.POINTER(MoeJob), _u32, _u32, _P, _u64, _P, _u64]),
+    "moe_h_rows": (_u32, [C.POINTER(MoeConfig)]),
+    "moe_sync": (_i32, [_P]),
+    "moe_stream": (_P, [_P]),
+    "moe_set_timing": (_i32, [_P, C.c_int]),
+    "moe_kernel_times": (_i32, [_P, C.POINTER(C.c_char_p), C.POINTER(_f32), _u32, C.POINTER(_u32)]),
+    "moe_device_bytes": (_u64, [_P]),
+    "moe_dequantize": (_i32, [_P, _u32, _P, _u32, _u32, _P]),
+    "moe_synth_normal": (None, [_u64, _u64, _f32, _P, _u64, C.c_int]),
+    "moe_quantize": (_i32, [_u32, _P, _u32, _u32, _P, C.c_int]),
+    "moe_synth_matrix": (_i32, [_u64, _u64, _f32, _u32, _u32, _u32, _P, C.c_int]),
+    "moe_zipf_bias": (None, [_u64, _u32, _f32, _P]),
+    "moe_row_bytes": (_u64, [_u32, _u32]),
+    "moe_abi_layout": (_u32, [C.POINTER(MoeAbiRow), _u32]),
+}
+EXPORTS = tuple(_SIGS)
+for _name, (_res, _args) in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+
+def _ptr(a):
+    return a.ctypes.data_as(_P) if a is not None else None
+
+
+class MoeError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__("moe status %d: %s" % (status, msg))
+        self.status = status
+
+
+def row_bytes(qtype, cols):
+    return int(lib.moe_row_bytes(qtype, cols))
+
+
+def synth_normal(seed, stream, n, sigma=1.0, nthreads=0):
+    out = np.empty(n, dtype=np.float32)
+    lib.moe_synth_normal(seed, stream, sigma, _ptr(out), n, nthreads)
+    return out
+
+
+def quantize(qtype, x, nthreads=0):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, cols = x.shape
+    out = np.empty(rows * row_bytes(qtype, cols), dtype=np.uint8)
+    st = lib.moe_quantize(qtype, _ptr(x), rows, cols, _ptr(out), nthreads)
+    if st != MOE_OK:
+        raise MoeError(st, "moe_quantize")
+    return out
+
+
+def synth_matrix(seed, stream, qtype, rows, cols, sigma=0.02, nthreads=0):
+    out = np.empty(rows * row_bytes(qtype, cols), dtype=np.uint8)
+    st = lib.moe_synth_matrix(seed, stream, sigma, qtype, rows, cols, _ptr(out), nthreads)
+    if st != MOE_OK:
+        raise MoeError(st, "moe_synth_matrix")
+    return out
+
+
+def zipf_bias(seed, n_expert, s=1.1):
+    out = np.empty(n_expert, dtype=np.float32)
+    lib.moe_zipf_bias(seed, n_expert, s, _ptr(out))
+    return out
+
+
+def abi_layout():
+    n = lib.moe_abi_layout(None, 0)
+    rows = (MoeAbiRow * n)()
+    lib.moe_abi_layout(rows, n)
+    return [(r.name.decode(), r.offset, r.size) for r in rows]
+
+
+class MoeBlock:
+    """One context of the HIP MoE block (moe_open .. moe_close)."""
+
+    def __init__(self, n_embd, n_ff, n_expert, n_used, gate_type, down_type, has_shared=True, sh_gate_type=None,
+                 sh_down_type=None, n_layer=1, max_tokens=16, swiglu_limit=0.0, device=0):
+        self.cfg = MoeConfig(n_embd=n_embd, n_ff=n_ff, n_expert=n_expert, n_used=n_used, n_layer=n_layer,
+                             gate_type=gate_type, down_type=down_type, has_shared=1 if has_shared else 0,
+                             sh_gate_type=sh_gate_type if sh_gate_type is not None else gate_type,
+                             sh_down_type=sh_down_type if sh_down_type is not None else down_type,
+                             max_tokens=max_tokens, swiglu_limit=swiglu_limit, device=device)
+        h = _P()
+        st = lib.moe_open(C.byref(self.cfg), C.byref(h))
+        if st != MOE_OK:
+            raise MoeError(st, lib.moe_last_error(None).decode())
+        self.h = h
+
+    def _check(self, st):
+        if st != MOE_OK:
+            raise MoeError(st, lib.moe_last_error(self.h).decode())
+
+    def close(self):
+        if self.h:
+            lib.moe_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def load_router(self, layer, router_bf16, bias=None):
+        r = np.ascontiguousarray(router_bf16, dtype=np.uint16)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self._check(lib.moe_load_router(self.h, layer, _ptr(r), _ptr(b)))
+
+    def load_expert(self, layer, expert, gate, up, down):
+        self._check(lib.moe_load_expert(self.h, layer, expert, _ptr(gate), _ptr(up), _ptr(down)))
+
+    def forward(self, layer, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T, H = x.shape
+        y = np.empty((T, H), dtype=np.float32)
+        K = self.cfg.n_used
+        ids = np.empty((T, K), dtype=np.int32)
+        w = np.empty((T, K), dtype=np.float32)
+        ro = MoeRouteOut(ids.ctypes.data_as(C.POINTER(C.c_int32)), w.ctypes.data_as(C.POINTER(C.c_float)))
+        self._check(lib.moe_forward(self.h, layer, _ptr(x), T, H, _ptr(y), H, C.byref(ro)))
+        return y, ids, w
+
+    def forward_async(self, layer, x_dev, ntok, y_dev, ids_dev=None, w_dev=None, stream=None):
+        self._check(lib.moe_forward_async(self.h, layer, x_dev, ntok, y_dev, ids_dev, w_dev, stream))
+
+    def forward_experts(self, jobs, x):
+        """jobs: list of (layer, expert, tok, w)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T, H = x.shape
+        arr = (MoeJob * max(1, len(jobs)))(*[MoeJob(*j) for j in jobs])
+        y = np.empty((T, H), dtype=np.float32)
+        self._check(lib.moe_forward_experts(self.h, arr, len(jobs), T, _ptr(x), H, _ptr(y), H))
+        return y
+
+    def dequantize(self, qtype, blocks, rows, cols):
+        out = np.empty((rows, cols), dtype=np.float32)
+        self._check(lib.moe_dequantize(self.h, qtype, _ptr(blocks), rows, cols, _ptr(out)))
+        return out
+
+    def sync(self):
+        self._check(lib.moe_sync(self.h))
+
+    def stream(self):
+        return lib.moe_stream(self.h)
+
+    def set_timing(self, on):
+        self._check(lib.moe_set_timing(self.h, 1 if on else 0))
+
+    def kernel_times(self):
+        names = (C.c_char_p * 8)()
+        ms = (C.c_float * 8)()
+        n = C.c_uint32()
+        self._check(lib.moe_kernel_times(self.h, names, ms, 8, C.byref(n)))
+        return {names[i].decode(): ms[i] for i in range(n.value)}
+
+    def device_bytes(self):
+        return int(lib.moe_device_bytes(self.h))

@@ -1,0 +1,469 @@
+// The C ABI (include/c0ven_moe.h): contexts, resident weights in the device layout, and the forward calls.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstddef>
+#include <cstring>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/c0ven_moe.h"
+#include "aux.h"
+#include "decode.h"
+#include "layout.h"
+#include "repack.h"
+
+using namespace c0ven;
+
+namespace {
+
+struct Error : std::runtime_error {
+  moe_status st;
+  Error(moe_status s, const std::string &m) : std::runtime_error(m), st(s) {}
+};
+
+void check(hipError_t e, const char *what) {
+  if (e != hipSuccess) throw Error(MOE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+}
+void require(bool ok, const std::string &why) {
+  if (!ok) throw Error(MOE_BAD_ARGUMENT, why);
+}
+
+bool pow2(uint32_t v) { return v && !(v & (v - 1)); }
+
+struct Layer {
+  uint16_t *router = nullptr;
+  float *bias = nullptr;
+  bool has_bias = false;
+  uint8_t *experts = nullptr;
+  uint8_t *shared = nullptr;
+};
+
+constexpr int kNumKernels = 3;
+const char *kKernelNames[kNumKernels] = {"moe_route", "moe_gate_up", "moe_down"};
+
+}  // namespace
+
+struct moe_ctx {
+  moe_config cfg{};
+  hipStream_t stream = nullptr;
+  std::vector<Layer> layers;
+  uint64_t ex_bytes = 0, ex_up = 0, ex_down = 0, sh_bytes = 0, sh_up = 0, sh_down = 0;
+  uint32_t tmax = 0, k1 = 0, gmax = 0;
+  // Staging for the host-memory calls.
+  float *x_dev = nullptr, *y_dev = nullptr, *w_stage = nullptr;
+  int32_t *ids_stage = nullptr;
+  // Scratch.
+  uint8_t *act_r = nullptr, *act_s = nullptr, *hact = nullptr;
+  float *logits = nullptr, *w = nullptr, *gs = nullptr, *terms_gu = nullptr, *terms_d = nullptr, *y_asg = nullptr;
+  int32_t *ids = nullptr;
+  MoeGroup *groups = nullptr;
+  uint32_t *ngroups = nullptr, *counters = nullptr, *tok_need = nullptr;
+  uint32_t *cnt_route = nullptr, *cnt_gu = nullptr, *cnt_d = nullptr, *cnt_tok = nullptr;
+  bool timing = false, timed = false;
+  hipEvent_t ev[kNumKernels + 1] = {};
+  std::vector<void *> allocs;
+  uint64_t dev_bytes = 0;
+  std::string err;
+
+  template <typename T>
+  T *alloc(uint64_t count) {
+    void *p = nullptr;
+    const uint64_t bytes = std::max<uint64_t>(count * sizeof(T), 256);
+    check(hipMalloc(&p, bytes), "hipMalloc");
+    allocs.push_back(p);
+    dev_bytes += bytes;
+    return (T *)p;
+  }
+};
+
+namespace {
+
+moe_status fail(moe_ctx *c, const Error &e) {
+  if (c) c->err = e.what();
+  return e.st;
+}
+
+thread_local std::string g_open_error;
+
+template <typename F>
+moe_status guarded(moe_ctx *c, F f) {
+  if (!c) return MOE_BAD_ARGUMENT;
+  try {
+    f();
+    c->err.clear();
+    return MOE_OK;
+  } catch (const Error &e) {
+    return fail(c, e);
+  } catch (const std::bad_alloc &) {
+    c->err = "out of host memory";
+    return MOE_ERROR;
+  } catch (const std::exception &e) {
+    c->err = e.what();
+    return MOE_ERROR;
+  }
+}
+
+void validate(const moe_config &c) {
+  require(c.n_embd && c.n_embd % 512 == 0 && pow2(c.n_embd / kUnit) && c.n_embd / kUnit <= kMaxUnits,
+          "n_embd must be 512 x a power of two, at most 8192");
+  require(c.n_ff && c.n_ff % kUnit == 0 && pow2(c.n_ff / kUnit) && c.n_ff / kUnit <= kMaxUnits,
+          "n_ff must be 256 x a power of two, at most 8192");
+  require(c.n_expert && c.n_expert <= kMaxExperts, "n_expert must be 1..512");
+  require(c.n_used && c.n_used <= kMaxUsed && c.n_used <= c.n_expert, "n_used must be 1..min(16, n_expert)");
+  require(quant_gpu_supported(c.gate_type) && quant_gpu_supported(c.down_type), "expert types must be Q8_0, Q4_K or IQ3_S");
+  require(!c.has_shared || (quant_gpu_supported(c.sh_gate_type) && quant_gpu_supported(c.sh_down_type)),
+          "shared expert types must be Q8_0, Q4_K or IQ3_S");
+  require(c.max_tokens <= kMaxDecodeTokens, "max_tokens above 16 needs the prefill path");
+  require(c.swiglu_limit >= 0.0f, "swiglu_limit must be >= 0");
+}
+
+DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
+  const moe_config &g = c->cfg;
+  const Layer &L = c->layers[layer];
+  DecodeParams p{};
+  p.H = g.n_embd, p.F = g.n_ff, p.E = g.n_expert, p.K = g.n_used, p.T = T;
+  p.gate_type = g.gate_type, p.down_type = g.down_type;
+  p.sh_gate_type = g.sh_gate_type, p.sh_down_type = g.sh_down_type, p.has_shared = g.has_shared;
+  p.xact_r = quant_vec_dot_type(g.gate_type);
+  p.xact_s = g.has_shared ? quant_vec_dot_type(g.sh_gate_type) : p.xact_r;
+  p.swiglu_limit = g.swiglu_limit;
+  p.route = 1;
+  p.router = L.router, p.bias = L.has_bias ? L.bias : nullptr;
+  p.experts = L.experts, p.ex_bytes = c->ex_bytes, p.ex_up_off = c->ex_up, p.ex_down_off = c->ex_down;
+  p.shared = L.shared, p.sh_up_off = c->sh_up, p.sh_down_off = c->sh_down;
+  p.act_r = c->act_r, p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
+  p.logits = c->logits, p.ids = c->ids, p.w = c->w, p.gs = c->gs;
+  p.groups = c->groups, p.ngroups = c->ngroups;
+  p.terms_gu = c->terms_gu, p.hact = c->hact, p.terms_d = c->terms_d, p.y_asg = c->y_asg;
+  p.cnt_route = c->cnt_route, p.cnt_gu = c->cnt_gu, p.cnt_d = c->cnt_d, p.cnt_tok = c->cnt_tok;
+  return p;
+}
+
+void launch(moe_ctx *c, const DecodeParams &p, uint32_t n_route_wg, hipStream_t s) {
+  const uint32_t G = max_groups(p.T, p.K);
+  const uint32_t g_gu = G * (p.F / kUnit) * 2 * (p.H / kUnit), g_d = G * (p.H / kUnit) * (p.F / kUnit);
+  const bool tm = c->timing && s == c->stream;
+  if (tm) check(hipEventRecord(c->ev[0], s), "hipEventRecord");
+  hipLaunchKernelGGL(moe_route, dim3(n_route_wg), dim3(256), 0, s, p);
+  if (tm) check(hipEventRecord(c->ev[1], s), "hipEventRecord");
+  hipLaunchKernelGGL(moe_gate_up, dim3(g_gu), dim3(256), 0, s, p);
+  if (tm) check(hipEventRecord(c->ev[2], s), "hipEventRecord");
+  hipLaunchKernelGGL(moe_down, dim3(g_d), dim3(256), 0, s, p);
+  if (tm) check(hipEventRecord(c->ev[3], s), "hipEventRecord");
+  check(hipGetLastError(), "kernel launch");
+  c->timed = tm;
+}
+
+void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *y, int32_t *ids, float *w,
+                 hipStream_t s) {
+  require(layer < c->cfg.n_layer, "layer out of range");
+  require(T >= 1 && T <= c->tmax, "ntok must be 1..max_tokens");
+  require(c->layers[layer].router != nullptr, "the layer's router is not loaded");
+  DecodeParams p = base_params(c, layer, T);
+  p.x = x, p.y = y;
+  const uint32_t nr = std::max((c->cfg.n_expert + 1 + 7) / 8, T);
+  launch(c, p, nr, s);
+  if (ids) check(hipMemcpyAsync(ids, c->ids, sizeof(int32_t) * T * p.K, hipMemcpyDeviceToDevice, s), "copy ids");
+  if (w) check(hipMemcpyAsync(w, c->w, sizeof(float) * T * p.K, hipMemcpyDeviceToDevice, s), "copy w");
+}
+
+}  // namespace
+
+extern "C" {
+
+MOE_API const char *moe_last_error(const moe_ctx *ctx) { return ctx ? ctx->err.c_str() : g_open_error.c_str(); }
+
+MOE_API uint32_t moe_h_rows(const moe_config *cfg) { return cfg && cfg->n_ff % kUnit == 0 ? kUnit : 0; }
+
+MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
+  if (!cfg || !out) {
+    g_open_error = "null argument";
+    return MOE_BAD_ARGUMENT;
+  }
+  *out = nullptr;
+  moe_ctx *c = nullptr;
+  try {
+    moe_config g = *cfg;
+    if (!g.n_layer) g.n_layer = 1;
+    if (!g.max_tokens) g.max_tokens = kMaxDecodeTokens;
+    validate(g);
+    c = new moe_ctx();
+    c->cfg = g;
+    int ndev = 0;
+    check(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+    require(g.device >= 0 && g.device < ndev, "no such device");
+    check(hipSetDevice(g.device), "hipSetDevice");
+    check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+    for (auto &e : c->ev) check(hipEventCreate(&e), "hipEventCreate");
+    const uint32_t H = g.n_embd, F = g.n_ff, E = g.n_expert;
+    const uint64_t gu = matrix_bytes(g.gate_type, F, H), dn = matrix_bytes(g.down_type, H, F);
+    c->ex_up = gu, c->ex_down = 2 * gu, c->ex_bytes = 2 * gu + dn;
+    if (g.has_shared) {
+      const uint64_t sgu = matrix_bytes(g.sh_gate_type, F, H), sdn = matrix_bytes(g.sh_down_type, H, F);
+      c->sh_up = sgu, c->sh_down = 2 * sgu, c->sh_bytes = 2 * sgu + sdn;
+    }
+    c->layers.resize(g.n_layer);
+    for (auto &L : c->layers) {
+      L.router = c->alloc<uint16_t>((uint64_t)(E + 1) * H);
+      L.bias = c->alloc<float>(E);
+      L.experts = c->alloc<uint8_t>(c->ex_bytes * E);
+      if (g.has_shared) L.shared = c->alloc<uint8_t>(c->sh_bytes);
+      check(hipMemset(L.experts, 0, c->ex_bytes * E), "hipMemset");
+      if (L.shared) check(hipMemset(L.shared, 0, c->sh_bytes), "hipMemset");
+    }
+    // Scratch for max_tokens tokens of n_used + 1 assignments (the pre-routed path may give a token its shared
+    // expert as a job).
+    const uint32_t T = g.max_tokens, K1 = g.n_used + 1, G = max_groups(T, K1), A = T * K1 + T;
+    c->tmax = T, c->k1 = K1, c->gmax = G;
+    const uint32_t Ug = H / kUnit, Ud = F / kUnit;
+    c->x_dev = c->alloc<float>((uint64_t)T * H);
+    c->y_dev = c->alloc<float>((uint64_t)T * H);
+    c->ids_stage = c->alloc<int32_t>((uint64_t)T * K1);
+    c->w_stage = c->alloc<float>((uint64_t)T * K1);
+    c->act_r = c->alloc<uint8_t>((uint64_t)T * Ug * kActBytes);
+    c->act_s = c->alloc<uint8_t>((uint64_t)T * Ug * kActBytes);
+    c->logits = c->alloc<float>((uint64_t)T * (E + 1));
+    c->ids = c->alloc<int32_t>((uint64_t)T * K1);
+    c->w = c->alloc<float>((uint64_t)T * K1);
+    c->gs = c->alloc<float>(T);
+    c->groups = c->alloc<MoeGroup>(G);
+    c->ngroups = c->alloc<uint32_t>(1);
+    c->tok_need = c->alloc<uint32_t>(T);
+    c->terms_gu = c->alloc<float>((uint64_t)G * 2 * Ug * MOE_GROUP_MAX * F);
+    c->hact = c->alloc<uint8_t>((uint64_t)A * Ud * kActBytes);
+    c->terms_d = c->alloc<float>((uint64_t)G * Ud * MOE_GROUP_MAX * H);
+    c->y_asg = c->alloc<float>((uint64_t)A * H);
+    const uint64_t ncnt = 1 + (uint64_t)G * (F / kUnit) + (uint64_t)G * (H / kUnit) + (uint64_t)T * (H / kUnit);
+    c->counters = c->alloc<uint32_t>(ncnt);
+    check(hipMemset(c->counters, 0, ncnt * sizeof(uint32_t)), "hipMemset");
+    c->cnt_route = c->counters;
+    c->cnt_gu = c->cnt_route + 1;
+    c->cnt_d = c->cnt_gu + (uint64_t)G * (F / kUnit);
+    c->cnt_tok = c->cnt_d + (uint64_t)G * (H / kUnit);
+    check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    *out = c;
+    return MOE_OK;
+  } catch (const Error &e) {
+    g_open_error = e.what();
+    moe_close(c);
+    return e.st;
+  } catch (const std::exception &e) {
+    g_open_error = e.what();
+    moe_close(c);
+    return MOE_ERROR;
+  }
+}
+
+MOE_API void moe_close(moe_ctx *c) {
+  if (!c) return;
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  for (void *p : c->allocs) (void)hipFree(p);
+  for (auto &e : c->ev)
+    if (e) (void)hipEventDestroy(e);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+MOE_API moe_status moe_load_router(moe_ctx *c, uint32_t layer, const uint16_t *router, const float *bias) {
+  return guarded(c, [&] {
+    require(layer < c->cfg.n_layer && router, "bad layer or null router");
+    Layer &L = c->layers[layer];
+    const uint64_t n = (uint64_t)(c->cfg.n_expert + 1) * c->cfg.n_embd;
+    check(hipMemcpy(L.router, router, n * sizeof(uint16_t), hipMemcpyHostToDevice), "upload router");
+    L.has_bias = bias != nullptr;
+    if (bias) check(hipMemcpy(L.bias, bias, c->cfg.n_expert * sizeof(float), hipMemcpyHostToDevice), "upload bias");
+  });
+}
+
+MOE_API moe_status moe_load_expert(moe_ctx *c, uint32_t layer, uint32_t expert, const uint8_t *gate, const uint8_t *up,
+                                   const uint8_t *down) {
+  return guarded(c, [&] {
+    const moe_config &g = c->cfg;
+    require(layer < g.n_layer && gate && up && down, "bad layer or null matrix");
+    const bool shared = expert == g.n_expert;
+    require(expert < g.n_expert || (shared && g.has_shared), "expert out of range");
+    const uint32_t gt = shared ? g.sh_gate_type : g.gate_type, dt = shared ? g.sh_down_type : g.down_type;
+    const uint64_t gu = matrix_bytes(gt, g.n_ff, g.n_embd), dn = matrix_bytes(dt, g.n_embd, g.n_ff);
+    std::vector<uint8_t> buf(2 * gu + dn);
+    repack_matrix(gt, gate, g.n_ff, g.n_embd, buf.data());
+    repack_matrix(gt, up, g.n_ff, g.n_embd, buf.data() + gu);
+    repack_matrix(dt, down, g.n_embd, g.n_ff, buf.data() + 2 * gu);
+    uint8_t *dst = shared ? c->layers[layer].shared : c->layers[layer].experts + (uint64_t)expert * c->ex_bytes;
+    check(hipMemcpy(dst, buf.data(), buf.size(), hipMemcpyHostToDevice), "upload expert");
+  });
+}
+
+MOE_API moe_status moe_forward(moe_ctx *c, uint32_t layer, const float *x, uint32_t ntok, uint64_t x_stride, float *y,
+                               uint64_t y_stride, moe_route_out *route) {
+  return guarded(c, [&] {
+    require(x && y && ntok >= 1 && ntok <= c->tmax, "bad x, y or ntok");
+    const uint32_t H = c->cfg.n_embd, K = c->cfg.n_used;
+    require(x_stride >= H && y_stride >= H, "strides below n_embd");
+    check(hipMemcpy2DAsync(c->x_dev, H * sizeof(float), x, x_stride * sizeof(float), H * sizeof(float), ntok,
+                           hipMemcpyHostToDevice, c->stream),
+          "upload x");
+    forward_dev(c, layer, c->x_dev, ntok, c->y_dev, nullptr, nullptr, c->stream);
+    check(hipMemcpy2DAsync(y, y_stride * sizeof(float), c->y_dev, H * sizeof(float), H * sizeof(float), ntok,
+                           hipMemcpyDeviceToHost, c->stream),
+          "download y");
+    if (route && route->ids)
+      check(hipMemcpyAsync(route->ids, c->ids, sizeof(int32_t) * ntok * K, hipMemcpyDeviceToHost, c->stream), "ids");
+    if (route && route->w)
+      check(hipMemcpyAsync(route->w, c->w, sizeof(float) * ntok * K, hipMemcpyDeviceToHost, c->stream), "w");
+    check(hipStreamSynchronize(c->stream), "forward");
+  });
+}
+
+MOE_API moe_status moe_forward_async(moe_ctx *c, uint32_t layer, const float *x_dev, uint32_t ntok, float *y_dev,
+                                     int32_t *ids_dev, float *w_dev, void *stream) {
+  return guarded(c, [&] {
+    require(x_dev && y_dev, "null x or y");
+    forward_dev(c, layer, x_dev, ntok, y_dev, ids_dev, w_dev, stream ? (hipStream_t)stream : c->stream);
+  });
+}
+
+MOE_API moe_status moe_forward_experts(moe_ctx *c, const moe_job *jobs, uint32_t njobs, uint32_t ntok, const float *x,
+                                       uint64_t x_stride, float *y, uint64_t y_stride) {
+  return guarded(c, [&] {
+    const moe_config &g = c->cfg;
+    const uint32_t H = g.n_embd;
+    require(x && y && ntok >= 1 && ntok <= c->tmax && x_stride >= H && y_stride >= H, "bad x, y, ntok or strides");
+    require(njobs == 0 || jobs, "null jobs");
+    const uint32_t layer = njobs ? jobs[0].layer : 0;
+    std::vector<uint32_t> per(ntok, 0);
+    for (uint32_t j = 0; j < njobs; j++) {
+      require(jobs[j].layer == layer, "the jobs of one call must share a layer");
+      require(jobs[j].tok < ntok, "job token out of range");
+      require(jobs[j].expert < g.n_expert || (jobs[j].expert == g.n_expert && g.has_shared), "job expert out of range");
+      per[jobs[j].tok]++;
+    }
+    require(layer < g.n_layer, "layer out of range");
+    uint32_t K = 1;
+    for (uint32_t t = 0; t < ntok; t++) K = std::max(K, per[t]);
+    require(K <= c->k1, "more jobs for one token than n_used + 1");
+    // Ranks in the given order per token; groups of the distinct experts in order of first job, 8 a group.
+    std::vector<int32_t> ids((size_t)ntok * K, -1);
+    std::vector<float> w((size_t)ntok * K, 0.0f);
+    std::vector<uint32_t> asg_of(njobs), fill(ntok, 0);
+    for (uint32_t j = 0; j < njobs; j++) {
+      const uint32_t t = jobs[j].tok, r = fill[t]++;
+      ids[(size_t)t * K + r] = (int32_t)jobs[j].expert;
+      w[(size_t)t * K + r] = jobs[j].w;
+      asg_of[j] = t * K + r;
+    }
+    std::vector<MoeGroup> groups;
+    std::vector<uint32_t> open_group(g.n_expert + 1, UINT32_MAX);
+    for (uint32_t j = 0; j < njobs; j++) {
+      const uint32_t e = jobs[j].expert;
+      uint32_t gi = open_group[e];
+      if (gi == UINT32_MAX || groups[gi].n == MOE_GROUP_MAX) {
+        MoeGroup m{};
+        m.slot = (int32_t)e;
+        groups.push_back(m);
+        gi = open_group[e] = (uint32_t)groups.size() - 1;
+      }
+      groups[gi].asg[groups[gi].n++] = asg_of[j];
+    }
+    const uint32_t ng = (uint32_t)groups.size();
+    require(ng <= max_groups(ntok, K), "too many groups");
+    hipStream_t s = c->stream;
+    check(hipMemcpy2DAsync(c->x_dev, H * sizeof(float), x, x_stride * sizeof(float), H * sizeof(float), ntok,
+                           hipMemcpyHostToDevice, s),
+          "upload x");
+    check(hipMemsetAsync(c->y_dev, 0, sizeof(float) * ntok * H, s), "clear y");
+    if (ng) check(hipMemcpyAsync(c->groups, groups.data(), sizeof(MoeGroup) * ng, hipMemcpyHostToDevice, s), "groups");
+    check(hipMemcpyAsync(c->ngroups, &ng, sizeof ng, hipMemcpyHostToDevice, s), "ngroups");
+    check(hipMemcpyAsync(c->ids, ids.data(), sizeof(int32_t) * ids.size(), hipMemcpyHostToDevice, s), "ids");
+    check(hipMemcpyAsync(c->w, w.data(), sizeof(float) * w.size(), hipMemcpyHostToDevice, s), "w");
+    check(hipMemcpyAsync(c->tok_need, per.data(), sizeof(uint32_t) * ntok, hipMemcpyHostToDevice, s), "tok_need");
+    DecodeParams p = base_params(c, layer, ntok);
+    p.K = K, p.route = 0, p.has_shared = 0, p.tok_need = c->tok_need;
+    p.xact_s = g.has_shared ? quant_vec_dot_type(g.sh_gate_type) : p.xact_r;
+    p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
+    p.x = c->x_dev, p.y = c->y_dev;
+    if (ng) launch(c, p, ntok, s);
+    check(hipMemcpy2DAsync(y, y_stride * sizeof(float), c->y_dev, H * sizeof(float), H * sizeof(float), ntok,
+                           hipMemcpyDeviceToHost, s),
+          "download y");
+    check(hipStreamSynchronize(s), "forward_experts");
+  });
+}
+
+MOE_API moe_status moe_sync(moe_ctx *c) {
+  return guarded(c, [&] { check(hipStreamSynchronize(c->stream), "hipStreamSynchronize"); });
+}
+
+MOE_API void *moe_stream(moe_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+MOE_API moe_status moe_set_timing(moe_ctx *c, int on) {
+  return guarded(c, [&] { c->timing = on != 0; });
+}
+
+MOE_API moe_status moe_kernel_times(moe_ctx *c, const char **names, float *ms, uint32_t cap, uint32_t *n) {
+  return guarded(c, [&] {
+    require(n != nullptr, "null n");
+    *n = 0;
+    if (!c->timed) return;
+    check(hipEventSynchronize(c->ev[kNumKernels]), "hipEventSynchronize");
+    for (int i = 0; i < kNumKernels && (uint32_t)i < cap; i++) {
+      float t = 0.0f;
+      check(hipEventElapsedTime(&t, c->ev[i], c->ev[i + 1]), "hipEventElapsedTime");
+      if (names) names[i] = kKernelNames[i];
+      if (ms) ms[i] = t;
+      *n = (uint32_t)i + 1;
+    }
+  });
+}
+
+MOE_API uint64_t moe_device_bytes(const moe_ctx *c) { return c ? c->dev_bytes : 0; }
+
+MOE_API moe_status moe_dequantize(moe_ctx *c, uint32_t type, const uint8_t *blocks, uint32_t rows, uint32_t cols,
+                                  float *out) {
+  return guarded(c, [&] {
+    require(quant_gpu_supported(type) && blocks && out && rows && cols && cols % kUnit == 0, "bad dequantize arguments");
+    const uint64_t mb = matrix_bytes(type, rows, cols);
+    std::vector<uint8_t> buf(mb);
+    repack_matrix(type, blocks, rows, cols, buf.data());
+    const uint32_t nrt = (rows + kTileRows - 1) / kTileRows;
+    uint8_t *dm = nullptr;
+    float *dout = nullptr;
+    check(hipMalloc(&dm, mb), "hipMalloc");
+    check(hipMalloc(&dout, (uint64_t)nrt * kTileRows * cols * sizeof(float)), "hipMalloc");
+    check(hipMemcpy(dm, buf.data(), mb, hipMemcpyHostToDevice), "upload");
+    hipLaunchKernelGGL(moe_dequant, dim3(nrt * (cols / kUnit)), dim3(64), 0, c->stream, dm, type, rows, cols, dout);
+    check(hipGetLastError(), "moe_dequant");
+    check(hipStreamSynchronize(c->stream), "moe_dequant");
+    check(hipMemcpy(out, dout, (uint64_t)rows * cols * sizeof(float), hipMemcpyDeviceToHost), "download");
+    (void)hipFree(dm);
+    (void)hipFree(dout);
+  });
+}
+
+#define ROW(s, f) {#s "." #f, (uint32_t)offsetof(s, f), (uint32_t)sizeof(((s *)0)->f)}
+#define STRUCT(s) {#s, 0u, (uint32_t)sizeof(s)}
+
+MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap) {
+  static const moe_abi_row rows[] = {
+      ROW(moe_config, n_embd),       ROW(moe_config, n_ff),         ROW(moe_config, n_expert),
+      ROW(moe_config, n_used),       ROW(moe_config, n_layer),      ROW(moe_config, gate_type),
+      ROW(moe_config, down_type),    ROW(moe_config, has_shared),   ROW(moe_config, sh_gate_type),
+      ROW(moe_config, sh_down_type), ROW(moe_config, max_tokens),   ROW(moe_config, swiglu_limit),
+      ROW(moe_config, device),       ROW(moe_config, reserved),     STRUCT(moe_config),
+      ROW(moe_route_out, ids),       ROW(moe_route_out, w),         STRUCT(moe_route_out),
+      ROW(moe_job, layer),           ROW(moe_job, expert),          ROW(moe_job, tok),
+      ROW(moe_job, w),               STRUCT(moe_job),               ROW(MoeTile, expert),
+      ROW(MoeTile, slot),            ROW(MoeTile, start),           ROW(MoeTile, count),
+      STRUCT(MoeTile),               ROW(MoeGroup, slot),           ROW(MoeGroup, n),
+      ROW(MoeGroup, asg),            STRUCT(MoeGroup),              ROW(moe_abi_row, name),
+      ROW(moe_abi_row, offset),      ROW(moe_abi_row, size),        STRUCT(moe_abi_row),
+  };
+  const uint32_t n = sizeof rows / sizeof rows[0];
+  if (table)
+    for (uint32_t i = 0; i < n && i < cap; i++) table[i] = rows[i];
+  return n;
+}
+
+}  // extern "C"

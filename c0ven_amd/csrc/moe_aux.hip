@@ -1,0 +1,53 @@
+// Decoding a matrix in the device layout back to fp32 with the kernels' own loaders (units.h): the check that the
+// layout and the field extraction give the format's values (moe_dequantize).
+#include <hip/hip_runtime.h>
+
+#include "aux.h"
+#include "iq3s_grid.h"
+#include "units.h"
+
+namespace c0ven {
+
+__device__ __constant__ static const uint32_t kGridAux[512] = {C0VEN_IQ3S_GRID_VALUES};
+
+// Grid: one work-group of 64 (a wave) per tile; lane l writes row rt * 64 + l, values u * 256 .. +256. The values are
+// formed as ggml's dequantize_row_* forms them: Q8_0 d q; Q4_K (d sc) q - (dmin m); IQ3_S (d (1 + 2 s)) (sign grid).
+__global__ void __launch_bounds__(64) moe_dequant(const uint8_t *mat, uint32_t type, uint32_t rows, uint32_t k,
+                                                  float *out) {
+  __shared__ uint32_t grid[512];
+  for (uint32_t i = threadIdx.x; i < 512; i += 64) grid[i] = kGridAux[i];
+  __syncthreads();
+  const uint32_t U = k / kUnit, rt = blockIdx.x / U, u = blockIdx.x % U, lane = threadIdx.x;
+  const uint32_t row = rt * kTileRows + lane;
+  const uint8_t *tile = mat + (uint64_t)blockIdx.x * tile_bytes(type);
+  float *o = out + (uint64_t)row * k + u * kUnit;
+  const bool live = row < rows;
+  if (type == QT_Q8_0) {
+    UnitQ8_0 w;
+    w.load(tile, lane);
+    if (live)
+      for (int i = 0; i < 256; i++) o[i] = __fmul_rn(w.d[i / 32], (float)(int8_t)(w.q[i / 4] >> (8 * (i % 4))));
+  } else if (type == QT_Q4_K) {
+    UnitQ4_K w;
+    w.load(tile, lane);
+    if (live)
+      for (int wd = 0; wd < 32; wd++)
+        for (int i = 0; i < 4; i++) {
+          const int c = wd / 8, v = 64 * c + 4 * (wd % 8) + i;
+          const float dl = __fmul_rn(w.d, (float)w.sc[2 * c]), ml = __fmul_rn(w.dmin, (float)w.mn[2 * c]);
+          const float dh = __fmul_rn(w.d, (float)w.sc[2 * c + 1]), mh = __fmul_rn(w.dmin, (float)w.mn[2 * c + 1]);
+          o[v] = __fsub_rn(__fmul_rn(dl, (float)((w.lo[wd] >> (8 * i)) & 0xff)), ml);
+          o[v + 32] = __fsub_rn(__fmul_rn(dh, (float)((w.hi[wd] >> (8 * i)) & 0xff)), mh);
+        }
+  } else {
+    UnitIQ3_S w;
+    w.load(tile, lane, grid);
+    if (live)
+      for (int i = 0; i < 256; i++) {
+        const float db = __fmul_rn(w.d, (float)w.ls[i / 32]);
+        o[i] = __fmul_rn(db, (float)(int8_t)(w.w[i / 4] >> (8 * (i % 4))));
+      }
+  }
+}
+
+}  // namespace c0ven

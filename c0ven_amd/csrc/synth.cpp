@@ -1,0 +1,253 @@
+// Seeded synthetic inputs and the weight quantisers (host). The configs' weights are N(0, sigma) fp32 values
+// quantised to the expert types; every machine draws the same values from (seed, stream, index).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "../../include/c0ven_moe.h"
+#include "iq3s_grid.h"
+
+namespace c0ven {
+namespace {
+
+inline uint64_t splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+// Normal i of (seed, stream): Box-Muller on two counter-based uniforms per pair of values.
+struct Normal {
+  uint64_t key;
+  Normal(uint64_t seed, uint64_t stream) : key(splitmix64(seed ^ splitmix64(stream * 0x2545f4914f6cdd1dull + 1))) {}
+  void pair(uint64_t p, double &z0, double &z1) const {
+    const uint64_t r1 = splitmix64(key + 2 * p), r2 = splitmix64(key + 2 * p + 1);
+    const double u1 = ((double)(r1 >> 11) + 1.0) * 0x1p-53, u2 = (double)(r2 >> 11) * 0x1p-53;
+    const double rad = std::sqrt(-2.0 * std::log(u1)), th = 6.283185307179586 * u2;
+    z0 = rad * std::cos(th);
+    z1 = rad * std::sin(th);
+  }
+  void fill(float sigma, float *out, uint64_t i0, uint64_t n) const {
+    for (uint64_t i = i0; i < i0 + n; i++) {
+      double z0, z1;
+      pair(i / 2, z0, z1);
+      out[i - i0] = (float)((i % 2 ? z1 : z0) * (double)sigma);
+    }
+  }
+};
+
+int threads_for(int nthreads) {
+  if (nthreads > 0) return nthreads;
+  const unsigned hc = std::thread::hardware_concurrency();
+  return hc ? (int)std::min(hc, 64u) : 1;
+}
+
+template <typename F>
+void parallel_for(uint64_t n, int nthreads, F f) {
+  const int nt = (int)std::min<uint64_t>((uint64_t)threads_for(nthreads), std::max<uint64_t>(n, 1));
+  if (nt <= 1) {
+    for (uint64_t i = 0; i < n; i++) f(i);
+    return;
+  }
+  std::vector<std::thread> th;
+  for (int t = 0; t < nt; t++)
+    th.emplace_back([=, &f] {
+      for (uint64_t i = n * t / nt; i < n * (t + 1) / nt; i++) f(i);
+    });
+  for (auto &x : th) x.join();
+}
+
+inline uint16_t fp16_bits(float f) {
+  _Float16 h = (_Float16)f;  // round to nearest even
+  uint16_t b;
+  std::memcpy(&b, &h, 2);
+  return b;
+}
+inline float fp16_value(uint16_t b) {
+  _Float16 h;
+  std::memcpy(&h, &b, 2);
+  return (float)h;
+}
+inline int nearest(float v) { return (int)std::nearbyint(v); }
+
+// ggml's quantize_row_q8_0_ref: d = amax / 127, q = round(x / d) (half away from zero), d stored as f16.
+void quant_q8_0(const float *x, uint8_t *y, uint32_t n) {
+  for (uint32_t b = 0; b < n / 32; b++, x += 32, y += 34) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) amax = std::max(amax, std::fabs(x[j]));
+    const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = fp16_bits(d);
+    std::memcpy(y, &dh, 2);
+    for (int j = 0; j < 32; j++) y[2 + j] = (uint8_t)(int8_t)std::round(x[j] * id);
+  }
+}
+
+// Q4_K: per sub-block of 32 the range [min(lo, 0), hi] in 15 steps, the steps and minimums as 6-bit multiples of
+// their largest / 63, codes rounded to nearest with the rounded scales. Valid blocks, but not ggml's
+// make_qkx2_quants search.
+void quant_q4_K(const float *x, uint8_t *y, uint32_t n) {
+  for (uint32_t b = 0; b < n / 256; b++, x += 256, y += 144) {
+    float step[8], mins[8];
+    for (int j = 0; j < 8; j++) {
+      float lo = 0.0f, hi = 0.0f;
+      for (int i = 0; i < 32; i++) lo = std::min(lo, x[32 * j + i]), hi = std::max(hi, x[32 * j + i]);
+      mins[j] = -lo;
+      step[j] = (hi - lo) / 15.0f;
+    }
+    const float smax = *std::max_element(step, step + 8), mmax = *std::max_element(mins, mins + 8);
+    const uint16_t dh = fp16_bits(smax / 63.0f), mh = fp16_bits(mmax / 63.0f);
+    const float d = fp16_value(dh), dmin = fp16_value(mh);
+    int sc[8], m[8];
+    for (int j = 0; j < 8; j++) {
+      sc[j] = d > 0.0f ? std::clamp(nearest(step[j] / d), 0, 63) : 0;
+      m[j] = dmin > 0.0f ? std::clamp(nearest(mins[j] / dmin), 0, 63) : 0;
+      if (step[j] > 0.0f && sc[j] == 0) sc[j] = 1;
+    }
+    std::memcpy(y, &dh, 2);
+    std::memcpy(y + 2, &mh, 2);
+    uint8_t *s = y + 4;
+    for (int j = 0; j < 4; j++) {
+      s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+      s[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+      s[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+    }
+    uint8_t q[256];
+    for (int j = 0; j < 8; j++) {
+      const float dj = d * (float)sc[j], mj = dmin * (float)m[j];
+      for (int i = 0; i < 32; i++) q[32 * j + i] = dj > 0.0f ? (uint8_t)std::clamp(nearest((x[32 * j + i] + mj) / dj), 0, 15) : 0;
+    }
+    for (int c = 0; c < 4; c++)
+      for (int l = 0; l < 32; l++) y[16 + 32 * c + l] = (uint8_t)(q[64 * c + l] | (q[64 * c + 32 + l] << 4));
+  }
+}
+
+// For each point of the 8^4 lattice of magnitude levels (2 l + 1), the nearest IQ3_S grid entry (squared distance,
+// ties to the lower entry).
+const std::vector<uint16_t> &iq3s_nearest() {
+  static const std::vector<uint16_t> map = [] {
+    std::vector<uint16_t> m(4096);
+    for (uint32_t c = 0; c < 4096; c++) {
+      int best = 0, bd = 1 << 30;
+      for (int g = 0; g < 512; g++) {
+        int dd = 0;
+        for (int j = 0; j < 4; j++) {
+          const int a = 2 * (int)((c >> (3 * j)) & 7) + 1, v = (int)((kIq3sGridHost[g] >> (8 * j)) & 0xff);
+          dd += (a - v) * (a - v);
+        }
+        if (dd < bd) bd = dd, best = g;
+      }
+      m[c] = (uint16_t)best;
+    }
+    return m;
+  }();
+  return map;
+}
+
+// IQ3_S: per sub-block of 32 a step amax / 15 as d (1 + 2 s), d = the largest step / 31; each group of four
+// magnitudes to its nearest lattice levels, then to the nearest grid entry; the signs stored plainly. Valid blocks,
+// not ggml's quantize_row_iq3_s search.
+void quant_iq3_s(const float *x, uint8_t *y, uint32_t n) {
+  const std::vector<uint16_t> &near = iq3s_nearest();
+  for (uint32_t b = 0; b < n / 256; b++, x += 256, y += 110) {
+    std::memset(y, 0, 110);
+    float step[8];
+    for (int j = 0; j < 8; j++) {
+      float a = 0.0f;
+      for (int i = 0; i < 32; i++) a = std::max(a, std::fabs(x[32 * j + i]));
+      step[j] = a / 15.0f;
+    }
+    const float smax = *std::max_element(step, step + 8);
+    const uint16_t dh = fp16_bits(smax / 31.0f);
+    const float d = fp16_value(dh);
+    std::memcpy(y, &dh, 2);
+    if (d <= 0.0f) continue;
+    uint8_t *qs = y + 2, *qh = y + 66, *signs = y + 74, *scales = y + 106;
+    for (int ib = 0; ib < 8; ib++) {
+      const int s = std::clamp(nearest((step[ib] / d - 1.0f) / 2.0f), 0, 15);
+      scales[ib / 2] |= (uint8_t)(s << (4 * (ib % 2)));
+      const float db = d * (float)(1 + 2 * s);
+      for (int k = 0; k < 8; k++) {
+        uint32_t code = 0;
+        for (int j = 0; j < 4; j++) {
+          const float v = x[32 * ib + 4 * k + j];
+          const int l = std::clamp(nearest((std::fabs(v) / db - 1.0f) / 2.0f), 0, 7);
+          code |= (uint32_t)l << (3 * j);
+          if (v < 0.0f) signs[4 * ib + (4 * k + j) / 8] |= (uint8_t)(1u << ((4 * k + j) % 8));
+        }
+        const uint32_t g = near[code];
+        qs[8 * ib + k] = (uint8_t)(g & 0xff);
+        qh[ib] |= (uint8_t)(((g >> 8) & 1u) << k);
+      }
+    }
+  }
+}
+
+bool quant_rows(uint32_t type, const float *x, uint32_t cols, uint8_t *out) {
+  switch (type) {
+    case QT_Q8_0: quant_q8_0(x, out, cols); return true;
+    case QT_Q4_K: quant_q4_K(x, out, cols); return true;
+    case QT_IQ3_S: quant_iq3_s(x, out, cols); return true;
+    default: return false;
+  }
+}
+
+}  // namespace
+}  // namespace c0ven
+
+using namespace c0ven;
+
+extern "C" {
+
+MOE_API uint64_t moe_row_bytes(uint32_t type, uint32_t cols) {
+  const uint32_t bv = quant_block_values(type);
+  return bv ? (uint64_t)cols / bv * quant_block_bytes(type) : 0;
+}
+
+MOE_API void moe_synth_normal(uint64_t seed, uint64_t stream, float sigma, float *out, uint64_t n, int nthreads) {
+  const Normal nr(seed, stream);
+  const uint64_t chunk = 1 << 16, nc = (n + chunk - 1) / chunk;
+  parallel_for(nc, nthreads, [&](uint64_t c) {
+    const uint64_t i0 = c * chunk;
+    nr.fill(sigma, out + i0, i0, std::min(chunk, n - i0));
+  });
+}
+
+MOE_API moe_status moe_quantize(uint32_t type, const float *x, uint32_t rows, uint32_t cols, uint8_t *out,
+                                int nthreads) {
+  if (!quant_gpu_supported(type) || cols % quant_block_values(type) || (type != QT_Q8_0 && cols % 256)) return MOE_BAD_ARGUMENT;
+  const uint64_t rb = moe_row_bytes(type, cols);
+  parallel_for(rows, nthreads, [&](uint64_t r) { quant_rows(type, x + r * cols, cols, out + r * rb); });
+  return MOE_OK;
+}
+
+MOE_API moe_status moe_synth_matrix(uint64_t seed, uint64_t stream, float sigma, uint32_t type, uint32_t rows,
+                                    uint32_t cols, uint8_t *out, int nthreads) {
+  if (!quant_gpu_supported(type) || cols % 256) return MOE_BAD_ARGUMENT;
+  const Normal nr(seed, stream);
+  const uint64_t rb = moe_row_bytes(type, cols);
+  const uint64_t per = std::max<uint64_t>(1, (1u << 16) / cols), nc = (rows + per - 1) / per;
+  parallel_for(nc, nthreads, [&](uint64_t c) {
+    std::vector<float> buf((size_t)per * cols);
+    const uint64_t r0 = c * per, nr_ = std::min<uint64_t>(per, rows - r0);
+    nr.fill(sigma, buf.data(), r0 * cols, nr_ * cols);
+    for (uint64_t r = 0; r < nr_; r++) quant_rows(type, buf.data() + r * cols, cols, out + (r0 + r) * rb);
+  });
+  return MOE_OK;
+}
+
+MOE_API void moe_zipf_bias(uint64_t seed, uint32_t n_expert, float s, float *out) {
+  std::vector<uint32_t> perm(n_expert);
+  for (uint32_t i = 0; i < n_expert; i++) perm[i] = i;
+  uint64_t st = splitmix64(seed ^ 0x5a17f00dull);
+  for (uint32_t i = n_expert; i > 1; i--) {  // Fisher-Yates
+    st = splitmix64(st);
+    std::swap(perm[i - 1], perm[st % i]);
+  }
+  for (uint32_t e = 0; e < n_expert; e++) out[e] = (float)(-(double)s * std::log(1.0 + (double)perm[e]));
+}
+
+}  // extern "C"

@@ -1,0 +1,159 @@
+/* The MoE block on one MI355X: a C ABI over HIP.
+ *
+ * Replaces, for the mixture-of-experts block of the qwen4exp model, the reference's expert executors:
+ *   - core/cpu/experts.h:32-60   CpuExperts::compute / compute_many / h_rows (the CPU expert path), and
+ *   - the decode and prefill kernel lists of that block, model.cpp:1348-1414 and prompt.cpp:609-655
+ *     (mv_xmx_bf16 router rows, router_group, moe_gate_up_g, moe_down_g, moe_combine; p_router, p_moe_count / scan /
+ *     fill / scatter, moe_gate_up_t, moe_down_t, p_moe_combine).
+ * The conventions are the reference's C ABI's (include/engine_api.h:1-10, :28-34, :384, :414-421):
+ *   - every call returns a moe_status with engine_status's values; moe_last_error(ctx) gives the message;
+ *   - no exception and no callback crosses the ABI; only plain structs, pointers and sizes do;
+ *   - the library owns device memory (it uploads and lays out the weights itself); the caller owns x and y;
+ *   - one host thread uses a context at a time; calls are synchronous unless named _async;
+ *   - y is overwritten, never accumulated into (core/cpu/experts.cpp:112, :256-258);
+ *   - exported symbols carry the moe_ prefix; everything else is hidden.
+ * The data contracts are c0ven_quant.h (shared/quant.h) and c0ven_moe_tile.h (shared/moe_tile.h). */
+#ifndef C0VEN_MOE_H
+#define C0VEN_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "c0ven_moe_tile.h"
+#include "c0ven_quant.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(C0VEN_MOE_EXPORT)
+#define MOE_API __attribute__((visibility("default")))
+#else
+#define MOE_API
+#endif
+
+#define MOE_API_VERSION 1
+
+typedef enum {
+  MOE_OK = 0,
+  MOE_ERROR = 1, /* see moe_last_error */
+  MOE_BAD_ARGUMENT = 2,
+  MOE_BUSY = 3,
+  MOE_TIMEOUT = 4
+} moe_status;
+
+typedef struct moe_ctx moe_ctx;
+
+/* The block's shape and types (ExpertShape, core/cpu/experts.h:24-31, with the router and the shared expert of
+ * docs/spec/MODEL_LAYER.md section 4). Zero means the default given here. */
+typedef struct {
+  uint32_t n_embd;       /* H: K of gate and up, rows of down; a multiple of 512 */
+  uint32_t n_ff;         /* F: rows of gate and up, K of down; a multiple of 256 */
+  uint32_t n_expert;     /* E routed experts, at most 512 */
+  uint32_t n_used;       /* k, at most 16 */
+  uint32_t n_layer;      /* layers held resident (default 1) */
+  uint32_t gate_type;    /* QT_Q8_0, QT_Q4_K or QT_IQ3_S: gate and up of the routed experts */
+  uint32_t down_type;    /* the same set: down of the routed experts */
+  uint32_t has_shared;   /* 1: one shared expert with a sigmoid gate (the router's row E) */
+  uint32_t sh_gate_type; /* the shared expert's types */
+  uint32_t sh_down_type;
+  uint32_t max_tokens;   /* the most tokens one forward takes (default 16) */
+  float swiglu_limit;    /* > 0: gate = min(gate, L), up = clamp(up, -L, L) before the SiLU; 0 = off */
+  int32_t device;        /* HIP device ordinal */
+  uint32_t reserved[4];
+} moe_config;
+
+/* The routing result of a forward, per token: k expert ids in rank order and their weights. */
+typedef struct {
+  int32_t *ids; /* ntok x n_used, or null */
+  float *w;     /* ntok x n_used, or null */
+} moe_route_out;
+
+/* A pre-routed expert job (CpuExperts::Job, core/cpu/experts.h:46-50): the expert (layer, index; n_expert names the
+ * shared expert), the token it serves and its weight. */
+typedef struct {
+  uint32_t layer;
+  uint32_t expert;
+  uint32_t tok;
+  float w;
+} moe_job;
+
+/* Opens a context on cfg->device and allocates the resident weights of every layer and the scratch. */
+MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out);
+MOE_API void moe_close(moe_ctx *ctx);
+/* The last error's message, valid until the next call on ctx (ctx may be null for moe_open's failures). */
+MOE_API const char *moe_last_error(const moe_ctx *ctx);
+
+/* The router of a layer: (n_expert + 1) x n_embd bf16, row-major, the last row the shared expert's gate
+ * (blk.N.ffn_gate_inp and ffn_gate_inp_shexp). bias: n_expert fp32 logit biases, or null for none. */
+MOE_API moe_status moe_load_router(moe_ctx *ctx, uint32_t layer, const uint16_t *router_bf16, const float *bias);
+/* One expert's three matrices in the file's layout (ggml blocks, row-major): gate and up n_ff x n_embd, down
+ * n_embd x n_ff, of the context's types (expert == n_expert: the shared expert, of the shared types). The library
+ * repacks them into its device layout; the caller's buffers are not kept. */
+MOE_API moe_status moe_load_expert(moe_ctx *ctx, uint32_t layer, uint32_t expert, const uint8_t *gate,
+                                   const uint8_t *up, const uint8_t *down);
+
+/* The block for ntok rows of x (host memory, rows x_stride floats apart) into y (y_stride): router, experts, shared
+ * expert, combine. Synchronous. route may be null. */
+MOE_API moe_status moe_forward(moe_ctx *ctx, uint32_t layer, const float *x, uint32_t ntok, uint64_t x_stride,
+                               float *y, uint64_t y_stride, moe_route_out *route);
+/* The same on device memory (x and y ntok x n_embd fp32, contiguous; ids and w ntok x n_used or null), enqueued on
+ * stream (a hipStream_t; null: the context's stream). Nothing is copied and nothing waits. */
+MOE_API moe_status moe_forward_async(moe_ctx *ctx, uint32_t layer, const float *x_dev, uint32_t ntok, float *y_dev,
+                                     int32_t *ids_dev, float *w_dev, void *stream);
+/* CpuExperts::compute_many on resident experts: y[tok] = sum over the jobs with that tok, in the order given, of
+ * w * expert(x[tok]); no router, no gate. Synchronous, host buffers. */
+MOE_API moe_status moe_forward_experts(moe_ctx *ctx, const moe_job *jobs, uint32_t njobs, uint32_t ntok,
+                                       const float *x, uint64_t x_stride, float *y, uint64_t y_stride);
+/* CpuExperts::h_rows (core/cpu/experts.h:52-56): the h rows one pass of the down kernels takes, 256 here (one unit;
+ * the GPU path has no task split). 0 when n_ff is not a multiple of it. */
+MOE_API uint32_t moe_h_rows(const moe_config *cfg);
+
+/* Waits for the context's stream. */
+MOE_API moe_status moe_sync(moe_ctx *ctx);
+/* The context's HIP stream (a hipStream_t). */
+MOE_API void *moe_stream(moe_ctx *ctx);
+
+/* Timing of the last forward's kernels with HIP events on the stream they ran on, when enabled (off by default:
+ * events cost a little). names and ms have room for cap entries; n receives how many. */
+MOE_API moe_status moe_set_timing(moe_ctx *ctx, int on);
+MOE_API moe_status moe_kernel_times(moe_ctx *ctx, const char **names, float *ms, uint32_t cap, uint32_t *n);
+
+/* Device bytes the context holds: resident weights and scratch. */
+MOE_API uint64_t moe_device_bytes(const moe_ctx *ctx);
+
+/* Decodes rows x cols values of a matrix of type in the file's layout through the device layout and the kernels'
+ * decoders, into out (host, rows x cols fp32). For checking the layout and the decoders against the format. */
+MOE_API moe_status moe_dequantize(moe_ctx *ctx, uint32_t type, const uint8_t *blocks, uint32_t rows, uint32_t cols,
+                                  float *out);
+
+/* Synthetic inputs (seeded, so that every machine draws the same values): counter-based normals, the library's
+ * quantisers, the Zipf logit bias of BASELINE's configs. nthreads <= 0: all cores. */
+MOE_API void moe_synth_normal(uint64_t seed, uint64_t stream, float sigma, float *out, uint64_t n, int nthreads);
+/* rows x cols fp32 (row-major) into blocks of type (Q8_0: ggml's quantize_row_q8_0_ref; Q4_K and IQ3_S: this
+ * library's own quantisers, which write valid blocks but are not ggml's search). Returns MOE_OK or BAD_ARGUMENT. */
+MOE_API moe_status moe_quantize(uint32_t type, const float *x, uint32_t rows, uint32_t cols, uint8_t *out,
+                                int nthreads);
+/* A matrix of N(0, sigma) values drawn from (seed, stream), quantised: the same bytes as moe_synth_normal followed by
+ * moe_quantize, without the fp32 copy. */
+MOE_API moe_status moe_synth_matrix(uint64_t seed, uint64_t stream, float sigma, uint32_t type, uint32_t rows,
+                                    uint32_t cols, uint8_t *out, int nthreads);
+/* bias[e] = -s ln(1 + pi(e)), pi a seeded permutation of the experts: softmax weights proportional to Zipf(s) ranks. */
+MOE_API void moe_zipf_bias(uint64_t seed, uint32_t n_expert, float s, float *out);
+/* Bytes of rows x cols values of type in the file's layout. */
+MOE_API uint64_t moe_row_bytes(uint32_t type, uint32_t cols);
+
+/* For the ABI test: one row per field of every struct above, "struct.field" with its offset and size, then one row
+ * per struct, "struct", offset 0 and its size. Returns the number of rows; table may be null. */
+typedef struct {
+  const char *name;
+  uint32_t offset;
+  uint32_t size;
+} moe_abi_row;
+MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,567 @@
+/* TEST INFRASTRUCTURE - the CPU oracle of the MoE block (see oracle.h). Built by oracle/Makefile with
+ * -ffp-contract=off, so every fp32 step rounds where the source says it does. */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "iq3s_lattice.h"
+
+#define QT_Q8_0 8
+#define QT_Q4_K 12
+#define QT_Q8_K 15
+#define QT_IQ3_S 21
+#define QK 256
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Scalars. */
+
+/* IEEE binary16 from binary32, rounded to nearest even (what F16C's vcvtps2ph with mode 0 and ggml's
+ * GGML_FP32_TO_FP16 give). */
+uint16_t orc_fp32_to_fp16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* 65520 and up round to infinity */
+  if (ax < 0x38800000u) {                                   /* below 2^-14: a subnormal half, units of 2^-24 */
+    float a;
+    memcpy(&a, &ax, 4);
+    return (uint16_t)(sign | (uint32_t)nearbyintf(a * 16777216.0f));
+  }
+  uint32_t h = ((((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13));
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+  return (uint16_t)(sign | h);
+}
+
+float orc_fp16_to_fp32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu;
+  uint32_t x;
+  if (e == 0) {
+    float v = (float)m * (1.0f / 16777216.0f); /* exact: m < 2^10 */
+    memcpy(&x, &v, 4);
+    x |= sign;
+  } else if (e == 31) {
+    x = sign | 0x7f800000u | (m << 13);
+  } else {
+    x = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &x, 4);
+  return f;
+}
+
+/* bf16 by round to nearest even, NaN kept quiet (ggml-impl.h GGML_FP32_TO_BF16). */
+uint16_t orc_fp32_to_bf16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 64u);
+  return (uint16_t)((x + (0x7fffu + ((x >> 16) & 1u))) >> 16);
+}
+
+static inline float bf16_to_fp32(uint16_t b) {
+  const uint32_t x = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &x, 4);
+  return f;
+}
+
+void orc_expf(const float *x, float *y, int64_t n) {
+  for (int64_t i = 0; i < n; i++) y[i] = expf(x[i]);
+}
+
+/* ggml's nearest_int (ggml-quants.c): round half to even through the float adder, for |v| < 2^22. */
+static inline int nearest_int(float v) {
+  const float t = v + 12582912.0f;
+  int32_t i;
+  memcpy(&i, &t, 4);
+  return (i & 0x007fffff) - 0x00400000;
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * The IQ3_S codebook: entry i is four bytes 2 l_j + 1 (j = 0..3, byte j), l_j the 3-bit fields of the lattice code
+ * kIq3sLattice[i] (l_0 in bits 0-2). These are the 512 points ggml's iq3xs_init_impl(512) (ggml-quants.c) builds
+ * iq3s_grid from; their table must hash to QUANT_FORMATS.md:546's sha256, which tests/test_oracle.py checks. */
+static uint32_t g_grid[512];
+static int g_grid_ready;
+
+static void grid_init(void) {
+  if (g_grid_ready) return;
+  for (int i = 0; i < 512; i++) {
+    const uint32_t c = kIq3sLattice[i];
+    uint32_t v = 0;
+    for (int j = 0; j < 4; j++) v |= (2u * ((c >> (3 * j)) & 7u) + 1u) << (8 * j);
+    g_grid[i] = v;
+  }
+  g_grid_ready = 1;
+}
+
+void orc_iq3s_grid(uint32_t *out) {
+  grid_init();
+  memcpy(out, g_grid, sizeof g_grid);
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Decoders (ggml-quants.c dequantize_row_*, as QUANT_FORMATS.md states them). */
+
+static inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* Q4_K's packed 6-bit scale and minimum of sub-block j (get_scale_min_k4, QUANT_FORMATS.md:383-389). */
+static inline void scale_min_k4(int j, const uint8_t *q, int *sc, int *m) {
+  if (j < 4) {
+    *sc = q[j] & 63;
+    *m = q[j + 4] & 63;
+  } else {
+    *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+/* Value v of an IQ3_S block as (grid magnitude, negative?) with its sub-block scale 1 + 2 s. */
+static inline void iq3s_value(const uint8_t *b, int v, int *mag, int *neg, int *ls) {
+  const uint8_t *qs = b + 2, *qh = b + 66, *signs = b + 74, *scales = b + 106;
+  const int ib = v / 32, k = (v % 32) / 4, j = v % 4, l = (v % 32) / 8;
+  const uint32_t idx = qs[8 * ib + k] | (((qh[ib] >> k) & 1u) << 8);
+  *mag = (int)((g_grid[idx] >> (8 * j)) & 0xffu);
+  *neg = (signs[4 * ib + l] >> (v % 8)) & 1;
+  *ls = 1 + 2 * ((scales[ib / 2] >> (4 * (ib % 2))) & 15);
+}
+
+int orc_dequantize_row(uint32_t type, const void *src, float *dst, int64_t n) {
+  const uint8_t *b = (const uint8_t *)src;
+  grid_init();
+  switch (type) {
+    case QT_Q8_0: /* y = d q (quants.c:553-567) */
+      if (n % 32) return -1;
+      for (int64_t i = 0; i < n / 32; i++, b += 34) {
+        const float d = orc_fp16_to_fp32(rd16(b));
+        for (int j = 0; j < 32; j++) dst[32 * i + j] = d * (float)(int8_t)b[2 + j];
+      }
+      return 0;
+    case QT_Q4_K: /* y = (d sc) q - (dmin m) (quants.c:1529-1551) */
+      if (n % QK) return -1;
+      for (int64_t i = 0; i < n / QK; i++, b += 144) {
+        const float d = orc_fp16_to_fp32(rd16(b)), dmin = orc_fp16_to_fp32(rd16(b + 2));
+        const uint8_t *q = b + 16;
+        float *y = dst + QK * i;
+        for (int c = 0; c < 4; c++, q += 32) {
+          int sc, m;
+          scale_min_k4(2 * c, b + 4, &sc, &m);
+          const float d1 = d * (float)sc, m1 = dmin * (float)m;
+          scale_min_k4(2 * c + 1, b + 4, &sc, &m);
+          const float d2 = d * (float)sc, m2 = dmin * (float)m;
+          for (int l = 0; l < 32; l++) y[64 * c + l] = d1 * (float)(q[l] & 0xF) - m1;
+          for (int l = 0; l < 32; l++) y[64 * c + 32 + l] = d2 * (float)(q[l] >> 4) - m2;
+        }
+      }
+      return 0;
+    case QT_IQ3_S: /* y = (d (1 + 2 s)) grid sign (quants.c:2607-2646) */
+      if (n % QK) return -1;
+      for (int64_t i = 0; i < n / QK; i++, b += 110) {
+        const float d = orc_fp16_to_fp32(rd16(b));
+        for (int v = 0; v < QK; v++) {
+          int mag, neg, ls;
+          iq3s_value(b, v, &mag, &neg, &ls);
+          const float db = d * (float)ls;
+          dst[QK * i + v] = db * (float)mag * (neg ? -1.0f : 1.0f);
+        }
+      }
+      return 0;
+    default: return -1;
+  }
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Activation quantisers. */
+
+/* q8_0 as ggml's x86 quantize_row_q8_0 makes it: d = amax / 127 stored as f16, codes round(x * (127 / amax)) to
+ * nearest even (QUANT_FORMATS.md:463-465 gives the rule; the AVX2 kernel scales by 127/amax and rounds with
+ * _MM_ROUND_NEAREST). */
+static void quantize_q8_0(const float *x, uint8_t *y, int64_t n) {
+  for (int64_t i = 0; i < n / 32; i++, x += 32, y += 34) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = amax / 127.0f, id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    const uint16_t dh = orc_fp32_to_fp16(d);
+    y[0] = (uint8_t)(dh & 0xff);
+    y[1] = (uint8_t)(dh >> 8);
+    for (int j = 0; j < 32; j++) y[2 + j] = (uint8_t)(int8_t)nearest_int(x[j] * id);
+  }
+}
+
+/* q8_K (quantize_row_q8_K_ref, QUANT_FORMATS.md:528-535): the value of largest magnitude max, iscale = -127 / max,
+ * q = min(127, nearest(iscale x)), d = 1 / iscale (f32), bsums the sums of each 16 codes. An all-zero block is d = 0,
+ * codes and sums 0. Layout: d f32 at 0, qs at 4, bsums int16 at 260 (292 B). */
+static void quantize_q8_K(const float *x, uint8_t *y, int64_t n) {
+  for (int64_t i = 0; i < n / QK; i++, x += QK, y += 292) {
+    float max = 0.0f, amax = 0.0f;
+    for (int j = 0; j < QK; j++) {
+      const float ax = fabsf(x[j]);
+      if (ax > amax) {
+        amax = ax;
+        max = x[j];
+      }
+    }
+    int8_t *qs = (int8_t *)(y + 4);
+    int16_t bs[16];
+    if (amax == 0.0f) {
+      memset(y, 0, 292);
+      continue;
+    }
+    const float iscale = -127.0f / max;
+    for (int j = 0; j < QK; j++) {
+      const int v = nearest_int(iscale * x[j]);
+      qs[j] = (int8_t)(v < 127 ? v : 127);
+    }
+    for (int j = 0; j < 16; j++) {
+      int s = 0;
+      for (int l = 0; l < 16; l++) s += qs[16 * j + l];
+      bs[j] = (int16_t)s;
+    }
+    memcpy(y + 260, bs, 32);
+    const float d = 1.0f / iscale;
+    memcpy(y, &d, 4);
+  }
+}
+
+int orc_quantize_act(uint32_t act_type, const float *src, void *dst, int64_t n) {
+  if (act_type == QT_Q8_0 && n % 32 == 0) {
+    quantize_q8_0(src, (uint8_t *)dst, n);
+    return 0;
+  }
+  if (act_type == QT_Q8_K && n % QK == 0) {
+    quantize_q8_K(src, (uint8_t *)dst, n);
+    return 0;
+  }
+  return -1;
+}
+
+static uint32_t act_type_of(uint32_t t) { return t == QT_Q8_0 ? QT_Q8_0 : (t == QT_Q4_K || t == QT_IQ3_S) ? QT_Q8_K : 0; }
+static uint64_t act_bytes(uint32_t act, uint64_t n) { return act == QT_Q8_0 ? n / 32 * 34 : n / QK * 292; }
+static uint64_t row_bytes(uint32_t t, uint64_t n) {
+  return t == QT_Q8_0 ? n / 32 * 34 : t == QT_Q4_K ? n / QK * 144 : t == QT_IQ3_S ? n / QK * 110 : 0;
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Block dot products. Each returns the block's fp32 term; the row is their pairwise sum (ORACLE ORDER). */
+
+static float pairwise(const float *a, int64_t n) {
+  if (n == 1) return a[0];
+  int64_t m = 1;
+  while (2 * m < n) m *= 2;
+  return pairwise(a, m) + pairwise(a + m, n - m);
+}
+
+/* Q8_0 x q8_0 (vec_dot_q8_0_q8_0, QUANT_FORMATS.md:468-470): (d_w d_a) sum q_w q_a. */
+static float term_q8_0(const uint8_t *w, const uint8_t *a) {
+  int32_t s = 0;
+  for (int j = 0; j < 32; j++) s += (int32_t)(int8_t)w[2 + j] * (int32_t)(int8_t)a[2 + j];
+  const float d = orc_fp16_to_fp32(rd16(w)) * orc_fp16_to_fp32(rd16(a));
+  return d * (float)s;
+}
+
+/* Q4_K x q8_K (vec_dot_q4_K_q8_K, QUANT_FORMATS.md:391-400): the scale part sum_j sc_j sum q q_a and the minimum part
+ * sum_j m_j (bsums of sub-block j), both exact integers, then (d_w d_a) isum - (dmin_w d_a) imin with one rounding
+ * for the second product and a fused multiply-add for the first. */
+static float term_q4_K(const uint8_t *w, const uint8_t *a) {
+  float ad;
+  memcpy(&ad, a, 4);
+  const int8_t *q8 = (const int8_t *)(a + 4);
+  int16_t bs[16];
+  memcpy(bs, a + 260, 32);
+  const uint8_t *q = w + 16;
+  int32_t isum = 0, imin = 0;
+  for (int j = 0; j < 8; j++) {
+    int sc, m;
+    scale_min_k4(j, w + 4, &sc, &m);
+    const uint8_t *qc = q + 32 * (j / 2);
+    int32_t dot = 0;
+    for (int l = 0; l < 32; l++) dot += (int32_t)((j & 1) ? qc[l] >> 4 : qc[l] & 0xF) * q8[32 * j + l];
+    isum += sc * dot;
+    imin += m * (bs[2 * j] + bs[2 * j + 1]);
+  }
+  const float d = orc_fp16_to_fp32(rd16(w)) * ad, dm = orc_fp16_to_fp32(rd16(w + 2)) * ad;
+  const float pm = dm * (float)imin;
+  return fmaf(d, (float)isum, -pm);
+}
+
+/* IQ3_S x q8_K (vec_dot_iq3_s_q8_K; core/cpu/multirow.cpp:179-245 states its integer steps): per sub-block
+ * (1 + 2 s) sum grid sign q_a, summed as an integer, times (d_w d_a). */
+static float term_iq3_s(const uint8_t *w, const uint8_t *a) {
+  float ad;
+  memcpy(&ad, a, 4);
+  const int8_t *q8 = (const int8_t *)(a + 4);
+  int32_t bsum = 0;
+  for (int ib = 0; ib < 8; ib++) {
+    int32_t s = 0, ls = 0;
+    for (int i = 0; i < 32; i++) {
+      int mag, neg;
+      iq3s_value(w, 32 * ib + i, &mag, &neg, &ls);
+      s += (neg ? -mag : mag) * q8[32 * ib + i];
+    }
+    bsum += ls * s;
+  }
+  const float d = orc_fp16_to_fp32(rd16(w)) * ad;
+  return d * (float)bsum;
+}
+
+static float dot_row(uint32_t type, int64_t n, const uint8_t *w, const uint8_t *a, float *terms) {
+  int64_t nb;
+  switch (type) {
+    case QT_Q8_0:
+      nb = n / 32;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_q8_0(w + 34 * i, a + 34 * i);
+      break;
+    case QT_Q4_K:
+      nb = n / QK;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_q4_K(w + 144 * i, a + 292 * i);
+      break;
+    default:
+      nb = n / QK;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_iq3_s(w + 110 * i, a + 292 * i);
+      break;
+  }
+  return pairwise(terms, nb);
+}
+
+int orc_vec_dot(uint32_t type, int64_t n, const void *w_row, const void *act, float *out) {
+  if (!act_type_of(type) || n % (type == QT_Q8_0 ? 32 : QK) || n <= 0) return -1;
+  grid_init();
+  float *terms = (float *)malloc(sizeof(float) * (size_t)(n / 32));
+  *out = dot_row(type, n, (const uint8_t *)w_row, (const uint8_t *)act, terms);
+  free(terms);
+  return 0;
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * CpuExperts (core/cpu/experts.cpp). */
+
+/* silu(g) * u with the optional clamp (experts.cpp:21-27): g / (1 + e^-g) * u, libm's expf. */
+static inline float swiglu_one(float g, float u, float limit) {
+  if (limit > 0.0f) {
+    g = fminf(g, limit);
+    u = u < -limit ? -limit : (u > limit ? limit : u);
+  }
+  return g / (1.0f + expf(-g)) * u;
+}
+
+static int shape_ok(const orc_shape *s) {
+  const uint32_t ga = act_type_of(s->gate_type), da = act_type_of(s->down_type);
+  if (!ga || !da || !s->n_embd || !s->n_ff) return 0;
+  if (s->n_embd % (ga == QT_Q8_0 ? 32 : QK) || s->n_ff % (da == QT_Q8_0 ? 32 : QK)) return 0;
+  return 1;
+}
+
+static void quantize_act_row(uint32_t act, const float *x, uint8_t *y, int64_t n) {
+  if (act == QT_Q8_0)
+    quantize_q8_0(x, y, n);
+  else
+    quantize_q8_K(x, y, n);
+}
+
+int orc_compute_many(const orc_shape *s, const orc_job *jobs, uint32_t njobs, uint32_t ntok, const float *x,
+                     uint64_t x_stride, float *y, uint64_t y_stride, int nthreads) {
+  const uint32_t E = s->n_embd, F = s->n_ff;
+  if (njobs == 0) {
+    for (uint32_t t = 0; t < ntok; t++) memset(y + t * y_stride, 0, sizeof(float) * E);
+    return 0;
+  }
+  if (!shape_ok(s)) return -1;
+  for (uint32_t j = 0; j < njobs; j++)
+    if (jobs[j].tok >= ntok || !jobs[j].gate || !jobs[j].up || !jobs[j].down) return -1;
+  grid_init();
+  if (nthreads <= 0) nthreads = 1;
+  const uint32_t ga = act_type_of(s->gate_type), da = act_type_of(s->down_type);
+  const uint64_t xq_bytes = act_bytes(ga, E), hq_bytes = act_bytes(da, F);
+  const uint64_t grow = row_bytes(s->gate_type, E), drow = row_bytes(s->down_type, F);
+  const uint32_t nterm = (E > F ? E : F) / 32;
+  uint8_t *xq = (uint8_t *)malloc(ntok * xq_bytes);
+  uint8_t *hq = (uint8_t *)malloc(njobs * hq_bytes);
+  float *h = (float *)malloc(sizeof(float) * njobs * F);
+  float *out = (float *)malloc(sizeof(float) * njobs * E);
+  uint32_t *dj = (uint32_t *)malloc(sizeof(uint32_t) * njobs); /* jobs ordered by distinct expert */
+  uint32_t *dstart = (uint32_t *)malloc(sizeof(uint32_t) * (njobs + 1));
+  if (!xq || !hq || !h || !out || !dj || !dstart) {
+    free(xq), free(hq), free(h), free(out), free(dj), free(dstart);
+    return -1;
+  }
+  for (uint32_t t = 0; t < ntok; t++) quantize_act_row(ga, x + t * x_stride, xq + t * xq_bytes, E);
+  /* The distinct experts by pointer equality on gate (experts.cpp:170-177), each with its jobs in order, so that an
+   * expert's rows are read once for all of them. */
+  uint32_t nd = 0, nj = 0;
+  {
+    uint8_t *taken = (uint8_t *)calloc(njobs, 1);
+    for (uint32_t j = 0; j < njobs; j++) {
+      if (taken[j]) continue;
+      dstart[nd++] = nj;
+      for (uint32_t i = j; i < njobs; i++)
+        if (!taken[i] && jobs[i].gate == jobs[j].gate) taken[i] = 1, dj[nj++] = i;
+    }
+    dstart[nd] = nj;
+    free(taken);
+  }
+  const int64_t tasks_gu = (int64_t)nd * F;
+#pragma omp parallel num_threads(nthreads)
+  {
+    float terms[nterm];
+#pragma omp for schedule(static)
+    for (int64_t task = 0; task < tasks_gu; task++) {
+      const uint32_t d = (uint32_t)(task / F), r = (uint32_t)(task % F);
+      for (uint32_t i = dstart[d]; i < dstart[d + 1]; i++) {
+        const orc_job *jb = &jobs[dj[i]];
+        const uint8_t *xa = xq + jb->tok * xq_bytes;
+        const float g = dot_row(s->gate_type, E, jb->gate + r * grow, xa, terms);
+        const float u = dot_row(s->gate_type, E, jb->up + r * grow, xa, terms);
+        h[(uint64_t)dj[i] * F + r] = swiglu_one(g, u, s->swiglu_limit);
+      }
+    }
+  }
+  /* h quantised whole per job: compute_many's blocks never straddle its task rows (experts.cpp:194-238), so this is
+   * the same bytes. */
+  for (uint32_t j = 0; j < njobs; j++) quantize_act_row(da, h + (uint64_t)j * F, hq + j * hq_bytes, F);
+  const int64_t tasks_d = (int64_t)nd * E;
+#pragma omp parallel num_threads(nthreads)
+  {
+    float terms[nterm];
+#pragma omp for schedule(static)
+    for (int64_t task = 0; task < tasks_d; task++) {
+      const uint32_t d = (uint32_t)(task / E), r = (uint32_t)(task % E);
+      for (uint32_t i = dstart[d]; i < dstart[d + 1]; i++) {
+        const uint32_t j = dj[i];
+        out[(uint64_t)j * E + r] = dot_row(s->down_type, F, jobs[j].down + r * drow, hq + j * hq_bytes, terms);
+      }
+    }
+  }
+  /* y overwritten, then each token's jobs added in the order given (experts.cpp:256-262): y += w out, the product
+   * rounded before the sum. */
+  for (uint32_t t = 0; t < ntok; t++) memset(y + t * y_stride, 0, sizeof(float) * E);
+  for (uint32_t j = 0; j < njobs; j++) {
+    float *yt = y + jobs[j].tok * y_stride;
+    const float w = jobs[j].w;
+    for (uint32_t r = 0; r < E; r++) yt[r] = yt[r] + w * out[(uint64_t)j * E + r];
+  }
+  free(xq), free(hq), free(h), free(out), free(dj), free(dstart);
+  return 0;
+}
+
+/* CpuExperts::compute (experts.cpp:109-150): one token; the same arithmetic as compute_many with every job on it. */
+int orc_compute(const orc_shape *s, const uint8_t *const *gate, const uint8_t *const *up, const uint8_t *const *down,
+                const float *w, uint32_t n, const float *x, float *y) {
+  orc_job *jobs = (orc_job *)malloc(sizeof(orc_job) * (n ? n : 1));
+  for (uint32_t i = 0; i < n; i++) {
+    jobs[i].gate = gate[i], jobs[i].up = up[i], jobs[i].down = down[i];
+    jobs[i].tok = 0, jobs[i].w = w[i];
+  }
+  const int rc = orc_compute_many(s, jobs, n, 1, x, s->n_embd, y, s->n_embd, 1);
+  free(jobs);
+  return rc;
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * The router (MODEL_LAYER.md:414-425). */
+
+/* The logits of one token: x rounded to bf16 (MODEL_LAYER.md:512), each product of two bf16 values exact in fp32,
+ * their sum taken in double and rounded once to fp32. ggml's BF16 vec_dot sums in an order of its own (unpinned);
+ * this is the exactly-rounded value it approximates. The bias, when given, is added after (not in the reference:
+ * the synthetic configs' Zipf skew). */
+static void logits_row(const uint16_t *router, const float *bias, uint32_t E, uint32_t H, const float *x,
+                       float *lg) {
+  uint16_t *xb = (uint16_t *)malloc(sizeof(uint16_t) * H);
+  for (uint32_t i = 0; i < H; i++) xb[i] = orc_fp32_to_bf16(x[i]);
+  for (uint32_t e = 0; e <= E; e++) {
+    const uint16_t *wr = router + (uint64_t)e * H;
+    double acc = 0.0;
+    for (uint32_t i = 0; i < H; i++) acc += (double)(bf16_to_fp32(wr[i]) * bf16_to_fp32(xb[i]));
+    float v = (float)acc;
+    if (bias && e < E) v = v + bias[e];
+    lg[e] = v;
+  }
+  free(xb);
+}
+
+/* Softmax, the top k, the weights for one token (route.h:33-99, layer.cl:765-804, ggml soft_max):
+ * P_e = expf(l_e - max) * (float)(1 / sum_e expf(l_e - max)), the sum in double in expert order; the k largest
+ * logits (so the k largest P), larger first, ties to the lower expert, -0 equal to +0; w_k = P_k / max(sum of the
+ * k P in rank order, 6.1035e-5). */
+static void topk_row(const float *lg, uint32_t E, uint32_t k, int32_t *ids, float *w) {
+  float mx = -INFINITY;
+  for (uint32_t e = 0; e < E; e++) mx = fmaxf(mx, lg[e]);
+  double sum = 0.0;
+  for (uint32_t e = 0; e < E; e++) sum += (double)expf(lg[e] - mx);
+  const float inv = (float)(1.0 / sum);
+  uint8_t *taken = (uint8_t *)calloc(E, 1);
+  float p[64];
+  for (uint32_t r = 0; r < k; r++) {
+    int32_t best = -1;
+    for (uint32_t e = 0; e < E; e++) {
+      if (taken[e]) continue;
+      if (best < 0 || lg[e] > lg[best]) best = (int32_t)e; /* strictly larger: an equal one keeps the lower id */
+    }
+    taken[best] = 1;
+    ids[r] = best;
+    p[r] = expf(lg[best] - mx) * inv;
+  }
+  float tot = 0.0f;
+  for (uint32_t r = 0; r < k; r++) tot = tot + p[r];
+  const float den = fmaxf(tot, 6.1035e-5f);
+  for (uint32_t r = 0; r < k; r++) w[r] = p[r] / den;
+  free(taken);
+}
+
+int orc_route(const uint16_t *router, const float *bias, uint32_t n_expert, uint32_t n_embd, uint32_t k,
+              const float *x, uint32_t ntok, uint64_t x_stride, float *logits, int32_t *ids, float *w) {
+  if (!router || !n_expert || !n_embd || k == 0 || k > n_expert || k > 64) return -1;
+  float *lg = (float *)malloc(sizeof(float) * (n_expert + 1));
+  for (uint32_t t = 0; t < ntok; t++) {
+    logits_row(router, bias, n_expert, n_embd, x + t * x_stride, lg);
+    if (logits) memcpy(logits + (uint64_t)t * (n_expert + 1), lg, sizeof(float) * (n_expert + 1));
+    topk_row(lg, n_expert, k, ids + (uint64_t)t * k, w + (uint64_t)t * k);
+  }
+  free(lg);
+  return 0;
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * The block (MODEL_LAYER.md section 4): y = sum_k w_k y_k (rank order, as compute_many sums its jobs) + gs s, the
+ * product gs s rounded before the sum, gs = 1 / (1 + expf(-l_E)). */
+int orc_moe_forward(const orc_layer *L, const float *x, uint32_t ntok, uint64_t x_stride, float *y, uint64_t y_stride,
+                    int32_t *ids_out, float *w_out, int nthreads) {
+  const uint32_t E = L->n_expert, H = L->n_embd, k = L->n_used;
+  if (ntok == 0) return 0;
+  float *lg = (float *)malloc(sizeof(float) * ntok * (E + 1));
+  int32_t *ids = (int32_t *)malloc(sizeof(int32_t) * ntok * k);
+  float *w = (float *)malloc(sizeof(float) * ntok * k);
+  orc_job *jobs = (orc_job *)malloc(sizeof(orc_job) * ntok * k);
+  float *s = (float *)malloc(sizeof(float) * ntok * H);
+  int rc = orc_route(L->router, L->bias, E, H, k, x, ntok, x_stride, lg, ids, w);
+  if (rc) goto done;
+  for (uint32_t t = 0; t < ntok; t++)
+    for (uint32_t r = 0; r < k; r++) {
+      orc_job *j = &jobs[t * k + r];
+      const int32_t e = ids[t * k + r];
+      j->gate = L->gate[e], j->up = L->up[e], j->down = L->down[e];
+      j->tok = t, j->w = w[t * k + r];
+    }
+  orc_shape sh = {L->gate_type, L->down_type, H, L->n_ff, L->swiglu_limit};
+  rc = orc_compute_many(&sh, jobs, ntok * k, ntok, x, x_stride, y, y_stride, nthreads);
+  if (rc || !L->sh_gate) goto done;
+  for (uint32_t t = 0; t < ntok; t++) {
+    jobs[t].gate = L->sh_gate, jobs[t].up = L->sh_up, jobs[t].down = L->sh_down;
+    jobs[t].tok = t, jobs[t].w = 1.0f;
+  }
+  orc_shape ss = {L->sh_gate_type, L->sh_down_type, H, L->n_ff, L->swiglu_limit};
+  rc = orc_compute_many(&ss, jobs, ntok, ntok, x, x_stride, s, H, nthreads);
+  if (rc) goto done;
+  for (uint32_t t = 0; t < ntok; t++) {
+    const float gs = 1.0f / (1.0f + expf(-lg[(uint64_t)t * (E + 1) + E]));
+    float *yt = y + t * y_stride;
+    for (uint32_t i = 0; i < H; i++) yt[i] = yt[i] + gs * s[(uint64_t)t * H + i];
+  }
+done:
+  if (!rc && ids_out) memcpy(ids_out, ids, sizeof(int32_t) * ntok * k);
+  if (!rc && w_out) memcpy(w_out, w, sizeof(float) * ntok * k);
+  free(lg), free(ids), free(w), free(jobs), free(s);
+  return rc;
+}

@@ -1,0 +1,96 @@
+/* TEST INFRASTRUCTURE - the CPU oracle of the MoE block. Not product code: only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg load it, as the checker; the product (c0ven_amd/) never links or calls it.
+ *
+ * A plain-C restatement of the reference's CPU expert path and of the block around it:
+ *   - the weight decoders (ggml's dequantize_row_q8_0 / _q4_K / _iq3_s, as docs/spec/QUANT_FORMATS.md:176-212,
+ *     :373-400, :447-466 state them);
+ *   - the activation quantisers the CPU path converts x and h with (q8_0, QUANT_FORMATS.md:463-465; q8_K,
+ *     :528-535), chosen per weight type as core/cpu/experts.cpp:114-123 does (ggml's vec_dot_type);
+ *   - the integer block dot products (vec_dot) of each weight type against its activation type;
+ *   - CpuExperts::compute / compute_many (core/cpu/experts.cpp:109-150, :152-284): h = silu(g) * u with the optional
+ *     clamp (:21-27), h quantised to the down's activation type, y overwritten with the jobs summed in job order;
+ *   - the router (docs/spec/MODEL_LAYER.md:414-425): bf16 logits, softmax with the max subtracted and the sum in
+ *     double, the top k with ties to the lower expert (kernels/models/qwen4exp/route.h:33-38), weights renormalised
+ *     with max(sum, 6.1035e-5) (layer.cl:781-804); the shared expert and its sigmoid gate (MODEL_LAYER.md:444-449);
+ *     the combine y = sum_k w_k y_k (rank order) + gs * s (layer.cl:869-884, llama-graph.cpp:2334-2343).
+ *
+ * Pinned by tests/test_oracle.py: the IQ3_S grid against the sha256 in QUANT_FORMATS.md:546, every decoder against
+ * its closed form on hand-made blocks, the dot products against float dots of the decoded blocks and against brute
+ * force, compute against compute_many, the router against brute-force sorting, and the block against a dense fp64
+ * SwiGLU FFN where k = E. What only ggml itself could pin (its SIMD float summation order, see ORACLE ORDER below,
+ * and its bf16 dot order) is stated as unpinned there. */
+#ifndef C0VEN_ORACLE_H
+#define C0VEN_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ORACLE ORDER. The integer part of every block dot product is exact, so only the fp32 steps fix the bits. ggml's
+ * SIMD kernels sum them in an architecture-dependent order that no source in the reference restates; the oracle uses
+ * one canonical order, stated per type in oracle.c, and the GPU kernels reproduce it:
+ *   - one fp32 term per block (Q8_0: 32 values) or super-block (Q4_K, IQ3_S: 256 values);
+ *   - the terms of a row summed as a pairwise tree: sum(a[0..n)) = sum(a[0..m)) + sum(a[m..n)), m the largest power
+ *     of two below n (n = 1: a[0]). */
+
+typedef struct {
+  uint32_t gate_type, down_type; /* QT_* of gate and up (always one type), and of down */
+  uint32_t n_embd;               /* K of gate and up, rows of down */
+  uint32_t n_ff;                 /* rows of gate and up, K of down */
+  float swiglu_limit;            /* > 0: gate = min(gate, L), up = clamp(up, -L, L) before the SiLU */
+} orc_shape;
+
+typedef struct {
+  const uint8_t *gate, *up, *down; /* the expert's three matrices in the file's layout (row-major blocks) */
+  uint32_t tok;
+  float w;
+} orc_job;
+
+typedef struct {
+  uint32_t n_embd, n_ff, n_expert, n_used;
+  uint32_t gate_type, down_type;       /* routed experts */
+  uint32_t sh_gate_type, sh_down_type; /* the shared expert */
+  float swiglu_limit;
+  const uint16_t *router;              /* (n_expert + 1) x n_embd bf16: the router rows, then the shared gate */
+  const float *bias;                   /* n_expert logit biases, or null */
+  const uint8_t *const *gate, *const *up, *const *down; /* n_expert pointers each, file layout */
+  const uint8_t *sh_gate, *sh_up, *sh_down;             /* null: no shared expert */
+} orc_layer;
+
+/* Scalars. */
+uint16_t orc_fp32_to_fp16(float f);
+float orc_fp16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_bf16(float f);
+void orc_expf(const float *x, float *y, int64_t n); /* libm's expf, element by element */
+
+/* The IQ3_S codebook, 512 x u32. */
+void orc_iq3s_grid(uint32_t *out);
+
+/* Returns 0, or -1 for a type it does not know or an n that is no whole number of blocks. */
+int orc_dequantize_row(uint32_t type, const void *src, float *dst, int64_t n);
+int orc_quantize_act(uint32_t act_type, const float *src, void *dst, int64_t n); /* QT_Q8_0 or QT_Q8_K */
+int orc_vec_dot(uint32_t type, int64_t n, const void *w_row, const void *act, float *out);
+
+/* CpuExperts::compute_many: y (ntok rows) overwritten; nthreads <= 0 uses one. Returns 0 or -1. */
+int orc_compute_many(const orc_shape *s, const orc_job *jobs, uint32_t njobs, uint32_t ntok, const float *x,
+                     uint64_t x_stride, float *y, uint64_t y_stride, int nthreads);
+/* CpuExperts::compute: one token, experts in order with weights w. */
+int orc_compute(const orc_shape *s, const uint8_t *const *gate, const uint8_t *const *up, const uint8_t *const *down,
+                const float *w, uint32_t n, const float *x, float *y);
+
+/* The router for ntok rows of x: logits (ntok x (n_expert + 1), the last the shared gate's pre-sigmoid value, may be
+ * null), ids and w (ntok x k). */
+int orc_route(const uint16_t *router, const float *bias, uint32_t n_expert, uint32_t n_embd, uint32_t k,
+              const float *x, uint32_t ntok, uint64_t x_stride, float *logits, int32_t *ids, float *w);
+
+/* The whole block. ids and w (ntok x n_used) may be null. */
+int orc_moe_forward(const orc_layer *L, const float *x, uint32_t ntok, uint64_t x_stride, float *y, uint64_t y_stride,
+                    int32_t *ids, float *w, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,236 @@
+"""Shared test helpers: the CPU oracle's bindings (oracle/liboracle.so, the checker), synthetic layers drawn with the
+library's seeded generator, and the parity metrics.
+
+The oracle is test infrastructure: it is loaded here, by the tests, smoke() and bench.py's cpu_baseline, and by
+nothing in c0ven_amd/.
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import c0ven_amd as moe  # noqa: E402
+
+ORACLE_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
+_P = C.c_void_p
+
+
+def _load_oracle():
+    if not os.path.exists(ORACLE_PATH):
+        raise ImportError("oracle/liboracle.so is not built; run __graft_entry__.build()")
+    o = C.CDLL(ORACLE_PATH)
+    sig = {
+        "orc_fp32_to_fp16": (C.c_uint16, [C.c_float]),
+        "orc_fp16_to_fp32": (C.c_float, [C.c_uint16]),
+        "orc_fp32_to_bf16": (C.c_uint16, [C.c_float]),
+        "orc_expf": (None, [_P, _P, C.c_int64]),
+        "orc_iq3s_grid": (None, [_P]),
+        "orc_dequantize_row": (C.c_int, [C.c_uint32, _P, _P, C.c_int64]),
+        "orc_quantize_act": (C.c_int, [C.c_uint32, _P, _P, C.c_int64]),
+        "orc_vec_dot": (C.c_int, [C.c_uint32, C.c_int64, _P, _P, C.POINTER(C.c_float)]),
+        "orc_compute_many": (C.c_int, [_P, _P, C.c_uint32, C.c_uint32, _P, C.c_uint64, _P, C.c_uint64, C.c_int]),
+        "orc_compute": (C.c_int, [_P, _P, _P, _P, _P, C.c_uint32, _P, _P]),
+        "orc_route": (C.c_int, [_P, _P, C.c_uint32, C.c_uint32, C.c_uint32, _P, C.c_uint32, C.c_uint64, _P, _P, _P]),
+        "orc_moe_forward": (C.c_int, [_P, _P, C.c_uint32, C.c_uint64, _P, C.c_uint64, _P, _P, C.c_int]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(o, name)
+        f.restype, f.argtypes = res, args
+    return o
+
+
+oracle = _load_oracle()
+
+
+class OrcShape(C.Structure):
+    _fields_ = [("gate_type", C.c_uint32), ("down_type", C.c_uint32), ("n_embd", C.c_uint32),
+                ("n_ff", C.c_uint32), ("swiglu_limit", C.c_float)]
+
+
+class OrcJob(C.Structure):
+    _fields_ = [("gate", _P), ("up", _P), ("down", _P), ("tok", C.c_uint32), ("w", C.c_float)]
+
+
+class OrcLayer(C.Structure):
+    _fields_ = [("n_embd", C.c_uint32), ("n_ff", C.c_uint32), ("n_expert", C.c_uint32), ("n_used", C.c_uint32),
+                ("gate_type", C.c_uint32), ("down_type", C.c_uint32), ("sh_gate_type", C.c_uint32),
+                ("sh_down_type", C.c_uint32), ("swiglu_limit", C.c_float), ("router", _P), ("bias", _P),
+                ("gate", C.POINTER(_P)), ("up", C.POINTER(_P)), ("down", C.POINTER(_P)),
+                ("sh_gate", _P), ("sh_up", _P), ("sh_down", _P)]
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data_as(_P)
+
+
+def act_bytes(act_type, n):
+    return n // 32 * 34 if act_type == moe.QT_Q8_0 else n // 256 * 292
+
+
+def vec_dot_type(t):
+    return moe.QT_Q8_0 if t == moe.QT_Q8_0 else moe.QT_Q8_K
+
+
+def orc_dequant(qtype, blocks, n):
+    out = np.empty(n, dtype=np.float32)
+    assert oracle.orc_dequantize_row(qtype, ptr(blocks), ptr(out), n) == 0
+    return out
+
+
+def orc_quant_act(act_type, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(act_bytes(act_type, x.size), dtype=np.uint8)
+    assert oracle.orc_quantize_act(act_type, ptr(x), ptr(out), x.size) == 0
+    return out
+
+
+def orc_vec_dot(qtype, n, w, a):
+    v = C.c_float()
+    assert oracle.orc_vec_dot(qtype, n, ptr(w), ptr(a), C.byref(v)) == 0
+    return v.value
+
+
+def orc_expf(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    oracle.orc_expf(ptr(x), ptr(y), x.size)
+    return y
+
+
+def orc_grid():
+    g = np.empty(512, dtype=np.uint32)
+    oracle.orc_iq3s_grid(ptr(g))
+    return g
+
+
+def to_bf16(x):
+    """fp32 -> bf16 bits, round to nearest even (NaN-free input)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(b):
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+class Layer:
+    """A synthetic MoE layer drawn from (seed, layer): experts N(0, sigma) quantised by the library's quantisers,
+    router and shared gate N(0, sigma) as bf16, optional Zipf logit bias. Expert e's matrices are streams
+    layer * 2^20 + 4 e + {0, 1, 2}; the shared expert is e = n_expert."""
+
+    def __init__(self, H, F, E, K, gate_type, down_type, sh_gate_type=None, sh_down_type=None, has_shared=True,
+                 seed=1234, layer=0, sigma=0.02, zipf=None, swiglu_limit=0.0, experts=None, nthreads=0):
+        self.H, self.F, self.E, self.K = H, F, E, K
+        self.gate_type, self.down_type = gate_type, down_type
+        self.sh_gate_type = gate_type if sh_gate_type is None else sh_gate_type
+        self.sh_down_type = down_type if sh_down_type is None else sh_down_type
+        self.has_shared, self.seed, self.layer, self.swiglu_limit = has_shared, seed, layer, swiglu_limit
+        base = layer << 20
+        r = moe.synth_normal(seed, base + 4 * (E + 1) + 3, (E + 1) * H, sigma, nthreads)
+        self.router = to_bf16(r).reshape(E + 1, H)
+        self.bias = None if zipf is None else moe.zipf_bias(seed * 7919 + layer, E, zipf)
+        self.experts = {}
+        wanted = range(E) if experts is None else experts
+        for e in wanted:
+            self.experts[e] = self._expert(e, gate_type, down_type, sigma, nthreads)
+        self.shared = self._expert(E, self.sh_gate_type, self.sh_down_type, sigma, nthreads) if has_shared else None
+
+    def _expert(self, e, gt, dt, sigma, nthreads):
+        s = (self.layer << 20) + 4 * e
+        H, F = self.H, self.F
+        return (moe.synth_matrix(self.seed, s, gt, F, H, sigma, nthreads),
+                moe.synth_matrix(self.seed, s + 1, gt, F, H, sigma, nthreads),
+                moe.synth_matrix(self.seed, s + 2, dt, H, F, sigma, nthreads))
+
+    def upload(self, blk, layer=0):
+        blk.load_router(layer, self.router, self.bias)
+        for e, (g, u, d) in self.experts.items():
+            blk.load_expert(layer, e, g, u, d)
+        if self.shared is not None:
+            blk.load_expert(layer, self.E, *self.shared)
+
+    def block(self, n_layer=1, max_tokens=16, device=0):
+        return moe.MoeBlock(self.H, self.F, self.E, self.K, self.gate_type, self.down_type, self.has_shared,
+                            self.sh_gate_type, self.sh_down_type, n_layer=n_layer, max_tokens=max_tokens,
+                            swiglu_limit=self.swiglu_limit, device=device)
+
+    def oracle_forward(self, x, nthreads=8):
+        """The whole block on the CPU oracle: y, ids, w."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T = x.shape[0]
+        E = self.E
+        if len(self.experts) != E:  # route first, then make sure every routed expert exists
+            _, ids, _ = self.oracle_route(x)
+            missing = sorted(set(int(i) for i in ids.ravel()) - set(self.experts))
+            for e in missing:
+                self.experts[e] = self._expert(e, self.gate_type, self.down_type, 0.02, 0)
+        zero = np.zeros(1, dtype=np.uint8)
+        arr = (_P * E)()
+        gp, up, dp = (_P * E)(), (_P * E)(), (_P * E)()
+        for e in range(E):
+            g, u, d = self.experts.get(e, (zero, zero, zero))
+            gp[e], up[e], dp[e] = g.ctypes.data, u.ctypes.data, d.ctypes.data
+        del arr
+        L = OrcLayer(self.H, self.F, E, self.K, self.gate_type, self.down_type, self.sh_gate_type, self.sh_down_type,
+                     self.swiglu_limit, ptr(self.router), ptr(self.bias), gp, up, dp,
+                     *(ptr(m) for m in (self.shared if self.shared is not None else (None, None, None))))
+        y = np.empty((T, self.H), dtype=np.float32)
+        ids = np.empty((T, self.K), dtype=np.int32)
+        w = np.empty((T, self.K), dtype=np.float32)
+        assert oracle.orc_moe_forward(C.byref(L), ptr(x), T, self.H, ptr(y), self.H, ptr(ids), ptr(w), nthreads) == 0
+        return y, ids, w
+
+    def oracle_route(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T = x.shape[0]
+        lg = np.empty((T, self.E + 1), dtype=np.float32)
+        ids = np.empty((T, self.K), dtype=np.int32)
+        w = np.empty((T, self.K), dtype=np.float32)
+        assert oracle.orc_route(ptr(self.router), ptr(self.bias), self.E, self.H, self.K, ptr(x), T, self.H,
+                                ptr(lg), ptr(ids), ptr(w)) == 0
+        return lg, ids, w
+
+
+def orc_compute_many(gate_type, down_type, H, F, jobs, x, swiglu_limit=0.0, nthreads=8):
+    """jobs: list of ((gate, up, down), tok, w)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    arr = (OrcJob * max(1, len(jobs)))(*[OrcJob(ptr(m[0]), ptr(m[1]), ptr(m[2]), t, w) for m, t, w in jobs])
+    s = OrcShape(gate_type, down_type, H, F, swiglu_limit)
+    y = np.full((T, H), np.nan, dtype=np.float32)
+    assert oracle.orc_compute_many(C.byref(s), arr, len(jobs), T, ptr(x), H, ptr(y), H, nthreads) == 0
+    return y
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def max_abs(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+def tokens(seed, T, H, stream=999):
+    return moe.synth_normal(seed, stream, T * H, 1.0).reshape(T, H)
+
+
+def smoke_check():
+    """One small forward on cuda:0 against the oracle (used by __graft_entry__.smoke)."""
+    L = Layer(512, 256, 32, 4, moe.QT_Q4_K, moe.QT_Q8_0, seed=7)
+    blk = L.block()
+    L.upload(blk)
+    x = tokens(7, 2, 512)
+    y, ids, w = blk.forward(0, x)
+    yo, io, wo = L.oracle_forward(x)
+    assert np.array_equal(ids, io), (ids, io)
+    assert max_abs(y, yo) <= 1e-3 and rel_l2(y, yo) <= 1e-4, (max_abs(y, yo), rel_l2(y, yo))
+    blk.close()
+    print("smoke ok: max_abs %.3g rel_l2 %.3g, ids equal, y bit-exact: %s" % (max_abs(y, yo), rel_l2(y, yo),
+                                                                             np.array_equal(y, yo)))

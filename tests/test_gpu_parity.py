@@ -1,0 +1,168 @@
+"""The HIP path against the CPU oracle, through the C ABI (libc0ven_moe.so), on the GPU.
+
+The bar (north_star): top-k expert ids and decoded weight blocks bit-exact; the block's output within max-abs 1e-3
+and rel-L2 1e-4. The decode path reproduces the oracle's every rounding (its ORACLE ORDER, libm's expf), so these
+tests also hold its output to bit equality, and report the distance when it is not.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from tests import harness as h
+from tests.harness import moe
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(7)
+TOL_ABS, TOL_REL = 1e-3, 1e-4
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def check_block(y, ids, w, yo, io, wo, exact=True):
+    assert np.array_equal(ids, io), "top-k ids differ"
+    ma, rl = h.max_abs(y, yo), h.rel_l2(y, yo)
+    assert ma <= TOL_ABS and rl <= TOL_REL, (ma, rl)
+    if exact:
+        assert np.array_equal(w, wo), "routing weights not bit-exact: max %g" % h.max_abs(w, wo)
+        assert np.array_equal(y, yo), "y not bit-exact: max-abs %g rel-L2 %g" % (ma, rl)
+
+
+def random_blocks(qtype, nblocks):
+    nv, nb = moe.BLOCK[qtype]
+    b = rng.integers(0, 256, size=(nblocks, nb), dtype=np.uint8)
+    reach = {moe.QT_Q8_0: [(0, 128)], moe.QT_Q4_K: [(0, 63 * 15), (2, 63)], moe.QT_IQ3_S: [(0, 31 * 15)]}[qtype]
+    for k in range(nblocks):
+        for off, r in reach:
+            v = np.ldexp(1.0 + rng.integers(0, 1024) / 1024.0, int(rng.integers(0, 3)) - 5) / r
+            b[k, off:off + 2] = np.frombuffer(np.float16(v).tobytes(), np.uint8)
+    return b.ravel()
+
+
+@pytest.fixture(scope="module")
+def tiny_block():
+    blk = moe.MoeBlock(512, 256, 8, 2, moe.QT_Q8_0, moe.QT_Q8_0)
+    yield blk
+    blk.close()
+
+
+@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S])
+@pytest.mark.parametrize("rows,cols", [(128, 512), (100, 256)])
+def test_dequantize_bit_exact(tiny_block, qtype, rows, cols):
+    say("dequantize", moe.TYPE_NAMES[qtype], rows, cols)
+    for src in ("random", "quantised"):
+        if src == "random":
+            m = random_blocks(qtype, rows * cols // moe.BLOCK[qtype][0])
+        else:
+            m = moe.synth_matrix(3, 1, qtype, rows, cols)
+        got = tiny_block.dequantize(qtype, m, rows, cols)
+        want = np.stack([h.orc_dequant(qtype, m[r * moe.row_bytes(qtype, cols):(r + 1) * moe.row_bytes(qtype, cols)],
+                                       cols) for r in range(rows)])
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), src
+
+
+SMALL_TYPES = [
+    (moe.QT_Q8_0, moe.QT_Q8_0, moe.QT_Q8_0, moe.QT_Q8_0),
+    (moe.QT_Q4_K, moe.QT_Q4_K, moe.QT_Q4_K, moe.QT_Q4_K),
+    (moe.QT_IQ3_S, moe.QT_IQ3_S, moe.QT_IQ3_S, moe.QT_IQ3_S),
+    (moe.QT_IQ3_S, moe.QT_Q4_K, moe.QT_Q8_0, moe.QT_Q8_0),  # config 5's mix
+    (moe.QT_Q4_K, moe.QT_Q8_0, moe.QT_IQ3_S, moe.QT_Q4_K),
+]
+
+
+@pytest.mark.parametrize("types", SMALL_TYPES, ids=lambda t: "-".join(moe.TYPE_NAMES[x] for x in t))
+def test_forward_small(types):
+    gt, dt, sgt, sdt = types
+    L = h.Layer(512, 256, 32, 4, gt, dt, sgt, sdt, seed=11, zipf=1.1)
+    blk = L.block()
+    L.upload(blk)
+    for T in (1, 3, 8, 16):
+        say("forward_small", [moe.TYPE_NAMES[t] for t in types], "T", T)
+        x = h.tokens(100 + T, T, 512)
+        y, ids, w = blk.forward(0, x)
+        check_block(y, ids, w, *L.oracle_forward(x))
+    blk.close()
+
+
+def test_forward_no_shared_and_swiglu_limit():
+    for has_shared, limit in ((False, 0.0), (True, 0.25), (False, 0.1)):
+        say("forward no-shared/limit", has_shared, limit)
+        L = h.Layer(512, 512, 16, 3, moe.QT_Q4_K, moe.QT_IQ3_S, has_shared=has_shared, seed=5, swiglu_limit=limit,
+                    sigma=0.05)
+        blk = L.block()
+        L.upload(blk)
+        x = h.tokens(5, 5, 512)
+        y, ids, w = blk.forward(0, x)
+        check_block(y, ids, w, *L.oracle_forward(x))
+        blk.close()
+
+
+def routed_layer(types, T, seed, zipf, E=512, K=10, H=2048, F=512):
+    """A full-size layer with only the experts x routes to drawn (the others stay zero on the device, never read)."""
+    gt, dt, sgt, sdt = types
+    L = h.Layer(H, F, E, K, gt, dt, sgt, sdt, seed=seed, zipf=zipf, experts=[])
+    x = h.tokens(seed, T, H)
+    _, ids, _ = L.oracle_route(x)
+    for e in sorted(set(ids.ravel().tolist())):
+        L.experts[e] = L._expert(e, gt, dt, 0.02, 0)
+    return L, x
+
+
+CONFIGS = [
+    ("config1-Q8_0-T1", (moe.QT_Q8_0,) * 4, 1, None),
+    ("config2-Q4_K-T8-zipf", (moe.QT_Q4_K,) * 4, 8, 1.1),
+    ("config3-IQ3_S-T1", (moe.QT_IQ3_S,) * 4, 1, None),
+    ("config3-IQ3_S-T4", (moe.QT_IQ3_S,) * 4, 4, None),
+    ("config5-mixed-T1", (moe.QT_IQ3_S, moe.QT_Q4_K, moe.QT_Q8_0, moe.QT_Q8_0), 1, 1.1),
+    ("config2-Q4_K-T16-zipf", (moe.QT_Q4_K,) * 4, 16, 1.1),
+]
+
+
+@pytest.mark.parametrize("name,types,T,zipf", CONFIGS, ids=[c[0] for c in CONFIGS])
+def test_forward_full_size(name, types, T, zipf):
+    say("full size", name)
+    L, x = routed_layer(types, T, 17, zipf)
+    blk = L.block()
+    L.upload(blk)
+    y, ids, w = blk.forward(0, x)
+    check_block(y, ids, w, *L.oracle_forward(x))
+    y2, _, _ = blk.forward(0, x)  # deterministic: the counters reset themselves
+    assert np.array_equal(y, y2)
+    blk.close()
+
+
+def test_forward_experts_is_compute_many():
+    say("forward_experts")
+    H, F, E = 512, 256, 6
+    for gt, dt in ((moe.QT_Q4_K, moe.QT_Q8_0), (moe.QT_IQ3_S, moe.QT_IQ3_S)):
+        L = h.Layer(H, F, E, 2, gt, dt, seed=21)
+        blk = L.block()
+        L.upload(blk)
+        x = h.tokens(21, 4, H)
+        jobs = [(0, 0, 0.5), (1, 0, 0.25), (1, 1, 0.75), (5, 1, 0.125), (1, 2, 1.0), (E, 2, 0.5), (3, 0, -0.5)]
+        y = blk.forward_experts([(0, e, t, w) for e, t, w in jobs], x)
+        mats = lambda e: L.shared if e == E else L.experts[e]
+        yo = h.orc_compute_many(gt, dt, H, F, [(mats(e), t, w) for e, t, w in jobs if e != E], x)
+        # the shared expert's job has the shared types; compute_many takes one shape, so sum it in separately
+        ys = h.orc_compute_many(L.sh_gate_type, L.sh_down_type, H, F, [(mats(E), 2, 0.5)], x)
+        yo[2] = yo[2] + ys[2]  # token 2: its routed job first, then the shared one, as the job order gives
+        assert not y[3].any()  # a token without jobs is zero
+        assert h.max_abs(y, yo) <= TOL_ABS and h.rel_l2(y, yo) <= TOL_REL
+        assert np.array_equal(y, yo)
+        blk.close()
+
+
+def test_bad_arguments_do_not_crash(tiny_block):
+    say("bad arguments")
+    x = np.zeros((17, 512), np.float32)
+    with pytest.raises(moe.MoeError) as e:
+        tiny_block.forward(0, x)
+    assert e.value.status == 2
+    with pytest.raises(moe.MoeError) as e:
+        tiny_block.forward(3, x[:1])
+    assert e.value.status == 2
+    with pytest.raises(moe.MoeError):
+        moe.MoeBlock(500, 256, 8, 2, moe.QT_Q8_0, moe.QT_Q8_0)
