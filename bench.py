@@ -1,0 +1,185 @@
+"""Benchmark of the MoE block on one MI355X (BASELINE.json's metric on its configs).
+
+A step is one forward of the block (router, experts, shared expert, combine) over one batch of synthetic tokens,
+inputs resident in HBM. The default workload is BASELINE.json configs[1] (config 2): the speculative-verify batch of
+8 tokens, Q4_K experts, hidden 2048, 512 experts, top-10 + shared, intermediate 512, Zipf(1.1) logit bias.
+
+Cache defeat: the MI355X's 256 MB Infinity Cache would hold one layer's touched weights, so the block is resident
+as several layers (independent routers and biases, so each step routes differently) whose touched bytes sum past
+512 MB, and step i runs layer i mod n_layers.
+
+Prints one JSON line. --config picks another of BASELINE's decode configs (1, 2, 3, 3b).
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+CONFIGS = {
+    "1": dict(name="config1: decode T=1, Q8_0", types=(8, 8, 8, 8), T=1, zipf=None),
+    "2": dict(name="config2: verify T=8, Q4_K, Zipf(1.1)", types=(12, 12, 12, 12), T=8, zipf=1.1),
+    "3": dict(name="config3: decode T=1, IQ3_S", types=(21, 21, 21, 21), T=1, zipf=None),
+    "3b": dict(name="config3: decode T=4, IQ3_S", types=(21, 21, 21, 21), T=4, zipf=None),
+}
+H, F, E, K = 2048, 512, 512, 10
+HBM_PEAK_GBS = 8000.0
+
+
+class Hip:
+    """The few HIP runtime calls the bench needs for its own device buffers."""
+
+    def __init__(self):
+        self.rt = C.CDLL("libamdhip64.so")
+        self.rt.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        self.rt.hipFree.argtypes = [C.c_void_p]
+        self.rt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        self.rt.hipDeviceSynchronize.argtypes = []
+
+    def malloc(self, n):
+        p = C.c_void_p()
+        assert self.rt.hipMalloc(C.byref(p), n) == 0, "hipMalloc"
+        return p
+
+    def h2d(self, dst, a):
+        assert self.rt.hipMemcpy(dst, a.ctypes.data_as(C.c_void_p), a.nbytes, 1) == 0
+
+    def d2h(self, a, src):
+        assert self.rt.hipMemcpy(a.ctypes.data_as(C.c_void_p), src, a.nbytes, 2) == 0
+
+    def sync(self):
+        assert self.rt.hipDeviceSynchronize() == 0
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--config", default="2", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the MoE block on one MI355X); --gpus %d is not run"
+              % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import c0ven_amd as moe
+    from tests import harness as h
+
+    cfg = CONFIGS[args.config]
+    gt, dt, sgt, sdt = cfg["types"]
+    T = cfg["T"]
+    hip = Hip()
+    t_setup = time.time()
+    # Layer 0's weights, drawn once; the other layers hold copies of its experts (other addresses, so no cache reuse)
+    # with routers and biases of their own.
+    L0 = h.Layer(H, F, E, K, gt, dt, sgt, sdt, seed=2026, layer=0, zipf=cfg["zipf"])
+    ex_bytes = 2 * moe.row_bytes(gt, H) * F + moe.row_bytes(dt, F) * H
+    sh_bytes = 2 * moe.row_bytes(sgt, H) * F + moe.row_bytes(sdt, F) * H
+    per_layer_touched = (min(E, T * K) * 0.6 + 1) * ex_bytes
+    n_layer = int(min(64, max(8, np.ceil(640e6 / per_layer_touched))))
+    blk = moe.MoeBlock(H, F, E, K, gt, dt, True, sgt, sdt, n_layer=n_layer, max_tokens=16)
+    L0.upload(blk, 0)
+    routers = [L0]
+    for l in range(1, n_layer):
+        Ll = h.Layer(H, F, E, K, gt, dt, sgt, sdt, seed=2026, layer=l, zipf=cfg["zipf"], experts=[],
+                     has_shared=False)
+        blk.load_router(l, Ll.router, Ll.bias)
+        blk.copy_experts(0, l)
+        routers.append(Ll)
+    x = h.tokens(2026, T, H)
+    xd, yd, idsd = hip.malloc(x.nbytes), hip.malloc(x.nbytes), hip.malloc(T * K * 4)
+    hip.h2d(xd, x)
+    # Routing per layer (outside the timed region): distinct experts, for the algorithmic bytes.
+    distinct = []
+    ids = np.empty((T, K), np.int32)
+    for l in range(n_layer):
+        blk.forward_async(l, xd, T, yd, idsd)
+        hip.sync()
+        hip.d2h(ids, idsd)
+        distinct.append(len(set(ids.ravel().tolist())))
+    setup_s = time.time() - t_setup
+
+    for i in range(args.warmup):
+        blk.forward_async(i % n_layer, xd, T, yd)
+    hip.sync()
+    blk.set_timing(True)
+    hip.sync()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        blk.forward_async(i % n_layer, xd, T, yd)
+    hip.sync()
+    t1 = time.perf_counter()
+    ktimes, nf = blk.kernel_times()
+    blk.set_timing(False)
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    tok_s = T * args.steps / (t1 - t0)
+
+    # Algorithmic bytes: the weights of every expert touched, the shared one, the router, once each.
+    nd = np.array([distinct[i % n_layer] for i in range(args.steps)], dtype=np.float64)
+    router_bytes = (E + 1) * H * 2
+    gu_bytes = (nd.mean() * 2 * moe.row_bytes(gt, H) * F + 2 * moe.row_bytes(sgt, H) * F)
+    dn_bytes = (nd.mean() * moe.row_bytes(dt, F) * H + moe.row_bytes(sdt, F) * H)
+    block_bytes = nd.mean() * ex_bytes + sh_bytes + router_bytes
+    k_gu = ktimes.get("moe_gate_up", float("nan"))
+    gu_gbs = gu_bytes / (k_gu * 1e-3) / 1e9
+    dn_gbs = dn_bytes / (ktimes.get("moe_down", float("nan")) * 1e-3) / 1e9
+    block_gbs = block_bytes / (ms_step * 1e-3) / 1e9
+
+    # Parity of this workload (layer 0) against the oracle, and the CPU baseline: the oracle timed on this host.
+    y = np.empty_like(x)
+    blk.forward_async(0, xd, T, yd, idsd)
+    hip.sync()
+    hip.d2h(y, yd)
+    hip.d2h(ids, idsd)
+    yo, io, wo = L0.oracle_forward(x, nthreads=16)
+    parity = dict(ids_equal=bool(np.array_equal(ids, io)), y_bit_exact=bool(np.array_equal(y, yo)),
+                  max_abs=h.max_abs(y, yo), rel_l2=h.rel_l2(y, yo))
+    cpu = None
+    if not args.no_cpu:
+        cores = min(16, os.cpu_count() or 1)
+        reps, tc0 = 0, time.perf_counter()
+        while True:
+            L0.oracle_forward(x, nthreads=cores)
+            reps += 1
+            if time.perf_counter() - tc0 >= args.cpu_seconds and reps >= 3:
+                break
+        cpu_s = (time.perf_counter() - tc0) / reps
+        cpu = {"value": round(T / cpu_s, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+               "sample": "%d forwards of layer 0 (the same %d tokens) by oracle/oracle.c with %d OpenMP threads, "
+                         "%.1f s" % (reps, T, cores, cpu_s * reps),
+               "gbs": round(block_bytes / 1e9 / cpu_s, 2)}
+
+    dominant = "moe_gate_up"
+    out = {
+        "metric": "MoE block tokens/s + achieved HBM GB/s (decode), TFLOP/s (prefill) on 1 GPU",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": cfg["name"], "n_embd": H, "n_ff": F, "n_expert": E, "n_used": K, "shared": True,
+                   "tokens": T, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]], "resident_layers": n_layer,
+                   "mean_distinct_experts": round(float(nd.mean()), 2)},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": int(gu_bytes), "avg_launch_ms": round(k_gu, 5)},
+        "block": {"achieved_gbs": round(block_gbs, 1), "frac": round(block_gbs / HBM_PEAK_GBS, 4),
+                  "algorithmic_bytes": int(block_bytes), "kernel_avg_ms": {k: round(v, 5) for k, v in ktimes.items()},
+                  "timed_forwards": nf, "down_gbs": round(dn_gbs, 1)},
+        "parity": parity,
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(out), flush=True)
+    blk.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -66,7 +66,9 @@ _SIGS = {
     "moe_sync": (_i32, [_P]),
     "moe_stream": (_P, [_P]),
     "moe_set_timing": (_i32, [_P, C.c_int]),
-    "moe_kernel_times": (_i32, [_P, C.POINTER(C.c_char_p), C.POINTER(_f32), _u32, C.POINTER(_u32)]),
+    "moe_kernel_times": (_i32, [_P, C.POINTER(C.c_char_p), C.POINTER(_f32), _u32, C.POINTER(_u32), C.POINTER(_u32)]),
+    "moe_copy_experts": (_i32, [_P, _u32, _u32]),
+    "moe_expert_bytes": (_i32, [_P, _u32, C.POINTER(_u64)]),
     "moe_device_bytes": (_u64, [_P]),
     "moe_dequantize": (_i32, [_P, _u32, _P, _u32, _u32, _P]),
     "moe_synth_normal": (None, [_u64, _u64, _f32, _P, _u64, C.c_int]),
@@ -211,11 +213,21 @@ class MoeBlock:
         self._check(lib.moe_set_timing(self.h, 1 if on else 0))
 
     def kernel_times(self):
+        """{kernel: average ms per launch} over the forwards timed since timing was set (and clears them), and the
+        number of forwards."""
         names = (C.c_char_p * 8)()
         ms = (C.c_float * 8)()
-        n = C.c_uint32()
-        self._check(lib.moe_kernel_times(self.h, names, ms, 8, C.byref(n)))
-        return {names[i].decode(): ms[i] for i in range(n.value)}
+        n, nf = C.c_uint32(), C.c_uint32()
+        self._check(lib.moe_kernel_times(self.h, names, ms, 8, C.byref(n), C.byref(nf)))
+        return {names[i].decode(): ms[i] for i in range(n.value)}, nf.value
+
+    def copy_experts(self, src_layer, dst_layer):
+        self._check(lib.moe_copy_experts(self.h, src_layer, dst_layer))
+
+    def expert_bytes(self, which):
+        v = C.c_uint64()
+        self._check(lib.moe_expert_bytes(self.h, which, C.byref(v)))
+        return v.value
 
     def device_bytes(self):
         return int(lib.moe_device_bytes(self.h))

@@ -40,15 +40,17 @@ struct DecodeParams {
   float *gs;               // T
   MoeGroup *groups;
   uint32_t *ngroups;
-  float *terms_gu;         // G x 2 x (H / 256) x MOE_GROUP_MAX x F
-  uint8_t *hact;           // (T K + T) x (F / 256) activation units of h
-  float *terms_d;          // G x (F / 256) x MOE_GROUP_MAX x H
-  float *y_asg;            // (T K + T) x H
+  float *h;                // (T K + T) x F: SwiGLU of each assignment, fp32
+  float *y_asg;            // (T K + T) x H: each assignment's expert output
   uint32_t *cnt_route;     // 1
-  uint32_t *cnt_gu;        // G x (F / 256)
-  uint32_t *cnt_d;         // G x (H / 256)
-  uint32_t *cnt_tok;       // T x (H / 256)
+  uint32_t *cnt_tok;       // T x (H / kDownRows): outputs in per (token, down row block)
 };
+
+// Work-group shapes. moe_gate_up: four waves, a lane one (row, unit) pair of gate or up, so a wave holds
+// 32 / U rows of both; moe_down: two waves, a lane one (row, unit) pair, 64 / U_down rows a wave.
+constexpr uint32_t kGateUpWG = 256, kDownWG = 128;
+constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kGateUpWG / 64) * (32 / Ug); }
+constexpr uint32_t down_rows(uint32_t Ud) { return (kDownWG / 64) * (64 / Ud); }
 
 __global__ void moe_route(DecodeParams p);
 __global__ void moe_gate_up(DecodeParams p);

@@ -1,15 +1,15 @@
 // The device layout of the expert matrices and of the quantised activations, shared by the host repacker and the
 // kernels.
 //
-// A matrix of R rows x K values is cut into tiles of 64 rows x one unit of 256 values (a super-block of Q4_K or IQ3_S,
-// eight blocks of Q8_0). The decode kernels give a wave one tile, a lane one row's unit, and sum a row's units as a
-// pairwise tree; the prefill kernels stage tiles through LDS. Tile (rt, u) is at (rt * U + u) * tile_bytes, U = K / 256.
-// Inside a tile each field is stored lane-minor: piece p of lane l at field_base + (p * 64 + l) * piece_bytes, so one
-// wave-wide load of piece p reads 64 * piece_bytes contiguous bytes. The bytes are those of the file's blocks,
-// permuted (nothing is decoded or re-rounded): the reference's runs layout (shared/quant.h:1-4,
-// core/load/runs.cpp:12-31) made wave-shaped for 64-wide wavefronts.
+// A matrix of R rows x K values is a sequence of row tiles of 64 rows. A row's K values are U = K / 256 units (a
+// super-block of Q4_K or IQ3_S, eight blocks of Q8_0). Inside a tile the 64 U (row, unit) pairs are numbered
+// idx = row * U + unit, and each field of the format is stored idx-minor: piece p of pair idx at
+// field_base + (p * 64 U + idx) * piece_bytes, field_base being the earlier fields' bytes times 64 U. The decode
+// kernels give a lane one (row, unit) pair, so a wave's load of piece p reads consecutive pairs: one contiguous run.
+// The bytes are those of the file's blocks, permuted (nothing is decoded or re-rounded): the reference's runs layout
+// (shared/quant.h:1-4, core/load/runs.cpp:12-31) shaped for 64-wide wavefronts.
 //
-//   Q8_0  (8 blocks, 272 B): qs 16 pieces x 16 B (values 16p..16p+15), then d: 1 piece x 16 B (8 f16, block order).
+//   Q8_0  (8 blocks, 272 B): qs 16 pieces x 16 B (values 16p..16p+15), then d 1 x 16 B (8 f16, block order).
 //   Q4_K  (144 B):           qs 8 x 16 B (the block's qs bytes 16p..16p+15), scales 3 x 4 B, then d|dmin 1 x 4 B.
 //   IQ3_S (110 B):           qs 4 x 16 B, signs 2 x 16 B, qh 2 x 4 B, scales 1 x 4 B, then d 1 x 2 B.
 #pragma once
@@ -27,30 +27,32 @@
 namespace c0ven {
 
 constexpr uint32_t kUnit = 256;     // values per unit
-constexpr uint32_t kTileRows = 64;  // rows per tile: one wave's lanes
+constexpr uint32_t kTileRows = 64;  // rows per tile
 
 C0VEN_HD uint32_t unit_bytes(uint32_t type) {
   return type == QT_Q8_0 ? 272u : type == QT_Q4_K ? 144u : type == QT_IQ3_S ? 110u : 0u;
 }
-C0VEN_HD uint32_t tile_bytes(uint32_t type) { return kTileRows * unit_bytes(type); }
+// A tile of 64 rows x U units.
+C0VEN_HD uint64_t tile_bytes(uint32_t type, uint32_t U) { return (uint64_t)kTileRows * U * unit_bytes(type); }
 
-// Field bases inside a tile.
-namespace q8_0t { constexpr uint32_t kQs = 0, kD = 16 * 1024; }
-namespace q4_kt { constexpr uint32_t kQs = 0, kScales = 8 * 1024, kDm = 8 * 1024 + 3 * 256; }
+// Field bases inside a tile, in units of nl = 64 U pairs.
+namespace q8_0t { constexpr uint32_t kQs = 0, kD = 16 * 16; }
+namespace q4_kt { constexpr uint32_t kQs = 0, kScales = 8 * 16, kDm = 8 * 16 + 3 * 4; }
 namespace iq3_st {
-constexpr uint32_t kQs = 0, kSigns = 4 * 1024, kQh = 6 * 1024, kScales = 6 * 1024 + 2 * 256, kD = kScales + 256;
+constexpr uint32_t kQs = 0, kSigns = 4 * 16, kQh = 6 * 16, kScales = 6 * 16 + 2 * 4, kD = 6 * 16 + 3 * 4;
 }
 
 // Bytes of an R x K matrix in the device layout (R rounded up to whole tiles).
 C0VEN_HD uint64_t matrix_bytes(uint32_t type, uint32_t rows, uint32_t k) {
   const uint64_t rt = (rows + kTileRows - 1) / kTileRows;
-  return rt * (k / kUnit) * tile_bytes(type);
+  return rt * tile_bytes(type, k / kUnit);
 }
 
-// A quantised activation unit (one token's or one assignment's 256 values), 320 B:
+// A quantised activation unit (one token's or one assignment's 256 values), 320 B in global memory:
 //   [0, 256)   the int8 codes;
 //   [256, 288) the scales as f32: q8_K's d at 256; q8_0's eight block d (their f16 values widened) at 256 + 4 b;
 //   [288, 320) q8_K only: the sums of each 32 codes as int32 (bsums[2j] + bsums[2j + 1]).
-constexpr uint32_t kActBytes = 320, kActScales = 256, kActSums = 288;
+// In LDS the kernels keep them kActLds apart, so the eight units a wave reads at once fall in distinct banks.
+constexpr uint32_t kActBytes = 320, kActScales = 256, kActSums = 288, kActLds = 336;
 
 }  // namespace c0ven

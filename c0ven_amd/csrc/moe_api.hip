@@ -56,14 +56,15 @@ struct moe_ctx {
   float *x_dev = nullptr, *y_dev = nullptr, *w_stage = nullptr;
   int32_t *ids_stage = nullptr;
   // Scratch.
-  uint8_t *act_r = nullptr, *act_s = nullptr, *hact = nullptr;
-  float *logits = nullptr, *w = nullptr, *gs = nullptr, *terms_gu = nullptr, *terms_d = nullptr, *y_asg = nullptr;
+  uint8_t *act_r = nullptr, *act_s = nullptr;
+  float *logits = nullptr, *w = nullptr, *gs = nullptr, *h = nullptr, *y_asg = nullptr;
   int32_t *ids = nullptr;
   MoeGroup *groups = nullptr;
   uint32_t *ngroups = nullptr, *counters = nullptr, *tok_need = nullptr;
-  uint32_t *cnt_route = nullptr, *cnt_gu = nullptr, *cnt_d = nullptr, *cnt_tok = nullptr;
-  bool timing = false, timed = false;
-  hipEvent_t ev[kNumKernels + 1] = {};
+  uint32_t *cnt_route = nullptr, *cnt_tok = nullptr;
+  bool timing = false;
+  std::vector<hipEvent_t> ev;  // (kNumKernels + 1) events per timed forward
+  uint32_t ev_used = 0;        // forwards recorded since the last moe_kernel_times
   std::vector<void *> allocs;
   uint64_t dev_bytes = 0;
   std::string err;
@@ -137,24 +138,36 @@ DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   p.act_r = c->act_r, p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
   p.logits = c->logits, p.ids = c->ids, p.w = c->w, p.gs = c->gs;
   p.groups = c->groups, p.ngroups = c->ngroups;
-  p.terms_gu = c->terms_gu, p.hact = c->hact, p.terms_d = c->terms_d, p.y_asg = c->y_asg;
-  p.cnt_route = c->cnt_route, p.cnt_gu = c->cnt_gu, p.cnt_d = c->cnt_d, p.cnt_tok = c->cnt_tok;
+  p.h = c->h, p.y_asg = c->y_asg;
+  p.cnt_route = c->cnt_route, p.cnt_tok = c->cnt_tok;
   return p;
 }
 
+// The events of the next timed forward (kNumKernels + 1 of them), or null when timing is off.
+hipEvent_t *timing_events(moe_ctx *c) {
+  if (!c->timing) return nullptr;
+  const size_t need = (size_t)(c->ev_used + 1) * (kNumKernels + 1);
+  while (c->ev.size() < need) {
+    hipEvent_t e;
+    check(hipEventCreate(&e), "hipEventCreate");
+    c->ev.push_back(e);
+  }
+  return &c->ev[(size_t)c->ev_used++ * (kNumKernels + 1)];
+}
+
 void launch(moe_ctx *c, const DecodeParams &p, uint32_t n_route_wg, hipStream_t s) {
-  const uint32_t G = max_groups(p.T, p.K);
-  const uint32_t g_gu = G * (p.F / kUnit) * 2 * (p.H / kUnit), g_d = G * (p.H / kUnit) * (p.F / kUnit);
-  const bool tm = c->timing && s == c->stream;
-  if (tm) check(hipEventRecord(c->ev[0], s), "hipEventRecord");
-  hipLaunchKernelGGL(moe_route, dim3(n_route_wg), dim3(256), 0, s, p);
-  if (tm) check(hipEventRecord(c->ev[1], s), "hipEventRecord");
-  hipLaunchKernelGGL(moe_gate_up, dim3(g_gu), dim3(256), 0, s, p);
-  if (tm) check(hipEventRecord(c->ev[2], s), "hipEventRecord");
-  hipLaunchKernelGGL(moe_down, dim3(g_d), dim3(256), 0, s, p);
-  if (tm) check(hipEventRecord(c->ev[3], s), "hipEventRecord");
+  const uint32_t G = max_groups(p.T, p.K), Ug = p.H / kUnit, Ud = p.F / kUnit;
+  const uint32_t g_gu = G * (p.F / gate_up_rows(Ug)), g_d = G * (p.H / down_rows(Ud));
+  const size_t lds_gu = (size_t)MOE_GROUP_MAX * Ug * kActLds, lds_d = (size_t)MOE_GROUP_MAX * Ud * kActLds;
+  hipEvent_t *ev = timing_events(c);
+  if (ev) check(hipEventRecord(ev[0], s), "hipEventRecord");
+  hipLaunchKernelGGL(moe_route, dim3(n_route_wg), dim3(512), 0, s, p);
+  if (ev) check(hipEventRecord(ev[1], s), "hipEventRecord");
+  hipLaunchKernelGGL(moe_gate_up, dim3(g_gu), dim3(kGateUpWG), lds_gu, s, p);
+  if (ev) check(hipEventRecord(ev[2], s), "hipEventRecord");
+  hipLaunchKernelGGL(moe_down, dim3(g_d), dim3(kDownWG), lds_d, s, p);
+  if (ev) check(hipEventRecord(ev[3], s), "hipEventRecord");
   check(hipGetLastError(), "kernel launch");
-  c->timed = tm;
 }
 
 void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *y, int32_t *ids, float *w,
@@ -164,7 +177,7 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
   require(c->layers[layer].router != nullptr, "the layer's router is not loaded");
   DecodeParams p = base_params(c, layer, T);
   p.x = x, p.y = y;
-  const uint32_t nr = std::max((c->cfg.n_expert + 1 + 7) / 8, T);
+  const uint32_t nr = std::max((c->cfg.n_expert + 1 + 15) / 16, T);
   launch(c, p, nr, s);
   if (ids) check(hipMemcpyAsync(ids, c->ids, sizeof(int32_t) * T * p.K, hipMemcpyDeviceToDevice, s), "copy ids");
   if (w) check(hipMemcpyAsync(w, c->w, sizeof(float) * T * p.K, hipMemcpyDeviceToDevice, s), "copy w");
@@ -197,7 +210,6 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     require(g.device >= 0 && g.device < ndev, "no such device");
     check(hipSetDevice(g.device), "hipSetDevice");
     check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
-    for (auto &e : c->ev) check(hipEventCreate(&e), "hipEventCreate");
     const uint32_t H = g.n_embd, F = g.n_ff, E = g.n_expert;
     const uint64_t gu = matrix_bytes(g.gate_type, F, H), dn = matrix_bytes(g.down_type, H, F);
     c->ex_up = gu, c->ex_down = 2 * gu, c->ex_bytes = 2 * gu + dn;
@@ -232,17 +244,13 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->groups = c->alloc<MoeGroup>(G);
     c->ngroups = c->alloc<uint32_t>(1);
     c->tok_need = c->alloc<uint32_t>(T);
-    c->terms_gu = c->alloc<float>((uint64_t)G * 2 * Ug * MOE_GROUP_MAX * F);
-    c->hact = c->alloc<uint8_t>((uint64_t)A * Ud * kActBytes);
-    c->terms_d = c->alloc<float>((uint64_t)G * Ud * MOE_GROUP_MAX * H);
+    c->h = c->alloc<float>((uint64_t)A * F);
     c->y_asg = c->alloc<float>((uint64_t)A * H);
-    const uint64_t ncnt = 1 + (uint64_t)G * (F / kUnit) + (uint64_t)G * (H / kUnit) + (uint64_t)T * (H / kUnit);
+    const uint64_t ncnt = 1 + (uint64_t)T * (H / down_rows(Ud));
     c->counters = c->alloc<uint32_t>(ncnt);
     check(hipMemset(c->counters, 0, ncnt * sizeof(uint32_t)), "hipMemset");
     c->cnt_route = c->counters;
-    c->cnt_gu = c->cnt_route + 1;
-    c->cnt_d = c->cnt_gu + (uint64_t)G * (F / kUnit);
-    c->cnt_tok = c->cnt_d + (uint64_t)G * (H / kUnit);
+    c->cnt_tok = c->cnt_route + 1;
     check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     *out = c;
     return MOE_OK;
@@ -261,8 +269,7 @@ MOE_API void moe_close(moe_ctx *c) {
   if (!c) return;
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   for (void *p : c->allocs) (void)hipFree(p);
-  for (auto &e : c->ev)
-    if (e) (void)hipEventDestroy(e);
+  for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -399,23 +406,58 @@ MOE_API moe_status moe_sync(moe_ctx *c) {
 MOE_API void *moe_stream(moe_ctx *c) { return c ? (void *)c->stream : nullptr; }
 
 MOE_API moe_status moe_set_timing(moe_ctx *c, int on) {
-  return guarded(c, [&] { c->timing = on != 0; });
+  return guarded(c, [&] {
+    c->timing = on != 0;
+    c->ev_used = 0;
+  });
 }
 
-MOE_API moe_status moe_kernel_times(moe_ctx *c, const char **names, float *ms, uint32_t cap, uint32_t *n) {
+MOE_API moe_status moe_kernel_times(moe_ctx *c, const char **names, float *avg_ms, uint32_t cap, uint32_t *n,
+                                    uint32_t *forwards) {
   return guarded(c, [&] {
     require(n != nullptr, "null n");
     *n = 0;
-    if (!c->timed) return;
-    check(hipEventSynchronize(c->ev[kNumKernels]), "hipEventSynchronize");
+    if (forwards) *forwards = c->ev_used;
+    if (!c->ev_used) return;
+    const uint32_t nf = c->ev_used;
+    check(hipEventSynchronize(c->ev[(size_t)nf * (kNumKernels + 1) - 1]), "hipEventSynchronize");
     for (int i = 0; i < kNumKernels && (uint32_t)i < cap; i++) {
-      float t = 0.0f;
-      check(hipEventElapsedTime(&t, c->ev[i], c->ev[i + 1]), "hipEventElapsedTime");
+      double sum = 0.0;
+      for (uint32_t f = 0; f < nf; f++) {
+        float t = 0.0f;
+        const hipEvent_t *e = &c->ev[(size_t)f * (kNumKernels + 1)];
+        check(hipEventElapsedTime(&t, e[i], e[i + 1]), "hipEventElapsedTime");
+        sum += t;
+      }
       if (names) names[i] = kKernelNames[i];
-      if (ms) ms[i] = t;
+      if (avg_ms) avg_ms[i] = (float)(sum / nf);
       *n = (uint32_t)i + 1;
     }
+    c->ev_used = 0;
   });
+}
+
+MOE_API moe_status moe_copy_experts(moe_ctx *c, uint32_t src_layer, uint32_t dst_layer) {
+  return guarded(c, [&] {
+    require(src_layer < c->cfg.n_layer && dst_layer < c->cfg.n_layer, "layer out of range");
+    if (src_layer == dst_layer) return;
+    const Layer &a = c->layers[src_layer], &b = c->layers[dst_layer];
+    check(hipMemcpy(b.experts, a.experts, c->ex_bytes * c->cfg.n_expert, hipMemcpyDeviceToDevice), "copy experts");
+    if (a.shared) check(hipMemcpy(b.shared, a.shared, c->sh_bytes, hipMemcpyDeviceToDevice), "copy shared");
+  });
+}
+
+MOE_API moe_status moe_expert_bytes(const moe_ctx *c, uint32_t which, uint64_t *bytes) {
+  if (!c || !bytes) return MOE_BAD_ARGUMENT;
+  const moe_config &g = c->cfg;
+  switch (which) {
+    case 0: *bytes = matrix_bytes(g.gate_type, g.n_ff, g.n_embd); break;
+    case 1: *bytes = matrix_bytes(g.down_type, g.n_embd, g.n_ff); break;
+    case 2: *bytes = g.has_shared ? matrix_bytes(g.sh_gate_type, g.n_ff, g.n_embd) : 0; break;
+    case 3: *bytes = g.has_shared ? matrix_bytes(g.sh_down_type, g.n_embd, g.n_ff) : 0; break;
+    default: return MOE_BAD_ARGUMENT;
+  }
+  return MOE_OK;
 }
 
 MOE_API uint64_t moe_device_bytes(const moe_ctx *c) { return c ? c->dev_bytes : 0; }
@@ -433,7 +475,7 @@ MOE_API moe_status moe_dequantize(moe_ctx *c, uint32_t type, const uint8_t *bloc
     check(hipMalloc(&dm, mb), "hipMalloc");
     check(hipMalloc(&dout, (uint64_t)nrt * kTileRows * cols * sizeof(float)), "hipMalloc");
     check(hipMemcpy(dm, buf.data(), mb, hipMemcpyHostToDevice), "upload");
-    hipLaunchKernelGGL(moe_dequant, dim3(nrt * (cols / kUnit)), dim3(64), 0, c->stream, dm, type, rows, cols, dout);
+    hipLaunchKernelGGL(moe_dequant, dim3(nrt), dim3(64), 0, c->stream, dm, type, rows, cols, dout);
     check(hipGetLastError(), "moe_dequant");
     check(hipStreamSynchronize(c->stream), "moe_dequant");
     check(hipMemcpy(out, dout, (uint64_t)rows * cols * sizeof(float), hipMemcpyDeviceToHost), "download");

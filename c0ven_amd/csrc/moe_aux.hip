@@ -10,26 +10,28 @@ namespace c0ven {
 
 __device__ __constant__ static const uint32_t kGridAux[512] = {C0VEN_IQ3S_GRID_VALUES};
 
-// Grid: one work-group of 64 (a wave) per tile; lane l writes row rt * 64 + l, values u * 256 .. +256. The values are
+// Grid: one work-group of 64 (a wave) per tile; lane l writes row rt * 64 + l, all its units. The values are
 // formed as ggml's dequantize_row_* forms them: Q8_0 d q; Q4_K (d sc) q - (dmin m); IQ3_S (d (1 + 2 s)) (sign grid).
 __global__ void __launch_bounds__(64) moe_dequant(const uint8_t *mat, uint32_t type, uint32_t rows, uint32_t k,
                                                   float *out) {
   __shared__ uint32_t grid[512];
   for (uint32_t i = threadIdx.x; i < 512; i += 64) grid[i] = kGridAux[i];
   __syncthreads();
-  const uint32_t U = k / kUnit, rt = blockIdx.x / U, u = blockIdx.x % U, lane = threadIdx.x;
+  const uint32_t U = k / kUnit, rt = blockIdx.x, lane = threadIdx.x, nl = kTileRows * U;
   const uint32_t row = rt * kTileRows + lane;
-  const uint8_t *tile = mat + (uint64_t)blockIdx.x * tile_bytes(type);
-  float *o = out + (uint64_t)row * k + u * kUnit;
+  const uint8_t *tile = mat + (uint64_t)rt * tile_bytes(type, U);
   const bool live = row < rows;
+  for (uint32_t u = 0; u < U; u++) {
+  const uint32_t idx = lane * U + u;
+  float *o = out + (uint64_t)row * k + u * kUnit;
   if (type == QT_Q8_0) {
     UnitQ8_0 w;
-    w.load(tile, lane);
+    w.load(tile, idx, nl);
     if (live)
       for (int i = 0; i < 256; i++) o[i] = __fmul_rn(w.d[i / 32], (float)(int8_t)(w.q[i / 4] >> (8 * (i % 4))));
   } else if (type == QT_Q4_K) {
     UnitQ4_K w;
-    w.load(tile, lane);
+    w.load(tile, idx, nl);
     if (live)
       for (int wd = 0; wd < 32; wd++)
         for (int i = 0; i < 4; i++) {
@@ -41,12 +43,13 @@ __global__ void __launch_bounds__(64) moe_dequant(const uint8_t *mat, uint32_t t
         }
   } else {
     UnitIQ3_S w;
-    w.load(tile, lane, grid);
+    w.load(tile, idx, nl, grid);
     if (live)
       for (int i = 0; i < 256; i++) {
         const float db = __fmul_rn(w.d, (float)w.ls[i / 32]);
         o[i] = __fmul_rn(db, (float)(int8_t)(w.w[i / 4] >> (8 * (i % 4))));
       }
+  }
   }
 }
 

@@ -27,24 +27,32 @@ __device__ __constant__ static const uint32_t kIq3sGridDev[512] = {C0VEN_IQ3S_GR
 
 namespace {
 
-constexpr uint32_t kWG = 256;  // threads of every decode work-group: four waves
+constexpr uint32_t kRouteWG = 512;  // threads of the router's work-groups: eight waves
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 __device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
 
-// Counts the work-group in on *cnt after its writes; true in every thread of the one that completes `total`.
+// Data one work-group writes and another reads within a launch goes through device-coherent accesses (agent-scope
+// relaxed atomics: the store writes through the XCD's L2, the load reads past a stale line), so no fence has to
+// write back or invalidate a whole L2.
+__device__ __forceinline__ void st_co(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ float ld_co(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Counts the work-group in on *cnt once its coherent stores have completed; true in every thread of the one that
+// completes `total` (which sets the counter back to zero).
 __device__ __forceinline__ bool arrive_last(uint32_t *cnt, uint32_t total, uint32_t *flag) {
-  __threadfence();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are done
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t old = atomicAdd(cnt, 1u);
+    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag = old == total - 1;
-    if (old == total - 1) atomicExch(cnt, 0u);
+    if (old == total - 1) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  const bool last = *flag != 0;
-  if (last) __threadfence();
-  return last;
+  return *flag != 0;
 }
 
 // One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
@@ -118,7 +126,7 @@ __device__ void route_token(const DecodeParams &p, uint32_t t, int32_t *ids_lds)
 #pragma unroll
   for (int i = 0; i < kPer; i++) {
     const uint32_t e = lane + 64 * i;
-    v[i] = e < E ? lg[e] : -INFINITY;
+    v[i] = e < E ? ld_co(lg + e) : -INFINITY;
     mx = fmaxf(mx, v[i]);
   }
   mx = wave_max(mx);
@@ -150,9 +158,10 @@ __device__ void route_token(const DecodeParams &p, uint32_t t, int32_t *ids_lds)
     }
     const uint32_t wid = 0xffffffffu - (uint32_t)wbest;
     if (bi >= 0 && best == wbest) taken[bi] = true;
-    if (lane == r) {
+    if (lane == r) {  // the logit back from its key
+      const uint32_t k = (uint32_t)(wbest >> 32);
       my_id = wid;
-      my_l = lg[wid];
+      my_l = __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
     }
   }
   const float pk = lane < K ? __fmul_rn(expf_libm(__fsub_rn(my_l, mx)), inv) : 0.0f;
@@ -164,21 +173,22 @@ __device__ void route_token(const DecodeParams &p, uint32_t t, int32_t *ids_lds)
     p.w[t * K + lane] = __fdiv_rn(pk, den);
     ids_lds[t * K + lane] = (int32_t)my_id;
   }
-  if (lane == 0) p.gs[t] = sigmoid_libm(lg[E]);
+  if (lane == 0) p.gs[t] = sigmoid_libm(ld_co(lg + E));
 }
 
 }  // namespace
 
-// Grid: max(ceil((E + 1) / 8), T) work-groups of 256. Work-group b < T quantises token b; every work-group takes 8
-// router rows (2 a wave); the last one to finish routes every token and groups the assignments.
-__global__ void __launch_bounds__(kWG) moe_route(DecodeParams p) {
+// Grid: max(ceil((E + 1) / 16), T) work-groups of 512. Work-group b < T quantises token b; every work-group takes 16
+// router rows (2 a wave); the last one to finish routes every token (a wave a token) and groups the assignments.
+__global__ void __launch_bounds__(kRouteWG) moe_route(DecodeParams p) {
   __shared__ int32_t ids_lds[kMaxDecodeTokens * kMaxUsed];
-  __shared__ uint32_t s_head[kWG], s_flag;
+  __shared__ uint32_t s_head[kRouteWG], s_flag;
+  __shared__ double part[kRouteWG / 64][2 * kMaxDecodeTokens][64];
   const uint32_t lane = lane_id(), wave = wave_id(), H = p.H, E = p.E, K = p.K, T = p.T;
   if (blockIdx.x < T) {
     // x[t] to the activation types of the routed and the shared gate: a half-wave per unit.
     const uint32_t t = blockIdx.x, l32 = threadIdx.x & 31u;
-    for (uint32_t u = threadIdx.x / 32; u < H / kUnit; u += kWG / 32) {
+    for (uint32_t u = threadIdx.x / 32; u < H / kUnit; u += kRouteWG / 32) {
       float v[8];
       const float4 *src = (const float4 *)(p.x + (uint64_t)t * H + u * kUnit + 8 * l32);
       const float4 a = src[0], b = src[1];
@@ -188,11 +198,12 @@ __global__ void __launch_bounds__(kWG) moe_route(DecodeParams p) {
     }
   }
   if (!p.route) return;
-  // Router rows: logit = sum of bf16(W) bf16(x), products exact, summed in fp64, rounded once, plus the bias.
+  // Router rows: logit = sum of bf16(W) bf16(x), products exact, summed in fp64, rounded once, plus the bias. A lane
+  // keeps one fp64 partial per (row, token); the wave then sums each pair's 64 partials through LDS.
+  const uint32_t r0 = blockIdx.x * 16 + wave * 2, npair = 2 * T;
   for (uint32_t rr = 0; rr < 2; rr++) {
-    const uint32_t r = blockIdx.x * 8 + wave * 2 + rr;
-    if (r > E) break;
-    const uint16_t *wr = p.router + (uint64_t)r * H;
+    const uint32_t r = r0 + rr;
+    const uint16_t *wr = p.router + (uint64_t)(r <= E ? r : E) * H;
     for (uint32_t t = 0; t < T; t++) {
       const float *xt = p.x + (uint64_t)t * H;
       double acc = 0.0;
@@ -207,16 +218,28 @@ __global__ void __launch_bounds__(kWG) moe_route(DecodeParams p) {
           acc = __builtin_fma((double)wf, (double)round_bf16(xx[i]), acc);
         }
       }
-      acc = wave_sum_d(acc);
-      if (lane == 0) {
-        float l = (float)acc;
-        if (r < E && p.bias) l = __fadd_rn(l, p.bias[r]);
-        p.logits[(uint64_t)t * (E + 1) + r] = l;
-      }
+      part[wave][rr * T + t][lane] = acc;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  {
+    uint32_t lp = 64;  // lanes per pair: 64 / the next power of two of npair
+    while (lp > 1 && (64 / lp) < npair) lp /= 2;
+    const uint32_t pr = lane / lp, q = lane % lp, span = 64 / lp;
+    double acc = 0.0;
+    if (pr < npair)
+      for (uint32_t i = 0; i < span; i++) acc = __dadd_rn(acc, part[wave][pr][q * span + i]);
+    for (uint32_t o = 1; o < lp; o <<= 1) acc = __dadd_rn(acc, __shfl_xor(acc, o, 64));
+    const uint32_t r = r0 + pr / T, t = pr % T;
+    if (pr < npair && q == 0 && r <= E) {
+      float l = (float)acc;
+      if (r < E && p.bias) l = __fadd_rn(l, p.bias[r]);
+      st_co(p.logits + (uint64_t)t * (E + 1) + r, l);
     }
   }
   if (!arrive_last(p.cnt_route, gridDim.x, &s_flag)) return;
-  for (uint32_t t = wave; t < T; t += kWG / 64) route_token(p, t, ids_lds);
+  for (uint32_t t = wave; t < T; t += kRouteWG / 64) route_token(p, t, ids_lds);
   __syncthreads();
   // MoeGroup records: an expert's assignments in order, MOE_GROUP_MAX a group, groups numbered by their first
   // assignment (as group_slots, layer.cl:894-942), then the shared expert's groups.
@@ -243,13 +266,13 @@ __global__ void __launch_bounds__(kWG) moe_route(DecodeParams p) {
   const bool head = a < n && rank % MOE_GROUP_MAX == 0;
   s_head[a] = head ? 1u : 0u;
   __syncthreads();
-  for (uint32_t off = 1; off < kWG; off <<= 1) {  // inclusive scan of the heads
+  for (uint32_t off = 1; off < kRouteWG; off <<= 1) {  // inclusive scan of the heads
     const uint32_t add = a >= off ? s_head[a - off] : 0u;
     __syncthreads();
     s_head[a] += add;
     __syncthreads();
   }
-  const uint32_t nr = s_head[kWG - 1];
+  const uint32_t nr = s_head[kRouteWG - 1];
   if (a < n) {
     const uint32_t g = s_head[head_a] - 1;
     p.groups[g].asg[rank % MOE_GROUP_MAX] = a;
@@ -270,22 +293,22 @@ __global__ void __launch_bounds__(kWG) moe_route(DecodeParams p) {
 
 namespace {
 
-// The tile (64 rows of one unit) a wave reads, and the matrix's type, for group g's expert.
+// Group g's matrix (0 gate, 1 up, 2 down) and its type.
 struct GroupMat {
   const uint8_t *mat;
   uint32_t type;
   bool shared;
 };
 
-__device__ __forceinline__ GroupMat group_mat(const DecodeParams &p, const MoeGroup &g, int which) {
+__device__ __forceinline__ GroupMat group_mat(const DecodeParams &p, int32_t slot, int which) {
   GroupMat m;
-  m.shared = g.slot == (int32_t)p.E;
+  m.shared = slot == (int32_t)p.E;
   if (m.shared) {
     m.type = which == 2 ? p.sh_down_type : p.sh_gate_type;
     m.mat = p.shared + (which == 0 ? 0 : which == 1 ? p.sh_up_off : p.sh_down_off);
   } else {
     m.type = which == 2 ? p.down_type : p.gate_type;
-    m.mat = p.experts + (uint64_t)g.slot * p.ex_bytes + (which == 0 ? 0 : which == 1 ? p.ex_up_off : p.ex_down_off);
+    m.mat = p.experts + (uint64_t)slot * p.ex_bytes + (which == 0 ? 0 : which == 1 ? p.ex_up_off : p.ex_down_off);
   }
   return m;
 }
@@ -295,126 +318,160 @@ __device__ __forceinline__ uint32_t asg_token(const DecodeParams &p, uint32_t as
   return asg < n ? asg / p.K : asg - n;
 }
 
-// The terms of one tile against the n activation units act(j), into out[j * stride].
-template <typename Act>
-__device__ __forceinline__ void tile_terms(uint32_t type, const uint8_t *tile, const uint32_t *grid_lds, uint32_t n,
-                                           Act act, float *out, uint64_t stride) {
-  const uint32_t lane = lane_id();
+__device__ __forceinline__ void load_grid(uint32_t *grid_lds, uint32_t nthreads) {
+  for (uint32_t i = threadIdx.x; i < 512; i += nthreads) grid_lds[i] = kIq3sGridDev[i];
+}
+
+// The n terms of one (row, unit) pair against the activation units act + j * kActLds / 4 dwords, into t[j].
+__device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, uint32_t idx, uint32_t nl,
+                                           const uint32_t *grid_lds, const uint32_t *act, uint32_t stride, uint32_t n,
+                                           float *t) {
   switch (type) {
     case QT_Q8_0: {
       UnitQ8_0 w;
-      w.load(tile, lane);
-      for (uint32_t j = 0; j < n; j++) out[j * stride] = w.term(ActUnit(act(j)));
+      w.load(tile, idx, nl);
+      #pragma unroll
+      for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
+        if (j < n) t[j] = w.term(Act(act + j * stride));
       break;
     }
     case QT_Q4_K: {
       UnitQ4_K w;
-      w.load(tile, lane);
-      for (uint32_t j = 0; j < n; j++) out[j * stride] = w.term(ActUnit(act(j)));
+      w.load(tile, idx, nl);
+      #pragma unroll
+      for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
+        if (j < n) t[j] = w.term(Act(act + j * stride));
       break;
     }
     default: {
       UnitIQ3_S w;
-      w.load(tile, lane, grid_lds);
-      for (uint32_t j = 0; j < n; j++) out[j * stride] = w.term(ActUnit(act(j)));
+      w.load(tile, idx, nl, grid_lds);
+      #pragma unroll
+      for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
+        if (j < n) t[j] = w.term(Act(act + j * stride));
       break;
     }
   }
 }
 
-__device__ __forceinline__ void load_grid(uint32_t *grid_lds) {
-  for (uint32_t i = threadIdx.x; i < 512; i += kWG) grid_lds[i] = kIq3sGridDev[i];
-  __syncthreads();
+// The pairwise sum over the U lanes of a row (U a power of two, the lanes consecutive): butterflies, which add the
+// halves in the oracle's tree order.
+__device__ __forceinline__ float row_sum(float t, uint32_t U) {
+  for (uint32_t o = 1; o < U; o <<= 1) t = __fadd_rn(t, __shfl_xor(t, o, 64));
+  return t;
 }
 
 }  // namespace
 
-// Grid: G_max x (F / 256) x 2 x (H / 256) work-groups of 256 (group slowest, then 256-row block, matrix, unit).
-__global__ void __launch_bounds__(kWG) moe_gate_up(DecodeParams p) {
+// Grid: G_max x (F / gate_up_rows(U)) work-groups of 256. A work-group takes gate_up_rows rows of gate and of up of
+// group g's expert, all U units of each: lane = m * 32 + r * U + u (m gate or up, r a row of the wave's 32 / U).
+// Each row's units are summed inside the wave, so h = silu(g) * u is whole here and stored as fp32.
+__global__ void __launch_bounds__(kGateUpWG) moe_gate_up(DecodeParams p) {
+  extern __shared__ uint32_t dyn_lds[];  // the group's activation units, kActLds apart
   __shared__ uint32_t grid_lds[512];
-  __shared__ float hbuf[MOE_GROUP_MAX][kUnit];
-  __shared__ uint32_t s_flag;
-  const uint32_t Ug = p.H / kUnit, nrb = p.F / kUnit;
-  uint32_t wg = blockIdx.x;
-  const uint32_t u = wg % Ug;
-  wg /= Ug;
-  const uint32_t m = wg % 2;
-  wg /= 2;
-  const uint32_t rb = wg % nrb, g = wg / nrb;
+  const uint32_t U = p.H / kUnit, rows = gate_up_rows(U), nwg = p.F / rows;
+  const uint32_t g = blockIdx.x / nwg, row0 = (blockIdx.x % nwg) * rows;
   if (g >= *p.ngroups) return;
-  const MoeGroup grp = p.groups[g];
-  const GroupMat gm = group_mat(p, grp, (int)m);
-  if (gm.type == QT_IQ3_S) load_grid(grid_lds);
+  const MoeGroup &grp = p.groups[g];
+  const uint32_t n = grp.n;
+  const GroupMat gm = group_mat(p, grp.slot, 0);
   const uint8_t *act = gm.shared ? p.act_s : p.act_r;
-  const uint32_t row = rb * kUnit + threadIdx.x;  // wave w holds rows rb * 256 + 64 w + lane
-  const uint8_t *tile = gm.mat + ((uint64_t)(rb * 4 + wave_id()) * Ug + u) * tile_bytes(gm.type);
-  float *terms = p.terms_gu + (((uint64_t)g * 2 + m) * Ug + u) * MOE_GROUP_MAX * p.F + row;
-  tile_terms(
-      gm.type, tile, grid_lds, grp.n,
-      [&](uint32_t j) { return act + ((uint64_t)asg_token(p, grp.asg[j]) * Ug + u) * kActBytes; }, terms, p.F);
-  if (!arrive_last(p.cnt_gu + (uint64_t)g * nrb + rb, 2 * Ug, &s_flag)) return;
-  // Finish rows rb * 256 .. +256: the units' pairwise sum, SwiGLU, h of each assignment quantised as one unit of the
-  // down's K.
-  const float *tg = p.terms_gu + ((uint64_t)g * 2 * Ug) * MOE_GROUP_MAX * p.F + row;
-  const float *tu = tg + (uint64_t)Ug * MOE_GROUP_MAX * p.F;
-  for (uint32_t j = 0; j < grp.n; j++) {
-    float a[kMaxUnits], b[kMaxUnits];
-    for (uint32_t k = 0; k < Ug; k++) {
-      a[k] = tg[((uint64_t)k * MOE_GROUP_MAX + j) * p.F];
-      b[k] = tu[((uint64_t)k * MOE_GROUP_MAX + j) * p.F];
-    }
-    hbuf[j][threadIdx.x] = swiglu_one(pairwise_pow2(a, Ug), pairwise_pow2(b, Ug), p.swiglu_limit);
+  // Stage the n assignments' activation units (their tokens' x, quantised by moe_route).
+  for (uint32_t i = threadIdx.x; i < n * U * (kActBytes / 16); i += kGateUpWG) {
+    const uint32_t unit = i / (kActBytes / 16), c = i % (kActBytes / 16), j = unit / U, u = unit % U;
+    const uint4 v = ((const uint4 *)(act + ((uint64_t)asg_token(p, grp.asg[j]) * U + u) * kActBytes))[c];
+    *(uint4 *)((uint8_t *)dyn_lds + unit * kActLds + 16 * c) = v;
   }
+  if (gm.type == QT_IQ3_S) load_grid(grid_lds, kGateUpWG);
   __syncthreads();
-  const uint32_t j = threadIdx.x / 32, l32 = threadIdx.x & 31u;
-  if (j < grp.n) {
-    float v[8];
+  const uint32_t lane = lane_id(), m = lane / 32, r = (lane % 32) / U, u = lane % U;
+  const uint32_t row = row0 + wave_id() * (32 / U) + r;
+  const uint8_t *mat = gm.mat + (m ? (gm.shared ? p.sh_up_off : p.ex_up_off) : 0);
+  const uint8_t *tile = mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
+  float t[MOE_GROUP_MAX];
+  pair_terms(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds, dyn_lds + u * (kActLds / 4),
+             U * (kActLds / 4), n, t);
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = hbuf[j][8 * l32 + i];
-    const uint32_t dact = quant_vec_dot_type(group_mat(p, grp, 2).type);
-    quant_unit(v, l32, dact, p.hact + ((uint64_t)grp.asg[j] * nrb + rb) * kActBytes);
+  for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
+    if (j >= n) break;
+    const float s = row_sum(t[j], U);                 // gate's row sum in lanes m = 0, up's in m = 1
+    const float su = __shfl_xor(s, 32, 64);           // the other matrix's
+    if (m == 0 && u == 0) p.h[(uint64_t)grp.asg[j] * p.F + row] = swiglu_one(s, su, p.swiglu_limit);
   }
 }
 
-// Grid: G_max x (H / 256) x (F / 256) work-groups of 256 (group slowest, then 256-row block, unit).
-__global__ void __launch_bounds__(kWG) moe_down(DecodeParams p) {
+// Grid: G_max x (H / down_rows(Ud)) work-groups of 128. A work-group first quantises its group's h (each assignment's
+// F values, as units of the down's activation type) into LDS, then takes down_rows rows of down, all Ud units:
+// lane = r * Ud + u. A row's units are summed inside the wave into the assignment's output; a token whose k + 1
+// outputs are all in for these rows is combined by the work-group that brought the last.
+__global__ void __launch_bounds__(kDownWG) moe_down(DecodeParams p) {
+  extern __shared__ uint32_t dyn_lds[];
   __shared__ uint32_t grid_lds[512];
-  __shared__ uint32_t s_flag;
-  const uint32_t Ud = p.F / kUnit, nrb = p.H / kUnit;
-  uint32_t wg = blockIdx.x;
-  const uint32_t u = wg % Ud;
-  wg /= Ud;
-  const uint32_t rb = wg % nrb, g = wg / nrb;
+  __shared__ uint32_t s_last[MOE_GROUP_MAX];
+  const uint32_t U = p.F / kUnit, rows = down_rows(U), nwg = p.H / rows;
+  const uint32_t g = blockIdx.x / nwg, rb = blockIdx.x % nwg, row0 = rb * rows;
   if (g >= *p.ngroups) return;
-  const MoeGroup grp = p.groups[g];
-  const GroupMat gm = group_mat(p, grp, 2);
-  if (gm.type == QT_IQ3_S) load_grid(grid_lds);
-  const uint32_t row = rb * kUnit + threadIdx.x;
-  const uint8_t *tile = gm.mat + ((uint64_t)(rb * 4 + wave_id()) * Ud + u) * tile_bytes(gm.type);
-  float *terms = p.terms_d + ((uint64_t)g * Ud + u) * MOE_GROUP_MAX * p.H + row;
-  tile_terms(
-      gm.type, tile, grid_lds, grp.n,
-      [&](uint32_t j) { return p.hact + ((uint64_t)grp.asg[j] * Ud + u) * kActBytes; }, terms, p.H);
-  if (!arrive_last(p.cnt_d + (uint64_t)g * nrb + rb, Ud, &s_flag)) return;
-  const float *td = p.terms_d + (uint64_t)g * Ud * MOE_GROUP_MAX * p.H + row;
-  for (uint32_t j = 0; j < grp.n; j++) {
-    float a[kMaxUnits];
-    for (uint32_t k = 0; k < Ud; k++) a[k] = td[((uint64_t)k * MOE_GROUP_MAX + j) * p.H];
-    p.y_asg[(uint64_t)grp.asg[j] * p.H + row] = pairwise_pow2(a, Ud);
+  const MoeGroup &grp = p.groups[g];
+  const uint32_t n = grp.n;
+  const GroupMat gm = group_mat(p, grp.slot, 2);
+  const uint32_t dact = quant_vec_dot_type(gm.type);
+  // h -> activation units in LDS: a half-wave a unit.
+  for (uint32_t unit = threadIdx.x / 32; unit < n * U; unit += kDownWG / 32) {
+    const uint32_t j = unit / U, u = unit % U, l32 = threadIdx.x & 31u;
+    const float4 *src = (const float4 *)(p.h + (uint64_t)grp.asg[j] * p.F + u * kUnit + 8 * l32);
+    const float4 a = src[0], b = src[1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    quant_unit(v, l32, dact, (uint8_t *)dyn_lds + unit * kActLds);
   }
-  // A token whose k routed outputs and shared output are all in: y = sum_k w_k y_k (rank order) + gs s.
-  for (uint32_t j = 0; j < grp.n; j++) {
-    const uint32_t t = asg_token(p, grp.asg[j]);
-    const uint32_t need = p.tok_need ? p.tok_need[t] : p.K + (p.has_shared ? 1u : 0u);
-    if (!arrive_last(p.cnt_tok + (uint64_t)t * nrb + rb, need, &s_flag)) continue;
-    const float *ya = p.y_asg + row;
-    const float *wt = p.w + (uint64_t)t * p.K;
-    const int32_t *it = p.ids + (uint64_t)t * p.K;
-    float acc = 0.0f;
-    for (uint32_t r = 0; r < p.K; r++)
-      if (it[r] >= 0) acc = __fadd_rn(acc, __fmul_rn(wt[r], ya[((uint64_t)t * p.K + r) * p.H]));
-    if (p.has_shared) acc = __fadd_rn(acc, __fmul_rn(p.gs[t], ya[((uint64_t)p.T * p.K + t) * p.H]));
-    p.y[(uint64_t)t * p.H + row] = acc;
+  if (gm.type == QT_IQ3_S) load_grid(grid_lds, kDownWG);
+  __syncthreads();
+  const uint32_t lane = lane_id(), r = lane / U, u = lane % U;
+  const uint32_t row = row0 + wave_id() * (64 / U) + r;
+  const uint8_t *tile = gm.mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
+  float t[MOE_GROUP_MAX];
+  pair_terms(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds, dyn_lds + u * (kActLds / 4),
+             U * (kActLds / 4), n, t);
+#pragma unroll
+  for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
+    if (j >= n) break;
+    const float s = row_sum(t[j], U);
+    if (u == 0) st_co(p.y_asg + (uint64_t)grp.asg[j] * p.H + row, s);
+  }
+  // Count this work-group's outputs in, one counter per (token, row block), all at once.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x < n) {
+    const uint32_t tk = asg_token(p, grp.asg[threadIdx.x]);
+    const uint32_t need = p.tok_need ? p.tok_need[tk] : p.K + (p.has_shared ? 1u : 0u);
+    uint32_t *cnt = p.cnt_tok + (uint64_t)tk * nwg + rb;
+    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last[threadIdx.x] = old == need - 1;
+    if (old == need - 1) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  // y = sum_k w_k y_k in rank order, then + gs s: every output loaded first, then summed in order.
+  for (uint32_t j = 0; j < n; j++) {
+    if (!s_last[j]) continue;
+    const uint32_t tk = asg_token(p, grp.asg[j]);
+    for (uint32_t i = threadIdx.x; i < rows; i += kDownWG) {
+      const uint32_t rr = row0 + i;
+      float yv[kMaxUsed + 1], wv[kMaxUsed];
+      bool on[kMaxUsed];
+#pragma unroll
+      for (uint32_t k = 0; k < kMaxUsed; k++) {
+        on[k] = k < p.K && p.ids[tk * p.K + k] >= 0;
+        wv[k] = k < p.K ? p.w[tk * p.K + k] : 0.0f;
+        yv[k] = on[k] ? ld_co(p.y_asg + ((uint64_t)tk * p.K + k) * p.H + rr) : 0.0f;
+      }
+      yv[kMaxUsed] = p.has_shared ? ld_co(p.y_asg + ((uint64_t)p.T * p.K + tk) * p.H + rr) : 0.0f;
+      float acc = 0.0f;
+#pragma unroll
+      for (uint32_t k = 0; k < kMaxUsed; k++)
+        if (on[k]) acc = __fadd_rn(acc, __fmul_rn(wv[k], yv[k]));
+      if (p.has_shared) acc = __fadd_rn(acc, __fmul_rn(p.gs[tk], yv[kMaxUsed]));
+      p.y[(uint64_t)tk * p.H + rr] = acc;
+    }
   }
 }
 

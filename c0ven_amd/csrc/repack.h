@@ -14,24 +14,25 @@ inline const uint8_t *file_unit(const uint8_t *m, uint32_t type, uint32_t k, uin
   return m + r * row + (uint64_t)u * unit_bytes(type);
 }
 
-// One unit's bytes into tile position (lane), the tile at dst.
-inline void put_unit(uint8_t *tile, uint32_t type, uint32_t lane, const uint8_t *b) {
+// One unit's bytes into pair idx of a tile of nl = 64 U pairs.
+inline void put_unit(uint8_t *tile, uint32_t type, uint32_t idx, uint32_t nl, const uint8_t *b) {
+  auto at = [&](uint32_t base, uint32_t p, uint32_t piece) { return tile + (uint64_t)base * nl + ((uint64_t)p * nl + idx) * piece; };
   switch (type) {
     case QT_Q8_0:
-      for (int p = 0; p < 16; p++) std::memcpy(tile + q8_0t::kQs + (p * 64 + lane) * 16, b + (p / 2) * 34 + 2 + (p % 2) * 16, 16);
-      for (int blk = 0; blk < 8; blk++) std::memcpy(tile + q8_0t::kD + lane * 16 + 2 * blk, b + blk * 34, 2);
+      for (uint32_t p = 0; p < 16; p++) std::memcpy(at(q8_0t::kQs, p, 16), b + (p / 2) * 34 + 2 + (p % 2) * 16, 16);
+      for (uint32_t blk = 0; blk < 8; blk++) std::memcpy(at(q8_0t::kD, 0, 16) + 2 * blk, b + blk * 34, 2);
       break;
     case QT_Q4_K:
-      for (int p = 0; p < 8; p++) std::memcpy(tile + q4_kt::kQs + (p * 64 + lane) * 16, b + 16 + 16 * p, 16);
-      for (int i = 0; i < 3; i++) std::memcpy(tile + q4_kt::kScales + (i * 64 + lane) * 4, b + 4 + 4 * i, 4);
-      std::memcpy(tile + q4_kt::kDm + lane * 4, b, 4);
+      for (uint32_t p = 0; p < 8; p++) std::memcpy(at(q4_kt::kQs, p, 16), b + 16 + 16 * p, 16);
+      for (uint32_t i = 0; i < 3; i++) std::memcpy(at(q4_kt::kScales, i, 4), b + 4 + 4 * i, 4);
+      std::memcpy(at(q4_kt::kDm, 0, 4), b, 4);
       break;
     case QT_IQ3_S:
-      for (int p = 0; p < 4; p++) std::memcpy(tile + iq3_st::kQs + (p * 64 + lane) * 16, b + 2 + 16 * p, 16);
-      for (int p = 0; p < 2; p++) std::memcpy(tile + iq3_st::kSigns + (p * 64 + lane) * 16, b + 74 + 16 * p, 16);
-      for (int i = 0; i < 2; i++) std::memcpy(tile + iq3_st::kQh + (i * 64 + lane) * 4, b + 66 + 4 * i, 4);
-      std::memcpy(tile + iq3_st::kScales + lane * 4, b + 106, 4);
-      std::memcpy(tile + iq3_st::kD + lane * 2, b, 2);
+      for (uint32_t p = 0; p < 4; p++) std::memcpy(at(iq3_st::kQs, p, 16), b + 2 + 16 * p, 16);
+      for (uint32_t p = 0; p < 2; p++) std::memcpy(at(iq3_st::kSigns, p, 16), b + 74 + 16 * p, 16);
+      for (uint32_t i = 0; i < 2; i++) std::memcpy(at(iq3_st::kQh, i, 4), b + 66 + 4 * i, 4);
+      std::memcpy(at(iq3_st::kScales, 0, 4), b + 106, 4);
+      std::memcpy(at(iq3_st::kD, 0, 2), b, 2);
       break;
   }
 }
@@ -39,14 +40,14 @@ inline void put_unit(uint8_t *tile, uint32_t type, uint32_t lane, const uint8_t 
 // rows x k values of type: file layout -> device layout (dst has matrix_bytes(type, rows, k); rows past the last of
 // the final tile are zero, which decodes to zero weights).
 inline void repack_matrix(uint32_t type, const uint8_t *src, uint32_t rows, uint32_t k, uint8_t *dst) {
-  const uint32_t U = k / kUnit, nrt = (rows + kTileRows - 1) / kTileRows, tb = tile_bytes(type);
+  const uint32_t U = k / kUnit, nrt = (rows + kTileRows - 1) / kTileRows, nl = kTileRows * U;
+  const uint64_t tb = tile_bytes(type, U);
   std::memset(dst, 0, matrix_bytes(type, rows, k));
-  for (uint32_t rt = 0; rt < nrt; rt++)
-    for (uint32_t u = 0; u < U; u++) {
-      uint8_t *tile = dst + ((uint64_t)rt * U + u) * tb;
-      for (uint32_t l = 0; l < kTileRows && rt * kTileRows + l < rows; l++)
-        put_unit(tile, type, l, file_unit(src, type, k, rt * kTileRows + l, u));
-    }
+  for (uint32_t rt = 0; rt < nrt; rt++) {
+    uint8_t *tile = dst + (uint64_t)rt * tb;
+    for (uint32_t l = 0; l < kTileRows && rt * kTileRows + l < rows; l++)
+      for (uint32_t u = 0; u < U; u++) put_unit(tile, type, l * U + u, nl, file_unit(src, type, k, rt * kTileRows + l, u));
+  }
 }
 
 }  // namespace c0ven

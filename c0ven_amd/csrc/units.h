@@ -1,9 +1,9 @@
 // One lane's unit (256 values of one weight row) of each weight type, and its term against a quantised activation unit.
 //
-// A lane holds one row's unit decoded to signed 8-bit words in registers; the activation unit is wave-uniform (the
-// compiler reads it with scalar loads), so each v_dot4 takes one word from each. A term is the unit's fp32 share of
-// the row sum, with the roundings the CPU oracle's block dot products have (its ORACLE ORDER): exact integer sums,
-// then per block (Q8_0) or super-block (Q4_K, IQ3_S) the same fp32 steps.
+// A lane holds one (row, unit) pair of a tile decoded to signed 8-bit words in registers (layout.h: pair idx of a tile
+// of nl = 64 U pairs) and takes the activation unit from LDS; each v_dot4 multiplies one word of each. A term is the
+// unit's fp32 share of the row sum, with the roundings the CPU oracle's block dot products have (its ORACLE ORDER):
+// exact integer sums, then per block (Q8_0) or super-block (Q4_K, IQ3_S) the same fp32 steps.
 #pragma once
 
 #include "device_math.h"
@@ -11,39 +11,43 @@
 
 namespace c0ven {
 
-// A wave-uniform activation unit (layout.h).
-struct ActUnit {
-  const int32_t *q;     // 64 words of codes
-  const float *scale;   // q8_K: [0]; q8_0: [0..7]
-  const int32_t *sums;  // q8_K: 8 sums of 32 codes
-  __device__ __forceinline__ explicit ActUnit(const uint8_t *p)
-      : q((const int32_t *)p), scale((const float *)(p + kActScales)), sums((const int32_t *)(p + kActSums)) {}
+// An activation unit (layout.h) as 80 dwords: 64 of codes, the scales at 64, the q8_K sums at 72.
+struct Act {
+  const uint32_t *d;
+  __device__ __forceinline__ explicit Act(const uint32_t *p) : d(p) {}
+  __device__ __forceinline__ uint32_t q(int i) const { return d[i]; }
+  __device__ __forceinline__ float scale(int b) const { return __uint_as_float(d[64 + b]); }
+  __device__ __forceinline__ int sum(int j) const { return (int)d[72 + j]; }
 };
+
+template <typename T>
+__device__ __forceinline__ const T *field(const uint8_t *tile, uint32_t base, uint32_t p, uint32_t idx, uint32_t nl) {
+  return (const T *)(tile + (uint64_t)base * nl) + (uint64_t)p * nl + idx;
+}
 
 // Q8_0: eight blocks of 32 (vec_dot_q8_0_q8_0). Term: the pairwise sum of (d_w d_a) sumi over the eight blocks.
 struct UnitQ8_0 {
   uint32_t q[64];
   float d[8];
-  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t lane) {
-    const uint4 *qs = (const uint4 *)(tile + q8_0t::kQs);
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl) {
 #pragma unroll
     for (int p = 0; p < 16; p++) {
-      const uint4 v = qs[p * 64 + lane];
+      const uint4 v = *field<uint4>(tile, q8_0t::kQs, p, idx, nl);
       q[4 * p] = v.x, q[4 * p + 1] = v.y, q[4 * p + 2] = v.z, q[4 * p + 3] = v.w;
     }
-    const uint4 dv = ((const uint4 *)(tile + q8_0t::kD))[lane];
+    const uint4 dv = *field<uint4>(tile, q8_0t::kD, 0, idx, nl);
     const uint32_t w[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
     for (int b = 0; b < 8; b++) d[b] = h2f((uint16_t)(w[b / 2] >> (16 * (b % 2))));
   }
-  __device__ __forceinline__ float term(const ActUnit &a) const {
+  __device__ __forceinline__ float term(const Act &a) const {
     float t[8];
 #pragma unroll
     for (int b = 0; b < 8; b++) {
       int s = 0;
 #pragma unroll
-      for (int i = 0; i < 8; i++) s = dot4(q[8 * b + i], (uint32_t)a.q[8 * b + i], s);
-      t[b] = __fmul_rn(__fmul_rn(d[b], a.scale[b]), (float)s);
+      for (int i = 0; i < 8; i++) s = dot4(q[8 * b + i], a.q(8 * b + i), s);
+      t[b] = __fmul_rn(__fmul_rn(d[b], a.scale(b)), (float)s);
     }
     return __fadd_rn(__fadd_rn(__fadd_rn(t[0], t[1]), __fadd_rn(t[2], t[3])),
                      __fadd_rn(__fadd_rn(t[4], t[5]), __fadd_rn(t[6], t[7])));
@@ -56,11 +60,10 @@ struct UnitQ4_K {
   uint32_t lo[32], hi[32];  // the nibbles of qs word w: lo values 64c + 4(w % 8) + 0..3, hi those + 32 (c = w / 8)
   int sc[8], mn[8];
   float d, dmin;
-  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t lane) {
-    const uint4 *qs = (const uint4 *)(tile + q4_kt::kQs);
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl) {
 #pragma unroll
     for (int p = 0; p < 8; p++) {
-      const uint4 v = qs[p * 64 + lane];
+      const uint4 v = *field<uint4>(tile, q4_kt::kQs, p, idx, nl);
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -68,11 +71,10 @@ struct UnitQ4_K {
         hi[4 * p + i] = (w[i] >> 4) & 0x0f0f0f0fu;
       }
     }
-    const uint32_t *s = (const uint32_t *)(tile + q4_kt::kScales);
     uint8_t b[12];
 #pragma unroll
     for (int i = 0; i < 3; i++) {
-      const uint32_t v = s[i * 64 + lane];
+      const uint32_t v = *field<uint32_t>(tile, q4_kt::kScales, i, idx, nl);
 #pragma unroll
       for (int j = 0; j < 4; j++) b[4 * i + j] = (uint8_t)(v >> (8 * j));
     }
@@ -86,25 +88,25 @@ struct UnitQ4_K {
         mn[j] = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
       }
     }
-    const uint32_t dm = ((const uint32_t *)(tile + q4_kt::kDm))[lane];
+    const uint32_t dm = *field<uint32_t>(tile, q4_kt::kDm, 0, idx, nl);
     d = h2f((uint16_t)dm);
     dmin = h2f((uint16_t)(dm >> 16));
   }
-  __device__ __forceinline__ float term(const ActUnit &a) const {
+  __device__ __forceinline__ float term(const Act &a) const {
     int isum = 0, imin = 0;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       int sl = 0, sh = 0;
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        sl = dot4(lo[8 * c + i], (uint32_t)a.q[16 * c + i], sl);
-        sh = dot4(hi[8 * c + i], (uint32_t)a.q[16 * c + 8 + i], sh);
+        sl = dot4(lo[8 * c + i], a.q(16 * c + i), sl);
+        sh = dot4(hi[8 * c + i], a.q(16 * c + 8 + i), sh);
       }
       isum += sc[2 * c] * sl + sc[2 * c + 1] * sh;
     }
 #pragma unroll
-    for (int j = 0; j < 8; j++) imin += mn[j] * a.sums[j];
-    const float ad = a.scale[0];
+    for (int j = 0; j < 8; j++) imin += mn[j] * a.sum(j);
+    const float ad = a.scale(0);
     const float dd = __fmul_rn(d, ad), dm = __fmul_rn(dmin, ad);
     const float pm = __fmul_rn(dm, (float)imin);
     return __builtin_fmaf(dd, (float)isum, -pm);
@@ -117,53 +119,43 @@ struct UnitIQ3_S {
   uint32_t w[64];  // group k's four values 4k..4k+3, signed
   int ls[8];
   float d;
-  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t lane, const uint32_t *grid) {
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl, const uint32_t *grid) {
     uint32_t qs[16], sg[8];
-    const uint4 *pq = (const uint4 *)(tile + iq3_st::kQs);
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-      const uint4 v = pq[p * 64 + lane];
+      const uint4 v = *field<uint4>(tile, iq3_st::kQs, p, idx, nl);
       qs[4 * p] = v.x, qs[4 * p + 1] = v.y, qs[4 * p + 2] = v.z, qs[4 * p + 3] = v.w;
     }
-    const uint4 *ps = (const uint4 *)(tile + iq3_st::kSigns);
 #pragma unroll
     for (int p = 0; p < 2; p++) {
-      const uint4 v = ps[p * 64 + lane];
+      const uint4 v = *field<uint4>(tile, iq3_st::kSigns, p, idx, nl);
       sg[4 * p] = v.x, sg[4 * p + 1] = v.y, sg[4 * p + 2] = v.z, sg[4 * p + 3] = v.w;
     }
-    const uint32_t *pqh = (const uint32_t *)(tile + iq3_st::kQh);
-    const uint32_t qh[2] = {pqh[lane], pqh[64 + lane]};
-    const uint32_t sc = ((const uint32_t *)(tile + iq3_st::kScales))[lane];
-    d = h2f(((const uint16_t *)(tile + iq3_st::kD))[lane]);
+    const uint32_t qh[2] = {*field<uint32_t>(tile, iq3_st::kQh, 0, idx, nl), *field<uint32_t>(tile, iq3_st::kQh, 1, idx, nl)};
+    const uint32_t sc = *field<uint32_t>(tile, iq3_st::kScales, 0, idx, nl);
+    d = h2f(*field<uint16_t>(tile, iq3_st::kD, 0, idx, nl));
 #pragma unroll
     for (int ib = 0; ib < 8; ib++) ls[ib] = 1 + 2 * (int)((sc >> (4 * ib)) & 15u);
 #pragma unroll
     for (int k = 0; k < 64; k++) {
-      const uint32_t idx = ((qs[k / 4] >> (8 * (k % 4))) & 0xffu) | (((qh[k / 32] >> (k % 32)) & 1u) << 8);
-      const uint32_t g = grid[idx];
+      const uint32_t ix = ((qs[k / 4] >> (8 * (k % 4))) & 0xffu) | (((qh[k / 32] >> (k % 32)) & 1u) << 8);
+      const uint32_t g = grid[ix];
       const uint32_t nib = (sg[k / 8] >> (4 * (k % 8))) & 15u;
       const uint32_t x = (nib * 0x00204081u) & 0x01010101u;  // byte j = bit j of the nibble
       w[k] = (g ^ (x * 0xffu)) + x;                          // bytes with the bit set negated, no carries
     }
   }
-  __device__ __forceinline__ float term(const ActUnit &a) const {
+  __device__ __forceinline__ float term(const Act &a) const {
     int bsum = 0;
 #pragma unroll
     for (int ib = 0; ib < 8; ib++) {
       int s = 0;
 #pragma unroll
-      for (int k = 0; k < 8; k++) s = dot4(w[8 * ib + k], (uint32_t)a.q[8 * ib + k], s);
+      for (int k = 0; k < 8; k++) s = dot4(w[8 * ib + k], a.q(8 * ib + k), s);
       bsum += ls[ib] * s;
     }
-    return __fmul_rn(__fmul_rn(d, a.scale[0]), (float)bsum);
+    return __fmul_rn(__fmul_rn(d, a.scale(0)), (float)bsum);
   }
 };
-
-// The pairwise sum of n terms, n a power of two (the oracle's order for power-of-two block counts).
-__device__ __forceinline__ float pairwise_pow2(float *t, uint32_t n) {
-  for (uint32_t s = 1; s < n; s *= 2)
-    for (uint32_t i = 0; i + s < n; i += 2 * s) t[i] = __fadd_rn(t[i], t[i + s]);
-  return t[0];
-}
 
 }  // namespace c0ven

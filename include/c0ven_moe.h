@@ -114,10 +114,19 @@ MOE_API moe_status moe_sync(moe_ctx *ctx);
 /* The context's HIP stream (a hipStream_t). */
 MOE_API void *moe_stream(moe_ctx *ctx);
 
-/* Timing of the last forward's kernels with HIP events on the stream they ran on, when enabled (off by default:
- * events cost a little). names and ms have room for cap entries; n receives how many. */
+/* Per-kernel timing with HIP events recorded on the stream each kernel runs on, around every launch of every forward
+ * while on (off by default; turning it on or off clears the record). moe_kernel_times waits for the recorded
+ * forwards, gives each kernel's average duration per launch over them (names and avg_ms have room for cap entries;
+ * n receives how many kernels, forwards how many forwards were averaged) and clears the record. */
 MOE_API moe_status moe_set_timing(moe_ctx *ctx, int on);
-MOE_API moe_status moe_kernel_times(moe_ctx *ctx, const char **names, float *ms, uint32_t cap, uint32_t *n);
+MOE_API moe_status moe_kernel_times(moe_ctx *ctx, const char **names, float *avg_ms, uint32_t cap, uint32_t *n,
+                                    uint32_t *forwards);
+
+/* Copies the resident experts (and shared expert) of src_layer over those of dst_layer, device to device. */
+MOE_API moe_status moe_copy_experts(moe_ctx *ctx, uint32_t src_layer, uint32_t dst_layer);
+/* Bytes of one resident matrix in the device layout: which = 0 routed gate (up is the same), 1 routed down,
+ * 2 shared gate, 3 shared down. These are the weights' own bytes, the block's algorithmic traffic per matrix. */
+MOE_API moe_status moe_expert_bytes(const moe_ctx *ctx, uint32_t which, uint64_t *bytes);
 
 /* Device bytes the context holds: resident weights and scratch. */
 MOE_API uint64_t moe_device_bytes(const moe_ctx *ctx);
