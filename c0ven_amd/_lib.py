@@ -68,6 +68,8 @@ _SIGS = {
     "moe_set_timing": (_i32, [_P, C.c_int]),
     "moe_kernel_times": (_i32, [_P, C.POINTER(C.c_char_p), C.POINTER(_f32), _u32, C.POINTER(_u32), C.POINTER(_u32)]),
     "moe_copy_experts": (_i32, [_P, _u32, _u32]),
+    "moe_set_trace": (_i32, [_P, C.c_int]),
+    "moe_trace": (_i32, [_P, _P, _u32, C.POINTER(_u32), _P]),
     "moe_expert_bytes": (_i32, [_P, _u32, C.POINTER(_u64)]),
     "moe_device_bytes": (_u64, [_P]),
     "moe_dequantize": (_i32, [_P, _u32, _P, _u32, _u32, _P]),
@@ -220,6 +222,19 @@ class MoeBlock:
         n, nf = C.c_uint32(), C.c_uint32()
         self._check(lib.moe_kernel_times(self.h, names, ms, 8, C.byref(n), C.byref(nf)))
         return {names[i].decode(): ms[i] for i in range(n.value)}, nf.value
+
+    def set_trace(self, on):
+        self._check(lib.moe_set_trace(self.h, 1 if on else 0))
+
+    def trace(self):
+        """The last forward's (start, end) s_memrealtime stamps (100 MHz) per work item, and where the router,
+        top-k, gate/up and down items begin (plus the end)."""
+        n = C.c_uint32()
+        bounds = np.zeros(5, dtype=np.uint32)
+        self._check(lib.moe_trace(self.h, None, 0, C.byref(n), _ptr(bounds)))
+        out = np.zeros((n.value, 2), dtype=np.uint64)
+        self._check(lib.moe_trace(self.h, _ptr(out), n.value, C.byref(n), _ptr(bounds)))
+        return out, bounds
 
     def copy_experts(self, src_layer, dst_layer):
         self._check(lib.moe_copy_experts(self.h, src_layer, dst_layer))

@@ -1,4 +1,4 @@
-// What the decode kernels take: one struct by value (the kernel-argument segment), filled by the host per call.
+// What the decode kernel takes: one struct by value (the kernel-argument segment), filled by the host per call.
 #pragma once
 
 #include <stdint.h>
@@ -7,21 +7,34 @@
 
 namespace c0ven {
 
-constexpr uint32_t kMaxExperts = 512;     // routed experts a layer may have
-constexpr uint32_t kMaxUsed = 16;         // k
-constexpr uint32_t kMaxDecodeTokens = 16; // tokens the decode path takes per call
-constexpr uint32_t kMaxUnits = 32;        // 256-value units per row: H and F up to 8192
+constexpr uint32_t kMaxExperts = 512;      // routed experts a layer may have
+constexpr uint32_t kMaxUsed = 16;          // k
+constexpr uint32_t kMaxDecodeTokens = 16;  // tokens the decode path takes per call
+constexpr uint32_t kMaxUnits = 32;         // 256-value units per row: H and F up to 8192
 
 // Groups one decode call can make: every assignment its own group, and the shared expert's.
 constexpr uint32_t max_groups(uint32_t T, uint32_t K) { return T * K + (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX; }
+
+// The work-group (four waves) and the work items of moe_decode, in the order every work-group walks them:
+//   router items   kRouteRows router rows each (2 a wave); item t < T also quantises x[t];
+//   top-k items    one a token (when routing);
+//   gate/up items  gate_up_rows(U) rows of gate and of up of one group, all units (lane = m * 32 + r * U + u);
+//   down items     down_rows(U_down) rows of down of one group, all units (lane = r * U_down + u).
+constexpr uint32_t kWG = 256, kRouteRows = 8;
+constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kWG / 64) * (32 / Ug); }
+constexpr uint32_t down_rows(uint32_t Ud) { return (kWG / 64) * (64 / Ud); }
+
+// Flags (64-bit, set to the launch's epoch): [0] the logits are in, [1] the groups are in, [2 + g] group g's h is in.
+constexpr uint32_t kFlagLogits = 0, kFlagRouted = 1, kFlagH = 2;
 
 struct DecodeParams {
   uint32_t H, F, E, K, T;
   uint32_t gate_type, down_type, sh_gate_type, sh_down_type, has_shared;
   uint32_t xact_r, xact_s;  // the activation types x is quantised to for the routed and the shared gate
   float swiglu_limit;
-  uint32_t route;          // 1: route x; 0: the host gave ids, w and the groups (pre-routed jobs); x is only quantised
+  uint32_t route;            // 1: route x; 0: the host gave ids, w and the groups (pre-routed jobs)
   const uint32_t *tok_need;  // pre-routed: outputs token t sums (its jobs); null: K + has_shared
+  uint64_t epoch;            // this launch's number: a flag is set when it holds it
   // The layer.
   const uint16_t *router;  // (E + 1) x H bf16, the last row the shared gate
   const float *bias;       // E, or null
@@ -32,7 +45,8 @@ struct DecodeParams {
   // Input and output: T x H fp32, rows contiguous.
   const float *x;
   float *y;
-  // Scratch (sized for kMaxDecodeTokens at open).
+  // Scratch (sized for max_tokens at open). Everything written here during a launch and read by another work-group
+  // goes through device-coherent stores and loads.
   uint8_t *act_r, *act_s;  // T x (H / 256) activation units; act_s == act_r when the two types agree
   float *logits;           // T x (E + 1)
   int32_t *ids;            // T x K
@@ -41,19 +55,19 @@ struct DecodeParams {
   MoeGroup *groups;
   uint32_t *ngroups;
   float *h;                // (T K + T) x F: SwiGLU of each assignment, fp32
+  uint8_t *hact;           // (T K + T) x (F / 256) activation units: h quantised to the down's type
   float *y_asg;            // (T K + T) x H: each assignment's expert output
-  uint32_t *cnt_route;     // 1
-  uint32_t *cnt_tok;       // T x (H / kDownRows): outputs in per (token, down row block)
+  uint64_t *flags;         // 2 + G
+  uint32_t *cnt_route;     // 1: router items in
+  uint32_t *cnt_topk;      // 1: tokens routed
+  uint32_t *cnt_hu;        // G x (F / 256): gate/up items in per (group, unit of h)
+  uint32_t *cnt_hq;        // G: units of h quantised per group
+  uint32_t *cnt_tok;       // T x (H / down_rows): outputs in per (token, down row block)
+  uint32_t *err;           // set when a wait gave up (never, unless a work-group could not run)
+  uint64_t *trace;         // null, or (start, end) s_memrealtime stamps per work item
+  uint32_t trace_cap;
 };
 
-// Work-group shapes. moe_gate_up: four waves, a lane one (row, unit) pair of gate or up, so a wave holds
-// 32 / U rows of both; moe_down: two waves, a lane one (row, unit) pair, 64 / U_down rows a wave.
-constexpr uint32_t kGateUpWG = 256, kDownWG = 128;
-constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kGateUpWG / 64) * (32 / Ug); }
-constexpr uint32_t down_rows(uint32_t Ud) { return (kDownWG / 64) * (64 / Ud); }
-
-__global__ void moe_route(DecodeParams p);
-__global__ void moe_gate_up(DecodeParams p);
-__global__ void moe_down(DecodeParams p);
+__global__ void moe_decode(DecodeParams p);
 
 }  // namespace c0ven

@@ -94,4 +94,56 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   return v;
 }
 
+// DPP lane exchanges (gfx9 controls): quad_perm(1,0,3,2) = lane ^ 1, quad_perm(2,3,0,1) = lane ^ 2,
+// row_half_mirror = 7 - lane within 8, row_mirror = 15 - lane within 16. Each pairs a lane with one in the other half
+// of its 2, 4, 8 or 16, so four steps reduce a row of 16 with every lane holding the result.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, 0xf, 0xf, false);
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
+
+// The wave's largest / smallest u32, wave-uniform.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<kDppXor1>(v));
+  v = max(v, dpp_u32<kDppXor2>(v));
+  v = max(v, dpp_u32<kDppHalfMirror>(v));
+  v = max(v, dpp_u32<kDppMirror>(v));
+  return max(max(readlane_u32(v, 0), readlane_u32(v, 16)), max(readlane_u32(v, 32), readlane_u32(v, 48)));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, dpp_u32<kDppXor1>(v));
+  v = min(v, dpp_u32<kDppXor2>(v));
+  v = min(v, dpp_u32<kDppHalfMirror>(v));
+  v = min(v, dpp_u32<kDppMirror>(v));
+  return min(min(readlane_u32(v, 0), readlane_u32(v, 16)), min(readlane_u32(v, 32), readlane_u32(v, 48)));
+}
+
+template <int kCtrl>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t r = (uint64_t)dpp_u32<kCtrl>((uint32_t)b) | ((uint64_t)dpp_u32<kCtrl>((uint32_t)(b >> 32)) << 32);
+  return __builtin_bit_cast(double, r);
+}
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  return __builtin_bit_cast(double, (uint64_t)readlane_u32((uint32_t)b, l) | ((uint64_t)readlane_u32((uint32_t)(b >> 32), l) << 32));
+}
+// The wave's fp64 sum in one fixed order (butterflies within rows of 16, then the four rows pairwise), wave-uniform.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v = __dadd_rn(v, dpp_f64<kDppXor1>(v));
+  v = __dadd_rn(v, dpp_f64<kDppXor2>(v));
+  v = __dadd_rn(v, dpp_f64<kDppHalfMirror>(v));
+  v = __dadd_rn(v, dpp_f64<kDppMirror>(v));
+  return __dadd_rn(__dadd_rn(readlane_f64(v, 0), readlane_f64(v, 16)), __dadd_rn(readlane_f64(v, 32), readlane_f64(v, 48)));
+}
+// A float's bits as a u32 that orders as the floats do (-0 taken as +0), and back.
+__device__ __forceinline__ uint32_t float_key(float f) {
+  uint32_t u = __float_as_uint(__fadd_rn(f, 0.0f));
+  return u ^ ((u >> 31) ? 0xffffffffu : 0x80000000u);
+}
+__device__ __forceinline__ float key_float(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k); }
+
 }  // namespace c0ven

@@ -41,8 +41,8 @@ struct Layer {
   uint8_t *shared = nullptr;
 };
 
-constexpr int kNumKernels = 3;
-const char *kKernelNames[kNumKernels] = {"moe_route", "moe_gate_up", "moe_down"};
+constexpr int kNumKernels = 1;
+const char *kKernelNames[kNumKernels] = {"moe_decode"};
 
 }  // namespace
 
@@ -56,13 +56,20 @@ struct moe_ctx {
   float *x_dev = nullptr, *y_dev = nullptr, *w_stage = nullptr;
   int32_t *ids_stage = nullptr;
   // Scratch.
-  uint8_t *act_r = nullptr, *act_s = nullptr;
+  uint8_t *act_r = nullptr, *act_s = nullptr, *hact = nullptr;
   float *logits = nullptr, *w = nullptr, *gs = nullptr, *h = nullptr, *y_asg = nullptr;
   int32_t *ids = nullptr;
   MoeGroup *groups = nullptr;
   uint32_t *ngroups = nullptr, *counters = nullptr, *tok_need = nullptr;
-  uint32_t *cnt_route = nullptr, *cnt_tok = nullptr;
+  uint32_t *cnt_route = nullptr, *cnt_topk = nullptr, *cnt_hu = nullptr, *cnt_hq = nullptr, *cnt_tok = nullptr;
+  uint32_t *err_flag = nullptr;
+  uint64_t *flags = nullptr;
+  uint64_t epoch = 0;          // the last launch's number
+  uint32_t grid = 0;           // co-resident work-groups of moe_decode
+  size_t lds = 0;              // its dynamic LDS
   bool timing = false;
+  uint64_t *trace = nullptr;   // per-item stamps of the last forward, when tracing
+  uint32_t trace_cap = 0, trace_bounds[5] = {0, 0, 0, 0, 0}, last_T = 0, last_route = 1;
   std::vector<hipEvent_t> ev;  // (kNumKernels + 1) events per timed forward
   uint32_t ev_used = 0;        // forwards recorded since the last moe_kernel_times
   std::vector<void *> allocs;
@@ -118,6 +125,8 @@ void validate(const moe_config &c) {
   require(!c.has_shared || (quant_gpu_supported(c.sh_gate_type) && quant_gpu_supported(c.sh_down_type)),
           "shared expert types must be Q8_0, Q4_K or IQ3_S");
   require(c.max_tokens <= kMaxDecodeTokens, "max_tokens above 16 needs the prefill path");
+  require((uint64_t)(c.max_tokens ? c.max_tokens : kMaxDecodeTokens) * c.n_embd * 2 <= 64 * 1024,
+          "max_tokens x n_embd bf16 must fit the router's 64 KiB of LDS");
   require(c.swiglu_limit >= 0.0f, "swiglu_limit must be >= 0");
 }
 
@@ -138,8 +147,10 @@ DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   p.act_r = c->act_r, p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
   p.logits = c->logits, p.ids = c->ids, p.w = c->w, p.gs = c->gs;
   p.groups = c->groups, p.ngroups = c->ngroups;
-  p.h = c->h, p.y_asg = c->y_asg;
-  p.cnt_route = c->cnt_route, p.cnt_tok = c->cnt_tok;
+  p.h = c->h, p.hact = c->hact, p.y_asg = c->y_asg;
+  p.flags = c->flags, p.err = c->err_flag;
+  p.cnt_route = c->cnt_route, p.cnt_topk = c->cnt_topk, p.cnt_hu = c->cnt_hu, p.cnt_hq = c->cnt_hq;
+  p.cnt_tok = c->cnt_tok;
   return p;
 }
 
@@ -155,19 +166,17 @@ hipEvent_t *timing_events(moe_ctx *c) {
   return &c->ev[(size_t)c->ev_used++ * (kNumKernels + 1)];
 }
 
-void launch(moe_ctx *c, const DecodeParams &p, uint32_t n_route_wg, hipStream_t s) {
-  const uint32_t G = max_groups(p.T, p.K), Ug = p.H / kUnit, Ud = p.F / kUnit;
-  const uint32_t g_gu = G * (p.F / gate_up_rows(Ug)), g_d = G * (p.H / down_rows(Ud));
-  const size_t lds_gu = (size_t)MOE_GROUP_MAX * Ug * kActLds, lds_d = (size_t)MOE_GROUP_MAX * Ud * kActLds;
+void launch(moe_ctx *c, const DecodeParams &p, hipStream_t s) {
   hipEvent_t *ev = timing_events(c);
+  DecodeParams q = p;
+  q.epoch = ++c->epoch;
+  if (c->trace) q.trace = c->trace, q.trace_cap = c->trace_cap;
+  c->last_T = p.T, c->last_route = p.route;
+  void *args[] = {&q};
   if (ev) check(hipEventRecord(ev[0], s), "hipEventRecord");
-  hipLaunchKernelGGL(moe_route, dim3(n_route_wg), dim3(512), 0, s, p);
+  check(hipLaunchCooperativeKernel((const void *)moe_decode, dim3(c->grid), dim3(kWG), args, c->lds, s),
+        "moe_decode launch");
   if (ev) check(hipEventRecord(ev[1], s), "hipEventRecord");
-  hipLaunchKernelGGL(moe_gate_up, dim3(g_gu), dim3(kGateUpWG), lds_gu, s, p);
-  if (ev) check(hipEventRecord(ev[2], s), "hipEventRecord");
-  hipLaunchKernelGGL(moe_down, dim3(g_d), dim3(kDownWG), lds_d, s, p);
-  if (ev) check(hipEventRecord(ev[3], s), "hipEventRecord");
-  check(hipGetLastError(), "kernel launch");
 }
 
 void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *y, int32_t *ids, float *w,
@@ -177,10 +186,19 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
   require(c->layers[layer].router != nullptr, "the layer's router is not loaded");
   DecodeParams p = base_params(c, layer, T);
   p.x = x, p.y = y;
-  const uint32_t nr = std::max((c->cfg.n_expert + 1 + 15) / 16, T);
-  launch(c, p, nr, s);
+  launch(c, p, s);
   if (ids) check(hipMemcpyAsync(ids, c->ids, sizeof(int32_t) * T * p.K, hipMemcpyDeviceToDevice, s), "copy ids");
   if (w) check(hipMemcpyAsync(w, c->w, sizeof(float) * T * p.K, hipMemcpyDeviceToDevice, s), "copy w");
+}
+
+// A wait inside moe_decode gave up: its result is not to be trusted.
+void check_err(moe_ctx *c) {
+  uint32_t e = 0;
+  check(hipMemcpy(&e, c->err_flag, 4, hipMemcpyDeviceToHost), "read error flag");
+  if (e) {
+    (void)hipMemset(c->err_flag, 0, 4);
+    throw Error(MOE_TIMEOUT, "moe_decode: a work item waited past its limit");
+  }
 }
 
 }  // namespace
@@ -245,12 +263,27 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->ngroups = c->alloc<uint32_t>(1);
     c->tok_need = c->alloc<uint32_t>(T);
     c->h = c->alloc<float>((uint64_t)A * F);
+    c->hact = c->alloc<uint8_t>((uint64_t)A * Ud * kActBytes);
     c->y_asg = c->alloc<float>((uint64_t)A * H);
-    const uint64_t ncnt = 1 + (uint64_t)T * (H / down_rows(Ud));
+    const uint64_t ncnt = 3 + (uint64_t)G * Ud + G + (uint64_t)T * (H / down_rows(Ud));
     c->counters = c->alloc<uint32_t>(ncnt);
     check(hipMemset(c->counters, 0, ncnt * sizeof(uint32_t)), "hipMemset");
     c->cnt_route = c->counters;
-    c->cnt_tok = c->cnt_route + 1;
+    c->cnt_topk = c->cnt_route + 1;
+    c->err_flag = c->cnt_topk + 1;
+    c->cnt_hu = c->err_flag + 1;
+    c->cnt_hq = c->cnt_hu + (uint64_t)G * Ud;
+    c->cnt_tok = c->cnt_hq + G;
+    c->flags = c->alloc<uint64_t>(2 + G);
+    check(hipMemset(c->flags, 0, (2 + G) * sizeof(uint64_t)), "hipMemset");
+    // The grid: every work-group the device holds at once (the launch is cooperative), LDS for the largest stage.
+    c->lds = std::max<size_t>({(size_t)T * H * 2, (size_t)MOE_GROUP_MAX * Ug * kActLds,
+                               (size_t)MOE_GROUP_MAX * Ud * kActLds, (size_t)kWG * 4});
+    int per_cu = 0, ncu = 0;
+    check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, moe_decode, kWG, c->lds), "occupancy");
+    check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, g.device), "CU count");
+    require(per_cu >= 1, "moe_decode does not fit a CU");
+    c->grid = (uint32_t)(per_cu * ncu);
     check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     *out = c;
     return MOE_OK;
@@ -321,6 +354,7 @@ MOE_API moe_status moe_forward(moe_ctx *c, uint32_t layer, const float *x, uint3
     if (route && route->w)
       check(hipMemcpyAsync(route->w, c->w, sizeof(float) * ntok * K, hipMemcpyDeviceToHost, c->stream), "w");
     check(hipStreamSynchronize(c->stream), "forward");
+    check_err(c);
   });
 }
 
@@ -391,16 +425,20 @@ MOE_API moe_status moe_forward_experts(moe_ctx *c, const moe_job *jobs, uint32_t
     p.xact_s = g.has_shared ? quant_vec_dot_type(g.sh_gate_type) : p.xact_r;
     p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
     p.x = c->x_dev, p.y = c->y_dev;
-    if (ng) launch(c, p, ntok, s);
+    if (ng) launch(c, p, s);
     check(hipMemcpy2DAsync(y, y_stride * sizeof(float), c->y_dev, H * sizeof(float), H * sizeof(float), ntok,
                            hipMemcpyDeviceToHost, s),
           "download y");
     check(hipStreamSynchronize(s), "forward_experts");
+    check_err(c);
   });
 }
 
 MOE_API moe_status moe_sync(moe_ctx *c) {
-  return guarded(c, [&] { check(hipStreamSynchronize(c->stream), "hipStreamSynchronize"); });
+  return guarded(c, [&] {
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    check_err(c);
+  });
 }
 
 MOE_API void *moe_stream(moe_ctx *c) { return c ? (void *)c->stream : nullptr; }
@@ -434,6 +472,39 @@ MOE_API moe_status moe_kernel_times(moe_ctx *c, const char **names, float *avg_m
       *n = (uint32_t)i + 1;
     }
     c->ev_used = 0;
+  });
+}
+
+MOE_API moe_status moe_set_trace(moe_ctx *c, int on) {
+  return guarded(c, [&] {
+    if (on && !c->trace) {
+      c->trace_cap = 1u << 16;
+      c->trace = c->alloc<uint64_t>((uint64_t)3 * c->trace_cap * 2);
+    } else if (!on && c->trace) {
+      check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+      c->trace = nullptr;  // the buffer stays with the context's allocations
+    }
+  });
+}
+
+MOE_API moe_status moe_trace(moe_ctx *c, uint64_t *stamps, uint32_t cap, uint32_t *n, uint32_t *bounds) {
+  return guarded(c, [&] {
+    require(n != nullptr, "null n");
+    require(c->trace != nullptr, "tracing is off");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    uint32_t ng = 0;
+    check(hipMemcpy(&ng, c->ngroups, 4, hipMemcpyDeviceToHost), "read ngroups");
+    const moe_config &g = c->cfg;
+    const uint32_t T = c->last_T, Ug = g.n_embd / kUnit, Ud = g.n_ff / kUnit;
+    const uint32_t nL = c->last_route ? std::max((g.n_expert + kRouteRows) / kRouteRows, T) : T;
+    const uint32_t b1 = nL + (c->last_route ? T : 0), b2 = b1 + ng * (g.n_ff / gate_up_rows(Ug));
+    const uint32_t end = b2 + ng * (g.n_embd / down_rows(Ud));
+    const uint32_t bb[5] = {0, nL, b1, b2, end};
+    if (bounds) std::memcpy(bounds, bb, sizeof bb);
+    *n = std::min(end, c->trace_cap);
+    if (stamps)
+      check(hipMemcpy(stamps, c->trace, sizeof(uint64_t) * 2 * std::min(cap, *n), hipMemcpyDeviceToHost),
+            "download trace");
   });
 }
 

@@ -122,6 +122,12 @@ MOE_API moe_status moe_set_timing(moe_ctx *ctx, int on);
 MOE_API moe_status moe_kernel_times(moe_ctx *ctx, const char **names, float *avg_ms, uint32_t cap, uint32_t *n,
                                     uint32_t *forwards);
 
+/* Tracing: while on, the decode kernel stamps the start and end of every work item (s_memrealtime, a 100 MHz clock).
+ * moe_trace gives the last forward's stamps as (start, end) pairs in item order, up to cap pairs; n receives the
+ * number of items, bounds (5 entries, or null) where each kind begins: router, top-k, gate/up, down, and the end. */
+MOE_API moe_status moe_set_trace(moe_ctx *ctx, int on);
+MOE_API moe_status moe_trace(moe_ctx *ctx, uint64_t *stamps, uint32_t cap, uint32_t *n, uint32_t *bounds);
+
 /* Copies the resident experts (and shared expert) of src_layer over those of dst_layer, device to device. */
 MOE_API moe_status moe_copy_experts(moe_ctx *ctx, uint32_t src_layer, uint32_t dst_layer);
 /* Bytes of one resident matrix in the device layout: which = 0 routed gate (up is the same), 1 routed down,
