@@ -24,7 +24,7 @@ __device__ __constant__ static const uint64_t kExp2Tab[32] = {
 // cubic, all in double, rounded once to float. The fused multiply-adds are where the FMA build fuses; with them the
 // result equals the host's expf on all 2^32 inputs (checked on the CPU by tests/test_expf.py's exhaustive run and on
 // the GPU against the host by tests/test_gpu_parity.py).
-__device__ __forceinline__ float expf_libm(float x) {
+__device__ __forceinline__ float expf_libm(float x, const uint64_t *tab = kExp2Tab) {
   const uint32_t ux = __float_as_uint(x);
   const uint32_t abstop = (ux >> 20) & 0x7ffu;
   if (abstop >= 0x42bu) {  // |x| >= 88, infinity or NaN
@@ -41,7 +41,7 @@ __device__ __forceinline__ float expf_libm(float x) {
   const uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd = __dsub_rn(kd, Shift);
   const double r = __builtin_fma(InvLn2N, xd, -kd);
-  const uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+  const uint64_t t = tab[ki % 32] + (ki << 47);
   const double s = __longlong_as_double((long long)t);
   const double z = __builtin_fma(C0, r, C1);
   const double r2 = __dmul_rn(r, r);
@@ -52,16 +52,18 @@ __device__ __forceinline__ float expf_libm(float x) {
 }
 
 // silu(g) * u with the optional clamp, each step rounded as the CPU path's g / (1 + expf(-g)) * u.
-__device__ __forceinline__ float swiglu_one(float g, float u, float limit) {
+__device__ __forceinline__ float swiglu_one(float g, float u, float limit, const uint64_t *tab = kExp2Tab) {
   if (limit > 0.0f) {
     g = fminf(g, limit);
     u = u < -limit ? -limit : (u > limit ? limit : u);
   }
-  const float den = __fadd_rn(1.0f, expf_libm(-g));
+  const float den = __fadd_rn(1.0f, expf_libm(-g, tab));
   return __fmul_rn(__fdiv_rn(g, den), u);
 }
 
-__device__ __forceinline__ float sigmoid_libm(float z) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_libm(-z))); }
+__device__ __forceinline__ float sigmoid_libm(float z, const uint64_t *tab = kExp2Tab) {
+  return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_libm(-z, tab)));
+}
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }

@@ -150,7 +150,7 @@ __device__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, ui
 // Top-k, weights and the shared gate for token t, by one wave (route.h:39-99 and layer.cl:765-804 restated): lane l
 // holds experts l + 64 i, sorted by (logit, lower id first); each of the k rounds takes the wave's largest head
 // (a DPP max of the logit keys, a ballot for equal keys, the lower id among them) and pops it.
-__device__ void route_token(const DecodeParams &p, uint32_t t) {
+__device__ void route_token(const DecodeParams &p, uint32_t t, const uint64_t *tab) {
   const uint32_t lane = lane_id(), E = p.E, K = p.K;
   const float *lg = p.logits + (uint64_t)t * (E + 1);
   constexpr int kPer = kMaxExperts / 64;
@@ -168,7 +168,7 @@ __device__ void route_token(const DecodeParams &p, uint32_t t) {
   double part = 0.0;
 #pragma unroll
   for (int i = 0; i < kPer; i++)
-    if (lane + 64 * i < E) part = __dadd_rn(part, (double)expf_libm(__fsub_rn(key_float(key[i]), mx)));
+    if (lane + 64 * i < E) part = __dadd_rn(part, (double)expf_libm(__fsub_rn(key_float(key[i]), mx), tab));
   const float inv = (float)(1.0 / wave_sum_f64(part));
   // Sort each lane's keys, largest first (ids ascending within a lane, so equal keys keep the lower id first).
   auto cswap = [&](int i, int j) {
@@ -197,7 +197,7 @@ __device__ void route_token(const DecodeParams &p, uint32_t t) {
       key[kPer - 1] = 0;
     }
   }
-  const float pk = lane < K ? __fmul_rn(expf_libm(__fsub_rn(key_float(my_key), mx)), inv) : 0.0f;
+  const float pk = lane < K ? __fmul_rn(expf_libm(__fsub_rn(key_float(my_key), mx), tab), inv) : 0.0f;
   float tot = 0.0f;
   for (uint32_t r = 0; r < K; r++) tot = __fadd_rn(tot, __uint_as_float(readlane_u32(__float_as_uint(pk), r)));
   const float den = fmaxf(tot, 6.1035e-5f);
@@ -205,7 +205,7 @@ __device__ void route_token(const DecodeParams &p, uint32_t t) {
     st_co(p.ids + t * K + lane, (int32_t)my_id);
     st_co(p.w + t * K + lane, __fdiv_rn(pk, den));
   }
-  if (lane == 0) st_co(p.gs + t, sigmoid_libm(ld_co(lg + E)));
+  if (lane == 0) st_co(p.gs + t, sigmoid_libm(ld_co(lg + E), tab));
 }
 
 // Group g's matrix (0 gate, 1 up, 2 down) and its type.
@@ -237,15 +237,19 @@ __device__ __forceinline__ void load_grid(uint32_t *grid_lds) {
   for (uint32_t i = threadIdx.x; i < 512; i += kWG) grid_lds[i] = kIq3sGridDev[i];
 }
 
-// The n terms of one (row, unit) pair against the activation units act + j * kActLds / 4 dwords, into t[j].
+// The n terms of one (row, unit) pair against the activation units act + j * stride dwords, into t[j]. The unit's
+// weights are loaded first; `ready` (run by the whole work-group) then makes the activations available, so the
+// weights' HBM latency overlaps whatever ready waits for.
+template <typename Ready>
 __device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, uint32_t idx, uint32_t nl,
-                                           const uint32_t *grid_lds, const uint32_t *act, uint32_t stride, uint32_t n,
-                                           float *t) {
+                                           const uint32_t *grid_lds, const uint32_t *act, uint32_t stride,
+                                           const uint32_t &n, float *t, Ready ready) {
   switch (type) {
     case QT_Q8_0: {
       UnitQ8_0 w;
       w.load(tile, idx, nl);
-      #pragma unroll
+      ready();
+#pragma unroll
       for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
         if (j < n) t[j] = w.term(Act(act + j * stride));
       break;
@@ -253,7 +257,8 @@ __device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, u
     case QT_Q4_K: {
       UnitQ4_K w;
       w.load(tile, idx, nl);
-      #pragma unroll
+      ready();
+#pragma unroll
       for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
         if (j < n) t[j] = w.term(Act(act + j * stride));
       break;
@@ -261,7 +266,8 @@ __device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, u
     default: {
       UnitIQ3_S w;
       w.load(tile, idx, nl, grid_lds);
-      #pragma unroll
+      ready();
+#pragma unroll
       for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
         if (j < n) t[j] = w.term(Act(act + j * stride));
       break;
@@ -425,26 +431,30 @@ __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *un
 
 // Gate and up of rows blk * gate_up_rows .. of group g: lane = m * 32 + r * U + u; h = silu(g) * u per row.
 __device__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
-                             GroupLds *sg, uint32_t *s_flag) {
+                             GroupLds *sg, uint32_t *s_flag, const uint64_t *tab) {
   read_group(p, g, sg);
   const uint32_t U = p.H / kUnit, rows = gate_up_rows(U), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 0);
-  stage_act(gm.shared ? p.act_s : p.act_r, sg->tok, n, U, lds);
-  if (gm.type == QT_IQ3_S) load_grid(grid_lds);
-  __syncthreads();
+  if (gm.type == QT_IQ3_S) {
+    load_grid(grid_lds);
+    __syncthreads();
+  }
   const uint32_t lane = lane_id(), m = lane / 32, r = (lane % 32) / U, u = lane % U;
   const uint32_t row = row0 + wave_id() * (32 / U) + r;
   const uint8_t *mat = gm.mat + (m ? (gm.shared ? p.sh_up_off : p.ex_up_off) : 0);
   const uint8_t *tile = mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
   float t[MOE_GROUP_MAX];
   pair_terms(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
-             (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t);
+             (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
+               stage_act(gm.shared ? p.act_s : p.act_r, sg->tok, n, U, lds);
+               __syncthreads();
+             });
 #pragma unroll
   for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
     if (j >= n) break;
     const float s = row_sum(t[j], U);        // gate's row sum in lanes m = 0, up's in m = 1
     const float su = __shfl_xor(s, 32, 64);  // the other matrix's
-    if (m == 0 && u == 0) st_co(p.h + (uint64_t)sg->asg[j] * p.F + row, swiglu_one(s, su, p.swiglu_limit));
+    if (m == 0 && u == 0) st_co(p.h + (uint64_t)sg->asg[j] * p.F + row, swiglu_one(s, su, p.swiglu_limit, tab));
   }
   // The last item of these 256 rows quantises them, one unit of the down's K per assignment, a half-wave each; the
   // last unit of the group sets its flag.
@@ -465,19 +475,23 @@ __device__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, ui
 // Down rows blk * down_rows .. of group g (lane = r * U + u), then the combine of every token this item completes.
 __device__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
                           GroupLds *sg, uint32_t *s_last) {
-  wait_flag(p, kFlagH + g);
   read_group(p, g, sg);
   const uint32_t U = p.F / kUnit, rows = down_rows(U), row0 = blk * rows, n = sg->n, nblk = p.H / rows;
   const GroupMat gm = group_mat(p, sg->slot, 2);
-  stage_act(p.hact, sg->asg, n, U, lds);
-  if (gm.type == QT_IQ3_S) load_grid(grid_lds);
-  __syncthreads();
+  if (gm.type == QT_IQ3_S) {
+    load_grid(grid_lds);
+    __syncthreads();
+  }
   const uint32_t lane = lane_id(), r = lane / U, u = lane % U;
   const uint32_t row = row0 + wave_id() * (64 / U) + r;
   const uint8_t *tile = gm.mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
   float t[MOE_GROUP_MAX];
   pair_terms(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
-             (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t);
+             (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
+               wait_flag(p, kFlagH + g);  // the weights are already on their way
+               stage_act(p.hact, sg->asg, n, U, lds);
+               __syncthreads();
+             });
 #pragma unroll
   for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
     if (j >= n) break;
@@ -531,6 +545,9 @@ __global__ void __launch_bounds__(kWG) moe_decode(DecodeParams p) {
   __shared__ uint32_t s_head[kWG];
   __shared__ uint32_t s_flag, s_ng, s_last[MOE_GROUP_MAX];
   __shared__ GroupLds sg;
+  __shared__ uint64_t exp_tab[32];  // expf's table, read at LDS latency
+  if (threadIdx.x < 32) exp_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
   const uint32_t T = p.T, E = p.E, Ug = p.H / kUnit, Ud = p.F / kUnit;
   const uint32_t nL = p.route ? max((E + kRouteRows) / kRouteRows, T) : T, nTop = p.route ? T : 0, B1 = nL + nTop;
   const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud);
@@ -553,13 +570,13 @@ __global__ void __launch_bounds__(kWG) moe_decode(DecodeParams p) {
       if (arrive_last(p.cnt_route, nL, &s_flag)) set_flag(p, p.route ? kFlagLogits : kFlagRouted);
     } else if (it < B1) {
       wait_flag(p, kFlagLogits);
-      if (wave_id() == 0) route_token(p, it - nL);
+      if (wave_id() == 0) route_token(p, it - nL, exp_tab);
       if (arrive_last(p.cnt_topk, T, &s_flag)) {
         make_groups(p, (int32_t *)lds, s_head);
         set_flag(p, kFlagRouted);
       }
     } else if (it < B1 + ng * nGU) {
-      gate_up_item(p, (it - B1) / nGU, (it - B1) % nGU, lds, grid_lds, &sg, &s_flag);
+      gate_up_item(p, (it - B1) / nGU, (it - B1) % nGU, lds, grid_lds, &sg, &s_flag, exp_tab);
     } else {
       const uint32_t i = it - B1 - ng * nGU;
       down_item(p, i / nD, i % nD, lds, grid_lds, &sg, s_last);
