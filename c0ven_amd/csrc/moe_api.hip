@@ -172,10 +172,9 @@ void launch(moe_ctx *c, const DecodeParams &p, hipStream_t s) {
   q.epoch = ++c->epoch;
   if (c->trace) q.trace = c->trace, q.trace_cap = c->trace_cap;
   c->last_T = p.T, c->last_route = p.route;
-  void *args[] = {&q};
   if (ev) check(hipEventRecord(ev[0], s), "hipEventRecord");
-  check(hipLaunchCooperativeKernel((const void *)moe_decode, dim3(c->grid), dim3(kWG), args, c->lds, s),
-        "moe_decode launch");
+  hipLaunchKernelGGL(moe_decode, dim3(c->grid), dim3(kWG), c->lds, s, q);
+  check(hipGetLastError(), "moe_decode launch");
   if (ev) check(hipEventRecord(ev[1], s), "hipEventRecord");
 }
 
@@ -276,7 +275,8 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->cnt_tok = c->cnt_hq + G;
     c->flags = c->alloc<uint64_t>(2 + G);
     check(hipMemset(c->flags, 0, (2 + G) * sizeof(uint64_t)), "hipMemset");
-    // The grid: every work-group the device holds at once (the launch is cooperative), LDS for the largest stage.
+    // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
+    // stage.
     c->lds = std::max<size_t>({(size_t)T * H * 2, (size_t)MOE_GROUP_MAX * Ug * kActLds,
                                (size_t)MOE_GROUP_MAX * Ud * kActLds, (size_t)kWG * 4});
     int per_cu = 0, ncu = 0;
