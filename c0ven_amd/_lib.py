@@ -70,6 +70,7 @@ _SIGS = {
     "moe_copy_experts": (_i32, [_P, _u32, _u32]),
     "moe_set_trace": (_i32, [_P, C.c_int]),
     "moe_trace": (_i32, [_P, _P, _u32, C.POINTER(_u32), _P]),
+    "moe_grid": (_u32, [_P]),
     "moe_expert_bytes": (_i32, [_P, _u32, C.POINTER(_u64)]),
     "moe_device_bytes": (_u64, [_P]),
     "moe_dequantize": (_i32, [_P, _u32, _P, _u32, _u32, _P]),
@@ -227,14 +228,17 @@ class MoeBlock:
         self._check(lib.moe_set_trace(self.h, 1 if on else 0))
 
     def trace(self):
-        """The last forward's (start, end) s_memrealtime stamps (100 MHz) per work item, and where the router,
-        top-k, gate/up and down items begin (plus the end)."""
+        """The last forward's (start, ready, computed, end) s_memrealtime stamps (100 MHz) per work item, and where
+        the lead (router), top-k, gate/up and down items begin (plus the end)."""
         n = C.c_uint32()
         bounds = np.zeros(5, dtype=np.uint32)
         self._check(lib.moe_trace(self.h, None, 0, C.byref(n), _ptr(bounds)))
-        out = np.zeros((n.value, 2), dtype=np.uint64)
+        out = np.zeros((n.value, 4), dtype=np.uint64)
         self._check(lib.moe_trace(self.h, _ptr(out), n.value, C.byref(n), _ptr(bounds)))
         return out, bounds
+
+    def grid(self):
+        return int(lib.moe_grid(self.h))
 
     def copy_experts(self, src_layer, dst_layer):
         self._check(lib.moe_copy_experts(self.h, src_layer, dst_layer))

@@ -16,16 +16,23 @@ constexpr uint32_t kMaxUnits = 32;         // 256-value units per row: H and F u
 constexpr uint32_t max_groups(uint32_t T, uint32_t K) { return T * K + (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX; }
 
 // The work-group (four waves) and the work items of moe_decode, in the order every work-group walks them:
-//   router items   kRouteRows router rows each (2 a wave); item t < T also quantises x[t];
+//   lead items     kRouteRows router rows each (two waves a row), when routing; item t < T also quantises x[t];
 //   top-k items    one a token (when routing);
 //   gate/up items  gate_up_rows(U) rows of gate and of up of one group, all units (lane = m * 32 + r * U + u);
 //   down items     down_rows(U_down) rows of down of one group, all units (lane = r * U_down + u).
-constexpr uint32_t kWG = 256, kRouteRows = 8;
+constexpr uint32_t kWG = 256, kRouteRows = 2;
+constexpr uint32_t lead_items(uint32_t T, uint32_t E, uint32_t route) {
+  return route ? ((E + kRouteRows) / kRouteRows > T ? (E + kRouteRows) / kRouteRows : T) : T;
+}
+constexpr uint32_t kMaxLeadItems = (kMaxExperts + kRouteRows) / kRouteRows;
+// LDS the grouping step takes from the dynamic allocation: T K ids, a token mask and two group numbers per expert.
+constexpr uint32_t kGroupingLds = kMaxDecodeTokens * kMaxUsed * 4 + kMaxExperts * 4 + kMaxExperts * 2 * 4;
 constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kWG / 64) * (32 / Ug); }
 constexpr uint32_t down_rows(uint32_t Ud) { return (kWG / 64) * (64 / Ud); }
 
-// Flags (64-bit, set to the launch's epoch): [0] the logits are in, [1] the groups are in, [2 + g] group g's h is in.
-constexpr uint32_t kFlagLogits = 0, kFlagRouted = 1, kFlagH = 2;
+// Flags (64-bit, set to the launch's epoch): [i < kMaxLeadItems] lead item i is done (its logits and quantised x are
+// in), [kFlagRouted] the groups are in, [kFlagH + g] group g's h is in.
+constexpr uint32_t kFlagLead = 0, kFlagRouted = kMaxLeadItems, kFlagH = kMaxLeadItems + 1;
 
 struct DecodeParams {
   uint32_t H, F, E, K, T;
@@ -57,14 +64,14 @@ struct DecodeParams {
   float *h;                // (T K + T) x F: SwiGLU of each assignment, fp32
   uint8_t *hact;           // (T K + T) x (F / 256) activation units: h quantised to the down's type
   float *y_asg;            // (T K + T) x H: each assignment's expert output
-  uint64_t *flags;         // 2 + G
-  uint32_t *cnt_route;     // 1: router items in
+  uint64_t *flags;         // kFlagH + G
+  uint32_t *cnt_route;     // 1: lead items in (pre-routed calls)
   uint32_t *cnt_topk;      // 1: tokens routed
   uint32_t *cnt_hu;        // G x (F / 256): gate/up items in per (group, unit of h)
   uint32_t *cnt_hq;        // G: units of h quantised per group
   uint32_t *cnt_tok;       // T x (H / down_rows): outputs in per (token, down row block)
   uint32_t *err;           // set when a wait gave up (never, unless a work-group could not run)
-  uint64_t *trace;         // null, or (start, end) s_memrealtime stamps per work item
+  uint64_t *trace;         // null, or (start, ready, computed, end) s_memrealtime stamps per work item
   uint32_t trace_cap;
 };
 

@@ -273,12 +273,12 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->cnt_hu = c->err_flag + 1;
     c->cnt_hq = c->cnt_hu + (uint64_t)G * Ud;
     c->cnt_tok = c->cnt_hq + G;
-    c->flags = c->alloc<uint64_t>(2 + G);
-    check(hipMemset(c->flags, 0, (2 + G) * sizeof(uint64_t)), "hipMemset");
+    c->flags = c->alloc<uint64_t>(kFlagH + G);
+    check(hipMemset(c->flags, 0, (kFlagH + G) * sizeof(uint64_t)), "hipMemset");
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
     c->lds = std::max<size_t>({(size_t)T * H * 2, (size_t)MOE_GROUP_MAX * Ug * kActLds,
-                               (size_t)MOE_GROUP_MAX * Ud * kActLds, (size_t)kWG * 4});
+                               (size_t)MOE_GROUP_MAX * Ud * kActLds, kGroupingLds});
     int per_cu = 0, ncu = 0;
     check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, moe_decode, kWG, c->lds), "occupancy");
     check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, g.device), "CU count");
@@ -475,11 +475,13 @@ MOE_API moe_status moe_kernel_times(moe_ctx *c, const char **names, float *avg_m
   });
 }
 
+MOE_API uint32_t moe_grid(const moe_ctx *c) { return c ? c->grid : 0; }
+
 MOE_API moe_status moe_set_trace(moe_ctx *c, int on) {
   return guarded(c, [&] {
     if (on && !c->trace) {
       c->trace_cap = 1u << 16;
-      c->trace = c->alloc<uint64_t>((uint64_t)3 * c->trace_cap * 2);
+      c->trace = c->alloc<uint64_t>((uint64_t)4 * c->trace_cap);
     } else if (!on && c->trace) {
       check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
       c->trace = nullptr;  // the buffer stays with the context's allocations
@@ -496,14 +498,14 @@ MOE_API moe_status moe_trace(moe_ctx *c, uint64_t *stamps, uint32_t cap, uint32_
     check(hipMemcpy(&ng, c->ngroups, 4, hipMemcpyDeviceToHost), "read ngroups");
     const moe_config &g = c->cfg;
     const uint32_t T = c->last_T, Ug = g.n_embd / kUnit, Ud = g.n_ff / kUnit;
-    const uint32_t nL = c->last_route ? std::max((g.n_expert + kRouteRows) / kRouteRows, T) : T;
+    const uint32_t nL = lead_items(T, g.n_expert, c->last_route);
     const uint32_t b1 = nL + (c->last_route ? T : 0), b2 = b1 + ng * (g.n_ff / gate_up_rows(Ug));
     const uint32_t end = b2 + ng * (g.n_embd / down_rows(Ud));
     const uint32_t bb[5] = {0, nL, b1, b2, end};
     if (bounds) std::memcpy(bounds, bb, sizeof bb);
     *n = std::min(end, c->trace_cap);
     if (stamps)
-      check(hipMemcpy(stamps, c->trace, sizeof(uint64_t) * 2 * std::min(cap, *n), hipMemcpyDeviceToHost),
+      check(hipMemcpy(stamps, c->trace, sizeof(uint64_t) * 4 * std::min(cap, *n), hipMemcpyDeviceToHost),
             "download trace");
   });
 }

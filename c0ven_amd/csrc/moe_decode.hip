@@ -3,10 +3,10 @@
 // Replaces the reference's decode kernel list for the block (model.cpp:1348-1414): the router's bf16 GEMV
 // (mv_xmx_bf16), router_group (layer.cl:984-1023), moe_gate_up_g (moe.cl:230-302), moe_down_g (moe.cl:416-471) and
 // moe_combine (layer.cl:869-884). Every work-group walks the work items b, b + grid, b + 2 grid, ... in one order
-// (decode.h): router items, top-k items, gate/up items, down items. An item that needs earlier work waits on a flag
-// the last contributor of that work sets (to this launch's epoch):
-//   - the last router item in: the logits are in (top-k items wait on it);
-//   - the last top-k item in: groups the assignments into MoeGroups and sets "routed" (gate/up items wait on it);
+// (decode.h): lead items (router rows; x quantised), top-k items, gate/up items, down items. An item that needs earlier
+// work waits on flags set (to this launch's epoch) by the work it needs:
+//   - each lead item sets its own flag; a top-k item waits for all of them (no counter the lead items contend on);
+//   - the last top-k item in groups the assignments into MoeGroups and sets "routed" (gate/up items wait on it);
 //   - the last gate/up item of a 256-row unit of group g quantises that unit of h for the down; the last unit sets
 //     group g's flag (its down items wait on it);
 //   - the last down item of a (token, row block) to finish combines that token's rows: sum_k w_k y_k + gs s.
@@ -92,6 +92,29 @@ __device__ __forceinline__ void wait_flag(const DecodeParams &p, uint32_t i) {
   __syncthreads();
 }
 
+// Waits until flags base .. base + count - 1 (count <= kMaxLeadItems) all hold this launch's epoch (wave 0 polls,
+// a flag a lane, all loads of a round in flight together; the work-group follows).
+__device__ __forceinline__ void wait_flags(const DecodeParams &p, uint32_t base, uint32_t count) {
+  if (wave_id() == 0) {
+    uint32_t n = 0;
+    for (;;) {
+      bool ok = true;
+#pragma unroll
+      for (uint32_t i = 0; i < (kMaxLeadItems + 63) / 64; i++) {
+        const uint32_t f = lane_id() + 64 * i;
+        if (f < count) ok &= ld_co(p.flags + base + f) == p.epoch;
+      }
+      if (__all(ok)) break;
+      __builtin_amdgcn_s_sleep(1);
+      if (++n == kSpinLimit) {
+        if (lane_id() == 0) st_co(p.err, 1u);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
 // One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
 // with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0).
 __device__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
@@ -149,65 +172,80 @@ __device__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, ui
   }
 }
 
-// Top-k, weights and the shared gate for token t, by one wave (route.h:39-99 and layer.cl:765-804 restated): lane l
-// holds experts l + 64 i, sorted by (logit, lower id first); each of the k rounds takes the wave's largest head
-// (a DPP max of the logit keys, a ballot for equal keys, the lower id among them) and pops it.
-__device__ void route_token(const DecodeParams &p, uint32_t t, const uint64_t *tab) {
+// Top-k, weights and the shared gate for token t (route.h:39-99 and layer.cl:765-804 restated). Two waves at once:
+// wave 1 takes the softmax's max and 1 / sum (the sum in double) and the shared gate; wave 0 selects: lane l holds
+// experts l + 64 i, sorted by (logit, lower id first), and each of the k rounds takes the wave's largest head (a DPP
+// max of the logit keys, a ballot for equal keys, the lower id among them) and pops it. Then wave 0 turns the k
+// winners into weights. The winners' ids and keys stay in sel (sel[j], sel[kMaxUsed + j]) for the grouping.
+__device__ void route_token(const DecodeParams &p, uint32_t t, const uint64_t *tab, uint32_t *sel, float *norm) {
   const uint32_t lane = lane_id(), E = p.E, K = p.K;
   const float *lg = p.logits + (uint64_t)t * (E + 1);
   constexpr int kPer = kMaxExperts / 64;
-  uint32_t key[kPer], id[kPer];
-  float mxl = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kPer; i++) {
-    const uint32_t e = lane + 64 * i;
-    const float v = e < E ? ld_co(lg + e) : -INFINITY;
-    mxl = fmaxf(mxl, v);
-    key[i] = e < E ? float_key(v) : 0u;
-    id[i] = e;
-  }
-  const float mx = key_float(wave_max_u32(float_key(mxl)));
-  double part = 0.0;
-#pragma unroll
-  for (int i = 0; i < kPer; i++)
-    if (lane + 64 * i < E) part = __dadd_rn(part, (double)expf_libm(__fsub_rn(key_float(key[i]), mx), tab));
-  const float inv = (float)(1.0 / wave_sum_f64(part));
-  // Sort each lane's keys, largest first (ids ascending within a lane, so equal keys keep the lower id first).
-  auto cswap = [&](int i, int j) {
-    const bool sw = key[j] > key[i] || (key[j] == key[i] && id[j] < id[i]);
-    const uint32_t ki = key[i], ii = id[i];
-    key[i] = sw ? key[j] : ki, id[i] = sw ? id[j] : ii;
-    key[j] = sw ? ki : key[j], id[j] = sw ? ii : id[j];
-  };
-  cswap(0, 1), cswap(2, 3), cswap(4, 5), cswap(6, 7), cswap(0, 2), cswap(1, 3), cswap(4, 6), cswap(5, 7);
-  cswap(1, 2), cswap(5, 6), cswap(0, 4), cswap(3, 7), cswap(1, 5), cswap(2, 6), cswap(1, 4), cswap(3, 6);
-  cswap(2, 4), cswap(3, 5), cswap(3, 4);
   uint32_t my_id = 0, my_key = 0;
-  for (uint32_t r = 0; r < K; r++) {
-    const uint32_t m = wave_max_u32(key[0]);
-    const uint64_t cand = __ballot(key[0] == m);
-    uint32_t wid;
-    if (__popcll(cand) == 1) {
-      wid = readlane_u32(id[0], __ffsll((long long)cand) - 1);
-    } else {
-      wid = wave_min_u32(key[0] == m ? id[0] : 0xffffffffu);
-    }
-    if (lane == r) my_id = wid, my_key = m;
-    if (key[0] == m && id[0] == wid) {  // pop the winner
+  if (wave_id() <= 1) {
+    uint32_t key[kPer], id[kPer];
 #pragma unroll
-      for (int i = 0; i < kPer - 1; i++) key[i] = key[i + 1], id[i] = id[i + 1];
-      key[kPer - 1] = 0;
+    for (int i = 0; i < kPer; i++) {
+      const uint32_t e = lane + 64 * i;
+      key[i] = e < E ? float_key(ld_co(lg + e)) : 0u;
+      id[i] = e;
+    }
+    if (wave_id() == 1) {
+      uint32_t mk = 0;
+#pragma unroll
+      for (int i = 0; i < kPer; i++) mk = max(mk, key[i]);
+      const float mx = key_float(wave_max_u32(mk));
+      double part = 0.0;
+#pragma unroll
+      for (int i = 0; i < kPer; i++)
+        if (lane + 64 * i < E) part = __dadd_rn(part, (double)expf_libm(__fsub_rn(key_float(key[i]), mx), tab));
+      const double sum = wave_sum_f64(part);
+      if (lane == 0) {
+        norm[0] = mx;
+        norm[1] = (float)(1.0 / sum);
+        st_co(p.gs + t, sigmoid_libm(ld_co(lg + E), tab));
+      }
+    } else {
+      // Sort each lane's keys, largest first (ids ascending within a lane, so equal keys keep the lower id first).
+      auto cswap = [&](int i, int j) {
+        const bool sw = key[j] > key[i] || (key[j] == key[i] && id[j] < id[i]);
+        const uint32_t ki = key[i], ii = id[i];
+        key[i] = sw ? key[j] : ki, id[i] = sw ? id[j] : ii;
+        key[j] = sw ? ki : key[j], id[j] = sw ? ii : id[j];
+      };
+      cswap(0, 1), cswap(2, 3), cswap(4, 5), cswap(6, 7), cswap(0, 2), cswap(1, 3), cswap(4, 6), cswap(5, 7);
+      cswap(1, 2), cswap(5, 6), cswap(0, 4), cswap(3, 7), cswap(1, 5), cswap(2, 6), cswap(1, 4), cswap(3, 6);
+      cswap(2, 4), cswap(3, 5), cswap(3, 4);
+      for (uint32_t r = 0; r < K; r++) {
+        const uint32_t m = wave_max_u32(key[0]);
+        const uint64_t cand = __ballot(key[0] == m);
+        uint32_t wid;
+        if (__popcll(cand) == 1) {
+          wid = readlane_u32(id[0], __ffsll((long long)cand) - 1);
+        } else {
+          wid = wave_min_u32(key[0] == m ? id[0] : 0xffffffffu);
+        }
+        if (lane == r) my_id = wid, my_key = m;
+        if (key[0] == m && id[0] == wid) {  // pop the winner
+#pragma unroll
+          for (int i = 0; i < kPer - 1; i++) key[i] = key[i + 1], id[i] = id[i + 1];
+          key[kPer - 1] = 0;
+        }
+      }
+      if (lane < K) sel[lane] = my_id, sel[kMaxUsed + lane] = my_key;
     }
   }
-  const float pk = lane < K ? __fmul_rn(expf_libm(__fsub_rn(key_float(my_key), mx), tab), inv) : 0.0f;
-  float tot = 0.0f;
-  for (uint32_t r = 0; r < K; r++) tot = __fadd_rn(tot, __uint_as_float(readlane_u32(__float_as_uint(pk), r)));
-  const float den = fmaxf(tot, 6.1035e-5f);
-  if (lane < K) {
-    st_co(p.ids + t * K + lane, (int32_t)my_id);
-    st_co(p.w + t * K + lane, __fdiv_rn(pk, den));
+  __syncthreads();
+  if (wave_id() == 0) {
+    const float pk = lane < K ? __fmul_rn(expf_libm(__fsub_rn(key_float(my_key), norm[0]), tab), norm[1]) : 0.0f;
+    float tot = 0.0f;
+    for (uint32_t r = 0; r < K; r++) tot = __fadd_rn(tot, __uint_as_float(readlane_u32(__float_as_uint(pk), r)));
+    const float den = fmaxf(tot, 6.1035e-5f);
+    if (lane < K) {
+      st_co(p.ids + t * K + lane, (int32_t)my_id);
+      st_co(p.w + t * K + lane, __fdiv_rn(pk, den));
+    }
   }
-  if (lane == 0) st_co(p.gs + t, sigmoid_libm(ld_co(lg + E), tab));
 }
 
 // Group g's matrix (0 gate, 1 up, 2 down) and its type.
@@ -304,94 +342,130 @@ __device__ void quantise_x(const DecodeParams &p, uint32_t t) {
   }
 }
 
-// Router rows (2 a wave) of item i: logit = sum of bf16(W) bf16(x), each product exact, summed in fp64 (a lane's
-// share, then the wave's in a fixed order), rounded once, plus the bias. x is staged as bf16 in xb.
-__device__ void router_rows(const DecodeParams &p, uint32_t item, uint16_t *xb) {
-  const uint32_t lane = lane_id(), H = p.H, T = p.T, E = p.E, NW = H / 512;
-  for (uint32_t i = threadIdx.x; i < T * H / 8; i += kWG) {  // x -> bf16 in LDS, 8 values a step
-    const float4 a = ((const float4 *)p.x)[2 * i], b = ((const float4 *)p.x)[2 * i + 1];
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint32_t o[4];
+// x (n8 runs of 8 fp32) to bf16 in LDS, eight runs a thread in flight at once (the loads are L2 hits; issued one
+// run at a time they would serialise).
+__device__ __forceinline__ void stage_x_bf16(const float *x, uint32_t n8, uint16_t *xb) {
+  constexpr uint32_t kBatch = 4;
+  for (uint32_t i0 = 0; i0 < n8; i0 += kBatch * kWG) {
+    float4 a[kBatch], b[kBatch];
 #pragma unroll
-    for (int k = 0; k < 4; k++)
-      o[k] = (__float_as_uint(round_bf16(v[2 * k])) >> 16) | (__float_as_uint(round_bf16(v[2 * k + 1])) & 0xffff0000u);
-    ((uint4 *)xb)[i] = make_uint4(o[0], o[1], o[2], o[3]);
-  }
-  __syncthreads();
-  for (uint32_t rr = 0; rr < 2; rr++) {
-    const uint32_t r = item * kRouteRows + wave_id() * 2 + rr;
-    if (r > E) break;
-    const uint16_t *wr = p.router + (uint64_t)r * H + lane * 8;
-    uint4 w0[4];  // the first 2048 values of the row stay in registers across the tokens
+    for (uint32_t j = 0; j < kBatch; j++) {
+      const uint32_t i = i0 + j * kWG + threadIdx.x;
+      if (i < n8) a[j] = ((const float4 *)x)[2 * i], b[j] = ((const float4 *)x)[2 * i + 1];
+    }
 #pragma unroll
-    for (uint32_t i = 0; i < 4; i++) w0[i] = i < NW ? *(const uint4 *)(wr + 512 * i) : make_uint4(0, 0, 0, 0);
-    for (uint32_t t = 0; t < T; t++) {
-      double acc = 0.0;
-      for (uint32_t c = 0; c < NW; c += 4) {
+    for (uint32_t j = 0; j < kBatch; j++) {
+      const uint32_t i = i0 + j * kWG + threadIdx.x;
+      if (i >= n8) break;
+      const float v[8] = {a[j].x, a[j].y, a[j].z, a[j].w, b[j].x, b[j].y, b[j].z, b[j].w};
+      uint32_t o[4];
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
-          if (c + i >= NW) break;
-          const uint4 wv = c == 0 ? w0[i] : *(const uint4 *)(wr + 512 * (c + i));
-          const uint4 xv = *(const uint4 *)(xb + (uint64_t)t * H + lane * 8 + 512 * (c + i));
-          const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, xx[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-          for (int k = 0; k < 8; k++) {
-            const float wf = __uint_as_float((k & 1) ? ww[k / 2] & 0xffff0000u : ww[k / 2] << 16);
-            const float xf = __uint_as_float((k & 1) ? xx[k / 2] & 0xffff0000u : xx[k / 2] << 16);
-            acc = __builtin_fma((double)wf, (double)xf, acc);
-          }
-        }
-      }
-      const double sum = wave_sum_f64(acc);
-      if (lane == 0) {
-        float l = (float)sum;
-        if (r < E && p.bias) l = __fadd_rn(l, p.bias[r]);
-        st_co(p.logits + (uint64_t)t * (E + 1) + r, l);
-      }
+      for (int k = 0; k < 4; k++)
+        o[k] = (__float_as_uint(round_bf16(v[2 * k])) >> 16) |
+               (__float_as_uint(round_bf16(v[2 * k + 1])) & 0xffff0000u);
+      ((uint4 *)xb)[i] = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
 }
 
-// MoeGroup records from the routed ids: an expert's assignments in order, MOE_GROUP_MAX a group, groups numbered by
-// their first assignment (as group_slots, layer.cl:894-942), then the shared expert's groups. One pass over the
-// earlier assignments gives a's rank among its expert's and its group's first (an expert has at most T <= 16
-// assignments: its 0th or its 8th).
-__device__ void make_groups(const DecodeParams &p, int32_t *ids_lds, uint32_t *s_head) {
-  const uint32_t T = p.T, K = p.K, E = p.E, n = T * K, a = threadIdx.x;
-  if (a < n) ids_lds[a] = ld_co(p.ids + a);
+// Router rows 2 i and 2 i + 1 of lead item i, two waves a row (waves 2 r and 2 r + 1 take alternate 512-value chunks
+// of row r): logit = sum of bf16(W) bf16(x), each product exact, summed in fp64 (a lane's share, the wave's in a fixed
+// order, then the two waves'), rounded once, plus the bias. The row's weights are loaded before x is staged (as bf16,
+// in xb); part holds the waves' sums.
+__device__ void router_rows(const DecodeParams &p, uint32_t item, uint16_t *xb, double *part) {
+  const uint32_t lane = lane_id(), wv = wave_id(), H = p.H, T = p.T, E = p.E, nC = H / 512;
+  const uint32_t row = item * kRouteRows + wv / 2, half = wv & 1u;
+  const bool on = row <= E;
+  const uint16_t *wr = p.router + (uint64_t)row * H + lane * 8;
+  // A wave's first two chunks (all of them up to H = 2048) stay in registers across the tokens.
+  uint4 w0[2];
+#pragma unroll
+  for (uint32_t i = 0; i < 2; i++) {
+    const uint32_t c = half + 2 * i;
+    w0[i] = on && c < nC ? *(const uint4 *)(wr + 512 * c) : make_uint4(0, 0, 0, 0);
+  }
+  stage_x_bf16(p.x, T * H / 8, xb);
   __syncthreads();
-  int32_t e = -1;
-  uint32_t rank = 0, total = 0, head_a = a;
-  if (a < n) {
-    e = ids_lds[a];
-    for (uint32_t b = 0; b < n; b++) {
-      const bool same = ids_lds[b] == e;
-      if (same && b < a) {
-        if (rank == 0 || rank == MOE_GROUP_MAX) head_a = b;
-        rank++;
+  // Four tokens at a time, so that their fp64 chains and reductions overlap.
+  for (uint32_t t0 = 0; t0 < T; t0 += 4) {
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    for (uint32_t c = half; c < nC; c += 2) {
+      const uint4 wq = c < 4 ? w0[c / 2] : *(const uint4 *)(wr + 512 * c);
+      const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+      double wd[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) wd[k] = (double)__uint_as_float((k & 1) ? ww[k / 2] & 0xffff0000u : ww[k / 2] << 16);
+#pragma unroll
+      for (uint32_t tt = 0; tt < 4; tt++) {
+        if (t0 + tt >= T) break;
+        const uint4 xv = *(const uint4 *)(xb + (uint64_t)(t0 + tt) * H + lane * 8 + 512 * c);
+        const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const float xf = __uint_as_float((k & 1) ? xx[k / 2] & 0xffff0000u : xx[k / 2] << 16);
+          acc[tt] = __builtin_fma(wd[k], (double)xf, acc[tt]);
+        }
       }
-      total += same;
     }
-    if (rank % MOE_GROUP_MAX == 0) head_a = a;
+#pragma unroll
+    for (uint32_t tt = 0; tt < 4; tt++) {
+      if (t0 + tt >= T) break;
+      const double sum = wave_sum_f64(acc[tt]);
+      if (lane == 0) part[wv * kMaxDecodeTokens + t0 + tt] = sum;
+    }
+  }
+  __syncthreads();
+  const uint32_t j = threadIdx.x, r = j / T, tt = j % T, rw = item * kRouteRows + r;
+  if (j < kRouteRows * T && rw <= E) {
+    float l = (float)__dadd_rn(part[2 * r * kMaxDecodeTokens + tt], part[(2 * r + 1) * kMaxDecodeTokens + tt]);
+    if (rw < E && p.bias) l = __fadd_rn(l, p.bias[rw]);
+    st_co(p.logits + (uint64_t)tt * (E + 1) + rw, l);
+  }
+}
+
+// MoeGroup records from the routed ids: an expert's assignments in order, MOE_GROUP_MAX a group, groups numbered by
+// their first assignment (as group_slots, layer.cl:894-942), then the shared expert's groups. An expert takes at
+// most one assignment a token, so a mask of the tokens that chose it gives each assignment its rank among the
+// expert's (and whether it heads a group); the heads' ballots give the group numbers. Token own's ids come from sel,
+// the others' from the coherent ids.
+__device__ void make_groups(const DecodeParams &p, uint32_t own, const uint32_t *sel, uint8_t *lds, uint64_t *hb) {
+  const uint32_t T = p.T, K = p.K, E = p.E, n = T * K, a = threadIdx.x, lane = lane_id();
+  uint32_t *ids = (uint32_t *)lds, *mask = ids + kMaxDecodeTokens * kMaxUsed, *gnum = mask + kMaxExperts;
+  for (uint32_t i = a; i < E; i += kWG) mask[i] = 0u;
+  const uint32_t t = a / K;
+  if (a < n) ids[a] = t == own ? sel[a % K] : (uint32_t)ld_co(p.ids + a);
+  __syncthreads();
+  uint32_t e = 0, rank = 0, total = 0;
+  if (a < n) {
+    e = ids[a];
+    atomicOr(mask + e, 1u << t);
+  }
+  __syncthreads();
+  if (a < n) {
+    const uint32_t m = mask[e];
+    rank = __popc(m & ((1u << t) - 1u));
+    total = __popc(m);
   }
   const bool head = a < n && rank % MOE_GROUP_MAX == 0;
-  s_head[a] = head ? 1u : 0u;
+  const uint64_t heads = __ballot(head);
+  if (lane == 0) hb[wave_id()] = heads;
   __syncthreads();
-  for (uint32_t off = 1; off < kWG; off <<= 1) {  // inclusive scan of the heads
-    const uint32_t add = a >= off ? s_head[a - off] : 0u;
-    __syncthreads();
-    s_head[a] += add;
-    __syncthreads();
+  uint32_t before = 0, nr = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < kWG / 64; w++) {
+    const uint32_t c = (uint32_t)__popcll(hb[w]);
+    before += w < wave_id() ? c : 0u;
+    nr += c;
   }
-  const uint32_t nr = s_head[kWG - 1];
-  if (a < n) {
-    MoeGroup *g = p.groups + (s_head[head_a] - 1);
-    st_co(g->asg + rank % MOE_GROUP_MAX, a);
-    if (head) {
-      st_co(&g->slot, e);
-      st_co(&g->n, min((uint32_t)MOE_GROUP_MAX, total - rank));
-    }
+  if (head) {
+    const uint32_t g = before + __builtin_amdgcn_mbcnt_hi((uint32_t)(heads >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)heads, 0u));
+    gnum[2 * e + rank / MOE_GROUP_MAX] = g;
+    st_co(&p.groups[g].slot, (int32_t)e);
+    st_co(&p.groups[g].n, min((uint32_t)MOE_GROUP_MAX, total - rank));
   }
+  __syncthreads();
+  if (a < n) st_co(p.groups[gnum[2 * e + rank / MOE_GROUP_MAX]].asg + rank % MOE_GROUP_MAX, a);
   const uint32_t ns = p.has_shared ? (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX : 0;
   if (a < ns) {
     MoeGroup *g = p.groups + nr + a;
@@ -433,7 +507,7 @@ __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *un
 
 // Gate and up of rows blk * gate_up_rows .. of group g: lane = m * 32 + r * U + u; h = silu(g) * u per row.
 __device__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
-                             GroupLds *sg, uint32_t *s_flag, const uint64_t *tab) {
+                             GroupLds *sg, uint32_t *s_flag, const uint64_t *tab, uint64_t *mark) {
   read_group(p, g, sg);
   const uint32_t U = p.H / kUnit, rows = gate_up_rows(U), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 0);
@@ -450,6 +524,7 @@ __device__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, ui
              (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
                stage_act(gm.shared ? p.act_s : p.act_r, sg->tok, n, U, lds);
                __syncthreads();
+               if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
              });
 #pragma unroll
   for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
@@ -458,6 +533,7 @@ __device__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, ui
     const float su = __shfl_xor(s, 32, 64);  // the other matrix's
     if (m == 0 && u == 0) st_co(p.h + (uint64_t)sg->asg[j] * p.F + row, swiglu_one(s, su, p.swiglu_limit, tab));
   }
+  if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
   // The last item of these 256 rows quantises them, one unit of the down's K per assignment, a half-wave each; the
   // last unit of the group sets its flag.
   const uint32_t Ud = p.F / kUnit, unit = row0 / kUnit;
@@ -476,7 +552,7 @@ __device__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, ui
 
 // Down rows blk * down_rows .. of group g (lane = r * U + u), then the combine of every token this item completes.
 __device__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
-                          GroupLds *sg, uint32_t *s_last) {
+                          GroupLds *sg, uint32_t *s_last, uint64_t *mark) {
   read_group(p, g, sg);
   const uint32_t U = p.F / kUnit, rows = down_rows(U), row0 = blk * rows, n = sg->n, nblk = p.H / rows;
   const GroupMat gm = group_mat(p, sg->slot, 2);
@@ -493,6 +569,7 @@ __device__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8
                wait_flag(p, kFlagH + g);  // the weights are already on their way
                stage_act(p.hact, sg->asg, n, U, lds);
                __syncthreads();
+               if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
              });
 #pragma unroll
   for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
@@ -500,6 +577,7 @@ __device__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8
     const float s = row_sum(t[j], U);
     if (u == 0) st_co(p.y_asg + (uint64_t)sg->asg[j] * p.H + row, s);
   }
+  if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
   // Count this item's outputs in, one counter per (token, row block), all at once.
   stores_done();
   if (threadIdx.x < n) {
@@ -539,19 +617,21 @@ __device__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8
 
 }  // namespace
 
-// Grid: the work-groups of 256 the device holds at once; dynamic LDS: the larger of the
-// staged x (T H bf16) and a group's activation units (MOE_GROUP_MAX x units x kActLds).
-__global__ void __launch_bounds__(kWG) moe_decode(DecodeParams p) {
-  extern __shared__ uint8_t lds[];
+// Grid: the work-groups of 256 the device holds at once; dynamic LDS: the largest of the staged x (T H bf16), a
+// group's activation units (MOE_GROUP_MAX x units x kActLds) and the grouping's tables (kGroupingLds).
+__global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) moe_decode(DecodeParams p) {
+  extern __shared__ __align__(16) uint8_t lds[];
   __shared__ uint32_t grid_lds[512];
-  __shared__ uint32_t s_head[kWG];
-  __shared__ uint32_t s_flag, s_ng, s_last[MOE_GROUP_MAX];
+  __shared__ uint32_t s_flag, s_ng, s_last[MOE_GROUP_MAX], s_sel[2 * kMaxUsed];
+  __shared__ float s_norm[2];
+  __shared__ uint64_t s_hb[kWG / 64];
+  __shared__ double s_part[(kWG / 64) * kMaxDecodeTokens];
   __shared__ GroupLds sg;
   __shared__ uint64_t exp_tab[32];  // expf's table, read at LDS latency
   if (threadIdx.x < 32) exp_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
   const uint32_t T = p.T, E = p.E, Ug = p.H / kUnit, Ud = p.F / kUnit;
-  const uint32_t nL = p.route ? max((E + kRouteRows) / kRouteRows, T) : T, nTop = p.route ? T : 0, B1 = nL + nTop;
+  const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nL + nTop;
   const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud);
   uint32_t ng = 0xffffffffu, end = 0xffffffffu;
   for (uint32_t it = blockIdx.x;; it += gridDim.x) {
@@ -565,25 +645,34 @@ __global__ void __launch_bounds__(kWG) moe_decode(DecodeParams p) {
       }
       if (it >= end) break;
     }
-    if (p.trace && threadIdx.x == 0 && it < p.trace_cap) p.trace[2 * it] = __builtin_amdgcn_s_memrealtime();
+    uint64_t *mark = p.trace && it < p.trace_cap ? p.trace + 4 * it : nullptr;
+    if (mark && threadIdx.x == 0) mark[0] = mark[1] = mark[2] = __builtin_amdgcn_s_memrealtime();
     if (it < nL) {
       if (it < T) quantise_x(p, it);
-      if (p.route && it * kRouteRows <= E) router_rows(p, it, (uint16_t *)lds);
-      if (arrive_last(p.cnt_route, nL, &s_flag)) set_flag(p, p.route ? kFlagLogits : kFlagRouted);
+      if (p.route) {
+        if (it * kRouteRows <= E) router_rows(p, it, (uint16_t *)lds, s_part);
+        if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
+        set_flag(p, kFlagLead + it);
+      } else if (arrive_last(p.cnt_route, nL, &s_flag)) {
+        set_flag(p, kFlagRouted);
+      }
     } else if (it < B1) {
-      wait_flag(p, kFlagLogits);
-      if (wave_id() == 0) route_token(p, it - nL, exp_tab);
-      if (arrive_last(p.cnt_topk, T, &s_flag)) {
-        make_groups(p, (int32_t *)lds, s_head);
+      const uint32_t t = it - nL;
+      wait_flags(p, kFlagLead, nL);
+      if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
+      route_token(p, t, exp_tab, s_sel, s_norm);
+      if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
+      if (T == 1 || arrive_last(p.cnt_topk, T, &s_flag)) {
+        make_groups(p, t, s_sel, lds, s_hb);
         set_flag(p, kFlagRouted);
       }
     } else if (it < B1 + ng * nGU) {
-      gate_up_item(p, (it - B1) / nGU, (it - B1) % nGU, lds, grid_lds, &sg, &s_flag, exp_tab);
+      gate_up_item(p, (it - B1) / nGU, (it - B1) % nGU, lds, grid_lds, &sg, &s_flag, exp_tab, mark);
     } else {
       const uint32_t i = it - B1 - ng * nGU;
-      down_item(p, i / nD, i % nD, lds, grid_lds, &sg, s_last);
+      down_item(p, i / nD, i % nD, lds, grid_lds, &sg, s_last, mark);
     }
-    if (p.trace && threadIdx.x == 0 && it < p.trace_cap) p.trace[2 * it + 1] = __builtin_amdgcn_s_memrealtime();
+    if (mark && threadIdx.x == 0) mark[3] = __builtin_amdgcn_s_memrealtime();
     __syncthreads();
   }
 }

@@ -11,13 +11,27 @@
 
 namespace c0ven {
 
-// An activation unit (layout.h) as 80 dwords: 64 of codes, the scales at 64, the q8_K sums at 72.
+// An activation unit (layout.h) as 80 dwords: 64 of codes, the scales at 64, the q8_K sums at 72. It sits in LDS at a
+// 16-byte aligned address and is read 16 bytes at a time (ds_read_b128).
 struct Act {
-  const uint32_t *d;
-  __device__ __forceinline__ explicit Act(const uint32_t *p) : d(p) {}
-  __device__ __forceinline__ uint32_t q(int i) const { return d[i]; }
-  __device__ __forceinline__ float scale(int b) const { return __uint_as_float(d[64 + b]); }
-  __device__ __forceinline__ int sum(int j) const { return (int)d[72 + j]; }
+  const uint4 *d;
+  __device__ __forceinline__ explicit Act(const uint32_t *p) : d((const uint4 *)p) {}
+  // Code words 8 i .. 8 i + 7 (the 32 codes of block i).
+  __device__ __forceinline__ void q8(int i, uint32_t *w) const {
+    const uint4 a = d[2 * i], b = d[2 * i + 1];
+    w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
+  }
+  __device__ __forceinline__ void scales(float *s) const {
+    const uint4 a = d[16], b = d[17];
+    s[0] = __uint_as_float(a.x), s[1] = __uint_as_float(a.y), s[2] = __uint_as_float(a.z), s[3] = __uint_as_float(a.w);
+    s[4] = __uint_as_float(b.x), s[5] = __uint_as_float(b.y), s[6] = __uint_as_float(b.z), s[7] = __uint_as_float(b.w);
+  }
+  __device__ __forceinline__ float scale0() const { return __uint_as_float(d[16].x); }
+  __device__ __forceinline__ void sums(int *s) const {
+    const uint4 a = d[18], b = d[19];
+    s[0] = (int)a.x, s[1] = (int)a.y, s[2] = (int)a.z, s[3] = (int)a.w;
+    s[4] = (int)b.x, s[5] = (int)b.y, s[6] = (int)b.z, s[7] = (int)b.w;
+  }
 };
 
 template <typename T>
@@ -41,13 +55,16 @@ struct UnitQ8_0 {
     for (int b = 0; b < 8; b++) d[b] = h2f((uint16_t)(w[b / 2] >> (16 * (b % 2))));
   }
   __device__ __forceinline__ float term(const Act &a) const {
-    float t[8];
+    float t[8], as[8];
+    a.scales(as);
 #pragma unroll
     for (int b = 0; b < 8; b++) {
+      uint32_t aw[8];
+      a.q8(b, aw);
       int s = 0;
 #pragma unroll
-      for (int i = 0; i < 8; i++) s = dot4(q[8 * b + i], a.q(8 * b + i), s);
-      t[b] = __fmul_rn(__fmul_rn(d[b], a.scale(b)), (float)s);
+      for (int i = 0; i < 8; i++) s = dot4(q[8 * b + i], aw[i], s);
+      t[b] = __fmul_rn(__fmul_rn(d[b], as[b]), (float)s);
     }
     return __fadd_rn(__fadd_rn(__fadd_rn(t[0], t[1]), __fadd_rn(t[2], t[3])),
                      __fadd_rn(__fadd_rn(t[4], t[5]), __fadd_rn(t[6], t[7])));
@@ -93,20 +110,24 @@ struct UnitQ4_K {
     dmin = h2f((uint16_t)(dm >> 16));
   }
   __device__ __forceinline__ float term(const Act &a) const {
-    int isum = 0, imin = 0;
+    int isum = 0, imin = 0, bs[8];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
+      uint32_t al[8], ah[8];
+      a.q8(2 * c, al);
+      a.q8(2 * c + 1, ah);
       int sl = 0, sh = 0;
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        sl = dot4(lo[8 * c + i], a.q(16 * c + i), sl);
-        sh = dot4(hi[8 * c + i], a.q(16 * c + 8 + i), sh);
+        sl = dot4(lo[8 * c + i], al[i], sl);
+        sh = dot4(hi[8 * c + i], ah[i], sh);
       }
       isum += sc[2 * c] * sl + sc[2 * c + 1] * sh;
     }
+    a.sums(bs);
 #pragma unroll
-    for (int j = 0; j < 8; j++) imin += mn[j] * a.sum(j);
-    const float ad = a.scale(0);
+    for (int j = 0; j < 8; j++) imin += mn[j] * bs[j];
+    const float ad = a.scale0();
     const float dd = __fmul_rn(d, ad), dm = __fmul_rn(dmin, ad);
     const float pm = __fmul_rn(dm, (float)imin);
     return __builtin_fmaf(dd, (float)isum, -pm);
@@ -149,12 +170,14 @@ struct UnitIQ3_S {
     int bsum = 0;
 #pragma unroll
     for (int ib = 0; ib < 8; ib++) {
+      uint32_t aw[8];
+      a.q8(ib, aw);
       int s = 0;
 #pragma unroll
-      for (int k = 0; k < 8; k++) s = dot4(w[8 * ib + k], a.q(8 * ib + k), s);
+      for (int k = 0; k < 8; k++) s = dot4(w[8 * ib + k], aw[k], s);
       bsum += ls[ib] * s;
     }
-    return __fmul_rn(__fmul_rn(d, a.scale(0)), (float)bsum);
+    return __fmul_rn(__fmul_rn(d, a.scale0()), (float)bsum);
   }
 };
 
