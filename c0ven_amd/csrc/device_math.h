@@ -7,30 +7,32 @@
 namespace c0ven {
 
 // 2^(i/32) for i = 0..31, each the nearest double, as its bits minus i << 47 (so that adding k << 47 for k = 32 q + i
-// gives 2^(k/32) once the exponent carries in q). tests/test_device_tables.py recomputes them to 60 digits.
-__device__ __constant__ static const uint64_t kExp2Tab[32] = {
-    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+// gives 2^(k/32) once the exponent carries in q). tests/test_device_tables.py recomputes them exactly.
+#define C0VEN_EXP2_TAB_VALUES \
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull, \
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull, \
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull, \
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull, \
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull, \
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull, \
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull, \
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull
+__device__ __constant__ static const uint64_t kExp2Tab[32] = {C0VEN_EXP2_TAB_VALUES};
 
 // expf with the bits of glibc 2.35's x86-64 expf on a CPU with FMA (its __expf_fma, which the host's libm runs and
 // which the CPU path's std::exp calls). The method is ARM optimized-routines' expf (MIT/Apache-2.0; glibc
 // sysdeps/ieee754/flt-32/e_expf.c): x / ln2 * 32 = k + r with |r| <= 1/2, 2^(k/32) from the table, 2^(r/32) from a
-// cubic, all in double, rounded once to float. The fused multiply-adds are where the FMA build fuses; with them the
-// result equals the host's expf on all 2^32 inputs (checked on the CPU by tests/test_expf.py's exhaustive run and on
-// the GPU against the host by tests/test_gpu_parity.py).
-__device__ __forceinline__ float expf_libm(float x, const uint64_t *tab = kExp2Tab) {
-  const uint32_t ux = __float_as_uint(x);
+// cubic, all in double, rounded once to float. The fused multiply-adds are where the FMA build fuses; everything else
+// is a single IEEE operation (the library builds with -ffp-contract=off). tab is the table above (in constant or LDS
+// memory on the device, a host copy on the CPU): the same source runs on both, and tests/test_expf.py checks the host
+// build against libm's expf on all 2^32 inputs.
+__host__ __device__ __forceinline__ float expf_libm(float x, const uint64_t *tab) {
+  const uint32_t ux = __builtin_bit_cast(uint32_t, x);
   const uint32_t abstop = (ux >> 20) & 0x7ffu;
   if (abstop >= 0x42bu) {  // |x| >= 88, infinity or NaN
     if (ux == 0xff800000u) return 0.0f;
     if (abstop >= 0x7f8u) return x + x;
-    if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
+    if (x > 0x1.62e42ep6f) return __builtin_bit_cast(float, 0x7f800000u);
     if (x < -0x1.9fe368p6f) return 0.0f;
   }
   const double InvLn2N = 0x1.71547652b82fep+0 * 32, Shift = 0x1.8p+52;
@@ -38,31 +40,31 @@ __device__ __forceinline__ float expf_libm(float x, const uint64_t *tab = kExp2T
                C2 = 0x1.62e42ff0c52d6p-1 / 32;
   const double xd = (double)x;
   double kd = __builtin_fma(InvLn2N, xd, Shift);
-  const uint64_t ki = (uint64_t)__double_as_longlong(kd);
-  kd = __dsub_rn(kd, Shift);
+  const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+  kd = kd - Shift;
   const double r = __builtin_fma(InvLn2N, xd, -kd);
   const uint64_t t = tab[ki % 32] + (ki << 47);
-  const double s = __longlong_as_double((long long)t);
+  const double sc = __builtin_bit_cast(double, t);
   const double z = __builtin_fma(C0, r, C1);
-  const double r2 = __dmul_rn(r, r);
+  const double r2 = r * r;
   double y = __builtin_fma(C2, r, 1.0);
   y = __builtin_fma(z, r2, y);
-  y = __dmul_rn(y, s);
+  y = y * sc;
   return (float)y;
 }
 
 // silu(g) * u with the optional clamp, each step rounded as the CPU path's g / (1 + expf(-g)) * u.
-__device__ __forceinline__ float swiglu_one(float g, float u, float limit, const uint64_t *tab = kExp2Tab) {
+__host__ __device__ __forceinline__ float swiglu_one(float g, float u, float limit, const uint64_t *tab) {
   if (limit > 0.0f) {
-    g = fminf(g, limit);
+    g = g < limit ? g : limit;
     u = u < -limit ? -limit : (u > limit ? limit : u);
   }
-  const float den = __fadd_rn(1.0f, expf_libm(-g, tab));
-  return __fmul_rn(__fdiv_rn(g, den), u);
+  const float den = 1.0f + expf_libm(-g, tab);
+  return (g / den) * u;
 }
 
-__device__ __forceinline__ float sigmoid_libm(float z, const uint64_t *tab = kExp2Tab) {
-  return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_libm(-z, tab)));
+__host__ __device__ __forceinline__ float sigmoid_libm(float z, const uint64_t *tab) {
+  return 1.0f / (1.0f + expf_libm(-z, tab));
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
