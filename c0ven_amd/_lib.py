@@ -63,6 +63,7 @@ _SIGS = {
     "moe_forward_async": (_i32, [_P, _u32, _P, _u32, _P, _P, _P, _P]),
     "moe_forward_experts": (_i32, [_P, C.POINTER(MoeJob), _u32, _u32, _P, _u64, _P, _u64]),
     "moe_h_rows": (_u32, [C.POINTER(MoeConfig)]),
+    "moe_prefill_dispatch": (_i32, [_P, C.POINTER(MoeTile), _u32, C.POINTER(_u32), _P]),
     "moe_sync": (_i32, [_P]),
     "moe_stream": (_P, [_P]),
     "moe_set_timing": (_i32, [_P, C.c_int]),
@@ -236,6 +237,16 @@ class MoeBlock:
         out = np.zeros((n.value, 4), dtype=np.uint64)
         self._check(lib.moe_trace(self.h, _ptr(out), n.value, C.byref(n), _ptr(bounds)))
         return out, bounds
+
+    def prefill_dispatch(self, ntok):
+        """The last prefill forward's MoeTiles (expert, slot, start, count) and perm (row -> assignment)."""
+        n = C.c_uint32()
+        self._check(lib.moe_prefill_dispatch(self.h, None, 0, C.byref(n), None))
+        tiles = (MoeTile * max(1, n.value))()
+        perm = np.empty(ntok * self.cfg.n_used, dtype=np.uint32)
+        self._check(lib.moe_prefill_dispatch(self.h, tiles, n.value, C.byref(n), _ptr(perm)))
+        t = np.array([(x.expert, x.slot, x.start, x.count) for x in tiles[:n.value]], dtype=np.uint32).reshape(-1, 4)
+        return t, perm
 
     def grid(self):
         return int(lib.moe_grid(self.h))

@@ -1,0 +1,87 @@
+// Device-coherent accesses and the activation quantiser, shared by the decode and prefill kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/c0ven_quant.h"
+#include "device_math.h"
+#include "layout.h"
+
+namespace c0ven {
+
+// Data one work-group writes and another reads within a launch goes through device-coherent accesses (agent-scope
+// relaxed atomics: the store writes through the XCD's L2, the load reads past a stale line), so no fence has to
+// write back or invalidate a whole L2. Kernel boundaries order everything else.
+template <typename T>
+__device__ __forceinline__ void st_co(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T ld_co(const T *p) {
+  return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes coherently, as four words.
+__device__ __forceinline__ uint4 ld_co4(const void *p) {
+  const uint32_t *q = (const uint32_t *)p;
+  return make_uint4(ld_co(q), ld_co(q + 1), ld_co(q + 2), ld_co(q + 3));
+}
+
+// One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
+// with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0).
+__device__ inline void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
+  uint32_t code[2] = {0u, 0u};
+  if (act_type == QT_Q8_K) {
+    // The value of largest magnitude, the first of equals: (|v|, index) reduced over the 32 lanes.
+    float amax = 0.0f, mx = 0.0f;
+    uint32_t at = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float a = fabsf(v[i]);
+      if (a > amax) amax = a, mx = v[i], at = 8 * l32 + i;
+    }
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
+      const float oa = __shfl_xor(amax, o, 32), om = __shfl_xor(mx, o, 32);
+      const uint32_t oi = __shfl_xor(at, o, 32);
+      if (oa > amax || (oa == amax && oi < at)) amax = oa, mx = om, at = oi;
+    }
+    float d = 0.0f;
+    int part = 0;
+    if (amax != 0.0f) {
+      const float iscale = __fdiv_rn(-127.0f, mx);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        int q = nearest_int(__fmul_rn(iscale, v[i]));
+        q = q < 127 ? q : 127;
+        part += q;
+        code[i / 4] |= ((uint32_t)q & 0xffu) << (8 * (i % 4));
+      }
+      d = __fdiv_rn(1.0f, iscale);
+    }
+    part += __shfl_xor(part, 1, 32);
+    part += __shfl_xor(part, 2, 32);
+    st_co((uint32_t *)out + 2 * l32, code[0]);
+    st_co((uint32_t *)out + 2 * l32 + 1, code[1]);
+    if ((l32 & 3u) == 0) st_co((int32_t *)(out + kActSums) + l32 / 4, part);
+    if (l32 == 0) st_co((float *)(out + kActScales), d);
+  } else {  // q8_0: blocks of 32, four lanes each
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 32));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 32));
+    const float d = __fdiv_rn(amax, 127.0f), id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int q = nearest_int(__fmul_rn(v[i], id));
+      code[i / 4] |= ((uint32_t)q & 0xffu) << (8 * (i % 4));
+    }
+    st_co((uint32_t *)out + 2 * l32, code[0]);
+    st_co((uint32_t *)out + 2 * l32 + 1, code[1]);
+    if ((l32 & 3u) == 0) st_co((float *)(out + kActScales) + l32 / 4, h2f(f2h(d)));
+    if ((l32 & 3u) == 0) st_co((int32_t *)(out + kActSums) + l32 / 4, 0);
+  }
+}
+
+}  // namespace c0ven

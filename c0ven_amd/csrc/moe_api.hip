@@ -13,6 +13,7 @@
 #include "aux.h"
 #include "decode.h"
 #include "layout.h"
+#include "prefill.h"
 #include "repack.h"
 
 using namespace c0ven;
@@ -41,8 +42,13 @@ struct Layer {
   uint8_t *shared = nullptr;
 };
 
-constexpr int kNumKernels = 1;
-const char *kKernelNames[kNumKernels] = {"moe_decode"};
+constexpr uint32_t kMaxPrefillTokens = 16384;  // tokens one forward takes (one prefill chunk)
+
+// A kernel launch timed with two events on its stream.
+struct TimedLaunch {
+  const char *name;
+  hipEvent_t a, b;
+};
 
 }  // namespace
 
@@ -51,7 +57,11 @@ struct moe_ctx {
   hipStream_t stream = nullptr;
   std::vector<Layer> layers;
   uint64_t ex_bytes = 0, ex_up = 0, ex_down = 0, sh_bytes = 0, sh_up = 0, sh_down = 0;
-  uint32_t tmax = 0, k1 = 0, gmax = 0;
+  uint32_t tmax = 0, tdec = 0, k1 = 0, gmax = 0;  // tokens a forward takes; of them, the decode kernel's
+  PfBufs pf{};                                      // prefill scratch (max_tokens > tdec)
+  const int32_t *last_ids = nullptr;                // where the last forward left its ids and weights
+  const float *last_w = nullptr;
+  uint32_t last_pf_T = 0;                           // tokens of the last prefill forward
   // Staging for the host-memory calls.
   float *x_dev = nullptr, *y_dev = nullptr, *w_stage = nullptr;
   int32_t *ids_stage = nullptr;
@@ -70,7 +80,9 @@ struct moe_ctx {
   bool timing = false;
   uint64_t *trace = nullptr;   // per-item stamps of the last forward, when tracing
   uint32_t trace_cap = 0, trace_bounds[5] = {0, 0, 0, 0, 0}, last_T = 0, last_route = 1;
-  std::vector<hipEvent_t> ev;  // (kNumKernels + 1) events per timed forward
+  std::vector<hipEvent_t> ev;  // the event pool
+  size_t ev_next = 0;          // events of the pool in use by the record
+  std::vector<TimedLaunch> timed;
   uint32_t ev_used = 0;        // forwards recorded since the last moe_kernel_times
   std::vector<void *> allocs;
   uint64_t dev_bytes = 0;
@@ -124,9 +136,10 @@ void validate(const moe_config &c) {
   require(quant_gpu_supported(c.gate_type) && quant_gpu_supported(c.down_type), "expert types must be Q8_0, Q4_K or IQ3_S");
   require(!c.has_shared || (quant_gpu_supported(c.sh_gate_type) && quant_gpu_supported(c.sh_down_type)),
           "shared expert types must be Q8_0, Q4_K or IQ3_S");
-  require(c.max_tokens <= kMaxDecodeTokens, "max_tokens above 16 needs the prefill path");
-  require((uint64_t)(c.max_tokens ? c.max_tokens : kMaxDecodeTokens) * c.n_embd * 2 <= 64 * 1024,
-          "max_tokens x n_embd bf16 must fit the router's 64 KiB of LDS");
+  require(c.max_tokens <= kMaxPrefillTokens, "max_tokens must be at most 16384");
+  require((uint64_t)std::min<uint32_t>(c.max_tokens ? c.max_tokens : kMaxDecodeTokens, kMaxDecodeTokens) * c.n_embd *
+                  2 <= 64 * 1024,
+          "min(max_tokens, 16) x n_embd bf16 must fit the decode router's 64 KiB of LDS");
   require(c.swiglu_limit >= 0.0f, "swiglu_limit must be >= 0");
 }
 
@@ -154,28 +167,35 @@ DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   return p;
 }
 
-// The events of the next timed forward (kNumKernels + 1 of them), or null when timing is off.
-hipEvent_t *timing_events(moe_ctx *c) {
-  if (!c->timing) return nullptr;
-  const size_t need = (size_t)(c->ev_used + 1) * (kNumKernels + 1);
-  while (c->ev.size() < need) {
+// Records an event on s for a timed launch (start or end), from the context's pool.
+hipEvent_t timing_event(moe_ctx *c, hipStream_t s) {
+  if (c->ev_next == c->ev.size()) {
     hipEvent_t e;
     check(hipEventCreate(&e), "hipEventCreate");
     c->ev.push_back(e);
   }
-  return &c->ev[(size_t)c->ev_used++ * (kNumKernels + 1)];
+  hipEvent_t e = c->ev[c->ev_next++];
+  check(hipEventRecord(e, s), "hipEventRecord");
+  return e;
+}
+void timing_hook(void *ctx, const char *name, int after, hipStream_t s) {
+  moe_ctx *c = (moe_ctx *)ctx;
+  if (!after) {
+    c->timed.push_back(TimedLaunch{name, timing_event(c, s), nullptr});
+  } else {
+    c->timed.back().b = timing_event(c, s);
+  }
 }
 
 void launch(moe_ctx *c, const DecodeParams &p, hipStream_t s) {
-  hipEvent_t *ev = timing_events(c);
   DecodeParams q = p;
   q.epoch = ++c->epoch;
   if (c->trace) q.trace = c->trace, q.trace_cap = c->trace_cap;
   c->last_T = p.T, c->last_route = p.route;
-  if (ev) check(hipEventRecord(ev[0], s), "hipEventRecord");
+  if (c->timing) timing_hook(c, "moe_decode", 0, s);
   hipLaunchKernelGGL(moe_decode, dim3(c->grid), dim3(kWG), c->lds, s, q);
   check(hipGetLastError(), "moe_decode launch");
-  if (ev) check(hipEventRecord(ev[1], s), "hipEventRecord");
+  if (c->timing) timing_hook(c, "moe_decode", 1, s);
 }
 
 void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *y, int32_t *ids, float *w,
@@ -183,11 +203,26 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
   require(layer < c->cfg.n_layer, "layer out of range");
   require(T >= 1 && T <= c->tmax, "ntok must be 1..max_tokens");
   require(c->layers[layer].router != nullptr, "the layer's router is not loaded");
-  DecodeParams p = base_params(c, layer, T);
-  p.x = x, p.y = y;
-  launch(c, p, s);
-  if (ids) check(hipMemcpyAsync(ids, c->ids, sizeof(int32_t) * T * p.K, hipMemcpyDeviceToDevice, s), "copy ids");
-  if (w) check(hipMemcpyAsync(w, c->w, sizeof(float) * T * p.K, hipMemcpyDeviceToDevice, s), "copy w");
+  const uint32_t K = c->cfg.n_used;
+  if (T <= c->tdec) {
+    DecodeParams p = base_params(c, layer, T);
+    p.x = x, p.y = y;
+    launch(c, p, s);
+    c->last_ids = c->ids, c->last_w = c->w;
+  } else {
+    const moe_config &g = c->cfg;
+    const Layer &L = c->layers[layer];
+    PfShape S{g.n_embd, g.n_ff, g.n_expert, K, T, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type,
+              g.has_shared, g.swiglu_limit};
+    PfLayer PL{L.router, L.has_bias ? L.bias : nullptr, L.experts, c->ex_bytes, c->ex_up, c->ex_down, L.shared,
+               c->sh_up, c->sh_down};
+    PfHook hook{c->timing ? timing_hook : nullptr, c};
+    check(prefill_forward(S, PL, c->pf, x, y, s, hook), "prefill launch");
+    c->last_ids = c->pf.ids, c->last_w = c->pf.w, c->last_pf_T = T;
+  }
+  if (c->timing) c->ev_used++;
+  if (ids) check(hipMemcpyAsync(ids, c->last_ids, sizeof(int32_t) * T * K, hipMemcpyDeviceToDevice, s), "copy ids");
+  if (w) check(hipMemcpyAsync(w, c->last_w, sizeof(float) * T * K, hipMemcpyDeviceToDevice, s), "copy w");
 }
 
 // A wait inside moe_decode gave up: its result is not to be trusted.
@@ -245,13 +280,39 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     }
     // Scratch for max_tokens tokens of n_used + 1 assignments (the pre-routed path may give a token its shared
     // expert as a job).
-    const uint32_t T = g.max_tokens, K1 = g.n_used + 1, G = max_groups(T, K1), A = T * K1 + T;
-    c->tmax = T, c->k1 = K1, c->gmax = G;
+    const uint32_t TM = g.max_tokens, T = std::min<uint32_t>(TM, kMaxDecodeTokens), K1 = g.n_used + 1;
+    const uint32_t G = max_groups(T, K1), A = T * K1 + T;
+    c->tmax = TM, c->tdec = T, c->k1 = K1, c->gmax = G;
     const uint32_t Ug = H / kUnit, Ud = F / kUnit;
-    c->x_dev = c->alloc<float>((uint64_t)T * H);
-    c->y_dev = c->alloc<float>((uint64_t)T * H);
+    c->x_dev = c->alloc<float>((uint64_t)TM * H);
+    c->y_dev = c->alloc<float>((uint64_t)TM * H);
     c->ids_stage = c->alloc<int32_t>((uint64_t)T * K1);
     c->w_stage = c->alloc<float>((uint64_t)T * K1);
+    if (TM > T) {  // the prefill path's scratch
+      const uint32_t K = g.n_used;
+      const uint64_t A2 = (uint64_t)TM * K;
+      PfBufs &b = c->pf;
+      b.act_r = c->alloc<uint8_t>((uint64_t)TM * Ug * kActBytes);
+      b.act_s = quant_vec_dot_type(g.sh_gate_type) != quant_vec_dot_type(g.gate_type) && g.has_shared
+                    ? c->alloc<uint8_t>((uint64_t)TM * Ug * kActBytes)
+                    : b.act_r;
+      b.logits = c->alloc<float>((uint64_t)TM * (E + 1));
+      b.ids = c->alloc<int32_t>(A2);
+      b.w = c->alloc<float>(A2);
+      b.gs = c->alloc<float>(TM);
+      b.perm = c->alloc<uint32_t>(A2);
+      b.inv = c->alloc<uint32_t>(A2);
+      b.tiles = c->alloc<MoeTile>(pf_max_tiles(TM, K, E));
+      b.ntiles = c->alloc<uint32_t>(1);
+      b.h = c->alloc<float>(A2 * F);
+      b.hact = c->alloc<uint8_t>(A2 * Ud * kActBytes);
+      b.y_asg = c->alloc<float>(A2 * H);
+      if (g.has_shared) {
+        b.h_sh = c->alloc<float>((uint64_t)TM * F);
+        b.hact_sh = c->alloc<uint8_t>((uint64_t)TM * Ud * kActBytes);
+        b.y_sh = c->alloc<float>((uint64_t)TM * H);
+      }
+    }
     c->act_r = c->alloc<uint8_t>((uint64_t)T * Ug * kActBytes);
     c->act_s = c->alloc<uint8_t>((uint64_t)T * Ug * kActBytes);
     c->logits = c->alloc<float>((uint64_t)T * (E + 1));
@@ -350,9 +411,10 @@ MOE_API moe_status moe_forward(moe_ctx *c, uint32_t layer, const float *x, uint3
                            hipMemcpyDeviceToHost, c->stream),
           "download y");
     if (route && route->ids)
-      check(hipMemcpyAsync(route->ids, c->ids, sizeof(int32_t) * ntok * K, hipMemcpyDeviceToHost, c->stream), "ids");
+      check(hipMemcpyAsync(route->ids, c->last_ids, sizeof(int32_t) * ntok * K, hipMemcpyDeviceToHost, c->stream),
+            "ids");
     if (route && route->w)
-      check(hipMemcpyAsync(route->w, c->w, sizeof(float) * ntok * K, hipMemcpyDeviceToHost, c->stream), "w");
+      check(hipMemcpyAsync(route->w, c->last_w, sizeof(float) * ntok * K, hipMemcpyDeviceToHost, c->stream), "w");
     check(hipStreamSynchronize(c->stream), "forward");
     check_err(c);
   });
@@ -371,7 +433,7 @@ MOE_API moe_status moe_forward_experts(moe_ctx *c, const moe_job *jobs, uint32_t
   return guarded(c, [&] {
     const moe_config &g = c->cfg;
     const uint32_t H = g.n_embd;
-    require(x && y && ntok >= 1 && ntok <= c->tmax && x_stride >= H && y_stride >= H, "bad x, y, ntok or strides");
+    require(x && y && ntok >= 1 && ntok <= c->tdec && x_stride >= H && y_stride >= H, "bad x, y, ntok or strides");
     require(njobs == 0 || jobs, "null jobs");
     const uint32_t layer = njobs ? jobs[0].layer : 0;
     std::vector<uint32_t> per(ntok, 0);
@@ -426,6 +488,7 @@ MOE_API moe_status moe_forward_experts(moe_ctx *c, const moe_job *jobs, uint32_t
     p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
     p.x = c->x_dev, p.y = c->y_dev;
     if (ng) launch(c, p, s);
+    if (c->timing) c->ev_used++;
     check(hipMemcpy2DAsync(y, y_stride * sizeof(float), c->y_dev, H * sizeof(float), H * sizeof(float), ntok,
                            hipMemcpyDeviceToHost, s),
           "download y");
@@ -445,8 +508,10 @@ MOE_API void *moe_stream(moe_ctx *c) { return c ? (void *)c->stream : nullptr; }
 
 MOE_API moe_status moe_set_timing(moe_ctx *c, int on) {
   return guarded(c, [&] {
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     c->timing = on != 0;
-    c->ev_used = 0;
+    c->ev_used = 0, c->ev_next = 0;
+    c->timed.clear();
   });
 }
 
@@ -456,22 +521,27 @@ MOE_API moe_status moe_kernel_times(moe_ctx *c, const char **names, float *avg_m
     require(n != nullptr, "null n");
     *n = 0;
     if (forwards) *forwards = c->ev_used;
-    if (!c->ev_used) return;
-    const uint32_t nf = c->ev_used;
-    check(hipEventSynchronize(c->ev[(size_t)nf * (kNumKernels + 1) - 1]), "hipEventSynchronize");
-    for (int i = 0; i < kNumKernels && (uint32_t)i < cap; i++) {
-      double sum = 0.0;
-      for (uint32_t f = 0; f < nf; f++) {
-        float t = 0.0f;
-        const hipEvent_t *e = &c->ev[(size_t)f * (kNumKernels + 1)];
-        check(hipEventElapsedTime(&t, e[i], e[i + 1]), "hipEventElapsedTime");
-        sum += t;
-      }
-      if (names) names[i] = kKernelNames[i];
-      if (avg_ms) avg_ms[i] = (float)(sum / nf);
+    if (c->timed.empty()) return;
+    check(hipEventSynchronize(c->timed.back().b), "hipEventSynchronize");
+    // Kernels in order of first launch; the average over their launches.
+    std::vector<const char *> order;
+    std::vector<double> sum;
+    std::vector<uint32_t> cnt;
+    for (const TimedLaunch &t : c->timed) {
+      size_t i = 0;
+      while (i < order.size() && std::strcmp(order[i], t.name) != 0) i++;
+      if (i == order.size()) order.push_back(t.name), sum.push_back(0.0), cnt.push_back(0);
+      float ms = 0.0f;
+      check(hipEventElapsedTime(&ms, t.a, t.b), "hipEventElapsedTime");
+      sum[i] += ms, cnt[i]++;
+    }
+    for (size_t i = 0; i < order.size() && i < cap; i++) {
+      if (names) names[i] = order[i];
+      if (avg_ms) avg_ms[i] = (float)(sum[i] / cnt[i]);
       *n = (uint32_t)i + 1;
     }
-    c->ev_used = 0;
+    c->ev_used = 0, c->ev_next = 0;
+    c->timed.clear();
   });
 }
 
@@ -559,6 +629,20 @@ MOE_API moe_status moe_dequantize(moe_ctx *c, uint32_t type, const uint8_t *bloc
 
 #define ROW(s, f) {#s "." #f, (uint32_t)offsetof(s, f), (uint32_t)sizeof(((s *)0)->f)}
 #define STRUCT(s) {#s, 0u, (uint32_t)sizeof(s)}
+
+MOE_API moe_status moe_prefill_dispatch(moe_ctx *c, MoeTile *tiles, uint32_t cap, uint32_t *ntiles, uint32_t *perm) {
+  return guarded(c, [&] {
+    require(ntiles != nullptr, "null ntiles");
+    require(c->last_pf_T > 0, "no prefill forward has run");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    check(hipMemcpy(ntiles, c->pf.ntiles, 4, hipMemcpyDeviceToHost), "read ntiles");
+    if (tiles && cap)
+      check(hipMemcpy(tiles, c->pf.tiles, sizeof(MoeTile) * std::min(cap, *ntiles), hipMemcpyDeviceToHost), "tiles");
+    if (perm)
+      check(hipMemcpy(perm, c->pf.perm, sizeof(uint32_t) * c->last_pf_T * c->cfg.n_used, hipMemcpyDeviceToHost),
+            "perm");
+  });
+}
 
 MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap) {
   static const moe_abi_row rows[] = {

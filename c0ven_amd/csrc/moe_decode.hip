@@ -17,7 +17,9 @@
 // Waits are bounded anyway: past kSpinLimit polls a wait gives up and sets *err.
 #include <hip/hip_runtime.h>
 
+#include "act_quant.h"
 #include "decode.h"
+#include "route.h"
 #include "device_math.h"
 #include "iq3s_grid.h"
 #include "layout.h"
@@ -33,23 +35,6 @@ constexpr uint32_t kSpinLimit = 1u << 22;
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 __device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
-
-// Data one work-group writes and another reads within a launch goes through device-coherent accesses (agent-scope
-// relaxed atomics: the store writes through the XCD's L2, the load reads past a stale line), so no fence has to
-// write back or invalidate a whole L2. Kernel boundaries order everything else.
-template <typename T>
-__device__ __forceinline__ void st_co(T *p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename T>
-__device__ __forceinline__ T ld_co(const T *p) {
-  return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// 16 bytes coherently, as four words.
-__device__ __forceinline__ uint4 ld_co4(const void *p) {
-  const uint32_t *q = (const uint32_t *)p;
-  return make_uint4(ld_co(q), ld_co(q + 1), ld_co(q + 2), ld_co(q + 3));
-}
 
 // This work-group's coherent stores are complete (every wave waits for its own, then the barrier).
 __device__ __forceinline__ void stores_done() {
@@ -115,63 +100,6 @@ __device__ __forceinline__ void wait_flags(const DecodeParams &p, uint32_t base,
   __syncthreads();
 }
 
-// One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
-// with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0).
-__device__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
-  uint32_t code[2] = {0u, 0u};
-  if (act_type == QT_Q8_K) {
-    // The value of largest magnitude, the first of equals: (|v|, index) reduced over the 32 lanes.
-    float amax = 0.0f, mx = 0.0f;
-    uint32_t at = 0xffffffffu;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float a = fabsf(v[i]);
-      if (a > amax) amax = a, mx = v[i], at = 8 * l32 + i;
-    }
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-      const float oa = __shfl_xor(amax, o, 32), om = __shfl_xor(mx, o, 32);
-      const uint32_t oi = __shfl_xor(at, o, 32);
-      if (oa > amax || (oa == amax && oi < at)) amax = oa, mx = om, at = oi;
-    }
-    float d = 0.0f;
-    int part = 0;
-    if (amax != 0.0f) {
-      const float iscale = __fdiv_rn(-127.0f, mx);
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        int q = nearest_int(__fmul_rn(iscale, v[i]));
-        q = q < 127 ? q : 127;
-        part += q;
-        code[i / 4] |= ((uint32_t)q & 0xffu) << (8 * (i % 4));
-      }
-      d = __fdiv_rn(1.0f, iscale);
-    }
-    part += __shfl_xor(part, 1, 32);
-    part += __shfl_xor(part, 2, 32);
-    st_co((uint32_t *)out + 2 * l32, code[0]);
-    st_co((uint32_t *)out + 2 * l32 + 1, code[1]);
-    if ((l32 & 3u) == 0) st_co((int32_t *)(out + kActSums) + l32 / 4, part);
-    if (l32 == 0) st_co((float *)(out + kActScales), d);
-  } else {  // q8_0: blocks of 32, four lanes each
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 32));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 32));
-    const float d = __fdiv_rn(amax, 127.0f), id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int q = nearest_int(__fmul_rn(v[i], id));
-      code[i / 4] |= ((uint32_t)q & 0xffu) << (8 * (i % 4));
-    }
-    st_co((uint32_t *)out + 2 * l32, code[0]);
-    st_co((uint32_t *)out + 2 * l32 + 1, code[1]);
-    if ((l32 & 3u) == 0) st_co((float *)(out + kActScales) + l32 / 4, h2f(f2h(d)));
-    if ((l32 & 3u) == 0) st_co((int32_t *)(out + kActSums) + l32 / 4, 0);
-  }
-}
-
 // Top-k, weights and the shared gate for token t (route.h:39-99 and layer.cl:765-804 restated). Two waves at once:
 // wave 1 takes the softmax's max and 1 / sum (the sum in double) and the shared gate; wave 0 selects: lane l holds
 // experts l + 64 i, sorted by (logit, lower id first), and each of the k rounds takes the wave's largest head (a DPP
@@ -180,70 +108,28 @@ __device__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, ui
 __device__ void route_token(const DecodeParams &p, uint32_t t, const uint64_t *tab, uint32_t *sel, float *norm) {
   const uint32_t lane = lane_id(), E = p.E, K = p.K;
   const float *lg = p.logits + (uint64_t)t * (E + 1);
-  constexpr int kPer = kMaxExperts / 64;
   uint32_t my_id = 0, my_key = 0;
   if (wave_id() <= 1) {
-    uint32_t key[kPer], id[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-      const uint32_t e = lane + 64 * i;
-      key[i] = e < E ? float_key(ld_co(lg + e)) : 0u;
-      id[i] = e;
-    }
+    uint32_t key[kRoutePer], id[kRoutePer];
+    route_load(lg, E, lane, key, id);
     if (wave_id() == 1) {
-      uint32_t mk = 0;
-#pragma unroll
-      for (int i = 0; i < kPer; i++) mk = max(mk, key[i]);
-      const float mx = key_float(wave_max_u32(mk));
-      double part = 0.0;
-#pragma unroll
-      for (int i = 0; i < kPer; i++)
-        if (lane + 64 * i < E) part = __dadd_rn(part, (double)expf_libm(__fsub_rn(key_float(key[i]), mx), tab));
-      const double sum = wave_sum_f64(part);
+      float mx, inv;
+      route_norm(key, E, lane, tab, &mx, &inv);
       if (lane == 0) {
-        norm[0] = mx;
-        norm[1] = (float)(1.0 / sum);
+        norm[0] = mx, norm[1] = inv;
         st_co(p.gs + t, sigmoid_libm(ld_co(lg + E), tab));
       }
     } else {
-      // Sort each lane's keys, largest first (ids ascending within a lane, so equal keys keep the lower id first).
-      auto cswap = [&](int i, int j) {
-        const bool sw = key[j] > key[i] || (key[j] == key[i] && id[j] < id[i]);
-        const uint32_t ki = key[i], ii = id[i];
-        key[i] = sw ? key[j] : ki, id[i] = sw ? id[j] : ii;
-        key[j] = sw ? ki : key[j], id[j] = sw ? ii : id[j];
-      };
-      cswap(0, 1), cswap(2, 3), cswap(4, 5), cswap(6, 7), cswap(0, 2), cswap(1, 3), cswap(4, 6), cswap(5, 7);
-      cswap(1, 2), cswap(5, 6), cswap(0, 4), cswap(3, 7), cswap(1, 5), cswap(2, 6), cswap(1, 4), cswap(3, 6);
-      cswap(2, 4), cswap(3, 5), cswap(3, 4);
-      for (uint32_t r = 0; r < K; r++) {
-        const uint32_t m = wave_max_u32(key[0]);
-        const uint64_t cand = __ballot(key[0] == m);
-        uint32_t wid;
-        if (__popcll(cand) == 1) {
-          wid = readlane_u32(id[0], __ffsll((long long)cand) - 1);
-        } else {
-          wid = wave_min_u32(key[0] == m ? id[0] : 0xffffffffu);
-        }
-        if (lane == r) my_id = wid, my_key = m;
-        if (key[0] == m && id[0] == wid) {  // pop the winner
-#pragma unroll
-          for (int i = 0; i < kPer - 1; i++) key[i] = key[i + 1], id[i] = id[i + 1];
-          key[kPer - 1] = 0;
-        }
-      }
+      route_select(key, id, K, lane, &my_id, &my_key);
       if (lane < K) sel[lane] = my_id, sel[kMaxUsed + lane] = my_key;
     }
   }
   __syncthreads();
   if (wave_id() == 0) {
-    const float pk = lane < K ? __fmul_rn(expf_libm(__fsub_rn(key_float(my_key), norm[0]), tab), norm[1]) : 0.0f;
-    float tot = 0.0f;
-    for (uint32_t r = 0; r < K; r++) tot = __fadd_rn(tot, __uint_as_float(readlane_u32(__float_as_uint(pk), r)));
-    const float den = fmaxf(tot, 6.1035e-5f);
+    const float w = route_weight(my_key, norm[0], norm[1], K, lane, tab);
     if (lane < K) {
       st_co(p.ids + t * K + lane, (int32_t)my_id);
-      st_co(p.w + t * K + lane, __fdiv_rn(pk, den));
+      st_co(p.w + t * K + lane, w);
     }
   }
 }

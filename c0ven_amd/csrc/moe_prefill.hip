@@ -1,0 +1,637 @@
+// The prefill path of the MoE block: router GEMM, top-k, counting-sort dispatch, grouped int8-MFMA expert GEMMs and
+// the combine. The kernel list and its reference counterparts are in prefill.h.
+//
+// Bits: every result equals the CPU oracle's (its ORACLE ORDER). The router sums exact bf16 products in fp64 in k
+// order, as the oracle does. The expert GEMMs take each 32-value block's integer dot product from one
+// v_mfma_i32_32x32x32_i8 (exact), then apply the block's integer scale (Q4_K, IQ3_S) or fp32 term (Q8_0) and each
+// unit's fp32 steps exactly as the decoders in units.h do, and sum a row's units as the same pairwise tree.
+#include <hip/hip_runtime.h>
+
+#include "act_quant.h"
+#include "device_math.h"
+#include "iq3s_grid.h"
+#include "layout.h"
+#include "prefill.h"
+#include "route.h"
+
+namespace c0ven {
+
+__device__ __constant__ static const uint32_t kIq3sGridPf[512] = {C0VEN_IQ3S_GRID_VALUES};
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t kPfWG = 256;
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
+__device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
+
+// ---------------------------------------------------------------------------------------------------------------
+// Activation units: one half-wave per (row, unit), eight values a lane; o2 (a second type) may be null.
+
+__global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_t ld, uint32_t rows, uint32_t U,
+                                                       uint32_t t1, uint8_t *o1, uint32_t t2, uint8_t *o2) {
+  const uint32_t hw = blockIdx.x * (kPfWG / 32) + threadIdx.x / 32, l32 = threadIdx.x & 31u;
+  const uint32_t row = hw / U, u = hw % U;
+  if (row >= rows) return;  // whole half-waves leave together
+  const float4 *p = (const float4 *)(src + (uint64_t)row * ld + u * kUnit + 8 * l32);
+  const float4 a = p[0], b = p[1];
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  quant_unit(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
+  if (o2) quant_unit(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Router: a 64-token x 64-row tile a work-group, 4 x 4 outputs a thread, K in chunks of 32 staged as doubles.
+// logits[t][e] = (float)(sum over k ascending of bf16(W[e][k]) bf16(x[t][k]), each product exact, in fp64)
+// (+ bias[e] for e < E): the oracle's sum, term for term.
+
+constexpr uint32_t kRtK = 32;
+
+__global__ void __launch_bounds__(kPfWG) pf_router(const float *x, uint32_t T, const uint16_t *W, const float *bias,
+                                                   uint32_t E, uint32_t H, float *logits) {
+  __shared__ double xs[kRtK][64], ws[kRtK][64];
+  const uint32_t t0 = blockIdx.x * 64, e0 = blockIdx.y * 64, tid = threadIdx.x;
+  const uint32_t tx = tid % 16, ty = tid / 16;  // rows 4 tx .., tokens 4 ty ..
+  const uint32_t sr = tid / 4, sk = 8 * (tid % 4);  // staging: row / token sr, values sk .. sk + 7
+  double acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = 0.0;
+  for (uint32_t k0 = 0; k0 < H; k0 += kRtK) {
+    float xv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint4 wv = make_uint4(0, 0, 0, 0);
+    if (t0 + sr < T) {
+      const float4 *p = (const float4 *)(x + (uint64_t)(t0 + sr) * H + k0 + sk);
+      const float4 a = p[0], b = p[1];
+      xv[0] = a.x, xv[1] = a.y, xv[2] = a.z, xv[3] = a.w, xv[4] = b.x, xv[5] = b.y, xv[6] = b.z, xv[7] = b.w;
+    }
+    if (e0 + sr <= E) wv = *(const uint4 *)(W + (uint64_t)(e0 + sr) * H + k0 + sk);
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      xs[sk + i][sr] = (double)round_bf16(xv[i]);
+      ws[sk + i][sr] = (double)__uint_as_float((i & 1) ? ww[i / 2] & 0xffff0000u : ww[i / 2] << 16);
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (uint32_t k = 0; k < kRtK; k++) {
+      double a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) a[i] = xs[k][4 * ty + i], b[i] = ws[k][4 * tx + i];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_fma(b[j], a[i], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t t = t0 + 4 * ty + i, e = e0 + 4 * tx + j;
+      if (t < T && e <= E) {
+        float l = (float)acc[i][j];
+        if (e < E && bias) l = __fadd_rn(l, bias[e]);
+        logits[(uint64_t)t * (E + 1) + e] = l;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Top-k: one wave a token (the decode kernel's steps, route.h, in one wave).
+
+__global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T, uint32_t E, uint32_t K,
+                                                 int32_t *ids, float *w, float *gs) {
+  __shared__ uint64_t tab[32];
+  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
+  const uint32_t t = blockIdx.x * (kPfWG / 64) + wave_id(), lane = lane_id();
+  if (t >= T) return;
+  const float *lg = logits + (uint64_t)t * (E + 1);
+  uint32_t key[kRoutePer], id[kRoutePer], my_id, my_key;
+  route_load(lg, E, lane, key, id);
+  float mx, inv;
+  route_norm(key, E, lane, tab, &mx, &inv);
+  route_select(key, id, K, lane, &my_id, &my_key);
+  const float wk = route_weight(my_key, mx, inv, K, lane, tab);
+  if (lane < K) {
+    ids[(uint64_t)t * K + lane] = (int32_t)my_id;
+    w[(uint64_t)t * K + lane] = wk;
+  }
+  if (lane == 0) gs[t] = sigmoid_libm(lg[E], tab);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Dispatch: one work-group of 1024. Counts per expert, exclusive scans of the counts and of the tiles, the MoeTile
+// records, then the positions 64 tokens at a time: an expert takes at most one assignment a token, so a 64-bit mask
+// of the tokens that chose it orders its assignments by token (stable, unlike p_moe_fill's atomic order).
+
+constexpr uint32_t kDispWG = 1024;
+
+__global__ void __launch_bounds__(kDispWG) pf_dispatch(const int32_t *ids, uint32_t T, uint32_t K, uint32_t E,
+                                                       uint32_t *perm, uint32_t *inv, MoeTile *tiles,
+                                                       uint32_t *ntiles) {
+  __shared__ uint32_t cnt[512], base[512], tb[512];
+  __shared__ unsigned long long mask[512];
+  const uint32_t tid = threadIdx.x, n = T * K;
+  if (tid < 512) cnt[tid] = 0u;
+  __syncthreads();
+  for (uint32_t a = tid; a < n; a += kDispWG) atomicAdd(&cnt[ids[a]], 1u);
+  __syncthreads();
+  // Inclusive scans (Hillis-Steele) of the counts and of the tiles per expert.
+  uint32_t c = tid < E ? cnt[tid] : 0u, nt = (c + MOE_TILE - 1) / MOE_TILE;
+  if (tid < 512) base[tid] = c, tb[tid] = nt;
+  __syncthreads();
+  for (uint32_t off = 1; off < 512; off <<= 1) {
+    uint32_t ab = 0, at = 0;
+    if (tid < 512 && tid >= off) ab = base[tid - off], at = tb[tid - off];
+    __syncthreads();
+    if (tid < 512) base[tid] += ab, tb[tid] += at;
+    __syncthreads();
+  }
+  if (tid < E) {
+    const uint32_t b0 = base[tid] - c, t0 = tb[tid] - nt;
+    for (uint32_t i = 0; i < nt; i++) {
+      MoeTile m;
+      m.expert = tid, m.slot = tid, m.start = b0 + MOE_TILE * i, m.count = min((uint32_t)MOE_TILE, c - MOE_TILE * i);
+      tiles[t0 + i] = m;
+    }
+  }
+  if (tid == 0) *ntiles = tb[511];
+  __syncthreads();
+  if (tid < 512) base[tid] -= (tid < E ? cnt[tid] : 0u);  // exclusive
+  __syncthreads();
+  for (uint32_t t0 = 0; t0 < T; t0 += 64) {
+    if (tid < 512) mask[tid] = 0ull;
+    __syncthreads();
+    const uint32_t a = t0 * K + tid;
+    const bool on = tid < 64 * K && a < n;
+    uint32_t e = 0, bit = 0;
+    if (on) {
+      e = (uint32_t)ids[a], bit = a / K - t0;
+      atomicOr(&mask[e], 1ull << bit);
+    }
+    __syncthreads();
+    if (on) {
+      const uint32_t pos = base[e] + (uint32_t)__popcll(mask[e] & ((1ull << bit) - 1ull));
+      perm[pos] = a;
+      inv[a] = pos;
+    }
+    __syncthreads();
+    if (tid < E) base[tid] += (uint32_t)__popcll(mask[tid]);
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Expert GEMMs on int8 MFMA.
+//
+// v_mfma_i32_32x32x32_i8: lane l gives A row l % 32, values 16 (l / 32) .. + 15 of the 32, and B column l % 32, the
+// same values; it receives D[m][l % 32] for m = 8 (r / 4) + 4 (l / 32) + r % 4, r < 16. Here A is activations (rows:
+// 32 of the tile's positions) and B is weights (columns: 32 weight rows), so a lane holds one weight row and 16
+// positions, and each 32-value block is one instruction.
+//
+// A lane's share of one unit (256 values) of its weight row: for block j, the 16 values 16 h .. 16 h + 15 (h = l / 32)
+// as int8 words, plus the block's integer scale (Q4_K, IQ3_S) or fp16 scale (Q8_0). The pieces come from the device
+// layout (layout.h) directly.
+
+__device__ __forceinline__ v4i as_v4i(uint4 v) {
+  v4i r;
+  r[0] = (int)v.x, r[1] = (int)v.y, r[2] = (int)v.z, r[3] = (int)v.w;
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ const T *pf_field(const uint8_t *tile, uint32_t base, uint32_t p, uint32_t idx, uint32_t nl) {
+  return (const T *)(tile + (uint64_t)base * nl) + (uint64_t)p * nl + idx;
+}
+
+struct SliceQ8_0 {
+  uint4 q[8];
+  float d[8];
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h, const uint32_t *) {
+#pragma unroll
+    for (int b = 0; b < 8; b++) q[b] = *pf_field<uint4>(tile, q8_0t::kQs, 2 * b + h, idx, nl);
+    const uint4 dv = *pf_field<uint4>(tile, q8_0t::kD, 0, idx, nl);
+    const uint32_t w[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+    for (int b = 0; b < 8; b++) d[b] = h2f((uint16_t)(w[b / 2] >> (16 * (b % 2))));
+  }
+  __device__ __forceinline__ v4i words(int j) const { return as_v4i(q[j]); }
+};
+
+struct SliceQ4_K {
+  uint4 q[4];  // qs pieces 2 c + h: bytes 32 c + 16 h .. + 15, low nibbles block 2 c, high nibbles block 2 c + 1
+  int sc[8], mn[8];
+  float d, dmin;
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h, const uint32_t *) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) q[c] = *pf_field<uint4>(tile, q4_kt::kQs, 2 * c + h, idx, nl);
+    uint8_t b[12];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const uint32_t v = *pf_field<uint32_t>(tile, q4_kt::kScales, i, idx, nl);
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[4 * i + j] = (uint8_t)(v >> (8 * j));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {  // get_scale_min_k4
+      if (j < 4) {
+        sc[j] = b[j] & 63;
+        mn[j] = b[j + 4] & 63;
+      } else {
+        sc[j] = (b[j + 4] & 0xF) | ((b[j - 4] >> 6) << 4);
+        mn[j] = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
+      }
+    }
+    const uint32_t dm = *pf_field<uint32_t>(tile, q4_kt::kDm, 0, idx, nl);
+    d = h2f((uint16_t)dm);
+    dmin = h2f((uint16_t)(dm >> 16));
+  }
+  __device__ __forceinline__ v4i words(int j) const {
+    const uint4 v = q[j / 2];
+    const int s = 4 * (j & 1);
+    v4i r;
+    r[0] = (int)((v.x >> s) & 0x0f0f0f0fu), r[1] = (int)((v.y >> s) & 0x0f0f0f0fu);
+    r[2] = (int)((v.z >> s) & 0x0f0f0f0fu), r[3] = (int)((v.w >> s) & 0x0f0f0f0fu);
+    return r;
+  }
+};
+
+struct SliceIQ3_S {
+  uint32_t qs[8], sg[8], qh[2];  // qs[ib]: the four grid-index bytes of block ib's half h (groups 8 ib + 4 h ..)
+  int ls[8];
+  float d;
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h, const uint32_t *) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) {  // qs piece p holds the index bytes of blocks 2 p and 2 p + 1 (words 0-1, 2-3)
+      const uint32_t *q = (const uint32_t *)pf_field<uint4>(tile, iq3_st::kQs, p, idx, nl) + h;
+      qs[2 * p] = q[0], qs[2 * p + 1] = q[2];
+    }
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const uint4 v = *pf_field<uint4>(tile, iq3_st::kSigns, p, idx, nl);
+      sg[4 * p] = v.x, sg[4 * p + 1] = v.y, sg[4 * p + 2] = v.z, sg[4 * p + 3] = v.w;
+    }
+    qh[0] = *pf_field<uint32_t>(tile, iq3_st::kQh, 0, idx, nl);
+    qh[1] = *pf_field<uint32_t>(tile, iq3_st::kQh, 1, idx, nl);
+    const uint32_t sc = *pf_field<uint32_t>(tile, iq3_st::kScales, 0, idx, nl);
+    d = h2f(*pf_field<uint16_t>(tile, iq3_st::kD, 0, idx, nl));
+#pragma unroll
+    for (int ib = 0; ib < 8; ib++) ls[ib] = 1 + 2 * (int)((sc >> (4 * ib)) & 15u);
+  }
+  // Block ib, half h: groups k = 8 ib + 4 h + g (four values each): index byte g of qs[ib], high bit
+  // 8 (ib % 4) + 4 h + g of qh word ib / 4, signs nibble 4 h + g of sign word ib.
+  __device__ __forceinline__ v4i words_h(int ib, uint32_t h, const uint32_t *grid) const {
+    const uint32_t qw = qs[ib];
+    const uint32_t hb = qh[ib / 4] >> (8 * (ib % 4) + 4 * h), sw = sg[ib] >> (16 * h);
+    v4i r;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const uint32_t ix = ((qw >> (8 * g)) & 0xffu) | (((hb >> g) & 1u) << 8);
+      const uint32_t gv = grid[ix];
+      const uint32_t nib = (sw >> (4 * g)) & 15u;
+      const uint32_t x = (nib * 0x00204081u) & 0x01010101u;
+      r[g] = (int)((gv ^ (x * 0xffu)) + x);
+    }
+    return r;
+  }
+};
+
+struct PfGemm {
+  const MoeTile *tiles;    // routed: the dispatch's tiles
+  const uint32_t *ntiles;
+  uint32_t shared_T;       // > 0: the shared expert over tokens 0 .. shared_T - 1 in order (implicit tiles)
+  const uint32_t *perm;    // routed gate/up: position -> assignment (token = assignment / K)
+  uint32_t K;
+  const uint8_t *act;      // activation units: by token (gate/up) or by position (down)
+  uint32_t act_by_pos;
+  const uint8_t *mat;      // expert e's matrix at mat + e * stride; up at + up_off
+  uint64_t stride, up_off;
+  float *out;              // position p's outputs at out + p * out_ld
+  uint32_t out_ld;
+  float limit;
+};
+
+// The pairwise tree of a row's units: unit u's terms are a leaf; pairs of equal size combine left + right as soon as
+// both exist (the oracle's order for a power-of-two number of units). The waiting left halves sit in LDS (a level, a
+// term, a lane: consecutive lanes at consecutive words); the root stays in registers.
+template <uint32_t kLU>
+__device__ __forceinline__ void tree_push(float *lvl, float (&t)[16], uint32_t u, uint32_t lane, float (&root)[16]) {
+  uint32_t b = 0;
+  for (; b < kLU && ((u >> b) & 1u); b++) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) t[r] = __fadd_rn(lvl[(b * 16 + r) * 64 + lane], t[r]);
+  }
+  if (b < kLU) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) lvl[(b * 16 + r) * 64 + lane] = t[r];
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; r++) root[r] = t[r];
+  }
+}
+
+// One tile (at most 64 positions) x 32 rows of gate and of up (kGU: waves 0-1 gate, 2-3 up, SwiGLU at the end) or x
+// 64 rows of down (waves 2 w + ..: rows 32 (w / 2)); waves of even / odd index take positions 0-31 / 32-63.
+template <uint32_t kType, uint32_t kLU, bool kGU>
+__global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
+  constexpr uint32_t U = 1u << kLU;
+  __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
+  __shared__ uint4 meta[64][4];     // per position: the unit's scales (dwords 0-7) and q8_K sums (8-15)
+  __shared__ float ub[kGU ? 64 : 1][33];
+  __shared__ uint32_t arow_lds[64];
+  __shared__ uint64_t tab[32];
+  __shared__ float tree_lds[(kPfWG / 64) * (kLU ? kLU : 1) * 16 * 64];
+  uint32_t start, count, e;
+  if (g.shared_T) {
+    start = MOE_TILE * blockIdx.x;
+    if (start >= g.shared_T) return;
+    count = min((uint32_t)MOE_TILE, g.shared_T - start), e = 0;
+  } else {
+    if (blockIdx.x >= *g.ntiles) return;
+    const MoeTile tl = g.tiles[blockIdx.x];
+    start = tl.start, count = tl.count, e = tl.slot;
+  }
+  const uint32_t tid = threadIdx.x, w = wave_id(), l = lane_id(), h = l / 32, n = l % 32, half = w & 1u;
+  if (tid < 32) tab[tid] = kExp2Tab[tid];
+  if (kType == QT_IQ3_S)
+    for (uint32_t i = tid; i < 512; i += kPfWG) grid_lds[i] = kIq3sGridPf[i];
+  if (tid < 64) {
+    const uint32_t pos = start + tid;
+    arow_lds[tid] = tid < count ? (g.act_by_pos ? pos : (g.perm ? g.perm[pos] / g.K : pos)) : 0xffffffffu;
+  }
+  __syncthreads();
+  const uint32_t mat = kGU ? (w >> 1) : 0u;
+  const uint32_t row = (kGU ? blockIdx.y * 32 : blockIdx.y * 64 + 32 * (w >> 1)) + n;
+  const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
+  const uint8_t *tile = M + (uint64_t)(row / kTileRows) * tile_bytes(kType, U);
+  const uint32_t idx0 = (row % kTileRows) * U, nl = kTileRows * U;
+  const uint32_t arow = arow_lds[32 * half + n];  // this lane's A row (position 32 half + l % 32)
+  const uint8_t *aptr = arow != 0xffffffffu ? g.act + (uint64_t)arow * U * kActBytes : nullptr;
+  float root[16];
+  float *lvl = tree_lds + (uint64_t)w * (kLU ? kLU : 1) * 16 * 64;
+  for (uint32_t u = 0; u < U; u++) {
+    // The unit's per-position scales and sums.
+    {
+      const uint32_t tk = tid / 4, part = tid % 4, ar = arow_lds[tk];
+      meta[tk][part] = ar != 0xffffffffu
+                           ? *(const uint4 *)(g.act + ((uint64_t)ar * U + u) * kActBytes + kActScales + 16 * part)
+                           : make_uint4(0, 0, 0, 0);
+    }
+    uint4 av[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      av[j] = aptr ? *(const uint4 *)(aptr + (uint64_t)u * kActBytes + 32 * j + 16 * h) : make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    float t[16];
+    if constexpr (kType == QT_Q8_0) {
+      SliceQ8_0 s;
+      s.load(tile, idx0 + u, nl, h, grid_lds);
+      float q[3][16];  // the eight block terms' pairwise tree
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(av[j]), s.words(j), v16i{}, 0, 0, 0);
+        float c[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
+          const float as = __uint_as_float(((const uint32_t *)&meta[m][0])[j]);
+          c[r] = __fmul_rn(__fmul_rn(s.d[j], as), (float)dv[r]);
+        }
+        // tree over j: levels 0..2
+        if ((j & 1) == 0) {
+#pragma unroll
+          for (int r = 0; r < 16; r++) q[0][r] = c[r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[0][r], c[r]);
+          if ((j & 2) == 0) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) q[1][r] = c[r];
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[1][r], c[r]);
+            if ((j & 4) == 0) {
+#pragma unroll
+              for (int r = 0; r < 16; r++) q[2][r] = c[r];
+            } else {
+#pragma unroll
+              for (int r = 0; r < 16; r++) t[r] = __fadd_rn(q[2][r], c[r]);
+            }
+          }
+        }
+      }
+    } else if constexpr (kType == QT_Q4_K) {
+      SliceQ4_K s;
+      s.load(tile, idx0 + u, nl, h, grid_lds);
+      int isum[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) isum[r] = 0;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(av[j]), s.words(j), v16i{}, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; r++) isum[r] += s.sc[j] * dv[r];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
+        const uint4 s0 = meta[m][2], s1 = meta[m][3];
+        const int bs[8] = {(int)s0.x, (int)s0.y, (int)s0.z, (int)s0.w, (int)s1.x, (int)s1.y, (int)s1.z, (int)s1.w};
+        int imin = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) imin += s.mn[j] * bs[j];
+        const float ad = __uint_as_float(meta[m][0].x);
+        const float dd = __fmul_rn(s.d, ad), dm = __fmul_rn(s.dmin, ad);
+        const float pm = __fmul_rn(dm, (float)imin);
+        t[r] = __builtin_fmaf(dd, (float)isum[r], -pm);
+      }
+    } else {
+      SliceIQ3_S s;
+      s.load(tile, idx0 + u, nl, h, grid_lds);
+      int isum[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) isum[r] = 0;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(av[j]), s.words_h(j, h, grid_lds), v16i{}, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; r++) isum[r] += s.ls[j] * dv[r];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
+        const float ad = __uint_as_float(meta[m][0].x);
+        t[r] = __fmul_rn(__fmul_rn(s.d, ad), (float)isum[r]);
+      }
+    }
+    tree_push<kLU>(lvl, t, u, l, root);
+    __syncthreads();  // meta is rewritten by the next unit
+  }
+  // Outputs: position 32 half + m_r, weight row `row`.
+  if constexpr (kGU) {
+    if (mat == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) ub[32 * half + 8 * (r / 4) + 4 * h + (r % 4)][n] = root[r];
+    }
+    __syncthreads();
+    if (mat == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
+        if (m < count)
+          g.out[(uint64_t)(start + m) * g.out_ld + row] = swiglu_one(root[r], ub[m][n], g.limit, tab);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
+      if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row] = root[r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Combine: y[t][r] = sum_k w[t][k] y_asg[inv[t K + k]][r] in rank order, then + gs[t] y_sh[t][r]; four rows a thread.
+
+__global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const uint32_t *inv, const float *w,
+                                                    uint32_t K, const float *y_sh, const float *gs, uint32_t T,
+                                                    uint32_t H, float *y) {
+  const uint64_t i = (uint64_t)blockIdx.x * kPfWG + threadIdx.x;
+  const uint32_t H4 = H / 4;
+  if (i >= (uint64_t)T * H4) return;
+  const uint32_t t = (uint32_t)(i / H4), r4 = (uint32_t)(i % H4);
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (uint32_t k = 0; k < K; k++) {
+    const float wk = w[(uint64_t)t * K + k];
+    const float4 v = ((const float4 *)(y_asg + (uint64_t)inv[(uint64_t)t * K + k] * H))[r4];
+    acc.x = __fadd_rn(acc.x, __fmul_rn(wk, v.x)), acc.y = __fadd_rn(acc.y, __fmul_rn(wk, v.y));
+    acc.z = __fadd_rn(acc.z, __fmul_rn(wk, v.z)), acc.w = __fadd_rn(acc.w, __fmul_rn(wk, v.w));
+  }
+  if (y_sh) {
+    const float g = gs[t];
+    const float4 v = ((const float4 *)(y_sh + (uint64_t)t * H))[r4];
+    acc.x = __fadd_rn(acc.x, __fmul_rn(g, v.x)), acc.y = __fadd_rn(acc.y, __fmul_rn(g, v.y));
+    acc.z = __fadd_rn(acc.z, __fmul_rn(g, v.z)), acc.w = __fadd_rn(acc.w, __fmul_rn(g, v.w));
+  }
+  ((float4 *)(y + (uint64_t)t * H))[r4] = acc;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Host side.
+
+template <uint32_t kType, bool kGU>
+void launch_gemm_lu(uint32_t LU, dim3 grid, const PfGemm &g, hipStream_t s) {
+  switch (LU) {
+    case 0: pf_gemm<kType, 0, kGU><<<grid, kPfWG, 0, s>>>(g); break;
+    case 1: pf_gemm<kType, 1, kGU><<<grid, kPfWG, 0, s>>>(g); break;
+    case 2: pf_gemm<kType, 2, kGU><<<grid, kPfWG, 0, s>>>(g); break;
+    case 3: pf_gemm<kType, 3, kGU><<<grid, kPfWG, 0, s>>>(g); break;
+    case 4: pf_gemm<kType, 4, kGU><<<grid, kPfWG, 0, s>>>(g); break;
+    default: pf_gemm<kType, 5, kGU><<<grid, kPfWG, 0, s>>>(g); break;
+  }
+}
+
+template <bool kGU>
+void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
+  uint32_t LU = 0;
+  while ((1u << LU) < U) LU++;
+  if (type == QT_Q8_0)
+    launch_gemm_lu<QT_Q8_0, kGU>(LU, grid, g, s);
+  else if (type == QT_Q4_K)
+    launch_gemm_lu<QT_Q4_K, kGU>(LU, grid, g, s);
+  else
+    launch_gemm_lu<QT_IQ3_S, kGU>(LU, grid, g, s);
+}
+
+struct HookScope {
+  const PfHook &h;
+  const char *name;
+  hipStream_t s;
+  HookScope(const PfHook &hk, const char *n, hipStream_t st) : h(hk), name(n), s(st) {
+    if (h.fn) h.fn(h.ctx, name, 0, s);
+  }
+  ~HookScope() {
+    if (h.fn) h.fn(h.ctx, name, 1, s);
+  }
+};
+
+}  // namespace
+
+hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, const float *x, float *y, hipStream_t st,
+                     const PfHook &hook) {
+  const uint32_t H = S.H, F = S.F, E = S.E, K = S.K, T = S.T, Ug = H / kUnit, Ud = F / kUnit;
+  const uint32_t xr = quant_vec_dot_type(S.gate_type);
+  const uint32_t xs = S.has_shared ? quant_vec_dot_type(S.sh_gate_type) : xr;
+  const uint32_t hr = quant_vec_dot_type(S.down_type), hs = quant_vec_dot_type(S.sh_down_type);
+  const uint32_t halfwaves = kPfWG / 32;
+  {
+    HookScope k(hook, "pf_quant_x", st);
+    pf_quant_rows<<<(T * Ug + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(x, H, T, Ug, xr, b.act_r, xs,
+                                                                            b.act_s != b.act_r ? b.act_s : nullptr);
+  }
+  {
+    HookScope k(hook, "pf_router", st);
+    pf_router<<<dim3((T + 63) / 64, (E + 1 + 63) / 64), kPfWG, 0, st>>>(x, T, L.router, L.bias, E, H, b.logits);
+  }
+  {
+    HookScope k(hook, "pf_topk", st);
+    pf_topk<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, T, E, K, b.ids, b.w, b.gs);
+  }
+  {
+    HookScope k(hook, "pf_dispatch", st);
+    pf_dispatch<<<1, kDispWG, 0, st>>>(b.ids, T, K, E, b.perm, b.inv, b.tiles, b.ntiles);
+  }
+  const uint32_t mt = pf_max_tiles(T, K, E), st_tiles = (T + MOE_TILE - 1) / MOE_TILE;
+  {
+    HookScope k(hook, "pf_gate_up", st);
+    PfGemm g{};
+    g.tiles = b.tiles, g.ntiles = b.ntiles, g.perm = b.perm, g.K = K, g.act = b.act_r, g.act_by_pos = 0;
+    g.mat = L.experts, g.stride = L.ex_bytes, g.up_off = L.ex_up_off, g.out = b.h, g.out_ld = F;
+    g.limit = S.swiglu_limit;
+    launch_gemm<true>(S.gate_type, Ug, dim3(mt, F / 32), g, st);
+    if (S.has_shared) {
+      PfGemm q = g;
+      q.tiles = nullptr, q.ntiles = nullptr, q.shared_T = T, q.perm = nullptr, q.act = b.act_s;
+      q.mat = L.shared, q.stride = 0, q.up_off = L.sh_up_off, q.out = b.h_sh;
+      launch_gemm<true>(S.sh_gate_type, Ug, dim3(st_tiles, F / 32), q, st);
+    }
+  }
+  {
+    HookScope k(hook, "pf_quant_h", st);
+    pf_quant_rows<<<(T * K * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(b.h, F, T * K, Ud, hr, b.hact, 0,
+                                                                              nullptr);
+    if (S.has_shared)
+      pf_quant_rows<<<(T * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(b.h_sh, F, T, Ud, hs, b.hact_sh, 0,
+                                                                            nullptr);
+  }
+  {
+    HookScope k(hook, "pf_down", st);
+    PfGemm g{};
+    g.tiles = b.tiles, g.ntiles = b.ntiles, g.K = K, g.act = b.hact, g.act_by_pos = 1;
+    g.mat = L.experts + L.ex_down_off, g.stride = L.ex_bytes, g.out = b.y_asg, g.out_ld = H;
+    launch_gemm<false>(S.down_type, Ud, dim3(mt, H / 64), g, st);
+    if (S.has_shared) {
+      PfGemm q = g;
+      q.tiles = nullptr, q.ntiles = nullptr, q.shared_T = T, q.act = b.hact_sh;
+      q.mat = L.shared + L.sh_down_off, q.stride = 0, q.out = b.y_sh;
+      launch_gemm<false>(S.sh_down_type, Ud, dim3(st_tiles, H / 64), q, st);
+    }
+  }
+  {
+    HookScope k(hook, "pf_combine", st);
+    const uint64_t n = (uint64_t)T * (H / 4);
+    pf_combine<<<(uint32_t)((n + kPfWG - 1) / kPfWG), kPfWG, 0, st>>>(b.y_asg, b.inv, b.w, K,
+                                                                        S.has_shared ? b.y_sh : nullptr, b.gs, T, H, y);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace c0ven

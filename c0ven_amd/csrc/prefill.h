@@ -1,0 +1,68 @@
+// The prefill path of the MoE block (more tokens than the decode kernel takes): its shapes, buffers and launcher.
+//
+// Replaces the reference's prefill kernel list for the block (prompt.cpp:609-655): p_router (prompt.cl:653-679),
+// p_moe_count / p_moe_scan / p_moe_fill / p_moe_scatter (prompt.cl:682-755), moe_gate_up_t (qgemm.cl:88-161),
+// moe_down_t (qgemm.cl:227-239) and p_moe_combine (prompt.cl:769-787). Kernels, in stream order:
+//   pf_quant_rows  x -> the experts' activation units (q8_K or q8_0, the CPU rules)
+//   pf_router      logits = bf16(W) bf16(x) summed in fp64 in k order (each product exact), rounded once, + bias
+//   pf_topk        one wave a token: softmax, top k, weights, shared gate
+//   pf_dispatch    counting sort of the T k assignments by expert (stable: token order within an expert) into
+//                  MoeTile[] of at most MOE_TILE rows, perm (position -> assignment) and inv (assignment -> position)
+//   pf_gemm<GU>    per tile and 32 rows: gate and up on int8 MFMA (one 32x32x32 instruction per 32-value block,
+//                  exact int32), the block's integer scales and the unit's fp32 term in the oracle's order, SwiGLU
+//   pf_quant_rows  h -> the down's activation units
+//   pf_gemm<D>     per tile and 64 rows: down, the same way
+//   pf_combine     y_t = sum_k w_k y_(t,k) in rank order + gs_t s_t
+// The shared expert runs through the same GEMMs over the tokens in order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/c0ven_moe_tile.h"
+
+namespace c0ven {
+
+struct PfShape {
+  uint32_t H, F, E, K, T;
+  uint32_t gate_type, down_type, sh_gate_type, sh_down_type, has_shared;
+  float swiglu_limit;
+};
+
+struct PfLayer {
+  const uint16_t *router;  // (E + 1) x H bf16
+  const float *bias;       // E or null
+  const uint8_t *experts;  // expert e at experts + e * ex_bytes (gate, up at ex_up_off, down at ex_down_off)
+  uint64_t ex_bytes, ex_up_off, ex_down_off;
+  const uint8_t *shared;
+  uint64_t sh_up_off, sh_down_off;
+};
+
+// Scratch for up to Tmax tokens (allocated at open).
+struct PfBufs {
+  uint8_t *act_r, *act_s;  // Tmax x (H / 256) activation units (act_s == act_r when the types agree)
+  float *logits;           // Tmax x (E + 1)
+  int32_t *ids;            // Tmax x K
+  float *w, *gs;           // Tmax x K, Tmax
+  uint32_t *perm, *inv;    // Tmax K
+  MoeTile *tiles;          // Tmax K / MOE_TILE + E
+  uint32_t *ntiles;        // 1
+  float *h, *h_sh;         // Tmax K x F (expert order), Tmax x F
+  uint8_t *hact, *hact_sh; // the same rows quantised, (F / 256) units each
+  float *y_asg, *y_sh;     // Tmax K x H (expert order), Tmax x H
+};
+
+// Called around every kernel launch (timing); may be null.
+struct PfHook {
+  void (*fn)(void *ctx, const char *kernel, int after, hipStream_t s);
+  void *ctx;
+};
+
+constexpr uint32_t pf_max_tiles(uint32_t T, uint32_t K, uint32_t E) { return (T * K + MOE_TILE - 1) / MOE_TILE + E; }
+
+// Enqueues the block for s.T tokens of x (T x H fp32, rows contiguous, device) into y (the same shape); returns the
+// launches' error state.
+hipError_t prefill_forward(const PfShape &s, const PfLayer &L, const PfBufs &b, const float *x, float *y, hipStream_t st,
+                     const PfHook &hook);
+
+}  // namespace c0ven

@@ -57,7 +57,7 @@ typedef struct {
   uint32_t has_shared;   /* 1: one shared expert with a sigmoid gate (the router's row E) */
   uint32_t sh_gate_type; /* the shared expert's types */
   uint32_t sh_down_type;
-  uint32_t max_tokens;   /* the most tokens one forward takes (default 16) */
+  uint32_t max_tokens;   /* the most tokens one forward takes, at most 16384 (default 16) */
   float swiglu_limit;    /* > 0: gate = min(gate, L), up = clamp(up, -L, L) before the SiLU; 0 = off */
   int32_t device;        /* HIP device ordinal */
   uint32_t reserved[4];
@@ -94,7 +94,9 @@ MOE_API moe_status moe_load_expert(moe_ctx *ctx, uint32_t layer, uint32_t expert
                                    const uint8_t *up, const uint8_t *down);
 
 /* The block for ntok rows of x (host memory, rows x_stride floats apart) into y (y_stride): router, experts, shared
- * expert, combine. Synchronous. route may be null. */
+ * expert, combine. Synchronous. route may be null. Up to 16 tokens run the decode kernel (the decode and verify
+ * shapes); more run the prefill kernels (router GEMM, counting-sort dispatch into MoeTiles, grouped MFMA expert GEMMs,
+ * combine), up to max_tokens. */
 MOE_API moe_status moe_forward(moe_ctx *ctx, uint32_t layer, const float *x, uint32_t ntok, uint64_t x_stride,
                                float *y, uint64_t y_stride, moe_route_out *route);
 /* The same on device memory (x and y ntok x n_embd fp32, contiguous; ids and w ntok x n_used or null), enqueued on
@@ -108,6 +110,12 @@ MOE_API moe_status moe_forward_experts(moe_ctx *ctx, const moe_job *jobs, uint32
 /* CpuExperts::h_rows (core/cpu/experts.h:52-56): the h rows one pass of the down kernels takes, 256 here (one unit;
  * the GPU path has no task split). 0 when n_ff is not a multiple of it. */
 MOE_API uint32_t moe_h_rows(const moe_config *cfg);
+
+/* The dispatch of the last prefill forward (p_moe_count / scan / fill, prompt.cl:682-738): ntiles receives the number
+ * of MoeTiles, tiles (room for cap) the tiles in expert order, perm (ntok x n_used, or null) the assignment
+ * (token * n_used + rank) at each row of the expert-ordered activations. Within an expert the rows are in token
+ * order (the reference's fill takes atomic order). Synchronous. */
+MOE_API moe_status moe_prefill_dispatch(moe_ctx *ctx, MoeTile *tiles, uint32_t cap, uint32_t *ntiles, uint32_t *perm);
 
 /* Waits for the context's stream. */
 MOE_API moe_status moe_sync(moe_ctx *ctx);

@@ -1,0 +1,108 @@
+"""The prefill path (more than 16 tokens: router GEMM, counting-sort dispatch, grouped int8-MFMA GEMMs, combine)
+against the CPU oracle, through the C ABI, on the GPU.
+
+Like the decode path it reproduces the oracle's every rounding, so ids, weights and y are held to bit equality (the
+bar itself is max-abs 1e-3 and rel-L2 1e-4). The dispatch is checked against a stable counting sort in numpy: the
+MoeTiles (shared/moe_tile.h:11-18) cover each expert's assignments in token order, at most MOE_TILE rows a tile.
+At BASELINE's config 4 size (2048 tokens, 512 experts, top-10) the oracle runs on a sample of the tokens, since each
+token's output depends on that token alone.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from tests import harness as h
+from tests.harness import moe
+
+pytestmark = pytest.mark.gpu
+Q8, Q4, I3 = moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def expected_dispatch(ids, E):
+    flat = ids.ravel()
+    perm, tiles = [], []
+    for e in range(E):
+        a = np.nonzero(flat == e)[0]
+        for i in range(0, len(a), 64):
+            tiles.append((e, e, len(perm) + i, min(64, len(a) - i)))
+        perm.extend(a.tolist())
+    return np.array(tiles, dtype=np.uint32).reshape(-1, 4), np.array(perm, dtype=np.uint32)
+
+
+def check_exact(y, ids, w, yo, io, wo):
+    assert np.array_equal(ids, io), "top-k ids differ"
+    ma, rl = h.max_abs(y, yo), h.rel_l2(y, yo)
+    assert ma <= 1e-3 and rl <= 1e-4, (ma, rl)
+    assert np.array_equal(w, wo), "weights not bit-exact: %g" % h.max_abs(w, wo)
+    assert np.array_equal(y, yo), "y not bit-exact: max-abs %g rel-L2 %g" % (ma, rl)
+
+
+@pytest.mark.parametrize("types", [(Q8, Q8, Q8, Q8), (Q4, Q4, Q4, Q4), (I3, I3, I3, I3), (I3, Q4, Q8, Q8),
+                                   (Q4, Q8, I3, Q4)])
+@pytest.mark.parametrize("T", [17, 100, 300])
+def test_prefill_small(types, T):
+    gt, dt, sgt, sdt = types
+    say("prefill small", [moe.TYPE_NAMES[t] for t in types], "T", T)
+    L = h.Layer(512, 256, 64, 4, gt, dt, sgt, sdt, seed=31 + T, zipf=1.1 if T == 100 else None)
+    blk = L.block(max_tokens=512)
+    L.upload(blk)
+    x = h.tokens(5 + T, T, 512)
+    y, ids, w = blk.forward(0, x)
+    tiles, perm = blk.prefill_dispatch(T)
+    et, ep = expected_dispatch(ids, L.E)
+    assert np.array_equal(tiles, et) and np.array_equal(perm, ep)
+    check_exact(y, ids, w, *L.oracle_forward(x))
+    blk.close()
+
+
+@pytest.mark.parametrize("H,F", [(1024, 512), (2048, 256)])
+def test_prefill_shapes_no_shared_and_limit(H, F):
+    say("prefill shapes", H, F)
+    L = h.Layer(H, F, 32, 8, Q4, I3, has_shared=False, seed=9, swiglu_limit=0.02)
+    blk = L.block(max_tokens=256)
+    L.upload(blk)
+    x = h.tokens(3, 130, H)
+    y, ids, w = blk.forward(0, x)
+    check_exact(y, ids, w, *L.oracle_forward(x))
+    blk.close()
+
+
+def test_prefill_then_decode_share_a_context():
+    """Both paths on one context, alternating: each call's result stands alone."""
+    say("prefill and decode alternate")
+    L = h.Layer(512, 256, 64, 6, Q4, Q8, seed=77)
+    blk = L.block(max_tokens=128)
+    L.upload(blk)
+    for T in (40, 3, 128, 16, 17):
+        x = h.tokens(T, T, 512)
+        y, ids, w = blk.forward(0, x)
+        check_exact(y, ids, w, *L.oracle_forward(x))
+    blk.close()
+
+
+def test_prefill_config4_sampled():
+    """2048 tokens, H 2048, F 512, 512 experts, top-10 + shared, Q4_K, Zipf(1.1)."""
+    say("prefill config 4")
+    L = h.Layer(2048, 512, 512, 10, Q4, Q4, seed=2026, zipf=1.1, nthreads=0)
+    blk = L.block(max_tokens=2048)
+    L.upload(blk)
+    T = 2048
+    x = h.tokens(2026, T, 2048)
+    y, ids, w = blk.forward(0, x)
+    tiles, perm = blk.prefill_dispatch(T)
+    et, ep = expected_dispatch(ids, L.E)
+    assert np.array_equal(tiles, et) and np.array_equal(perm, ep)
+    assert tiles[:, 3].sum() == T * 10 and tiles[:, 3].max() <= 64
+    _, io, wo = L.oracle_route(x)
+    assert np.array_equal(ids, io) and np.array_equal(w, wo)
+    sample = np.r_[0:48, 1000:1016, T - 48:T]
+    yo, io2, _ = L.oracle_forward(x[sample], nthreads=16)
+    assert np.array_equal(io2, ids[sample])
+    check_exact(y[sample], ids[sample], w[sample], yo, io2, w[sample])
+    blk.close()
