@@ -8,7 +8,8 @@ Cache defeat: the MI355X's 256 MB Infinity Cache would hold one layer's touched 
 as several layers (independent routers and biases, so each step routes differently) whose touched bytes sum past
 512 MB, and step i runs layer i mod n_layers.
 
-Prints one JSON line. --config picks another of BASELINE's decode configs (1, 2, 3, 3b).
+Prints one JSON line. --config picks another of BASELINE's configs: decode 1, 2, 3, 3b; prefill 4 (2048 tokens, where
+the roofline object is the dominant kernel's int8 MFMA rate and the block's HBM rate is reported beside it).
 """
 import argparse
 import ctypes as C
@@ -27,9 +28,11 @@ CONFIGS = {
     "2": dict(name="config2: verify T=8, Q4_K, Zipf(1.1)", types=(12, 12, 12, 12), T=8, zipf=1.1),
     "3": dict(name="config3: decode T=1, IQ3_S", types=(21, 21, 21, 21), T=1, zipf=None),
     "3b": dict(name="config3: decode T=4, IQ3_S", types=(21, 21, 21, 21), T=4, zipf=None),
+    "4": dict(name="config4: prefill T=2048, Q4_K, Zipf(1.1)", types=(12, 12, 12, 12), T=2048, zipf=1.1),
 }
 H, F, E, K = 2048, 512, 512, 10
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
 
 
 class Hip:
@@ -60,8 +63,8 @@ class Hip:
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=None, help="default 2000 (decode), 100 (prefill)")
+    ap.add_argument("--warmup", type=int, default=None, help="default 200 (decode), 10 (prefill)")
     ap.add_argument("--config", default="2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
     ap.add_argument("--no-cpu", action="store_true")
@@ -77,6 +80,10 @@ def main():
     cfg = CONFIGS[args.config]
     gt, dt, sgt, sdt = cfg["types"]
     T = cfg["T"]
+    if T > 16:
+        return prefill(args, cfg, moe, h)
+    args.steps = 2000 if args.steps is None else args.steps
+    args.warmup = 200 if args.warmup is None else args.warmup
     hip = Hip()
     t_setup = time.time()
     # Layer 0's weights, drawn once; the other layers hold copies of its experts (other addresses, so no cache reuse)
@@ -172,6 +179,92 @@ def main():
         "block": {"achieved_gbs": round(block_gbs, 1), "frac": round(block_gbs / HBM_PEAK_GBS, 4),
                   "gate_up_bytes": int(gu_bytes), "down_bytes": int(dn_bytes),
                   "kernel_avg_ms": {k: round(v, 5) for k, v in ktimes.items()}, "timed_forwards": nf},
+        "parity": parity,
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(out), flush=True)
+    blk.close()
+
+
+def prefill(args, cfg, moe, h):
+    """Config 4: one forward of 2048 tokens is a step. One resident layer: its 906 MB of experts already exceed the
+    Infinity Cache, and every step reads all of them."""
+    steps = 100 if args.steps is None else args.steps
+    warmup = 10 if args.warmup is None else args.warmup
+    gt, dt, sgt, sdt = cfg["types"]
+    T = cfg["T"]
+    hip = Hip()
+    t_setup = time.time()
+    L0 = h.Layer(H, F, E, K, gt, dt, sgt, sdt, seed=2026, layer=0, zipf=cfg["zipf"])
+    blk = moe.MoeBlock(H, F, E, K, gt, dt, True, sgt, sdt, n_layer=1, max_tokens=T)
+    L0.upload(blk, 0)
+    x = h.tokens(2026, T, H)
+    xd, yd, idsd = hip.malloc(x.nbytes), hip.malloc(x.nbytes), hip.malloc(T * K * 4)
+    hip.h2d(xd, x)
+    ids = np.empty((T, K), np.int32)
+    blk.forward_async(0, xd, T, yd, idsd)
+    hip.sync()
+    hip.d2h(ids, idsd)
+    touched = len(set(ids.ravel().tolist()))
+    setup_s = time.time() - t_setup
+    for _ in range(warmup):
+        blk.forward_async(0, xd, T, yd)
+    hip.sync()
+    blk.set_timing(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        blk.forward_async(0, xd, T, yd)
+    hip.sync()
+    t1 = time.perf_counter()
+    ktimes, nf = blk.kernel_times()
+    blk.set_timing(False)
+    ms_step = (t1 - t0) * 1e3 / steps
+    tok_s = T * steps / (t1 - t0)
+    # Algorithmic work (SURVEY 8(d)): 2 FLOP per weight per assignment (gate, up, down), the shared expert per token,
+    # the router's (E + 1) rows per token; bytes: every touched expert's weights, the shared one, the router, once.
+    ex_bytes = 2 * moe.row_bytes(gt, H) * F + moe.row_bytes(dt, F) * H
+    sh_bytes = 2 * moe.row_bytes(sgt, H) * F + moe.row_bytes(sdt, F) * H
+    gu_flop = 2.0 * (T * K + T) * 2 * F * H
+    dn_flop = 2.0 * (T * K + T) * F * H
+    router_flop = 2.0 * T * (E + 1) * H
+    block_flop = gu_flop + dn_flop + router_flop
+    block_bytes = touched * ex_bytes + sh_bytes + (E + 1) * H * 2
+    gu_ms = ktimes.get("pf_gate_up", float("nan"))
+    gu_tops = gu_flop / (gu_ms * 1e-3) / 1e12
+    # Parity on a sample of tokens (each token's output depends on that token alone), and the CPU baseline.
+    y = np.empty_like(x)
+    blk.forward_async(0, xd, T, yd, idsd)
+    hip.sync()
+    hip.d2h(y, yd)
+    hip.d2h(ids, idsd)
+    sample = np.r_[0:32, T - 32:T]
+    tc0 = time.perf_counter()
+    yo, io, _ = L0.oracle_forward(x[sample], nthreads=min(16, os.cpu_count() or 1))
+    cpu_s = time.perf_counter() - tc0
+    parity = dict(sample_tokens=len(sample), ids_equal=bool(np.array_equal(ids[sample], io)),
+                  y_bit_exact=bool(np.array_equal(y[sample], yo)), max_abs=h.max_abs(y[sample], yo),
+                  rel_l2=h.rel_l2(y[sample], yo))
+    cores = min(16, os.cpu_count() or 1)
+    cpu = None if args.no_cpu else {
+        "value": round(len(sample) / cpu_s, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+        "sample": "%d of the %d tokens (routing, experts, shared expert, combine) by oracle/oracle.c with %d OpenMP "
+                  "threads, %.1f s" % (len(sample), T, cores, cpu_s)}
+    out = {
+        "metric": "MoE block tokens/s + achieved HBM GB/s (decode), TFLOP/s (prefill) on 1 GPU",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": cfg["name"], "n_embd": H, "n_ff": F, "n_expert": E, "n_used": K, "shared": True,
+                   "tokens": T, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]], "touched_experts": touched},
+        "roofline": {"bound": "mfma", "kernel": "pf_gate_up", "achieved": round(gu_tops, 2), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(gu_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "algorithmic_flop_per_launch": gu_flop, "avg_launch_ms": round(gu_ms, 4)},
+        "block": {"tflops": round(block_flop / (ms_step * 1e-3) / 1e12, 2),
+                  "hbm_gbs": round(block_bytes / (ms_step * 1e-3) / 1e9, 1),
+                  "hbm_frac": round(block_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                  "algorithmic_flop": block_flop, "algorithmic_bytes": block_bytes,
+                  "kernel_avg_ms": {k: round(v, 4) for k, v in ktimes.items()}, "timed_forwards": nf},
         "parity": parity,
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),
