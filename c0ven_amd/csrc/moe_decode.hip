@@ -201,15 +201,16 @@ __device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, u
   }
 }
 
-// The pairwise sum over the U lanes of a row (U a power of two, the lanes consecutive): butterflies, which add the
-// halves in the oracle's tree order.
+// A row's sum over its U lanes (consecutive, U a power of two, one unit each), in the oracle's order: acc = 0, then
+// acc + t_u for u ascending. The partial passes one lane up at each step; every lane of the row receives the total.
 __device__ __forceinline__ float row_sum(float t, uint32_t U) {
-  if (U >= 2) t = __fadd_rn(t, __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(t))));
-  if (U >= 4) t = __fadd_rn(t, __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(t))));
-  if (U >= 8) t = __fadd_rn(t, __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(t))));
-  if (U >= 16) t = __fadd_rn(t, __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(t))));
-  if (U >= 32) t = __fadd_rn(t, __shfl_xor(t, 16, 64));
-  return t;
+  const uint32_t lane = lane_id(), u = lane & (U - 1);
+  float x = u == 0 ? __fadd_rn(0.0f, t) : t;
+  for (uint32_t i = 1; i < U; i++) {
+    const float prev = U <= 16 ? __uint_as_float(dpp_u32<kDppShr1>(__float_as_uint(x))) : __shfl_up(x, 1, 64);
+    if (u == i) x = __fadd_rn(prev, t);
+  }
+  return __shfl(x, (int)((lane & ~(U - 1)) + U - 1), 64);
 }
 
 

@@ -4,7 +4,7 @@
 // Bits: every result equals the CPU oracle's (its ORACLE ORDER). The router sums exact bf16 products in fp64 in k
 // order, as the oracle does. The expert GEMMs take each 32-value block's integer dot product from one
 // v_mfma_i32_32x32x32_i8 (exact), then apply the block's integer scale (Q4_K, IQ3_S) or fp32 term (Q8_0) and each
-// unit's fp32 steps exactly as the decoders in units.h do, and sum a row's units as the same pairwise tree.
+// unit's fp32 steps exactly as the decoders in units.h do, and add a row's units in sequence, as the oracle does.
 #include <hip/hip_runtime.h>
 
 #include "act_quant.h"
@@ -318,25 +318,6 @@ struct PfGemm {
   float limit;
 };
 
-// The pairwise tree of a row's units: unit u's terms are a leaf; pairs of equal size combine left + right as soon as
-// both exist (the oracle's order for a power-of-two number of units). The waiting left halves sit in LDS (a level, a
-// term, a lane: consecutive lanes at consecutive words); the root stays in registers.
-template <uint32_t kLU>
-__device__ __forceinline__ void tree_push(float *lvl, float (&t)[16], uint32_t u, uint32_t lane, float (&root)[16]) {
-  uint32_t b = 0;
-  for (; b < kLU && ((u >> b) & 1u); b++) {
-#pragma unroll
-    for (int r = 0; r < 16; r++) t[r] = __fadd_rn(lvl[(b * 16 + r) * 64 + lane], t[r]);
-  }
-  if (b < kLU) {
-#pragma unroll
-    for (int r = 0; r < 16; r++) lvl[(b * 16 + r) * 64 + lane] = t[r];
-  } else {
-#pragma unroll
-    for (int r = 0; r < 16; r++) root[r] = t[r];
-  }
-}
-
 // One tile (at most 64 positions) x 32 rows of gate and of up (kGU: waves 0-1 gate, 2-3 up, SwiGLU at the end) or x
 // 64 rows of down (waves 2 w + ..: rows 32 (w / 2)); waves of even / odd index take positions 0-31 / 32-63.
 template <uint32_t kType, uint32_t kLU, bool kGU>
@@ -347,7 +328,6 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   __shared__ float ub[kGU ? 64 : 1][33];
   __shared__ uint32_t arow_lds[64];
   __shared__ uint64_t tab[32];
-  __shared__ float tree_lds[(kPfWG / 64) * (kLU ? kLU : 1) * 16 * 64];
   uint32_t start, count, e;
   if (g.shared_T) {
     start = MOE_TILE * blockIdx.x;
@@ -374,8 +354,9 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   const uint32_t idx0 = (row % kTileRows) * U, nl = kTileRows * U;
   const uint32_t arow = arow_lds[32 * half + n];  // this lane's A row (position 32 half + l % 32)
   const uint8_t *aptr = arow != 0xffffffffu ? g.act + (uint64_t)arow * U * kActBytes : nullptr;
-  float root[16];
-  float *lvl = tree_lds + (uint64_t)w * (kLU ? kLU : 1) * 16 * 64;
+  float root[16];  // the row's units summed in sequence (ORACLE ORDER)
+#pragma unroll
+  for (int r = 0; r < 16; r++) root[r] = 0.0f;
   for (uint32_t u = 0; u < U; u++) {
     // The unit's per-position scales and sums.
     {
@@ -471,7 +452,8 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
         t[r] = __fmul_rn(__fmul_rn(s.d, ad), (float)isum[r]);
       }
     }
-    tree_push<kLU>(lvl, t, u, l, root);
+#pragma unroll
+    for (int r = 0; r < 16; r++) root[r] = __fadd_rn(root[r], t[r]);
     __syncthreads();  // meta is rewritten by the next unit
   }
   // Outputs: position 32 half + m_r, weight row `row`.

@@ -245,7 +245,8 @@ static uint64_t row_bytes(uint32_t t, uint64_t n) {
 }
 
 /* ---------------------------------------------------------------------------------------------------------------
- * Block dot products. Each returns the block's fp32 term; the row is their pairwise sum (ORACLE ORDER). */
+ * Block dot products. Each returns the block's fp32 term; the row sums them in ORACLE ORDER: a pairwise tree within
+ * each unit of 256 values (Q8_0's eight blocks; a Q4_K or IQ3_S super-block is one term), the units in sequence. */
 
 static float pairwise(const float *a, int64_t n) {
   if (n == 1) return a[0];
@@ -323,7 +324,10 @@ static float dot_row(uint32_t type, int64_t n, const uint8_t *w, const uint8_t *
       for (int64_t i = 0; i < nb; i++) terms[i] = term_iq3_s(w + 110 * i, a + 292 * i);
       break;
   }
-  return pairwise(terms, nb);
+  const int64_t per = type == QT_Q8_0 ? 8 : 1;  /* terms a unit of 256 values has */
+  float acc = 0.0f;
+  for (int64_t i = 0; i < nb; i += per) acc += pairwise(terms + i, nb - i < per ? nb - i : per);
+  return acc;
 }
 
 int orc_vec_dot(uint32_t type, int64_t n, const void *w_row, const void *act, float *out) {

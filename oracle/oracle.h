@@ -32,8 +32,9 @@ extern "C" {
  * SIMD kernels sum them in an architecture-dependent order that no source in the reference restates; the oracle uses
  * one canonical order, stated per type in oracle.c, and the GPU kernels reproduce it:
  *   - one fp32 term per block (Q8_0: 32 values) or super-block (Q4_K, IQ3_S: 256 values);
- *   - the terms of a row summed as a pairwise tree: sum(a[0..n)) = sum(a[0..m)) + sum(a[m..n)), m the largest power
- *     of two below n (n = 1: a[0]). */
+ *   - a unit of 256 values (eight Q8_0 blocks, one super-block) sums its terms as a pairwise tree:
+ *     sum(a[0..n)) = sum(a[0..m)) + sum(a[m..n)), m the largest power of two below n (n = 1: a[0]);
+ *   - a row adds its units in sequence, from 0.0f: acc = acc + unit_u, u ascending. */
 
 typedef struct {
   uint32_t gate_type, down_type; /* QT_* of gate and up (always one type), and of down */
