@@ -211,13 +211,16 @@ __device__ __forceinline__ const T *pf_field(const uint8_t *tile, uint32_t base,
   return (const T *)(tile + (uint64_t)base * nl) + (uint64_t)p * nl + idx;
 }
 
+// Each slice is fetched (raw bytes into registers, one unit ahead of its use) and then decoded.
 struct SliceQ8_0 {
-  uint4 q[8];
+  uint4 q[8], dv;
   float d[8];
-  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h, const uint32_t *) {
+  __device__ __forceinline__ void fetch(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h) {
 #pragma unroll
     for (int b = 0; b < 8; b++) q[b] = *pf_field<uint4>(tile, q8_0t::kQs, 2 * b + h, idx, nl);
-    const uint4 dv = *pf_field<uint4>(tile, q8_0t::kD, 0, idx, nl);
+    dv = *pf_field<uint4>(tile, q8_0t::kD, 0, idx, nl);
+  }
+  __device__ __forceinline__ void decode() {
     const uint32_t w[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
     for (int b = 0; b < 8; b++) d[b] = h2f((uint16_t)(w[b / 2] >> (16 * (b % 2))));
@@ -227,18 +230,22 @@ struct SliceQ8_0 {
 
 struct SliceQ4_K {
   uint4 q[4];  // qs pieces 2 c + h: bytes 32 c + 16 h .. + 15, low nibbles block 2 c, high nibbles block 2 c + 1
+  uint32_t sw[3], dm;
   int sc[8], mn[8];
   float d, dmin;
-  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h, const uint32_t *) {
+  __device__ __forceinline__ void fetch(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h) {
 #pragma unroll
     for (int c = 0; c < 4; c++) q[c] = *pf_field<uint4>(tile, q4_kt::kQs, 2 * c + h, idx, nl);
+#pragma unroll
+    for (int i = 0; i < 3; i++) sw[i] = *pf_field<uint32_t>(tile, q4_kt::kScales, i, idx, nl);
+    dm = *pf_field<uint32_t>(tile, q4_kt::kDm, 0, idx, nl);
+  }
+  __device__ __forceinline__ void decode() {
     uint8_t b[12];
 #pragma unroll
-    for (int i = 0; i < 3; i++) {
-      const uint32_t v = *pf_field<uint32_t>(tile, q4_kt::kScales, i, idx, nl);
+    for (int i = 0; i < 3; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) b[4 * i + j] = (uint8_t)(v >> (8 * j));
-    }
+      for (int j = 0; j < 4; j++) b[4 * i + j] = (uint8_t)(sw[i] >> (8 * j));
 #pragma unroll
     for (int j = 0; j < 8; j++) {  // get_scale_min_k4
       if (j < 4) {
@@ -249,25 +256,26 @@ struct SliceQ4_K {
         mn[j] = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
       }
     }
-    const uint32_t dm = *pf_field<uint32_t>(tile, q4_kt::kDm, 0, idx, nl);
     d = h2f((uint16_t)dm);
     dmin = h2f((uint16_t)(dm >> 16));
   }
-  __device__ __forceinline__ v4i words(int j) const {
+  // Block j's codes times k (k <= 7): every byte stays below 106, so one 32-bit product carries nothing across bytes.
+  __device__ __forceinline__ v4i words_times(int j, uint32_t k) const {
     const uint4 v = q[j / 2];
     const int s = 4 * (j & 1);
     v4i r;
-    r[0] = (int)((v.x >> s) & 0x0f0f0f0fu), r[1] = (int)((v.y >> s) & 0x0f0f0f0fu);
-    r[2] = (int)((v.z >> s) & 0x0f0f0f0fu), r[3] = (int)((v.w >> s) & 0x0f0f0f0fu);
+    r[0] = (int)(((v.x >> s) & 0x0f0f0f0fu) * k), r[1] = (int)(((v.y >> s) & 0x0f0f0f0fu) * k);
+    r[2] = (int)(((v.z >> s) & 0x0f0f0f0fu) * k), r[3] = (int)(((v.w >> s) & 0x0f0f0f0fu) * k);
     return r;
   }
 };
 
 struct SliceIQ3_S {
-  uint32_t qs[8], sg[8], qh[2];  // qs[ib]: the four grid-index bytes of block ib's half h (groups 8 ib + 4 h ..)
+  uint32_t qs[8], sg[8], qh[2], scw;  // qs[ib]: the four grid-index bytes of block ib's half h (groups 8 ib + 4 h ..)
+  uint16_t dh;
   int ls[8];
   float d;
-  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h, const uint32_t *) {
+  __device__ __forceinline__ void fetch(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h) {
 #pragma unroll
     for (int p = 0; p < 4; p++) {  // qs piece p holds the index bytes of blocks 2 p and 2 p + 1 (words 0-1, 2-3)
       const uint32_t *q = (const uint32_t *)pf_field<uint4>(tile, iq3_st::kQs, p, idx, nl) + h;
@@ -280,10 +288,13 @@ struct SliceIQ3_S {
     }
     qh[0] = *pf_field<uint32_t>(tile, iq3_st::kQh, 0, idx, nl);
     qh[1] = *pf_field<uint32_t>(tile, iq3_st::kQh, 1, idx, nl);
-    const uint32_t sc = *pf_field<uint32_t>(tile, iq3_st::kScales, 0, idx, nl);
-    d = h2f(*pf_field<uint16_t>(tile, iq3_st::kD, 0, idx, nl));
+    scw = *pf_field<uint32_t>(tile, iq3_st::kScales, 0, idx, nl);
+    dh = *pf_field<uint16_t>(tile, iq3_st::kD, 0, idx, nl);
+  }
+  __device__ __forceinline__ void decode() {
+    d = h2f(dh);
 #pragma unroll
-    for (int ib = 0; ib < 8; ib++) ls[ib] = 1 + 2 * (int)((sc >> (4 * ib)) & 15u);
+    for (int ib = 0; ib < 8; ib++) ls[ib] = 1 + 2 * (int)((scw >> (4 * ib)) & 15u);
   }
   // Block ib, half h: groups k = 8 ib + 4 h + g (four values each): index byte g of qs[ib], high bit
   // 8 (ib % 4) + 4 h + g of qh word ib / 4, signs nibble 4 h + g of sign word ib.
@@ -303,6 +314,21 @@ struct SliceIQ3_S {
   }
 };
 
+template <uint32_t kType>
+struct SliceOf;
+template <>
+struct SliceOf<QT_Q8_0> {
+  using T = SliceQ8_0;
+};
+template <>
+struct SliceOf<QT_Q4_K> {
+  using T = SliceQ4_K;
+};
+template <>
+struct SliceOf<QT_IQ3_S> {
+  using T = SliceIQ3_S;
+};
+
 struct PfGemm {
   const MoeTile *tiles;    // routed: the dispatch's tiles
   const uint32_t *ntiles;
@@ -318,14 +344,56 @@ struct PfGemm {
   float limit;
 };
 
-// One tile (at most 64 positions) x 32 rows of gate and of up (kGU: waves 0-1 gate, 2-3 up, SwiGLU at the end) or x
-// 64 rows of down (waves 2 w + ..: rows 32 (w / 2)); waves of even / odd index take positions 0-31 / 32-63.
+// Rows a work-group of pf_gemm takes: 64 of gate and of up (waves 0-1 gate, 2-3 up, rows 32 (w % 2) ..), or 128 of
+// down (wave w rows 32 w ..). Every wave takes all of the tile's (at most) 64 positions as two MFMA row blocks, so one
+// decoded weight fragment serves two MFMAs.
+template <bool kGU>
+constexpr uint32_t gemm_rows() { return kGU ? 64 : 128; }
+
+// The tile's activation unit u (64 positions x 320 B) into LDS (positions kActLds apart, so the 32 rows one MFMA
+// operand read touches fall in distinct banks): 1280 16-byte pieces, five a thread, loaded into registers first.
+struct ActStage {
+  uint4 v[5];
+  __device__ __forceinline__ void load(const uint8_t *act, const uint32_t *arow, uint32_t U, uint32_t u) {
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+      const uint32_t piece = threadIdx.x + kPfWG * i, tk = piece / 20, c = piece % 20, ar = arow[tk];
+      v[i] = ar != 0xffffffffu ? *(const uint4 *)(act + ((uint64_t)ar * U + u) * kActBytes + 16 * c)
+                               : make_uint4(0, 0, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void store(uint8_t *buf) const {
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+      const uint32_t piece = threadIdx.x + kPfWG * i, tk = piece / 20, c = piece % 20;
+      *(uint4 *)(buf + tk * kActLds + 16 * c) = v[i];
+    }
+  }
+};
+
+// Q4_K's minimum part as MFMA: imin[m][row] = sum_j bsum_j(m) mn_j(row), with bsum_j = 64 hi_j + lo_j (hi in
+// [-64, 63], lo in [0, 63], both int8). Lanes of half 0 give A = (hi_0..7, lo_0..7) and B = (mn_0..7, 0 x 8) for the hi
+// product or (0 x 8, mn_0..7) for the lo product; lanes of half 1 give zeros (values 16..31).
+__device__ __forceinline__ v4i bsum_split(const uint8_t *unit) {
+  const uint4 a = *(const uint4 *)(unit + kActSums), b = *(const uint4 *)(unit + kActSums + 16);
+  const int bs[8] = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
+  uint32_t hi[2] = {0, 0}, lo[2] = {0, 0};
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    hi[j / 4] |= ((uint32_t)(bs[j] >> 6) & 0xffu) << (8 * (j % 4));
+    lo[j / 4] |= ((uint32_t)(bs[j] & 63)) << (8 * (j % 4));
+  }
+  v4i r;
+  r[0] = (int)hi[0], r[1] = (int)hi[1], r[2] = (int)lo[0], r[3] = (int)lo[1];
+  return r;
+}
+
 template <uint32_t kType, uint32_t kLU, bool kGU>
 __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   constexpr uint32_t U = 1u << kLU;
+  __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
   __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
-  __shared__ uint4 meta[64][4];     // per position: the unit's scales (dwords 0-7) and q8_K sums (8-15)
-  __shared__ float ub[kGU ? 64 : 1][33];
+  __shared__ float ub[kGU ? 64 : 1][65];
   __shared__ uint32_t arow_lds[64];
   __shared__ uint64_t tab[32];
   uint32_t start, count, e;
@@ -338,7 +406,7 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
     const MoeTile tl = g.tiles[blockIdx.x];
     start = tl.start, count = tl.count, e = tl.slot;
   }
-  const uint32_t tid = threadIdx.x, w = wave_id(), l = lane_id(), h = l / 32, n = l % 32, half = w & 1u;
+  const uint32_t tid = threadIdx.x, w = wave_id(), l = lane_id(), h = l / 32, n = l % 32;
   if (tid < 32) tab[tid] = kExp2Tab[tid];
   if (kType == QT_IQ3_S)
     for (uint32_t i = tid; i < 512; i += kPfWG) grid_lds[i] = kIq3sGridPf[i];
@@ -348,135 +416,174 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   }
   __syncthreads();
   const uint32_t mat = kGU ? (w >> 1) : 0u;
-  const uint32_t row = (kGU ? blockIdx.y * 32 : blockIdx.y * 64 + 32 * (w >> 1)) + n;
+  const uint32_t row = blockIdx.y * gemm_rows<kGU>() + (kGU ? 32 * (w & 1) : 32 * w) + n;
   const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
   const uint8_t *tile = M + (uint64_t)(row / kTileRows) * tile_bytes(kType, U);
   const uint32_t idx0 = (row % kTileRows) * U, nl = kTileRows * U;
-  const uint32_t arow = arow_lds[32 * half + n];  // this lane's A row (position 32 half + l % 32)
-  const uint8_t *aptr = arow != 0xffffffffu ? g.act + (uint64_t)arow * U * kActBytes : nullptr;
-  float root[16];  // the row's units summed in sequence (ORACLE ORDER)
+  typename SliceOf<kType>::T s;  // this unit's weights; the next unit's are fetched while it is used
+  s.fetch(tile, idx0, nl, h);
+  ActStage stage;
+  stage.load(g.act, arow_lds, U, 0);
+  stage.store(abuf[0]);
+  __syncthreads();
+  float acc[2][16];  // the row's units summed in sequence (ORACLE ORDER), for positions m_r and 32 + m_r
 #pragma unroll
-  for (int r = 0; r < 16; r++) root[r] = 0.0f;
+  for (int b = 0; b < 2; b++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[b][r] = 0.0f;
+#pragma unroll 1
   for (uint32_t u = 0; u < U; u++) {
-    // The unit's per-position scales and sums.
-    {
-      const uint32_t tk = tid / 4, part = tid % 4, ar = arow_lds[tk];
-      meta[tk][part] = ar != 0xffffffffu
-                           ? *(const uint4 *)(g.act + ((uint64_t)ar * U + u) * kActBytes + kActScales + 16 * part)
-                           : make_uint4(0, 0, 0, 0);
+    typename SliceOf<kType>::T s_next;
+    if (u + 1 < U) {
+      stage.load(g.act, arow_lds, U, u + 1);
+      s_next.fetch(tile, idx0 + u + 1, nl, h);
     }
-    uint4 av[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-      av[j] = aptr ? *(const uint4 *)(aptr + (uint64_t)u * kActBytes + 32 * j + 16 * h) : make_uint4(0, 0, 0, 0);
-    __syncthreads();
-    float t[16];
+    s.decode();
+    const uint8_t *buf = abuf[u & 1];
+    // This lane's A rows (positions n, 32 + n; its half of each block), and the base of the scales of the positions
+    // its results belong to (32 b + 8 (r / 4) + 4 h + r % 4): every LDS read below is a base plus a constant offset.
+    const uint8_t *arow0 = buf + n * kActLds + 16 * h, *arow1 = arow0 + 32 * kActLds;
+    const uint8_t *mbase = buf + 4 * h * kActLds + kActScales;
     if constexpr (kType == QT_Q8_0) {
-      SliceQ8_0 s;
-      s.load(tile, idx0 + u, nl, h, grid_lds);
-      float q[3][16];  // the eight block terms' pairwise tree
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(av[j]), s.words(j), v16i{}, 0, 0, 0);
-        float c[16];
+      for (int b = 0; b < 2; b++) {
+        const uint8_t *ar = b ? arow1 : arow0;
+        float q[3][16];  // the eight block terms' pairwise tree
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
-          const float as = __uint_as_float(((const uint32_t *)&meta[m][0])[j]);
-          c[r] = __fmul_rn(__fmul_rn(s.d[j], as), (float)dv[r]);
-        }
-        // tree over j: levels 0..2
-        if ((j & 1) == 0) {
+        for (int j = 0; j < 8; j++) {
+          const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
+          const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words(j), v16i{}, 0, 0, 0);
+          float c[16];
 #pragma unroll
-          for (int r = 0; r < 16; r++) q[0][r] = c[r];
-        } else {
+          for (int r = 0; r < 16; r++) {
+            const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
+            const float as = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds + 4 * j);
+            c[r] = __fmul_rn(__fmul_rn(s.d[j], as), (float)dv[r]);
+          }
 #pragma unroll
-          for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[0][r], c[r]);
-          if ((j & 2) == 0) {
+          for (int r = 0; r < 16; r++) asm volatile("" : "+v"(c[r]));
+          __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
+          if ((j & 1) == 0) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) q[1][r] = c[r];
+            for (int r = 0; r < 16; r++) q[0][r] = c[r];
           } else {
 #pragma unroll
-            for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[1][r], c[r]);
-            if ((j & 4) == 0) {
+            for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[0][r], c[r]);
+            if ((j & 2) == 0) {
 #pragma unroll
-              for (int r = 0; r < 16; r++) q[2][r] = c[r];
+              for (int r = 0; r < 16; r++) q[1][r] = c[r];
             } else {
 #pragma unroll
-              for (int r = 0; r < 16; r++) t[r] = __fadd_rn(q[2][r], c[r]);
+              for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[1][r], c[r]);
+              if ((j & 4) == 0) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) q[2][r] = c[r];
+              } else {
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[b][r] = __fadd_rn(acc[b][r], __fadd_rn(q[2][r], c[r]));
+              }
             }
           }
         }
       }
     } else if constexpr (kType == QT_Q4_K) {
-      SliceQ4_K s;
-      s.load(tile, idx0 + u, nl, h, grid_lds);
-      int isum[16];
+      // isum = sum_j sc_j (q . a)_j with sc_j = 8 hi_j + lo_j: the scale is folded into the weights (q lo_j and
+      // q hi_j, each below 106 a byte) and both products accumulate over the eight blocks inside the MFMA, exactly.
+      v4i bmh, bml;  // the minimum part's B operands
+      {
+        uint32_t m0 = 0, m1 = 0;
 #pragma unroll
-      for (int r = 0; r < 16; r++) isum[r] = 0;
+        for (int j = 0; j < 8; j++) (j < 4 ? m0 : m1) |= (uint32_t)s.mn[j] << (8 * (j % 4));
+        const bool z = h != 0;
+        bmh[0] = z ? 0 : (int)m0, bmh[1] = z ? 0 : (int)m1, bmh[2] = 0, bmh[3] = 0;
+        bml[0] = 0, bml[1] = 0, bml[2] = z ? 0 : (int)m0, bml[3] = z ? 0 : (int)m1;
+      }
+      v16i dhi[2] = {v16i{}, v16i{}}, dlo[2] = {v16i{}, v16i{}};
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(av[j]), s.words(j), v16i{}, 0, 0, 0);
+        const v4i bl = s.words_times(j, (uint32_t)s.sc[j] & 7u), bh = s.words_times(j, (uint32_t)s.sc[j] >> 3);
 #pragma unroll
-        for (int r = 0; r < 16; r++) isum[r] += s.sc[j] * dv[r];
+        for (int b = 0; b < 2; b++) {
+          const v4i aw = as_v4i(*(const uint4 *)((b ? arow1 : arow0) + 32 * j));
+          dlo[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bl, dlo[b], 0, 0, 0);
+          dhi[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bh, dhi[b], 0, 0, 0);
+        }
       }
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
-        const uint4 s0 = meta[m][2], s1 = meta[m][3];
-        const int bs[8] = {(int)s0.x, (int)s0.y, (int)s0.z, (int)s0.w, (int)s1.x, (int)s1.y, (int)s1.z, (int)s1.w};
-        int imin = 0;
+      for (int b = 0; b < 2; b++) {
+        const uint8_t *ar = b ? arow1 : arow0;
+        v4i am = bsum_split(ar - 16 * h);
+        if (h) am = v4i{0, 0, 0, 0};
+        const v16i dh = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bmh, v16i{}, 0, 0, 0);
+        const v16i dl = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bml, v16i{}, 0, 0, 0);
 #pragma unroll
-        for (int j = 0; j < 8; j++) imin += s.mn[j] * bs[j];
-        const float ad = __uint_as_float(meta[m][0].x);
-        const float dd = __fmul_rn(s.d, ad), dm = __fmul_rn(s.dmin, ad);
-        const float pm = __fmul_rn(dm, (float)imin);
-        t[r] = __builtin_fmaf(dd, (float)isum[r], -pm);
+        for (int r = 0; r < 16; r++) {
+          const int isum = 8 * dhi[b][r] + dlo[b][r], imin = 64 * dh[r] + dl[r];
+          const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
+          const float dd = __fmul_rn(s.d, ad), dm = __fmul_rn(s.dmin, ad);
+          const float pm = __fmul_rn(dm, (float)imin);
+          acc[b][r] = __fadd_rn(acc[b][r], __builtin_fmaf(dd, (float)isum, -pm));
+        }
       }
     } else {
-      SliceIQ3_S s;
-      s.load(tile, idx0 + u, nl, h, grid_lds);
-      int isum[16];
 #pragma unroll
-      for (int r = 0; r < 16; r++) isum[r] = 0;
+      for (int b = 0; b < 2; b++) {
+        const uint8_t *ar = b ? arow1 : arow0;
+        int isum[16];
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(av[j]), s.words_h(j, h, grid_lds), v16i{}, 0, 0, 0);
+        for (int r = 0; r < 16; r++) isum[r] = 0;
 #pragma unroll
-        for (int r = 0; r < 16; r++) isum[r] += s.ls[j] * dv[r];
-      }
+        for (int j = 0; j < 8; j++) {
+          const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
+          const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words_h(j, h, grid_lds), v16i{}, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
-        const float ad = __uint_as_float(meta[m][0].x);
-        t[r] = __fmul_rn(__fmul_rn(s.d, ad), (float)isum[r]);
+          for (int r = 0; r < 16; r++) isum[r] += s.ls[j] * dv[r];
+#pragma unroll
+          for (int r = 0; r < 16; r++) asm volatile("" : "+v"(isum[r]));  // keeps the sums in block order
+          __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
+          const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
+          acc[b][r] = __fadd_rn(acc[b][r], __fmul_rn(__fmul_rn(s.d, ad), (float)isum[r]));
+        }
       }
     }
-#pragma unroll
-    for (int r = 0; r < 16; r++) root[r] = __fadd_rn(root[r], t[r]);
-    __syncthreads();  // meta is rewritten by the next unit
+    if (u + 1 < U) {
+      stage.store(abuf[(u + 1) & 1]);
+      s = s_next;
+    }
+    __syncthreads();
   }
-  // Outputs: position 32 half + m_r, weight row `row`.
+  // Outputs: positions 32 b + m_r, weight row `row`.
   if constexpr (kGU) {
+    const uint32_t col = 32 * (w & 1) + n;
     if (mat == 1) {
 #pragma unroll
-      for (int r = 0; r < 16; r++) ub[32 * half + 8 * (r / 4) + 4 * h + (r % 4)][n] = root[r];
+      for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) ub[32 * b + 8 * (r / 4) + 4 * h + (r % 4)][col] = acc[b][r];
     }
     __syncthreads();
     if (mat == 0) {
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
-        if (m < count)
-          g.out[(uint64_t)(start + m) * g.out_ld + row] = swiglu_one(root[r], ub[m][n], g.limit, tab);
-      }
+      for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
+          if (m < count)
+            g.out[(uint64_t)(start + m) * g.out_ld + row] = swiglu_one(acc[b][r], ub[m][col], g.limit, tab);
+        }
     }
   } else {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const uint32_t m = 32 * half + 8 * (r / 4) + 4 * h + (r % 4);
-      if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row] = root[r];
-    }
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
+        if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row] = acc[b][r];
+      }
   }
 }
 
@@ -578,12 +685,12 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     g.tiles = b.tiles, g.ntiles = b.ntiles, g.perm = b.perm, g.K = K, g.act = b.act_r, g.act_by_pos = 0;
     g.mat = L.experts, g.stride = L.ex_bytes, g.up_off = L.ex_up_off, g.out = b.h, g.out_ld = F;
     g.limit = S.swiglu_limit;
-    launch_gemm<true>(S.gate_type, Ug, dim3(mt, F / 32), g, st);
+    launch_gemm<true>(S.gate_type, Ug, dim3(mt, F / gemm_rows<true>()), g, st);
     if (S.has_shared) {
       PfGemm q = g;
       q.tiles = nullptr, q.ntiles = nullptr, q.shared_T = T, q.perm = nullptr, q.act = b.act_s;
       q.mat = L.shared, q.stride = 0, q.up_off = L.sh_up_off, q.out = b.h_sh;
-      launch_gemm<true>(S.sh_gate_type, Ug, dim3(st_tiles, F / 32), q, st);
+      launch_gemm<true>(S.sh_gate_type, Ug, dim3(st_tiles, F / gemm_rows<true>()), q, st);
     }
   }
   {
@@ -599,12 +706,12 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     PfGemm g{};
     g.tiles = b.tiles, g.ntiles = b.ntiles, g.K = K, g.act = b.hact, g.act_by_pos = 1;
     g.mat = L.experts + L.ex_down_off, g.stride = L.ex_bytes, g.out = b.y_asg, g.out_ld = H;
-    launch_gemm<false>(S.down_type, Ud, dim3(mt, H / 64), g, st);
+    launch_gemm<false>(S.down_type, Ud, dim3(mt, H / gemm_rows<false>()), g, st);
     if (S.has_shared) {
       PfGemm q = g;
       q.tiles = nullptr, q.ntiles = nullptr, q.shared_T = T, q.act = b.hact_sh;
       q.mat = L.shared + L.sh_down_off, q.stride = 0, q.out = b.y_sh;
-      launch_gemm<false>(S.sh_down_type, Ud, dim3(st_tiles, H / 64), q, st);
+      launch_gemm<false>(S.sh_down_type, Ud, dim3(st_tiles, H / gemm_rows<false>()), q, st);
     }
   }
   {
