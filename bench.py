@@ -29,6 +29,10 @@ CONFIGS = {
     "3": dict(name="config3: decode T=1, IQ3_S", types=(21, 21, 21, 21), T=1, zipf=None),
     "3b": dict(name="config3: decode T=4, IQ3_S", types=(21, 21, 21, 21), T=4, zipf=None),
     "4": dict(name="config4: prefill T=2048, Q4_K, Zipf(1.1)", types=(12, 12, 12, 12), T=2048, zipf=1.1),
+    "5": dict(name="config5: 48-layer stack, decode T=1, gate/up IQ3_S, down Q4_K, shared Q8_0, Zipf(1.1) per layer",
+              types=(21, 12, 8, 8), T=1, zipf=1.1, layers=48),
+    "5p": dict(name="config5: 48-layer stack, prefill 4096 tokens in 2 chunks of 2048, gate/up IQ3_S, down Q4_K, "
+                    "shared Q8_0, Zipf(1.1) per layer", types=(21, 12, 8, 8), T=4096, chunk=2048, zipf=1.1, layers=48),
 }
 H, F, E, K = 2048, 512, 512, 10
 HBM_PEAK_GBS = 8000.0
@@ -80,6 +84,8 @@ def main():
     cfg = CONFIGS[args.config]
     gt, dt, sgt, sdt = cfg["types"]
     T = cfg["T"]
+    if "layers" in cfg:
+        return stack(args, cfg, moe, h)
     if T > 16:
         return prefill(args, cfg, moe, h)
     args.steps = 2000 if args.steps is None else args.steps
@@ -178,6 +184,127 @@ def main():
                      "algorithmic_bytes_per_launch": int(block_bytes), "avg_launch_ms": round(k_ms, 5)},
         "block": {"achieved_gbs": round(block_gbs, 1), "frac": round(block_gbs / HBM_PEAK_GBS, 4),
                   "gate_up_bytes": int(gu_bytes), "down_bytes": int(dn_bytes),
+                  "kernel_avg_ms": {k: round(v, 5) for k, v in ktimes.items()}, "timed_forwards": nf},
+        "parity": parity,
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(out), flush=True)
+    blk.close()
+
+
+def stack(args, cfg, moe, h):
+    """Config 5: the model's 48 MoE blocks in sequence (attention and DeltaNet omitted). With those omitted there is no
+    residual stream to keep the activations RMSNorm-like, so every block takes the step's synthetic tokens (N(0, 1),
+    as at the configs' block input) and the blocks run one after another on one stream; chaining the raw block
+    outputs instead would shrink them layer by layer and collapse the routing onto a few experts. The layers have
+    their own routers and Zipf biases; their experts are device copies of layer 0's (other addresses, so every
+    layer's weights are read from HBM: 48 x 763 MB resident). A step is one token (decode) or 4096 tokens in two
+    chunks of 2048 (prefill) through all 48 layers."""
+    gt, dt, sgt, sdt = cfg["types"]
+    NL, T = cfg["layers"], cfg["T"]
+    chunk = cfg.get("chunk", T)
+    decode = T <= 16
+    steps = (200 if decode else 3) if args.steps is None else args.steps
+    warmup = (20 if decode else 1) if args.warmup is None else args.warmup
+    hip = Hip()
+    t_setup = time.time()
+    L0 = h.Layer(H, F, E, K, gt, dt, sgt, sdt, seed=2026, layer=0, zipf=cfg["zipf"])
+    blk = moe.MoeBlock(H, F, E, K, gt, dt, True, sgt, sdt, n_layer=NL, max_tokens=chunk)
+    L0.upload(blk, 0)
+    layers = [L0]
+    for l in range(1, NL):
+        Ll = h.Layer(H, F, E, K, gt, dt, sgt, sdt, seed=2026, layer=l, zipf=cfg["zipf"], experts=[], has_shared=False)
+        blk.load_router(l, Ll.router, Ll.bias)
+        blk.copy_experts(0, l)
+        Ll.experts, Ll.shared, Ll.has_shared = L0.experts, L0.shared, True  # the oracle's view of the copies
+        layers.append(Ll)
+    x = h.tokens(2026, T, H)
+    bufs = [hip.malloc(chunk * H * 4), hip.malloc(chunk * H * 4)]
+    idsd = hip.malloc(chunk * K * 4)
+
+    xdev = hip.malloc(T * H * 4)
+    hip.h2d(xdev, x)
+
+    def run(c0, n, collect=None):
+        xc = C.c_void_p(xdev.value + c0 * H * 4)
+        for l in range(NL):
+            blk.forward_async(l, xc, n, bufs[l % 2], idsd if collect is not None else None)
+            if collect is not None:
+                hip.sync()
+                ids = np.empty((n, K), np.int32)
+                hip.d2h(ids, idsd)
+                collect.append(len(set(ids.ravel().tolist())))
+
+    distinct = []
+    run(0, min(chunk, T), distinct)
+    hip.sync()
+    setup_s = time.time() - t_setup
+    for _ in range(warmup):
+        for c0 in range(0, T, chunk):
+            run(c0, min(chunk, T - c0))
+    hip.sync()
+    blk.set_timing(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for c0 in range(0, T, chunk):
+            run(c0, min(chunk, T - c0))
+    hip.sync()
+    t1 = time.perf_counter()
+    ktimes, nf = blk.kernel_times()
+    blk.set_timing(False)
+    ms_step = (t1 - t0) * 1e3 / steps
+    tok_s = T * steps / (t1 - t0)
+    ex_bytes = 2 * moe.row_bytes(gt, H) * F + moe.row_bytes(dt, F) * H
+    sh_bytes = 2 * moe.row_bytes(sgt, H) * F + moe.row_bytes(sdt, F) * H
+    router_bytes = (E + 1) * H * 2
+    layer_bytes = np.mean(distinct) * ex_bytes + sh_bytes + router_bytes  # per layer (first chunk's routing)
+    # Parity: the oracle through the same 48 layers, on a sample of the tokens.
+    sample = np.r_[0:min(T, 4)] if decode else np.r_[0:4, chunk:chunk + 4]
+    y = np.empty((chunk, H), np.float32)
+    outs = []
+    for c0 in range(0, T, chunk):
+        n = min(chunk, T - c0)
+        run(c0, n)
+        hip.sync()
+        yy = np.empty((n, H), np.float32)
+        hip.d2h(yy, bufs[(NL - 1) % 2])
+        outs.append(yy)
+    yg = np.concatenate(outs)[sample]
+    tc0 = time.perf_counter()
+    for l in range(NL):  # the CPU does every layer too; the last layer's output is compared
+        xo, io, _ = layers[l].oracle_forward(x[sample], nthreads=min(16, os.cpu_count() or 1))
+    cpu_s = time.perf_counter() - tc0
+    parity = dict(sample_tokens=len(sample), y_bit_exact=bool(np.array_equal(yg, xo)), max_abs=h.max_abs(yg, xo),
+                  rel_l2=h.rel_l2(yg, xo))
+    cores = min(16, os.cpu_count() or 1)
+    cpu = None if args.no_cpu else {
+        "value": round(len(sample) / cpu_s, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+        "sample": "%d tokens through the 48 layers by oracle/oracle.c with %d OpenMP threads, %.1f s"
+                  % (len(sample), cores, cpu_s)}
+    if decode:
+        k_ms = ktimes.get("moe_decode", float("nan"))
+        roof = {"bound": "hbm", "kernel": "moe_decode", "achieved": round(layer_bytes / (k_ms * 1e-3) / 1e9, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(layer_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "traffic": None, "algorithmic_bytes_per_launch": int(layer_bytes), "avg_launch_ms": round(k_ms, 5)}
+    else:
+        gu_ms = ktimes.get("pf_gate_up", float("nan"))
+        gu_flop = 2.0 * (chunk * K + chunk) * 2 * F * H
+        roof = {"bound": "mfma", "kernel": "pf_gate_up", "achieved": round(gu_flop / (gu_ms * 1e-3) / 1e12, 2),
+                "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                "frac": round(gu_flop / (gu_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4), "traffic": None,
+                "algorithmic_flop_per_launch": gu_flop, "avg_launch_ms": round(gu_ms, 4)}
+    out = {
+        "metric": "MoE block tokens/s + achieved HBM GB/s (decode), TFLOP/s (prefill) on 1 GPU",
+        "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": cfg["name"], "layers": NL, "n_embd": H, "n_ff": F, "n_expert": E, "n_used": K,
+                   "tokens": T, "chunk": chunk, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]],
+                   "mean_distinct_experts_per_layer": round(float(np.mean(distinct)), 2)},
+        "roofline": roof,
+        "block": {"stack_hbm_gbs": round(NL * layer_bytes * (T // chunk if not decode else 1) / (ms_step * 1e-3) / 1e9, 1)
+                  if decode else None,
                   "kernel_avg_ms": {k: round(v, 5) for k, v in ktimes.items()}, "timed_forwards": nf},
         "parity": parity,
         "cpu_baseline": cpu,
