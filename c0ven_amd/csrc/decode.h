@@ -16,15 +16,19 @@ constexpr uint32_t kMaxUnits = 32;         // 256-value units per row: H and F u
 constexpr uint32_t max_groups(uint32_t T, uint32_t K) { return T * K + (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX; }
 
 // The work-group (four waves) and the work items of moe_decode, in the order every work-group walks them:
-//   lead items     kRouteRows router rows each (two waves a row), when routing; item t < T also quantises x[t];
+//   lead items     two router rows each (half a row a wave), when routing; item t < T also quantises x[t];
 //   top-k items    one a token (when routing);
 //   gate/up items  gate_up_rows(U) rows of gate and of up of one group, all units (lane = m * 32 + r * U + u);
 //   down items     down_rows(U_down) rows of down of one group, all units (lane = r * U_down + u).
-constexpr uint32_t kWG = 256, kRouteRows = 2;
+constexpr uint32_t kWG = 256;
+// Lead items: two router rows each (two waves a row); item t < T also quantises x[t]. The shared gate's row (row E)
+// is taken by the top-k items instead, while they wait for the lead items (they run on work-groups the lead items
+// leave free).
+constexpr uint32_t kRouteRows = 2;
 constexpr uint32_t lead_items(uint32_t T, uint32_t E, uint32_t route) {
-  return route ? ((E + kRouteRows) / kRouteRows > T ? (E + kRouteRows) / kRouteRows : T) : T;
+  return route ? ((E + kRouteRows - 1) / kRouteRows > T ? (E + kRouteRows - 1) / kRouteRows : T) : T;
 }
-constexpr uint32_t kMaxLeadItems = (kMaxExperts + kRouteRows) / kRouteRows;
+constexpr uint32_t kMaxLeadItems = kMaxExperts / kRouteRows;
 // LDS the grouping step takes from the dynamic allocation: T K ids, a token mask and two group numbers per expert.
 constexpr uint32_t kGroupingLds = kMaxDecodeTokens * kMaxUsed * 4 + kMaxExperts * 4 + kMaxExperts * 2 * 4;
 constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kWG / 64) * (32 / Ug); }

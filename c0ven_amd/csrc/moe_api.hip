@@ -137,9 +137,6 @@ void validate(const moe_config &c) {
   require(!c.has_shared || (quant_gpu_supported(c.sh_gate_type) && quant_gpu_supported(c.sh_down_type)),
           "shared expert types must be Q8_0, Q4_K or IQ3_S");
   require(c.max_tokens <= kMaxPrefillTokens, "max_tokens must be at most 16384");
-  require((uint64_t)std::min<uint32_t>(c.max_tokens ? c.max_tokens : kMaxDecodeTokens, kMaxDecodeTokens) * c.n_embd *
-                  2 <= 64 * 1024,
-          "min(max_tokens, 16) x n_embd bf16 must fit the decode router's 64 KiB of LDS");
   require(c.swiglu_limit >= 0.0f, "swiglu_limit must be >= 0");
 }
 
@@ -338,8 +335,8 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     check(hipMemset(c->flags, 0, (kFlagH + G) * sizeof(uint64_t)), "hipMemset");
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
-    c->lds = std::max<size_t>({(size_t)T * H * 2, (size_t)MOE_GROUP_MAX * Ug * kActLds,
-                               (size_t)MOE_GROUP_MAX * Ud * kActLds, kGroupingLds});
+    c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * Ug * kActLds, (size_t)MOE_GROUP_MAX * Ud * kActLds,
+                               kGroupingLds});
     int per_cu = 0, ncu = 0;
     check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, moe_decode, kWG, c->lds), "occupancy");
     check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, g.device), "CU count");

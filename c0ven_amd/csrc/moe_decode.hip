@@ -100,12 +100,12 @@ __device__ __forceinline__ void wait_flags(const DecodeParams &p, uint32_t base,
   __syncthreads();
 }
 
-// Top-k, weights and the shared gate for token t (route.h:39-99 and layer.cl:765-804 restated). Two waves at once:
-// wave 1 takes the softmax's max and 1 / sum (the sum in double) and the shared gate; wave 0 selects: lane l holds
+// Top-k and weights for token t (route.h:39-99 and layer.cl:765-804 restated). Two waves at once: wave 1 takes the
+// softmax's max and 1 / sum (the sum in double); wave 0 selects: lane l holds
 // experts l + 64 i, sorted by (logit, lower id first), and each of the k rounds takes the wave's largest head (a DPP
 // max of the logit keys, a ballot for equal keys, the lower id among them) and pops it. Then wave 0 turns the k
 // winners into weights. The winners' ids and keys stay in sel (sel[j], sel[kMaxUsed + j]) for the grouping.
-__device__ void route_token(const DecodeParams &p, uint32_t t, const uint64_t *tab, uint32_t *sel, float *norm) {
+__device__ __forceinline__ void route_token(const DecodeParams &p, uint32_t t, const uint64_t *tab, uint32_t *sel, float *norm) {
   const uint32_t lane = lane_id(), E = p.E, K = p.K;
   const float *lg = p.logits + (uint64_t)t * (E + 1);
   uint32_t my_id = 0, my_key = 0;
@@ -115,10 +115,7 @@ __device__ void route_token(const DecodeParams &p, uint32_t t, const uint64_t *t
     if (wave_id() == 1) {
       float mx, inv;
       route_norm(key, E, lane, tab, &mx, &inv);
-      if (lane == 0) {
-        norm[0] = mx, norm[1] = inv;
-        st_co(p.gs + t, sigmoid_libm(ld_co(lg + E), tab));
-      }
+      if (lane == 0) norm[0] = mx, norm[1] = inv;
     } else {
       route_select(key, id, K, lane, &my_id, &my_key);
       if (lane < K) sel[lane] = my_id, sel[kMaxUsed + lane] = my_key;
@@ -218,7 +215,7 @@ __device__ __forceinline__ float row_sum(float t, uint32_t U) {
 // Router items
 
 // x[t] to the activation types of the routed and the shared gate: a half-wave per unit.
-__device__ void quantise_x(const DecodeParams &p, uint32_t t) {
+__device__ __forceinline__ void quantise_x(const DecodeParams &p, uint32_t t) {
   const uint32_t H = p.H, l32 = threadIdx.x & 31u;
   for (uint32_t u = threadIdx.x / 32; u < H / kUnit; u += kWG / 32) {
     const float4 *src = (const float4 *)(p.x + (uint64_t)t * H + u * kUnit + 8 * l32);
@@ -229,84 +226,79 @@ __device__ void quantise_x(const DecodeParams &p, uint32_t t) {
   }
 }
 
-// x (n8 runs of 8 fp32) to bf16 in LDS, eight runs a thread in flight at once (the loads are L2 hits; issued one
-// run at a time they would serialise).
-__device__ __forceinline__ void stage_x_bf16(const float *x, uint32_t n8, uint16_t *xb) {
-  constexpr uint32_t kBatch = 4;
-  for (uint32_t i0 = 0; i0 < n8; i0 += kBatch * kWG) {
-    float4 a[kBatch], b[kBatch];
-#pragma unroll
-    for (uint32_t j = 0; j < kBatch; j++) {
-      const uint32_t i = i0 + j * kWG + threadIdx.x;
-      if (i < n8) a[j] = ((const float4 *)x)[2 * i], b[j] = ((const float4 *)x)[2 * i + 1];
-    }
-#pragma unroll
-    for (uint32_t j = 0; j < kBatch; j++) {
-      const uint32_t i = i0 + j * kWG + threadIdx.x;
-      if (i >= n8) break;
-      const float v[8] = {a[j].x, a[j].y, a[j].z, a[j].w, b[j].x, b[j].y, b[j].z, b[j].w};
-      uint32_t o[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++)
-        o[k] = (__float_as_uint(round_bf16(v[2 * k])) >> 16) |
-               (__float_as_uint(round_bf16(v[2 * k + 1])) & 0xffff0000u);
-      ((uint4 *)xb)[i] = make_uint4(o[0], o[1], o[2], o[3]);
-    }
-  }
-}
-
-// Router rows 2 i and 2 i + 1 of lead item i, two waves a row (waves 2 r and 2 r + 1 take alternate 512-value chunks
-// of row r): logit = sum of bf16(W) bf16(x), each product exact, summed in fp64 (a lane's share, the wave's in a fixed
-// order, then the two waves'), rounded once, plus the bias. The row's weights are loaded before x is staged (as bf16,
-// in xb); part holds the waves' sums.
-__device__ void router_rows(const DecodeParams &p, uint32_t item, uint16_t *xb, double *part) {
-  const uint32_t lane = lane_id(), wv = wave_id(), H = p.H, T = p.T, E = p.E, nC = H / 512;
-  const uint32_t row = item * kRouteRows + wv / 2, half = wv & 1u;
-  const bool on = row <= E;
+// Router row dot products with tokens t_begin .. t_end - 1, in part[wave][t]: wave w takes row `row`'s 512-value
+// chunks c0, c0 + step, ..., a lane eight values of each, every product bf16(W) bf16(x) exact and summed in fp64 (the lane's share,
+// then the wave's in a fixed order). x is read straight from global memory (it is L2-resident: every lead item reads
+// it), four tokens' worth in flight at once.
+__device__ __forceinline__ void row_dots(const DecodeParams &p, uint32_t row, uint32_t c0, uint32_t step,
+                                         uint32_t t_begin, uint32_t t_end, double *part) {
+  const uint32_t lane = lane_id(), wv = wave_id(), H = p.H, nC = H / 512;
   const uint16_t *wr = p.router + (uint64_t)row * H + lane * 8;
-  // A wave's first two chunks (all of them up to H = 2048) stay in registers across the tokens.
-  uint4 w0[2];
+  const float *xl = p.x + lane * 8;
+  const uint32_t c1 = c0 + step;  // the wave's first two chunks stay in registers, their x loads in flight together
+  const uint4 w0 = c0 < nC ? *(const uint4 *)(wr + 512 * c0) : make_uint4(0, 0, 0, 0);
+  const uint4 w1 = c1 < nC ? *(const uint4 *)(wr + 512 * c1) : make_uint4(0, 0, 0, 0);
+  auto fma8 = [](const uint4 &wq, const float4 &xa, const float4 &xb, double acc) {
+    const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+    const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-  for (uint32_t i = 0; i < 2; i++) {
-    const uint32_t c = half + 2 * i;
-    w0[i] = on && c < nC ? *(const uint4 *)(wr + 512 * c) : make_uint4(0, 0, 0, 0);
-  }
-  stage_x_bf16(p.x, T * H / 8, xb);
-  __syncthreads();
-  // Four tokens at a time, so that their fp64 chains and reductions overlap.
-  for (uint32_t t0 = 0; t0 < T; t0 += 4) {
+    for (int k = 0; k < 8; k++) {
+      const double wd = (double)__uint_as_float((k & 1) ? ww[k / 2] & 0xffff0000u : ww[k / 2] << 16);
+      acc = __builtin_fma(wd, (double)round_bf16(xs[k]), acc);
+    }
+    return acc;
+  };
+  for (uint32_t t0 = t_begin; t0 < t_end; t0 += 4) {
+    float4 xa[4], xb[4], ya[4], yb[4];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 4; tt++) {
+      const float *xt = xl + (uint64_t)min(t0 + tt, t_end - 1) * H;
+      const float4 *q = (const float4 *)(xt + 512 * min(c0, nC - 1));
+      const float4 *q1 = (const float4 *)(xt + 512 * min(c1, nC - 1));
+      xa[tt] = q[0], xb[tt] = q[1], ya[tt] = q1[0], yb[tt] = q1[1];
+    }
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (uint32_t c = half; c < nC; c += 2) {
-      const uint4 wq = c < 4 ? w0[c / 2] : *(const uint4 *)(wr + 512 * c);
-      const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
-      double wd[8];
+    if (c0 < nC) {
 #pragma unroll
-      for (int k = 0; k < 8; k++) wd[k] = (double)__uint_as_float((k & 1) ? ww[k / 2] & 0xffff0000u : ww[k / 2] << 16);
+      for (uint32_t tt = 0; tt < 4; tt++) acc[tt] = fma8(w0, xa[tt], xb[tt], acc[tt]);
+    }
+    if (c1 < nC) {
+#pragma unroll
+      for (uint32_t tt = 0; tt < 4; tt++) acc[tt] = fma8(w1, ya[tt], yb[tt], acc[tt]);
+    }
+    for (uint32_t c = c1 + step; c < nC; c += step) {  // long rows
+      const uint4 wq = *(const uint4 *)(wr + 512 * c);
 #pragma unroll
       for (uint32_t tt = 0; tt < 4; tt++) {
-        if (t0 + tt >= T) break;
-        const uint4 xv = *(const uint4 *)(xb + (uint64_t)(t0 + tt) * H + lane * 8 + 512 * c);
-        const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-          const float xf = __uint_as_float((k & 1) ? xx[k / 2] & 0xffff0000u : xx[k / 2] << 16);
-          acc[tt] = __builtin_fma(wd[k], (double)xf, acc[tt]);
-        }
+        const float4 *q = (const float4 *)(xl + (uint64_t)min(t0 + tt, t_end - 1) * H + 512 * c);
+        acc[tt] = fma8(wq, q[0], q[1], acc[tt]);
       }
     }
 #pragma unroll
     for (uint32_t tt = 0; tt < 4; tt++) {
-      if (t0 + tt >= T) break;
       const double sum = wave_sum_f64(acc[tt]);
-      if (lane == 0) part[wv * kMaxDecodeTokens + t0 + tt] = sum;
+      if (lane == 0 && t0 + tt < t_end) part[wv * kMaxDecodeTokens + t0 + tt] = sum;
     }
   }
   __syncthreads();
-  const uint32_t j = threadIdx.x, r = j / T, tt = j % T, rw = item * kRouteRows + r;
-  if (j < kRouteRows * T && rw <= E) {
-    float l = (float)__dadd_rn(part[2 * r * kMaxDecodeTokens + tt], part[(2 * r + 1) * kMaxDecodeTokens + tt]);
-    if (rw < E && p.bias) l = __fadd_rn(l, p.bias[rw]);
-    st_co(p.logits + (uint64_t)tt * (E + 1) + rw, l);
+}
+
+// The four waves' sums of token t, in a fixed order (the shared gate's row).
+__device__ __forceinline__ float row_total4(const double *part, uint32_t t) {
+  return (float)__dadd_rn(__dadd_rn(part[t], part[kMaxDecodeTokens + t]),
+                          __dadd_rn(part[2 * kMaxDecodeTokens + t], part[3 * kMaxDecodeTokens + t]));
+}
+
+// Lead item i: router rows 2 i and 2 i + 1 (waves 2 r and 2 r + 1 take the even and odd chunks of row 2 i + r) for all
+// T tokens, plus the bias.
+__device__ __forceinline__ void router_rows(const DecodeParams &p, uint32_t item, double *part) {
+  const uint32_t r = wave_id() / 2, row = min(item * kRouteRows + r, p.E - 1);
+  row_dots(p, row, wave_id() & 1u, 2, 0, p.T, part);
+  const uint32_t j = threadIdx.x, rr = j / p.T, t = j % p.T, rw = item * kRouteRows + rr;
+  if (j < kRouteRows * p.T && rw < p.E) {
+    float l = (float)__dadd_rn(part[2 * rr * kMaxDecodeTokens + t], part[(2 * rr + 1) * kMaxDecodeTokens + t]);
+    if (p.bias) l = __fadd_rn(l, p.bias[rw]);
+    st_co(p.logits + (uint64_t)t * (p.E + 1) + rw, l);
   }
 }
 
@@ -315,7 +307,7 @@ __device__ void router_rows(const DecodeParams &p, uint32_t item, uint16_t *xb, 
 // most one assignment a token, so a mask of the tokens that chose it gives each assignment its rank among the
 // expert's (and whether it heads a group); the heads' ballots give the group numbers. Token own's ids come from sel,
 // the others' from the coherent ids.
-__device__ void make_groups(const DecodeParams &p, uint32_t own, const uint32_t *sel, uint8_t *lds, uint64_t *hb) {
+__device__ __forceinline__ void make_groups(const DecodeParams &p, uint32_t own, const uint32_t *sel, uint8_t *lds, uint64_t *hb) {
   const uint32_t T = p.T, K = p.K, E = p.E, n = T * K, a = threadIdx.x, lane = lane_id();
   uint32_t *ids = (uint32_t *)lds, *mask = ids + kMaxDecodeTokens * kMaxUsed, *gnum = mask + kMaxExperts;
   for (uint32_t i = a; i < E; i += kWG) mask[i] = 0u;
@@ -393,7 +385,7 @@ __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *un
 }
 
 // Gate and up of rows blk * gate_up_rows .. of group g: lane = m * 32 + r * U + u; h = silu(g) * u per row.
-__device__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
+__device__ __forceinline__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
                              GroupLds *sg, uint32_t *s_flag, const uint64_t *tab, uint64_t *mark) {
   read_group(p, g, sg);
   const uint32_t U = p.H / kUnit, rows = gate_up_rows(U), row0 = blk * rows, n = sg->n;
@@ -438,7 +430,7 @@ __device__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, ui
 }
 
 // Down rows blk * down_rows .. of group g (lane = r * U + u), then the combine of every token this item completes.
-__device__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
+__device__ __forceinline__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
                           GroupLds *sg, uint32_t *s_last, uint64_t *mark) {
   read_group(p, g, sg);
   const uint32_t U = p.F / kUnit, rows = down_rows(U), row0 = blk * rows, n = sg->n, nblk = p.H / rows;
@@ -504,8 +496,8 @@ __device__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8
 
 }  // namespace
 
-// Grid: the work-groups of 256 the device holds at once; dynamic LDS: the largest of the staged x (T H bf16), a
-// group's activation units (MOE_GROUP_MAX x units x kActLds) and the grouping's tables (kGroupingLds).
+// Grid: the work-groups of 256 the device holds at once; dynamic LDS: the larger of a group's activation units
+// (MOE_GROUP_MAX x units x kActLds) and the grouping's tables (kGroupingLds).
 __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) moe_decode(DecodeParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ uint32_t grid_lds[512];
@@ -537,7 +529,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) m
     if (it < nL) {
       if (it < T) quantise_x(p, it);
       if (p.route) {
-        if (it * kRouteRows <= E) router_rows(p, it, (uint16_t *)lds, s_part);
+        if (it * kRouteRows < E) router_rows(p, it, s_part);
         if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
         set_flag(p, kFlagLead + it);
       } else if (arrive_last(p.cnt_route, nL, &s_flag)) {
@@ -545,6 +537,9 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) m
       }
     } else if (it < B1) {
       const uint32_t t = it - nL;
+      // The shared gate's logit (router row E) for this token while the lead items finish: gs = sigmoid of it.
+      row_dots(p, E, wave_id(), 4, t, t + 1, s_part);
+      if (threadIdx.x == 0) st_co(p.gs + t, sigmoid_libm(row_total4(s_part, t), exp_tab));
       wait_flags(p, kFlagLead, nL);
       if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
       route_token(p, t, exp_tab, s_sel, s_norm);
