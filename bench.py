@@ -64,6 +64,16 @@ class Hip:
         assert self.rt.hipDeviceSynchronize() == 0
 
 
+def measured_traffic(config):
+    """HBM bytes per moe_decode launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes (copy-calibrated) and
+    recorded in profiles/traffic_moe_decode.json with the commands that made them; None if not measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic_moe_decode.json")) as f:
+            return json.load(f)["moe_decode"][config]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -180,7 +190,7 @@ def main():
                    "tokens": T, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]], "resident_layers": n_layer,
                    "mean_distinct_experts": round(float(nd.mean()), 2)},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config),
                      "algorithmic_bytes_per_launch": int(block_bytes), "avg_launch_ms": round(k_ms, 5)},
         "block": {"achieved_gbs": round(block_gbs, 1), "frac": round(block_gbs / HBM_PEAK_GBS, 4),
                   "gate_up_bytes": int(gu_bytes), "down_bytes": int(dn_bytes),
