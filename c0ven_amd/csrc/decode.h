@@ -29,8 +29,10 @@ constexpr uint32_t lead_items(uint32_t T, uint32_t E, uint32_t route) {
   return route ? ((E + kRouteRows - 1) / kRouteRows > T ? (E + kRouteRows - 1) / kRouteRows : T) : T;
 }
 constexpr uint32_t kMaxLeadItems = kMaxExperts / kRouteRows;
-// LDS the grouping step takes from the dynamic allocation: T K ids, a token mask and two group numbers per expert.
-constexpr uint32_t kGroupingLds = kMaxDecodeTokens * kMaxUsed * 4 + kMaxExperts * 4 + kMaxExperts * 2 * 4;
+// LDS the grouping step takes from the dynamic allocation: T K ids, a token mask and two group numbers per expert,
+// and a sort key per group.
+constexpr uint32_t kGroupingLds =
+    kMaxDecodeTokens * kMaxUsed * 4 + kMaxExperts * 4 + kMaxExperts * 2 * 4 + (kMaxDecodeTokens * kMaxUsed + 2) * 4;
 constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kWG / 64) * (32 / Ug); }
 constexpr uint32_t down_rows(uint32_t Ud) { return (kWG / 64) * (64 / Ud); }
 

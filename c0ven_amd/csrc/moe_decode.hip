@@ -302,8 +302,8 @@ __device__ __forceinline__ void router_rows(const DecodeParams &p, uint32_t item
   }
 }
 
-// MoeGroup records from the routed ids: an expert's assignments in order, MOE_GROUP_MAX a group, groups numbered by
-// their first assignment (as group_slots, layer.cl:894-942), then the shared expert's groups. An expert takes at
+// MoeGroup records from the routed ids: an expert's assignments in order, MOE_GROUP_MAX a group (as group_slots,
+// layer.cl:894-942), and the shared expert's groups; numbered by decreasing size, then by first assignment. An expert takes at
 // most one assignment a token, so a mask of the tokens that chose it gives each assignment its rank among the
 // expert's (and whether it heads a group); the heads' ballots give the group numbers. Token own's ids come from sel,
 // the others' from the coherent ids.
@@ -336,23 +336,40 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint32_t own,
     before += w < wave_id() ? c : 0u;
     nr += c;
   }
+  // Groups in order of first assignment (routed, then the shared expert's) get the index o; they are numbered by
+  // decreasing size, o breaking ties, so that the heaviest groups' items come first (work-groups take items in index
+  // order).
+  const uint32_t ns = p.has_shared ? (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX : 0, G = nr + ns;
+  uint32_t *gkey = gnum + 2 * kMaxExperts;
+  uint32_t o = 0, gn = 0;
   if (head) {
-    const uint32_t g = before + __builtin_amdgcn_mbcnt_hi((uint32_t)(heads >> 32),
-                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)heads, 0u));
+    o = before + __builtin_amdgcn_mbcnt_hi((uint32_t)(heads >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)heads, 0u));
+    gn = min((uint32_t)MOE_GROUP_MAX, total - rank);
+    gkey[o] = (MOE_GROUP_MAX - gn) * 1024u + o;
+  }
+  const uint32_t sn = a < ns ? min((uint32_t)MOE_GROUP_MAX, T - a * MOE_GROUP_MAX) : 0u;
+  if (a < ns) gkey[nr + a] = (MOE_GROUP_MAX - sn) * 1024u + nr + a;
+  __syncthreads();
+  auto order = [&](uint32_t key) {
+    uint32_t r = 0;
+    for (uint32_t i = 0; i < G; i++) r += gkey[i] < key;
+    return r;
+  };
+  if (head) {
+    const uint32_t g = order((MOE_GROUP_MAX - gn) * 1024u + o);
     gnum[2 * e + rank / MOE_GROUP_MAX] = g;
     st_co(&p.groups[g].slot, (int32_t)e);
-    st_co(&p.groups[g].n, min((uint32_t)MOE_GROUP_MAX, total - rank));
+    st_co(&p.groups[g].n, gn);
   }
-  __syncthreads();
-  if (a < n) st_co(p.groups[gnum[2 * e + rank / MOE_GROUP_MAX]].asg + rank % MOE_GROUP_MAX, a);
-  const uint32_t ns = p.has_shared ? (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX : 0;
   if (a < ns) {
-    MoeGroup *g = p.groups + nr + a;
+    MoeGroup *g = p.groups + order((MOE_GROUP_MAX - sn) * 1024u + nr + a);
     st_co(&g->slot, (int32_t)E);
-    st_co(&g->n, min((uint32_t)MOE_GROUP_MAX, T - a * MOE_GROUP_MAX));
+    st_co(&g->n, sn);
     for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
       if (a * MOE_GROUP_MAX + j < T) st_co(g->asg + j, n + a * MOE_GROUP_MAX + j);
   }
+  __syncthreads();
+  if (a < n) st_co(p.groups[gnum[2 * e + rank / MOE_GROUP_MAX]].asg + rank % MOE_GROUP_MAX, a);
   if (a == 0) st_co(p.ngroups, nr + ns);
 }
 
