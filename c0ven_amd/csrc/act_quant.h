@@ -29,7 +29,7 @@ __device__ __forceinline__ uint4 ld_co4(const void *p) {
 
 // One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
 // with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0).
-__device__ inline void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
+__device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
   uint32_t code[2] = {0u, 0u};
   if (act_type == QT_Q8_K) {
     // The value of largest magnitude, the first of equals: (|v|, index) reduced over the 32 lanes.

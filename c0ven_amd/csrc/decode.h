@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include "../../include/c0ven_moe_tile.h"
+#include "../../include/c0ven_quant.h"
 
 namespace c0ven {
 
@@ -81,6 +82,23 @@ struct DecodeParams {
   uint32_t trace_cap;
 };
 
+// The weight types a launch may meet, as a set (bits below): moe_decode is compiled once per set, so a context whose
+// matrices share one type carries no other type's code (and no register pressure from it).
+constexpr uint32_t kTypeQ8_0 = 1, kTypeQ4_K = 2, kTypeIQ3_S = 4;
+constexpr uint32_t type_bit(uint32_t qt) { return qt == QT_Q8_0 ? kTypeQ8_0 : qt == QT_Q4_K ? kTypeQ4_K : kTypeIQ3_S; }
+
+// The activation type (q8_0 for Q8_0 weights, q8_K for the others), fixed at compile time where the set allows.
+template <uint32_t kTypes>
+__device__ __forceinline__ uint32_t act_type(uint32_t runtime) {
+  if constexpr (kTypes == kTypeQ8_0) return QT_Q8_0;
+  if constexpr ((kTypes & kTypeQ8_0) == 0) return QT_Q8_K;
+  return runtime;
+}
+
+template <uint32_t kTypes>
 __global__ void moe_decode(DecodeParams p);
+
+// The instantiation for a type set (1 .. 7), as a kernel handle for hipLaunchKernel.
+const void *decode_kernel(uint32_t types);
 
 }  // namespace c0ven

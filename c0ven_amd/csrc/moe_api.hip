@@ -76,6 +76,7 @@ struct moe_ctx {
   uint64_t *flags = nullptr;
   uint64_t epoch = 0;          // the last launch's number
   uint32_t grid = 0;           // co-resident work-groups of moe_decode
+  const void *kernel = nullptr;  // moe_decode for the context's set of weight types
   size_t lds = 0;              // its dynamic LDS
   bool timing = false;
   uint64_t *trace = nullptr;   // per-item stamps of the last forward, when tracing
@@ -190,7 +191,8 @@ void launch(moe_ctx *c, const DecodeParams &p, hipStream_t s) {
   if (c->trace) q.trace = c->trace, q.trace_cap = c->trace_cap;
   c->last_T = p.T, c->last_route = p.route;
   if (c->timing) timing_hook(c, "moe_decode", 0, s);
-  hipLaunchKernelGGL(moe_decode, dim3(c->grid), dim3(kWG), c->lds, s, q);
+  void *args[] = {&q};
+  check(hipLaunchKernel(c->kernel, dim3(c->grid), dim3(kWG), args, c->lds, s), "moe_decode launch");
   check(hipGetLastError(), "moe_decode launch");
   if (c->timing) timing_hook(c, "moe_decode", 1, s);
 }
@@ -338,7 +340,10 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * Ug * kActLds, (size_t)MOE_GROUP_MAX * Ud * kActLds,
                                kGroupingLds});
     int per_cu = 0, ncu = 0;
-    check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, moe_decode, kWG, c->lds), "occupancy");
+    uint32_t types = type_bit(g.gate_type) | type_bit(g.down_type);
+    if (g.has_shared) types |= type_bit(g.sh_gate_type) | type_bit(g.sh_down_type);
+    c->kernel = decode_kernel(types);
+    check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, c->kernel, kWG, c->lds), "occupancy");
     check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, g.device), "CU count");
     require(per_cu >= 1, "moe_decode does not fit a CU");
     c->grid = (uint32_t)(per_cu * ncu);

@@ -32,6 +32,9 @@ __device__ __constant__ static const uint32_t kIq3sGridDev[512] = {C0VEN_IQ3S_GR
 namespace {
 
 constexpr uint32_t kSpinLimit = 1u << 22;
+#ifndef C0VEN_POLL_SLEEP
+#define C0VEN_POLL_SLEEP 1
+#endif
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 __device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
@@ -67,7 +70,7 @@ __device__ __forceinline__ void wait_flag(const DecodeParams &p, uint32_t i) {
   if (threadIdx.x == 0) {
     uint32_t n = 0;
     while (ld_co(p.flags + i) != p.epoch) {
-      __builtin_amdgcn_s_sleep(1);
+      __builtin_amdgcn_s_sleep(C0VEN_POLL_SLEEP);
       if (++n == kSpinLimit) {
         st_co(p.err, 1u);
         break;
@@ -163,38 +166,39 @@ __device__ __forceinline__ void load_grid(uint32_t *grid_lds) {
 // The n terms of one (row, unit) pair against the activation units act + j * stride dwords, into t[j]. The unit's
 // weights are loaded first; `ready` (run by the whole work-group) then makes the activations available, so the
 // weights' HBM latency overlaps whatever ready waits for.
-template <typename Ready>
+template <uint32_t kTypes, typename Ready>
 __device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, uint32_t idx, uint32_t nl,
                                            const uint32_t *grid_lds, const uint32_t *act, uint32_t stride,
                                            const uint32_t &n, float *t, Ready ready) {
-  switch (type) {
-    case QT_Q8_0: {
+  if constexpr ((kTypes & kTypeQ8_0) != 0) {
+    if (kTypes == kTypeQ8_0 || type == QT_Q8_0) {
       UnitQ8_0 w;
       w.load(tile, idx, nl);
       ready();
 #pragma unroll
       for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
         if (j < n) t[j] = w.term(Act(act + j * stride));
-      break;
+      return;
     }
-    case QT_Q4_K: {
+  }
+  if constexpr ((kTypes & kTypeQ4_K) != 0) {
+    if ((kTypes & ~kTypeQ8_0) == kTypeQ4_K || type == QT_Q4_K) {
       UnitQ4_K w;
       w.load(tile, idx, nl);
       ready();
 #pragma unroll
       for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
         if (j < n) t[j] = w.term(Act(act + j * stride));
-      break;
+      return;
     }
-    default: {
-      UnitIQ3_S w;
-      w.load(tile, idx, nl, grid_lds);
-      ready();
+  }
+  if constexpr ((kTypes & kTypeIQ3_S) != 0) {
+    UnitIQ3_S w;
+    w.load(tile, idx, nl, grid_lds);
+    ready();
 #pragma unroll
-      for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
-        if (j < n) t[j] = w.term(Act(act + j * stride));
-      break;
-    }
+    for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
+      if (j < n) t[j] = w.term(Act(act + j * stride));
   }
 }
 
@@ -215,14 +219,15 @@ __device__ __forceinline__ float row_sum(float t, uint32_t U) {
 // Router items
 
 // x[t] to the activation types of the routed and the shared gate: a half-wave per unit.
+template <uint32_t kTypes>
 __device__ __forceinline__ void quantise_x(const DecodeParams &p, uint32_t t) {
   const uint32_t H = p.H, l32 = threadIdx.x & 31u;
   for (uint32_t u = threadIdx.x / 32; u < H / kUnit; u += kWG / 32) {
     const float4 *src = (const float4 *)(p.x + (uint64_t)t * H + u * kUnit + 8 * l32);
     const float4 a = src[0], b = src[1];
     const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    quant_unit(v, l32, p.xact_r, p.act_r + ((uint64_t)t * (H / kUnit) + u) * kActBytes);
-    if (p.act_s != p.act_r) quant_unit(v, l32, p.xact_s, p.act_s + ((uint64_t)t * (H / kUnit) + u) * kActBytes);
+    quant_unit(v, l32, act_type<kTypes>(p.xact_r), p.act_r + ((uint64_t)t * (H / kUnit) + u) * kActBytes);
+    if (p.act_s != p.act_r) quant_unit(v, l32, act_type<kTypes>(p.xact_s), p.act_s + ((uint64_t)t * (H / kUnit) + u) * kActBytes);
   }
 }
 
@@ -402,12 +407,13 @@ __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *un
 }
 
 // Gate and up of rows blk * gate_up_rows .. of group g: lane = m * 32 + r * U + u; h = silu(g) * u per row.
+template <uint32_t kTypes>
 __device__ __forceinline__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
                              GroupLds *sg, uint32_t *s_flag, const uint64_t *tab, uint64_t *mark) {
   read_group(p, g, sg);
   const uint32_t U = p.H / kUnit, rows = gate_up_rows(U), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 0);
-  if (gm.type == QT_IQ3_S) {
+  if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
     load_grid(grid_lds);
     __syncthreads();
   }
@@ -416,7 +422,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, uint32_t g, 
   const uint8_t *mat = gm.mat + (m ? (gm.shared ? p.sh_up_off : p.ex_up_off) : 0);
   const uint8_t *tile = mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
   float t[MOE_GROUP_MAX];
-  pair_terms(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
+  pair_terms<kTypes>(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
              (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
                stage_act(gm.shared ? p.act_s : p.act_r, sg->tok, n, U, lds);
                __syncthreads();
@@ -440,19 +446,20 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, uint32_t g, 
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = ld_co(src + i);
-    const uint32_t dact = quant_vec_dot_type(group_mat(p, sg->slot, 2).type);
+    const uint32_t dact = act_type<kTypes>(quant_vec_dot_type(group_mat(p, sg->slot, 2).type));
     quant_unit(v, l32, dact, p.hact + ((uint64_t)sg->asg[j] * Ud + unit) * kActBytes);
   }
   if (arrive_last(p.cnt_hq + g, Ud, s_flag)) set_flag(p, kFlagH + g);
 }
 
 // Down rows blk * down_rows .. of group g (lane = r * U + u), then the combine of every token this item completes.
+template <uint32_t kTypes>
 __device__ __forceinline__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
                           GroupLds *sg, uint32_t *s_last, uint64_t *mark) {
   read_group(p, g, sg);
   const uint32_t U = p.F / kUnit, rows = down_rows(U), row0 = blk * rows, n = sg->n, nblk = p.H / rows;
   const GroupMat gm = group_mat(p, sg->slot, 2);
-  if (gm.type == QT_IQ3_S) {
+  if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
     load_grid(grid_lds);
     __syncthreads();
   }
@@ -460,7 +467,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, uint32_t g, uin
   const uint32_t row = row0 + wave_id() * (64 / U) + r;
   const uint8_t *tile = gm.mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
   float t[MOE_GROUP_MAX];
-  pair_terms(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
+  pair_terms<kTypes>(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
              (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
                wait_flag(p, kFlagH + g);  // the weights are already on their way
                stage_act(p.hact, sg->asg, n, U, lds);
@@ -515,6 +522,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, uint32_t g, uin
 
 // Grid: the work-groups of 256 the device holds at once; dynamic LDS: the larger of a group's activation units
 // (MOE_GROUP_MAX x units x kActLds) and the grouping's tables (kGroupingLds).
+template <uint32_t kTypes>
 __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) moe_decode(DecodeParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ uint32_t grid_lds[512];
@@ -544,7 +552,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) m
     uint64_t *mark = p.trace && it < p.trace_cap ? p.trace + 4 * it : nullptr;
     if (mark && threadIdx.x == 0) mark[0] = mark[1] = mark[2] = __builtin_amdgcn_s_memrealtime();
     if (it < nL) {
-      if (it < T) quantise_x(p, it);
+      if (it < T) quantise_x<kTypes>(p, it);
       if (p.route) {
         if (it * kRouteRows < E) router_rows(p, it, s_part);
         if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
@@ -566,13 +574,33 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) m
         set_flag(p, kFlagRouted);
       }
     } else if (it < B1 + ng * nGU) {
-      gate_up_item(p, (it - B1) / nGU, (it - B1) % nGU, lds, grid_lds, &sg, &s_flag, exp_tab, mark);
+      gate_up_item<kTypes>(p, (it - B1) / nGU, (it - B1) % nGU, lds, grid_lds, &sg, &s_flag, exp_tab, mark);
     } else {
       const uint32_t i = it - B1 - ng * nGU;
-      down_item(p, i / nD, i % nD, lds, grid_lds, &sg, s_last, mark);
+      down_item<kTypes>(p, i / nD, i % nD, lds, grid_lds, &sg, s_last, mark);
     }
     if (mark && threadIdx.x == 0) mark[3] = __builtin_amdgcn_s_memrealtime();
     __syncthreads();
+  }
+}
+
+template __global__ void moe_decode<1>(DecodeParams);
+template __global__ void moe_decode<2>(DecodeParams);
+template __global__ void moe_decode<3>(DecodeParams);
+template __global__ void moe_decode<4>(DecodeParams);
+template __global__ void moe_decode<5>(DecodeParams);
+template __global__ void moe_decode<6>(DecodeParams);
+template __global__ void moe_decode<7>(DecodeParams);
+
+const void *decode_kernel(uint32_t types) {
+  switch (types) {
+    case 1: return (const void *)moe_decode<1>;
+    case 2: return (const void *)moe_decode<2>;
+    case 3: return (const void *)moe_decode<3>;
+    case 4: return (const void *)moe_decode<4>;
+    case 5: return (const void *)moe_decode<5>;
+    case 6: return (const void *)moe_decode<6>;
+    default: return (const void *)moe_decode<7>;
   }
 }
 

@@ -45,7 +45,7 @@ __device__ __forceinline__ void route_norm(const uint32_t key[kRoutePer], uint32
 __device__ __forceinline__ void route_select(uint32_t key[kRoutePer], uint32_t id[kRoutePer], uint32_t K,
                                              uint32_t lane, uint32_t *my_id, uint32_t *my_key) {
   auto cswap = [&](int i, int j) {
-    const bool sw = key[j] > key[i] || (key[j] == key[i] && id[j] < id[i]);
+    const bool sw = (key[j] > key[i]) | ((key[j] == key[i]) & (id[j] < id[i]));  // no short circuit: no branches
     const uint32_t ki = key[i], ii = id[i];
     key[i] = sw ? key[j] : ki, id[i] = sw ? id[j] : ii;
     key[j] = sw ? ki : key[j], id[j] = sw ? ii : id[j];

@@ -75,7 +75,7 @@ def cfg(**kw):
 
 @pytest.mark.parametrize("bad", [dict(n_embd=1000), dict(n_embd=768), dict(n_ff=384), dict(n_expert=513),
                                  dict(n_used=17), dict(n_used=0), dict(gate_type=2), dict(down_type=15),
-                                 dict(sh_gate_type=30), dict(max_tokens=17), dict(n_embd=8192, max_tokens=8),
+                                 dict(sh_gate_type=30), dict(max_tokens=16385), dict(n_ff=16384),
                                  dict(swiglu_limit=-1.0)])
 def test_open_rejects_bad_config_before_the_device(bad):
     out = C.c_void_p()
