@@ -21,14 +21,36 @@ template <typename T>
 __device__ __forceinline__ T ld_co(const T *p) {
   return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A tagged record: a 32-bit value in the low word, the writing launch's tag in the high word, stored and loaded as one
+// 64-bit access (single-copy atomic), so a reader that sees its launch's tag sees the value written with it.
+__device__ __forceinline__ void st_tag(uint64_t *p, uint32_t v, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_tag(const uint64_t *p) {
+  return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t tag_of(uint64_t v) { return (uint32_t)(v >> 32); }
+
 // 16 bytes coherently, as four words.
 __device__ __forceinline__ uint4 ld_co4(const void *p) {
   const uint32_t *q = (const uint32_t *)p;
   return make_uint4(ld_co(q), ld_co(q + 1), ld_co(q + 2), ld_co(q + 3));
 }
 
+// A word of a quantised unit: to global memory (coherent, for other work-groups) or to LDS (for this one).
+template <bool kLds, typename T>
+__device__ __forceinline__ void put_word(uint8_t *out, uint32_t off, T v) {
+  if constexpr (kLds) {
+    *(T *)(out + off) = v;
+  } else {
+    st_co((T *)(out + off), v);
+  }
+}
+
 // One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
-// with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0).
+// with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0). out is in global
+// memory, or in LDS when kLds.
+template <bool kLds = false>
 __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
   uint32_t code[2] = {0u, 0u};
   if (act_type == QT_Q8_K) {
@@ -61,10 +83,10 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
     }
     part += __shfl_xor(part, 1, 32);
     part += __shfl_xor(part, 2, 32);
-    st_co((uint32_t *)out + 2 * l32, code[0]);
-    st_co((uint32_t *)out + 2 * l32 + 1, code[1]);
-    if ((l32 & 3u) == 0) st_co((int32_t *)(out + kActSums) + l32 / 4, part);
-    if (l32 == 0) st_co((float *)(out + kActScales), d);
+    put_word<kLds>(out, 8 * l32, code[0]);
+    put_word<kLds>(out, 8 * l32 + 4, code[1]);
+    if ((l32 & 3u) == 0) put_word<kLds>(out, kActSums + l32, part);
+    if (l32 == 0) put_word<kLds>(out, kActScales, d);
   } else {  // q8_0: blocks of 32, four lanes each
     float amax = 0.0f;
 #pragma unroll
@@ -77,10 +99,10 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
       const int q = nearest_int(__fmul_rn(v[i], id));
       code[i / 4] |= ((uint32_t)q & 0xffu) << (8 * (i % 4));
     }
-    st_co((uint32_t *)out + 2 * l32, code[0]);
-    st_co((uint32_t *)out + 2 * l32 + 1, code[1]);
-    if ((l32 & 3u) == 0) st_co((float *)(out + kActScales) + l32 / 4, h2f(f2h(d)));
-    if ((l32 & 3u) == 0) st_co((int32_t *)(out + kActSums) + l32 / 4, 0);
+    put_word<kLds>(out, 8 * l32, code[0]);
+    put_word<kLds>(out, 8 * l32 + 4, code[1]);
+    if ((l32 & 3u) == 0) put_word<kLds>(out, kActScales + l32, h2f(f2h(d)));
+    if ((l32 & 3u) == 0) put_word<kLds>(out, kActSums + l32, 0);
   }
 }
 

@@ -17,19 +17,25 @@ constexpr uint32_t kMaxUnits = 32;         // 256-value units per row: H and F u
 constexpr uint32_t max_groups(uint32_t T, uint32_t K) { return T * K + (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX; }
 
 // The work-group (four waves) and the work items of moe_decode, in the order every work-group walks them:
-//   lead items     two router rows each (half a row a wave), when routing; item t < T also quantises x[t];
-//   top-k items    one a token (when routing);
-//   gate/up items  gate_up_rows(U) rows of gate and of up of one group, all units (lane = m * 32 + r * U + u);
-//   down items     down_rows(U_down) rows of down of one group, all units (lane = r * U_down + u).
+//   lead items       one router row each (a 512-value chunk a wave), when routing; item t < T also
+//                    quantises x[t];
+//   top-k items      one a token (when routing): the shared gate's row, then softmax, top-k and weights;
+//   shared items     (when routing with a shared expert) the shared expert's gate/up then down items, for each chunk
+//                    of MOE_GROUP_MAX tokens: they need no routing, so they run beside the router;
+//   gate/up items    gate_up_rows(U) rows of gate and of up of one routed group, all units (lane = m * 32 + r * U + u);
+//   down items       down_rows(U_down) rows of down of one routed group (lane = r * U_down + u).
 constexpr uint32_t kWG = 256;
-// Lead items: two router rows each (two waves a row); item t < T also quantises x[t]. The shared gate's row (row E)
-// is taken by the top-k items instead, while they wait for the lead items (they run on work-groups the lead items
-// leave free).
-constexpr uint32_t kRouteRows = 2;
+constexpr uint32_t kRouteRows = 1;
 constexpr uint32_t lead_items(uint32_t T, uint32_t E, uint32_t route) {
   return route ? ((E + kRouteRows - 1) / kRouteRows > T ? (E + kRouteRows - 1) / kRouteRows : T) : T;
 }
 constexpr uint32_t kMaxLeadItems = kMaxExperts / kRouteRows;
+// Chunks of the shared expert's tokens (one group's worth each) when it runs beside the router.
+constexpr uint32_t shared_chunks(uint32_t T, uint32_t route, uint32_t has_shared) {
+  return route && has_shared ? (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX : 0;
+}
+// Groups a launch may have: routed (every assignment its own, at worst), or a pre-routed call's jobs.
+constexpr uint32_t kMaxGroups = max_groups(kMaxDecodeTokens, kMaxUsed + 1);
 // LDS the grouping step takes from the dynamic allocation: T K ids, a token mask and two group numbers per expert,
 // and a sort key per group.
 constexpr uint32_t kGroupingLds =
@@ -37,9 +43,11 @@ constexpr uint32_t kGroupingLds =
 constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kWG / 64) * (32 / Ug); }
 constexpr uint32_t down_rows(uint32_t Ud) { return (kWG / 64) * (64 / Ud); }
 
-// Flags (64-bit, set to the launch's epoch): [i < kMaxLeadItems] lead item i is done (its logits and quantised x are
-// in), [kFlagRouted] the groups are in, [kFlagH + g] group g's h is in.
-constexpr uint32_t kFlagLead = 0, kFlagRouted = kMaxLeadItems, kFlagH = kMaxLeadItems + 1;
+// Flags (64-bit, set to the launch's epoch): [i < kMaxLeadItems] lead item i is done (its quantised x is in, for
+// the shared expert's items), [kFlagRouted] a pre-routed call's x is quantised. Data handed from one work item to the
+// next inside a launch (logits, ids, weights, the shared gate, h) travels as tagged records instead: 64-bit words
+// whose high half is the launch's tag, so the reader polls the data itself and needs no flag.
+constexpr uint32_t kFlagLead = 0, kFlagRouted = kMaxLeadItems, kFlagCount = kMaxLeadItems + 1;
 
 struct DecodeParams {
   uint32_t H, F, E, K, T;
@@ -49,6 +57,7 @@ struct DecodeParams {
   uint32_t route;            // 1: route x; 0: the host gave ids, w and the groups (pre-routed jobs)
   const uint32_t *tok_need;  // pre-routed: outputs token t sums (its jobs); null: K + has_shared
   uint64_t epoch;            // this launch's number: a flag is set when it holds it
+  uint32_t tag;              // its low 32 bits: a tagged record (value in the low word) is valid when it holds it
   // The layer.
   const uint16_t *router;  // (E + 1) x H bf16, the last row the shared gate
   const float *bias;       // E, or null
@@ -62,20 +71,18 @@ struct DecodeParams {
   // Scratch (sized for max_tokens at open). Everything written here during a launch and read by another work-group
   // goes through device-coherent stores and loads.
   uint8_t *act_r, *act_s;  // T x (H / 256) activation units; act_s == act_r when the two types agree
-  float *logits;           // T x (E + 1)
-  int32_t *ids;            // T x K
-  float *w;                // T x K
-  float *gs;               // T
+  uint64_t *logits;        // T x (E + 1) tagged records (the fp32 bits)
+  int32_t *ids;            // T x K: the routed ids as the caller reads them, or a pre-routed call's
+  float *w;                // T x K: the same for the weights
+  uint64_t *ids_t, *w_t;   // T x K tagged records of the routed ids and weights
+  uint64_t *gs;            // T tagged records: the shared expert's gate
   MoeGroup *groups;
   uint32_t *ngroups;
-  float *h;                // (T K + T) x F: SwiGLU of each assignment, fp32
-  uint8_t *hact;           // (T K + T) x (F / 256) activation units: h quantised to the down's type
+  uint64_t *h;             // (T K + T) x F tagged records: SwiGLU of each assignment, fp32
   float *y_asg;            // (T K + T) x H: each assignment's expert output
   uint64_t *flags;         // kFlagH + G
   uint32_t *cnt_route;     // 1: lead items in (pre-routed calls)
   uint32_t *cnt_topk;      // 1: tokens routed
-  uint32_t *cnt_hu;        // G x (F / 256): gate/up items in per (group, unit of h)
-  uint32_t *cnt_hq;        // G: units of h quantised per group
   uint32_t *cnt_tok;       // T x (H / down_rows): outputs in per (token, down row block)
   uint32_t *err;           // set when a wait gave up (never, unless a work-group could not run)
   uint64_t *trace;         // null, or (start, ready, computed, end) s_memrealtime stamps per work item

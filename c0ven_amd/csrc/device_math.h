@@ -27,18 +27,14 @@ __device__ __constant__ static const uint64_t kExp2Tab[32] = {C0VEN_EXP2_TAB_VAL
 // memory on the device, a host copy on the CPU): the same source runs on both, and tests/test_expf.py checks the host
 // build against libm's expf on all 2^32 inputs.
 __host__ __device__ __forceinline__ float expf_libm(float x, const uint64_t *tab) {
-  const uint32_t ux = __builtin_bit_cast(uint32_t, x);
-  const uint32_t abstop = (ux >> 20) & 0x7ffu;
-  if (abstop >= 0x42bu) {  // |x| >= 88, infinity or NaN
-    if (ux == 0xff800000u) return 0.0f;
-    if (abstop >= 0x7f8u) return x + x;
-    if (x > 0x1.62e42ep6f) return __builtin_bit_cast(float, 0x7f800000u);
-    if (x < -0x1.9fe368p6f) return 0.0f;
-  }
+  // The main path runs for every input and the out-of-range cases are selected at the end, so the code has no
+  // branches: a wave evaluates several of these interleaved. Outside (-0x1.9fe368p6, 0x1.62e42ep6) the result is
+  // 0 or infinity (both infinities included), a NaN gives x + x; those are exactly libm's special cases.
   const double InvLn2N = 0x1.71547652b82fep+0 * 32, Shift = 0x1.8p+52;
   const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                C2 = 0x1.62e42ff0c52d6p-1 / 32;
-  const double xd = (double)x;
+  const bool under = x < -0x1.9fe368p6f, over = x > 0x1.62e42ep6f, nan = x != x;
+  const double xd = (double)(under | over | nan ? 0.0f : x);
   double kd = __builtin_fma(InvLn2N, xd, Shift);
   const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
   kd = kd - Shift;
@@ -50,7 +46,10 @@ __host__ __device__ __forceinline__ float expf_libm(float x, const uint64_t *tab
   double y = __builtin_fma(C2, r, 1.0);
   y = __builtin_fma(z, r2, y);
   y = y * sc;
-  return (float)y;
+  float res = (float)y;
+  res = under ? 0.0f : res;
+  res = over ? __builtin_bit_cast(float, 0x7f800000u) : res;
+  return nan ? x + x : res;
 }
 
 // silu(g) * u with the optional clamp, each step rounded as the CPU path's g / (1 + expf(-g)) * u.
@@ -72,9 +71,10 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 // bf16 by round to nearest even (ggml's GGML_FP32_TO_BF16), NaN kept quiet.
 __device__ __forceinline__ float round_bf16(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return __uint_as_float(((x >> 16) | 64u) << 16);
-  return __uint_as_float(((x + (0x7fffu + ((x >> 16) & 1u))) >> 16) << 16);
+  const uint32_t x = __float_as_uint(f);
+  const uint32_t quiet = (x | 0x00400000u) & 0xffff0000u;  // NaN: truncated, quiet bit set (no branch: a select)
+  const uint32_t rne = (x + (0x7fffu + ((x >> 16) & 1u))) & 0xffff0000u;
+  return __uint_as_float((x & 0x7fffffffu) > 0x7f800000u ? quiet : rne);
 }
 
 // ggml's nearest_int: round half to even, |v| < 2^22.
@@ -99,13 +99,13 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 }
 
 // DPP lane exchanges (gfx9 controls): quad_perm(1,0,3,2) = lane ^ 1, quad_perm(2,3,0,1) = lane ^ 2,
-// row_half_mirror = 7 - lane within 8, row_mirror = 15 - lane within 16. Each pairs a lane with one in the other half
+// quad_perm(3,2,1,0) = 3 - lane within 4, row_half_mirror = 7 - lane within 8, row_mirror = 15 - lane within 16. Each pairs a lane with one in the other half
 // of its 2, 4, 8 or 16, so four steps reduce a row of 16 with every lane holding the result.
 template <int kCtrl>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, 0xf, 0xf, false);
 }
-constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppQuadRev = 0x1B, kDppHalfMirror = 0x141, kDppMirror = 0x140;
 constexpr int kDppShr1 = 0x111;  // row_shr:1 (lane - 1 within a row of 16)
 
 __device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }

@@ -66,21 +66,23 @@ struct moe_ctx {
   float *x_dev = nullptr, *y_dev = nullptr, *w_stage = nullptr;
   int32_t *ids_stage = nullptr;
   // Scratch.
-  uint8_t *act_r = nullptr, *act_s = nullptr, *hact = nullptr;
-  float *logits = nullptr, *w = nullptr, *gs = nullptr, *h = nullptr, *y_asg = nullptr;
+  uint8_t *act_r = nullptr, *act_s = nullptr;
+  float *w = nullptr, *y_asg = nullptr;
+  uint64_t *logits = nullptr, *gs = nullptr, *h = nullptr, *ids_t = nullptr, *w_t = nullptr;  // tagged records
   int32_t *ids = nullptr;
   MoeGroup *groups = nullptr;
   uint32_t *ngroups = nullptr, *counters = nullptr, *tok_need = nullptr;
-  uint32_t *cnt_route = nullptr, *cnt_topk = nullptr, *cnt_hu = nullptr, *cnt_hq = nullptr, *cnt_tok = nullptr;
+  uint32_t *cnt_route = nullptr, *cnt_topk = nullptr, *cnt_tok = nullptr;
   uint32_t *err_flag = nullptr;
   uint64_t *flags = nullptr;
   uint64_t epoch = 0;          // the last launch's number
+  std::vector<std::pair<uint64_t *, uint64_t>> tagged;  // the tagged-record buffers (pointer, records)
   uint32_t grid = 0;           // co-resident work-groups of moe_decode
   const void *kernel = nullptr;  // moe_decode for the context's set of weight types
   size_t lds = 0;              // its dynamic LDS
   bool timing = false;
   uint64_t *trace = nullptr;   // per-item stamps of the last forward, when tracing
-  uint32_t trace_cap = 0, trace_bounds[5] = {0, 0, 0, 0, 0}, last_T = 0, last_route = 1;
+  uint32_t trace_cap = 0, last_T = 0, last_route = 1;
   std::vector<hipEvent_t> ev;  // the event pool
   size_t ev_next = 0;          // events of the pool in use by the record
   std::vector<TimedLaunch> timed;
@@ -156,11 +158,11 @@ DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   p.experts = L.experts, p.ex_bytes = c->ex_bytes, p.ex_up_off = c->ex_up, p.ex_down_off = c->ex_down;
   p.shared = L.shared, p.sh_up_off = c->sh_up, p.sh_down_off = c->sh_down;
   p.act_r = c->act_r, p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
-  p.logits = c->logits, p.ids = c->ids, p.w = c->w, p.gs = c->gs;
+  p.logits = c->logits, p.ids = c->ids, p.w = c->w, p.gs = c->gs, p.ids_t = c->ids_t, p.w_t = c->w_t;
   p.groups = c->groups, p.ngroups = c->ngroups;
-  p.h = c->h, p.hact = c->hact, p.y_asg = c->y_asg;
+  p.h = c->h, p.y_asg = c->y_asg;
   p.flags = c->flags, p.err = c->err_flag;
-  p.cnt_route = c->cnt_route, p.cnt_topk = c->cnt_topk, p.cnt_hu = c->cnt_hu, p.cnt_hq = c->cnt_hq;
+  p.cnt_route = c->cnt_route, p.cnt_topk = c->cnt_topk;
   p.cnt_tok = c->cnt_tok;
   return p;
 }
@@ -185,9 +187,19 @@ void timing_hook(void *ctx, const char *name, int after, hipStream_t s) {
   }
 }
 
+// Zeroes the tagged-record buffers (tag 0 is never a launch's).
+void clear_tagged(moe_ctx *c, hipStream_t s) {
+  for (const auto &b : c->tagged) check(hipMemsetAsync(b.first, 0, b.second * sizeof(uint64_t), s), "hipMemsetAsync");
+}
+
 void launch(moe_ctx *c, const DecodeParams &p, hipStream_t s) {
   DecodeParams q = p;
   q.epoch = ++c->epoch;
+  if ((uint32_t)q.epoch == 0) {  // the 32-bit tags wrap (every 2^32 launches): old records must not match
+    clear_tagged(c, s);
+    q.epoch = ++c->epoch;
+  }
+  q.tag = (uint32_t)q.epoch;
   if (c->trace) q.trace = c->trace, q.trace_cap = c->trace_cap;
   c->last_T = p.T, c->last_route = p.route;
   if (c->timing) timing_hook(c, "moe_decode", 0, s);
@@ -314,27 +326,29 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     }
     c->act_r = c->alloc<uint8_t>((uint64_t)T * Ug * kActBytes);
     c->act_s = c->alloc<uint8_t>((uint64_t)T * Ug * kActBytes);
-    c->logits = c->alloc<float>((uint64_t)T * (E + 1));
+    c->logits = c->alloc<uint64_t>((uint64_t)T * (E + 1));
     c->ids = c->alloc<int32_t>((uint64_t)T * K1);
     c->w = c->alloc<float>((uint64_t)T * K1);
-    c->gs = c->alloc<float>(T);
+    c->gs = c->alloc<uint64_t>(T);
+    c->ids_t = c->alloc<uint64_t>((uint64_t)T * K1);
+    c->w_t = c->alloc<uint64_t>((uint64_t)T * K1);
     c->groups = c->alloc<MoeGroup>(G);
     c->ngroups = c->alloc<uint32_t>(1);
     c->tok_need = c->alloc<uint32_t>(T);
-    c->h = c->alloc<float>((uint64_t)A * F);
-    c->hact = c->alloc<uint8_t>((uint64_t)A * Ud * kActBytes);
+    c->h = c->alloc<uint64_t>((uint64_t)A * F);
     c->y_asg = c->alloc<float>((uint64_t)A * H);
-    const uint64_t ncnt = 3 + (uint64_t)G * Ud + G + (uint64_t)T * (H / down_rows(Ud));
+    const uint64_t ncnt = 3 + (uint64_t)T * (H / down_rows(Ud));
     c->counters = c->alloc<uint32_t>(ncnt);
     check(hipMemset(c->counters, 0, ncnt * sizeof(uint32_t)), "hipMemset");
     c->cnt_route = c->counters;
     c->cnt_topk = c->cnt_route + 1;
     c->err_flag = c->cnt_topk + 1;
-    c->cnt_hu = c->err_flag + 1;
-    c->cnt_hq = c->cnt_hu + (uint64_t)G * Ud;
-    c->cnt_tok = c->cnt_hq + G;
-    c->flags = c->alloc<uint64_t>(kFlagH + G);
-    check(hipMemset(c->flags, 0, (kFlagH + G) * sizeof(uint64_t)), "hipMemset");
+    c->cnt_tok = c->err_flag + 1;
+    c->flags = c->alloc<uint64_t>(kFlagCount);
+    check(hipMemset(c->flags, 0, kFlagCount * sizeof(uint64_t)), "hipMemset");
+    c->tagged = {{c->logits, (uint64_t)T * (E + 1)}, {c->gs, T}, {c->ids_t, (uint64_t)T * K1}, {c->w_t, (uint64_t)T * K1},
+                 {c->h, (uint64_t)A * F}};
+    clear_tagged(c, nullptr);
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
     c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * Ug * kActLds, (size_t)MOE_GROUP_MAX * Ud * kActLds,
@@ -570,10 +584,11 @@ MOE_API moe_status moe_trace(moe_ctx *c, uint64_t *stamps, uint32_t cap, uint32_
     check(hipMemcpy(&ng, c->ngroups, 4, hipMemcpyDeviceToHost), "read ngroups");
     const moe_config &g = c->cfg;
     const uint32_t T = c->last_T, Ug = g.n_embd / kUnit, Ud = g.n_ff / kUnit;
-    const uint32_t nL = lead_items(T, g.n_expert, c->last_route);
-    const uint32_t b1 = nL + (c->last_route ? T : 0), b2 = b1 + ng * (g.n_ff / gate_up_rows(Ug));
-    const uint32_t end = b2 + ng * (g.n_embd / down_rows(Ud));
-    const uint32_t bb[5] = {0, nL, b1, b2, end};
+    const uint32_t nL = lead_items(T, g.n_expert, c->last_route), ns = shared_chunks(T, c->last_route, g.has_shared);
+    const uint32_t nGU = g.n_ff / gate_up_rows(Ug), nD = g.n_embd / down_rows(Ud);
+    const uint32_t b1 = nL + (c->last_route ? T : 0), b2 = b1 + ns * nGU, b3 = b2 + ns * nD, b4 = b3 + ng * nGU;
+    const uint32_t end = b4 + ng * nD;
+    const uint32_t bb[7] = {0, nL, b1, b2, b3, b4, end};
     if (bounds) std::memcpy(bounds, bb, sizeof bb);
     *n = std::min(end, c->trace_cap);
     if (stamps)

@@ -17,6 +17,8 @@
 // Waits are bounded anyway: past kSpinLimit polls a wait gives up and sets *err.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "act_quant.h"
 #include "decode.h"
 #include "route.h"
@@ -103,33 +105,78 @@ __device__ __forceinline__ void wait_flags(const DecodeParams &p, uint32_t base,
   __syncthreads();
 }
 
-// Top-k and weights for token t (route.h:39-99 and layer.cl:765-804 restated). Two waves at once: wave 1 takes the
-// softmax's max and 1 / sum (the sum in double); wave 0 selects: lane l holds
-// experts l + 64 i, sorted by (logit, lower id first), and each of the k rounds takes the wave's largest head (a DPP
-// max of the logit keys, a ballot for equal keys, the lower id among them) and pops it. Then wave 0 turns the k
-// winners into weights. The winners' ids and keys stay in sel (sel[j], sel[kMaxUsed + j]) for the grouping.
-__device__ __forceinline__ void route_token(const DecodeParams &p, uint32_t t, const uint64_t *tab, uint32_t *sel, float *norm) {
-  const uint32_t lane = lane_id(), E = p.E, K = p.K;
-  const float *lg = p.logits + (uint64_t)t * (E + 1);
-  uint32_t my_id = 0, my_key = 0;
-  if (wave_id() <= 1) {
-    uint32_t key[kRoutePer], id[kRoutePer];
-    route_load(lg, E, lane, key, id);
-    if (wave_id() == 1) {
-      float mx, inv;
-      route_norm(key, E, lane, tab, &mx, &inv);
-      if (lane == 0) norm[0] = mx, norm[1] = inv;
-    } else {
-      route_select(key, id, K, lane, &my_id, &my_key);
-      if (lane < K) sel[lane] = my_id, sel[kMaxUsed + lane] = my_key;
+// The value of a tagged record once it holds this launch's tag (the calling thread polls; past kSpinLimit polls it
+// gives up, sets *err and returns what it has).
+__device__ __forceinline__ uint32_t poll_tag(const DecodeParams &p, const uint64_t *q) {
+  uint64_t v = ld_tag(q);
+  uint32_t n = 0;
+  while (tag_of(v) != p.tag) {
+    __builtin_amdgcn_s_sleep(C0VEN_POLL_SLEEP);
+    if (++n == kSpinLimit) {
+      st_co(p.err, 1u);
+      break;
+    }
+    v = ld_tag(q);
+  }
+  return (uint32_t)v;
+}
+
+// Token t's logits as order keys, lane l holding experts l + 64 i: the wave polls the tagged records until every one
+// holds this launch's tag (the lead items' stores are the hand-off; no flag).
+__device__ __forceinline__ void load_logits(const DecodeParams &p, uint32_t t, uint32_t key[kRoutePer], uint32_t id[kRoutePer]) {
+  const uint32_t lane = lane_id(), E = p.E;
+  const uint64_t *lg = p.logits + (uint64_t)t * (E + 1);
+  uint64_t v[kRoutePer];
+  for (uint32_t n = 0;; n++) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < kRoutePer; i++) {
+      const uint32_t e = lane + 64 * i;
+      v[i] = ld_tag(lg + min(e, E - 1));
+    }
+#pragma unroll
+    for (int i = 0; i < kRoutePer; i++) ok &= tag_of(v[i]) == p.tag;
+    if (__all(ok)) break;
+    __builtin_amdgcn_s_sleep(C0VEN_POLL_SLEEP);
+    if (n == kSpinLimit) {
+      if (lane == 0) st_co(p.err, 1u);
+      break;
     }
   }
+#pragma unroll
+  for (int i = 0; i < kRoutePer; i++) {
+    const uint32_t e = lane + 64 * i;
+    key[i] = e < E ? float_key(__uint_as_float((uint32_t)v[i])) : 0u;
+    id[i] = e;
+  }
+}
+
+// Top-k and weights for token t (route.h:39-99 and layer.cl:765-804 restated). Every wave loads the token's logits
+// (lane l holds experts l + 64 i). Wave 0 selects the top k (route_select_lds: a threshold, then the candidates
+// ranked in LDS). Waves 1..3 meanwhile take the softmax's max and a third of its sum each (in double); the sum is
+// their three parts in order. Then wave 0 turns the k winners into weights and stores ids and w.
+__device__ __forceinline__ void route_token(const DecodeParams &p, uint32_t t, const uint64_t *tab, double *dpart,
+                                            uint2 *cand) {
+  const uint32_t lane = lane_id(), wv = wave_id(), E = p.E, K = p.K;
+  uint32_t key[kRoutePer], id[kRoutePer];
+  load_logits(p, t, key, id);
+  const float mx = route_max(key);
+  uint32_t my_id = 0, my_key = 0;
+  if (wv == 0) {
+    route_select_lds(key, id, K, lane, cand, &my_id, &my_key);
+  } else {
+    const double part = route_sum_part(key, E, lane, wv - 1, mx, tab);
+    if (lane == 0) dpart[wv - 1] = part;
+  }
   __syncthreads();
-  if (wave_id() == 0) {
-    const float w = route_weight(my_key, norm[0], norm[1], K, lane, tab);
+  if (wv == 0) {
+    const float inv = (float)(1.0 / __dadd_rn(__dadd_rn(dpart[0], dpart[1]), dpart[2]));
+    const float w = route_weight(my_key, mx, inv, K, lane, tab);
     if (lane < K) {
-      st_co(p.ids + t * K + lane, (int32_t)my_id);
-      st_co(p.w + t * K + lane, w);
+      st_tag(p.ids_t + t * K + lane, my_id, p.tag);
+      st_tag(p.w_t + t * K + lane, __float_as_uint(w), p.tag);
+      p.ids[t * K + lane] = (int32_t)my_id;  // the caller's copies, read after the launch
+      p.w[t * K + lane] = w;
     }
   }
 }
@@ -152,11 +199,6 @@ __device__ __forceinline__ GroupMat group_mat(const DecodeParams &p, int32_t slo
     m.mat = p.experts + (uint64_t)slot * p.ex_bytes + (which == 0 ? 0 : which == 1 ? p.ex_up_off : p.ex_down_off);
   }
   return m;
-}
-
-__device__ __forceinline__ uint32_t asg_token(const DecodeParams &p, uint32_t asg) {
-  const uint32_t n = p.T * p.K;
-  return asg < n ? asg / p.K : asg - n;
 }
 
 __device__ __forceinline__ void load_grid(uint32_t *grid_lds) {
@@ -231,93 +273,156 @@ __device__ __forceinline__ void quantise_x(const DecodeParams &p, uint32_t t) {
   }
 }
 
-// Router row dot products with tokens t_begin .. t_end - 1, in part[wave][t]: wave w takes row `row`'s 512-value
-// chunks c0, c0 + step, ..., a lane eight values of each, every product bf16(W) bf16(x) exact and summed in fp64 (the lane's share,
-// then the wave's in a fixed order). x is read straight from global memory (it is L2-resident: every lead item reads
-// it), four tokens' worth in flight at once.
-__device__ __forceinline__ void row_dots(const DecodeParams &p, uint32_t row, uint32_t c0, uint32_t step,
-                                         uint32_t t_begin, uint32_t t_end, double *part) {
-  const uint32_t lane = lane_id(), wv = wave_id(), H = p.H, nC = H / 512;
-  const uint16_t *wr = p.router + (uint64_t)row * H + lane * 8;
-  const float *xl = p.x + lane * 8;
-  const uint32_t c1 = c0 + step;  // the wave's first two chunks stay in registers, their x loads in flight together
-  const uint4 w0 = c0 < nC ? *(const uint4 *)(wr + 512 * c0) : make_uint4(0, 0, 0, 0);
-  const uint4 w1 = c1 < nC ? *(const uint4 *)(wr + 512 * c1) : make_uint4(0, 0, 0, 0);
-  auto fma8 = [](const uint4 &wq, const float4 &xa, const float4 &xb, double acc) {
-    const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
-    const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+// A double summed over the 16 lanes of its row (butterflies: lane ^ 1, ^ 2, then the mirrors of 8 and 16); every lane
+// of the row receives it.
+__device__ __forceinline__ double row16_sum_f64(double v) {
+  v = __dadd_rn(v, dpp_f64<kDppXor1>(v));
+  v = __dadd_rn(v, dpp_f64<kDppXor2>(v));
+  v = __dadd_rn(v, dpp_f64<kDppHalfMirror>(v));
+  return __dadd_rn(v, dpp_f64<kDppMirror>(v));
+}
+
+// Eight doubles of every lane summed over the 16 lanes of its row, by halving exchanges (the partner across the row's
+// mirror, then the 8-lane mirror and the quad reverse, each keeping the half of the values its lane bit picks; then
+// lane ^ 1): lane l of the row receives the total of v[(l % 16) / 2].
+__device__ __forceinline__ double row16_reduce8_f64(double v[8]) {
+  const uint32_t l = lane_id();
+  auto step = [&](auto ctrl_tag, uint32_t half, uint32_t keep_hi) {
+    constexpr int kCtrl = decltype(ctrl_tag)::value;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const double wd = (double)__uint_as_float((k & 1) ? ww[k / 2] & 0xffff0000u : ww[k / 2] << 16);
-      acc = __builtin_fma(wd, (double)round_bf16(xs[k]), acc);
+    for (uint32_t i = 0; i < 4; i++) {
+      if (i >= half) break;
+      const double send = keep_hi ? v[i] : v[half + i], keep = keep_hi ? v[half + i] : v[i];
+      v[i] = __dadd_rn(keep, dpp_f64<kCtrl>(send));
     }
-    return acc;
   };
-  for (uint32_t t0 = t_begin; t0 < t_end; t0 += 4) {
-    float4 xa[4], xb[4], ya[4], yb[4];
+  step(std::integral_constant<int, kDppMirror>{}, 4, (l >> 3) & 1u);
+  step(std::integral_constant<int, kDppHalfMirror>{}, 2, (l >> 2) & 1u);
+  step(std::integral_constant<int, kDppQuadRev>{}, 1, (l >> 1) & 1u);
+  return __dadd_rn(v[0], dpp_f64<kDppXor1>(v[0]));
+}
+
+// Router dot products of row `row` with tokens t0 .. t0 + nt - 1 (nt <= 16): tot[t] = sum over the row of
+// bf16(W) bf16(x), each product exact, summed in fp64. Wave w takes the 512-value chunks w, w + 4, ..., lane l values
+// 8 l .. 8 l + 7 of each: a lane converts its weights once for all tokens. Eight tokens at a time (x of four in flight
+// while four are used), each chunk's eight sums are reduced over the 16 lanes of a row (one value a lane pair left) and
+// added to that row of lanes' partial in LDS; the sixteen partials of an output (four rows of lanes, four waves) are
+// then added in a fixed order.
+__device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, uint32_t t0, uint32_t nt, double *part,
+                                           double *tot) {
+  const uint32_t lane = lane_id(), wv = wave_id(), H = p.H, nC = H / 512;
+  const uint32_t pslot = 4 * wv + lane / 16;
+  for (uint32_t c = wv; c < nC; c += kWG / 64) {
+    const uint4 wa = *(const uint4 *)(p.router + (uint64_t)row * H + 512 * c + 8 * lane);
+    const float *xc = p.x + (uint64_t)t0 * H + 512 * c + 8 * lane;
+    double wd[8];
+    {
+      const uint32_t w0[4] = {wa.x, wa.y, wa.z, wa.w};
 #pragma unroll
-    for (uint32_t tt = 0; tt < 4; tt++) {
-      const float *xt = xl + (uint64_t)min(t0 + tt, t_end - 1) * H;
-      const float4 *q = (const float4 *)(xt + 512 * min(c0, nC - 1));
-      const float4 *q1 = (const float4 *)(xt + 512 * min(c1, nC - 1));
-      xa[tt] = q[0], xb[tt] = q[1], ya[tt] = q1[0], yb[tt] = q1[1];
+      for (int k = 0; k < 8; k++) wd[k] = (double)__uint_as_float((k & 1) ? w0[k / 2] & 0xffff0000u : w0[k / 2] << 16);
     }
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    if (c0 < nC) {
-#pragma unroll
-      for (uint32_t tt = 0; tt < 4; tt++) acc[tt] = fma8(w0, xa[tt], xb[tt], acc[tt]);
-    }
-    if (c1 < nC) {
-#pragma unroll
-      for (uint32_t tt = 0; tt < 4; tt++) acc[tt] = fma8(w1, ya[tt], yb[tt], acc[tt]);
-    }
-    for (uint32_t c = c1 + step; c < nC; c += step) {  // long rows
-      const uint4 wq = *(const uint4 *)(wr + 512 * c);
+    for (uint32_t tb = 0; tb < nt; tb += 8) {
+      const uint32_t nb = min(8u, nt - tb);
+      double v[8];
+      float4 xq[2][4][2];
 #pragma unroll
       for (uint32_t tt = 0; tt < 4; tt++) {
-        const float4 *q = (const float4 *)(xl + (uint64_t)min(t0 + tt, t_end - 1) * H + 512 * c);
-        acc[tt] = fma8(wq, q[0], q[1], acc[tt]);
+        const float4 *q = (const float4 *)(xc + (uint64_t)(tb + min(tt, nb - 1)) * H);
+        xq[0][tt][0] = q[0], xq[0][tt][1] = q[1];
+      }
+#pragma unroll
+      for (uint32_t tt = 0; tt < 8; tt++) {
+        if (tt == 0 && nb > 4) {
+#pragma unroll
+          for (uint32_t u = 0; u < 4; u++) {
+            const float4 *q = (const float4 *)(xc + (uint64_t)(tb + min(4 + u, nb - 1)) * H);
+            xq[1][u][0] = q[0], xq[1][u][1] = q[1];
+          }
+        }
+        double a = 0.0;
+        if (tt < nb) {
+          const float4 xa = xq[tt / 4][tt % 4][0], xb = xq[tt / 4][tt % 4][1];
+          const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+          for (int k = 0; k < 8; k++) a = __builtin_fma(wd[k], (double)round_bf16(xs[k]), a);
+        }
+        v[tt] = a;
+      }
+      double s;
+      uint32_t tt;
+      if (nb == 1) {
+        s = row16_sum_f64(v[0]), tt = 0;
+      } else {
+        s = row16_reduce8_f64(v), tt = (lane & 15u) / 2;
+      }
+      if ((lane & (nb == 1 ? 15u : 1u)) == 0 && tt < nb) {
+        double *q = part + (tb + tt) * 16 + pslot;
+        *q = c == wv ? s : __dadd_rn(*q, s);
       }
     }
+  }
+  if (wv >= nC && (lane & 15u) == 0) {  // waves without a chunk (H < 2048) give zeros
+    for (uint32_t t = 0; t < nt; t++) part[t * 16 + pslot] = 0.0;
+  }
+  __syncthreads();
+  const uint32_t j = threadIdx.x;
+  if (j < nt) {
+    double s = 0.0;
 #pragma unroll
-    for (uint32_t tt = 0; tt < 4; tt++) {
-      const double sum = wave_sum_f64(acc[tt]);
-      if (lane == 0 && t0 + tt < t_end) part[wv * kMaxDecodeTokens + t0 + tt] = sum;
-    }
+    for (uint32_t i = 0; i < 16; i++) s = __dadd_rn(s, part[16 * j + i]);
+    tot[j] = s;
   }
   __syncthreads();
 }
 
-// The four waves' sums of token t, in a fixed order (the shared gate's row).
-__device__ __forceinline__ float row_total4(const double *part, uint32_t t) {
-  return (float)__dadd_rn(__dadd_rn(part[t], part[kMaxDecodeTokens + t]),
-                          __dadd_rn(part[2 * kMaxDecodeTokens + t], part[3 * kMaxDecodeTokens + t]));
-}
-
-// Lead item i: router rows 2 i and 2 i + 1 (waves 2 r and 2 r + 1 take the even and odd chunks of row 2 i + r) for all
-// T tokens, plus the bias.
-__device__ __forceinline__ void router_rows(const DecodeParams &p, uint32_t item, double *part) {
-  const uint32_t r = wave_id() / 2, row = min(item * kRouteRows + r, p.E - 1);
-  row_dots(p, row, wave_id() & 1u, 2, 0, p.T, part);
-  const uint32_t j = threadIdx.x, rr = j / p.T, t = j % p.T, rw = item * kRouteRows + rr;
-  if (j < kRouteRows * p.T && rw < p.E) {
-    float l = (float)__dadd_rn(part[2 * rr * kMaxDecodeTokens + t], part[(2 * rr + 1) * kMaxDecodeTokens + t]);
-    if (p.bias) l = __fadd_rn(l, p.bias[rw]);
-    st_co(p.logits + (uint64_t)t * (p.E + 1) + rw, l);
+// Lead item i: router row i for all T tokens, plus the bias.
+__device__ __forceinline__ void router_row(const DecodeParams &p, uint32_t row, double *part, double *tot) {
+  router_dot(p, row, 0, p.T, part, tot);
+  const uint32_t t = threadIdx.x;
+  if (t < p.T) {
+    float l = (float)tot[t];
+    if (p.bias) l = __fadd_rn(l, p.bias[row]);
+    st_tag(p.logits + (uint64_t)t * (p.E + 1) + row, __float_as_uint(l), p.tag);
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Groups
+
+// The launch's groups, in LDS: each work-group builds the table itself from the routed ids (the same table in every
+// work-group), or copies a pre-routed call's from the host's.
+struct GroupTab {
+  uint32_t ng, have_w;                                 // have_w: w and gs below are filled (routed launches)
+  float w[kMaxDecodeTokens * kMaxUsed], gs[kMaxDecodeTokens];
+  int32_t slot[kMaxGroups];
+  uint32_t n[kMaxGroups];
+  uint16_t asg[kMaxGroups][MOE_GROUP_MAX];
+};
+
 // MoeGroup records from the routed ids: an expert's assignments in order, MOE_GROUP_MAX a group (as group_slots,
-// layer.cl:894-942), and the shared expert's groups; numbered by decreasing size, then by first assignment. An expert takes at
-// most one assignment a token, so a mask of the tokens that chose it gives each assignment its rank among the
-// expert's (and whether it heads a group); the heads' ballots give the group numbers. Token own's ids come from sel,
-// the others' from the coherent ids.
-__device__ __forceinline__ void make_groups(const DecodeParams &p, uint32_t own, const uint32_t *sel, uint8_t *lds, uint64_t *hb) {
+// layer.cl:894-942); numbered by decreasing size, then by first assignment. An expert takes at most one assignment a
+// token, so a mask of the tokens that chose it gives each assignment its rank among the expert's (and whether it heads
+// a group); the heads' ballots give the group numbers.
+__device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds, uint64_t *hb, GroupTab *tab) {
   const uint32_t T = p.T, K = p.K, E = p.E, n = T * K, a = threadIdx.x, lane = lane_id();
   uint32_t *ids = (uint32_t *)lds, *mask = ids + kMaxDecodeTokens * kMaxUsed, *gnum = mask + kMaxExperts;
   for (uint32_t i = a; i < E; i += kWG) mask[i] = 0u;
   const uint32_t t = a / K;
-  if (a < n) ids[a] = t == own ? sel[a % K] : (uint32_t)ld_co(p.ids + a);
+  if (a < n) {  // the routed ids and weights, polled together
+    uint64_t ri, rw;
+    for (uint32_t k = 0;; k++) {
+      ri = ld_tag(p.ids_t + a), rw = ld_tag(p.w_t + a);
+      if (tag_of(ri) == p.tag && tag_of(rw) == p.tag) break;
+      __builtin_amdgcn_s_sleep(C0VEN_POLL_SLEEP);
+      if (k == kSpinLimit) {
+        st_co(p.err, 1u);
+        break;
+      }
+    }
+    ids[a] = (uint32_t)ri;
+    tab->w[a] = __uint_as_float((uint32_t)rw);
+  }
+  if (p.has_shared && a < T) tab->gs[a] = __uint_as_float(poll_tag(p, p.gs + a));
   __syncthreads();
   uint32_t e = 0, rank = 0, total = 0;
   if (a < n) {
@@ -334,17 +439,15 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint32_t own,
   const uint64_t heads = __ballot(head);
   if (lane == 0) hb[wave_id()] = heads;
   __syncthreads();
-  uint32_t before = 0, nr = 0;
+  uint32_t before = 0, G = 0;
 #pragma unroll
   for (uint32_t w = 0; w < kWG / 64; w++) {
     const uint32_t c = (uint32_t)__popcll(hb[w]);
     before += w < wave_id() ? c : 0u;
-    nr += c;
+    G += c;
   }
-  // Groups in order of first assignment (routed, then the shared expert's) get the index o; they are numbered by
-  // decreasing size, o breaking ties, so that the heaviest groups' items come first (work-groups take items in index
-  // order).
-  const uint32_t ns = p.has_shared ? (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX : 0, G = nr + ns;
+  // Groups in order of first assignment get the index o; they are numbered by decreasing size, o breaking ties, so
+  // that the heaviest groups' items come first (work-groups take items in index order).
   uint32_t *gkey = gnum + 2 * kMaxExperts;
   uint32_t o = 0, gn = 0;
   if (head) {
@@ -352,30 +455,33 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint32_t own,
     gn = min((uint32_t)MOE_GROUP_MAX, total - rank);
     gkey[o] = (MOE_GROUP_MAX - gn) * 1024u + o;
   }
-  const uint32_t sn = a < ns ? min((uint32_t)MOE_GROUP_MAX, T - a * MOE_GROUP_MAX) : 0u;
-  if (a < ns) gkey[nr + a] = (MOE_GROUP_MAX - sn) * 1024u + nr + a;
   __syncthreads();
-  auto order = [&](uint32_t key) {
-    uint32_t r = 0;
-    for (uint32_t i = 0; i < G; i++) r += gkey[i] < key;
-    return r;
-  };
   if (head) {
-    const uint32_t g = order((MOE_GROUP_MAX - gn) * 1024u + o);
+    const uint32_t key = (MOE_GROUP_MAX - gn) * 1024u + o;
+    uint32_t g = 0;
+    for (uint32_t i = 0; i < G; i++) g += gkey[i] < key;
     gnum[2 * e + rank / MOE_GROUP_MAX] = g;
-    st_co(&p.groups[g].slot, (int32_t)e);
-    st_co(&p.groups[g].n, gn);
-  }
-  if (a < ns) {
-    MoeGroup *g = p.groups + order((MOE_GROUP_MAX - sn) * 1024u + nr + a);
-    st_co(&g->slot, (int32_t)E);
-    st_co(&g->n, sn);
-    for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
-      if (a * MOE_GROUP_MAX + j < T) st_co(g->asg + j, n + a * MOE_GROUP_MAX + j);
+    tab->slot[g] = (int32_t)e;
+    tab->n[g] = gn;
   }
   __syncthreads();
-  if (a < n) st_co(p.groups[gnum[2 * e + rank / MOE_GROUP_MAX]].asg + rank % MOE_GROUP_MAX, a);
-  if (a == 0) st_co(p.ngroups, nr + ns);
+  if (a < n) tab->asg[gnum[2 * e + rank / MOE_GROUP_MAX]][rank % MOE_GROUP_MAX] = (uint16_t)a;
+  if (a == 0) tab->ng = G, tab->have_w = 1;
+  __syncthreads();
+}
+
+// A pre-routed call's groups (written by the host before the launch) into the table.
+__device__ __forceinline__ void copy_groups(const DecodeParams &p, GroupTab *tab) {
+  const uint32_t ng = *p.ngroups;
+  for (uint32_t g = threadIdx.x; g < ng; g += kWG) {
+    const MoeGroup m = p.groups[g];
+    tab->slot[g] = m.slot;
+    tab->n[g] = m.n;
+#pragma unroll
+    for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) tab->asg[g][j] = (uint16_t)m.asg[j];
+  }
+  if (threadIdx.x == 0) tab->ng = ng, tab->have_w = 0;
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -383,14 +489,26 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint32_t own,
 
 struct GroupLds {
   int32_t slot;
-  uint32_t n, asg[MOE_GROUP_MAX], tok[MOE_GROUP_MAX];
+  uint32_t n, gid, asg[MOE_GROUP_MAX], tok[MOE_GROUP_MAX];
 };
 
-__device__ __forceinline__ void read_group(const DecodeParams &p, uint32_t g, GroupLds *s) {
-  const MoeGroup *grp = p.groups + g;
-  if (threadIdx.x == 0) s->slot = ld_co(&grp->slot), s->n = ld_co(&grp->n);
+__device__ __forceinline__ uint32_t asg_token(const DecodeParams &p, uint32_t asg) {
+  const uint32_t n = p.T * p.K;
+  return asg < n ? asg / p.K : asg - n;
+}
+
+// Group g of the table (gid g), or the shared expert's token chunk c (gid T K + c: assignments T K + 8 c + j).
+__device__ __forceinline__ void read_group(const DecodeParams &p, const GroupTab *tab, bool shared, uint32_t g,
+                                           GroupLds *s) {
+  if (threadIdx.x == 0) {
+    if (shared) {
+      s->slot = (int32_t)p.E, s->n = min((uint32_t)MOE_GROUP_MAX, p.T - MOE_GROUP_MAX * g), s->gid = p.T * p.K + g;
+    } else {
+      s->slot = tab->slot[g], s->n = tab->n[g], s->gid = g;
+    }
+  }
   if (threadIdx.x < MOE_GROUP_MAX) {
-    const uint32_t a = ld_co(grp->asg + threadIdx.x);
+    const uint32_t a = shared ? p.T * p.K + MOE_GROUP_MAX * g + threadIdx.x : tab->asg[g][threadIdx.x];
     s->asg[threadIdx.x] = a;
     s->tok[threadIdx.x] = asg_token(p, a);
   }
@@ -406,11 +524,41 @@ __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *un
   }
 }
 
-// Gate and up of rows blk * gate_up_rows .. of group g: lane = m * 32 + r * U + u; h = silu(g) * u per row.
+// h of the group's assignments quantised to the down's activation type straight into LDS: unit (j, u) at
+// (j U + u) kActLds, a half-wave a unit. The values are polled as tagged records (the gate/up items' stores are the
+// hand-off). Every down item of the group quantises the same h the same way.
+__device__ __forceinline__ void stage_h(const DecodeParams &p, const GroupLds *sg, uint32_t dact, uint32_t U,
+                                        uint8_t *lds) {
+  const uint32_t l32 = threadIdx.x & 31u;
+  for (uint32_t i = threadIdx.x / 32; i < sg->n * U; i += kWG / 32) {
+    const uint32_t j = i / U, u = i % U;
+    const uint64_t *src = p.h + (uint64_t)sg->asg[j] * p.F + u * kUnit + 8 * l32;
+    uint64_t r[8];
+    for (uint32_t n = 0;; n++) {
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < 8; k++) r[k] = ld_tag(src + k);
+#pragma unroll
+      for (int k = 0; k < 8; k++) ok &= tag_of(r[k]) == p.tag;
+      if (ok) break;
+      __builtin_amdgcn_s_sleep(C0VEN_POLL_SLEEP);
+      if (n == kSpinLimit) {
+        st_co(p.err, 1u);
+        break;
+      }
+    }
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = __uint_as_float((uint32_t)r[k]);
+    quant_unit<true>(v, l32, dact, lds + i * kActLds);
+  }
+}
+
+// Gate and up of rows blk * gate_up_rows .. of the group: lane = m * 32 + r * U + u; h = silu(g) * u per row, stored
+// as tagged records.
 template <uint32_t kTypes>
-__device__ __forceinline__ void gate_up_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
-                             GroupLds *sg, uint32_t *s_flag, const uint64_t *tab, uint64_t *mark) {
-  read_group(p, g, sg);
+__device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupLds *sg, uint32_t blk, uint8_t *lds,
+                                             uint32_t *grid_lds, const uint64_t *tab, uint64_t *mark) {
   const uint32_t U = p.H / kUnit, rows = gate_up_rows(U), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 0);
   if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
@@ -424,6 +572,9 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, uint32_t g, 
   float t[MOE_GROUP_MAX];
   pair_terms<kTypes>(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
              (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
+               // The shared expert's items run beside the router: x of their tokens is quantised by lead items
+               // 8 c .. (their flags); routed groups exist only once every lead item is in.
+               if (gm.shared && p.route) wait_flags(p, kFlagLead + sg->tok[0], n);
                stage_act(gm.shared ? p.act_s : p.act_r, sg->tok, n, U, lds);
                __syncthreads();
                if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
@@ -433,30 +584,16 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, uint32_t g, 
     if (j >= n) break;
     const float s = row_sum(t[j], U);        // gate's row sum in lanes m = 0, up's in m = 1
     const float su = __shfl_xor(s, 32, 64);  // the other matrix's
-    if (m == 0 && u == 0) st_co(p.h + (uint64_t)sg->asg[j] * p.F + row, swiglu_one(s, su, p.swiglu_limit, tab));
+    if (m == 0 && u == 0)
+      st_tag(p.h + (uint64_t)sg->asg[j] * p.F + row, __float_as_uint(swiglu_one(s, su, p.swiglu_limit, tab)), p.tag);
   }
   if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
-  // The last item of these 256 rows quantises them, one unit of the down's K per assignment, a half-wave each; the
-  // last unit of the group sets its flag.
-  const uint32_t Ud = p.F / kUnit, unit = row0 / kUnit;
-  if (!arrive_last(p.cnt_hu + (uint64_t)g * Ud + unit, kUnit / rows, s_flag)) return;
-  const uint32_t j = threadIdx.x / 32, l32 = threadIdx.x & 31u;
-  if (j < n) {
-    const float *src = p.h + (uint64_t)sg->asg[j] * p.F + unit * kUnit + 8 * l32;
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = ld_co(src + i);
-    const uint32_t dact = act_type<kTypes>(quant_vec_dot_type(group_mat(p, sg->slot, 2).type));
-    quant_unit(v, l32, dact, p.hact + ((uint64_t)sg->asg[j] * Ud + unit) * kActBytes);
-  }
-  if (arrive_last(p.cnt_hq + g, Ud, s_flag)) set_flag(p, kFlagH + g);
 }
 
-// Down rows blk * down_rows .. of group g (lane = r * U + u), then the combine of every token this item completes.
+// Down rows blk * down_rows .. of the group (lane = r * U + u), then the combine of every token this item completes.
 template <uint32_t kTypes>
-__device__ __forceinline__ void down_item(const DecodeParams &p, uint32_t g, uint32_t blk, uint8_t *lds, uint32_t *grid_lds,
-                          GroupLds *sg, uint32_t *s_last, uint64_t *mark) {
-  read_group(p, g, sg);
+__device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds *sg, const GroupTab *tab, uint32_t blk,
+                                          uint8_t *lds, uint32_t *grid_lds, uint32_t *s_last, uint64_t *mark) {
   const uint32_t U = p.F / kUnit, rows = down_rows(U), row0 = blk * rows, n = sg->n, nblk = p.H / rows;
   const GroupMat gm = group_mat(p, sg->slot, 2);
   if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
@@ -469,8 +606,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, uint32_t g, uin
   float t[MOE_GROUP_MAX];
   pair_terms<kTypes>(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
              (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
-               wait_flag(p, kFlagH + g);  // the weights are already on their way
-               stage_act(p.hact, sg->asg, n, U, lds);
+               stage_h(p, sg, act_type<kTypes>(quant_vec_dot_type(gm.type)), U, lds);
                __syncthreads();
                if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
              });
@@ -504,11 +640,16 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, uint32_t g, uin
 #pragma unroll
     for (uint32_t k = 0; k < kMaxUsed; k++) {
       on[k] = k < K && (p.route || ld_co(p.ids + tk * K + k) >= 0);
-      wv[k] = k < K ? ld_co(p.w + tk * K + k) : 0.0f;
       yv[k] = on[k] ? ld_co(p.y_asg + ((uint64_t)tk * K + k) * p.H + rr) : 0.0f;
     }
+    // The weights: from the group table where this work-group built it, else polled (a shared item that finishes a
+    // token before any routed item ran here), or a pre-routed call's.
+#pragma unroll
+    for (uint32_t k = 0; k < kMaxUsed; k++)
+      wv[k] = k >= K ? 0.0f : tab->have_w ? tab->w[tk * K + k] : p.route ? __uint_as_float(poll_tag(p, p.w_t + tk * K + k))
+                                                                    : ld_co(p.w + tk * K + k);
     const float ys = p.has_shared ? ld_co(p.y_asg + ((uint64_t)p.T * K + tk) * p.H + rr) : 0.0f;
-    const float gs = p.has_shared ? ld_co(p.gs + tk) : 0.0f;
+    const float gs = !p.has_shared ? 0.0f : tab->have_w ? tab->gs[tk] : __uint_as_float(poll_tag(p, p.gs + tk));
     float acc = 0.0f;
 #pragma unroll
     for (uint32_t k = 0; k < kMaxUsed; k++)
@@ -526,26 +667,33 @@ template <uint32_t kTypes>
 __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) moe_decode(DecodeParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ uint32_t grid_lds[512];
-  __shared__ uint32_t s_flag, s_ng, s_last[MOE_GROUP_MAX], s_sel[2 * kMaxUsed];
-  __shared__ float s_norm[2];
+  __shared__ uint32_t s_flag, s_last[MOE_GROUP_MAX];
   __shared__ uint64_t s_hb[kWG / 64];
-  __shared__ double s_part[(kWG / 64) * kMaxDecodeTokens];
+  __shared__ double s_part[kMaxDecodeTokens * 16], s_tot[kMaxDecodeTokens];
   __shared__ GroupLds sg;
+  __shared__ GroupTab gtab;
   __shared__ uint64_t exp_tab[32];  // expf's table, read at LDS latency
   if (threadIdx.x < 32) exp_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  if (threadIdx.x == 0) gtab.have_w = 0;
   __syncthreads();
   const uint32_t T = p.T, E = p.E, Ug = p.H / kUnit, Ud = p.F / kUnit;
   const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nL + nTop;
   const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud);
+  const uint32_t ns = shared_chunks(T, p.route, p.has_shared), B2 = B1 + ns * (nGU + nD);
   uint32_t ng = 0xffffffffu, end = 0xffffffffu;
   for (uint32_t it = blockIdx.x;; it += gridDim.x) {
-    if (it >= B1) {
+    if (it >= B2) {
       if (ng == 0xffffffffu) {
-        wait_flag(p, kFlagRouted);
-        if (threadIdx.x == 0) s_ng = ld_co(p.ngroups);
-        __syncthreads();
-        ng = s_ng;
-        end = B1 + ng * (nGU + nD);
+        // The routed groups: every work-group builds the table from the ids once they are all in.
+        if (p.route) {
+          make_groups(p, lds, s_hb, &gtab);
+          if (blockIdx.x == 0 && threadIdx.x == 0) st_co(p.ngroups, gtab.ng);
+        } else {
+          wait_flag(p, kFlagRouted);
+          copy_groups(p, &gtab);
+        }
+        ng = gtab.ng;
+        end = B2 + ng * (nGU + nD);
       }
       if (it >= end) break;
     }
@@ -554,7 +702,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) m
     if (it < nL) {
       if (it < T) quantise_x<kTypes>(p, it);
       if (p.route) {
-        if (it * kRouteRows < E) router_rows(p, it, s_part);
+        if (it < E) router_row(p, it, s_part, s_tot);
         if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
         set_flag(p, kFlagLead + it);
       } else if (arrive_last(p.cnt_route, nL, &s_flag)) {
@@ -563,21 +711,27 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) m
     } else if (it < B1) {
       const uint32_t t = it - nL;
       // The shared gate's logit (router row E) for this token while the lead items finish: gs = sigmoid of it.
-      row_dots(p, E, wave_id(), 4, t, t + 1, s_part);
-      if (threadIdx.x == 0) st_co(p.gs + t, sigmoid_libm(row_total4(s_part, t), exp_tab));
-      wait_flags(p, kFlagLead, nL);
+      router_dot(p, E, t, 1, s_part, s_tot);
+      if (threadIdx.x == 0) st_tag(p.gs + t, __float_as_uint(sigmoid_libm((float)s_tot[0], exp_tab)), p.tag);
       if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
-      route_token(p, t, exp_tab, s_sel, s_norm);
+      route_token(p, t, exp_tab, s_part, (uint2 *)lds);
       if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
-      if (T == 1 || arrive_last(p.cnt_topk, T, &s_flag)) {
-        make_groups(p, t, s_sel, lds, s_hb);
-        set_flag(p, kFlagRouted);
+    } else if (it < B2) {
+      const uint32_t i = it - B1;
+      if (i < ns * nGU) {
+        read_group(p, &gtab, true, i / nGU, &sg);
+        gate_up_item<kTypes>(p, &sg, i % nGU, lds, grid_lds, exp_tab, mark);
+      } else {
+        read_group(p, &gtab, true, (i - ns * nGU) / nD, &sg);
+        down_item<kTypes>(p, &sg, &gtab, (i - ns * nGU) % nD, lds, grid_lds, s_last, mark);
       }
-    } else if (it < B1 + ng * nGU) {
-      gate_up_item<kTypes>(p, (it - B1) / nGU, (it - B1) % nGU, lds, grid_lds, &sg, &s_flag, exp_tab, mark);
+    } else if (it < B2 + ng * nGU) {
+      read_group(p, &gtab, false, (it - B2) / nGU, &sg);
+      gate_up_item<kTypes>(p, &sg, (it - B2) % nGU, lds, grid_lds, exp_tab, mark);
     } else {
-      const uint32_t i = it - B1 - ng * nGU;
-      down_item<kTypes>(p, i / nD, i % nD, lds, grid_lds, &sg, s_last, mark);
+      const uint32_t i = it - B2 - ng * nGU;
+      read_group(p, &gtab, false, i / nD, &sg);
+      down_item<kTypes>(p, &sg, &gtab, i % nD, lds, grid_lds, s_last, mark);
     }
     if (mark && threadIdx.x == 0) mark[3] = __builtin_amdgcn_s_memrealtime();
     __syncthreads();

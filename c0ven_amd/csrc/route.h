@@ -39,6 +39,31 @@ __device__ __forceinline__ void route_norm(const uint32_t key[kRoutePer], uint32
   *inv_out = (float)(1.0 / sum);
 }
 
+// The softmax's max (wave-uniform) from a lane's keys.
+__device__ __forceinline__ float route_max(const uint32_t key[kRoutePer]) {
+  uint32_t mk = 0;
+#pragma unroll
+  for (int i = 0; i < kRoutePer; i++) mk = max(mk, key[i]);
+  return key_float(wave_max_u32(mk));
+}
+
+// Part `part` (0, 1 or 2) of the softmax's sum: the wave's double sum of expf(l_e - mx) over the lane slots
+// i = part, part + 3, ... (the three parts together cover every expert once).
+__device__ __forceinline__ double route_sum_part(const uint32_t key[kRoutePer], uint32_t E, uint32_t lane, uint32_t part,
+                                                 float mx, const uint64_t *tab) {
+  double acc = 0.0;
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    const uint32_t i = part + 3 * k;  // wave-uniform; the select keeps the key in a register
+    // Masks rather than a select of array elements, which the compiler would turn into an indexed (scratch) load.
+    const uint32_t m0 = 0u - (uint32_t)(part == 0), m1 = 0u - (uint32_t)(part == 1), m2 = 0u - (uint32_t)(part == 2);
+    const uint32_t kk = (key[3 * k] & m0) | (key[(3 * k + 1) % kRoutePer] & m1) | (key[(3 * k + 2) % kRoutePer] & m2);
+    const float e = expf_libm(__fsub_rn(key_float(kk), mx), tab);
+    acc = __dadd_rn(acc, i < kRoutePer && lane + 64 * i < E ? (double)e : 0.0);
+  }
+  return wave_sum_f64(acc);
+}
+
 // The top K: lane r < K receives the r-th winner's id and key. Sorts each lane's keys, largest first (ids ascending
 // within a lane, so equal keys keep the lower id first); each round takes the wave's largest head (a DPP max, a
 // ballot for equal keys, the lower id among them) and pops it. key and id are consumed.
@@ -71,6 +96,54 @@ __device__ __forceinline__ void route_select(uint32_t key[kRoutePer], uint32_t i
     }
   }
   *my_id = mi, *my_key = mk;
+}
+
+// The top K as route_select gives them (same winners, same order), by a threshold instead of K rounds: tau, the K-th
+// largest of the lanes' maxima, is found bit by bit with ballots; at least K keys are >= tau (one a lane of those K
+// lanes), so every winner is among the keys >= tau. Those candidates (usually little more than K) are packed into
+// cand (LDS, room for 64 kRoutePer + K entries) and each is ranked against all of them: rank = the number that beat it
+// (a larger key, or an equal key with a lower id). One wave runs this; key and id are kept.
+__device__ __forceinline__ void route_select_lds(const uint32_t key[kRoutePer], const uint32_t id[kRoutePer], uint32_t K,
+                                                 uint32_t lane, uint2 *cand, uint32_t *my_id, uint32_t *my_key) {
+  uint32_t m = key[0];
+#pragma unroll
+  for (int i = 1; i < kRoutePer; i++) m = max(m, key[i]);
+  uint32_t tau = 0;
+  for (int b = 31; b >= 0; b--) {
+    const uint32_t c = tau | (1u << b);
+    if ((uint32_t)__popcll(__ballot(m >= c)) >= K) tau = c;
+  }
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int i = 0; i < kRoutePer; i++) cnt += key[i] >= tau ? 1u : 0u;
+  uint32_t pos = 0, total = 0;  // this lane's first slot (the counts of the lanes below it) and the wave's count
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    const uint64_t bal = __ballot((cnt >> b) & 1u);
+    pos += __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u)) << b;
+    total += (uint32_t)__popcll(bal) << b;
+  }
+#pragma unroll
+  for (int i = 0; i < kRoutePer; i++) {
+    if (key[i] >= tau) cand[pos] = make_uint2(key[i], id[i]);
+    pos += key[i] >= tau ? 1u : 0u;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS stores are done before it reads them back
+  __builtin_amdgcn_wave_barrier();
+  uint2 *sel = cand + 64 * kRoutePer;
+  for (uint32_t j = lane; j < total; j += 64) {
+    const uint2 me = cand[j];
+    uint32_t rank = 0;
+    for (uint32_t i = 0; i < total; i++) {
+      const uint2 o = cand[i];
+      rank += (o.x > me.x) | ((o.x == me.x) & (o.y < me.y));
+    }
+    if (rank < K) sel[rank] = me;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  const uint2 w = lane < K ? sel[lane] : make_uint2(0u, 0u);
+  *my_key = w.x, *my_id = w.y;
 }
 
 // Lane r < K's renormalised weight (the whole wave takes part).
