@@ -40,6 +40,10 @@ constexpr uint32_t kMaxGroups = max_groups(kMaxDecodeTokens, kMaxUsed + 1);
 // and a sort key per group.
 constexpr uint32_t kGroupingLds =
     kMaxDecodeTokens * kMaxUsed * 4 + kMaxExperts * 4 + kMaxExperts * 2 * 4 + (kMaxDecodeTokens * kMaxUsed + 2) * 4;
+constexpr uint32_t kDynLists = 8;     // lists the routed items are dealt from (one counter each)
+constexpr uint32_t kDynStride = 64;   // words between two list counters
+// LDS after a group's activation units for the matrix-core gate/up item's exchanges (unit terms, then sums).
+constexpr uint32_t kMfmaXchBytes = (2 * 4 * 4 * 64 + 2 * 16 * 16) * 4;
 constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kWG / 64) * (32 / Ug); }
 constexpr uint32_t down_rows(uint32_t Ud) { return (kWG / 64) * (64 / Ud); }
 
@@ -84,6 +88,7 @@ struct DecodeParams {
   uint32_t *cnt_route;     // 1: lead items in (pre-routed calls)
   uint32_t *cnt_topk;      // 1: tokens routed
   uint32_t *cnt_tok;       // T x (H / down_rows): outputs in per (token, down row block)
+  uint32_t *cnt_dyn;       // 2 x kDynLists counters, kDynStride apart: the routed items' lists (alternate launches)
   uint32_t *err;           // set when a wait gave up (never, unless a work-group could not run)
   uint64_t *trace;         // null, or (start, ready, computed, end) s_memrealtime stamps per work item
   uint32_t trace_cap;

@@ -1,0 +1,132 @@
+// Q4_K weights against a group's activations on the matrix cores: 16 weight rows x 16 token columns x one unit (256
+// values) per set of v_mfma_i32_16x16x32_i8, with the same integers and fp32 steps as UnitQ4_K::term (units.h).
+//
+// Operand layout (one wave): lane l holds A row l % 16 and B column l % 16, bytes 8 g .. 8 g + 7 of each 32-value
+// block, g = l / 16; the result D[row][col] sits in lane 16 (row / 4) + col as element row % 4. Here A is the weights
+// (row = weight row) and B the activations (col = token), so lane l ends with rows 4 g + i (i < 4) of token l % 16.
+//
+// Exactness: Q4_K's sub-block scale sc_j (6 bits) is split as 8 hi + lo (3 bits each) and folded into the codes
+// (q <= 15 times at most 7 fits a byte), so one accumulating chain gives sum_j (q lo_j) . a and another
+// sum_j (q hi_j) . a: isum = 8 D_hi + D_lo, exactly the integer of the CPU path. The minimum part
+// imin = sum_j mn_j bsum_j takes two more: bsum_j = 64 hi + lo (hi in [-64, 63], lo in [0, 63]).
+#pragma once
+
+#include "device_math.h"
+#include "layout.h"
+
+namespace c0ven {
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+// Each byte of w (at most 15) times k (at most 7): two 16-bit products per word, no carry between bytes.
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t w, uint32_t k) {
+  const u16x2_t a = __builtin_bit_cast(u16x2_t, w), b = {(unsigned short)k, (unsigned short)k};
+  return __builtin_bit_cast(uint32_t, a * b);
+}
+__device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
+
+// One lane's raw bytes of a 16-row x 1-unit Q4_K tile: its A row's qs (8 bytes of each 64-value chunk) and scales,
+// and the d|dmin words of its four D rows.
+struct Q4kRaw {
+  uint2 qs[4];
+  uint32_t sc[3], dm[4];
+  // Rows row0 .. row0 + 15 (row0 a multiple of 16) of the matrix at mat (U units a row), unit u.
+  __device__ __forceinline__ void load(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
+    const uint32_t g = lane / 16, nl = kTileRows * U;
+    const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q4_K, U);
+    const uint32_t ia = ((row0 % kTileRows) + lane % 16) * U + u;
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++)
+      qs[c] = *(const uint2 *)(tile + ((uint64_t)(q4_kt::kQs / 16 + 2 * c + g / 2) * nl + ia) * 16 + 8 * (g % 2));
+#pragma unroll
+    for (uint32_t i = 0; i < 3; i++) sc[i] = *(const uint32_t *)(tile + (uint64_t)q4_kt::kScales * nl + ((uint64_t)i * nl + ia) * 4);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      const uint32_t id = ((row0 % kTileRows) + 4 * g + i) * U + u;
+      dm[i] = *(const uint32_t *)(tile + (uint64_t)q4_kt::kDm * nl + (uint64_t)id * 4);
+    }
+  }
+};
+
+// The A operands of one tile-unit and its D rows' scales.
+struct Q4kA {
+  long lo[8], hi[8], mn;
+  float d[4], dmin[4];
+  __device__ __forceinline__ void decode(const Q4kRaw &r, uint32_t lane) {
+    uint8_t b[12];
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[4 * i + j] = (uint8_t)(r.sc[i] >> (8 * j));
+    uint32_t sc[8], m[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {  // get_scale_min_k4
+      if (j < 4) {
+        sc[j] = b[j] & 63u;
+        m[j] = b[j + 4] & 63u;
+      } else {
+        sc[j] = (b[j + 4] & 0xFu) | ((b[j - 4] >> 6) << 4);
+        m[j] = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const uint32_t w0 = r.qs[c].x, w1 = r.qs[c].y;
+      const uint32_t l0 = w0 & 0x0f0f0f0fu, l1 = w1 & 0x0f0f0f0fu;
+      const uint32_t h0 = (w0 >> 4) & 0x0f0f0f0fu, h1 = (w1 >> 4) & 0x0f0f0f0fu;
+      lo[2 * c] = pack2(mul_bytes(l0, sc[2 * c] & 7u), mul_bytes(l1, sc[2 * c] & 7u));
+      hi[2 * c] = pack2(mul_bytes(l0, sc[2 * c] >> 3), mul_bytes(l1, sc[2 * c] >> 3));
+      lo[2 * c + 1] = pack2(mul_bytes(h0, sc[2 * c + 1] & 7u), mul_bytes(h1, sc[2 * c + 1] & 7u));
+      hi[2 * c + 1] = pack2(mul_bytes(h0, sc[2 * c + 1] >> 3), mul_bytes(h1, sc[2 * c + 1] >> 3));
+    }
+    const uint32_t m0 = m[0] | (m[1] << 8) | (m[2] << 16) | (m[3] << 24), m1 = m[4] | (m[5] << 8) | (m[6] << 16) | (m[7] << 24);
+    mn = lane < 16 ? pack2(m0, m1) : 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) d[i] = h2f((uint16_t)r.dm[i]), dmin[i] = h2f((uint16_t)(r.dm[i] >> 16));
+  }
+};
+
+// One lane's B operands of an activation unit (token l % 16 of the group, clamped to the last real one): the codes of
+// each 32-value block, the block sums split for the minimum part, and the unit's scale.
+struct ActB {
+  long q[8], bh, bl;
+  float ad;
+  __device__ __forceinline__ void load(const uint8_t *unit, uint32_t lane) {
+    const uint32_t g = lane / 16;
+#pragma unroll
+    for (int s = 0; s < 8; s++) q[s] = *(const long *)(unit + 32 * s + 8 * g);
+    const uint4 a = *(const uint4 *)(unit + kActSums), c = *(const uint4 *)(unit + kActSums + 16);
+    const int bs[8] = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)c.x, (int)c.y, (int)c.z, (int)c.w};
+    uint32_t h[2] = {0u, 0u}, l[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      h[j / 4] |= ((uint32_t)(bs[j] >> 6) & 0xffu) << (8 * (j % 4));
+      l[j / 4] |= ((uint32_t)bs[j] & 63u) << (8 * (j % 4));
+    }
+    bh = g == 0 ? pack2(h[0], h[1]) : 0;
+    bl = g == 0 ? pack2(l[0], l[1]) : 0;
+    ad = *(const float *)(unit + kActScales);
+  }
+};
+
+// The unit's terms t[i] (rows 4 g + i, token l % 16): fma(d ad, isum, -((dmin ad) imin)) as UnitQ4_K::term.
+__device__ __forceinline__ void q4k_terms(const Q4kA &a, const ActB &b, float t[4]) {
+  v4i_t dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.lo[s], b.q[s], dlo, 0, 0, 0);
+    dhi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.hi[s], b.q[s], dhi, 0, 0, 0);
+  }
+  const v4i_t mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.mn, b.bh, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+  const v4i_t ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.mn, b.bl, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int isum = 8 * dhi[i] + dlo[i], imin = 64 * mh[i] + ml[i];
+    const float dd = __fmul_rn(a.d[i], b.ad), dm = __fmul_rn(a.dmin[i], b.ad);
+    const float pm = __fmul_rn(dm, (float)imin);
+    t[i] = __builtin_fmaf(dd, (float)isum, -pm);
+  }
+}
+
+}  // namespace c0ven

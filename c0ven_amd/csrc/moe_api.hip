@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cstddef>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <stdexcept>
@@ -72,7 +73,7 @@ struct moe_ctx {
   int32_t *ids = nullptr;
   MoeGroup *groups = nullptr;
   uint32_t *ngroups = nullptr, *counters = nullptr, *tok_need = nullptr;
-  uint32_t *cnt_route = nullptr, *cnt_topk = nullptr, *cnt_tok = nullptr;
+  uint32_t *cnt_route = nullptr, *cnt_topk = nullptr, *cnt_tok = nullptr, *cnt_dyn = nullptr;
   uint32_t *err_flag = nullptr;
   uint64_t *flags = nullptr;
   uint64_t epoch = 0;          // the last launch's number
@@ -163,7 +164,7 @@ DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   p.h = c->h, p.y_asg = c->y_asg;
   p.flags = c->flags, p.err = c->err_flag;
   p.cnt_route = c->cnt_route, p.cnt_topk = c->cnt_topk;
-  p.cnt_tok = c->cnt_tok;
+  p.cnt_tok = c->cnt_tok, p.cnt_dyn = c->cnt_dyn;
   return p;
 }
 
@@ -187,7 +188,7 @@ void timing_hook(void *ctx, const char *name, int after, hipStream_t s) {
   }
 }
 
-// Zeroes the tagged-record buffers (tag 0 is never a launch's).
+// Zeroes the tagged-record buffers (tag 0 is never a launch's) and the list counters.
 void clear_tagged(moe_ctx *c, hipStream_t s) {
   for (const auto &b : c->tagged) check(hipMemsetAsync(b.first, 0, b.second * sizeof(uint64_t), s), "hipMemsetAsync");
 }
@@ -337,22 +338,23 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->tok_need = c->alloc<uint32_t>(T);
     c->h = c->alloc<uint64_t>((uint64_t)A * F);
     c->y_asg = c->alloc<float>((uint64_t)A * H);
-    const uint64_t ncnt = 3 + (uint64_t)T * (H / down_rows(Ud));
+    const uint64_t ncnt = 3 + (uint64_t)T * (H / down_rows(Ud)) + 2 * kDynLists * kDynStride + kDynStride;
     c->counters = c->alloc<uint32_t>(ncnt);
     check(hipMemset(c->counters, 0, ncnt * sizeof(uint32_t)), "hipMemset");
     c->cnt_route = c->counters;
     c->cnt_topk = c->cnt_route + 1;
     c->err_flag = c->cnt_topk + 1;
     c->cnt_tok = c->err_flag + 1;
+    c->cnt_dyn = c->cnt_tok + (uint64_t)T * (H / down_rows(Ud)) + kDynStride;  // (a line of its own)
     c->flags = c->alloc<uint64_t>(kFlagCount);
     check(hipMemset(c->flags, 0, kFlagCount * sizeof(uint64_t)), "hipMemset");
     c->tagged = {{c->logits, (uint64_t)T * (E + 1)}, {c->gs, T}, {c->ids_t, (uint64_t)T * K1}, {c->w_t, (uint64_t)T * K1},
-                 {c->h, (uint64_t)A * F}};
+                 {c->h, (uint64_t)A * F}, {(uint64_t *)c->cnt_dyn, kDynLists * kDynStride}};  // (and both sets of list counters)
     clear_tagged(c, nullptr);
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
-    c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * Ug * kActLds, (size_t)MOE_GROUP_MAX * Ud * kActLds,
-                               kGroupingLds});
+    c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * Ug * kActLds + (Ug == 8 ? kMfmaXchBytes : 0),
+                               (size_t)MOE_GROUP_MAX * Ud * kActLds, kGroupingLds});
     int per_cu = 0, ncu = 0;
     uint32_t types = type_bit(g.gate_type) | type_bit(g.down_type);
     if (g.has_shared) types |= type_bit(g.sh_gate_type) | type_bit(g.sh_down_type);
@@ -360,6 +362,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, c->kernel, kWG, c->lds), "occupancy");
     check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, g.device), "CU count");
     require(per_cu >= 1, "moe_decode does not fit a CU");
+    if (const char *e = std::getenv("C0VEN_DECODE_WG_PER_CU")) per_cu = std::max(1, std::min(per_cu, std::atoi(e)));
     c->grid = (uint32_t)(per_cu * ncu);
     check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     *out = c;

@@ -25,6 +25,7 @@
 #include "device_math.h"
 #include "iq3s_grid.h"
 #include "layout.h"
+#include "mfma_q4k.h"
 #include "units.h"
 
 namespace c0ven {
@@ -38,8 +39,16 @@ constexpr uint32_t kSpinLimit = 1u << 22;
 #define C0VEN_POLL_SLEEP 1
 #endif
 
-__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
-__device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
+// The thread index, read afresh where it is used: the empty asm hides that it is the same value everywhere, so the
+// compiler recomputes addresses derived from it at their use instead of hoisting them out of the item loop, where the
+// kernel's register pressure would spill them to scratch (each reload a memory round trip in a hand-off).
+__device__ __forceinline__ uint32_t tid() {
+  uint32_t t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+__device__ __forceinline__ uint32_t lane_id() { return tid() & 63u; }
+__device__ __forceinline__ uint32_t wave_id() { return tid() >> 6; }
 
 // This work-group's coherent stores are complete (every wave waits for its own, then the barrier).
 __device__ __forceinline__ void stores_done() {
@@ -52,7 +61,7 @@ __device__ __forceinline__ void stores_done() {
 // `total` (which sets the counter back to zero for the next launch).
 __device__ __forceinline__ bool arrive_last(uint32_t *cnt, uint32_t total, uint32_t *flag) {
   stores_done();
-  if (threadIdx.x == 0) {
+  if (tid() == 0) {
     const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag = old == total - 1;
     if (old == total - 1) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -64,12 +73,12 @@ __device__ __forceinline__ bool arrive_last(uint32_t *cnt, uint32_t total, uint3
 // Sets flag i to this launch's epoch once the work-group's stores are complete.
 __device__ __forceinline__ void set_flag(const DecodeParams &p, uint32_t i) {
   stores_done();
-  if (threadIdx.x == 0) st_co(p.flags + i, p.epoch);
+  if (tid() == 0) st_co(p.flags + i, p.epoch);
 }
 
 // Waits until flag i holds this launch's epoch (thread 0 polls, the work-group follows).
 __device__ __forceinline__ void wait_flag(const DecodeParams &p, uint32_t i) {
-  if (threadIdx.x == 0) {
+  if (tid() == 0) {
     uint32_t n = 0;
     while (ld_co(p.flags + i) != p.epoch) {
       __builtin_amdgcn_s_sleep(C0VEN_POLL_SLEEP);
@@ -119,6 +128,14 @@ __device__ __forceinline__ uint32_t poll_tag(const DecodeParams &p, const uint64
     v = ld_tag(q);
   }
   return (uint32_t)v;
+}
+
+// Waits (thread 0 polls, the work-group follows) until one tagged record holds this launch's tag: the cheap first
+// wait before a work-group reads a whole set of records written at about the same time (each read still checks its own
+// tag), so that hundreds of work-groups do not poll the whole set.
+__device__ __forceinline__ void wait_tag(const DecodeParams &p, const uint64_t *q) {
+  if (tid() == 0) (void)poll_tag(p, q);
+  __syncthreads();
 }
 
 // Token t's logits as order keys, lane l holding experts l + 64 i: the wave polls the tagged records until every one
@@ -202,7 +219,7 @@ __device__ __forceinline__ GroupMat group_mat(const DecodeParams &p, int32_t slo
 }
 
 __device__ __forceinline__ void load_grid(uint32_t *grid_lds) {
-  for (uint32_t i = threadIdx.x; i < 512; i += kWG) grid_lds[i] = kIq3sGridDev[i];
+  for (uint32_t i = tid(); i < 512; i += kWG) grid_lds[i] = kIq3sGridDev[i];
 }
 
 // The n terms of one (row, unit) pair against the activation units act + j * stride dwords, into t[j]. The unit's
@@ -263,8 +280,8 @@ __device__ __forceinline__ float row_sum(float t, uint32_t U) {
 // x[t] to the activation types of the routed and the shared gate: a half-wave per unit.
 template <uint32_t kTypes>
 __device__ __forceinline__ void quantise_x(const DecodeParams &p, uint32_t t) {
-  const uint32_t H = p.H, l32 = threadIdx.x & 31u;
-  for (uint32_t u = threadIdx.x / 32; u < H / kUnit; u += kWG / 32) {
+  const uint32_t H = p.H, l32 = tid() & 31u;
+  for (uint32_t u = tid() / 32; u < H / kUnit; u += kWG / 32) {
     const float4 *src = (const float4 *)(p.x + (uint64_t)t * H + u * kUnit + 8 * l32);
     const float4 a = src[0], b = src[1];
     const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -365,7 +382,7 @@ __device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, 
     for (uint32_t t = 0; t < nt; t++) part[t * 16 + pslot] = 0.0;
   }
   __syncthreads();
-  const uint32_t j = threadIdx.x;
+  const uint32_t j = tid();
   if (j < nt) {
     double s = 0.0;
 #pragma unroll
@@ -378,7 +395,7 @@ __device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, 
 // Lead item i: router row i for all T tokens, plus the bias.
 __device__ __forceinline__ void router_row(const DecodeParams &p, uint32_t row, double *part, double *tot) {
   router_dot(p, row, 0, p.T, part, tot);
-  const uint32_t t = threadIdx.x;
+  const uint32_t t = tid();
   if (t < p.T) {
     float l = (float)tot[t];
     if (p.bias) l = __fadd_rn(l, p.bias[row]);
@@ -404,10 +421,11 @@ struct GroupTab {
 // token, so a mask of the tokens that chose it gives each assignment its rank among the expert's (and whether it heads
 // a group); the heads' ballots give the group numbers.
 __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds, uint64_t *hb, GroupTab *tab) {
-  const uint32_t T = p.T, K = p.K, E = p.E, n = T * K, a = threadIdx.x, lane = lane_id();
+  const uint32_t T = p.T, K = p.K, E = p.E, n = T * K, a = tid(), lane = lane_id();
   uint32_t *ids = (uint32_t *)lds, *mask = ids + kMaxDecodeTokens * kMaxUsed, *gnum = mask + kMaxExperts;
   for (uint32_t i = a; i < E; i += kWG) mask[i] = 0u;
   const uint32_t t = a / K;
+  wait_tag(p, p.ids_t + n - 1);  // the last token's last id, then every id and weight
   if (a < n) {  // the routed ids and weights, polled together
     uint64_t ri, rw;
     for (uint32_t k = 0;; k++) {
@@ -473,14 +491,14 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds,
 // A pre-routed call's groups (written by the host before the launch) into the table.
 __device__ __forceinline__ void copy_groups(const DecodeParams &p, GroupTab *tab) {
   const uint32_t ng = *p.ngroups;
-  for (uint32_t g = threadIdx.x; g < ng; g += kWG) {
+  for (uint32_t g = tid(); g < ng; g += kWG) {
     const MoeGroup m = p.groups[g];
     tab->slot[g] = m.slot;
     tab->n[g] = m.n;
 #pragma unroll
     for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) tab->asg[g][j] = (uint16_t)m.asg[j];
   }
-  if (threadIdx.x == 0) tab->ng = ng, tab->have_w = 0;
+  if (tid() == 0) tab->ng = ng, tab->have_w = 0;
   __syncthreads();
 }
 
@@ -500,17 +518,17 @@ __device__ __forceinline__ uint32_t asg_token(const DecodeParams &p, uint32_t as
 // Group g of the table (gid g), or the shared expert's token chunk c (gid T K + c: assignments T K + 8 c + j).
 __device__ __forceinline__ void read_group(const DecodeParams &p, const GroupTab *tab, bool shared, uint32_t g,
                                            GroupLds *s) {
-  if (threadIdx.x == 0) {
+  if (tid() == 0) {
     if (shared) {
       s->slot = (int32_t)p.E, s->n = min((uint32_t)MOE_GROUP_MAX, p.T - MOE_GROUP_MAX * g), s->gid = p.T * p.K + g;
     } else {
       s->slot = tab->slot[g], s->n = tab->n[g], s->gid = g;
     }
   }
-  if (threadIdx.x < MOE_GROUP_MAX) {
-    const uint32_t a = shared ? p.T * p.K + MOE_GROUP_MAX * g + threadIdx.x : tab->asg[g][threadIdx.x];
-    s->asg[threadIdx.x] = a;
-    s->tok[threadIdx.x] = asg_token(p, a);
+  if (tid() < MOE_GROUP_MAX) {
+    const uint32_t a = shared ? p.T * p.K + MOE_GROUP_MAX * g + tid() : tab->asg[g][tid()];
+    s->asg[tid()] = a;
+    s->tok[tid()] = asg_token(p, a);
   }
   __syncthreads();
 }
@@ -518,7 +536,7 @@ __device__ __forceinline__ void read_group(const DecodeParams &p, const GroupTab
 // Activation units (act + unit index * kActBytes, coherent) of the group's assignments into LDS, kActLds apart.
 __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *unit_of_j, uint32_t n, uint32_t U,
                                           uint8_t *lds) {
-  for (uint32_t i = threadIdx.x; i < n * U * (kActBytes / 16); i += kWG) {
+  for (uint32_t i = tid(); i < n * U * (kActBytes / 16); i += kWG) {
     const uint32_t unit = i / (kActBytes / 16), c = i % (kActBytes / 16), j = unit / U, u = unit % U;
     *(uint4 *)(lds + unit * kActLds + 16 * c) = ld_co4(act + ((uint64_t)unit_of_j[j] * U + u) * kActBytes + 16 * c);
   }
@@ -529,8 +547,9 @@ __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *un
 // hand-off). Every down item of the group quantises the same h the same way.
 __device__ __forceinline__ void stage_h(const DecodeParams &p, const GroupLds *sg, uint32_t dact, uint32_t U,
                                         uint8_t *lds) {
-  const uint32_t l32 = threadIdx.x & 31u;
-  for (uint32_t i = threadIdx.x / 32; i < sg->n * U; i += kWG / 32) {
+  const uint32_t l32 = tid() & 31u;
+  wait_tag(p, p.h + (uint64_t)sg->asg[sg->n - 1] * p.F + p.F - 1);  // one record first, then all
+  for (uint32_t i = tid() / 32; i < sg->n * U; i += kWG / 32) {
     const uint32_t j = i / U, u = i % U;
     const uint64_t *src = p.h + (uint64_t)sg->asg[j] * p.F + u * kUnit + 8 * l32;
     uint64_t r[8];
@@ -554,6 +573,111 @@ __device__ __forceinline__ void stage_h(const DecodeParams &p, const GroupLds *s
   }
 }
 
+// Groups of at least this many tokens take the matrix-core paths (Q4_K weights, 8 units a gate/up row, 2 a down row);
+// smaller ones the dot4 paths, where the 16 token columns of an MFMA would be mostly padding.
+constexpr uint32_t kMfmaMinTokens = 3;
+
+template <uint32_t kTypes>
+__device__ __forceinline__ bool use_mfma(uint32_t type, uint32_t U, uint32_t U_mfma, uint32_t n) {
+  return (kTypes & kTypeQ4_K) != 0 && type == QT_Q4_K && U == U_mfma && n >= kMfmaMinTokens;
+}
+
+// Gate and up of rows 16 blk .. 16 blk + 15 on the matrix cores (U = 8). Wave w takes matrix w & 1 and units
+// 4 (w >> 1) .. + 3 of the 16 rows for all tokens (q4k_terms); the second half's unit terms go through LDS (xch) to
+// the first, which adds them to its sums in unit order (0 + t_0 + t_1 ...: the oracle's sequence). The gate and up
+// sums then go through LDS and each thread takes one (row, token): h = swiglu, stored as a tagged record.
+__device__ __forceinline__ void gate_up_mfma(const DecodeParams &p, const GroupLds *sg, const GroupMat &gm, uint32_t blk,
+                                             uint8_t *lds, float *xch, const uint64_t *tab, uint64_t *mark) {
+  constexpr uint32_t U = 8;
+  const uint32_t lane = lane_id(), w = wave_id(), m = w & 1u, half = w >> 1, n = sg->n, row0 = 16 * blk;
+  const uint8_t *mat = gm.mat + (m ? (gm.shared ? p.sh_up_off : p.ex_up_off) : 0);
+  Q4kRaw raw[4];  // all four units' weights in flight before the activations are waited for
+#pragma unroll
+  for (uint32_t k = 0; k < 4; k++) raw[k].load(mat, U, row0, 4 * half + k, lane);
+  if (gm.shared && p.route) wait_flags(p, kFlagLead + sg->tok[0], n);
+  stage_act(gm.shared ? p.act_s : p.act_r, sg->tok, n, U, lds);
+  __syncthreads();
+  if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
+  const uint32_t j = min(lane % 16, n - 1);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (uint32_t k = 0; k < 4; k++) {
+    const uint32_t u = 4 * half + k;
+    Q4kA a;
+    a.decode(raw[k], lane);
+    ActB b;
+    b.load(lds + (j * U + u) * kActLds, lane);
+    float t[4];
+    q4k_terms(a, b, t);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      if (half == 0) {
+        acc[i] = __fadd_rn(acc[i], t[i]);
+      } else {
+        xch[((m * 4 + k) * 4 + i) * 64 + lane] = t[i];
+      }
+    }
+  }
+  __syncthreads();
+  float *sums = xch + 2 * 4 * 4 * 64;  // [matrix][row][token]
+  if (half == 0) {
+#pragma unroll
+    for (uint32_t k = 0; k < 4; k++)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; i++) acc[i] = __fadd_rn(acc[i], xch[((m * 4 + k) * 4 + i) * 64 + lane]);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) sums[(m * 16 + 4 * (lane / 16) + i) * 16 + lane % 16] = acc[i];
+  }
+  __syncthreads();
+  const uint32_t r = tid() / 16, tok = tid() % 16;
+  if (tok < n) {
+    const float g = sums[r * 16 + tok], up = sums[(16 + r) * 16 + tok];
+    st_tag(p.h + (uint64_t)sg->asg[tok] * p.F + row0 + r, __float_as_uint(swiglu_one(g, up, p.swiglu_limit, tab)), p.tag);
+  }
+  if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
+}
+
+// Down rows 128 blk .. 128 blk + 127 on the matrix cores (U = 2): wave w takes rows 32 w .. + 31 as two 16-row tiles,
+// both units in order; each lane stores its rows 4 g + i of token l % 16.
+__device__ __forceinline__ void down_mfma(const DecodeParams &p, const GroupLds *sg, const GroupMat &gm, uint32_t blk,
+                                          uint8_t *lds, uint64_t *mark) {
+  constexpr uint32_t U = 2;
+  const uint32_t lane = lane_id(), n = sg->n, row0 = 128 * blk + 32 * wave_id();
+  Q4kRaw raw[2][U];  // every tile-unit's weights in flight before h is waited for
+#pragma unroll
+  for (uint32_t tt = 0; tt < 2; tt++)
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) raw[tt][u].load(gm.mat, U, row0 + 16 * tt, u, lane);
+  stage_h(p, sg, QT_Q8_K, U, lds);
+  __syncthreads();
+  if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
+  const uint32_t j = min(lane % 16, n - 1);
+  float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+  for (uint32_t u = 0; u < U; u++) {
+    ActB b;
+    b.load(lds + (j * U + u) * kActLds, lane);
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; tt++) {
+      Q4kA a;
+      a.decode(raw[tt][u], lane);
+      float t[4];
+      q4k_terms(a, b, t);
+#pragma unroll
+      for (uint32_t i = 0; i < 4; i++) acc[tt][i] = __fadd_rn(acc[tt][i], t[i]);
+    }
+  }
+  const uint32_t tok = lane % 16;
+  if (tok < n) {
+    float *dst = p.y_asg + (uint64_t)sg->asg[tok] * p.H + row0 + 4 * (lane / 16);
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; tt++)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; i++) st_co(dst + 16 * tt + i, acc[tt][i]);
+  }
+  if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
+}
+
 // Gate and up of rows blk * gate_up_rows .. of the group: lane = m * 32 + r * U + u; h = silu(g) * u per row, stored
 // as tagged records.
 template <uint32_t kTypes>
@@ -561,6 +685,10 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
                                              uint32_t *grid_lds, const uint64_t *tab, uint64_t *mark) {
   const uint32_t U = p.H / kUnit, rows = gate_up_rows(U), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 0);
+  if (use_mfma<kTypes>(gm.type, U, 8, n)) {
+    gate_up_mfma(p, sg, gm, blk, lds, (float *)(lds + MOE_GROUP_MAX * U * kActLds), tab, mark);
+    return;
+  }
   if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
     load_grid(grid_lds);
     __syncthreads();
@@ -577,7 +705,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
                if (gm.shared && p.route) wait_flags(p, kFlagLead + sg->tok[0], n);
                stage_act(gm.shared ? p.act_s : p.act_r, sg->tok, n, U, lds);
                __syncthreads();
-               if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
+               if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
              });
 #pragma unroll
   for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
@@ -587,7 +715,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
     if (m == 0 && u == 0)
       st_tag(p.h + (uint64_t)sg->asg[j] * p.F + row, __float_as_uint(swiglu_one(s, su, p.swiglu_limit, tab)), p.tag);
   }
-  if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
+  if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
 }
 
 // Down rows blk * down_rows .. of the group (lane = r * U + u), then the combine of every token this item completes.
@@ -596,35 +724,39 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
                                           uint8_t *lds, uint32_t *grid_lds, uint32_t *s_last, uint64_t *mark) {
   const uint32_t U = p.F / kUnit, rows = down_rows(U), row0 = blk * rows, n = sg->n, nblk = p.H / rows;
   const GroupMat gm = group_mat(p, sg->slot, 2);
-  if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
-    load_grid(grid_lds);
-    __syncthreads();
-  }
-  const uint32_t lane = lane_id(), r = lane / U, u = lane % U;
-  const uint32_t row = row0 + wave_id() * (64 / U) + r;
-  const uint8_t *tile = gm.mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
-  float t[MOE_GROUP_MAX];
-  pair_terms<kTypes>(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
-             (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
-               stage_h(p, sg, act_type<kTypes>(quant_vec_dot_type(gm.type)), U, lds);
-               __syncthreads();
-               if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
-             });
+  if (use_mfma<kTypes>(gm.type, U, 2, n)) {
+    down_mfma(p, sg, gm, blk, lds, mark);
+  } else {
+    if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
+      load_grid(grid_lds);
+      __syncthreads();
+    }
+    const uint32_t lane = lane_id(), r = lane / U, u = lane % U;
+    const uint32_t row = row0 + wave_id() * (64 / U) + r;
+    const uint8_t *tile = gm.mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
+    float t[MOE_GROUP_MAX];
+    pair_terms<kTypes>(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
+               (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
+                 stage_h(p, sg, act_type<kTypes>(quant_vec_dot_type(gm.type)), U, lds);
+                 __syncthreads();
+                 if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
+               });
 #pragma unroll
-  for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
-    if (j >= n) break;
-    const float s = row_sum(t[j], U);
-    if (u == 0) st_co(p.y_asg + (uint64_t)sg->asg[j] * p.H + row, s);
+    for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
+      if (j >= n) break;
+      const float s = row_sum(t[j], U);
+      if (u == 0) st_co(p.y_asg + (uint64_t)sg->asg[j] * p.H + row, s);
+    }
+    if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
   }
-  if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
   // Count this item's outputs in, one counter per (token, row block), all at once.
   stores_done();
-  if (threadIdx.x < n) {
-    const uint32_t tk = sg->tok[threadIdx.x];
+  if (tid() < n) {
+    const uint32_t tk = sg->tok[tid()];
     const uint32_t need = p.tok_need ? p.tok_need[tk] : p.K + (p.has_shared ? 1u : 0u);
     uint32_t *cnt = p.cnt_tok + (uint64_t)tk * nblk + blk;
     const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last[threadIdx.x] = old == need - 1;
+    s_last[tid()] = old == need - 1;
     if (old == need - 1) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
@@ -633,7 +765,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
   uint32_t done[MOE_GROUP_MAX], nd = 0;
   for (uint32_t j = 0; j < n; j++)
     if (s_last[j]) done[nd++] = sg->tok[j];
-  for (uint32_t i = threadIdx.x; i < nd * rows; i += kWG) {
+  for (uint32_t i = tid(); i < nd * rows; i += kWG) {
     const uint32_t tk = done[i / rows], rr = row0 + i % rows, K = p.K;
     float yv[kMaxUsed], wv[kMaxUsed];
     bool on[kMaxUsed];
@@ -664,7 +796,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
 // Grid: the work-groups of 256 the device holds at once; dynamic LDS: the larger of a group's activation units
 // (MOE_GROUP_MAX x units x kActLds) and the grouping's tables (kGroupingLds).
 template <uint32_t kTypes>
-__global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) moe_decode(DecodeParams p) {
+__global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) moe_decode(DecodeParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ uint32_t grid_lds[512];
   __shared__ uint32_t s_flag, s_last[MOE_GROUP_MAX];
@@ -673,37 +805,53 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) m
   __shared__ GroupLds sg;
   __shared__ GroupTab gtab;
   __shared__ uint64_t exp_tab[32];  // expf's table, read at LDS latency
-  if (threadIdx.x < 32) exp_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
-  if (threadIdx.x == 0) gtab.have_w = 0;
+  if (tid() < 32) exp_tab[tid()] = kExp2Tab[tid()];
+  if (tid() == 0) gtab.have_w = 0;
   __syncthreads();
   const uint32_t T = p.T, E = p.E, Ug = p.H / kUnit, Ud = p.F / kUnit;
   const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nL + nTop;
   const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud);
   const uint32_t ns = shared_chunks(T, p.route, p.has_shared), B2 = B1 + ns * (nGU + nD);
-  uint32_t ng = 0xffffffffu, end = 0xffffffffu;
-  for (uint32_t it = blockIdx.x;; it += gridDim.x) {
-    if (it >= B2) {
-      if (ng == 0xffffffffu) {
-        // The routed groups: every work-group builds the table from the ids once they are all in.
-        if (p.route) {
-          make_groups(p, lds, s_hb, &gtab);
-          if (blockIdx.x == 0 && threadIdx.x == 0) st_co(p.ngroups, gtab.ng);
-        } else {
-          wait_flag(p, kFlagRouted);
-          copy_groups(p, &gtab);
-        }
-        ng = gtab.ng;
-        end = B2 + ng * (nGU + nD);
+  // Items below B2 go round-robin (work-group b takes b, b + grid, ...). The routed items, whose cost varies with their
+  // group's size, are handed out dynamically: item B2 + x + kDynLists k is the k-th of list x, and the work-groups with
+  // blockIdx % kDynLists == x take list x's items in order from its counter (one counter a list keeps the atomics
+  // spread; each on a line of its own). A work-group asks for its next item while it runs the current one.
+  uint32_t *dyn = p.cnt_dyn + (p.epoch & 1u) * kDynLists * kDynStride;
+  if (blockIdx.x == 0 && tid() < kDynLists)
+    p.cnt_dyn[(((p.epoch + 1) & 1u) * kDynLists + tid()) * kDynStride] = 0u;
+  const uint32_t list = blockIdx.x % kDynLists;
+  uint32_t ng = 0xffffffffu, end = 0xffffffffu, grab = 0;
+  bool dynamic = false;
+  for (uint32_t it = blockIdx.x;;) {
+    if (!dynamic && it >= B2) {
+      dynamic = true;
+      if (tid() == 0) grab = __hip_atomic_fetch_add(dyn + list * kDynStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // The routed groups: every work-group builds the table from the ids once they are all in.
+      if (p.route) {
+        make_groups(p, lds, s_hb, &gtab);
+        if (blockIdx.x == 0 && tid() == 0) st_co(p.ngroups, gtab.ng);
+      } else {
+        wait_flag(p, kFlagRouted);
+        copy_groups(p, &gtab);
       }
+      ng = gtab.ng;
+      end = B2 + ng * (nGU + nD);
+      if (tid() == 0) s_flag = grab;
+      __syncthreads();
+      it = B2 + list + kDynLists * s_flag;
+      __syncthreads();
+    }
+    if (dynamic) {
       if (it >= end) break;
+      if (tid() == 0) grab = __hip_atomic_fetch_add(dyn + list * kDynStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     uint64_t *mark = p.trace && it < p.trace_cap ? p.trace + 4 * it : nullptr;
-    if (mark && threadIdx.x == 0) mark[0] = mark[1] = mark[2] = __builtin_amdgcn_s_memrealtime();
+    if (mark && tid() == 0) mark[0] = mark[1] = mark[2] = __builtin_amdgcn_s_memrealtime();
     if (it < nL) {
       if (it < T) quantise_x<kTypes>(p, it);
       if (p.route) {
         if (it < E) router_row(p, it, s_part, s_tot);
-        if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
+        if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
         set_flag(p, kFlagLead + it);
       } else if (arrive_last(p.cnt_route, nL, &s_flag)) {
         set_flag(p, kFlagRouted);
@@ -712,10 +860,10 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) m
       const uint32_t t = it - nL;
       // The shared gate's logit (router row E) for this token while the lead items finish: gs = sigmoid of it.
       router_dot(p, E, t, 1, s_part, s_tot);
-      if (threadIdx.x == 0) st_tag(p.gs + t, __float_as_uint(sigmoid_libm((float)s_tot[0], exp_tab)), p.tag);
-      if (mark && threadIdx.x == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
+      if (tid() == 0) st_tag(p.gs + t, __float_as_uint(sigmoid_libm((float)s_tot[0], exp_tab)), p.tag);
+      if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
       route_token(p, t, exp_tab, s_part, (uint2 *)lds);
-      if (mark && threadIdx.x == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
+      if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
     } else if (it < B2) {
       const uint32_t i = it - B1;
       if (i < ns * nGU) {
@@ -733,7 +881,14 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(2))) m
       read_group(p, &gtab, false, i / nD, &sg);
       down_item<kTypes>(p, &sg, &gtab, i % nD, lds, grid_lds, s_last, mark);
     }
-    if (mark && threadIdx.x == 0) mark[3] = __builtin_amdgcn_s_memrealtime();
+    if (mark && tid() == 0) mark[3] = __builtin_amdgcn_s_memrealtime();
+    if (dynamic) {
+      if (tid() == 0) s_flag = grab;
+      __syncthreads();
+      it = B2 + list + kDynLists * s_flag;
+    } else {
+      it += gridDim.x;
+    }
     __syncthreads();
   }
 }
