@@ -11,6 +11,7 @@
 #include "device_math.h"
 #include "iq3s_grid.h"
 #include "layout.h"
+#include "mfma_q4k.h"
 #include "prefill.h"
 #include "route.h"
 
@@ -25,8 +26,15 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kPfWG = 256;
 
-__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
-__device__ __forceinline__ uint32_t wave_id() { return threadIdx.x >> 6; }
+// The thread index, read afresh where it is used (the empty asm hides that it is the same value everywhere), so the
+// compiler recomputes what derives from it at the use instead of hoisting it out of the loops and spilling it.
+__device__ __forceinline__ uint32_t tid_fresh() {
+  uint32_t t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+__device__ __forceinline__ uint32_t lane_id() { return tid_fresh() & 63u; }
+__device__ __forceinline__ uint32_t wave_id() { return tid_fresh() >> 6; }
 
 // ---------------------------------------------------------------------------------------------------------------
 // Activation units: one half-wave per (row, unit), eight values a lane; o2 (a second type) may be null.
@@ -44,62 +52,113 @@ __global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Router: a 64-token x 64-row tile a work-group, 4 x 4 outputs a thread, K in chunks of 32 staged as doubles.
+// Router: a 64-token x 64-row tile per work-group (rows < E) on the fp64 matrix cores. v_mfma_f64_16x16x4_f64 adds its
+// four k terms to the accumulator one fused multiply-add after another in k order (checked against the fma chain), so
+// a chain of them over k = 0, 4, 8, ... is the oracle's sum term for term. Wave w takes rows 32 (w % 2) .. and tokens
+// 32 (w / 2) .. as 2 x 2 tiles of 16 x 16. K goes in chunks of 32 staged as doubles in two LDS buffers: chunk c + 1 is
+// loaded into registers while chunk c is used, and stored to the other buffer after it (one barrier a chunk). The
+// shared gate's row E takes an extra row of work-groups: a thread a token, k ascending.
 // logits[t][e] = (float)(sum over k ascending of bf16(W[e][k]) bf16(x[t][k]), each product exact, in fp64)
-// (+ bias[e] for e < E): the oracle's sum, term for term.
+// (+ bias[e] for e < E).
 
-constexpr uint32_t kRtK = 32;
+constexpr uint32_t kRtK = 32, kRtPad = 66;  // the padded row of a staged k (doubles): the four k of a step fall apart
+
+typedef double v4d_t __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(kPfWG) pf_router(const float *x, uint32_t T, const uint16_t *W, const float *bias,
                                                    uint32_t E, uint32_t H, float *logits) {
-  __shared__ double xs[kRtK][64], ws[kRtK][64];
+  __shared__ double xs[2][kRtK][kRtPad], ws[2][kRtK][kRtPad];
   const uint32_t t0 = blockIdx.x * 64, e0 = blockIdx.y * 64, tid = threadIdx.x;
-  const uint32_t tx = tid % 16, ty = tid / 16;  // rows 4 tx .., tokens 4 ty ..
-  const uint32_t sr = tid / 4, sk = 8 * (tid % 4);  // staging: row / token sr, values sk .. sk + 7
-  double acc[4][4];
+  if (e0 >= E) {  // the gate row: thread t of the first 64 a token
+    double *wrow = &ws[0][0][0];  // W[E] as doubles, 2048 a pass
+    const uint32_t t = t0 + tid;
+    double acc = 0.0;
+    for (uint32_t k0 = 0; k0 < H; k0 += 2048) {
+      const uint32_t nk = min(2048u, H - k0);
+      __syncthreads();
+      for (uint32_t k = tid; k < nk; k += kPfWG) wrow[k] = (double)bf2f(W[(uint64_t)E * H + k0 + k]);
+      __syncthreads();
+      if (tid < 64 && t < T) {
+        const float4 *xr = (const float4 *)(x + (uint64_t)t * H + k0);
+        for (uint32_t k = 0; k < nk; k += 32) {
+          float4 q[8];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+          for (int i = 0; i < 8; i++) q[i] = xr[k / 4 + i];
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = 0.0;
-  for (uint32_t k0 = 0; k0 < H; k0 += kRtK) {
-    float xv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    uint4 wv = make_uint4(0, 0, 0, 0);
+          for (int i = 0; i < 8; i++) {
+            acc = __builtin_fma(wrow[k + 4 * i], (double)round_bf16(q[i].x), acc);
+            acc = __builtin_fma(wrow[k + 4 * i + 1], (double)round_bf16(q[i].y), acc);
+            acc = __builtin_fma(wrow[k + 4 * i + 2], (double)round_bf16(q[i].z), acc);
+            acc = __builtin_fma(wrow[k + 4 * i + 3], (double)round_bf16(q[i].w), acc);
+          }
+        }
+      }
+    }
+    if (tid < 64 && t < T) logits[(uint64_t)t * (E + 1) + E] = (float)acc;
+    return;
+  }
+  const uint32_t l = lane_id(), w = wave_id(), g = l / 16, c16 = l % 16;
+  const uint32_t rb = 32 * (w % 2), tb = 32 * (w / 2);  // the wave's rows and tokens within the tile
+  const uint32_t sr = tid / 4, sk = 8 * (tid % 4);      // staging: row / token sr, values sk .. sk + 7
+  v4d_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = v4d_t{0.0, 0.0, 0.0, 0.0};
+  float xv[8];
+  uint4 wv;
+  auto fetch = [&](uint32_t k0) {
     if (t0 + sr < T) {
       const float4 *p = (const float4 *)(x + (uint64_t)(t0 + sr) * H + k0 + sk);
       const float4 a = p[0], b = p[1];
       xv[0] = a.x, xv[1] = a.y, xv[2] = a.z, xv[3] = a.w, xv[4] = b.x, xv[5] = b.y, xv[6] = b.z, xv[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) xv[i] = 0.0f;
     }
-    if (e0 + sr <= E) wv = *(const uint4 *)(W + (uint64_t)(e0 + sr) * H + k0 + sk);
+    wv = e0 + sr < E ? *(const uint4 *)(W + (uint64_t)(e0 + sr) * H + k0 + sk) : make_uint4(0, 0, 0, 0);
+  };
+  auto stage = [&](uint32_t buf) {
     const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      xs[sk + i][sr] = (double)round_bf16(xv[i]);
-      ws[sk + i][sr] = (double)__uint_as_float((i & 1) ? ww[i / 2] & 0xffff0000u : ww[i / 2] << 16);
+      xs[buf][sk + i][sr] = (double)round_bf16(xv[i]);
+      ws[buf][sk + i][sr] = (double)__uint_as_float((i & 1) ? ww[i / 2] & 0xffff0000u : ww[i / 2] << 16);
     }
-    __syncthreads();
-#pragma unroll 8
-    for (uint32_t k = 0; k < kRtK; k++) {
-      double a[4], b[4];
+  };
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (uint32_t k0 = 0, c = 0; k0 < H; k0 += kRtK, c ^= 1u) {
+    const bool more = k0 + kRtK < H;
+    if (more) fetch(k0 + kRtK);
 #pragma unroll
-      for (int i = 0; i < 4; i++) a[i] = xs[k][4 * ty + i], b[i] = ws[k][4 * tx + i];
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_fma(b[j], a[i], acc[i][j]);
+    for (uint32_t s = 0; s < kRtK / 4; s++) {
+      const uint32_t k = 4 * s + g;
+      const double a0 = ws[c][k][rb + c16], a1 = ws[c][k][rb + 16 + c16];
+      const double b0 = xs[c][k][tb + c16], b1 = xs[c][k][tb + 16 + c16];
+      acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
     }
+    if (more) stage(c ^ 1u);
     __syncthreads();
   }
+  // acc[i][j][q]: row rb + 16 i + g + 4 q, token tb + 16 j + c16.
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t t = t0 + 4 * ty + i, e = e0 + 4 * tx + j;
-      if (t < T && e <= E) {
-        float l = (float)acc[i][j];
-        if (e < E && bias) l = __fadd_rn(l, bias[e]);
-        logits[(uint64_t)t * (E + 1) + e] = l;
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t t = t0 + tb + 16 * j + c16, e = e0 + rb + 16 * i + g + 4 * q;
+        if (t < T && e < E) {
+          float lg = (float)acc[i][j][q];
+          if (bias) lg = __fadd_rn(lg, bias[e]);
+          logits[(uint64_t)t * (E + 1) + e] = lg;
+        }
       }
-    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -263,9 +322,9 @@ struct SliceQ4_K {
   __device__ __forceinline__ v4i words_times(int j, uint32_t k) const {
     const uint4 v = q[j / 2];
     const int s = 4 * (j & 1);
-    v4i r;
-    r[0] = (int)(((v.x >> s) & 0x0f0f0f0fu) * k), r[1] = (int)(((v.y >> s) & 0x0f0f0f0fu) * k);
-    r[2] = (int)(((v.z >> s) & 0x0f0f0f0fu) * k), r[3] = (int)(((v.w >> s) & 0x0f0f0f0fu) * k);
+    v4i r;  // two 16-bit products a word (v_pk_mul_lo_u16, full rate)
+    r[0] = (int)mul_bytes((v.x >> s) & 0x0f0f0f0fu, k), r[1] = (int)mul_bytes((v.y >> s) & 0x0f0f0f0fu, k);
+    r[2] = (int)mul_bytes((v.z >> s) & 0x0f0f0f0fu, k), r[3] = (int)mul_bytes((v.w >> s) & 0x0f0f0f0fu, k);
     return r;
   }
 };
@@ -442,8 +501,9 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
     const uint8_t *buf = abuf[u & 1];
     // This lane's A rows (positions n, 32 + n; its half of each block), and the base of the scales of the positions
     // its results belong to (32 b + 8 (r / 4) + 4 h + r % 4): every LDS read below is a base plus a constant offset.
-    const uint8_t *arow0 = buf + n * kActLds + 16 * h, *arow1 = arow0 + 32 * kActLds;
-    const uint8_t *mbase = buf + 4 * h * kActLds + kActScales;
+    const uint32_t lf = lane_id(), hf = lf / 32, nf = lf % 32;  // (fresh: see tid_fresh)
+    const uint8_t *arow0 = buf + nf * kActLds + 16 * hf, *arow1 = arow0 + 32 * kActLds;
+    const uint8_t *mbase = buf + 4 * hf * kActLds + kActScales;
     if constexpr (kType == QT_Q8_0) {
 #pragma unroll
       for (int b = 0; b < 2; b++) {
@@ -668,7 +728,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
   }
   {
     HookScope k(hook, "pf_router", st);
-    pf_router<<<dim3((T + 63) / 64, (E + 1 + 63) / 64), kPfWG, 0, st>>>(x, T, L.router, L.bias, E, H, b.logits);
+    pf_router<<<dim3((T + 63) / 64, (E + 63) / 64 + 1), kPfWG, 0, st>>>(x, T, L.router, L.bias, E, H, b.logits);
   }
   {
     HookScope k(hook, "pf_topk", st);
