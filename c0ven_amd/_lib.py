@@ -230,9 +230,9 @@ class MoeBlock:
 
     def trace(self):
         """The last forward's (start, ready, computed, end) s_memrealtime stamps (100 MHz) per work item, and where
-        the lead (router), top-k, shared gate/up, shared down, gate/up and down items begin (plus the end)."""
+        the lead (router), top-k, shared gate/up, shared down, gate/up, down and combine items begin (plus the end)."""
         n = C.c_uint32()
-        bounds = np.zeros(7, dtype=np.uint32)
+        bounds = np.zeros(8, dtype=np.uint32)
         self._check(lib.moe_trace(self.h, None, 0, C.byref(n), _ptr(bounds)))
         out = np.zeros((n.value, 4), dtype=np.uint64)
         self._check(lib.moe_trace(self.h, _ptr(out), n.value, C.byref(n), _ptr(bounds)))

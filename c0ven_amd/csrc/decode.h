@@ -23,7 +23,8 @@ constexpr uint32_t max_groups(uint32_t T, uint32_t K) { return T * K + (T + MOE_
 //   shared items     (when routing with a shared expert) the shared expert's gate/up then down items, for each chunk
 //                    of MOE_GROUP_MAX tokens: they need no routing, so they run beside the router;
 //   gate/up items    gate_up_rows(U) rows of gate and of up of one routed group, all units (lane = m * 32 + r * U + u);
-//   down items       down_rows(U_down) rows of down of one routed group (lane = r * U_down + u).
+//   down items       down_rows(U_down) rows of down of one routed group (lane = r * U_down + u);
+//   combine items    one a (token, down row block): the token's outputs summed in rank order (after all down items).
 constexpr uint32_t kWG = 256;
 constexpr uint32_t kRouteRows = 1;
 constexpr uint32_t lead_items(uint32_t T, uint32_t E, uint32_t route) {
@@ -83,11 +84,10 @@ struct DecodeParams {
   MoeGroup *groups;
   uint32_t *ngroups;
   uint64_t *h;             // (T K + T) x F tagged records: SwiGLU of each assignment, fp32
-  float *y_asg;            // (T K + T) x H: each assignment's expert output
+  uint64_t *y_asg;         // (T K + T) x H tagged records: each assignment's expert output
   uint64_t *flags;         // kFlagH + G
   uint32_t *cnt_route;     // 1: lead items in (pre-routed calls)
   uint32_t *cnt_topk;      // 1: tokens routed
-  uint32_t *cnt_tok;       // T x (H / down_rows): outputs in per (token, down row block)
   uint32_t *cnt_dyn;       // 2 x kDynLists counters, kDynStride apart: the routed items' lists (alternate launches)
   uint32_t *err;           // set when a wait gave up (never, unless a work-group could not run)
   uint64_t *trace;         // null, or (start, ready, computed, end) s_memrealtime stamps per work item

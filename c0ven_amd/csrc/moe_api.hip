@@ -68,12 +68,12 @@ struct moe_ctx {
   int32_t *ids_stage = nullptr;
   // Scratch.
   uint8_t *act_r = nullptr, *act_s = nullptr;
-  float *w = nullptr, *y_asg = nullptr;
-  uint64_t *logits = nullptr, *gs = nullptr, *h = nullptr, *ids_t = nullptr, *w_t = nullptr;  // tagged records
+  float *w = nullptr;
+  uint64_t *y_asg = nullptr, *logits = nullptr, *gs = nullptr, *h = nullptr, *ids_t = nullptr, *w_t = nullptr;  // tagged records
   int32_t *ids = nullptr;
   MoeGroup *groups = nullptr;
   uint32_t *ngroups = nullptr, *counters = nullptr, *tok_need = nullptr;
-  uint32_t *cnt_route = nullptr, *cnt_topk = nullptr, *cnt_tok = nullptr, *cnt_dyn = nullptr;
+  uint32_t *cnt_route = nullptr, *cnt_topk = nullptr, *cnt_dyn = nullptr;
   uint32_t *err_flag = nullptr;
   uint64_t *flags = nullptr;
   uint64_t epoch = 0;          // the last launch's number
@@ -164,7 +164,7 @@ DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   p.h = c->h, p.y_asg = c->y_asg;
   p.flags = c->flags, p.err = c->err_flag;
   p.cnt_route = c->cnt_route, p.cnt_topk = c->cnt_topk;
-  p.cnt_tok = c->cnt_tok, p.cnt_dyn = c->cnt_dyn;
+  p.cnt_dyn = c->cnt_dyn;
   return p;
 }
 
@@ -337,19 +337,18 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->ngroups = c->alloc<uint32_t>(1);
     c->tok_need = c->alloc<uint32_t>(T);
     c->h = c->alloc<uint64_t>((uint64_t)A * F);
-    c->y_asg = c->alloc<float>((uint64_t)A * H);
-    const uint64_t ncnt = 3 + (uint64_t)T * (H / down_rows(Ud)) + 2 * kDynLists * kDynStride + kDynStride;
+    c->y_asg = c->alloc<uint64_t>((uint64_t)A * H);
+    const uint64_t ncnt = 3 + 2 * kDynLists * kDynStride + kDynStride;
     c->counters = c->alloc<uint32_t>(ncnt);
     check(hipMemset(c->counters, 0, ncnt * sizeof(uint32_t)), "hipMemset");
     c->cnt_route = c->counters;
     c->cnt_topk = c->cnt_route + 1;
     c->err_flag = c->cnt_topk + 1;
-    c->cnt_tok = c->err_flag + 1;
-    c->cnt_dyn = c->cnt_tok + (uint64_t)T * (H / down_rows(Ud)) + kDynStride;  // (a line of its own)
+    c->cnt_dyn = c->err_flag + kDynStride;  // (a line of its own)
     c->flags = c->alloc<uint64_t>(kFlagCount);
     check(hipMemset(c->flags, 0, kFlagCount * sizeof(uint64_t)), "hipMemset");
     c->tagged = {{c->logits, (uint64_t)T * (E + 1)}, {c->gs, T}, {c->ids_t, (uint64_t)T * K1}, {c->w_t, (uint64_t)T * K1},
-                 {c->h, (uint64_t)A * F}, {(uint64_t *)c->cnt_dyn, kDynLists * kDynStride}};  // (and both sets of list counters)
+                 {c->h, (uint64_t)A * F}, {c->y_asg, (uint64_t)A * H}, {(uint64_t *)c->cnt_dyn, kDynLists * kDynStride}};  // (and both sets of list counters)
     clear_tagged(c, nullptr);
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
@@ -590,8 +589,8 @@ MOE_API moe_status moe_trace(moe_ctx *c, uint64_t *stamps, uint32_t cap, uint32_
     const uint32_t nL = lead_items(T, g.n_expert, c->last_route), ns = shared_chunks(T, c->last_route, g.has_shared);
     const uint32_t nGU = g.n_ff / gate_up_rows(Ug), nD = g.n_embd / down_rows(Ud);
     const uint32_t b1 = nL + (c->last_route ? T : 0), b2 = b1 + ns * nGU, b3 = b2 + ns * nD, b4 = b3 + ng * nGU;
-    const uint32_t end = b4 + ng * nD;
-    const uint32_t bb[7] = {0, nL, b1, b2, b3, b4, end};
+    const uint32_t b5 = b4 + ng * nD, end = b5 + T * nD;
+    const uint32_t bb[8] = {0, nL, b1, b2, b3, b4, b5, end};
     if (bounds) std::memcpy(bounds, bb, sizeof bb);
     *n = std::min(end, c->trace_cap);
     if (stamps)

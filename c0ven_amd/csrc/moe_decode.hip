@@ -669,11 +669,11 @@ __device__ __forceinline__ void down_mfma(const DecodeParams &p, const GroupLds 
   }
   const uint32_t tok = lane % 16;
   if (tok < n) {
-    float *dst = p.y_asg + (uint64_t)sg->asg[tok] * p.H + row0 + 4 * (lane / 16);
+    uint64_t *dst = p.y_asg + (uint64_t)sg->asg[tok] * p.H + row0 + 4 * (lane / 16);
 #pragma unroll
     for (uint32_t tt = 0; tt < 2; tt++)
 #pragma unroll
-      for (uint32_t i = 0; i < 4; i++) st_co(dst + 16 * tt + i, acc[tt][i]);
+      for (uint32_t i = 0; i < 4; i++) st_tag(dst + 16 * tt + i, __float_as_uint(acc[tt][i]), p.tag);
   }
   if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
 }
@@ -720,9 +720,9 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
 
 // Down rows blk * down_rows .. of the group (lane = r * U + u), then the combine of every token this item completes.
 template <uint32_t kTypes>
-__device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds *sg, const GroupTab *tab, uint32_t blk,
-                                          uint8_t *lds, uint32_t *grid_lds, uint32_t *s_last, uint64_t *mark) {
-  const uint32_t U = p.F / kUnit, rows = down_rows(U), row0 = blk * rows, n = sg->n, nblk = p.H / rows;
+__device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds *sg, uint32_t blk, uint8_t *lds,
+                                          uint32_t *grid_lds, uint64_t *mark) {
+  const uint32_t U = p.F / kUnit, rows = down_rows(U), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 2);
   if (use_mfma<kTypes>(gm.type, U, 2, n)) {
     down_mfma(p, sg, gm, blk, lds, mark);
@@ -745,50 +745,61 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
     for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
       if (j >= n) break;
       const float s = row_sum(t[j], U);
-      if (u == 0) st_co(p.y_asg + (uint64_t)sg->asg[j] * p.H + row, s);
+      if (u == 0) st_tag(p.y_asg + (uint64_t)sg->asg[j] * p.H + row, __float_as_uint(s), p.tag);
     }
     if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
   }
-  // Count this item's outputs in, one counter per (token, row block), all at once.
-  stores_done();
-  if (tid() < n) {
-    const uint32_t tk = sg->tok[tid()];
-    const uint32_t need = p.tok_need ? p.tok_need[tk] : p.K + (p.has_shared ? 1u : 0u);
-    uint32_t *cnt = p.cnt_tok + (uint64_t)tk * nblk + blk;
-    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last[tid()] = old == need - 1;
-    if (old == need - 1) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  // The completed tokens' rows, a (token, row) pair a thread: y = sum_k w_k y_k in rank order, then + gs s; every
-  // operand loaded first, then summed in order.
-  uint32_t done[MOE_GROUP_MAX], nd = 0;
-  for (uint32_t j = 0; j < n; j++)
-    if (s_last[j]) done[nd++] = sg->tok[j];
-  for (uint32_t i = tid(); i < nd * rows; i += kWG) {
-    const uint32_t tk = done[i / rows], rr = row0 + i % rows, K = p.K;
-    float yv[kMaxUsed], wv[kMaxUsed];
+}
+
+// Combine item (token t, rows blk * down_rows ..): y = sum_k w_k y_k in rank order, then + gs s, a row a thread. The
+// per-assignment outputs are polled as tagged records (one first, then all of the row's); the combine items come after
+// every down item, so what they wait for has a smaller number.
+__device__ __forceinline__ void combine_item(const DecodeParams &p, const GroupTab *tab, uint32_t t, uint32_t blk,
+                                             uint64_t *mark) {
+  const uint32_t rows = down_rows(p.F / kUnit), K = p.K, row = blk * rows + tid();
+  const uint32_t ns = p.has_shared ? 1u : 0u;
+  if (p.route) wait_tag(p, p.y_asg + ((uint64_t)t * K + K - 1) * p.H + blk * rows + rows - 1);
+  if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
+  if (tid() < rows) {
     bool on[kMaxUsed];
+    float wv[kMaxUsed], yv[kMaxUsed];
 #pragma unroll
     for (uint32_t k = 0; k < kMaxUsed; k++) {
-      on[k] = k < K && (p.route || ld_co(p.ids + tk * K + k) >= 0);
-      yv[k] = on[k] ? ld_co(p.y_asg + ((uint64_t)tk * K + k) * p.H + rr) : 0.0f;
+      on[k] = k < K && (p.route || ld_co(p.ids + t * K + k) >= 0);
+      wv[k] = k >= K ? 0.0f : tab->have_w ? tab->w[t * K + k] : p.route ? __uint_as_float(poll_tag(p, p.w_t + t * K + k))
+                                                                   : ld_co(p.w + t * K + k);
     }
-    // The weights: from the group table where this work-group built it, else polled (a shared item that finishes a
-    // token before any routed item ran here), or a pre-routed call's.
+    const float gs = !ns ? 0.0f : tab->have_w ? tab->gs[t] : __uint_as_float(poll_tag(p, p.gs + t));
+    // The K (+ shared) outputs of this row: all loads in flight together, polled as a set.
+    float ys = 0.0f;
+    for (uint32_t n = 0;; n++) {
+      bool ok = true;
 #pragma unroll
-    for (uint32_t k = 0; k < kMaxUsed; k++)
-      wv[k] = k >= K ? 0.0f : tab->have_w ? tab->w[tk * K + k] : p.route ? __uint_as_float(poll_tag(p, p.w_t + tk * K + k))
-                                                                    : ld_co(p.w + tk * K + k);
-    const float ys = p.has_shared ? ld_co(p.y_asg + ((uint64_t)p.T * K + tk) * p.H + rr) : 0.0f;
-    const float gs = !p.has_shared ? 0.0f : tab->have_w ? tab->gs[tk] : __uint_as_float(poll_tag(p, p.gs + tk));
+      for (uint32_t k = 0; k < kMaxUsed; k++) {
+        const uint64_t r = on[k] ? ld_tag(p.y_asg + ((uint64_t)t * K + k) * p.H + row) : ((uint64_t)p.tag << 32);
+        ok &= tag_of(r) == p.tag;
+        yv[k] = __uint_as_float((uint32_t)r);
+      }
+      if (ns) {
+        const uint64_t r = ld_tag(p.y_asg + ((uint64_t)p.T * K + t) * p.H + row);
+        ok &= tag_of(r) == p.tag;
+        ys = __uint_as_float((uint32_t)r);
+      }
+      if (ok) break;
+      __builtin_amdgcn_s_sleep(C0VEN_POLL_SLEEP);
+      if (n == kSpinLimit) {
+        st_co(p.err, 1u);
+        break;
+      }
+    }
     float acc = 0.0f;
 #pragma unroll
     for (uint32_t k = 0; k < kMaxUsed; k++)
       if (on[k]) acc = __fadd_rn(acc, __fmul_rn(wv[k], yv[k]));
-    if (p.has_shared) acc = __fadd_rn(acc, __fmul_rn(gs, ys));
-    p.y[(uint64_t)tk * p.H + rr] = acc;
+    if (ns) acc = __fadd_rn(acc, __fmul_rn(gs, ys));
+    p.y[(uint64_t)t * p.H + row] = acc;
   }
+  if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
 }
 
 }  // namespace
@@ -799,7 +810,7 @@ template <uint32_t kTypes>
 __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) moe_decode(DecodeParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ uint32_t grid_lds[512];
-  __shared__ uint32_t s_flag, s_last[MOE_GROUP_MAX];
+  __shared__ uint32_t s_flag;
   __shared__ uint64_t s_hb[kWG / 64];
   __shared__ double s_part[kMaxDecodeTokens * 16], s_tot[kMaxDecodeTokens];
   __shared__ GroupLds sg;
@@ -810,7 +821,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   __syncthreads();
   const uint32_t T = p.T, E = p.E, Ug = p.H / kUnit, Ud = p.F / kUnit;
   const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nL + nTop;
-  const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud);
+  const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud), nBlk = nD;  // combine items: T x nBlk
   const uint32_t ns = shared_chunks(T, p.route, p.has_shared), B2 = B1 + ns * (nGU + nD);
   // Items below B2 go round-robin (work-group b takes b, b + grid, ...). The routed items, whose cost varies with their
   // group's size, are handed out dynamically: item B2 + x + kDynLists k is the k-th of list x, and the work-groups with
@@ -835,7 +846,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
         copy_groups(p, &gtab);
       }
       ng = gtab.ng;
-      end = B2 + ng * (nGU + nD);
+      end = B2 + ng * (nGU + nD) + T * nBlk;
       if (tid() == 0) s_flag = grab;
       __syncthreads();
       it = B2 + list + kDynLists * s_flag;
@@ -871,15 +882,19 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
         gate_up_item<kTypes>(p, &sg, i % nGU, lds, grid_lds, exp_tab, mark);
       } else {
         read_group(p, &gtab, true, (i - ns * nGU) / nD, &sg);
-        down_item<kTypes>(p, &sg, &gtab, (i - ns * nGU) % nD, lds, grid_lds, s_last, mark);
+        down_item<kTypes>(p, &sg, (i - ns * nGU) % nD, lds, grid_lds, mark);
       }
     } else if (it < B2 + ng * nGU) {
       read_group(p, &gtab, false, (it - B2) / nGU, &sg);
       gate_up_item<kTypes>(p, &sg, (it - B2) % nGU, lds, grid_lds, exp_tab, mark);
     } else {
       const uint32_t i = it - B2 - ng * nGU;
-      read_group(p, &gtab, false, i / nD, &sg);
-      down_item<kTypes>(p, &sg, &gtab, i % nD, lds, grid_lds, s_last, mark);
+      if (i < ng * nD) {
+        read_group(p, &gtab, false, i / nD, &sg);
+        down_item<kTypes>(p, &sg, i % nD, lds, grid_lds, mark);
+      } else {
+        combine_item(p, &gtab, (i - ng * nD) / nBlk, (i - ng * nD) % nBlk, mark);
+      }
     }
     if (mark && tid() == 0) mark[3] = __builtin_amdgcn_s_memrealtime();
     if (dynamic) {
