@@ -82,7 +82,18 @@ def main():
     ap.add_argument("--config", default="2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run five 256 MiB device-to-device copies (the reference transfer for rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE passes) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        hip = Hip()
+        n = 256 << 20
+        a, b = hip.malloc(n), hip.malloc(n)
+        for _ in range(5):
+            assert hip.rt.hipMemcpy(b, a, n, 3) == 0
+        hip.sync()
+        return
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the MoE block on one MI355X); --gpus %d is not run"
               % args.gpus, file=sys.stderr)
