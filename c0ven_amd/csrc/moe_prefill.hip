@@ -7,6 +7,8 @@
 // unit's fp32 steps exactly as the decoders in units.h do, and add a row's units in sequence, as the oracle does.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "act_quant.h"
 #include "device_math.h"
 #include "iq3s_grid.h"
@@ -485,165 +487,175 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   stage.load(g.act, arow_lds, U, 0);
   stage.store(abuf[0]);
   __syncthreads();
-  float acc[2][16];  // the row's units summed in sequence (ORACLE ORDER), for positions m_r and 32 + m_r
-#pragma unroll
-  for (int b = 0; b < 2; b++)
-#pragma unroll
-    for (int r = 0; r < 16; r++) acc[b][r] = 0.0f;
-#pragma unroll 1
-  for (uint32_t u = 0; u < U; u++) {
-    typename SliceOf<kType>::T s_next;
-    if (u + 1 < U) {
-      stage.load(g.act, arow_lds, U, u + 1);
-      s_next.fetch(tile, idx0 + u + 1, nl, h);
-    }
-    s.decode();
-    const uint8_t *buf = abuf[u & 1];
-    // This lane's A rows (positions n, 32 + n; its half of each block), and the base of the scales of the positions
-    // its results belong to (32 b + 8 (r / 4) + 4 h + r % 4): every LDS read below is a base plus a constant offset.
-    const uint32_t lf = lane_id(), hf = lf / 32, nf = lf % 32;  // (fresh: see tid_fresh)
-    const uint8_t *arow0 = buf + nf * kActLds + 16 * hf, *arow1 = arow0 + 32 * kActLds;
-    const uint8_t *mbase = buf + 4 * hf * kActLds + kActScales;
-    if constexpr (kType == QT_Q8_0) {
-#pragma unroll
-      for (int b = 0; b < 2; b++) {
-        const uint8_t *ar = b ? arow1 : arow0;
-        float q[3][16];  // the eight block terms' pairwise tree
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
-          const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words(j), v16i{}, 0, 0, 0);
-          float c[16];
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
-            const float as = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds + 4 * j);
-            c[r] = __fmul_rn(__fmul_rn(s.d[j], as), (float)dv[r]);
-          }
-#pragma unroll
-          for (int r = 0; r < 16; r++) asm volatile("" : "+v"(c[r]));
-          __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
-          if ((j & 1) == 0) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) q[0][r] = c[r];
-          } else {
-#pragma unroll
-            for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[0][r], c[r]);
-            if ((j & 2) == 0) {
-#pragma unroll
-              for (int r = 0; r < 16; r++) q[1][r] = c[r];
+  // A tile of at most 32 positions takes one MFMA row block (kNB = 1): the second block's MFMAs and epilogue would
+  // only produce outputs that are not stored. Each case is compiled on its own.
+  auto run = [&](auto nb_tag) {
+    constexpr int kNB = decltype(nb_tag)::value;
+    float acc[2][16];  // the row's units summed in sequence (ORACLE ORDER), for positions m_r and 32 + m_r
+  #pragma unroll
+    for (int b = 0; b < kNB; b++)
+  #pragma unroll
+      for (int r = 0; r < 16; r++) acc[b][r] = 0.0f;
+  #pragma unroll 1
+    for (uint32_t u = 0; u < U; u++) {
+      typename SliceOf<kType>::T s_next;
+      if (u + 1 < U) {
+        stage.load(g.act, arow_lds, U, u + 1);
+        s_next.fetch(tile, idx0 + u + 1, nl, h);
+      }
+      s.decode();
+      const uint8_t *buf = abuf[u & 1];
+      // This lane's A rows (positions n, 32 + n; its half of each block), and the base of the scales of the positions
+      // its results belong to (32 b + 8 (r / 4) + 4 h + r % 4): every LDS read below is a base plus a constant offset.
+      const uint32_t lf = lane_id(), hf = lf / 32, nf = lf % 32;  // (fresh: see tid_fresh)
+      const uint8_t *arow0 = buf + nf * kActLds + 16 * hf, *arow1 = arow0 + 32 * kActLds;
+      const uint8_t *mbase = buf + 4 * hf * kActLds + kActScales;
+      if constexpr (kType == QT_Q8_0) {
+  #pragma unroll
+        for (int b = 0; b < kNB; b++) {
+          const uint8_t *ar = b ? arow1 : arow0;
+          float q[3][16];  // the eight block terms' pairwise tree
+  #pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
+            const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words(j), v16i{}, 0, 0, 0);
+            float c[16];
+  #pragma unroll
+            for (int r = 0; r < 16; r++) {
+              const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
+              const float as = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds + 4 * j);
+              c[r] = __fmul_rn(__fmul_rn(s.d[j], as), (float)dv[r]);
+            }
+  #pragma unroll
+            for (int r = 0; r < 16; r++) asm volatile("" : "+v"(c[r]));
+            __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
+            if ((j & 1) == 0) {
+  #pragma unroll
+              for (int r = 0; r < 16; r++) q[0][r] = c[r];
             } else {
-#pragma unroll
-              for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[1][r], c[r]);
-              if ((j & 4) == 0) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) q[2][r] = c[r];
+  #pragma unroll
+              for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[0][r], c[r]);
+              if ((j & 2) == 0) {
+  #pragma unroll
+                for (int r = 0; r < 16; r++) q[1][r] = c[r];
               } else {
-#pragma unroll
-                for (int r = 0; r < 16; r++) acc[b][r] = __fadd_rn(acc[b][r], __fadd_rn(q[2][r], c[r]));
+  #pragma unroll
+                for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[1][r], c[r]);
+                if ((j & 4) == 0) {
+  #pragma unroll
+                  for (int r = 0; r < 16; r++) q[2][r] = c[r];
+                } else {
+  #pragma unroll
+                  for (int r = 0; r < 16; r++) acc[b][r] = __fadd_rn(acc[b][r], __fadd_rn(q[2][r], c[r]));
+                }
               }
             }
           }
         }
-      }
-    } else if constexpr (kType == QT_Q4_K) {
-      // isum = sum_j sc_j (q . a)_j with sc_j = 8 hi_j + lo_j: the scale is folded into the weights (q lo_j and
-      // q hi_j, each below 106 a byte) and both products accumulate over the eight blocks inside the MFMA, exactly.
-      v4i bmh, bml;  // the minimum part's B operands
-      {
-        uint32_t m0 = 0, m1 = 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) (j < 4 ? m0 : m1) |= (uint32_t)s.mn[j] << (8 * (j % 4));
-        const bool z = h != 0;
-        bmh[0] = z ? 0 : (int)m0, bmh[1] = z ? 0 : (int)m1, bmh[2] = 0, bmh[3] = 0;
-        bml[0] = 0, bml[1] = 0, bml[2] = z ? 0 : (int)m0, bml[3] = z ? 0 : (int)m1;
-      }
-      v16i dhi[2] = {v16i{}, v16i{}}, dlo[2] = {v16i{}, v16i{}};
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const v4i bl = s.words_times(j, (uint32_t)s.sc[j] & 7u), bh = s.words_times(j, (uint32_t)s.sc[j] >> 3);
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-          const v4i aw = as_v4i(*(const uint4 *)((b ? arow1 : arow0) + 32 * j));
-          dlo[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bl, dlo[b], 0, 0, 0);
-          dhi[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bh, dhi[b], 0, 0, 0);
+      } else if constexpr (kType == QT_Q4_K) {
+        // isum = sum_j sc_j (q . a)_j with sc_j = 8 hi_j + lo_j: the scale is folded into the weights (q lo_j and
+        // q hi_j, each below 106 a byte) and both products accumulate over the eight blocks inside the MFMA, exactly.
+        v4i bmh, bml;  // the minimum part's B operands
+        {
+          uint32_t m0 = 0, m1 = 0;
+  #pragma unroll
+          for (int j = 0; j < 8; j++) (j < 4 ? m0 : m1) |= (uint32_t)s.mn[j] << (8 * (j % 4));
+          const bool z = h != 0;
+          bmh[0] = z ? 0 : (int)m0, bmh[1] = z ? 0 : (int)m1, bmh[2] = 0, bmh[3] = 0;
+          bml[0] = 0, bml[1] = 0, bml[2] = z ? 0 : (int)m0, bml[3] = z ? 0 : (int)m1;
+        }
+        v16i dhi[2] = {v16i{}, v16i{}}, dlo[2] = {v16i{}, v16i{}};
+  #pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const v4i bl = s.words_times(j, (uint32_t)s.sc[j] & 7u), bh = s.words_times(j, (uint32_t)s.sc[j] >> 3);
+  #pragma unroll
+          for (int b = 0; b < kNB; b++) {
+            const v4i aw = as_v4i(*(const uint4 *)((b ? arow1 : arow0) + 32 * j));
+            dlo[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bl, dlo[b], 0, 0, 0);
+            dhi[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bh, dhi[b], 0, 0, 0);
+          }
+        }
+  #pragma unroll
+        for (int b = 0; b < kNB; b++) {
+          const uint8_t *ar = b ? arow1 : arow0;
+          v4i am = bsum_split(ar - 16 * h);
+          if (h) am = v4i{0, 0, 0, 0};
+          const v16i dh = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bmh, v16i{}, 0, 0, 0);
+          const v16i dl = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bml, v16i{}, 0, 0, 0);
+  #pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const int isum = 8 * dhi[b][r] + dlo[b][r], imin = 64 * dh[r] + dl[r];
+            const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
+            const float dd = __fmul_rn(s.d, ad), dm = __fmul_rn(s.dmin, ad);
+            const float pm = __fmul_rn(dm, (float)imin);
+            acc[b][r] = __fadd_rn(acc[b][r], __builtin_fmaf(dd, (float)isum, -pm));
+          }
+        }
+      } else {
+  #pragma unroll
+        for (int b = 0; b < kNB; b++) {
+          const uint8_t *ar = b ? arow1 : arow0;
+          int isum[16];
+  #pragma unroll
+          for (int r = 0; r < 16; r++) isum[r] = 0;
+  #pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
+            const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words_h(j, h, grid_lds), v16i{}, 0, 0, 0);
+  #pragma unroll
+            for (int r = 0; r < 16; r++) isum[r] += s.ls[j] * dv[r];
+  #pragma unroll
+            for (int r = 0; r < 16; r++) asm volatile("" : "+v"(isum[r]));  // keeps the sums in block order
+            __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
+          }
+  #pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
+            const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
+            acc[b][r] = __fadd_rn(acc[b][r], __fmul_rn(__fmul_rn(s.d, ad), (float)isum[r]));
+          }
         }
       }
-#pragma unroll
-      for (int b = 0; b < 2; b++) {
-        const uint8_t *ar = b ? arow1 : arow0;
-        v4i am = bsum_split(ar - 16 * h);
-        if (h) am = v4i{0, 0, 0, 0};
-        const v16i dh = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bmh, v16i{}, 0, 0, 0);
-        const v16i dl = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bml, v16i{}, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int isum = 8 * dhi[b][r] + dlo[b][r], imin = 64 * dh[r] + dl[r];
-          const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
-          const float dd = __fmul_rn(s.d, ad), dm = __fmul_rn(s.dmin, ad);
-          const float pm = __fmul_rn(dm, (float)imin);
-          acc[b][r] = __fadd_rn(acc[b][r], __builtin_fmaf(dd, (float)isum, -pm));
-        }
+      if (u + 1 < U) {
+        stage.store(abuf[(u + 1) & 1]);
+        s = s_next;
+      }
+      __syncthreads();
+    }
+    // Outputs: positions 32 b + m_r, weight row `row`.
+    if constexpr (kGU) {
+      const uint32_t col = 32 * (w & 1) + n;
+      if (mat == 1) {
+  #pragma unroll
+        for (int b = 0; b < kNB; b++)
+  #pragma unroll
+          for (int r = 0; r < 16; r++) ub[32 * b + 8 * (r / 4) + 4 * h + (r % 4)][col] = acc[b][r];
+      }
+      __syncthreads();
+      if (mat == 0) {
+  #pragma unroll
+        for (int b = 0; b < kNB; b++)
+  #pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
+            if (m < count)
+              g.out[(uint64_t)(start + m) * g.out_ld + row] = swiglu_one(acc[b][r], ub[m][col], g.limit, tab);
+          }
       }
     } else {
-#pragma unroll
-      for (int b = 0; b < 2; b++) {
-        const uint8_t *ar = b ? arow1 : arow0;
-        int isum[16];
-#pragma unroll
-        for (int r = 0; r < 16; r++) isum[r] = 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
-          const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words_h(j, h, grid_lds), v16i{}, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 16; r++) isum[r] += s.ls[j] * dv[r];
-#pragma unroll
-          for (int r = 0; r < 16; r++) asm volatile("" : "+v"(isum[r]));  // keeps the sums in block order
-          __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
-        }
-#pragma unroll
+  #pragma unroll
+      for (int b = 0; b < kNB; b++)
+  #pragma unroll
         for (int r = 0; r < 16; r++) {
           const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
-          const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
-          acc[b][r] = __fadd_rn(acc[b][r], __fmul_rn(__fmul_rn(s.d, ad), (float)isum[r]));
-        }
-      }
-    }
-    if (u + 1 < U) {
-      stage.store(abuf[(u + 1) & 1]);
-      s = s_next;
-    }
-    __syncthreads();
-  }
-  // Outputs: positions 32 b + m_r, weight row `row`.
-  if constexpr (kGU) {
-    const uint32_t col = 32 * (w & 1) + n;
-    if (mat == 1) {
-#pragma unroll
-      for (int b = 0; b < 2; b++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) ub[32 * b + 8 * (r / 4) + 4 * h + (r % 4)][col] = acc[b][r];
-    }
-    __syncthreads();
-    if (mat == 0) {
-#pragma unroll
-      for (int b = 0; b < 2; b++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
-          if (m < count)
-            g.out[(uint64_t)(start + m) * g.out_ld + row] = swiglu_one(acc[b][r], ub[m][col], g.limit, tab);
+          if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row] = acc[b][r];
         }
     }
+  };
+  if (count > 32) {
+    run(std::integral_constant<int, 2>{});
   } else {
-#pragma unroll
-    for (int b = 0; b < 2; b++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
-        if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row] = acc[b][r];
-      }
+    run(std::integral_constant<int, 1>{});
   }
 }
 
