@@ -425,7 +425,9 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds,
   uint32_t *ids = (uint32_t *)lds, *mask = ids + kMaxDecodeTokens * kMaxUsed, *gnum = mask + kMaxExperts;
   for (uint32_t i = a; i < E; i += kWG) mask[i] = 0u;
   const uint32_t t = a / K;
-  wait_tag(p, p.ids_t + n - 1);  // the last token's last id, then every id and weight
+  // The last token's last id first, then every id and weight; for a few records (a token or so) every reader polls its
+  // own directly, one round trip less.
+  if (n > 32) wait_tag(p, p.ids_t + n - 1);
   if (a < n) {  // the routed ids and weights, polled together
     uint64_t ri, rw;
     for (uint32_t k = 0;; k++) {
@@ -442,6 +444,16 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds,
   }
   if (p.has_shared && a < T) tab->gs[a] = __uint_as_float(poll_tag(p, p.gs + a));
   __syncthreads();
+  if (T == 1) {  // one token: every group is one assignment, in rank order (what the general numbering gives)
+    if (a < K) {
+      tab->slot[a] = (int32_t)ids[a];
+      tab->n[a] = 1u;
+      tab->asg[a][0] = (uint16_t)a;
+    }
+    if (a == 0) tab->ng = K, tab->have_w = 1;
+    __syncthreads();
+    return;
+  }
   uint32_t e = 0, rank = 0, total = 0;
   if (a < n) {
     e = ids[a];
