@@ -71,10 +71,16 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 // bf16 by round to nearest even (ggml's GGML_FP32_TO_BF16), NaN kept quiet.
 __device__ __forceinline__ float round_bf16(float f) {
-  const uint32_t x = __float_as_uint(f);
-  const uint32_t quiet = (x | 0x00400000u) & 0xffff0000u;  // NaN: truncated, quiet bit set (no branch: a select)
-  const uint32_t rne = (x + (0x7fffu + ((x >> 16) & 1u))) & 0xffff0000u;
-  return __uint_as_float((x & 0x7fffffffu) > 0x7f800000u ? quiet : rne);
+  // gfx950's v_cvt_pk_bf16_f32 rounds to nearest even and quiets a NaN exactly this way: checked on the GPU against
+  // the bit formula (x + 0x7fff + lsb, truncated; NaN: truncated with the quiet bit set) for all 2^32 inputs.
+  return __uint_as_float((uint32_t)__builtin_bit_cast(unsigned short, (__bf16)f) << 16);
+}
+// Two at once (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ void round_bf16_2(float a, float b, float &ra, float &rb) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));
+  ra = __uint_as_float(w << 16), rb = __uint_as_float(w & 0xffff0000u);
 }
 
 // ggml's nearest_int: round half to even, |v| < 2^22.

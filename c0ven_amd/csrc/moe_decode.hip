@@ -359,9 +359,11 @@ __device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, 
         double a = 0.0;
         if (tt < nb) {
           const float4 xa = xq[tt / 4][tt % 4][0], xb = xq[tt / 4][tt % 4][1];
-          const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+          float xs[8];
+          round_bf16_2(xa.x, xa.y, xs[0], xs[1]), round_bf16_2(xa.z, xa.w, xs[2], xs[3]);
+          round_bf16_2(xb.x, xb.y, xs[4], xs[5]), round_bf16_2(xb.z, xb.w, xs[6], xs[7]);
 #pragma unroll
-          for (int k = 0; k < 8; k++) a = __builtin_fma(wd[k], (double)round_bf16(xs[k]), a);
+          for (int k = 0; k < 8; k++) a = __builtin_fma(wd[k], (double)xs[k], a);
         }
         v[tt] = a;
       }
