@@ -320,7 +320,16 @@ struct SliceQ4_K {
     d = h2f((uint16_t)dm);
     dmin = h2f((uint16_t)(dm >> 16));
   }
-  // Block j's codes times k (k <= 7): every byte stays below 106, so one 32-bit product carries nothing across bytes.
+  // Block j's codes times lo and hi (each <= 7; every byte stays below 106, so the products carry nothing across
+  // bytes), the nibbles extracted once for both.
+  __device__ __forceinline__ void words_times2(int j, uint32_t lo, uint32_t hi, v4i &rl, v4i &rh) const {
+    const uint4 v = q[j / 2];
+    const int s = 4 * (j & 1);
+    const uint32_t w[4] = {(v.x >> s) & 0x0f0f0f0fu, (v.y >> s) & 0x0f0f0f0fu, (v.z >> s) & 0x0f0f0f0fu, (v.w >> s) & 0x0f0f0f0fu};
+#pragma unroll
+    for (int i = 0; i < 4; i++) rl[i] = (int)mul_bytes(w[i], lo), rh[i] = (int)mul_bytes(w[i], hi);
+  }
+  // Block j's codes times k (k <= 7).
   __device__ __forceinline__ v4i words_times(int j, uint32_t k) const {
     const uint4 v = q[j / 2];
     const int s = 4 * (j & 1);
@@ -492,9 +501,9 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   auto run = [&](auto nb_tag) {
     constexpr int kNB = decltype(nb_tag)::value;
     float acc[2][16];  // the row's units summed in sequence (ORACLE ORDER), for positions m_r and 32 + m_r
-  #pragma unroll
+#pragma unroll
     for (int b = 0; b < kNB; b++)
-  #pragma unroll
+#pragma unroll
       for (int r = 0; r < 16; r++) acc[b][r] = 0.0f;
   #pragma unroll 1
     for (uint32_t u = 0; u < U; u++) {
@@ -511,41 +520,41 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
       const uint8_t *arow0 = buf + nf * kActLds + 16 * hf, *arow1 = arow0 + 32 * kActLds;
       const uint8_t *mbase = buf + 4 * hf * kActLds + kActScales;
       if constexpr (kType == QT_Q8_0) {
-  #pragma unroll
+#pragma unroll
         for (int b = 0; b < kNB; b++) {
           const uint8_t *ar = b ? arow1 : arow0;
           float q[3][16];  // the eight block terms' pairwise tree
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 8; j++) {
             const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
             const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words(j), v16i{}, 0, 0, 0);
             float c[16];
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 16; r++) {
               const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
               const float as = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds + 4 * j);
               c[r] = __fmul_rn(__fmul_rn(s.d[j], as), (float)dv[r]);
             }
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 16; r++) asm volatile("" : "+v"(c[r]));
             __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
             if ((j & 1) == 0) {
-  #pragma unroll
+#pragma unroll
               for (int r = 0; r < 16; r++) q[0][r] = c[r];
             } else {
-  #pragma unroll
+#pragma unroll
               for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[0][r], c[r]);
               if ((j & 2) == 0) {
-  #pragma unroll
+#pragma unroll
                 for (int r = 0; r < 16; r++) q[1][r] = c[r];
               } else {
-  #pragma unroll
+#pragma unroll
                 for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[1][r], c[r]);
                 if ((j & 4) == 0) {
-  #pragma unroll
+#pragma unroll
                   for (int r = 0; r < 16; r++) q[2][r] = c[r];
                 } else {
-  #pragma unroll
+#pragma unroll
                   for (int r = 0; r < 16; r++) acc[b][r] = __fadd_rn(acc[b][r], __fadd_rn(q[2][r], c[r]));
                 }
               }
@@ -558,31 +567,32 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
         v4i bmh, bml;  // the minimum part's B operands
         {
           uint32_t m0 = 0, m1 = 0;
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 8; j++) (j < 4 ? m0 : m1) |= (uint32_t)s.mn[j] << (8 * (j % 4));
           const bool z = h != 0;
           bmh[0] = z ? 0 : (int)m0, bmh[1] = z ? 0 : (int)m1, bmh[2] = 0, bmh[3] = 0;
           bml[0] = 0, bml[1] = 0, bml[2] = z ? 0 : (int)m0, bml[3] = z ? 0 : (int)m1;
         }
         v16i dhi[2] = {v16i{}, v16i{}}, dlo[2] = {v16i{}, v16i{}};
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < 8; j++) {
-          const v4i bl = s.words_times(j, (uint32_t)s.sc[j] & 7u), bh = s.words_times(j, (uint32_t)s.sc[j] >> 3);
-  #pragma unroll
+          v4i bl, bh;
+        s.words_times2(j, (uint32_t)s.sc[j] & 7u, (uint32_t)s.sc[j] >> 3, bl, bh);
+#pragma unroll
           for (int b = 0; b < kNB; b++) {
             const v4i aw = as_v4i(*(const uint4 *)((b ? arow1 : arow0) + 32 * j));
             dlo[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bl, dlo[b], 0, 0, 0);
             dhi[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bh, dhi[b], 0, 0, 0);
           }
         }
-  #pragma unroll
+#pragma unroll
         for (int b = 0; b < kNB; b++) {
           const uint8_t *ar = b ? arow1 : arow0;
           v4i am = bsum_split(ar - 16 * h);
           if (h) am = v4i{0, 0, 0, 0};
           const v16i dh = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bmh, v16i{}, 0, 0, 0);
           const v16i dl = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bml, v16i{}, 0, 0, 0);
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 16; r++) {
             const int isum = 8 * dhi[b][r] + dlo[b][r], imin = 64 * dh[r] + dl[r];
             const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
@@ -592,23 +602,23 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
           }
         }
       } else {
-  #pragma unroll
+#pragma unroll
         for (int b = 0; b < kNB; b++) {
           const uint8_t *ar = b ? arow1 : arow0;
           int isum[16];
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 16; r++) isum[r] = 0;
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 8; j++) {
             const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
             const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words_h(j, h, grid_lds), v16i{}, 0, 0, 0);
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 16; r++) isum[r] += s.ls[j] * dv[r];
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 16; r++) asm volatile("" : "+v"(isum[r]));  // keeps the sums in block order
             __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
           }
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 16; r++) {
             const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
             const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
@@ -626,16 +636,16 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
     if constexpr (kGU) {
       const uint32_t col = 32 * (w & 1) + n;
       if (mat == 1) {
-  #pragma unroll
+#pragma unroll
         for (int b = 0; b < kNB; b++)
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 16; r++) ub[32 * b + 8 * (r / 4) + 4 * h + (r % 4)][col] = acc[b][r];
       }
       __syncthreads();
       if (mat == 0) {
-  #pragma unroll
+#pragma unroll
         for (int b = 0; b < kNB; b++)
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 16; r++) {
             const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
             if (m < count)
@@ -643,9 +653,9 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
           }
       }
     } else {
-  #pragma unroll
+#pragma unroll
       for (int b = 0; b < kNB; b++)
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 16; r++) {
           const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
           if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row] = acc[b][r];
