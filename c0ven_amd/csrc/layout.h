@@ -54,5 +54,7 @@ C0VEN_HD uint64_t matrix_bytes(uint32_t type, uint32_t rows, uint32_t k) {
 //   [288, 320) q8_K only: the sums of each 32 codes as int32 (bsums[2j] + bsums[2j + 1]).
 // In LDS the kernels keep them kActLds apart, so the eight units a wave reads at once fall in distinct banks.
 constexpr uint32_t kActBytes = 320, kActScales = 256, kActSums = 288, kActLds = 336;
+// In LDS the 16 bytes of padding after a unit may hold its sums split for the Q4_K minimum MFMA (hi bytes, lo bytes).
+constexpr uint32_t kActSplit = 320;
 
 }  // namespace c0ven

@@ -96,17 +96,40 @@ struct ActB {
     const uint32_t g = lane / 16;
 #pragma unroll
     for (int s = 0; s < 8; s++) q[s] = *(const long *)(unit + 32 * s + 8 * g);
+    split_sums(unit, g);
+    ad = *(const float *)(unit + kActScales);
+  }
+  // The same, with the sums' split already in the unit's LDS padding (kActSplit, written by put_split).
+  __device__ __forceinline__ void load_presplit(const uint8_t *unit, uint32_t lane) {
+    const uint32_t g = lane / 16;
+#pragma unroll
+    for (int s = 0; s < 8; s++) q[s] = *(const long *)(unit + 32 * s + 8 * g);
+    const uint4 v = *(const uint4 *)(unit + kActSplit);
+    bh = g == 0 ? pack2(v.x, v.y) : 0;
+    bl = g == 0 ? pack2(v.z, v.w) : 0;
+    ad = *(const float *)(unit + kActScales);
+  }
+  // Writes a unit's split sums (hi bytes, then lo bytes) into its LDS padding at kActSplit.
+  __device__ static __forceinline__ void put_split(uint8_t *unit) {
+    uint32_t h[2], l[2];
+    split_words(unit, h, l);
+    *(uint4 *)(unit + kActSplit) = make_uint4(h[0], h[1], l[0], l[1]);
+  }
+  __device__ static __forceinline__ void split_words(const uint8_t *unit, uint32_t h[2], uint32_t l[2]) {
     const uint4 a = *(const uint4 *)(unit + kActSums), c = *(const uint4 *)(unit + kActSums + 16);
     const int bs[8] = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)c.x, (int)c.y, (int)c.z, (int)c.w};
-    uint32_t h[2] = {0u, 0u}, l[2] = {0u, 0u};
+    h[0] = h[1] = l[0] = l[1] = 0u;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       h[j / 4] |= ((uint32_t)(bs[j] >> 6) & 0xffu) << (8 * (j % 4));
       l[j / 4] |= ((uint32_t)bs[j] & 63u) << (8 * (j % 4));
     }
+  }
+  __device__ __forceinline__ void split_sums(const uint8_t *unit, uint32_t g) {
+    uint32_t h[2], l[2];
+    split_words(unit, h, l);
     bh = g == 0 ? pack2(h[0], h[1]) : 0;
     bl = g == 0 ? pack2(l[0], l[1]) : 0;
-    ad = *(const float *)(unit + kActScales);
   }
 };
 

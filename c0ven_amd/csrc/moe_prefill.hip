@@ -412,6 +412,7 @@ struct PfGemm {
   float *out;              // position p's outputs at out + p * out_ld
   uint32_t out_ld;
   float limit;
+  uint32_t row_blocks;     // pf_gemm_q4k: row blocks a tile (its 1-D grid is tiles x row_blocks)
 };
 
 // Rows a work-group of pf_gemm takes: 64 of gate and of up (waves 0-1 gate, 2-3 up, rows 32 (w % 2) ..), or 128 of
@@ -437,6 +438,27 @@ struct ActStage {
     for (int i = 0; i < 5; i++) {
       const uint32_t piece = threadIdx.x + kPfWG * i, tk = piece / 20, c = piece % 20;
       *(uint4 *)(buf + tk * kActLds + 16 * c) = v[i];
+    }
+  }
+  // The same, and the holders of the sums (pieces 18 and 19: sums 0-3 and 4-7) also write them split into hi and lo
+  // bytes in the unit's padding (kActSplit: hi bytes of sums 0-7, then lo bytes), as ActB::load_presplit reads them.
+  __device__ __forceinline__ void store_split(uint8_t *buf) const {
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+      const uint32_t piece = threadIdx.x + kPfWG * i, tk = piece / 20, c = piece % 20;
+      uint8_t *unit = buf + tk * kActLds;
+      *(uint4 *)(unit + 16 * c) = v[i];
+      if (c >= 18) {
+        const int bs[4] = {(int)v[i].x, (int)v[i].y, (int)v[i].z, (int)v[i].w};
+        uint32_t h = 0, l = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          h |= ((uint32_t)(bs[j] >> 6) & 0xffu) << (8 * j);
+          l |= ((uint32_t)bs[j] & 63u) << (8 * j);
+        }
+        *(uint32_t *)(unit + kActSplit + 4 * (c - 18)) = h;
+        *(uint32_t *)(unit + kActSplit + 8 + 4 * (c - 18)) = l;
+      }
     }
   }
 };
@@ -669,6 +691,127 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   }
 }
 
+// Work-group b of a 1-D grid of n runs on XCD b % 8 (the dispatcher deals work-groups to the eight XCDs in turn).
+// Its logical index puts consecutive logical indices on one XCD: (b % 8) ceil(n / 8) + b / 8. With the row block
+// fastest in the logical index, a tile's row blocks run together on one XCD (its activations come from that XCD's
+// L2), and the next tile of the same expert follows on the same XCD (its weights too). Returns n or more for the
+// slots past n.
+__device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
+  const uint32_t per = (n + 7) / 8;
+  return (b % 8) * per + b / 8;
+}
+
+// Q4_K on 16 x 16 x 32 int8 MFMA (mfma_q4k.h, the decode path's tile): wave w takes 16 weight rows (gate/up: matrix
+// w / 2, rows 16 (w % 2) .. of the work-group's 32 of each; down: rows 16 w .. of its 64) against the tile's positions
+// in 16-position tiles (only those holding positions run), unit by unit: the same integers and fp32 steps as
+// UnitQ4_K::term, units added in sequence. Its accumulators are a quarter of the 32 x 32 kernel's, so three
+// work-groups share a CU.
+template <uint32_t kLU, bool kGU>
+__global__ void __launch_bounds__(kPfWG) pf_gemm_q4k(PfGemm g) {
+  constexpr uint32_t U = 1u << kLU, kRows = kGU ? 32 : 64;
+  __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
+  __shared__ float ub[kGU ? 32 : 1][65];  // up sums [row][position]
+  __shared__ uint32_t arow_lds[64];
+  __shared__ uint64_t tab[32];
+  // 1-D grid of (tile, row block) pairs, the row block fastest in the XCD-aware logical index over the pairs that
+  // exist (the grid is sized for the most tiles a dispatch can make).
+  const uint32_t nrb = g.row_blocks;
+  const uint32_t ntl = g.shared_T ? (g.shared_T + MOE_TILE - 1) / MOE_TILE : *g.ntiles, n = ntl * nrb;
+  if (blockIdx.x >= n) return;
+  const uint32_t L = xcd_logical(blockIdx.x, n);
+  if (L >= n) return;
+  const uint32_t tile_i = L / nrb, rb = L % nrb;
+  uint32_t start, count, e;
+  if (g.shared_T) {
+    start = MOE_TILE * tile_i;
+    if (start >= g.shared_T) return;
+    count = min((uint32_t)MOE_TILE, g.shared_T - start), e = 0;
+  } else {
+    if (tile_i >= *g.ntiles) return;
+    const MoeTile tl = g.tiles[tile_i];
+    start = tl.start, count = tl.count, e = tl.slot;
+  }
+  const uint32_t tid = tid_fresh(), w = wave_id();
+  if (tid < 32) tab[tid] = kExp2Tab[tid];
+  if (tid < 64) {
+    const uint32_t pos = start + tid;
+    arow_lds[tid] = tid < count ? (g.act_by_pos ? pos : (g.perm ? g.perm[pos] / g.K : pos)) : 0xffffffffu;
+  }
+  __syncthreads();
+  const uint32_t mat = kGU ? (w >> 1) : 0u;
+  const uint32_t row0 = rb * kRows + (kGU ? 16 * (w & 1) : 16 * w);
+  const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
+  const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
+  Q4kRaw raw;
+  raw.load(M, U, row0, 0, lane_id());
+  ActStage stage;
+  stage.load(g.act, arow_lds, U, 0);
+  stage.store_split(abuf[0]);
+  __syncthreads();
+  float acc[4][4];
+#pragma unroll
+  for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[pt][i] = 0.0f;
+#pragma unroll 1
+  for (uint32_t u = 0; u < U; u++) {
+    Q4kRaw next;
+    if (u + 1 < U) {
+      stage.load(g.act, arow_lds, U, u + 1);
+      next.load(M, U, row0, u + 1, lane_id());
+    }
+    Q4kA a;
+    a.decode(raw, lane_id());
+    const uint8_t *buf = abuf[u & 1];
+#pragma unroll
+    for (uint32_t pt = 0; pt < 4; pt++) {
+      if (pt < npt) {
+        ActB b;
+        b.load_presplit(buf + (16 * pt + lane_id() % 16) * kActLds, lane_id());
+        float t[4];
+        q4k_terms(a, b, t);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[pt][i] = __fadd_rn(acc[pt][i], t[i]);
+      }
+    }
+    if (u + 1 < U) {
+      stage.store_split(abuf[(u + 1) & 1]);
+      raw = next;
+    }
+    __syncthreads();
+  }
+  // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16.
+  const uint32_t l = lane_id(), r4 = 4 * (l / 16), c16 = l % 16;
+  if constexpr (kGU) {
+    if (mat == 1) {
+#pragma unroll
+      for (uint32_t pt = 0; pt < 4; pt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) ub[16 * (w & 1) + r4 + i][16 * pt + c16] = acc[pt][i];
+    }
+    __syncthreads();
+    if (mat == 0) {
+#pragma unroll
+      for (uint32_t pt = 0; pt < 4; pt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const uint32_t m = 16 * pt + c16;
+          if (m < count)
+            g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] =
+                swiglu_one(acc[pt][i], ub[16 * (w & 1) + r4 + i][m], g.limit, tab);
+        }
+    }
+  } else {
+#pragma unroll
+    for (uint32_t pt = 0; pt < 4; pt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t m = 16 * pt + c16;
+        if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = acc[pt][i];
+      }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Combine: y[t][r] = sum_k w[t][k] y_asg[inv[t K + k]][r] in rank order, then + gs[t] y_sh[t][r]; four rows a thread.
 
@@ -714,12 +857,24 @@ template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
   uint32_t LU = 0;
   while ((1u << LU) < U) LU++;
-  if (type == QT_Q8_0)
+  if (type == QT_Q8_0) {
     launch_gemm_lu<QT_Q8_0, kGU>(LU, grid, g, s);
-  else if (type == QT_Q4_K)
-    launch_gemm_lu<QT_Q4_K, kGU>(LU, grid, g, s);
-  else
+  } else if (type == QT_Q4_K) {  // the 16 x 16 MFMA kernel: half the rows a work-group, a 1-D XCD-aware grid
+    PfGemm q = g;
+    q.row_blocks = grid.y * gemm_rows<kGU>() / (kGU ? 32 : 64);
+    const dim3 g2(grid.x * q.row_blocks);
+    switch (LU) {
+      case 0: pf_gemm_q4k<0, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+      case 1: pf_gemm_q4k<1, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+      case 2: pf_gemm_q4k<2, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+      case 3: pf_gemm_q4k<3, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+      case 4: pf_gemm_q4k<4, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+      default: pf_gemm_q4k<5, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    }
+  }
+  else {
     launch_gemm_lu<QT_IQ3_S, kGU>(LU, grid, g, s);
+  }
 }
 
 struct HookScope {
