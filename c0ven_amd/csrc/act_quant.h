@@ -31,10 +31,21 @@ __device__ __forceinline__ uint64_t ld_tag(const uint64_t *p) {
 }
 __device__ __forceinline__ uint32_t tag_of(uint64_t v) { return (uint32_t)(v >> 32); }
 
-// 16 bytes coherently, as four words.
-__device__ __forceinline__ uint4 ld_co4(const void *p) {
-  const uint32_t *q = (const uint32_t *)p;
-  return make_uint4(ld_co(q), ld_co(q + 1), ld_co(q + 2), ld_co(q + 3));
+// 16 bytes at base + off (base uniform over the wave), read past the work-group's caches as the agent-scope loads
+// above are (the SC1 policy bit), in one request: a buffer load, whose resource is built from the uniform base.
+// Records written by single 8-byte stores stay whole in it (an aligned 16-byte piece of one cache line).
+__device__ __forceinline__ uint4 ld_co16(const void *base, uint32_t off) {
+  typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+  constexpr int kSc1 = 16;                   // cache policy: SC1 (agent-coherent)
+  constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer: 32-bit data format, no swizzle
+  const uint64_t b = (uint64_t)base;
+  // readfirstlane returns int: each half goes through uint32_t, or the low half would sign-extend into the high.
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint64_t bu = ((uint64_t)hi << 32) | lo;
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)bu, 0, 0xffffffffu, kRsrcWord3);
+  const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1);
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // A word of a quantised unit: to global memory (coherent, for other work-groups) or to LDS (for this one).

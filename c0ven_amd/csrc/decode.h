@@ -22,7 +22,8 @@ constexpr uint32_t max_groups(uint32_t T, uint32_t K) { return T * K + (T + MOE_
 //   top-k items      one a token (when routing): the shared gate's row, then softmax, top-k and weights;
 //   shared items     (when routing with a shared expert) the shared expert's gate/up then down items, for each chunk
 //                    of MOE_GROUP_MAX tokens: they need no routing, so they run beside the router;
-//   gate/up items    gate_up_rows(U) rows of gate and of up of one routed group, all units (lane = m * 32 + r * U + u);
+//   gate/up items    gate_up_rows(U) rows of gate and of up of one routed group, all units (wave w: matrix w % 2,
+//                    rows (w / 2) 64 / U .., lane = r * U + u);
 //   down items       down_rows(U_down) rows of down of one routed group (lane = r * U_down + u);
 //   combine items    one a (token, down row block): the token's outputs summed in rank order (after all down items).
 constexpr uint32_t kWG = 256;
@@ -46,6 +47,8 @@ constexpr uint32_t kDynStride = 64;   // words between two list counters
 // LDS after a group's activation units for the matrix-core gate/up item's exchanges (unit terms, then sums).
 constexpr uint32_t kMfmaXchBytes = (2 * 4 * 4 * 64 + 2 * 16 * 16) * 4;
 constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kWG / 64) * (32 / Ug); }
+// LDS after the activation units in which a dot4 gate/up item's up waves hand their row sums to the gate waves.
+constexpr uint32_t gate_up_xch_bytes(uint32_t Ug) { return gate_up_rows(Ug) * MOE_GROUP_MAX * 4; }
 constexpr uint32_t down_rows(uint32_t Ud) { return (kWG / 64) * (64 / Ud); }
 
 // Flags (64-bit, set to the launch's epoch): [i < kMaxLeadItems] lead item i is done (its quantised x is in, for

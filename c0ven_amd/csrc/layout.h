@@ -3,9 +3,11 @@
 //
 // A matrix of R rows x K values is a sequence of row tiles of 64 rows. A row's K values are U = K / 256 units (a
 // super-block of Q4_K or IQ3_S, eight blocks of Q8_0). Inside a tile the 64 U (row, unit) pairs are numbered
-// idx = row * U + unit, and each field of the format is stored idx-minor: piece p of pair idx at
-// field_base + (p * 64 U + idx) * piece_bytes, field_base being the earlier fields' bytes times 64 U. The decode
-// kernels give a lane one (row, unit) pair, so a wave's load of piece p reads consecutive pairs: one contiguous run.
+// unit-major, idx = unit * 64 + row (pair_idx), and each field of the format is stored idx-minor: piece p of pair idx
+// at field_base + (p * 64 U + idx) * piece_bytes, field_base being the earlier fields' bytes times 64 U. A wave's load
+// of piece p then reads whole runs: the matrix-core paths' 16 or 32 rows of one unit are 256 or 512 consecutive
+// bytes, the dot4 paths' eight rows of each unit (a row's units on consecutive lanes) a 128-byte line per unit. A
+// work item's rows of the U units lie 64 pieces apart, spread over more memory channels than one run would be.
 // The bytes are those of the file's blocks, permuted (nothing is decoded or re-rounded): the reference's runs layout
 // (shared/quant.h:1-4, core/load/runs.cpp:12-31) shaped for 64-wide wavefronts.
 //
@@ -32,6 +34,8 @@ constexpr uint32_t kTileRows = 64;  // rows per tile
 C0VEN_HD uint32_t unit_bytes(uint32_t type) {
   return type == QT_Q8_0 ? 272u : type == QT_Q4_K ? 144u : type == QT_IQ3_S ? 110u : 0u;
 }
+// The number of pair (row in tile, unit) inside its tile.
+C0VEN_HD uint32_t pair_idx(uint32_t row, uint32_t u) { return u * kTileRows + row; }
 // A tile of 64 rows x U units.
 C0VEN_HD uint64_t tile_bytes(uint32_t type, uint32_t U) { return (uint64_t)kTileRows * U * unit_bytes(type); }
 

@@ -35,7 +35,7 @@ struct Q4kRaw {
   __device__ __forceinline__ void load(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
     const uint32_t g = lane / 16, nl = kTileRows * U;
     const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q4_K, U);
-    const uint32_t ia = ((row0 % kTileRows) + lane % 16) * U + u;
+    const uint32_t ia = pair_idx((row0 % kTileRows) + lane % 16, u);
 #pragma unroll
     for (uint32_t c = 0; c < 4; c++)
       qs[c] = *(const uint2 *)(tile + ((uint64_t)(q4_kt::kQs / 16 + 2 * c + g / 2) * nl + ia) * 16 + 8 * (g % 2));
@@ -43,7 +43,7 @@ struct Q4kRaw {
     for (uint32_t i = 0; i < 3; i++) sc[i] = *(const uint32_t *)(tile + (uint64_t)q4_kt::kScales * nl + ((uint64_t)i * nl + ia) * 4);
 #pragma unroll
     for (uint32_t i = 0; i < 4; i++) {
-      const uint32_t id = ((row0 % kTileRows) + 4 * g + i) * U + u;
+      const uint32_t id = pair_idx((row0 % kTileRows) + 4 * g + i, u);
       dm[i] = *(const uint32_t *)(tile + (uint64_t)q4_kt::kDm * nl + (uint64_t)id * 4);
     }
   }

@@ -336,6 +336,8 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->groups = c->alloc<MoeGroup>(G);
     c->ngroups = c->alloc<uint32_t>(1);
     c->tok_need = c->alloc<uint32_t>(T);
+    // moe_decode reads h and the activation units at 32-bit byte offsets from their bases.
+    require((uint64_t)A * F * sizeof(uint64_t) <= 0xffffffffull, "n_ff x assignments too large for the decode path");
     c->h = c->alloc<uint64_t>((uint64_t)A * F);
     c->y_asg = c->alloc<uint64_t>((uint64_t)A * H);
     const uint64_t ncnt = 3 + 2 * kDynLists * kDynStride + kDynStride;
@@ -352,7 +354,8 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     clear_tagged(c, nullptr);
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
-    c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * Ug * kActLds + (Ug == 8 ? kMfmaXchBytes : 0),
+    c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * Ug * kActLds +
+                                   std::max<size_t>(Ug == 8 ? kMfmaXchBytes : 0, gate_up_xch_bytes(Ug)),
                                (size_t)MOE_GROUP_MAX * Ud * kActLds, kGroupingLds});
     int per_cu = 0, ncu = 0;
     uint32_t types = type_bit(g.gate_type) | type_bit(g.down_type);

@@ -22,7 +22,7 @@ __global__ void __launch_bounds__(64) moe_dequant(const uint8_t *mat, uint32_t t
   const uint8_t *tile = mat + (uint64_t)rt * tile_bytes(type, U);
   const bool live = row < rows;
   for (uint32_t u = 0; u < U; u++) {
-  const uint32_t idx = lane * U + u;
+  const uint32_t idx = pair_idx(lane, u);
   float *o = out + (uint64_t)row * k + u * kUnit;
   if (type == QT_Q8_0) {
     UnitQ8_0 w;

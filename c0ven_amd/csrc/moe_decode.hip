@@ -552,25 +552,28 @@ __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *un
                                           uint8_t *lds) {
   for (uint32_t i = tid(); i < n * U * (kActBytes / 16); i += kWG) {
     const uint32_t unit = i / (kActBytes / 16), c = i % (kActBytes / 16), j = unit / U, u = unit % U;
-    *(uint4 *)(lds + unit * kActLds + 16 * c) = ld_co4(act + ((uint64_t)unit_of_j[j] * U + u) * kActBytes + 16 * c);
+    *(uint4 *)(lds + unit * kActLds + 16 * c) = ld_co16(act, (unit_of_j[j] * U + u) * kActBytes + 16 * c);
   }
 }
 
 // h of the group's assignments quantised to the down's activation type straight into LDS: unit (j, u) at
 // (j U + u) kActLds, a half-wave a unit. The values are polled as tagged records (the gate/up items' stores are the
-// hand-off). Every down item of the group quantises the same h the same way.
+// hand-off), two records a 16-byte load. Every down item of the group quantises the same h the same way.
 __device__ __forceinline__ void stage_h(const DecodeParams &p, const GroupLds *sg, uint32_t dact, uint32_t U,
                                         uint8_t *lds) {
   const uint32_t l32 = tid() & 31u;
   wait_tag(p, p.h + (uint64_t)sg->asg[sg->n - 1] * p.F + p.F - 1);  // one record first, then all
   for (uint32_t i = tid() / 32; i < sg->n * U; i += kWG / 32) {
     const uint32_t j = i / U, u = i % U;
-    const uint64_t *src = p.h + (uint64_t)sg->asg[j] * p.F + u * kUnit + 8 * l32;
+    const uint32_t off = (sg->asg[j] * p.F + u * kUnit + 8 * l32) * (uint32_t)sizeof(uint64_t);
     uint64_t r[8];
     for (uint32_t n = 0;; n++) {
       bool ok = true;
 #pragma unroll
-      for (int k = 0; k < 8; k++) r[k] = ld_tag(src + k);
+      for (int k = 0; k < 4; k++) {
+        const uint4 v = ld_co16(p.h, off + 16 * k);
+        r[2 * k] = ((uint64_t)v.y << 32) | v.x, r[2 * k + 1] = ((uint64_t)v.w << 32) | v.z;
+      }
 #pragma unroll
       for (int k = 0; k < 8; k++) ok &= tag_of(r[k]) == p.tag;
       if (ok) break;
@@ -692,8 +695,9 @@ __device__ __forceinline__ void down_mfma(const DecodeParams &p, const GroupLds 
   if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
 }
 
-// Gate and up of rows blk * gate_up_rows .. of the group: lane = m * 32 + r * U + u; h = silu(g) * u per row, stored
-// as tagged records.
+// Gate and up of rows blk * gate_up_rows .. of the group: wave w takes matrix w % 2 and rows (w / 2) 64 / U .. (lane
+// r U + u), so that a load of one piece reads 64 / U consecutive rows of each unit (a whole line at U = 8); the up waves
+// hand their row sums to the gate waves through LDS, which store h = silu(g) * u per row as tagged records.
 template <uint32_t kTypes>
 __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupLds *sg, uint32_t blk, uint8_t *lds,
                                              uint32_t *grid_lds, const uint64_t *tab, uint64_t *mark) {
@@ -707,12 +711,12 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
     load_grid(grid_lds);
     __syncthreads();
   }
-  const uint32_t lane = lane_id(), m = lane / 32, r = (lane % 32) / U, u = lane % U;
-  const uint32_t row = row0 + wave_id() * (32 / U) + r;
+  const uint32_t lane = lane_id(), m = wave_id() & 1u, r = lane / U, u = lane % U;
+  const uint32_t rl = (wave_id() >> 1) * (64 / U) + r, row = row0 + rl;  // rl: the row within the item
   const uint8_t *mat = gm.mat + (m ? (gm.shared ? p.sh_up_off : p.ex_up_off) : 0);
   const uint8_t *tile = mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
   float t[MOE_GROUP_MAX];
-  pair_terms<kTypes>(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
+  pair_terms<kTypes>(gm.type, tile, pair_idx(row % kTileRows, u), kTileRows * U, grid_lds,
              (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
                // The shared expert's items run beside the router: x of their tokens is quantised by lead items
                // 8 c .. (their flags); routed groups exist only once every lead item is in.
@@ -721,13 +725,21 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
                __syncthreads();
                if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
              });
+  float *xs = (float *)(lds + MOE_GROUP_MAX * U * kActLds);  // up's row sums [row in item][token]
 #pragma unroll
   for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
     if (j >= n) break;
-    const float s = row_sum(t[j], U);        // gate's row sum in lanes m = 0, up's in m = 1
-    const float su = __shfl_xor(s, 32, 64);  // the other matrix's
-    if (m == 0 && u == 0)
-      st_tag(p.h + (uint64_t)sg->asg[j] * p.F + row, __float_as_uint(swiglu_one(s, su, p.swiglu_limit, tab)), p.tag);
+    t[j] = row_sum(t[j], U);  // the row's sum in every lane of the row
+    if (m == 1 && u == 0) xs[rl * MOE_GROUP_MAX + j] = t[j];
+  }
+  __syncthreads();
+  if (m == 0 && u == 0) {
+#pragma unroll
+    for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
+      if (j >= n) break;
+      st_tag(p.h + (uint64_t)sg->asg[j] * p.F + row,
+             __float_as_uint(swiglu_one(t[j], xs[rl * MOE_GROUP_MAX + j], p.swiglu_limit, tab)), p.tag);
+    }
   }
   if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
 }
@@ -749,7 +761,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
     const uint32_t row = row0 + wave_id() * (64 / U) + r;
     const uint8_t *tile = gm.mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
     float t[MOE_GROUP_MAX];
-    pair_terms<kTypes>(gm.type, tile, (row % kTileRows) * U + u, kTileRows * U, grid_lds,
+    pair_terms<kTypes>(gm.type, tile, pair_idx(row % kTileRows, u), kTileRows * U, grid_lds,
                (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
                  stage_h(p, sg, act_type<kTypes>(quant_vec_dot_type(gm.type)), U, lds);
                  __syncthreads();

@@ -511,9 +511,9 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   const uint32_t row = blockIdx.y * gemm_rows<kGU>() + (kGU ? 32 * (w & 1) : 32 * w) + n;
   const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
   const uint8_t *tile = M + (uint64_t)(row / kTileRows) * tile_bytes(kType, U);
-  const uint32_t idx0 = (row % kTileRows) * U, nl = kTileRows * U;
+  const uint32_t rr = row % kTileRows, nl = kTileRows * U;
   typename SliceOf<kType>::T s;  // this unit's weights; the next unit's are fetched while it is used
-  s.fetch(tile, idx0, nl, h);
+  s.fetch(tile, pair_idx(rr, 0), nl, h);
   ActStage stage;
   stage.load(g.act, arow_lds, U, 0);
   stage.store(abuf[0]);
@@ -532,7 +532,7 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
       typename SliceOf<kType>::T s_next;
       if (u + 1 < U) {
         stage.load(g.act, arow_lds, U, u + 1);
-        s_next.fetch(tile, idx0 + u + 1, nl, h);
+        s_next.fetch(tile, pair_idx(rr, u + 1), nl, h);
       }
       s.decode();
       const uint8_t *buf = abuf[u & 1];

@@ -46,7 +46,7 @@ inline void repack_matrix(uint32_t type, const uint8_t *src, uint32_t rows, uint
   for (uint32_t rt = 0; rt < nrt; rt++) {
     uint8_t *tile = dst + (uint64_t)rt * tb;
     for (uint32_t l = 0; l < kTileRows && rt * kTileRows + l < rows; l++)
-      for (uint32_t u = 0; u < U; u++) put_unit(tile, type, l * U + u, nl, file_unit(src, type, k, rt * kTileRows + l, u));
+      for (uint32_t u = 0; u < U; u++) put_unit(tile, type, pair_idx(l, u), nl, file_unit(src, type, k, rt * kTileRows + l, u));
   }
 }
 
