@@ -5,6 +5,7 @@
 
 #include "../../include/c0ven_moe_tile.h"
 #include "../../include/c0ven_quant.h"
+#include "layout.h"
 
 namespace c0ven {
 
@@ -47,6 +48,13 @@ constexpr uint32_t kDynStride = 64;   // words between two list counters
 // LDS after a group's activation units for the matrix-core gate/up item's exchanges (unit terms, then sums).
 constexpr uint32_t kMfmaXchBytes = (2 * 4 * 4 * 64 + 2 * 16 * 16) * 4;
 constexpr uint32_t gate_up_rows(uint32_t Ug) { return (kWG / 64) * (32 / Ug); }
+// Bytes between two tokens' activation units in LDS (a token's U units are kActLds apart): padded to an odd multiple
+// of 8 words modulo 32 banks, so that the matrix-core B operand's 16 tokens x 4 eight-byte pieces read at the
+// 4-way minimum (U = 8 unpadded puts every token on the same bank).
+constexpr uint32_t act_tok_stride(uint32_t U) {
+  return (U * (kActLds / 4) + (24 - (U * (kActLds / 4)) % 16) % 16) * 4;
+}
+static_assert(act_tok_stride(8) % 128 == 32 && act_tok_stride(2) == 2 * kActLds, "activation token stride");
 // LDS after the activation units in which a dot4 gate/up item's up waves hand their row sums to the gate waves.
 constexpr uint32_t gate_up_xch_bytes(uint32_t Ug) { return gate_up_rows(Ug) * MOE_GROUP_MAX * 4; }
 constexpr uint32_t down_rows(uint32_t Ud) { return (kWG / 64) * (64 / Ud); }

@@ -354,9 +354,9 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     clear_tagged(c, nullptr);
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
-    c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * Ug * kActLds +
+    c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * act_tok_stride(Ug) +
                                    std::max<size_t>(Ug == 8 ? kMfmaXchBytes : 0, gate_up_xch_bytes(Ug)),
-                               (size_t)MOE_GROUP_MAX * Ud * kActLds, kGroupingLds});
+                               (size_t)MOE_GROUP_MAX * act_tok_stride(Ud), kGroupingLds});
     int per_cu = 0, ncu = 0;
     uint32_t types = type_bit(g.gate_type) | type_bit(g.down_type);
     if (g.has_shared) types |= type_bit(g.sh_gate_type) | type_bit(g.sh_down_type);

@@ -547,18 +547,20 @@ __device__ __forceinline__ void read_group(const DecodeParams &p, const GroupTab
   __syncthreads();
 }
 
-// Activation units (act + unit index * kActBytes, coherent) of the group's assignments into LDS, kActLds apart.
+// Activation units (act + unit index * kActBytes, coherent) of the group's assignments into LDS: unit (j, u) at
+// j act_tok_stride(U) + u kActLds.
 __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *unit_of_j, uint32_t n, uint32_t U,
                                           uint8_t *lds) {
   for (uint32_t i = tid(); i < n * U * (kActBytes / 16); i += kWG) {
     const uint32_t unit = i / (kActBytes / 16), c = i % (kActBytes / 16), j = unit / U, u = unit % U;
-    *(uint4 *)(lds + unit * kActLds + 16 * c) = ld_co16(act, (unit_of_j[j] * U + u) * kActBytes + 16 * c);
+    *(uint4 *)(lds + j * act_tok_stride(U) + u * kActLds + 16 * c) =
+        ld_co16(act, (unit_of_j[j] * U + u) * kActBytes + 16 * c);
   }
 }
 
 // h of the group's assignments quantised to the down's activation type straight into LDS: unit (j, u) at
-// (j U + u) kActLds, a half-wave a unit. The values are polled as tagged records (the gate/up items' stores are the
-// hand-off), two records a 16-byte load. Every down item of the group quantises the same h the same way.
+// j act_tok_stride(U) + u kActLds, a half-wave a unit. The values are polled as tagged records (the gate/up items'
+// stores are the hand-off), two records a 16-byte load. Every down item of the group quantises the same h the same way.
 __device__ __forceinline__ void stage_h(const DecodeParams &p, const GroupLds *sg, uint32_t dact, uint32_t U,
                                         uint8_t *lds) {
   const uint32_t l32 = tid() & 31u;
@@ -586,7 +588,7 @@ __device__ __forceinline__ void stage_h(const DecodeParams &p, const GroupLds *s
     float v[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) v[k] = __uint_as_float((uint32_t)r[k]);
-    quant_unit<true>(v, l32, dact, lds + i * kActLds);
+    quant_unit<true>(v, l32, dact, lds + j * act_tok_stride(U) + u * kActLds);
   }
 }
 
@@ -623,7 +625,7 @@ __device__ __forceinline__ void gate_up_mfma(const DecodeParams &p, const GroupL
     Q4kA a;
     a.decode(raw[k], lane);
     ActB b;
-    b.load(lds + (j * U + u) * kActLds, lane);
+    b.load(lds + j * act_tok_stride(U) + u * kActLds, lane);
     float t[4];
     q4k_terms(a, b, t);
 #pragma unroll
@@ -673,7 +675,7 @@ __device__ __forceinline__ void down_mfma(const DecodeParams &p, const GroupLds 
 #pragma unroll
   for (uint32_t u = 0; u < U; u++) {
     ActB b;
-    b.load(lds + (j * U + u) * kActLds, lane);
+    b.load(lds + j * act_tok_stride(U) + u * kActLds, lane);
 #pragma unroll
     for (uint32_t tt = 0; tt < 2; tt++) {
       Q4kA a;
@@ -704,7 +706,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
   const uint32_t U = p.H / kUnit, rows = gate_up_rows(U), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 0);
   if (use_mfma<kTypes>(gm.type, U, 8, n)) {
-    gate_up_mfma(p, sg, gm, blk, lds, (float *)(lds + MOE_GROUP_MAX * U * kActLds), tab, mark);
+    gate_up_mfma(p, sg, gm, blk, lds, (float *)(lds + MOE_GROUP_MAX * act_tok_stride(U)), tab, mark);
     return;
   }
   if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
@@ -717,7 +719,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
   const uint8_t *tile = mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
   float t[MOE_GROUP_MAX];
   pair_terms<kTypes>(gm.type, tile, pair_idx(row % kTileRows, u), kTileRows * U, grid_lds,
-             (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
+             (const uint32_t *)lds + u * (kActLds / 4), act_tok_stride(U) / 4, n, t, [&] {
                // The shared expert's items run beside the router: x of their tokens is quantised by lead items
                // 8 c .. (their flags); routed groups exist only once every lead item is in.
                if (gm.shared && p.route) wait_flags(p, kFlagLead + sg->tok[0], n);
@@ -725,7 +727,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
                __syncthreads();
                if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
              });
-  float *xs = (float *)(lds + MOE_GROUP_MAX * U * kActLds);  // up's row sums [row in item][token]
+  float *xs = (float *)(lds + MOE_GROUP_MAX * act_tok_stride(U));  // up's row sums [row in item][token]
 #pragma unroll
   for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
     if (j >= n) break;
@@ -762,7 +764,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
     const uint8_t *tile = gm.mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
     float t[MOE_GROUP_MAX];
     pair_terms<kTypes>(gm.type, tile, pair_idx(row % kTileRows, u), kTileRows * U, grid_lds,
-               (const uint32_t *)lds + u * (kActLds / 4), U * (kActLds / 4), n, t, [&] {
+               (const uint32_t *)lds + u * (kActLds / 4), act_tok_stride(U) / 4, n, t, [&] {
                  stage_h(p, sg, act_type<kTypes>(quant_vec_dot_type(gm.type)), U, lds);
                  __syncthreads();
                  if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
@@ -831,7 +833,7 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, const GroupT
 }  // namespace
 
 // Grid: the work-groups of 256 the device holds at once; dynamic LDS: the larger of a group's activation units
-// (MOE_GROUP_MAX x units x kActLds) and the grouping's tables (kGroupingLds).
+// (MOE_GROUP_MAX x act_tok_stride) and the grouping's tables (kGroupingLds).
 template <uint32_t kTypes>
 __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) moe_decode(DecodeParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
