@@ -100,6 +100,29 @@ def test_forward_no_shared_and_swiglu_limit():
         blk.close()
 
 
+@pytest.mark.parametrize("tie", ["pairs", "all"])
+def test_routing_ties(tie):
+    """Exactly equal logits: the lower expert id ranks first (route.h's order). "pairs" makes experts 2i and 2i + 1
+    equal; "all" makes every logit of a token equal, so every key is a top-k candidate (K = 16, the most)."""
+    L = h.Layer(512, 256, 128, 16, moe.QT_Q8_0, moe.QT_Q8_0, seed=23)
+    E = L.E
+    if tie == "pairs":
+        L.router[1:E:2] = L.router[0:E:2]
+    else:
+        L.router[:E] = L.router[0]
+    blk = L.block(max_tokens=32)
+    L.upload(blk)
+    for T in (1, 5, 16, 24):  # 24: the prefill path
+        say("routing ties", tie, "T", T)
+        x = h.tokens(300 + T, T, 512)
+        y, ids, w = blk.forward(0, x)
+        yo, io, wo = L.oracle_forward(x)
+        if tie == "all":
+            assert (io == np.arange(16)).all()
+        check_block(y, ids, w, yo, io, wo)
+    blk.close()
+
+
 def routed_layer(types, T, seed, zipf, E=512, K=10, H=2048, F=512):
     """A full-size layer with only the experts x routes to drawn (the others stay zero on the device, never read)."""
     gt, dt, sgt, sdt = types
