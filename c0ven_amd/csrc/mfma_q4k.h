@@ -1,5 +1,6 @@
 // Q4_K weights against a group's activations on the matrix cores: 16 weight rows x 16 token columns x one unit (256
-// values) per set of v_mfma_i32_16x16x32_i8, with the same integers and fp32 steps as UnitQ4_K::term (units.h).
+// values) per set of v_mfma_i32_16x16x64_i8 (the codes) and v_mfma_i32_16x16x32_i8 (the minimum part), with the same
+// integers and fp32 steps as UnitQ4_K::term (units.h).
 //
 // Operand layout (one wave): lane l holds A row l % 16 and B column l % 16, bytes 8 g .. 8 g + 7 of each 32-value
 // block, g = l / 16; the result D[row][col] sits in lane 16 (row / 4) + col as element row % 4. Here A is the weights
@@ -133,13 +134,21 @@ struct ActB {
   }
 };
 
+// Two 8-byte operand pieces as one 16-byte operand of v_mfma_i32_16x16x64_i8.
+__device__ __forceinline__ v4i_t join2(long x, long y) {
+  return v4i_t{(int)x, (int)((uint64_t)x >> 32), (int)y, (int)((uint64_t)y >> 32)};
+}
+
 // The unit's terms t[i] (rows 4 g + i, token l % 16): fma(d ad, isum, -((dmin ad) imin)) as UnitQ4_K::term.
+// The code chains take two blocks per v_mfma_i32_16x16x64_i8 (blocks 2 c and 2 c + 1: a lane's eight bytes of each,
+// in A and in B alike, so every A byte still meets its own activation byte; the sum over K is the same integer).
 __device__ __forceinline__ void q4k_terms(const Q4kA &a, const ActB &b, float t[4]) {
   v4i_t dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0};
 #pragma unroll
-  for (int s = 0; s < 8; s++) {
-    dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.lo[s], b.q[s], dlo, 0, 0, 0);
-    dhi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.hi[s], b.q[s], dhi, 0, 0, 0);
+  for (int c = 0; c < 4; c++) {
+    const v4i_t bq = join2(b.q[2 * c], b.q[2 * c + 1]);
+    dlo = __builtin_amdgcn_mfma_i32_16x16x64_i8(join2(a.lo[2 * c], a.lo[2 * c + 1]), bq, dlo, 0, 0, 0);
+    dhi = __builtin_amdgcn_mfma_i32_16x16x64_i8(join2(a.hi[2 * c], a.hi[2 * c + 1]), bq, dhi, 0, 0, 0);
   }
   const v4i_t mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.mn, b.bh, v4i_t{0, 0, 0, 0}, 0, 0, 0);
   const v4i_t ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.mn, b.bl, v4i_t{0, 0, 0, 0}, 0, 0, 0);
