@@ -592,6 +592,13 @@ __device__ __forceinline__ void stage_h(const DecodeParams &p, const GroupLds *s
   }
 }
 
+// The q8_K units in LDS (n tokens x U) get their block sums split for the matrix cores' minimum part, once for the
+// work-group (ActB::put_split), instead of once per wave and unit.
+__device__ __forceinline__ void presplit(uint32_t n, uint32_t U, uint8_t *lds) {
+  if (tid() < n * U) ActB::put_split(lds + (tid() / U) * act_tok_stride(U) + (tid() % U) * kActLds);
+  __syncthreads();
+}
+
 // Groups of at least this many tokens take the matrix-core paths (Q4_K weights, 8 units a gate/up row, 2 a down row);
 // smaller ones the dot4 paths, where the 16 token columns of an MFMA would be mostly padding.
 constexpr uint32_t kMfmaMinTokens = 3;
@@ -616,6 +623,7 @@ __device__ __forceinline__ void gate_up_mfma(const DecodeParams &p, const GroupL
   if (gm.shared && p.route) wait_flags(p, kFlagLead + sg->tok[0], n);
   stage_act(gm.shared ? p.act_s : p.act_r, sg->tok, n, U, lds);
   __syncthreads();
+  presplit(n, U, lds);
   if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
   const uint32_t j = min(lane % 16, n - 1);
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -625,7 +633,7 @@ __device__ __forceinline__ void gate_up_mfma(const DecodeParams &p, const GroupL
     Q4kA a;
     a.decode(raw[k], lane);
     ActB b;
-    b.load(lds + j * act_tok_stride(U) + u * kActLds, lane);
+    b.load_presplit(lds + j * act_tok_stride(U) + u * kActLds, lane);
     float t[4];
     q4k_terms(a, b, t);
 #pragma unroll
@@ -669,13 +677,14 @@ __device__ __forceinline__ void down_mfma(const DecodeParams &p, const GroupLds 
     for (uint32_t u = 0; u < U; u++) raw[tt][u].load(gm.mat, U, row0 + 16 * tt, u, lane);
   stage_h(p, sg, QT_Q8_K, U, lds);
   __syncthreads();
+  presplit(n, U, lds);
   if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
   const uint32_t j = min(lane % 16, n - 1);
   float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
   for (uint32_t u = 0; u < U; u++) {
     ActB b;
-    b.load(lds + j * act_tok_stride(U) + u * kActLds, lane);
+    b.load_presplit(lds + j * act_tok_stride(U) + u * kActLds, lane);
 #pragma unroll
     for (uint32_t tt = 0; tt < 2; tt++) {
       Q4kA a;
