@@ -20,10 +20,10 @@ namespace c0ven {
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
-// Each byte of w (at most 15) times k (at most 7): two 16-bit products per word, no carry between bytes.
-__device__ __forceinline__ uint32_t mul_bytes(uint32_t w, uint32_t k) {
-  const u16x2_t a = __builtin_bit_cast(u16x2_t, w), b = {(unsigned short)k, (unsigned short)k};
-  return __builtin_bit_cast(uint32_t, a * b);
+// Each byte of w (at most 15) times k (at most 7, in both 16-bit halves of kk): two 16-bit products per word, no
+// carry between bytes.
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t w, uint32_t kk) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2_t, w) * __builtin_bit_cast(u16x2_t, kk));
 }
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
@@ -50,39 +50,39 @@ struct Q4kRaw {
   }
 };
 
-// The A operands of one tile-unit and its D rows' scales.
+// {byte b of v, 0, byte b of v, 0}: a byte as the two 16-bit halves of a packed multiplier.
+__device__ __forceinline__ uint32_t bcast_byte(uint32_t v, uint32_t b) {
+  return __builtin_amdgcn_perm(0u, v, 0x0c000c00u | (b << 16) | b);
+}
+
+// The A operands of one tile-unit and its D rows' scales. The six-bit scales and minima of the eight blocks are
+// unpacked four to a word (get_scale_min_k4 on all four bytes at once): blocks 0-3 are the low six bits of bytes
+// 0-3 (scales) and 4-7 (minima); blocks 4-7 take four bits from bytes 8-11 and their top two from the top bits of
+// bytes 0-3 (scales) and 4-7 (minima).
 struct Q4kA {
   long lo[8], hi[8], mn;
   float d[4], dmin[4];
   __device__ __forceinline__ void decode(const Q4kRaw &r, uint32_t lane) {
-    uint8_t b[12];
-#pragma unroll
-    for (int i = 0; i < 3; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) b[4 * i + j] = (uint8_t)(r.sc[i] >> (8 * j));
-    uint32_t sc[8], m[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) {  // get_scale_min_k4
-      if (j < 4) {
-        sc[j] = b[j] & 63u;
-        m[j] = b[j + 4] & 63u;
-      } else {
-        sc[j] = (b[j + 4] & 0xFu) | ((b[j - 4] >> 6) << 4);
-        m[j] = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
-      }
-    }
+    const uint32_t w0 = r.sc[0], w1 = r.sc[1], w2 = r.sc[2];
+    const uint32_t sc03 = w0 & 0x3f3f3f3fu, sc47 = (w2 & 0x0f0f0f0fu) | ((w0 >> 2) & 0x30303030u);
+    const uint32_t m03 = w1 & 0x3f3f3f3fu, m47 = ((w2 >> 4) & 0x0f0f0f0fu) | ((w1 >> 2) & 0x30303030u);
+    // Each scale split 8 hi + lo (three bits each), four blocks a word.
+    const uint32_t slo[2] = {sc03 & 0x07070707u, sc47 & 0x07070707u};
+    const uint32_t shi[2] = {(sc03 >> 3) & 0x07070707u, (sc47 >> 3) & 0x07070707u};
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const uint32_t w0 = r.qs[c].x, w1 = r.qs[c].y;
-      const uint32_t l0 = w0 & 0x0f0f0f0fu, l1 = w1 & 0x0f0f0f0fu;
-      const uint32_t h0 = (w0 >> 4) & 0x0f0f0f0fu, h1 = (w1 >> 4) & 0x0f0f0f0fu;
-      lo[2 * c] = pack2(mul_bytes(l0, sc[2 * c] & 7u), mul_bytes(l1, sc[2 * c] & 7u));
-      hi[2 * c] = pack2(mul_bytes(l0, sc[2 * c] >> 3), mul_bytes(l1, sc[2 * c] >> 3));
-      lo[2 * c + 1] = pack2(mul_bytes(h0, sc[2 * c + 1] & 7u), mul_bytes(h1, sc[2 * c + 1] & 7u));
-      hi[2 * c + 1] = pack2(mul_bytes(h0, sc[2 * c + 1] >> 3), mul_bytes(h1, sc[2 * c + 1] >> 3));
+      const uint32_t w0q = r.qs[c].x, w1q = r.qs[c].y;
+      const uint32_t l0 = w0q & 0x0f0f0f0fu, l1 = w1q & 0x0f0f0f0fu;
+      const uint32_t h0 = (w0q >> 4) & 0x0f0f0f0fu, h1 = (w1q >> 4) & 0x0f0f0f0fu;
+      const uint32_t bl = (2 * c) % 4, bh = (2 * c + 1) % 4, hw = c / 2;  // blocks 2 c, 2 c + 1: bytes, word
+      const uint32_t kl_lo = bcast_byte(slo[hw], bl), kl_hi = bcast_byte(shi[hw], bl);
+      const uint32_t kh_lo = bcast_byte(slo[hw], bh), kh_hi = bcast_byte(shi[hw], bh);
+      lo[2 * c] = pack2(mul_bytes(l0, kl_lo), mul_bytes(l1, kl_lo));
+      hi[2 * c] = pack2(mul_bytes(l0, kl_hi), mul_bytes(l1, kl_hi));
+      lo[2 * c + 1] = pack2(mul_bytes(h0, kh_lo), mul_bytes(h1, kh_lo));
+      hi[2 * c + 1] = pack2(mul_bytes(h0, kh_hi), mul_bytes(h1, kh_hi));
     }
-    const uint32_t m0 = m[0] | (m[1] << 8) | (m[2] << 16) | (m[3] << 24), m1 = m[4] | (m[5] << 8) | (m[6] << 16) | (m[7] << 24);
-    mn = lane < 16 ? pack2(m0, m1) : 0;
+    mn = lane < 16 ? pack2(m03, m47) : 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) d[i] = h2f((uint16_t)r.dm[i]), dmin[i] = h2f((uint16_t)(r.dm[i] >> 16));
   }

@@ -327,15 +327,19 @@ struct SliceQ4_K {
     const int s = 4 * (j & 1);
     const uint32_t w[4] = {(v.x >> s) & 0x0f0f0f0fu, (v.y >> s) & 0x0f0f0f0fu, (v.z >> s) & 0x0f0f0f0fu, (v.w >> s) & 0x0f0f0f0fu};
 #pragma unroll
-    for (int i = 0; i < 4; i++) rl[i] = (int)mul_bytes(w[i], lo), rh[i] = (int)mul_bytes(w[i], hi);
+    for (int i = 0; i < 4; i++) {
+      rl[i] = (int)mul_bytes(w[i], lo * 0x10001u);
+      rh[i] = (int)mul_bytes(w[i], hi * 0x10001u);
+    }
   }
   // Block j's codes times k (k <= 7).
   __device__ __forceinline__ v4i words_times(int j, uint32_t k) const {
     const uint4 v = q[j / 2];
     const int s = 4 * (j & 1);
     v4i r;  // two 16-bit products a word (v_pk_mul_lo_u16, full rate)
-    r[0] = (int)mul_bytes((v.x >> s) & 0x0f0f0f0fu, k), r[1] = (int)mul_bytes((v.y >> s) & 0x0f0f0f0fu, k);
-    r[2] = (int)mul_bytes((v.z >> s) & 0x0f0f0f0fu, k), r[3] = (int)mul_bytes((v.w >> s) & 0x0f0f0f0fu, k);
+    const uint32_t kk = k * 0x10001u;
+    r[0] = (int)mul_bytes((v.x >> s) & 0x0f0f0f0fu, kk), r[1] = (int)mul_bytes((v.y >> s) & 0x0f0f0f0fu, kk);
+    r[2] = (int)mul_bytes((v.z >> s) & 0x0f0f0f0fu, kk), r[3] = (int)mul_bytes((v.w >> s) & 0x0f0f0f0fu, kk);
     return r;
   }
 };
