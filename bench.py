@@ -63,6 +63,51 @@ class Hip:
     def sync(self):
         assert self.rt.hipDeviceSynchronize() == 0
 
+    def event(self):
+        e = C.c_void_p()
+        assert self.rt.hipEventCreate(C.byref(e)) == 0, "hipEventCreate"
+        return e
+
+    def record(self, e, stream):
+        assert self.rt.hipEventRecord(e, C.c_void_p(stream)) == 0, "hipEventRecord"
+
+    def elapsed_ms(self, a, b):
+        ms = C.c_float()
+        assert self.rt.hipEventElapsedTime(C.byref(ms), a, b) == 0, "hipEventElapsedTime"
+        return ms.value
+
+
+def timed_steps(hip, blk, steps_once, launches):
+    """The timed region of a decode run: the K steps bracketed by synchronisations, with one HIP event before and one
+    after them on the stream the kernel is launched on (the block's). moe_decode is the only kernel in the region, so
+    the events' elapsed time over its `launches` launches is its average launch duration (the gaps between launches
+    included). Events around every launch would put their own packets between the launches and slow the job."""
+    stream = blk.stream()
+    ea, eb = hip.event(), hip.event()
+    hip.sync()
+    t0 = time.perf_counter()
+    hip.record(ea, stream)
+    steps_once()
+    hip.record(eb, stream)
+    hip.sync()
+    t1 = time.perf_counter()
+    return t0, t1, {"moe_decode": hip.elapsed_ms(ea, eb) / launches}, launches
+
+
+def timed_steps_per_launch(hip, blk, steps_once):
+    """The timed region of a prefill run: the K steps bracketed by synchronisations, with HIP events around each
+    kernel launch on the block's stream (the library's timing hook) for the per-kernel averages; several kernels make
+    a prefill forward, so the events have to bracket each one."""
+    blk.set_timing(True)
+    hip.sync()
+    t0 = time.perf_counter()
+    steps_once()
+    hip.sync()
+    t1 = time.perf_counter()
+    ktimes, nf = blk.kernel_times()
+    blk.set_timing(False)
+    return t0, t1, ktimes, nf
+
 
 def measured_traffic(config):
     """HBM bytes per moe_decode launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes (copy-calibrated) and
@@ -145,15 +190,11 @@ def main():
     for i in range(args.warmup):
         blk.forward_async(i % n_layer, xd, T, yd)
     hip.sync()
-    blk.set_timing(True)
-    hip.sync()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        blk.forward_async(i % n_layer, xd, T, yd)
-    hip.sync()
-    t1 = time.perf_counter()
-    ktimes, nf = blk.kernel_times()
-    blk.set_timing(False)
+    def steps_once():
+        for i in range(args.steps):
+            blk.forward_async(i % n_layer, xd, T, yd)
+
+    t0, t1, ktimes, nf = timed_steps(hip, blk, steps_once, args.steps)
     ms_step = (t1 - t0) * 1e3 / args.steps
     tok_s = T * args.steps / (t1 - t0)
 
@@ -265,15 +306,15 @@ def stack(args, cfg, moe, h):
         for c0 in range(0, T, chunk):
             run(c0, min(chunk, T - c0))
     hip.sync()
-    blk.set_timing(True)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        for c0 in range(0, T, chunk):
-            run(c0, min(chunk, T - c0))
-    hip.sync()
-    t1 = time.perf_counter()
-    ktimes, nf = blk.kernel_times()
-    blk.set_timing(False)
+    def steps_once():
+        for _ in range(steps):
+            for c0 in range(0, T, chunk):
+                run(c0, min(chunk, T - c0))
+
+    if decode:
+        t0, t1, ktimes, nf = timed_steps(hip, blk, steps_once, steps * NL)
+    else:
+        t0, t1, ktimes, nf = timed_steps_per_launch(hip, blk, steps_once)
     ms_step = (t1 - t0) * 1e3 / steps
     tok_s = T * steps / (t1 - t0)
     ex_bytes = 2 * moe.row_bytes(gt, H) * F + moe.row_bytes(dt, F) * H
@@ -359,14 +400,11 @@ def prefill(args, cfg, moe, h):
     for _ in range(warmup):
         blk.forward_async(0, xd, T, yd)
     hip.sync()
-    blk.set_timing(True)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        blk.forward_async(0, xd, T, yd)
-    hip.sync()
-    t1 = time.perf_counter()
-    ktimes, nf = blk.kernel_times()
-    blk.set_timing(False)
+    def steps_once():
+        for _ in range(steps):
+            blk.forward_async(0, xd, T, yd)
+
+    t0, t1, ktimes, nf = timed_steps_per_launch(hip, blk, steps_once)
     ms_step = (t1 - t0) * 1e3 / steps
     tok_s = T * steps / (t1 - t0)
     # Algorithmic work: 2 FLOP per weight per assignment (gate, up, down), the shared expert per token,
