@@ -214,7 +214,8 @@ class MoeBlock:
         return lib.moe_stream(self.h)
 
     def set_timing(self, on):
-        self._check(lib.moe_set_timing(self.h, 1 if on else 0))
+        """on: False, True (every kernel) or 2 (only the decode kernel and the prefill gate/up launches)."""
+        self._check(lib.moe_set_timing(self.h, 2 if on == 2 else 1 if on else 0))
 
     def kernel_times(self):
         """{kernel: average ms per launch} over the forwards timed since timing was set (and clears them), and the

@@ -81,7 +81,7 @@ struct moe_ctx {
   uint32_t grid = 0;           // co-resident work-groups of moe_decode
   const void *kernel = nullptr;  // moe_decode for the context's set of weight types
   size_t lds = 0;              // its dynamic LDS
-  bool timing = false;
+  int timing = 0;  // 0 off, 1 every kernel, 2 the decode kernel and the prefill gate/up launches
   uint64_t *trace = nullptr;   // per-item stamps of the last forward, when tracing
   uint32_t trace_cap = 0, last_T = 0, last_route = 1;
   std::vector<hipEvent_t> ev;  // the event pool
@@ -181,6 +181,7 @@ hipEvent_t timing_event(moe_ctx *c, hipStream_t s) {
 }
 void timing_hook(void *ctx, const char *name, int after, hipStream_t s) {
   moe_ctx *c = (moe_ctx *)ctx;
+  if (c->timing == 2 && std::strcmp(name, "moe_decode") != 0 && std::strcmp(name, "pf_gate_up") != 0) return;
   if (!after) {
     c->timed.push_back(TimedLaunch{name, timing_event(c, s), nullptr});
   } else {
@@ -530,7 +531,8 @@ MOE_API void *moe_stream(moe_ctx *c) { return c ? (void *)c->stream : nullptr; }
 MOE_API moe_status moe_set_timing(moe_ctx *c, int on) {
   return guarded(c, [&] {
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    c->timing = on != 0;
+    require(on >= 0 && on <= 2, "timing must be 0, 1 or 2");
+    c->timing = on;
     c->ev_used = 0, c->ev_next = 0;
     c->timed.clear();
   });

@@ -123,9 +123,11 @@ MOE_API moe_status moe_sync(moe_ctx *ctx);
 MOE_API void *moe_stream(moe_ctx *ctx);
 
 /* Per-kernel timing with HIP events recorded on the stream each kernel runs on, around every launch of every forward
- * while on (off by default; turning it on or off clears the record). moe_kernel_times waits for the recorded
- * forwards, gives each kernel's average duration per launch over them (names and avg_ms have room for cap entries;
- * n receives how many kernels, forwards how many forwards were averaged) and clears the record. */
+ * while on (off by default; turning it on or off clears the record). on = 1 times every kernel; on = 2 only the
+ * decode kernel and the prefill gate/up launches (each event pair puts packets between the launches, so fewer pairs
+ * disturb a timed run less). moe_kernel_times waits for the recorded forwards, gives each kernel's average duration
+ * per launch over them (names and avg_ms have room for cap entries; n receives how many kernels, forwards how many
+ * forwards were averaged) and clears the record. */
 MOE_API moe_status moe_set_timing(moe_ctx *ctx, int on);
 MOE_API moe_status moe_kernel_times(moe_ctx *ctx, const char **names, float *avg_ms, uint32_t cap, uint32_t *n,
                                     uint32_t *forwards);
