@@ -220,11 +220,12 @@ class MoeBlock:
     def kernel_times(self):
         """{kernel: average ms per launch} over the forwards timed since timing was set (and clears them), and the
         number of forwards."""
-        names = (C.c_char_p * 8)()
-        ms = (C.c_float * 8)()
+        cap = 32
+        names = (C.c_char_p * cap)()
+        ms = (C.c_float * cap)()
         n, nf = C.c_uint32(), C.c_uint32()
-        self._check(lib.moe_kernel_times(self.h, names, ms, 8, C.byref(n), C.byref(nf)))
-        return {names[i].decode(): ms[i] for i in range(n.value)}, nf.value
+        self._check(lib.moe_kernel_times(self.h, names, ms, cap, C.byref(n), C.byref(nf)))
+        return {names[i].decode(): ms[i] for i in range(min(n.value, cap))}, nf.value
 
     def set_trace(self, on):
         self._check(lib.moe_set_trace(self.h, 1 if on else 0))

@@ -181,7 +181,7 @@ hipEvent_t timing_event(moe_ctx *c, hipStream_t s) {
 }
 void timing_hook(void *ctx, const char *name, int after, hipStream_t s) {
   moe_ctx *c = (moe_ctx *)ctx;
-  if (c->timing == 2 && std::strcmp(name, "moe_decode") != 0 && std::strcmp(name, "pf_gate_up") != 0) return;
+  if (c->timing == 2 && std::strcmp(name, "moe_decode") != 0 && std::strncmp(name, "pf_gate_up", 10) != 0) return;
   if (!after) {
     c->timed.push_back(TimedLaunch{name, timing_event(c, s), nullptr});
   } else {
@@ -324,6 +324,9 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
         b.h_sh = c->alloc<float>((uint64_t)TM * F);
         b.hact_sh = c->alloc<uint8_t>((uint64_t)TM * Ud * kActBytes);
         b.y_sh = c->alloc<float>((uint64_t)TM * H);
+        check(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking), "hipStreamCreate");
+        check(hipEventCreateWithFlags(&b.fork, hipEventDisableTiming), "hipEventCreate");
+        check(hipEventCreateWithFlags(&b.join, hipEventDisableTiming), "hipEventCreate");
       }
     }
     c->act_r = c->alloc<uint8_t>((uint64_t)T * Ug * kActBytes);
@@ -384,8 +387,12 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
 MOE_API void moe_close(moe_ctx *c) {
   if (!c) return;
   if (c->stream) (void)hipStreamSynchronize(c->stream);
+  if (c->pf.side) (void)hipStreamSynchronize(c->pf.side);
   for (void *p : c->allocs) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  if (c->pf.fork) (void)hipEventDestroy(c->pf.fork);
+  if (c->pf.join) (void)hipEventDestroy(c->pf.join);
+  if (c->pf.side) (void)hipStreamDestroy(c->pf.side);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }

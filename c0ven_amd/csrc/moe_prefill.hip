@@ -907,6 +907,33 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     pf_quant_rows<<<(T * Ug + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(x, H, T, Ug, xr, b.act_r, xs,
                                                                             b.act_s != b.act_r ? b.act_s : nullptr);
   }
+  const uint32_t mt = pf_max_tiles(T, K, E), st_tiles = (T + MOE_TILE - 1) / MOE_TILE;
+  if (S.has_shared) {  // the shared expert needs no routing: its launches run beside the router on the side stream
+    hipStream_t ss = b.side;
+    if (hipEventRecord(b.fork, st) != hipSuccess || hipStreamWaitEvent(ss, b.fork, 0) != hipSuccess)
+      return hipGetLastError();
+    {
+      HookScope k(hook, "pf_gate_up_shared", ss);
+      PfGemm q{};
+      q.shared_T = T, q.K = K, q.act = b.act_s, q.act_by_pos = 0;
+      q.mat = L.shared, q.stride = 0, q.up_off = L.sh_up_off, q.out = b.h_sh, q.out_ld = F;
+      q.limit = S.swiglu_limit;
+      launch_gemm<true>(S.sh_gate_type, Ug, dim3(st_tiles, F / gemm_rows<true>()), q, ss);
+    }
+    {
+      HookScope k(hook, "pf_quant_h_shared", ss);
+      pf_quant_rows<<<(T * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, ss>>>(b.h_sh, F, T, Ud, hs, b.hact_sh, 0,
+                                                                            nullptr);
+    }
+    {
+      HookScope k(hook, "pf_down_shared", ss);
+      PfGemm q{};
+      q.shared_T = T, q.K = K, q.act = b.hact_sh, q.act_by_pos = 1;
+      q.mat = L.shared + L.sh_down_off, q.stride = 0, q.out = b.y_sh, q.out_ld = H;
+      launch_gemm<false>(S.sh_down_type, Ud, dim3(st_tiles, H / gemm_rows<false>()), q, ss);
+    }
+    if (hipEventRecord(b.join, ss) != hipSuccess) return hipGetLastError();
+  }
   {
     HookScope k(hook, "pf_router", st);
     pf_router<<<dim3((T + 63) / 64, (E + 63) / 64 + 1), kPfWG, 0, st>>>(x, T, L.router, L.bias, E, H, b.logits);
@@ -919,7 +946,6 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     HookScope k(hook, "pf_dispatch", st);
     pf_dispatch<<<1, kDispWG, 0, st>>>(b.ids, T, K, E, b.perm, b.inv, b.tiles, b.ntiles);
   }
-  const uint32_t mt = pf_max_tiles(T, K, E), st_tiles = (T + MOE_TILE - 1) / MOE_TILE;
   {
     HookScope k(hook, "pf_gate_up", st);
     PfGemm g{};
@@ -927,20 +953,11 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     g.mat = L.experts, g.stride = L.ex_bytes, g.up_off = L.ex_up_off, g.out = b.h, g.out_ld = F;
     g.limit = S.swiglu_limit;
     launch_gemm<true>(S.gate_type, Ug, dim3(mt, F / gemm_rows<true>()), g, st);
-    if (S.has_shared) {
-      PfGemm q = g;
-      q.tiles = nullptr, q.ntiles = nullptr, q.shared_T = T, q.perm = nullptr, q.act = b.act_s;
-      q.mat = L.shared, q.stride = 0, q.up_off = L.sh_up_off, q.out = b.h_sh;
-      launch_gemm<true>(S.sh_gate_type, Ug, dim3(st_tiles, F / gemm_rows<true>()), q, st);
-    }
   }
   {
     HookScope k(hook, "pf_quant_h", st);
     pf_quant_rows<<<(T * K * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(b.h, F, T * K, Ud, hr, b.hact, 0,
                                                                               nullptr);
-    if (S.has_shared)
-      pf_quant_rows<<<(T * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(b.h_sh, F, T, Ud, hs, b.hact_sh, 0,
-                                                                            nullptr);
   }
   {
     HookScope k(hook, "pf_down", st);
@@ -948,13 +965,8 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     g.tiles = b.tiles, g.ntiles = b.ntiles, g.K = K, g.act = b.hact, g.act_by_pos = 1;
     g.mat = L.experts + L.ex_down_off, g.stride = L.ex_bytes, g.out = b.y_asg, g.out_ld = H;
     launch_gemm<false>(S.down_type, Ud, dim3(mt, H / gemm_rows<false>()), g, st);
-    if (S.has_shared) {
-      PfGemm q = g;
-      q.tiles = nullptr, q.ntiles = nullptr, q.shared_T = T, q.act = b.hact_sh;
-      q.mat = L.shared + L.sh_down_off, q.stride = 0, q.out = b.y_sh;
-      launch_gemm<false>(S.sh_down_type, Ud, dim3(st_tiles, H / gemm_rows<false>()), q, st);
-    }
   }
+  if (S.has_shared && hipStreamWaitEvent(st, b.join, 0) != hipSuccess) return hipGetLastError();
   {
     HookScope k(hook, "pf_combine", st);
     const uint64_t n = (uint64_t)T * (H / 4);
