@@ -194,15 +194,23 @@ __global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T
 
 constexpr uint32_t kDispWG = 1024;
 
+constexpr uint32_t kDispCache = 40960;  // ids the dispatch keeps in LDS (T K up to 40960: 2048 tokens at k <= 20)
+
 __global__ void __launch_bounds__(kDispWG) pf_dispatch(const int32_t *ids, uint32_t T, uint32_t K, uint32_t E,
                                                        uint32_t *perm, uint32_t *inv, MoeTile *tiles,
                                                        uint32_t *ntiles) {
   __shared__ uint32_t cnt[512], base[512], tb[512];
   __shared__ unsigned long long mask[512];
+  __shared__ uint16_t ids_lds[kDispCache];  // the ids, when they fit (the position pass reads them again)
   const uint32_t tid = threadIdx.x, n = T * K;
+  const bool cached = n <= kDispCache;
   if (tid < 512) cnt[tid] = 0u;
   __syncthreads();
-  for (uint32_t a = tid; a < n; a += kDispWG) atomicAdd(&cnt[ids[a]], 1u);
+  for (uint32_t a = tid; a < n; a += kDispWG) {
+    const uint32_t e = (uint32_t)ids[a];
+    atomicAdd(&cnt[e], 1u);
+    if (cached) ids_lds[a] = (uint16_t)e;
+  }
   __syncthreads();
   // Inclusive scans (Hillis-Steele) of the counts and of the tiles per expert.
   uint32_t c = tid < E ? cnt[tid] : 0u, nt = (c + MOE_TILE - 1) / MOE_TILE;
@@ -234,7 +242,7 @@ __global__ void __launch_bounds__(kDispWG) pf_dispatch(const int32_t *ids, uint3
     const bool on = tid < 64 * K && a < n;
     uint32_t e = 0, bit = 0;
     if (on) {
-      e = (uint32_t)ids[a], bit = a / K - t0;
+      e = cached ? (uint32_t)ids_lds[a] : (uint32_t)ids[a], bit = a / K - t0;
       atomicOr(&mask[e], 1ull << bit);
     }
     __syncthreads();
