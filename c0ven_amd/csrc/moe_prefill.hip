@@ -2,9 +2,10 @@
 // the combine. The kernel list and its reference counterparts are in prefill.h.
 //
 // Bits: every result equals the CPU oracle's (its ORACLE ORDER). The router sums exact bf16 products in fp64 in k
-// order, as the oracle does. The expert GEMMs take each 32-value block's integer dot product from one
-// v_mfma_i32_32x32x32_i8 (exact), then apply the block's integer scale (Q4_K, IQ3_S) or fp32 term (Q8_0) and each
-// unit's fp32 steps exactly as the decoders in units.h do, and add a row's units in sequence, as the oracle does.
+// order, as the oracle does. The Q8_0 and IQ3_S expert GEMMs (pf_gemm) take each 32-value block's integer dot product
+// from one v_mfma_i32_32x32x32_i8 (exact), then apply the block's integer scale (IQ3_S) or fp32 term (Q8_0); the Q4_K
+// ones (pf_gemm_q4k) take the unit's integer sums from the 16 x 16 tiles of mfma_q4k.h. Both then follow each unit's
+// fp32 steps exactly as the decoders in units.h do, and add a row's units in sequence, as the oracle does.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -297,61 +298,6 @@ struct SliceQ8_0 {
   __device__ __forceinline__ v4i words(int j) const { return as_v4i(q[j]); }
 };
 
-struct SliceQ4_K {
-  uint4 q[4];  // qs pieces 2 c + h: bytes 32 c + 16 h .. + 15, low nibbles block 2 c, high nibbles block 2 c + 1
-  uint32_t sw[3], dm;
-  int sc[8], mn[8];
-  float d, dmin;
-  __device__ __forceinline__ void fetch(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h) {
-#pragma unroll
-    for (int c = 0; c < 4; c++) q[c] = *pf_field<uint4>(tile, q4_kt::kQs, 2 * c + h, idx, nl);
-#pragma unroll
-    for (int i = 0; i < 3; i++) sw[i] = *pf_field<uint32_t>(tile, q4_kt::kScales, i, idx, nl);
-    dm = *pf_field<uint32_t>(tile, q4_kt::kDm, 0, idx, nl);
-  }
-  __device__ __forceinline__ void decode() {
-    uint8_t b[12];
-#pragma unroll
-    for (int i = 0; i < 3; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) b[4 * i + j] = (uint8_t)(sw[i] >> (8 * j));
-#pragma unroll
-    for (int j = 0; j < 8; j++) {  // get_scale_min_k4
-      if (j < 4) {
-        sc[j] = b[j] & 63;
-        mn[j] = b[j + 4] & 63;
-      } else {
-        sc[j] = (b[j + 4] & 0xF) | ((b[j - 4] >> 6) << 4);
-        mn[j] = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
-      }
-    }
-    d = h2f((uint16_t)dm);
-    dmin = h2f((uint16_t)(dm >> 16));
-  }
-  // Block j's codes times lo and hi (each <= 7; every byte stays below 106, so the products carry nothing across
-  // bytes), the nibbles extracted once for both.
-  __device__ __forceinline__ void words_times2(int j, uint32_t lo, uint32_t hi, v4i &rl, v4i &rh) const {
-    const uint4 v = q[j / 2];
-    const int s = 4 * (j & 1);
-    const uint32_t w[4] = {(v.x >> s) & 0x0f0f0f0fu, (v.y >> s) & 0x0f0f0f0fu, (v.z >> s) & 0x0f0f0f0fu, (v.w >> s) & 0x0f0f0f0fu};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      rl[i] = (int)mul_bytes(w[i], lo * 0x10001u);
-      rh[i] = (int)mul_bytes(w[i], hi * 0x10001u);
-    }
-  }
-  // Block j's codes times k (k <= 7).
-  __device__ __forceinline__ v4i words_times(int j, uint32_t k) const {
-    const uint4 v = q[j / 2];
-    const int s = 4 * (j & 1);
-    v4i r;  // two 16-bit products a word (v_pk_mul_lo_u16, full rate)
-    const uint32_t kk = k * 0x10001u;
-    r[0] = (int)mul_bytes((v.x >> s) & 0x0f0f0f0fu, kk), r[1] = (int)mul_bytes((v.y >> s) & 0x0f0f0f0fu, kk);
-    r[2] = (int)mul_bytes((v.z >> s) & 0x0f0f0f0fu, kk), r[3] = (int)mul_bytes((v.w >> s) & 0x0f0f0f0fu, kk);
-    return r;
-  }
-};
-
 struct SliceIQ3_S {
   uint32_t qs[8], sg[8], qh[2], scw;  // qs[ib]: the four grid-index bytes of block ib's half h (groups 8 ib + 4 h ..)
   uint16_t dh;
@@ -401,10 +347,6 @@ struct SliceOf;
 template <>
 struct SliceOf<QT_Q8_0> {
   using T = SliceQ8_0;
-};
-template <>
-struct SliceOf<QT_Q4_K> {
-  using T = SliceQ4_K;
 };
 template <>
 struct SliceOf<QT_IQ3_S> {
@@ -474,23 +416,6 @@ struct ActStage {
     }
   }
 };
-
-// Q4_K's minimum part as MFMA: imin[m][row] = sum_j bsum_j(m) mn_j(row), with bsum_j = 64 hi_j + lo_j (hi in
-// [-64, 63], lo in [0, 63], both int8). Lanes of half 0 give A = (hi_0..7, lo_0..7) and B = (mn_0..7, 0 x 8) for the hi
-// product or (0 x 8, mn_0..7) for the lo product; lanes of half 1 give zeros (values 16..31).
-__device__ __forceinline__ v4i bsum_split(const uint8_t *unit) {
-  const uint4 a = *(const uint4 *)(unit + kActSums), b = *(const uint4 *)(unit + kActSums + 16);
-  const int bs[8] = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
-  uint32_t hi[2] = {0, 0}, lo[2] = {0, 0};
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    hi[j / 4] |= ((uint32_t)(bs[j] >> 6) & 0xffu) << (8 * (j % 4));
-    lo[j / 4] |= ((uint32_t)(bs[j] & 63)) << (8 * (j % 4));
-  }
-  v4i r;
-  r[0] = (int)hi[0], r[1] = (int)hi[1], r[2] = (int)lo[0], r[3] = (int)lo[1];
-  return r;
-}
 
 template <uint32_t kType, uint32_t kLU, bool kGU>
 __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
@@ -593,46 +518,6 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
                 }
               }
             }
-          }
-        }
-      } else if constexpr (kType == QT_Q4_K) {
-        // isum = sum_j sc_j (q . a)_j with sc_j = 8 hi_j + lo_j: the scale is folded into the weights (q lo_j and
-        // q hi_j, each below 106 a byte) and both products accumulate over the eight blocks inside the MFMA, exactly.
-        v4i bmh, bml;  // the minimum part's B operands
-        {
-          uint32_t m0 = 0, m1 = 0;
-#pragma unroll
-          for (int j = 0; j < 8; j++) (j < 4 ? m0 : m1) |= (uint32_t)s.mn[j] << (8 * (j % 4));
-          const bool z = h != 0;
-          bmh[0] = z ? 0 : (int)m0, bmh[1] = z ? 0 : (int)m1, bmh[2] = 0, bmh[3] = 0;
-          bml[0] = 0, bml[1] = 0, bml[2] = z ? 0 : (int)m0, bml[3] = z ? 0 : (int)m1;
-        }
-        v16i dhi[2] = {v16i{}, v16i{}}, dlo[2] = {v16i{}, v16i{}};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          v4i bl, bh;
-        s.words_times2(j, (uint32_t)s.sc[j] & 7u, (uint32_t)s.sc[j] >> 3, bl, bh);
-#pragma unroll
-          for (int b = 0; b < kNB; b++) {
-            const v4i aw = as_v4i(*(const uint4 *)((b ? arow1 : arow0) + 32 * j));
-            dlo[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bl, dlo[b], 0, 0, 0);
-            dhi[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bh, dhi[b], 0, 0, 0);
-          }
-        }
-#pragma unroll
-        for (int b = 0; b < kNB; b++) {
-          const uint8_t *ar = b ? arow1 : arow0;
-          v4i am = bsum_split(ar - 16 * h);
-          if (h) am = v4i{0, 0, 0, 0};
-          const v16i dh = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bmh, v16i{}, 0, 0, 0);
-          const v16i dl = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bml, v16i{}, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const int isum = 8 * dhi[b][r] + dlo[b][r], imin = 64 * dh[r] + dl[r];
-            const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
-            const float dd = __fmul_rn(s.d, ad), dm = __fmul_rn(s.dmin, ad);
-            const float pm = __fmul_rn(dm, (float)imin);
-            acc[b][r] = __fadd_rn(acc[b][r], __builtin_fmaf(dd, (float)isum, -pm));
           }
         }
       } else {
