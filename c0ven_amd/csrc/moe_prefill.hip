@@ -604,10 +604,15 @@ __device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
 // UnitQ4_K::term, units added in sequence. Its accumulators are a quarter of the 32 x 32 kernel's, so three
 // work-groups share a CU.
 template <uint32_t kLU, bool kGU>
-__global__ void __launch_bounds__(kPfWG) pf_gemm_q4k(PfGemm g) {
+__global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3))) pf_gemm_q4k(PfGemm g) {
   constexpr uint32_t U = 1u << kLU, kRows = kGU ? 32 : 64;
-  __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
-  __shared__ float ub[kGU ? 32 : 1][65];  // up sums [row][position]
+  // One activation buffer, refilled after every wave is done with the unit, and the next unit's activations loaded
+  // only after the unit's MFMAs: their registers are not live across the compute, so three waves fit a SIMD (two
+  // with a second buffer and the loads issued a unit ahead; measured slower).
+  __shared__ __align__(16) uint8_t abuf[64 * kActLds];
+  // Up sums [row][position], written after the unit loop's last barrier: they reuse the activation buffer.
+  static_assert(32 * 65 * sizeof(float) <= 64 * kActLds, "ub must fit in one activation buffer");
+  float(*ub)[65] = reinterpret_cast<float(*)[65]>(abuf);
   __shared__ uint32_t arow_lds[64];
   __shared__ uint64_t tab[32];
   // 1-D grid of (tile, row block) pairs, the row block fastest in the XCD-aware logical index over the pairs that
@@ -643,7 +648,7 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm_q4k(PfGemm g) {
   raw.load(M, U, row0, 0, lane_id());
   ActStage stage;
   stage.load(g.act, arow_lds, U, 0);
-  stage.store_split(abuf[0]);
+  stage.store_split(abuf);
   __syncthreads();
   float acc[4][4];
 #pragma unroll
@@ -654,12 +659,11 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm_q4k(PfGemm g) {
   for (uint32_t u = 0; u < U; u++) {
     Q4kRaw next;
     if (u + 1 < U) {
-      stage.load(g.act, arow_lds, U, u + 1);
       next.load(M, U, row0, u + 1, lane_id());
     }
+    const uint8_t *buf = abuf;
     Q4kA a;
     a.decode(raw, lane_id());
-    const uint8_t *buf = abuf[u & 1];
 #pragma unroll
     for (uint32_t pt = 0; pt < 4; pt++) {
       if (pt < npt) {
@@ -672,7 +676,9 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm_q4k(PfGemm g) {
       }
     }
     if (u + 1 < U) {
-      stage.store_split(abuf[(u + 1) & 1]);
+      stage.load(g.act, arow_lds, U, u + 1);
+      __syncthreads();  // every wave is done with the buffer before it is overwritten
+      stage.store_split(abuf);
       raw = next;
     }
     __syncthreads();
@@ -751,6 +757,18 @@ void launch_gemm_lu(uint32_t LU, dim3 grid, const PfGemm &g, hipStream_t s) {
 }
 
 template <bool kGU>
+void launch_q4k_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
+  switch (LU) {
+    case 0: pf_gemm_q4k<0, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    case 1: pf_gemm_q4k<1, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    case 2: pf_gemm_q4k<2, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    case 3: pf_gemm_q4k<3, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    case 4: pf_gemm_q4k<4, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    default: pf_gemm_q4k<5, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+  }
+}
+
+template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
   uint32_t LU = 0;
   while ((1u << LU) < U) LU++;
@@ -760,14 +778,7 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
     PfGemm q = g;
     q.row_blocks = grid.y * gemm_rows<kGU>() / (kGU ? 32 : 64);
     const dim3 g2(grid.x * q.row_blocks);
-    switch (LU) {
-      case 0: pf_gemm_q4k<0, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-      case 1: pf_gemm_q4k<1, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-      case 2: pf_gemm_q4k<2, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-      case 3: pf_gemm_q4k<3, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-      case 4: pf_gemm_q4k<4, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-      default: pf_gemm_q4k<5, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    }
+    launch_q4k_lu<kGU>(LU, g2, q, s);
   }
   else {
     launch_gemm_lu<QT_IQ3_S, kGU>(LU, grid, g, s);
