@@ -125,6 +125,16 @@ def measured_traffic(config):
         return None
 
 
+def measured_prefill_traffic(config):
+    """HBM bytes per routed gate/up launch (copy-calibrated FETCH_SIZE + WRITE_SIZE) recorded in
+    profiles/traffic_prefill.json; None if not measured for this config."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic_prefill.json")) as f:
+            return json.load(f)["pf_gate_up"][config]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -454,7 +464,8 @@ def prefill(args, cfg, moe, h):
         "config": {"workload": cfg["name"], "n_embd": H, "n_ff": F, "n_expert": E, "n_used": K, "shared": True,
                    "tokens": T, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]], "touched_experts": touched},
         "roofline": {"bound": "mfma", "kernel": "pf_gate_up", "achieved": round(gu_tops, 2), "peak": INT8_PEAK_TOPS,
-                     "unit": "TFLOP/s", "frac": round(gu_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(gu_tops / INT8_PEAK_TOPS, 4),
+                     "traffic": measured_prefill_traffic(args.config),
                      "algorithmic_flop_per_launch": gu_routed_flop, "avg_launch_ms": round(gu_ms, 4)},
         "block": {"tflops": round(block_flop / (ms_step * 1e-3) / 1e12, 2),
                   "hbm_gbs": round(block_bytes / (ms_step * 1e-3) / 1e9, 1),
