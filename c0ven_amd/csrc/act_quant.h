@@ -61,7 +61,7 @@ __device__ __forceinline__ void put_word(uint8_t *out, uint32_t off, T v) {
 // One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
 // with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0). out is in global
 // memory, or in LDS when kLds.
-template <bool kLds = false>
+template <bool kLds = false, bool kSplitG = false>
 __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
   uint32_t code[2] = {0u, 0u};
   if (act_type == QT_Q8_K) {
@@ -98,6 +98,13 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
     put_word<kLds>(out, 8 * l32 + 4, code[1]);
     if ((l32 & 3u) == 0) put_word<kLds>(out, kActSums + l32, part);
     if (l32 == 0) put_word<kLds>(out, kActScales, d);
+    if constexpr (kSplitG) {
+      // Block sum j = l32 / 4 split as 64 hi + lo (hi in [-64, 63], lo in [0, 63]) into the padding at kActSplitG.
+      if ((l32 & 3u) == 0) {
+        out[kActSplitG + l32 / 4] = (uint8_t)((uint32_t)(part >> 6) & 0xffu);
+        out[kActSplitG + 8 + l32 / 4] = (uint8_t)((uint32_t)part & 63u);
+      }
+    }
   } else {  // q8_0: blocks of 32, four lanes each
     float amax = 0.0f;
 #pragma unroll

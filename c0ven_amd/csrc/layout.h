@@ -60,5 +60,8 @@ C0VEN_HD uint64_t matrix_bytes(uint32_t type, uint32_t rows, uint32_t k) {
 constexpr uint32_t kActBytes = 320, kActScales = 256, kActSums = 288, kActLds = 336;
 // In LDS the 16 bytes of padding after a unit may hold its sums split for the Q4_K minimum MFMA (hi bytes, lo bytes).
 constexpr uint32_t kActSplit = 320;
+// In a q8_K unit in global memory written by the prefill quantiser, bytes 272-287 of the padding hold the same split
+// of the block sums (hi bytes of sums 0-7, then lo bytes), so that a unit can be copied to LDS verbatim.
+constexpr uint32_t kActSplitG = 272;
 
 }  // namespace c0ven

@@ -100,12 +100,13 @@ struct ActB {
     split_sums(unit, g);
     ad = *(const float *)(unit + kActScales);
   }
-  // The same, with the sums' split already in the unit's LDS padding (kActSplit, written by put_split).
-  __device__ __forceinline__ void load_presplit(const uint8_t *unit, uint32_t lane) {
+  // The same, with the sums' split already in the unit's padding (at split: kActSplit, written by put_split, or
+  // kActSplitG, written by the prefill quantiser).
+  __device__ __forceinline__ void load_presplit(const uint8_t *unit, uint32_t lane, uint32_t split = kActSplit) {
     const uint32_t g = lane / 16;
 #pragma unroll
     for (int s = 0; s < 8; s++) q[s] = *(const long *)(unit + 32 * s + 8 * g);
-    const uint4 v = *(const uint4 *)(unit + kActSplit);
+    const uint4 v = *(const uint4 *)(unit + split);
     bh = g == 0 ? pack2(v.x, v.y) : 0;
     bl = g == 0 ? pack2(v.z, v.w) : 0;
     ad = *(const float *)(unit + kActScales);

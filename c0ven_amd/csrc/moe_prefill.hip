@@ -50,8 +50,8 @@ __global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_
   const float4 *p = (const float4 *)(src + (uint64_t)row * ld + u * kUnit + 8 * l32);
   const float4 a = p[0], b = p[1];
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  quant_unit(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
-  if (o2) quant_unit(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
+  quant_unit<false, true>(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
+  if (o2) quant_unit<false, true>(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -606,13 +606,12 @@ __device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
 template <uint32_t kLU, bool kGU>
 __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3))) pf_gemm_q4k(PfGemm g) {
   constexpr uint32_t U = 1u << kLU, kRows = kGU ? 32 : 64;
-  // One activation buffer, refilled after every wave is done with the unit, and the next unit's activations loaded
-  // only after the unit's MFMAs: their registers are not live across the compute, so three waves fit a SIMD (two
-  // with a second buffer and the loads issued a unit ahead; measured slower).
-  __shared__ __align__(16) uint8_t abuf[64 * kActLds];
+  // Two activation buffers filled by direct global-to-LDS loads (no registers held), the next unit's issued before
+  // the current unit's MFMAs and waited for after them: one barrier a unit, three waves a SIMD.
+  __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
   // Up sums [row][position], written after the unit loop's last barrier: they reuse the activation buffer.
   static_assert(32 * 65 * sizeof(float) <= 64 * kActLds, "ub must fit in one activation buffer");
-  float(*ub)[65] = reinterpret_cast<float(*)[65]>(abuf);
+  float(*ub)[65] = reinterpret_cast<float(*)[65]>(&abuf[0][0]);
   __shared__ uint32_t arow_lds[64];
   __shared__ uint64_t tab[32];
   // 1-D grid of (tile, row block) pairs, the row block fastest in the XCD-aware logical index over the pairs that
@@ -646,9 +645,23 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
   Q4kRaw raw;
   raw.load(M, U, row0, 0, lane_id());
-  ActStage stage;
-  stage.load(g.act, arow_lds, U, 0);
-  stage.store_split(abuf);
+  // Unit u of the tile's positions into buffer b: LDS holds 21 pieces of 16 B a position (kActLds = 336), so the
+  // wave's i-th load covers pieces 64 i .. 64 i + 63 contiguously; pieces 0-19 are the global unit verbatim (its
+  // split sums at kActSplitG), piece 20 and positions past count are not loaded (their columns are never stored).
+  const auto dma = [&](uint32_t u, uint32_t b) {
+    constexpr uint32_t kPieces = 64 * kActLds / 16, kLoads = kPieces / 64;
+    static_assert(kActLds == 21 * 16 && kPieces % 64 == 0, "activation pieces");
+#pragma unroll
+    for (uint32_t i = wave_id(); i < kLoads; i += kPfWG / 64) {
+      const uint32_t piece = 64 * i + lane_id(), pos = piece / 21, c = piece % 21, ar = arow_lds[pos];
+      if (c < 20 && ar != 0xffffffffu)
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void *)(g.act + ((uint64_t)ar * U + u) * kActBytes + 16 * c),
+            (__attribute__((address_space(3))) void *)(&abuf[b][0] + 64 * 16 * i), 16, 0, 0);
+    }
+  };
+  dma(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   float acc[4][4];
 #pragma unroll
@@ -659,28 +672,25 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   for (uint32_t u = 0; u < U; u++) {
     Q4kRaw next;
     if (u + 1 < U) {
+      dma(u + 1, (u + 1) & 1);
       next.load(M, U, row0, u + 1, lane_id());
     }
-    const uint8_t *buf = abuf;
+    const uint8_t *buf = abuf[u & 1];
     Q4kA a;
     a.decode(raw, lane_id());
 #pragma unroll
     for (uint32_t pt = 0; pt < 4; pt++) {
       if (pt < npt) {
         ActB b;
-        b.load_presplit(buf + (16 * pt + lane_id() % 16) * kActLds, lane_id());
+        b.load_presplit(buf + (16 * pt + lane_id() % 16) * kActLds, lane_id(), kActSplitG);
         float t[4];
         q4k_terms(a, b, t);
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[pt][i] = __fadd_rn(acc[pt][i], t[i]);
       }
     }
-    if (u + 1 < U) {
-      stage.load(g.act, arow_lds, U, u + 1);
-      __syncthreads();  // every wave is done with the buffer before it is overwritten
-      stage.store_split(abuf);
-      raw = next;
-    }
+    if (u + 1 < U) raw = next;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of unit u + 1 have landed in LDS
     __syncthreads();
   }
   // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16.
