@@ -1,0 +1,66 @@
+// IQ3_S weights against activation units on the matrix cores: 16 weight rows x 16 position columns x one 32-value
+// block per v_mfma_i32_16x16x32_i8, with the integers and fp32 steps of UnitIQ3_S::term (units.h).
+//
+// Operand layout (one wave), as in mfma_q4k.h: lane l holds A row l % 16 and B column l % 16, bytes 8 g .. 8 g + 7
+// of each 32-value block, g = l / 16; D[row][col] sits in lane 16 (row / 4) + col as element row % 4. A lane's eight
+// bytes of block ib are the grid groups 8 ib + 2 g and 8 ib + 2 g + 1, decoded to signed bytes from the grid in LDS.
+//
+// Exactness: each block's D is the exact int32 dot of the signed codes with the activation codes; the block's odd
+// scale ls = 1 + 2 s (at most 31, so it does not fit a folded int8 code) multiplies D as an integer and the eight
+// products are added in block order, which is the CPU path's bsum.
+#pragma once
+
+#include "device_math.h"
+#include "layout.h"
+
+namespace c0ven {
+
+// One lane's raw bytes of a 16-row x 1-unit IQ3_S tile: for its A row, the word of each block's index bytes that
+// holds groups 2 g and 2 g + 1 (in halfword g % 2), the eight sign words and the two high-bit words; for its four D
+// rows (4 g + i), the scales word and d.
+struct Iq3sRaw {
+  uint32_t qs[8], sg[8], qh[2], sc[4], dh[4];
+  // Rows row0 .. row0 + 15 (row0 a multiple of 16) of the matrix at mat (U units a row), unit u.
+  __device__ __forceinline__ void load(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
+    const uint32_t g = lane / 16, nl = kTileRows * U;
+    const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_IQ3_S, U);
+    const uint32_t ia = pair_idx((row0 % kTileRows) + lane % 16, u);
+#pragma unroll
+    for (uint32_t ib = 0; ib < 8; ib++)  // qs piece ib / 2 holds blocks 2 p (bytes 0-7) and 2 p + 1 (bytes 8-15)
+      qs[ib] = *(const uint32_t *)(tile + ((uint64_t)(ib / 2) * nl + ia) * 16 + 8 * (ib % 2) + 4 * (g / 2));
+#pragma unroll
+    for (uint32_t p = 0; p < 2; p++) {
+      const uint4 v = *(const uint4 *)(tile + (uint64_t)iq3_st::kSigns * nl + ((uint64_t)p * nl + ia) * 16);
+      sg[4 * p] = v.x, sg[4 * p + 1] = v.y, sg[4 * p + 2] = v.z, sg[4 * p + 3] = v.w;
+    }
+#pragma unroll
+    for (uint32_t p = 0; p < 2; p++)
+      qh[p] = *(const uint32_t *)(tile + (uint64_t)iq3_st::kQh * nl + ((uint64_t)p * nl + ia) * 4);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      const uint32_t id = pair_idx((row0 % kTileRows) + 4 * g + i, u);
+      sc[i] = *(const uint32_t *)(tile + (uint64_t)iq3_st::kScales * nl + (uint64_t)id * 4);
+      dh[i] = *(const uint16_t *)(tile + (uint64_t)iq3_st::kD * nl + (uint64_t)id * 2);
+    }
+  }
+  // The A operand of block ib: groups k = 8 ib + 2 g + j (j = 0, 1), each four signed bytes (grid bytes, negated
+  // where the group's sign bits are set), as UnitIQ3_S::load decodes them.
+  __device__ __forceinline__ long a_block(uint32_t ib, uint32_t lane, const uint32_t *grid) const {
+    const uint32_t g = lane / 16;
+    uint32_t w[2];
+#pragma unroll
+    for (uint32_t j = 0; j < 2; j++) {
+      const uint32_t byte = (qs[ib] >> (8 * (2 * (g % 2) + j))) & 0xffu;
+      const uint32_t hb = (qh[ib / 4] >> (8 * (ib % 4) + 2 * g + j)) & 1u;
+      const uint32_t gv = grid[byte | (hb << 8)];
+      const uint32_t nib = (sg[ib] >> (4 * (2 * g + j))) & 15u;
+      const uint32_t x = (nib * 0x00204081u) & 0x01010101u;  // byte t = bit t of the nibble
+      w[j] = (gv ^ (x * 0xffu)) + x;                         // grid bytes >= 1: negation has no carries
+    }
+    return (long)(((uint64_t)w[1] << 32) | w[0]);
+  }
+  // Block ib's scale of D row 4 g + i: 1 + 2 s.
+  __device__ __forceinline__ int ls(uint32_t i, uint32_t ib) const { return 1 + 2 * (int)((sc[i] >> (4 * ib)) & 15u); }
+};
+
+}  // namespace c0ven

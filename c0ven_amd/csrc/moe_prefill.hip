@@ -2,10 +2,10 @@
 // the combine. The kernel list and its reference counterparts are in prefill.h.
 //
 // Bits: every result equals the CPU oracle's (its ORACLE ORDER). The router sums exact bf16 products in fp64 in k
-// order, as the oracle does. The Q8_0 and IQ3_S expert GEMMs (pf_gemm) take each 32-value block's integer dot product
-// from one v_mfma_i32_32x32x32_i8 (exact), then apply the block's integer scale (IQ3_S) or fp32 term (Q8_0); the Q4_K
-// ones (pf_gemm_q4k) take the unit's integer sums from the 16 x 16 tiles of mfma_q4k.h. Both then follow each unit's
-// fp32 steps exactly as the decoders in units.h do, and add a row's units in sequence, as the oracle does.
+// order, as the oracle does. The Q8_0 expert GEMM (pf_gemm) takes each 32-value block's integer dot product from one
+// v_mfma_i32_32x32x32_i8 (exact), then the block's fp32 term; the Q4_K and IQ3_S ones (pf_gemm16) take the unit's
+// integer sums from 16 x 16 tiles (mfma_q4k.h, mfma_iq3s.h). All then follow each unit's fp32 steps exactly as the
+// decoders in units.h do, and add a row's units in sequence, as the oracle does.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -14,6 +14,7 @@
 #include "device_math.h"
 #include "iq3s_grid.h"
 #include "layout.h"
+#include "mfma_iq3s.h"
 #include "mfma_q4k.h"
 #include "prefill.h"
 #include "route.h"
@@ -267,8 +268,7 @@ __global__ void __launch_bounds__(kDispWG) pf_dispatch(const int32_t *ids, uint3
 // positions, and each 32-value block is one instruction.
 //
 // A lane's share of one unit (256 values) of its weight row: for block j, the 16 values 16 h .. 16 h + 15 (h = l / 32)
-// as int8 words, plus the block's integer scale (Q4_K, IQ3_S) or fp16 scale (Q8_0). The pieces come from the device
-// layout (layout.h) directly.
+// as int8 words, plus the block's fp16 scale (Q8_0). The pieces come from the device layout (layout.h) directly.
 
 __device__ __forceinline__ v4i as_v4i(uint4 v) {
   v4i r;
@@ -298,59 +298,11 @@ struct SliceQ8_0 {
   __device__ __forceinline__ v4i words(int j) const { return as_v4i(q[j]); }
 };
 
-struct SliceIQ3_S {
-  uint32_t qs[8], sg[8], qh[2], scw;  // qs[ib]: the four grid-index bytes of block ib's half h (groups 8 ib + 4 h ..)
-  uint16_t dh;
-  int ls[8];
-  float d;
-  __device__ __forceinline__ void fetch(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h) {
-#pragma unroll
-    for (int p = 0; p < 4; p++) {  // qs piece p holds the index bytes of blocks 2 p and 2 p + 1 (words 0-1, 2-3)
-      const uint32_t *q = (const uint32_t *)pf_field<uint4>(tile, iq3_st::kQs, p, idx, nl) + h;
-      qs[2 * p] = q[0], qs[2 * p + 1] = q[2];
-    }
-#pragma unroll
-    for (int p = 0; p < 2; p++) {
-      const uint4 v = *pf_field<uint4>(tile, iq3_st::kSigns, p, idx, nl);
-      sg[4 * p] = v.x, sg[4 * p + 1] = v.y, sg[4 * p + 2] = v.z, sg[4 * p + 3] = v.w;
-    }
-    qh[0] = *pf_field<uint32_t>(tile, iq3_st::kQh, 0, idx, nl);
-    qh[1] = *pf_field<uint32_t>(tile, iq3_st::kQh, 1, idx, nl);
-    scw = *pf_field<uint32_t>(tile, iq3_st::kScales, 0, idx, nl);
-    dh = *pf_field<uint16_t>(tile, iq3_st::kD, 0, idx, nl);
-  }
-  __device__ __forceinline__ void decode() {
-    d = h2f(dh);
-#pragma unroll
-    for (int ib = 0; ib < 8; ib++) ls[ib] = 1 + 2 * (int)((scw >> (4 * ib)) & 15u);
-  }
-  // Block ib, half h: groups k = 8 ib + 4 h + g (four values each): index byte g of qs[ib], high bit
-  // 8 (ib % 4) + 4 h + g of qh word ib / 4, signs nibble 4 h + g of sign word ib.
-  __device__ __forceinline__ v4i words_h(int ib, uint32_t h, const uint32_t *grid) const {
-    const uint32_t qw = qs[ib];
-    const uint32_t hb = qh[ib / 4] >> (8 * (ib % 4) + 4 * h), sw = sg[ib] >> (16 * h);
-    v4i r;
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const uint32_t ix = ((qw >> (8 * g)) & 0xffu) | (((hb >> g) & 1u) << 8);
-      const uint32_t gv = grid[ix];
-      const uint32_t nib = (sw >> (4 * g)) & 15u;
-      const uint32_t x = (nib * 0x00204081u) & 0x01010101u;
-      r[g] = (int)((gv ^ (x * 0xffu)) + x);
-    }
-    return r;
-  }
-};
-
 template <uint32_t kType>
 struct SliceOf;
 template <>
 struct SliceOf<QT_Q8_0> {
   using T = SliceQ8_0;
-};
-template <>
-struct SliceOf<QT_IQ3_S> {
-  using T = SliceIQ3_S;
 };
 
 struct PfGemm {
@@ -366,7 +318,7 @@ struct PfGemm {
   float *out;              // position p's outputs at out + p * out_ld
   uint32_t out_ld;
   float limit;
-  uint32_t row_blocks;     // pf_gemm_q4k: row blocks a tile (its 1-D grid is tiles x row_blocks)
+  uint32_t row_blocks;     // pf_gemm16: row blocks a tile (its 1-D grid is tiles x row_blocks)
 };
 
 // Rows a work-group of pf_gemm takes: 64 of gate and of up (waves 0-1 gate, 2-3 up, rows 32 (w % 2) ..), or 128 of
@@ -417,11 +369,28 @@ struct ActStage {
   }
 };
 
+// Unit u of a tile's 64 positions (global rows arow[], 0xffffffff for none) into LDS at buf by direct global-to-LDS
+// loads, issued by the calling wave's share. LDS holds 21 pieces of 16 B a position (kActLds = 336), so the wave's
+// i-th load fills pieces 64 i .. 64 i + 63 contiguously; pieces 0-19 are the 320-byte global unit verbatim (with the
+// split block sums at kActSplitG for q8_K), piece 20 and positions without a row are not loaded (their MFMA columns
+// are never stored). The caller waits (s_waitcnt vmcnt(0)) and synchronises before reading.
+__device__ __forceinline__ void pf_act_dma(const uint8_t *act, const uint32_t *arow, uint32_t U, uint32_t u, uint8_t *buf) {
+  constexpr uint32_t kPieces = 64 * kActLds / 16, kLoads = kPieces / 64;
+  static_assert(kActLds == 21 * 16 && kPieces % 64 == 0, "activation pieces");
+#pragma unroll
+  for (uint32_t i = wave_id(); i < kLoads; i += kPfWG / 64) {
+    const uint32_t piece = 64 * i + lane_id(), pos = piece / 21, c = piece % 21, ar = arow[pos];
+    if (c < 20 && ar != 0xffffffffu)
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)(act + ((uint64_t)ar * U + u) * kActBytes + 16 * c),
+          (__attribute__((address_space(3))) void *)(buf + 64 * 16 * i), 16, 0, 0);
+  }
+}
+
 template <uint32_t kType, uint32_t kLU, bool kGU>
 __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   constexpr uint32_t U = 1u << kLU;
   __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
-  __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
   __shared__ float ub[kGU ? 64 : 1][65];
   __shared__ uint32_t arow_lds[64];
   __shared__ uint64_t tab[32];
@@ -437,8 +406,6 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   }
   const uint32_t tid = threadIdx.x, w = wave_id(), l = lane_id(), h = l / 32, n = l % 32;
   if (tid < 32) tab[tid] = kExp2Tab[tid];
-  if (kType == QT_IQ3_S)
-    for (uint32_t i = tid; i < 512; i += kPfWG) grid_lds[i] = kIq3sGridPf[i];
   if (tid < 64) {
     const uint32_t pos = start + tid;
     arow_lds[tid] = tid < count ? (g.act_by_pos ? pos : (g.perm ? g.perm[pos] / g.K : pos)) : 0xffffffffu;
@@ -451,9 +418,8 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
   const uint32_t rr = row % kTileRows, nl = kTileRows * U;
   typename SliceOf<kType>::T s;  // this unit's weights; the next unit's are fetched while it is used
   s.fetch(tile, pair_idx(rr, 0), nl, h);
-  ActStage stage;
-  stage.load(g.act, arow_lds, U, 0);
-  stage.store(abuf[0]);
+  pf_act_dma(g.act, arow_lds, U, 0, &abuf[0][0]);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   // A tile of at most 32 positions takes one MFMA row block (kNB = 1): the second block's MFMAs and epilogue would
   // only produce outputs that are not stored. Each case is compiled on its own.
@@ -468,7 +434,7 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
     for (uint32_t u = 0; u < U; u++) {
       typename SliceOf<kType>::T s_next;
       if (u + 1 < U) {
-        stage.load(g.act, arow_lds, U, u + 1);
+        pf_act_dma(g.act, arow_lds, U, u + 1, &abuf[(u + 1) & 1][0]);
         s_next.fetch(tile, pair_idx(rr, u + 1), nl, h);
       }
       s.decode();
@@ -478,7 +444,7 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
       const uint32_t lf = lane_id(), hf = lf / 32, nf = lf % 32;  // (fresh: see tid_fresh)
       const uint8_t *arow0 = buf + nf * kActLds + 16 * hf, *arow1 = arow0 + 32 * kActLds;
       const uint8_t *mbase = buf + 4 * hf * kActLds + kActScales;
-      if constexpr (kType == QT_Q8_0) {
+      {
 #pragma unroll
         for (int b = 0; b < kNB; b++) {
           const uint8_t *ar = b ? arow1 : arow0;
@@ -520,35 +486,9 @@ __global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
             }
           }
         }
-      } else {
-#pragma unroll
-        for (int b = 0; b < kNB; b++) {
-          const uint8_t *ar = b ? arow1 : arow0;
-          int isum[16];
-#pragma unroll
-          for (int r = 0; r < 16; r++) isum[r] = 0;
-#pragma unroll
-          for (int j = 0; j < 8; j++) {
-            const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
-            const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words_h(j, h, grid_lds), v16i{}, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; r++) isum[r] += s.ls[j] * dv[r];
-#pragma unroll
-            for (int r = 0; r < 16; r++) asm volatile("" : "+v"(isum[r]));  // keeps the sums in block order
-            __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
-          }
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
-            const float ad = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds);
-            acc[b][r] = __fadd_rn(acc[b][r], __fmul_rn(__fmul_rn(s.d, ad), (float)isum[r]));
-          }
-        }
       }
-      if (u + 1 < U) {
-        stage.store(abuf[(u + 1) & 1]);
-        s = s_next;
-      }
+      if (u + 1 < U) s = s_next;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of unit u + 1 have landed in LDS
       __syncthreads();
     }
     // Outputs: positions 32 b + m_r, weight row `row`.
@@ -598,13 +538,13 @@ __device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
   return (b % 8) * per + b / 8;
 }
 
-// Q4_K on 16 x 16 x 32 int8 MFMA (mfma_q4k.h, the decode path's tile): wave w takes 16 weight rows (gate/up: matrix
-// w / 2, rows 16 (w % 2) .. of the work-group's 32 of each; down: rows 16 w .. of its 64) against the tile's positions
-// in 16-position tiles (only those holding positions run), unit by unit: the same integers and fp32 steps as
-// UnitQ4_K::term, units added in sequence. Its accumulators are a quarter of the 32 x 32 kernel's, so three
-// work-groups share a CU.
-template <uint32_t kLU, bool kGU>
-__global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3))) pf_gemm_q4k(PfGemm g) {
+// Q4_K and IQ3_S on 16 x 16 int8 MFMA tiles (mfma_q4k.h, the decode path's tile; mfma_iq3s.h): wave w takes 16
+// weight rows (gate/up: matrix w / 2, rows 16 (w % 2) .. of the work-group's 32 of each; down: rows 16 w .. of its 64)
+// against the tile's positions in 16-position tiles (only those holding positions run), unit by unit: the same
+// integers and fp32 steps as UnitQ4_K::term / UnitIQ3_S::term, units added in sequence. Its accumulators are a quarter
+// of the 32 x 32 kernel's, so three work-groups share a CU.
+template <uint32_t kType, uint32_t kLU, bool kGU>
+__global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3))) pf_gemm16(PfGemm g) {
   constexpr uint32_t U = 1u << kLU, kRows = kGU ? 32 : 64;
   // Two activation buffers filled by direct global-to-LDS loads (no registers held), the next unit's issued before
   // the current unit's MFMAs and waited for after them: one barrier a unit, three waves a SIMD.
@@ -614,6 +554,8 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   float(*ub)[65] = reinterpret_cast<float(*)[65]>(&abuf[0][0]);
   __shared__ uint32_t arow_lds[64];
   __shared__ uint64_t tab[32];
+  __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
+  using Raw = std::conditional_t<kType == QT_IQ3_S, Iq3sRaw, Q4kRaw>;
   // 1-D grid of (tile, row block) pairs, the row block fastest in the XCD-aware logical index over the pairs that
   // exist (the grid is sized for the most tiles a dispatch can make).
   const uint32_t nrb = g.row_blocks;
@@ -634,6 +576,8 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   }
   const uint32_t tid = tid_fresh(), w = wave_id();
   if (tid < 32) tab[tid] = kExp2Tab[tid];
+  if constexpr (kType == QT_IQ3_S)
+    for (uint32_t i = tid; i < 512; i += kPfWG) grid_lds[i] = kIq3sGridPf[i];
   if (tid < 64) {
     const uint32_t pos = start + tid;
     arow_lds[tid] = tid < count ? (g.act_by_pos ? pos : (g.perm ? g.perm[pos] / g.K : pos)) : 0xffffffffu;
@@ -643,24 +587,9 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   const uint32_t row0 = rb * kRows + (kGU ? 16 * (w & 1) : 16 * w);
   const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
   const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
-  Q4kRaw raw;
+  Raw raw;
   raw.load(M, U, row0, 0, lane_id());
-  // Unit u of the tile's positions into buffer b: LDS holds 21 pieces of 16 B a position (kActLds = 336), so the
-  // wave's i-th load covers pieces 64 i .. 64 i + 63 contiguously; pieces 0-19 are the global unit verbatim (its
-  // split sums at kActSplitG), piece 20 and positions past count are not loaded (their columns are never stored).
-  const auto dma = [&](uint32_t u, uint32_t b) {
-    constexpr uint32_t kPieces = 64 * kActLds / 16, kLoads = kPieces / 64;
-    static_assert(kActLds == 21 * 16 && kPieces % 64 == 0, "activation pieces");
-#pragma unroll
-    for (uint32_t i = wave_id(); i < kLoads; i += kPfWG / 64) {
-      const uint32_t piece = 64 * i + lane_id(), pos = piece / 21, c = piece % 21, ar = arow_lds[pos];
-      if (c < 20 && ar != 0xffffffffu)
-        __builtin_amdgcn_global_load_lds(
-            (const __attribute__((address_space(1))) void *)(g.act + ((uint64_t)ar * U + u) * kActBytes + 16 * c),
-            (__attribute__((address_space(3))) void *)(&abuf[b][0] + 64 * 16 * i), 16, 0, 0);
-    }
-  };
-  dma(0, 0);
+  pf_act_dma(g.act, arow_lds, U, 0, &abuf[0][0]);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   float acc[4][4];
@@ -670,23 +599,60 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
     for (int i = 0; i < 4; i++) acc[pt][i] = 0.0f;
 #pragma unroll 1
   for (uint32_t u = 0; u < U; u++) {
-    Q4kRaw next;
+    Raw next;
     if (u + 1 < U) {
-      dma(u + 1, (u + 1) & 1);
+      pf_act_dma(g.act, arow_lds, U, u + 1, &abuf[(u + 1) & 1][0]);
       next.load(M, U, row0, u + 1, lane_id());
     }
     const uint8_t *buf = abuf[u & 1];
-    Q4kA a;
-    a.decode(raw, lane_id());
+    if constexpr (kType == QT_IQ3_S) {
+      // Block by block: one MFMA a position tile, its D times the row's block scale added to the unit's integer sum
+      // in block order; then d ad isum as UnitIQ3_S::term.
+      int isum[4][4];
 #pragma unroll
-    for (uint32_t pt = 0; pt < 4; pt++) {
-      if (pt < npt) {
-        ActB b;
-        b.load_presplit(buf + (16 * pt + lane_id() % 16) * kActLds, lane_id(), kActSplitG);
-        float t[4];
-        q4k_terms(a, b, t);
+      for (int pt = 0; pt < 4; pt++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[pt][i] = __fadd_rn(acc[pt][i], t[i]);
+        for (int i = 0; i < 4; i++) isum[pt][i] = 0;
+      const uint32_t g8 = 8 * (lane_id() / 16);
+#pragma unroll
+      for (uint32_t ib = 0; ib < 8; ib++) {
+        const long aw = raw.a_block(ib, lane_id(), grid_lds);
+        int ls[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) ls[i] = raw.ls(i, ib);
+#pragma unroll
+        for (uint32_t pt = 0; pt < 4; pt++) {
+          if (pt < npt) {
+            const long bw = *(const long *)(buf + (16 * pt + lane_id() % 16) * kActLds + 32 * ib + g8);
+            const v4i_t dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) isum[pt][i] += ls[i] * dv[i];
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one block's operands live at a time
+      }
+#pragma unroll
+      for (uint32_t pt = 0; pt < 4; pt++) {
+        if (pt < npt) {
+          const float ad = *(const float *)(buf + (16 * pt + lane_id() % 16) * kActLds + kActScales);
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            acc[pt][i] = __fadd_rn(acc[pt][i], __fmul_rn(__fmul_rn(h2f((uint16_t)raw.dh[i]), ad), (float)isum[pt][i]));
+        }
+      }
+    } else {
+      Q4kA a;
+      a.decode(raw, lane_id());
+#pragma unroll
+      for (uint32_t pt = 0; pt < 4; pt++) {
+        if (pt < npt) {
+          ActB b;
+          b.load_presplit(buf + (16 * pt + lane_id() % 16) * kActLds, lane_id(), kActSplitG);
+          float t[4];
+          q4k_terms(a, b, t);
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[pt][i] = __fadd_rn(acc[pt][i], t[i]);
+        }
       }
     }
     if (u + 1 < U) raw = next;
@@ -766,15 +732,15 @@ void launch_gemm_lu(uint32_t LU, dim3 grid, const PfGemm &g, hipStream_t s) {
   }
 }
 
-template <bool kGU>
-void launch_q4k_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
+template <uint32_t kType, bool kGU>
+void launch_gemm16_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
   switch (LU) {
-    case 0: pf_gemm_q4k<0, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    case 1: pf_gemm_q4k<1, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    case 2: pf_gemm_q4k<2, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    case 3: pf_gemm_q4k<3, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    case 4: pf_gemm_q4k<4, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    default: pf_gemm_q4k<5, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    case 0: pf_gemm16<kType, 0, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    case 1: pf_gemm16<kType, 1, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    case 2: pf_gemm16<kType, 2, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    case 3: pf_gemm16<kType, 3, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    case 4: pf_gemm16<kType, 4, kGU><<<g2, kPfWG, 0, s>>>(q); break;
+    default: pf_gemm16<kType, 5, kGU><<<g2, kPfWG, 0, s>>>(q); break;
   }
 }
 
@@ -784,14 +750,14 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
   while ((1u << LU) < U) LU++;
   if (type == QT_Q8_0) {
     launch_gemm_lu<QT_Q8_0, kGU>(LU, grid, g, s);
-  } else if (type == QT_Q4_K) {  // the 16 x 16 MFMA kernel: half the rows a work-group, a 1-D XCD-aware grid
+  } else {  // Q4_K, IQ3_S: the 16 x 16 MFMA kernel, half the rows a work-group, a 1-D XCD-aware grid
     PfGemm q = g;
     q.row_blocks = grid.y * gemm_rows<kGU>() / (kGU ? 32 : 64);
     const dim3 g2(grid.x * q.row_blocks);
-    launch_q4k_lu<kGU>(LU, g2, q, s);
-  }
-  else {
-    launch_gemm_lu<QT_IQ3_S, kGU>(LU, grid, g, s);
+    if (type == QT_Q4_K)
+      launch_gemm16_lu<QT_Q4_K, kGU>(LU, g2, q, s);
+    else
+      launch_gemm16_lu<QT_IQ3_S, kGU>(LU, g2, q, s);
   }
 }
 

@@ -8,10 +8,11 @@
 //   pf_topk        one wave a token: softmax, top k, weights, shared gate
 //   pf_dispatch    counting sort of the T k assignments by expert (stable: token order within an expert) into
 //                  MoeTile[] of at most MOE_TILE rows, perm (position -> assignment) and inv (assignment -> position)
-//   pf_gemm<GU>    per tile and 32 rows: gate and up on int8 MFMA (one 32x32x32 instruction per 32-value block,
-//                  exact int32), the block's integer scales and the unit's fp32 term in the oracle's order, SwiGLU
+//   gate/up        per tile: gate and up on int8 MFMA, exact int32 block sums, the blocks' integer scales and the
+//                  unit's fp32 term in the oracle's order, SwiGLU. Q4_K and IQ3_S: pf_gemm16 (16 x 16 tiles, 32 rows
+//                  of each a work-group, activations copied straight to LDS); Q8_0: pf_gemm (32 x 32 x 32, 64 rows)
 //   pf_quant_rows  h -> the down's activation units
-//   pf_gemm<D>     per tile and 64 rows: down, the same way
+//   down           per tile: the same kernels (64 or 128 rows a work-group)
 //   pf_combine     y_t = sum_k w_k y_(t,k) in rank order + gs_t s_t
 // The shared expert runs through the same GEMMs over the tokens in order.
 #pragma once
