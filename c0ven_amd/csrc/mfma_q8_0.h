@@ -1,0 +1,40 @@
+// Q8_0 weights against q8_0 activation units on the matrix cores: 16 weight rows x 16 position columns x one 32-value
+// block per v_mfma_i32_16x16x32_i8 (the exact int32 block dot), with the fp32 steps of UnitQ8_0::term (units.h): each
+// block's term (d_w d_a) dot, the eight terms of a unit added as a pairwise tree.
+//
+// Operand layout (one wave), as in mfma_q4k.h: lane l holds A row l % 16 and B column l % 16, bytes 8 g .. 8 g + 7
+// of each block, g = l / 16; D[row][col] sits in lane 16 (row / 4) + col as element row % 4.
+#pragma once
+
+#include "device_math.h"
+#include "layout.h"
+
+namespace c0ven {
+
+// One lane's raw bytes of a 16-row x 1-unit Q8_0 tile: its A row's eight bytes of each block, and the eight f16 block
+// scales of each of its four D rows (4 g + i).
+struct Q80Raw {
+  long qs[8];
+  uint4 dv[4];
+  // Rows row0 .. row0 + 15 (row0 a multiple of 16) of the matrix at mat (U units a row), unit u.
+  __device__ __forceinline__ void load(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
+    const uint32_t g = lane / 16, nl = kTileRows * U;
+    const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q8_0, U);
+    const uint32_t ia = pair_idx((row0 % kTileRows) + lane % 16, u);
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++)  // block j is qs pieces 2 j (values 0-15) and 2 j + 1 (16-31)
+      qs[j] = *(const long *)(tile + ((uint64_t)(2 * j + g / 2) * nl + ia) * 16 + 8 * (g % 2));
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      const uint32_t id = pair_idx((row0 % kTileRows) + 4 * g + i, u);
+      dv[i] = *(const uint4 *)(tile + (uint64_t)q8_0t::kD * nl + (uint64_t)id * 16);
+    }
+  }
+  // Block j's scale of D row 4 g + i.
+  __device__ __forceinline__ float d(uint32_t i, uint32_t j) const {
+    const uint32_t w[4] = {dv[i].x, dv[i].y, dv[i].z, dv[i].w};
+    return h2f((uint16_t)(w[j / 2] >> (16 * (j % 2))));
+  }
+};
+
+}  // namespace c0ven

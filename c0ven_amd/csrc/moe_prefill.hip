@@ -2,10 +2,9 @@
 // the combine. The kernel list and its reference counterparts are in prefill.h.
 //
 // Bits: every result equals the CPU oracle's (its ORACLE ORDER). The router sums exact bf16 products in fp64 in k
-// order, as the oracle does. The Q8_0 expert GEMM (pf_gemm) takes each 32-value block's integer dot product from one
-// v_mfma_i32_32x32x32_i8 (exact), then the block's fp32 term; the Q4_K and IQ3_S ones (pf_gemm16) take the unit's
-// integer sums from 16 x 16 tiles (mfma_q4k.h, mfma_iq3s.h). All then follow each unit's fp32 steps exactly as the
-// decoders in units.h do, and add a row's units in sequence, as the oracle does.
+// order, as the oracle does. The expert GEMMs (pf_gemm16) take exact int32 block or unit sums from 16 x 16 int8 MFMA
+// tiles (mfma_q4k.h, mfma_iq3s.h, mfma_q8_0.h), then follow each unit's fp32 steps exactly as the decoders in units.h
+// do, and add a row's units in sequence, as the oracle does.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -16,6 +15,7 @@
 #include "layout.h"
 #include "mfma_iq3s.h"
 #include "mfma_q4k.h"
+#include "mfma_q8_0.h"
 #include "prefill.h"
 #include "route.h"
 
@@ -24,9 +24,6 @@ namespace c0ven {
 __device__ __constant__ static const uint32_t kIq3sGridPf[512] = {C0VEN_IQ3S_GRID_VALUES};
 
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kPfWG = 256;
 
@@ -262,49 +259,6 @@ __global__ void __launch_bounds__(kDispWG) pf_dispatch(const int32_t *ids, uint3
 // ---------------------------------------------------------------------------------------------------------------
 // Expert GEMMs on int8 MFMA.
 //
-// v_mfma_i32_32x32x32_i8: lane l gives A row l % 32, values 16 (l / 32) .. + 15 of the 32, and B column l % 32, the
-// same values; it receives D[m][l % 32] for m = 8 (r / 4) + 4 (l / 32) + r % 4, r < 16. Here A is activations (rows:
-// 32 of the tile's positions) and B is weights (columns: 32 weight rows), so a lane holds one weight row and 16
-// positions, and each 32-value block is one instruction.
-//
-// A lane's share of one unit (256 values) of its weight row: for block j, the 16 values 16 h .. 16 h + 15 (h = l / 32)
-// as int8 words, plus the block's fp16 scale (Q8_0). The pieces come from the device layout (layout.h) directly.
-
-__device__ __forceinline__ v4i as_v4i(uint4 v) {
-  v4i r;
-  r[0] = (int)v.x, r[1] = (int)v.y, r[2] = (int)v.z, r[3] = (int)v.w;
-  return r;
-}
-
-template <typename T>
-__device__ __forceinline__ const T *pf_field(const uint8_t *tile, uint32_t base, uint32_t p, uint32_t idx, uint32_t nl) {
-  return (const T *)(tile + (uint64_t)base * nl) + (uint64_t)p * nl + idx;
-}
-
-// Each slice is fetched (raw bytes into registers, one unit ahead of its use) and then decoded.
-struct SliceQ8_0 {
-  uint4 q[8], dv;
-  float d[8];
-  __device__ __forceinline__ void fetch(const uint8_t *tile, uint32_t idx, uint32_t nl, uint32_t h) {
-#pragma unroll
-    for (int b = 0; b < 8; b++) q[b] = *pf_field<uint4>(tile, q8_0t::kQs, 2 * b + h, idx, nl);
-    dv = *pf_field<uint4>(tile, q8_0t::kD, 0, idx, nl);
-  }
-  __device__ __forceinline__ void decode() {
-    const uint32_t w[4] = {dv.x, dv.y, dv.z, dv.w};
-#pragma unroll
-    for (int b = 0; b < 8; b++) d[b] = h2f((uint16_t)(w[b / 2] >> (16 * (b % 2))));
-  }
-  __device__ __forceinline__ v4i words(int j) const { return as_v4i(q[j]); }
-};
-
-template <uint32_t kType>
-struct SliceOf;
-template <>
-struct SliceOf<QT_Q8_0> {
-  using T = SliceQ8_0;
-};
-
 struct PfGemm {
   const MoeTile *tiles;    // routed: the dispatch's tiles
   const uint32_t *ntiles;
@@ -321,53 +275,10 @@ struct PfGemm {
   uint32_t row_blocks;     // pf_gemm16: row blocks a tile (its 1-D grid is tiles x row_blocks)
 };
 
-// Rows a work-group of pf_gemm takes: 64 of gate and of up (waves 0-1 gate, 2-3 up, rows 32 (w % 2) ..), or 128 of
-// down (wave w rows 32 w ..). Every wave takes all of the tile's (at most) 64 positions as two MFMA row blocks, so one
-// decoded weight fragment serves two MFMAs.
+// Rows of one grid.y step of the (tiles x row groups) grid the host computes: 64 of gate and of up, or 128 of down.
+// pf_gemm16 splits each into row blocks of 32 gate + 32 up rows, or 64 down rows, one work-group each.
 template <bool kGU>
 constexpr uint32_t gemm_rows() { return kGU ? 64 : 128; }
-
-// The tile's activation unit u (64 positions x 320 B) into LDS (positions kActLds apart, so the 32 rows one MFMA
-// operand read touches fall in distinct banks): 1280 16-byte pieces, five a thread, loaded into registers first.
-struct ActStage {
-  uint4 v[5];
-  __device__ __forceinline__ void load(const uint8_t *act, const uint32_t *arow, uint32_t U, uint32_t u) {
-#pragma unroll
-    for (int i = 0; i < 5; i++) {
-      const uint32_t piece = threadIdx.x + kPfWG * i, tk = piece / 20, c = piece % 20, ar = arow[tk];
-      v[i] = ar != 0xffffffffu ? *(const uint4 *)(act + ((uint64_t)ar * U + u) * kActBytes + 16 * c)
-                               : make_uint4(0, 0, 0, 0);
-    }
-  }
-  __device__ __forceinline__ void store(uint8_t *buf) const {
-#pragma unroll
-    for (int i = 0; i < 5; i++) {
-      const uint32_t piece = threadIdx.x + kPfWG * i, tk = piece / 20, c = piece % 20;
-      *(uint4 *)(buf + tk * kActLds + 16 * c) = v[i];
-    }
-  }
-  // The same, and the holders of the sums (pieces 18 and 19: sums 0-3 and 4-7) also write them split into hi and lo
-  // bytes in the unit's padding (kActSplit: hi bytes of sums 0-7, then lo bytes), as ActB::load_presplit reads them.
-  __device__ __forceinline__ void store_split(uint8_t *buf) const {
-#pragma unroll
-    for (int i = 0; i < 5; i++) {
-      const uint32_t piece = threadIdx.x + kPfWG * i, tk = piece / 20, c = piece % 20;
-      uint8_t *unit = buf + tk * kActLds;
-      *(uint4 *)(unit + 16 * c) = v[i];
-      if (c >= 18) {
-        const int bs[4] = {(int)v[i].x, (int)v[i].y, (int)v[i].z, (int)v[i].w};
-        uint32_t h = 0, l = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          h |= ((uint32_t)(bs[j] >> 6) & 0xffu) << (8 * j);
-          l |= ((uint32_t)bs[j] & 63u) << (8 * j);
-        }
-        *(uint32_t *)(unit + kActSplit + 4 * (c - 18)) = h;
-        *(uint32_t *)(unit + kActSplit + 8 + 4 * (c - 18)) = l;
-      }
-    }
-  }
-};
 
 // Unit u of a tile's 64 positions (global rows arow[], 0xffffffff for none) into LDS at buf by direct global-to-LDS
 // loads, issued by the calling wave's share. LDS holds 21 pieces of 16 B a position (kActLds = 336), so the wave's
@@ -387,147 +298,6 @@ __device__ __forceinline__ void pf_act_dma(const uint8_t *act, const uint32_t *a
   }
 }
 
-template <uint32_t kType, uint32_t kLU, bool kGU>
-__global__ void __launch_bounds__(kPfWG) pf_gemm(PfGemm g) {
-  constexpr uint32_t U = 1u << kLU;
-  __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
-  __shared__ float ub[kGU ? 64 : 1][65];
-  __shared__ uint32_t arow_lds[64];
-  __shared__ uint64_t tab[32];
-  uint32_t start, count, e;
-  if (g.shared_T) {
-    start = MOE_TILE * blockIdx.x;
-    if (start >= g.shared_T) return;
-    count = min((uint32_t)MOE_TILE, g.shared_T - start), e = 0;
-  } else {
-    if (blockIdx.x >= *g.ntiles) return;
-    const MoeTile tl = g.tiles[blockIdx.x];
-    start = tl.start, count = tl.count, e = tl.slot;
-  }
-  const uint32_t tid = threadIdx.x, w = wave_id(), l = lane_id(), h = l / 32, n = l % 32;
-  if (tid < 32) tab[tid] = kExp2Tab[tid];
-  if (tid < 64) {
-    const uint32_t pos = start + tid;
-    arow_lds[tid] = tid < count ? (g.act_by_pos ? pos : (g.perm ? g.perm[pos] / g.K : pos)) : 0xffffffffu;
-  }
-  __syncthreads();
-  const uint32_t mat = kGU ? (w >> 1) : 0u;
-  const uint32_t row = blockIdx.y * gemm_rows<kGU>() + (kGU ? 32 * (w & 1) : 32 * w) + n;
-  const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
-  const uint8_t *tile = M + (uint64_t)(row / kTileRows) * tile_bytes(kType, U);
-  const uint32_t rr = row % kTileRows, nl = kTileRows * U;
-  typename SliceOf<kType>::T s;  // this unit's weights; the next unit's are fetched while it is used
-  s.fetch(tile, pair_idx(rr, 0), nl, h);
-  pf_act_dma(g.act, arow_lds, U, 0, &abuf[0][0]);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  // A tile of at most 32 positions takes one MFMA row block (kNB = 1): the second block's MFMAs and epilogue would
-  // only produce outputs that are not stored. Each case is compiled on its own.
-  auto run = [&](auto nb_tag) {
-    constexpr int kNB = decltype(nb_tag)::value;
-    float acc[2][16];  // the row's units summed in sequence (ORACLE ORDER), for positions m_r and 32 + m_r
-#pragma unroll
-    for (int b = 0; b < kNB; b++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[b][r] = 0.0f;
-  #pragma unroll 1
-    for (uint32_t u = 0; u < U; u++) {
-      typename SliceOf<kType>::T s_next;
-      if (u + 1 < U) {
-        pf_act_dma(g.act, arow_lds, U, u + 1, &abuf[(u + 1) & 1][0]);
-        s_next.fetch(tile, pair_idx(rr, u + 1), nl, h);
-      }
-      s.decode();
-      const uint8_t *buf = abuf[u & 1];
-      // This lane's A rows (positions n, 32 + n; its half of each block), and the base of the scales of the positions
-      // its results belong to (32 b + 8 (r / 4) + 4 h + r % 4): every LDS read below is a base plus a constant offset.
-      const uint32_t lf = lane_id(), hf = lf / 32, nf = lf % 32;  // (fresh: see tid_fresh)
-      const uint8_t *arow0 = buf + nf * kActLds + 16 * hf, *arow1 = arow0 + 32 * kActLds;
-      const uint8_t *mbase = buf + 4 * hf * kActLds + kActScales;
-      {
-#pragma unroll
-        for (int b = 0; b < kNB; b++) {
-          const uint8_t *ar = b ? arow1 : arow0;
-          float q[3][16];  // the eight block terms' pairwise tree
-#pragma unroll
-          for (int j = 0; j < 8; j++) {
-            const v4i aw = as_v4i(*(const uint4 *)(ar + 32 * j));
-            const v16i dv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, s.words(j), v16i{}, 0, 0, 0);
-            float c[16];
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-              const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
-              const float as = *(const float *)(mbase + (32 * b + 8 * (r / 4) + (r % 4)) * kActLds + 4 * j);
-              c[r] = __fmul_rn(__fmul_rn(s.d[j], as), (float)dv[r]);
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) asm volatile("" : "+v"(c[r]));
-            __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
-            if ((j & 1) == 0) {
-#pragma unroll
-              for (int r = 0; r < 16; r++) q[0][r] = c[r];
-            } else {
-#pragma unroll
-              for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[0][r], c[r]);
-              if ((j & 2) == 0) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) q[1][r] = c[r];
-              } else {
-#pragma unroll
-                for (int r = 0; r < 16; r++) c[r] = __fadd_rn(q[1][r], c[r]);
-                if ((j & 4) == 0) {
-#pragma unroll
-                  for (int r = 0; r < 16; r++) q[2][r] = c[r];
-                } else {
-#pragma unroll
-                  for (int r = 0; r < 16; r++) acc[b][r] = __fadd_rn(acc[b][r], __fadd_rn(q[2][r], c[r]));
-                }
-              }
-            }
-          }
-        }
-      }
-      if (u + 1 < U) s = s_next;
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of unit u + 1 have landed in LDS
-      __syncthreads();
-    }
-    // Outputs: positions 32 b + m_r, weight row `row`.
-    if constexpr (kGU) {
-      const uint32_t col = 32 * (w & 1) + n;
-      if (mat == 1) {
-#pragma unroll
-        for (int b = 0; b < kNB; b++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) ub[32 * b + 8 * (r / 4) + 4 * h + (r % 4)][col] = acc[b][r];
-      }
-      __syncthreads();
-      if (mat == 0) {
-#pragma unroll
-        for (int b = 0; b < kNB; b++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
-            if (m < count)
-              g.out[(uint64_t)(start + m) * g.out_ld + row] = swiglu_one(acc[b][r], ub[m][col], g.limit, tab);
-          }
-      }
-    } else {
-#pragma unroll
-      for (int b = 0; b < kNB; b++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const uint32_t m = 32 * b + 8 * (r / 4) + 4 * h + (r % 4);
-          if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row] = acc[b][r];
-        }
-    }
-  };
-  if (count > 32) {
-    run(std::integral_constant<int, 2>{});
-  } else {
-    run(std::integral_constant<int, 1>{});
-  }
-}
-
 // Work-group b of a 1-D grid of n runs on XCD b % 8 (the dispatcher deals work-groups to the eight XCDs in turn).
 // Its logical index puts consecutive logical indices on one XCD: (b % 8) ceil(n / 8) + b / 8. With the row block
 // fastest in the logical index, a tile's row blocks run together on one XCD (its activations come from that XCD's
@@ -538,11 +308,11 @@ __device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
   return (b % 8) * per + b / 8;
 }
 
-// Q4_K and IQ3_S on 16 x 16 int8 MFMA tiles (mfma_q4k.h, the decode path's tile; mfma_iq3s.h): wave w takes 16
-// weight rows (gate/up: matrix w / 2, rows 16 (w % 2) .. of the work-group's 32 of each; down: rows 16 w .. of its 64)
-// against the tile's positions in 16-position tiles (only those holding positions run), unit by unit: the same
-// integers and fp32 steps as UnitQ4_K::term / UnitIQ3_S::term, units added in sequence. Its accumulators are a quarter
-// of the 32 x 32 kernel's, so three work-groups share a CU.
+// Q4_K, IQ3_S and Q8_0 on 16 x 16 int8 MFMA tiles (mfma_q4k.h, the decode path's tile; mfma_iq3s.h; mfma_q8_0.h):
+// wave w takes 16 weight rows (gate/up: matrix w / 2, rows 16 (w % 2) .. of the work-group's 32 of each; down: rows
+// 16 w .. of its 64) against the tile's positions in 16-position tiles (only those holding positions run), unit by
+// unit: the same integers and fp32 steps as UnitQ4_K::term / UnitIQ3_S::term / UnitQ8_0::term, units added in
+// sequence; three work-groups share a CU.
 template <uint32_t kType, uint32_t kLU, bool kGU>
 __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3))) pf_gemm16(PfGemm g) {
   constexpr uint32_t U = 1u << kLU, kRows = kGU ? 32 : 64;
@@ -555,7 +325,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   __shared__ uint32_t arow_lds[64];
   __shared__ uint64_t tab[32];
   __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
-  using Raw = std::conditional_t<kType == QT_IQ3_S, Iq3sRaw, Q4kRaw>;
+  using Raw = std::conditional_t<kType == QT_IQ3_S, Iq3sRaw, std::conditional_t<kType == QT_Q8_0, Q80Raw, Q4kRaw>>;
   // 1-D grid of (tile, row block) pairs, the row block fastest in the XCD-aware logical index over the pairs that
   // exist (the grid is sized for the most tiles a dispatch can make).
   const uint32_t nrb = g.row_blocks;
@@ -640,6 +410,45 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
             acc[pt][i] = __fadd_rn(acc[pt][i], __fmul_rn(__fmul_rn(h2f((uint16_t)raw.dh[i]), ad), (float)isum[pt][i]));
         }
       }
+    } else if constexpr (kType == QT_Q8_0) {
+      // Block by block: one MFMA a position tile, the block's term (d_w d_a) dot; the eight terms of the unit as the
+      // pairwise tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then added to the row's sum.
+      float q[3][4][4];  // the tree's pending partial sums: q[level][pt][row]
+      const uint32_t g8 = 8 * (lane_id() / 16);
+#pragma unroll
+      for (uint32_t j = 0; j < 8; j++) {
+        float dw[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) dw[i] = raw.d(i, j);
+#pragma unroll
+        for (uint32_t pt = 0; pt < 4; pt++) {
+          if (pt < npt) {
+            const uint8_t *unit = buf + (16 * pt + lane_id() % 16) * kActLds;
+            const v4i_t dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(raw.qs[j], *(const long *)(unit + 32 * j + g8),
+                                                                  v4i_t{0, 0, 0, 0}, 0, 0, 0);
+            const float as = *(const float *)(unit + kActScales + 4 * j);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              float c = __fmul_rn(__fmul_rn(dw[i], as), (float)dv[i]);
+              if ((j & 1) == 0) {
+                q[0][pt][i] = c;
+              } else {
+                c = __fadd_rn(q[0][pt][i], c);
+                if ((j & 2) == 0) {
+                  q[1][pt][i] = c;
+                } else {
+                  c = __fadd_rn(q[1][pt][i], c);
+                  if ((j & 4) == 0)
+                    q[2][pt][i] = c;
+                  else
+                    acc[pt][i] = __fadd_rn(acc[pt][i], __fadd_rn(q[2][pt][i], c));
+                }
+              }
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one block's operands live at a time
+      }
     } else {
       Q4kA a;
       a.decode(raw, lane_id());
@@ -721,18 +530,6 @@ __global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const ui
 // Host side.
 
 template <uint32_t kType, bool kGU>
-void launch_gemm_lu(uint32_t LU, dim3 grid, const PfGemm &g, hipStream_t s) {
-  switch (LU) {
-    case 0: pf_gemm<kType, 0, kGU><<<grid, kPfWG, 0, s>>>(g); break;
-    case 1: pf_gemm<kType, 1, kGU><<<grid, kPfWG, 0, s>>>(g); break;
-    case 2: pf_gemm<kType, 2, kGU><<<grid, kPfWG, 0, s>>>(g); break;
-    case 3: pf_gemm<kType, 3, kGU><<<grid, kPfWG, 0, s>>>(g); break;
-    case 4: pf_gemm<kType, 4, kGU><<<grid, kPfWG, 0, s>>>(g); break;
-    default: pf_gemm<kType, 5, kGU><<<grid, kPfWG, 0, s>>>(g); break;
-  }
-}
-
-template <uint32_t kType, bool kGU>
 void launch_gemm16_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
   switch (LU) {
     case 0: pf_gemm16<kType, 0, kGU><<<g2, kPfWG, 0, s>>>(q); break;
@@ -748,17 +545,16 @@ template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
   uint32_t LU = 0;
   while ((1u << LU) < U) LU++;
-  if (type == QT_Q8_0) {
-    launch_gemm_lu<QT_Q8_0, kGU>(LU, grid, g, s);
-  } else {  // Q4_K, IQ3_S: the 16 x 16 MFMA kernel, half the rows a work-group, a 1-D XCD-aware grid
-    PfGemm q = g;
-    q.row_blocks = grid.y * gemm_rows<kGU>() / (kGU ? 32 : 64);
-    const dim3 g2(grid.x * q.row_blocks);
-    if (type == QT_Q4_K)
-      launch_gemm16_lu<QT_Q4_K, kGU>(LU, g2, q, s);
-    else
-      launch_gemm16_lu<QT_IQ3_S, kGU>(LU, g2, q, s);
-  }
+  // The 16 x 16 MFMA kernel: half the rows a work-group, a 1-D XCD-aware grid.
+  PfGemm q = g;
+  q.row_blocks = grid.y * gemm_rows<kGU>() / (kGU ? 32 : 64);
+  const dim3 g2(grid.x * q.row_blocks);
+  if (type == QT_Q4_K)
+    launch_gemm16_lu<QT_Q4_K, kGU>(LU, g2, q, s);
+  else if (type == QT_IQ3_S)
+    launch_gemm16_lu<QT_IQ3_S, kGU>(LU, g2, q, s);
+  else
+    launch_gemm16_lu<QT_Q8_0, kGU>(LU, g2, q, s);
 }
 
 struct HookScope {
