@@ -188,10 +188,10 @@ __global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T
 
 // ---------------------------------------------------------------------------------------------------------------
 // Dispatch: one work-group of 1024. Counts per expert, exclusive scans of the counts and of the tiles, the MoeTile
-// records, then the positions 64 tokens at a time: an expert takes at most one assignment a token, so a 64-bit mask
-// of the tokens that chose it orders its assignments by token (stable, unlike p_moe_fill's atomic order).
+// records, then the positions 256 tokens at a time: an expert takes at most one assignment a token, so 64-bit masks
+// of the tokens that chose it order its assignments by token (stable, unlike p_moe_fill's atomic order).
 
-constexpr uint32_t kDispWG = 1024;
+constexpr uint32_t kDispWG = 1024, kDispWin = 4;  // kDispWin: 64-token masks per position pass
 
 constexpr uint32_t kDispCache = 40960;  // ids the dispatch keeps in LDS (T K up to 40960: 2048 tokens at k <= 20)
 
@@ -199,7 +199,7 @@ __global__ void __launch_bounds__(kDispWG) pf_dispatch(const int32_t *ids, uint3
                                                        uint32_t *perm, uint32_t *inv, MoeTile *tiles,
                                                        uint32_t *ntiles) {
   __shared__ uint32_t cnt[512], base[512], tb[512];
-  __shared__ unsigned long long mask[512];
+  __shared__ unsigned long long mask[kDispWin][512];
   __shared__ uint16_t ids_lds[kDispCache];  // the ids, when they fit (the position pass reads them again)
   const uint32_t tid = threadIdx.x, n = T * K;
   const bool cached = n <= kDispCache;
@@ -234,24 +234,32 @@ __global__ void __launch_bounds__(kDispWG) pf_dispatch(const int32_t *ids, uint3
   __syncthreads();
   if (tid < 512) base[tid] -= (tid < E ? cnt[tid] : 0u);  // exclusive
   __syncthreads();
-  for (uint32_t t0 = 0; t0 < T; t0 += 64) {
-    if (tid < 512) mask[tid] = 0ull;
+  // kDispWin masks of 64 tokens a pass: an assignment's position is its expert's base, plus the earlier masks'
+  // tokens, plus the lower bits of its own mask.
+  const auto expert_of = [&](uint32_t a) { return cached ? (uint32_t)ids_lds[a] : (uint32_t)ids[a]; };
+  for (uint32_t t0 = 0; t0 < T; t0 += 64 * kDispWin) {
+    for (uint32_t i = tid; i < kDispWin * 512; i += kDispWG) (&mask[0][0])[i] = 0ull;
     __syncthreads();
-    const uint32_t a = t0 * K + tid;
-    const bool on = tid < 64 * K && a < n;
-    uint32_t e = 0, bit = 0;
-    if (on) {
-      e = cached ? (uint32_t)ids_lds[a] : (uint32_t)ids[a], bit = a / K - t0;
-      atomicOr(&mask[e], 1ull << bit);
+    const uint32_t a0 = t0 * K, a1 = min(n, (t0 + 64 * kDispWin) * K);
+    for (uint32_t a = a0 + tid; a < a1; a += kDispWG) {
+      const uint32_t tok = a / K - t0;
+      atomicOr(&mask[tok / 64][expert_of(a)], 1ull << (tok % 64));
     }
     __syncthreads();
-    if (on) {
-      const uint32_t pos = base[e] + (uint32_t)__popcll(mask[e] & ((1ull << bit) - 1ull));
+    for (uint32_t a = a0 + tid; a < a1; a += kDispWG) {
+      const uint32_t tok = a / K - t0, e = expert_of(a), w = tok / 64;
+      uint32_t pos = base[e] + (uint32_t)__popcll(mask[w][e] & ((1ull << (tok % 64)) - 1ull));
+      for (uint32_t v = 0; v < w; v++) pos += (uint32_t)__popcll(mask[v][e]);
       perm[pos] = a;
       inv[a] = pos;
     }
     __syncthreads();
-    if (tid < E) base[tid] += (uint32_t)__popcll(mask[tid]);
+    if (tid < E) {
+      uint32_t add = 0;
+#pragma unroll
+      for (uint32_t v = 0; v < kDispWin; v++) add += (uint32_t)__popcll(mask[v][tid]);
+      base[tid] += add;
+    }
     __syncthreads();
   }
 }
