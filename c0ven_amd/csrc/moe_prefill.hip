@@ -205,10 +205,22 @@ __global__ void __launch_bounds__(kDispWG) pf_dispatch(const int32_t *ids, uint3
   const bool cached = n <= kDispCache;
   if (tid < 512) cnt[tid] = 0u;
   __syncthreads();
-  for (uint32_t a = tid; a < n; a += kDispWG) {
-    const uint32_t e = (uint32_t)ids[a];
-    atomicAdd(&cnt[e], 1u);
-    if (cached) ids_lds[a] = (uint16_t)e;
+  // Eight loads in flight before their counts (one at a time, each load waited for behind the previous atomic).
+  for (uint32_t a0 = tid; a0 < n; a0 += 8 * kDispWG) {
+    uint32_t ev[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) {
+      const uint32_t a = a0 + j * kDispWG;
+      ev[j] = a < n ? (uint32_t)ids[a] : 0u;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) {
+      const uint32_t a = a0 + j * kDispWG;
+      if (a < n) {
+        atomicAdd(&cnt[ev[j]], 1u);
+        if (cached) ids_lds[a] = (uint16_t)ev[j];
+      }
+    }
   }
   __syncthreads();
   // Inclusive scans (Hillis-Steele) of the counts and of the tiles per expert.
