@@ -348,11 +348,21 @@ def stack(args, cfg, moe, h):
         yy = np.empty((n, H), np.float32)
         hip.d2h(yy, bufs[(NL - 1) % 2])
         outs.append(yy)
-    yg = np.concatenate(outs)[sample]
-    tc0 = time.perf_counter()
-    for l in range(NL):  # the CPU does every layer too; the last layer's output is compared
-        xo, io, _ = layers[l].oracle_forward(x[sample], nthreads=min(16, os.cpu_count() or 1))
-    cpu_s = time.perf_counter() - tc0
+    yall = np.concatenate(outs)
+
+    def oracle_stack(smp):
+        t0_ = time.perf_counter()
+        for l in range(NL):  # the CPU does every layer too; the last layer's output is compared
+            xo_, _, _ = layers[l].oracle_forward(x[smp], nthreads=min(16, os.cpu_count() or 1))
+        return xo_, time.perf_counter() - t0_
+
+    xo, cpu_s = oracle_stack(sample)
+    if not args.no_cpu and not decode:  # prefill: as many tokens as --cpu-seconds allows, from both chunks
+        per = max(4, int(len(sample) * args.cpu_seconds / max(cpu_s, 1e-6)) // 2)
+        if 2 * per > len(sample):
+            sample = np.r_[0:min(per, chunk), chunk:chunk + min(per, T - chunk)]
+            xo, cpu_s = oracle_stack(sample)
+    yg = yall[sample]
     parity = dict(sample_tokens=len(sample), y_bit_exact=bool(np.array_equal(yg, xo)), max_abs=h.max_abs(yg, xo),
                   rel_l2=h.rel_l2(yg, xo))
     cores = min(16, os.cpu_count() or 1)
@@ -444,10 +454,18 @@ def prefill(args, cfg, moe, h):
     hip.sync()
     hip.d2h(y, yd)
     hip.d2h(ids, idsd)
+    # A first 64-token sample gives the oracle's rate; the baseline then runs on as many tokens as --cpu-seconds
+    # allows (all T when they fit), and parity is checked on those.
     sample = np.r_[0:32, T - 32:T]
     tc0 = time.perf_counter()
     yo, io, _ = L0.oracle_forward(x[sample], nthreads=min(16, os.cpu_count() or 1))
     cpu_s = time.perf_counter() - tc0
+    n_more = min(T, int(len(sample) * args.cpu_seconds / max(cpu_s, 1e-6)))
+    if not args.no_cpu and n_more > len(sample):
+        sample = np.r_[0:n_more]
+        tc0 = time.perf_counter()
+        yo, io, _ = L0.oracle_forward(x[sample], nthreads=min(16, os.cpu_count() or 1))
+        cpu_s = time.perf_counter() - tc0
     parity = dict(sample_tokens=len(sample), ids_equal=bool(np.array_equal(ids[sample], io)),
                   y_bit_exact=bool(np.array_equal(y[sample], yo)), max_abs=h.max_abs(y[sample], yo),
                   rel_l2=h.rel_l2(y[sample], yo))
