@@ -381,7 +381,8 @@ def stack(args, cfg, moe, h):
         gu_flop = 2.0 * (chunk * K) * 2 * F * H
         roof = {"bound": "mfma", "kernel": "pf_gate_up", "achieved": round(gu_flop / (gu_ms * 1e-3) / 1e12, 2),
                 "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                "frac": round(gu_flop / (gu_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4), "traffic": None,
+                "frac": round(gu_flop / (gu_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+                "traffic": measured_prefill_traffic(args.config),
                 "algorithmic_flop_per_launch": gu_flop, "avg_launch_ms": round(gu_ms, 4)}
     out = {
         "metric": "MoE block tokens/s + achieved HBM GB/s (decode), TFLOP/s (prefill) on 1 GPU",
