@@ -65,6 +65,7 @@ _SIGS = {
     "moe_h_rows": (_u32, [C.POINTER(MoeConfig)]),
     "moe_prefill_dispatch": (_i32, [_P, C.POINTER(MoeTile), _u32, C.POINTER(_u32), _P]),
     "moe_sync": (_i32, [_P]),
+    "moe_check": (_i32, [_P, _P]),
     "moe_stream": (_P, [_P]),
     "moe_set_timing": (_i32, [_P, C.c_int]),
     "moe_kernel_times": (_i32, [_P, C.POINTER(C.c_char_p), C.POINTER(_f32), _u32, C.POINTER(_u32), C.POINTER(_u32)]),
@@ -209,6 +210,11 @@ class MoeBlock:
 
     def sync(self):
         self._check(lib.moe_sync(self.h))
+
+    def check(self, stream=None):
+        """Waits for stream (default: the context's) and raises MoeError (MOE_TIMEOUT) if a forward's internal wait
+        gave up since the last check."""
+        self._check(lib.moe_check(self.h, stream))
 
     def stream(self):
         return lib.moe_stream(self.h)

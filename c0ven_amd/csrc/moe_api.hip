@@ -51,6 +51,26 @@ struct TimedLaunch {
   hipEvent_t a, b;
 };
 
+// A kernel's timed launches folded into a sum (the event pool is bounded: past kTimedFold pending launches the record
+// waits for them and folds them here).
+struct TimedSum {
+  const char *name;
+  double ms;
+  uint32_t n;
+};
+constexpr size_t kTimedFold = 4096;
+
+// Device memory released when the scope ends, also when a check throws.
+struct DevBuf {
+  void *p = nullptr;
+  DevBuf() = default;
+  DevBuf(const DevBuf &) = delete;
+  DevBuf &operator=(const DevBuf &) = delete;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+};
+
 }  // namespace
 
 struct moe_ctx {
@@ -87,6 +107,7 @@ struct moe_ctx {
   std::vector<hipEvent_t> ev;  // the event pool
   size_t ev_next = 0;          // events of the pool in use by the record
   std::vector<TimedLaunch> timed;
+  std::vector<TimedSum> timed_sums;  // launches folded out of `timed`
   uint32_t ev_used = 0;        // forwards recorded since the last moe_kernel_times
   std::vector<void *> allocs;
   uint64_t dev_bytes = 0;
@@ -179,9 +200,26 @@ hipEvent_t timing_event(moe_ctx *c, hipStream_t s) {
   check(hipEventRecord(e, s), "hipEventRecord");
   return e;
 }
+// Waits for the recorded launches and adds their durations to the per-kernel sums; the pool is then free again.
+void fold_timed(moe_ctx *c) {
+  if (c->timed.empty()) return;
+  check(hipEventSynchronize(c->timed.back().b), "hipEventSynchronize");
+  for (const TimedLaunch &t : c->timed) {
+    size_t i = 0;
+    while (i < c->timed_sums.size() && std::strcmp(c->timed_sums[i].name, t.name) != 0) i++;
+    if (i == c->timed_sums.size()) c->timed_sums.push_back(TimedSum{t.name, 0.0, 0});
+    float ms = 0.0f;
+    check(hipEventElapsedTime(&ms, t.a, t.b), "hipEventElapsedTime");
+    c->timed_sums[i].ms += ms, c->timed_sums[i].n++;
+  }
+  c->timed.clear();
+  c->ev_next = 0;
+}
+
 void timing_hook(void *ctx, const char *name, int after, hipStream_t s) {
   moe_ctx *c = (moe_ctx *)ctx;
   if (c->timing == 2 && std::strcmp(name, "moe_decode") != 0 && std::strncmp(name, "pf_gate_up", 10) != 0) return;
+  if (!after && c->timed.size() >= kTimedFold) fold_timed(c);
   if (!after) {
     c->timed.push_back(TimedLaunch{name, timing_event(c, s), nullptr});
   } else {
@@ -238,7 +276,8 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
   if (w) check(hipMemcpyAsync(w, c->last_w, sizeof(float) * T * K, hipMemcpyDeviceToDevice, s), "copy w");
 }
 
-// A wait inside moe_decode gave up: its result is not to be trusted.
+// A wait inside moe_decode gave up: its result is not to be trusted. The caller has synchronised the stream the
+// forward ran on.
 void check_err(moe_ctx *c) {
   uint32_t e = 0;
   check(hipMemcpy(&e, c->err_flag, 4, hipMemcpyDeviceToHost), "read error flag");
@@ -533,6 +572,14 @@ MOE_API moe_status moe_sync(moe_ctx *c) {
   });
 }
 
+MOE_API moe_status moe_check(moe_ctx *c, void *stream) {
+  return guarded(c, [&] {
+    check(hipStreamSynchronize(stream ? (hipStream_t)stream : c->stream), "hipStreamSynchronize");
+    if (c->pf.side) check(hipStreamSynchronize(c->pf.side), "hipStreamSynchronize");
+    check_err(c);
+  });
+}
+
 MOE_API void *moe_stream(moe_ctx *c) { return c ? (void *)c->stream : nullptr; }
 
 MOE_API moe_status moe_set_timing(moe_ctx *c, int on) {
@@ -542,6 +589,7 @@ MOE_API moe_status moe_set_timing(moe_ctx *c, int on) {
     c->timing = on;
     c->ev_used = 0, c->ev_next = 0;
     c->timed.clear();
+    c->timed_sums.clear();
   });
 }
 
@@ -551,27 +599,16 @@ MOE_API moe_status moe_kernel_times(moe_ctx *c, const char **names, float *avg_m
     require(n != nullptr, "null n");
     *n = 0;
     if (forwards) *forwards = c->ev_used;
-    if (c->timed.empty()) return;
-    check(hipEventSynchronize(c->timed.back().b), "hipEventSynchronize");
     // Kernels in order of first launch; the average over their launches.
-    std::vector<const char *> order;
-    std::vector<double> sum;
-    std::vector<uint32_t> cnt;
-    for (const TimedLaunch &t : c->timed) {
-      size_t i = 0;
-      while (i < order.size() && std::strcmp(order[i], t.name) != 0) i++;
-      if (i == order.size()) order.push_back(t.name), sum.push_back(0.0), cnt.push_back(0);
-      float ms = 0.0f;
-      check(hipEventElapsedTime(&ms, t.a, t.b), "hipEventElapsedTime");
-      sum[i] += ms, cnt[i]++;
-    }
-    for (size_t i = 0; i < order.size() && i < cap; i++) {
-      if (names) names[i] = order[i];
-      if (avg_ms) avg_ms[i] = (float)(sum[i] / cnt[i]);
+    fold_timed(c);
+    for (size_t i = 0; i < c->timed_sums.size() && i < cap; i++) {
+      if (names) names[i] = c->timed_sums[i].name;
+      if (avg_ms) avg_ms[i] = (float)(c->timed_sums[i].ms / c->timed_sums[i].n);
       *n = (uint32_t)i + 1;
     }
     c->ev_used = 0, c->ev_next = 0;
     c->timed.clear();
+    c->timed_sums.clear();
   });
 }
 
@@ -644,17 +681,15 @@ MOE_API moe_status moe_dequantize(moe_ctx *c, uint32_t type, const uint8_t *bloc
     std::vector<uint8_t> buf(mb);
     repack_matrix(type, blocks, rows, cols, buf.data());
     const uint32_t nrt = (rows + kTileRows - 1) / kTileRows;
-    uint8_t *dm = nullptr;
-    float *dout = nullptr;
-    check(hipMalloc(&dm, mb), "hipMalloc");
-    check(hipMalloc(&dout, (uint64_t)nrt * kTileRows * cols * sizeof(float)), "hipMalloc");
-    check(hipMemcpy(dm, buf.data(), mb, hipMemcpyHostToDevice), "upload");
-    hipLaunchKernelGGL(moe_dequant, dim3(nrt), dim3(64), 0, c->stream, dm, type, rows, cols, dout);
+    DevBuf dm, dout;
+    check(hipMalloc(&dm.p, mb), "hipMalloc");
+    check(hipMalloc(&dout.p, (uint64_t)nrt * kTileRows * cols * sizeof(float)), "hipMalloc");
+    check(hipMemcpy(dm.p, buf.data(), mb, hipMemcpyHostToDevice), "upload");
+    hipLaunchKernelGGL(moe_dequant, dim3(nrt), dim3(64), 0, c->stream, (const uint8_t *)dm.p, type, rows, cols,
+                       (float *)dout.p);
     check(hipGetLastError(), "moe_dequant");
     check(hipStreamSynchronize(c->stream), "moe_dequant");
-    check(hipMemcpy(out, dout, (uint64_t)rows * cols * sizeof(float), hipMemcpyDeviceToHost), "download");
-    (void)hipFree(dm);
-    (void)hipFree(dout);
+    check(hipMemcpy(out, dout.p, (uint64_t)rows * cols * sizeof(float), hipMemcpyDeviceToHost), "download");
   });
 }
 

@@ -100,7 +100,10 @@ MOE_API moe_status moe_load_expert(moe_ctx *ctx, uint32_t layer, uint32_t expert
 MOE_API moe_status moe_forward(moe_ctx *ctx, uint32_t layer, const float *x, uint32_t ntok, uint64_t x_stride,
                                float *y, uint64_t y_stride, moe_route_out *route);
 /* The same on device memory (x and y ntok x n_embd fp32, contiguous; ids and w ntok x n_used or null), enqueued on
- * stream (a hipStream_t; null: the context's stream). Nothing is copied and nothing waits. */
+ * stream (a hipStream_t; null: the context's stream). Nothing is copied and nothing waits. A context's forwards share
+ * its scratch (work counters, hand-off records, intermediate buffers), so they must be ordered: enqueue them on one
+ * stream, or make each stream wait for the previous forward's (an event) before enqueueing the next. moe_check
+ * reports a forward whose internal waits gave up (MOE_TIMEOUT). */
 MOE_API moe_status moe_forward_async(moe_ctx *ctx, uint32_t layer, const float *x_dev, uint32_t ntok, float *y_dev,
                                      int32_t *ids_dev, float *w_dev, void *stream);
 /* CpuExperts::compute_many on resident experts: y[tok] = sum over the jobs with that tok, in the order given, of
@@ -119,6 +122,10 @@ MOE_API moe_status moe_prefill_dispatch(moe_ctx *ctx, MoeTile *tiles, uint32_t c
 
 /* Waits for the context's stream. */
 MOE_API moe_status moe_sync(moe_ctx *ctx);
+/* Waits for stream (null: the context's stream), then reports whether any forward since the last check had a wait
+ * inside the decode kernel give up (MOE_TIMEOUT: its y is not to be trusted) and clears that state. Call it after
+ * moe_forward_async calls on a stream of the caller's. */
+MOE_API moe_status moe_check(moe_ctx *ctx, void *stream);
 /* The context's HIP stream (a hipStream_t). */
 MOE_API void *moe_stream(moe_ctx *ctx);
 

@@ -106,3 +106,48 @@ def test_prefill_config4_sampled():
     assert np.array_equal(io2, ids[sample])
     check_exact(y[sample], ids[sample], w[sample], yo, io2, w[sample])
     blk.close()
+
+
+def test_prefill_dispatch_past_lds_cache():
+    """More assignments than the dispatch keeps in LDS (T k > 40960: the ids are read from global memory on the
+    position pass). Tiles and perm against the stable counting sort; ids, w and y against the oracle on a sample."""
+    say("prefill dispatch, 4200 tokens x k 10")
+    L = h.Layer(512, 256, 64, 10, Q4, Q8, seed=4200, zipf=1.1)
+    T = 4200
+    blk = L.block(max_tokens=T)
+    L.upload(blk)
+    x = h.tokens(4200, T, 512)
+    y, ids, w = blk.forward(0, x)
+    tiles, perm = blk.prefill_dispatch(T)
+    et, ep = expected_dispatch(ids, L.E)
+    assert T * 10 > 40960
+    assert np.array_equal(tiles, et) and np.array_equal(perm, ep)
+    _, io, wo = L.oracle_route(x)
+    assert np.array_equal(ids, io) and np.array_equal(w, wo)
+    sample = np.r_[0:40, 2090:2110, T - 40:T]
+    yo, io2, wo2 = L.oracle_forward(x[sample], nthreads=16)
+    check_exact(y[sample], ids[sample], w[sample], yo, io2, wo2)
+    blk.close()
+
+
+def test_prefill_config5_chunk_sampled():
+    """BASELINE config 5's layer at full size, one 2048-token prefill chunk: H 2048, F 512, 512 experts, top-10,
+    gate/up IQ3_S, down Q4_K, shared expert Q8_0, Zipf(1.1). Hot experts span many 64-row tiles. ids and w on every
+    token, y on a sample (each token's y depends on that token alone)."""
+    say("prefill config 5 chunk")
+    L = h.Layer(2048, 512, 512, 10, I3, Q4, Q8, Q8, seed=2026, zipf=1.1, nthreads=0)
+    blk = L.block(max_tokens=2048)
+    L.upload(blk)
+    T = 2048
+    x = h.tokens(2027, T, 2048)
+    y, ids, w = blk.forward(0, x)
+    tiles, perm = blk.prefill_dispatch(T)
+    et, ep = expected_dispatch(ids, L.E)
+    assert np.array_equal(tiles, et) and np.array_equal(perm, ep)
+    assert tiles[:, 3].sum() == T * 10 and np.bincount(tiles[:, 0]).max() >= 8  # a hot expert over >= 8 tiles
+    _, io, wo = L.oracle_route(x)
+    assert np.array_equal(ids, io) and np.array_equal(w, wo)
+    sample = np.r_[0:32, 1024:1040, T - 32:T]
+    yo, io2, wo2 = L.oracle_forward(x[sample], nthreads=16)
+    check_exact(y[sample], ids[sample], w[sample], yo, io2, wo2)
+    blk.close()
