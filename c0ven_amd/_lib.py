@@ -61,6 +61,7 @@ _SIGS = {
     "moe_load_expert": (_i32, [_P, _u32, _u32, _P, _P, _P]),
     "moe_forward": (_i32, [_P, _u32, _P, _u32, _u64, _P, _u64, C.POINTER(MoeRouteOut)]),
     "moe_forward_async": (_i32, [_P, _u32, _P, _u32, _P, _P, _P, _P]),
+    "moe_forward_async_noalloc": (_i32, [_P, _u32, _P, _u32, _P, _P, _P, _P]),
     "moe_forward_experts": (_i32, [_P, C.POINTER(MoeJob), _u32, _u32, _P, _u64, _P, _u64]),
     "moe_h_rows": (_u32, [C.POINTER(MoeConfig)]),
     "moe_prefill_dispatch": (_i32, [_P, C.POINTER(MoeTile), _u32, C.POINTER(_u32), _P]),
@@ -193,6 +194,9 @@ class MoeBlock:
 
     def forward_async(self, layer, x_dev, ntok, y_dev, ids_dev=None, w_dev=None, stream=None):
         self._check(lib.moe_forward_async(self.h, layer, x_dev, ntok, y_dev, ids_dev, w_dev, stream))
+
+    def forward_async_noalloc(self, layer, x_dev, ntok, y_dev, ids_dev=None, w_dev=None, stream=None):
+        self._check(lib.moe_forward_async_noalloc(self.h, layer, x_dev, ntok, y_dev, ids_dev, w_dev, stream))
 
     def forward_experts(self, jobs, x):
         """jobs: list of (layer, expert, tok, w)."""

@@ -2,9 +2,11 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstddef>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -73,6 +75,96 @@ struct DevBuf {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------------------------------------------
+// The decode kernel's scratch for moe_forward_async_noalloc: one array per GPU, in the library's own device memory
+// (no call allocates it). Host code never passes the array's name to a kernel: on the host that name is a stand-in,
+// not a device address. Each device's address comes from hipGetSymbolAddress, taken once per device (with it
+// current) when the first context opens on it, and is used everywhere instead. Calls on one GPU share the array and
+// the launch tags below, so they must be ordered (one stream, or event waits); overlapping calls race.
+constexpr uint64_t kNoAllocScratchBytes = 16ull << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct NoAllocScratch {
+  uint8_t *ptr = nullptr;            // this device's copy of `scratch`
+  std::atomic<uint64_t> epoch{0};    // the last no-alloc launch's number on this device (tags every record)
+};
+NoAllocScratch g_noalloc[kMaxDevices];
+std::mutex g_noalloc_mu;
+
+// Zeroes n words (a fill kernel, not hipMemsetAsync: the no-alloc path may be captured into a HIP graph).
+__global__ void fill_zero_u32(uint32_t *p, uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+void zero_words(void *p, uint64_t bytes, hipStream_t s) {
+  const uint64_t n = bytes / 4;
+  hipLaunchKernelGGL(fill_zero_u32, dim3((uint32_t)std::min<uint64_t>((n + 255) / 256, 2048)), dim3(256), 0, s,
+                     (uint32_t *)p, n);
+  check(hipGetLastError(), "fill_zero_u32");
+}
+
+// Once per device (the device current): the array's address, and its contents zeroed (tag 0 is never a launch's).
+void noalloc_setup(int dev) {
+  std::lock_guard<std::mutex> g(g_noalloc_mu);
+  NoAllocScratch &d = g_noalloc[dev];
+  if (d.ptr) return;
+  void *ptr = nullptr;
+  check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  zero_words(ptr, kNoAllocScratchBytes, nullptr);
+  check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  d.ptr = (uint8_t *)ptr;
+}
+
+// Where the decode scratch of a context's shape sits inside a base (the array's device address, or null to size it).
+struct NoAllocLayout {
+  uint8_t *act_r, *act_s;
+  uint64_t *logits, *gs, *ids_t, *w_t, *h, *y_asg, *flags;
+  int32_t *ids;
+  float *w;
+  MoeGroup *groups;
+  uint32_t *ngroups, *counters;
+  uint64_t bytes, tagged_bytes;  // all of it; the leading part of it that holds tagged records and counters
+};
+
+NoAllocLayout noalloc_layout(const moe_config &g, uint8_t *base) {
+  const uint32_t T = std::min<uint32_t>(g.max_tokens, kMaxDecodeTokens), K1 = g.n_used + 1;
+  const uint32_t A = T * K1 + T, Ug = g.n_embd / kUnit, E = g.n_expert;
+  uint64_t off = 0;
+  auto take = [&](uint64_t bytes) {
+    uint8_t *q = base ? base + off : nullptr;
+    off += (bytes + 255) / 256 * 256;
+    return q;
+  };
+  NoAllocLayout L{};
+  // The counters and flags first, at the same place for every shape: contexts of different shapes share them, and a
+  // launch relies on the previous launch (of any context) having reset the list counters it will use. Then the
+  // tagged records: with the counters and flags, the part a tag wrap clears.
+  L.counters = (uint32_t *)take((uint64_t)(3 + 2 * kDynLists * kDynStride + kDynStride) * 4);
+  L.flags = (uint64_t *)take((uint64_t)kFlagCount * 8);
+  L.logits = (uint64_t *)take((uint64_t)T * (E + 1) * 8);
+  L.gs = (uint64_t *)take((uint64_t)T * 8);
+  L.ids_t = (uint64_t *)take((uint64_t)T * K1 * 8);
+  L.w_t = (uint64_t *)take((uint64_t)T * K1 * 8);
+  L.h = (uint64_t *)take((uint64_t)A * g.n_ff * 8);
+  L.y_asg = (uint64_t *)take((uint64_t)A * g.n_embd * 8);
+  L.tagged_bytes = off;
+  L.act_r = take((uint64_t)T * Ug * kActBytes);
+  L.act_s = take((uint64_t)T * Ug * kActBytes);
+  L.ids = (int32_t *)take((uint64_t)T * K1 * 4);
+  L.w = (float *)take((uint64_t)T * K1 * 4);
+  L.groups = (MoeGroup *)take((uint64_t)max_groups(T, K1) * sizeof(MoeGroup));
+  L.ngroups = (uint32_t *)take(4);
+  L.bytes = off;
+  return L;
+}
+
+}  // namespace
+
 struct moe_ctx {
   moe_config cfg{};
   hipStream_t stream = nullptr;
@@ -96,6 +188,7 @@ struct moe_ctx {
   uint32_t *cnt_route = nullptr, *cnt_topk = nullptr, *cnt_dyn = nullptr;
   uint32_t *err_flag = nullptr;
   uint64_t *flags = nullptr;
+  uint64_t noalloc_bytes = 0;  // the no-alloc path's share of the device's scratch array for this shape
   uint64_t epoch = 0;          // the last launch's number
   std::vector<std::pair<uint64_t *, uint64_t>> tagged;  // the tagged-record buffers (pointer, records)
   uint32_t grid = 0;           // co-resident work-groups of moe_decode
@@ -287,6 +380,19 @@ void check_err(moe_ctx *c) {
   }
 }
 
+// The same for the no-alloc path's error word (in the device's scratch array).
+void check_err_noalloc(moe_ctx *c) {
+  uint8_t *base = g_noalloc[c->cfg.device].ptr;
+  if (!base || c->noalloc_bytes > kNoAllocScratchBytes) return;
+  uint32_t *err = noalloc_layout(c->cfg, base).counters + 2;
+  uint32_t e = 0;
+  check(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost), "read error flag");
+  if (e) {
+    (void)hipMemset(err, 0, 4);
+    throw Error(MOE_TIMEOUT, "moe_decode (no-alloc): a work item waited past its limit");
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -409,6 +515,9 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     require(per_cu >= 1, "moe_decode does not fit a CU");
     if (const char *e = std::getenv("C0VEN_DECODE_WG_PER_CU")) per_cu = std::max(1, std::min(per_cu, std::atoi(e)));
     c->grid = (uint32_t)(per_cu * ncu);
+    require(g.device < kMaxDevices, "device ordinal too large");
+    noalloc_setup(g.device);
+    c->noalloc_bytes = noalloc_layout(g, nullptr).bytes;
     check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     *out = c;
     return MOE_OK;
@@ -577,6 +686,42 @@ MOE_API moe_status moe_check(moe_ctx *c, void *stream) {
     check(hipStreamSynchronize(stream ? (hipStream_t)stream : c->stream), "hipStreamSynchronize");
     if (c->pf.side) check(hipStreamSynchronize(c->pf.side), "hipStreamSynchronize");
     check_err(c);
+    check_err_noalloc(c);
+  });
+}
+
+MOE_API moe_status moe_forward_async_noalloc(moe_ctx *c, uint32_t layer, const float *x_dev, uint32_t ntok,
+                                             float *y_dev, int32_t *ids_dev, float *w_dev, void *stream) {
+  return guarded(c, [&] {
+    require(x_dev && y_dev, "null x or y");
+    require(layer < c->cfg.n_layer, "layer out of range");
+    require(ntok >= 1 && ntok <= c->tdec, "moe_forward_async_noalloc takes 1..min(max_tokens, 16) tokens (the decode kernel)");
+    require(c->layers[layer].router != nullptr, "the layer's router is not loaded");
+    require(c->noalloc_bytes <= kNoAllocScratchBytes,
+            "the context's decode scratch (" + std::to_string(c->noalloc_bytes) + " B) exceeds the no-alloc array (" +
+                std::to_string(kNoAllocScratchBytes) + " B)");
+    NoAllocScratch &d = g_noalloc[c->cfg.device];
+    require(d.ptr != nullptr, "no-alloc scratch not set up on this device");
+    hipStream_t s = stream ? (hipStream_t)stream : c->stream;
+    const NoAllocLayout L = noalloc_layout(c->cfg, d.ptr);
+    DecodeParams p = base_params(c, layer, ntok);
+    p.act_r = L.act_r, p.act_s = p.xact_s == p.xact_r ? L.act_r : L.act_s;
+    p.logits = L.logits, p.ids = L.ids, p.w = L.w, p.gs = L.gs, p.ids_t = L.ids_t, p.w_t = L.w_t;
+    p.groups = L.groups, p.ngroups = L.ngroups, p.h = L.h, p.y_asg = L.y_asg, p.flags = L.flags;
+    p.cnt_route = L.counters, p.cnt_topk = L.counters + 1, p.err = L.counters + 2, p.cnt_dyn = L.counters + 2 + kDynStride;
+    p.x = x_dev, p.y = y_dev;
+    p.epoch = ++d.epoch;
+    if ((uint32_t)p.epoch == 0) {  // the 32-bit tags wrap: clear the records (a fill kernel), then take the next tag
+      zero_words(d.ptr, L.tagged_bytes, s);
+      p.epoch = ++d.epoch;
+    }
+    p.tag = (uint32_t)p.epoch;
+    void *args[] = {&p};
+    check(hipLaunchKernel(c->kernel, dim3(c->grid), dim3(kWG), args, c->lds, s), "moe_decode launch");
+    check(hipGetLastError(), "moe_decode launch");
+    const uint32_t K = c->cfg.n_used;
+    if (ids_dev) check(hipMemcpyAsync(ids_dev, L.ids, sizeof(int32_t) * ntok * K, hipMemcpyDeviceToDevice, s), "copy ids");
+    if (w_dev) check(hipMemcpyAsync(w_dev, L.w, sizeof(float) * ntok * K, hipMemcpyDeviceToDevice, s), "copy w");
   });
 }
 

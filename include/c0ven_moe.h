@@ -106,6 +106,14 @@ MOE_API moe_status moe_forward(moe_ctx *ctx, uint32_t layer, const float *x, uin
  * reports a forward whose internal waits gave up (MOE_TIMEOUT). */
 MOE_API moe_status moe_forward_async(moe_ctx *ctx, uint32_t layer, const float *x_dev, uint32_t ntok, float *y_dev,
                                      int32_t *ids_dev, float *w_dev, void *stream);
+/* No counterpart in the reference: moe_forward_async for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The decode kernel only (ntok at most
+ * min(max_tokens, 16)); its scratch lives in one statically sized array per GPU (16 MiB, set up when the first context
+ * opens on that GPU) instead of the context's, and the call allocates nothing. A context whose decode scratch would
+ * exceed the array is refused with MOE_BAD_ARGUMENT. Every call on a GPU shares that GPU's array, so calls on one GPU
+ * must be ordered (one stream, or event waits): calls that overlap on one GPU race. Results equal moe_forward_async's. */
+MOE_API moe_status moe_forward_async_noalloc(moe_ctx *ctx, uint32_t layer, const float *x_dev, uint32_t ntok,
+                                             float *y_dev, int32_t *ids_dev, float *w_dev, void *stream);
 /* CpuExperts::compute_many on resident experts: y[tok] = sum over the jobs with that tok, in the order given, of
  * w * expert(x[tok]); no router, no gate. Synchronous, host buffers. */
 MOE_API moe_status moe_forward_experts(moe_ctx *ctx, const moe_job *jobs, uint32_t njobs, uint32_t ntok,
