@@ -58,11 +58,19 @@ __device__ __forceinline__ void put_word(uint8_t *out, uint32_t off, T v) {
   }
 }
 
+// The byte offset of codes 8 j .. 8 j + 7 of a unit in the prefill (matrix-core) order: the eight bytes lane group
+// g = j % 4 takes of 32-value block b = j / 4 sit next to those it takes of block b ^ 1, so that one 16-byte read gives
+// a lane its operand of a v_mfma_i32_16x16x64_i8 (blocks 2 c and 2 c + 1: 64 c + 16 g, then + 8 for the odd block).
+__host__ __device__ __forceinline__ constexpr uint32_t mfma_code_off(uint32_t j) {
+  return 64 * (j / 8) + 16 * (j % 4) + 8 * ((j / 4) % 2);
+}
+
 // One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
 // with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0). out is in global
-// memory, or in LDS when kLds.
-template <bool kLds = false, bool kSplitG = false>
+// memory, or in LDS when kLds. kMfma: the codes in the prefill order (mfma_code_off) instead of value order.
+template <bool kLds = false, bool kSplitG = false, bool kMfma = false>
 __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
+  const uint32_t coff = kMfma ? mfma_code_off(l32) : 8 * l32;
   uint32_t code[2] = {0u, 0u};
   if (act_type == QT_Q8_K) {
     // The value of largest magnitude, the first of equals: (|v|, index) reduced over the 32 lanes.
@@ -94,8 +102,8 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
     }
     part += __shfl_xor(part, 1, 32);
     part += __shfl_xor(part, 2, 32);
-    put_word<kLds>(out, 8 * l32, code[0]);
-    put_word<kLds>(out, 8 * l32 + 4, code[1]);
+    put_word<kLds>(out, coff, code[0]);
+    put_word<kLds>(out, coff + 4, code[1]);
     if ((l32 & 3u) == 0) put_word<kLds>(out, kActSums + l32, part);
     if (l32 == 0) put_word<kLds>(out, kActScales, d);
     if constexpr (kSplitG) {
@@ -117,8 +125,8 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
       const int q = nearest_int(__fmul_rn(v[i], id));
       code[i / 4] |= ((uint32_t)q & 0xffu) << (8 * (i % 4));
     }
-    put_word<kLds>(out, 8 * l32, code[0]);
-    put_word<kLds>(out, 8 * l32 + 4, code[1]);
+    put_word<kLds>(out, coff, code[0]);
+    put_word<kLds>(out, coff + 4, code[1]);
     if ((l32 & 3u) == 0) put_word<kLds>(out, kActScales + l32, h2f(f2h(d)));
     if ((l32 & 3u) == 0) put_word<kLds>(out, kActSums + l32, 0);
   }

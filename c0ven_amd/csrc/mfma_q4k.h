@@ -60,7 +60,8 @@ __device__ __forceinline__ uint32_t bcast_byte(uint32_t v, uint32_t b) {
 // 0-3 (scales) and 4-7 (minima); blocks 4-7 take four bits from bytes 8-11 and their top two from the top bits of
 // bytes 0-3 (scales) and 4-7 (minima).
 struct Q4kA {
-  long lo[8], hi[8], mn;
+  v4i_t lo[4], hi[4];  // chain step c: blocks 2 c (elements 0-1) and 2 c + 1 (elements 2-3), as join2 packs them
+  long mn;
   float d[4], dmin[4];
   __device__ __forceinline__ void decode(const Q4kRaw &r, uint32_t lane) {
     const uint32_t w0 = r.sc[0], w1 = r.sc[1], w2 = r.sc[2];
@@ -77,10 +78,8 @@ struct Q4kA {
       const uint32_t bl = (2 * c) % 4, bh = (2 * c + 1) % 4, hw = c / 2;  // blocks 2 c, 2 c + 1: bytes, word
       const uint32_t kl_lo = bcast_byte(slo[hw], bl), kl_hi = bcast_byte(shi[hw], bl);
       const uint32_t kh_lo = bcast_byte(slo[hw], bh), kh_hi = bcast_byte(shi[hw], bh);
-      lo[2 * c] = pack2(mul_bytes(l0, kl_lo), mul_bytes(l1, kl_lo));
-      hi[2 * c] = pack2(mul_bytes(l0, kl_hi), mul_bytes(l1, kl_hi));
-      lo[2 * c + 1] = pack2(mul_bytes(h0, kh_lo), mul_bytes(h1, kh_lo));
-      hi[2 * c + 1] = pack2(mul_bytes(h0, kh_hi), mul_bytes(h1, kh_hi));
+      lo[c] = v4i_t{(int)mul_bytes(l0, kl_lo), (int)mul_bytes(l1, kl_lo), (int)mul_bytes(h0, kh_lo), (int)mul_bytes(h1, kh_lo)};
+      hi[c] = v4i_t{(int)mul_bytes(l0, kl_hi), (int)mul_bytes(l1, kl_hi), (int)mul_bytes(h0, kh_hi), (int)mul_bytes(h1, kh_hi)};
     }
     mn = lane < 16 ? pack2(m03, m47) : 0;
 #pragma unroll
@@ -143,23 +142,47 @@ __device__ __forceinline__ v4i_t join2(long x, long y) {
 // The unit's terms t[i] (rows 4 g + i, token l % 16): fma(d ad, isum, -((dmin ad) imin)) as UnitQ4_K::term.
 // The code chains take two blocks per v_mfma_i32_16x16x64_i8 (blocks 2 c and 2 c + 1: a lane's eight bytes of each,
 // in A and in B alike, so every A byte still meets its own activation byte; the sum over K is the same integer).
-__device__ __forceinline__ void q4k_terms(const Q4kA &a, const ActB &b, float t[4]) {
+// bq[c]: the lane's B operand of chain step c; bh, bl: the split block sums (lanes < 16); ad: the unit's scale.
+__device__ __forceinline__ void q4k_terms_v(const Q4kA &a, const v4i_t bq[4], long bh, long bl, float ad, float t[4]) {
   v4i_t dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0};
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    const v4i_t bq = join2(b.q[2 * c], b.q[2 * c + 1]);
-    dlo = __builtin_amdgcn_mfma_i32_16x16x64_i8(join2(a.lo[2 * c], a.lo[2 * c + 1]), bq, dlo, 0, 0, 0);
-    dhi = __builtin_amdgcn_mfma_i32_16x16x64_i8(join2(a.hi[2 * c], a.hi[2 * c + 1]), bq, dhi, 0, 0, 0);
+    dlo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.lo[c], bq[c], dlo, 0, 0, 0);
+    dhi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.hi[c], bq[c], dhi, 0, 0, 0);
   }
-  const v4i_t mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.mn, b.bh, v4i_t{0, 0, 0, 0}, 0, 0, 0);
-  const v4i_t ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.mn, b.bl, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+  const v4i_t mh = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.mn, bh, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+  const v4i_t ml = __builtin_amdgcn_mfma_i32_16x16x32_i8(a.mn, bl, v4i_t{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int isum = 8 * dhi[i] + dlo[i], imin = 64 * mh[i] + ml[i];
-    const float dd = __fmul_rn(a.d[i], b.ad), dm = __fmul_rn(a.dmin[i], b.ad);
+    const float dd = __fmul_rn(a.d[i], ad), dm = __fmul_rn(a.dmin[i], ad);
     const float pm = __fmul_rn(dm, (float)imin);
     t[i] = __builtin_fmaf(dd, (float)isum, -pm);
   }
 }
+
+__device__ __forceinline__ void q4k_terms(const Q4kA &a, const ActB &b, float t[4]) {
+  v4i_t bq[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) bq[c] = join2(b.q[2 * c], b.q[2 * c + 1]);
+  q4k_terms_v(a, bq, b.bh, b.bl, b.ad, t);
+}
+
+// A prefill activation unit's B operands (codes in the mfma_code_off order, split sums at kActSplitG): four 16-byte
+// reads for the code chains.
+struct ActBP {
+  v4i_t q[4];
+  long bh, bl;
+  float ad;
+  __device__ __forceinline__ void load(const uint8_t *unit, uint32_t lane) {
+    const uint32_t g = lane / 16;
+#pragma unroll
+    for (int c = 0; c < 4; c++) q[c] = *(const v4i_t *)(unit + 64 * c + 16 * g);
+    const uint4 v = *(const uint4 *)(unit + kActSplitG);
+    bh = g == 0 ? pack2(v.x, v.y) : 0;
+    bl = g == 0 ? pack2(v.z, v.w) : 0;
+    ad = *(const float *)(unit + kActScales);
+  }
+};
 
 }  // namespace c0ven

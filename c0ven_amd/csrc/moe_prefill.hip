@@ -38,7 +38,8 @@ __device__ __forceinline__ uint32_t lane_id() { return tid_fresh() & 63u; }
 __device__ __forceinline__ uint32_t wave_id() { return tid_fresh() >> 6; }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Activation units: one half-wave per (row, unit), eight values a lane; o2 (a second type) may be null.
+// Activation units: one half-wave per (row, unit), eight values a lane; o2 (a second type) may be null. The codes are
+// stored in the matrix-core order (mfma_code_off), which every prefill GEMM reads.
 
 __global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_t ld, uint32_t rows, uint32_t U,
                                                        uint32_t t1, uint8_t *o1, uint32_t t2, uint8_t *o2) {
@@ -48,8 +49,8 @@ __global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_
   const float4 *p = (const float4 *)(src + (uint64_t)row * ld + u * kUnit + 8 * l32);
   const float4 a = p[0], b = p[1];
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  quant_unit<false, true>(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
-  if (o2) quant_unit<false, true>(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
+  quant_unit<false, true, true>(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
+  if (o2) quant_unit<false, true, true>(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -300,32 +301,47 @@ struct PfGemm {
 template <bool kGU>
 constexpr uint32_t gemm_rows() { return kGU ? 64 : 128; }
 
-// Unit u of a tile's 64 positions (global rows arow[], 0xffffffff for none) into LDS at buf by direct global-to-LDS
-// loads, issued by the calling wave's share. LDS holds 21 pieces of 16 B a position (kActLds = 336), so the wave's
-// i-th load fills pieces 64 i .. 64 i + 63 contiguously; pieces 0-19 are the 320-byte global unit verbatim (with the
-// split block sums at kActSplitG for q8_K), piece 20 and positions without a row are not loaded (their MFMA columns
-// are never stored). The caller waits (s_waitcnt vmcnt(0)) and synchronises before reading.
-__device__ __forceinline__ void pf_act_dma(const uint8_t *act, const uint32_t *arow, uint32_t U, uint32_t u, uint8_t *buf) {
-  constexpr uint32_t kPieces = 64 * kActLds / 16, kLoads = kPieces / 64;
-  static_assert(kActLds == 21 * 16 && kPieces % 64 == 0, "activation pieces");
+// A tile's 64 positions' activation units go into LDS by direct global-to-LDS loads: LDS holds 21 pieces of 16 B a
+// position (kActLds = 336), so load i (of 21) fills pieces 64 i .. 64 i + 63 contiguously, lane l piece 64 i + l, of
+// position (64 i + l) / 21. Pieces 0-19 are the 320-byte global unit verbatim (with the split block sums at kActSplitG
+// for q8_K). The 21 loads are dealt to the four waves (load i to wave i % 4); a wave's global offsets are the same for
+// every unit but for + u kActBytes, so they are worked out once (dma_plan). Piece 20 (padding) and positions without a
+// row load the first unit instead: the bytes land where no operand is read (padding, or MFMA columns never stored),
+// and every lane issues its loads, without branches.
+constexpr uint32_t kDmaLoads = 64 * kActLds / 16 / 64, kDmaPer = (kDmaLoads + 3) / 4;
+static_assert(kActLds == 21 * 16 && kDmaLoads == 21, "activation pieces");
+
+__device__ __forceinline__ void dma_plan(const uint32_t *arow, uint32_t U, uint32_t off[kDmaPer]) {
 #pragma unroll
-  for (uint32_t i = wave_id(); i < kLoads; i += kPfWG / 64) {
-    const uint32_t piece = 64 * i + lane_id(), pos = piece / 21, c = piece % 21, ar = arow[pos];
-    if (c < 20 && ar != 0xffffffffu)
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void *)(act + ((uint64_t)ar * U + u) * kActBytes + 16 * c),
-          (__attribute__((address_space(3))) void *)(buf + 64 * 16 * i), 16, 0, 0);
+  for (uint32_t k = 0; k < kDmaPer; k++) {
+    const uint32_t i = wave_id() + 4 * k, piece = 64 * i + lane_id(), pos = piece / 21, c = piece % 21;
+    const uint32_t ar = i < kDmaLoads ? arow[pos] : 0xffffffffu;
+    off[k] = c < 20 && ar != 0xffffffffu ? ar * U * kActBytes + 16 * c : 0u;
   }
 }
 
-// Work-group b of a 1-D grid of n runs on XCD b % 8 (the dispatcher deals work-groups to the eight XCDs in turn).
-// Its logical index puts consecutive logical indices on one XCD: (b % 8) ceil(n / 8) + b / 8. With the row block
-// fastest in the logical index, a tile's row blocks run together on one XCD (its activations come from that XCD's
-// L2), and the next tile of the same expert follows on the same XCD (its weights too). Returns n or more for the
-// slots past n.
+// Unit u of the planned positions into LDS at buf (the calling wave's share of the 21 loads). The caller waits
+// (s_waitcnt vmcnt(0)) and synchronises before reading.
+__device__ __forceinline__ void pf_act_dma(const uint8_t *act, const uint32_t off[kDmaPer], uint32_t u, uint8_t *buf) {
+  const uint8_t *base = act + (uint64_t)u * kActBytes;
+#pragma unroll
+  for (uint32_t k = 0; k < kDmaPer; k++) {
+    const uint32_t i = wave_id() + 4 * k;
+    if (i < kDmaLoads)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(base + off[k]),
+                                       (__attribute__((address_space(3))) void *)(buf + 64 * 16 * i), 16, 0, 0);
+  }
+}
+
+// Work-group b (< n) of a 1-D grid runs on XCD b % 8 (the dispatcher deals work-groups to the eight XCDs in turn), as
+// the (b / 8)-th of the cnt_x = floor((n - x + 7) / 8) that XCD x receives among the first n. Its logical index puts
+// consecutive logical indices on one XCD: XCD x takes [off_x, off_x + cnt_x), off_x = x floor(n / 8) + min(x, n % 8),
+// a bijection of [0, n) for any n. With the row block fastest in the logical index, a tile's row blocks run together
+// on one XCD (its activations come from that XCD's L2), and the next tile of the same expert follows on the same XCD
+// (its weights too). The caller returns for b >= n.
 __device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
-  const uint32_t per = (n + 7) / 8;
-  return (b % 8) * per + b / 8;
+  const uint32_t x = b % 8, q = n / 8, r = n % 8;
+  return x * q + min(x, r) + b / 8;
 }
 
 // Q4_K, IQ3_S and Q8_0 on 16 x 16 int8 MFMA tiles (mfma_q4k.h, the decode path's tile; mfma_iq3s.h; mfma_q8_0.h):
@@ -377,9 +393,11 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   const uint32_t row0 = rb * kRows + (kGU ? 16 * (w & 1) : 16 * w);
   const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
   const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
+  uint32_t doff[kDmaPer];
+  dma_plan(arow_lds, U, doff);
   Raw raw;
   raw.load(M, U, row0, 0, lane_id());
-  pf_act_dma(g.act, arow_lds, U, 0, &abuf[0][0]);
+  pf_act_dma(g.act, doff, 0, &abuf[0][0]);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   float acc[4][4];
@@ -391,7 +409,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   for (uint32_t u = 0; u < U; u++) {
     Raw next;
     if (u + 1 < U) {
-      pf_act_dma(g.act, arow_lds, U, u + 1, &abuf[(u + 1) & 1][0]);
+      pf_act_dma(g.act, doff, u + 1, &abuf[(u + 1) & 1][0]);
       next.load(M, U, row0, u + 1, lane_id());
     }
     const uint8_t *buf = abuf[u & 1];
@@ -403,9 +421,9 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
       for (int pt = 0; pt < 4; pt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) isum[pt][i] = 0;
-      const uint32_t g8 = 8 * (lane_id() / 16);
 #pragma unroll
       for (uint32_t ib = 0; ib < 8; ib++) {
+        const uint32_t bofs = mfma_code_off(4 * ib + lane_id() / 16);  // the lane's 8 codes of block ib
         const long aw = raw.a_block(ib, lane_id(), grid_lds);
         int ls[4];
 #pragma unroll
@@ -413,7 +431,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
 #pragma unroll
         for (uint32_t pt = 0; pt < 4; pt++) {
           if (pt < npt) {
-            const long bw = *(const long *)(buf + (16 * pt + lane_id() % 16) * kActLds + 32 * ib + g8);
+            const long bw = *(const long *)(buf + (16 * pt + lane_id() % 16) * kActLds + bofs);
             const v4i_t dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) isum[pt][i] += ls[i] * dv[i];
@@ -434,9 +452,9 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
       // Block by block: one MFMA a position tile, the block's term (d_w d_a) dot; the eight terms of the unit as the
       // pairwise tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then added to the row's sum.
       float q[3][4][4];  // the tree's pending partial sums: q[level][pt][row]
-      const uint32_t g8 = 8 * (lane_id() / 16);
 #pragma unroll
       for (uint32_t j = 0; j < 8; j++) {
+        const uint32_t bofs = mfma_code_off(4 * j + lane_id() / 16);  // the lane's 8 codes of block j
         float dw[4];
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) dw[i] = raw.d(i, j);
@@ -444,7 +462,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
         for (uint32_t pt = 0; pt < 4; pt++) {
           if (pt < npt) {
             const uint8_t *unit = buf + (16 * pt + lane_id() % 16) * kActLds;
-            const v4i_t dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(raw.qs[j], *(const long *)(unit + 32 * j + g8),
+            const v4i_t dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(raw.qs[j], *(const long *)(unit + bofs),
                                                                   v4i_t{0, 0, 0, 0}, 0, 0, 0);
             const float as = *(const float *)(unit + kActScales + 4 * j);
 #pragma unroll
@@ -475,10 +493,10 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
 #pragma unroll
       for (uint32_t pt = 0; pt < 4; pt++) {
         if (pt < npt) {
-          ActB b;
-          b.load_presplit(buf + (16 * pt + lane_id() % 16) * kActLds, lane_id(), kActSplitG);
+          ActBP b;
+          b.load(buf + (16 * pt + lane_id() % 16) * kActLds, lane_id());
           float t[4];
-          q4k_terms(a, b, t);
+          q4k_terms_v(a, b.q, b.bh, b.bl, b.ad, t);
 #pragma unroll
           for (int i = 0; i < 4; i++) acc[pt][i] = __fadd_rn(acc[pt][i], t[i]);
         }
@@ -518,6 +536,152 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
         if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = acc[pt][i];
       }
   }
+}
+
+// Gate/up for Q4_K and IQ3_S, both matrices in one wave: wave w takes rows 16 w .. 16 w + 15 of gate AND of up (a
+// work-group 64 rows of each), so every activation operand read from LDS feeds two MFMA chains and SwiGLU pairs
+// gate and up in the same lane (no exchange). A unit's weights are decoded for both matrices, then its raw bytes'
+// registers take the next unit's loads (issued before the MFMAs, waited for after them with the activations).
+// The integers and fp32 steps are pf_gemm16's: UnitQ4_K::term / UnitIQ3_S::term, units added in sequence.
+struct Iq3sA {
+  long a[8];       // the eight blocks' A operands (signed codes)
+  uint32_t sc[4];  // the scale nibbles of the lane's D rows
+  float d[4];
+  __device__ __forceinline__ void decode(const Iq3sRaw &r, uint32_t lane, const uint32_t *grid) {
+#pragma unroll
+    for (uint32_t ib = 0; ib < 8; ib++) a[ib] = r.a_block(ib, lane, grid);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) sc[i] = r.sc[i], d[i] = h2f((uint16_t)r.dh[i]);
+  }
+  // Block ib's odd scale 1 + 2 s of D row 4 g + i.
+  __device__ __forceinline__ int ls(uint32_t i, uint32_t ib) const { return 1 + 2 * (int)((sc[i] >> (4 * ib)) & 15u); }
+};
+
+template <uint32_t kType, uint32_t kLU>
+__global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(2))) pf_gate_up(PfGemm g) {
+  static_assert(kType == QT_Q4_K || kType == QT_IQ3_S, "pf_gate_up: Q4_K and IQ3_S");
+  constexpr uint32_t U = 1u << kLU;
+  __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
+  __shared__ uint32_t arow_lds[64];
+  __shared__ uint64_t tab[32];
+  __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
+  using Raw = std::conditional_t<kType == QT_IQ3_S, Iq3sRaw, Q4kRaw>;
+  using Dec = std::conditional_t<kType == QT_IQ3_S, Iq3sA, Q4kA>;
+  const uint32_t nrb = g.row_blocks;
+  const uint32_t ntl = g.shared_T ? (g.shared_T + MOE_TILE - 1) / MOE_TILE : *g.ntiles, n = ntl * nrb;
+  if (blockIdx.x >= n) return;
+  const uint32_t L = xcd_logical(blockIdx.x, n);
+  if (L >= n) return;
+  const uint32_t tile_i = L / nrb, rb = L % nrb;
+  uint32_t start, count, e;
+  if (g.shared_T) {
+    start = MOE_TILE * tile_i;
+    count = min((uint32_t)MOE_TILE, g.shared_T - start), e = 0;
+  } else {
+    const MoeTile tl = g.tiles[tile_i];
+    start = tl.start, count = tl.count, e = tl.slot;
+  }
+  const uint32_t tid = tid_fresh();
+  if (tid < 32) tab[tid] = kExp2Tab[tid];
+  if constexpr (kType == QT_IQ3_S)
+    for (uint32_t i = tid; i < 512; i += kPfWG) grid_lds[i] = kIq3sGridPf[i];
+  if (tid < 64) {
+    const uint32_t pos = start + tid;
+    arow_lds[tid] = tid < count ? (g.perm ? g.perm[pos] / g.K : pos) : 0xffffffffu;
+  }
+  __syncthreads();
+  const uint32_t row0 = rb * 64 + 16 * (uint32_t)__builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
+  const uint8_t *Mg = g.mat + (uint64_t)e * g.stride, *Mu = Mg + g.up_off;
+  const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
+  uint32_t doff[kDmaPer];
+  dma_plan(arow_lds, U, doff);
+  Raw rg, ru;
+  rg.load(Mg, U, row0, 0, lane);
+  ru.load(Mu, U, row0, 0, lane);
+  pf_act_dma(g.act, doff, 0, &abuf[0][0]);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  float accg[4][4], accu[4][4];
+#pragma unroll
+  for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) accg[pt][i] = accu[pt][i] = 0.0f;
+#pragma unroll 1
+  for (uint32_t u = 0; u < U; u++) {
+    Dec ag, au;
+    if constexpr (kType == QT_IQ3_S) {
+      ag.decode(rg, lane, grid_lds);
+      au.decode(ru, lane, grid_lds);
+    } else {
+      ag.decode(rg, lane);
+      au.decode(ru, lane);
+    }
+    if (u + 1 < U) {  // the raw registers are free: the next unit's weights and activations are loaded meanwhile
+      pf_act_dma(g.act, doff, u + 1, &abuf[(u + 1) & 1][0]);
+      rg.load(Mg, U, row0, u + 1, lane);
+      ru.load(Mu, U, row0, u + 1, lane);
+    }
+    const uint8_t *buf = abuf[u & 1];
+    if constexpr (kType == QT_IQ3_S) {
+      int isg[4][4], isu[4][4];
+#pragma unroll
+      for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) isg[pt][i] = isu[pt][i] = 0;
+#pragma unroll
+      for (uint32_t ib = 0; ib < 8; ib++) {
+        const uint32_t bofs = mfma_code_off(4 * ib + lane / 16);  // the lane's 8 codes of block ib
+        int lg[4], lu[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) lg[i] = ag.ls(i, ib), lu[i] = au.ls(i, ib);
+#pragma unroll
+        for (uint32_t pt = 0; pt < 4; pt++) {
+          if (pt < npt) {
+            const long bw = *(const long *)(buf + (16 * pt + lane % 16) * kActLds + bofs);
+            const v4i_t dg = __builtin_amdgcn_mfma_i32_16x16x32_i8(ag.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+            const v4i_t du = __builtin_amdgcn_mfma_i32_16x16x32_i8(au.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) isg[pt][i] += __mul24(lg[i], dg[i]), isu[pt][i] += __mul24(lu[i], du[i]);
+          }
+        }
+      }
+#pragma unroll
+      for (uint32_t pt = 0; pt < 4; pt++) {
+        if (pt < npt) {
+          const float ad = *(const float *)(buf + (16 * pt + lane % 16) * kActLds + kActScales);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            accg[pt][i] = __fadd_rn(accg[pt][i], __fmul_rn(__fmul_rn(ag.d[i], ad), (float)isg[pt][i]));
+            accu[pt][i] = __fadd_rn(accu[pt][i], __fmul_rn(__fmul_rn(au.d[i], ad), (float)isu[pt][i]));
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (uint32_t pt = 0; pt < 4; pt++) {
+        if (pt < npt) {
+          ActBP b;
+          b.load(buf + (16 * pt + lane % 16) * kActLds, lane);
+          float tg[4], tu[4];
+          q4k_terms_v(ag, b.q, b.bh, b.bl, b.ad, tg);
+          q4k_terms_v(au, b.q, b.bh, b.bl, b.ad, tu);
+#pragma unroll
+          for (int i = 0; i < 4; i++) accg[pt][i] = __fadd_rn(accg[pt][i], tg[i]), accu[pt][i] = __fadd_rn(accu[pt][i], tu[i]);
+        }
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of unit u + 1 have landed
+    __syncthreads();
+  }
+  // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16, gate and up alike.
+  const uint32_t l = lane, r4 = 4 * (l / 16), c16 = l % 16;
+#pragma unroll
+  for (uint32_t pt = 0; pt < 4; pt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t m = 16 * pt + c16;
+      if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = swiglu_one(accg[pt][i], accu[pt][i], g.limit, tab);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -561,10 +725,32 @@ void launch_gemm16_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
   }
 }
 
+template <uint32_t kType>
+void launch_gate_up_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
+  switch (LU) {
+    case 0: pf_gate_up<kType, 0><<<g2, kPfWG, 0, s>>>(q); break;
+    case 1: pf_gate_up<kType, 1><<<g2, kPfWG, 0, s>>>(q); break;
+    case 2: pf_gate_up<kType, 2><<<g2, kPfWG, 0, s>>>(q); break;
+    case 3: pf_gate_up<kType, 3><<<g2, kPfWG, 0, s>>>(q); break;
+    case 4: pf_gate_up<kType, 4><<<g2, kPfWG, 0, s>>>(q); break;
+    default: pf_gate_up<kType, 5><<<g2, kPfWG, 0, s>>>(q); break;
+  }
+}
+
 template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
   uint32_t LU = 0;
   while ((1u << LU) < U) LU++;
+  if (kGU && type != QT_Q8_0) {  // gate and up in one wave: 64 rows of each a work-group
+    PfGemm q = g;
+    q.row_blocks = grid.y;
+    const dim3 g2(grid.x * q.row_blocks);
+    if (type == QT_Q4_K)
+      launch_gate_up_lu<QT_Q4_K>(LU, g2, q, s);
+    else
+      launch_gate_up_lu<QT_IQ3_S>(LU, g2, q, s);
+    return;
+  }
   // The 16 x 16 MFMA kernel: half the rows a work-group, a 1-D XCD-aware grid.
   PfGemm q = g;
   q.row_blocks = grid.y * gemm_rows<kGU>() / (kGU ? 32 : 64);
