@@ -184,96 +184,102 @@ __global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T
     ids[(uint64_t)t * K + lane] = (int32_t)my_id;
     w[(uint64_t)t * K + lane] = wk;
   }
-  if (lane == 0) gs[t] = sigmoid_libm(lg[E], tab);
+  if (lane == 0 && gs) gs[t] = sigmoid_libm(lg[E], tab);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Dispatch: one work-group of 1024. Counts per expert, exclusive scans of the counts and of the tiles, the MoeTile
-// records, then the positions 256 tokens at a time: an expert takes at most one assignment a token, so 64-bit masks
-// of the tokens that chose it order its assignments by token (stable, unlike p_moe_fill's atomic order).
+// Dispatch (p_moe_count / p_moe_scan / p_moe_fill, prompt.cl:682-738): a counting sort of the T k assignments by
+// expert, stable (token order within an expert; the reference's fill takes atomic order). An expert takes at most one
+// assignment a token, so a 64-bit mask per (64-token window, expert) of the tokens that chose it gives both the counts
+// and each assignment's rank inside its window. Three kernels:
+//   pf_masks  one work-group a window: the window's masks (LDS atomics), written out whole;
+//   pf_scan   one work-group: per expert the window offsets (a scan over windows) and the total; the experts' bases
+//             (a scan over experts); the MoeTile records (at most MOE_TILE rows);
+//   pf_fill   one work-group a window: position = start of (window, expert) + the lower bits of the mask; perm and inv.
 
-constexpr uint32_t kDispWG = 1024, kDispWin = 4;  // kDispWin: 64-token masks per position pass
+constexpr uint32_t kDispWG = 512;
 
-constexpr uint32_t kDispCache = 40960;  // ids the dispatch keeps in LDS (T K up to 40960: 2048 tokens at k <= 20)
-
-__global__ void __launch_bounds__(kDispWG) pf_dispatch(const int32_t *ids, uint32_t T, uint32_t K, uint32_t E,
-                                                       uint32_t *perm, uint32_t *inv, MoeTile *tiles,
-                                                       uint32_t *ntiles) {
-  __shared__ uint32_t cnt[512], base[512], tb[512];
-  __shared__ unsigned long long mask[kDispWin][512];
-  __shared__ uint16_t ids_lds[kDispCache];  // the ids, when they fit (the position pass reads them again)
-  const uint32_t tid = threadIdx.x, n = T * K;
-  const bool cached = n <= kDispCache;
-  if (tid < 512) cnt[tid] = 0u;
+__global__ void __launch_bounds__(kDispWG) pf_masks(const int32_t *ids, uint32_t T, uint32_t K, uint32_t E,
+                                                    unsigned long long *masks) {
+  __shared__ unsigned long long m[512];
+  const uint32_t w = blockIdx.x, t0 = 64 * w, tid = threadIdx.x;
+  m[tid] = 0ull;
   __syncthreads();
-  // Eight loads in flight before their counts (one at a time, each load waited for behind the previous atomic).
-  for (uint32_t a0 = tid; a0 < n; a0 += 8 * kDispWG) {
-    uint32_t ev[8];
+  const uint32_t a0 = t0 * K, a1 = min(T, t0 + 64) * K;
+  for (uint32_t a = a0 + tid; a < a1; a += kDispWG) atomicOr(&m[(uint32_t)ids[a]], 1ull << (a / K - t0));
+  __syncthreads();
+  if (tid < E) masks[(uint64_t)w * E + tid] = m[tid];
+}
+
+// An inclusive scan of v over the work-group's 512 threads (wave scans, then the waves' totals).
+__device__ __forceinline__ uint32_t block_scan512(uint32_t v, uint32_t *wsum) {
+  const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
 #pragma unroll
-    for (uint32_t j = 0; j < 8; j++) {
-      const uint32_t a = a0 + j * kDispWG;
-      ev[j] = a < n ? (uint32_t)ids[a] : 0u;
-    }
+  for (uint32_t o = 1; o < 64; o <<= 1) {
+    const uint32_t x = __shfl_up(v, o, 64);
+    if (lane >= o) v += x;
+  }
+  if (lane == 63) wsum[wv] = v;
+  __syncthreads();
+  uint32_t add = 0;
+  for (uint32_t i = 0; i < wv; i++) add += wsum[i];
+  __syncthreads();
+  return v + add;
+}
+
+constexpr uint32_t kScanBatch = 32;  // window masks a thread holds at once (all of them up to 2048 tokens)
+
+__global__ void __launch_bounds__(kDispWG) pf_scan(const unsigned long long *masks, uint32_t nwin, uint32_t E,
+                                                   uint32_t *wstart, MoeTile *tiles, uint32_t *ntiles) {
+  __shared__ uint32_t wsum[kDispWG / 64];
+  const uint32_t e = threadIdx.x;
+  // The counts of the first kScanBatch windows stay in registers for the offsets; the loads are all issued first.
+  uint32_t cw[kScanBatch];
+  {
+    // Unconditional loads (clamped indices, masked after), so that all are in flight before the first is used.
+    unsigned long long mm[kScanBatch];
+    const uint32_t ec = min(e, E - 1);
 #pragma unroll
-    for (uint32_t j = 0; j < 8; j++) {
-      const uint32_t a = a0 + j * kDispWG;
-      if (a < n) {
-        atomicAdd(&cnt[ev[j]], 1u);
-        if (cached) ids_lds[a] = (uint16_t)ev[j];
-      }
-    }
+    for (uint32_t j = 0; j < kScanBatch; j++) mm[j] = masks[(uint64_t)min(j, nwin - 1) * E + ec];
+#pragma unroll
+    for (uint32_t j = 0; j < kScanBatch; j++) cw[j] = e < E && j < nwin ? (uint32_t)__popcll(mm[j]) : 0u;
   }
-  __syncthreads();
-  // Inclusive scans (Hillis-Steele) of the counts and of the tiles per expert.
-  uint32_t c = tid < E ? cnt[tid] : 0u, nt = (c + MOE_TILE - 1) / MOE_TILE;
-  if (tid < 512) base[tid] = c, tb[tid] = nt;
-  __syncthreads();
-  for (uint32_t off = 1; off < 512; off <<= 1) {
-    uint32_t ab = 0, at = 0;
-    if (tid < 512 && tid >= off) ab = base[tid - off], at = tb[tid - off];
-    __syncthreads();
-    if (tid < 512) base[tid] += ab, tb[tid] += at;
-    __syncthreads();
-  }
-  if (tid < E) {
-    const uint32_t b0 = base[tid] - c, t0 = tb[tid] - nt;
+  uint32_t c = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < kScanBatch; j++) c += cw[j];
+  if (e < E)
+    for (uint32_t w = kScanBatch; w < nwin; w++) c += (uint32_t)__popcll(masks[(uint64_t)w * E + e]);
+  const uint32_t nt = (c + MOE_TILE - 1) / MOE_TILE;
+  const uint32_t base = block_scan512(c, wsum) - c, t0 = block_scan512(nt, wsum) - nt;
+  if (e < E) {
     for (uint32_t i = 0; i < nt; i++) {
       MoeTile m;
-      m.expert = tid, m.slot = tid, m.start = b0 + MOE_TILE * i, m.count = min((uint32_t)MOE_TILE, c - MOE_TILE * i);
+      m.expert = e, m.slot = e, m.start = base + MOE_TILE * i, m.count = min((uint32_t)MOE_TILE, c - MOE_TILE * i);
       tiles[t0 + i] = m;
     }
-  }
-  if (tid == 0) *ntiles = tb[511];
-  __syncthreads();
-  if (tid < 512) base[tid] -= (tid < E ? cnt[tid] : 0u);  // exclusive
-  __syncthreads();
-  // kDispWin masks of 64 tokens a pass: an assignment's position is its expert's base, plus the earlier masks'
-  // tokens, plus the lower bits of its own mask.
-  const auto expert_of = [&](uint32_t a) { return cached ? (uint32_t)ids_lds[a] : (uint32_t)ids[a]; };
-  for (uint32_t t0 = 0; t0 < T; t0 += 64 * kDispWin) {
-    for (uint32_t i = tid; i < kDispWin * 512; i += kDispWG) (&mask[0][0])[i] = 0ull;
-    __syncthreads();
-    const uint32_t a0 = t0 * K, a1 = min(n, (t0 + 64 * kDispWin) * K);
-    for (uint32_t a = a0 + tid; a < a1; a += kDispWG) {
-      const uint32_t tok = a / K - t0;
-      atomicOr(&mask[tok / 64][expert_of(a)], 1ull << (tok % 64));
-    }
-    __syncthreads();
-    for (uint32_t a = a0 + tid; a < a1; a += kDispWG) {
-      const uint32_t tok = a / K - t0, e = expert_of(a), w = tok / 64;
-      uint32_t pos = base[e] + (uint32_t)__popcll(mask[w][e] & ((1ull << (tok % 64)) - 1ull));
-      for (uint32_t v = 0; v < w; v++) pos += (uint32_t)__popcll(mask[v][e]);
-      perm[pos] = a;
-      inv[a] = pos;
-    }
-    __syncthreads();
-    if (tid < E) {
-      uint32_t add = 0;
+    uint32_t run = base;
 #pragma unroll
-      for (uint32_t v = 0; v < kDispWin; v++) add += (uint32_t)__popcll(mask[v][tid]);
-      base[tid] += add;
+    for (uint32_t j = 0; j < kScanBatch; j++)
+      if (j < nwin) wstart[(uint64_t)j * E + e] = run, run += cw[j];
+    for (uint32_t w = kScanBatch; w < nwin; w++) {
+      wstart[(uint64_t)w * E + e] = run;
+      run += (uint32_t)__popcll(masks[(uint64_t)w * E + e]);
     }
-    __syncthreads();
+  }
+  if (e == E - 1) *ntiles = t0 + nt;
+}
+
+__global__ void __launch_bounds__(kDispWG) pf_fill(const int32_t *ids, uint32_t T, uint32_t K, uint32_t E,
+                                                   const unsigned long long *masks, const uint32_t *wstart,
+                                                   uint32_t *perm, uint32_t *inv) {
+  const uint32_t w = blockIdx.x, t0 = 64 * w;
+  const uint32_t a0 = t0 * K, a1 = min(T, t0 + 64) * K;
+  for (uint32_t a = a0 + threadIdx.x; a < a1; a += kDispWG) {
+    const uint32_t e = (uint32_t)ids[a], t = a / K - t0;
+    const uint64_t we = (uint64_t)w * E + e;
+    const uint32_t pos = wstart[we] + (uint32_t)__popcll(masks[we] & ((1ull << t) - 1ull));
+    perm[pos] = a;
+    inv[a] = pos;
   }
 }
 
@@ -301,37 +307,40 @@ struct PfGemm {
 template <bool kGU>
 constexpr uint32_t gemm_rows() { return kGU ? 64 : 128; }
 
-// A tile's 64 positions' activation units go into LDS by direct global-to-LDS loads: LDS holds 21 pieces of 16 B a
-// position (kActLds = 336), so load i (of 21) fills pieces 64 i .. 64 i + 63 contiguously, lane l piece 64 i + l, of
+// A work-group's kPos positions' activation units go into LDS by direct global-to-LDS loads: LDS holds 21 pieces of
+// 16 B a position (kActLds = 336), so load i fills pieces 64 i .. 64 i + 63 contiguously, lane l piece 64 i + l, of
 // position (64 i + l) / 21. Pieces 0-19 are the 320-byte global unit verbatim (with the split block sums at kActSplitG
-// for q8_K). The 21 loads are dealt to the four waves (load i to wave i % 4); a wave's global offsets are the same for
-// every unit but for + u kActBytes, so they are worked out once (dma_plan). Piece 20 (padding) and positions without a
+// for q8_K). The loads are dealt to the waves (load i to wave i % kWaves); a wave's global offsets are the same for
+// every unit but for + u kActBytes, so they are worked out once (plan). Piece 20 (padding) and positions without a
 // row load the first unit instead: the bytes land where no operand is read (padding, or MFMA columns never stored),
 // and every lane issues its loads, without branches.
-constexpr uint32_t kDmaLoads = 64 * kActLds / 16 / 64, kDmaPer = (kDmaLoads + 3) / 4;
-static_assert(kActLds == 21 * 16 && kDmaLoads == 21, "activation pieces");
-
-__device__ __forceinline__ void dma_plan(const uint32_t *arow, uint32_t U, uint32_t off[kDmaPer]) {
+template <uint32_t kPos, uint32_t kWaves>
+struct Dma {
+  static constexpr uint32_t kLoads = kPos * kActLds / 16 / 64, kPer = (kLoads + kWaves - 1) / kWaves;
+  static_assert(kActLds == 21 * 16 && kPos * 21 % 64 == 0, "activation pieces");
+  uint32_t off[kPer];
+  // The calling wave's global offsets (unit 0) of its loads, from the positions' rows arow[] (0xffffffff: none).
+  __device__ __forceinline__ void plan(const uint32_t *arow, uint32_t U) {
 #pragma unroll
-  for (uint32_t k = 0; k < kDmaPer; k++) {
-    const uint32_t i = wave_id() + 4 * k, piece = 64 * i + lane_id(), pos = piece / 21, c = piece % 21;
-    const uint32_t ar = i < kDmaLoads ? arow[pos] : 0xffffffffu;
-    off[k] = c < 20 && ar != 0xffffffffu ? ar * U * kActBytes + 16 * c : 0u;
+    for (uint32_t k = 0; k < kPer; k++) {
+      const uint32_t i = wave_id() + kWaves * k, piece = 64 * i + lane_id(), pos = piece / 21, c = piece % 21;
+      const uint32_t ar = i < kLoads ? arow[pos] : 0xffffffffu;
+      off[k] = c < 20 && ar != 0xffffffffu ? ar * U * kActBytes + 16 * c : 0u;
+    }
   }
-}
-
-// Unit u of the planned positions into LDS at buf (the calling wave's share of the 21 loads). The caller waits
-// (s_waitcnt vmcnt(0)) and synchronises before reading.
-__device__ __forceinline__ void pf_act_dma(const uint8_t *act, const uint32_t off[kDmaPer], uint32_t u, uint8_t *buf) {
-  const uint8_t *base = act + (uint64_t)u * kActBytes;
+  // Unit u of the planned positions into LDS at buf (the calling wave's share of the loads). The caller waits
+  // (s_waitcnt vmcnt(0)) and synchronises before reading.
+  __device__ __forceinline__ void load(const uint8_t *act, uint32_t u, uint8_t *buf) const {
+    const uint8_t *base = act + (uint64_t)u * kActBytes;
 #pragma unroll
-  for (uint32_t k = 0; k < kDmaPer; k++) {
-    const uint32_t i = wave_id() + 4 * k;
-    if (i < kDmaLoads)
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(base + off[k]),
-                                       (__attribute__((address_space(3))) void *)(buf + 64 * 16 * i), 16, 0, 0);
+    for (uint32_t k = 0; k < kPer; k++) {
+      const uint32_t i = wave_id() + kWaves * k;
+      if (i < kLoads)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(base + off[k]),
+                                         (__attribute__((address_space(3))) void *)(buf + 64 * 16 * i), 16, 0, 0);
+    }
   }
-}
+};
 
 // Work-group b (< n) of a 1-D grid runs on XCD b % 8 (the dispatcher deals work-groups to the eight XCDs in turn), as
 // the (b / 8)-th of the cnt_x = floor((n - x + 7) / 8) that XCD x receives among the first n. Its logical index puts
@@ -393,11 +402,11 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   const uint32_t row0 = rb * kRows + (kGU ? 16 * (w & 1) : 16 * w);
   const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
   const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
-  uint32_t doff[kDmaPer];
-  dma_plan(arow_lds, U, doff);
+  Dma<64, 4> dma;
+  dma.plan(arow_lds, U);
   Raw raw;
   raw.load(M, U, row0, 0, lane_id());
-  pf_act_dma(g.act, doff, 0, &abuf[0][0]);
+  dma.load(g.act, 0, &abuf[0][0]);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   float acc[4][4];
@@ -409,7 +418,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   for (uint32_t u = 0; u < U; u++) {
     Raw next;
     if (u + 1 < U) {
-      pf_act_dma(g.act, doff, u + 1, &abuf[(u + 1) & 1][0]);
+      dma.load(g.act, u + 1, &abuf[(u + 1) & 1][0]);
       next.load(M, U, row0, u + 1, lane_id());
     }
     const uint8_t *buf = abuf[u & 1];
@@ -557,53 +566,56 @@ struct Iq3sA {
   __device__ __forceinline__ int ls(uint32_t i, uint32_t ib) const { return 1 + 2 * (int)((sc[i] >> (4 * ib)) & 15u); }
 };
 
-template <uint32_t kType, uint32_t kLU>
-__global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(2))) pf_gate_up(PfGemm g) {
+
+// A work-group takes kPos positions of one expert (a MoeTile) and 16 rows a wave of gate and of up (kPos / 16 waves),
+// so that a unit's weights, once decoded, meet kPos / 16 position tiles of 16. (128 positions, eight waves, one
+// work-group a CU by LDS, measured slower at config 4: 269 against 223 us.)
+template <uint32_t kType, uint32_t kLU, uint32_t kPos>
+__global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2))) pf_gate_up(PfGemm g) {
   static_assert(kType == QT_Q4_K || kType == QT_IQ3_S, "pf_gate_up: Q4_K and IQ3_S");
-  constexpr uint32_t U = 1u << kLU;
-  __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
-  __shared__ uint32_t arow_lds[64];
+  constexpr uint32_t U = 1u << kLU, kWaves = kPos / 16, kThreads = 64 * kWaves, kRows = 16 * kWaves, kPt = kPos / 16;
+  __shared__ __align__(16) uint8_t abuf[2][kPos * kActLds];
+  __shared__ uint32_t arow_lds[kPos];
   __shared__ uint64_t tab[32];
   __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
   using Raw = std::conditional_t<kType == QT_IQ3_S, Iq3sRaw, Q4kRaw>;
   using Dec = std::conditional_t<kType == QT_IQ3_S, Iq3sA, Q4kA>;
   const uint32_t nrb = g.row_blocks;
-  const uint32_t ntl = g.shared_T ? (g.shared_T + MOE_TILE - 1) / MOE_TILE : *g.ntiles, n = ntl * nrb;
+  const uint32_t nch = g.shared_T ? (g.shared_T + kPos - 1) / kPos : *g.ntiles, n = nch * nrb;
   if (blockIdx.x >= n) return;
   const uint32_t L = xcd_logical(blockIdx.x, n);
-  if (L >= n) return;
-  const uint32_t tile_i = L / nrb, rb = L % nrb;
+  const uint32_t ch_i = L / nrb, rb = L % nrb;
   uint32_t start, count, e;
   if (g.shared_T) {
-    start = MOE_TILE * tile_i;
-    count = min((uint32_t)MOE_TILE, g.shared_T - start), e = 0;
+    start = kPos * ch_i;
+    count = min(kPos, g.shared_T - start), e = 0;
   } else {
-    const MoeTile tl = g.tiles[tile_i];
+    const MoeTile tl = g.tiles[ch_i];
     start = tl.start, count = tl.count, e = tl.slot;
   }
   const uint32_t tid = tid_fresh();
   if (tid < 32) tab[tid] = kExp2Tab[tid];
   if constexpr (kType == QT_IQ3_S)
-    for (uint32_t i = tid; i < 512; i += kPfWG) grid_lds[i] = kIq3sGridPf[i];
-  if (tid < 64) {
+    for (uint32_t i = tid; i < 512; i += kThreads) grid_lds[i] = kIq3sGridPf[i];
+  if (tid < kPos) {
     const uint32_t pos = start + tid;
     arow_lds[tid] = tid < count ? (g.perm ? g.perm[pos] / g.K : pos) : 0xffffffffu;
   }
   __syncthreads();
-  const uint32_t row0 = rb * 64 + 16 * (uint32_t)__builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
+  const uint32_t row0 = rb * kRows + 16 * (uint32_t)__builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
   const uint8_t *Mg = g.mat + (uint64_t)e * g.stride, *Mu = Mg + g.up_off;
   const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
-  uint32_t doff[kDmaPer];
-  dma_plan(arow_lds, U, doff);
+  Dma<kPos, kWaves> dma;
+  dma.plan(arow_lds, U);
   Raw rg, ru;
   rg.load(Mg, U, row0, 0, lane);
   ru.load(Mu, U, row0, 0, lane);
-  pf_act_dma(g.act, doff, 0, &abuf[0][0]);
+  dma.load(g.act, 0, &abuf[0][0]);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  float accg[4][4], accu[4][4];
+  float accg[kPt][4], accu[kPt][4];
 #pragma unroll
-  for (int pt = 0; pt < 4; pt++)
+  for (int pt = 0; pt < (int)kPt; pt++)
 #pragma unroll
     for (int i = 0; i < 4; i++) accg[pt][i] = accu[pt][i] = 0.0f;
 #pragma unroll 1
@@ -617,15 +629,17 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(2)))
       au.decode(ru, lane);
     }
     if (u + 1 < U) {  // the raw registers are free: the next unit's weights and activations are loaded meanwhile
-      pf_act_dma(g.act, doff, u + 1, &abuf[(u + 1) & 1][0]);
+      dma.load(g.act, u + 1, &abuf[(u + 1) & 1][0]);
       rg.load(Mg, U, row0, u + 1, lane);
       ru.load(Mu, U, row0, u + 1, lane);
     }
     const uint8_t *buf = abuf[u & 1];
     if constexpr (kType == QT_IQ3_S) {
-      int isg[4][4], isu[4][4];
+      // Block by block: the block dots of gate and up for every position tile, each times its row's odd block scale,
+      // added to the unit's integer sums in block order; then d ad isum as UnitIQ3_S::term.
+      int isg[kPt][4], isu[kPt][4];
 #pragma unroll
-      for (int pt = 0; pt < 4; pt++)
+      for (int pt = 0; pt < (int)kPt; pt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) isg[pt][i] = isu[pt][i] = 0;
 #pragma unroll
@@ -635,7 +649,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) lg[i] = ag.ls(i, ib), lu[i] = au.ls(i, ib);
 #pragma unroll
-        for (uint32_t pt = 0; pt < 4; pt++) {
+        for (uint32_t pt = 0; pt < kPt; pt++) {
           if (pt < npt) {
             const long bw = *(const long *)(buf + (16 * pt + lane % 16) * kActLds + bofs);
             const v4i_t dg = __builtin_amdgcn_mfma_i32_16x16x32_i8(ag.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
@@ -646,7 +660,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(2)))
         }
       }
 #pragma unroll
-      for (uint32_t pt = 0; pt < 4; pt++) {
+      for (uint32_t pt = 0; pt < kPt; pt++) {
         if (pt < npt) {
           const float ad = *(const float *)(buf + (16 * pt + lane % 16) * kActLds + kActScales);
 #pragma unroll
@@ -658,7 +672,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(2)))
       }
     } else {
 #pragma unroll
-      for (uint32_t pt = 0; pt < 4; pt++) {
+      for (uint32_t pt = 0; pt < kPt; pt++) {
         if (pt < npt) {
           ActBP b;
           b.load(buf + (16 * pt + lane % 16) * kActLds, lane);
@@ -674,15 +688,18 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(2)))
     __syncthreads();
   }
   // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16, gate and up alike.
-  const uint32_t l = lane, r4 = 4 * (l / 16), c16 = l % 16;
+  const uint32_t r4 = 4 * (lane / 16), c16 = lane % 16;
 #pragma unroll
-  for (uint32_t pt = 0; pt < 4; pt++)
+  for (uint32_t pt = 0; pt < kPt; pt++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const uint32_t m = 16 * pt + c16;
       if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = swiglu_one(accg[pt][i], accu[pt][i], g.limit, tab);
     }
 }
+
+// Positions a gate/up work-group takes for a weight type (the kernel's kPos).
+constexpr uint32_t gu_pos(uint32_t) { return MOE_TILE; }
 
 // ---------------------------------------------------------------------------------------------------------------
 // Combine: y[t][r] = sum_k w[t][k] y_asg[inv[t K + k]][r] in rank order, then + gs[t] y_sh[t][r]; four rows a thread.
@@ -727,13 +744,14 @@ void launch_gemm16_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
 
 template <uint32_t kType>
 void launch_gate_up_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
+  constexpr uint32_t P = gu_pos(kType), W = 4 * P;
   switch (LU) {
-    case 0: pf_gate_up<kType, 0><<<g2, kPfWG, 0, s>>>(q); break;
-    case 1: pf_gate_up<kType, 1><<<g2, kPfWG, 0, s>>>(q); break;
-    case 2: pf_gate_up<kType, 2><<<g2, kPfWG, 0, s>>>(q); break;
-    case 3: pf_gate_up<kType, 3><<<g2, kPfWG, 0, s>>>(q); break;
-    case 4: pf_gate_up<kType, 4><<<g2, kPfWG, 0, s>>>(q); break;
-    default: pf_gate_up<kType, 5><<<g2, kPfWG, 0, s>>>(q); break;
+    case 0: pf_gate_up<kType, 0, P><<<g2, W, 0, s>>>(q); break;
+    case 1: pf_gate_up<kType, 1, P><<<g2, W, 0, s>>>(q); break;
+    case 2: pf_gate_up<kType, 2, P><<<g2, W, 0, s>>>(q); break;
+    case 3: pf_gate_up<kType, 3, P><<<g2, W, 0, s>>>(q); break;
+    case 4: pf_gate_up<kType, 4, P><<<g2, W, 0, s>>>(q); break;
+    default: pf_gate_up<kType, 5, P><<<g2, W, 0, s>>>(q); break;
   }
 }
 
@@ -741,7 +759,7 @@ template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
   uint32_t LU = 0;
   while ((1u << LU) < U) LU++;
-  if (kGU && type != QT_Q8_0) {  // gate and up in one wave: 64 rows of each a work-group
+  if (kGU && type != QT_Q8_0) {  // gate and up in one wave: grid.x chunks (or tiles) x grid.y row blocks of gu_pos rows
     PfGemm q = g;
     q.row_blocks = grid.y;
     const dim3 g2(grid.x * q.row_blocks);
@@ -775,6 +793,15 @@ struct HookScope {
   }
 };
 
+// Gate/up (SwiGLU into h) over nx tiles or chunks (at most; the kernel reads how many there are): Q8_0 on pf_gemm16
+// (64-position tiles, 32 rows of gate and of up a work-group), Q4_K and IQ3_S on pf_gate_up (gu_pos positions and
+// rows of each a work-group).
+void launch_gate_up(uint32_t type, const PfGemm &q, uint32_t T, uint32_t F, uint32_t Ug, uint32_t nx, hipStream_t s) {
+  (void)T;
+  const uint32_t ny = type == QT_Q8_0 ? F / gemm_rows<true>() : F / gu_pos(type);
+  launch_gemm<true>(type, Ug, dim3(nx, ny), q, s);
+}
+
 }  // namespace
 
 hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, const float *x, float *y, hipStream_t st,
@@ -800,7 +827,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
       q.shared_T = T, q.K = K, q.act = b.act_s, q.act_by_pos = 0;
       q.mat = L.shared, q.stride = 0, q.up_off = L.sh_up_off, q.out = b.h_sh, q.out_ld = F;
       q.limit = S.swiglu_limit;
-      launch_gemm<true>(S.sh_gate_type, Ug, dim3(st_tiles, F / gemm_rows<true>()), q, ss);
+      launch_gate_up(S.sh_gate_type, q, T, F, Ug, (T + gu_pos(S.sh_gate_type) - 1) / gu_pos(S.sh_gate_type), ss);
     }
     {
       HookScope k(hook, "pf_quant_h_shared", ss);
@@ -822,11 +849,14 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
   }
   {
     HookScope k(hook, "pf_topk", st);
-    pf_topk<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, T, E, K, b.ids, b.w, b.gs);
+    pf_topk<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, T, E, K, b.ids, b.w, S.has_shared ? b.gs : nullptr);
   }
   {
     HookScope k(hook, "pf_dispatch", st);
-    pf_dispatch<<<1, kDispWG, 0, st>>>(b.ids, T, K, E, b.perm, b.inv, b.tiles, b.ntiles);
+    const uint32_t nwin = pf_windows(T);
+    pf_masks<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, b.masks);
+    pf_scan<<<1, kDispWG, 0, st>>>(b.masks, nwin, E, b.wstart, b.tiles, b.ntiles);
+    pf_fill<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, b.masks, b.wstart, b.perm, b.inv);
   }
   {
     HookScope k(hook, "pf_gate_up", st);
@@ -834,7 +864,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     g.tiles = b.tiles, g.ntiles = b.ntiles, g.perm = b.perm, g.K = K, g.act = b.act_r, g.act_by_pos = 0;
     g.mat = L.experts, g.stride = L.ex_bytes, g.up_off = L.ex_up_off, g.out = b.h, g.out_ld = F;
     g.limit = S.swiglu_limit;
-    launch_gemm<true>(S.gate_type, Ug, dim3(mt, F / gemm_rows<true>()), g, st);
+    launch_gate_up(S.gate_type, g, T, F, Ug, mt, st);
   }
   {
     HookScope k(hook, "pf_quant_h", st);

@@ -6,7 +6,8 @@
 //   pf_quant_rows  x -> the experts' activation units (q8_K or q8_0, the CPU rules)
 //   pf_router      logits = bf16(W) bf16(x) summed in fp64 in k order (each product exact), rounded once, + bias
 //   pf_topk        one wave a token: softmax, top k, weights, shared gate
-//   pf_dispatch    counting sort of the T k assignments by expert (stable: token order within an expert) into
+//   pf_masks, pf_scan, pf_fill
+//                  counting sort of the T k assignments by expert (stable: token order within an expert) into
 //                  MoeTile[] of at most MOE_TILE rows, perm (position -> assignment) and inv (assignment -> position)
 //   gate/up        per tile: gate and up on int8 MFMA, exact int32 block sums, the blocks' integer scales and the
 //                  unit's fp32 term in the oracle's order, SwiGLU. Q4_K and IQ3_S: pf_gemm16 (16 x 16 tiles, 32 rows
@@ -48,6 +49,8 @@ struct PfBufs {
   uint32_t *perm, *inv;    // Tmax K
   MoeTile *tiles;          // Tmax K / MOE_TILE + E
   uint32_t *ntiles;        // 1
+  unsigned long long *masks;  // windows x E: the tokens of each 64-token window that chose each expert
+  uint32_t *wstart;        // windows x E: where each (window, expert)'s assignments start
   float *h, *h_sh;         // Tmax K x F (expert order), Tmax x F
   uint8_t *hact, *hact_sh; // the same rows quantised, (F / 256) units each
   float *y_asg, *y_sh;     // Tmax K x H (expert order), Tmax x H
@@ -64,6 +67,8 @@ struct PfHook {
 };
 
 constexpr uint32_t pf_max_tiles(uint32_t T, uint32_t K, uint32_t E) { return (T * K + MOE_TILE - 1) / MOE_TILE + E; }
+// 64-token windows of the dispatch's masks.
+constexpr uint32_t pf_windows(uint32_t T) { return (T + 63) / 64; }
 
 // Enqueues the block for s.T tokens of x (T x H fp32, rows contiguous, device) into y (the same shape); returns the
 // launches' error state.
