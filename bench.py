@@ -1,15 +1,20 @@
 """Benchmark of the MoE block on one MI355X (BASELINE.json's metric on its configs).
 
 A step is one forward of the block (router, experts, shared expert, combine) over one batch of synthetic tokens,
-inputs resident in HBM. The default workload is BASELINE.json configs[1] (config 2): the speculative-verify batch of
-8 tokens, Q4_K experts, hidden 2048, 512 experts, top-10 + shared, intermediate 512, Zipf(1.1) logit bias.
+inputs resident in HBM. The default run measures both halves of BASELINE's metric and prints them in one JSON line:
+  - decode (the line's value): BASELINE.json configs[1] (config 2), the speculative-verify batch of 8 tokens, Q4_K
+    experts, hidden 2048, 512 experts, top-10 + shared, intermediate 512, Zipf(1.1) logit bias; roofline: HBM GB/s;
+  - prefill (the "prefill" object): config 4, one 2048-token chunk, Q4_K, Zipf(1.1); roofline: the routed gate/up
+    launch's int8 MFMA rate.
+Each has a cpu_baseline: oracle/cpu_fast.c (the oracle's bits, SIMD integer dots, OpenMP) timed on this host's
+physical cores and on one core, the median of 20 or more repetitions.
 
-Cache defeat: the MI355X's 256 MB Infinity Cache would hold one layer's touched weights, so the block is resident
-as several layers (independent routers and biases, so each step routes differently) whose touched bytes sum past
-512 MB, and step i runs layer i mod n_layers.
+Cache defeat (decode): the MI355X's 256 MB Infinity Cache would hold one layer's touched weights, so the block is
+resident as several layers (independent routers and biases, so each step routes differently) whose touched bytes,
+counted from each layer's own routing, sum past 512 MB; step i runs layer i mod n_layers.
 
-Prints one JSON line. --config picks another of BASELINE's configs: decode 1, 2, 3, 3b; prefill 4 (2048 tokens, where
-the roofline object is the dominant kernel's int8 MFMA rate and the block's HBM rate is reported beside it).
+--config picks one of BASELINE's configs alone: decode 1, 2, 3, 3b; prefill 4; the 48-layer stack 5 (decode) and
+5p (prefill, two chunks of 2048).
 """
 import argparse
 import ctypes as C
@@ -135,14 +140,82 @@ def measured_prefill_traffic(config):
         return None
 
 
+def cpu_host():
+    """The host the CPU baseline runs on: its model, its physical cores among the CPUs this process may use, and the
+    thread count used (one a physical core)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    allowed = sorted(os.sched_getaffinity(0))
+    cores = set()
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu", "-p=CPU,CORE,SOCKET"], stdout=subprocess.PIPE, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("#"):
+                continue
+            cpu, core, sock = (int(v) for v in line.split(",")[:3])
+            if cpu in allowed:
+                cores.add((sock, core))
+    except Exception:
+        pass
+    physical = len(cores) if cores else len(allowed)
+    return {"model": model, "physical_cores": physical, "allowed_cpus": len(allowed)}
+
+
+def cpu_median(fn, reps=20, max_s=20.0):
+    """Median seconds of fn over at least `reps` calls (stopping early, with at least 3, past max_s)."""
+    ts = []
+    t_all = time.perf_counter()
+    while len(ts) < reps:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > max_s and len(ts) >= 3:
+            break
+    ts.sort()
+    return ts[len(ts) // 2], len(ts)
+
+
+def cpu_baseline(h, layer, x, unit_per_token, unit, check=None, one_core_tokens=None):
+    """oracle/cpu_fast.c on this host: all physical cores and one core, medians of >= 20 repetitions on the sample x
+    (the first one_core_tokens rows for the one-core figure). unit_per_token converts tokens/s into the metric's
+    second unit (GB/s or TFLOP/s). check: y the GPU gave for x, compared bit for bit."""
+    info = cpu_host()
+    n = max(1, info["physical_cores"])
+    y, _, _ = h.fast_forward(layer, x, nthreads=n)  # warm: the router transpose, page-in
+    same = None if check is None else bool(np.array_equal(y, check))
+    med, reps = cpu_median(lambda: h.fast_forward(layer, x, nthreads=n))
+    x1 = x if one_core_tokens is None else x[:one_core_tokens]
+    med1, reps1 = cpu_median(lambda: h.fast_forward(layer, x1, nthreads=1), max_s=15.0)
+    T, T1 = x.shape[0], x1.shape[0]
+    return {"value": round(T / med, 2), "unit": "tokens/s", "cores": n, "kind": "port",
+            "isa": h.oracle.orc_fast_isa().decode(), "cpu_model": info["model"],
+            "allowed_cpus": info["allowed_cpus"],
+            "second_unit": {unit: round(unit_per_token * T / med, 3)},
+            "one_core": {"value": round(T1 / med1, 2), "unit": "tokens/s", unit: round(unit_per_token * T1 / med1, 3),
+                         "reps": reps1, "tokens": T1},
+            "reps": reps, "equals_gpu_y": same,
+            "sample": "%d tokens a forward, median of %d forwards on %d threads (one a physical core) by "
+                      "oracle/cpu_fast.c: the oracle's arithmetic, bit for bit, with %s integer dot products"
+                      % (T, reps, n, h.oracle.orc_fast_isa().decode())}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="default 2000 (decode), 100 (prefill)")
     ap.add_argument("--warmup", type=int, default=None, help="default 200 (decode), 10 (prefill)")
-    ap.add_argument("--config", default="2", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length")
+    ap.add_argument("--config", default=None, choices=sorted(CONFIGS),
+                    help="one config alone; default: config 2 (decode, the line's value) and config 4 (prefill)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="the 48-layer stack's CPU sample length")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run five 256 MiB device-to-device copies (the reference transfer for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE passes) and exit")
@@ -163,15 +236,27 @@ def main():
     import c0ven_amd as moe
     from tests import harness as h
 
+    if args.config is None:
+        out = decode(args, CONFIGS["2"], "2", moe, h)
+        pf = prefill(args, CONFIGS["4"], "4", moe, h)
+        out["prefill"] = {k: pf[k] for k in ("value", "unit", "ms_per_step", "steps", "warmup", "config", "roofline",
+                                             "block", "parity", "cpu_baseline")}
+        out["prefill"]["metric"] = "MoE block tokens/s and TFLOP/s (prefill, config 4)"
+        print(json.dumps(out), flush=True)
+        return
     cfg = CONFIGS[args.config]
-    gt, dt, sgt, sdt = cfg["types"]
-    T = cfg["T"]
     if "layers" in cfg:
         return stack(args, cfg, moe, h)
-    if T > 16:
-        return prefill(args, cfg, moe, h)
-    args.steps = 2000 if args.steps is None else args.steps
-    args.warmup = 200 if args.warmup is None else args.warmup
+    out = (prefill if cfg["T"] > 16 else decode)(args, cfg, args.config, moe, h)
+    print(json.dumps(out), flush=True)
+
+
+def decode(args, cfg, key, moe, h):
+    """A decode config (T <= 16): one launch of moe_decode a step, layers resident past 512 MB of touched weights."""
+    gt, dt, sgt, sdt = cfg["types"]
+    T = cfg["T"]
+    steps = 2000 if args.steps is None else args.steps
+    warmup = 200 if args.warmup is None else args.warmup
     hip = Hip()
     t_setup = time.time()
     # Layer 0's weights, drawn once; the other layers hold copies of its experts (other addresses, so no cache reuse)
@@ -179,18 +264,20 @@ def main():
     L0 = h.Layer(H, F, E, K, gt, dt, sgt, sdt, seed=2026, layer=0, zipf=cfg["zipf"])
     ex_bytes = 2 * moe.row_bytes(gt, H) * F + moe.row_bytes(dt, F) * H
     sh_bytes = 2 * moe.row_bytes(sgt, H) * F + moe.row_bytes(sdt, F) * H
-    per_layer_touched = (min(E, T * K) * 0.6 + 1) * ex_bytes
-    n_layer = int(min(64, max(8, np.ceil(640e6 / per_layer_touched))))
+    router_bytes = (E + 1) * H * 2
+    x = h.tokens(2026, T, H)
+    # Layers: enough that the touched bytes (each layer's distinct experts from its own routing, its shared expert and
+    # router) pass 512 MB; layer 0's routing (on the CPU) sizes the first estimate.
+    _, ids0, _ = L0.oracle_route(x)
+    est = len(set(ids0.ravel().tolist())) * ex_bytes + sh_bytes + router_bytes
+    n_layer = int(min(64, max(8, np.ceil(600e6 / est))))
     blk = moe.MoeBlock(H, F, E, K, gt, dt, True, sgt, sdt, n_layer=n_layer, max_tokens=16)
     L0.upload(blk, 0)
-    routers = [L0]
     for l in range(1, n_layer):
         Ll = h.Layer(H, F, E, K, gt, dt, sgt, sdt, seed=2026, layer=l, zipf=cfg["zipf"], experts=[],
                      has_shared=False)
         blk.load_router(l, Ll.router, Ll.bias)
         blk.copy_experts(0, l)
-        routers.append(Ll)
-    x = h.tokens(2026, T, H)
     xd, yd, idsd = hip.malloc(x.nbytes), hip.malloc(x.nbytes), hip.malloc(T * K * 4)
     hip.h2d(xd, x)
     # Routing per layer (outside the timed region): distinct experts, for the algorithmic bytes.
@@ -201,22 +288,25 @@ def main():
         hip.sync()
         hip.d2h(ids, idsd)
         distinct.append(len(set(ids.ravel().tolist())))
+    touched_all = sum(d * ex_bytes + sh_bytes + router_bytes for d in distinct)
     setup_s = time.time() - t_setup
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         blk.forward_async(i % n_layer, xd, T, yd)
-    hip.sync()
+    blk.check()  # fails the run on a decode wait that gave up (MOE_TIMEOUT)
+
     def steps_once():
-        for i in range(args.steps):
+        for i in range(steps):
             blk.forward_async(i % n_layer, xd, T, yd)
 
-    t0, t1, ktimes, nf = timed_steps(hip, blk, steps_once, args.steps)
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    tok_s = T * args.steps / (t1 - t0)
+    t0, t1, ktimes, nf = timed_steps(hip, blk, steps_once, steps)
+    blk.check()
+    ms_step = (t1 - t0) * 1e3 / steps
+    tok_s = T * steps / (t1 - t0)
 
-    # Algorithmic bytes: the weights of every expert touched, the shared one, the router, once each.
-    nd = np.array([distinct[i % n_layer] for i in range(args.steps)], dtype=np.float64)
-    router_bytes = (E + 1) * H * 2
+    # Algorithmic bytes (the weights of every expert touched, the shared one, the router, once each), per step from
+    # that step's layer's routing.
+    nd = np.array([distinct[i % n_layer] for i in range(steps)], dtype=np.float64)
     gu_bytes = (nd.mean() * 2 * moe.row_bytes(gt, H) * F + 2 * moe.row_bytes(sgt, H) * F)
     dn_bytes = (nd.mean() * moe.row_bytes(dt, F) * H + moe.row_bytes(sdt, F) * H)
     block_bytes = nd.mean() * ex_bytes + sh_bytes + router_bytes
@@ -224,7 +314,7 @@ def main():
     k_gbs = block_bytes / (k_ms * 1e-3) / 1e9
     block_gbs = block_bytes / (ms_step * 1e-3) / 1e9
 
-    # Parity of this workload (layer 0) against the oracle, and the CPU baseline: the oracle timed on this host.
+    # Parity of this workload (layer 0) against the oracle, and the CPU baseline.
     y = np.empty_like(x)
     blk.forward_async(0, xd, T, yd, idsd)
     hip.sync()
@@ -235,30 +325,18 @@ def main():
                   max_abs=h.max_abs(y, yo), rel_l2=h.rel_l2(y, yo))
     cpu = None
     if not args.no_cpu:
-        cores = min(16, os.cpu_count() or 1)
-        reps, tc0 = 0, time.perf_counter()
-        while True:
-            L0.oracle_forward(x, nthreads=cores)
-            reps += 1
-            if time.perf_counter() - tc0 >= args.cpu_seconds and reps >= 3:
-                break
-        cpu_s = (time.perf_counter() - tc0) / reps
-        cpu = {"value": round(T / cpu_s, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-               "sample": "%d forwards of layer 0 (the same %d tokens) by oracle/oracle.c with %d OpenMP threads, "
-                         "%.1f s" % (reps, T, cores, cpu_s * reps),
-               "gbs": round(block_bytes / 1e9 / cpu_s, 2)}
-
-    dominant = "moe_decode"
+        cpu = cpu_baseline(h, L0, x, block_bytes / T / 1e9, "GB/s", check=y)
     out = {
         "metric": "MoE block tokens/s + achieved HBM GB/s (decode), TFLOP/s (prefill) on 1 GPU",
-        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8", "data": "synthetic",
         "config": {"workload": cfg["name"], "n_embd": H, "n_ff": F, "n_expert": E, "n_used": K, "shared": True,
                    "tokens": T, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]], "resident_layers": n_layer,
-                   "mean_distinct_experts": round(float(nd.mean()), 2)},
-        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config),
+                   "mean_distinct_experts": round(float(nd.mean()), 2),
+                   "touched_bytes_all_layers": int(touched_all)},
+        "roofline": {"bound": "hbm", "kernel": "moe_decode", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(key),
                      "algorithmic_bytes_per_launch": int(block_bytes), "avg_launch_ms": round(k_ms, 5)},
         "block": {"achieved_gbs": round(block_gbs, 1), "frac": round(block_gbs / HBM_PEAK_GBS, 4),
                   "gate_up_bytes": int(gu_bytes), "down_bytes": int(dn_bytes),
@@ -267,8 +345,8 @@ def main():
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),
     }
-    print(json.dumps(out), flush=True)
     blk.close()
+    return out
 
 
 def stack(args, cfg, moe, h):
@@ -327,10 +405,12 @@ def stack(args, cfg, moe, h):
             for c0 in range(0, T, chunk):
                 run(c0, min(chunk, T - c0))
 
+    blk.check()
     if decode:
         t0, t1, ktimes, nf = timed_steps(hip, blk, steps_once, steps * NL)
     else:
         t0, t1, ktimes, nf = timed_steps_per_launch(hip, blk, steps_once)
+    blk.check()
     ms_step = (t1 - t0) * 1e3 / steps
     tok_s = T * steps / (t1 - t0)
     ex_bytes = 2 * moe.row_bytes(gt, H) * F + moe.row_bytes(dt, F) * H
@@ -404,7 +484,7 @@ def stack(args, cfg, moe, h):
     blk.close()
 
 
-def prefill(args, cfg, moe, h):
+def prefill(args, cfg, key, moe, h):
     """Config 4: one forward of 2048 tokens is a step. One resident layer: its 906 MB of experts already exceed the
     Infinity Cache, and every step reads all of them."""
     steps = 100 if args.steps is None else args.steps
@@ -427,16 +507,18 @@ def prefill(args, cfg, moe, h):
     setup_s = time.time() - t_setup
     for _ in range(warmup):
         blk.forward_async(0, xd, T, yd)
-    hip.sync()
+    blk.check()
+
     def steps_once():
         for _ in range(steps):
             blk.forward_async(0, xd, T, yd)
 
     t0, t1, ktimes, nf = timed_steps_per_launch(hip, blk, steps_once)
+    blk.check()
     ms_step = (t1 - t0) * 1e3 / steps
     tok_s = T * steps / (t1 - t0)
-    # Algorithmic work: 2 FLOP per weight per assignment (gate, up, down), the shared expert per token,
-    # the router's (E + 1) rows per token; bytes: every touched expert's weights, the shared one, the router, once.
+    # Algorithmic work: 2 FLOP per weight per assignment (gate, up, down), the shared expert per token, the router's
+    # (E + 1) rows per token; bytes: every touched expert's weights, the shared one, the router, once.
     ex_bytes = 2 * moe.row_bytes(gt, H) * F + moe.row_bytes(dt, F) * H
     sh_bytes = 2 * moe.row_bytes(sgt, H) * F + moe.row_bytes(sdt, F) * H
     gu_flop = 2.0 * (T * K + T) * 2 * F * H
@@ -449,32 +531,25 @@ def prefill(args, cfg, moe, h):
     gu_ms = ktimes.get("pf_gate_up", float("nan"))
     gu_routed_flop = 2.0 * (T * K) * 2 * F * H
     gu_tops = gu_routed_flop / (gu_ms * 1e-3) / 1e12
-    # Parity on a sample of tokens (each token's output depends on that token alone), and the CPU baseline.
+    # Parity on a sample of tokens (each token's output depends on that token alone): ids and w on all tokens, y on
+    # the sample, against the oracle.
     y = np.empty_like(x)
-    blk.forward_async(0, xd, T, yd, idsd)
+    w = np.empty((T, K), np.float32)
+    wd = hip.malloc(T * K * 4)
+    blk.forward_async(0, xd, T, yd, idsd, wd)
     hip.sync()
     hip.d2h(y, yd)
     hip.d2h(ids, idsd)
-    # A first 64-token sample gives the oracle's rate; the baseline then runs on as many tokens as --cpu-seconds
-    # allows (all T when they fit), and parity is checked on those.
-    sample = np.r_[0:32, T - 32:T]
-    tc0 = time.perf_counter()
-    yo, io, _ = L0.oracle_forward(x[sample], nthreads=min(16, os.cpu_count() or 1))
-    cpu_s = time.perf_counter() - tc0
-    n_more = min(T, int(len(sample) * args.cpu_seconds / max(cpu_s, 1e-6)))
-    if not args.no_cpu and n_more > len(sample):
-        sample = np.r_[0:n_more]
-        tc0 = time.perf_counter()
-        yo, io, _ = L0.oracle_forward(x[sample], nthreads=min(16, os.cpu_count() or 1))
-        cpu_s = time.perf_counter() - tc0
-    parity = dict(sample_tokens=len(sample), ids_equal=bool(np.array_equal(ids[sample], io)),
-                  y_bit_exact=bool(np.array_equal(y[sample], yo)), max_abs=h.max_abs(y[sample], yo),
-                  rel_l2=h.rel_l2(y[sample], yo))
-    cores = min(16, os.cpu_count() or 1)
-    cpu = None if args.no_cpu else {
-        "value": round(len(sample) / cpu_s, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-        "sample": "%d of the %d tokens (routing, experts, shared expert, combine) by oracle/oracle.c with %d OpenMP "
-                  "threads, %.1f s" % (len(sample), T, cores, cpu_s)}
+    hip.d2h(w, wd)
+    _, io, wo = L0.oracle_route(x)
+    sample = np.r_[0:64, T // 2:T // 2 + 64, T - 64:T]
+    yo, _, _ = L0.oracle_forward(x[sample], nthreads=min(16, os.cpu_count() or 1))
+    parity = dict(sample_tokens=len(sample), ids_equal_all_tokens=bool(np.array_equal(ids, io)),
+                  w_bit_exact_all_tokens=bool(np.array_equal(w, wo)), y_bit_exact=bool(np.array_equal(y[sample], yo)),
+                  max_abs=h.max_abs(y[sample], yo), rel_l2=h.rel_l2(y[sample], yo))
+    cpu = None
+    if not args.no_cpu:  # a bounded sample: 192 of the chunk's tokens (all cores), 32 (one core)
+        cpu = cpu_baseline(h, L0, x[sample], block_flop / T / 1e12, "TFLOP/s", check=y[sample], one_core_tokens=32)
     out = {
         "metric": "MoE block tokens/s + achieved HBM GB/s (decode), TFLOP/s (prefill) on 1 GPU",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -484,7 +559,7 @@ def prefill(args, cfg, moe, h):
                    "tokens": T, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]], "touched_experts": touched},
         "roofline": {"bound": "mfma", "kernel": "pf_gate_up", "achieved": round(gu_tops, 2), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(gu_tops / INT8_PEAK_TOPS, 4),
-                     "traffic": measured_prefill_traffic(args.config),
+                     "traffic": measured_prefill_traffic(key),
                      "algorithmic_flop_per_launch": gu_routed_flop, "avg_launch_ms": round(gu_ms, 4)},
         "block": {"tflops": round(block_flop / (ms_step * 1e-3) / 1e12, 2),
                   "hbm_gbs": round(block_bytes / (ms_step * 1e-3) / 1e9, 1),
@@ -495,8 +570,8 @@ def prefill(args, cfg, moe, h):
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),
     }
-    print(json.dumps(out), flush=True)
     blk.close()
+    return out
 
 
 if __name__ == "__main__":

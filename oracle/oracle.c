@@ -514,6 +514,12 @@ static void topk_row(const float *lg, uint32_t E, uint32_t k, int32_t *ids, floa
   free(taken);
 }
 
+int orc_topk_logits(const float *logits, uint32_t n_expert, uint32_t k, int32_t *ids, float *w) {
+  if (!n_expert || k == 0 || k > n_expert || k > 64) return -1;
+  topk_row(logits, n_expert, k, ids, w);
+  return 0;
+}
+
 int orc_route(const uint16_t *router, const float *bias, uint32_t n_expert, uint32_t n_embd, uint32_t k,
               const float *x, uint32_t ntok, uint64_t x_stride, float *logits, int32_t *ids, float *w) {
   if (!router || !n_expert || !n_embd || k == 0 || k > n_expert || k > 64) return -1;

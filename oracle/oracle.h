@@ -86,9 +86,19 @@ int orc_compute(const orc_shape *s, const uint8_t *const *gate, const uint8_t *c
 int orc_route(const uint16_t *router, const float *bias, uint32_t n_expert, uint32_t n_embd, uint32_t k,
               const float *x, uint32_t ntok, uint64_t x_stride, float *logits, int32_t *ids, float *w);
 
+/* topk_row on given logits (n_expert values): ids and w (k each), as orc_route does after its logits. */
+int orc_topk_logits(const float *logits, uint32_t n_expert, uint32_t k, int32_t *ids, float *w);
+
 /* The whole block. ids and w (ntok x n_used) may be null. */
 int orc_moe_forward(const orc_layer *L, const float *x, uint32_t ntok, uint64_t x_stride, float *y, uint64_t y_stride,
                     int32_t *ids, float *w, int nthreads);
+
+/* The CPU baseline (cpu_fast.c): the same block, the same bits as orc_moe_forward, with SIMD integer dot products
+ * (AVX-512BW when the CPU has it, else AVX2), the router's rows as SIMD lanes each summed in k order, and
+ * OpenMP over rows. Returns 0 or -1. orc_fast_isa names the instruction set it uses. */
+int orc_fast_moe_forward(const orc_layer *L, const float *x, uint32_t ntok, uint64_t x_stride, float *y,
+                         uint64_t y_stride, int32_t *ids, float *w, int nthreads);
+const char *orc_fast_isa(void);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,8 @@ def _load_oracle():
         "orc_compute": (C.c_int, [_P, _P, _P, _P, _P, C.c_uint32, _P, _P]),
         "orc_route": (C.c_int, [_P, _P, C.c_uint32, C.c_uint32, C.c_uint32, _P, C.c_uint32, C.c_uint64, _P, _P, _P]),
         "orc_moe_forward": (C.c_int, [_P, _P, C.c_uint32, C.c_uint64, _P, C.c_uint64, _P, _P, C.c_int]),
+        "orc_fast_moe_forward": (C.c_int, [_P, _P, C.c_uint32, C.c_uint64, _P, C.c_uint64, _P, _P, C.c_int]),
+        "orc_fast_isa": (C.c_char_p, []),
     }
     for name, (res, args) in sig.items():
         f = getattr(o, name)
@@ -185,6 +187,18 @@ class Layer:
         assert oracle.orc_moe_forward(C.byref(L), ptr(x), T, self.H, ptr(y), self.H, ptr(ids), ptr(w), nthreads) == 0
         return y, ids, w
 
+    def _orc_layer(self):
+        E = self.E
+        zero = np.zeros(1, dtype=np.uint8)
+        gp, up, dp = (_P * E)(), (_P * E)(), (_P * E)()
+        for e in range(E):
+            g, u, d = self.experts.get(e, (zero, zero, zero))
+            gp[e], up[e], dp[e] = g.ctypes.data, u.ctypes.data, d.ctypes.data
+        L = OrcLayer(self.H, self.F, E, self.K, self.gate_type, self.down_type, self.sh_gate_type, self.sh_down_type,
+                     self.swiglu_limit, ptr(self.router), ptr(self.bias), gp, up, dp,
+                     *(ptr(m) for m in (self.shared if self.shared is not None else (None, None, None))))
+        return L, (gp, up, dp)
+
     def oracle_route(self, x):
         x = np.ascontiguousarray(x, dtype=np.float32)
         T = x.shape[0]
@@ -194,6 +208,19 @@ class Layer:
         assert oracle.orc_route(ptr(self.router), ptr(self.bias), self.E, self.H, self.K, ptr(x), T, self.H,
                                 ptr(lg), ptr(ids), ptr(w)) == 0
         return lg, ids, w
+
+
+def fast_forward(layer, x, nthreads=8):
+    """The CPU baseline (oracle/cpu_fast.c): the block with the oracle's bits, SIMD inside. All experts must exist."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    L, keep = layer._orc_layer()
+    y = np.empty((T, layer.H), dtype=np.float32)
+    ids = np.empty((T, layer.K), dtype=np.int32)
+    w = np.empty((T, layer.K), dtype=np.float32)
+    assert oracle.orc_fast_moe_forward(C.byref(L), ptr(x), T, layer.H, ptr(y), layer.H, ptr(ids), ptr(w), nthreads) == 0
+    del keep
+    return y, ids, w
 
 
 def orc_compute_many(gate_type, down_type, H, F, jobs, x, swiglu_limit=0.0, nthreads=8):
