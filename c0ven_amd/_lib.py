@@ -27,7 +27,8 @@ class MoeConfig(C.Structure):
         ("n_embd", C.c_uint32), ("n_ff", C.c_uint32), ("n_expert", C.c_uint32), ("n_used", C.c_uint32),
         ("n_layer", C.c_uint32), ("gate_type", C.c_uint32), ("down_type", C.c_uint32), ("has_shared", C.c_uint32),
         ("sh_gate_type", C.c_uint32), ("sh_down_type", C.c_uint32), ("max_tokens", C.c_uint32),
-        ("swiglu_limit", C.c_float), ("device", C.c_int32), ("reserved", C.c_uint32 * 4),
+        ("swiglu_limit", C.c_float), ("device", C.c_int32), ("borrowed_immutable", C.c_uint32),
+        ("reserved", C.c_uint32 * 3),
     ]
 
 
@@ -37,6 +38,15 @@ class MoeRouteOut(C.Structure):
 
 class MoeJob(C.Structure):
     _fields_ = [("layer", C.c_uint32), ("expert", C.c_uint32), ("tok", C.c_uint32), ("w", C.c_float)]
+
+
+class MoeExpertWeights(C.Structure):
+    _fields_ = [("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p), ("down_parts", C.c_uint32),
+                ("down_blocks", C.c_uint16 * 2)]
+
+
+class MoeCmJob(C.Structure):
+    _fields_ = [("expert", MoeExpertWeights), ("tok", C.c_uint32), ("w", C.c_float)]
 
 
 class MoeAbiRow(C.Structure):
@@ -62,6 +72,7 @@ _SIGS = {
     "moe_forward": (_i32, [_P, _u32, _P, _u32, _u64, _P, _u64, C.POINTER(MoeRouteOut)]),
     "moe_forward_async": (_i32, [_P, _u32, _P, _u32, _P, _P, _P, _P]),
     "moe_forward_async_noalloc": (_i32, [_P, _u32, _P, _u32, _P, _P, _P, _P]),
+    "moe_compute_many": (_i32, [_P, C.POINTER(MoeCmJob), _u32, _u32, _P, _u64, _P, _u64]),
     "moe_forward_experts": (_i32, [_P, C.POINTER(MoeJob), _u32, _u32, _P, _u64, _P, _u64]),
     "moe_h_rows": (_u32, [C.POINTER(MoeConfig)]),
     "moe_prefill_dispatch": (_i32, [_P, C.POINTER(MoeTile), _u32, C.POINTER(_u32), _P]),
@@ -146,12 +157,13 @@ class MoeBlock:
     """One context of the HIP MoE block (moe_open .. moe_close)."""
 
     def __init__(self, n_embd, n_ff, n_expert, n_used, gate_type, down_type, has_shared=True, sh_gate_type=None,
-                 sh_down_type=None, n_layer=1, max_tokens=16, swiglu_limit=0.0, device=0):
+                 sh_down_type=None, n_layer=1, max_tokens=16, swiglu_limit=0.0, device=0, borrowed_immutable=0):
         self.cfg = MoeConfig(n_embd=n_embd, n_ff=n_ff, n_expert=n_expert, n_used=n_used, n_layer=n_layer,
                              gate_type=gate_type, down_type=down_type, has_shared=1 if has_shared else 0,
                              sh_gate_type=sh_gate_type if sh_gate_type is not None else gate_type,
                              sh_down_type=sh_down_type if sh_down_type is not None else down_type,
-                             max_tokens=max_tokens, swiglu_limit=swiglu_limit, device=device)
+                             max_tokens=max_tokens, swiglu_limit=swiglu_limit, device=device,
+                             borrowed_immutable=borrowed_immutable)
         h = _P()
         st = lib.moe_open(C.byref(self.cfg), C.byref(h))
         if st != MOE_OK:
@@ -205,6 +217,21 @@ class MoeBlock:
         arr = (MoeJob * max(1, len(jobs)))(*[MoeJob(*j) for j in jobs])
         y = np.empty((T, H), dtype=np.float32)
         self._check(lib.moe_forward_experts(self.h, arr, len(jobs), T, _ptr(x), H, _ptr(y), H))
+        return y
+
+    def compute_many(self, jobs, x):
+        """jobs: list of ((gate, up, down), tok, w) or ((gate, up, down, down_parts, (b0, b1)), tok, w) with the
+        matrices as uint8 arrays in the file's layout (borrowed for the call)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T, H = x.shape
+        arr = (MoeCmJob * max(1, len(jobs)))()
+        for i, (m, tok, w) in enumerate(jobs):
+            parts, blocks = (m[3], m[4]) if len(m) > 3 else (1, (0, 0))
+            arr[i].expert = MoeExpertWeights(m[0].ctypes.data, m[1].ctypes.data, m[2].ctypes.data, parts,
+                                             (C.c_uint16 * 2)(*blocks))
+            arr[i].tok, arr[i].w = tok, w
+        y = np.empty((T, H), dtype=np.float32)
+        self._check(lib.moe_compute_many(self.h, arr, len(jobs), T, _ptr(x), H, _ptr(y), H))
         return y
 
     def dequantize(self, qtype, blocks, rows, cols):

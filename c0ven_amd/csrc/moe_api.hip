@@ -189,6 +189,12 @@ struct moe_ctx {
   uint32_t *err_flag = nullptr;
   uint64_t *flags = nullptr;
   uint64_t noalloc_bytes = 0;  // the no-alloc path's share of the device's scratch array for this shape
+  // moe_compute_many's device copies of borrowed experts (routed types, ex_bytes each), keyed by gate pointer.
+  uint8_t *bc_base = nullptr;
+  uint32_t bc_slots = 0;
+  std::vector<const uint8_t *> bc_key;
+  std::vector<uint64_t> bc_used;  // the call that last used the slot
+  uint64_t bc_calls = 0;
   uint64_t epoch = 0;          // the last launch's number
   std::vector<std::pair<uint64_t *, uint64_t>> tagged;  // the tagged-record buffers (pointer, records)
   uint32_t grid = 0;           // co-resident work-groups of moe_decode
@@ -446,8 +452,8 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->y_dev = c->alloc<float>((uint64_t)TM * H);
     c->ids_stage = c->alloc<int32_t>((uint64_t)T * K1);
     c->w_stage = c->alloc<float>((uint64_t)T * K1);
-    if (TM > T) {  // the prefill path's scratch
-      const uint32_t K = g.n_used;
+    if (TM > T) {  // the prefill path's scratch (a pre-routed call's token may take n_used + 1 jobs)
+      const uint32_t K = g.n_used + 1;
       const uint64_t A2 = (uint64_t)TM * K;
       PfBufs &b = c->pf;
       b.act_r = c->alloc<uint8_t>((uint64_t)TM * Ug * kActBytes);
@@ -460,10 +466,11 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
       b.gs = c->alloc<float>(TM);
       b.perm = c->alloc<uint32_t>(A2);
       b.inv = c->alloc<uint32_t>(A2);
-      b.tiles = c->alloc<MoeTile>(pf_max_tiles(TM, K, E));
+      // Up to kMaxExperts experts: a layer's, or a pre-routed call's borrowed ones.
+      b.tiles = c->alloc<MoeTile>(pf_max_tiles(TM, K, kMaxExperts));
       b.ntiles = c->alloc<uint32_t>(1);
-      b.masks = c->alloc<unsigned long long>((uint64_t)pf_windows(TM) * E);
-      b.wstart = c->alloc<uint32_t>((uint64_t)pf_windows(TM) * E);
+      b.masks = c->alloc<unsigned long long>((uint64_t)pf_windows(TM) * kMaxExperts);
+      b.wstart = c->alloc<uint32_t>((uint64_t)pf_windows(TM) * kMaxExperts);
       b.h = c->alloc<float>(A2 * F);
       b.hact = c->alloc<uint8_t>(A2 * Ud * kActBytes);
       b.y_asg = c->alloc<float>(A2 * H);
@@ -604,6 +611,197 @@ MOE_API moe_status moe_forward_async(moe_ctx *c, uint32_t layer, const float *x_
   return guarded(c, [&] {
     require(x_dev && y_dev, "null x or y");
     forward_dev(c, layer, x_dev, ntok, y_dev, ids_dev, w_dev, stream ? (hipStream_t)stream : c->stream);
+  });
+}
+
+// The jobs of a pre-routed decode launch: the expert (its index in the weights at p.experts), the token, the weight.
+struct PreJob {
+  uint32_t expert, tok;
+  float w;
+};
+
+// A pre-routed decode launch (ntok <= tdec) of jobs on experts at base (routed types; expert E with a shared expert:
+// the context's shared expert), x and y on the device.
+void decode_prerouted(moe_ctx *c, uint32_t layer, const uint8_t *base, const std::vector<PreJob> &jobs, uint32_t ntok,
+                      hipStream_t s) {
+  const moe_config &g = c->cfg;
+  const uint32_t njobs = (uint32_t)jobs.size(), H = g.n_embd;
+  std::vector<uint32_t> per(ntok, 0);
+  for (const PreJob &j : jobs) per[j.tok]++;
+  uint32_t K = 1;
+  for (uint32_t t = 0; t < ntok; t++) K = std::max(K, per[t]);
+  require(K <= c->k1, "more jobs for one token than n_used + 1");
+  // Ranks in the given order per token; groups of the distinct experts in order of first job, 8 a group.
+  std::vector<int32_t> ids((size_t)ntok * K, -1);
+  std::vector<float> w((size_t)ntok * K, 0.0f);
+  std::vector<uint32_t> asg_of(njobs), fill(ntok, 0);
+  uint32_t emax = 0;
+  for (uint32_t j = 0; j < njobs; j++) {
+    const uint32_t t = jobs[j].tok, r = fill[t]++;
+    ids[(size_t)t * K + r] = (int32_t)jobs[j].expert;
+    w[(size_t)t * K + r] = jobs[j].w;
+    asg_of[j] = t * K + r;
+    emax = std::max(emax, jobs[j].expert);
+  }
+  std::vector<MoeGroup> groups;
+  std::vector<uint32_t> open_group(emax + 1, UINT32_MAX);
+  for (uint32_t j = 0; j < njobs; j++) {
+    const uint32_t e = jobs[j].expert;
+    uint32_t gi = open_group[e];
+    if (gi == UINT32_MAX || groups[gi].n == MOE_GROUP_MAX) {
+      MoeGroup m{};
+      m.slot = (int32_t)e;
+      groups.push_back(m);
+      gi = open_group[e] = (uint32_t)groups.size() - 1;
+    }
+    groups[gi].asg[groups[gi].n++] = asg_of[j];
+  }
+  const uint32_t ng = (uint32_t)groups.size();
+  require(ng <= max_groups(ntok, K), "too many groups");
+  check(hipMemsetAsync(c->y_dev, 0, sizeof(float) * ntok * H, s), "clear y");
+  if (ng) check(hipMemcpyAsync(c->groups, groups.data(), sizeof(MoeGroup) * ng, hipMemcpyHostToDevice, s), "groups");
+  check(hipMemcpyAsync(c->ngroups, &ng, sizeof ng, hipMemcpyHostToDevice, s), "ngroups");
+  check(hipMemcpyAsync(c->ids, ids.data(), sizeof(int32_t) * ids.size(), hipMemcpyHostToDevice, s), "ids");
+  check(hipMemcpyAsync(c->w, w.data(), sizeof(float) * w.size(), hipMemcpyHostToDevice, s), "w");
+  check(hipMemcpyAsync(c->tok_need, per.data(), sizeof(uint32_t) * ntok, hipMemcpyHostToDevice, s), "tok_need");
+  DecodeParams p = base_params(c, layer, ntok);
+  p.K = K, p.route = 0, p.has_shared = 0, p.tok_need = c->tok_need;
+  p.xact_s = g.has_shared ? quant_vec_dot_type(g.sh_gate_type) : p.xact_r;
+  p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
+  if (base != c->layers[layer].experts) {  // borrowed copies: slots 0 .. 511, none of which names the shared expert
+    p.experts = base;
+    p.E = kMaxExperts;
+  }
+  p.x = c->x_dev, p.y = c->y_dev;
+  if (ng) launch(c, p, s);
+  if (c->timing) c->ev_used++;
+  // The host's vectors must outlive the copies above.
+  check(hipStreamSynchronize(s), "pre-routed launch");
+}
+
+// One borrowed expert's three matrices (file layout) repacked into the device layout at dst (ex_bytes).
+void repack_borrowed(const moe_ctx *c, const moe_expert_weights &ew, std::vector<uint8_t> &buf,
+                     std::vector<uint8_t> &joined) {
+  const moe_config &g = c->cfg;
+  const uint32_t H = g.n_embd, F = g.n_ff;
+  const uint64_t gu = c->ex_up;
+  buf.resize(c->ex_bytes);
+  repack_matrix(g.gate_type, ew.gate, F, H, buf.data());
+  repack_matrix(g.gate_type, ew.up, F, H, buf.data() + gu);
+  const uint8_t *down = ew.down;
+  if (ew.down_parts == 2) {
+    // The two regions joined row by row into the file's rows: part 0 of every row, then part 1 of every row.
+    const uint64_t bb = quant_block_bytes(g.down_type), bv = quant_block_values(g.down_type);
+    const uint64_t nb = F / bv;
+    const uint64_t b0 = ew.down_blocks[0] ? ew.down_blocks[0] : nb / 2, b1 = ew.down_blocks[0] ? ew.down_blocks[1] : nb - nb / 2;
+    require(b0 + b1 == nb, "down_blocks do not sum to a row");
+    joined.resize(nb * bb * H);
+    for (uint32_t r = 0; r < H; r++) {
+      std::memcpy(joined.data() + r * nb * bb, ew.down + r * b0 * bb, b0 * bb);
+      std::memcpy(joined.data() + r * nb * bb + b0 * bb, ew.down + H * b0 * bb + r * b1 * bb, b1 * bb);
+    }
+    down = joined.data();
+  }
+  repack_matrix(g.down_type, down, H, F, buf.data() + 2 * gu);
+}
+
+MOE_API moe_status moe_compute_many(moe_ctx *c, const moe_cm_job *jobs, uint32_t njobs, uint32_t ntok, const float *x,
+                                    uint64_t x_stride, float *y, uint64_t y_stride) {
+  return guarded(c, [&] {
+    const moe_config &g = c->cfg;
+    const uint32_t H = g.n_embd, F = g.n_ff;
+    require(x && y && ntok >= 1 && x_stride >= H && y_stride >= H, "bad x, y, ntok or strides");
+    require(ntok <= c->tdec || (ntok <= c->tmax && c->tmax > c->tdec),
+            "ntok must be at most 16, or at most max_tokens when that exceeds 16");
+    require(njobs == 0 || jobs, "null jobs");
+    // The distinct experts by gate pointer (experts.cpp:170-177), in order of first job.
+    std::vector<const uint8_t *> dg;
+    std::vector<uint32_t> dj(njobs);
+    std::vector<uint32_t> per(ntok, 0);
+    for (uint32_t j = 0; j < njobs; j++) {
+      const moe_expert_weights &ew = jobs[j].expert;
+      require(ew.gate && ew.up && ew.down, "null expert matrix");
+      require(jobs[j].tok < ntok, "job token out of range");
+      require(ew.down_parts == 1 || ew.down_parts == 2, "down_parts must be 1 or 2");
+      require(ew.down_parts == 1 || ew.down_blocks[0] || F / 2 == kUnit,
+              "equal down parts are supported when each is one 256-value unit (n_ff 512)");
+      require(++per[jobs[j].tok] <= c->k1, "more jobs for one token than n_used + 1");
+      uint32_t d = 0;
+      while (d < dg.size() && dg[d] != ew.gate) d++;
+      if (d == dg.size()) dg.push_back(ew.gate);
+      dj[j] = d;
+    }
+    const uint32_t nd = (uint32_t)dg.size();
+    require(nd <= kMaxExperts, "more than 512 distinct experts in one call");
+    // Device copies: grow the slots to hold this call's experts (at least 64), then map each expert to a slot.
+    if (nd > c->bc_slots) {
+      check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+      if (c->bc_base) {
+        c->allocs.erase(std::find(c->allocs.begin(), c->allocs.end(), (void *)c->bc_base));
+        c->dev_bytes -= (uint64_t)c->bc_slots * c->ex_bytes;
+        check(hipFree(c->bc_base), "hipFree");
+        c->bc_base = nullptr;
+      }
+      c->bc_slots = std::max<uint32_t>({nd, 64u, c->bc_slots * 2});
+      c->bc_slots = std::min<uint32_t>(c->bc_slots, kMaxExperts);
+      c->bc_base = c->alloc<uint8_t>((uint64_t)c->bc_slots * c->ex_bytes);
+      c->bc_key.assign(c->bc_slots, nullptr);
+      c->bc_used.assign(c->bc_slots, 0);
+    }
+    const uint64_t call = ++c->bc_calls;
+    std::vector<uint32_t> slot(nd, UINT32_MAX);
+    if (g.borrowed_immutable)
+      for (uint32_t d = 0; d < nd; d++)
+        for (uint32_t sl = 0; sl < c->bc_slots; sl++)
+          if (c->bc_key[sl] == dg[d]) slot[d] = sl, c->bc_used[sl] = call;
+    std::vector<uint8_t> buf, joined;
+    for (uint32_t d = 0; d < nd; d++) {
+      if (slot[d] != UINT32_MAX) continue;
+      uint32_t best = 0;  // the least recently used slot this call has not taken
+      for (uint32_t sl = 1; sl < c->bc_slots; sl++)
+        if (c->bc_used[sl] < c->bc_used[best]) best = sl;
+      require(c->bc_used[best] != call, "expert copies exhausted");
+      slot[d] = best, c->bc_used[best] = call, c->bc_key[best] = dg[d];
+      uint32_t j0 = 0;
+      while (dj[j0] != d) j0++;
+      repack_borrowed(c, jobs[j0].expert, buf, joined);
+      check(hipMemcpy(c->bc_base + (uint64_t)best * c->ex_bytes, buf.data(), buf.size(), hipMemcpyHostToDevice),
+            "upload expert");
+    }
+    hipStream_t s = c->stream;
+    check(hipMemcpy2DAsync(c->x_dev, H * sizeof(float), x, x_stride * sizeof(float), H * sizeof(float), ntok,
+                           hipMemcpyHostToDevice, s),
+          "upload x");
+    std::vector<PreJob> pj(njobs);
+    for (uint32_t j = 0; j < njobs; j++) pj[j] = PreJob{slot[dj[j]], jobs[j].tok, jobs[j].w};
+    if (njobs == 0) {
+      check(hipMemsetAsync(c->y_dev, 0, sizeof(float) * ntok * H, s), "clear y");
+    } else if (ntok <= c->tdec) {
+      decode_prerouted(c, 0, c->bc_base, pj, ntok, s);
+    } else {
+      uint32_t K = 1;
+      for (uint32_t t = 0; t < ntok; t++) K = std::max(K, per[t]);
+      std::vector<int32_t> ids((size_t)ntok * K, -1);
+      std::vector<float> w((size_t)ntok * K, 0.0f);
+      std::vector<uint32_t> fill(ntok, 0);
+      for (const PreJob &q : pj) {
+        const uint32_t r = fill[q.tok]++;
+        ids[(size_t)q.tok * K + r] = (int32_t)q.expert, w[(size_t)q.tok * K + r] = q.w;
+      }
+      check(hipMemcpyAsync(c->pf.ids, ids.data(), sizeof(int32_t) * ids.size(), hipMemcpyHostToDevice, s), "ids");
+      check(hipMemcpyAsync(c->pf.w, w.data(), sizeof(float) * w.size(), hipMemcpyHostToDevice, s), "w");
+      PfShape S{H, F, c->bc_slots, K, ntok, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type, 0, g.swiglu_limit};
+      PfLayer PL{nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0};
+      PfHook hook{c->timing ? timing_hook : nullptr, c};
+      check(prefill_jobs(S, PL, c->pf, c->x_dev, c->y_dev, s, hook), "prefill launch");
+      c->last_ids = c->pf.ids, c->last_w = c->pf.w, c->last_pf_T = ntok;
+      check(hipStreamSynchronize(s), "pre-routed prefill");  // the host's ids and w must outlive the copies
+    }
+    check(hipMemcpy2DAsync(y, y_stride * sizeof(float), c->y_dev, H * sizeof(float), H * sizeof(float), ntok,
+                           hipMemcpyDeviceToHost, s),
+          "download y");
+    check(hipStreamSynchronize(s), "compute_many");
+    check_err(c);
   });
 }
 
@@ -863,7 +1061,11 @@ MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap) {
       ROW(moe_config, n_used),       ROW(moe_config, n_layer),      ROW(moe_config, gate_type),
       ROW(moe_config, down_type),    ROW(moe_config, has_shared),   ROW(moe_config, sh_gate_type),
       ROW(moe_config, sh_down_type), ROW(moe_config, max_tokens),   ROW(moe_config, swiglu_limit),
-      ROW(moe_config, device),       ROW(moe_config, reserved),     STRUCT(moe_config),
+      ROW(moe_config, device),       ROW(moe_config, borrowed_immutable), ROW(moe_config, reserved),
+      STRUCT(moe_config),            ROW(moe_expert_weights, gate), ROW(moe_expert_weights, up),
+      ROW(moe_expert_weights, down), ROW(moe_expert_weights, down_parts), ROW(moe_expert_weights, down_blocks),
+      STRUCT(moe_expert_weights),    ROW(moe_cm_job, expert),       ROW(moe_cm_job, tok),
+      ROW(moe_cm_job, w),            STRUCT(moe_cm_job),
       ROW(moe_route_out, ids),       ROW(moe_route_out, w),         STRUCT(moe_route_out),
       ROW(moe_job, layer),           ROW(moe_job, expert),          ROW(moe_job, tok),
       ROW(moe_job, w),               STRUCT(moe_job),               ROW(MoeTile, expert),

@@ -206,7 +206,10 @@ __global__ void __launch_bounds__(kDispWG) pf_masks(const int32_t *ids, uint32_t
   m[tid] = 0ull;
   __syncthreads();
   const uint32_t a0 = t0 * K, a1 = min(T, t0 + 64) * K;
-  for (uint32_t a = a0 + tid; a < a1; a += kDispWG) atomicOr(&m[(uint32_t)ids[a]], 1ull << (a / K - t0));
+  for (uint32_t a = a0 + tid; a < a1; a += kDispWG) {
+    const int32_t id = ids[a];  // < 0: no assignment (a pre-routed call's token with fewer jobs)
+    if (id >= 0) atomicOr(&m[(uint32_t)id], 1ull << (a / K - t0));
+  }
   __syncthreads();
   if (tid < E) masks[(uint64_t)w * E + tid] = m[tid];
 }
@@ -275,6 +278,7 @@ __global__ void __launch_bounds__(kDispWG) pf_fill(const int32_t *ids, uint32_t 
   const uint32_t w = blockIdx.x, t0 = 64 * w;
   const uint32_t a0 = t0 * K, a1 = min(T, t0 + 64) * K;
   for (uint32_t a = a0 + threadIdx.x; a < a1; a += kDispWG) {
+    if (ids[a] < 0) continue;
     const uint32_t e = (uint32_t)ids[a], t = a / K - t0;
     const uint64_t we = (uint64_t)w * E + e;
     const uint32_t pos = wstart[we] + (uint32_t)__popcll(masks[we] & ((1ull << t) - 1ull));
@@ -702,17 +706,19 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2
 constexpr uint32_t gu_pos(uint32_t) { return MOE_TILE; }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Combine: y[t][r] = sum_k w[t][k] y_asg[inv[t K + k]][r] in rank order, then + gs[t] y_sh[t][r]; four rows a thread.
+// Combine: y[t][r] = sum_k w[t][k] y_asg[inv[t K + k]][r] in rank order (ranks with a negative id skipped), then
+// + gs[t] y_sh[t][r]; four rows a thread.
 
-__global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const uint32_t *inv, const float *w,
-                                                    uint32_t K, const float *y_sh, const float *gs, uint32_t T,
-                                                    uint32_t H, float *y) {
+__global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const uint32_t *inv, const int32_t *ids,
+                                                    const float *w, uint32_t K, const float *y_sh, const float *gs,
+                                                    uint32_t T, uint32_t H, float *y) {
   const uint64_t i = (uint64_t)blockIdx.x * kPfWG + threadIdx.x;
   const uint32_t H4 = H / 4;
   if (i >= (uint64_t)T * H4) return;
   const uint32_t t = (uint32_t)(i / H4), r4 = (uint32_t)(i % H4);
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (uint32_t k = 0; k < K; k++) {
+    if (ids[(uint64_t)t * K + k] < 0) continue;  // a pre-routed token's unused rank
     const float wk = w[(uint64_t)t * K + k];
     const float4 v = ((const float4 *)(y_asg + (uint64_t)inv[(uint64_t)t * K + k] * H))[r4];
     acc.x = __fadd_rn(acc.x, __fmul_rn(wk, v.x)), acc.y = __fadd_rn(acc.y, __fmul_rn(wk, v.y));
@@ -802,6 +808,43 @@ void launch_gate_up(uint32_t type, const PfGemm &q, uint32_t T, uint32_t F, uint
   launch_gemm<true>(type, Ug, dim3(nx, ny), q, s);
 }
 
+// The routed experts of a forward whose ids and w (T x K, ids < 0 for no assignment) are in b: dispatch, gate/up,
+// h quantiser, down (y per assignment in b.y_asg).
+hipError_t routed_experts(const PfShape &S, const PfLayer &L, const PfBufs &b, hipStream_t st, const PfHook &hook) {
+  const uint32_t H = S.H, F = S.F, E = S.E, K = S.K, T = S.T, Ug = H / kUnit, Ud = F / kUnit;
+  const uint32_t hr = quant_vec_dot_type(S.down_type);
+  const uint32_t halfwaves = kPfWG / 32;
+  const uint32_t mt = pf_max_tiles(T, K, E);
+  {
+    HookScope k(hook, "pf_dispatch", st);
+    const uint32_t nwin = pf_windows(T);
+    pf_masks<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, b.masks);
+    pf_scan<<<1, kDispWG, 0, st>>>(b.masks, nwin, E, b.wstart, b.tiles, b.ntiles);
+    pf_fill<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, b.masks, b.wstart, b.perm, b.inv);
+  }
+  {
+    HookScope k(hook, "pf_gate_up", st);
+    PfGemm g{};
+    g.tiles = b.tiles, g.ntiles = b.ntiles, g.perm = b.perm, g.K = K, g.act = b.act_r, g.act_by_pos = 0;
+    g.mat = L.experts, g.stride = L.ex_bytes, g.up_off = L.ex_up_off, g.out = b.h, g.out_ld = F;
+    g.limit = S.swiglu_limit;
+    launch_gate_up(S.gate_type, g, T, F, Ug, mt, st);
+  }
+  {
+    HookScope k(hook, "pf_quant_h", st);
+    pf_quant_rows<<<(T * K * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(b.h, F, T * K, Ud, hr, b.hact, 0,
+                                                                              nullptr);
+  }
+  {
+    HookScope k(hook, "pf_down", st);
+    PfGemm g{};
+    g.tiles = b.tiles, g.ntiles = b.ntiles, g.K = K, g.act = b.hact, g.act_by_pos = 1;
+    g.mat = L.experts + L.ex_down_off, g.stride = L.ex_bytes, g.out = b.y_asg, g.out_ld = H;
+    launch_gemm<false>(S.down_type, Ud, dim3(mt, H / gemm_rows<false>()), g, st);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, const float *x, float *y, hipStream_t st,
@@ -851,39 +894,34 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     HookScope k(hook, "pf_topk", st);
     pf_topk<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, T, E, K, b.ids, b.w, S.has_shared ? b.gs : nullptr);
   }
-  {
-    HookScope k(hook, "pf_dispatch", st);
-    const uint32_t nwin = pf_windows(T);
-    pf_masks<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, b.masks);
-    pf_scan<<<1, kDispWG, 0, st>>>(b.masks, nwin, E, b.wstart, b.tiles, b.ntiles);
-    pf_fill<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, b.masks, b.wstart, b.perm, b.inv);
-  }
-  {
-    HookScope k(hook, "pf_gate_up", st);
-    PfGemm g{};
-    g.tiles = b.tiles, g.ntiles = b.ntiles, g.perm = b.perm, g.K = K, g.act = b.act_r, g.act_by_pos = 0;
-    g.mat = L.experts, g.stride = L.ex_bytes, g.up_off = L.ex_up_off, g.out = b.h, g.out_ld = F;
-    g.limit = S.swiglu_limit;
-    launch_gate_up(S.gate_type, g, T, F, Ug, mt, st);
-  }
-  {
-    HookScope k(hook, "pf_quant_h", st);
-    pf_quant_rows<<<(T * K * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(b.h, F, T * K, Ud, hr, b.hact, 0,
-                                                                              nullptr);
-  }
-  {
-    HookScope k(hook, "pf_down", st);
-    PfGemm g{};
-    g.tiles = b.tiles, g.ntiles = b.ntiles, g.K = K, g.act = b.hact, g.act_by_pos = 1;
-    g.mat = L.experts + L.ex_down_off, g.stride = L.ex_bytes, g.out = b.y_asg, g.out_ld = H;
-    launch_gemm<false>(S.down_type, Ud, dim3(mt, H / gemm_rows<false>()), g, st);
-  }
+  const hipError_t e = routed_experts(S, L, b, st, hook);
+  if (e != hipSuccess) return e;
   if (S.has_shared && hipStreamWaitEvent(st, b.join, 0) != hipSuccess) return hipGetLastError();
   {
     HookScope k(hook, "pf_combine", st);
     const uint64_t n = (uint64_t)T * (H / 4);
-    pf_combine<<<(uint32_t)((n + kPfWG - 1) / kPfWG), kPfWG, 0, st>>>(b.y_asg, b.inv, b.w, K,
+    pf_combine<<<(uint32_t)((n + kPfWG - 1) / kPfWG), kPfWG, 0, st>>>(b.y_asg, b.inv, b.ids, b.w, K,
                                                                         S.has_shared ? b.y_sh : nullptr, b.gs, T, H, y);
+  }
+  return hipGetLastError();
+}
+
+hipError_t prefill_jobs(const PfShape &S, const PfLayer &L, const PfBufs &b, const float *x, float *y, hipStream_t st,
+                        const PfHook &hook) {
+  const uint32_t H = S.H, K = S.K, T = S.T, Ug = H / kUnit;
+  const uint32_t halfwaves = kPfWG / 32;
+  {
+    HookScope k(hook, "pf_quant_x", st);
+    pf_quant_rows<<<(T * Ug + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(x, H, T, Ug, quant_vec_dot_type(S.gate_type),
+                                                                            b.act_r, 0, nullptr);
+  }
+  const hipError_t e = routed_experts(S, L, b, st, hook);
+  if (e != hipSuccess) return e;
+  {
+    HookScope k(hook, "pf_combine", st);
+    const uint64_t n = (uint64_t)T * (H / 4);
+    pf_combine<<<(uint32_t)((n + kPfWG - 1) / kPfWG), kPfWG, 0, st>>>(b.y_asg, b.inv, b.ids, b.w, K, nullptr, nullptr,
+                                                                        T, H, y);
   }
   return hipGetLastError();
 }

@@ -74,5 +74,9 @@ constexpr uint32_t pf_windows(uint32_t T) { return (T + 63) / 64; }
 // launches' error state.
 hipError_t prefill_forward(const PfShape &s, const PfLayer &L, const PfBufs &b, const float *x, float *y, hipStream_t st,
                      const PfHook &hook);
+// Pre-routed (CpuExperts::compute_many's jobs): b.ids and b.w already hold s.T x s.K ranks (ids < 0 where a token has
+// fewer jobs; s.K at most the scratch's width); no router, no shared expert. y[t] = the token's jobs in rank order.
+hipError_t prefill_jobs(const PfShape &s, const PfLayer &L, const PfBufs &b, const float *x, float *y, hipStream_t st,
+                        const PfHook &hook);
 
 }  // namespace c0ven

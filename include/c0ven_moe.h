@@ -60,7 +60,10 @@ typedef struct {
   uint32_t max_tokens;   /* the most tokens one forward takes, at most 16384 (default 16) */
   float swiglu_limit;    /* > 0: gate = min(gate, L), up = clamp(up, -L, L) before the SiLU; 0 = off */
   int32_t device;        /* HIP device ordinal */
-  uint32_t reserved[4];
+  uint32_t borrowed_immutable; /* 1: the bytes behind moe_compute_many's expert pointers do not change while the
+                                * context lives, so their device copies are kept (keyed by pointer) across calls;
+                                * 0: they are uploaded again on every call */
+  uint32_t reserved[3];
 } moe_config;
 
 /* The routing result of a forward, per token: k expert ids in rank order and their weights. */
@@ -114,6 +117,32 @@ MOE_API moe_status moe_forward_async(moe_ctx *ctx, uint32_t layer, const float *
  * must be ordered (one stream, or event waits): calls that overlap on one GPU race. Results equal moe_forward_async's. */
 MOE_API moe_status moe_forward_async_noalloc(moe_ctx *ctx, uint32_t layer, const float *x_dev, uint32_t ntok,
                                              float *y_dev, int32_t *ids_dev, float *w_dev, void *stream);
+/* An expert's matrices borrowed from the caller in the file's layout (ExpertWeights, core/cpu/experts.h:14-22): gate
+ * and up n_ff x n_embd, down n_embd x n_ff, of the context's routed types. down_parts 2 stores down as two regions,
+ * the first part of every row's blocks, then the second: with down_blocks {0, 0} the parts are equal and each row is
+ * two dots added in order (supported where a part is one 256-value unit or the types have one term a row part), with
+ * down_blocks set they are the parts' widths in blocks and the row is joined again (the file row's bits). */
+typedef struct {
+  const uint8_t *gate, *up, *down;
+  uint32_t down_parts;
+  uint16_t down_blocks[2];
+} moe_expert_weights;
+
+/* A job (CpuExperts::Job, core/cpu/experts.h:40-45): its expert's borrowed weights, the token and the weight. Jobs with
+ * the same gate pointer are one expert, read once for all their tokens. */
+typedef struct {
+  moe_expert_weights expert;
+  uint32_t tok;
+  float w;
+} moe_cm_job;
+
+/* CpuExperts::compute_many (core/cpu/experts.h:40-49, experts.cpp:152-284) on borrowed weights: y (ntok rows, y_stride
+ * floats apart; host memory) overwritten with, for each token, its jobs in the order given of w * down(silu(gate x) *
+ * (up x)). The distinct experts are repacked and uploaded to the context's device copies (again on every call unless
+ * borrowed_immutable), then ntok <= 16 runs the decode kernel and more the prefill kernels (up to max_tokens, which must
+ * then exceed 16). A token takes at most n_used + 1 jobs. Synchronous. */
+MOE_API moe_status moe_compute_many(moe_ctx *ctx, const moe_cm_job *jobs, uint32_t njobs, uint32_t ntok, const float *x,
+                                    uint64_t x_stride, float *y, uint64_t y_stride);
 /* CpuExperts::compute_many on resident experts: y[tok] = sum over the jobs with that tok, in the order given, of
  * w * expert(x[tok]); no router, no gate. Synchronous, host buffers. */
 MOE_API moe_status moe_forward_experts(moe_ctx *ctx, const moe_job *jobs, uint32_t njobs, uint32_t ntok,

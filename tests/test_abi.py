@@ -39,7 +39,8 @@ def test_exports_match_header():
 def test_struct_layout_matches_ctypes():
     rows = {name: (off, size) for name, off, size in moe.abi_layout()}
     mirrors = {"moe_config": _lib.MoeConfig, "moe_route_out": _lib.MoeRouteOut, "moe_job": _lib.MoeJob,
-               "MoeTile": _lib.MoeTile, "MoeGroup": _lib.MoeGroup, "moe_abi_row": _lib.MoeAbiRow}
+               "MoeTile": _lib.MoeTile, "MoeGroup": _lib.MoeGroup, "moe_abi_row": _lib.MoeAbiRow,
+               "moe_expert_weights": _lib.MoeExpertWeights, "moe_cm_job": _lib.MoeCmJob}
     for sname, cls in mirrors.items():
         assert rows[sname] == (0, C.sizeof(cls)), sname
         for fname, _ in cls._fields_:

@@ -189,3 +189,46 @@ def test_bad_arguments_do_not_crash(tiny_block):
     assert e.value.status == 2
     with pytest.raises(moe.MoeError):
         moe.MoeBlock(500, 256, 8, 2, moe.QT_Q8_0, moe.QT_Q8_0)
+
+
+def _cm_jobs(L, T, K, rng_seed, parts=False):
+    """CpuExperts-style jobs: each token K distinct experts of L in a random order with random weights, plus the shared
+    expert on some tokens; with parts, down given as two regions (equal halves, or 1/3 + 2/3 as down_blocks)."""
+    r = np.random.default_rng(rng_seed)
+    jobs, ojobs = [], []
+    bv, bb = {moe.QT_Q8_0: (32, 34), moe.QT_Q4_K: (256, 144), moe.QT_IQ3_S: (256, 110)}[L.down_type]
+    nb = L.F // bv
+    for t in range(T):
+        es = r.choice(L.E, size=K, replace=False).tolist() + ([L.E] if t % 3 == 0 else [])
+        for e in es:
+            g, u, d = L.experts[e] if e < L.E else L.shared
+            if e == L.E and (L.sh_gate_type, L.sh_down_type) != (L.gate_type, L.down_type):
+                continue
+            w = float(r.uniform(0.05, 1.0))
+            m = (g, u, d)
+            if parts:
+                b0 = nb // 2 if e % 2 == 0 or nb < 3 else nb // 3
+                rows = d.reshape(L.H, nb * bb)
+                d2 = np.ascontiguousarray(np.concatenate([rows[:, :b0 * bb].ravel(), rows[:, b0 * bb:].ravel()]))
+                m = (g, u, d2, 2, (0, 0) if b0 == nb // 2 and nb == 2 else (b0, nb - b0))
+            jobs.append((m, t, w))
+            ojobs.append(((g, u, d), t, w))
+    return jobs, ojobs
+
+
+@pytest.mark.parametrize("T", [1, 8, 64])
+@pytest.mark.parametrize("types", [(moe.QT_Q4_K, moe.QT_Q4_K), (moe.QT_IQ3_S, moe.QT_Q8_0)])
+def test_compute_many_borrowed(T, types):
+    """moe_compute_many on borrowed file-layout weights equals the oracle's compute_many bit for bit: T 1 and 8 run
+    the decode kernel, 64 the prefill kernels; down given in two parts on some experts (down_parts)."""
+    gt, dt = types
+    say("compute_many borrowed", moe.TYPE_NAMES[gt], moe.TYPE_NAMES[dt], "T", T)
+    L = h.Layer(512, 512, 32, 4, gt, dt, seed=90 + T)
+    blk = moe.MoeBlock(512, 512, 32, 4, gt, dt, has_shared=False, max_tokens=64)
+    x = h.tokens(91 + T, T, 512)
+    for parts in (False, True):
+        jobs, ojobs = _cm_jobs(L, T, 4, T + 7, parts)
+        y = blk.compute_many(jobs, x)
+        yo = h.orc_compute_many(gt, dt, 512, 512, ojobs, x)
+        assert np.array_equal(y, yo), (parts, h.max_abs(y, yo))
+    blk.close()
