@@ -31,6 +31,17 @@ namespace c0ven {
 constexpr uint32_t kUnit = 256;     // values per unit
 constexpr uint32_t kTileRows = 64;  // rows per tile
 
+// Units of a K-value row: a partial last unit (K not a multiple of 256; types with 32-value blocks) is stored as a whole
+// one whose missing blocks are zero (zero weights, zero scales).
+C0VEN_HD uint32_t units_of(uint32_t k) { return (k + kUnit - 1) / kUnit; }
+// The lanes the decode kernel's dot4 items give a row: the units rounded up to a power of two (lanes past the real
+// units add exact zeros).
+C0VEN_HD uint32_t unit_lanes(uint32_t U) {
+  uint32_t l = 1;
+  while (l < U) l <<= 1;
+  return l;
+}
+
 C0VEN_HD uint32_t unit_bytes(uint32_t type) {
   return type == QT_Q8_0 ? 272u : type == QT_Q4_K ? 144u : type == QT_IQ3_S ? 110u : 0u;
 }
@@ -49,7 +60,7 @@ constexpr uint32_t kQs = 0, kSigns = 4 * 16, kQh = 6 * 16, kScales = 6 * 16 + 2 
 // Bytes of an R x K matrix in the device layout (R rounded up to whole tiles).
 C0VEN_HD uint64_t matrix_bytes(uint32_t type, uint32_t rows, uint32_t k) {
   const uint64_t rt = (rows + kTileRows - 1) / kTileRows;
-  return rt * tile_bytes(type, k / kUnit);
+  return rt * tile_bytes(type, units_of(k));
 }
 
 // A quantised activation unit (one token's or one assignment's 256 values), 320 B in global memory:

@@ -133,7 +133,7 @@ struct NoAllocLayout {
 
 NoAllocLayout noalloc_layout(const moe_config &g, uint8_t *base) {
   const uint32_t T = std::min<uint32_t>(g.max_tokens, kMaxDecodeTokens), K1 = g.n_used + 1;
-  const uint32_t A = T * K1 + T, Ug = g.n_embd / kUnit, E = g.n_expert;
+  const uint32_t A = T * K1 + T, Ug = units_of(g.n_embd), E = g.n_expert;
   uint64_t off = 0;
   auto take = [&](uint64_t bytes) {
     uint8_t *q = base ? base + off : nullptr;
@@ -251,10 +251,14 @@ moe_status guarded(moe_ctx *c, F f) {
 }
 
 void validate(const moe_config &c) {
-  require(c.n_embd && c.n_embd % 512 == 0 && pow2(c.n_embd / kUnit) && c.n_embd / kUnit <= kMaxUnits,
-          "n_embd must be 512 x a power of two, at most 8192");
-  require(c.n_ff && c.n_ff % kUnit == 0 && pow2(c.n_ff / kUnit) && c.n_ff / kUnit <= kMaxUnits,
-          "n_ff must be 256 x a power of two, at most 8192");
+  require(c.n_embd && c.n_embd % 512 == 0 && c.n_embd / kUnit <= kMaxUnits, "n_embd must be a multiple of 512, at most 8192");
+  require(c.n_ff && c.n_ff % 64 == 0 && units_of(c.n_ff) <= kMaxUnits, "n_ff must be a multiple of 64, at most 8192");
+  const auto down_ok = [&](uint32_t t) { return c.n_ff % quant_block_values(t) == 0; };
+  require(down_ok(c.down_type) && (!c.has_shared || down_ok(c.sh_down_type)),
+          "n_ff must be a whole number of the down type's blocks (256 for Q4_K and IQ3_S)");
+  require(c.n_ff % gate_up_rows(unit_lanes(units_of(c.n_embd))) == 0 &&
+              c.n_embd % down_rows(unit_lanes(units_of(c.n_ff))) == 0,
+          "n_ff and n_embd must be whole numbers of the decode kernel's row blocks");
   require(c.n_expert && c.n_expert <= kMaxExperts, "n_expert must be 1..512");
   require(c.n_used && c.n_used <= kMaxUsed && c.n_used <= c.n_expert, "n_used must be 1..min(16, n_expert)");
   require(quant_gpu_supported(c.gate_type) && quant_gpu_supported(c.down_type), "expert types must be Q8_0, Q4_K or IQ3_S");
@@ -447,7 +451,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     const uint32_t TM = g.max_tokens, T = std::min<uint32_t>(TM, kMaxDecodeTokens), K1 = g.n_used + 1;
     const uint32_t G = max_groups(T, K1), A = T * K1 + T;
     c->tmax = TM, c->tdec = T, c->k1 = K1, c->gmax = G;
-    const uint32_t Ug = H / kUnit, Ud = F / kUnit;
+    const uint32_t Ug = units_of(H), Ud = units_of(F);
     c->x_dev = c->alloc<float>((uint64_t)TM * H);
     c->y_dev = c->alloc<float>((uint64_t)TM * H);
     c->ids_stage = c->alloc<int32_t>((uint64_t)T * K1);
@@ -513,7 +517,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
     c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * act_tok_stride(Ug) +
-                                   std::max<size_t>(Ug == 8 ? kMfmaXchBytes : 0, gate_up_xch_bytes(Ug)),
+                                   std::max<size_t>(Ug == 8 ? kMfmaXchBytes : 0, gate_up_xch_bytes(unit_lanes(Ug))),
                                (size_t)MOE_GROUP_MAX * act_tok_stride(Ud), kGroupingLds});
     int per_cu = 0, ncu = 0;
     uint32_t types = type_bit(g.gate_type) | type_bit(g.down_type);
@@ -979,7 +983,7 @@ MOE_API moe_status moe_trace(moe_ctx *c, uint64_t *stamps, uint32_t cap, uint32_
     uint32_t ng = 0;
     check(hipMemcpy(&ng, c->ngroups, 4, hipMemcpyDeviceToHost), "read ngroups");
     const moe_config &g = c->cfg;
-    const uint32_t T = c->last_T, Ug = g.n_embd / kUnit, Ud = g.n_ff / kUnit;
+    const uint32_t T = c->last_T, Ug = unit_lanes(units_of(g.n_embd)), Ud = unit_lanes(units_of(g.n_ff));
     const uint32_t nL = lead_items(T, g.n_expert, c->last_route), ns = shared_chunks(T, c->last_route, g.has_shared);
     const uint32_t nGU = g.n_ff / gate_up_rows(Ug), nD = g.n_embd / down_rows(Ud);
     const uint32_t b1 = nL + (c->last_route ? T : 0), b2 = b1 + ns * nGU, b3 = b2 + ns * nD, b4 = b3 + ng * nGU;
@@ -1021,7 +1025,8 @@ MOE_API uint64_t moe_device_bytes(const moe_ctx *c) { return c ? c->dev_bytes : 
 MOE_API moe_status moe_dequantize(moe_ctx *c, uint32_t type, const uint8_t *blocks, uint32_t rows, uint32_t cols,
                                   float *out) {
   return guarded(c, [&] {
-    require(quant_gpu_supported(type) && blocks && out && rows && cols && cols % kUnit == 0, "bad dequantize arguments");
+    require(quant_gpu_supported(type) && blocks && out && rows && cols && cols % quant_block_values(type) == 0,
+            "bad dequantize arguments");
     const uint64_t mb = matrix_bytes(type, rows, cols);
     std::vector<uint8_t> buf(mb);
     repack_matrix(type, blocks, rows, cols, buf.data());

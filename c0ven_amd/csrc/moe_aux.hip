@@ -17,18 +17,18 @@ __global__ void __launch_bounds__(64) moe_dequant(const uint8_t *mat, uint32_t t
   __shared__ uint32_t grid[512];
   for (uint32_t i = threadIdx.x; i < 512; i += 64) grid[i] = kGridAux[i];
   __syncthreads();
-  const uint32_t U = k / kUnit, rt = blockIdx.x, lane = threadIdx.x, nl = kTileRows * U;
+  const uint32_t U = units_of(k), rt = blockIdx.x, lane = threadIdx.x, nl = kTileRows * U;
   const uint32_t row = rt * kTileRows + lane;
   const uint8_t *tile = mat + (uint64_t)rt * tile_bytes(type, U);
   const bool live = row < rows;
   for (uint32_t u = 0; u < U; u++) {
-  const uint32_t idx = pair_idx(lane, u);
+  const uint32_t idx = pair_idx(lane, u), nv = min(kUnit, k - u * kUnit);  // nv: the unit's values (partial last)
   float *o = out + (uint64_t)row * k + u * kUnit;
   if (type == QT_Q8_0) {
     UnitQ8_0 w;
     w.load(tile, idx, nl);
     if (live)
-      for (int i = 0; i < 256; i++) o[i] = __fmul_rn(w.d[i / 32], (float)(int8_t)(w.q[i / 4] >> (8 * (i % 4))));
+      for (uint32_t i = 0; i < nv; i++) o[i] = __fmul_rn(w.d[i / 32], (float)(int8_t)(w.q[i / 4] >> (8 * (i % 4))));
   } else if (type == QT_Q4_K) {
     UnitQ4_K w;
     w.load(tile, idx, nl);

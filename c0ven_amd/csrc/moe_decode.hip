@@ -569,6 +569,10 @@ __device__ __forceinline__ void stage_h(const DecodeParams &p, const GroupLds *s
     const uint32_t j = i / U, u = i % U;
     const uint32_t off = (sg->asg[j] * p.F + u * kUnit + 8 * l32) * (uint32_t)sizeof(uint64_t);
     uint64_t r[8];
+    if (u * kUnit + 8 * l32 >= p.F) {  // past the row's end (a partial last unit): zeros
+#pragma unroll
+      for (int k = 0; k < 8; k++) r[k] = 0;
+    } else
     for (uint32_t n = 0;; n++) {
       bool ok = true;
 #pragma unroll
@@ -712,7 +716,8 @@ __device__ __forceinline__ void down_mfma(const DecodeParams &p, const GroupLds 
 template <uint32_t kTypes>
 __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupLds *sg, uint32_t blk, uint8_t *lds,
                                              uint32_t *grid_lds, const uint64_t *tab, uint64_t *mark) {
-  const uint32_t U = p.H / kUnit, rows = gate_up_rows(U), row0 = blk * rows, n = sg->n;
+  // U units a row, UL lanes a row (U rounded up to a power of two; lanes past U add exact zeros).
+  const uint32_t U = units_of(p.H), UL = unit_lanes(U), rows = gate_up_rows(UL), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 0);
   if (use_mfma<kTypes>(gm.type, U, 8, n)) {
     gate_up_mfma(p, sg, gm, blk, lds, (float *)(lds + MOE_GROUP_MAX * act_tok_stride(U)), tab, mark);
@@ -722,13 +727,13 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
     load_grid(grid_lds);
     __syncthreads();
   }
-  const uint32_t lane = lane_id(), m = wave_id() & 1u, r = lane / U, u = lane % U;
-  const uint32_t rl = (wave_id() >> 1) * (64 / U) + r, row = row0 + rl;  // rl: the row within the item
+  const uint32_t lane = lane_id(), m = wave_id() & 1u, r = lane / UL, u = lane % UL, ue = u < U ? u : 0u;
+  const uint32_t rl = (wave_id() >> 1) * (64 / UL) + r, row = row0 + rl;  // rl: the row within the item
   const uint8_t *mat = gm.mat + (m ? (gm.shared ? p.sh_up_off : p.ex_up_off) : 0);
   const uint8_t *tile = mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
   float t[MOE_GROUP_MAX];
-  pair_terms<kTypes>(gm.type, tile, pair_idx(row % kTileRows, u), kTileRows * U, grid_lds,
-             (const uint32_t *)lds + u * (kActLds / 4), act_tok_stride(U) / 4, n, t, [&] {
+  pair_terms<kTypes>(gm.type, tile, pair_idx(row % kTileRows, ue), kTileRows * U, grid_lds,
+             (const uint32_t *)lds + ue * (kActLds / 4), act_tok_stride(U) / 4, n, t, [&] {
                // The shared expert's items run beside the router: x of their tokens is quantised by lead items
                // 8 c .. (their flags); routed groups exist only once every lead item is in.
                if (gm.shared && p.route) wait_flags(p, kFlagLead + sg->tok[0], n);
@@ -740,7 +745,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
 #pragma unroll
   for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
     if (j >= n) break;
-    t[j] = row_sum(t[j], U);  // the row's sum in every lane of the row
+    t[j] = row_sum(u < U ? t[j] : 0.0f, UL);  // the row's sum in every lane of the row
     if (m == 1 && u == 0) xs[rl * MOE_GROUP_MAX + j] = t[j];
   }
   __syncthreads();
@@ -759,21 +764,21 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
 template <uint32_t kTypes>
 __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds *sg, uint32_t blk, uint8_t *lds,
                                           uint32_t *grid_lds, uint64_t *mark) {
-  const uint32_t U = p.F / kUnit, rows = down_rows(U), row0 = blk * rows, n = sg->n;
+  const uint32_t U = units_of(p.F), UL = unit_lanes(U), rows = down_rows(UL), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 2);
-  if (use_mfma<kTypes>(gm.type, U, 2, n)) {
+  if (use_mfma<kTypes>(gm.type, U, 2, n) && p.F == 2 * kUnit) {
     down_mfma(p, sg, gm, blk, lds, mark);
   } else {
     if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
       load_grid(grid_lds);
       __syncthreads();
     }
-    const uint32_t lane = lane_id(), r = lane / U, u = lane % U;
-    const uint32_t row = row0 + wave_id() * (64 / U) + r;
+    const uint32_t lane = lane_id(), r = lane / UL, u = lane % UL, ue = u < U ? u : 0u;
+    const uint32_t row = row0 + wave_id() * (64 / UL) + r;
     const uint8_t *tile = gm.mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
     float t[MOE_GROUP_MAX];
-    pair_terms<kTypes>(gm.type, tile, pair_idx(row % kTileRows, u), kTileRows * U, grid_lds,
-               (const uint32_t *)lds + u * (kActLds / 4), act_tok_stride(U) / 4, n, t, [&] {
+    pair_terms<kTypes>(gm.type, tile, pair_idx(row % kTileRows, ue), kTileRows * U, grid_lds,
+               (const uint32_t *)lds + ue * (kActLds / 4), act_tok_stride(U) / 4, n, t, [&] {
                  stage_h(p, sg, act_type<kTypes>(quant_vec_dot_type(gm.type)), U, lds);
                  __syncthreads();
                  if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
@@ -781,7 +786,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
 #pragma unroll
     for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) {
       if (j >= n) break;
-      const float s = row_sum(t[j], U);
+      const float s = row_sum(u < U ? t[j] : 0.0f, UL);
       if (u == 0) st_tag(p.y_asg + (uint64_t)sg->asg[j] * p.H + row, __float_as_uint(s), p.tag);
     }
     if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
@@ -793,7 +798,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
 // every down item, so what they wait for has a smaller number.
 __device__ __forceinline__ void combine_item(const DecodeParams &p, const GroupTab *tab, uint32_t t, uint32_t blk,
                                              uint64_t *mark) {
-  const uint32_t rows = down_rows(p.F / kUnit), K = p.K, row = blk * rows + tid();
+  const uint32_t rows = down_rows(unit_lanes(units_of(p.F))), K = p.K, row = blk * rows + tid();
   const uint32_t ns = p.has_shared ? 1u : 0u;
   if (p.route) wait_tag(p, p.y_asg + ((uint64_t)t * K + K - 1) * p.H + blk * rows + rows - 1);
   if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
@@ -856,7 +861,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   if (tid() < 32) exp_tab[tid()] = kExp2Tab[tid()];
   if (tid() == 0) gtab.have_w = 0;
   __syncthreads();
-  const uint32_t T = p.T, E = p.E, Ug = p.H / kUnit, Ud = p.F / kUnit;
+  const uint32_t T = p.T, E = p.E, Ug = unit_lanes(units_of(p.H)), Ud = unit_lanes(units_of(p.F));
   const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nL + nTop;
   const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud), nBlk = nD;  // combine items: T x nBlk
   const uint32_t ns = shared_chunks(T, p.route, p.has_shared), B2 = B1 + ns * (nGU + nD);

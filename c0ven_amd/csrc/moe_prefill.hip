@@ -46,8 +46,13 @@ __global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_
   const uint32_t hw = blockIdx.x * (kPfWG / 32) + threadIdx.x / 32, l32 = threadIdx.x & 31u;
   const uint32_t row = hw / U, u = hw % U;
   if (row >= rows) return;  // whole half-waves leave together
-  const float4 *p = (const float4 *)(src + (uint64_t)row * ld + u * kUnit + 8 * l32);
-  const float4 a = p[0], b = p[1];
+  // A row has ld values: past them (a partial last unit) the values are zeros (their q8_0 blocks: d 0, codes 0).
+  const uint32_t v0 = u * kUnit + 8 * l32;
+  float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+  if (v0 < ld) {
+    const float4 *p = (const float4 *)(src + (uint64_t)row * ld + v0);
+    a = p[0], b = p[1];
+  }
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   quant_unit<false, true, true>(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
   if (o2) quant_unit<false, true, true>(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
@@ -303,7 +308,8 @@ struct PfGemm {
   float *out;              // position p's outputs at out + p * out_ld
   uint32_t out_ld;
   float limit;
-  uint32_t row_blocks;     // pf_gemm16: row blocks a tile (its 1-D grid is tiles x row_blocks)
+  uint32_t row_blocks;     // row blocks a tile (the 1-D grid is tiles x row_blocks)
+  uint32_t U;              // 256-value units of K (a partial last one padded with zeros)
 };
 
 // Rows of one grid.y step of the (tiles x row groups) grid the host computes: 64 of gate and of up, or 128 of down.
@@ -362,9 +368,10 @@ __device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
 // 16 w .. of its 64) against the tile's positions in 16-position tiles (only those holding positions run), unit by
 // unit: the same integers and fp32 steps as UnitQ4_K::term / UnitIQ3_S::term / UnitQ8_0::term, units added in
 // sequence; three work-groups share a CU.
-template <uint32_t kType, uint32_t kLU, bool kGU>
+template <uint32_t kType, bool kGU>
 __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3))) pf_gemm16(PfGemm g) {
-  constexpr uint32_t U = 1u << kLU, kRows = kGU ? 32 : 64;
+  const uint32_t U = g.U;
+  constexpr uint32_t kRows = kGU ? 32 : 64;
   // Two activation buffers filled by direct global-to-LDS loads (no registers held), the next unit's issued before
   // the current unit's MFMAs and waited for after them: one barrier a unit, three waves a SIMD.
   __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
@@ -574,10 +581,11 @@ struct Iq3sA {
 // A work-group takes kPos positions of one expert (a MoeTile) and 16 rows a wave of gate and of up (kPos / 16 waves),
 // so that a unit's weights, once decoded, meet kPos / 16 position tiles of 16. (128 positions, eight waves, one
 // work-group a CU by LDS, measured slower at config 4: 269 against 223 us.)
-template <uint32_t kType, uint32_t kLU, uint32_t kPos>
+template <uint32_t kType, uint32_t kPos>
 __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2))) pf_gate_up(PfGemm g) {
   static_assert(kType == QT_Q4_K || kType == QT_IQ3_S, "pf_gate_up: Q4_K and IQ3_S");
-  constexpr uint32_t U = 1u << kLU, kWaves = kPos / 16, kThreads = 64 * kWaves, kRows = 16 * kWaves, kPt = kPos / 16;
+  const uint32_t U = g.U;
+  constexpr uint32_t kWaves = kPos / 16, kThreads = 64 * kWaves, kRows = 16 * kWaves, kPt = kPos / 16;
   __shared__ __align__(16) uint8_t abuf[2][kPos * kActLds];
   __shared__ uint32_t arow_lds[kPos];
   __shared__ uint64_t tab[32];
@@ -736,55 +744,28 @@ __global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const ui
 // ---------------------------------------------------------------------------------------------------------------
 // Host side.
 
-template <uint32_t kType, bool kGU>
-void launch_gemm16_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
-  switch (LU) {
-    case 0: pf_gemm16<kType, 0, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    case 1: pf_gemm16<kType, 1, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    case 2: pf_gemm16<kType, 2, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    case 3: pf_gemm16<kType, 3, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    case 4: pf_gemm16<kType, 4, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-    default: pf_gemm16<kType, 5, kGU><<<g2, kPfWG, 0, s>>>(q); break;
-  }
-}
-
-template <uint32_t kType>
-void launch_gate_up_lu(uint32_t LU, dim3 g2, const PfGemm &q, hipStream_t s) {
-  constexpr uint32_t P = gu_pos(kType), W = 4 * P;
-  switch (LU) {
-    case 0: pf_gate_up<kType, 0, P><<<g2, W, 0, s>>>(q); break;
-    case 1: pf_gate_up<kType, 1, P><<<g2, W, 0, s>>>(q); break;
-    case 2: pf_gate_up<kType, 2, P><<<g2, W, 0, s>>>(q); break;
-    case 3: pf_gate_up<kType, 3, P><<<g2, W, 0, s>>>(q); break;
-    case 4: pf_gate_up<kType, 4, P><<<g2, W, 0, s>>>(q); break;
-    default: pf_gate_up<kType, 5, P><<<g2, W, 0, s>>>(q); break;
-  }
-}
-
 template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
-  uint32_t LU = 0;
-  while ((1u << LU) < U) LU++;
-  if (kGU && type != QT_Q8_0) {  // gate and up in one wave: grid.x chunks (or tiles) x grid.y row blocks of gu_pos rows
-    PfGemm q = g;
+  PfGemm q = g;
+  q.U = U;
+  if (kGU && type != QT_Q8_0) {  // gate and up in one wave: grid.x tiles x grid.y row blocks of gu_pos rows
     q.row_blocks = grid.y;
-    const dim3 g2(grid.x * q.row_blocks);
+    const dim3 g2(grid.x * q.row_blocks), wg(4 * MOE_TILE);
     if (type == QT_Q4_K)
-      launch_gate_up_lu<QT_Q4_K>(LU, g2, q, s);
+      pf_gate_up<QT_Q4_K, MOE_TILE><<<g2, wg, 0, s>>>(q);
     else
-      launch_gate_up_lu<QT_IQ3_S>(LU, g2, q, s);
+      pf_gate_up<QT_IQ3_S, MOE_TILE><<<g2, wg, 0, s>>>(q);
     return;
   }
-  // The 16 x 16 MFMA kernel: half the rows a work-group, a 1-D XCD-aware grid.
-  PfGemm q = g;
+  // The 16 x 16 MFMA kernel: 32 gate + 32 up rows, or 64 down rows, a work-group; a 1-D XCD-aware grid.
   q.row_blocks = grid.y * gemm_rows<kGU>() / (kGU ? 32 : 64);
   const dim3 g2(grid.x * q.row_blocks);
   if (type == QT_Q4_K)
-    launch_gemm16_lu<QT_Q4_K, kGU>(LU, g2, q, s);
+    pf_gemm16<QT_Q4_K, kGU><<<g2, kPfWG, 0, s>>>(q);
   else if (type == QT_IQ3_S)
-    launch_gemm16_lu<QT_IQ3_S, kGU>(LU, g2, q, s);
+    pf_gemm16<QT_IQ3_S, kGU><<<g2, kPfWG, 0, s>>>(q);
   else
-    launch_gemm16_lu<QT_Q8_0, kGU>(LU, g2, q, s);
+    pf_gemm16<QT_Q8_0, kGU><<<g2, kPfWG, 0, s>>>(q);
 }
 
 struct HookScope {
@@ -811,7 +792,7 @@ void launch_gate_up(uint32_t type, const PfGemm &q, uint32_t T, uint32_t F, uint
 // The routed experts of a forward whose ids and w (T x K, ids < 0 for no assignment) are in b: dispatch, gate/up,
 // h quantiser, down (y per assignment in b.y_asg).
 hipError_t routed_experts(const PfShape &S, const PfLayer &L, const PfBufs &b, hipStream_t st, const PfHook &hook) {
-  const uint32_t H = S.H, F = S.F, E = S.E, K = S.K, T = S.T, Ug = H / kUnit, Ud = F / kUnit;
+  const uint32_t H = S.H, F = S.F, E = S.E, K = S.K, T = S.T, Ug = units_of(H), Ud = units_of(F);
   const uint32_t hr = quant_vec_dot_type(S.down_type);
   const uint32_t halfwaves = kPfWG / 32;
   const uint32_t mt = pf_max_tiles(T, K, E);
@@ -849,7 +830,7 @@ hipError_t routed_experts(const PfShape &S, const PfLayer &L, const PfBufs &b, h
 
 hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, const float *x, float *y, hipStream_t st,
                      const PfHook &hook) {
-  const uint32_t H = S.H, F = S.F, E = S.E, K = S.K, T = S.T, Ug = H / kUnit, Ud = F / kUnit;
+  const uint32_t H = S.H, F = S.F, E = S.E, K = S.K, T = S.T, Ug = units_of(H), Ud = units_of(F);
   const uint32_t xr = quant_vec_dot_type(S.gate_type);
   const uint32_t xs = S.has_shared ? quant_vec_dot_type(S.sh_gate_type) : xr;
   const uint32_t hr = quant_vec_dot_type(S.down_type), hs = quant_vec_dot_type(S.sh_down_type);
@@ -908,7 +889,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
 
 hipError_t prefill_jobs(const PfShape &S, const PfLayer &L, const PfBufs &b, const float *x, float *y, hipStream_t st,
                         const PfHook &hook) {
-  const uint32_t H = S.H, K = S.K, T = S.T, Ug = H / kUnit;
+  const uint32_t H = S.H, K = S.K, T = S.T, Ug = units_of(H);
   const uint32_t halfwaves = kPfWG / 32;
   {
     HookScope k(hook, "pf_quant_x", st);

@@ -38,15 +38,26 @@ inline void put_unit(uint8_t *tile, uint32_t type, uint32_t idx, uint32_t nl, co
 }
 
 // rows x k values of type: file layout -> device layout (dst has matrix_bytes(type, rows, k); rows past the last of
-// the final tile are zero, which decodes to zero weights).
+// the final tile are zero, which decodes to zero weights). A partial last unit (k % 256, 32-value block types) takes
+// its blocks and leaves the rest zero.
 inline void repack_matrix(uint32_t type, const uint8_t *src, uint32_t rows, uint32_t k, uint8_t *dst) {
-  const uint32_t U = k / kUnit, nrt = (rows + kTileRows - 1) / kTileRows, nl = kTileRows * U;
+  const uint32_t U = units_of(k), nrt = (rows + kTileRows - 1) / kTileRows, nl = kTileRows * U;
   const uint64_t tb = tile_bytes(type, U);
+  const uint32_t bv = quant_block_values(type), bb = quant_block_bytes(type);
+  std::vector<uint8_t> part(unit_bytes(type));
   std::memset(dst, 0, matrix_bytes(type, rows, k));
   for (uint32_t rt = 0; rt < nrt; rt++) {
     uint8_t *tile = dst + (uint64_t)rt * tb;
     for (uint32_t l = 0; l < kTileRows && rt * kTileRows + l < rows; l++)
-      for (uint32_t u = 0; u < U; u++) put_unit(tile, type, pair_idx(l, u), nl, file_unit(src, type, k, rt * kTileRows + l, u));
+      for (uint32_t u = 0; u < U; u++) {
+        const uint8_t *b = file_unit(src, type, k, rt * kTileRows + l, u);
+        if ((u + 1) * kUnit > k) {  // the partial last unit: its blocks, then zero blocks
+          std::memset(part.data(), 0, part.size());
+          std::memcpy(part.data(), b, (uint64_t)(k - u * kUnit) / bv * bb);
+          b = part.data();
+        }
+        put_unit(tile, type, pair_idx(l, u), nl, b);
+      }
   }
 }
 

@@ -226,7 +226,8 @@ MOE_API moe_status moe_quantize(uint32_t type, const float *x, uint32_t rows, ui
 
 MOE_API moe_status moe_synth_matrix(uint64_t seed, uint64_t stream, float sigma, uint32_t type, uint32_t rows,
                                     uint32_t cols, uint8_t *out, int nthreads) {
-  if (!quant_gpu_supported(type) || cols % 256) return MOE_BAD_ARGUMENT;
+  if (!quant_gpu_supported(type) || cols % quant_block_values(type) || (type != QT_Q8_0 && cols % 256))
+    return MOE_BAD_ARGUMENT;
   const Normal nr(seed, stream);
   const uint64_t rb = moe_row_bytes(type, cols);
   const uint64_t per = std::max<uint64_t>(1, (1u << 16) / cols), nc = (rows + per - 1) / per;

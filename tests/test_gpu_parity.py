@@ -232,3 +232,30 @@ def test_compute_many_borrowed(T, types):
         yo = h.orc_compute_many(gt, dt, 512, 512, ojobs, x)
         assert np.array_equal(y, yo), (parts, h.max_abs(y, yo))
     blk.close()
+
+
+@pytest.mark.parametrize("types", [(moe.QT_Q4_K, moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_Q8_0),
+                                   (moe.QT_IQ3_S, moe.QT_Q8_0, moe.QT_Q8_0, moe.QT_Q8_0)])
+@pytest.mark.parametrize("T", [1, 8, 100])
+def test_model_shape_2560_640(types, T):
+    """The reference model's own expert shape (MODEL_LAYER.md:51, :69): n_embd 2560 (ten 256-value units, not a power of
+    two), n_ff 640 (down's K two and a half units: its last unit half blocks, half zero padding). Decode (T 1, 8) and
+    prefill (T 100) against the oracle, bit for bit."""
+    gt, dt, sgt, sdt = types
+    say("shape 2560 x 640", [moe.TYPE_NAMES[t] for t in types], "T", T)
+    L = h.Layer(2560, 640, 64, 8, gt, dt, sgt, sdt, seed=2560 + T, zipf=1.1)
+    blk = L.block(max_tokens=128)
+    L.upload(blk)
+    x = h.tokens(640 + T, T, 2560)
+    y, ids, w = blk.forward(0, x)
+    check_block(y, ids, w, *L.oracle_forward(x))
+    blk.close()
+
+
+def test_dequantize_partial_unit(tiny_block):
+    """A row of 640 values (two and a half units) of Q8_0 through the device layout: the partial unit's blocks decode
+    as the format says and nothing past the row is written."""
+    m = moe.synth_matrix(5, 2, moe.QT_Q8_0, 70, 640)
+    got = tiny_block.dequantize(moe.QT_Q8_0, m, 70, 640)
+    want = np.stack([h.orc_dequant(moe.QT_Q8_0, m[r * 680:(r + 1) * 680], 640) for r in range(70)])
+    assert np.array_equal(got, want)
