@@ -15,9 +15,10 @@ if not os.path.exists(LIB_PATH):
     raise ImportError("c0ven_amd: %s is not built; run __graft_entry__.build()" % LIB_PATH)
 lib = C.CDLL(LIB_PATH)
 
-QT_Q8_0, QT_Q4_K, QT_Q8_K, QT_IQ3_S = 8, 12, 15, 21
-TYPE_NAMES = {QT_Q8_0: "Q8_0", QT_Q4_K: "Q4_K", QT_IQ3_S: "IQ3_S"}
-BLOCK = {QT_Q8_0: (32, 34), QT_Q4_K: (256, 144), QT_IQ3_S: (256, 110)}
+QT_Q8_0, QT_Q4_K, QT_Q8_K, QT_IQ4_NL, QT_IQ3_S, QT_Q2_0 = 8, 12, 15, 20, 21, 42
+TYPE_NAMES = {QT_Q8_0: "Q8_0", QT_Q4_K: "Q4_K", QT_IQ3_S: "IQ3_S", QT_IQ4_NL: "IQ4_NL", QT_Q2_0: "Q2_0"}
+BLOCK = {QT_Q8_0: (32, 34), QT_Q4_K: (256, 144), QT_IQ3_S: (256, 110), QT_IQ4_NL: (32, 18), QT_Q2_0: (64, 18)}
+Q8_FAMILY = (QT_Q8_0, QT_IQ4_NL, QT_Q2_0)  # the weight types whose dot products take q8_0 activations
 
 MOE_OK, MOE_ERROR, MOE_BAD_ARGUMENT, MOE_BUSY, MOE_TIMEOUT = 0, 1, 2, 3, 4
 

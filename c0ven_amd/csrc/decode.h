@@ -106,9 +106,12 @@ struct DecodeParams {
 };
 
 // The weight types a launch may meet, as a set (bits below): moe_decode is compiled once per set, so a context whose
-// matrices share one type carries no other type's code (and no register pressure from it).
+// matrices share one type carries no other type's code (and no register pressure from it). kTypeQ8_0 stands for the
+// 32-value block types that meet q8_0 activations (Q8_0, IQ4_NL, Q2_0): they differ only in how a unit decodes.
 constexpr uint32_t kTypeQ8_0 = 1, kTypeQ4_K = 2, kTypeIQ3_S = 4;
-constexpr uint32_t type_bit(uint32_t qt) { return qt == QT_Q8_0 ? kTypeQ8_0 : qt == QT_Q4_K ? kTypeQ4_K : kTypeIQ3_S; }
+constexpr uint32_t type_bit(uint32_t qt) {
+  return (qt == QT_Q8_0 || qt == QT_IQ4_NL || qt == QT_Q2_0) ? kTypeQ8_0 : qt == QT_Q4_K ? kTypeQ4_K : kTypeIQ3_S;
+}
 
 // The activation type (q8_0 for Q8_0 weights, q8_K for the others), fixed at compile time where the set allows.
 template <uint32_t kTypes>

@@ -12,6 +12,8 @@
 // (shared/quant.h:1-4, core/load/runs.cpp:12-31) shaped for 64-wide wavefronts.
 //
 //   Q8_0  (8 blocks, 272 B): qs 16 pieces x 16 B (values 16p..16p+15), then d 1 x 16 B (8 f16, block order).
+//   IQ4_NL (8 blocks, 144 B): qs 8 x 16 B (block p's 16 bytes), then d 1 x 16 B (8 f16).
+//   Q2_0  (4 blocks of 64, 72 B): qs 4 x 16 B (block p's 16 bytes), then d 1 x 8 B (4 f16).
 //   Q4_K  (144 B):           qs 8 x 16 B (the block's qs bytes 16p..16p+15), scales 3 x 4 B, then d|dmin 1 x 4 B.
 //   IQ3_S (110 B):           qs 4 x 16 B, signs 2 x 16 B, qh 2 x 4 B, scales 1 x 4 B, then d 1 x 2 B.
 #pragma once
@@ -43,8 +45,15 @@ C0VEN_HD uint32_t unit_lanes(uint32_t U) {
 }
 
 C0VEN_HD uint32_t unit_bytes(uint32_t type) {
-  return type == QT_Q8_0 ? 272u : type == QT_Q4_K ? 144u : type == QT_IQ3_S ? 110u : 0u;
+  return type == QT_Q8_0    ? 272u
+         : type == QT_Q4_K  ? 144u
+         : type == QT_IQ3_S ? 110u
+         : type == QT_IQ4_NL ? 144u
+         : type == QT_Q2_0  ? 72u
+                            : 0u;
 }
+// The 32-value block types that meet q8_0 activations (one fp32 term a 32-value block, or half a Q2_0 block).
+C0VEN_HD constexpr bool q8_family(uint32_t type) { return type == QT_Q8_0 || type == QT_IQ4_NL || type == QT_Q2_0; }
 // The number of pair (row in tile, unit) inside its tile.
 C0VEN_HD uint32_t pair_idx(uint32_t row, uint32_t u) { return u * kTileRows + row; }
 // A tile of 64 rows x U units.
@@ -53,6 +62,8 @@ C0VEN_HD uint64_t tile_bytes(uint32_t type, uint32_t U) { return (uint64_t)kTile
 // Field bases inside a tile, in units of nl = 64 U pairs.
 namespace q8_0t { constexpr uint32_t kQs = 0, kD = 16 * 16; }
 namespace q4_kt { constexpr uint32_t kQs = 0, kScales = 8 * 16, kDm = 8 * 16 + 3 * 4; }
+namespace iq4_nlt { constexpr uint32_t kQs = 0, kD = 8 * 16; }
+namespace q2_0t { constexpr uint32_t kQs = 0, kD = 4 * 16; }
 namespace iq3_st {
 constexpr uint32_t kQs = 0, kSigns = 4 * 16, kQh = 6 * 16, kScales = 6 * 16 + 2 * 4, kD = 6 * 16 + 3 * 4;
 }

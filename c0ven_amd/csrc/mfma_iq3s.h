@@ -55,7 +55,7 @@ struct Iq3sRaw {
       const uint32_t gv = grid[byte | (hb << 8)];
       const uint32_t nib = (sg[ib] >> (4 * (2 * g + j))) & 15u;
       const uint32_t x = (nib * 0x00204081u) & 0x01010101u;  // byte t = bit t of the nibble
-      w[j] = (gv ^ (x * 0xffu)) + x;                         // grid bytes >= 1: negation has no carries
+      w[j] = (gv ^ ((x << 8) - x)) + x;                      // grid bytes >= 1: negation has no carries
     }
     return (long)(((uint64_t)w[1] << 32) | w[0]);
   }

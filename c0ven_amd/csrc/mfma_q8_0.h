@@ -8,6 +8,7 @@
 
 #include "device_math.h"
 #include "layout.h"
+#include "units.h"
 
 namespace c0ven {
 
@@ -34,6 +35,57 @@ struct Q80Raw {
   __device__ __forceinline__ float d(uint32_t i, uint32_t j) const {
     const uint32_t w[4] = {dv[i].x, dv[i].y, dv[i].z, dv[i].w};
     return h2f((uint16_t)(w[j / 2] >> (16 * (j % 2))));
+  }
+};
+
+// The same operands for IQ4_NL (the lane's eight codes of block j looked up in kvalues_iq4nl) and Q2_0 (half j of block
+// j / 2 as codes q - 1, its scale the block's): the Q8_0 kernel's steps then apply unchanged.
+struct Iq4nlRaw {
+  long qs[8];
+  uint4 dv[4];
+  __device__ __forceinline__ void load(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
+    const uint32_t g = lane / 16, nl = kTileRows * U;
+    const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_IQ4_NL, U);
+    const uint32_t ia = pair_idx((row0 % kTileRows) + lane % 16, u);
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) {  // values 8 g .. 8 g + 7: nibbles (g / 2 high) of bytes 8 (g % 2) .. + 7
+      const uint2 b = *(const uint2 *)(tile + ((uint64_t)(iq4_nlt::kQs / 16 + j) * nl + ia) * 16 + 8 * (g % 2));
+      const uint32_t sh = 4 * (g / 2);
+      qs[j] = (long)(((uint64_t)iq4nl_lookup((b.y >> sh) & 0x0f0f0f0fu) << 32) | iq4nl_lookup((b.x >> sh) & 0x0f0f0f0fu));
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      const uint32_t id = pair_idx((row0 % kTileRows) + 4 * g + i, u);
+      dv[i] = *(const uint4 *)(tile + (uint64_t)iq4_nlt::kD * nl + (uint64_t)id * 16);
+    }
+  }
+  __device__ __forceinline__ float d(uint32_t i, uint32_t j) const {
+    const uint32_t w[4] = {dv[i].x, dv[i].y, dv[i].z, dv[i].w};
+    return h2f((uint16_t)(w[j / 2] >> (16 * (j % 2))));
+  }
+};
+
+struct Q20Raw {
+  long qs[8];
+  uint2 dv[4];
+  __device__ __forceinline__ void load(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
+    const uint32_t g = lane / 16, nl = kTileRows * U;
+    const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q2_0, U);
+    const uint32_t ia = pair_idx((row0 % kTileRows) + lane % 16, u);
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) {  // half j: values 8 g .. 8 g + 7 are bytes 8 (j % 2) + 2 g, + 1 of block j / 2
+      const uint32_t b = *(const uint16_t *)(tile + ((uint64_t)(q2_0t::kQs / 16 + j / 2) * nl + ia) * 16 + 8 * (j % 2) + 2 * g);
+      qs[j] = (long)(((uint64_t)q2_spread(b >> 8) << 32) | q2_spread(b & 0xffu));
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      const uint32_t id = pair_idx((row0 % kTileRows) + 4 * g + i, u);
+      dv[i] = *(const uint2 *)(tile + (uint64_t)q2_0t::kD * nl + (uint64_t)id * 8);
+    }
+  }
+  __device__ __forceinline__ float d(uint32_t i, uint32_t j) const {
+    const uint32_t w = (j / 4) ? dv[i].y : dv[i].x;
+    return h2f((uint16_t)(w >> (16 * ((j / 2) % 2))));
   }
 };
 

@@ -255,15 +255,15 @@ void validate(const moe_config &c) {
   require(c.n_ff && c.n_ff % 64 == 0 && units_of(c.n_ff) <= kMaxUnits, "n_ff must be a multiple of 64, at most 8192");
   const auto down_ok = [&](uint32_t t) { return c.n_ff % quant_block_values(t) == 0; };
   require(down_ok(c.down_type) && (!c.has_shared || down_ok(c.sh_down_type)),
-          "n_ff must be a whole number of the down type's blocks (256 for Q4_K and IQ3_S)");
+          "n_ff must be a whole number of the down type's blocks (64 for Q2_0, 256 for Q4_K and IQ3_S)");
   require(c.n_ff % gate_up_rows(unit_lanes(units_of(c.n_embd))) == 0 &&
               c.n_embd % down_rows(unit_lanes(units_of(c.n_ff))) == 0,
           "n_ff and n_embd must be whole numbers of the decode kernel's row blocks");
   require(c.n_expert && c.n_expert <= kMaxExperts, "n_expert must be 1..512");
   require(c.n_used && c.n_used <= kMaxUsed && c.n_used <= c.n_expert, "n_used must be 1..min(16, n_expert)");
-  require(quant_gpu_supported(c.gate_type) && quant_gpu_supported(c.down_type), "expert types must be Q8_0, Q4_K or IQ3_S");
+  require(quant_gpu_supported(c.gate_type) && quant_gpu_supported(c.down_type), "expert types must be Q8_0, Q4_K, IQ3_S, IQ4_NL or Q2_0");
   require(!c.has_shared || (quant_gpu_supported(c.sh_gate_type) && quant_gpu_supported(c.sh_down_type)),
-          "shared expert types must be Q8_0, Q4_K or IQ3_S");
+          "shared expert types must be Q8_0, Q4_K, IQ3_S, IQ4_NL or Q2_0");
   require(c.max_tokens <= kMaxPrefillTokens, "max_tokens must be at most 16384");
   require(c.swiglu_limit >= 0.0f, "swiglu_limit must be >= 0");
 }

@@ -24,9 +24,14 @@ __global__ void __launch_bounds__(64) moe_dequant(const uint8_t *mat, uint32_t t
   for (uint32_t u = 0; u < U; u++) {
   const uint32_t idx = pair_idx(lane, u), nv = min(kUnit, k - u * kUnit);  // nv: the unit's values (partial last)
   float *o = out + (uint64_t)row * k + u * kUnit;
-  if (type == QT_Q8_0) {
+  if (q8_family(type)) {  // a code and its 32-value block's scale: d q, d kvalues[nibble], d (q - 1)
     UnitQ8_0 w;
-    w.load(tile, idx, nl);
+    if (type == QT_IQ4_NL)
+      static_cast<UnitIQ4_NL &>(w).load(tile, idx, nl);
+    else if (type == QT_Q2_0)
+      static_cast<UnitQ2_0 &>(w).load(tile, idx, nl);
+    else
+      w.load(tile, idx, nl);
     if (live)
       for (uint32_t i = 0; i < nv; i++) o[i] = __fmul_rn(w.d[i / 32], (float)(int8_t)(w.q[i / 4] >> (8 * (i % 4))));
   } else if (type == QT_Q4_K) {

@@ -230,9 +230,14 @@ __device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, u
                                            const uint32_t *grid_lds, const uint32_t *act, uint32_t stride,
                                            const uint32_t &n, float *t, Ready ready) {
   if constexpr ((kTypes & kTypeQ8_0) != 0) {
-    if (kTypes == kTypeQ8_0 || type == QT_Q8_0) {
+    if (kTypes == kTypeQ8_0 || q8_family(type)) {
       UnitQ8_0 w;
-      w.load(tile, idx, nl);
+      if (type == QT_IQ4_NL)
+        static_cast<UnitIQ4_NL &>(w).load(tile, idx, nl);
+      else if (type == QT_Q2_0)
+        static_cast<UnitQ2_0 &>(w).load(tile, idx, nl);
+      else
+        w.load(tile, idx, nl);
       ready();
 #pragma unroll
       for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)

@@ -381,7 +381,11 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   __shared__ uint32_t arow_lds[64];
   __shared__ uint64_t tab[32];
   __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
-  using Raw = std::conditional_t<kType == QT_IQ3_S, Iq3sRaw, std::conditional_t<kType == QT_Q8_0, Q80Raw, Q4kRaw>>;
+  using Raw = std::conditional_t<
+      kType == QT_IQ3_S, Iq3sRaw,
+      std::conditional_t<kType == QT_Q8_0, Q80Raw,
+                         std::conditional_t<kType == QT_IQ4_NL, Iq4nlRaw,
+                                            std::conditional_t<kType == QT_Q2_0, Q20Raw, Q4kRaw>>>>;
   // 1-D grid of (tile, row block) pairs, the row block fastest in the XCD-aware logical index over the pairs that
   // exist (the grid is sized for the most tiles a dispatch can make).
   const uint32_t nrb = g.row_blocks;
@@ -468,7 +472,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
             acc[pt][i] = __fadd_rn(acc[pt][i], __fmul_rn(__fmul_rn(h2f((uint16_t)raw.dh[i]), ad), (float)isum[pt][i]));
         }
       }
-    } else if constexpr (kType == QT_Q8_0) {
+    } else if constexpr (q8_family(kType)) {
       // Block by block: one MFMA a position tile, the block's term (d_w d_a) dot; the eight terms of the unit as the
       // pairwise tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then added to the row's sum.
       float q[3][4][4];  // the tree's pending partial sums: q[level][pt][row]
@@ -748,7 +752,7 @@ template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
   PfGemm q = g;
   q.U = U;
-  if (kGU && type != QT_Q8_0) {  // gate and up in one wave: grid.x tiles x grid.y row blocks of gu_pos rows
+  if (kGU && !q8_family(type)) {  // gate and up in one wave: grid.x tiles x grid.y row blocks of gu_pos rows
     q.row_blocks = grid.y;
     const dim3 g2(grid.x * q.row_blocks), wg(4 * MOE_TILE);
     if (type == QT_Q4_K)
@@ -764,6 +768,10 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
     pf_gemm16<QT_Q4_K, kGU><<<g2, kPfWG, 0, s>>>(q);
   else if (type == QT_IQ3_S)
     pf_gemm16<QT_IQ3_S, kGU><<<g2, kPfWG, 0, s>>>(q);
+  else if (type == QT_IQ4_NL)
+    pf_gemm16<QT_IQ4_NL, kGU><<<g2, kPfWG, 0, s>>>(q);
+  else if (type == QT_Q2_0)
+    pf_gemm16<QT_Q2_0, kGU><<<g2, kPfWG, 0, s>>>(q);
   else
     pf_gemm16<QT_Q8_0, kGU><<<g2, kPfWG, 0, s>>>(q);
 }
@@ -785,7 +793,7 @@ struct HookScope {
 // rows of each a work-group).
 void launch_gate_up(uint32_t type, const PfGemm &q, uint32_t T, uint32_t F, uint32_t Ug, uint32_t nx, hipStream_t s) {
   (void)T;
-  const uint32_t ny = type == QT_Q8_0 ? F / gemm_rows<true>() : F / gu_pos(type);
+  const uint32_t ny = q8_family(type) ? F / gemm_rows<true>() : F / gu_pos(type);
   launch_gemm<true>(type, Ug, dim3(nx, ny), q, s);
 }
 

@@ -8,7 +8,8 @@
 
 namespace c0ven {
 
-// Row r's unit u in the file's layout: the bytes of its blocks (Q8_0: 8 blocks of 34 B; Q4_K, IQ3_S: one block).
+// Row r's unit u in the file's layout: the bytes of its blocks (Q8_0: 8 blocks of 34 B; IQ4_NL: 8 of 18 B; Q2_0: 4
+// of 18 B; Q4_K, IQ3_S: one block).
 inline const uint8_t *file_unit(const uint8_t *m, uint32_t type, uint32_t k, uint32_t r, uint32_t u) {
   const uint64_t row = (uint64_t)k / quant_block_values(type) * quant_block_bytes(type);
   return m + r * row + (uint64_t)u * unit_bytes(type);
@@ -26,6 +27,14 @@ inline void put_unit(uint8_t *tile, uint32_t type, uint32_t idx, uint32_t nl, co
       for (uint32_t p = 0; p < 8; p++) std::memcpy(at(q4_kt::kQs, p, 16), b + 16 + 16 * p, 16);
       for (uint32_t i = 0; i < 3; i++) std::memcpy(at(q4_kt::kScales, i, 4), b + 4 + 4 * i, 4);
       std::memcpy(at(q4_kt::kDm, 0, 4), b, 4);
+      break;
+    case QT_IQ4_NL:
+      for (uint32_t p = 0; p < 8; p++) std::memcpy(at(iq4_nlt::kQs, p, 16), b + 18 * p + 2, 16);
+      for (uint32_t blk = 0; blk < 8; blk++) std::memcpy(at(iq4_nlt::kD, 0, 16) + 2 * blk, b + 18 * blk, 2);
+      break;
+    case QT_Q2_0:
+      for (uint32_t p = 0; p < 4; p++) std::memcpy(at(q2_0t::kQs, p, 16), b + 18 * p + 2, 16);
+      for (uint32_t blk = 0; blk < 4; blk++) std::memcpy(at(q2_0t::kD, 0, 8) + 2 * blk, b + 18 * blk, 2);
       break;
     case QT_IQ3_S:
       for (uint32_t p = 0; p < 4; p++) std::memcpy(at(iq3_st::kQs, p, 16), b + 2 + 16 * p, 16);

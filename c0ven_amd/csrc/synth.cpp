@@ -186,11 +186,59 @@ void quant_iq3_s(const float *x, uint8_t *y, uint32_t n) {
   }
 }
 
+// IQ4_NL (block_iq4_nl): per block of 32 the value of largest magnitude m, d = m / -127 (kvalues_iq4nl's first
+// entry), each value the nearest table entry of x / d. Simpler than ggml's scale search; any d and codes are a valid
+// block, and the tests read the blocks the same way on both sides.
+constexpr int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+void quant_iq4_nl(const float *x, uint8_t *y, uint32_t n) {
+  for (uint32_t b = 0; b < n / 32; b++, x += 32, y += 18) {
+    float m = 0.0f;
+    for (int j = 0; j < 32; j++)
+      if (std::fabs(x[j]) > std::fabs(m)) m = x[j];
+    const uint16_t dh = fp16_bits(m / -127.0f);
+    const float d = fp16_value(dh), id = d != 0.0f ? 1.0f / d : 0.0f;
+    std::memcpy(y, &dh, 2);
+    uint8_t code[32];
+    for (int j = 0; j < 32; j++) {
+      const float v = x[j] * id;
+      int best = 0;
+      for (int k = 1; k < 16; k++)
+        if (std::fabs(v - kIq4nl[k]) < std::fabs(v - kIq4nl[best])) best = k;
+      code[j] = (uint8_t)best;
+    }
+    for (int j = 0; j < 16; j++) y[2 + j] = (uint8_t)(code[j] | (code[j + 16] << 4));
+  }
+}
+
+// Q2_0 (block_q2_0): per block of 64, d = amax / 2 and code q = clamp(round(x / d) + 1, 0, 3), y = (q - 1) d.
+void quant_q2_0(const float *x, uint8_t *y, uint32_t n) {
+  for (uint32_t b = 0; b < n / 64; b++, x += 64, y += 18) {
+    float amax = 0.0f;
+    for (int j = 0; j < 64; j++) amax = std::max(amax, std::fabs(x[j]));
+    const uint16_t dh = fp16_bits(amax / 2.0f);
+    const float d = fp16_value(dh), id = d != 0.0f ? 1.0f / d : 0.0f;
+    std::memcpy(y, &dh, 2);
+    std::memset(y + 2, 0, 16);
+    for (int j = 0; j < 64; j++) {
+      const int q = std::min(3, std::max(0, nearest(x[j] * id) + 1));
+      y[2 + j / 4] |= (uint8_t)(q << (2 * (j % 4)));
+    }
+  }
+}
+
+// Whether a row of cols values is whole blocks of a GPU type.
+bool cols_ok(uint32_t type, uint32_t cols) {
+  const uint32_t bv = quant_block_values(type);
+  return quant_gpu_supported(type) && bv && cols % bv == 0 && cols > 0;
+}
+
 bool quant_rows(uint32_t type, const float *x, uint32_t cols, uint8_t *out) {
   switch (type) {
     case QT_Q8_0: quant_q8_0(x, out, cols); return true;
     case QT_Q4_K: quant_q4_K(x, out, cols); return true;
     case QT_IQ3_S: quant_iq3_s(x, out, cols); return true;
+    case QT_IQ4_NL: quant_iq4_nl(x, out, cols); return true;
+    case QT_Q2_0: quant_q2_0(x, out, cols); return true;
     default: return false;
   }
 }
@@ -218,7 +266,7 @@ MOE_API void moe_synth_normal(uint64_t seed, uint64_t stream, float sigma, float
 
 MOE_API moe_status moe_quantize(uint32_t type, const float *x, uint32_t rows, uint32_t cols, uint8_t *out,
                                 int nthreads) {
-  if (!quant_gpu_supported(type) || cols % quant_block_values(type) || (type != QT_Q8_0 && cols % 256)) return MOE_BAD_ARGUMENT;
+  if (!cols_ok(type, cols)) return MOE_BAD_ARGUMENT;
   const uint64_t rb = moe_row_bytes(type, cols);
   parallel_for(rows, nthreads, [&](uint64_t r) { quant_rows(type, x + r * cols, cols, out + r * rb); });
   return MOE_OK;
@@ -226,8 +274,7 @@ MOE_API moe_status moe_quantize(uint32_t type, const float *x, uint32_t rows, ui
 
 MOE_API moe_status moe_synth_matrix(uint64_t seed, uint64_t stream, float sigma, uint32_t type, uint32_t rows,
                                     uint32_t cols, uint8_t *out, int nthreads) {
-  if (!quant_gpu_supported(type) || cols % quant_block_values(type) || (type != QT_Q8_0 && cols % 256))
-    return MOE_BAD_ARGUMENT;
+  if (!cols_ok(type, cols)) return MOE_BAD_ARGUMENT;
   const Normal nr(seed, stream);
   const uint64_t rb = moe_row_bytes(type, cols);
   const uint64_t per = std::max<uint64_t>(1, (1u << 16) / cols), nc = (rows + per - 1) / per;

@@ -163,7 +163,7 @@ struct UnitIQ3_S {
       const uint32_t g = grid[ix];
       const uint32_t nib = (sg[k / 8] >> (4 * (k % 8))) & 15u;
       const uint32_t x = (nib * 0x00204081u) & 0x01010101u;  // byte j = bit j of the nibble
-      w[k] = (g ^ (x * 0xffu)) + x;                          // bytes with the bit set negated, no carries
+      w[k] = (g ^ ((x << 8) - x)) + x;                       // bytes with the bit set negated, no carries
     }
   }
   __device__ __forceinline__ float term(const Act &a) const {
@@ -178,6 +178,65 @@ struct UnitIQ3_S {
       bsum += ls[ib] * s;
     }
     return __fmul_rn(__fmul_rn(d, a.scale0()), (float)bsum);
+  }
+};
+
+// kvalues_iq4nl (ggml-common.h; -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113, whose
+// sha256 docs/spec/QUANT_FORMATS.md:547 records) as four little-endian words of table bytes 0-3, 4-7, 8-11, 12-15.
+constexpr uint32_t kIq4nlW0 = 0xBFAD9881u, kIq4nlW1 = 0xF6EADDCFu, kIq4nlW2 = 0x26190D01u, kIq4nlW3 = 0x71594535u;
+
+// Four nibbles (the bytes of n, each 0..15) to their four codebook values (signed bytes): two byte permutes pick from
+// table bytes 0-7 and 8-15, bit 3 of each nibble chooses between them.
+__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t n) {
+  const uint32_t sel = n & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(kIq4nlW1, kIq4nlW0, sel), hi = __builtin_amdgcn_perm(kIq4nlW3, kIq4nlW2, sel);
+  const uint32_t b = (n >> 3) & 0x01010101u, m = (b << 8) - b;  // 0xff where the nibble is 8..15
+  return (hi & m) | (lo & ~m);
+}
+
+// The four 2-bit codes of byte x (value j at bits 2 j) as four signed bytes q - 1 (Q2_0's -1, 0, 1, 2).
+__device__ __forceinline__ uint32_t q2_spread(uint32_t x) {
+  const uint32_t s = (x | (x << 6) | (x << 12) | (x << 18)) & 0x03030303u;
+  return ((s | 0x80808080u) - 0x01010101u) ^ 0x80808080u;  // per byte (0x80 + q) - 1, no borrows, back to q - 1
+}
+
+// IQ4_NL: eight blocks of 32, y = d kvalues[nibble] (dequantize_row_iq4_nl; vec_dot_iq4_nl_q8_0 against q8_0). The
+// codes decode to the signed bytes a Q8_0 block holds, so the term is UnitQ8_0's: pairwise over the eight blocks of
+// (d_w d_a) sumi.
+struct UnitIQ4_NL : UnitQ8_0 {
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl) {
+#pragma unroll
+    for (int p = 0; p < 8; p++) {  // block p: values 0-15 the low nibbles of its 16 bytes, 16-31 the high ones
+      const uint4 v = *field<uint4>(tile, iq4_nlt::kQs, p, idx, nl);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        q[8 * p + i] = iq4nl_lookup(w[i] & 0x0f0f0f0fu);
+        q[8 * p + 4 + i] = iq4nl_lookup((w[i] >> 4) & 0x0f0f0f0fu);
+      }
+    }
+    const uint4 dv = *field<uint4>(tile, iq4_nlt::kD, 0, idx, nl);
+    const uint32_t w[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+    for (int b = 0; b < 8; b++) d[b] = h2f((uint16_t)(w[b / 2] >> (16 * (b % 2))));
+  }
+};
+
+// Q2_0: four blocks of 64 with one f16 scale, y = (q - 1) d (dequantize_row_q2_0), against q8_0 blocks of 32: each
+// half block is a Q8_0-like block of codes q - 1 with the block's d, so the term is UnitQ8_0's over the eight halves.
+struct UnitQ2_0 : UnitQ8_0 {
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) {  // block p: half 2 p is bytes 0-7, half 2 p + 1 bytes 8-15, four codes a byte
+      const uint4 v = *field<uint4>(tile, q2_0t::kQs, p, idx, nl);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 16; i++) q[16 * p + i] = q2_spread((w[i / 4] >> (8 * (i % 4))) & 0xffu);
+    }
+    const uint2 dv = *field<uint2>(tile, q2_0t::kD, 0, idx, nl);
+    const uint32_t w[2] = {dv.x, dv.y};
+#pragma unroll
+    for (int h = 0; h < 8; h++) d[h] = h2f((uint16_t)(w[h / 4] >> (16 * ((h / 2) % 2))));
   }
 };
 

@@ -3,9 +3,9 @@
  * Replaces the reference's shared/quant.h (ids :9-33, values per block :36-44, bytes per block :47-75, field tables
  * :78-166, run offsets :172-176, QUANT_FILE_PAD :180, codebook buffer offsets :189-196). The numeric values, the field
  * order (quants first, the f16 scales last) and the codebook buffer offsets are the same, so a caller that built
- * buffers for the reference's headers builds the same bytes for these. Only the three types this block implements on
- * the GPU (Q8_0, Q4_K, IQ3_S) and the two activation types (q8_0, q8_K) carry field tables; the other ids are kept so
- * that a caller's switch over them still compiles. C and HIP device code both include this header. */
+ * buffers for the reference's headers builds the same bytes for these. Only the five types this block implements on
+ * the GPU (Q8_0, Q4_K, IQ3_S, IQ4_NL, Q2_0) and the two activation types (q8_0, q8_K) carry field tables; the other
+ * ids are kept so that a caller's switch over them still compiles. C and HIP device code both include this header. */
 #ifndef C0VEN_QUANT_H
 #define C0VEN_QUANT_H
 
@@ -90,13 +90,16 @@ C0VEN_FN uint32_t quant_block_bytes(uint32_t t) {
 }
 
 /* Whether the GPU block implements a weight type. */
-C0VEN_FN int quant_gpu_supported(uint32_t t) { return t == QT_Q8_0 || t == QT_Q4_K || t == QT_IQ3_S; }
+C0VEN_FN int quant_gpu_supported(uint32_t t) {
+  return t == QT_Q8_0 || t == QT_Q4_K || t == QT_IQ3_S || t == QT_IQ4_NL || t == QT_Q2_0;
+}
 
 /* The activation type a weight type's integer dot product takes on the CPU (ggml-cpu.c vec_dot_type): q8_K for the
- * K- and i-quants, q8_0 for Q8_0. 0 (F32) for a type without one here. */
+ * K- and i-quants of 256-value blocks, q8_0 for Q8_0, IQ4_NL and Q2_0 (ggml-cpu.c :272, :380, :234). 0 (F32) for a
+ * type without one here. */
 C0VEN_FN uint32_t quant_vec_dot_type(uint32_t t) {
   switch (t) {
-    case QT_Q8_0: return QT_Q8_0;
+    case QT_Q8_0: case QT_IQ4_NL: case QT_Q2_0: return QT_Q8_0;
     case QT_Q4_K: case QT_IQ3_S: return QT_Q8_K;
     default: return QT_F32;
   }
@@ -107,7 +110,7 @@ C0VEN_FN uint32_t quant_nfields(uint32_t t) {
   switch (t) {
     case QT_IQ3_S: return 5;
     case QT_Q4_K: return 3;
-    case QT_Q8_0: return 2;
+    case QT_Q8_0: case QT_IQ4_NL: case QT_Q2_0: return 2;
     case QT_Q8_K: return 3;
     default: return 1;
   }
@@ -122,6 +125,8 @@ C0VEN_FN uint32_t quant_field_(uint32_t t, uint32_t f) {
       return f == 0 ? (16u << 8) | 128 : f == 1 ? (4u << 8) | 12 : (0u << 8) | 4;
     case QT_Q8_0: /* qs, d */
       return f == 0 ? (2u << 8) | 32 : (0u << 8) | 2;
+    case QT_IQ4_NL: case QT_Q2_0: /* qs, d */
+      return f == 0 ? (2u << 8) | 16 : (0u << 8) | 2;
     case QT_Q8_K: /* qs (256 int8), bsums (16 int16), d (f32) */
       return f == 0 ? (4u << 8) | 256 : f == 1 ? (260u << 8) | 32 : (0u << 8) | 4;
     default: return quant_block_bytes(t);
@@ -142,7 +147,8 @@ C0VEN_FN uint64_t quant_run_offset(uint32_t t, uint32_t f, uint64_t n) {
 #define QUANT_FILE_PAD 8
 
 /* The codebook buffer's layout, as the reference packs ggml-common.h's tables for its cards. This build fills only
- * the IQ3_S grid (512 x u32) and kvalues; the other regions are kept at their offsets and left zero. */
+ * the IQ3_S grid (512 x u32) and kvalues (kvalues_iq4nl: -127 .. 113); the other regions are kept at their offsets
+ * and left zero. */
 #define QGRID_IQ2S 0        /* u64 x 1024 */
 #define QGRID_IQ3XXS 8192   /* u32 x 256 */
 #define QGRID_IQ3S 9216     /* u32 x 512 */

@@ -238,6 +238,10 @@ static int fast_compute_many(const orc_shape *s, const orc_job *jobs, uint32_t n
   for (uint32_t t = 0; t < ntok; t++) memset(y + t * y_stride, 0, sizeof(float) * E);
   if (njobs == 0) return 0;
   if (E % QK || F % QK) return -1;
+  for (int m = 0; m < 2; m++) { /* the config types: Q8_0, Q4_K, IQ3_S */
+    const uint32_t t = m ? s->down_type : s->gate_type;
+    if (t != QT_Q8_0 && t != QT_Q4_K && t != QT_IQ3_S) return -1;
+  }
   const uint32_t ga = act_type_of(s->gate_type), da = act_type_of(s->down_type);
   const uint64_t xq_bytes = act_bytes(ga, E), hq_bytes = act_bytes(da, F);
   const uint64_t grow = row_bytes(s->gate_type, E), drow = row_bytes(s->down_type, F);

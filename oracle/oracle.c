@@ -12,7 +12,15 @@
 #define QT_Q4_K 12
 #define QT_Q8_K 15
 #define QT_IQ3_S 21
+#define QT_IQ4_NL 20
+#define QT_Q2_0 42
 #define QK 256
+
+/* kvalues_iq4nl (ggml-common.h:1120-1122): the IQ4_NL codebook, which must hash to QUANT_FORMATS.md:547's sha256
+ * (tests/test_oracle.py checks it). */
+static const int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+void orc_iq4nl_values(int8_t *out) { memcpy(out, kIq4nl, 16); }
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Scalars. */
@@ -169,6 +177,23 @@ int orc_dequantize_row(uint32_t type, const void *src, float *dst, int64_t n) {
         }
       }
       return 0;
+    case QT_IQ4_NL: /* y = d kvalues[nibble]; byte j holds value j (low nibble) and j + 16 (QUANT_FORMATS.md:234-245) */
+      if (n % 32) return -1;
+      for (int64_t i = 0; i < n / 32; i++, b += 18) {
+        const float d = orc_fp16_to_fp32(rd16(b));
+        for (int j = 0; j < 16; j++) {
+          dst[32 * i + j] = d * (float)kIq4nl[b[2 + j] & 15];
+          dst[32 * i + j + 16] = d * (float)kIq4nl[b[2 + j] >> 4];
+        }
+      }
+      return 0;
+    case QT_Q2_0: /* y = (q - 1) d, value j bits 2 (j mod 4) of byte j / 4 (QUANT_FORMATS.md:251-262, quants.c:439-457) */
+      if (n % 64) return -1;
+      for (int64_t i = 0; i < n / 64; i++, b += 18) {
+        const float d = orc_fp16_to_fp32(rd16(b));
+        for (int j = 0; j < 64; j++) dst[64 * i + j] = (float)((int)((b[2 + j / 4] >> (2 * (j % 4))) & 3) - 1) * d;
+      }
+      return 0;
     default: return -1;
   }
 }
@@ -238,11 +263,20 @@ int orc_quantize_act(uint32_t act_type, const float *src, void *dst, int64_t n) 
   return -1;
 }
 
-static uint32_t act_type_of(uint32_t t) { return t == QT_Q8_0 ? QT_Q8_0 : (t == QT_Q4_K || t == QT_IQ3_S) ? QT_Q8_K : 0; }
+/* The 32-value block types: q8_0 activations (ggml-cpu.c vec_dot_type: Q8_0, IQ4_NL :380, Q2_0 :234). */
+static int q8_family(uint32_t t) { return t == QT_Q8_0 || t == QT_IQ4_NL || t == QT_Q2_0; }
+static uint32_t act_type_of(uint32_t t) { return q8_family(t) ? QT_Q8_0 : (t == QT_Q4_K || t == QT_IQ3_S) ? QT_Q8_K : 0; }
 static uint64_t act_bytes(uint32_t act, uint64_t n) { return act == QT_Q8_0 ? n / 32 * 34 : n / QK * 292; }
 static uint64_t row_bytes(uint32_t t, uint64_t n) {
-  return t == QT_Q8_0 ? n / 32 * 34 : t == QT_Q4_K ? n / QK * 144 : t == QT_IQ3_S ? n / QK * 110 : 0;
+  return t == QT_Q8_0 ? n / 32 * 34
+         : t == QT_IQ4_NL ? n / 32 * 18
+         : t == QT_Q2_0   ? n / 64 * 18
+         : t == QT_Q4_K   ? n / QK * 144
+         : t == QT_IQ3_S  ? n / QK * 110
+                          : 0;
 }
+/* The values a row's length must be a multiple of: the type's block. */
+static int64_t row_block(uint32_t t) { return t == QT_Q8_0 || t == QT_IQ4_NL ? 32 : t == QT_Q2_0 ? 64 : QK; }
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Block dot products. Each returns the block's fp32 term; the row sums them in ORACLE ORDER: a pairwise tree within
@@ -259,6 +293,27 @@ static float pairwise(const float *a, int64_t n) {
 static float term_q8_0(const uint8_t *w, const uint8_t *a) {
   int32_t s = 0;
   for (int j = 0; j < 32; j++) s += (int32_t)(int8_t)w[2 + j] * (int32_t)(int8_t)a[2 + j];
+  const float d = orc_fp16_to_fp32(rd16(w)) * orc_fp16_to_fp32(rd16(a));
+  return d * (float)s;
+}
+
+/* IQ4_NL x q8_0 (vec_dot_iq4_nl_q8_0, QUANT_FORMATS.md:243-246): (d_w d_a) sum kvalues[nibble] q_a. */
+static float term_iq4_nl(const uint8_t *w, const uint8_t *a) {
+  int32_t s = 0;
+  for (int j = 0; j < 16; j++)
+    s += kIq4nl[w[2 + j] & 15] * (int32_t)(int8_t)a[2 + j] + kIq4nl[w[2 + j] >> 4] * (int32_t)(int8_t)a[2 + j + 16];
+  const float d = orc_fp16_to_fp32(rd16(w)) * orc_fp16_to_fp32(rd16(a));
+  return d * (float)s;
+}
+
+/* Q2_0 x q8_0, half h (0, 1) of a 64-value block against one 32-value q8_0 block (QUANT_FORMATS.md:264-270: one
+ * term a half, d d_a sumi with the codes unpacked to q - 1): (d_w d_a) sum (q - 1) q_a. */
+static float term_q2_0(const uint8_t *w, int h, const uint8_t *a) {
+  int32_t s = 0;
+  for (int j = 0; j < 32; j++) {
+    const int v = 32 * h + j;
+    s += ((int)((w[2 + v / 4] >> (2 * (v % 4))) & 3) - 1) * (int32_t)(int8_t)a[2 + j];
+  }
   const float d = orc_fp16_to_fp32(rd16(w)) * orc_fp16_to_fp32(rd16(a));
   return d * (float)s;
 }
@@ -315,6 +370,14 @@ static float dot_row(uint32_t type, int64_t n, const uint8_t *w, const uint8_t *
       nb = n / 32;
       for (int64_t i = 0; i < nb; i++) terms[i] = term_q8_0(w + 34 * i, a + 34 * i);
       break;
+    case QT_IQ4_NL:
+      nb = n / 32;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_iq4_nl(w + 18 * i, a + 34 * i);
+      break;
+    case QT_Q2_0:  /* two terms a block, one per 32-value half */
+      nb = n / 32;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_q2_0(w + 18 * (i / 2), (int)(i % 2), a + 34 * i);
+      break;
     case QT_Q4_K:
       nb = n / QK;
       for (int64_t i = 0; i < nb; i++) terms[i] = term_q4_K(w + 144 * i, a + 292 * i);
@@ -324,14 +387,14 @@ static float dot_row(uint32_t type, int64_t n, const uint8_t *w, const uint8_t *
       for (int64_t i = 0; i < nb; i++) terms[i] = term_iq3_s(w + 110 * i, a + 292 * i);
       break;
   }
-  const int64_t per = type == QT_Q8_0 ? 8 : 1;  /* terms a unit of 256 values has */
+  const int64_t per = q8_family(type) ? 8 : 1;  /* terms a unit of 256 values has */
   float acc = 0.0f;
   for (int64_t i = 0; i < nb; i += per) acc += pairwise(terms + i, nb - i < per ? nb - i : per);
   return acc;
 }
 
 int orc_vec_dot(uint32_t type, int64_t n, const void *w_row, const void *act, float *out) {
-  if (!act_type_of(type) || n % (type == QT_Q8_0 ? 32 : QK) || n <= 0) return -1;
+  if (!act_type_of(type) || n % row_block(type) || n <= 0) return -1;
   grid_init();
   float *terms = (float *)malloc(sizeof(float) * (size_t)(n / 32));
   *out = dot_row(type, n, (const uint8_t *)w_row, (const uint8_t *)act, terms);
@@ -354,7 +417,7 @@ static inline float swiglu_one(float g, float u, float limit) {
 static int shape_ok(const orc_shape *s) {
   const uint32_t ga = act_type_of(s->gate_type), da = act_type_of(s->down_type);
   if (!ga || !da || !s->n_embd || !s->n_ff) return 0;
-  if (s->n_embd % (ga == QT_Q8_0 ? 32 : QK) || s->n_ff % (da == QT_Q8_0 ? 32 : QK)) return 0;
+  if (s->n_embd % row_block(s->gate_type) || s->n_ff % row_block(s->down_type)) return 0;
   return 1;
 }
 

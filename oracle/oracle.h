@@ -2,8 +2,8 @@
  * bench.py's cpu_baseline leg load it, as the checker; the product (c0ven_amd/) never links or calls it.
  *
  * A plain-C restatement of the reference's CPU expert path and of the block around it:
- *   - the weight decoders (ggml's dequantize_row_q8_0 / _q4_K / _iq3_s, as docs/spec/QUANT_FORMATS.md:176-212,
- *     :373-400, :447-466 state them);
+ *   - the weight decoders (ggml's dequantize_row_q8_0 / _q4_K / _iq3_s / _iq4_nl / _q2_0, as
+ *     docs/spec/QUANT_FORMATS.md:176-212, :373-400, :447-466, :234-246, :251-270 state them);
  *   - the activation quantisers the CPU path converts x and h with (q8_0, QUANT_FORMATS.md:463-465; q8_K,
  *     :528-535), chosen per weight type as core/cpu/experts.cpp:114-123 does (ggml's vec_dot_type);
  *   - the integer block dot products (vec_dot) of each weight type against its activation type;
@@ -14,11 +14,13 @@
  *     with max(sum, 6.1035e-5) (layer.cl:781-804); the shared expert and its sigmoid gate (MODEL_LAYER.md:444-449);
  *     the combine y = sum_k w_k y_k (rank order) + gs * s (layer.cl:869-884, llama-graph.cpp:2334-2343).
  *
- * Pinned by tests/test_oracle.py: the IQ3_S grid against the sha256 in QUANT_FORMATS.md:546, every decoder against
+ * Pinned by tests/test_oracle.py: the IQ3_S grid and kvalues_iq4nl against the sha256s in QUANT_FORMATS.md:546-547,
+ * every decoder against
  * its closed form on hand-made blocks, the dot products against float dots of the decoded blocks and against brute
  * force, compute against compute_many, the router against brute-force sorting, and the block against a dense fp64
  * SwiGLU FFN where k = E. What only ggml itself could pin (its SIMD float summation order, see ORACLE ORDER below,
- * and its bf16 dot order) is stated as unpinned there. */
+ * its bf16 dot order, and the fp32 steps of its CPU Q2_0 dot, whose source the reference does not hold: the oracle
+ * takes the CUDA kernel's one term a 32-value half) is stated as unpinned there. */
 #ifndef C0VEN_ORACLE_H
 #define C0VEN_ORACLE_H
 
@@ -31,8 +33,10 @@ extern "C" {
 /* ORACLE ORDER. The integer part of every block dot product is exact, so only the fp32 steps fix the bits. ggml's
  * SIMD kernels sum them in an architecture-dependent order that no source in the reference restates; the oracle uses
  * one canonical order, stated per type in oracle.c, and the GPU kernels reproduce it:
- *   - one fp32 term per block (Q8_0: 32 values) or super-block (Q4_K, IQ3_S: 256 values);
- *   - a unit of 256 values (eight Q8_0 blocks, one super-block) sums its terms as a pairwise tree:
+ *   - one fp32 term per 32 values for the q8_0 types (a Q8_0 or IQ4_NL block, half a Q2_0 block, as the CUDA
+ *     kernels split Q2_0: QUANT_FORMATS.md:264-268) or per super-block (Q4_K, IQ3_S: 256 values);
+ *   - a unit of 256 values (eight 32-value terms, one super-block) sums its terms as a pairwise tree; a row's last,
+ *     partial unit (n_ff = 640: half a unit) sums the terms it has the same way:
  *     sum(a[0..n)) = sum(a[0..m)) + sum(a[m..n)), m the largest power of two below n (n = 1: a[0]);
  *   - a row adds its units in sequence, from 0.0f: acc = acc + unit_u, u ascending. */
 
@@ -68,6 +72,7 @@ void orc_expf(const float *x, float *y, int64_t n); /* libm's expf, element by e
 
 /* The IQ3_S codebook, 512 x u32. */
 void orc_iq3s_grid(uint32_t *out);
+void orc_iq4nl_values(int8_t *out); /* kvalues_iq4nl, 16 signed bytes */
 
 /* Returns 0, or -1 for a type it does not know or an n that is no whole number of blocks. */
 int orc_dequantize_row(uint32_t type, const void *src, float *dst, int64_t n);

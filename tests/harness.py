@@ -30,6 +30,7 @@ def _load_oracle():
         "orc_fp32_to_bf16": (C.c_uint16, [C.c_float]),
         "orc_expf": (None, [_P, _P, C.c_int64]),
         "orc_iq3s_grid": (None, [_P]),
+        "orc_iq4nl_values": (None, [_P]),
         "orc_dequantize_row": (C.c_int, [C.c_uint32, _P, _P, C.c_int64]),
         "orc_quantize_act": (C.c_int, [C.c_uint32, _P, _P, C.c_int64]),
         "orc_vec_dot": (C.c_int, [C.c_uint32, C.c_int64, _P, _P, C.POINTER(C.c_float)]),
@@ -75,7 +76,7 @@ def act_bytes(act_type, n):
 
 
 def vec_dot_type(t):
-    return moe.QT_Q8_0 if t == moe.QT_Q8_0 else moe.QT_Q8_K
+    return moe.QT_Q8_0 if t in moe.Q8_FAMILY else moe.QT_Q8_K
 
 
 def orc_dequant(qtype, blocks, n):
@@ -108,6 +109,12 @@ def orc_grid():
     g = np.empty(512, dtype=np.uint32)
     oracle.orc_iq3s_grid(ptr(g))
     return g
+
+
+def orc_iq4nl():
+    v = np.empty(16, dtype=np.int8)
+    oracle.orc_iq4nl_values(ptr(v))
+    return v
 
 
 def to_bf16(x):

@@ -34,7 +34,8 @@ def check_block(y, ids, w, yo, io, wo, exact=True):
 def random_blocks(qtype, nblocks):
     nv, nb = moe.BLOCK[qtype]
     b = rng.integers(0, 256, size=(nblocks, nb), dtype=np.uint8)
-    reach = {moe.QT_Q8_0: [(0, 128)], moe.QT_Q4_K: [(0, 63 * 15), (2, 63)], moe.QT_IQ3_S: [(0, 31 * 15)]}[qtype]
+    reach = {moe.QT_Q8_0: [(0, 128)], moe.QT_Q4_K: [(0, 63 * 15), (2, 63)], moe.QT_IQ3_S: [(0, 31 * 15)],
+             moe.QT_IQ4_NL: [(0, 127)], moe.QT_Q2_0: [(0, 2)]}[qtype]
     for k in range(nblocks):
         for off, r in reach:
             v = np.ldexp(1.0 + rng.integers(0, 1024) / 1024.0, int(rng.integers(0, 3)) - 5) / r
@@ -49,7 +50,7 @@ def tiny_block():
     blk.close()
 
 
-@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S])
+@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q2_0])
 @pytest.mark.parametrize("rows,cols", [(128, 512), (100, 256)])
 def test_dequantize_bit_exact(tiny_block, qtype, rows, cols):
     say("dequantize", moe.TYPE_NAMES[qtype], rows, cols)
@@ -196,7 +197,7 @@ def _cm_jobs(L, T, K, rng_seed, parts=False):
     expert on some tokens; with parts, down given as two regions (equal halves, or 1/3 + 2/3 as down_blocks)."""
     r = np.random.default_rng(rng_seed)
     jobs, ojobs = [], []
-    bv, bb = {moe.QT_Q8_0: (32, 34), moe.QT_Q4_K: (256, 144), moe.QT_IQ3_S: (256, 110)}[L.down_type]
+    bv, bb = moe.BLOCK[L.down_type]
     nb = L.F // bv
     for t in range(T):
         es = r.choice(L.E, size=K, replace=False).tolist() + ([L.E] if t % 3 == 0 else [])
@@ -235,12 +236,16 @@ def test_compute_many_borrowed(T, types):
 
 
 @pytest.mark.parametrize("types", [(moe.QT_Q4_K, moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_Q8_0),
-                                   (moe.QT_IQ3_S, moe.QT_Q8_0, moe.QT_Q8_0, moe.QT_Q8_0)])
+                                   (moe.QT_IQ3_S, moe.QT_Q8_0, moe.QT_Q8_0, moe.QT_Q8_0),
+                                   (moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q8_0, moe.QT_IQ4_NL),
+                                   (moe.QT_IQ3_S, moe.QT_Q2_0, moe.QT_Q8_0, moe.QT_Q2_0),
+                                   (moe.QT_IQ4_NL, moe.QT_Q2_0, moe.QT_Q2_0, moe.QT_IQ4_NL)])
 @pytest.mark.parametrize("T", [1, 8, 100])
 def test_model_shape_2560_640(types, T):
     """The reference model's own expert shape (MODEL_LAYER.md:51, :69): n_embd 2560 (ten 256-value units, not a power of
-    two), n_ff 640 (down's K two and a half units: its last unit half blocks, half zero padding). Decode (T 1, 8) and
-    prefill (T 100) against the oracle, bit for bit."""
+    two), n_ff 640 (down's K two and a half units: its last unit half blocks, half zero padding), with the file's down
+    types (IQ4_NL, Q2_0: QUANT_FORMATS.md:43-44) and both as gate/up too. Decode (T 1, 8) and prefill (T 100) against
+    the oracle, bit for bit."""
     gt, dt, sgt, sdt = types
     say("shape 2560 x 640", [moe.TYPE_NAMES[t] for t in types], "T", T)
     L = h.Layer(2560, 640, 64, 8, gt, dt, sgt, sdt, seed=2560 + T, zipf=1.1)
@@ -252,10 +257,12 @@ def test_model_shape_2560_640(types, T):
     blk.close()
 
 
-def test_dequantize_partial_unit(tiny_block):
-    """A row of 640 values (two and a half units) of Q8_0 through the device layout: the partial unit's blocks decode
-    as the format says and nothing past the row is written."""
-    m = moe.synth_matrix(5, 2, moe.QT_Q8_0, 70, 640)
-    got = tiny_block.dequantize(moe.QT_Q8_0, m, 70, 640)
-    want = np.stack([h.orc_dequant(moe.QT_Q8_0, m[r * 680:(r + 1) * 680], 640) for r in range(70)])
+@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_IQ4_NL, moe.QT_Q2_0])
+def test_dequantize_partial_unit(tiny_block, qtype):
+    """A row of 640 values (two and a half units) through the device layout: the partial unit's blocks decode as the
+    format says and nothing past the row is written."""
+    m = moe.synth_matrix(5, 2, qtype, 70, 640)
+    rb = moe.row_bytes(qtype, 640)
+    got = tiny_block.dequantize(qtype, m, 70, 640)
+    want = np.stack([h.orc_dequant(qtype, m[r * rb:(r + 1) * rb], 640) for r in range(70)])
     assert np.array_equal(got, want)

@@ -2,17 +2,18 @@
 
 The reference commits no golden vectors for this path (its tests call ggml at run time; docs/TESTING.md:60-74), and
 ggml is absent here, so each function is pinned by what the format and the mathematics fix:
-  - the IQ3_S grid against the sha256 the reference records (docs/spec/QUANT_FORMATS.md:546);
+  - the IQ3_S grid and kvalues_iq4nl against the sha256s the reference records (docs/spec/QUANT_FORMATS.md:546-547);
   - each decoder on hand-built blocks whose values the format's tables (QUANT_FORMATS.md:176-212, :373-400,
-    :447-466) give position by position;
+    :447-466, :234-246, :251-262) give position by position;
   - the activation quantisers by their invariants and by exact ties (the rounding rule);
   - the dot products against float64 dots of the decoded operands, to the reference's own tolerance (1e-4 of
     sum |w a|, docs/TESTING.md:45-58), and exactly where every fp32 step is exact;
   - compute against compute_many bit for bit (core/tests/cpu_experts_test.cpp:240-275), y overwritten;
   - the experts and the block against a float64 SwiGLU FFN on the decoded weights;
   - the router against a float64 softmax and a sort with ties to the lower expert (core/tests/topk_test.cpp:60-67).
-What only ggml could pin - its SIMD fp32 summation order, its bf16 dot order - is "parity unpinned" (the oracle sums
-block terms in a stated canonical order instead).
+What only ggml could pin - its SIMD fp32 summation order, its bf16 dot order, the fp32 steps of its CPU Q2_0 dot (a
+ggml fork's source the reference does not hold) - is "parity unpinned" (the oracle sums block terms in a stated
+canonical order instead, Q2_0 as one term a 32-value half like the CUDA kernel).
 """
 import hashlib
 
@@ -40,6 +41,13 @@ def test_iq3s_grid_matches_pinned_sha256():
     b = g.view(np.uint8)
     assert set(np.unique(b).tolist()) == {1, 3, 5, 7, 9, 11, 13, 15}
     assert len(np.unique(g)) == 512
+
+
+def test_iq4nl_values_match_pinned_sha256():
+    v = h.orc_iq4nl()
+    assert hashlib.sha256(v.tobytes()).hexdigest() == (
+        "61aa47540aa024b5d6ddaa839b84ffe59f3d5a349af5c6c7ffcb5e0474b46163")
+    assert v[0] == -127 and v[-1] == 113 and (np.diff(v.astype(int)) > 0).all()
 
 
 def test_fp16_conversions_match_ieee():
@@ -83,6 +91,28 @@ def test_q8_0_decoder():
     blk = np.concatenate([f16(0.5), q.view(np.uint8)])
     y = h.orc_dequant(moe.QT_Q8_0, blk, 32)
     assert np.array_equal(y, (np.float32(0.5) * q.astype(np.float32)))
+
+
+def test_iq4_nl_decoder():
+    """Byte j holds value j in its low nibble and value j + 16 in its high one; y = d kvalues[nibble]."""
+    kv = h.orc_iq4nl().astype(np.float32)
+    lo = np.arange(16, dtype=np.uint8)
+    hi = (np.arange(16, dtype=np.uint8) * 7 + 3) % 16
+    blk = np.concatenate([f16(0.25), lo | (hi << 4)]).astype(np.uint8)
+    y = h.orc_dequant(moe.QT_IQ4_NL, blk, 32)
+    assert np.array_equal(y, np.float32(0.25) * np.concatenate([kv[lo], kv[hi]]))
+
+
+def test_q2_0_decoder():
+    """Value j is bits 2 (j mod 4), 2 (j mod 4) + 1 of byte j / 4; y = (q - 1) d: codes mean -1, 0, 1, 2."""
+    q = rng.integers(0, 4, size=64)
+    qs = np.zeros(16, dtype=np.uint8)
+    for j in range(64):
+        qs[j // 4] |= np.uint8(q[j] << (2 * (j % 4)))
+    y = h.orc_dequant(moe.QT_Q2_0, np.concatenate([f16(-1.5), qs]), 64)
+    assert np.array_equal(y, (q - 1).astype(np.float32) * np.float32(-1.5))
+    assert np.array_equal(h.orc_dequant(moe.QT_Q2_0, np.concatenate([f16(2.0), np.full(16, 0xE4, np.uint8)]), 64),
+                          np.tile(np.array([-2, 0, 2, 4], np.float32), 16))  # 0xE4: codes 0, 1, 2, 3
 
 
 def pack_q4_k_scales(sc, m):
@@ -200,7 +230,8 @@ def random_blocks(qtype, n):
     """n blocks of random bytes with scales set so values stay small (core/tests/test_util.h:62-103's rule)."""
     nv, nbytes = moe.BLOCK[qtype]
     b = rng.integers(0, 256, size=(n, nbytes), dtype=np.uint8)
-    reach = {moe.QT_Q8_0: [(0, 128)], moe.QT_Q4_K: [(0, 63 * 15), (2, 63)], moe.QT_IQ3_S: [(0, 31 * 15)]}[qtype]
+    reach = {moe.QT_Q8_0: [(0, 128)], moe.QT_Q4_K: [(0, 63 * 15), (2, 63)], moe.QT_IQ3_S: [(0, 31 * 15)],
+             moe.QT_IQ4_NL: [(0, 127)], moe.QT_Q2_0: [(0, 2)]}[qtype]
     for k in range(n):
         for off, r in reach:
             v = np.ldexp(1.0 + rng.integers(0, 1024) / 1024.0, int(rng.integers(0, 3)) - 5) / r
@@ -208,7 +239,7 @@ def random_blocks(qtype, n):
     return b.ravel()
 
 
-@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S])
+@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q2_0])
 @pytest.mark.parametrize("n", [256, 2048])
 def test_vec_dot_against_decoded_float64(qtype, n):
     for trial in range(20):
@@ -245,6 +276,20 @@ def test_vec_dot_exact_when_every_step_is_exact():
     a[:, 2:] = rng.integers(-20, 21, size=(n // 32, 32), dtype=np.int8).view(np.uint8)
     exact = float((w[:, 2:].view(np.int8).astype(np.int64) * a[:, 2:].view(np.int8).astype(np.int64)).sum()) * 2.0**-9
     assert h.orc_vec_dot(moe.QT_Q8_0, n, w.ravel(), a.ravel()) == exact
+    # IQ4_NL and Q2_0 against the same q8_0 blocks: codebook values and codes q - 1, scale 2^-6
+    ad = a[:, 2:].view(np.int8).astype(np.int64).ravel()
+    kv = h.orc_iq4nl().astype(np.int64)
+    nib = rng.integers(0, 16, size=(n // 32, 32))
+    w4 = np.zeros((n // 32, 18), dtype=np.uint8)
+    w4[:, :2] = f16(2.0**-6)
+    w4[:, 2:] = (nib[:, :16] | (nib[:, 16:] << 4)).astype(np.uint8)
+    assert h.orc_vec_dot(moe.QT_IQ4_NL, n, w4.ravel(), a.ravel()) == float((kv[nib].ravel() * ad).sum()) * 2.0**-9
+    q2 = rng.integers(0, 4, size=(n // 64, 64))
+    w2 = np.zeros((n // 64, 18), dtype=np.uint8)
+    w2[:, :2] = f16(2.0**-6)
+    for j in range(64):
+        w2[:, 2 + j // 4] |= (q2[:, j] << (2 * (j % 4))).astype(np.uint8)
+    assert h.orc_vec_dot(moe.QT_Q2_0, n, w2.ravel(), a.ravel()) == float(((q2 - 1).ravel() * ad).sum()) * 2.0**-9
     # Q4_K and IQ3_S against q8_K with d = 2^-4
     x = rng.integers(-20, 21, size=n).astype(np.float32)
     x[::256] = -127.0  # max = -127: iscale = 1, codes = x, d = 1
@@ -273,7 +318,7 @@ def dense_ffn(gate, up, down, gt, dt, H, F, x, limit=0.0):
 
 
 TYPES = [(moe.QT_Q8_0, moe.QT_Q8_0), (moe.QT_Q4_K, moe.QT_Q4_K), (moe.QT_IQ3_S, moe.QT_Q4_K), (moe.QT_IQ3_S, moe.QT_IQ3_S),
-         (moe.QT_Q4_K, moe.QT_Q8_0)]
+         (moe.QT_Q4_K, moe.QT_Q8_0), (moe.QT_Q4_K, moe.QT_IQ4_NL), (moe.QT_IQ4_NL, moe.QT_Q2_0)]
 
 
 @pytest.mark.parametrize("gt,dt", TYPES)
