@@ -40,9 +40,9 @@ constexpr uint32_t shared_chunks(uint32_t T, uint32_t route, uint32_t has_shared
 // Groups a launch may have: routed (every assignment its own, at worst), or a pre-routed call's jobs.
 constexpr uint32_t kMaxGroups = max_groups(kMaxDecodeTokens, kMaxUsed + 1);
 // LDS the grouping step takes from the dynamic allocation: T K ids, a token mask and two group numbers per expert,
-// and a sort key per group.
+// and a count of heads per wave and group size.
 constexpr uint32_t kGroupingLds =
-    kMaxDecodeTokens * kMaxUsed * 4 + kMaxExperts * 4 + kMaxExperts * 2 * 4 + (kMaxDecodeTokens * kMaxUsed + 2) * 4;
+    kMaxDecodeTokens * kMaxUsed * 4 + kMaxExperts * 4 + kMaxExperts * 2 * 4 + (kWG / 64) * MOE_GROUP_MAX * 4;
 constexpr uint32_t kDynLists = 8;     // lists the routed items are dealt from (one counter each)
 constexpr uint32_t kDynStride = 64;   // words between two list counters
 // LDS after a group's activation units for the matrix-core gate/up item's exchanges (unit terms, then sums).

@@ -34,7 +34,7 @@ __host__ __device__ __forceinline__ float expf_libm(float x, const uint64_t *tab
   const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                C2 = 0x1.62e42ff0c52d6p-1 / 32;
   const bool under = x < -0x1.9fe368p6f, over = x > 0x1.62e42ep6f, nan = x != x;
-  const double xd = (double)(under | over | nan ? 0.0f : x);
+  const double xd = (double)((under | over | nan) ? 0.0f : x);
   double kd = __builtin_fma(InvLn2N, xd, Shift);
   const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
   kd = kd - Shift;

@@ -992,7 +992,7 @@ MOE_API moe_status moe_trace(moe_ctx *c, uint64_t *stamps, uint32_t cap, uint32_
     if (bounds) std::memcpy(bounds, bb, sizeof bb);
     *n = std::min(end, c->trace_cap);
     if (stamps)
-      check(hipMemcpy(stamps, c->trace, sizeof(uint64_t) * 4 * std::min(cap, *n), hipMemcpyDeviceToHost),
+      check(hipMemcpy(stamps, c->trace, sizeof(uint64_t) * 4 * std::min(cap, c->trace_cap), hipMemcpyDeviceToHost),
             "download trace");
   });
 }

@@ -416,8 +416,7 @@ __device__ __forceinline__ void router_row(const DecodeParams &p, uint32_t row, 
 // The launch's groups, in LDS: each work-group builds the table itself from the routed ids (the same table in every
 // work-group), or copies a pre-routed call's from the host's.
 struct GroupTab {
-  uint32_t ng, have_w;                                 // have_w: w and gs below are filled (routed launches)
-  float w[kMaxDecodeTokens * kMaxUsed], gs[kMaxDecodeTokens];
+  uint32_t ng;
   int32_t slot[kMaxGroups];
   uint32_t n[kMaxGroups];
   uint16_t asg[kMaxGroups][MOE_GROUP_MAX];
@@ -426,20 +425,23 @@ struct GroupTab {
 // MoeGroup records from the routed ids: an expert's assignments in order, MOE_GROUP_MAX a group (as group_slots,
 // layer.cl:894-942); numbered by decreasing size, then by first assignment. An expert takes at most one assignment a
 // token, so a mask of the tokens that chose it gives each assignment its rank among the expert's (and whether it heads
-// a group); the heads' ballots give the group numbers.
-__device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds, uint64_t *hb, GroupTab *tab) {
-  const uint32_t T = p.T, K = p.K, E = p.E, n = T * K, a = tid(), lane = lane_id();
+// a group). A head's number is the count of heads of larger groups plus those of its size at lower assignments: a
+// ballot per size and wave gives both. Only the ids are read here (every work-group reads them, so the fewer lines the
+// better); the combine reads the weights.
+__device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds, GroupTab *tab) {
+  const uint32_t T = p.T, K = p.K, E = p.E, n = T * K, a = tid(), lane = lane_id(), wv = wave_id();
   uint32_t *ids = (uint32_t *)lds, *mask = ids + kMaxDecodeTokens * kMaxUsed, *gnum = mask + kMaxExperts;
+  uint32_t *cnt = gnum + 2 * kMaxExperts;  // [wave][size 1 .. MOE_GROUP_MAX]
   for (uint32_t i = a; i < E; i += kWG) mask[i] = 0u;
   const uint32_t t = a / K;
-  // The last token's last id first, then every id and weight; for a few records (a token or so) every reader polls its
-  // own directly, one round trip less.
+  // The last token's last id first, then every id; for a few records (a token or so) every reader polls its own
+  // directly, one round trip less.
   if (n > 32) wait_tag(p, p.ids_t + n - 1);
-  if (a < n) {  // the routed ids and weights, polled together
-    uint64_t ri, rw;
+  if (a < n) {
+    uint64_t ri;
     for (uint32_t k = 0;; k++) {
-      ri = ld_tag(p.ids_t + a), rw = ld_tag(p.w_t + a);
-      if (tag_of(ri) == p.tag && tag_of(rw) == p.tag) break;
+      ri = ld_tag(p.ids_t + a);
+      if (tag_of(ri) == p.tag) break;
       __builtin_amdgcn_s_sleep(C0VEN_POLL_SLEEP);
       if (k == kSpinLimit) {
         st_co(p.err, 1u);
@@ -447,9 +449,7 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds,
       }
     }
     ids[a] = (uint32_t)ri;
-    tab->w[a] = __uint_as_float((uint32_t)rw);
   }
-  if (p.has_shared && a < T) tab->gs[a] = __uint_as_float(poll_tag(p, p.gs + a));
   __syncthreads();
   if (T == 1) {  // one token: every group is one assignment, in rank order (what the general numbering gives)
     if (a < K) {
@@ -457,7 +457,7 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds,
       tab->n[a] = 1u;
       tab->asg[a][0] = (uint16_t)a;
     }
-    if (a == 0) tab->ng = K, tab->have_w = 1;
+    if (a == 0) tab->ng = K;
     __syncthreads();
     return;
   }
@@ -473,37 +473,32 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds,
     total = __popc(m);
   }
   const bool head = a < n && rank % MOE_GROUP_MAX == 0;
-  const uint64_t heads = __ballot(head);
-  if (lane == 0) hb[wave_id()] = heads;
-  __syncthreads();
-  uint32_t before = 0, G = 0;
+  const uint32_t gn = head ? min((uint32_t)MOE_GROUP_MAX, total - rank) : 0u;
+  uint32_t before = 0;  // heads of this size at lower assignments of this wave
 #pragma unroll
-  for (uint32_t w = 0; w < kWG / 64; w++) {
-    const uint32_t c = (uint32_t)__popcll(hb[w]);
-    before += w < wave_id() ? c : 0u;
-    G += c;
-  }
-  // Groups in order of first assignment get the index o; they are numbered by decreasing size, o breaking ties, so
-  // that the heaviest groups' items come first (work-groups take items in index order).
-  uint32_t *gkey = gnum + 2 * kMaxExperts;
-  uint32_t o = 0, gn = 0;
-  if (head) {
-    o = before + __builtin_amdgcn_mbcnt_hi((uint32_t)(heads >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)heads, 0u));
-    gn = min((uint32_t)MOE_GROUP_MAX, total - rank);
-    gkey[o] = (MOE_GROUP_MAX - gn) * 1024u + o;
+  for (uint32_t sz = 1; sz <= MOE_GROUP_MAX; sz++) {
+    const uint64_t b = __ballot(gn == sz);
+    if (gn == sz) before = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+    if (lane == 0) cnt[wv * MOE_GROUP_MAX + sz - 1] = (uint32_t)__popcll(b);
   }
   __syncthreads();
+  uint32_t g = before, G = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < kWG / 64; w++)
+#pragma unroll
+    for (uint32_t sz = 1; sz <= MOE_GROUP_MAX; sz++) {
+      const uint32_t c = cnt[w * MOE_GROUP_MAX + sz - 1];
+      G += c;
+      g += (sz > gn || (sz == gn && w < wv)) ? c : 0u;
+    }
   if (head) {
-    const uint32_t key = (MOE_GROUP_MAX - gn) * 1024u + o;
-    uint32_t g = 0;
-    for (uint32_t i = 0; i < G; i++) g += gkey[i] < key;
     gnum[2 * e + rank / MOE_GROUP_MAX] = g;
     tab->slot[g] = (int32_t)e;
     tab->n[g] = gn;
   }
   __syncthreads();
   if (a < n) tab->asg[gnum[2 * e + rank / MOE_GROUP_MAX]][rank % MOE_GROUP_MAX] = (uint16_t)a;
-  if (a == 0) tab->ng = G, tab->have_w = 1;
+  if (a == 0) tab->ng = G;
   __syncthreads();
 }
 
@@ -517,7 +512,7 @@ __device__ __forceinline__ void copy_groups(const DecodeParams &p, GroupTab *tab
 #pragma unroll
     for (uint32_t j = 0; j < MOE_GROUP_MAX; j++) tab->asg[g][j] = (uint16_t)m.asg[j];
   }
-  if (tid() == 0) tab->ng = ng, tab->have_w = 0;
+  if (tid() == 0) tab->ng = ng;
   __syncthreads();
 }
 
@@ -556,10 +551,25 @@ __device__ __forceinline__ void read_group(const DecodeParams &p, const GroupTab
 // j act_tok_stride(U) + u kActLds.
 __device__ __forceinline__ void stage_act(const uint8_t *act, const uint32_t *unit_of_j, uint32_t n, uint32_t U,
                                           uint8_t *lds) {
-  for (uint32_t i = tid(); i < n * U * (kActBytes / 16); i += kWG) {
-    const uint32_t unit = i / (kActBytes / 16), c = i % (kActBytes / 16), j = unit / U, u = unit % U;
-    *(uint4 *)(lds + j * act_tok_stride(U) + u * kActLds + 16 * c) =
-        ld_co16(act, (unit_of_j[j] * U + u) * kActBytes + 16 * c);
+  // Eight loads of a thread in flight before their stores (one round trip a batch, not one a chunk).
+  constexpr uint32_t kBatch = 8;
+  const uint32_t total = n * U * (kActBytes / 16);
+  for (uint32_t i0 = 0; i0 < total; i0 += kBatch * kWG) {
+    uint4 v[kBatch];
+#pragma unroll
+    for (uint32_t k = 0; k < kBatch; k++) {
+      const uint32_t i = min(i0 + k * kWG + tid(), total - 1);
+      const uint32_t unit = i / (kActBytes / 16), c = i % (kActBytes / 16), j = unit / U, u = unit % U;
+      v[k] = ld_co16(act, (unit_of_j[j] * U + u) * kActBytes + 16 * c);
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kBatch; k++) {
+      const uint32_t i = i0 + k * kWG + tid();
+      if (i < total) {
+        const uint32_t unit = i / (kActBytes / 16), c = i % (kActBytes / 16), j = unit / U, u = unit % U;
+        *(uint4 *)(lds + j * act_tok_stride(U) + u * kActLds + 16 * c) = v[k];
+      }
+    }
   }
 }
 
@@ -799,24 +809,36 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
 }
 
 // Combine item (token t, rows blk * down_rows ..): y = sum_k w_k y_k in rank order, then + gs s, a row a thread. The
-// per-assignment outputs are polled as tagged records (one first, then all of the row's); the combine items come after
+// token's weights (and, for a pre-routed call, which of its assignments are live) are read once into LDS; the
+// per-assignment outputs are polled as tagged records (one first, then all of the row's). The combine items come after
 // every down item, so what they wait for has a smaller number.
-__device__ __forceinline__ void combine_item(const DecodeParams &p, const GroupTab *tab, uint32_t t, uint32_t blk,
+__device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, uint32_t blk, float *wl,
                                              uint64_t *mark) {
   const uint32_t rows = down_rows(unit_lanes(units_of(p.F))), K = p.K, row = blk * rows + tid();
   const uint32_t ns = p.has_shared ? 1u : 0u;
+  {
+    const uint32_t k = tid();
+    if (k < K) {  // thread k: w_k and whether assignment k is live (a pre-routed call marks a dead one id < 0)
+      const float w = p.route ? __uint_as_float(poll_tag(p, p.w_t + t * K + k)) : ld_co(p.w + t * K + k);
+      const bool on = p.route || ld_co(p.ids + t * K + k) >= 0;
+      wl[k] = w;
+      wl[kMaxUsed + 1 + k] = on ? 1.0f : 0.0f;
+    } else if (k == K && ns) {  // thread K: the shared expert's gate
+      wl[K] = __uint_as_float(poll_tag(p, p.gs + t));
+    }
+  }
   if (p.route) wait_tag(p, p.y_asg + ((uint64_t)t * K + K - 1) * p.H + blk * rows + rows - 1);
+  else __syncthreads();
   if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
   if (tid() < rows) {
     bool on[kMaxUsed];
     float wv[kMaxUsed], yv[kMaxUsed];
 #pragma unroll
     for (uint32_t k = 0; k < kMaxUsed; k++) {
-      on[k] = k < K && (p.route || ld_co(p.ids + t * K + k) >= 0);
-      wv[k] = k >= K ? 0.0f : tab->have_w ? tab->w[t * K + k] : p.route ? __uint_as_float(poll_tag(p, p.w_t + t * K + k))
-                                                                   : ld_co(p.w + t * K + k);
+      on[k] = k < K && wl[kMaxUsed + 1 + k] != 0.0f;
+      wv[k] = k < K ? wl[k] : 0.0f;
     }
-    const float gs = !ns ? 0.0f : tab->have_w ? tab->gs[t] : __uint_as_float(poll_tag(p, p.gs + t));
+    const float gs = ns ? wl[K] : 0.0f;
     // The K (+ shared) outputs of this row: all loads in flight together, polled as a set.
     float ys = 0.0f;
     for (uint32_t n = 0;; n++) {
@@ -858,13 +880,12 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ uint32_t grid_lds[512];
   __shared__ uint32_t s_flag;
-  __shared__ uint64_t s_hb[kWG / 64];
+  __shared__ float s_wl[2 * kMaxUsed + 1];  // a combine item's weights (and gs), then which assignments are live
   __shared__ double s_part[kMaxDecodeTokens * 16], s_tot[kMaxDecodeTokens];
   __shared__ GroupLds sg;
   __shared__ GroupTab gtab;
   __shared__ uint64_t exp_tab[32];  // expf's table, read at LDS latency
   if (tid() < 32) exp_tab[tid()] = kExp2Tab[tid()];
-  if (tid() == 0) gtab.have_w = 0;
   __syncthreads();
   const uint32_t T = p.T, E = p.E, Ug = unit_lanes(units_of(p.H)), Ud = unit_lanes(units_of(p.F));
   const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nL + nTop;
@@ -886,7 +907,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
       if (tid() == 0) grab = __hip_atomic_fetch_add(dyn + list * kDynStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // The routed groups: every work-group builds the table from the ids once they are all in.
       if (p.route) {
-        make_groups(p, lds, s_hb, &gtab);
+        make_groups(p, lds, &gtab);
         if (blockIdx.x == 0 && tid() == 0) st_co(p.ngroups, gtab.ng);
       } else {
         wait_flag(p, kFlagRouted);
@@ -940,7 +961,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
         read_group(p, &gtab, false, i / nD, &sg);
         down_item<kTypes>(p, &sg, i % nD, lds, grid_lds, mark);
       } else {
-        combine_item(p, &gtab, (i - ng * nD) / nBlk, (i - ng * nD) % nBlk, mark);
+        combine_item(p, (i - ng * nD) / nBlk, (i - ng * nD) % nBlk, s_wl, mark);
       }
     }
     if (mark && tid() == 0) mark[3] = __builtin_amdgcn_s_memrealtime();

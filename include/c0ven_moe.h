@@ -179,9 +179,11 @@ MOE_API moe_status moe_kernel_times(moe_ctx *ctx, const char **names, float *avg
 /* Tracing: while on, the decode kernel stamps every work item (s_memrealtime, a 100 MHz clock) when it starts, when
  * what it waits for is in (its operands staged), when its results are computed and stored, and when it ends (after
  * the hand-off work it does as the last of its kind). moe_trace gives the last forward's stamps as (start, ready,
- * computed, end) quadruples in item order, up to cap of them; n receives the number of items, bounds (8 entries, or
- * null) where each kind begins: lead (router rows), top-k, the shared expert's gate/up and down (which run beside
- * the router), the routed gate/up and down, the combine, and the end. Item i ran on work-group i mod moe_grid(ctx). */
+ * computed, end) quadruples in item order, up to cap of them (a cap past n copies the rest of the 65536-quadruple
+ * buffer too); n receives the number of items, bounds (8 entries, or null) where each kind begins: lead (router
+ * rows), top-k, the shared expert's gate/up and down (which run beside the router), the routed gate/up and down, the
+ * combine, and the end. The items before the routed ones ran on work-group i mod moe_grid(ctx); the routed ones are
+ * dealt out dynamically. */
 MOE_API uint32_t moe_grid(const moe_ctx *ctx);
 MOE_API moe_status moe_set_trace(moe_ctx *ctx, int on);
 MOE_API moe_status moe_trace(moe_ctx *ctx, uint64_t *stamps, uint32_t cap, uint32_t *n, uint32_t *bounds);
