@@ -15,9 +15,14 @@ if not os.path.exists(LIB_PATH):
     raise ImportError("c0ven_amd: %s is not built; run __graft_entry__.build()" % LIB_PATH)
 lib = C.CDLL(LIB_PATH)
 
-QT_Q8_0, QT_Q4_K, QT_Q8_K, QT_IQ4_NL, QT_IQ3_S, QT_Q2_0 = 8, 12, 15, 20, 21, 42
-TYPE_NAMES = {QT_Q8_0: "Q8_0", QT_Q4_K: "Q4_K", QT_IQ3_S: "IQ3_S", QT_IQ4_NL: "IQ4_NL", QT_Q2_0: "Q2_0"}
-BLOCK = {QT_Q8_0: (32, 34), QT_Q4_K: (256, 144), QT_IQ3_S: (256, 110), QT_IQ4_NL: (32, 18), QT_Q2_0: (64, 18)}
+QT_Q8_0, QT_Q4_K, QT_Q8_K, QT_IQ3_XXS, QT_IQ4_NL, QT_IQ3_S, QT_IQ2_S, QT_Q2_0 = 8, 12, 15, 18, 20, 21, 22, 42
+TYPE_NAMES = {QT_Q8_0: "Q8_0", QT_Q4_K: "Q4_K", QT_IQ3_S: "IQ3_S", QT_IQ4_NL: "IQ4_NL", QT_Q2_0: "Q2_0",
+              QT_IQ3_XXS: "IQ3_XXS", QT_IQ2_S: "IQ2_S"}
+BLOCK = {QT_Q8_0: (32, 34), QT_Q4_K: (256, 144), QT_IQ3_S: (256, 110), QT_IQ4_NL: (32, 18), QT_Q2_0: (64, 18),
+         QT_IQ3_XXS: (256, 98), QT_IQ2_S: (256, 82)}
+CODEBOOK_TYPES = (QT_IQ3_XXS, QT_IQ2_S)  # decoded through the caller's codebooks (set_codebooks)
+# The codebook buffer's layout (c0ven_quant.h QGRID_*): byte offsets of iq2s_grid, iq3xxs_grid, iq3s_grid, kvalues.
+QGRID_IQ2S, QGRID_IQ3XXS, QGRID_IQ3S, QGRID_KVALUES, QGRID_BYTES = 0, 8192, 9216, 11264, 33808
 Q8_FAMILY = (QT_Q8_0, QT_IQ4_NL, QT_Q2_0)  # the weight types whose dot products take q8_0 activations
 
 MOE_OK, MOE_ERROR, MOE_BAD_ARGUMENT, MOE_BUSY, MOE_TIMEOUT = 0, 1, 2, 3, 4
@@ -92,6 +97,8 @@ _SIGS = {
     "moe_synth_normal": (None, [_u64, _u64, _f32, _P, _u64, C.c_int]),
     "moe_quantize": (_i32, [_u32, _P, _u32, _u32, _P, C.c_int]),
     "moe_synth_matrix": (_i32, [_u64, _u64, _f32, _u32, _u32, _u32, _P, C.c_int]),
+    "moe_set_codebooks": (_i32, [_P, _P, _u64]),
+    "moe_synth_set_codebooks": (_i32, [_P, _u64]),
     "moe_zipf_bias": (None, [_u64, _u32, _f32, _P]),
     "moe_row_bytes": (_u64, [_u32, _u32]),
     "moe_abi_layout": (_u32, [C.POINTER(MoeAbiRow), _u32]),
@@ -139,6 +146,14 @@ def synth_matrix(seed, stream, qtype, rows, cols, sigma=0.02, nthreads=0):
     if st != MOE_OK:
         raise MoeError(st, "moe_synth_matrix")
     return out
+
+
+def synth_set_codebooks(qgrid):
+    """The codebooks (a QGRID-layout uint8 buffer) the IQ3_XXS and IQ2_S quantisers search."""
+    qgrid = np.ascontiguousarray(qgrid, dtype=np.uint8)
+    st = lib.moe_synth_set_codebooks(_ptr(qgrid), qgrid.size)
+    if st != MOE_OK:
+        raise MoeError(st, "moe_synth_set_codebooks")
 
 
 def zipf_bias(seed, n_expert, s=1.1):
@@ -239,6 +254,11 @@ class MoeBlock:
         out = np.empty((rows, cols), dtype=np.float32)
         self._check(lib.moe_dequantize(self.h, qtype, _ptr(blocks), rows, cols, _ptr(out)))
         return out
+
+    def set_codebooks(self, qgrid):
+        """iq2s_grid and iq3xxs_grid from a QGRID-layout uint8 buffer (its IQ3_S region must be ggml's grid)."""
+        qgrid = np.ascontiguousarray(qgrid, dtype=np.uint8)
+        self._check(lib.moe_set_codebooks(self.h, _ptr(qgrid), qgrid.size))
 
     def sync(self):
         self._check(lib.moe_sync(self.h))

@@ -103,15 +103,22 @@ struct DecodeParams {
   uint32_t *err;           // set when a wait gave up (never, unless a work-group could not run)
   uint64_t *trace;         // null, or (start, ready, computed, end) s_memrealtime stamps per work item
   uint32_t trace_cap;
+  const uint8_t *codebooks;  // the caller's codebook buffer (QGRID layout) on the device, or null
 };
 
 // The weight types a launch may meet, as a set (bits below): moe_decode is compiled once per set, so a context whose
 // matrices share one type carries no other type's code (and no register pressure from it). kTypeQ8_0 stands for the
-// 32-value block types that meet q8_0 activations (Q8_0, IQ4_NL, Q2_0): they differ only in how a unit decodes.
-constexpr uint32_t kTypeQ8_0 = 1, kTypeQ4_K = 2, kTypeIQ3_S = 4;
+// 32-value block types that meet q8_0 activations (Q8_0, IQ4_NL, Q2_0), which differ only in how a unit decodes, and
+// kTypeIQ2 for the codebook types (IQ3_XXS, IQ2_S).
+constexpr uint32_t kTypeQ8_0 = 1, kTypeQ4_K = 2, kTypeIQ3_S = 4, kTypeIQ2 = 8;
 constexpr uint32_t type_bit(uint32_t qt) {
-  return (qt == QT_Q8_0 || qt == QT_IQ4_NL || qt == QT_Q2_0) ? kTypeQ8_0 : qt == QT_Q4_K ? kTypeQ4_K : kTypeIQ3_S;
+  return (qt == QT_Q8_0 || qt == QT_IQ4_NL || qt == QT_Q2_0) ? kTypeQ8_0
+         : qt == QT_Q4_K                                     ? kTypeQ4_K
+         : qt == QT_IQ3_S                                    ? kTypeIQ3_S
+                                                             : kTypeIQ2;
 }
+// Words of LDS a grid type's codebook takes (IQ2_S: 1024 entries of two words).
+constexpr uint32_t kGridWords = 2048;
 
 // The activation type (q8_0 for Q8_0 weights, q8_K for the others), fixed at compile time where the set allows.
 template <uint32_t kTypes>
@@ -124,7 +131,7 @@ __device__ __forceinline__ uint32_t act_type(uint32_t runtime) {
 template <uint32_t kTypes>
 __global__ void moe_decode(DecodeParams p);
 
-// The instantiation for a type set (1 .. 7), as a kernel handle for hipLaunchKernel.
+// The instantiation for a type set (1 .. 15), as a kernel handle for hipLaunchKernel.
 const void *decode_kernel(uint32_t types);
 
 }  // namespace c0ven

@@ -16,6 +16,9 @@
 //   Q2_0  (4 blocks of 64, 72 B): qs 4 x 16 B (block p's 16 bytes), then d 1 x 8 B (4 f16).
 //   Q4_K  (144 B):           qs 8 x 16 B (the block's qs bytes 16p..16p+15), scales 3 x 4 B, then d|dmin 1 x 4 B.
 //   IQ3_S (110 B):           qs 4 x 16 B, signs 2 x 16 B, qh 2 x 4 B, scales 1 x 4 B, then d 1 x 2 B.
+//   IQ3_XXS (98 B):          qs 4 x 16 B (grid indices, sub-blocks 2p, 2p+1), scale-and-sign words 2 x 16 B, d 1 x 2 B.
+//   IQ2_S (82 B):            qs 2 x 16 B (index low bits, sub-blocks 4p..4p+3), signs 2 x 16 B, qh 1 x 8 B,
+//                            scales 1 x 8 B, then d 1 x 2 B.
 #pragma once
 
 #include <stdint.h>
@@ -50,7 +53,13 @@ C0VEN_HD uint32_t unit_bytes(uint32_t type) {
          : type == QT_IQ3_S ? 110u
          : type == QT_IQ4_NL ? 144u
          : type == QT_Q2_0  ? 72u
+         : type == QT_IQ3_XXS ? 98u
+         : type == QT_IQ2_S ? 82u
                             : 0u;
+}
+// The 256-value types whose values come from a grid codebook (decoded with the grid in LDS).
+C0VEN_HD constexpr bool grid_family(uint32_t type) {
+  return type == QT_IQ3_S || type == QT_IQ3_XXS || type == QT_IQ2_S;
 }
 // The 32-value block types that meet q8_0 activations (one fp32 term a 32-value block, or half a Q2_0 block).
 C0VEN_HD constexpr bool q8_family(uint32_t type) { return type == QT_Q8_0 || type == QT_IQ4_NL || type == QT_Q2_0; }
@@ -64,6 +73,8 @@ namespace q8_0t { constexpr uint32_t kQs = 0, kD = 16 * 16; }
 namespace q4_kt { constexpr uint32_t kQs = 0, kScales = 8 * 16, kDm = 8 * 16 + 3 * 4; }
 namespace iq4_nlt { constexpr uint32_t kQs = 0, kD = 8 * 16; }
 namespace q2_0t { constexpr uint32_t kQs = 0, kD = 4 * 16; }
+namespace iq3_xxst { constexpr uint32_t kQs = 0, kSs = 4 * 16, kD = 6 * 16; }
+namespace iq2_st { constexpr uint32_t kQs = 0, kSigns = 2 * 16, kQh = 4 * 16, kScales = 4 * 16 + 8, kD = 4 * 16 + 16; }
 namespace iq3_st {
 constexpr uint32_t kQs = 0, kSigns = 4 * 16, kQh = 6 * 16, kScales = 6 * 16 + 2 * 4, kD = 6 * 16 + 3 * 4;
 }

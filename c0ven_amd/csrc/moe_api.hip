@@ -15,6 +15,7 @@
 #include "../../include/c0ven_moe.h"
 #include "aux.h"
 #include "decode.h"
+#include "iq3s_grid.h"
 #include "layout.h"
 #include "prefill.h"
 #include "repack.h"
@@ -198,6 +199,8 @@ struct moe_ctx {
   uint64_t epoch = 0;          // the last launch's number
   std::vector<std::pair<uint64_t *, uint64_t>> tagged;  // the tagged-record buffers (pointer, records)
   uint32_t grid = 0;           // co-resident work-groups of moe_decode
+  uint8_t *codebooks = nullptr;  // the caller's iq2s_grid and iq3xxs_grid (QGRID layout, up to QGRID_IQ3S)
+  bool have_codebooks = false;
   const void *kernel = nullptr;  // moe_decode for the context's set of weight types
   size_t lds = 0;              // its dynamic LDS
   int timing = 0;  // 0 off, 1 every kernel, 2 the decode kernel and the prefill gate/up launches
@@ -268,8 +271,16 @@ void validate(const moe_config &c) {
   require(c.swiglu_limit >= 0.0f, "swiglu_limit must be >= 0");
 }
 
+// Types that decode through the caller's codebooks need them set first.
+void need_codebooks(const moe_ctx *c, std::initializer_list<uint32_t> types) {
+  for (uint32_t t : types)
+    require(!quant_needs_codebook(t) || c->have_codebooks,
+            "IQ3_XXS and IQ2_S weights need ggml's codebooks: call moe_set_codebooks first");
+}
+
 DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   const moe_config &g = c->cfg;
+  need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_down_type : 0u});
   const Layer &L = c->layers[layer];
   DecodeParams p{};
   p.H = g.n_embd, p.F = g.n_ff, p.E = g.n_expert, p.K = g.n_used, p.T = T;
@@ -283,6 +294,7 @@ DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   p.experts = L.experts, p.ex_bytes = c->ex_bytes, p.ex_up_off = c->ex_up, p.ex_down_off = c->ex_down;
   p.shared = L.shared, p.sh_up_off = c->sh_up, p.sh_down_off = c->sh_down;
   p.act_r = c->act_r, p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
+  p.codebooks = c->codebooks;
   p.logits = c->logits, p.ids = c->ids, p.w = c->w, p.gs = c->gs, p.ids_t = c->ids_t, p.w_t = c->w_t;
   p.groups = c->groups, p.ngroups = c->ngroups;
   p.h = c->h, p.y_asg = c->y_asg;
@@ -358,6 +370,8 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
   require(T >= 1 && T <= c->tmax, "ntok must be 1..max_tokens");
   require(c->layers[layer].router != nullptr, "the layer's router is not loaded");
   const uint32_t K = c->cfg.n_used;
+  need_codebooks(c, {c->cfg.gate_type, c->cfg.down_type, c->cfg.has_shared ? c->cfg.sh_gate_type : 0u,
+                     c->cfg.has_shared ? c->cfg.sh_down_type : 0u});
   if (T <= c->tdec) {
     DecodeParams p = base_params(c, layer, T);
     p.x = x, p.y = y;
@@ -369,7 +383,7 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
     PfShape S{g.n_embd, g.n_ff, g.n_expert, K, T, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type,
               g.has_shared, g.swiglu_limit};
     PfLayer PL{L.router, L.has_bias ? L.bias : nullptr, L.experts, c->ex_bytes, c->ex_up, c->ex_down, L.shared,
-               c->sh_up, c->sh_down};
+               c->sh_up, c->sh_down, c->codebooks};
     PfHook hook{c->timing ? timing_hook : nullptr, c};
     check(prefill_forward(S, PL, c->pf, x, y, s, hook), "prefill launch");
     c->last_ids = c->pf.ids, c->last_w = c->pf.w, c->last_pf_T = T;
@@ -511,6 +525,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->cnt_dyn = c->err_flag + kDynStride;  // (a line of its own)
     c->flags = c->alloc<uint64_t>(kFlagCount);
     check(hipMemset(c->flags, 0, kFlagCount * sizeof(uint64_t)), "hipMemset");
+    c->codebooks = c->alloc<uint8_t>(QGRID_IQ3S);
     c->tagged = {{c->logits, (uint64_t)T * (E + 1)}, {c->gs, T}, {c->ids_t, (uint64_t)T * K1}, {c->w_t, (uint64_t)T * K1},
                  {c->h, (uint64_t)A * F}, {c->y_asg, (uint64_t)A * H}, {(uint64_t *)c->cnt_dyn, kDynLists * kDynStride}};  // (and both sets of list counters)
     clear_tagged(c, nullptr);
@@ -715,6 +730,7 @@ MOE_API moe_status moe_compute_many(moe_ctx *c, const moe_cm_job *jobs, uint32_t
     const moe_config &g = c->cfg;
     const uint32_t H = g.n_embd, F = g.n_ff;
     require(x && y && ntok >= 1 && x_stride >= H && y_stride >= H, "bad x, y, ntok or strides");
+    need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_down_type : 0u});
     require(ntok <= c->tdec || (ntok <= c->tmax && c->tmax > c->tdec),
             "ntok must be at most 16, or at most max_tokens when that exceeds 16");
     require(njobs == 0 || jobs, "null jobs");
@@ -795,7 +811,7 @@ MOE_API moe_status moe_compute_many(moe_ctx *c, const moe_cm_job *jobs, uint32_t
       check(hipMemcpyAsync(c->pf.ids, ids.data(), sizeof(int32_t) * ids.size(), hipMemcpyHostToDevice, s), "ids");
       check(hipMemcpyAsync(c->pf.w, w.data(), sizeof(float) * w.size(), hipMemcpyHostToDevice, s), "w");
       PfShape S{H, F, c->bc_slots, K, ntok, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type, 0, g.swiglu_limit};
-      PfLayer PL{nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0};
+      PfLayer PL{nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0, c->codebooks};
       PfHook hook{c->timing ? timing_hook : nullptr, c};
       check(prefill_jobs(S, PL, c->pf, c->x_dev, c->y_dev, s, hook), "prefill launch");
       c->last_ids = c->pf.ids, c->last_w = c->pf.w, c->last_pf_T = ntok;
@@ -1027,6 +1043,7 @@ MOE_API moe_status moe_dequantize(moe_ctx *c, uint32_t type, const uint8_t *bloc
   return guarded(c, [&] {
     require(quant_gpu_supported(type) && blocks && out && rows && cols && cols % quant_block_values(type) == 0,
             "bad dequantize arguments");
+    need_codebooks(c, {type});
     const uint64_t mb = matrix_bytes(type, rows, cols);
     std::vector<uint8_t> buf(mb);
     repack_matrix(type, blocks, rows, cols, buf.data());
@@ -1036,10 +1053,21 @@ MOE_API moe_status moe_dequantize(moe_ctx *c, uint32_t type, const uint8_t *bloc
     check(hipMalloc(&dout.p, (uint64_t)nrt * kTileRows * cols * sizeof(float)), "hipMalloc");
     check(hipMemcpy(dm.p, buf.data(), mb, hipMemcpyHostToDevice), "upload");
     hipLaunchKernelGGL(moe_dequant, dim3(nrt), dim3(64), 0, c->stream, (const uint8_t *)dm.p, type, rows, cols,
-                       (float *)dout.p);
+                       (const uint8_t *)c->codebooks, (float *)dout.p);
     check(hipGetLastError(), "moe_dequant");
     check(hipStreamSynchronize(c->stream), "moe_dequant");
     check(hipMemcpy(out, dout.p, (uint64_t)rows * cols * sizeof(float), hipMemcpyDeviceToHost), "download");
+  });
+}
+
+MOE_API moe_status moe_set_codebooks(moe_ctx *c, const uint8_t *qgrid, uint64_t bytes) {
+  return guarded(c, [&] {
+    require(qgrid != nullptr && bytes >= QGRID_KVALUES, "the codebook buffer must hold QGRID_IQ2S .. QGRID_KVALUES");
+    // The IQ3_S region must be ggml's iq3s_grid (which this build carries): a check that the buffer has the layout.
+    require(std::memcmp(qgrid + QGRID_IQ3S, kIq3sGridHost, sizeof kIq3sGridHost) == 0,
+            "the buffer's IQ3_S region is not ggml's iq3s_grid: not a QGRID-layout codebook buffer");
+    check(hipMemcpy(c->codebooks, qgrid, QGRID_IQ3S, hipMemcpyHostToDevice), "upload codebooks");
+    c->have_codebooks = true;
   });
 }
 

@@ -11,11 +11,17 @@ namespace c0ven {
 __device__ __constant__ static const uint32_t kGridAux[512] = {C0VEN_IQ3S_GRID_VALUES};
 
 // Grid: one work-group of 64 (a wave) per tile; lane l writes row rt * 64 + l, all its units. The values are
-// formed as ggml's dequantize_row_* forms them: Q8_0 d q; Q4_K (d sc) q - (dmin m); IQ3_S (d (1 + 2 s)) (sign grid).
+// formed as ggml's dequantize_row_* forms them: Q8_0 d q; Q4_K (d sc) q - (dmin m); IQ3_S (d (1 + 2 s)) (sign grid);
+// IQ3_XXS and IQ2_S with the grid the caller's codebooks hold.
 __global__ void __launch_bounds__(64) moe_dequant(const uint8_t *mat, uint32_t type, uint32_t rows, uint32_t k,
-                                                  float *out) {
-  __shared__ uint32_t grid[512];
-  for (uint32_t i = threadIdx.x; i < 512; i += 64) grid[i] = kGridAux[i];
+                                                  const uint8_t *codebooks, float *out) {
+  __shared__ uint32_t grid[2048];
+  if (type == QT_IQ3_S) {
+    for (uint32_t i = threadIdx.x; i < 512; i += 64) grid[i] = kGridAux[i];
+  } else if (type == QT_IQ3_XXS || type == QT_IQ2_S) {
+    const uint32_t *src = (const uint32_t *)(codebooks + (type == QT_IQ2_S ? QGRID_IQ2S : QGRID_IQ3XXS));
+    for (uint32_t i = threadIdx.x; i < (type == QT_IQ2_S ? 2048u : 256u); i += 64) grid[i] = src[i];
+  }
   __syncthreads();
   const uint32_t U = units_of(k), rt = blockIdx.x, lane = threadIdx.x, nl = kTileRows * U;
   const uint32_t row = rt * kTileRows + lane;
@@ -46,6 +52,22 @@ __global__ void __launch_bounds__(64) moe_dequant(const uint8_t *mat, uint32_t t
           o[v] = __fsub_rn(__fmul_rn(dl, (float)((w.lo[wd] >> (8 * i)) & 0xff)), ml);
           o[v + 32] = __fsub_rn(__fmul_rn(dh, (float)((w.hi[wd] >> (8 * i)) & 0xff)), mh);
         }
+  } else if (type == QT_IQ3_XXS) {  // (d (0.5 + s)) 0.5, times the signed grid value
+    UnitIQ3_XXS w;
+    w.load(tile, idx, nl, grid);
+    if (live)
+      for (int i = 0; i < 256; i++) {
+        const float db = __fmul_rn(__fmul_rn(w.d, 0.5f + (float)((w.ls[i / 32] - 1) / 2)), 0.5f);
+        o[i] = __fmul_rn(db, (float)(int8_t)(w.w[i / 4] >> (8 * (i % 4))));
+      }
+  } else if (type == QT_IQ2_S) {  // (d (0.5 + s)) 0.25 for each half sub-block, times the signed grid value
+    UnitIQ2_S w;
+    w.load(tile, idx, nl, grid);
+    if (live)
+      for (int i = 0; i < 256; i++) {
+        const float db = __fmul_rn(__fmul_rn(w.d, 0.5f + (float)((w.ls[i / 16] - 1) / 2)), 0.25f);
+        o[i] = __fmul_rn(db, (float)(int8_t)(w.w[i / 4] >> (8 * (i % 4))));
+      }
   } else {
     UnitIQ3_S w;
     w.load(tile, idx, nl, grid);

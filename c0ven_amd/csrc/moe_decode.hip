@@ -218,8 +218,19 @@ __device__ __forceinline__ GroupMat group_mat(const DecodeParams &p, int32_t slo
   return m;
 }
 
-__device__ __forceinline__ void load_grid(uint32_t *grid_lds) {
-  for (uint32_t i = tid(); i < 512; i += kWG) grid_lds[i] = kIq3sGridDev[i];
+// The codebook of a grid type into LDS, unless the work-group's previous item left it there (*have: the type it holds).
+__device__ __forceinline__ void load_grid(const DecodeParams &p, uint32_t type, uint32_t *grid_lds, uint32_t *have) {
+  if (*have == type) return;
+  if (type == QT_IQ3_S) {
+    for (uint32_t i = tid(); i < 512; i += kWG) grid_lds[i] = kIq3sGridDev[i];
+  } else {
+    const uint32_t *src = (const uint32_t *)(p.codebooks + (type == QT_IQ2_S ? QGRID_IQ2S : QGRID_IQ3XXS));
+    const uint32_t n = type == QT_IQ2_S ? 2048u : 256u;
+    for (uint32_t i = tid(); i < n; i += kWG) grid_lds[i] = src[i];
+  }
+  __syncthreads();
+  if (tid() == 0) *have = type;
+  __syncthreads();
 }
 
 // The n terms of one (row, unit) pair against the activation units act + j * stride dwords, into t[j]. The unit's
@@ -256,13 +267,28 @@ __device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, u
       return;
     }
   }
-  if constexpr ((kTypes & kTypeIQ3_S) != 0) {
-    UnitIQ3_S w;
+  const auto run = [&](auto &w) {
     w.load(tile, idx, nl, grid_lds);
     ready();
 #pragma unroll
     for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
       if (j < n) t[j] = w.term(Act(act + j * stride));
+  };
+  if constexpr ((kTypes & kTypeIQ3_S) != 0) {
+    if ((kTypes & ~(kTypeQ8_0 | kTypeQ4_K)) == kTypeIQ3_S || type == QT_IQ3_S) {
+      UnitIQ3_S w;
+      run(w);
+      return;
+    }
+  }
+  if constexpr ((kTypes & kTypeIQ2) != 0) {
+    if (type == QT_IQ3_XXS) {
+      UnitIQ3_XXS w;
+      run(w);
+    } else {
+      UnitIQ2_S w;
+      run(w);
+    }
   }
 }
 
@@ -730,7 +756,8 @@ __device__ __forceinline__ void down_mfma(const DecodeParams &p, const GroupLds 
 // hand their row sums to the gate waves through LDS, which store h = silu(g) * u per row as tagged records.
 template <uint32_t kTypes>
 __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupLds *sg, uint32_t blk, uint8_t *lds,
-                                             uint32_t *grid_lds, const uint64_t *tab, uint64_t *mark) {
+                                             uint32_t *grid_lds, uint32_t *grid_have, const uint64_t *tab,
+                                             uint64_t *mark) {
   // U units a row, UL lanes a row (U rounded up to a power of two; lanes past U add exact zeros).
   const uint32_t U = units_of(p.H), UL = unit_lanes(U), rows = gate_up_rows(UL), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 0);
@@ -738,10 +765,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
     gate_up_mfma(p, sg, gm, blk, lds, (float *)(lds + MOE_GROUP_MAX * act_tok_stride(U)), tab, mark);
     return;
   }
-  if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
-    load_grid(grid_lds);
-    __syncthreads();
-  }
+  if ((kTypes & (kTypeIQ3_S | kTypeIQ2)) && grid_family(gm.type)) load_grid(p, gm.type, grid_lds, grid_have);
   const uint32_t lane = lane_id(), m = wave_id() & 1u, r = lane / UL, u = lane % UL, ue = u < U ? u : 0u;
   const uint32_t rl = (wave_id() >> 1) * (64 / UL) + r, row = row0 + rl;  // rl: the row within the item
   const uint8_t *mat = gm.mat + (m ? (gm.shared ? p.sh_up_off : p.ex_up_off) : 0);
@@ -778,16 +802,13 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
 // Down rows blk * down_rows .. of the group (lane = r * U + u), then the combine of every token this item completes.
 template <uint32_t kTypes>
 __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds *sg, uint32_t blk, uint8_t *lds,
-                                          uint32_t *grid_lds, uint64_t *mark) {
+                                          uint32_t *grid_lds, uint32_t *grid_have, uint64_t *mark) {
   const uint32_t U = units_of(p.F), UL = unit_lanes(U), rows = down_rows(UL), row0 = blk * rows, n = sg->n;
   const GroupMat gm = group_mat(p, sg->slot, 2);
   if (use_mfma<kTypes>(gm.type, U, 2, n) && p.F == 2 * kUnit) {
     down_mfma(p, sg, gm, blk, lds, mark);
   } else {
-    if ((kTypes & kTypeIQ3_S) && gm.type == QT_IQ3_S) {
-      load_grid(grid_lds);
-      __syncthreads();
-    }
+    if ((kTypes & (kTypeIQ3_S | kTypeIQ2)) && grid_family(gm.type)) load_grid(p, gm.type, grid_lds, grid_have);
     const uint32_t lane = lane_id(), r = lane / UL, u = lane % UL, ue = u < U ? u : 0u;
     const uint32_t row = row0 + wave_id() * (64 / UL) + r;
     const uint8_t *tile = gm.mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
@@ -878,7 +899,8 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
 template <uint32_t kTypes>
 __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) moe_decode(DecodeParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ uint32_t grid_lds[512];
+  __shared__ uint32_t grid_lds[(kTypes & kTypeIQ2) ? kGridWords : (kTypes & kTypeIQ3_S) ? 512 : 1];
+  __shared__ uint32_t s_grid;  // the grid type whose codebook grid_lds holds
   __shared__ uint32_t s_flag;
   __shared__ float s_wl[2 * kMaxUsed + 1];  // a combine item's weights (and gs), then which assignments are live
   __shared__ double s_part[kMaxDecodeTokens * 16], s_tot[kMaxDecodeTokens];
@@ -886,6 +908,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   __shared__ GroupTab gtab;
   __shared__ uint64_t exp_tab[32];  // expf's table, read at LDS latency
   if (tid() < 32) exp_tab[tid()] = kExp2Tab[tid()];
+  if (tid() == 0) s_grid = 0xffffffffu;
   __syncthreads();
   const uint32_t T = p.T, E = p.E, Ug = unit_lanes(units_of(p.H)), Ud = unit_lanes(units_of(p.F));
   const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nL + nTop;
@@ -947,19 +970,19 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
       const uint32_t i = it - B1;
       if (i < ns * nGU) {
         read_group(p, &gtab, true, i / nGU, &sg);
-        gate_up_item<kTypes>(p, &sg, i % nGU, lds, grid_lds, exp_tab, mark);
+        gate_up_item<kTypes>(p, &sg, i % nGU, lds, grid_lds, &s_grid, exp_tab, mark);
       } else {
         read_group(p, &gtab, true, (i - ns * nGU) / nD, &sg);
-        down_item<kTypes>(p, &sg, (i - ns * nGU) % nD, lds, grid_lds, mark);
+        down_item<kTypes>(p, &sg, (i - ns * nGU) % nD, lds, grid_lds, &s_grid, mark);
       }
     } else if (it < B2 + ng * nGU) {
       read_group(p, &gtab, false, (it - B2) / nGU, &sg);
-      gate_up_item<kTypes>(p, &sg, (it - B2) % nGU, lds, grid_lds, exp_tab, mark);
+      gate_up_item<kTypes>(p, &sg, (it - B2) % nGU, lds, grid_lds, &s_grid, exp_tab, mark);
     } else {
       const uint32_t i = it - B2 - ng * nGU;
       if (i < ng * nD) {
         read_group(p, &gtab, false, i / nD, &sg);
-        down_item<kTypes>(p, &sg, i % nD, lds, grid_lds, mark);
+        down_item<kTypes>(p, &sg, i % nD, lds, grid_lds, &s_grid, mark);
       } else {
         combine_item(p, (i - ng * nD) / nBlk, (i - ng * nD) % nBlk, s_wl, mark);
       }
@@ -976,6 +999,24 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   }
 }
 
+// The type sets are instantiated in two translation units that build in parallel: this one (sets 1 - 7 and the
+// dispatch) and moe_decode_iq2.hip (the sets with the codebook types, 8 - 15), which includes this file.
+#ifdef C0VEN_DECODE_IQ2_SETS
+#define C0VEN_DECODE_SET(n) template __global__ void moe_decode<n>(DecodeParams);
+#else
+#define C0VEN_DECODE_SET(n) extern template __global__ void moe_decode<n>(DecodeParams);
+#endif
+C0VEN_DECODE_SET(8)
+C0VEN_DECODE_SET(9)
+C0VEN_DECODE_SET(10)
+C0VEN_DECODE_SET(11)
+C0VEN_DECODE_SET(12)
+C0VEN_DECODE_SET(13)
+C0VEN_DECODE_SET(14)
+C0VEN_DECODE_SET(15)
+#undef C0VEN_DECODE_SET
+
+#ifndef C0VEN_DECODE_IQ2_SETS
 template __global__ void moe_decode<1>(DecodeParams);
 template __global__ void moe_decode<2>(DecodeParams);
 template __global__ void moe_decode<3>(DecodeParams);
@@ -992,8 +1033,17 @@ const void *decode_kernel(uint32_t types) {
     case 4: return (const void *)moe_decode<4>;
     case 5: return (const void *)moe_decode<5>;
     case 6: return (const void *)moe_decode<6>;
-    default: return (const void *)moe_decode<7>;
+    case 7: return (const void *)moe_decode<7>;
+    case 8: return (const void *)moe_decode<8>;
+    case 9: return (const void *)moe_decode<9>;
+    case 10: return (const void *)moe_decode<10>;
+    case 11: return (const void *)moe_decode<11>;
+    case 12: return (const void *)moe_decode<12>;
+    case 13: return (const void *)moe_decode<13>;
+    case 14: return (const void *)moe_decode<14>;
+    default: return (const void *)moe_decode<15>;
   }
 }
+#endif
 
 }  // namespace c0ven

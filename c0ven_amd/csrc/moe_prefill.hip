@@ -310,6 +310,7 @@ struct PfGemm {
   float limit;
   uint32_t row_blocks;     // row blocks a tile (the 1-D grid is tiles x row_blocks)
   uint32_t U;              // 256-value units of K (a partial last one padded with zeros)
+  const uint8_t *codebooks;  // the caller's codebooks (QGRID layout) for IQ3_XXS and IQ2_S
 };
 
 // Rows of one grid.y step of the (tiles x row groups) grid the host computes: 64 of gate and of up, or 128 of down.
@@ -380,12 +381,16 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   float(*ub)[65] = reinterpret_cast<float(*)[65]>(&abuf[0][0]);
   __shared__ uint32_t arow_lds[64];
   __shared__ uint64_t tab[32];
-  __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
+  __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : kType == QT_IQ3_XXS ? 256 : kType == QT_IQ2_S ? 2048 : 1];
   using Raw = std::conditional_t<
       kType == QT_IQ3_S, Iq3sRaw,
-      std::conditional_t<kType == QT_Q8_0, Q80Raw,
-                         std::conditional_t<kType == QT_IQ4_NL, Iq4nlRaw,
-                                            std::conditional_t<kType == QT_Q2_0, Q20Raw, Q4kRaw>>>>;
+      std::conditional_t<
+          kType == QT_IQ3_XXS, Iq3xxsRaw,
+          std::conditional_t<
+              kType == QT_IQ2_S, Iq2sRaw,
+              std::conditional_t<kType == QT_Q8_0, Q80Raw,
+                                 std::conditional_t<kType == QT_IQ4_NL, Iq4nlRaw,
+                                                    std::conditional_t<kType == QT_Q2_0, Q20Raw, Q4kRaw>>>>>>;
   // 1-D grid of (tile, row block) pairs, the row block fastest in the XCD-aware logical index over the pairs that
   // exist (the grid is sized for the most tiles a dispatch can make).
   const uint32_t nrb = g.row_blocks;
@@ -408,6 +413,10 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   if (tid < 32) tab[tid] = kExp2Tab[tid];
   if constexpr (kType == QT_IQ3_S)
     for (uint32_t i = tid; i < 512; i += kPfWG) grid_lds[i] = kIq3sGridPf[i];
+  if constexpr (kType == QT_IQ3_XXS || kType == QT_IQ2_S) {
+    const uint32_t *src = (const uint32_t *)(g.codebooks + (kType == QT_IQ2_S ? QGRID_IQ2S : QGRID_IQ3XXS));
+    for (uint32_t i = tid; i < (kType == QT_IQ2_S ? 2048u : 256u); i += kPfWG) grid_lds[i] = src[i];
+  }
   if (tid < 64) {
     const uint32_t pos = start + tid;
     arow_lds[tid] = tid < count ? (g.act_by_pos ? pos : (g.perm ? g.perm[pos] / g.K : pos)) : 0xffffffffu;
@@ -437,9 +446,11 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
       next.load(M, U, row0, u + 1, lane_id());
     }
     const uint8_t *buf = abuf[u & 1];
-    if constexpr (kType == QT_IQ3_S) {
-      // Block by block: one MFMA a position tile, its D times the row's block scale added to the unit's integer sum
-      // in block order; then d ad isum as UnitIQ3_S::term.
+    if constexpr (grid_family(kType)) {
+      // Block by block: one MFMA a position tile (IQ2_S: one a half block, the other half's A lanes zero), its D
+      // times the row's block scale added to the unit's integer sum in block order; then kFactor ((d ad) isum) as
+      // UnitIQ3_S / UnitIQ3_XXS / UnitIQ2_S::term.
+      raw.prep(lane_id());
       int isum[4][4];
 #pragma unroll
       for (int pt = 0; pt < 4; pt++)
@@ -449,16 +460,34 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
       for (uint32_t ib = 0; ib < 8; ib++) {
         const uint32_t bofs = mfma_code_off(4 * ib + lane_id() / 16);  // the lane's 8 codes of block ib
         const long aw = raw.a_block(ib, lane_id(), grid_lds);
-        int ls[4];
+        if constexpr (kType == QT_IQ2_S) {
+          const bool lo = lane_id() < 32;
+          const long a0 = lo ? aw : 0, a1 = lo ? 0 : aw;
+          int l0[4], l1[4];
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) ls[i] = raw.ls(i, ib);
+          for (uint32_t i = 0; i < 4; i++) l0[i] = raw.ls(i, ib, 0), l1[i] = raw.ls(i, ib, 1);
 #pragma unroll
-        for (uint32_t pt = 0; pt < 4; pt++) {
-          if (pt < npt) {
-            const long bw = *(const long *)(buf + (16 * pt + lane_id() % 16) * kActLds + bofs);
-            const v4i_t dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+          for (uint32_t pt = 0; pt < 4; pt++) {
+            if (pt < npt) {
+              const long bw = *(const long *)(buf + (16 * pt + lane_id() % 16) * kActLds + bofs);
+              const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+              const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; i++) isum[pt][i] += ls[i] * dv[i];
+              for (int i = 0; i < 4; i++) isum[pt][i] += l0[i] * d0[i] + l1[i] * d1[i];
+            }
+          }
+        } else {
+          int ls[4];
+#pragma unroll
+          for (uint32_t i = 0; i < 4; i++) ls[i] = raw.ls(i, ib);
+#pragma unroll
+          for (uint32_t pt = 0; pt < 4; pt++) {
+            if (pt < npt) {
+              const long bw = *(const long *)(buf + (16 * pt + lane_id() % 16) * kActLds + bofs);
+              const v4i_t dv = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+              for (int i = 0; i < 4; i++) isum[pt][i] += ls[i] * dv[i];
+            }
           }
         }
         __builtin_amdgcn_sched_barrier(0);  // one block's operands live at a time
@@ -468,8 +497,11 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
         if (pt < npt) {
           const float ad = *(const float *)(buf + (16 * pt + lane_id() % 16) * kActLds + kActScales);
 #pragma unroll
-          for (int i = 0; i < 4; i++)
-            acc[pt][i] = __fadd_rn(acc[pt][i], __fmul_rn(__fmul_rn(h2f((uint16_t)raw.dh[i]), ad), (float)isum[pt][i]));
+          for (int i = 0; i < 4; i++) {
+            float t = __fmul_rn(__fmul_rn(h2f((uint16_t)raw.dh[i]), ad), (float)isum[pt][i]);
+            if constexpr (Raw::kFactor != 1.0f) t = __fmul_rn(Raw::kFactor, t);
+            acc[pt][i] = __fadd_rn(acc[pt][i], t);
+          }
         }
       }
     } else if constexpr (q8_family(kType)) {
@@ -716,6 +748,8 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2
 
 // Positions a gate/up work-group takes for a weight type (the kernel's kPos).
 constexpr uint32_t gu_pos(uint32_t) { return MOE_TILE; }
+// The gate/up types that run on pf_gate_up (gate and up of a row in one wave); the others on pf_gemm16.
+constexpr bool gu_fused(uint32_t type) { return type == QT_Q4_K || type == QT_IQ3_S; }
 
 // ---------------------------------------------------------------------------------------------------------------
 // Combine: y[t][r] = sum_k w[t][k] y_asg[inv[t K + k]][r] in rank order (ranks with a negative id skipped), then
@@ -752,7 +786,7 @@ template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
   PfGemm q = g;
   q.U = U;
-  if (kGU && !q8_family(type)) {  // gate and up in one wave: grid.x tiles x grid.y row blocks of gu_pos rows
+  if (kGU && gu_fused(type)) {  // gate and up in one wave: grid.x tiles x grid.y row blocks of gu_pos rows
     q.row_blocks = grid.y;
     const dim3 g2(grid.x * q.row_blocks), wg(4 * MOE_TILE);
     if (type == QT_Q4_K)
@@ -770,6 +804,10 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
     pf_gemm16<QT_IQ3_S, kGU><<<g2, kPfWG, 0, s>>>(q);
   else if (type == QT_IQ4_NL)
     pf_gemm16<QT_IQ4_NL, kGU><<<g2, kPfWG, 0, s>>>(q);
+  else if (type == QT_IQ3_XXS)
+    pf_gemm16<QT_IQ3_XXS, kGU><<<g2, kPfWG, 0, s>>>(q);
+  else if (type == QT_IQ2_S)
+    pf_gemm16<QT_IQ2_S, kGU><<<g2, kPfWG, 0, s>>>(q);
   else if (type == QT_Q2_0)
     pf_gemm16<QT_Q2_0, kGU><<<g2, kPfWG, 0, s>>>(q);
   else
@@ -793,7 +831,7 @@ struct HookScope {
 // rows of each a work-group).
 void launch_gate_up(uint32_t type, const PfGemm &q, uint32_t T, uint32_t F, uint32_t Ug, uint32_t nx, hipStream_t s) {
   (void)T;
-  const uint32_t ny = q8_family(type) ? F / gemm_rows<true>() : F / gu_pos(type);
+  const uint32_t ny = gu_fused(type) ? F / gu_pos(type) : F / gemm_rows<true>();
   launch_gemm<true>(type, Ug, dim3(nx, ny), q, s);
 }
 
@@ -816,6 +854,7 @@ hipError_t routed_experts(const PfShape &S, const PfLayer &L, const PfBufs &b, h
     PfGemm g{};
     g.tiles = b.tiles, g.ntiles = b.ntiles, g.perm = b.perm, g.K = K, g.act = b.act_r, g.act_by_pos = 0;
     g.mat = L.experts, g.stride = L.ex_bytes, g.up_off = L.ex_up_off, g.out = b.h, g.out_ld = F;
+    g.codebooks = L.codebooks;
     g.limit = S.swiglu_limit;
     launch_gate_up(S.gate_type, g, T, F, Ug, mt, st);
   }
@@ -829,6 +868,7 @@ hipError_t routed_experts(const PfShape &S, const PfLayer &L, const PfBufs &b, h
     PfGemm g{};
     g.tiles = b.tiles, g.ntiles = b.ntiles, g.K = K, g.act = b.hact, g.act_by_pos = 1;
     g.mat = L.experts + L.ex_down_off, g.stride = L.ex_bytes, g.out = b.y_asg, g.out_ld = H;
+    g.codebooks = L.codebooks;
     launch_gemm<false>(S.down_type, Ud, dim3(mt, H / gemm_rows<false>()), g, st);
   }
   return hipGetLastError();
@@ -858,6 +898,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
       PfGemm q{};
       q.shared_T = T, q.K = K, q.act = b.act_s, q.act_by_pos = 0;
       q.mat = L.shared, q.stride = 0, q.up_off = L.sh_up_off, q.out = b.h_sh, q.out_ld = F;
+      q.codebooks = L.codebooks;
       q.limit = S.swiglu_limit;
       launch_gate_up(S.sh_gate_type, q, T, F, Ug, (T + gu_pos(S.sh_gate_type) - 1) / gu_pos(S.sh_gate_type), ss);
     }
@@ -871,6 +912,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
       PfGemm q{};
       q.shared_T = T, q.K = K, q.act = b.hact_sh, q.act_by_pos = 1;
       q.mat = L.shared + L.sh_down_off, q.stride = 0, q.out = b.y_sh, q.out_ld = H;
+      q.codebooks = L.codebooks;
       launch_gemm<false>(S.sh_down_type, Ud, dim3(st_tiles, H / gemm_rows<false>()), q, ss);
     }
     if (hipEventRecord(b.join, ss) != hipSuccess) return hipGetLastError();

@@ -38,6 +38,7 @@ struct PfLayer {
   uint64_t ex_bytes, ex_up_off, ex_down_off;
   const uint8_t *shared;
   uint64_t sh_up_off, sh_down_off;
+  const uint8_t *codebooks;  // the caller's codebooks (QGRID layout) for IQ3_XXS and IQ2_S
 };
 
 // Scratch for up to Tmax tokens (allocated at open).

@@ -9,7 +9,7 @@
 namespace c0ven {
 
 // Row r's unit u in the file's layout: the bytes of its blocks (Q8_0: 8 blocks of 34 B; IQ4_NL: 8 of 18 B; Q2_0: 4
-// of 18 B; Q4_K, IQ3_S: one block).
+// of 18 B; Q4_K, IQ3_S, IQ3_XXS, IQ2_S: one block).
 inline const uint8_t *file_unit(const uint8_t *m, uint32_t type, uint32_t k, uint32_t r, uint32_t u) {
   const uint64_t row = (uint64_t)k / quant_block_values(type) * quant_block_bytes(type);
   return m + r * row + (uint64_t)u * unit_bytes(type);
@@ -35,6 +35,18 @@ inline void put_unit(uint8_t *tile, uint32_t type, uint32_t idx, uint32_t nl, co
     case QT_Q2_0:
       for (uint32_t p = 0; p < 4; p++) std::memcpy(at(q2_0t::kQs, p, 16), b + 18 * p + 2, 16);
       for (uint32_t blk = 0; blk < 4; blk++) std::memcpy(at(q2_0t::kD, 0, 8) + 2 * blk, b + 18 * blk, 2);
+      break;
+    case QT_IQ3_XXS:
+      for (uint32_t p = 0; p < 4; p++) std::memcpy(at(iq3_xxst::kQs, p, 16), b + 2 + 16 * p, 16);
+      for (uint32_t p = 0; p < 2; p++) std::memcpy(at(iq3_xxst::kSs, p, 16), b + 66 + 16 * p, 16);
+      std::memcpy(at(iq3_xxst::kD, 0, 2), b, 2);
+      break;
+    case QT_IQ2_S:
+      for (uint32_t p = 0; p < 2; p++) std::memcpy(at(iq2_st::kQs, p, 16), b + 2 + 16 * p, 16);
+      for (uint32_t p = 0; p < 2; p++) std::memcpy(at(iq2_st::kSigns, p, 16), b + 34 + 16 * p, 16);
+      std::memcpy(at(iq2_st::kQh, 0, 8), b + 66, 8);
+      std::memcpy(at(iq2_st::kScales, 0, 8), b + 74, 8);
+      std::memcpy(at(iq2_st::kD, 0, 2), b, 2);
       break;
     case QT_IQ3_S:
       for (uint32_t p = 0; p < 4; p++) std::memcpy(at(iq3_st::kQs, p, 16), b + 2 + 16 * p, 16);

@@ -186,6 +186,141 @@ void quant_iq3_s(const float *x, uint8_t *y, uint32_t n) {
   }
 }
 
+// The caller's iq2s_grid and iq3xxs_grid (moe_synth_set_codebooks), and for each point of their magnitude-level
+// lattices (IQ3_XXS: 8 levels 4, 12, .., 52, 62 for 4 values; IQ2_S: 3 levels 8, 25, 43 for 8 values) the nearest
+// entry (squared distance, ties to the lower entry).
+struct CodebookMaps {
+  std::vector<uint64_t> iq2s;
+  std::vector<uint32_t> iq3xxs;
+  std::vector<uint16_t> near2, near3;
+};
+std::mutex g_cb_mu;
+CodebookMaps *g_cb = nullptr;  // set once per call of moe_synth_set_codebooks; kept until the process ends
+
+constexpr int kIq3xxsLevel[8] = {4, 12, 20, 28, 36, 44, 52, 62};
+constexpr int kIq2sLevel[3] = {8, 25, 43};
+
+CodebookMaps *make_maps(const uint8_t *qgrid) {
+  auto *m = new CodebookMaps;
+  m->iq2s.resize(1024);
+  m->iq3xxs.resize(256);
+  std::memcpy(m->iq2s.data(), qgrid + QGRID_IQ2S, 8192);
+  std::memcpy(m->iq3xxs.data(), qgrid + QGRID_IQ3XXS, 1024);
+  m->near3.resize(4096);
+  for (uint32_t c = 0; c < 4096; c++) {
+    int best = 0, bd = 1 << 30;
+    for (int g = 0; g < 256; g++) {
+      int dd = 0;
+      for (int j = 0; j < 4; j++) {
+        const int a = kIq3xxsLevel[(c >> (3 * j)) & 7], v = (int)((m->iq3xxs[g] >> (8 * j)) & 0xff);
+        dd += (a - v) * (a - v);
+      }
+      if (dd < bd) bd = dd, best = g;
+    }
+    m->near3[c] = (uint16_t)best;
+  }
+  m->near2.resize(6561);
+  for (uint32_t c = 0; c < 6561; c++) {
+    int best = 0, bd = 1 << 30;
+    for (int g = 0; g < 1024; g++) {
+      int dd = 0;
+      uint32_t r = c;
+      for (int j = 0; j < 8; j++, r /= 3) {
+        const int a = kIq2sLevel[r % 3], v = (int)((m->iq2s[g] >> (8 * j)) & 0xff);
+        dd += (a - v) * (a - v);
+      }
+      if (dd < bd) bd = dd, best = g;
+    }
+    m->near2[c] = (uint16_t)best;
+  }
+  return m;
+}
+
+// IQ3_XXS: per sub-block of 32 a step amax / 62 as d (2 s + 1) / 4, d = the largest step 4 / 31; each group of four
+// magnitudes to the nearest levels, then to the nearest grid entry; in each sign group of eight the sign of the
+// smallest magnitude flipped where needed to make the count of negatives even (the eighth sign is implied).
+void quant_iq3_xxs(const float *x, uint8_t *y, uint32_t n) {
+  const CodebookMaps &cb = *g_cb;
+  for (uint32_t b = 0; b < n / 256; b++, x += 256, y += 98) {
+    std::memset(y, 0, 98);
+    float step[8];
+    for (int j = 0; j < 8; j++) {
+      float a = 0.0f;
+      for (int i = 0; i < 32; i++) a = std::max(a, std::fabs(x[32 * j + i]));
+      step[j] = a / 62.0f;
+    }
+    const float smax = *std::max_element(step, step + 8);
+    const uint16_t dh = fp16_bits(smax * 4.0f / 31.0f);
+    const float d = fp16_value(dh);
+    std::memcpy(y, &dh, 2);
+    if (d <= 0.0f) continue;
+    for (int ib = 0; ib < 8; ib++) {
+      const int s = std::clamp(nearest((step[ib] * 4.0f / d - 1.0f) / 2.0f), 0, 15);
+      const float db = d * (float)(2 * s + 1) / 4.0f;
+      uint32_t word = (uint32_t)s << 28;
+      for (int l = 0; l < 4; l++) {
+        const float *v = x + 32 * ib + 8 * l;
+        uint32_t sb = 0;
+        int small = 0;
+        for (int j = 0; j < 8; j++) {
+          if (v[j] < 0.0f) sb |= 1u << j;
+          if (std::fabs(v[j]) < std::fabs(v[small])) small = j;
+        }
+        if (__builtin_popcount(sb) & 1) sb ^= 1u << small;
+        word |= (sb & 127u) << (7 * l);
+        for (int h = 0; h < 2; h++) {
+          uint32_t code = 0;
+          for (int j = 0; j < 4; j++)
+            code |= (uint32_t)std::clamp(nearest((std::fabs(v[4 * h + j]) / db - 4.0f) / 8.0f), 0, 7) << (3 * j);
+          y[2 + 8 * ib + 2 * l + h] = (uint8_t)cb.near3[code];
+        }
+      }
+      std::memcpy(y + 66 + 4 * ib, &word, 4);
+    }
+  }
+}
+
+// IQ2_S: per half sub-block of 16 a step amax / 43 as d (2 s + 1) / 8, d = the largest step 8 / 31; each group of
+// eight magnitudes to the nearest levels, then to the nearest grid entry; the signs stored plainly.
+void quant_iq2_s(const float *x, uint8_t *y, uint32_t n) {
+  const CodebookMaps &cb = *g_cb;
+  for (uint32_t b = 0; b < n / 256; b++, x += 256, y += 82) {
+    std::memset(y, 0, 82);
+    float step[16];
+    for (int h = 0; h < 16; h++) {
+      float a = 0.0f;
+      for (int i = 0; i < 16; i++) a = std::max(a, std::fabs(x[16 * h + i]));
+      step[h] = a / 43.0f;
+    }
+    const float smax = *std::max_element(step, step + 16);
+    const uint16_t dh = fp16_bits(smax * 8.0f / 31.0f);
+    const float d = fp16_value(dh);
+    std::memcpy(y, &dh, 2);
+    if (d <= 0.0f) continue;
+    for (int h = 0; h < 16; h++) {
+      const int s = std::clamp(nearest((step[h] * 8.0f / d - 1.0f) / 2.0f), 0, 15);
+      y[74 + h / 2] |= (uint8_t)(s << (4 * (h % 2)));
+      const float db = d * (float)(2 * s + 1) / 8.0f;
+      for (int g2 = 0; g2 < 2; g2++) {  // the half's two groups of eight: group g = 2 (h % 2) + g2 of sub-block h / 2
+        const int ib = h / 2, g = 2 * (h % 2) + g2;
+        const float *v = x + 32 * ib + 8 * g;
+        uint32_t code = 0, mul = 1;
+        uint8_t sb = 0;
+        for (int j = 0; j < 8; j++, mul *= 3) {
+          const float a = std::fabs(v[j]) / db;
+          const int l = a < 16.5f ? 0 : a < 34.0f ? 1 : 2;
+          code += (uint32_t)l * mul;
+          if (v[j] < 0.0f) sb |= (uint8_t)(1u << j);
+        }
+        const uint32_t idx = cb.near2[code];
+        y[2 + 4 * ib + g] = (uint8_t)(idx & 0xff);
+        y[66 + ib] |= (uint8_t)(((idx >> 8) & 3u) << (2 * g));
+        y[34 + 4 * ib + g] = sb;
+      }
+    }
+  }
+}
+
 // IQ4_NL (block_iq4_nl): per block of 32 the value of largest magnitude m, d = m / -127 (kvalues_iq4nl's first
 // entry), each value the nearest table entry of x / d. Simpler than ggml's scale search; any d and codes are a valid
 // block, and the tests read the blocks the same way on both sides.
@@ -226,9 +361,13 @@ void quant_q2_0(const float *x, uint8_t *y, uint32_t n) {
   }
 }
 
-// Whether a row of cols values is whole blocks of a GPU type.
+// Whether a row of cols values is whole blocks of a GPU type (and, for the codebook types, the codebooks are set).
 bool cols_ok(uint32_t type, uint32_t cols) {
   const uint32_t bv = quant_block_values(type);
+  if (quant_needs_codebook(type)) {
+    std::lock_guard<std::mutex> g(g_cb_mu);
+    if (!g_cb) return false;
+  }
   return quant_gpu_supported(type) && bv && cols % bv == 0 && cols > 0;
 }
 
@@ -239,6 +378,8 @@ bool quant_rows(uint32_t type, const float *x, uint32_t cols, uint8_t *out) {
     case QT_IQ3_S: quant_iq3_s(x, out, cols); return true;
     case QT_IQ4_NL: quant_iq4_nl(x, out, cols); return true;
     case QT_Q2_0: quant_q2_0(x, out, cols); return true;
+    case QT_IQ3_XXS: quant_iq3_xxs(x, out, cols); return true;
+    case QT_IQ2_S: quant_iq2_s(x, out, cols); return true;
     default: return false;
   }
 }
@@ -253,6 +394,14 @@ extern "C" {
 MOE_API uint64_t moe_row_bytes(uint32_t type, uint32_t cols) {
   const uint32_t bv = quant_block_values(type);
   return bv ? (uint64_t)cols / bv * quant_block_bytes(type) : 0;
+}
+
+MOE_API moe_status moe_synth_set_codebooks(const uint8_t *qgrid, uint64_t bytes) {
+  if (!qgrid || bytes < QGRID_IQ3S) return MOE_BAD_ARGUMENT;
+  CodebookMaps *m = make_maps(qgrid);
+  std::lock_guard<std::mutex> g(g_cb_mu);
+  g_cb = m;  // an earlier set stays allocated: a quantiser running on another thread may still read it
+  return MOE_OK;
 }
 
 MOE_API void moe_synth_normal(uint64_t seed, uint64_t stream, float sigma, float *out, uint64_t n, int nthreads) {

@@ -39,6 +39,12 @@ __device__ __forceinline__ const T *field(const uint8_t *tile, uint32_t base, ui
   return (const T *)(tile + (uint64_t)base * nl) + (uint64_t)p * nl + idx;
 }
 
+// Bytes of g (each at least 1) negated where the matching bit of the four-bit nibble is set, without carries.
+__device__ __forceinline__ uint32_t sign4(uint32_t g, uint32_t nib) {
+  const uint32_t x = (nib * 0x00204081u) & 0x01010101u;  // byte j = bit j of the nibble
+  return (g ^ ((x << 8) - x)) + x;
+}
+
 // Q8_0: eight blocks of 32 (vec_dot_q8_0_q8_0). Term: the pairwise sum of (d_w d_a) sumi over the eight blocks.
 struct UnitQ8_0 {
   uint32_t q[64];
@@ -161,9 +167,7 @@ struct UnitIQ3_S {
     for (int k = 0; k < 64; k++) {
       const uint32_t ix = ((qs[k / 4] >> (8 * (k % 4))) & 0xffu) | (((qh[k / 32] >> (k % 32)) & 1u) << 8);
       const uint32_t g = grid[ix];
-      const uint32_t nib = (sg[k / 8] >> (4 * (k % 8))) & 15u;
-      const uint32_t x = (nib * 0x00204081u) & 0x01010101u;  // byte j = bit j of the nibble
-      w[k] = (g ^ ((x << 8) - x)) + x;                       // bytes with the bit set negated, no carries
+      w[k] = sign4(g, (sg[k / 8] >> (4 * (k % 8))) & 15u);
     }
   }
   __device__ __forceinline__ float term(const Act &a) const {
@@ -178,6 +182,96 @@ struct UnitIQ3_S {
       bsum += ls[ib] * s;
     }
     return __fmul_rn(__fmul_rn(d, a.scale0()), (float)bsum);
+  }
+};
+
+// IQ3_XXS: eight sub-blocks of 32, each eight grid groups of 4 (iq3xxs_grid, 256 entries in LDS) with signs in fours
+// of seven bits, the eighth the parity (multirow.cpp:126-176, vec_dot_iq3_xxs_q8_K). Term: 0.25 ((d_w d_a) isum),
+// isum = sum over sub-blocks of (2 s + 1) times the sub-block's exact dot; the factor 0.25 is a power of two.
+struct UnitIQ3_XXS {
+  uint32_t w[64];  // group k's four values 4k..4k+3, signed
+  int ls[8];
+  float d;
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl, const uint32_t *grid) {
+    uint32_t qs[16], ss[8];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const uint4 v = *field<uint4>(tile, iq3_xxst::kQs, p, idx, nl);
+      qs[4 * p] = v.x, qs[4 * p + 1] = v.y, qs[4 * p + 2] = v.z, qs[4 * p + 3] = v.w;
+    }
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const uint4 v = *field<uint4>(tile, iq3_xxst::kSs, p, idx, nl);
+      ss[4 * p] = v.x, ss[4 * p + 1] = v.y, ss[4 * p + 2] = v.z, ss[4 * p + 3] = v.w;
+    }
+    d = h2f(*field<uint16_t>(tile, iq3_xxst::kD, 0, idx, nl));
+#pragma unroll
+    for (int b = 0; b < 8; b++) ls[b] = 2 * (int)(ss[b] >> 28) + 1;
+#pragma unroll
+    for (int k = 0; k < 64; k++) {  // group k: sub-block k / 8, sign group (k % 8) / 2, its half k % 2
+      const uint32_t s7 = (ss[k / 8] >> (7 * ((k % 8) / 2))) & 127u;
+      const uint32_t sb = s7 | ((uint32_t)(__popc(s7) & 1) << 7);
+      w[k] = sign4(grid[(qs[k / 4] >> (8 * (k % 4))) & 0xffu], (sb >> (4 * (k % 2))) & 15u);
+    }
+  }
+  __device__ __forceinline__ float term(const Act &a) const {
+    int bsum = 0;
+#pragma unroll
+    for (int ib = 0; ib < 8; ib++) {
+      uint32_t aw[8];
+      a.q8(ib, aw);
+      int s = 0;
+#pragma unroll
+      for (int k = 0; k < 8; k++) s = dot4(w[8 * ib + k], aw[k], s);
+      bsum += ls[ib] * s;
+    }
+    return __fmul_rn(0.25f, __fmul_rn(__fmul_rn(d, a.scale0()), (float)bsum));
+  }
+};
+
+// IQ2_S: eight sub-blocks of 32, each four groups of 8 values from iq2s_grid (1024 entries of 8 bytes, in LDS as
+// word pairs) with a 10-bit index and 8 sign bits; a 4-bit scale for each half sub-block (multirow.cpp:68-124,
+// vec_dot_iq2_s_q8_K). Term: 0.125 ((d_w d_a) isum), isum = sum over half sub-blocks of (2 s + 1) times the exact dot.
+struct UnitIQ2_S {
+  uint32_t w[64];  // values 4k..4k+3, signed
+  int ls[16];      // half sub-block h: values 16 h .. 16 h + 15
+  float d;
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl, const uint32_t *grid) {
+    uint32_t qs[8], sg[8];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const uint4 v = *field<uint4>(tile, iq2_st::kQs, p, idx, nl), u = *field<uint4>(tile, iq2_st::kSigns, p, idx, nl);
+      qs[4 * p] = v.x, qs[4 * p + 1] = v.y, qs[4 * p + 2] = v.z, qs[4 * p + 3] = v.w;
+      sg[4 * p] = u.x, sg[4 * p + 1] = u.y, sg[4 * p + 2] = u.z, sg[4 * p + 3] = u.w;
+    }
+    const uint2 qh = *field<uint2>(tile, iq2_st::kQh, 0, idx, nl), sc = *field<uint2>(tile, iq2_st::kScales, 0, idx, nl);
+    d = h2f(*field<uint16_t>(tile, iq2_st::kD, 0, idx, nl));
+#pragma unroll
+    for (int h = 0; h < 16; h++) ls[h] = 2 * (int)((((h < 8) ? sc.x : sc.y) >> (4 * (h % 8))) & 15u) + 1;
+#pragma unroll
+    for (int gi = 0; gi < 32; gi++) {  // group gi = 4 b + g: sub-block b, values 8 g .. 8 g + 7 of it
+      const uint32_t b = gi / 4, g = gi % 4;
+      const uint32_t hbits = (((b < 4) ? qh.x : qh.y) >> (8 * (b % 4) + 2 * g)) & 3u;
+      const uint32_t ix = ((qs[gi / 4] >> (8 * (gi % 4))) & 0xffu) | (hbits << 8);
+      const uint32_t sb = (sg[gi / 4] >> (8 * (gi % 4))) & 0xffu;
+      w[2 * gi] = sign4(grid[2 * ix], sb & 15u);
+      w[2 * gi + 1] = sign4(grid[2 * ix + 1], sb >> 4);
+    }
+  }
+  __device__ __forceinline__ float term(const Act &a) const {
+    int isum = 0;
+#pragma unroll
+    for (int ib = 0; ib < 8; ib++) {
+      uint32_t aw[8];
+      a.q8(ib, aw);
+      int s0 = 0, s1 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) s0 = dot4(w[8 * ib + k], aw[k], s0);
+#pragma unroll
+      for (int k = 4; k < 8; k++) s1 = dot4(w[8 * ib + k], aw[k], s1);
+      isum += ls[2 * ib] * s0 + ls[2 * ib + 1] * s1;
+    }
+    return __fmul_rn(0.125f, __fmul_rn(__fmul_rn(d, a.scale0()), (float)isum));
   }
 };
 

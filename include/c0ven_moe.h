@@ -48,11 +48,12 @@ typedef struct moe_ctx moe_ctx;
  * docs/spec/MODEL_LAYER.md section 4). Zero means the default given here. */
 typedef struct {
   uint32_t n_embd;       /* H: K of gate and up, rows of down; a multiple of 512 */
-  uint32_t n_ff;         /* F: rows of gate and up, K of down; a multiple of 256 */
+  uint32_t n_ff;         /* F: rows of gate and up, K of down; a multiple of 64 and of down's block */
   uint32_t n_expert;     /* E routed experts, at most 512 */
   uint32_t n_used;       /* k, at most 16 */
   uint32_t n_layer;      /* layers held resident (default 1) */
-  uint32_t gate_type;    /* QT_Q8_0, QT_Q4_K or QT_IQ3_S: gate and up of the routed experts */
+  uint32_t gate_type;    /* QT_Q8_0, QT_Q4_K, QT_IQ3_S, QT_IQ4_NL, QT_Q2_0, QT_IQ3_XXS or QT_IQ2_S: gate and up of
+                          * the routed experts (the last two need moe_set_codebooks) */
   uint32_t down_type;    /* the same set: down of the routed experts */
   uint32_t has_shared;   /* 1: one shared expert with a sigmoid gate (the router's row E) */
   uint32_t sh_gate_type; /* the shared expert's types */
@@ -202,11 +203,23 @@ MOE_API uint64_t moe_device_bytes(const moe_ctx *ctx);
 MOE_API moe_status moe_dequantize(moe_ctx *ctx, uint32_t type, const uint8_t *blocks, uint32_t rows, uint32_t cols,
                                   float *out);
 
+/* The codebooks IQ3_XXS and IQ2_S decode through: a buffer in the QGRID layout of c0ven_quant.h, as the reference
+ * packs ggml-common.h's tables (core/load/codebooks.cpp:14-33), at least QGRID_KVALUES bytes. iq2s_grid and
+ * iq3xxs_grid are taken from it (this build does not carry them); its IQ3_S region must equal ggml's iq3s_grid, the
+ * check that the buffer has the layout. A context whose types include IQ3_XXS or IQ2_S refuses forwards and
+ * moe_dequantize of those types until this is called. No counterpart call in the reference, whose kernels receive the
+ * same buffer at load time. */
+MOE_API moe_status moe_set_codebooks(moe_ctx *ctx, const uint8_t *qgrid, uint64_t bytes);
+
 /* Synthetic inputs (seeded, so that every machine draws the same values): counter-based normals, the library's
  * quantisers, the Zipf logit bias of BASELINE's configs. nthreads <= 0: all cores. */
 MOE_API void moe_synth_normal(uint64_t seed, uint64_t stream, float sigma, float *out, uint64_t n, int nthreads);
-/* rows x cols fp32 (row-major) into blocks of type (Q8_0: ggml's quantize_row_q8_0_ref; Q4_K and IQ3_S: this
- * library's own quantisers, which write valid blocks but are not ggml's search). Returns MOE_OK or BAD_ARGUMENT. */
+/* rows x cols fp32 (row-major) into blocks of type (Q8_0: ggml's quantize_row_q8_0_ref; the others: this library's
+ * own quantisers, which write valid blocks but are not ggml's search). IQ3_XXS and IQ2_S search the codebooks of the
+ * last moe_synth_set_codebooks. Returns MOE_OK or BAD_ARGUMENT. */
+/* The codebooks the IQ3_XXS and IQ2_S quantisers below search (a QGRID-layout buffer, as for moe_set_codebooks);
+ * kept until the process ends. */
+MOE_API moe_status moe_synth_set_codebooks(const uint8_t *qgrid, uint64_t bytes);
 MOE_API moe_status moe_quantize(uint32_t type, const float *x, uint32_t rows, uint32_t cols, uint8_t *out,
                                 int nthreads);
 /* A matrix of N(0, sigma) values drawn from (seed, stream), quantised: the same bytes as moe_synth_normal followed by

@@ -3,8 +3,9 @@
  * Replaces the reference's shared/quant.h (ids :9-33, values per block :36-44, bytes per block :47-75, field tables
  * :78-166, run offsets :172-176, QUANT_FILE_PAD :180, codebook buffer offsets :189-196). The numeric values, the field
  * order (quants first, the f16 scales last) and the codebook buffer offsets are the same, so a caller that built
- * buffers for the reference's headers builds the same bytes for these. Only the five types this block implements on
- * the GPU (Q8_0, Q4_K, IQ3_S, IQ4_NL, Q2_0) and the two activation types (q8_0, q8_K) carry field tables; the other
+ * buffers for the reference's headers builds the same bytes for these. Only the seven types this block implements on
+ * the GPU (Q8_0, Q4_K, IQ3_S, IQ4_NL, Q2_0, IQ3_XXS, IQ2_S) and the two activation types (q8_0, q8_K) carry field
+ * tables; the other
  * ids are kept so that a caller's switch over them still compiles. C and HIP device code both include this header. */
 #ifndef C0VEN_QUANT_H
 #define C0VEN_QUANT_H
@@ -91,8 +92,13 @@ C0VEN_FN uint32_t quant_block_bytes(uint32_t t) {
 
 /* Whether the GPU block implements a weight type. */
 C0VEN_FN int quant_gpu_supported(uint32_t t) {
-  return t == QT_Q8_0 || t == QT_Q4_K || t == QT_IQ3_S || t == QT_IQ4_NL || t == QT_Q2_0;
+  return t == QT_Q8_0 || t == QT_Q4_K || t == QT_IQ3_S || t == QT_IQ4_NL || t == QT_Q2_0 || t == QT_IQ3_XXS ||
+         t == QT_IQ2_S;
 }
+
+/* Whether a weight type decodes through a codebook the caller supplies (ggml-common.h's iq3xxs_grid and iq2s_grid,
+ * which this build does not carry: moe_set_codebooks). */
+C0VEN_FN int quant_needs_codebook(uint32_t t) { return t == QT_IQ3_XXS || t == QT_IQ2_S; }
 
 /* The activation type a weight type's integer dot product takes on the CPU (ggml-cpu.c vec_dot_type): q8_K for the
  * K- and i-quants of 256-value blocks, q8_0 for Q8_0, IQ4_NL and Q2_0 (ggml-cpu.c :272, :380, :234). 0 (F32) for a
@@ -100,7 +106,7 @@ C0VEN_FN int quant_gpu_supported(uint32_t t) {
 C0VEN_FN uint32_t quant_vec_dot_type(uint32_t t) {
   switch (t) {
     case QT_Q8_0: case QT_IQ4_NL: case QT_Q2_0: return QT_Q8_0;
-    case QT_Q4_K: case QT_IQ3_S: return QT_Q8_K;
+    case QT_Q4_K: case QT_IQ3_S: case QT_IQ3_XXS: case QT_IQ2_S: return QT_Q8_K;
     default: return QT_F32;
   }
 }
@@ -108,8 +114,8 @@ C0VEN_FN uint32_t quant_vec_dot_type(uint32_t t) {
 /* Fields of a block in run order: (offset in the file's block << 8) | size. Quants first, f16 scales last. */
 C0VEN_FN uint32_t quant_nfields(uint32_t t) {
   switch (t) {
-    case QT_IQ3_S: return 5;
-    case QT_Q4_K: return 3;
+    case QT_IQ3_S: case QT_IQ2_S: return 5;
+    case QT_Q4_K: case QT_IQ3_XXS: return 3;
     case QT_Q8_0: case QT_IQ4_NL: case QT_Q2_0: return 2;
     case QT_Q8_K: return 3;
     default: return 1;
@@ -121,6 +127,11 @@ C0VEN_FN uint32_t quant_field_(uint32_t t, uint32_t f) {
     case QT_IQ3_S: /* qs, signs, qh, scales, d */
       return f == 0 ? (2u << 8) | 64 : f == 1 ? (74u << 8) | 32 : f == 2 ? (66u << 8) | 8 : f == 3 ? (106u << 8) | 4
                                                                                                 : (0u << 8) | 2;
+    case QT_IQ2_S: /* qs (grid index low bits), signs, qh, scales, d */
+      return f == 0 ? (2u << 8) | 32 : f == 1 ? (34u << 8) | 32 : f == 2 ? (66u << 8) | 8 : f == 3 ? (74u << 8) | 8
+                                                                                                : (0u << 8) | 2;
+    case QT_IQ3_XXS: /* grid indices, scale-and-sign words, d */
+      return f == 0 ? (2u << 8) | 64 : f == 1 ? (66u << 8) | 32 : (0u << 8) | 2;
     case QT_Q4_K: /* qs, scales, d and dmin */
       return f == 0 ? (16u << 8) | 128 : f == 1 ? (4u << 8) | 12 : (0u << 8) | 4;
     case QT_Q8_0: /* qs, d */
@@ -146,9 +157,9 @@ C0VEN_FN uint64_t quant_run_offset(uint32_t t, uint32_t f, uint64_t n) {
 /* Bytes a reader may touch past a slice's last block in the file's layout. */
 #define QUANT_FILE_PAD 8
 
-/* The codebook buffer's layout, as the reference packs ggml-common.h's tables for its cards. This build fills only
- * the IQ3_S grid (512 x u32) and kvalues (kvalues_iq4nl: -127 .. 113); the other regions are kept at their offsets
- * and left zero. */
+/* The codebook buffer's layout, as the reference packs ggml-common.h's tables for its cards (core/load/codebooks.cpp).
+ * This build carries the IQ3_S grid (512 x u32) and kvalues (kvalues_iq4nl: -127 .. 113) itself; iq2s_grid and
+ * iq3xxs_grid come from the caller in a buffer of this layout (moe_set_codebooks). */
 #define QGRID_IQ2S 0        /* u64 x 1024 */
 #define QGRID_IQ3XXS 8192   /* u32 x 256 */
 #define QGRID_IQ3S 9216     /* u32 x 512 */

@@ -14,6 +14,10 @@
 #define QT_IQ3_S 21
 #define QT_IQ4_NL 20
 #define QT_Q2_0 42
+#define QT_IQ3_XXS 18
+#define QT_IQ2_S 22
+#define QGRID_IQ2S 0
+#define QGRID_IQ3XXS 8192
 #define QK 256
 
 /* kvalues_iq4nl (ggml-common.h:1120-1122): the IQ4_NL codebook, which must hash to QUANT_FORMATS.md:547's sha256
@@ -127,6 +131,40 @@ static inline void scale_min_k4(int j, const uint8_t *q, int *sc, int *m) {
   }
 }
 
+/* iq2s_grid and iq3xxs_grid, which ggml-common.h holds and this repository does not: the caller's, from a buffer in
+ * the QGRID layout (core/load/codebooks.cpp:14-33 packs ggml's tables so). */
+static uint64_t g_iq2s[1024];
+static uint32_t g_iq3xxs[256];
+
+void orc_set_codebooks(const uint8_t *qgrid) {
+  memcpy(g_iq2s, qgrid + QGRID_IQ2S, sizeof g_iq2s);
+  memcpy(g_iq3xxs, qgrid + QGRID_IQ3XXS, sizeof g_iq3xxs);
+}
+
+/* Value v of an IQ3_XXS block (QUANT_FORMATS.md:147-166): (grid magnitude, negative?) and the sub-block's scale
+ * nibble s. Sign group l = (v % 32) / 8 of sub-block b is the 7-bit index (w >> 7 l) & 127 of the sub-block's word,
+ * its eighth bit the index's parity (ksigns_iq2xs). */
+static inline void iq3xxs_value(const uint8_t *b, int v, int *mag, int *neg, int *s) {
+  const int ib = v / 32, j = v % 32, l = j / 8;
+  uint32_t w;
+  memcpy(&w, b + 66 + 4 * ib, 4);
+  const uint32_t idx7 = (w >> (7 * l)) & 127u, sb = idx7 | ((uint32_t)(__builtin_popcount(idx7) & 1) << 7);
+  const uint8_t q = b[2 + 8 * ib + 2 * l + (j % 8) / 4];
+  *mag = (int)((g_iq3xxs[q] >> (8 * (j % 4))) & 0xffu);
+  *neg = (int)((sb >> (j % 8)) & 1u);
+  *s = (int)(w >> 28);
+}
+
+/* Value v of an IQ2_S block (QUANT_FORMATS.md:115-137): (grid magnitude, negative?) and its half sub-block's scale
+ * nibble (low nibble for values 0-15 of the sub-block, high for 16-31). */
+static inline void iq2s_value(const uint8_t *b, int v, int *mag, int *neg, int *s) {
+  const int ib = v / 32, j = v % 32, g = j / 8;
+  const uint32_t idx = b[2 + 4 * ib + g] | (((uint32_t)(b[66 + ib] >> (2 * g)) & 3u) << 8);
+  *mag = (int)((g_iq2s[idx] >> (8 * (j % 8))) & 0xffu);
+  *neg = (int)((b[34 + 4 * ib + g] >> (j % 8)) & 1u);
+  *s = (int)((b[74 + ib] >> (4 * (j / 16))) & 15u);
+}
+
 /* Value v of an IQ3_S block as (grid magnitude, negative?) with its sub-block scale 1 + 2 s. */
 static inline void iq3s_value(const uint8_t *b, int v, int *mag, int *neg, int *ls) {
   const uint8_t *qs = b + 2, *qh = b + 66, *signs = b + 74, *scales = b + 106;
@@ -192,6 +230,30 @@ int orc_dequantize_row(uint32_t type, const void *src, float *dst, int64_t n) {
       for (int64_t i = 0; i < n / 64; i++, b += 18) {
         const float d = orc_fp16_to_fp32(rd16(b));
         for (int j = 0; j < 64; j++) dst[64 * i + j] = (float)((int)((b[2 + j / 4] >> (2 * (j % 4))) & 3) - 1) * d;
+      }
+      return 0;
+    case QT_IQ3_XXS: /* y = ((d (0.5 + s)) 0.5) grid sign (quants.c:2575-2603) */
+      if (n % QK) return -1;
+      for (int64_t i = 0; i < n / QK; i++, b += 98) {
+        const float d = orc_fp16_to_fp32(rd16(b));
+        for (int v = 0; v < QK; v++) {
+          int mag, neg, sc;
+          iq3xxs_value(b, v, &mag, &neg, &sc);
+          const float db = d * (0.5f + (float)sc) * 0.5f;
+          dst[QK * i + v] = db * (float)mag * (neg ? -1.0f : 1.0f);
+        }
+      }
+      return 0;
+    case QT_IQ2_S: /* y = ((d (0.5 + s)) 0.25) grid sign (quants.c:2543-2571) */
+      if (n % QK) return -1;
+      for (int64_t i = 0; i < n / QK; i++, b += 82) {
+        const float d = orc_fp16_to_fp32(rd16(b));
+        for (int v = 0; v < QK; v++) {
+          int mag, neg, sc;
+          iq2s_value(b, v, &mag, &neg, &sc);
+          const float db = d * (0.5f + (float)sc) * 0.25f;
+          dst[QK * i + v] = db * (float)mag * (neg ? -1.0f : 1.0f);
+        }
       }
       return 0;
     default: return -1;
@@ -265,7 +327,9 @@ int orc_quantize_act(uint32_t act_type, const float *src, void *dst, int64_t n) 
 
 /* The 32-value block types: q8_0 activations (ggml-cpu.c vec_dot_type: Q8_0, IQ4_NL :380, Q2_0 :234). */
 static int q8_family(uint32_t t) { return t == QT_Q8_0 || t == QT_IQ4_NL || t == QT_Q2_0; }
-static uint32_t act_type_of(uint32_t t) { return q8_family(t) ? QT_Q8_0 : (t == QT_Q4_K || t == QT_IQ3_S) ? QT_Q8_K : 0; }
+static uint32_t act_type_of(uint32_t t) {
+  return q8_family(t) ? QT_Q8_0 : (t == QT_Q4_K || t == QT_IQ3_S || t == QT_IQ3_XXS || t == QT_IQ2_S) ? QT_Q8_K : 0;
+}
 static uint64_t act_bytes(uint32_t act, uint64_t n) { return act == QT_Q8_0 ? n / 32 * 34 : n / QK * 292; }
 static uint64_t row_bytes(uint32_t t, uint64_t n) {
   return t == QT_Q8_0 ? n / 32 * 34
@@ -273,6 +337,8 @@ static uint64_t row_bytes(uint32_t t, uint64_t n) {
          : t == QT_Q2_0   ? n / 64 * 18
          : t == QT_Q4_K   ? n / QK * 144
          : t == QT_IQ3_S  ? n / QK * 110
+         : t == QT_IQ3_XXS ? n / QK * 98
+         : t == QT_IQ2_S  ? n / QK * 82
                           : 0;
 }
 /* The values a row's length must be a multiple of: the type's block. */
@@ -363,6 +429,48 @@ static float term_iq3_s(const uint8_t *w, const uint8_t *a) {
   return d * (float)bsum;
 }
 
+/* IQ3_XXS x q8_K (vec_dot_iq3_xxs_q8_K; core/cpu/multirow.cpp:126-176 states its integer steps): per sub-block
+ * (2 s + 1) sum grid sign q_a, summed as an integer, then 0.25 ((d_w d_a) isum) (the power of two exact). */
+static float term_iq3_xxs(const uint8_t *w, const uint8_t *a) {
+  float ad;
+  memcpy(&ad, a, 4);
+  const int8_t *q8 = (const int8_t *)(a + 4);
+  int32_t isum = 0;
+  for (int ib = 0; ib < 8; ib++) {
+    int32_t s = 0;
+    int sc = 0;
+    for (int i = 0; i < 32; i++) {
+      int mag, neg;
+      iq3xxs_value(w, 32 * ib + i, &mag, &neg, &sc);
+      s += (neg ? -mag : mag) * q8[32 * ib + i];
+    }
+    isum += (2 * sc + 1) * s;
+  }
+  const float d = orc_fp16_to_fp32(rd16(w)) * ad;
+  return 0.25f * (d * (float)isum);
+}
+
+/* IQ2_S x q8_K (vec_dot_iq2_s_q8_K; core/cpu/multirow.cpp:68-124): per half sub-block (2 s + 1) sum grid sign q_a,
+ * summed as an integer, then 0.125 ((d_w d_a) isum). */
+static float term_iq2_s(const uint8_t *w, const uint8_t *a) {
+  float ad;
+  memcpy(&ad, a, 4);
+  const int8_t *q8 = (const int8_t *)(a + 4);
+  int32_t isum = 0;
+  for (int h = 0; h < 16; h++) {
+    int32_t s = 0;
+    int sc = 0;
+    for (int i = 0; i < 16; i++) {
+      int mag, neg;
+      iq2s_value(w, 16 * h + i, &mag, &neg, &sc);
+      s += (neg ? -mag : mag) * q8[16 * h + i];
+    }
+    isum += (2 * sc + 1) * s;
+  }
+  const float d = orc_fp16_to_fp32(rd16(w)) * ad;
+  return 0.125f * (d * (float)isum);
+}
+
 static float dot_row(uint32_t type, int64_t n, const uint8_t *w, const uint8_t *a, float *terms) {
   int64_t nb;
   switch (type) {
@@ -381,6 +489,14 @@ static float dot_row(uint32_t type, int64_t n, const uint8_t *w, const uint8_t *
     case QT_Q4_K:
       nb = n / QK;
       for (int64_t i = 0; i < nb; i++) terms[i] = term_q4_K(w + 144 * i, a + 292 * i);
+      break;
+    case QT_IQ3_XXS:
+      nb = n / QK;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_iq3_xxs(w + 98 * i, a + 292 * i);
+      break;
+    case QT_IQ2_S:
+      nb = n / QK;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_iq2_s(w + 82 * i, a + 292 * i);
       break;
     default:
       nb = n / QK;

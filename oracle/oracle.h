@@ -2,8 +2,9 @@
  * bench.py's cpu_baseline leg load it, as the checker; the product (c0ven_amd/) never links or calls it.
  *
  * A plain-C restatement of the reference's CPU expert path and of the block around it:
- *   - the weight decoders (ggml's dequantize_row_q8_0 / _q4_K / _iq3_s / _iq4_nl / _q2_0, as
- *     docs/spec/QUANT_FORMATS.md:176-212, :373-400, :447-466, :234-246, :251-270 state them);
+ *   - the weight decoders (ggml's dequantize_row_q8_0 / _q4_K / _iq3_s / _iq4_nl / _q2_0 / _iq3_xxs / _iq2_s, as
+ *     docs/spec/QUANT_FORMATS.md:176-212, :373-400, :447-466, :234-246, :251-270, :147-168, :115-137 state them;
+ *     the last two through codebooks the caller supplies, as ggml-common.h is absent);
  *   - the activation quantisers the CPU path converts x and h with (q8_0, QUANT_FORMATS.md:463-465; q8_K,
  *     :528-535), chosen per weight type as core/cpu/experts.cpp:114-123 does (ggml's vec_dot_type);
  *   - the integer block dot products (vec_dot) of each weight type against its activation type;
@@ -73,6 +74,8 @@ void orc_expf(const float *x, float *y, int64_t n); /* libm's expf, element by e
 /* The IQ3_S codebook, 512 x u32. */
 void orc_iq3s_grid(uint32_t *out);
 void orc_iq4nl_values(int8_t *out); /* kvalues_iq4nl, 16 signed bytes */
+/* iq2s_grid and iq3xxs_grid from a QGRID-layout buffer (IQ3_XXS and IQ2_S decode through them). */
+void orc_set_codebooks(const uint8_t *qgrid);
 
 /* Returns 0, or -1 for a type it does not know or an n that is no whole number of blocks. */
 int orc_dequantize_row(uint32_t type, const void *src, float *dst, int64_t n);

@@ -31,6 +31,7 @@ def _load_oracle():
         "orc_expf": (None, [_P, _P, C.c_int64]),
         "orc_iq3s_grid": (None, [_P]),
         "orc_iq4nl_values": (None, [_P]),
+        "orc_set_codebooks": (None, [_P]),
         "orc_dequantize_row": (C.c_int, [C.c_uint32, _P, _P, C.c_int64]),
         "orc_quantize_act": (C.c_int, [C.c_uint32, _P, _P, C.c_int64]),
         "orc_vec_dot": (C.c_int, [C.c_uint32, C.c_int64, _P, _P, C.POINTER(C.c_float)]),
@@ -117,6 +118,33 @@ def orc_iq4nl():
     return v
 
 
+def synth_codebooks(seed=4242):
+    """A QGRID-layout codebook buffer with stand-ins for ggml's iq2s_grid and iq3xxs_grid (absent here): distinct
+    entries drawn from each table's byte values (8, 25, 43; 4, 12, .., 52, 62), seeded; the real iq3s_grid and
+    kvalues_iq4nl in their regions. Parity against the oracle holds for any table, so the tests use this one; the
+    tables' content is what only ggml-common.h could pin."""
+    r = np.random.default_rng(seed)
+    buf = np.zeros(moe.QGRID_BYTES, dtype=np.uint8)
+    lv2 = np.array([8, 25, 43], dtype=np.uint8)
+    lv3 = np.array([4, 12, 20, 28, 36, 44, 52, 62], dtype=np.uint8)
+    g2 = set()
+    while len(g2) < 1024:
+        g2.add(bytes(lv2[r.integers(0, 3, size=8)]))
+    g3 = set()
+    while len(g3) < 256:
+        g3.add(bytes(lv3[r.integers(0, 8, size=4)]))
+    buf[moe.QGRID_IQ2S:moe.QGRID_IQ2S + 8192] = np.frombuffer(b"".join(sorted(g2)), np.uint8)
+    buf[moe.QGRID_IQ3XXS:moe.QGRID_IQ3XXS + 1024] = np.frombuffer(b"".join(sorted(g3)), np.uint8)
+    buf[moe.QGRID_IQ3S:moe.QGRID_IQ3S + 2048] = orc_grid().view(np.uint8)
+    buf[moe.QGRID_KVALUES:moe.QGRID_KVALUES + 16] = orc_iq4nl().view(np.uint8)
+    return buf
+
+
+CODEBOOKS = synth_codebooks()
+oracle.orc_set_codebooks(ptr(CODEBOOKS))
+moe.synth_set_codebooks(CODEBOOKS)
+
+
 def to_bf16(x):
     """fp32 -> bf16 bits, round to nearest even (NaN-free input)."""
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
@@ -157,6 +185,8 @@ class Layer:
                 moe.synth_matrix(self.seed, s + 2, dt, H, F, sigma, nthreads))
 
     def upload(self, blk, layer=0):
+        if {self.gate_type, self.down_type, self.sh_gate_type, self.sh_down_type} & set(moe.CODEBOOK_TYPES):
+            blk.set_codebooks(CODEBOOKS)
         blk.load_router(layer, self.router, self.bias)
         for e, (g, u, d) in self.experts.items():
             blk.load_expert(layer, e, g, u, d)

@@ -35,7 +35,8 @@ def random_blocks(qtype, nblocks):
     nv, nb = moe.BLOCK[qtype]
     b = rng.integers(0, 256, size=(nblocks, nb), dtype=np.uint8)
     reach = {moe.QT_Q8_0: [(0, 128)], moe.QT_Q4_K: [(0, 63 * 15), (2, 63)], moe.QT_IQ3_S: [(0, 31 * 15)],
-             moe.QT_IQ4_NL: [(0, 127)], moe.QT_Q2_0: [(0, 2)]}[qtype]
+             moe.QT_IQ4_NL: [(0, 127)], moe.QT_Q2_0: [(0, 2)], moe.QT_IQ3_XXS: [(0, 62 * 31)],
+             moe.QT_IQ2_S: [(0, 43 * 31)]}[qtype]
     for k in range(nblocks):
         for off, r in reach:
             v = np.ldexp(1.0 + rng.integers(0, 1024) / 1024.0, int(rng.integers(0, 3)) - 5) / r
@@ -46,11 +47,13 @@ def random_blocks(qtype, nblocks):
 @pytest.fixture(scope="module")
 def tiny_block():
     blk = moe.MoeBlock(512, 256, 8, 2, moe.QT_Q8_0, moe.QT_Q8_0)
+    blk.set_codebooks(h.CODEBOOKS)
     yield blk
     blk.close()
 
 
-@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q2_0])
+@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q2_0, moe.QT_IQ3_XXS,
+                                   moe.QT_IQ2_S])
 @pytest.mark.parametrize("rows,cols", [(128, 512), (100, 256)])
 def test_dequantize_bit_exact(tiny_block, qtype, rows, cols):
     say("dequantize", moe.TYPE_NAMES[qtype], rows, cols)
@@ -218,7 +221,7 @@ def _cm_jobs(L, T, K, rng_seed, parts=False):
 
 
 @pytest.mark.parametrize("T", [1, 8, 64])
-@pytest.mark.parametrize("types", [(moe.QT_Q4_K, moe.QT_Q4_K), (moe.QT_IQ3_S, moe.QT_Q8_0)])
+@pytest.mark.parametrize("types", [(moe.QT_Q4_K, moe.QT_Q4_K), (moe.QT_IQ3_S, moe.QT_Q8_0), (moe.QT_IQ2_S, moe.QT_Q2_0)])
 def test_compute_many_borrowed(T, types):
     """moe_compute_many on borrowed file-layout weights equals the oracle's compute_many bit for bit: T 1 and 8 run
     the decode kernel, 64 the prefill kernels; down given in two parts on some experts (down_parts)."""
@@ -226,6 +229,8 @@ def test_compute_many_borrowed(T, types):
     say("compute_many borrowed", moe.TYPE_NAMES[gt], moe.TYPE_NAMES[dt], "T", T)
     L = h.Layer(512, 512, 32, 4, gt, dt, seed=90 + T)
     blk = moe.MoeBlock(512, 512, 32, 4, gt, dt, has_shared=False, max_tokens=64)
+    if gt in moe.CODEBOOK_TYPES:
+        blk.set_codebooks(h.CODEBOOKS)
     x = h.tokens(91 + T, T, 512)
     for parts in (False, True):
         jobs, ojobs = _cm_jobs(L, T, 4, T + 7, parts)
@@ -239,13 +244,17 @@ def test_compute_many_borrowed(T, types):
                                    (moe.QT_IQ3_S, moe.QT_Q8_0, moe.QT_Q8_0, moe.QT_Q8_0),
                                    (moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q8_0, moe.QT_IQ4_NL),
                                    (moe.QT_IQ3_S, moe.QT_Q2_0, moe.QT_Q8_0, moe.QT_Q2_0),
-                                   (moe.QT_IQ4_NL, moe.QT_Q2_0, moe.QT_Q2_0, moe.QT_IQ4_NL)])
+                                   (moe.QT_IQ4_NL, moe.QT_Q2_0, moe.QT_Q2_0, moe.QT_IQ4_NL),
+                                   (moe.QT_IQ3_XXS, moe.QT_IQ4_NL, moe.QT_Q4_K, moe.QT_IQ4_NL),
+                                   (moe.QT_IQ2_S, moe.QT_Q2_0, moe.QT_Q4_K, moe.QT_IQ4_NL),
+                                   (moe.QT_IQ2_S, moe.QT_IQ4_NL, moe.QT_IQ3_XXS, moe.QT_IQ4_NL)])
 @pytest.mark.parametrize("T", [1, 8, 100])
 def test_model_shape_2560_640(types, T):
     """The reference model's own expert shape (MODEL_LAYER.md:51, :69): n_embd 2560 (ten 256-value units, not a power of
-    two), n_ff 640 (down's K two and a half units: its last unit half blocks, half zero padding), with the file's down
-    types (IQ4_NL, Q2_0: QUANT_FORMATS.md:43-44) and both as gate/up too. Decode (T 1, 8) and prefill (T 100) against
-    the oracle, bit for bit."""
+    two), n_ff 640 (down's K two and a half units: its last unit half blocks, half zero padding), with the file's
+    types (docs/model/tensors-IQ3_S.tsv: gate/up IQ3_XXS, IQ2_S or IQ3_S, down IQ4_NL or Q2_0, the shared expert's
+    gate Q4_K; IQ3_XXS and IQ2_S through the tests' stand-in codebooks) and the 32-value types as gate/up too. Decode
+    (T 1, 8) and prefill (T 100) against the oracle, bit for bit."""
     gt, dt, sgt, sdt = types
     say("shape 2560 x 640", [moe.TYPE_NAMES[t] for t in types], "T", T)
     L = h.Layer(2560, 640, 64, 8, gt, dt, sgt, sdt, seed=2560 + T, zipf=1.1)
@@ -266,3 +275,27 @@ def test_dequantize_partial_unit(tiny_block, qtype):
     got = tiny_block.dequantize(qtype, m, 70, 640)
     want = np.stack([h.orc_dequant(qtype, m[r * rb:(r + 1) * rb], 640) for r in range(70)])
     assert np.array_equal(got, want)
+
+
+def test_codebooks_required_and_checked():
+    """IQ3_XXS / IQ2_S contexts refuse to run before moe_set_codebooks; a buffer whose IQ3_S region is not ggml's grid
+    (so not the QGRID layout) is refused; after a good buffer the forward runs and matches the oracle."""
+    say("codebooks required")
+    L = h.Layer(512, 256, 16, 4, moe.QT_IQ3_XXS, moe.QT_IQ4_NL, has_shared=False, seed=77)
+    blk = L.block()
+    blk.load_router(0, L.router, L.bias)
+    for e, (g, u, d) in L.experts.items():
+        blk.load_expert(0, e, g, u, d)
+    x = h.tokens(78, 2, 512)
+    with pytest.raises(moe.MoeError):
+        blk.forward(0, x)
+    bad = h.CODEBOOKS.copy()
+    bad[moe.QGRID_IQ3S] ^= 2
+    with pytest.raises(moe.MoeError):
+        blk.set_codebooks(bad)
+    with pytest.raises(moe.MoeError):
+        blk.set_codebooks(h.CODEBOOKS[:moe.QGRID_IQ3S])
+    blk.set_codebooks(h.CODEBOOKS)
+    y, ids, w = blk.forward(0, x)
+    check_block(y, ids, w, *L.oracle_forward(x))
+    blk.close()

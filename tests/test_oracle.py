@@ -115,6 +115,51 @@ def test_q2_0_decoder():
                           np.tile(np.array([-2, 0, 2, 4], np.float32), 16))  # 0xE4: codes 0, 1, 2, 3
 
 
+def test_iq3_xxs_decoder():
+    """Sub-block b: index bytes 8 b .. 8 b + 7 (groups of four values), then its word: four 7-bit sign indices (the
+    eighth sign the parity) and the scale s in bits 28-31; y = ((d (0.5 + s)) 0.5) grid sign. The grid is the tests'
+    stand-in table (h.CODEBOOKS)."""
+    grid = h.CODEBOOKS[moe.QGRID_IQ3XXS:moe.QGRID_IQ3XXS + 1024].view("<u4")
+    idx = rng.integers(0, 256, size=64)
+    s = rng.integers(0, 16, size=8)
+    s7 = rng.integers(0, 128, size=(8, 4))
+    words = np.zeros(8, np.uint32)
+    for b in range(8):
+        words[b] = (int(s[b]) << 28) | sum(int(s7[b, l]) << (7 * l) for l in range(4))
+    blk = np.concatenate([f16(0.125), idx.astype(np.uint8), words.view(np.uint8)])
+    y = h.orc_dequant(moe.QT_IQ3_XXS, blk, 256)
+    d = np.float32(0.125)
+    for v in range(256):
+        b, j = v // 32, v % 32
+        l = j // 8
+        sb = int(s7[b, l]) | ((bin(int(s7[b, l])).count("1") & 1) << 7)
+        mag = (int(grid[idx[8 * b + 2 * l + (j % 8) // 4]]) >> (8 * (j % 4))) & 0xFF
+        db = np.float32(np.float32(d * np.float32(0.5 + s[b])) * np.float32(0.5))
+        want = np.float32(db * np.float32(mag)) * (-1 if (sb >> (j % 8)) & 1 else 1)
+        assert y[v] == want, v
+
+
+def test_iq2_s_decoder():
+    """Group g of sub-block b: index qs[4 b + g] | ((qh[b] >> 2 g) & 3) << 8, sign byte signs[4 b + g], scale the low
+    nibble of scales[b] for values 0-15 and the high for 16-31; y = ((d (0.5 + s)) 0.25) grid sign."""
+    grid = h.CODEBOOKS[moe.QGRID_IQ2S:moe.QGRID_IQ2S + 8192].view("<u8")
+    qs = rng.integers(0, 256, size=32).astype(np.uint8)
+    sg = rng.integers(0, 256, size=32).astype(np.uint8)
+    qh = rng.integers(0, 256, size=8).astype(np.uint8)
+    sc = rng.integers(0, 256, size=8).astype(np.uint8)
+    blk = np.concatenate([f16(0.25), qs, sg, qh, sc])
+    y = h.orc_dequant(moe.QT_IQ2_S, blk, 256)
+    for v in range(256):
+        b, j = v // 32, v % 32
+        g = j // 8
+        ix = int(qs[4 * b + g]) | (((int(qh[b]) >> (2 * g)) & 3) << 8)
+        mag = (int(grid[ix]) >> (8 * (j % 8))) & 0xFF
+        s = (int(sc[b]) >> (4 * (j // 16))) & 15
+        db = np.float32(np.float32(np.float32(0.25) * np.float32(0.5 + s)) * np.float32(0.25))
+        want = np.float32(db * np.float32(mag)) * (-1 if (int(sg[4 * b + g]) >> (j % 8)) & 1 else 1)
+        assert y[v] == want, v
+
+
 def pack_q4_k_scales(sc, m):
     """QUANT_FORMATS.md's table for the 12 scale bytes (bytes 0-3, 4-7, 8-11)."""
     b = np.zeros(12, dtype=np.uint8)
@@ -231,7 +276,8 @@ def random_blocks(qtype, n):
     nv, nbytes = moe.BLOCK[qtype]
     b = rng.integers(0, 256, size=(n, nbytes), dtype=np.uint8)
     reach = {moe.QT_Q8_0: [(0, 128)], moe.QT_Q4_K: [(0, 63 * 15), (2, 63)], moe.QT_IQ3_S: [(0, 31 * 15)],
-             moe.QT_IQ4_NL: [(0, 127)], moe.QT_Q2_0: [(0, 2)]}[qtype]
+             moe.QT_IQ4_NL: [(0, 127)], moe.QT_Q2_0: [(0, 2)], moe.QT_IQ3_XXS: [(0, 62 * 31)],
+             moe.QT_IQ2_S: [(0, 43 * 31)]}[qtype]
     for k in range(n):
         for off, r in reach:
             v = np.ldexp(1.0 + rng.integers(0, 1024) / 1024.0, int(rng.integers(0, 3)) - 5) / r
@@ -239,7 +285,8 @@ def random_blocks(qtype, n):
     return b.ravel()
 
 
-@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q2_0])
+@pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q2_0, moe.QT_IQ3_XXS,
+                                   moe.QT_IQ2_S])
 @pytest.mark.parametrize("n", [256, 2048])
 def test_vec_dot_against_decoded_float64(qtype, n):
     for trial in range(20):
@@ -294,7 +341,7 @@ def test_vec_dot_exact_when_every_step_is_exact():
     x = rng.integers(-20, 21, size=n).astype(np.float32)
     x[::256] = -127.0  # max = -127: iscale = 1, codes = x, d = 1
     aq = h.orc_quant_act(moe.QT_Q8_K, x)
-    for qtype in (moe.QT_Q4_K, moe.QT_IQ3_S):
+    for qtype in (moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ3_XXS, moe.QT_IQ2_S):
         wq = random_blocks(qtype, n // 256).reshape(n // 256, -1)
         wq[:, :2] = f16(2.0**-4)
         if qtype == moe.QT_Q4_K:
@@ -318,7 +365,8 @@ def dense_ffn(gate, up, down, gt, dt, H, F, x, limit=0.0):
 
 
 TYPES = [(moe.QT_Q8_0, moe.QT_Q8_0), (moe.QT_Q4_K, moe.QT_Q4_K), (moe.QT_IQ3_S, moe.QT_Q4_K), (moe.QT_IQ3_S, moe.QT_IQ3_S),
-         (moe.QT_Q4_K, moe.QT_Q8_0), (moe.QT_Q4_K, moe.QT_IQ4_NL), (moe.QT_IQ4_NL, moe.QT_Q2_0)]
+         (moe.QT_Q4_K, moe.QT_Q8_0), (moe.QT_Q4_K, moe.QT_IQ4_NL), (moe.QT_IQ4_NL, moe.QT_Q2_0),
+         (moe.QT_IQ3_XXS, moe.QT_IQ4_NL), (moe.QT_IQ2_S, moe.QT_Q2_0)]
 
 
 @pytest.mark.parametrize("gt,dt", TYPES)
