@@ -67,6 +67,11 @@ class MoeGroup(C.Structure):
     _fields_ = [("slot", C.c_int32), ("n", C.c_uint32), ("asg", C.c_uint32 * 8)]
 
 
+class GgufTensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("type", C.c_uint32), ("n_dims", C.c_uint32), ("shape", C.c_uint64 * 4),
+                ("shard", C.c_uint32), ("offset", C.c_uint64), ("bytes", C.c_uint64), ("data", C.c_void_p)]
+
+
 _P = C.c_void_p
 _u32, _u64, _i32, _f32 = C.c_uint32, C.c_uint64, C.c_int32, C.c_float
 _SIGS = {
@@ -102,6 +107,22 @@ _SIGS = {
     "moe_zipf_bias": (None, [_u64, _u32, _f32, _P]),
     "moe_row_bytes": (_u64, [_u32, _u32]),
     "moe_abi_layout": (_u32, [C.POINTER(MoeAbiRow), _u32]),
+    "moe_load_layer_gguf": (_i32, [_P, _u32, _P, _u32]),
+    "gguf_open": (_i32, [C.c_char_p, C.POINTER(_P)]),
+    "gguf_close": (None, [_P]),
+    "gguf_last_error": (C.c_char_p, [_P]),
+    "gguf_n_files": (_u32, [_P]),
+    "gguf_n_tensors": (_u64, [_P]),
+    "gguf_tensor_at": (_i32, [_P, _u64, C.POINTER(GgufTensorInfo)]),
+    "gguf_find_tensor": (_i32, [_P, C.c_char_p, C.POINTER(GgufTensorInfo)]),
+    "gguf_has_key": (C.c_int, [_P, C.c_char_p]),
+    "gguf_get_int": (_i32, [_P, C.c_char_p, C.POINTER(C.c_int64)]),
+    "gguf_get_float": (_i32, [_P, C.c_char_p, C.POINTER(C.c_double)]),
+    "gguf_get_string": (_i32, [_P, C.c_char_p, C.c_char_p, _u64, C.POINTER(_u64)]),
+    "gguf_get_ints": (_i32, [_P, C.c_char_p, C.POINTER(C.c_int64), _u64, C.POINTER(_u64)]),
+    "gguf_architecture": (_i32, [C.c_char_p, C.c_char_p, _u64]),
+    "gguf_release": (_i32, [_P, C.c_char_p, _u64, _u64]),
+    "gguf_type_bytes": (_u64, [_u32, _u64]),
 }
 EXPORTS = tuple(_SIGS)
 for _name, (_res, _args) in _SIGS.items():
@@ -154,6 +175,96 @@ def synth_set_codebooks(qgrid):
     st = lib.moe_synth_set_codebooks(_ptr(qgrid), qgrid.size)
     if st != MOE_OK:
         raise MoeError(st, "moe_synth_set_codebooks")
+
+
+class GgufFile:
+    """A GGUF v3 model file (or its shards) mapped read-only (include/c0ven_gguf.h)."""
+
+    def __init__(self, path):
+        self.h = None
+        h = _P()
+        st = lib.gguf_open(path.encode(), C.byref(h))
+        if st != MOE_OK:
+            raise MoeError(st, lib.gguf_last_error(None).decode())
+        self.h = h
+
+    def _check(self, st):
+        if st != MOE_OK:
+            raise MoeError(st, lib.gguf_last_error(self.h).decode())
+
+    def close(self):
+        if self.h:
+            lib.gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def n_files(self):
+        return int(lib.gguf_n_files(self.h))
+
+    @staticmethod
+    def _info(t):
+        return {"name": t.name.decode(), "type": t.type, "shape": tuple(t.shape[:t.n_dims]), "shard": t.shard,
+                "offset": t.offset, "bytes": t.bytes, "data": t.data}
+
+    def tensors(self):
+        out = []
+        for i in range(int(lib.gguf_n_tensors(self.h))):
+            t = GgufTensorInfo()
+            self._check(lib.gguf_tensor_at(self.h, i, C.byref(t)))
+            out.append(self._info(t))
+        return out
+
+    def tensor(self, name):
+        t = GgufTensorInfo()
+        self._check(lib.gguf_find_tensor(self.h, name.encode(), C.byref(t)))
+        return self._info(t)
+
+    def tensor_bytes(self, name):
+        """A copy of a tensor's bytes as uint8."""
+        t = self.tensor(name)
+        return np.ctypeslib.as_array((C.c_uint8 * t["bytes"]).from_address(t["data"])).copy()
+
+    def has(self, key):
+        return bool(lib.gguf_has_key(self.h, key.encode()))
+
+    def get_int(self, key):
+        v = C.c_int64()
+        self._check(lib.gguf_get_int(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def get_float(self, key):
+        v = C.c_double()
+        self._check(lib.gguf_get_float(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def get_string(self, key):
+        n = _u64()
+        self._check(lib.gguf_get_string(self.h, key.encode(), None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value + 1)
+        self._check(lib.gguf_get_string(self.h, key.encode(), buf, n.value + 1, C.byref(n)))
+        return buf.value.decode()
+
+    def get_ints(self, key):
+        n = _u64()
+        self._check(lib.gguf_get_ints(self.h, key.encode(), None, 0, C.byref(n)))
+        out = (C.c_int64 * max(1, n.value))()
+        self._check(lib.gguf_get_ints(self.h, key.encode(), out, n.value, C.byref(n)))
+        return list(out[:n.value])
+
+    def release(self, name, off=0, nbytes=None):
+        t = self.tensor(name)
+        self._check(lib.gguf_release(self.h, name.encode(), off, t["bytes"] - off if nbytes is None else nbytes))
+
+
+def gguf_architecture(path):
+    buf = C.create_string_buffer(256)
+    st = lib.gguf_architecture(path.encode(), buf, 256)
+    if st != MOE_OK:
+        raise MoeError(st, lib.gguf_last_error(None).decode())
+    return buf.value.decode()
 
 
 def zipf_bias(seed, n_expert, s=1.1):
@@ -254,6 +365,10 @@ class MoeBlock:
         out = np.empty((rows, cols), dtype=np.float32)
         self._check(lib.moe_dequantize(self.h, qtype, _ptr(blocks), rows, cols, _ptr(out)))
         return out
+
+    def load_layer_gguf(self, layer, gguf, blk):
+        """Block blk's router and experts from a GgufFile into layer."""
+        self._check(lib.moe_load_layer_gguf(self.h, layer, gguf.h, blk))
 
     def set_codebooks(self, qgrid):
         """iq2s_grid and iq3xxs_grid from a QGRID-layout uint8 buffer (its IQ3_S region must be ggml's grid)."""

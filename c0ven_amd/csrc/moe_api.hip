@@ -15,6 +15,7 @@
 #include "../../include/c0ven_moe.h"
 #include "aux.h"
 #include "decode.h"
+#include "gguf_reader.h"
 #include "iq3s_grid.h"
 #include "layout.h"
 #include "prefill.h"
@@ -602,6 +603,45 @@ MOE_API moe_status moe_load_expert(moe_ctx *c, uint32_t layer, uint32_t expert, 
   });
 }
 
+MOE_API moe_status moe_load_layer_gguf(moe_ctx *c, uint32_t layer, const c0ven_gguf *file, uint32_t blk) {
+  return guarded(c, [&] {
+    const moe_config &g = c->cfg;
+    require(file != nullptr && layer < g.n_layer, "null file or layer out of range");
+    const uint64_t H = g.n_embd, F = g.n_ff, E = g.n_expert;
+    const std::string pre = "blk." + std::to_string(blk) + ".";
+    // The tensor of a name with the given type and shape (ggml order), or an error naming what differs.
+    const auto tensor = [&](const std::string &name, uint32_t type, std::initializer_list<uint64_t> shape) {
+      const GgufEntry *e = file->file->find(pre + name);
+      require(e != nullptr, "tensor missing from the file: " + pre + name);
+      const gguf_tensor_info &t = e->info;
+      bool same = t.type == type && t.n_dims == shape.size();
+      uint32_t d = 0;
+      for (uint64_t v : shape) same = same && t.shape[d++] == v;
+      require(same, pre + name + ": type " + std::to_string(t.type) + " or shape differs from the context's (type " +
+                        std::to_string(type) + ")");
+      return t.data;
+    };
+    // The router: n_expert rows of n_embd bf16, then the shared expert's gate row (zero without a shared expert).
+    std::vector<uint16_t> router((E + 1) * H, 0);
+    std::memcpy(router.data(), tensor("ffn_gate_inp.weight", QT_BF16, {H, E}), E * H * 2);
+    if (g.has_shared) std::memcpy(router.data() + E * H, tensor("ffn_gate_inp_shexp.weight", QT_BF16, {H}), H * 2);
+    if (moe_load_router(c, layer, router.data(), nullptr) != MOE_OK) throw Error(MOE_ERROR, c->err);
+    const uint8_t *gate = tensor("ffn_gate_exps.weight", g.gate_type, {H, F, E});
+    const uint8_t *up = tensor("ffn_up_exps.weight", g.gate_type, {H, F, E});
+    const uint8_t *down = tensor("ffn_down_exps.weight", g.down_type, {F, H, E});
+    const uint64_t gb = F * gguf_type_bytes(g.gate_type, H), db = H * gguf_type_bytes(g.down_type, F);
+    for (uint32_t e = 0; e < E; e++)
+      if (moe_load_expert(c, layer, e, gate + e * gb, up + e * gb, down + e * db) != MOE_OK)
+        throw Error(MOE_ERROR, c->err);
+    if (g.has_shared) {
+      const uint8_t *sg = tensor("ffn_gate_shexp.weight", g.sh_gate_type, {H, F});
+      const uint8_t *su = tensor("ffn_up_shexp.weight", g.sh_gate_type, {H, F});
+      const uint8_t *sd = tensor("ffn_down_shexp.weight", g.sh_down_type, {F, H});
+      if (moe_load_expert(c, layer, (uint32_t)E, sg, su, sd) != MOE_OK) throw Error(MOE_ERROR, c->err);
+    }
+  });
+}
+
 MOE_API moe_status moe_forward(moe_ctx *c, uint32_t layer, const float *x, uint32_t ntok, uint64_t x_stride, float *y,
                                uint64_t y_stride, moe_route_out *route) {
   return guarded(c, [&] {
@@ -1099,6 +1139,9 @@ MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap) {
       ROW(moe_expert_weights, down), ROW(moe_expert_weights, down_parts), ROW(moe_expert_weights, down_blocks),
       STRUCT(moe_expert_weights),    ROW(moe_cm_job, expert),       ROW(moe_cm_job, tok),
       ROW(moe_cm_job, w),            STRUCT(moe_cm_job),
+      ROW(gguf_tensor_info, name),   ROW(gguf_tensor_info, type),   ROW(gguf_tensor_info, n_dims),
+      ROW(gguf_tensor_info, shape),  ROW(gguf_tensor_info, shard),  ROW(gguf_tensor_info, offset),
+      ROW(gguf_tensor_info, bytes),  ROW(gguf_tensor_info, data),   STRUCT(gguf_tensor_info),
       ROW(moe_route_out, ids),       ROW(moe_route_out, w),         STRUCT(moe_route_out),
       ROW(moe_job, layer),           ROW(moe_job, expert),          ROW(moe_job, tok),
       ROW(moe_job, w),               STRUCT(moe_job),               ROW(MoeTile, expert),

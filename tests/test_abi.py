@@ -16,18 +16,18 @@ from tests import harness as h
 from tests.harness import moe
 from c0ven_amd import _lib
 
-HEADER = os.path.join(h.ROOT, "include", "c0ven_moe.h")
+HEADERS = [os.path.join(h.ROOT, "include", f) for f in ("c0ven_moe.h", "c0ven_gguf.h")]
 
 
 def declared():
-    text = open(HEADER).read()
-    return set(re.findall(r"MOE_API\s+[\w\s\*]+?\b(moe_\w+)\s*\(", text))
+    text = "".join(open(f).read() for f in HEADERS)
+    return set(re.findall(r"MOE_API\s+[\w\s\*]+?\b((?:moe|gguf)_\w+)\s*\(", text))
 
 
 def test_exports_match_header():
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
                          check=True).stdout
-    exported = {l.split()[-1] for l in out.splitlines() if l.split()[-1].startswith("moe_")}
+    exported = {l.split()[-1] for l in out.splitlines() if l.split()[-1].startswith(("moe_", "gguf_"))}
     want = declared()
     assert len(want) >= 25
     assert exported == want
@@ -40,7 +40,8 @@ def test_struct_layout_matches_ctypes():
     rows = {name: (off, size) for name, off, size in moe.abi_layout()}
     mirrors = {"moe_config": _lib.MoeConfig, "moe_route_out": _lib.MoeRouteOut, "moe_job": _lib.MoeJob,
                "MoeTile": _lib.MoeTile, "MoeGroup": _lib.MoeGroup, "moe_abi_row": _lib.MoeAbiRow,
-               "moe_expert_weights": _lib.MoeExpertWeights, "moe_cm_job": _lib.MoeCmJob}
+               "moe_expert_weights": _lib.MoeExpertWeights, "moe_cm_job": _lib.MoeCmJob,
+               "gguf_tensor_info": _lib.GgufTensorInfo}
     for sname, cls in mirrors.items():
         assert rows[sname] == (0, C.sizeof(cls)), sname
         for fname, _ in cls._fields_:
