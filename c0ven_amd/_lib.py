@@ -34,7 +34,7 @@ class MoeConfig(C.Structure):
         ("n_layer", C.c_uint32), ("gate_type", C.c_uint32), ("down_type", C.c_uint32), ("has_shared", C.c_uint32),
         ("sh_gate_type", C.c_uint32), ("sh_down_type", C.c_uint32), ("max_tokens", C.c_uint32),
         ("swiglu_limit", C.c_float), ("device", C.c_int32), ("borrowed_immutable", C.c_uint32),
-        ("reserved", C.c_uint32 * 3),
+        ("hc_lr", C.c_uint32), ("reserved", C.c_uint32 * 2),
     ]
 
 
@@ -108,6 +108,9 @@ _SIGS = {
     "moe_row_bytes": (_u64, [_u32, _u32]),
     "moe_abi_layout": (_u32, [C.POINTER(MoeAbiRow), _u32]),
     "moe_load_layer_gguf": (_i32, [_P, _u32, _P, _u32]),
+    "moe_load_hc": (_i32, [_P, _u32, _P, _P, _P, _P]),
+    "moe_forward_hc_async": (_i32, [_P, _u32, _P, _u32, _P, _P, _P, _P]),
+    "moe_forward_hc": (_i32, [_P, _u32, _P, _u32, _P, C.POINTER(MoeRouteOut)]),
     "gguf_open": (_i32, [C.c_char_p, C.POINTER(_P)]),
     "gguf_close": (None, [_P]),
     "gguf_last_error": (C.c_char_p, [_P]),
@@ -284,13 +287,14 @@ class MoeBlock:
     """One context of the HIP MoE block (moe_open .. moe_close)."""
 
     def __init__(self, n_embd, n_ff, n_expert, n_used, gate_type, down_type, has_shared=True, sh_gate_type=None,
-                 sh_down_type=None, n_layer=1, max_tokens=16, swiglu_limit=0.0, device=0, borrowed_immutable=0):
+                 sh_down_type=None, n_layer=1, max_tokens=16, swiglu_limit=0.0, device=0, borrowed_immutable=0,
+                 hc_lr=0):
         self.cfg = MoeConfig(n_embd=n_embd, n_ff=n_ff, n_expert=n_expert, n_used=n_used, n_layer=n_layer,
                              gate_type=gate_type, down_type=down_type, has_shared=1 if has_shared else 0,
                              sh_gate_type=sh_gate_type if sh_gate_type is not None else gate_type,
                              sh_down_type=sh_down_type if sh_down_type is not None else down_type,
                              max_tokens=max_tokens, swiglu_limit=swiglu_limit, device=device,
-                             borrowed_immutable=borrowed_immutable)
+                             borrowed_immutable=borrowed_immutable, hc_lr=hc_lr)
         h = _P()
         st = lib.moe_open(C.byref(self.cfg), C.byref(h))
         if st != MOE_OK:
@@ -330,6 +334,28 @@ class MoeBlock:
         ro = MoeRouteOut(ids.ctypes.data_as(C.POINTER(C.c_int32)), w.ctypes.data_as(C.POINTER(C.c_float)))
         self._check(lib.moe_forward(self.h, layer, _ptr(x), T, H, _ptr(y), H, C.byref(ro)))
         return y, ids, w
+
+    def load_hc(self, layer, gamma, w_down, w_inject, w_up):
+        """The layer's hyper-connection module: gamma (4 H fp32), W_down (lr x 4H), W_inject (4 x 4H), W_up (4H x lr)
+        as bf16 bits (uint16)."""
+        args = [np.ascontiguousarray(gamma, dtype=np.float32)] + [np.ascontiguousarray(a, dtype=np.uint16)
+                                                                  for a in (w_down, w_inject, w_up)]
+        self._check(lib.moe_load_hc(self.h, layer, *[_ptr(a) for a in args]))
+
+    def forward_hc(self, layer, R):
+        """The block with its hyper-connection mix and combine: R (T x 4 x H) in; R updated, y, ids, w out."""
+        R = np.array(R, dtype=np.float32, copy=True, order="C")
+        T = R.shape[0]
+        H, K = self.cfg.n_embd, self.cfg.n_used
+        y = np.empty((T, H), dtype=np.float32)
+        ids = np.empty((T, K), dtype=np.int32)
+        w = np.empty((T, K), dtype=np.float32)
+        ro = MoeRouteOut(ids.ctypes.data_as(C.POINTER(C.c_int32)), w.ctypes.data_as(C.POINTER(C.c_float)))
+        self._check(lib.moe_forward_hc(self.h, layer, _ptr(R), T, _ptr(y), C.byref(ro)))
+        return R, y, ids, w
+
+    def forward_hc_async(self, layer, R_dev, ntok, y_dev=None, ids_dev=None, w_dev=None, stream=None):
+        self._check(lib.moe_forward_hc_async(self.h, layer, R_dev, ntok, y_dev, ids_dev, w_dev, stream))
 
     def forward_async(self, layer, x_dev, ntok, y_dev, ids_dev=None, w_dev=None, stream=None):
         self._check(lib.moe_forward_async(self.h, layer, x_dev, ntok, y_dev, ids_dev, w_dev, stream))

@@ -45,6 +45,10 @@ struct Layer {
   bool has_bias = false;
   uint8_t *experts = nullptr;
   uint8_t *shared = nullptr;
+  // The hyper-connection module before the block (hc_lr > 0).
+  float *hc_gamma = nullptr;
+  uint16_t *hc_down = nullptr, *hc_inj = nullptr, *hc_up = nullptr;
+  bool has_hc = false;
 };
 
 constexpr uint32_t kMaxPrefillTokens = 16384;  // tokens one forward takes (one prefill chunk)
@@ -200,6 +204,9 @@ struct moe_ctx {
   uint64_t epoch = 0;          // the last launch's number
   std::vector<std::pair<uint64_t *, uint64_t>> tagged;  // the tagged-record buffers (pointer, records)
   uint32_t grid = 0;           // co-resident work-groups of moe_decode
+  float *hc_n = nullptr, *hc_l = nullptr, *hc_x = nullptr;  // the hyper-connection mix's scratch (hc_lr > 0)
+  uint32_t *cnt_hc = nullptr;
+  float *hc_R_stage = nullptr;  // moe_forward_hc's device copy of R
   uint8_t *codebooks = nullptr;  // the caller's iq2s_grid and iq3xxs_grid (QGRID layout, up to QGRID_IQ3S)
   bool have_codebooks = false;
   const void *kernel = nullptr;  // moe_decode for the context's set of weight types
@@ -207,6 +214,7 @@ struct moe_ctx {
   int timing = 0;  // 0 off, 1 every kernel, 2 the decode kernel and the prefill gate/up launches
   uint64_t *trace = nullptr;   // per-item stamps of the last forward, when tracing
   uint32_t trace_cap = 0, last_T = 0, last_route = 1;
+  bool last_hc = false;
   std::vector<hipEvent_t> ev;  // the event pool
   size_t ev_next = 0;          // events of the pool in use by the record
   std::vector<TimedLaunch> timed;
@@ -270,6 +278,7 @@ void validate(const moe_config &c) {
           "shared expert types must be Q8_0, Q4_K, IQ3_S, IQ4_NL or Q2_0");
   require(c.max_tokens <= kMaxPrefillTokens, "max_tokens must be at most 16384");
   require(c.swiglu_limit >= 0.0f, "swiglu_limit must be >= 0");
+  require(c.hc_lr <= kHcMaxLr && c.hc_lr % 8 == 0, "hc_lr must be a multiple of 8, at most 512");
 }
 
 // Types that decode through the caller's codebooks need them set first.
@@ -357,7 +366,7 @@ void launch(moe_ctx *c, const DecodeParams &p, hipStream_t s) {
   }
   q.tag = (uint32_t)q.epoch;
   if (c->trace) q.trace = c->trace, q.trace_cap = c->trace_cap;
-  c->last_T = p.T, c->last_route = p.route;
+  c->last_T = p.T, c->last_route = p.route, c->last_hc = p.hc_R != nullptr;
   if (c->timing) timing_hook(c, "moe_decode", 0, s);
   void *args[] = {&q};
   check(hipLaunchKernel(c->kernel, dim3(c->grid), dim3(kWG), args, c->lds, s), "moe_decode launch");
@@ -460,6 +469,12 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
       if (g.has_shared) L.shared = c->alloc<uint8_t>(c->sh_bytes);
       check(hipMemset(L.experts, 0, c->ex_bytes * E), "hipMemset");
       if (L.shared) check(hipMemset(L.shared, 0, c->sh_bytes), "hipMemset");
+      if (g.hc_lr) {
+        L.hc_gamma = c->alloc<float>((uint64_t)kHcStreams * H);
+        L.hc_down = c->alloc<uint16_t>((uint64_t)g.hc_lr * kHcStreams * H);
+        L.hc_inj = c->alloc<uint16_t>((uint64_t)kHcStreams * kHcStreams * H);
+        L.hc_up = c->alloc<uint16_t>((uint64_t)kHcStreams * H * g.hc_lr);
+      }
     }
     // Scratch for max_tokens tokens of n_used + 1 assignments (the pre-routed path may give a token its shared
     // expert as a job).
@@ -527,12 +542,21 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     c->flags = c->alloc<uint64_t>(kFlagCount);
     check(hipMemset(c->flags, 0, kFlagCount * sizeof(uint64_t)), "hipMemset");
     c->codebooks = c->alloc<uint8_t>(QGRID_IQ3S);
+    if (g.hc_lr) {
+      c->hc_n = c->alloc<float>((uint64_t)T * kHcStreams * H);
+      c->hc_l = c->alloc<float>((uint64_t)T * (g.hc_lr + kHcStreams));
+      c->hc_x = c->alloc<float>((uint64_t)T * H);
+      c->cnt_hc = c->alloc<uint32_t>(2 * kDynStride);
+      c->hc_R_stage = c->alloc<float>((uint64_t)T * kHcStreams * H);
+      check(hipMemset(c->cnt_hc, 0, 2 * kDynStride * sizeof(uint32_t)), "hipMemset");
+    }
     c->tagged = {{c->logits, (uint64_t)T * (E + 1)}, {c->gs, T}, {c->ids_t, (uint64_t)T * K1}, {c->w_t, (uint64_t)T * K1},
                  {c->h, (uint64_t)A * F}, {c->y_asg, (uint64_t)A * H}, {(uint64_t *)c->cnt_dyn, kDynLists * kDynStride}};  // (and both sets of list counters)
     clear_tagged(c, nullptr);
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
-    c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * act_tok_stride(Ug) +
+    const size_t hc_lds = g.hc_lr ? ((size_t)T * g.hc_lr + (size_t)T * kHcStreams * kHcUpValues) * 4 : 0;
+    c->lds = std::max<size_t>({hc_lds, (size_t)MOE_GROUP_MAX * act_tok_stride(Ug) +
                                    std::max<size_t>(Ug == 8 ? kMfmaXchBytes : 0, gate_up_xch_bytes(unit_lanes(Ug))),
                                (size_t)MOE_GROUP_MAX * act_tok_stride(Ud), kGroupingLds});
     int per_cu = 0, ncu = 0;
@@ -670,6 +694,70 @@ MOE_API moe_status moe_forward_async(moe_ctx *c, uint32_t layer, const float *x_
   return guarded(c, [&] {
     require(x_dev && y_dev, "null x or y");
     forward_dev(c, layer, x_dev, ntok, y_dev, ids_dev, w_dev, stream ? (hipStream_t)stream : c->stream);
+  });
+}
+
+MOE_API moe_status moe_load_hc(moe_ctx *c, uint32_t layer, const float *gamma, const uint16_t *w_down,
+                               const uint16_t *w_inject, const uint16_t *w_up) {
+  return guarded(c, [&] {
+    const moe_config &g = c->cfg;
+    require(g.hc_lr > 0, "the context has no hyper-connection module (hc_lr = 0)");
+    require(layer < g.n_layer && gamma && w_down && w_inject && w_up, "bad layer or null tensor");
+    Layer &L = c->layers[layer];
+    const uint64_t D = (uint64_t)kHcStreams * g.n_embd;
+    check(hipMemcpy(L.hc_gamma, gamma, D * sizeof(float), hipMemcpyHostToDevice), "upload hc gamma");
+    check(hipMemcpy(L.hc_down, w_down, (uint64_t)g.hc_lr * D * 2, hipMemcpyHostToDevice), "upload hc down");
+    check(hipMemcpy(L.hc_inj, w_inject, (uint64_t)kHcStreams * D * 2, hipMemcpyHostToDevice), "upload hc inject");
+    check(hipMemcpy(L.hc_up, w_up, D * g.hc_lr * 2, hipMemcpyHostToDevice), "upload hc up");
+    L.has_hc = true;
+  });
+}
+
+MOE_API moe_status moe_forward_hc_async(moe_ctx *c, uint32_t layer, float *R_dev, uint32_t ntok, float *y_dev,
+                                        int32_t *ids_dev, float *w_dev, void *stream) {
+  return guarded(c, [&] {
+    const moe_config &g = c->cfg;
+    require(R_dev != nullptr, "null R");
+    require(layer < g.n_layer && c->layers[layer].router != nullptr, "layer out of range or its router not loaded");
+    require(c->layers[layer].has_hc, "the layer's hyper-connection module is not loaded (moe_load_hc)");
+    require(ntok >= 1 && ntok <= c->tdec, "moe_forward_hc_async takes 1..min(max_tokens, 16) tokens");
+    need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_down_type : 0u});
+    const Layer &L = c->layers[layer];
+    hipStream_t s = stream ? (hipStream_t)stream : c->stream;
+    DecodeParams p = base_params(c, layer, ntok);
+    p.hc_R = R_dev, p.hc_gamma = L.hc_gamma, p.hc_down = L.hc_down, p.hc_inj = L.hc_inj, p.hc_up = L.hc_up;
+    p.hc_lr = g.hc_lr, p.hc_n = c->hc_n, p.hc_l = c->hc_l, p.hc_x = c->hc_x, p.cnt_hc = c->cnt_hc;
+    p.x = c->hc_x, p.y = y_dev;
+    launch(c, p, s);
+    c->last_ids = c->ids, c->last_w = c->w;
+    if (c->timing) c->ev_used++;
+    const uint32_t K = g.n_used;
+    if (ids_dev) check(hipMemcpyAsync(ids_dev, c->ids, sizeof(int32_t) * ntok * K, hipMemcpyDeviceToDevice, s), "ids");
+    if (w_dev) check(hipMemcpyAsync(w_dev, c->w, sizeof(float) * ntok * K, hipMemcpyDeviceToDevice, s), "w");
+  });
+}
+
+MOE_API moe_status moe_forward_hc(moe_ctx *c, uint32_t layer, float *R, uint32_t ntok, float *y, moe_route_out *route) {
+  return guarded(c, [&] {
+    require(R != nullptr && c->cfg.hc_lr > 0, "null R or no hyper-connection module");
+    require(ntok >= 1 && ntok <= c->tdec, "moe_forward_hc takes 1..min(max_tokens, 16) tokens");
+    const uint64_t rb = (uint64_t)ntok * kHcStreams * c->cfg.n_embd * sizeof(float);
+    const uint32_t K = c->cfg.n_used;
+    check(hipMemcpyAsync(c->hc_R_stage, R, rb, hipMemcpyHostToDevice, c->stream), "upload R");
+    if (moe_forward_hc_async(c, layer, c->hc_R_stage, ntok, y ? c->y_dev : nullptr, nullptr, nullptr, c->stream) !=
+        MOE_OK)
+      throw Error(MOE_BAD_ARGUMENT, c->err);
+    check(hipMemcpyAsync(R, c->hc_R_stage, rb, hipMemcpyDeviceToHost, c->stream), "download R");
+    if (y)
+      check(hipMemcpyAsync(y, c->y_dev, (uint64_t)ntok * c->cfg.n_embd * sizeof(float), hipMemcpyDeviceToHost,
+                           c->stream),
+            "download y");
+    if (route && route->ids)
+      check(hipMemcpyAsync(route->ids, c->ids, sizeof(int32_t) * ntok * K, hipMemcpyDeviceToHost, c->stream), "ids");
+    if (route && route->w)
+      check(hipMemcpyAsync(route->w, c->w, sizeof(float) * ntok * K, hipMemcpyDeviceToHost, c->stream), "w");
+    check(hipStreamSynchronize(c->stream), "forward_hc");
+    check_err(c);
   });
 }
 
@@ -1042,9 +1130,10 @@ MOE_API moe_status moe_trace(moe_ctx *c, uint64_t *stamps, uint32_t cap, uint32_
     const uint32_t T = c->last_T, Ug = unit_lanes(units_of(g.n_embd)), Ud = unit_lanes(units_of(g.n_ff));
     const uint32_t nL = lead_items(T, g.n_expert, c->last_route), ns = shared_chunks(T, c->last_route, g.has_shared);
     const uint32_t nGU = g.n_ff / gate_up_rows(Ug), nD = g.n_embd / down_rows(Ud);
-    const uint32_t b1 = nL + (c->last_route ? T : 0), b2 = b1 + ns * nGU, b3 = b2 + ns * nD, b4 = b3 + ng * nGU;
+    const uint32_t nH = c->last_hc ? hc_items(T, g.n_embd, g.hc_lr) : 0;  // the hyper-connection items come first
+    const uint32_t b1 = nH + nL + (c->last_route ? T : 0), b2 = b1 + ns * nGU, b3 = b2 + ns * nD, b4 = b3 + ng * nGU;
     const uint32_t b5 = b4 + ng * nD, end = b5 + T * nD;
-    const uint32_t bb[8] = {0, nL, b1, b2, b3, b4, b5, end};
+    const uint32_t bb[8] = {nH, nH + nL, b1, b2, b3, b4, b5, end};
     if (bounds) std::memcpy(bounds, bb, sizeof bb);
     *n = std::min(end, c->trace_cap);
     if (stamps)
@@ -1134,7 +1223,8 @@ MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap) {
       ROW(moe_config, n_used),       ROW(moe_config, n_layer),      ROW(moe_config, gate_type),
       ROW(moe_config, down_type),    ROW(moe_config, has_shared),   ROW(moe_config, sh_gate_type),
       ROW(moe_config, sh_down_type), ROW(moe_config, max_tokens),   ROW(moe_config, swiglu_limit),
-      ROW(moe_config, device),       ROW(moe_config, borrowed_immutable), ROW(moe_config, reserved),
+      ROW(moe_config, device),       ROW(moe_config, borrowed_immutable), ROW(moe_config, hc_lr),
+      ROW(moe_config, reserved),
       STRUCT(moe_config),            ROW(moe_expert_weights, gate), ROW(moe_expert_weights, up),
       ROW(moe_expert_weights, down), ROW(moe_expert_weights, down_parts), ROW(moe_expert_weights, down_blocks),
       STRUCT(moe_expert_weights),    ROW(moe_cm_job, expert),       ROW(moe_cm_job, tok),

@@ -313,21 +313,19 @@ template <uint32_t kTypes>
 __device__ __forceinline__ void quantise_x(const DecodeParams &p, uint32_t t) {
   const uint32_t H = p.H, l32 = tid() & 31u;
   for (uint32_t u = tid() / 32; u < H / kUnit; u += kWG / 32) {
-    const float4 *src = (const float4 *)(p.x + (uint64_t)t * H + u * kUnit + 8 * l32);
-    const float4 a = src[0], b = src[1];
+    float4 a, b;
+    const uint64_t e = (uint64_t)t * H + u * kUnit + 8 * l32;
+    if (p.hc_R) {  // x from this launch's up items
+      const uint4 ua = ld_co16(p.x, (uint32_t)(4 * e)), ub = ld_co16(p.x, (uint32_t)(4 * e + 16));
+      a = make_float4(__uint_as_float(ua.x), __uint_as_float(ua.y), __uint_as_float(ua.z), __uint_as_float(ua.w));
+      b = make_float4(__uint_as_float(ub.x), __uint_as_float(ub.y), __uint_as_float(ub.z), __uint_as_float(ub.w));
+    } else {
+      a = ((const float4 *)(p.x + e))[0], b = ((const float4 *)(p.x + e))[1];
+    }
     const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     quant_unit(v, l32, act_type<kTypes>(p.xact_r), p.act_r + ((uint64_t)t * (H / kUnit) + u) * kActBytes);
     if (p.act_s != p.act_r) quant_unit(v, l32, act_type<kTypes>(p.xact_s), p.act_s + ((uint64_t)t * (H / kUnit) + u) * kActBytes);
   }
-}
-
-// A double summed over the 16 lanes of its row (butterflies: lane ^ 1, ^ 2, then the mirrors of 8 and 16); every lane
-// of the row receives it.
-__device__ __forceinline__ double row16_sum_f64(double v) {
-  v = __dadd_rn(v, dpp_f64<kDppXor1>(v));
-  v = __dadd_rn(v, dpp_f64<kDppXor2>(v));
-  v = __dadd_rn(v, dpp_f64<kDppHalfMirror>(v));
-  return __dadd_rn(v, dpp_f64<kDppMirror>(v));
 }
 
 // Eight doubles of every lane summed over the 16 lanes of its row, by halving exchanges (the partner across the row's
@@ -350,19 +348,30 @@ __device__ __forceinline__ double row16_reduce8_f64(double v[8]) {
   return __dadd_rn(v[0], dpp_f64<kDppXor1>(v[0]));
 }
 
-// Router dot products of row `row` with tokens t0 .. t0 + nt - 1 (nt <= 16): tot[t] = sum over the row of
+// Dot products of a bf16 row W of K values (a multiple of 512) with tokens t0 .. t0 + nt - 1 (nt <= 16) of x (rows
+// ldx apart; read past the caches when co, for x written in this launch): tot[t] = sum over the row of
 // bf16(W) bf16(x), each product exact, summed in fp64. Wave w takes the 512-value chunks w, w + 4, ..., lane l values
 // 8 l .. 8 l + 7 of each: a lane converts its weights once for all tokens. Eight tokens at a time (x of four in flight
 // while four are used), each chunk's eight sums are reduced over the 16 lanes of a row (one value a lane pair left) and
 // added to that row of lanes' partial in LDS; the sixteen partials of an output (four rows of lanes, four waves) are
 // then added in a fixed order.
-__device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, uint32_t t0, uint32_t nt, double *part,
-                                           double *tot) {
-  const uint32_t lane = lane_id(), wv = wave_id(), H = p.H, nC = H / 512;
+__device__ __forceinline__ void bf16_dot(const uint16_t *W, const float *x, uint32_t K, uint32_t ldx, bool co,
+                                         uint32_t t0, uint32_t nt, double *part, double *tot) {
+  const uint32_t lane = lane_id(), wv = wave_id(), nC = K / 512;
   const uint32_t pslot = 4 * wv + lane / 16;
+  // Values 8 lane .. + 7 of chunk c of token t, as two float4.
+  const auto ldx8 = [&](uint32_t t, uint32_t c, float4 &a, float4 &b) {
+    const uint64_t e = (uint64_t)t * ldx + 512 * c + 8 * lane;
+    if (co) {
+      const uint4 u = ld_co16(x, (uint32_t)(4 * e)), v = ld_co16(x, (uint32_t)(4 * e + 16));
+      a = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+      b = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    } else {
+      a = ((const float4 *)(x + e))[0], b = ((const float4 *)(x + e))[1];
+    }
+  };
   for (uint32_t c = wv; c < nC; c += kWG / 64) {
-    const uint4 wa = *(const uint4 *)(p.router + (uint64_t)row * H + 512 * c + 8 * lane);
-    const float *xc = p.x + (uint64_t)t0 * H + 512 * c + 8 * lane;
+    const uint4 wa = *(const uint4 *)(W + 512 * c + 8 * lane);
     double wd[8];
     {
       const uint32_t w0[4] = {wa.x, wa.y, wa.z, wa.w};
@@ -374,18 +383,12 @@ __device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, 
       double v[8];
       float4 xq[2][4][2];
 #pragma unroll
-      for (uint32_t tt = 0; tt < 4; tt++) {
-        const float4 *q = (const float4 *)(xc + (uint64_t)(tb + min(tt, nb - 1)) * H);
-        xq[0][tt][0] = q[0], xq[0][tt][1] = q[1];
-      }
+      for (uint32_t tt = 0; tt < 4; tt++) ldx8(t0 + tb + min(tt, nb - 1), c, xq[0][tt][0], xq[0][tt][1]);
 #pragma unroll
       for (uint32_t tt = 0; tt < 8; tt++) {
         if (tt == 0 && nb > 4) {
 #pragma unroll
-          for (uint32_t u = 0; u < 4; u++) {
-            const float4 *q = (const float4 *)(xc + (uint64_t)(tb + min(4 + u, nb - 1)) * H);
-            xq[1][u][0] = q[0], xq[1][u][1] = q[1];
-          }
+          for (uint32_t u = 0; u < 4; u++) ldx8(t0 + tb + min(4 + u, nb - 1), c, xq[1][u][0], xq[1][u][1]);
         }
         double a = 0.0;
         if (tt < nb) {
@@ -398,20 +401,17 @@ __device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, 
         }
         v[tt] = a;
       }
-      double s;
-      uint32_t tt;
-      if (nb == 1) {
-        s = row16_sum_f64(v[0]), tt = 0;
-      } else {
-        s = row16_reduce8_f64(v), tt = (lane & 15u) / 2;
-      }
-      if ((lane & (nb == 1 ? 15u : 1u)) == 0 && tt < nb) {
+      // One tree for every token count (tokens past nb add zeros), so a token's sum does not depend on T:
+      // ((P0 + P7) + (P3 + P4)) + ((P1 + P6) + (P2 + P5)), P_m = a_m + a_(15 - m) over the row's 16 lanes.
+      const double s = row16_reduce8_f64(v);
+      const uint32_t tt = (lane & 15u) / 2;
+      if ((lane & 1u) == 0 && tt < nb) {
         double *q = part + (tb + tt) * 16 + pslot;
         *q = c == wv ? s : __dadd_rn(*q, s);
       }
     }
   }
-  if (wv >= nC && (lane & 15u) == 0) {  // waves without a chunk (H < 2048) give zeros
+  if (wv >= nC && (lane & 15u) == 0) {  // waves without a chunk (K < 2048) give zeros
     for (uint32_t t = 0; t < nt; t++) part[t * 16 + pslot] = 0.0;
   }
   __syncthreads();
@@ -423,6 +423,116 @@ __device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, 
     tot[j] = s;
   }
   __syncthreads();
+}
+
+// Router row `row` (row E: the shared gate) against tokens t0 .. t0 + nt - 1 of x.
+__device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, uint32_t t0, uint32_t nt, double *part,
+                                           double *tot) {
+  bf16_dot(p.router + (uint64_t)row * p.H, p.x, p.H, p.H, p.hc_R != nullptr, t0, nt, part, tot);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Hyper-connection items (the mix before the block; its combine is in combine_item)
+
+// A double summed over the work-group in a fixed order (each wave's lanes by halving exchanges, then the four waves
+// in order); every thread receives it. red: 4 doubles of LDS.
+__device__ __forceinline__ double wg_sum_f64(double v, double *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = __dadd_rn(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if (lane_id() == 0) red[wave_id()] = v;
+  __syncthreads();
+  return __dadd_rn(__dadd_rn(red[0], red[1]), __dadd_rn(red[2], red[3]));
+}
+
+// Norm item t: each stream s of token t as RMSNorm(R_s) gamma_s (MODEL_LAYER.md 1.1 step 1; ggml_compute_forward_
+// rms_norm_f32: the squares summed in double, mean = sum / H rounded to fp32, scale = 1 / sqrtf(mean + 1e-6), then
+// (R scale) gamma), stored for the down and up items.
+__device__ __forceinline__ void hc_norm_item(const DecodeParams &p, uint32_t t, double *red) {
+  const uint32_t H = p.H;
+  for (uint32_t s = 0; s < kHcStreams; s++) {
+    const float *R = p.hc_R + ((uint64_t)t * kHcStreams + s) * H;
+    double ss = 0.0;
+    for (uint32_t i = tid(); i < H; i += kWG) {
+      const float v = R[i];
+      ss = __dadd_rn(ss, (double)__fmul_rn(v, v));
+    }
+    ss = wg_sum_f64(ss, red);
+    const float mean = (float)(ss / (double)H);
+    // sqrtf is the correctly rounded square root here (__fsqrt_rn is the hardware approximation in this build).
+    const float scale = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, 1e-6f)));
+    float *n = p.hc_n + ((uint64_t)t * kHcStreams + s) * H;
+    for (uint32_t i = tid(); i < H; i += kWG) st_co(n + i, __fmul_rn(__fmul_rn(R[i], scale), p.hc_gamma[s * H + i]));
+  }
+  set_flag(p, kFlagHcNorm + t);
+}
+
+// Down item r (after every norm item): row r of W_down (r < lr) or of W_inject (r - lr) against bf16(n) of every
+// token, in fp64 as the router's rows; W_down's rows become silu(v / 4) (1.1 step 2), the inject rows stay logits
+// (step 4). The last down item in raises kFlagHcDown.
+__device__ __forceinline__ void hc_down_item(const DecodeParams &p, uint32_t r, double *part, double *tot,
+                                             const uint64_t *tab, uint32_t *s_flag) {
+  const uint32_t K = kHcStreams * p.H, lr = p.hc_lr;
+  wait_flags(p, kFlagHcNorm, p.T);
+  const uint16_t *W = r < lr ? p.hc_down + (uint64_t)r * K : p.hc_inj + (uint64_t)(r - lr) * K;
+  bf16_dot(W, p.hc_n, K, K, true, 0, p.T, part, tot);
+  const uint32_t t = tid();
+  if (t < p.T) {
+    const float v = (float)tot[t];
+    float o = v;
+    if (r < lr) {  // silu(v / 4): the quarter is exact; silu(z) = z / (1 + e^-z)
+      const float z = __fmul_rn(v, 0.25f);
+      o = __fdiv_rn(z, __fadd_rn(1.0f, expf_libm(-z, tab)));
+    }
+    st_co(p.hc_l + (uint64_t)t * (lr + kHcStreams) + r, o);
+  }
+  if (arrive_last(p.cnt_hc, lr + kHcStreams, s_flag)) set_flag(p, kFlagHcDown);
+}
+
+// Up item j (after the down items): values i = kHcUpValues j .. + kHcUpValues - 1 of x. Rows s H + i of W_up (one a
+// quarter of the threads, the tokens dealt to the four threads of a row) against bf16(l) of every token in fp64,
+// k ascending; then x[i] = (sum over s in order of n_s[i] sigma(a_s[i])) / 4 (1.1 step 3). The last up item in raises
+// kFlagHcX.
+__device__ __forceinline__ void hc_up_item(const DecodeParams &p, uint32_t j, uint8_t *lds, const uint64_t *tab,
+                                           uint32_t *s_flag) {
+  const uint32_t H = p.H, T = p.T, lr = p.hc_lr, lw = lr + kHcStreams, i0 = kHcUpValues * j;
+  wait_flag(p, kFlagHcDown);
+  float *lb = (float *)lds;                                   // [t][k] bf16(l) as floats
+  float *a = lb + T * lr;                                     // [t][s][i - i0]
+  for (uint32_t e = tid(); e < T * lr; e += kWG) lb[e] = round_bf16(ld_co(p.hc_l + (uint64_t)(e / lr) * lw + e % lr));
+  __syncthreads();
+  {
+    const uint32_t rr = tid() / 4, q = tid() % 4;  // row rr of the item's 4 kHcUpValues (64), token group q
+    const uint32_t s = rr / kHcUpValues, i = i0 + rr % kHcUpValues;
+    const uint16_t *W = p.hc_up + ((uint64_t)s * H + i) * lr;
+    for (uint32_t t = q; t < T; t += 4) {
+      double acc = 0.0;
+      for (uint32_t k = 0; k < lr; k += 8) {
+        const uint4 w = *(const uint4 *)(W + k);
+        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+          const float wf = __uint_as_float((m & 1) ? wv[m / 2] & 0xffff0000u : wv[m / 2] << 16);
+          acc = __builtin_fma((double)wf, (double)lb[t * lr + k + m], acc);
+        }
+      }
+      a[(t * kHcStreams + s) * kHcUpValues + rr % kHcUpValues] = (float)acc;
+    }
+  }
+  __syncthreads();
+  {
+    const uint32_t t = tid() / kHcUpValues, di = tid() % kHcUpValues, i = i0 + di;
+    if (t < T) {
+      float acc = 0.0f;
+#pragma unroll
+      for (uint32_t s = 0; s < kHcStreams; s++) {
+        const float n = ld_co(p.hc_n + ((uint64_t)t * kHcStreams + s) * H + i);
+        acc = __fadd_rn(acc, __fmul_rn(n, sigmoid_libm(a[(t * kHcStreams + s) * kHcUpValues + di], tab)));
+      }
+      st_co(p.hc_x + (uint64_t)t * H + i, __fmul_rn(acc, 0.25f));
+    }
+  }
+  if (arrive_last(p.cnt_hc + kDynStride, H / kHcUpValues, s_flag)) set_flag(p, kFlagHcX);
 }
 
 // Lead item i: router row i for all T tokens, plus the bias.
@@ -834,7 +944,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
 // per-assignment outputs are polled as tagged records (one first, then all of the row's). The combine items come after
 // every down item, so what they wait for has a smaller number.
 __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, uint32_t blk, float *wl,
-                                             uint64_t *mark) {
+                                             const uint64_t *tab, uint64_t *mark) {
   const uint32_t rows = down_rows(unit_lanes(units_of(p.F))), K = p.K, row = blk * rows + tid();
   const uint32_t ns = p.has_shared ? 1u : 0u;
   {
@@ -846,6 +956,10 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
       wl[kMaxUsed + 1 + k] = on ? 1.0f : 0.0f;
     } else if (k == K && ns) {  // thread K: the shared expert's gate
       wl[K] = __uint_as_float(poll_tag(p, p.gs + t));
+    } else if (p.hc_R && k >= K + 1 && k < K + 1 + kHcStreams) {  // stream s's weight 2 sigma(inject_s / 4)
+      const uint32_t s = k - K - 1;
+      const float inj = ld_co(p.hc_l + (uint64_t)t * (p.hc_lr + kHcStreams) + p.hc_lr + s);
+      wl[2 * kMaxUsed + 1 + s] = __fmul_rn(2.0f, sigmoid_libm(__fmul_rn(inj, 0.25f), tab));
     }
   }
   if (p.route) wait_tag(p, p.y_asg + ((uint64_t)t * K + K - 1) * p.H + blk * rows + rows - 1);
@@ -887,7 +1001,14 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
     for (uint32_t k = 0; k < kMaxUsed; k++)
       if (on[k]) acc = __fadd_rn(acc, __fmul_rn(wv[k], yv[k]));
     if (ns) acc = __fadd_rn(acc, __fmul_rn(gs, ys));
-    p.y[(uint64_t)t * p.H + row] = acc;
+    if (p.y) p.y[(uint64_t)t * p.H + row] = acc;
+    if (p.hc_R) {  // the combine (MODEL_LAYER.md 1.2): R_s += 2 sigma(inject_s / 4) y
+#pragma unroll
+      for (uint32_t s = 0; s < kHcStreams; s++) {
+        float *r = p.hc_R + ((uint64_t)t * kHcStreams + s) * p.H + row;
+        *r = __fadd_rn(*r, __fmul_rn(wl[2 * kMaxUsed + 1 + s], acc));
+      }
+    }
   }
   if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
 }
@@ -902,7 +1023,8 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   __shared__ uint32_t grid_lds[(kTypes & kTypeIQ2) ? kGridWords : (kTypes & kTypeIQ3_S) ? 512 : 1];
   __shared__ uint32_t s_grid;  // the grid type whose codebook grid_lds holds
   __shared__ uint32_t s_flag;
-  __shared__ float s_wl[2 * kMaxUsed + 1];  // a combine item's weights (and gs), then which assignments are live
+  // A combine item's weights (and gs), which assignments are live, and the streams' weights 2 sigma(inject / 4).
+  __shared__ float s_wl[2 * kMaxUsed + 1 + kHcStreams];
   __shared__ double s_part[kMaxDecodeTokens * 16], s_tot[kMaxDecodeTokens];
   __shared__ GroupLds sg;
   __shared__ GroupTab gtab;
@@ -911,7 +1033,8 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   if (tid() == 0) s_grid = 0xffffffffu;
   __syncthreads();
   const uint32_t T = p.T, E = p.E, Ug = unit_lanes(units_of(p.H)), Ud = unit_lanes(units_of(p.F));
-  const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nL + nTop;
+  const uint32_t nH = p.hc_R ? hc_items(T, p.H, p.hc_lr) : 0u;  // the hyper-connection mix's items come first
+  const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nH + nL + nTop;
   const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud), nBlk = nD;  // combine items: T x nBlk
   const uint32_t ns = shared_chunks(T, p.route, p.has_shared), B2 = B1 + ns * (nGU + nD);
   // Items below B2 go round-robin (work-group b takes b, b + grid, ...). The routed items, whose cost varies with their
@@ -949,17 +1072,28 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
     }
     uint64_t *mark = p.trace && it < p.trace_cap ? p.trace + 4 * it : nullptr;
     if (mark && tid() == 0) mark[0] = mark[1] = mark[2] = __builtin_amdgcn_s_memrealtime();
-    if (it < nL) {
-      if (it < T) quantise_x<kTypes>(p, it);
+    if (it < nH) {
+      const uint32_t lw = p.hc_lr + kHcStreams;
+      if (it < T)
+        hc_norm_item(p, it, s_part);
+      else if (it < T + lw)
+        hc_down_item(p, it - T, s_part, s_tot, exp_tab, &s_flag);
+      else
+        hc_up_item(p, it - T - lw, lds, exp_tab, &s_flag);
+    } else if (it < nH + nL) {
+      const uint32_t li = it - nH;
+      if (nH) wait_flag(p, kFlagHcX);
+      if (li < T) quantise_x<kTypes>(p, li);
       if (p.route) {
-        if (it < E) router_row(p, it, s_part, s_tot);
+        if (li < E) router_row(p, li, s_part, s_tot);
         if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
-        set_flag(p, kFlagLead + it);
+        set_flag(p, kFlagLead + li);
       } else if (arrive_last(p.cnt_route, nL, &s_flag)) {
         set_flag(p, kFlagRouted);
       }
     } else if (it < B1) {
-      const uint32_t t = it - nL;
+      const uint32_t t = it - nH - nL;
+      if (nH) wait_flag(p, kFlagHcX);
       // The shared gate's logit (router row E) for this token while the lead items finish: gs = sigmoid of it.
       router_dot(p, E, t, 1, s_part, s_tot);
       if (tid() == 0) st_tag(p.gs + t, __float_as_uint(sigmoid_libm((float)s_tot[0], exp_tab)), p.tag);
@@ -984,7 +1118,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
         read_group(p, &gtab, false, i / nD, &sg);
         down_item<kTypes>(p, &sg, i % nD, lds, grid_lds, &s_grid, mark);
       } else {
-        combine_item(p, (i - ng * nD) / nBlk, (i - ng * nD) % nBlk, s_wl, mark);
+        combine_item(p, (i - ng * nD) / nBlk, (i - ng * nD) % nBlk, s_wl, exp_tab, mark);
       }
     }
     if (mark && tid() == 0) mark[3] = __builtin_amdgcn_s_memrealtime();

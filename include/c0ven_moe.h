@@ -64,7 +64,9 @@ typedef struct {
   uint32_t borrowed_immutable; /* 1: the bytes behind moe_compute_many's expert pointers do not change while the
                                 * context lives, so their device copies are kept (keyed by pointer) across calls;
                                 * 0: they are uploaded again on every call */
-  uint32_t reserved[3];
+  uint32_t hc_lr;        /* > 0: the layers hold a hyper-connection mix and combine of this low rank (at most 512, a
+                          * multiple of 8; the model's is 320) for moe_forward_hc */
+  uint32_t reserved[2];
 } moe_config;
 
 /* The routing result of a forward, per token: k expert ids in rank order and their weights. */
@@ -158,6 +160,22 @@ MOE_API uint32_t moe_h_rows(const moe_config *cfg);
  * order (the reference's fill takes atomic order). Synchronous. */
 MOE_API moe_status moe_prefill_dispatch(moe_ctx *ctx, MoeTile *tiles, uint32_t cap, uint32_t *ntiles, uint32_t *perm);
 
+/* The hyper-connection module before a layer's block (docs/spec/MODEL_LAYER.md 1.1-1.2; the hc_ffn_* tensors of
+ * blk.N): gamma 4 n_embd fp32 (hc_ffn_norm, the folded 1 + w), W_down hc_lr x 4 n_embd bf16, W_inject 4 x 4 n_embd
+ * bf16, W_up 4 n_embd x hc_lr bf16 (row s n_embd + i), each row-major as the file holds it. Needs hc_lr > 0. */
+MOE_API moe_status moe_load_hc(moe_ctx *ctx, uint32_t layer, const float *gamma, const uint16_t *w_down,
+                               const uint16_t *w_inject, const uint16_t *w_up);
+/* The block with its hyper-connection mix and combine fused into the decode launch (model.cpp:1350-1416: hc_mix, the
+ * block, hc_combine): R_dev (device, ntok x 4 x n_embd fp32, the residual streams) gives the block's input
+ * x = (1/4) sum_s n_s sigma(a_s) and receives R_s += 2 sigma(inject_s / 4) y. y_dev (ntok x n_embd, may be null),
+ * ids_dev and w_dev (may be null) receive y and the routing. 1 <= ntok <= min(max_tokens, 16). No counterpart entry
+ * point in the reference, whose kernel list runs the same steps as separate launches. */
+MOE_API moe_status moe_forward_hc_async(moe_ctx *ctx, uint32_t layer, float *R_dev, uint32_t ntok, float *y_dev,
+                                        int32_t *ids_dev, float *w_dev, void *stream);
+/* The same with R (ntok x 4 x n_embd) and y (ntok x n_embd, may be null) in host memory; synchronous. */
+MOE_API moe_status moe_forward_hc(moe_ctx *ctx, uint32_t layer, float *R, uint32_t ntok, float *y,
+                                  moe_route_out *route);
+
 /* Waits for the context's stream. */
 MOE_API moe_status moe_sync(moe_ctx *ctx);
 /* Waits for stream (null: the context's stream), then reports whether any forward since the last check had a wait
@@ -182,7 +200,7 @@ MOE_API moe_status moe_kernel_times(moe_ctx *ctx, const char **names, float *avg
  * the hand-off work it does as the last of its kind). moe_trace gives the last forward's stamps as (start, ready,
  * computed, end) quadruples in item order, up to cap of them (a cap past n copies the rest of the 65536-quadruple
  * buffer too); n receives the number of items, bounds (8 entries, or null) where each kind begins: lead (router
- * rows), top-k, the shared expert's gate/up and down (which run beside the router), the routed gate/up and down, the
+ * rows; the hyper-connection mix's items, when moe_forward_hc ran, are the ones before it), top-k, the shared expert's gate/up and down (which run beside the router), the routed gate/up and down, the
  * combine, and the end. The items before the routed ones ran on work-group i mod moe_grid(ctx); the routed ones are
  * dealt out dynamically. */
 MOE_API uint32_t moe_grid(const moe_ctx *ctx);

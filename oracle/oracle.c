@@ -754,3 +754,91 @@ done:
   free(lg), free(ids), free(w), free(jobs), free(s);
   return rc;
 }
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * The hyper-connection mix and combine around the block (docs/spec/MODEL_LAYER.md 1.1-1.2: build_hc_mix and
+ * build_hc_combine; the CPU ops ggml_compute_forward_rms_norm_f32 and the BF16 products, whose fp32 sums run in an
+ * order of ggml's own, unpinned: here every BF16 product is exact and the products are summed in double, W_down's
+ * and W_inject's rows in dot_tree_bf16's order, W_up's in k order, then rounded once). */
+
+static inline float bf16r(float x) { return bf16_to_fp32(orc_fp32_to_bf16(x)); }
+static inline float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+/* The decode kernel's order for a bf16 row of K values (a multiple of 512) against bf16(x): K in chunks of 512, lane
+ * l of a chunk the values 8 l .. 8 l + 7 (a fused chain in k order from 0, each product exact); the 16 lanes of a
+ * lane row r as ((P0 + P7) + (P3 + P4)) + ((P1 + P6) + (P2 + P5)), P_m = a_m + a_(15 - m); slot 4 w + r (wave w takes
+ * chunks w, w + 4, ..) the chunks' sums in chunk order; the result the 16 slots added in order from 0. Where the
+ * double sum is not exact (K of 10240 values of wide range), this fixes its rounding. */
+static double dot_tree_bf16(const uint16_t *w, const float *x, uint32_t K) {
+  const uint32_t nC = K / 512;
+  double part[16] = {0};
+  for (uint32_t c = 0; c < nC; c++) {
+    const uint32_t wv = c % 4;
+    for (uint32_t r = 0; r < 4; r++) {
+      double a[16];
+      for (uint32_t m = 0; m < 16; m++) {
+        const uint32_t k0 = 512 * c + 8 * (16 * r + m);
+        double acc = 0.0;
+        for (uint32_t k = 0; k < 8; k++) acc += (double)bf16_to_fp32(w[k0 + k]) * (double)bf16r(x[k0 + k]);
+        a[m] = acc;
+      }
+      double P[8];
+      for (uint32_t m = 0; m < 8; m++) P[m] = a[m] + a[15 - m];
+      const double S = ((P[0] + P[7]) + (P[3] + P[4])) + ((P[1] + P[6]) + (P[2] + P[5]));
+      double *q = part + 4 * wv + r;
+      *q = c < 4 ? S : *q + S;
+    }
+  }
+  double s = 0.0;
+  for (uint32_t i = 0; i < 16; i++) s += part[i];
+  return s;
+}
+
+int orc_hc_pre(const float *R, uint32_t T, uint32_t H, uint32_t lr, const float *gamma, const uint16_t *w_down,
+               const uint16_t *w_inj, const uint16_t *w_up, float *x, float *inject) {
+  const uint64_t D = 4ull * H;
+  float *n = (float *)malloc(sizeof(float) * D), *l = (float *)malloc(sizeof(float) * (lr ? lr : 1));
+  if (!n || !l) return -1;
+  for (uint32_t t = 0; t < T; t++) {
+    const float *r = R + (uint64_t)t * D;
+    for (uint32_t s = 0; s < 4; s++) { /* step 1: RMSNorm_1e-6(R_s) g_s, the squares summed in double */
+      double ss = 0.0;
+      for (uint32_t i = 0; i < H; i++) ss += (double)(r[s * H + i] * r[s * H + i]);
+      const float mean = (float)(ss / (double)H);
+      const float scale = 1.0f / sqrtf(mean + 1e-6f);
+      for (uint32_t i = 0; i < H; i++) n[s * H + i] = (r[s * H + i] * scale) * gamma[s * H + i];
+    }
+    for (uint32_t j = 0; j < lr + 4; j++) { /* step 2: l = silu((W_down n) / 4); step 4: inject = W_inj n */
+      const uint16_t *w = j < lr ? w_down + (uint64_t)j * D : w_inj + (uint64_t)(j - lr) * D;
+      const float v = (float)dot_tree_bf16(w, n, (uint32_t)D);
+      if (j < lr) {
+        const float z = v * 0.25f;
+        l[j] = z / (1.0f + expf(-z));
+      } else {
+        inject[(uint64_t)t * 4 + (j - lr)] = v;
+      }
+    }
+    for (uint32_t i = 0; i < H; i++) { /* a = W_up l; step 3: x[i] = (sum_s n_s[i] sigma(a_s[i])) / 4 */
+      float mix = 0.0f;
+      for (uint32_t s = 0; s < 4; s++) {
+        const uint16_t *w = w_up + ((uint64_t)s * H + i) * lr;
+        double acc = 0.0;
+        for (uint32_t k = 0; k < lr; k++) acc += (double)bf16_to_fp32(w[k]) * (double)bf16r(l[k]);
+        mix = mix + n[s * H + i] * sigmoidf_((float)acc);
+      }
+      x[(uint64_t)t * H + i] = mix * 0.25f;
+    }
+  }
+  free(n);
+  free(l);
+  return 0;
+}
+
+void orc_hc_post(float *R, uint32_t T, uint32_t H, const float *inject, const float *y) {
+  for (uint32_t t = 0; t < T; t++)
+    for (uint32_t s = 0; s < 4; s++) {
+      const float w = 2.0f * sigmoidf_(inject[(uint64_t)t * 4 + s] * 0.25f);
+      float *r = R + ((uint64_t)t * 4 + s) * H;
+      for (uint32_t i = 0; i < H; i++) r[i] = r[i] + w * y[(uint64_t)t * H + i];
+    }
+}

@@ -108,6 +108,13 @@ int orc_fast_moe_forward(const orc_layer *L, const float *x, uint32_t ntok, uint
                          uint64_t y_stride, int32_t *ids, float *w, int nthreads);
 const char *orc_fast_isa(void);
 
+/* The hyper-connection mix before the block (MODEL_LAYER.md 1.1): R (T x 4 x H) to x (T x H) and the inject logits
+ * (T x 4), with gamma (4 H), W_down (lr x 4H bf16), W_inject (4 x 4H bf16), W_up (4H x lr bf16, row s H + i). */
+int orc_hc_pre(const float *R, uint32_t T, uint32_t H, uint32_t lr, const float *gamma, const uint16_t *w_down,
+               const uint16_t *w_inj, const uint16_t *w_up, float *x, float *inject);
+/* The combine after it (1.2): R_s += 2 sigma(inject_s / 4) y. */
+void orc_hc_post(float *R, uint32_t T, uint32_t H, const float *inject, const float *y);
+
 #ifdef __cplusplus
 }
 #endif

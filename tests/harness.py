@@ -32,6 +32,8 @@ def _load_oracle():
         "orc_iq3s_grid": (None, [_P]),
         "orc_iq4nl_values": (None, [_P]),
         "orc_set_codebooks": (None, [_P]),
+        "orc_hc_pre": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.c_uint32, _P, _P, _P, _P, _P, _P]),
+        "orc_hc_post": (None, [_P, C.c_uint32, C.c_uint32, _P, _P]),
         "orc_dequantize_row": (C.c_int, [C.c_uint32, _P, _P, C.c_int64]),
         "orc_quantize_act": (C.c_int, [C.c_uint32, _P, _P, C.c_int64]),
         "orc_vec_dot": (C.c_int, [C.c_uint32, C.c_int64, _P, _P, C.POINTER(C.c_float)]),
@@ -245,6 +247,41 @@ class Layer:
         assert oracle.orc_route(ptr(self.router), ptr(self.bias), self.E, self.H, self.K, ptr(x), T, self.H,
                                 ptr(lg), ptr(ids), ptr(w)) == 0
         return lg, ids, w
+
+
+class HcModule:
+    """A layer's hyper-connection module (MODEL_LAYER.md 1.1): gamma = 1 + N(0, 0.1) (the folded norm weight),
+    W_down, W_inject, W_up N(0, sigma) as bf16 bits, drawn from (seed, layer)."""
+
+    def __init__(self, H, lr, seed=5, layer=0, sigma=0.02):
+        self.H, self.lr = H, lr
+        base = (layer << 20) + (1 << 19)
+        D = 4 * H
+        self.gamma = (1.0 + moe.synth_normal(seed, base, D, 0.1)).astype(np.float32)
+        self.down = to_bf16(moe.synth_normal(seed, base + 1, lr * D, sigma)).reshape(lr, D)
+        self.inj = to_bf16(moe.synth_normal(seed, base + 2, 4 * D, sigma)).reshape(4, D)
+        self.up = to_bf16(moe.synth_normal(seed, base + 3, D * lr, sigma)).reshape(D, lr)
+
+    def load(self, blk, layer=0):
+        blk.load_hc(layer, self.gamma, self.down, self.inj, self.up)
+
+    def pre(self, R):
+        """The oracle's mix: x (T x H) and the inject logits (T x 4)."""
+        R = np.ascontiguousarray(R, dtype=np.float32)
+        T = R.shape[0]
+        x = np.empty((T, self.H), np.float32)
+        inj = np.empty((T, 4), np.float32)
+        assert oracle.orc_hc_pre(ptr(R), T, self.H, self.lr, ptr(self.gamma), ptr(self.down), ptr(self.inj),
+                                 ptr(self.up), ptr(x), ptr(inj)) == 0
+        return x, inj
+
+    @staticmethod
+    def post(R, inj, y):
+        """The oracle's combine: R_s + 2 sigma(inject_s / 4) y, as a new array."""
+        R = np.array(R, dtype=np.float32, copy=True, order="C")
+        oracle.orc_hc_post(ptr(R), R.shape[0], R.shape[2], ptr(np.ascontiguousarray(inj, np.float32)),
+                           ptr(np.ascontiguousarray(y, np.float32)))
+        return R
 
 
 def fast_forward(layer, x, nthreads=8):

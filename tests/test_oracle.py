@@ -463,3 +463,42 @@ def test_block_reduces_to_dense_ffn_when_k_is_all_and_experts_equal():
         ref = dense_ffn(*L.experts[0], moe.QT_Q4_K, moe.QT_Q4_K, H, F, x[t]) * (float(w[t].sum()) + gs)
         assert h.rel_l2(y[t], ref) < 3e-2
         assert sorted(ids[t].tolist()) == list(range(E))
+
+
+# --------------------------------------------------------------------------------------------------------------
+# The hyper-connection mix and combine
+
+
+def test_hc_mix_against_float64_and_closed_forms():
+    """orc_hc_pre against a float64 restatement of MODEL_LAYER.md 1.1 (bf16 roundings included) to 1e-5, and two
+    closed forms: with W_up = 0 every gate is sigma(0) = 1/2, so x = (sum_s n_s / 2) / 4 exactly as the fp32 steps
+    give it; with W_inject = 0 the combine is R_s + y bit for bit (2 sigma(0) = 1)."""
+    H, lr, T = 512, 64, 3
+    hc = h.HcModule(H, lr, seed=3)
+    R = rng.standard_normal((T, 4, H)).astype(np.float32)
+    x, inj = hc.pre(R)
+    bf = lambda a: h.bf16_to_f32(h.to_bf16(np.asarray(a, np.float32))).astype(np.float64)
+    Wd, Wi, Wu = (h.bf16_to_f32(m).astype(np.float64) for m in (hc.down, hc.inj, hc.up))
+    for t in range(T):
+        r = R[t].astype(np.float64)
+        n = r / np.sqrt((r * r).mean(axis=1, keepdims=True) + 1e-6) * hc.gamma.reshape(4, H)
+        z = Wd @ bf(n.ravel()) / 4
+        l = z / (1 + np.exp(-z))
+        a = (Wu @ bf(l)).reshape(4, H)
+        want = (n / (1 + np.exp(-a))).sum(axis=0) / 4
+        assert np.allclose(x[t], want, rtol=1e-5, atol=1e-6)
+        assert np.allclose(inj[t], Wi @ bf(n.ravel()), rtol=1e-5, atol=1e-6)
+    hc0 = h.HcModule(H, lr, seed=3)
+    hc0.up[:] = 0
+    x0, _ = hc0.pre(R)
+    for t in range(T):
+        r = R[t]
+        acc = np.zeros(H, np.float32)
+        for s in range(4):
+            ss = float(np.sum((r[s] * r[s]).astype(np.float64)))  # fp32 squares summed in double (exact here)
+            scale = np.float32(1.0) / np.sqrt(np.float32(np.float32(ss / H) + np.float32(1e-6)), dtype=np.float32)
+            n = (r[s] * scale) * hc0.gamma[s * H:(s + 1) * H]
+            acc = acc + n * np.float32(0.5)
+        assert np.array_equal(x0[t], acc * np.float32(0.25))
+    y = rng.standard_normal((T, H)).astype(np.float32)
+    assert np.array_equal(h.HcModule.post(R, np.zeros((T, 4), np.float32), y), R + y[:, None, :])
