@@ -155,10 +155,11 @@ __device__ __forceinline__ uint32_t act_type(uint32_t runtime) {
   return runtime;
 }
 
-template <uint32_t kTypes>
+template <uint32_t kTypes, bool kHc>
 __global__ void moe_decode(DecodeParams p);
 
-// The instantiation for a type set (1 .. 15), as a kernel handle for hipLaunchKernel.
-const void *decode_kernel(uint32_t types);
+// The instantiation for a type set (1 .. 15), with the hyper-connection items or not, as a kernel handle for
+// hipLaunchKernel.
+const void *decode_kernel(uint32_t types, bool hc);
 
 }  // namespace c0ven

@@ -210,6 +210,9 @@ struct moe_ctx {
   uint8_t *codebooks = nullptr;  // the caller's iq2s_grid and iq3xxs_grid (QGRID layout, up to QGRID_IQ3S)
   bool have_codebooks = false;
   const void *kernel = nullptr;  // moe_decode for the context's set of weight types
+  const void *kernel_hc = nullptr;  // the same with the hyper-connection items (hc_lr > 0)
+  uint32_t grid_hc = 0;
+  size_t lds_hc = 0;
   size_t lds = 0;              // its dynamic LDS
   int timing = 0;  // 0 off, 1 every kernel, 2 the decode kernel and the prefill gate/up launches
   uint64_t *trace = nullptr;   // per-item stamps of the last forward, when tracing
@@ -369,7 +372,10 @@ void launch(moe_ctx *c, const DecodeParams &p, hipStream_t s) {
   c->last_T = p.T, c->last_route = p.route, c->last_hc = p.hc_R != nullptr;
   if (c->timing) timing_hook(c, "moe_decode", 0, s);
   void *args[] = {&q};
-  check(hipLaunchKernel(c->kernel, dim3(c->grid), dim3(kWG), args, c->lds, s), "moe_decode launch");
+  if (q.hc_R)
+    check(hipLaunchKernel(c->kernel_hc, dim3(c->grid_hc), dim3(kWG), args, c->lds_hc, s), "moe_decode launch");
+  else
+    check(hipLaunchKernel(c->kernel, dim3(c->grid), dim3(kWG), args, c->lds, s), "moe_decode launch");
   check(hipGetLastError(), "moe_decode launch");
   if (c->timing) timing_hook(c, "moe_decode", 1, s);
 }
@@ -556,18 +562,26 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     // The grid: every work-group the device holds at once (no more, so that all run together), LDS for the largest
     // stage.
     const size_t hc_lds = g.hc_lr ? ((size_t)T * g.hc_lr + (size_t)T * kHcStreams * kHcUpValues) * 4 : 0;
-    c->lds = std::max<size_t>({hc_lds, (size_t)MOE_GROUP_MAX * act_tok_stride(Ug) +
+    c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * act_tok_stride(Ug) +
                                    std::max<size_t>(Ug == 8 ? kMfmaXchBytes : 0, gate_up_xch_bytes(unit_lanes(Ug))),
                                (size_t)MOE_GROUP_MAX * act_tok_stride(Ud), kGroupingLds});
     int per_cu = 0, ncu = 0;
     uint32_t types = type_bit(g.gate_type) | type_bit(g.down_type);
     if (g.has_shared) types |= type_bit(g.sh_gate_type) | type_bit(g.sh_down_type);
-    c->kernel = decode_kernel(types);
+    c->kernel = decode_kernel(types, false);
     check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, c->kernel, kWG, c->lds), "occupancy");
     check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, g.device), "CU count");
     require(per_cu >= 1, "moe_decode does not fit a CU");
     if (const char *e = std::getenv("C0VEN_DECODE_WG_PER_CU")) per_cu = std::max(1, std::min(per_cu, std::atoi(e)));
     c->grid = (uint32_t)(per_cu * ncu);
+    if (g.hc_lr) {  // the variant with the hyper-connection items: its own occupancy (every work-group resident)
+      c->kernel_hc = decode_kernel(types, true);
+      c->lds_hc = std::max(c->lds, hc_lds);
+      int hc_per_cu = 0;
+      check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&hc_per_cu, c->kernel_hc, kWG, c->lds_hc), "occupancy");
+      require(hc_per_cu >= 1, "moe_decode with the hyper-connection items does not fit a CU");
+      c->grid_hc = (uint32_t)(std::min(hc_per_cu, per_cu) * ncu);
+    }
     require(g.device < kMaxDevices, "device ordinal too large");
     noalloc_setup(g.device);
     c->noalloc_bytes = noalloc_layout(g, nullptr).bytes;

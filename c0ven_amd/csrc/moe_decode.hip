@@ -309,13 +309,13 @@ __device__ __forceinline__ float row_sum(float t, uint32_t U) {
 // Router items
 
 // x[t] to the activation types of the routed and the shared gate: a half-wave per unit.
-template <uint32_t kTypes>
+template <uint32_t kTypes, bool kHc>
 __device__ __forceinline__ void quantise_x(const DecodeParams &p, uint32_t t) {
   const uint32_t H = p.H, l32 = tid() & 31u;
   for (uint32_t u = tid() / 32; u < H / kUnit; u += kWG / 32) {
     float4 a, b;
     const uint64_t e = (uint64_t)t * H + u * kUnit + 8 * l32;
-    if (p.hc_R) {  // x from this launch's up items
+    if constexpr (kHc) {  // x from this launch's up items
       const uint4 ua = ld_co16(p.x, (uint32_t)(4 * e)), ub = ld_co16(p.x, (uint32_t)(4 * e + 16));
       a = make_float4(__uint_as_float(ua.x), __uint_as_float(ua.y), __uint_as_float(ua.z), __uint_as_float(ua.w));
       b = make_float4(__uint_as_float(ub.x), __uint_as_float(ub.y), __uint_as_float(ub.z), __uint_as_float(ub.w));
@@ -349,20 +349,21 @@ __device__ __forceinline__ double row16_reduce8_f64(double v[8]) {
 }
 
 // Dot products of a bf16 row W of K values (a multiple of 512) with tokens t0 .. t0 + nt - 1 (nt <= 16) of x (rows
-// ldx apart; read past the caches when co, for x written in this launch): tot[t] = sum over the row of
+// ldx apart; read past the caches when kCo, for x written in this launch): tot[t] = sum over the row of
 // bf16(W) bf16(x), each product exact, summed in fp64. Wave w takes the 512-value chunks w, w + 4, ..., lane l values
 // 8 l .. 8 l + 7 of each: a lane converts its weights once for all tokens. Eight tokens at a time (x of four in flight
 // while four are used), each chunk's eight sums are reduced over the 16 lanes of a row (one value a lane pair left) and
 // added to that row of lanes' partial in LDS; the sixteen partials of an output (four rows of lanes, four waves) are
 // then added in a fixed order.
-__device__ __forceinline__ void bf16_dot(const uint16_t *W, const float *x, uint32_t K, uint32_t ldx, bool co,
-                                         uint32_t t0, uint32_t nt, double *part, double *tot) {
+template <bool kCo>
+__device__ __forceinline__ void bf16_dot(const uint16_t *W, const float *x, uint32_t K, uint32_t ldx, uint32_t t0,
+                                         uint32_t nt, double *part, double *tot) {
   const uint32_t lane = lane_id(), wv = wave_id(), nC = K / 512;
   const uint32_t pslot = 4 * wv + lane / 16;
   // Values 8 lane .. + 7 of chunk c of token t, as two float4.
   const auto ldx8 = [&](uint32_t t, uint32_t c, float4 &a, float4 &b) {
     const uint64_t e = (uint64_t)t * ldx + 512 * c + 8 * lane;
-    if (co) {
+    if constexpr (kCo) {
       const uint4 u = ld_co16(x, (uint32_t)(4 * e)), v = ld_co16(x, (uint32_t)(4 * e + 16));
       a = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
       b = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
@@ -425,10 +426,11 @@ __device__ __forceinline__ void bf16_dot(const uint16_t *W, const float *x, uint
   __syncthreads();
 }
 
-// Router row `row` (row E: the shared gate) against tokens t0 .. t0 + nt - 1 of x.
+// Router row `row` (row E: the shared gate) against tokens t0 .. t0 + nt - 1 of x (written in this launch with kHc).
+template <bool kHc>
 __device__ __forceinline__ void router_dot(const DecodeParams &p, uint32_t row, uint32_t t0, uint32_t nt, double *part,
                                            double *tot) {
-  bf16_dot(p.router + (uint64_t)row * p.H, p.x, p.H, p.H, p.hc_R != nullptr, t0, nt, part, tot);
+  bf16_dot<kHc>(p.router + (uint64_t)row * p.H, p.x, p.H, p.H, t0, nt, part, tot);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -475,7 +477,7 @@ __device__ __forceinline__ void hc_down_item(const DecodeParams &p, uint32_t r, 
   const uint32_t K = kHcStreams * p.H, lr = p.hc_lr;
   wait_flags(p, kFlagHcNorm, p.T);
   const uint16_t *W = r < lr ? p.hc_down + (uint64_t)r * K : p.hc_inj + (uint64_t)(r - lr) * K;
-  bf16_dot(W, p.hc_n, K, K, true, 0, p.T, part, tot);
+  bf16_dot<true>(W, p.hc_n, K, K, 0, p.T, part, tot);
   const uint32_t t = tid();
   if (t < p.T) {
     const float v = (float)tot[t];
@@ -536,8 +538,9 @@ __device__ __forceinline__ void hc_up_item(const DecodeParams &p, uint32_t j, ui
 }
 
 // Lead item i: router row i for all T tokens, plus the bias.
+template <bool kHc>
 __device__ __forceinline__ void router_row(const DecodeParams &p, uint32_t row, double *part, double *tot) {
-  router_dot(p, row, 0, p.T, part, tot);
+  router_dot<kHc>(p, row, 0, p.T, part, tot);
   const uint32_t t = tid();
   if (t < p.T) {
     float l = (float)tot[t];
@@ -943,6 +946,7 @@ __device__ __forceinline__ void down_item(const DecodeParams &p, const GroupLds 
 // token's weights (and, for a pre-routed call, which of its assignments are live) are read once into LDS; the
 // per-assignment outputs are polled as tagged records (one first, then all of the row's). The combine items come after
 // every down item, so what they wait for has a smaller number.
+template <bool kHc>
 __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, uint32_t blk, float *wl,
                                              const uint64_t *tab, uint64_t *mark) {
   const uint32_t rows = down_rows(unit_lanes(units_of(p.F))), K = p.K, row = blk * rows + tid();
@@ -956,7 +960,7 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
       wl[kMaxUsed + 1 + k] = on ? 1.0f : 0.0f;
     } else if (k == K && ns) {  // thread K: the shared expert's gate
       wl[K] = __uint_as_float(poll_tag(p, p.gs + t));
-    } else if (p.hc_R && k >= K + 1 && k < K + 1 + kHcStreams) {  // stream s's weight 2 sigma(inject_s / 4)
+    } else if (kHc && k >= K + 1 && k < K + 1 + kHcStreams) {  // stream s's weight 2 sigma(inject_s / 4)
       const uint32_t s = k - K - 1;
       const float inj = ld_co(p.hc_l + (uint64_t)t * (p.hc_lr + kHcStreams) + p.hc_lr + s);
       wl[2 * kMaxUsed + 1 + s] = __fmul_rn(2.0f, sigmoid_libm(__fmul_rn(inj, 0.25f), tab));
@@ -1002,7 +1006,7 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
       if (on[k]) acc = __fadd_rn(acc, __fmul_rn(wv[k], yv[k]));
     if (ns) acc = __fadd_rn(acc, __fmul_rn(gs, ys));
     if (p.y) p.y[(uint64_t)t * p.H + row] = acc;
-    if (p.hc_R) {  // the combine (MODEL_LAYER.md 1.2): R_s += 2 sigma(inject_s / 4) y
+    if constexpr (kHc) {  // the combine (MODEL_LAYER.md 1.2): R_s += 2 sigma(inject_s / 4) y
 #pragma unroll
       for (uint32_t s = 0; s < kHcStreams; s++) {
         float *r = p.hc_R + ((uint64_t)t * kHcStreams + s) * p.H + row;
@@ -1017,7 +1021,7 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
 
 // Grid: the work-groups of 256 the device holds at once; dynamic LDS: the larger of a group's activation units
 // (MOE_GROUP_MAX x act_tok_stride) and the grouping's tables (kGroupingLds).
-template <uint32_t kTypes>
+template <uint32_t kTypes, bool kHc>
 __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) moe_decode(DecodeParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ uint32_t grid_lds[(kTypes & kTypeIQ2) ? kGridWords : (kTypes & kTypeIQ3_S) ? 512 : 1];
@@ -1033,7 +1037,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   if (tid() == 0) s_grid = 0xffffffffu;
   __syncthreads();
   const uint32_t T = p.T, E = p.E, Ug = unit_lanes(units_of(p.H)), Ud = unit_lanes(units_of(p.F));
-  const uint32_t nH = p.hc_R ? hc_items(T, p.H, p.hc_lr) : 0u;  // the hyper-connection mix's items come first
+  const uint32_t nH = kHc ? hc_items(T, p.H, p.hc_lr) : 0u;  // the hyper-connection mix's items come first
   const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nH + nL + nTop;
   const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud), nBlk = nD;  // combine items: T x nBlk
   const uint32_t ns = shared_chunks(T, p.route, p.has_shared), B2 = B1 + ns * (nGU + nD);
@@ -1072,7 +1076,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
     }
     uint64_t *mark = p.trace && it < p.trace_cap ? p.trace + 4 * it : nullptr;
     if (mark && tid() == 0) mark[0] = mark[1] = mark[2] = __builtin_amdgcn_s_memrealtime();
-    if (it < nH) {
+    if (kHc && it < nH) {
       const uint32_t lw = p.hc_lr + kHcStreams;
       if (it < T)
         hc_norm_item(p, it, s_part);
@@ -1082,10 +1086,10 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
         hc_up_item(p, it - T - lw, lds, exp_tab, &s_flag);
     } else if (it < nH + nL) {
       const uint32_t li = it - nH;
-      if (nH) wait_flag(p, kFlagHcX);
-      if (li < T) quantise_x<kTypes>(p, li);
+      if (kHc) wait_flag(p, kFlagHcX);
+      if (li < T) quantise_x<kTypes, kHc>(p, li);
       if (p.route) {
-        if (li < E) router_row(p, li, s_part, s_tot);
+        if (li < E) router_row<kHc>(p, li, s_part, s_tot);
         if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
         set_flag(p, kFlagLead + li);
       } else if (arrive_last(p.cnt_route, nL, &s_flag)) {
@@ -1093,9 +1097,9 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
       }
     } else if (it < B1) {
       const uint32_t t = it - nH - nL;
-      if (nH) wait_flag(p, kFlagHcX);
+      if (kHc) wait_flag(p, kFlagHcX);
       // The shared gate's logit (router row E) for this token while the lead items finish: gs = sigmoid of it.
-      router_dot(p, E, t, 1, s_part, s_tot);
+      router_dot<kHc>(p, E, t, 1, s_part, s_tot);
       if (tid() == 0) st_tag(p.gs + t, __float_as_uint(sigmoid_libm((float)s_tot[0], exp_tab)), p.tag);
       if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
       route_token(p, t, exp_tab, s_part, (uint2 *)lds);
@@ -1118,7 +1122,7 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
         read_group(p, &gtab, false, i / nD, &sg);
         down_item<kTypes>(p, &sg, i % nD, lds, grid_lds, &s_grid, mark);
       } else {
-        combine_item(p, (i - ng * nD) / nBlk, (i - ng * nD) % nBlk, s_wl, exp_tab, mark);
+        combine_item<kHc>(p, (i - ng * nD) / nBlk, (i - ng * nD) % nBlk, s_wl, exp_tab, mark);
       }
     }
     if (mark && tid() == 0) mark[3] = __builtin_amdgcn_s_memrealtime();
@@ -1133,49 +1137,103 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   }
 }
 
-// The type sets are instantiated in two translation units that build in parallel: this one (sets 1 - 7 and the
-// dispatch) and moe_decode_iq2.hip (the sets with the codebook types, 8 - 15), which includes this file.
-#ifdef C0VEN_DECODE_IQ2_SETS
-#define C0VEN_DECODE_SET(n) template __global__ void moe_decode<n>(DecodeParams);
+// The type sets are instantiated in four translation units that build in parallel: this one (sets 1 - 7, without
+// the hyper-connection items, and the dispatch), moe_decode_iq2.hip (sets 8 - 15, the codebook types),
+// moe_decode_hc.hip and moe_decode_hc_iq2.hip (sets 1 - 7 and 8 - 15 with them), which include this file.
+#define C0VEN_EXTERN(n, hc) extern template __global__ void moe_decode<n, hc>(DecodeParams);
+#define C0VEN_INST(n, hc) template __global__ void moe_decode<n, hc>(DecodeParams);
+#if defined(C0VEN_DECODE_IQ2_SETS)
+#define C0VEN_SET_LO(n) C0VEN_EXTERN(n, false)
+#define C0VEN_SET_HI(n) C0VEN_INST(n, false)
+#define C0VEN_SET_HC_LO(n) C0VEN_EXTERN(n, true)
+#define C0VEN_SET_HC_HI(n) C0VEN_EXTERN(n, true)
+#elif defined(C0VEN_DECODE_HC_SETS)
+#define C0VEN_SET_LO(n) C0VEN_EXTERN(n, false)
+#define C0VEN_SET_HI(n) C0VEN_EXTERN(n, false)
+#define C0VEN_SET_HC_LO(n) C0VEN_INST(n, true)
+#define C0VEN_SET_HC_HI(n) C0VEN_EXTERN(n, true)
+#elif defined(C0VEN_DECODE_HC_IQ2_SETS)
+#define C0VEN_SET_LO(n) C0VEN_EXTERN(n, false)
+#define C0VEN_SET_HI(n) C0VEN_EXTERN(n, false)
+#define C0VEN_SET_HC_LO(n) C0VEN_EXTERN(n, true)
+#define C0VEN_SET_HC_HI(n) C0VEN_INST(n, true)
 #else
-#define C0VEN_DECODE_SET(n) extern template __global__ void moe_decode<n>(DecodeParams);
+#define C0VEN_SET_LO(n) C0VEN_INST(n, false)
+#define C0VEN_SET_HI(n) C0VEN_EXTERN(n, false)
+#define C0VEN_SET_HC_LO(n) C0VEN_EXTERN(n, true)
+#define C0VEN_SET_HC_HI(n) C0VEN_EXTERN(n, true)
 #endif
-C0VEN_DECODE_SET(8)
-C0VEN_DECODE_SET(9)
-C0VEN_DECODE_SET(10)
-C0VEN_DECODE_SET(11)
-C0VEN_DECODE_SET(12)
-C0VEN_DECODE_SET(13)
-C0VEN_DECODE_SET(14)
-C0VEN_DECODE_SET(15)
-#undef C0VEN_DECODE_SET
+C0VEN_SET_LO(1)
+C0VEN_SET_LO(2)
+C0VEN_SET_LO(3)
+C0VEN_SET_LO(4)
+C0VEN_SET_LO(5)
+C0VEN_SET_LO(6)
+C0VEN_SET_LO(7)
+C0VEN_SET_HI(8)
+C0VEN_SET_HI(9)
+C0VEN_SET_HI(10)
+C0VEN_SET_HI(11)
+C0VEN_SET_HI(12)
+C0VEN_SET_HI(13)
+C0VEN_SET_HI(14)
+C0VEN_SET_HI(15)
+C0VEN_SET_HC_LO(1)
+C0VEN_SET_HC_LO(2)
+C0VEN_SET_HC_LO(3)
+C0VEN_SET_HC_LO(4)
+C0VEN_SET_HC_LO(5)
+C0VEN_SET_HC_LO(6)
+C0VEN_SET_HC_LO(7)
+C0VEN_SET_HC_HI(8)
+C0VEN_SET_HC_HI(9)
+C0VEN_SET_HC_HI(10)
+C0VEN_SET_HC_HI(11)
+C0VEN_SET_HC_HI(12)
+C0VEN_SET_HC_HI(13)
+C0VEN_SET_HC_HI(14)
+C0VEN_SET_HC_HI(15)
+#undef C0VEN_SET_LO
+#undef C0VEN_SET_HI
+#undef C0VEN_SET_HC_LO
+#undef C0VEN_SET_HC_HI
+#undef C0VEN_EXTERN
+#undef C0VEN_INST
 
-#ifndef C0VEN_DECODE_IQ2_SETS
-template __global__ void moe_decode<1>(DecodeParams);
-template __global__ void moe_decode<2>(DecodeParams);
-template __global__ void moe_decode<3>(DecodeParams);
-template __global__ void moe_decode<4>(DecodeParams);
-template __global__ void moe_decode<5>(DecodeParams);
-template __global__ void moe_decode<6>(DecodeParams);
-template __global__ void moe_decode<7>(DecodeParams);
-
-const void *decode_kernel(uint32_t types) {
-  switch (types) {
-    case 1: return (const void *)moe_decode<1>;
-    case 2: return (const void *)moe_decode<2>;
-    case 3: return (const void *)moe_decode<3>;
-    case 4: return (const void *)moe_decode<4>;
-    case 5: return (const void *)moe_decode<5>;
-    case 6: return (const void *)moe_decode<6>;
-    case 7: return (const void *)moe_decode<7>;
-    case 8: return (const void *)moe_decode<8>;
-    case 9: return (const void *)moe_decode<9>;
-    case 10: return (const void *)moe_decode<10>;
-    case 11: return (const void *)moe_decode<11>;
-    case 12: return (const void *)moe_decode<12>;
-    case 13: return (const void *)moe_decode<13>;
-    case 14: return (const void *)moe_decode<14>;
-    default: return (const void *)moe_decode<15>;
+#if !defined(C0VEN_DECODE_IQ2_SETS) && !defined(C0VEN_DECODE_HC_SETS) && !defined(C0VEN_DECODE_HC_IQ2_SETS)
+const void *decode_kernel(uint32_t types, bool hc) {
+  switch (types + (hc ? 16 : 0)) {
+    case 1: return (const void *)moe_decode<1, false>;
+    case 2: return (const void *)moe_decode<2, false>;
+    case 3: return (const void *)moe_decode<3, false>;
+    case 4: return (const void *)moe_decode<4, false>;
+    case 5: return (const void *)moe_decode<5, false>;
+    case 6: return (const void *)moe_decode<6, false>;
+    case 7: return (const void *)moe_decode<7, false>;
+    case 8: return (const void *)moe_decode<8, false>;
+    case 9: return (const void *)moe_decode<9, false>;
+    case 10: return (const void *)moe_decode<10, false>;
+    case 11: return (const void *)moe_decode<11, false>;
+    case 12: return (const void *)moe_decode<12, false>;
+    case 13: return (const void *)moe_decode<13, false>;
+    case 14: return (const void *)moe_decode<14, false>;
+    case 15: return (const void *)moe_decode<15, false>;
+    case 17: return (const void *)moe_decode<1, true>;
+    case 18: return (const void *)moe_decode<2, true>;
+    case 19: return (const void *)moe_decode<3, true>;
+    case 20: return (const void *)moe_decode<4, true>;
+    case 21: return (const void *)moe_decode<5, true>;
+    case 22: return (const void *)moe_decode<6, true>;
+    case 23: return (const void *)moe_decode<7, true>;
+    case 24: return (const void *)moe_decode<8, true>;
+    case 25: return (const void *)moe_decode<9, true>;
+    case 26: return (const void *)moe_decode<10, true>;
+    case 27: return (const void *)moe_decode<11, true>;
+    case 28: return (const void *)moe_decode<12, true>;
+    case 29: return (const void *)moe_decode<13, true>;
+    case 30: return (const void *)moe_decode<14, true>;
+    case 31: return (const void *)moe_decode<15, true>;
+    default: return nullptr;
   }
 }
 #endif
