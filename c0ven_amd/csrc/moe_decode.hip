@@ -242,17 +242,29 @@ __device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, u
                                            const uint32_t &n, float *t, Ready ready) {
   if constexpr ((kTypes & kTypeQ8_0) != 0) {
     if (kTypes == kTypeQ8_0 || q8_family(type)) {
-      UnitQ8_0 w;
-      if (type == QT_IQ4_NL)
-        static_cast<UnitIQ4_NL &>(w).load(tile, idx, nl);
-      else if (type == QT_Q2_0)
-        static_cast<UnitQ2_0 &>(w).load(tile, idx, nl);
-      else
-        w.load(tile, idx, nl);
-      ready();
+      const auto run = [&](auto &w) {
 #pragma unroll
-      for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
-        if (j < n) t[j] = w.term(Act(act + j * stride));
+        for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
+          if (j < n) t[j] = w.term(Act(act + j * stride));
+      };
+      if (type == QT_Q2_0) {  // a branch a type, so that no two types' registers are live together
+        UnitQ8Split<QT_Q2_0> w;
+        w.load_raw(tile, idx, nl);
+        ready();
+        w.widen();
+        run(w);
+      } else if (type == QT_IQ4_NL) {
+        UnitQ8Split<QT_IQ4_NL> w;
+        w.load_raw(tile, idx, nl);
+        ready();
+        w.widen();
+        run(w);
+      } else {
+        UnitQ8_0 w;
+        w.load(tile, idx, nl);
+        ready();
+        run(w);
+      }
       return;
     }
   }

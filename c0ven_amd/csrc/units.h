@@ -334,4 +334,49 @@ struct UnitQ2_0 : UnitQ8_0 {
   }
 };
 
+// IQ4_NL and Q2_0 as UnitQ8_0 with the decode split from the loads: load_raw issues a unit's loads (IQ4_NL its 32
+// nibble words into q[0..31]; Q2_0 its 16 code words into q[0..15]; the f16 scale words into dw), and widen, once
+// they have arrived, decodes them in place exactly as UnitIQ4_NL::load / UnitQ2_0::load do. A caller that takes
+// the type at run time gives each type its own branch of load_raw, wait, widen and terms, so that no two types'
+// registers are live together.
+template <uint32_t kT>
+struct UnitQ8Split : UnitQ8_0 {
+  static_assert(kT == QT_IQ4_NL || kT == QT_Q2_0, "UnitQ8Split: IQ4_NL or Q2_0");
+  static constexpr uint32_t kPieces = kT == QT_IQ4_NL ? 8 : 4;  // 16-byte pieces of codes
+  uint32_t dw[4];
+  __device__ __forceinline__ void load_raw(const uint8_t *tile, uint32_t idx, uint32_t nl) {
+#pragma unroll
+    for (uint32_t p = 0; p < kPieces; p++) {
+      const uint4 v = *field<uint4>(tile, 0, p, idx, nl);
+      q[4 * p] = v.x, q[4 * p + 1] = v.y, q[4 * p + 2] = v.z, q[4 * p + 3] = v.w;
+    }
+    if constexpr (kT == QT_Q2_0) {
+      const uint2 v = *field<uint2>(tile, q2_0t::kD, 0, idx, nl);
+      dw[0] = v.x, dw[1] = v.y;
+    } else {
+      const uint4 v = *field<uint4>(tile, iq4_nlt::kD, 0, idx, nl);
+      dw[0] = v.x, dw[1] = v.y, dw[2] = v.z, dw[3] = v.w;
+    }
+  }
+  __device__ __forceinline__ void widen() {
+#pragma unroll
+    for (int p = (int)kPieces - 1; p >= 0; p--) {  // descending: piece p's words move to 8p.. or 16p.., never onto a
+      const uint32_t w[4] = {q[4 * p], q[4 * p + 1], q[4 * p + 2], q[4 * p + 3]};  // piece not yet read
+      if constexpr (kT == QT_IQ4_NL) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          q[8 * p + i] = iq4nl_lookup(w[i] & 0x0f0f0f0fu);
+          q[8 * p + 4 + i] = iq4nl_lookup((w[i] >> 4) & 0x0f0f0f0fu);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) q[16 * p + i] = q2_spread((w[i / 4] >> (8 * (i % 4))) & 0xffu);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 8; b++)
+      d[b] = h2f((uint16_t)(kT == QT_Q2_0 ? dw[b / 4] >> (16 * ((b / 2) % 2)) : dw[b / 2] >> (16 * (b % 2))));
+  }
+};
+
 }  // namespace c0ven
