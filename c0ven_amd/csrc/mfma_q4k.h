@@ -32,21 +32,30 @@ __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long)(
 struct Q4kRaw {
   uint2 qs[4];
   uint32_t sc[3], dm[4];
-  // Rows row0 .. row0 + 15 (row0 a multiple of 16) of the matrix at mat (U units a row), unit u.
+  // Rows row0 .. row0 + 15 (row0 a multiple of 16) of the matrix at mat (U units a row), unit u: the codes (four
+  // 8-byte loads) and the scales with d|dmin (four loads), which load_qs / load_meta issue separately.
   __device__ __forceinline__ void load(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
+    load_qs(mat, U, row0, u, lane);
+    load_meta(mat, U, row0, u, lane);
+  }
+  // Addresses as a wave-uniform pointer (tile, field, unit) plus a 32-bit lane offset, so that each load is one
+  // global load on a scalar base with no per-load vector address arithmetic.
+  __device__ __forceinline__ void load_qs(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
     const uint32_t g = lane / 16, nl = kTileRows * U;
-    const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q4_K, U);
-    const uint32_t ia = pair_idx((row0 % kTileRows) + lane % 16, u);
+    const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q4_K, U) + (uint64_t)u * kTileRows * 16;
+    const uint32_t lo = (g / 2) * nl * 16 + ((row0 % kTileRows) + lane % 16) * 16 + 8 * (g % 2);
 #pragma unroll
-    for (uint32_t c = 0; c < 4; c++)
-      qs[c] = *(const uint2 *)(tile + ((uint64_t)(q4_kt::kQs / 16 + 2 * c + g / 2) * nl + ia) * 16 + 8 * (g % 2));
+    for (uint32_t c = 0; c < 4; c++) qs[c] = *(const uint2 *)(tile + (uint64_t)(q4_kt::kQs / 16 + 2 * c) * nl * 16 + lo);
+  }
+  __device__ __forceinline__ void load_meta(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
+    const uint32_t g = lane / 16, nl = kTileRows * U;
+    const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q4_K, U) + (uint64_t)u * kTileRows * 4;
+    const uint32_t ls = ((row0 % kTileRows) + lane % 16) * 4, ld = ((row0 % kTileRows) + 4 * g) * 4;
 #pragma unroll
-    for (uint32_t i = 0; i < 3; i++) sc[i] = *(const uint32_t *)(tile + (uint64_t)q4_kt::kScales * nl + ((uint64_t)i * nl + ia) * 4);
-#pragma unroll
-    for (uint32_t i = 0; i < 4; i++) {
-      const uint32_t id = pair_idx((row0 % kTileRows) + 4 * g + i, u);
-      dm[i] = *(const uint32_t *)(tile + (uint64_t)q4_kt::kDm * nl + (uint64_t)id * 4);
-    }
+    for (uint32_t i = 0; i < 3; i++) sc[i] = *(const uint32_t *)(tile + (uint64_t)(q4_kt::kScales + 4 * i) * nl + ls);
+    // The four D rows' words are consecutive pairs (16-byte aligned: 4 g + row0 % 64 is a multiple of 4): one load.
+    const uint4 v = *(const uint4 *)(tile + (uint64_t)q4_kt::kDm * nl + ld);
+    dm[0] = v.x, dm[1] = v.y, dm[2] = v.z, dm[3] = v.w;
   }
 };
 

@@ -339,6 +339,19 @@ struct Dma {
       off[k] = c < 20 && ar != 0xffffffffu ? ar * U * kActBytes + 16 * c : 0u;
     }
   }
+  // As load, but every wave issues kPer loads, those past kLoads into dump (1 KB of LDS no one reads): no branches,
+  // and the same count of loads in every wave, so that a wait can leave exactly the later units' loads in flight.
+  // Buffer loads on a resource over act (uniform base, the lane's 32-bit offset, the unit's scalar offset) and LDS
+  // destinations from the wave's uniform index: no vector address arithmetic a load.
+  __device__ __forceinline__ void load_all(__amdgpu_buffer_rsrc_t act, uint32_t u, uint8_t *buf, uint8_t *dump) const {
+    const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(wave_id());
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; k++) {
+      const uint32_t i = w + kWaves * k;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(act, (__attribute__((address_space(3))) void *)(i < kLoads ? buf + 64 * 16 * i : dump),
+                                               16, off[k], u * kActBytes, 0, 0);
+    }
+  }
   // Unit u of the planned positions into LDS at buf (the calling wave's share of the loads). The caller waits
   // (s_waitcnt vmcnt(0)) and synchronises before reading.
   __device__ __forceinline__ void load(const uint8_t *act, uint32_t u, uint8_t *buf) const {
@@ -614,15 +627,96 @@ struct Iq3sA {
 };
 
 
+// The s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory loads are outstanding and
+// leaves the other counters alone.
+constexpr uint32_t vm_wait(uint32_t n) { return (n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8); }
+
+// A raw buffer resource over p (wave-uniform), the whole 32-bit offset range.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *p) {
+  const uint64_t b = (uint64_t)p;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0, 0xffffffffu, 0x00020000u);
+}
+
+// Q4kRaw's loads for gate and up as buffer loads on the wave's 16-row tiles: a resource over each tile, the lane's
+// three 32-bit offsets (the same for both) worked out once, each field's and unit's offset scalar (the same bytes as
+// Q4kRaw::load_qs / load_meta).
+struct Q4kBuf {
+  const uint8_t *base[2];  // the resources are made at each load (scalar work the compiler keeps out of the loop)
+  uint32_t nl, lq, ls, ld;
+  __device__ __forceinline__ void init(const uint8_t *gate, const uint8_t *up, uint32_t U, uint32_t row0, uint32_t lane) {
+    const uint32_t g = lane / 16, rr = row0 % kTileRows;
+    const uint64_t t = (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q4_K, U);
+    nl = kTileRows * U;
+    base[0] = gate + t, base[1] = up + t;
+    lq = (g / 2) * nl * 16 + (rr + lane % 16) * 16 + 8 * (g % 2);
+    ls = (rr + lane % 16) * 4;
+    ld = (rr + 4 * g) * 4;
+  }
+  __device__ __forceinline__ void load_qs(uint32_t m, Q4kRaw &w, uint32_t u) const {
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(uniform_rsrc(base[m]), lq, (q4_kt::kQs / 16 + 2 * c) * nl * 16 + u * kTileRows * 16, 0);
+      w.qs[c] = make_uint2(v[0], v[1]);
+    }
+  }
+  __device__ __forceinline__ void load_meta(uint32_t m, Q4kRaw &w, uint32_t u) const {
+#pragma unroll
+    for (uint32_t i = 0; i < 3; i++)
+      w.sc[i] = __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(base[m]), ls, (q4_kt::kScales + 4 * i) * nl + u * kTileRows * 4, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(uniform_rsrc(base[m]), ld, q4_kt::kDm * nl + u * kTileRows * 4, 0);
+    w.dm[0] = v[0], w.dm[1] = v[1], w.dm[2] = v[2], w.dm[3] = v[3];
+  }
+};
+
+// A work-group barrier without __syncthreads' fence (which would wait for every load in flight): LDS reads done, then
+// s_barrier, with compiler barriers either side so that no LDS access moves across it.
+__device__ __forceinline__ void unit_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// The decoded operands as the outputs of an empty volatile asm with a memory clobber: the decode is done there (it
+// cannot sink below to its uses), and the next unit's loads, issued after it, cannot rise above it. Otherwise the
+// compiler moves the decode past the loads, the old and new raw words are live together, and the waits it inserts
+// for them cover the loads just issued.
+__device__ __forceinline__ void pin(Q4kA &a) {
+  asm volatile("" : "+v"(a.lo[0]), "+v"(a.lo[1]), "+v"(a.lo[2]), "+v"(a.lo[3]), "+v"(a.hi[0]), "+v"(a.hi[1]),
+               "+v"(a.hi[2]), "+v"(a.hi[3]), "+v"(a.mn), "+v"(a.d[0]), "+v"(a.d[1]), "+v"(a.d[2]), "+v"(a.d[3]),
+               "+v"(a.dmin[0]), "+v"(a.dmin[1]), "+v"(a.dmin[2]), "+v"(a.dmin[3]) :: "memory");
+}
+__device__ __forceinline__ void pin(Q4kRaw &r) {
+  asm volatile("" : "+v"(r.qs[0]), "+v"(r.qs[1]), "+v"(r.qs[2]), "+v"(r.qs[3]), "+v"(r.sc[0]), "+v"(r.sc[1]),
+               "+v"(r.sc[2]), "+v"(r.dm[0]), "+v"(r.dm[1]), "+v"(r.dm[2]), "+v"(r.dm[3]) :: "memory");
+}
+__device__ __forceinline__ void pin(Iq3sRaw &r) {
+  asm volatile("" : "+v"(r.qs[0]), "+v"(r.qs[1]), "+v"(r.qs[2]), "+v"(r.qs[3]), "+v"(r.qs[4]), "+v"(r.qs[5]),
+               "+v"(r.qs[6]), "+v"(r.qs[7]), "+v"(r.sg[0]), "+v"(r.sg[1]), "+v"(r.sg[2]), "+v"(r.sg[3]), "+v"(r.sg[4]),
+               "+v"(r.sg[5]), "+v"(r.sg[6]), "+v"(r.sg[7]) :: "memory");
+  asm volatile("" : "+v"(r.qh[0]), "+v"(r.qh[1]), "+v"(r.sc[0]), "+v"(r.sc[1]), "+v"(r.sc[2]), "+v"(r.sc[3]),
+               "+v"(r.dh[0]), "+v"(r.dh[1]), "+v"(r.dh[2]), "+v"(r.dh[3]) :: "memory");
+}
+__device__ __forceinline__ void pin(Iq3sA &a) {
+  asm volatile("" : "+v"(a.a[0]), "+v"(a.a[1]), "+v"(a.a[2]), "+v"(a.a[3]), "+v"(a.a[4]), "+v"(a.a[5]),
+               "+v"(a.a[6]), "+v"(a.a[7]), "+v"(a.sc[0]), "+v"(a.sc[1]), "+v"(a.sc[2]), "+v"(a.sc[3]), "+v"(a.d[0]),
+               "+v"(a.d[1]), "+v"(a.d[2]), "+v"(a.d[3]) :: "memory");
+}
+
 // A work-group takes kPos positions of one expert (a MoeTile) and 16 rows a wave of gate and of up (kPos / 16 waves),
 // so that a unit's weights, once decoded, meet kPos / 16 position tiles of 16. (128 positions, eight waves, one
 // work-group a CU by LDS, measured slower at config 4: 269 against 223 us.)
 template <uint32_t kType, uint32_t kPos>
 __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2))) pf_gate_up(PfGemm g) {
   static_assert(kType == QT_Q4_K || kType == QT_IQ3_S, "pf_gate_up: Q4_K and IQ3_S");
-  const uint32_t U = g.U;
+  const uint32_t U = g.U;  // at least 2: n_embd is a multiple of 512
   constexpr uint32_t kWaves = kPos / 16, kThreads = 64 * kWaves, kRows = 16 * kWaves, kPt = kPos / 16;
-  __shared__ __align__(16) uint8_t abuf[2][kPos * kActLds];
+  // The activations are loaded two units ahead (three LDS buffers), the weights one unit ahead (the registers of the
+  // raw bytes, free once the unit is decoded).
+  constexpr uint32_t kBufs = 3;
+  __shared__ __align__(16) uint8_t abuf[kBufs][kPos * kActLds];
+  __shared__ __align__(16) uint8_t dump[64 * 16];
   __shared__ uint32_t arow_lds[kPos];
   __shared__ uint64_t tab[32];
   __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
@@ -655,86 +749,118 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2
   const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
   Dma<kPos, kWaves> dma;
   dma.plan(arow_lds, U);
+  const __amdgpu_buffer_rsrc_t act_r = uniform_rsrc(g.act);
+  Q4kBuf wb;  // Q4_K's weight loads (IQ3_S loads through Iq3sRaw::load)
+  if constexpr (kType == QT_Q4_K) wb.init(Mg, Mu, U, row0, lane);
   Raw rg, ru;
-  rg.load(Mg, U, row0, 0, lane);
-  ru.load(Mu, U, row0, 0, lane);
-  dma.load(g.act, 0, &abuf[0][0]);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  const auto load_w = [&](uint32_t u) {
+    if constexpr (kType == QT_Q4_K) {
+      wb.load_qs(0, rg, u), wb.load_meta(0, rg, u);
+      wb.load_qs(1, ru, u), wb.load_meta(1, ru, u);
+    } else {
+      rg.load(Mg, U, row0, u, lane);
+      ru.load(Mu, U, row0, u, lane);
+    }
+  };
+  // The end of unit u waits for unit u + 1's loads, leaving in flight only the activation loads of unit u + 2 (issued
+  // after them): kPer a wave (load_all issues the same count in every wave). As the builtin, not asm, so that the
+  // compiler's own tracking knows what has landed.
+  const auto wait_next = [&](bool more) {
+    if (more)
+      __builtin_amdgcn_s_waitcnt(vm_wait(Dma<kPos, kWaves>::kPer));
+    else
+      __builtin_amdgcn_s_waitcnt(vm_wait(0));
+  };
+  load_w(0);
+  dma.load_all(act_r, 0, &abuf[0][0], dump);
+  dma.load_all(act_r, 1, &abuf[1][0], dump);
+  wait_next(true);  // unit 0's loads
+  unit_barrier();
   float accg[kPt][4], accu[kPt][4];
 #pragma unroll
   for (int pt = 0; pt < (int)kPt; pt++)
 #pragma unroll
     for (int i = 0; i < 4; i++) accg[pt][i] = accu[pt][i] = 0.0f;
-#pragma unroll 1
-  for (uint32_t u = 0; u < U; u++) {
-    Dec ag, au;
-    if constexpr (kType == QT_IQ3_S) {
-      ag.decode(rg, lane, grid_lds);
-      au.decode(ru, lane, grid_lds);
-    } else {
-      ag.decode(rg, lane);
-      au.decode(ru, lane);
-    }
-    if (u + 1 < U) {  // the raw registers are free: the next unit's weights and activations are loaded meanwhile
-      dma.load(g.act, u + 1, &abuf[(u + 1) & 1][0]);
-      rg.load(Mg, U, row0, u + 1, lane);
-      ru.load(Mu, U, row0, u + 1, lane);
-    }
-    const uint8_t *buf = abuf[u & 1];
-    if constexpr (kType == QT_IQ3_S) {
-      // Block by block: the block dots of gate and up for every position tile, each times its row's odd block scale,
-      // added to the unit's integer sums in block order; then d ad isum as UnitIQ3_S::term.
-      int isg[kPt][4], isu[kPt][4];
+  // Unit u. kNext: unit u + 1 exists (its weights are loaded here); kMore: unit u + 2 exists (its activations are
+  // loaded here). Both compile-time, so that the compiler's waits for the weight registers count the loads issued
+  // after them exactly (a run-time condition makes it wait for all). buf (read) and nbuf (filled) are restrict
+  // pointers: the compiler then knows the reads of buf need not wait for the global-to-LDS loads into nbuf.
+  const auto unit = [&](uint32_t u, auto kNext, auto kMore) {
+    const auto body = [&](const uint8_t *__restrict__ buf, uint8_t *__restrict__ nbuf) {
+      constexpr bool next = decltype(kNext)::value, more = decltype(kMore)::value;
+      Dec ag, au;
+      pin(rg), pin(ru);  // the decode starts here, after the previous unit's barrier, not above it
+      if constexpr (kType == QT_IQ3_S) {
+        ag.decode(rg, lane, grid_lds);
+        au.decode(ru, lane, grid_lds);
+      } else {
+        ag.decode(rg, lane);
+        au.decode(ru, lane);
+      }
+      pin(ag), pin(au);  // and ends here, before the next unit's loads into the raw registers
+      if constexpr (next) load_w(u + 1);
+      if constexpr (more) dma.load_all(act_r, u + 2, nbuf, dump);  // the buffer unit u - 1 read before the barrier
+      if constexpr (kType == QT_IQ3_S) {
+        // Block by block: the block dots of gate and up for every position tile, each times its row's odd block
+        // scale, added to the unit's integer sums in block order; then d ad isum as UnitIQ3_S::term.
+        int isg[kPt][4], isu[kPt][4];
 #pragma unroll
-      for (int pt = 0; pt < (int)kPt; pt++)
+        for (int pt = 0; pt < (int)kPt; pt++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) isg[pt][i] = isu[pt][i] = 0;
+          for (int i = 0; i < 4; i++) isg[pt][i] = isu[pt][i] = 0;
 #pragma unroll
-      for (uint32_t ib = 0; ib < 8; ib++) {
-        const uint32_t bofs = mfma_code_off(4 * ib + lane / 16);  // the lane's 8 codes of block ib
-        int lg[4], lu[4];
+        for (uint32_t ib = 0; ib < 8; ib++) {
+          const uint32_t bofs = mfma_code_off(4 * ib + lane / 16);  // the lane's 8 codes of block ib
+          int lg[4], lu[4];
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) lg[i] = ag.ls(i, ib), lu[i] = au.ls(i, ib);
+          for (uint32_t i = 0; i < 4; i++) lg[i] = ag.ls(i, ib), lu[i] = au.ls(i, ib);
+#pragma unroll
+          for (uint32_t pt = 0; pt < kPt; pt++) {
+            if (pt < npt) {
+              const long bw = *(const long *)(buf + (16 * pt + lane % 16) * kActLds + bofs);
+              const v4i_t dg = __builtin_amdgcn_mfma_i32_16x16x32_i8(ag.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+              const v4i_t du = __builtin_amdgcn_mfma_i32_16x16x32_i8(au.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+              for (int i = 0; i < 4; i++) isg[pt][i] += __mul24(lg[i], dg[i]), isu[pt][i] += __mul24(lu[i], du[i]);
+            }
+          }
+        }
 #pragma unroll
         for (uint32_t pt = 0; pt < kPt; pt++) {
           if (pt < npt) {
-            const long bw = *(const long *)(buf + (16 * pt + lane % 16) * kActLds + bofs);
-            const v4i_t dg = __builtin_amdgcn_mfma_i32_16x16x32_i8(ag.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
-            const v4i_t du = __builtin_amdgcn_mfma_i32_16x16x32_i8(au.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+            const float ad = *(const float *)(buf + (16 * pt + lane % 16) * kActLds + kActScales);
 #pragma unroll
-            for (int i = 0; i < 4; i++) isg[pt][i] += __mul24(lg[i], dg[i]), isu[pt][i] += __mul24(lu[i], du[i]);
+            for (int i = 0; i < 4; i++) {
+              accg[pt][i] = __fadd_rn(accg[pt][i], __fmul_rn(__fmul_rn(ag.d[i], ad), (float)isg[pt][i]));
+              accu[pt][i] = __fadd_rn(accu[pt][i], __fmul_rn(__fmul_rn(au.d[i], ad), (float)isu[pt][i]));
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (uint32_t pt = 0; pt < kPt; pt++) {
+          if (pt < npt) {
+            ActBP b;
+            b.load(buf + (16 * pt + lane % 16) * kActLds, lane);
+            float tg[4], tu[4];
+            q4k_terms_v(ag, b.q, b.bh, b.bl, b.ad, tg);
+            q4k_terms_v(au, b.q, b.bh, b.bl, b.ad, tu);
+#pragma unroll
+            for (int i = 0; i < 4; i++) accg[pt][i] = __fadd_rn(accg[pt][i], tg[i]), accu[pt][i] = __fadd_rn(accu[pt][i], tu[i]);
           }
         }
       }
-#pragma unroll
-      for (uint32_t pt = 0; pt < kPt; pt++) {
-        if (pt < npt) {
-          const float ad = *(const float *)(buf + (16 * pt + lane % 16) * kActLds + kActScales);
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            accg[pt][i] = __fadd_rn(accg[pt][i], __fmul_rn(__fmul_rn(ag.d[i], ad), (float)isg[pt][i]));
-            accu[pt][i] = __fadd_rn(accu[pt][i], __fmul_rn(__fmul_rn(au.d[i], ad), (float)isu[pt][i]));
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (uint32_t pt = 0; pt < kPt; pt++) {
-        if (pt < npt) {
-          ActBP b;
-          b.load(buf + (16 * pt + lane % 16) * kActLds, lane);
-          float tg[4], tu[4];
-          q4k_terms_v(ag, b.q, b.bh, b.bl, b.ad, tg);
-          q4k_terms_v(au, b.q, b.bh, b.bl, b.ad, tu);
-#pragma unroll
-          for (int i = 0; i < 4; i++) accg[pt][i] = __fadd_rn(accg[pt][i], tg[i]), accu[pt][i] = __fadd_rn(accu[pt][i], tu[i]);
-        }
-      }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of unit u + 1 have landed
-    __syncthreads();
-  }
+      wait_next(more);  // unit u + 1's loads have landed (this wave's) ...
+      unit_barrier();   // ... and every wave's; every wave is done with buffer u % 3, which unit u + 3 fills
+    };
+    body(abuf[u % kBufs], abuf[(u + 2) % kBufs]);
+  };
+  using yes = std::true_type;
+  using no = std::false_type;
+#pragma unroll 1
+  for (uint32_t u = 0; u + 2 < U; u++) unit(u, yes{}, yes{});
+  unit(U - 2, yes{}, no{});
+  unit(U - 1, no{}, no{});
   // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16, gate and up alike.
   const uint32_t r4 = 4 * (lane / 16), c16 = lane % 16;
 #pragma unroll
@@ -829,6 +955,14 @@ struct HookScope {
 // Gate/up (SwiGLU into h) over nx tiles or chunks (at most; the kernel reads how many there are): Q8_0 on pf_gemm16
 // (64-position tiles, 32 rows of gate and of up a work-group), Q4_K and IQ3_S on pf_gate_up (gu_pos positions and
 // rows of each a work-group).
+// Explicit instantiations: with only the implicit ones, this compiler's host pass emits the launch stub of the
+// first pf_gate_up instantiation it meets and silently drops the second (and with it launch_gemm<false>), which
+// then fails at load time as an undefined symbol.
+template __global__ void pf_gate_up<QT_Q4_K, MOE_TILE>(PfGemm);
+template __global__ void pf_gate_up<QT_IQ3_S, MOE_TILE>(PfGemm);
+template void launch_gemm<false>(uint32_t, uint32_t, dim3, const PfGemm &, hipStream_t);
+template void launch_gemm<true>(uint32_t, uint32_t, dim3, const PfGemm &, hipStream_t);
+
 void launch_gate_up(uint32_t type, const PfGemm &q, uint32_t T, uint32_t F, uint32_t Ug, uint32_t nx, hipStream_t s) {
   (void)T;
   const uint32_t ny = gu_fused(type) ? F / gu_pos(type) : F / gemm_rows<true>();
