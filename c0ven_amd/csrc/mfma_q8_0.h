@@ -31,6 +31,7 @@ struct Q80Raw {
       dv[i] = *(const uint4 *)(tile + (uint64_t)q8_0t::kD * nl + (uint64_t)id * 16);
     }
   }
+  __device__ __forceinline__ void widen(uint32_t) {}  // the codes are the bytes
   // Block j's scale of D row 4 g + i.
   __device__ __forceinline__ float d(uint32_t i, uint32_t j) const {
     const uint32_t w[4] = {dv[i].x, dv[i].y, dv[i].z, dv[i].w};
@@ -50,13 +51,23 @@ struct Iq4nlRaw {
 #pragma unroll
     for (uint32_t j = 0; j < 8; j++) {  // values 8 g .. 8 g + 7: nibbles (g / 2 high) of bytes 8 (g % 2) .. + 7
       const uint2 b = *(const uint2 *)(tile + ((uint64_t)(iq4_nlt::kQs / 16 + j) * nl + ia) * 16 + 8 * (g % 2));
-      const uint32_t sh = 4 * (g / 2);
-      qs[j] = (long)(((uint64_t)iq4nl_lookup((b.y >> sh) & 0x0f0f0f0fu) << 32) | iq4nl_lookup((b.x >> sh) & 0x0f0f0f0fu));
+      qs[j] = (long)(((uint64_t)b.y << 32) | b.x);  // raw bytes: widen() looks the nibbles up
     }
 #pragma unroll
     for (uint32_t i = 0; i < 4; i++) {
       const uint32_t id = pair_idx((row0 % kTileRows) + 4 * g + i, u);
       dv[i] = *(const uint4 *)(tile + (uint64_t)iq4_nlt::kD * nl + (uint64_t)id * 16);
+    }
+  }
+  // The codes from the raw bytes load left in qs (done once they have arrived, so that a load of the next unit
+  // holds only the raw words).
+  __device__ __forceinline__ void widen(uint32_t lane) {
+    const uint32_t sh = 4 * (lane / 32);
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) {
+      const uint64_t b = (uint64_t)qs[j];
+      qs[j] = (long)(((uint64_t)iq4nl_lookup(((uint32_t)(b >> 32) >> sh) & 0x0f0f0f0fu) << 32) |
+                     iq4nl_lookup(((uint32_t)b >> sh) & 0x0f0f0f0fu));
     }
   }
   __device__ __forceinline__ float d(uint32_t i, uint32_t j) const {
@@ -74,13 +85,19 @@ struct Q20Raw {
     const uint32_t ia = pair_idx((row0 % kTileRows) + lane % 16, u);
 #pragma unroll
     for (uint32_t j = 0; j < 8; j++) {  // half j: values 8 g .. 8 g + 7 are bytes 8 (j % 2) + 2 g, + 1 of block j / 2
-      const uint32_t b = *(const uint16_t *)(tile + ((uint64_t)(q2_0t::kQs / 16 + j / 2) * nl + ia) * 16 + 8 * (j % 2) + 2 * g);
-      qs[j] = (long)(((uint64_t)q2_spread(b >> 8) << 32) | q2_spread(b & 0xffu));
-    }
+      qs[j] = *(const uint16_t *)(tile + ((uint64_t)(q2_0t::kQs / 16 + j / 2) * nl + ia) * 16 + 8 * (j % 2) + 2 * g);
+    }  // raw bytes: widen() spreads the codes
 #pragma unroll
     for (uint32_t i = 0; i < 4; i++) {
       const uint32_t id = pair_idx((row0 % kTileRows) + 4 * g + i, u);
       dv[i] = *(const uint2 *)(tile + (uint64_t)q2_0t::kD * nl + (uint64_t)id * 8);
+    }
+  }
+  __device__ __forceinline__ void widen(uint32_t) {
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) {
+      const uint32_t b = (uint32_t)qs[j];
+      qs[j] = (long)(((uint64_t)q2_spread(b >> 8) << 32) | q2_spread(b & 0xffu));
     }
   }
   __device__ __forceinline__ float d(uint32_t i, uint32_t j) const {

@@ -377,6 +377,71 @@ __device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
   return x * q + min(x, r) + b / 8;
 }
 
+// The s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory loads are outstanding and
+// leaves the other counters alone.
+constexpr uint32_t vm_wait(uint32_t n) { return (n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8); }
+
+// The decoded operands as the outputs of an empty volatile asm with a memory clobber: the decode is done there (it
+// cannot sink below to its uses), and the next unit's loads, issued after it, cannot rise above it. Otherwise the
+// compiler moves the decode past the loads, the old and new raw words are live together, and the waits it inserts
+// for them cover the loads just issued.
+__device__ __forceinline__ void pin(Q4kA &a) {
+  asm volatile("" : "+v"(a.lo[0]), "+v"(a.lo[1]), "+v"(a.lo[2]), "+v"(a.lo[3]), "+v"(a.hi[0]), "+v"(a.hi[1]),
+               "+v"(a.hi[2]), "+v"(a.hi[3]), "+v"(a.mn), "+v"(a.d[0]), "+v"(a.d[1]), "+v"(a.d[2]), "+v"(a.d[3]),
+               "+v"(a.dmin[0]), "+v"(a.dmin[1]), "+v"(a.dmin[2]), "+v"(a.dmin[3]) :: "memory");
+}
+__device__ __forceinline__ void pin(Q4kRaw &r) {
+  asm volatile("" : "+v"(r.qs[0]), "+v"(r.qs[1]), "+v"(r.qs[2]), "+v"(r.qs[3]), "+v"(r.sc[0]), "+v"(r.sc[1]),
+               "+v"(r.sc[2]), "+v"(r.dm[0]), "+v"(r.dm[1]), "+v"(r.dm[2]), "+v"(r.dm[3]) :: "memory");
+}
+
+// A raw buffer resource over p (wave-uniform), the whole 32-bit offset range.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *p) {
+  const uint64_t b = (uint64_t)p;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0, 0xffffffffu, 0x00020000u);
+}
+
+// Q4kRaw's loads for gate and up as buffer loads on the wave's 16-row tiles: a resource over each tile, the lane's
+// three 32-bit offsets (the same for both) worked out once, each field's and unit's offset scalar (the same bytes as
+// Q4kRaw::load_qs / load_meta).
+struct Q4kBuf {
+  const uint8_t *base[2];  // the resources are made at each load (scalar work the compiler keeps out of the loop)
+  uint32_t nl, lq, ls, ld;
+  __device__ __forceinline__ void init(const uint8_t *gate, const uint8_t *up, uint32_t U, uint32_t row0, uint32_t lane) {
+    const uint32_t g = lane / 16, rr = row0 % kTileRows;
+    const uint64_t t = (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q4_K, U);
+    nl = kTileRows * U;
+    base[0] = gate + t, base[1] = up + t;
+    lq = (g / 2) * nl * 16 + (rr + lane % 16) * 16 + 8 * (g % 2);
+    ls = (rr + lane % 16) * 4;
+    ld = (rr + 4 * g) * 4;
+  }
+  __device__ __forceinline__ void load_qs(uint32_t m, Q4kRaw &w, uint32_t u) const {
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(uniform_rsrc(base[m]), lq, (q4_kt::kQs / 16 + 2 * c) * nl * 16 + u * kTileRows * 16, 0);
+      w.qs[c] = make_uint2(v[0], v[1]);
+    }
+  }
+  __device__ __forceinline__ void load_meta(uint32_t m, Q4kRaw &w, uint32_t u) const {
+#pragma unroll
+    for (uint32_t i = 0; i < 3; i++)
+      w.sc[i] = __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(base[m]), ls, (q4_kt::kScales + 4 * i) * nl + u * kTileRows * 4, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(uniform_rsrc(base[m]), ld, q4_kt::kDm * nl + u * kTileRows * 4, 0);
+    w.dm[0] = v[0], w.dm[1] = v[1], w.dm[2] = v[2], w.dm[3] = v[3];
+  }
+};
+
+// A work-group barrier without __syncthreads' fence (which would wait for every load in flight): LDS reads done, then
+// s_barrier, with compiler barriers either side so that no LDS access moves across it.
+__device__ __forceinline__ void unit_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Q4_K, IQ3_S and Q8_0 on 16 x 16 int8 MFMA tiles (mfma_q4k.h, the decode path's tile; mfma_iq3s.h; mfma_q8_0.h):
 // wave w takes 16 weight rows (gate/up: matrix w / 2, rows 16 (w % 2) .. of the work-group's 32 of each; down: rows
 // 16 w .. of its 64) against the tile's positions in 16-position tiles (only those holding positions run), unit by
@@ -389,6 +454,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   // Two activation buffers filled by direct global-to-LDS loads (no registers held), the next unit's issued before
   // the current unit's MFMAs and waited for after them: one barrier a unit, three waves a SIMD.
   __shared__ __align__(16) uint8_t abuf[2][64 * kActLds];
+  __shared__ __align__(16) uint8_t dump[64 * 16];
   // Up sums [row][position], written after the unit loop's last barrier: they reuse the activation buffer.
   static_assert(32 * 65 * sizeof(float) <= 64 * kActLds, "ub must fit in one activation buffer");
   float(*ub)[65] = reinterpret_cast<float(*)[65]>(&abuf[0][0]);
@@ -441,24 +507,36 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
   Dma<64, 4> dma;
   dma.plan(arow_lds, U);
+  const __amdgpu_buffer_rsrc_t act_r = uniform_rsrc(g.act);
+  Q4kBuf wb;  // Q4_K's weight loads as buffer loads (the other types through their Raw::load)
+  if constexpr (kType == QT_Q4_K) wb.init(M, M, U, row0, lane_id());
+  const auto load_w = [&](Raw &r, uint32_t u) {
+    if constexpr (kType == QT_Q4_K)
+      wb.load_qs(0, r, u), wb.load_meta(0, r, u);
+    else
+      r.load(M, U, row0, u, lane_id());
+  };
   Raw raw;
-  raw.load(M, U, row0, 0, lane_id());
-  dma.load(g.act, 0, &abuf[0][0]);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  load_w(raw, 0);
+  dma.load_all(act_r, 0, &abuf[0][0], dump);
+  __builtin_amdgcn_s_waitcnt(vm_wait(0));
+  unit_barrier();
   float acc[4][4];
 #pragma unroll
   for (int pt = 0; pt < 4; pt++)
 #pragma unroll
     for (int i = 0; i < 4; i++) acc[pt][i] = 0.0f;
-#pragma unroll 1
-  for (uint32_t u = 0; u < U; u++) {
+  // buf (read) and nbuf (filled) as restrict pointers: the compiler then knows the reads of buf need not wait for the
+  // global-to-LDS loads into nbuf (without it, each position tile's first LDS read waited for every load in flight).
+  const auto body = [&](uint32_t u, const uint8_t *__restrict__ buf, uint8_t *__restrict__ nbuf) {
+    // Q4_K decodes the unit's raw words first and loads the next unit's into the same registers; the other types read
+    // theirs in the MFMAs and load the next unit's into a second set.
+    constexpr bool kInPlace = kType == QT_Q4_K;
     Raw next;
     if (u + 1 < U) {
-      dma.load(g.act, u + 1, &abuf[(u + 1) & 1][0]);
-      next.load(M, U, row0, u + 1, lane_id());
+      dma.load_all(act_r, u + 1, nbuf, dump);
+      if constexpr (!kInPlace) load_w(next, u + 1);
     }
-    const uint8_t *buf = abuf[u & 1];
     if constexpr (grid_family(kType)) {
       // Block by block: one MFMA a position tile (IQ2_S: one a half block, the other half's A lanes zero), its D
       // times the row's block scale added to the unit's integer sum in block order; then kFactor ((d ad) isum) as
@@ -520,6 +598,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
     } else if constexpr (q8_family(kType)) {
       // Block by block: one MFMA a position tile, the block's term (d_w d_a) dot; the eight terms of the unit as the
       // pairwise tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then added to the row's sum.
+      raw.widen(lane_id());  // IQ4_NL, Q2_0: codes from the raw bytes
       float q[3][4][4];  // the tree's pending partial sums: q[level][pt][row]
 #pragma unroll
       for (uint32_t j = 0; j < 8; j++) {
@@ -558,7 +637,10 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
       }
     } else {
       Q4kA a;
+      pin(raw);  // the decode starts after the previous unit's barrier ...
       a.decode(raw, lane_id());
+      pin(a);  // ... and ends before the next unit's loads into the raw registers
+      if (u + 1 < U) load_w(raw, u + 1);
 #pragma unroll
       for (uint32_t pt = 0; pt < 4; pt++) {
         if (pt < npt) {
@@ -571,10 +653,13 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
         }
       }
     }
-    if (u + 1 < U) raw = next;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of unit u + 1 have landed in LDS
-    __syncthreads();
-  }
+    if constexpr (!kInPlace)
+      if (u + 1 < U) raw = next;
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));  // this wave's loads of unit u + 1 have landed ...
+    unit_barrier();                          // ... and every wave's
+  };
+#pragma unroll 1
+  for (uint32_t u = 0; u < U; u++) body(u, abuf[u & 1], abuf[(u + 1) & 1]);
   // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16.
   const uint32_t l = lane_id(), r4 = 4 * (l / 16), c16 = l % 16;
   if constexpr (kGU) {
@@ -627,70 +712,6 @@ struct Iq3sA {
 };
 
 
-// The s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory loads are outstanding and
-// leaves the other counters alone.
-constexpr uint32_t vm_wait(uint32_t n) { return (n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8); }
-
-// A raw buffer resource over p (wave-uniform), the whole 32-bit offset range.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *p) {
-  const uint64_t b = (uint64_t)p;
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-  return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0, 0xffffffffu, 0x00020000u);
-}
-
-// Q4kRaw's loads for gate and up as buffer loads on the wave's 16-row tiles: a resource over each tile, the lane's
-// three 32-bit offsets (the same for both) worked out once, each field's and unit's offset scalar (the same bytes as
-// Q4kRaw::load_qs / load_meta).
-struct Q4kBuf {
-  const uint8_t *base[2];  // the resources are made at each load (scalar work the compiler keeps out of the loop)
-  uint32_t nl, lq, ls, ld;
-  __device__ __forceinline__ void init(const uint8_t *gate, const uint8_t *up, uint32_t U, uint32_t row0, uint32_t lane) {
-    const uint32_t g = lane / 16, rr = row0 % kTileRows;
-    const uint64_t t = (uint64_t)(row0 / kTileRows) * tile_bytes(QT_Q4_K, U);
-    nl = kTileRows * U;
-    base[0] = gate + t, base[1] = up + t;
-    lq = (g / 2) * nl * 16 + (rr + lane % 16) * 16 + 8 * (g % 2);
-    ls = (rr + lane % 16) * 4;
-    ld = (rr + 4 * g) * 4;
-  }
-  __device__ __forceinline__ void load_qs(uint32_t m, Q4kRaw &w, uint32_t u) const {
-#pragma unroll
-    for (uint32_t c = 0; c < 4; c++) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(uniform_rsrc(base[m]), lq, (q4_kt::kQs / 16 + 2 * c) * nl * 16 + u * kTileRows * 16, 0);
-      w.qs[c] = make_uint2(v[0], v[1]);
-    }
-  }
-  __device__ __forceinline__ void load_meta(uint32_t m, Q4kRaw &w, uint32_t u) const {
-#pragma unroll
-    for (uint32_t i = 0; i < 3; i++)
-      w.sc[i] = __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(base[m]), ls, (q4_kt::kScales + 4 * i) * nl + u * kTileRows * 4, 0);
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(uniform_rsrc(base[m]), ld, q4_kt::kDm * nl + u * kTileRows * 4, 0);
-    w.dm[0] = v[0], w.dm[1] = v[1], w.dm[2] = v[2], w.dm[3] = v[3];
-  }
-};
-
-// A work-group barrier without __syncthreads' fence (which would wait for every load in flight): LDS reads done, then
-// s_barrier, with compiler barriers either side so that no LDS access moves across it.
-__device__ __forceinline__ void unit_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// The decoded operands as the outputs of an empty volatile asm with a memory clobber: the decode is done there (it
-// cannot sink below to its uses), and the next unit's loads, issued after it, cannot rise above it. Otherwise the
-// compiler moves the decode past the loads, the old and new raw words are live together, and the waits it inserts
-// for them cover the loads just issued.
-__device__ __forceinline__ void pin(Q4kA &a) {
-  asm volatile("" : "+v"(a.lo[0]), "+v"(a.lo[1]), "+v"(a.lo[2]), "+v"(a.lo[3]), "+v"(a.hi[0]), "+v"(a.hi[1]),
-               "+v"(a.hi[2]), "+v"(a.hi[3]), "+v"(a.mn), "+v"(a.d[0]), "+v"(a.d[1]), "+v"(a.d[2]), "+v"(a.d[3]),
-               "+v"(a.dmin[0]), "+v"(a.dmin[1]), "+v"(a.dmin[2]), "+v"(a.dmin[3]) :: "memory");
-}
-__device__ __forceinline__ void pin(Q4kRaw &r) {
-  asm volatile("" : "+v"(r.qs[0]), "+v"(r.qs[1]), "+v"(r.qs[2]), "+v"(r.qs[3]), "+v"(r.sc[0]), "+v"(r.sc[1]),
-               "+v"(r.sc[2]), "+v"(r.dm[0]), "+v"(r.dm[1]), "+v"(r.dm[2]), "+v"(r.dm[3]) :: "memory");
-}
 __device__ __forceinline__ void pin(Iq3sRaw &r) {
   asm volatile("" : "+v"(r.qs[0]), "+v"(r.qs[1]), "+v"(r.qs[2]), "+v"(r.qs[3]), "+v"(r.qs[4]), "+v"(r.qs[5]),
                "+v"(r.qs[6]), "+v"(r.qs[7]), "+v"(r.sg[0]), "+v"(r.sg[1]), "+v"(r.sg[2]), "+v"(r.sg[3]), "+v"(r.sg[4]),
@@ -956,10 +977,21 @@ struct HookScope {
 // (64-position tiles, 32 rows of gate and of up a work-group), Q4_K and IQ3_S on pf_gate_up (gu_pos positions and
 // rows of each a work-group).
 // Explicit instantiations: with only the implicit ones, this compiler's host pass emits the launch stub of the
-// first pf_gate_up instantiation it meets and silently drops the second (and with it launch_gemm<false>), which
-// then fails at load time as an undefined symbol.
+// first instantiation of a kernel template whose body holds a lambda and silently drops the later ones (and with
+// them launch_gemm<false>), which then fail at load time as undefined symbols.
 template __global__ void pf_gate_up<QT_Q4_K, MOE_TILE>(PfGemm);
 template __global__ void pf_gate_up<QT_IQ3_S, MOE_TILE>(PfGemm);
+#define C0VEN_PF_GEMM16(T)                          \
+  template __global__ void pf_gemm16<T, true>(PfGemm); \
+  template __global__ void pf_gemm16<T, false>(PfGemm);
+C0VEN_PF_GEMM16(QT_Q4_K)
+C0VEN_PF_GEMM16(QT_IQ3_S)
+C0VEN_PF_GEMM16(QT_Q8_0)
+C0VEN_PF_GEMM16(QT_IQ4_NL)
+C0VEN_PF_GEMM16(QT_Q2_0)
+C0VEN_PF_GEMM16(QT_IQ3_XXS)
+C0VEN_PF_GEMM16(QT_IQ2_S)
+#undef C0VEN_PF_GEMM16
 template void launch_gemm<false>(uint32_t, uint32_t, dim3, const PfGemm &, hipStream_t);
 template void launch_gemm<true>(uint32_t, uint32_t, dim3, const PfGemm &, hipStream_t);
 
