@@ -73,6 +73,22 @@ def test_prefill_shapes_no_shared_and_limit(H, F):
     blk.close()
 
 
+@pytest.mark.parametrize("H,F,types", [(2560, 640, (Q4, Q8, Q4, Q8)), (2560, 640, (I3, Q8, I3, Q8)),
+                                         (1536, 256, (Q4, Q4, I3, Q4))])
+def test_prefill_unit_counts(H, F, types):
+    # The fused gate/up kernel runs its unit loop for U - 2 units and then the last two apart (the loads of the
+    # next units issued from compile-time flags): U = 10 and 6 here, besides 2, 4 and 8 above.
+    gt, dt, sgt, sdt = types
+    say("prefill unit counts", H, F, [moe.TYPE_NAMES[t] for t in types])
+    L = h.Layer(H, F, 32, 6, gt, dt, sgt, sdt, seed=77 + H)
+    blk = L.block(max_tokens=256)
+    L.upload(blk)
+    x = h.tokens(11, 150, H)
+    y, ids, w = blk.forward(0, x)
+    check_exact(y, ids, w, *L.oracle_forward(x))
+    blk.close()
+
+
 def test_prefill_then_decode_share_a_context():
     """Both paths on one context, alternating: each call's result stands alone."""
     say("prefill and decode alternate")
