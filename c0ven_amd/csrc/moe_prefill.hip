@@ -692,11 +692,11 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   }
 }
 
-// Gate/up for Q4_K and IQ3_S, both matrices in one wave: wave w takes rows 16 w .. 16 w + 15 of gate AND of up (a
-// work-group 64 rows of each), so every activation operand read from LDS feeds two MFMA chains and SwiGLU pairs
-// gate and up in the same lane (no exchange). A unit's weights are decoded for both matrices, then its raw bytes'
-// registers take the next unit's loads (issued before the MFMAs, waited for after them with the activations).
-// The integers and fp32 steps are pf_gemm16's: UnitQ4_K::term / UnitIQ3_S::term, units added in sequence.
+// IQ3_S gate/up, both matrices in one wave: wave w takes rows 16 w .. 16 w + 15 of gate AND of up (a work-group 64
+// rows of each), so every activation operand read from LDS feeds two MFMA chains and SwiGLU pairs gate and up in the
+// same lane (no exchange). A unit's weights are decoded for both matrices, then its raw bytes' registers take the next
+// unit's loads (issued before the MFMAs, waited for after them with the activations). The integers and fp32 steps
+// are pf_gemm16's (UnitIQ3_S::term), units added in sequence. Q4_K runs on pf_gate_up_q4k below.
 struct Iq3sA {
   long a[8];       // the eight blocks' A operands (signed codes)
   uint32_t sc[4];  // the scale nibbles of the lane's D rows
@@ -730,7 +730,7 @@ __device__ __forceinline__ void pin(Iq3sA &a) {
 // work-group a CU by LDS, measured slower at config 4: 269 against 223 us.)
 template <uint32_t kType, uint32_t kPos>
 __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2))) pf_gate_up(PfGemm g) {
-  static_assert(kType == QT_Q4_K || kType == QT_IQ3_S, "pf_gate_up: Q4_K and IQ3_S");
+  static_assert(kType == QT_IQ3_S, "pf_gate_up: IQ3_S (Q4_K runs on pf_gate_up_seq)");
   const uint32_t U = g.U;  // at least 2: n_embd is a multiple of 512
   constexpr uint32_t kWaves = kPos / 16, kThreads = 64 * kWaves, kRows = 16 * kWaves, kPt = kPos / 16;
   // The activations are loaded two units ahead (three LDS buffers), the weights one unit ahead (the registers of the
@@ -740,9 +740,9 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2
   __shared__ __align__(16) uint8_t dump[64 * 16];
   __shared__ uint32_t arow_lds[kPos];
   __shared__ uint64_t tab[32];
-  __shared__ uint32_t grid_lds[kType == QT_IQ3_S ? 512 : 1];
-  using Raw = std::conditional_t<kType == QT_IQ3_S, Iq3sRaw, Q4kRaw>;
-  using Dec = std::conditional_t<kType == QT_IQ3_S, Iq3sA, Q4kA>;
+  __shared__ uint32_t grid_lds[512];
+  using Raw = Iq3sRaw;
+  using Dec = Iq3sA;
   const uint32_t nrb = g.row_blocks;
   const uint32_t nch = g.shared_T ? (g.shared_T + kPos - 1) / kPos : *g.ntiles, n = nch * nrb;
   if (blockIdx.x >= n) return;
@@ -758,8 +758,7 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2
   }
   const uint32_t tid = tid_fresh();
   if (tid < 32) tab[tid] = kExp2Tab[tid];
-  if constexpr (kType == QT_IQ3_S)
-    for (uint32_t i = tid; i < 512; i += kThreads) grid_lds[i] = kIq3sGridPf[i];
+  for (uint32_t i = tid; i < 512; i += kThreads) grid_lds[i] = kIq3sGridPf[i];
   if (tid < kPos) {
     const uint32_t pos = start + tid;
     arow_lds[tid] = tid < count ? (g.perm ? g.perm[pos] / g.K : pos) : 0xffffffffu;
@@ -771,17 +770,10 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2
   Dma<kPos, kWaves> dma;
   dma.plan(arow_lds, U);
   const __amdgpu_buffer_rsrc_t act_r = uniform_rsrc(g.act);
-  Q4kBuf wb;  // Q4_K's weight loads (IQ3_S loads through Iq3sRaw::load)
-  if constexpr (kType == QT_Q4_K) wb.init(Mg, Mu, U, row0, lane);
   Raw rg, ru;
   const auto load_w = [&](uint32_t u) {
-    if constexpr (kType == QT_Q4_K) {
-      wb.load_qs(0, rg, u), wb.load_meta(0, rg, u);
-      wb.load_qs(1, ru, u), wb.load_meta(1, ru, u);
-    } else {
-      rg.load(Mg, U, row0, u, lane);
-      ru.load(Mu, U, row0, u, lane);
-    }
+    rg.load(Mg, U, row0, u, lane);
+    ru.load(Mu, U, row0, u, lane);
   };
   // The end of unit u waits for unit u + 1's loads, leaving in flight only the activation loads of unit u + 2 (issued
   // after them): kPer a wave (load_all issues the same count in every wave). As the builtin, not asm, so that the
@@ -811,63 +803,43 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2
       constexpr bool next = decltype(kNext)::value, more = decltype(kMore)::value;
       Dec ag, au;
       pin(rg), pin(ru);  // the decode starts here, after the previous unit's barrier, not above it
-      if constexpr (kType == QT_IQ3_S) {
-        ag.decode(rg, lane, grid_lds);
-        au.decode(ru, lane, grid_lds);
-      } else {
-        ag.decode(rg, lane);
-        au.decode(ru, lane);
-      }
+      ag.decode(rg, lane, grid_lds);
+      au.decode(ru, lane, grid_lds);
       pin(ag), pin(au);  // and ends here, before the next unit's loads into the raw registers
       if constexpr (next) load_w(u + 1);
       if constexpr (more) dma.load_all(act_r, u + 2, nbuf, dump);  // the buffer unit u - 1 read before the barrier
-      if constexpr (kType == QT_IQ3_S) {
-        // Block by block: the block dots of gate and up for every position tile, each times its row's odd block
-        // scale, added to the unit's integer sums in block order; then d ad isum as UnitIQ3_S::term.
-        int isg[kPt][4], isu[kPt][4];
+      // Block by block: the block dots of gate and up for every position tile, each times its row's odd block
+      // scale, added to the unit's integer sums in block order; then d ad isum as UnitIQ3_S::term.
+      int isg[kPt][4], isu[kPt][4];
 #pragma unroll
-        for (int pt = 0; pt < (int)kPt; pt++)
+      for (int pt = 0; pt < (int)kPt; pt++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) isg[pt][i] = isu[pt][i] = 0;
+        for (int i = 0; i < 4; i++) isg[pt][i] = isu[pt][i] = 0;
 #pragma unroll
-        for (uint32_t ib = 0; ib < 8; ib++) {
-          const uint32_t bofs = mfma_code_off(4 * ib + lane / 16);  // the lane's 8 codes of block ib
-          int lg[4], lu[4];
+      for (uint32_t ib = 0; ib < 8; ib++) {
+        const uint32_t bofs = mfma_code_off(4 * ib + lane / 16);  // the lane's 8 codes of block ib
+        int lg[4], lu[4];
 #pragma unroll
-          for (uint32_t i = 0; i < 4; i++) lg[i] = ag.ls(i, ib), lu[i] = au.ls(i, ib);
-#pragma unroll
-          for (uint32_t pt = 0; pt < kPt; pt++) {
-            if (pt < npt) {
-              const long bw = *(const long *)(buf + (16 * pt + lane % 16) * kActLds + bofs);
-              const v4i_t dg = __builtin_amdgcn_mfma_i32_16x16x32_i8(ag.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
-              const v4i_t du = __builtin_amdgcn_mfma_i32_16x16x32_i8(au.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-              for (int i = 0; i < 4; i++) isg[pt][i] += __mul24(lg[i], dg[i]), isu[pt][i] += __mul24(lu[i], du[i]);
-            }
-          }
-        }
+        for (uint32_t i = 0; i < 4; i++) lg[i] = ag.ls(i, ib), lu[i] = au.ls(i, ib);
 #pragma unroll
         for (uint32_t pt = 0; pt < kPt; pt++) {
           if (pt < npt) {
-            const float ad = *(const float *)(buf + (16 * pt + lane % 16) * kActLds + kActScales);
+            const long bw = *(const long *)(buf + (16 * pt + lane % 16) * kActLds + bofs);
+            const v4i_t dg = __builtin_amdgcn_mfma_i32_16x16x32_i8(ag.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+            const v4i_t du = __builtin_amdgcn_mfma_i32_16x16x32_i8(au.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-              accg[pt][i] = __fadd_rn(accg[pt][i], __fmul_rn(__fmul_rn(ag.d[i], ad), (float)isg[pt][i]));
-              accu[pt][i] = __fadd_rn(accu[pt][i], __fmul_rn(__fmul_rn(au.d[i], ad), (float)isu[pt][i]));
-            }
+            for (int i = 0; i < 4; i++) isg[pt][i] += __mul24(lg[i], dg[i]), isu[pt][i] += __mul24(lu[i], du[i]);
           }
         }
-      } else {
+      }
 #pragma unroll
-        for (uint32_t pt = 0; pt < kPt; pt++) {
-          if (pt < npt) {
-            ActBP b;
-            b.load(buf + (16 * pt + lane % 16) * kActLds, lane);
-            float tg[4], tu[4];
-            q4k_terms_v(ag, b.q, b.bh, b.bl, b.ad, tg);
-            q4k_terms_v(au, b.q, b.bh, b.bl, b.ad, tu);
+      for (uint32_t pt = 0; pt < kPt; pt++) {
+        if (pt < npt) {
+          const float ad = *(const float *)(buf + (16 * pt + lane % 16) * kActLds + kActScales);
 #pragma unroll
-            for (int i = 0; i < 4; i++) accg[pt][i] = __fadd_rn(accg[pt][i], tg[i]), accu[pt][i] = __fadd_rn(accu[pt][i], tu[i]);
+          for (int i = 0; i < 4; i++) {
+            accg[pt][i] = __fadd_rn(accg[pt][i], __fmul_rn(__fmul_rn(ag.d[i], ad), (float)isg[pt][i]));
+            accu[pt][i] = __fadd_rn(accu[pt][i], __fmul_rn(__fmul_rn(au.d[i], ad), (float)isu[pt][i]));
           }
         }
       }
@@ -882,6 +854,109 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2
   for (uint32_t u = 0; u + 2 < U; u++) unit(u, yes{}, yes{});
   unit(U - 2, yes{}, no{});
   unit(U - 1, no{}, no{});
+  // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16, gate and up alike.
+  const uint32_t r4 = 4 * (lane / 16), c16 = lane % 16;
+#pragma unroll
+  for (uint32_t pt = 0; pt < kPt; pt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t m = 16 * pt + c16;
+      if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = swiglu_one(accg[pt][i], accu[pt][i], g.limit, tab);
+    }
+}
+
+// Q4_K gate/up at three waves a SIMD: a unit's gate products come before its up products, so that one matrix's
+// decoded operands are live at a time (150 registers; the activation operands are read from LDS once for each), and
+// the activations are loaded one unit ahead into two LDS buffers (44 KB a work-group, three a CU). Wave w takes rows
+// 16 w .. 16 w + 15 of gate and of up (a work-group 64 rows of each, kPos = 64 positions, four waves), so SwiGLU pairs
+// gate and up in the same lane. A matrix's weights are decoded, then the registers of its raw bytes take the next
+// unit's loads (buffer loads on scalar bases), which the end of the unit waits for with the activations; the
+// barriers are plain ones (a fence would wait for every load in flight). The integers and fp32 steps are pf_gemm16's
+// (UnitQ4_K::term), units added in sequence. (IQ3_S in this form, at two waves a SIMD by registers, measured slower
+// than pf_gate_up: 411 against 370 us at config 5p.)
+template <uint32_t kPos>
+__global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3))) pf_gate_up_q4k(PfGemm g) {
+  const uint32_t U = g.U;
+  constexpr uint32_t kWaves = kPos / 16, kRows = 16 * kWaves, kPt = kPos / 16;
+  __shared__ __align__(16) uint8_t abuf[2][kPos * kActLds];
+  __shared__ __align__(16) uint8_t dump[64 * 16];
+  __shared__ uint32_t arow_lds[kPos];
+  __shared__ uint64_t tab[32];
+  const uint32_t nrb = g.row_blocks;
+  const uint32_t nch = g.shared_T ? (g.shared_T + kPos - 1) / kPos : *g.ntiles, n = nch * nrb;
+  if (blockIdx.x >= n) return;
+  const uint32_t L = xcd_logical(blockIdx.x, n);
+  const uint32_t ch_i = L / nrb, rb = L % nrb;
+  uint32_t start, count, e;
+  if (g.shared_T) {
+    start = kPos * ch_i;
+    count = min(kPos, g.shared_T - start), e = 0;
+  } else {
+    const MoeTile tl = g.tiles[ch_i];
+    start = tl.start, count = tl.count, e = tl.slot;
+  }
+  const uint32_t tid = tid_fresh();
+  if (tid < 32) tab[tid] = kExp2Tab[tid];
+  if (tid < kPos) {
+    const uint32_t pos = start + tid;
+    arow_lds[tid] = tid < count ? (g.perm ? g.perm[pos] / g.K : pos) : 0xffffffffu;
+  }
+  __syncthreads();
+  const uint32_t row0 = rb * kRows + 16 * (uint32_t)__builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
+  const uint8_t *Mg = g.mat + (uint64_t)e * g.stride, *Mu = Mg + g.up_off;
+  const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
+  Dma<kPos, kWaves> dma;
+  dma.plan(arow_lds, U);
+  const __amdgpu_buffer_rsrc_t act_r = uniform_rsrc(g.act);
+  Q4kBuf wb;
+  wb.init(Mg, Mu, U, row0, lane);
+  const auto load_w = [&](Q4kRaw &raw, uint32_t m, uint32_t u) { wb.load_qs(m, raw, u), wb.load_meta(m, raw, u); };
+  Q4kRaw rg, ru;
+  load_w(rg, 0, 0);
+  load_w(ru, 1, 0);
+  dma.load_all(act_r, 0, &abuf[0][0], dump);
+  __builtin_amdgcn_s_waitcnt(vm_wait(0));
+  unit_barrier();
+  float accg[kPt][4], accu[kPt][4];
+#pragma unroll
+  for (int pt = 0; pt < (int)kPt; pt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) accg[pt][i] = accu[pt][i] = 0.0f;
+  // Unit u; kNext: unit u + 1 exists (its loads are issued here). Compile-time, so that the compiler's waits for the
+  // weight registers count the loads issued after them exactly. buf (read) and nbuf (filled) are restrict pointers:
+  // the compiler then knows the reads of buf need not wait for the global-to-LDS loads into nbuf.
+  const auto unit = [&](uint32_t u, auto kNext) {
+    const auto body = [&](const uint8_t *__restrict__ buf, uint8_t *__restrict__ nbuf) {
+      constexpr bool next = decltype(kNext)::value;
+      if constexpr (next) dma.load_all(act_r, u + 1, nbuf, dump);  // the buffer unit u - 1 read before the barrier
+      const auto pass = [&](Q4kRaw &raw, uint32_t m, float (&acc)[kPt][4]) {
+        Q4kA a;
+        pin(raw);  // the decode starts after the previous barrier ...
+        a.decode(raw, lane);
+        pin(a);  // ... and ends before the next unit's loads into the raw registers
+        if constexpr (next) load_w(raw, m, u + 1);
+#pragma unroll
+        for (uint32_t pt = 0; pt < kPt; pt++) {
+          if (pt < npt) {
+            ActBP b;
+            b.load(buf + (16 * pt + lane % 16) * kActLds, lane);
+            float t[4];
+            q4k_terms_v(a, b.q, b.bh, b.bl, b.ad, t);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[pt][i] = __fadd_rn(acc[pt][i], t[i]);
+          }
+        }
+      };
+      pass(rg, 0, accg);
+      pass(ru, 1, accu);
+      __builtin_amdgcn_s_waitcnt(vm_wait(0));  // unit u + 1's loads (this wave's) ...
+      unit_barrier();                          // ... and every wave's; buffer u % 2 is free for unit u + 2
+    };
+    body(abuf[u & 1], abuf[(u + 1) & 1]);
+  };
+#pragma unroll 1
+  for (uint32_t u = 0; u + 1 < U; u++) unit(u, std::true_type{});
+  unit(U - 1, std::false_type{});
   // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16, gate and up alike.
   const uint32_t r4 = 4 * (lane / 16), c16 = lane % 16;
 #pragma unroll
@@ -937,7 +1012,7 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
     q.row_blocks = grid.y;
     const dim3 g2(grid.x * q.row_blocks), wg(4 * MOE_TILE);
     if (type == QT_Q4_K)
-      pf_gate_up<QT_Q4_K, MOE_TILE><<<g2, wg, 0, s>>>(q);
+      pf_gate_up_q4k<MOE_TILE><<<g2, wg, 0, s>>>(q);
     else
       pf_gate_up<QT_IQ3_S, MOE_TILE><<<g2, wg, 0, s>>>(q);
     return;
@@ -979,7 +1054,7 @@ struct HookScope {
 // Explicit instantiations: with only the implicit ones, this compiler's host pass emits the launch stub of the
 // first instantiation of a kernel template whose body holds a lambda and silently drops the later ones (and with
 // them launch_gemm<false>), which then fail at load time as undefined symbols.
-template __global__ void pf_gate_up<QT_Q4_K, MOE_TILE>(PfGemm);
+template __global__ void pf_gate_up_q4k<MOE_TILE>(PfGemm);
 template __global__ void pf_gate_up<QT_IQ3_S, MOE_TILE>(PfGemm);
 #define C0VEN_PF_GEMM16(T)                          \
   template __global__ void pf_gemm16<T, true>(PfGemm); \
@@ -1047,14 +1122,14 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
   const uint32_t H = S.H, F = S.F, E = S.E, K = S.K, T = S.T, Ug = units_of(H), Ud = units_of(F);
   const uint32_t xr = quant_vec_dot_type(S.gate_type);
   const uint32_t xs = S.has_shared ? quant_vec_dot_type(S.sh_gate_type) : xr;
-  const uint32_t hr = quant_vec_dot_type(S.down_type), hs = quant_vec_dot_type(S.sh_down_type);
+  const uint32_t hs = quant_vec_dot_type(S.sh_down_type);
   const uint32_t halfwaves = kPfWG / 32;
   {
     HookScope k(hook, "pf_quant_x", st);
     pf_quant_rows<<<(T * Ug + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(x, H, T, Ug, xr, b.act_r, xs,
                                                                             b.act_s != b.act_r ? b.act_s : nullptr);
   }
-  const uint32_t mt = pf_max_tiles(T, K, E), st_tiles = (T + MOE_TILE - 1) / MOE_TILE;
+  const uint32_t st_tiles = (T + MOE_TILE - 1) / MOE_TILE;
   if (S.has_shared) {  // the shared expert needs no routing: its launches run beside the router on the side stream
     hipStream_t ss = b.side;
     if (hipEventRecord(b.fork, st) != hipSuccess || hipStreamWaitEvent(ss, b.fork, 0) != hipSuccess)
