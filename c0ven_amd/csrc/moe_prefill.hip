@@ -692,177 +692,12 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   }
 }
 
-// IQ3_S gate/up, both matrices in one wave: wave w takes rows 16 w .. 16 w + 15 of gate AND of up (a work-group 64
-// rows of each), so every activation operand read from LDS feeds two MFMA chains and SwiGLU pairs gate and up in the
-// same lane (no exchange). A unit's weights are decoded for both matrices, then its raw bytes' registers take the next
-// unit's loads (issued before the MFMAs, waited for after them with the activations). The integers and fp32 steps
-// are pf_gemm16's (UnitIQ3_S::term), units added in sequence. Q4_K runs on pf_gate_up_q4k below.
-struct Iq3sA {
-  long a[8];       // the eight blocks' A operands (signed codes)
-  uint32_t sc[4];  // the scale nibbles of the lane's D rows
-  float d[4];
-  __device__ __forceinline__ void decode(const Iq3sRaw &r, uint32_t lane, const uint32_t *grid) {
-#pragma unroll
-    for (uint32_t ib = 0; ib < 8; ib++) a[ib] = r.a_block(ib, lane, grid);
-#pragma unroll
-    for (uint32_t i = 0; i < 4; i++) sc[i] = r.sc[i], d[i] = h2f((uint16_t)r.dh[i]);
-  }
-  // Block ib's odd scale 1 + 2 s of D row 4 g + i.
-  __device__ __forceinline__ int ls(uint32_t i, uint32_t ib) const { return 1 + 2 * (int)((sc[i] >> (4 * ib)) & 15u); }
-};
-
-
 __device__ __forceinline__ void pin(Iq3sRaw &r) {
   asm volatile("" : "+v"(r.qs[0]), "+v"(r.qs[1]), "+v"(r.qs[2]), "+v"(r.qs[3]), "+v"(r.qs[4]), "+v"(r.qs[5]),
                "+v"(r.qs[6]), "+v"(r.qs[7]), "+v"(r.sg[0]), "+v"(r.sg[1]), "+v"(r.sg[2]), "+v"(r.sg[3]), "+v"(r.sg[4]),
                "+v"(r.sg[5]), "+v"(r.sg[6]), "+v"(r.sg[7]) :: "memory");
   asm volatile("" : "+v"(r.qh[0]), "+v"(r.qh[1]), "+v"(r.sc[0]), "+v"(r.sc[1]), "+v"(r.sc[2]), "+v"(r.sc[3]),
                "+v"(r.dh[0]), "+v"(r.dh[1]), "+v"(r.dh[2]), "+v"(r.dh[3]) :: "memory");
-}
-__device__ __forceinline__ void pin(Iq3sA &a) {
-  asm volatile("" : "+v"(a.a[0]), "+v"(a.a[1]), "+v"(a.a[2]), "+v"(a.a[3]), "+v"(a.a[4]), "+v"(a.a[5]),
-               "+v"(a.a[6]), "+v"(a.a[7]), "+v"(a.sc[0]), "+v"(a.sc[1]), "+v"(a.sc[2]), "+v"(a.sc[3]), "+v"(a.d[0]),
-               "+v"(a.d[1]), "+v"(a.d[2]), "+v"(a.d[3]) :: "memory");
-}
-
-// A work-group takes kPos positions of one expert (a MoeTile) and 16 rows a wave of gate and of up (kPos / 16 waves),
-// so that a unit's weights, once decoded, meet kPos / 16 position tiles of 16. (128 positions, eight waves, one
-// work-group a CU by LDS, measured slower at config 4: 269 against 223 us.)
-template <uint32_t kType, uint32_t kPos>
-__global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2))) pf_gate_up(PfGemm g) {
-  static_assert(kType == QT_IQ3_S, "pf_gate_up: IQ3_S (Q4_K runs on pf_gate_up_seq)");
-  const uint32_t U = g.U;  // at least 2: n_embd is a multiple of 512
-  constexpr uint32_t kWaves = kPos / 16, kThreads = 64 * kWaves, kRows = 16 * kWaves, kPt = kPos / 16;
-  // The activations are loaded two units ahead (three LDS buffers), the weights one unit ahead (the registers of the
-  // raw bytes, free once the unit is decoded).
-  constexpr uint32_t kBufs = 3;
-  __shared__ __align__(16) uint8_t abuf[kBufs][kPos * kActLds];
-  __shared__ __align__(16) uint8_t dump[64 * 16];
-  __shared__ uint32_t arow_lds[kPos];
-  __shared__ uint64_t tab[32];
-  __shared__ uint32_t grid_lds[512];
-  using Raw = Iq3sRaw;
-  using Dec = Iq3sA;
-  const uint32_t nrb = g.row_blocks;
-  const uint32_t nch = g.shared_T ? (g.shared_T + kPos - 1) / kPos : *g.ntiles, n = nch * nrb;
-  if (blockIdx.x >= n) return;
-  const uint32_t L = xcd_logical(blockIdx.x, n);
-  const uint32_t ch_i = L / nrb, rb = L % nrb;
-  uint32_t start, count, e;
-  if (g.shared_T) {
-    start = kPos * ch_i;
-    count = min(kPos, g.shared_T - start), e = 0;
-  } else {
-    const MoeTile tl = g.tiles[ch_i];
-    start = tl.start, count = tl.count, e = tl.slot;
-  }
-  const uint32_t tid = tid_fresh();
-  if (tid < 32) tab[tid] = kExp2Tab[tid];
-  for (uint32_t i = tid; i < 512; i += kThreads) grid_lds[i] = kIq3sGridPf[i];
-  if (tid < kPos) {
-    const uint32_t pos = start + tid;
-    arow_lds[tid] = tid < count ? (g.perm ? g.perm[pos] / g.K : pos) : 0xffffffffu;
-  }
-  __syncthreads();
-  const uint32_t row0 = rb * kRows + 16 * (uint32_t)__builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
-  const uint8_t *Mg = g.mat + (uint64_t)e * g.stride, *Mu = Mg + g.up_off;
-  const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
-  Dma<kPos, kWaves> dma;
-  dma.plan(arow_lds, U);
-  const __amdgpu_buffer_rsrc_t act_r = uniform_rsrc(g.act);
-  Raw rg, ru;
-  const auto load_w = [&](uint32_t u) {
-    rg.load(Mg, U, row0, u, lane);
-    ru.load(Mu, U, row0, u, lane);
-  };
-  // The end of unit u waits for unit u + 1's loads, leaving in flight only the activation loads of unit u + 2 (issued
-  // after them): kPer a wave (load_all issues the same count in every wave). As the builtin, not asm, so that the
-  // compiler's own tracking knows what has landed.
-  const auto wait_next = [&](bool more) {
-    if (more)
-      __builtin_amdgcn_s_waitcnt(vm_wait(Dma<kPos, kWaves>::kPer));
-    else
-      __builtin_amdgcn_s_waitcnt(vm_wait(0));
-  };
-  load_w(0);
-  dma.load_all(act_r, 0, &abuf[0][0], dump);
-  dma.load_all(act_r, 1, &abuf[1][0], dump);
-  wait_next(true);  // unit 0's loads
-  unit_barrier();
-  float accg[kPt][4], accu[kPt][4];
-#pragma unroll
-  for (int pt = 0; pt < (int)kPt; pt++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) accg[pt][i] = accu[pt][i] = 0.0f;
-  // Unit u. kNext: unit u + 1 exists (its weights are loaded here); kMore: unit u + 2 exists (its activations are
-  // loaded here). Both compile-time, so that the compiler's waits for the weight registers count the loads issued
-  // after them exactly (a run-time condition makes it wait for all). buf (read) and nbuf (filled) are restrict
-  // pointers: the compiler then knows the reads of buf need not wait for the global-to-LDS loads into nbuf.
-  const auto unit = [&](uint32_t u, auto kNext, auto kMore) {
-    const auto body = [&](const uint8_t *__restrict__ buf, uint8_t *__restrict__ nbuf) {
-      constexpr bool next = decltype(kNext)::value, more = decltype(kMore)::value;
-      Dec ag, au;
-      pin(rg), pin(ru);  // the decode starts here, after the previous unit's barrier, not above it
-      ag.decode(rg, lane, grid_lds);
-      au.decode(ru, lane, grid_lds);
-      pin(ag), pin(au);  // and ends here, before the next unit's loads into the raw registers
-      if constexpr (next) load_w(u + 1);
-      if constexpr (more) dma.load_all(act_r, u + 2, nbuf, dump);  // the buffer unit u - 1 read before the barrier
-      // Block by block: the block dots of gate and up for every position tile, each times its row's odd block
-      // scale, added to the unit's integer sums in block order; then d ad isum as UnitIQ3_S::term.
-      int isg[kPt][4], isu[kPt][4];
-#pragma unroll
-      for (int pt = 0; pt < (int)kPt; pt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) isg[pt][i] = isu[pt][i] = 0;
-#pragma unroll
-      for (uint32_t ib = 0; ib < 8; ib++) {
-        const uint32_t bofs = mfma_code_off(4 * ib + lane / 16);  // the lane's 8 codes of block ib
-        int lg[4], lu[4];
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++) lg[i] = ag.ls(i, ib), lu[i] = au.ls(i, ib);
-#pragma unroll
-        for (uint32_t pt = 0; pt < kPt; pt++) {
-          if (pt < npt) {
-            const long bw = *(const long *)(buf + (16 * pt + lane % 16) * kActLds + bofs);
-            const v4i_t dg = __builtin_amdgcn_mfma_i32_16x16x32_i8(ag.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
-            const v4i_t du = __builtin_amdgcn_mfma_i32_16x16x32_i8(au.a[ib], bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) isg[pt][i] += __mul24(lg[i], dg[i]), isu[pt][i] += __mul24(lu[i], du[i]);
-          }
-        }
-      }
-#pragma unroll
-      for (uint32_t pt = 0; pt < kPt; pt++) {
-        if (pt < npt) {
-          const float ad = *(const float *)(buf + (16 * pt + lane % 16) * kActLds + kActScales);
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            accg[pt][i] = __fadd_rn(accg[pt][i], __fmul_rn(__fmul_rn(ag.d[i], ad), (float)isg[pt][i]));
-            accu[pt][i] = __fadd_rn(accu[pt][i], __fmul_rn(__fmul_rn(au.d[i], ad), (float)isu[pt][i]));
-          }
-        }
-      }
-      wait_next(more);  // unit u + 1's loads have landed (this wave's) ...
-      unit_barrier();   // ... and every wave's; every wave is done with buffer u % 3, which unit u + 3 fills
-    };
-    body(abuf[u % kBufs], abuf[(u + 2) % kBufs]);
-  };
-  using yes = std::true_type;
-  using no = std::false_type;
-#pragma unroll 1
-  for (uint32_t u = 0; u + 2 < U; u++) unit(u, yes{}, yes{});
-  unit(U - 2, yes{}, no{});
-  unit(U - 1, no{}, no{});
-  // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16, gate and up alike.
-  const uint32_t r4 = 4 * (lane / 16), c16 = lane % 16;
-#pragma unroll
-  for (uint32_t pt = 0; pt < kPt; pt++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t m = 16 * pt + c16;
-      if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = swiglu_one(accg[pt][i], accu[pt][i], g.limit, tab);
-    }
 }
 
 // Q4_K gate/up at three waves a SIMD: a unit's gate products come before its up products, so that one matrix's
@@ -872,8 +707,7 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(2
 // gate and up in the same lane. A matrix's weights are decoded, then the registers of its raw bytes take the next
 // unit's loads (buffer loads on scalar bases), which the end of the unit waits for with the activations; the
 // barriers are plain ones (a fence would wait for every load in flight). The integers and fp32 steps are pf_gemm16's
-// (UnitQ4_K::term), units added in sequence. (IQ3_S in this form, at two waves a SIMD by registers, measured slower
-// than pf_gate_up: 411 against 370 us at config 5p.)
+// (UnitQ4_K::term), units added in sequence.
 template <uint32_t kPos>
 __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3))) pf_gate_up_q4k(PfGemm g) {
   const uint32_t U = g.U;
@@ -968,6 +802,129 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3
     }
 }
 
+// IQ3_S gate/up at three waves a SIMD, in pf_gate_up_q4k's form: gate's products before up's, the activations one
+// unit ahead in two LDS buffers, plain barriers. A block's A operand is decoded from the raw words (grid lookups in
+// LDS) just before its MFMAs, so only the raw words and one block's operand are live (168 registers, a few words
+// reloaded from scratch once a unit); each block's dots times the row's odd block scale are added to the unit's
+// integer sums in block order, then d ad isum as UnitIQ3_S::term, units added in sequence. The raw registers take the
+// next unit's loads once the pass has read them. Against the earlier form (both matrices in one wave, 220 registers,
+// two waves a SIMD, activations two units ahead): 367 -> 350 us a launch at config 5p.
+template <uint32_t kPos>
+__global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3))) pf_gate_up_iq3s(PfGemm g) {
+  const uint32_t U = g.U;
+  constexpr uint32_t kWaves = kPos / 16, kRows = 16 * kWaves, kPt = kPos / 16;
+  __shared__ __align__(16) uint8_t abuf[2][kPos * kActLds];
+  __shared__ __align__(16) uint8_t dump[64 * 16];
+  __shared__ uint32_t arow_lds[kPos];
+  __shared__ uint64_t tab[32];
+  __shared__ uint32_t grid_lds[512];
+  const uint32_t nrb = g.row_blocks;
+  const uint32_t nch = g.shared_T ? (g.shared_T + kPos - 1) / kPos : *g.ntiles, n = nch * nrb;
+  if (blockIdx.x >= n) return;
+  const uint32_t L = xcd_logical(blockIdx.x, n);
+  const uint32_t ch_i = L / nrb, rb = L % nrb;
+  uint32_t start, count, e;
+  if (g.shared_T) {
+    start = kPos * ch_i;
+    count = min(kPos, g.shared_T - start), e = 0;
+  } else {
+    const MoeTile tl = g.tiles[ch_i];
+    start = tl.start, count = tl.count, e = tl.slot;
+  }
+  const uint32_t tid = tid_fresh();
+  if (tid < 32) tab[tid] = kExp2Tab[tid];
+  for (uint32_t i = tid; i < 512; i += 64 * kWaves) grid_lds[i] = kIq3sGridPf[i];
+  if (tid < kPos) {
+    const uint32_t pos = start + tid;
+    arow_lds[tid] = tid < count ? (g.perm ? g.perm[pos] / g.K : pos) : 0xffffffffu;
+  }
+  __syncthreads();
+  const uint32_t row0 = rb * kRows + 16 * (uint32_t)__builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
+  const uint8_t *Mg = g.mat + (uint64_t)e * g.stride, *Mu = Mg + g.up_off;
+  const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
+  Dma<kPos, kWaves> dma;
+  dma.plan(arow_lds, U);
+  const __amdgpu_buffer_rsrc_t act_r = uniform_rsrc(g.act);
+  const auto load_w = [&](Iq3sRaw &raw, uint32_t m, uint32_t u) { raw.load(m ? Mu : Mg, U, row0, u, lane); };
+  Iq3sRaw rg, ru;
+  load_w(rg, 0, 0);
+  load_w(ru, 1, 0);
+  dma.load_all(act_r, 0, &abuf[0][0], dump);
+  __builtin_amdgcn_s_waitcnt(vm_wait(0));
+  unit_barrier();
+  float accg[kPt][4], accu[kPt][4];
+#pragma unroll
+  for (int pt = 0; pt < (int)kPt; pt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) accg[pt][i] = accu[pt][i] = 0.0f;
+  // Unit u; kNext: unit u + 1 exists (its loads are issued here). Compile-time, so that the compiler's waits for the
+  // weight registers count the loads issued after them exactly. buf (read) and nbuf (filled) are restrict pointers:
+  // the compiler then knows the reads of buf need not wait for the global-to-LDS loads into nbuf.
+  const auto unit = [&](uint32_t u, auto kNext) {
+    const auto body = [&](const uint8_t *__restrict__ buf, uint8_t *__restrict__ nbuf) {
+      constexpr bool next = decltype(kNext)::value;
+      if constexpr (next) dma.load_all(act_r, u + 1, nbuf, dump);  // the buffer unit u - 1 read before the barrier
+      const auto pass = [&](Iq3sRaw &raw, uint32_t m, float (&acc)[kPt][4]) {
+        // Block by block: the block's A operand decoded (grid lookups), its dots for every position tile times the
+        // row's odd block scale, added to the unit's integer sums in block order; then d ad isum.
+        pin(raw);
+        int is[kPt][4];
+#pragma unroll
+        for (int pt = 0; pt < (int)kPt; pt++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) is[pt][i] = 0;
+#pragma unroll
+        for (uint32_t ib = 0; ib < 8; ib++) {
+          const long aw = raw.a_block(ib, lane, grid_lds);
+          const uint32_t bofs = mfma_code_off(4 * ib + lane / 16);
+          int ls[4];
+#pragma unroll
+          for (uint32_t i = 0; i < 4; i++) ls[i] = raw.ls(i, ib);
+#pragma unroll
+          for (uint32_t pt = 0; pt < kPt; pt++) {
+            if (pt < npt) {
+              const long bw = *(const long *)(buf + (16 * pt + lane % 16) * kActLds + bofs);
+              const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bw, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+              for (int i = 0; i < 4; i++) is[pt][i] += __mul24(ls[i], d[i]);
+            }
+          }
+        }
+        float dd[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) dd[i] = h2f((uint16_t)raw.dh[i]);
+        pin(raw);
+        if constexpr (next) load_w(raw, m, u + 1);  // the raw registers are free once the pass has read them
+#pragma unroll
+        for (uint32_t pt = 0; pt < kPt; pt++) {
+          if (pt < npt) {
+            const float ad = *(const float *)(buf + (16 * pt + lane % 16) * kActLds + kActScales);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[pt][i] = __fadd_rn(acc[pt][i], __fmul_rn(__fmul_rn(dd[i], ad), (float)is[pt][i]));
+          }
+        }
+      };
+      pass(rg, 0, accg);
+      pass(ru, 1, accu);
+      __builtin_amdgcn_s_waitcnt(vm_wait(0));  // unit u + 1's loads (this wave's) ...
+      unit_barrier();                          // ... and every wave's; buffer u % 2 is free for unit u + 2
+    };
+    body(abuf[u & 1], abuf[(u + 1) & 1]);
+  };
+#pragma unroll 1
+  for (uint32_t u = 0; u + 1 < U; u++) unit(u, std::true_type{});
+  unit(U - 1, std::false_type{});
+  // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16, gate and up alike.
+  const uint32_t r4 = 4 * (lane / 16), c16 = lane % 16;
+#pragma unroll
+  for (uint32_t pt = 0; pt < kPt; pt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t m = 16 * pt + c16;
+      if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = swiglu_one(accg[pt][i], accu[pt][i], g.limit, tab);
+    }
+}
+
 // Positions a gate/up work-group takes for a weight type (the kernel's kPos).
 constexpr uint32_t gu_pos(uint32_t) { return MOE_TILE; }
 // The gate/up types that run on pf_gate_up (gate and up of a row in one wave); the others on pf_gemm16.
@@ -1014,7 +971,7 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
     if (type == QT_Q4_K)
       pf_gate_up_q4k<MOE_TILE><<<g2, wg, 0, s>>>(q);
     else
-      pf_gate_up<QT_IQ3_S, MOE_TILE><<<g2, wg, 0, s>>>(q);
+      pf_gate_up_iq3s<MOE_TILE><<<g2, wg, 0, s>>>(q);
     return;
   }
   // The 16 x 16 MFMA kernel: 32 gate + 32 up rows, or 64 down rows, a work-group; a 1-D XCD-aware grid.
@@ -1055,7 +1012,7 @@ struct HookScope {
 // first instantiation of a kernel template whose body holds a lambda and silently drops the later ones (and with
 // them launch_gemm<false>), which then fail at load time as undefined symbols.
 template __global__ void pf_gate_up_q4k<MOE_TILE>(PfGemm);
-template __global__ void pf_gate_up<QT_IQ3_S, MOE_TILE>(PfGemm);
+template __global__ void pf_gate_up_iq3s<MOE_TILE>(PfGemm);
 #define C0VEN_PF_GEMM16(T)                          \
   template __global__ void pf_gemm16<T, true>(PfGemm); \
   template __global__ void pf_gemm16<T, false>(PfGemm);
