@@ -510,7 +510,6 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
       b.tiles = c->alloc<MoeTile>(pf_max_tiles(TM, K, kMaxExperts));
       b.ntiles = c->alloc<uint32_t>(1);
       b.masks = c->alloc<unsigned long long>((uint64_t)pf_windows(TM) * kMaxExperts);
-      b.wstart = c->alloc<uint32_t>((uint64_t)pf_windows(TM) * kMaxExperts);
       b.h = c->alloc<float>(A2 * F);
       b.hact = c->alloc<uint8_t>(A2 * Ud * kActBytes);
       b.y_asg = c->alloc<float>(A2 * H);

@@ -64,7 +64,8 @@ __global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_
 // a chain of them over k = 0, 4, 8, ... is the oracle's sum term for term. Wave w takes rows 32 (w % 2) .. and tokens
 // 32 (w / 2) .. as 2 x 2 tiles of 16 x 16. K goes in chunks of 32 staged as doubles in two LDS buffers: chunk c + 1 is
 // loaded into registers while chunk c is used, and stored to the other buffer after it (one barrier a chunk). The
-// shared gate's row E takes an extra row of work-groups: a thread a token, k ascending.
+// shared gate's row E takes an extra row of work-groups: a thread a token, k ascending; they also clear their 64-token
+// window's dispatch masks for pf_topk.
 // logits[t][e] = (float)(sum over k ascending of bf16(W[e][k]) bf16(x[t][k]), each product exact, in fp64)
 // (+ bias[e] for e < E).
 
@@ -73,10 +74,11 @@ constexpr uint32_t kRtK = 32, kRtPad = 66;  // the padded row of a staged k (dou
 typedef double v4d_t __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(kPfWG) pf_router(const float *x, uint32_t T, const uint16_t *W, const float *bias,
-                                                   uint32_t E, uint32_t H, float *logits) {
+                                                   uint32_t E, uint32_t H, float *logits, unsigned long long *masks) {
   __shared__ double xs[2][kRtK][kRtPad], ws[2][kRtK][kRtPad];
   const uint32_t t0 = blockIdx.x * 64, e0 = blockIdx.y * 64, tid = threadIdx.x;
   if (e0 >= E) {  // the gate row: thread t of the first 64 a token
+    for (uint32_t i = tid; i < E; i += kPfWG) masks[(uint64_t)blockIdx.x * E + i] = 0ull;  // the window's masks
     double *wrow = &ws[0][0][0];  // W[E] as doubles, 2048 a pass
     const uint32_t t = t0 + tid;
     double acc = 0.0;
@@ -169,10 +171,11 @@ __global__ void __launch_bounds__(kPfWG) pf_router(const float *x, uint32_t T, c
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Top-k: one wave a token (the decode kernel's steps, route.h, in one wave).
+// Top-k: one wave a token (the decode kernel's steps, route.h, in one wave); each chosen expert's bit goes into the
+// token's window mask for the dispatch.
 
 __global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T, uint32_t E, uint32_t K,
-                                                 int32_t *ids, float *w, float *gs) {
+                                                 int32_t *ids, float *w, float *gs, unsigned long long *masks) {
   __shared__ uint64_t tab[32];
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
@@ -188,6 +191,7 @@ __global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T
   if (lane < K) {
     ids[(uint64_t)t * K + lane] = (int32_t)my_id;
     w[(uint64_t)t * K + lane] = wk;
+    atomicOr(&masks[(uint64_t)(t / 64) * E + my_id], 1ull << (t % 64));  // the dispatch's window mask
   }
   if (lane == 0 && gs) gs[t] = sigmoid_libm(lg[E], tab);
 }
@@ -196,11 +200,11 @@ __global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T
 // Dispatch (p_moe_count / p_moe_scan / p_moe_fill, prompt.cl:682-738): a counting sort of the T k assignments by
 // expert, stable (token order within an expert; the reference's fill takes atomic order). An expert takes at most one
 // assignment a token, so a 64-bit mask per (64-token window, expert) of the tokens that chose it gives both the counts
-// and each assignment's rank inside its window. Three kernels:
-//   pf_masks  one work-group a window: the window's masks (LDS atomics), written out whole;
-//   pf_scan   one work-group: per expert the window offsets (a scan over windows) and the total; the experts' bases
-//             (a scan over experts); the MoeTile records (at most MOE_TILE rows);
-//   pf_fill   one work-group a window: position = start of (window, expert) + the lower bits of the mask; perm and inv.
+// and each assignment's rank inside its window. Two steps:
+//   the masks  built by pf_topk as it selects (global atomics on masks the router's gate-row work-groups cleared),
+//              or, for pre-routed ids, by pf_masks (one work-group a window, LDS atomics, written out whole);
+//   pf_place   one work-group a window: the counts, the experts' bases and the window's starts from the masks, then
+//              position = start of (window, expert) + the lower bits of the mask; perm and inv; the MoeTile records.
 
 constexpr uint32_t kDispWG = 512;
 
@@ -237,56 +241,50 @@ __device__ __forceinline__ uint32_t block_scan512(uint32_t v, uint32_t *wsum) {
 
 constexpr uint32_t kScanBatch = 32;  // window masks a thread holds at once (all of them up to 2048 tokens)
 
-__global__ void __launch_bounds__(kDispWG) pf_scan(const unsigned long long *masks, uint32_t nwin, uint32_t E,
-                                                   uint32_t *wstart, MoeTile *tiles, uint32_t *ntiles) {
-  __shared__ uint32_t wsum[kDispWG / 64];
-  const uint32_t e = threadIdx.x;
-  // The counts of the first kScanBatch windows stay in registers for the offsets; the loads are all issued first.
-  uint32_t cw[kScanBatch];
-  {
+// One work-group a window. Thread e counts expert e's assignments in every window (the masks' popcounts, all loaded
+// before the first is used) and in the windows before this one; a scan over experts gives each expert's base, so the
+// (window, expert) start is base + the earlier windows' count. The window's assignments are then placed at that start
+// plus the popcount of the lower mask bits; window 0's work-group also writes the MoeTile records (at most MOE_TILE
+// rows) and their count.
+__global__ void __launch_bounds__(kDispWG) pf_place(const int32_t *ids, uint32_t T, uint32_t K, uint32_t E,
+                                                    uint32_t nwin, const unsigned long long *masks, MoeTile *tiles,
+                                                    uint32_t *ntiles, uint32_t *perm, uint32_t *inv) {
+  __shared__ uint32_t wsum[kDispWG / 64], start[kDispWG];
+  __shared__ unsigned long long mine[kDispWG];
+  const uint32_t w = blockIdx.x, e = threadIdx.x, ec = min(e, E - 1);
+  uint32_t c = 0, before = 0;
+  for (uint32_t j0 = 0; j0 < nwin; j0 += kScanBatch) {
     // Unconditional loads (clamped indices, masked after), so that all are in flight before the first is used.
     unsigned long long mm[kScanBatch];
-    const uint32_t ec = min(e, E - 1);
 #pragma unroll
-    for (uint32_t j = 0; j < kScanBatch; j++) mm[j] = masks[(uint64_t)min(j, nwin - 1) * E + ec];
+    for (uint32_t j = 0; j < kScanBatch; j++) mm[j] = masks[(uint64_t)min(j0 + j, nwin - 1) * E + ec];
 #pragma unroll
-    for (uint32_t j = 0; j < kScanBatch; j++) cw[j] = e < E && j < nwin ? (uint32_t)__popcll(mm[j]) : 0u;
-  }
-  uint32_t c = 0;
-#pragma unroll
-  for (uint32_t j = 0; j < kScanBatch; j++) c += cw[j];
-  if (e < E)
-    for (uint32_t w = kScanBatch; w < nwin; w++) c += (uint32_t)__popcll(masks[(uint64_t)w * E + e]);
-  const uint32_t nt = (c + MOE_TILE - 1) / MOE_TILE;
-  const uint32_t base = block_scan512(c, wsum) - c, t0 = block_scan512(nt, wsum) - nt;
-  if (e < E) {
-    for (uint32_t i = 0; i < nt; i++) {
-      MoeTile m;
-      m.expert = e, m.slot = e, m.start = base + MOE_TILE * i, m.count = min((uint32_t)MOE_TILE, c - MOE_TILE * i);
-      tiles[t0 + i] = m;
-    }
-    uint32_t run = base;
-#pragma unroll
-    for (uint32_t j = 0; j < kScanBatch; j++)
-      if (j < nwin) wstart[(uint64_t)j * E + e] = run, run += cw[j];
-    for (uint32_t w = kScanBatch; w < nwin; w++) {
-      wstart[(uint64_t)w * E + e] = run;
-      run += (uint32_t)__popcll(masks[(uint64_t)w * E + e]);
+    for (uint32_t j = 0; j < kScanBatch; j++) {
+      const uint32_t n = e < E && j0 + j < nwin ? (uint32_t)__popcll(mm[j]) : 0u;
+      c += n;
+      before += j0 + j < w ? n : 0u;
     }
   }
-  if (e == E - 1) *ntiles = t0 + nt;
-}
-
-__global__ void __launch_bounds__(kDispWG) pf_fill(const int32_t *ids, uint32_t T, uint32_t K, uint32_t E,
-                                                   const unsigned long long *masks, const uint32_t *wstart,
-                                                   uint32_t *perm, uint32_t *inv) {
-  const uint32_t w = blockIdx.x, t0 = 64 * w;
-  const uint32_t a0 = t0 * K, a1 = min(T, t0 + 64) * K;
-  for (uint32_t a = a0 + threadIdx.x; a < a1; a += kDispWG) {
-    if (ids[a] < 0) continue;
-    const uint32_t e = (uint32_t)ids[a], t = a / K - t0;
-    const uint64_t we = (uint64_t)w * E + e;
-    const uint32_t pos = wstart[we] + (uint32_t)__popcll(masks[we] & ((1ull << t) - 1ull));
+  const uint32_t base = block_scan512(c, wsum) - c;
+  start[e] = base + before;
+  mine[e] = e < E ? masks[(uint64_t)w * E + e] : 0ull;
+  if (w == 0) {
+    const uint32_t nt = (c + MOE_TILE - 1) / MOE_TILE, t0 = block_scan512(nt, wsum) - nt;
+    if (e < E)
+      for (uint32_t i = 0; i < nt; i++) {
+        MoeTile m;
+        m.expert = e, m.slot = e, m.start = base + MOE_TILE * i, m.count = min((uint32_t)MOE_TILE, c - MOE_TILE * i);
+        tiles[t0 + i] = m;
+      }
+    if (e == E - 1) *ntiles = t0 + nt;
+  }
+  __syncthreads();
+  const uint32_t t0 = 64 * w, a0 = t0 * K, a1 = min(T, t0 + 64) * K;
+  for (uint32_t a = a0 + e; a < a1; a += kDispWG) {
+    const int32_t id = ids[a];
+    if (id < 0) continue;
+    const uint32_t t = a / K - t0;
+    const uint32_t pos = start[id] + (uint32_t)__popcll(mine[id] & ((1ull << t) - 1ull));
     perm[pos] = a;
     inv[a] = pos;
   }
@@ -1034,8 +1032,9 @@ void launch_gate_up(uint32_t type, const PfGemm &q, uint32_t T, uint32_t F, uint
 }
 
 // The routed experts of a forward whose ids and w (T x K, ids < 0 for no assignment) are in b: dispatch, gate/up,
-// h quantiser, down (y per assignment in b.y_asg).
-hipError_t routed_experts(const PfShape &S, const PfLayer &L, const PfBufs &b, hipStream_t st, const PfHook &hook) {
+// h quantiser, down (y per assignment in b.y_asg). masks_built: b.masks already hold the ids' window masks (pf_topk).
+hipError_t routed_experts(const PfShape &S, const PfLayer &L, const PfBufs &b, hipStream_t st, const PfHook &hook,
+                          bool masks_built) {
   const uint32_t H = S.H, F = S.F, E = S.E, K = S.K, T = S.T, Ug = units_of(H), Ud = units_of(F);
   const uint32_t hr = quant_vec_dot_type(S.down_type);
   const uint32_t halfwaves = kPfWG / 32;
@@ -1043,9 +1042,8 @@ hipError_t routed_experts(const PfShape &S, const PfLayer &L, const PfBufs &b, h
   {
     HookScope k(hook, "pf_dispatch", st);
     const uint32_t nwin = pf_windows(T);
-    pf_masks<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, b.masks);
-    pf_scan<<<1, kDispWG, 0, st>>>(b.masks, nwin, E, b.wstart, b.tiles, b.ntiles);
-    pf_fill<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, b.masks, b.wstart, b.perm, b.inv);
+    if (!masks_built) pf_masks<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, b.masks);
+    pf_place<<<nwin, kDispWG, 0, st>>>(b.ids, T, K, E, nwin, b.masks, b.tiles, b.ntiles, b.perm, b.inv);
   }
   {
     HookScope k(hook, "pf_gate_up", st);
@@ -1117,13 +1115,14 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
   }
   {
     HookScope k(hook, "pf_router", st);
-    pf_router<<<dim3((T + 63) / 64, (E + 63) / 64 + 1), kPfWG, 0, st>>>(x, T, L.router, L.bias, E, H, b.logits);
+    pf_router<<<dim3((T + 63) / 64, (E + 63) / 64 + 1), kPfWG, 0, st>>>(x, T, L.router, L.bias, E, H, b.logits,
+                                                                       b.masks);
   }
   {
     HookScope k(hook, "pf_topk", st);
-    pf_topk<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, T, E, K, b.ids, b.w, S.has_shared ? b.gs : nullptr);
+    pf_topk<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, T, E, K, b.ids, b.w, S.has_shared ? b.gs : nullptr, b.masks);
   }
-  const hipError_t e = routed_experts(S, L, b, st, hook);
+  const hipError_t e = routed_experts(S, L, b, st, hook, true);
   if (e != hipSuccess) return e;
   if (S.has_shared && hipStreamWaitEvent(st, b.join, 0) != hipSuccess) return hipGetLastError();
   {
@@ -1144,7 +1143,7 @@ hipError_t prefill_jobs(const PfShape &S, const PfLayer &L, const PfBufs &b, con
     pf_quant_rows<<<(T * Ug + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(x, H, T, Ug, quant_vec_dot_type(S.gate_type),
                                                                             b.act_r, 0, nullptr);
   }
-  const hipError_t e = routed_experts(S, L, b, st, hook);
+  const hipError_t e = routed_experts(S, L, b, st, hook, false);
   if (e != hipSuccess) return e;
   {
     HookScope k(hook, "pf_combine", st);

@@ -5,13 +5,14 @@
 // moe_down_t (qgemm.cl:227-239) and p_moe_combine (prompt.cl:769-787). Kernels, in stream order:
 //   pf_quant_rows  x -> the experts' activation units (q8_K or q8_0, the CPU rules)
 //   pf_router      logits = bf16(W) bf16(x) summed in fp64 in k order (each product exact), rounded once, + bias
-//   pf_topk        one wave a token: softmax, top k, weights, shared gate
-//   pf_masks, pf_scan, pf_fill
-//                  counting sort of the T k assignments by expert (stable: token order within an expert) into
+//   pf_topk        one wave a token: softmax, top k, weights, shared gate; each choice's bit in its window's mask
+//   pf_place       counting sort of the T k assignments by expert (stable: token order within an expert) into
 //                  MoeTile[] of at most MOE_TILE rows, perm (position -> assignment) and inv (assignment -> position)
+//                  (pre-routed ids: pf_masks builds the masks first)
 //   gate/up        per tile: gate and up on int8 MFMA, exact int32 block sums, the blocks' integer scales and the
-//                  unit's fp32 term in the oracle's order, SwiGLU. Q4_K and IQ3_S: pf_gemm16 (16 x 16 tiles, 32 rows
-//                  of each a work-group, activations copied straight to LDS); Q8_0: pf_gemm (32 x 32 x 32, 64 rows)
+//                  unit's fp32 term in the oracle's order, SwiGLU. Q4_K: pf_gate_up_q4k, IQ3_S: pf_gate_up_iq3s (64
+//                  rows of each a work-group); the other types: pf_gemm16 (32 rows of each); activations loaded
+//                  straight to LDS
 //   pf_quant_rows  h -> the down's activation units
 //   down           per tile: the same kernels (64 or 128 rows a work-group)
 //   pf_combine     y_t = sum_k w_k y_(t,k) in rank order + gs_t s_t
@@ -51,7 +52,6 @@ struct PfBufs {
   MoeTile *tiles;          // Tmax K / MOE_TILE + E
   uint32_t *ntiles;        // 1
   unsigned long long *masks;  // windows x E: the tokens of each 64-token window that chose each expert
-  uint32_t *wstart;        // windows x E: where each (window, expert)'s assignments start
   float *h, *h_sh;         // Tmax K x F (expert order), Tmax x F
   uint8_t *hact, *hact_sh; // the same rows quantised, (F / 256) units each
   float *y_asg, *y_sh;     // Tmax K x H (expert order), Tmax x H
