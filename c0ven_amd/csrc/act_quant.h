@@ -48,10 +48,11 @@ __device__ __forceinline__ uint4 ld_co16(const void *base, uint32_t off) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// A word of a quantised unit: to global memory (coherent, for other work-groups) or to LDS (for this one).
-template <bool kLds, typename T>
+// A word of a quantised unit: to global memory (coherent, for other work-groups of the launch) or to LDS (for this
+// one), or with kPlain a plain store (read by later launches only).
+template <bool kLds, typename T, bool kPlain = false>
 __device__ __forceinline__ void put_word(uint8_t *out, uint32_t off, T v) {
-  if constexpr (kLds) {
+  if constexpr (kLds || kPlain) {
     *(T *)(out + off) = v;
   } else {
     st_co((T *)(out + off), v);
@@ -67,8 +68,9 @@ __host__ __device__ __forceinline__ constexpr uint32_t mfma_code_off(uint32_t j)
 
 // One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
 // with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0). out is in global
-// memory, or in LDS when kLds. kMfma: the codes in the prefill order (mfma_code_off) instead of value order.
-template <bool kLds = false, bool kSplitG = false, bool kMfma = false>
+// memory, or in LDS when kLds. kMfma: the codes in the prefill order (mfma_code_off) instead of value order. kPlain:
+// plain global stores (the unit is read by later launches only).
+template <bool kLds = false, bool kSplitG = false, bool kMfma = false, bool kPlain = false>
 __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
   const uint32_t coff = kMfma ? mfma_code_off(l32) : 8 * l32;
   uint32_t code[2] = {0u, 0u};
@@ -102,10 +104,9 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
     }
     part += __shfl_xor(part, 1, 32);
     part += __shfl_xor(part, 2, 32);
-    put_word<kLds>(out, coff, code[0]);
-    put_word<kLds>(out, coff + 4, code[1]);
-    if ((l32 & 3u) == 0) put_word<kLds>(out, kActSums + l32, part);
-    if (l32 == 0) put_word<kLds>(out, kActScales, d);
+    put_word<kLds, uint64_t, kPlain>(out, coff, ((uint64_t)code[1] << 32) | code[0]);
+    if ((l32 & 3u) == 0) put_word<kLds, int, kPlain>(out, kActSums + l32, part);
+    if (l32 == 0) put_word<kLds, float, kPlain>(out, kActScales, d);
     if constexpr (kSplitG) {
       // Block sum j = l32 / 4 split as 64 hi + lo (hi in [-64, 63], lo in [0, 63]) into the padding at kActSplitG.
       if ((l32 & 3u) == 0) {
@@ -125,10 +126,9 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
       const int q = nearest_int(__fmul_rn(v[i], id));
       code[i / 4] |= ((uint32_t)q & 0xffu) << (8 * (i % 4));
     }
-    put_word<kLds>(out, coff, code[0]);
-    put_word<kLds>(out, coff + 4, code[1]);
-    if ((l32 & 3u) == 0) put_word<kLds>(out, kActScales + l32, h2f(f2h(d)));
-    if ((l32 & 3u) == 0) put_word<kLds>(out, kActSums + l32, 0);
+    put_word<kLds, uint64_t, kPlain>(out, coff, ((uint64_t)code[1] << 32) | code[0]);
+    if ((l32 & 3u) == 0) put_word<kLds, float, kPlain>(out, kActScales + l32, h2f(f2h(d)));
+    if ((l32 & 3u) == 0) put_word<kLds, int, kPlain>(out, kActSums + l32, 0);
   }
 }
 

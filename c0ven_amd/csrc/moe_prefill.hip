@@ -54,8 +54,8 @@ __global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_
     a = p[0], b = p[1];
   }
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  quant_unit<false, true, true>(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
-  if (o2) quant_unit<false, true, true>(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
+  quant_unit<false, true, true, true>(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
+  if (o2) quant_unit<false, true, true, true>(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -930,7 +930,10 @@ constexpr bool gu_fused(uint32_t type) { return type == QT_Q4_K || type == QT_IQ
 
 // ---------------------------------------------------------------------------------------------------------------
 // Combine: y[t][r] = sum_k w[t][k] y_asg[inv[t K + k]][r] in rank order (ranks with a negative id skipped), then
-// + gs[t] y_sh[t][r]; four rows a thread.
+// + gs[t] y_sh[t][r]; four rows a thread. The ranks go in batches of eight whose row loads are all issued before the
+// first is added (rows of skipped ranks are not loaded and add nothing).
+
+constexpr uint32_t kCombBatch = 8;
 
 __global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const uint32_t *inv, const int32_t *ids,
                                                     const float *w, uint32_t K, const float *y_sh, const float *gs,
@@ -940,12 +943,24 @@ __global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const ui
   if (i >= (uint64_t)T * H4) return;
   const uint32_t t = (uint32_t)(i / H4), r4 = (uint32_t)(i % H4);
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (uint32_t k = 0; k < K; k++) {
-    if (ids[(uint64_t)t * K + k] < 0) continue;  // a pre-routed token's unused rank
-    const float wk = w[(uint64_t)t * K + k];
-    const float4 v = ((const float4 *)(y_asg + (uint64_t)inv[(uint64_t)t * K + k] * H))[r4];
-    acc.x = __fadd_rn(acc.x, __fmul_rn(wk, v.x)), acc.y = __fadd_rn(acc.y, __fmul_rn(wk, v.y));
-    acc.z = __fadd_rn(acc.z, __fmul_rn(wk, v.z)), acc.w = __fadd_rn(acc.w, __fmul_rn(wk, v.w));
+  for (uint32_t k0 = 0; k0 < K; k0 += kCombBatch) {
+    float wk[kCombBatch];
+    float4 v[kCombBatch];
+    uint32_t used = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kCombBatch; j++) {
+      const uint64_t a = (uint64_t)t * K + k0 + j;
+      const bool use = k0 + j < K && ids[a] >= 0;  // a pre-routed token's unused rank: skipped
+      used |= (uint32_t)use << j;
+      wk[j] = use ? w[a] : 0.0f;
+      v[j] = use ? ((const float4 *)(y_asg + (uint64_t)inv[a] * H))[r4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kCombBatch; j++) {
+      if (!(used >> j & 1u)) continue;
+      acc.x = __fadd_rn(acc.x, __fmul_rn(wk[j], v[j].x)), acc.y = __fadd_rn(acc.y, __fmul_rn(wk[j], v[j].y));
+      acc.z = __fadd_rn(acc.z, __fmul_rn(wk[j], v[j].z)), acc.w = __fadd_rn(acc.w, __fmul_rn(wk[j], v[j].w));
+    }
   }
   if (y_sh) {
     const float g = gs[t];
