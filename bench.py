@@ -42,6 +42,8 @@ CONFIGS = {
 H, F, E, K = 2048, 512, 512, 10
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+# The routed gate/up kernel of a gate type (the launch the prefill roofline is quoted on); pf_gemm16 for the others.
+GU_KERNEL = {12: "pf_gate_up_q4k", 21: "pf_gate_up_iq3s"}  # Q4_K, IQ3_S
 
 
 class Hip:
@@ -459,7 +461,8 @@ def stack(args, cfg, moe, h):
         # The routed gate/up launch (the shared expert's runs beside the router on a second stream).
         gu_ms = ktimes.get("pf_gate_up", float("nan"))
         gu_flop = 2.0 * (chunk * K) * 2 * F * H
-        roof = {"bound": "mfma", "kernel": "pf_gate_up", "achieved": round(gu_flop / (gu_ms * 1e-3) / 1e12, 2),
+        roof = {"bound": "mfma", "kernel": GU_KERNEL.get(cfg["types"][0], "pf_gemm16"),
+                "achieved": round(gu_flop / (gu_ms * 1e-3) / 1e12, 2),
                 "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                 "frac": round(gu_flop / (gu_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
                 "traffic": measured_prefill_traffic(args.config),
@@ -557,7 +560,8 @@ def prefill(args, cfg, key, moe, h):
         "dtype": "int8", "data": "synthetic",
         "config": {"workload": cfg["name"], "n_embd": H, "n_ff": F, "n_expert": E, "n_used": K, "shared": True,
                    "tokens": T, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]], "touched_experts": touched},
-        "roofline": {"bound": "mfma", "kernel": "pf_gate_up", "achieved": round(gu_tops, 2), "peak": INT8_PEAK_TOPS,
+        "roofline": {"bound": "mfma", "kernel": GU_KERNEL.get(cfg["types"][0], "pf_gemm16"), "achieved": round(gu_tops, 2),
+                     "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(gu_tops / INT8_PEAK_TOPS, 4),
                      "traffic": measured_prefill_traffic(key),
                      "algorithmic_flop_per_launch": gu_routed_flop, "avg_launch_ms": round(gu_ms, 4)},
