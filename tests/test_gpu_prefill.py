@@ -124,9 +124,10 @@ def test_prefill_config4_sampled():
     blk.close()
 
 
-def test_prefill_dispatch_past_lds_cache():
-    """More assignments than the dispatch keeps in LDS (T k > 40960: the ids are read from global memory on the
-    position pass). Tiles and perm against the stable counting sort; ids, w and y against the oracle on a sample."""
+def test_prefill_dispatch_many_windows():
+    """A long prefill (T k > 40960; 66 windows of 64 tokens, more than the 32 masks a dispatch thread loads at once,
+    so its count runs over several batches of windows). Tiles and perm against the stable counting sort; ids, w and
+    y against the oracle on a sample."""
     say("prefill dispatch, 4200 tokens x k 10")
     L = h.Layer(512, 256, 64, 10, Q4, Q8, seed=4200, zipf=1.1)
     T = 4200
