@@ -33,10 +33,10 @@ def test_decode_instantiations_do_not_spill():
 
 
 def test_prefill_kernels_do_not_spill():
-    # The measured configurations' kernels (routing, combine, quantiser; the expert GEMMs of Q4_K = 12, IQ3_S = 21 and
+    # The measured configurations' kernels (routing, dispatch, combine, quantiser; the expert GEMMs of Q4_K = 12, IQ3_S = 21 and
     # Q8_0 = 8) hold everything in registers; the other types' GEMMs may keep a few words outside the unit loop.
     rows = _rows()
-    pf = {n: r for n, r in rows.items() if re.search(r"pf_(gate_up|gemm16|router|combine|quant_rows|topk)", n)}
+    pf = {n: r for n, r in rows.items() if re.search(r"pf_(gate_up|gemm16|router|combine|quant_rows|topk|place|masks)", n)}
     assert pf
     for n, r in pf.items():
         hot = not re.search(r"pf_gemm16ILj(\d+)E|pf_gate_up_iq3s", n) or re.search(r"pf_gemm16ILj(12|21|8)E", n)
