@@ -1031,6 +1031,11 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
 
 }  // namespace
 
+#ifndef C0VEN_QUANT_TOP_MIN
+#define C0VEN_QUANT_TOP_MIN 5
+#endif
+constexpr uint32_t kQuantTopMin = C0VEN_QUANT_TOP_MIN;
+
 // Grid: the work-groups of 256 the device holds at once; dynamic LDS: the larger of a group's activation units
 // (MOE_GROUP_MAX x act_tok_stride) and the grouping's tables (kGroupingLds).
 template <uint32_t kTypes, bool kHc>
@@ -1053,6 +1058,9 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nH + nL + nTop;
   const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud), nBlk = nD;  // combine items: T x nBlk
   const uint32_t ns = shared_chunks(T, p.route, p.has_shared), B2 = B1 + ns * (nGU + nD);
+  // x is quantised by the top-k items from kQuantTopMin tokens on (the router rows that would otherwise do it then
+  // finish last), by the first T lead items below that (one top-k item would do it serially).
+  const bool quant_top = p.route && T >= kQuantTopMin;
   // Items below B2 go round-robin (work-group b takes b, b + grid, ...). The routed items, whose cost varies with their
   // group's size, are handed out dynamically: item B2 + x + kDynLists k is the k-th of list x, and the work-groups with
   // blockIdx % kDynLists == x take list x's items in order from its counter (one counter a list keeps the atomics
@@ -1099,17 +1107,24 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
     } else if (it < nH + nL) {
       const uint32_t li = it - nH;
       if (kHc) wait_flag(p, kFlagHcX);
-      if (li < T) quantise_x<kTypes, kHc>(p, li);
-      if (p.route) {
+      if (p.route) {  // a router row; x[li] too unless the token's top-k item quantises it (quant_top)
+        if (li < T && !quant_top) quantise_x<kTypes, kHc>(p, li);
         if (li < E) router_row<kHc>(p, li, s_part, s_tot);
         if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
-        set_flag(p, kFlagLead + li);
-      } else if (arrive_last(p.cnt_route, nL, &s_flag)) {
-        set_flag(p, kFlagRouted);
+        if (li < T && !quant_top) set_flag(p, kFlagLead + li);
+      } else {
+        if (li < T) quantise_x<kTypes, kHc>(p, li);
+        if (arrive_last(p.cnt_route, nL, &s_flag)) set_flag(p, kFlagRouted);
       }
     } else if (it < B1) {
       const uint32_t t = it - nH - nL;
       if (kHc) wait_flag(p, kFlagHcX);
+      // With quant_top, x[t] to the experts' activation types first (the shared expert's items wait for its flag),
+      // then the rest while the lead items finish the logits.
+      if (quant_top) {
+        quantise_x<kTypes, kHc>(p, t);
+        set_flag(p, kFlagLead + t);
+      }
       // The shared gate's logit (router row E) for this token while the lead items finish: gs = sigmoid of it.
       router_dot<kHc>(p, E, t, 1, s_part, s_tot);
       if (tid() == 0) st_tag(p.gs + t, __float_as_uint(sigmoid_libm((float)s_tot[0], exp_tab)), p.tag);
