@@ -520,6 +520,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
         check(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking), "hipStreamCreate");
         check(hipEventCreateWithFlags(&b.fork, hipEventDisableTiming), "hipEventCreate");
         check(hipEventCreateWithFlags(&b.join, hipEventDisableTiming), "hipEventCreate");
+        check(hipEventCreateWithFlags(&b.xq, hipEventDisableTiming), "hipEventCreate");
       }
     }
     c->act_r = c->alloc<uint8_t>((uint64_t)T * Ug * kActBytes);
@@ -606,6 +607,7 @@ MOE_API void moe_close(moe_ctx *c) {
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   if (c->pf.fork) (void)hipEventDestroy(c->pf.fork);
   if (c->pf.join) (void)hipEventDestroy(c->pf.join);
+  if (c->pf.xq) (void)hipEventDestroy(c->pf.xq);
   if (c->pf.side) (void)hipStreamDestroy(c->pf.side);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;

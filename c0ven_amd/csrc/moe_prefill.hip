@@ -1094,16 +1094,21 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
   const uint32_t xs = S.has_shared ? quant_vec_dot_type(S.sh_gate_type) : xr;
   const uint32_t hs = quant_vec_dot_type(S.sh_down_type);
   const uint32_t halfwaves = kPfWG / 32;
-  {
-    HookScope k(hook, "pf_quant_x", st);
-    pf_quant_rows<<<(T * Ug + halfwaves - 1) / halfwaves, kPfWG, 0, st>>>(x, H, T, Ug, xr, b.act_r, xs,
-                                                                            b.act_s != b.act_r ? b.act_s : nullptr);
-  }
+  // The x quantiser: on the side stream with a shared expert (the router reads x itself; the routed launches wait for
+  // it after the top-k), else first on the block's stream.
+  const auto quant_x = [&](hipStream_t s) {
+    HookScope k(hook, "pf_quant_x", s);
+    pf_quant_rows<<<(T * Ug + halfwaves - 1) / halfwaves, kPfWG, 0, s>>>(x, H, T, Ug, xr, b.act_r, xs,
+                                                                           b.act_s != b.act_r ? b.act_s : nullptr);
+  };
   const uint32_t st_tiles = (T + MOE_TILE - 1) / MOE_TILE;
+  if (!S.has_shared) quant_x(st);
   if (S.has_shared) {  // the shared expert needs no routing: its launches run beside the router on the side stream
     hipStream_t ss = b.side;
     if (hipEventRecord(b.fork, st) != hipSuccess || hipStreamWaitEvent(ss, b.fork, 0) != hipSuccess)
       return hipGetLastError();
+    quant_x(ss);
+    if (hipEventRecord(b.xq, ss) != hipSuccess) return hipGetLastError();
     {
       HookScope k(hook, "pf_gate_up_shared", ss);
       PfGemm q{};
@@ -1137,6 +1142,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     HookScope k(hook, "pf_topk", st);
     pf_topk<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, T, E, K, b.ids, b.w, S.has_shared ? b.gs : nullptr, b.masks);
   }
+  if (S.has_shared && hipStreamWaitEvent(st, b.xq, 0) != hipSuccess) return hipGetLastError();
   const hipError_t e = routed_experts(S, L, b, st, hook, true);
   if (e != hipSuccess) return e;
   if (S.has_shared && hipStreamWaitEvent(st, b.join, 0) != hipSuccess) return hipGetLastError();

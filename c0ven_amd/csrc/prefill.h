@@ -55,10 +55,11 @@ struct PfBufs {
   float *h, *h_sh;         // Tmax K x F (expert order), Tmax x F
   uint8_t *hact, *hact_sh; // the same rows quantised, (F / 256) units each
   float *y_asg, *y_sh;     // Tmax K x H (expert order), Tmax x H
-  // The shared expert's launches run on `side` (default priority), forked after the x quantiser and joined before the
-  // combine, so they overlap the router instead of following the routed ones.
+  // With a shared expert, the x quantiser and the shared expert's launches run on `side` (default priority), forked at
+  // the start and joined before the combine, so they overlap the router instead of preceding or following the routed
+  // ones; the routed launches wait for xq (the quantiser done) after the top-k.
   hipStream_t side;
-  hipEvent_t fork, join;
+  hipEvent_t fork, join, xq;
 };
 
 // Called around every kernel launch (timing); may be null.
