@@ -925,7 +925,8 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3
 
 // Positions a gate/up work-group takes for a weight type (the kernel's kPos).
 constexpr uint32_t gu_pos(uint32_t) { return MOE_TILE; }
-// The gate/up types that run on pf_gate_up (gate and up of a row in one wave); the others on pf_gemm16.
+// The gate/up types that run on pf_gate_up_q4k / pf_gate_up_iq3s (gate and up of a row in one wave); the others on
+// pf_gemm16.
 constexpr bool gu_fused(uint32_t type) { return type == QT_Q4_K || type == QT_IQ3_S; }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1018,9 +1019,9 @@ struct HookScope {
   }
 };
 
-// Gate/up (SwiGLU into h) over nx tiles or chunks (at most; the kernel reads how many there are): Q8_0 on pf_gemm16
-// (64-position tiles, 32 rows of gate and of up a work-group), Q4_K and IQ3_S on pf_gate_up (gu_pos positions and
-// rows of each a work-group).
+// Gate/up (SwiGLU into h) over nx tiles or chunks (at most; the kernel reads how many there are): Q4_K and IQ3_S on
+// pf_gate_up_q4k / pf_gate_up_iq3s (gu_pos positions and rows of each a work-group), the other types on pf_gemm16
+// (64-position tiles, 32 rows of gate and of up a work-group).
 // Explicit instantiations: with only the implicit ones, this compiler's host pass emits the launch stub of the
 // first instantiation of a kernel template whose body holds a lambda and silently drops the later ones (and with
 // them launch_gemm<false>), which then fail at load time as undefined symbols.

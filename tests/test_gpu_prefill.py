@@ -76,8 +76,8 @@ def test_prefill_shapes_no_shared_and_limit(H, F):
 @pytest.mark.parametrize("H,F,types", [(2560, 640, (Q4, Q8, Q4, Q8)), (2560, 640, (I3, Q8, I3, Q8)),
                                          (1536, 256, (Q4, Q4, I3, Q4))])
 def test_prefill_unit_counts(H, F, types):
-    # The fused gate/up kernel runs its unit loop for U - 2 units and then the last two apart (the loads of the
-    # next units issued from compile-time flags): U = 10 and 6 here, besides 2, 4 and 8 above.
+    # The Q4_K and IQ3_S gate/up kernels run their unit loop for U - 1 units and then the last one apart (whether a
+    # next unit's loads are issued is a compile-time flag): U = 10 and 6 here, besides 2, 4 and 8 above.
     gt, dt, sgt, sdt = types
     say("prefill unit counts", H, F, [moe.TYPE_NAMES[t] for t in types])
     L = h.Layer(H, F, 32, 6, gt, dt, sgt, sdt, seed=77 + H)
