@@ -102,6 +102,23 @@ def test_prefill_then_decode_share_a_context():
     blk.close()
 
 
+def test_prefill_forwards_in_a_row():
+    """Prefill forwards of different lengths on one context: each clears the dispatch masks its routing sets (a shorter
+    forward leaves an earlier one's bits in windows it does not read), so tiles, perm and y stand alone."""
+    say("prefill forwards in a row")
+    L = h.Layer(512, 256, 64, 6, Q4, Q4, seed=123, zipf=1.1)
+    blk = L.block(max_tokens=320)
+    L.upload(blk)
+    for i, T in enumerate((300, 17, 300, 130)):
+        x = h.tokens(200 + i, T, 512)
+        y, ids, w = blk.forward(0, x)
+        tiles, perm = blk.prefill_dispatch(T)
+        et, ep = expected_dispatch(ids, L.E)
+        assert np.array_equal(tiles, et) and np.array_equal(perm, ep), T
+        check_exact(y, ids, w, *L.oracle_forward(x))
+    blk.close()
+
+
 def test_prefill_config4_sampled():
     """2048 tokens, H 2048, F 512, 512 experts, top-10 + shared, Q4_K, Zipf(1.1)."""
     say("prefill config 4")
