@@ -432,6 +432,42 @@ struct Q4kBuf {
   }
 };
 
+// Iq3sRaw's loads for gate and up as buffer loads on the wave's 16-row tiles, as Q4kBuf's: the lane's offsets worked
+// out once, each field's, piece's and unit's offset scalar (the same bytes as Iq3sRaw::load; the four D rows' d words
+// are consecutive, one 8-byte load).
+struct Iq3sBuf {
+  const uint8_t *base[2];
+  uint32_t nl, lq, la, ld;
+  __device__ __forceinline__ void init(const uint8_t *gate, const uint8_t *up, uint32_t U, uint32_t row0, uint32_t lane) {
+    const uint32_t g = lane / 16, rr = row0 % kTileRows;
+    const uint64_t t = (uint64_t)(row0 / kTileRows) * tile_bytes(QT_IQ3_S, U);
+    nl = kTileRows * U;
+    base[0] = gate + t, base[1] = up + t;
+    la = rr + lane % 16;      // the A row's pair index within a unit
+    lq = la * 16 + 4 * (g / 2);
+    ld = rr + 4 * g;          // the first D row's
+  }
+  __device__ __forceinline__ void load(uint32_t m, Iq3sRaw &w, uint32_t u) const {
+    const uint32_t pu = u * kTileRows;
+#pragma unroll
+    for (uint32_t ib = 0; ib < 8; ib++)
+      w.qs[ib] = __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(base[m]), lq + 8 * (ib % 2), ((ib / 2) * nl + pu) * 16, 0);
+#pragma unroll
+    for (uint32_t p = 0; p < 2; p++) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(uniform_rsrc(base[m]), la * 16, iq3_st::kSigns * nl + (p * nl + pu) * 16, 0);
+      w.sg[4 * p] = v[0], w.sg[4 * p + 1] = v[1], w.sg[4 * p + 2] = v[2], w.sg[4 * p + 3] = v[3];
+    }
+#pragma unroll
+    for (uint32_t p = 0; p < 2; p++)
+      w.qh[p] = __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(base[m]), la * 4, iq3_st::kQh * nl + (p * nl + pu) * 4, 0);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++)
+      w.sc[i] = __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(base[m]), (ld + i) * 4, iq3_st::kScales * nl + pu * 4, 0);
+    const auto d = __builtin_amdgcn_raw_buffer_load_b64(uniform_rsrc(base[m]), ld * 2, iq3_st::kD * nl + pu * 2, 0);
+    w.dh[0] = d[0] & 0xffffu, w.dh[1] = d[0] >> 16, w.dh[2] = d[1] & 0xffffu, w.dh[3] = d[1] >> 16;
+  }
+};
+
 // A work-group barrier without __syncthreads' fence (which would wait for every load in flight): LDS reads done, then
 // s_barrier, with compiler barriers either side so that no LDS access moves across it.
 __device__ __forceinline__ void unit_barrier() {
@@ -802,11 +838,12 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3
 
 // IQ3_S gate/up at three waves a SIMD, in pf_gate_up_q4k's form: gate's products before up's, the activations one
 // unit ahead in two LDS buffers, plain barriers. A block's A operand is decoded from the raw words (grid lookups in
-// LDS) just before its MFMAs, so only the raw words and one block's operand are live (168 registers, a few words
-// reloaded from scratch once a unit); each block's dots times the row's odd block scale are added to the unit's
-// integer sums in block order, then d ad isum as UnitIQ3_S::term, units added in sequence. The raw registers take the
-// next unit's loads once the pass has read them. Against the earlier form (both matrices in one wave, 220 registers,
-// two waves a SIMD, activations two units ahead): 367 -> 350 us a launch at config 5p.
+// LDS) just before its MFMAs, so only the raw words and one block's operand are live (144 registers); each block's
+// dots times the row's odd block scale are added to the unit's integer sums in block order, then d ad isum as
+// UnitIQ3_S::term, units added in sequence. The raw registers take the next unit's loads (buffer loads on scalar
+// bases, Iq3sBuf) once the pass has read them. Against the earlier form (both matrices in one wave, 220 registers,
+// two waves a SIMD, activations two units ahead): 367 -> 350 us a launch at config 5p; the buffer loads (in place
+// of global loads, 168 registers and a reload from scratch a unit) 358 -> 329 us.
 template <uint32_t kPos>
 __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3))) pf_gate_up_iq3s(PfGemm g) {
   const uint32_t U = g.U;
@@ -843,7 +880,9 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3
   Dma<kPos, kWaves> dma;
   dma.plan(arow_lds, U);
   const __amdgpu_buffer_rsrc_t act_r = uniform_rsrc(g.act);
-  const auto load_w = [&](Iq3sRaw &raw, uint32_t m, uint32_t u) { raw.load(m ? Mu : Mg, U, row0, u, lane); };
+  Iq3sBuf wb;  // buffer loads on scalar bases (168 registers and a reload from scratch a unit with global loads)
+  wb.init(Mg, Mu, U, row0, lane);
+  const auto load_w = [&](Iq3sRaw &raw, uint32_t m, uint32_t u) { wb.load(m, raw, u); };
   Iq3sRaw rg, ru;
   load_w(rg, 0, 0);
   load_w(ru, 1, 0);

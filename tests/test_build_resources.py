@@ -39,7 +39,5 @@ def test_prefill_kernels_do_not_spill():
     pf = {n: r for n, r in rows.items() if re.search(r"pf_(gate_up|gemm16|router|combine|quant_rows|topk|place|masks)", n)}
     assert pf
     for n, r in pf.items():
-        hot = not re.search(r"pf_gemm16ILj(\d+)E|pf_gate_up_iq3s", n) or re.search(r"pf_gemm16ILj(12|21|8)E", n)
-        # pf_gate_up_iq3s runs at three waves a SIMD with a few words reloaded from scratch once a unit (faster than
-        # the spill-free form at two waves)
+        hot = not re.search(r"pf_gemm16ILj(\d+)E", n) or re.search(r"pf_gemm16ILj(12|21|8)E", n)
         assert r["scratch"] <= (0 if hot else 16), (n, r)
