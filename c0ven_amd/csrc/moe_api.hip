@@ -15,7 +15,7 @@
 #include "../../include/c0ven_moe.h"
 #include "aux.h"
 #include "decode.h"
-#include "gguf_reader.h"
+#include "gguf_index.h"
 #include "iq3s_grid.h"
 #include "layout.h"
 #include "prefill.h"
@@ -650,9 +650,9 @@ MOE_API moe_status moe_load_layer_gguf(moe_ctx *c, uint32_t layer, const c0ven_g
     const std::string pre = "blk." + std::to_string(blk) + ".";
     // The tensor of a name with the given type and shape (ggml order), or an error naming what differs.
     const auto tensor = [&](const std::string &name, uint32_t type, std::initializer_list<uint64_t> shape) {
-      const GgufEntry *e = file->file->find(pre + name);
-      require(e != nullptr, "tensor missing from the file: " + pre + name);
-      const gguf_tensor_info &t = e->info;
+      const gguf_tensor_info *tp = file->ix.tensor((pre + name).c_str());
+      require(tp != nullptr, "the file has no tensor " + pre + name);
+      const gguf_tensor_info &t = *tp;
       bool same = t.type == type && t.n_dims == shape.size();
       uint32_t d = 0;
       for (uint64_t v : shape) same = same && t.shape[d++] == v;

@@ -4,6 +4,7 @@ files, header-only architecture reads, page release, and the errors of malformed
 the real model (core/tests/gguf_test.cpp:12-56), which is not on this machine; its census
 (docs/model/tensors-IQ3_S.tsv) gives the names and shapes the MoE loader expects."""
 import os
+import struct
 
 import numpy as np
 import pytest
@@ -117,3 +118,33 @@ def test_type_bytes():
     assert tb(moe.QT_Q4_K, 2560) == 10 * 144 and tb(moe.QT_IQ4_NL, 640) == 20 * 18 and tb(moe.QT_Q2_0, 640) == 180
     assert tb(moe.QT_IQ3_XXS, 2560 * 640) == 6400 * 98 and tb(moe.QT_IQ2_S, 256) == 82 and tb(30, 5) == 10
     assert tb(0, 3) == 12 and tb(moe.QT_Q4_K, 100) == 0 and tb(99, 256) == 0
+
+
+def test_hostile_offsets_and_shapes(tmp_path):
+    """Tensor records whose offset or element count would wrap 64-bit arithmetic are refused, not mapped."""
+    path = str(tmp_path / "h.gguf")
+    q4 = np.zeros(144, np.uint8)
+    gw.write(path, KV, [("x", moe.QT_Q4_K, (256,), q4)])
+    raw = bytearray(open(path, "rb").read())
+    at = raw.find(b"x" + struct.pack("<I", 1)) + 1 + 4 + 8 + 4  # name, dims, shape[0], type: the offset
+    for off in (2**64 - 32, 2**63, len(raw) * 2 // 32 * 32):
+        bad = bytearray(raw)
+        bad[at:at + 8] = struct.pack("<Q", off)
+        open(path, "wb").write(bytes(bad))
+        with pytest.raises(moe.MoeError):
+            moe.GgufFile(path)
+    gw.write(path, KV, [("x", moe.QT_Q4_K, (256, 2**62, 8), q4)])  # 2^73 elements
+    with pytest.raises(moe.MoeError):
+        moe.GgufFile(path)
+
+
+def test_split_shard_alignment_is_its_own(tmp_path):
+    """Each file of a set places its data section at its own general.alignment, whatever the first file says."""
+    stem = str(tmp_path / "s")
+    ts = tensors()
+    gw.write(stem + "-00001-of-00002.gguf", KV, ts[:1], alignment=256)
+    gw.write(stem + "-00002-of-00002.gguf", [], ts[1:])  # default 32
+    g = moe.GgufFile(stem + "-00001-of-00002.gguf")
+    for tname, _, _, data in ts:
+        assert np.array_equal(g.tensor_bytes(tname), data)
+    g.close()
