@@ -16,10 +16,12 @@ if not os.path.exists(LIB_PATH):
 lib = C.CDLL(LIB_PATH)
 
 QT_Q8_0, QT_Q4_K, QT_Q8_K, QT_IQ3_XXS, QT_IQ4_NL, QT_IQ3_S, QT_IQ2_S, QT_Q2_0 = 8, 12, 15, 18, 20, 21, 22, 42
-TYPE_NAMES = {QT_Q8_0: "Q8_0", QT_Q4_K: "Q4_K", QT_IQ3_S: "IQ3_S", QT_IQ4_NL: "IQ4_NL", QT_Q2_0: "Q2_0",
-              QT_IQ3_XXS: "IQ3_XXS", QT_IQ2_S: "IQ2_S"}
-BLOCK = {QT_Q8_0: (32, 34), QT_Q4_K: (256, 144), QT_IQ3_S: (256, 110), QT_IQ4_NL: (32, 18), QT_Q2_0: (64, 18),
-         QT_IQ3_XXS: (256, 98), QT_IQ2_S: (256, 82)}
+QT_Q5_K, QT_Q6_K, QT_IQ4_XS = 13, 14, 23
+TYPE_NAMES = {QT_Q8_0: "Q8_0", QT_Q4_K: "Q4_K", QT_Q5_K: "Q5_K", QT_Q6_K: "Q6_K", QT_IQ3_S: "IQ3_S",
+              QT_IQ4_NL: "IQ4_NL", QT_IQ4_XS: "IQ4_XS", QT_Q2_0: "Q2_0", QT_IQ3_XXS: "IQ3_XXS", QT_IQ2_S: "IQ2_S"}
+TYPE_IDS = {v: k for k, v in TYPE_NAMES.items()}
+BLOCK = {QT_Q8_0: (32, 34), QT_Q4_K: (256, 144), QT_Q5_K: (256, 176), QT_Q6_K: (256, 210), QT_IQ3_S: (256, 110),
+         QT_IQ4_NL: (32, 18), QT_IQ4_XS: (256, 136), QT_Q2_0: (64, 18), QT_IQ3_XXS: (256, 98), QT_IQ2_S: (256, 82)}
 CODEBOOK_TYPES = (QT_IQ3_XXS, QT_IQ2_S)  # decoded through the caller's codebooks (set_codebooks)
 # The codebook buffer's layout (c0ven_quant.h QGRID_*): byte offsets of iq2s_grid, iq3xxs_grid, iq3s_grid, kvalues.
 QGRID_IQ2S, QGRID_IQ3XXS, QGRID_IQ3S, QGRID_KVALUES, QGRID_BYTES = 0, 8192, 9216, 11264, 33808
@@ -34,7 +36,7 @@ class MoeConfig(C.Structure):
         ("n_layer", C.c_uint32), ("gate_type", C.c_uint32), ("down_type", C.c_uint32), ("has_shared", C.c_uint32),
         ("sh_gate_type", C.c_uint32), ("sh_down_type", C.c_uint32), ("max_tokens", C.c_uint32),
         ("swiglu_limit", C.c_float), ("device", C.c_int32), ("borrowed_immutable", C.c_uint32),
-        ("hc_lr", C.c_uint32), ("reserved", C.c_uint32 * 2),
+        ("hc_lr", C.c_uint32), ("sh_up_type", C.c_uint32), ("reserved", C.c_uint32 * 1),
     ]
 
 
@@ -86,6 +88,7 @@ _SIGS = {
     "moe_compute_many": (_i32, [_P, C.POINTER(MoeCmJob), _u32, _u32, _P, _u64, _P, _u64]),
     "moe_forward_experts": (_i32, [_P, C.POINTER(MoeJob), _u32, _u32, _P, _u64, _P, _u64]),
     "moe_h_rows": (_u32, [C.POINTER(MoeConfig)]),
+    "moe_check_config": (_i32, [C.POINTER(MoeConfig)]),
     "moe_prefill_dispatch": (_i32, [_P, C.POINTER(MoeTile), _u32, C.POINTER(_u32), _P]),
     "moe_sync": (_i32, [_P]),
     "moe_check": (_i32, [_P, _P]),
@@ -288,13 +291,14 @@ class MoeBlock:
 
     def __init__(self, n_embd, n_ff, n_expert, n_used, gate_type, down_type, has_shared=True, sh_gate_type=None,
                  sh_down_type=None, n_layer=1, max_tokens=16, swiglu_limit=0.0, device=0, borrowed_immutable=0,
-                 hc_lr=0):
+                 hc_lr=0, sh_up_type=None):
         self.cfg = MoeConfig(n_embd=n_embd, n_ff=n_ff, n_expert=n_expert, n_used=n_used, n_layer=n_layer,
                              gate_type=gate_type, down_type=down_type, has_shared=1 if has_shared else 0,
                              sh_gate_type=sh_gate_type if sh_gate_type is not None else gate_type,
                              sh_down_type=sh_down_type if sh_down_type is not None else down_type,
                              max_tokens=max_tokens, swiglu_limit=swiglu_limit, device=device,
-                             borrowed_immutable=borrowed_immutable, hc_lr=hc_lr)
+                             borrowed_immutable=borrowed_immutable, hc_lr=hc_lr,
+                             sh_up_type=0 if sh_up_type is None else sh_up_type)
         h = _P()
         st = lib.moe_open(C.byref(self.cfg), C.byref(h))
         if st != MOE_OK:

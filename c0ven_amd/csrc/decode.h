@@ -84,6 +84,7 @@ constexpr uint32_t hc_items(uint32_t T, uint32_t H, uint32_t lr) {
 struct DecodeParams {
   uint32_t H, F, E, K, T;
   uint32_t gate_type, down_type, sh_gate_type, sh_down_type, has_shared;
+  uint32_t sh_up_type;       // the shared expert's up (its gate's activation type; a grid type only if equal to gate's)
   uint32_t xact_r, xact_s;  // the activation types x is quantised to for the routed and the shared gate
   float swiglu_limit;
   uint32_t route;            // 1: route x; 0: the host gave ids, w and the groups (pre-routed jobs)
@@ -135,12 +136,13 @@ struct DecodeParams {
 
 // The weight types a launch may meet, as a set (bits below): moe_decode is compiled once per set, so a context whose
 // matrices share one type carries no other type's code (and no register pressure from it). kTypeQ8_0 stands for the
-// 32-value block types that meet q8_0 activations (Q8_0, IQ4_NL, Q2_0), which differ only in how a unit decodes, and
-// kTypeIQ2 for the codebook types (IQ3_XXS, IQ2_S).
+// 32-value block types that meet q8_0 activations (Q8_0, IQ4_NL, Q2_0), which differ only in how a unit decodes,
+// kTypeQ4_K for the q8_K types without a codebook (Q4_K, Q5_K, Q6_K, IQ4_XS) and kTypeIQ2 for the codebook types
+// (IQ3_XXS, IQ2_S).
 constexpr uint32_t kTypeQ8_0 = 1, kTypeQ4_K = 2, kTypeIQ3_S = 4, kTypeIQ2 = 8;
 constexpr uint32_t type_bit(uint32_t qt) {
   return (qt == QT_Q8_0 || qt == QT_IQ4_NL || qt == QT_Q2_0) ? kTypeQ8_0
-         : qt == QT_Q4_K                                     ? kTypeQ4_K
+         : kq_family(qt)                                     ? kTypeQ4_K
          : qt == QT_IQ3_S                                    ? kTypeIQ3_S
                                                              : kTypeIQ2;
 }

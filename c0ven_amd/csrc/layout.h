@@ -19,6 +19,10 @@
 //   IQ3_XXS (98 B):          qs 4 x 16 B (grid indices, sub-blocks 2p, 2p+1), scale-and-sign words 2 x 16 B, d 1 x 2 B.
 //   IQ2_S (82 B):            qs 2 x 16 B (index low bits, sub-blocks 4p..4p+3), signs 2 x 16 B, qh 1 x 8 B,
 //                            scales 1 x 8 B, then d 1 x 2 B.
+//   IQ4_XS (136 B):          qs 8 x 16 B (sub-block p's 16 bytes), then the block's first 8 bytes 1 x 8 B (d,
+//                            scales_h, scales_l as the file has them).
+//   Q5_K (176 B):            qs 8 x 16 B (as Q4_K), qh 2 x 16 B, scales 3 x 4 B, then d|dmin 1 x 4 B.
+//   Q6_K (210 B):            ql 8 x 16 B, qh 4 x 16 B, scales 1 x 16 B, then d 1 x 2 B.
 #pragma once
 
 #include <stdint.h>
@@ -55,11 +59,23 @@ C0VEN_HD uint32_t unit_bytes(uint32_t type) {
          : type == QT_Q2_0  ? 72u
          : type == QT_IQ3_XXS ? 98u
          : type == QT_IQ2_S ? 82u
+         : type == QT_IQ4_XS ? 136u
+         : type == QT_Q5_K  ? 176u
+         : type == QT_Q6_K  ? 210u
                             : 0u;
 }
 // The 256-value types whose values come from a grid codebook (decoded with the grid in LDS).
 C0VEN_HD constexpr bool grid_family(uint32_t type) {
   return type == QT_IQ3_S || type == QT_IQ3_XXS || type == QT_IQ2_S;
+}
+// The q8_K types decoded without a codebook: their A operands come from the unit's own bytes.
+C0VEN_HD constexpr bool kq_family(uint32_t type) {
+  return type == QT_Q4_K || type == QT_Q5_K || type == QT_Q6_K || type == QT_IQ4_XS;
+}
+// The 256-value types the prefill GEMM takes block by block (one MFMA a 32-value block or half block, then the
+// block's integer scale): the grid types and IQ4_XS, Q5_K, Q6_K.
+C0VEN_HD constexpr bool block_scaled(uint32_t type) {
+  return grid_family(type) || type == QT_IQ4_XS || type == QT_Q5_K || type == QT_Q6_K;
 }
 // The 32-value block types that meet q8_0 activations (one fp32 term a 32-value block, or half a Q2_0 block).
 C0VEN_HD constexpr bool q8_family(uint32_t type) { return type == QT_Q8_0 || type == QT_IQ4_NL || type == QT_Q2_0; }
@@ -75,6 +91,9 @@ namespace iq4_nlt { constexpr uint32_t kQs = 0, kD = 8 * 16; }
 namespace q2_0t { constexpr uint32_t kQs = 0, kD = 4 * 16; }
 namespace iq3_xxst { constexpr uint32_t kQs = 0, kSs = 4 * 16, kD = 6 * 16; }
 namespace iq2_st { constexpr uint32_t kQs = 0, kSigns = 2 * 16, kQh = 4 * 16, kScales = 4 * 16 + 8, kD = 4 * 16 + 16; }
+namespace iq4_xst { constexpr uint32_t kQs = 0, kMeta = 8 * 16; }
+namespace q5_kt { constexpr uint32_t kQs = 0, kQh = 8 * 16, kScales = 8 * 16 + 2 * 16, kDm = 8 * 16 + 2 * 16 + 3 * 4; }
+namespace q6_kt { constexpr uint32_t kQl = 0, kQh = 8 * 16, kScales = 8 * 16 + 4 * 16, kD = 8 * 16 + 4 * 16 + 16; }
 namespace iq3_st {
 constexpr uint32_t kQs = 0, kSigns = 4 * 16, kQh = 6 * 16, kScales = 6 * 16 + 2 * 4, kD = 6 * 16 + 3 * 4;
 }

@@ -64,6 +64,8 @@ struct Iq3sRaw {
   __device__ __forceinline__ int ls(uint32_t i, uint32_t ib) const { return 1 + 2 * (int)((sc[i] >> (4 * ib)) & 15u); }
   __device__ __forceinline__ void prep(uint32_t) {}
   static constexpr float kFactor = 1.0f;  // the super-block term: kFactor ((d d_a) isum)
+  static constexpr uint32_t kHalves = 1;  // MFMAs a block (2: its 16-value halves have scales of their own)
+  static constexpr bool kMin = false;     // a minimum term from the activations' block sums (Q5_K)
 };
 
 // IQ3_XXS (UnitIQ3_XXS::term): the lane's eight bytes of block ib are its groups 2 g and 2 g + 1, the block's sign
@@ -108,6 +110,8 @@ struct Iq3xxsRaw {
   }
   __device__ __forceinline__ int ls(uint32_t i, uint32_t ib) const { return 1 + 2 * (int)((sc[i] >> (4 * ib)) & 15u); }
   static constexpr float kFactor = 0.25f;
+  static constexpr uint32_t kHalves = 1;
+  static constexpr bool kMin = false;
 };
 
 // IQ2_S (UnitIQ2_S::term): the lane's eight bytes of block ib are group g of it (a 10-bit grid index into iq2s_grid,
@@ -117,6 +121,7 @@ struct Iq3xxsRaw {
 struct Iq2sRaw {
   uint32_t qs[8], sg[8], qh[2], scw[2], sc[4][2], dh[4];
   static constexpr uint32_t kHalves = 2;
+  static constexpr bool kMin = false;
   __device__ __forceinline__ void load(const uint8_t *mat, uint32_t U, uint32_t row0, uint32_t u, uint32_t lane) {
     const uint32_t g = lane / 16, nl = kTileRows * U;
     const uint8_t *tile = mat + (uint64_t)(row0 / kTileRows) * tile_bytes(QT_IQ2_S, U);

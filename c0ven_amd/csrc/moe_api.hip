@@ -276,9 +276,20 @@ void validate(const moe_config &c) {
           "n_ff and n_embd must be whole numbers of the decode kernel's row blocks");
   require(c.n_expert && c.n_expert <= kMaxExperts, "n_expert must be 1..512");
   require(c.n_used && c.n_used <= kMaxUsed && c.n_used <= c.n_expert, "n_used must be 1..min(16, n_expert)");
-  require(quant_gpu_supported(c.gate_type) && quant_gpu_supported(c.down_type), "expert types must be Q8_0, Q4_K, IQ3_S, IQ4_NL or Q2_0");
-  require(!c.has_shared || (quant_gpu_supported(c.sh_gate_type) && quant_gpu_supported(c.sh_down_type)),
-          "shared expert types must be Q8_0, Q4_K, IQ3_S, IQ4_NL or Q2_0");
+  const char *kTypes = "Q8_0, Q4_K, Q5_K, Q6_K, IQ3_S, IQ4_NL, IQ4_XS, Q2_0, IQ3_XXS or IQ2_S";
+  require(quant_gpu_supported(c.gate_type) && quant_gpu_supported(c.down_type),
+          std::string("expert types must be ") + kTypes);
+  if (c.has_shared) {
+    require(quant_gpu_supported(c.sh_gate_type) && quant_gpu_supported(c.sh_up_type) &&
+                quant_gpu_supported(c.sh_down_type),
+            std::string("shared expert types must be ") + kTypes);
+    require(c.sh_up_type == c.sh_gate_type ||
+                (quant_vec_dot_type(c.sh_up_type) == quant_vec_dot_type(c.sh_gate_type) &&
+                 !grid_family(c.sh_gate_type) && !grid_family(c.sh_up_type)),
+            "the shared expert's gate and up may differ only among types of one activation type without a codebook");
+    require(c.sh_up_type == c.sh_gate_type || c.n_ff % 128 == 0,
+            "a shared expert with gate and up of different types needs n_ff a multiple of 128");
+  }
   require(c.max_tokens <= kMaxPrefillTokens, "max_tokens must be at most 16384");
   require(c.swiglu_limit >= 0.0f, "swiglu_limit must be >= 0");
   require(c.hc_lr <= kHcMaxLr && c.hc_lr % 8 == 0, "hc_lr must be a multiple of 8, at most 512");
@@ -293,12 +304,14 @@ void need_codebooks(const moe_ctx *c, std::initializer_list<uint32_t> types) {
 
 DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   const moe_config &g = c->cfg;
-  need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_down_type : 0u});
+  need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_up_type : 0u,
+                     g.has_shared ? g.sh_down_type : 0u});
   const Layer &L = c->layers[layer];
   DecodeParams p{};
   p.H = g.n_embd, p.F = g.n_ff, p.E = g.n_expert, p.K = g.n_used, p.T = T;
   p.gate_type = g.gate_type, p.down_type = g.down_type;
   p.sh_gate_type = g.sh_gate_type, p.sh_down_type = g.sh_down_type, p.has_shared = g.has_shared;
+  p.sh_up_type = g.sh_up_type;
   p.xact_r = quant_vec_dot_type(g.gate_type);
   p.xact_s = g.has_shared ? quant_vec_dot_type(g.sh_gate_type) : p.xact_r;
   p.swiglu_limit = g.swiglu_limit;
@@ -387,7 +400,7 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
   require(c->layers[layer].router != nullptr, "the layer's router is not loaded");
   const uint32_t K = c->cfg.n_used;
   need_codebooks(c, {c->cfg.gate_type, c->cfg.down_type, c->cfg.has_shared ? c->cfg.sh_gate_type : 0u,
-                     c->cfg.has_shared ? c->cfg.sh_down_type : 0u});
+                     c->cfg.has_shared ? c->cfg.sh_up_type : 0u, c->cfg.has_shared ? c->cfg.sh_down_type : 0u});
   if (T <= c->tdec) {
     DecodeParams p = base_params(c, layer, T);
     p.x = x, p.y = y;
@@ -397,7 +410,7 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
     const moe_config &g = c->cfg;
     const Layer &L = c->layers[layer];
     PfShape S{g.n_embd, g.n_ff, g.n_expert, K, T, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type,
-              g.has_shared, g.swiglu_limit};
+              g.has_shared, g.swiglu_limit, g.sh_up_type};
     PfLayer PL{L.router, L.has_bias ? L.bias : nullptr, L.experts, c->ex_bytes, c->ex_up, c->ex_down, L.shared,
                c->sh_up, c->sh_down, c->codebooks};
     PfHook hook{c->timing ? timing_hook : nullptr, c};
@@ -441,6 +454,25 @@ MOE_API const char *moe_last_error(const moe_ctx *ctx) { return ctx ? ctx->err.c
 
 MOE_API uint32_t moe_h_rows(const moe_config *cfg) { return cfg && cfg->n_ff % kUnit == 0 ? kUnit : 0; }
 
+MOE_API moe_status moe_check_config(const moe_config *cfg) {
+  if (!cfg) {
+    g_open_error = "null argument";
+    return MOE_BAD_ARGUMENT;
+  }
+  try {
+    moe_config g = *cfg;
+    if (!g.n_layer) g.n_layer = 1;
+    if (!g.max_tokens) g.max_tokens = kMaxDecodeTokens;
+    if (!g.sh_up_type) g.sh_up_type = g.sh_gate_type;
+    validate(g);
+  } catch (const Error &e) {
+    g_open_error = e.what();
+    return e.st;
+  }
+  g_open_error.clear();
+  return MOE_OK;
+}
+
 MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
   if (!cfg || !out) {
     g_open_error = "null argument";
@@ -452,6 +484,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     moe_config g = *cfg;
     if (!g.n_layer) g.n_layer = 1;
     if (!g.max_tokens) g.max_tokens = kMaxDecodeTokens;
+    if (!g.sh_up_type) g.sh_up_type = g.sh_gate_type;
     validate(g);
     c = new moe_ctx();
     c->cfg = g;
@@ -464,8 +497,9 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     const uint64_t gu = matrix_bytes(g.gate_type, F, H), dn = matrix_bytes(g.down_type, H, F);
     c->ex_up = gu, c->ex_down = 2 * gu, c->ex_bytes = 2 * gu + dn;
     if (g.has_shared) {
-      const uint64_t sgu = matrix_bytes(g.sh_gate_type, F, H), sdn = matrix_bytes(g.sh_down_type, H, F);
-      c->sh_up = sgu, c->sh_down = 2 * sgu, c->sh_bytes = 2 * sgu + sdn;
+      const uint64_t sg = matrix_bytes(g.sh_gate_type, F, H), su = matrix_bytes(g.sh_up_type, F, H);
+      const uint64_t sdn = matrix_bytes(g.sh_down_type, H, F);
+      c->sh_up = sg, c->sh_down = sg + su, c->sh_bytes = sg + su + sdn;
     }
     c->layers.resize(g.n_layer);
     for (auto &L : c->layers) {
@@ -515,6 +549,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
       b.y_asg = c->alloc<float>(A2 * H);
       if (g.has_shared) {
         b.h_sh = c->alloc<float>((uint64_t)TM * F);
+        if (g.sh_up_type != g.sh_gate_type) b.h_sh_up = c->alloc<float>((uint64_t)TM * F);
         b.hact_sh = c->alloc<uint8_t>((uint64_t)TM * Ud * kActBytes);
         b.y_sh = c->alloc<float>((uint64_t)TM * H);
         check(hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking), "hipStreamCreate");
@@ -567,7 +602,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
                                (size_t)MOE_GROUP_MAX * act_tok_stride(Ud), kGroupingLds});
     int per_cu = 0, ncu = 0;
     uint32_t types = type_bit(g.gate_type) | type_bit(g.down_type);
-    if (g.has_shared) types |= type_bit(g.sh_gate_type) | type_bit(g.sh_down_type);
+    if (g.has_shared) types |= type_bit(g.sh_gate_type) | type_bit(g.sh_up_type) | type_bit(g.sh_down_type);
     c->kernel = decode_kernel(types, false);
     check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, c->kernel, kWG, c->lds), "occupancy");
     check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, g.device), "CU count");
@@ -631,12 +666,14 @@ MOE_API moe_status moe_load_expert(moe_ctx *c, uint32_t layer, uint32_t expert, 
     require(layer < g.n_layer && gate && up && down, "bad layer or null matrix");
     const bool shared = expert == g.n_expert;
     require(expert < g.n_expert || (shared && g.has_shared), "expert out of range");
-    const uint32_t gt = shared ? g.sh_gate_type : g.gate_type, dt = shared ? g.sh_down_type : g.down_type;
-    const uint64_t gu = matrix_bytes(gt, g.n_ff, g.n_embd), dn = matrix_bytes(dt, g.n_embd, g.n_ff);
-    std::vector<uint8_t> buf(2 * gu + dn);
+    const uint32_t gt = shared ? g.sh_gate_type : g.gate_type, ut = shared ? g.sh_up_type : g.gate_type;
+    const uint32_t dt = shared ? g.sh_down_type : g.down_type;
+    const uint64_t gb = matrix_bytes(gt, g.n_ff, g.n_embd), ub = matrix_bytes(ut, g.n_ff, g.n_embd);
+    const uint64_t dn = matrix_bytes(dt, g.n_embd, g.n_ff);
+    std::vector<uint8_t> buf(gb + ub + dn);
     repack_matrix(gt, gate, g.n_ff, g.n_embd, buf.data());
-    repack_matrix(gt, up, g.n_ff, g.n_embd, buf.data() + gu);
-    repack_matrix(dt, down, g.n_embd, g.n_ff, buf.data() + 2 * gu);
+    repack_matrix(ut, up, g.n_ff, g.n_embd, buf.data() + gb);
+    repack_matrix(dt, down, g.n_embd, g.n_ff, buf.data() + gb + ub);
     uint8_t *dst = shared ? c->layers[layer].shared : c->layers[layer].experts + (uint64_t)expert * c->ex_bytes;
     check(hipMemcpy(dst, buf.data(), buf.size(), hipMemcpyHostToDevice), "upload expert");
   });
@@ -674,7 +711,7 @@ MOE_API moe_status moe_load_layer_gguf(moe_ctx *c, uint32_t layer, const c0ven_g
         throw Error(MOE_ERROR, c->err);
     if (g.has_shared) {
       const uint8_t *sg = tensor("ffn_gate_shexp.weight", g.sh_gate_type, {H, F});
-      const uint8_t *su = tensor("ffn_up_shexp.weight", g.sh_gate_type, {H, F});
+      const uint8_t *su = tensor("ffn_up_shexp.weight", g.sh_up_type, {H, F});
       const uint8_t *sd = tensor("ffn_down_shexp.weight", g.sh_down_type, {F, H});
       if (moe_load_expert(c, layer, (uint32_t)E, sg, su, sd) != MOE_OK) throw Error(MOE_ERROR, c->err);
     }
@@ -736,7 +773,8 @@ MOE_API moe_status moe_forward_hc_async(moe_ctx *c, uint32_t layer, float *R_dev
     require(layer < g.n_layer && c->layers[layer].router != nullptr, "layer out of range or its router not loaded");
     require(c->layers[layer].has_hc, "the layer's hyper-connection module is not loaded (moe_load_hc)");
     require(ntok >= 1 && ntok <= c->tdec, "moe_forward_hc_async takes 1..min(max_tokens, 16) tokens");
-    need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_down_type : 0u});
+    need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_up_type : 0u,
+                     g.has_shared ? g.sh_down_type : 0u});
     const Layer &L = c->layers[layer];
     hipStream_t s = stream ? (hipStream_t)stream : c->stream;
     DecodeParams p = base_params(c, layer, ntok);
@@ -873,7 +911,8 @@ MOE_API moe_status moe_compute_many(moe_ctx *c, const moe_cm_job *jobs, uint32_t
     const moe_config &g = c->cfg;
     const uint32_t H = g.n_embd, F = g.n_ff;
     require(x && y && ntok >= 1 && x_stride >= H && y_stride >= H, "bad x, y, ntok or strides");
-    need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_down_type : 0u});
+    need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_up_type : 0u,
+                     g.has_shared ? g.sh_down_type : 0u});
     require(ntok <= c->tdec || (ntok <= c->tmax && c->tmax > c->tdec),
             "ntok must be at most 16, or at most max_tokens when that exceeds 16");
     require(njobs == 0 || jobs, "null jobs");
@@ -953,7 +992,8 @@ MOE_API moe_status moe_compute_many(moe_ctx *c, const moe_cm_job *jobs, uint32_t
       }
       check(hipMemcpyAsync(c->pf.ids, ids.data(), sizeof(int32_t) * ids.size(), hipMemcpyHostToDevice, s), "ids");
       check(hipMemcpyAsync(c->pf.w, w.data(), sizeof(float) * w.size(), hipMemcpyHostToDevice, s), "w");
-      PfShape S{H, F, c->bc_slots, K, ntok, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type, 0, g.swiglu_limit};
+      PfShape S{H, F, c->bc_slots, K, ntok, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type, 0, g.swiglu_limit,
+                g.sh_up_type};
       PfLayer PL{nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0, c->codebooks};
       PfHook hook{c->timing ? timing_hook : nullptr, c};
       check(prefill_jobs(S, PL, c->pf, c->x_dev, c->y_dev, s, hook), "prefill launch");
@@ -1175,6 +1215,7 @@ MOE_API moe_status moe_expert_bytes(const moe_ctx *c, uint32_t which, uint64_t *
     case 1: *bytes = matrix_bytes(g.down_type, g.n_embd, g.n_ff); break;
     case 2: *bytes = g.has_shared ? matrix_bytes(g.sh_gate_type, g.n_ff, g.n_embd) : 0; break;
     case 3: *bytes = g.has_shared ? matrix_bytes(g.sh_down_type, g.n_embd, g.n_ff) : 0; break;
+    case 4: *bytes = g.has_shared ? matrix_bytes(g.sh_up_type, g.n_ff, g.n_embd) : 0; break;
     default: return MOE_BAD_ARGUMENT;
   }
   return MOE_OK;
@@ -1239,7 +1280,7 @@ MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap) {
       ROW(moe_config, down_type),    ROW(moe_config, has_shared),   ROW(moe_config, sh_gate_type),
       ROW(moe_config, sh_down_type), ROW(moe_config, max_tokens),   ROW(moe_config, swiglu_limit),
       ROW(moe_config, device),       ROW(moe_config, borrowed_immutable), ROW(moe_config, hc_lr),
-      ROW(moe_config, reserved),
+      ROW(moe_config, sh_up_type),   ROW(moe_config, reserved),
       STRUCT(moe_config),            ROW(moe_expert_weights, gate), ROW(moe_expert_weights, up),
       ROW(moe_expert_weights, down), ROW(moe_expert_weights, down_parts), ROW(moe_expert_weights, down_blocks),
       STRUCT(moe_expert_weights),    ROW(moe_cm_job, expert),       ROW(moe_cm_job, tok),

@@ -52,6 +52,30 @@ __global__ void __launch_bounds__(64) moe_dequant(const uint8_t *mat, uint32_t t
           o[v] = __fsub_rn(__fmul_rn(dl, (float)((w.lo[wd] >> (8 * i)) & 0xff)), ml);
           o[v + 32] = __fsub_rn(__fmul_rn(dh, (float)((w.hi[wd] >> (8 * i)) & 0xff)), mh);
         }
+  } else if (type == QT_Q5_K) {  // (d sc) q - (dmin m), q 0..31
+    UnitQ5_K w;
+    w.load(tile, idx, nl);
+    if (live)
+      for (int wd = 0; wd < 32; wd++)
+        for (int i = 0; i < 4; i++) {
+          const int c = wd / 8, v = 64 * c + 4 * (wd % 8) + i;
+          const float dl = __fmul_rn(w.d, (float)w.sc[2 * c]), ml = __fmul_rn(w.dmin, (float)w.mn[2 * c]);
+          const float dh = __fmul_rn(w.d, (float)w.sc[2 * c + 1]), mh = __fmul_rn(w.dmin, (float)w.mn[2 * c + 1]);
+          o[v] = __fsub_rn(__fmul_rn(dl, (float)((w.lo[wd] >> (8 * i)) & 0xff)), ml);
+          o[v + 32] = __fsub_rn(__fmul_rn(dh, (float)((w.hi[wd] >> (8 * i)) & 0xff)), mh);
+        }
+  } else if (type == QT_Q6_K) {  // (d sc) (q - 32)
+    UnitQ6_K w;
+    w.load(tile, idx, nl);
+    if (live)
+      for (int i = 0; i < 256; i++)
+        o[i] = __fmul_rn(__fmul_rn(w.d, (float)w.sc[i / 16]), (float)(int8_t)(w.w[i / 4] >> (8 * (i % 4))));
+  } else if (type == QT_IQ4_XS) {  // (d (ls - 32)) kvalues[nibble]
+    UnitIQ4_XS w;
+    w.load(tile, idx, nl);
+    if (live)
+      for (int i = 0; i < 256; i++)
+        o[i] = __fmul_rn(__fmul_rn(w.d, (float)w.ls[i / 32]), (float)(int8_t)(w.q[i / 4] >> (8 * (i % 4))));
   } else if (type == QT_IQ3_XXS) {  // (d (0.5 + s)) 0.5, times the signed grid value
     UnitIQ3_XXS w;
     w.load(tile, idx, nl, grid);

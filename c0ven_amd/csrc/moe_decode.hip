@@ -209,7 +209,7 @@ __device__ __forceinline__ GroupMat group_mat(const DecodeParams &p, int32_t slo
   GroupMat m;
   m.shared = slot == (int32_t)p.E;
   if (m.shared) {
-    m.type = which == 2 ? p.sh_down_type : p.sh_gate_type;
+    m.type = which == 2 ? p.sh_down_type : which == 1 ? p.sh_up_type : p.sh_gate_type;
     m.mat = p.shared + (which == 0 ? 0 : which == 1 ? p.sh_up_off : p.sh_down_off);
   } else {
     m.type = which == 2 ? p.down_type : p.gate_type;
@@ -269,13 +269,27 @@ __device__ __forceinline__ void pair_terms(uint32_t type, const uint8_t *tile, u
     }
   }
   if constexpr ((kTypes & kTypeQ4_K) != 0) {
-    if ((kTypes & ~kTypeQ8_0) == kTypeQ4_K || type == QT_Q4_K) {
-      UnitQ4_K w;
-      w.load(tile, idx, nl);
-      ready();
+    if ((kTypes & ~kTypeQ8_0) == kTypeQ4_K || kq_family(type)) {
+      const auto run = [&](auto &w) {
+        w.load(tile, idx, nl);
+        ready();
 #pragma unroll
-      for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
-        if (j < n) t[j] = w.term(Act(act + j * stride));
+        for (uint32_t j = 0; j < MOE_GROUP_MAX; j++)
+          if (j < n) t[j] = w.term(Act(act + j * stride));
+      };
+      if (type == QT_Q4_K) {  // a branch a type, so that no two types' registers are live together
+        UnitQ4_K w;
+        run(w);
+      } else if (type == QT_Q6_K) {
+        UnitQ6_K w;
+        run(w);
+      } else if (type == QT_IQ4_XS) {
+        UnitIQ4_XS w;
+        run(w);
+      } else {
+        UnitQ5_K w;
+        run(w);
+      }
       return;
     }
   }
@@ -885,15 +899,17 @@ __device__ __forceinline__ void gate_up_item(const DecodeParams &p, const GroupL
                                              uint64_t *mark) {
   // U units a row, UL lanes a row (U rounded up to a power of two; lanes past U add exact zeros).
   const uint32_t U = units_of(p.H), UL = unit_lanes(U), rows = gate_up_rows(UL), row0 = blk * rows, n = sg->n;
-  const GroupMat gm = group_mat(p, sg->slot, 0);
-  if (use_mfma<kTypes>(gm.type, U, 8, n)) {
-    gate_up_mfma(p, sg, gm, blk, lds, (float *)(lds + MOE_GROUP_MAX * act_tok_stride(U)), tab, mark);
+  const GroupMat gm0 = group_mat(p, sg->slot, 0);
+  // Gate and up share a type except for a shared expert whose matrices differ (both then codebook-free).
+  if (use_mfma<kTypes>(gm0.type, U, 8, n) && (!gm0.shared || p.sh_up_type == gm0.type)) {
+    gate_up_mfma(p, sg, gm0, blk, lds, (float *)(lds + MOE_GROUP_MAX * act_tok_stride(U)), tab, mark);
     return;
   }
-  if ((kTypes & (kTypeIQ3_S | kTypeIQ2)) && grid_family(gm.type)) load_grid(p, gm.type, grid_lds, grid_have);
+  if ((kTypes & (kTypeIQ3_S | kTypeIQ2)) && grid_family(gm0.type)) load_grid(p, gm0.type, grid_lds, grid_have);
   const uint32_t lane = lane_id(), m = wave_id() & 1u, r = lane / UL, u = lane % UL, ue = u < U ? u : 0u;
   const uint32_t rl = (wave_id() >> 1) * (64 / UL) + r, row = row0 + rl;  // rl: the row within the item
-  const uint8_t *mat = gm.mat + (m ? (gm.shared ? p.sh_up_off : p.ex_up_off) : 0);
+  const GroupMat gm = m ? group_mat(p, sg->slot, 1) : gm0;  // this wave's matrix (wave-uniform)
+  const uint8_t *mat = gm.mat;
   const uint8_t *tile = mat + (uint64_t)(row / kTileRows) * tile_bytes(gm.type, U);
   float t[MOE_GROUP_MAX];
   pair_terms<kTypes>(gm.type, tile, pair_idx(row % kTileRows, ue), kTileRows * U, grid_lds,

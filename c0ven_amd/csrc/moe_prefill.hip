@@ -14,6 +14,7 @@
 #include "iq3s_grid.h"
 #include "layout.h"
 #include "mfma_iq3s.h"
+#include "mfma_kq.h"
 #include "mfma_q4k.h"
 #include "mfma_q8_0.h"
 #include "prefill.h"
@@ -56,6 +57,29 @@ __global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   quant_unit<false, true, true, true>(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
   if (o2) quant_unit<false, true, true, true>(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
+}
+
+// h = silu(g) u of gate and up rows computed apart (a shared expert whose gate and up differ in type), quantised as
+// pf_quant_rows quantises h: the same SwiGLU as the fused gate/up kernels' epilogue, then the same units.
+__global__ void __launch_bounds__(kPfWG) pf_quant_swiglu(const float *g, const float *up, uint32_t ld, uint32_t rows,
+                                                         uint32_t U, float limit, uint32_t t1, uint8_t *o1) {
+  __shared__ uint64_t tab[32];
+  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
+  const uint32_t hw = blockIdx.x * (kPfWG / 32) + threadIdx.x / 32, l32 = threadIdx.x & 31u;
+  const uint32_t row = hw / U, u = hw % U;
+  if (row >= rows) return;
+  const uint32_t v0 = u * kUnit + 8 * l32;
+  float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (v0 < ld) {
+    const float4 *pg = (const float4 *)(g + (uint64_t)row * ld + v0), *pu = (const float4 *)(up + (uint64_t)row * ld + v0);
+    const float4 g0 = pg[0], g1 = pg[1], u0 = pu[0], u1 = pu[1];
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = swiglu_one(gv[i], uv[i], limit, tab);
+  }
+  quant_unit<false, true, true, true>(v, l32, t1, o1 + ((uint64_t)row * U + u) * kActBytes);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -501,9 +525,16 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
           kType == QT_IQ3_XXS, Iq3xxsRaw,
           std::conditional_t<
               kType == QT_IQ2_S, Iq2sRaw,
-              std::conditional_t<kType == QT_Q8_0, Q80Raw,
-                                 std::conditional_t<kType == QT_IQ4_NL, Iq4nlRaw,
-                                                    std::conditional_t<kType == QT_Q2_0, Q20Raw, Q4kRaw>>>>>>;
+              std::conditional_t<
+                  kType == QT_Q8_0, Q80Raw,
+                  std::conditional_t<
+                      kType == QT_IQ4_NL, Iq4nlRaw,
+                      std::conditional_t<
+                          kType == QT_Q2_0, Q20Raw,
+                          std::conditional_t<
+                              kType == QT_IQ4_XS, Iq4xsRaw,
+                              std::conditional_t<kType == QT_Q5_K, Q5kRaw,
+                                                 std::conditional_t<kType == QT_Q6_K, Q6kRaw, Q4kRaw>>>>>>>>>;
   // 1-D grid of (tile, row block) pairs, the row block fastest in the XCD-aware logical index over the pairs that
   // exist (the grid is sized for the most tiles a dispatch can make).
   const uint32_t nrb = g.row_blocks;
@@ -565,16 +596,17 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   const auto body = [&](uint32_t u, const uint8_t *__restrict__ buf, uint8_t *__restrict__ nbuf) {
     // Q4_K decodes the unit's raw words first and loads the next unit's into the same registers; the other types read
     // theirs in the MFMAs and load the next unit's into a second set.
-    constexpr bool kInPlace = kType == QT_Q4_K;
+    constexpr bool kInPlace = kType == QT_Q4_K || kType == QT_Q5_K;  // Q5_K: registers for one unit's words only
     Raw next;
     if (u + 1 < U) {
       dma.load_all(act_r, u + 1, nbuf, dump);
       if constexpr (!kInPlace) load_w(next, u + 1);
     }
-    if constexpr (grid_family(kType)) {
-      // Block by block: one MFMA a position tile (IQ2_S: one a half block, the other half's A lanes zero), its D
-      // times the row's block scale added to the unit's integer sum in block order; then kFactor ((d ad) isum) as
-      // UnitIQ3_S / UnitIQ3_XXS / UnitIQ2_S::term.
+    if constexpr (block_scaled(kType)) {
+      // Block by block: one MFMA a position tile (IQ2_S, Q6_K: one a half block, the other half's A lanes zero), its
+      // D times the row's block scale added to the unit's integer sum in block order; then kFactor ((d ad) isum) as
+      // UnitIQ3_S / UnitIQ3_XXS / UnitIQ2_S / UnitIQ4_XS / UnitQ6_K::term, or Q5_K's fma(d ad, isum, -((dmin ad)
+      // imin)) with imin from the positions' block sums (UnitQ4_K::term).
       raw.prep(lane_id());
       int isum[4][4];
 #pragma unroll
@@ -585,7 +617,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
       for (uint32_t ib = 0; ib < 8; ib++) {
         const uint32_t bofs = mfma_code_off(4 * ib + lane_id() / 16);  // the lane's 8 codes of block ib
         const long aw = raw.a_block(ib, lane_id(), grid_lds);
-        if constexpr (kType == QT_IQ2_S) {
+        if constexpr (Raw::kHalves == 2) {
           const bool lo = lane_id() < 32;
           const long a0 = lo ? aw : 0, a1 = lo ? 0 : aw;
           int l0[4], l1[4];
@@ -620,15 +652,33 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
 #pragma unroll
       for (uint32_t pt = 0; pt < 4; pt++) {
         if (pt < npt) {
-          const float ad = *(const float *)(buf + (16 * pt + lane_id() % 16) * kActLds + kActScales);
+          const uint8_t *unit = buf + (16 * pt + lane_id() % 16) * kActLds;
+          const float ad = *(const float *)(unit + kActScales);
+          if constexpr (Raw::kMin) {
+            int bs[8];
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            float t = __fmul_rn(__fmul_rn(h2f((uint16_t)raw.dh[i]), ad), (float)isum[pt][i]);
-            if constexpr (Raw::kFactor != 1.0f) t = __fmul_rn(Raw::kFactor, t);
-            acc[pt][i] = __fadd_rn(acc[pt][i], t);
+            for (uint32_t j = 0; j < 8; j++) bs[j] = *(const int *)(unit + kActSums + 4 * j);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              int imin = 0;
+#pragma unroll
+              for (uint32_t j = 0; j < 8; j++) imin += raw.mn(i, j) * bs[j];
+              const float dd = __fmul_rn(h2f((uint16_t)raw.dh[i]), ad), dm = __fmul_rn(raw.dmin(i), ad);
+              const float t = __builtin_fmaf(dd, (float)isum[pt][i], -__fmul_rn(dm, (float)imin));
+              acc[pt][i] = __fadd_rn(acc[pt][i], t);
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              float t = __fmul_rn(__fmul_rn(h2f((uint16_t)raw.dh[i]), ad), (float)isum[pt][i]);
+              if constexpr (Raw::kFactor != 1.0f) t = __fmul_rn(Raw::kFactor, t);
+              acc[pt][i] = __fadd_rn(acc[pt][i], t);
+            }
           }
         }
       }
+      if constexpr (kInPlace)
+        if (u + 1 < U) load_w(raw, u + 1);
     } else if constexpr (q8_family(kType)) {
       // Block by block: one MFMA a position tile, the block's term (d_w d_a) dot; the eight terms of the unit as the
       // pairwise tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then added to the row's sum.
@@ -1042,6 +1092,12 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
     pf_gemm16<QT_IQ2_S, kGU><<<g2, kPfWG, 0, s>>>(q);
   else if (type == QT_Q2_0)
     pf_gemm16<QT_Q2_0, kGU><<<g2, kPfWG, 0, s>>>(q);
+  else if (type == QT_IQ4_XS)
+    pf_gemm16<QT_IQ4_XS, kGU><<<g2, kPfWG, 0, s>>>(q);
+  else if (type == QT_Q5_K)
+    pf_gemm16<QT_Q5_K, kGU><<<g2, kPfWG, 0, s>>>(q);
+  else if (type == QT_Q6_K)
+    pf_gemm16<QT_Q6_K, kGU><<<g2, kPfWG, 0, s>>>(q);
   else
     pf_gemm16<QT_Q8_0, kGU><<<g2, kPfWG, 0, s>>>(q);
 }
@@ -1076,6 +1132,9 @@ C0VEN_PF_GEMM16(QT_IQ4_NL)
 C0VEN_PF_GEMM16(QT_Q2_0)
 C0VEN_PF_GEMM16(QT_IQ3_XXS)
 C0VEN_PF_GEMM16(QT_IQ2_S)
+C0VEN_PF_GEMM16(QT_IQ4_XS)
+C0VEN_PF_GEMM16(QT_Q5_K)
+C0VEN_PF_GEMM16(QT_Q6_K)
 #undef C0VEN_PF_GEMM16
 template void launch_gemm<false>(uint32_t, uint32_t, dim3, const PfGemm &, hipStream_t);
 template void launch_gemm<true>(uint32_t, uint32_t, dim3, const PfGemm &, hipStream_t);
@@ -1149,19 +1208,33 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
       return hipGetLastError();
     quant_x(ss);
     if (hipEventRecord(b.xq, ss) != hipSuccess) return hipGetLastError();
-    {
-      HookScope k(hook, "pf_gate_up_shared", ss);
-      PfGemm q{};
-      q.shared_T = T, q.K = K, q.act = b.act_s, q.act_by_pos = 0;
-      q.mat = L.shared, q.stride = 0, q.up_off = L.sh_up_off, q.out = b.h_sh, q.out_ld = F;
-      q.codebooks = L.codebooks;
-      q.limit = S.swiglu_limit;
-      launch_gate_up(S.sh_gate_type, q, T, F, Ug, (T + gu_pos(S.sh_gate_type) - 1) / gu_pos(S.sh_gate_type), ss);
-    }
-    {
+    if (S.sh_up_type == S.sh_gate_type) {
+      {
+        HookScope k(hook, "pf_gate_up_shared", ss);
+        PfGemm q{};
+        q.shared_T = T, q.K = K, q.act = b.act_s, q.act_by_pos = 0;
+        q.mat = L.shared, q.stride = 0, q.up_off = L.sh_up_off, q.out = b.h_sh, q.out_ld = F;
+        q.codebooks = L.codebooks;
+        q.limit = S.swiglu_limit;
+        launch_gate_up(S.sh_gate_type, q, T, F, Ug, (T + gu_pos(S.sh_gate_type) - 1) / gu_pos(S.sh_gate_type), ss);
+      }
+      {
+        HookScope k(hook, "pf_quant_h_shared", ss);
+        pf_quant_rows<<<(T * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, ss>>>(b.h_sh, F, T, Ud, hs, b.hact_sh, 0,
+                                                                              nullptr);
+      }
+    } else {  // gate and up of different types: two plain GEMMs (the reference's two matvecs), SwiGLU in the quantiser
+      for (uint32_t m = 0; m < 2; m++) {
+        HookScope k(hook, m ? "pf_up_shared" : "pf_gate_shared", ss);
+        PfGemm q{};
+        q.shared_T = T, q.K = K, q.act = b.act_s, q.act_by_pos = 0;
+        q.mat = L.shared + (m ? L.sh_up_off : 0), q.stride = 0, q.out = m ? b.h_sh_up : b.h_sh, q.out_ld = F;
+        q.codebooks = L.codebooks;
+        launch_gemm<false>(m ? S.sh_up_type : S.sh_gate_type, Ug, dim3(st_tiles, F / gemm_rows<false>()), q, ss);
+      }
       HookScope k(hook, "pf_quant_h_shared", ss);
-      pf_quant_rows<<<(T * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, ss>>>(b.h_sh, F, T, Ud, hs, b.hact_sh, 0,
-                                                                            nullptr);
+      pf_quant_swiglu<<<(T * Ud + halfwaves - 1) / halfwaves, kPfWG, 0, ss>>>(b.h_sh, b.h_sh_up, F, T, Ud,
+                                                                              S.swiglu_limit, hs, b.hact_sh);
     }
     {
       HookScope k(hook, "pf_down_shared", ss);

@@ -30,6 +30,7 @@ struct PfShape {
   uint32_t H, F, E, K, T;
   uint32_t gate_type, down_type, sh_gate_type, sh_down_type, has_shared;
   float swiglu_limit;
+  uint32_t sh_up_type;  // the shared expert's up; when it is not sh_gate_type, gate and up run as two GEMMs
 };
 
 struct PfLayer {
@@ -53,6 +54,7 @@ struct PfBufs {
   uint32_t *ntiles;        // 1
   unsigned long long *masks;  // windows x E: the tokens of each 64-token window that chose each expert
   float *h, *h_sh;         // Tmax K x F (expert order), Tmax x F
+  float *h_sh_up;          // Tmax x F: the shared up's rows when its type differs from the gate's (h_sh holds gate's)
   uint8_t *hact, *hact_sh; // the same rows quantised, (F / 256) units each
   float *y_asg, *y_sh;     // Tmax K x H (expert order), Tmax x H
   // With a shared expert, the x quantiser and the shared expert's launches run on `side` (default priority), forked at

@@ -9,7 +9,7 @@
 namespace c0ven {
 
 // Row r's unit u in the file's layout: the bytes of its blocks (Q8_0: 8 blocks of 34 B; IQ4_NL: 8 of 18 B; Q2_0: 4
-// of 18 B; Q4_K, IQ3_S, IQ3_XXS, IQ2_S: one block).
+// of 18 B; the 256-value types: one block).
 inline const uint8_t *file_unit(const uint8_t *m, uint32_t type, uint32_t k, uint32_t r, uint32_t u) {
   const uint64_t row = (uint64_t)k / quant_block_values(type) * quant_block_bytes(type);
   return m + r * row + (uint64_t)u * unit_bytes(type);
@@ -47,6 +47,22 @@ inline void put_unit(uint8_t *tile, uint32_t type, uint32_t idx, uint32_t nl, co
       std::memcpy(at(iq2_st::kQh, 0, 8), b + 66, 8);
       std::memcpy(at(iq2_st::kScales, 0, 8), b + 74, 8);
       std::memcpy(at(iq2_st::kD, 0, 2), b, 2);
+      break;
+    case QT_IQ4_XS:
+      for (uint32_t p = 0; p < 8; p++) std::memcpy(at(iq4_xst::kQs, p, 16), b + 8 + 16 * p, 16);
+      std::memcpy(at(iq4_xst::kMeta, 0, 8), b, 8);
+      break;
+    case QT_Q5_K:
+      for (uint32_t p = 0; p < 8; p++) std::memcpy(at(q5_kt::kQs, p, 16), b + 48 + 16 * p, 16);
+      for (uint32_t p = 0; p < 2; p++) std::memcpy(at(q5_kt::kQh, p, 16), b + 16 + 16 * p, 16);
+      for (uint32_t i = 0; i < 3; i++) std::memcpy(at(q5_kt::kScales, i, 4), b + 4 + 4 * i, 4);
+      std::memcpy(at(q5_kt::kDm, 0, 4), b, 4);
+      break;
+    case QT_Q6_K:
+      for (uint32_t p = 0; p < 8; p++) std::memcpy(at(q6_kt::kQl, p, 16), b + 16 * p, 16);
+      for (uint32_t p = 0; p < 4; p++) std::memcpy(at(q6_kt::kQh, p, 16), b + 128 + 16 * p, 16);
+      std::memcpy(at(q6_kt::kScales, 0, 16), b + 192, 16);
+      std::memcpy(at(q6_kt::kD, 0, 2), b + 208, 2);
       break;
     case QT_IQ3_S:
       for (uint32_t p = 0; p < 4; p++) std::memcpy(at(iq3_st::kQs, p, 16), b + 2 + 16 * p, 16);

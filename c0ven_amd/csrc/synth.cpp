@@ -361,6 +361,117 @@ void quant_q2_0(const float *x, uint8_t *y, uint32_t n) {
   }
 }
 
+// Q5_K: Q4_K's scheme with 31 steps a sub-block; the fifth bit of each code goes to qh (bit j of byte l for value
+// 32 j + l). Valid blocks, not ggml's search.
+void quant_q5_K(const float *x, uint8_t *y, uint32_t n) {
+  for (uint32_t b = 0; b < n / 256; b++, x += 256, y += 176) {
+    float step[8], mins[8];
+    for (int j = 0; j < 8; j++) {
+      float lo = 0.0f, hi = 0.0f;
+      for (int i = 0; i < 32; i++) lo = std::min(lo, x[32 * j + i]), hi = std::max(hi, x[32 * j + i]);
+      mins[j] = -lo;
+      step[j] = (hi - lo) / 31.0f;
+    }
+    const float smax = *std::max_element(step, step + 8), mmax = *std::max_element(mins, mins + 8);
+    const uint16_t dh = fp16_bits(smax / 63.0f), mh = fp16_bits(mmax / 63.0f);
+    const float d = fp16_value(dh), dmin = fp16_value(mh);
+    int sc[8], m[8];
+    for (int j = 0; j < 8; j++) {
+      sc[j] = d > 0.0f ? std::clamp(nearest(step[j] / d), 0, 63) : 0;
+      m[j] = dmin > 0.0f ? std::clamp(nearest(mins[j] / dmin), 0, 63) : 0;
+      if (step[j] > 0.0f && sc[j] == 0) sc[j] = 1;
+    }
+    std::memset(y, 0, 176);
+    std::memcpy(y, &dh, 2);
+    std::memcpy(y + 2, &mh, 2);
+    uint8_t *s = y + 4;
+    for (int j = 0; j < 4; j++) {
+      s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+      s[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+      s[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+    }
+    uint8_t q[256];
+    for (int j = 0; j < 8; j++) {
+      const float dj = d * (float)sc[j], mj = dmin * (float)m[j];
+      for (int i = 0; i < 32; i++) q[32 * j + i] = dj > 0.0f ? (uint8_t)std::clamp(nearest((x[32 * j + i] + mj) / dj), 0, 31) : 0;
+    }
+    uint8_t *qh = y + 16, *qs = y + 48;
+    for (int v = 0; v < 256; v++) qh[v % 32] |= (uint8_t)(((q[v] >> 4) & 1) << (v / 32));
+    for (int c = 0; c < 4; c++)
+      for (int l = 0; l < 32; l++) qs[32 * c + l] = (uint8_t)((q[64 * c + l] & 15) | ((q[64 * c + 32 + l] & 15) << 4));
+  }
+}
+
+// Q6_K: per sub-block of 16 a step amax / 31 as d sc, d = the largest step / 127 (signed scales: the sub-block's
+// value of largest magnitude sets the sign, so that its code is -31); codes q - 32 = round(x / (d sc)), clamped.
+void quant_q6_K(const float *x, uint8_t *y, uint32_t n) {
+  for (uint32_t b = 0; b < n / 256; b++, x += 256, y += 210) {
+    float st[16];
+    for (int j = 0; j < 16; j++) {
+      float m = 0.0f;
+      for (int i = 0; i < 16; i++)
+        if (std::fabs(x[16 * j + i]) > std::fabs(m)) m = x[16 * j + i];
+      st[j] = m / -31.0f;
+    }
+    float amax = 0.0f;
+    for (int j = 0; j < 16; j++) amax = std::max(amax, std::fabs(st[j]));
+    const uint16_t dh = fp16_bits(amax / 127.0f);
+    const float d = fp16_value(dh);
+    std::memset(y, 0, 210);
+    int8_t *sc = (int8_t *)(y + 192);
+    uint8_t q[256];
+    for (int j = 0; j < 16; j++) {
+      sc[j] = (int8_t)(d > 0.0f ? std::clamp(nearest(st[j] / d), -127, 127) : 0);
+      const float dj = d * (float)sc[j];
+      for (int i = 0; i < 16; i++)
+        q[16 * j + i] = (uint8_t)(dj != 0.0f ? std::clamp(nearest(x[16 * j + i] / dj), -32, 31) + 32 : 32);
+    }
+    uint8_t *ql = y, *qh = y + 128;
+    for (int v = 0; v < 256; v++) {  // v = 128 h + 32 j + l
+      const int h = v / 128, j = (v % 128) / 32, l = v % 32;
+      ql[64 * h + 32 * (j % 2) + l] |= (uint8_t)((q[v] & 15) << (4 * (j / 2)));
+      qh[32 * h + l] |= (uint8_t)((q[v] >> 4) << (2 * j));
+    }
+    std::memcpy(y + 208, &dh, 2);
+  }
+}
+
+// IQ4_XS: per sub-block of 32 a step (the value of largest magnitude / -127, kvalues' first entry) as d (ls - 32),
+// d = the largest step's magnitude / 32 with the sign that lets ls - 32 reach -32; codes the nearest table entries.
+void quant_iq4_xs(const float *x, uint8_t *y, uint32_t n) {
+  for (uint32_t b = 0; b < n / 256; b++, x += 256, y += 136) {
+    float st[8], amax = 0.0f;
+    for (int j = 0; j < 8; j++) {
+      float m = 0.0f;
+      for (int i = 0; i < 32; i++)
+        if (std::fabs(x[32 * j + i]) > std::fabs(m)) m = x[32 * j + i];
+      st[j] = m / -127.0f;
+      amax = std::max(amax, std::fabs(st[j]));
+    }
+    const uint16_t dh = fp16_bits(-amax / 32.0f);
+    const float d = fp16_value(dh);
+    std::memset(y, 0, 136);
+    std::memcpy(y, &dh, 2);
+    uint16_t sh = 0;
+    for (int j = 0; j < 8; j++) {
+      const int ls = d != 0.0f ? std::clamp(nearest(st[j] / d), -32, 31) + 32 : 32;
+      y[4 + j / 2] |= (uint8_t)((ls & 15) << (4 * (j % 2)));
+      sh |= (uint16_t)(((ls >> 4) & 3) << (2 * j));
+      const float dl = d * (float)(ls - 32), id = dl != 0.0f ? 1.0f / dl : 0.0f;
+      uint8_t code[32];
+      for (int i = 0; i < 32; i++) {
+        const float v = x[32 * j + i] * id;
+        int best = 0;
+        for (int k = 1; k < 16; k++)
+          if (std::fabs(v - kIq4nl[k]) < std::fabs(v - kIq4nl[best])) best = k;
+        code[i] = (uint8_t)best;
+      }
+      for (int i = 0; i < 16; i++) y[8 + 16 * j + i] = (uint8_t)(code[i] | (code[i + 16] << 4));
+    }
+    std::memcpy(y + 2, &sh, 2);
+  }
+}
+
 // Whether a row of cols values is whole blocks of a GPU type (and, for the codebook types, the codebooks are set).
 bool cols_ok(uint32_t type, uint32_t cols) {
   const uint32_t bv = quant_block_values(type);
@@ -380,6 +491,9 @@ bool quant_rows(uint32_t type, const float *x, uint32_t cols, uint8_t *out) {
     case QT_Q2_0: quant_q2_0(x, out, cols); return true;
     case QT_IQ3_XXS: quant_iq3_xxs(x, out, cols); return true;
     case QT_IQ2_S: quant_iq2_s(x, out, cols); return true;
+    case QT_Q5_K: quant_q5_K(x, out, cols); return true;
+    case QT_Q6_K: quant_q6_K(x, out, cols); return true;
+    case QT_IQ4_XS: quant_iq4_xs(x, out, cols); return true;
     default: return false;
   }
 }

@@ -334,6 +334,143 @@ struct UnitQ2_0 : UnitQ8_0 {
   }
 };
 
+// IQ4_XS: eight sub-blocks of 32 with a 6-bit scale ls (4 bits in scales_l, 2 in scales_h), values d (ls - 32)
+// kvalues[nibble] (QUANT_FORMATS.md:213-232; vec_dot_iq4_xs_q8_K). Term: (d_w d_a) isum, isum = sum over sub-blocks
+// of (ls - 32) times the sub-block's exact dot.
+struct UnitIQ4_XS {
+  uint32_t q[64];  // sub-block p: words 8 p .. 8 p + 3 values 0-15 (low nibbles), 8 p + 4 .. values 16-31
+  int ls[8];
+  float d;
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl) {
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const uint4 v = *field<uint4>(tile, iq4_xst::kQs, p, idx, nl);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        q[8 * p + i] = iq4nl_lookup(w[i] & 0x0f0f0f0fu);
+        q[8 * p + 4 + i] = iq4nl_lookup((w[i] >> 4) & 0x0f0f0f0fu);
+      }
+    }
+    const uint2 m = *field<uint2>(tile, iq4_xst::kMeta, 0, idx, nl);  // d | scales_h << 16, scales_l
+    d = h2f((uint16_t)m.x);
+#pragma unroll
+    for (int b = 0; b < 8; b++)
+      ls[b] = (int)(((m.y >> (4 * b)) & 15u) | (((m.x >> (16 + 2 * b)) & 3u) << 4)) - 32;
+  }
+  __device__ __forceinline__ float term(const Act &a) const {
+    int bsum = 0;
+#pragma unroll
+    for (int ib = 0; ib < 8; ib++) {
+      uint32_t aw[8];
+      a.q8(ib, aw);
+      int s = 0;
+#pragma unroll
+      for (int k = 0; k < 8; k++) s = dot4(q[8 * ib + k], aw[k], s);
+      bsum += ls[ib] * s;
+    }
+    return __fmul_rn(__fmul_rn(d, a.scale0()), (float)bsum);
+  }
+};
+
+// Q5_K: Q4_K with a fifth bit per value from qh (bit k of byte l is bit 4 of value 32 k + l; QUANT_FORMATS.md:401-417,
+// vec_dot_q5_K_q8_K). The codes are 0..31 and the term is Q4_K's.
+struct UnitQ5_K : UnitQ4_K {
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl) {
+    uint32_t qh[8];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const uint4 v = *field<uint4>(tile, q5_kt::kQh, p, idx, nl);
+      qh[4 * p] = v.x, qh[4 * p + 1] = v.y, qh[4 * p + 2] = v.z, qh[4 * p + 3] = v.w;
+    }
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const uint4 v = *field<uint4>(tile, q5_kt::kQs, p, idx, nl);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {  // word 4 p + i: chunk c = p / 2, bytes 4 (w % 8) .. of it
+        const uint32_t wi = 4 * p + i, c = wi / 8, h = qh[wi % 8];
+        lo[wi] = (w[i] & 0x0f0f0f0fu) | (((h >> (2 * c)) & 0x01010101u) << 4);
+        hi[wi] = ((w[i] >> 4) & 0x0f0f0f0fu) | (((h >> (2 * c + 1)) & 0x01010101u) << 4);
+      }
+    }
+    uint8_t b[12];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const uint32_t v = *field<uint32_t>(tile, q5_kt::kScales, i, idx, nl);
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[4 * i + j] = (uint8_t)(v >> (8 * j));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {  // get_scale_min_k4
+      if (j < 4) {
+        sc[j] = b[j] & 63;
+        mn[j] = b[j + 4] & 63;
+      } else {
+        sc[j] = (b[j + 4] & 0xF) | ((b[j - 4] >> 6) << 4);
+        mn[j] = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
+      }
+    }
+    const uint32_t dm = *field<uint32_t>(tile, q5_kt::kDm, 0, idx, nl);
+    d = h2f((uint16_t)dm);
+    dmin = h2f((uint16_t)(dm >> 16));
+  }
+};
+
+// Four bytes of six-bit codes (0..63) less 32, as signed bytes: per byte (0x80 + c) - 32 has no borrow, then back.
+__device__ __forceinline__ uint32_t sub32_bytes(uint32_t c) { return ((c | 0x80808080u) - 0x20202020u) ^ 0x80808080u; }
+
+// The word (values 4 k .. 4 k + 3) of a Q6_K super-block from its ql and qh words (QUANT_FORMATS.md:419-445): value
+// v = 128 h + 32 j + l takes the nibble 4 (j / 2) of ql byte 64 h + 32 (j % 2) + l and bits 2 j of qh byte 32 h + l.
+__device__ __forceinline__ uint32_t q6k_word(const uint32_t *ql, const uint32_t *qh, uint32_t k) {
+  const uint32_t v = 4 * k, h = v / 128, j = (v % 128) / 32, l = v % 32;
+  const uint32_t lw = ql[(64 * h + 32 * (j % 2) + l) / 4], hw = qh[(32 * h + l) / 4];
+  return sub32_bytes(((lw >> (4 * (j / 2))) & 0x0f0f0f0fu) | (((hw >> (2 * j)) & 0x03030303u) << 4));
+}
+
+// Q6_K: sixteen sub-blocks of 16 with signed 8-bit scales, values d sc (q - 32) (vec_dot_q6_K_q8_K). Term:
+// (d_w d_a) isum, isum = sum over sub-blocks of sc times the sub-block's exact dot.
+struct UnitQ6_K {
+  uint32_t w[64];  // values 4 k .. 4 k + 3, signed
+  int sc[16];
+  float d;
+  __device__ __forceinline__ void load(const uint8_t *tile, uint32_t idx, uint32_t nl) {
+    uint32_t ql[32], qh[16];
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const uint4 v = *field<uint4>(tile, q6_kt::kQl, p, idx, nl);
+      ql[4 * p] = v.x, ql[4 * p + 1] = v.y, ql[4 * p + 2] = v.z, ql[4 * p + 3] = v.w;
+    }
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const uint4 v = *field<uint4>(tile, q6_kt::kQh, p, idx, nl);
+      qh[4 * p] = v.x, qh[4 * p + 1] = v.y, qh[4 * p + 2] = v.z, qh[4 * p + 3] = v.w;
+    }
+    const uint4 s = *field<uint4>(tile, q6_kt::kScales, 0, idx, nl);
+    const uint32_t sw[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int i = 0; i < 16; i++) sc[i] = (int)(int8_t)(sw[i / 4] >> (8 * (i % 4)));
+    d = h2f(*field<uint16_t>(tile, q6_kt::kD, 0, idx, nl));
+#pragma unroll
+    for (uint32_t k = 0; k < 64; k++) w[k] = q6k_word(ql, qh, k);
+  }
+  __device__ __forceinline__ float term(const Act &a) const {
+    int isum = 0;
+#pragma unroll
+    for (int ib = 0; ib < 8; ib++) {
+      uint32_t aw[8];
+      a.q8(ib, aw);
+      int s0 = 0, s1 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) s0 = dot4(w[8 * ib + k], aw[k], s0);
+#pragma unroll
+      for (int k = 4; k < 8; k++) s1 = dot4(w[8 * ib + k], aw[k], s1);
+      isum += sc[2 * ib] * s0 + sc[2 * ib + 1] * s1;
+    }
+    return __fmul_rn(__fmul_rn(d, a.scale0()), (float)isum);
+  }
+};
+
 // IQ4_NL and Q2_0 as UnitQ8_0 with the decode split from the loads: load_raw issues a unit's loads (IQ4_NL its 32
 // nibble words into q[0..31]; Q2_0 its 16 code words into q[0..15]; the f16 scale words into dw), and widen, once
 // they have arrived, decodes them in place exactly as UnitIQ4_NL::load / UnitQ2_0::load do. A caller that takes

@@ -52,11 +52,11 @@ typedef struct {
   uint32_t n_expert;     /* E routed experts, at most 512 */
   uint32_t n_used;       /* k, at most 16 */
   uint32_t n_layer;      /* layers held resident (default 1) */
-  uint32_t gate_type;    /* QT_Q8_0, QT_Q4_K, QT_IQ3_S, QT_IQ4_NL, QT_Q2_0, QT_IQ3_XXS or QT_IQ2_S: gate and up of
-                          * the routed experts (the last two need moe_set_codebooks) */
+  uint32_t gate_type;    /* QT_Q8_0, QT_Q4_K, QT_Q5_K, QT_Q6_K, QT_IQ3_S, QT_IQ4_NL, QT_IQ4_XS, QT_Q2_0, QT_IQ3_XXS or
+                          * QT_IQ2_S: gate and up of the routed experts (the last two need moe_set_codebooks) */
   uint32_t down_type;    /* the same set: down of the routed experts */
   uint32_t has_shared;   /* 1: one shared expert with a sigmoid gate (the router's row E) */
-  uint32_t sh_gate_type; /* the shared expert's types */
+  uint32_t sh_gate_type; /* the shared expert's gate (and up, unless sh_up_type says otherwise) */
   uint32_t sh_down_type;
   uint32_t max_tokens;   /* the most tokens one forward takes, at most 16384 (default 16) */
   float swiglu_limit;    /* > 0: gate = min(gate, L), up = clamp(up, -L, L) before the SiLU; 0 = off */
@@ -66,7 +66,11 @@ typedef struct {
                                 * 0: they are uploaded again on every call */
   uint32_t hc_lr;        /* > 0: the layers hold a hyper-connection mix and combine of this low rank (at most 512, a
                           * multiple of 8; the model's is 320) for moe_forward_hc */
-  uint32_t reserved[2];
+  uint32_t sh_up_type;   /* the shared expert's up, when it differs from its gate (0: sh_gate_type). The model file
+                          * mixes them per layer (blk.0: gate Q4_K, up IQ4_XS), as the reference runs the shared gate,
+                          * up and down as three matvecs of their own types (model.cpp:828-830). Gate and up must take
+                          * the same activation type, and may differ only among the types without a codebook. */
+  uint32_t reserved[1];
 } moe_config;
 
 /* The routing result of a forward, per token: k expert ids in rank order and their weights. */
@@ -94,7 +98,8 @@ MOE_API const char *moe_last_error(const moe_ctx *ctx);
  * (blk.N.ffn_gate_inp and ffn_gate_inp_shexp). bias: n_expert fp32 logit biases, or null for none. */
 MOE_API moe_status moe_load_router(moe_ctx *ctx, uint32_t layer, const uint16_t *router_bf16, const float *bias);
 /* One expert's three matrices in the file's layout (ggml blocks, row-major): gate and up n_ff x n_embd, down
- * n_embd x n_ff, of the context's types (expert == n_expert: the shared expert, of the shared types). The library
+ * n_embd x n_ff, of the context's types (expert == n_expert: the shared expert, of the shared types: gate
+ * sh_gate_type, up sh_up_type, down sh_down_type). The library
  * repacks them into its device layout; the caller's buffers are not kept. */
 MOE_API moe_status moe_load_expert(moe_ctx *ctx, uint32_t layer, uint32_t expert, const uint8_t *gate,
                                    const uint8_t *up, const uint8_t *down);
@@ -153,6 +158,10 @@ MOE_API moe_status moe_forward_experts(moe_ctx *ctx, const moe_job *jobs, uint32
 /* CpuExperts::h_rows (core/cpu/experts.h:52-56): the h rows one pass of the down kernels takes, 256 here (one unit;
  * the GPU path has no task split). 0 when n_ff is not a multiple of it. */
 MOE_API uint32_t moe_h_rows(const moe_config *cfg);
+/* Whether moe_open would accept cfg's shape and types (the checks it makes before it touches a device); the reason
+ * of a refusal is moe_last_error(null). No device is needed. No counterpart in the reference, whose loader checks a
+ * file's types as it reads them. */
+MOE_API moe_status moe_check_config(const moe_config *cfg);
 
 /* The dispatch of the last prefill forward (p_moe_count / scan / fill, prompt.cl:682-738): ntiles receives the number
  * of MoeTiles, tiles (room for cap) the tiles in expert order, perm (ntok x n_used, or null) the assignment
@@ -210,7 +219,7 @@ MOE_API moe_status moe_trace(moe_ctx *ctx, uint64_t *stamps, uint32_t cap, uint3
 /* Copies the resident experts (and shared expert) of src_layer over those of dst_layer, device to device. */
 MOE_API moe_status moe_copy_experts(moe_ctx *ctx, uint32_t src_layer, uint32_t dst_layer);
 /* Bytes of one resident matrix in the device layout: which = 0 routed gate (up is the same), 1 routed down,
- * 2 shared gate, 3 shared down. These are the weights' own bytes, the block's algorithmic traffic per matrix. */
+ * 2 shared gate, 3 shared down, 4 shared up. These are the weights' own bytes, the block's algorithmic traffic per matrix. */
 MOE_API moe_status moe_expert_bytes(const moe_ctx *ctx, uint32_t which, uint64_t *bytes);
 
 /* Device bytes the context holds: resident weights and scratch. */

@@ -3,10 +3,9 @@
  * Replaces the reference's shared/quant.h (ids :9-33, values per block :36-44, bytes per block :47-75, field tables
  * :78-166, run offsets :172-176, QUANT_FILE_PAD :180, codebook buffer offsets :189-196). The numeric values, the field
  * order (quants first, the f16 scales last) and the codebook buffer offsets are the same, so a caller that built
- * buffers for the reference's headers builds the same bytes for these. Only the seven types this block implements on
- * the GPU (Q8_0, Q4_K, IQ3_S, IQ4_NL, Q2_0, IQ3_XXS, IQ2_S) and the two activation types (q8_0, q8_K) carry field
- * tables; the other
- * ids are kept so that a caller's switch over them still compiles. C and HIP device code both include this header. */
+ * buffers for the reference's headers builds the same bytes for these. Only the ten types this block implements on
+ * the GPU (Q8_0, Q4_K, Q5_K, Q6_K, IQ3_S, IQ4_NL, IQ4_XS, Q2_0, IQ3_XXS, IQ2_S) and the two activation types (q8_0,
+ * q8_K) carry field tables; the other ids are kept so that a caller's switch over them still compiles. C and HIP device code both include this header. */
 #ifndef C0VEN_QUANT_H
 #define C0VEN_QUANT_H
 
@@ -92,8 +91,8 @@ C0VEN_FN uint32_t quant_block_bytes(uint32_t t) {
 
 /* Whether the GPU block implements a weight type. */
 C0VEN_FN int quant_gpu_supported(uint32_t t) {
-  return t == QT_Q8_0 || t == QT_Q4_K || t == QT_IQ3_S || t == QT_IQ4_NL || t == QT_Q2_0 || t == QT_IQ3_XXS ||
-         t == QT_IQ2_S;
+  return t == QT_Q8_0 || t == QT_Q4_K || t == QT_Q5_K || t == QT_Q6_K || t == QT_IQ3_S || t == QT_IQ4_NL ||
+         t == QT_IQ4_XS || t == QT_Q2_0 || t == QT_IQ3_XXS || t == QT_IQ2_S;
 }
 
 /* Whether a weight type decodes through a codebook the caller supplies (ggml-common.h's iq3xxs_grid and iq2s_grid,
@@ -106,7 +105,8 @@ C0VEN_FN int quant_needs_codebook(uint32_t t) { return t == QT_IQ3_XXS || t == Q
 C0VEN_FN uint32_t quant_vec_dot_type(uint32_t t) {
   switch (t) {
     case QT_Q8_0: case QT_IQ4_NL: case QT_Q2_0: return QT_Q8_0;
-    case QT_Q4_K: case QT_IQ3_S: case QT_IQ3_XXS: case QT_IQ2_S: return QT_Q8_K;
+    case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_IQ3_S: case QT_IQ4_XS: case QT_IQ3_XXS: case QT_IQ2_S:
+      return QT_Q8_K;
     default: return QT_F32;
   }
 }
@@ -115,6 +115,7 @@ C0VEN_FN uint32_t quant_vec_dot_type(uint32_t t) {
 C0VEN_FN uint32_t quant_nfields(uint32_t t) {
   switch (t) {
     case QT_IQ3_S: case QT_IQ2_S: return 5;
+    case QT_Q5_K: case QT_Q6_K: case QT_IQ4_XS: return 4;
     case QT_Q4_K: case QT_IQ3_XXS: return 3;
     case QT_Q8_0: case QT_IQ4_NL: case QT_Q2_0: return 2;
     case QT_Q8_K: return 3;
@@ -132,6 +133,12 @@ C0VEN_FN uint32_t quant_field_(uint32_t t, uint32_t f) {
                                                                                                 : (0u << 8) | 2;
     case QT_IQ3_XXS: /* grid indices, scale-and-sign words, d */
       return f == 0 ? (2u << 8) | 64 : f == 1 ? (66u << 8) | 32 : (0u << 8) | 2;
+    case QT_Q5_K: /* qs, qh, scales, d and dmin */
+      return f == 0 ? (48u << 8) | 128 : f == 1 ? (16u << 8) | 32 : f == 2 ? (4u << 8) | 12 : (0u << 8) | 4;
+    case QT_Q6_K: /* ql, qh, scales, d (the file already has the f16 scale last) */
+      return f == 0 ? (0u << 8) | 128 : f == 1 ? (128u << 8) | 64 : f == 2 ? (192u << 8) | 16 : (208u << 8) | 2;
+    case QT_IQ4_XS: /* qs, scales_l, scales_h, d */
+      return f == 0 ? (8u << 8) | 128 : f == 1 ? (4u << 8) | 4 : f == 2 ? (2u << 8) | 2 : (0u << 8) | 2;
     case QT_Q4_K: /* qs, scales, d and dmin */
       return f == 0 ? (16u << 8) | 128 : f == 1 ? (4u << 8) | 12 : (0u << 8) | 4;
     case QT_Q8_0: /* qs, d */

@@ -238,6 +238,7 @@ static int fast_compute_many(const orc_shape *s, const orc_job *jobs, uint32_t n
   for (uint32_t t = 0; t < ntok; t++) memset(y + t * y_stride, 0, sizeof(float) * E);
   if (njobs == 0) return 0;
   if (E % QK || F % QK) return -1;
+  if (s->up_type && s->up_type != s->gate_type) return -1;
   for (int m = 0; m < 2; m++) { /* the config types: Q8_0, Q4_K, IQ3_S */
     const uint32_t t = m ? s->down_type : s->gate_type;
     if (t != QT_Q8_0 && t != QT_Q4_K && t != QT_IQ3_S) return -1;
@@ -397,14 +398,14 @@ int orc_fast_moe_forward(const orc_layer *L, const float *x, uint32_t ntok, uint
       j->gate = L->gate[e], j->up = L->up[e], j->down = L->down[e];
       j->tok = t, j->w = w[t * k + r];
     }
-  orc_shape sh = {L->gate_type, L->down_type, H, L->n_ff, L->swiglu_limit};
+  orc_shape sh = {L->gate_type, L->down_type, H, L->n_ff, L->swiglu_limit, 0};
   rc = fast_compute_many(&sh, jobs, ntok * k, ntok, x, x_stride, y, y_stride, nthreads);
   if (!rc && L->sh_gate) {
     for (uint32_t t = 0; t < ntok; t++) {
       jobs[t].gate = L->sh_gate, jobs[t].up = L->sh_up, jobs[t].down = L->sh_down;
       jobs[t].tok = t, jobs[t].w = 1.0f;
     }
-    orc_shape ss = {L->sh_gate_type, L->sh_down_type, H, L->n_ff, L->swiglu_limit};
+    orc_shape ss = {L->sh_gate_type, L->sh_down_type, H, L->n_ff, L->swiglu_limit, L->sh_up_type};
     rc = fast_compute_many(&ss, jobs, ntok, ntok, x, x_stride, s, H, nthreads);
     if (!rc)
       for (uint32_t t = 0; t < ntok; t++) {

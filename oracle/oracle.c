@@ -16,6 +16,9 @@
 #define QT_Q2_0 42
 #define QT_IQ3_XXS 18
 #define QT_IQ2_S 22
+#define QT_Q5_K 13
+#define QT_Q6_K 14
+#define QT_IQ4_XS 23
 #define QGRID_IQ2S 0
 #define QGRID_IQ3XXS 8192
 #define QK 256
@@ -175,6 +178,36 @@ static inline void iq3s_value(const uint8_t *b, int v, int *mag, int *neg, int *
   *ls = 1 + 2 * ((scales[ib / 2] >> (4 * (ib % 2))) & 15);
 }
 
+/* Q5_K value v's code 0..31: the Q4_K nibble (chunk v / 64: byte v % 32 of it, high nibble for the second 32) and
+ * bit v / 32 of qh byte v % 32 as bit 4 (QUANT_FORMATS.md:405-411). */
+static inline int q5k_code(const uint8_t *b, int v) {
+  const uint8_t *qs = b + 48, *qh = b + 16;
+  const int c = v / 64, l = v % 32, hi = (v % 64) / 32;
+  const int q4 = hi ? qs[32 * c + l] >> 4 : qs[32 * c + l] & 15;
+  return q4 | (((qh[l] >> (v / 32)) & 1) << 4);
+}
+
+/* Q6_K value v's code less 32, by the table of QUANT_FORMATS.md:433-441: h = v / 128, j = (v % 128) / 32, l = v % 32;
+ * the low four bits are nibble j / 2 of ql[64 h + 32 (j % 2) + l], the high two bits 2 j of qh[32 h + l]. */
+static inline int q6k_code(const uint8_t *b, int v) {
+  const int h = v / 128, j = (v % 128) / 32, l = v % 32;
+  const int lo = (b[64 * h + 32 * (j % 2) + l] >> (4 * (j / 2))) & 15;
+  const int hi = (b[128 + 32 * h + l] >> (2 * j)) & 3;
+  return (lo | (hi << 4)) - 32;
+}
+
+/* IQ4_XS sub-block ib's scale less 32: bits 0-3 from scales_l byte ib / 2 (low nibble for even ib), bits 4-5 from
+ * bits 2 ib of scales_h (QUANT_FORMATS.md:217-224). */
+static inline int iq4xs_scale(const uint8_t *b, int ib) {
+  const int lo = (b[4 + ib / 2] >> (4 * (ib % 2))) & 15, hi = (rd16(b + 2) >> (2 * ib)) & 3;
+  return (lo | (hi << 4)) - 32;
+}
+/* IQ4_XS value v's nibble: byte 16 (v / 32) + v % 16 of qs, low nibble for v % 32 < 16. */
+static inline int iq4xs_nibble(const uint8_t *b, int v) {
+  const uint8_t q = b[8 + 16 * (v / 32) + v % 16];
+  return (v % 32) < 16 ? q & 15 : q >> 4;
+}
+
 int orc_dequantize_row(uint32_t type, const void *src, float *dst, int64_t n) {
   const uint8_t *b = (const uint8_t *)src;
   grid_init();
@@ -230,6 +263,35 @@ int orc_dequantize_row(uint32_t type, const void *src, float *dst, int64_t n) {
       for (int64_t i = 0; i < n / 64; i++, b += 18) {
         const float d = orc_fp16_to_fp32(rd16(b));
         for (int j = 0; j < 64; j++) dst[64 * i + j] = (float)((int)((b[2 + j / 4] >> (2 * (j % 4))) & 3) - 1) * d;
+      }
+      return 0;
+    case QT_Q5_K: /* y = (d sc) (q4 + 16 h) - (dmin m) (QUANT_FORMATS.md:401-417, quants.c:1731-1756) */
+      if (n % QK) return -1;
+      for (int64_t i = 0; i < n / QK; i++, b += 176) {
+        const float d = orc_fp16_to_fp32(rd16(b)), dmin = orc_fp16_to_fp32(rd16(b + 2));
+        for (int v = 0; v < QK; v++) {
+          int sc, m;
+          scale_min_k4(v / 32, b + 4, &sc, &m);
+          const float dl = d * (float)sc, ml = dmin * (float)m;
+          dst[QK * i + v] = dl * (float)q5k_code(b, v) - ml;
+        }
+      }
+      return 0;
+    case QT_Q6_K: /* y = (d sc[v / 16]) (q - 32) (QUANT_FORMATS.md:419-445, quants.c:1939-1968) */
+      if (n % QK) return -1;
+      for (int64_t i = 0; i < n / QK; i++, b += 210) {
+        const float d = orc_fp16_to_fp32(rd16(b + 208));
+        for (int v = 0; v < QK; v++) dst[QK * i + v] = d * (float)(int8_t)b[192 + v / 16] * (float)q6k_code(b, v);
+      }
+      return 0;
+    case QT_IQ4_XS: /* y = (d (ls - 32)) kvalues[nibble] (QUANT_FORMATS.md:213-232, quants.c:2743-2764) */
+      if (n % QK) return -1;
+      for (int64_t i = 0; i < n / QK; i++, b += 136) {
+        const float d = orc_fp16_to_fp32(rd16(b));
+        for (int v = 0; v < QK; v++) {
+          const float dl = d * (float)iq4xs_scale(b, v / 32);
+          dst[QK * i + v] = dl * (float)kIq4nl[iq4xs_nibble(b, v)];
+        }
       }
       return 0;
     case QT_IQ3_XXS: /* y = ((d (0.5 + s)) 0.5) grid sign (quants.c:2575-2603) */
@@ -328,7 +390,11 @@ int orc_quantize_act(uint32_t act_type, const float *src, void *dst, int64_t n) 
 /* The 32-value block types: q8_0 activations (ggml-cpu.c vec_dot_type: Q8_0, IQ4_NL :380, Q2_0 :234). */
 static int q8_family(uint32_t t) { return t == QT_Q8_0 || t == QT_IQ4_NL || t == QT_Q2_0; }
 static uint32_t act_type_of(uint32_t t) {
-  return q8_family(t) ? QT_Q8_0 : (t == QT_Q4_K || t == QT_IQ3_S || t == QT_IQ3_XXS || t == QT_IQ2_S) ? QT_Q8_K : 0;
+  return q8_family(t) ? QT_Q8_0
+         : (t == QT_Q4_K || t == QT_Q5_K || t == QT_Q6_K || t == QT_IQ3_S || t == QT_IQ4_XS || t == QT_IQ3_XXS ||
+            t == QT_IQ2_S)
+             ? QT_Q8_K
+             : 0;
 }
 static uint64_t act_bytes(uint32_t act, uint64_t n) { return act == QT_Q8_0 ? n / 32 * 34 : n / QK * 292; }
 static uint64_t row_bytes(uint32_t t, uint64_t n) {
@@ -339,6 +405,9 @@ static uint64_t row_bytes(uint32_t t, uint64_t n) {
          : t == QT_IQ3_S  ? n / QK * 110
          : t == QT_IQ3_XXS ? n / QK * 98
          : t == QT_IQ2_S  ? n / QK * 82
+         : t == QT_IQ4_XS ? n / QK * 136
+         : t == QT_Q5_K   ? n / QK * 176
+         : t == QT_Q6_K   ? n / QK * 210
                           : 0;
 }
 /* The values a row's length must be a multiple of: the type's block. */
@@ -471,6 +540,59 @@ static float term_iq2_s(const uint8_t *w, const uint8_t *a) {
   return 0.125f * (d * (float)isum);
 }
 
+/* Q5_K x q8_K (vec_dot_q5_K_q8_K): Q4_K's term with the five-bit codes. */
+static float term_q5_K(const uint8_t *w, const uint8_t *a) {
+  float ad;
+  memcpy(&ad, a, 4);
+  const int8_t *q8 = (const int8_t *)(a + 4);
+  int16_t bs[16];
+  memcpy(bs, a + 260, 32);
+  int32_t isum = 0, imin = 0;
+  for (int j = 0; j < 8; j++) {
+    int sc, m;
+    scale_min_k4(j, w + 4, &sc, &m);
+    int32_t dot = 0;
+    for (int l = 0; l < 32; l++) dot += q5k_code(w, 32 * j + l) * q8[32 * j + l];
+    isum += sc * dot;
+    imin += m * (bs[2 * j] + bs[2 * j + 1]);
+  }
+  const float d = orc_fp16_to_fp32(rd16(w)) * ad, dm = orc_fp16_to_fp32(rd16(w + 2)) * ad;
+  const float pm = dm * (float)imin;
+  return fmaf(d, (float)isum, -pm);
+}
+
+/* Q6_K x q8_K (vec_dot_q6_K_q8_K, QUANT_FORMATS.md:443-445): per sub-block of 16 its signed scale times the exact
+ * dot of (q - 32) with q_a, summed as an integer, then (d_w d_a) isum. */
+static float term_q6_K(const uint8_t *w, const uint8_t *a) {
+  float ad;
+  memcpy(&ad, a, 4);
+  const int8_t *q8 = (const int8_t *)(a + 4);
+  int32_t isum = 0;
+  for (int s = 0; s < 16; s++) {
+    int32_t dot = 0;
+    for (int l = 0; l < 16; l++) dot += q6k_code(w, 16 * s + l) * q8[16 * s + l];
+    isum += (int32_t)(int8_t)w[192 + s] * dot;
+  }
+  const float d = orc_fp16_to_fp32(rd16(w + 208)) * ad;
+  return d * (float)isum;
+}
+
+/* IQ4_XS x q8_K (vec_dot_iq4_xs_q8_K, QUANT_FORMATS.md:230-232): per sub-block (ls - 32) times the exact dot of
+ * kvalues[nibble] with q_a, summed as an integer, then (d_w d_a) isum. */
+static float term_iq4_xs(const uint8_t *w, const uint8_t *a) {
+  float ad;
+  memcpy(&ad, a, 4);
+  const int8_t *q8 = (const int8_t *)(a + 4);
+  int32_t isum = 0;
+  for (int ib = 0; ib < 8; ib++) {
+    int32_t dot = 0;
+    for (int l = 0; l < 32; l++) dot += kIq4nl[iq4xs_nibble(w, 32 * ib + l)] * q8[32 * ib + l];
+    isum += iq4xs_scale(w, ib) * dot;
+  }
+  const float d = orc_fp16_to_fp32(rd16(w)) * ad;
+  return d * (float)isum;
+}
+
 static float dot_row(uint32_t type, int64_t n, const uint8_t *w, const uint8_t *a, float *terms) {
   int64_t nb;
   switch (type) {
@@ -497,6 +619,18 @@ static float dot_row(uint32_t type, int64_t n, const uint8_t *w, const uint8_t *
     case QT_IQ2_S:
       nb = n / QK;
       for (int64_t i = 0; i < nb; i++) terms[i] = term_iq2_s(w + 82 * i, a + 292 * i);
+      break;
+    case QT_Q5_K:
+      nb = n / QK;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_q5_K(w + 176 * i, a + 292 * i);
+      break;
+    case QT_Q6_K:
+      nb = n / QK;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_q6_K(w + 210 * i, a + 292 * i);
+      break;
+    case QT_IQ4_XS:
+      nb = n / QK;
+      for (int64_t i = 0; i < nb; i++) terms[i] = term_iq4_xs(w + 136 * i, a + 292 * i);
       break;
     default:
       nb = n / QK;
@@ -533,6 +667,7 @@ static inline float swiglu_one(float g, float u, float limit) {
 static int shape_ok(const orc_shape *s) {
   const uint32_t ga = act_type_of(s->gate_type), da = act_type_of(s->down_type);
   if (!ga || !da || !s->n_embd || !s->n_ff) return 0;
+  if (s->up_type && act_type_of(s->up_type) != ga) return 0;  /* gate and up read one quantised x */
   if (s->n_embd % row_block(s->gate_type) || s->n_ff % row_block(s->down_type)) return 0;
   return 1;
 }
@@ -558,7 +693,8 @@ int orc_compute_many(const orc_shape *s, const orc_job *jobs, uint32_t njobs, ui
   if (nthreads <= 0) nthreads = 1;
   const uint32_t ga = act_type_of(s->gate_type), da = act_type_of(s->down_type);
   const uint64_t xq_bytes = act_bytes(ga, E), hq_bytes = act_bytes(da, F);
-  const uint64_t grow = row_bytes(s->gate_type, E), drow = row_bytes(s->down_type, F);
+  const uint32_t ut = s->up_type ? s->up_type : s->gate_type;
+  const uint64_t grow = row_bytes(s->gate_type, E), urow = row_bytes(ut, E), drow = row_bytes(s->down_type, F);
   const uint32_t nterm = (E > F ? E : F) / 32;
   uint8_t *xq = (uint8_t *)malloc(ntok * xq_bytes);
   uint8_t *hq = (uint8_t *)malloc(njobs * hq_bytes);
@@ -596,7 +732,7 @@ int orc_compute_many(const orc_shape *s, const orc_job *jobs, uint32_t njobs, ui
         const orc_job *jb = &jobs[dj[i]];
         const uint8_t *xa = xq + jb->tok * xq_bytes;
         const float g = dot_row(s->gate_type, E, jb->gate + r * grow, xa, terms);
-        const float u = dot_row(s->gate_type, E, jb->up + r * grow, xa, terms);
+        const float u = dot_row(ut, E, jb->up + r * urow, xa, terms);
         h[(uint64_t)dj[i] * F + r] = swiglu_one(g, u, s->swiglu_limit);
       }
     }
@@ -733,14 +869,14 @@ int orc_moe_forward(const orc_layer *L, const float *x, uint32_t ntok, uint64_t 
       j->gate = L->gate[e], j->up = L->up[e], j->down = L->down[e];
       j->tok = t, j->w = w[t * k + r];
     }
-  orc_shape sh = {L->gate_type, L->down_type, H, L->n_ff, L->swiglu_limit};
+  orc_shape sh = {L->gate_type, L->down_type, H, L->n_ff, L->swiglu_limit, 0};
   rc = orc_compute_many(&sh, jobs, ntok * k, ntok, x, x_stride, y, y_stride, nthreads);
   if (rc || !L->sh_gate) goto done;
   for (uint32_t t = 0; t < ntok; t++) {
     jobs[t].gate = L->sh_gate, jobs[t].up = L->sh_up, jobs[t].down = L->sh_down;
     jobs[t].tok = t, jobs[t].w = 1.0f;
   }
-  orc_shape ss = {L->sh_gate_type, L->sh_down_type, H, L->n_ff, L->swiglu_limit};
+  orc_shape ss = {L->sh_gate_type, L->sh_down_type, H, L->n_ff, L->swiglu_limit, L->sh_up_type};
   rc = orc_compute_many(&ss, jobs, ntok, ntok, x, x_stride, s, H, nthreads);
   if (rc) goto done;
   for (uint32_t t = 0; t < ntok; t++) {

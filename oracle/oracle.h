@@ -2,8 +2,9 @@
  * bench.py's cpu_baseline leg load it, as the checker; the product (c0ven_amd/) never links or calls it.
  *
  * A plain-C restatement of the reference's CPU expert path and of the block around it:
- *   - the weight decoders (ggml's dequantize_row_q8_0 / _q4_K / _iq3_s / _iq4_nl / _q2_0 / _iq3_xxs / _iq2_s, as
- *     docs/spec/QUANT_FORMATS.md:176-212, :373-400, :447-466, :234-246, :251-270, :147-168, :115-137 state them;
+ *   - the weight decoders (ggml's dequantize_row_q8_0 / _q4_K / _q5_K / _q6_K / _iq3_s / _iq4_nl / _iq4_xs / _q2_0 /
+ *     _iq3_xxs / _iq2_s, as docs/spec/QUANT_FORMATS.md:176-212, :373-400, :401-417, :419-445, :447-466, :234-246,
+ *     :213-232, :251-270, :147-168, :115-137 state them;
  *     the last two through codebooks the caller supplies, as ggml-common.h is absent);
  *   - the activation quantisers the CPU path converts x and h with (q8_0, QUANT_FORMATS.md:463-465; q8_K,
  *     :528-535), chosen per weight type as core/cpu/experts.cpp:114-123 does (ggml's vec_dot_type);
@@ -42,10 +43,11 @@ extern "C" {
  *   - a row adds its units in sequence, from 0.0f: acc = acc + unit_u, u ascending. */
 
 typedef struct {
-  uint32_t gate_type, down_type; /* QT_* of gate and up (always one type), and of down */
+  uint32_t gate_type, down_type; /* QT_* of gate (and of up unless up_type says otherwise), and of down */
   uint32_t n_embd;               /* K of gate and up, rows of down */
   uint32_t n_ff;                 /* rows of gate and up, K of down */
   float swiglu_limit;            /* > 0: gate = min(gate, L), up = clamp(up, -L, L) before the SiLU */
+  uint32_t up_type;              /* up's type when it is not gate_type (0: gate_type); same activation type */
 } orc_shape;
 
 typedef struct {
@@ -63,6 +65,7 @@ typedef struct {
   const float *bias;                   /* n_expert logit biases, or null */
   const uint8_t *const *gate, *const *up, *const *down; /* n_expert pointers each, file layout */
   const uint8_t *sh_gate, *sh_up, *sh_down;             /* null: no shared expert */
+  uint32_t sh_up_type;                 /* the shared up's type when it is not sh_gate_type (0: the same) */
 } orc_layer;
 
 /* Scalars. */

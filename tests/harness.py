@@ -55,7 +55,7 @@ oracle = _load_oracle()
 
 class OrcShape(C.Structure):
     _fields_ = [("gate_type", C.c_uint32), ("down_type", C.c_uint32), ("n_embd", C.c_uint32),
-                ("n_ff", C.c_uint32), ("swiglu_limit", C.c_float)]
+                ("n_ff", C.c_uint32), ("swiglu_limit", C.c_float), ("up_type", C.c_uint32)]
 
 
 class OrcJob(C.Structure):
@@ -67,7 +67,7 @@ class OrcLayer(C.Structure):
                 ("gate_type", C.c_uint32), ("down_type", C.c_uint32), ("sh_gate_type", C.c_uint32),
                 ("sh_down_type", C.c_uint32), ("swiglu_limit", C.c_float), ("router", _P), ("bias", _P),
                 ("gate", C.POINTER(_P)), ("up", C.POINTER(_P)), ("down", C.POINTER(_P)),
-                ("sh_gate", _P), ("sh_up", _P), ("sh_down", _P)]
+                ("sh_gate", _P), ("sh_up", _P), ("sh_down", _P), ("sh_up_type", C.c_uint32)]
 
 
 def ptr(a):
@@ -163,10 +163,12 @@ class Layer:
     layer * 2^20 + 4 e + {0, 1, 2}; the shared expert is e = n_expert."""
 
     def __init__(self, H, F, E, K, gate_type, down_type, sh_gate_type=None, sh_down_type=None, has_shared=True,
-                 seed=1234, layer=0, sigma=0.02, zipf=None, swiglu_limit=0.0, experts=None, nthreads=0):
+                 seed=1234, layer=0, sigma=0.02, zipf=None, swiglu_limit=0.0, experts=None, nthreads=0,
+                 sh_up_type=None):
         self.H, self.F, self.E, self.K = H, F, E, K
         self.gate_type, self.down_type = gate_type, down_type
         self.sh_gate_type = gate_type if sh_gate_type is None else sh_gate_type
+        self.sh_up_type = self.sh_gate_type if sh_up_type is None else sh_up_type
         self.sh_down_type = down_type if sh_down_type is None else sh_down_type
         self.has_shared, self.seed, self.layer, self.swiglu_limit = has_shared, seed, layer, swiglu_limit
         base = layer << 20
@@ -177,17 +179,18 @@ class Layer:
         wanted = range(E) if experts is None else experts
         for e in wanted:
             self.experts[e] = self._expert(e, gate_type, down_type, sigma, nthreads)
-        self.shared = self._expert(E, self.sh_gate_type, self.sh_down_type, sigma, nthreads) if has_shared else None
+        self.shared = (self._expert(E, self.sh_gate_type, self.sh_down_type, sigma, nthreads, self.sh_up_type)
+                       if has_shared else None)
 
-    def _expert(self, e, gt, dt, sigma, nthreads):
+    def _expert(self, e, gt, dt, sigma, nthreads, ut=None):
         s = (self.layer << 20) + 4 * e
         H, F = self.H, self.F
         return (moe.synth_matrix(self.seed, s, gt, F, H, sigma, nthreads),
-                moe.synth_matrix(self.seed, s + 1, gt, F, H, sigma, nthreads),
+                moe.synth_matrix(self.seed, s + 1, gt if ut is None else ut, F, H, sigma, nthreads),
                 moe.synth_matrix(self.seed, s + 2, dt, H, F, sigma, nthreads))
 
     def upload(self, blk, layer=0):
-        if {self.gate_type, self.down_type, self.sh_gate_type, self.sh_down_type} & set(moe.CODEBOOK_TYPES):
+        if {self.gate_type, self.down_type, self.sh_gate_type, self.sh_up_type, self.sh_down_type} & set(moe.CODEBOOK_TYPES):
             blk.set_codebooks(CODEBOOKS)
         blk.load_router(layer, self.router, self.bias)
         for e, (g, u, d) in self.experts.items():
@@ -198,7 +201,7 @@ class Layer:
     def block(self, n_layer=1, max_tokens=16, device=0):
         return moe.MoeBlock(self.H, self.F, self.E, self.K, self.gate_type, self.down_type, self.has_shared,
                             self.sh_gate_type, self.sh_down_type, n_layer=n_layer, max_tokens=max_tokens,
-                            swiglu_limit=self.swiglu_limit, device=device)
+                            swiglu_limit=self.swiglu_limit, device=device, sh_up_type=self.sh_up_type)
 
     def oracle_forward(self, x, nthreads=8):
         """The whole block on the CPU oracle: y, ids, w."""
@@ -219,7 +222,8 @@ class Layer:
         del arr
         L = OrcLayer(self.H, self.F, E, self.K, self.gate_type, self.down_type, self.sh_gate_type, self.sh_down_type,
                      self.swiglu_limit, ptr(self.router), ptr(self.bias), gp, up, dp,
-                     *(ptr(m) for m in (self.shared if self.shared is not None else (None, None, None))))
+                     *(ptr(m) for m in (self.shared if self.shared is not None else (None, None, None))),
+                     self.sh_up_type)
         y = np.empty((T, self.H), dtype=np.float32)
         ids = np.empty((T, self.K), dtype=np.int32)
         w = np.empty((T, self.K), dtype=np.float32)
@@ -235,7 +239,8 @@ class Layer:
             gp[e], up[e], dp[e] = g.ctypes.data, u.ctypes.data, d.ctypes.data
         L = OrcLayer(self.H, self.F, E, self.K, self.gate_type, self.down_type, self.sh_gate_type, self.sh_down_type,
                      self.swiglu_limit, ptr(self.router), ptr(self.bias), gp, up, dp,
-                     *(ptr(m) for m in (self.shared if self.shared is not None else (None, None, None))))
+                     *(ptr(m) for m in (self.shared if self.shared is not None else (None, None, None))),
+                     self.sh_up_type)
         return L, (gp, up, dp)
 
     def oracle_route(self, x):

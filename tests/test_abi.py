@@ -110,7 +110,8 @@ def test_synth_is_deterministic_and_thread_count_free():
 
 @pytest.mark.parametrize("qtype, tol", [(moe.QT_Q8_0, 0.0), (moe.QT_Q4_K, 0.2), (moe.QT_IQ3_S, 0.35),
                                         (moe.QT_IQ4_NL, 0.1), (moe.QT_Q2_0, 0.5), (moe.QT_IQ3_XXS, 0.35),
-                                        (moe.QT_IQ2_S, 0.45)])
+                                        (moe.QT_IQ2_S, 0.45), (moe.QT_Q5_K, 0.1), (moe.QT_Q6_K, 0.06),
+                                        (moe.QT_IQ4_XS, 0.15)])
 def test_quantisers_write_valid_blocks(qtype, tol):
     """Q8_0 is ggml's reference rule, so each value is within half a step of its code; the others are bounded in
     relative L2 (their exact choice of codes is this library's, not ggml's search)."""

@@ -28,18 +28,21 @@ def write_block(path, L, blk):
           (pre + "ffn_up_exps.weight", L.gate_type, (H, F, E), np.concatenate([L.experts[e][1] for e in range(E)])),
           (pre + "ffn_down_exps.weight", L.down_type, (F, H, E), np.concatenate([L.experts[e][2] for e in range(E)])),
           (pre + "ffn_gate_shexp.weight", L.sh_gate_type, (H, F), L.shared[0]),
-          (pre + "ffn_up_shexp.weight", L.sh_gate_type, (H, F), L.shared[1]),
+          (pre + "ffn_up_shexp.weight", L.sh_up_type, (H, F), L.shared[1]),
           (pre + "ffn_down_shexp.weight", L.sh_down_type, (F, H), L.shared[2]),
           ("output_norm.weight", 0, (H,), np.zeros(4 * H, np.uint8))]
     gw.write(path, [("general.architecture", gw.STRING, "qwen4exp"), ("qwen4exp.expert_count", gw.U32, E)], ts)
 
 
-@pytest.mark.parametrize("types", [(moe.QT_IQ3_XXS, moe.QT_IQ4_NL, moe.QT_Q4_K, moe.QT_IQ4_NL),
-                                   (moe.QT_Q4_K, moe.QT_Q8_0, moe.QT_Q8_0, moe.QT_Q8_0)])
+@pytest.mark.parametrize("types", [(moe.QT_IQ3_XXS, moe.QT_IQ4_NL, moe.QT_Q4_K, moe.QT_IQ4_NL, moe.QT_IQ4_XS),
+                                   (moe.QT_Q4_K, moe.QT_Q8_0, moe.QT_Q8_0, moe.QT_Q8_0, moe.QT_Q8_0),
+                                   (moe.QT_IQ4_XS, moe.QT_IQ4_NL, moe.QT_Q4_K, moe.QT_Q8_0, moe.QT_Q5_K)])
 def test_load_layer_from_gguf(tmp_path, types):
-    gt, dt, sgt, sdt = types
+    """(routed gate/up, routed down, shared gate, shared down, shared up): the first is the file's blk.0 (shared gate
+    Q4_K, up IQ4_XS), the last its blk.47 (routed IQ4_XS, shared down Q8_0, up Q5_K)."""
+    gt, dt, sgt, sdt, sut = types
     say("load_layer_gguf", [moe.TYPE_NAMES[t] for t in types])
-    L = h.Layer(2560, 640, 32, 8, gt, dt, sgt, sdt, seed=31)
+    L = h.Layer(2560, 640, 32, 8, gt, dt, sgt, sdt, seed=31, sh_up_type=sut)
     path = str(tmp_path / "block.gguf")
     write_block(path, L, 5)
     g = moe.GgufFile(path)
@@ -55,7 +58,13 @@ def test_load_layer_from_gguf(tmp_path, types):
     with pytest.raises(moe.MoeError):  # no block 4 in the file
         blk.load_layer_gguf(0, g, 4)
     blk.close()
-    other = moe.MoeBlock(2560, 640, 32, 8, moe.QT_IQ3_S, dt, True, sgt, sdt)  # gate type differs from the file's
+    other = moe.MoeBlock(2560, 640, 32, 8, moe.QT_IQ3_S, dt, True, sgt, sdt, sh_up_type=sut)  # gate type differs
+    with pytest.raises(moe.MoeError):
+        other.load_layer_gguf(0, g, 5)
+    other.close()
+    other = moe.MoeBlock(2560, 640, 32, 8, gt, dt, True, sgt, sdt, sh_up_type=sgt if sut != sgt else moe.QT_IQ4_NL)
+    if gt in moe.CODEBOOK_TYPES:
+        other.set_codebooks(h.CODEBOOKS)
     with pytest.raises(moe.MoeError):
         other.load_layer_gguf(0, g, 5)
     other.close()

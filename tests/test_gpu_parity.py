@@ -36,7 +36,8 @@ def random_blocks(qtype, nblocks):
     b = rng.integers(0, 256, size=(nblocks, nb), dtype=np.uint8)
     reach = {moe.QT_Q8_0: [(0, 128)], moe.QT_Q4_K: [(0, 63 * 15), (2, 63)], moe.QT_IQ3_S: [(0, 31 * 15)],
              moe.QT_IQ4_NL: [(0, 127)], moe.QT_Q2_0: [(0, 2)], moe.QT_IQ3_XXS: [(0, 62 * 31)],
-             moe.QT_IQ2_S: [(0, 43 * 31)]}[qtype]
+             moe.QT_IQ2_S: [(0, 43 * 31)], moe.QT_Q5_K: [(0, 63 * 31), (2, 63)], moe.QT_Q6_K: [(208, 127 * 32)],
+             moe.QT_IQ4_XS: [(0, 31 * 127)]}[qtype]
     for k in range(nblocks):
         for off, r in reach:
             v = np.ldexp(1.0 + rng.integers(0, 1024) / 1024.0, int(rng.integers(0, 3)) - 5) / r
@@ -53,7 +54,7 @@ def tiny_block():
 
 
 @pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q2_0, moe.QT_IQ3_XXS,
-                                   moe.QT_IQ2_S])
+                                   moe.QT_IQ2_S, moe.QT_Q5_K, moe.QT_Q6_K, moe.QT_IQ4_XS])
 @pytest.mark.parametrize("rows,cols", [(128, 512), (100, 256)])
 def test_dequantize_bit_exact(tiny_block, qtype, rows, cols):
     say("dequantize", moe.TYPE_NAMES[qtype], rows, cols)

@@ -219,6 +219,72 @@ def test_iq3_s_decoder():
     assert np.array_equal(y, want)
 
 
+def test_q5_k_decoder():
+    """Q4_K's scales and nibbles (chunk c, byte l: values 64c + l and 64c + 32 + l) plus qh: bit k of byte l is bit 4 of
+    value 32 k + l (QUANT_FORMATS.md:401-417); y = (d sc) q - dmin m with q = nibble + 16 bit."""
+    sc = [1, 17, 33, 63, 20, 36, 50, 61]
+    m = [5, 18, 40, 63, 0, 33, 47, 60]
+    q = (np.arange(256) * 11 + 5) % 32
+    qs = np.zeros(128, dtype=np.uint8)
+    for c in range(4):
+        for l in range(32):
+            qs[32 * c + l] = (q[64 * c + l] & 15) | ((q[64 * c + 32 + l] & 15) << 4)
+    qh = np.zeros(32, dtype=np.uint8)
+    for v in range(256):
+        qh[v % 32] |= ((q[v] >> 4) & 1) << (v // 32)
+    d, dmin = np.float32(0.5), np.float32(0.0625)
+    blk = np.concatenate([f16(d), f16(dmin), pack_q4_k_scales(sc, m), qh, qs])
+    assert blk.size == 176
+    y = h.orc_dequant(moe.QT_Q5_K, blk, 256)
+    want = np.array([(d * np.float32(sc[v // 32])) * np.float32(q[v]) - dmin * np.float32(m[v // 32])
+                     for v in range(256)], dtype=np.float32)
+    assert np.array_equal(y, want)
+
+
+def test_q6_k_decoder():
+    """QUANT_FORMATS.md:419-445 position by position: value v (h = v / 128, l = v % 32) takes its low four bits from
+    ql[64h + l] (low nibble: v - 128h < 32; high nibble: 64..95), ql[64h + 32 + l] (32..63 low, 96..127 high), its high
+    two bits from qh[32h + l] at bits 0, 2, 4, 6 for the four 32-value quarters; scales[v / 16] signed; d last;
+    y = (d sc) (q - 32)."""
+    q = (np.arange(256) * 37 + 9) % 64
+    ql = np.zeros(128, dtype=np.uint8)
+    qh = np.zeros(64, dtype=np.uint8)
+    for v in range(256):
+        hh, r, l = v // 128, v % 128, v % 32
+        quarter = r // 32
+        byte = 64 * hh + (32 if quarter in (1, 3) else 0) + l
+        ql[byte] |= (q[v] & 15) << (4 if quarter >= 2 else 0)
+        qh[32 * hh + l] |= (q[v] >> 4) << (2 * quarter)
+    scales = np.array([-128, -77, -1, 0, 1, 5, 33, 127, -20, 64, -64, 100, -100, 2, -2, 90], dtype=np.int8)
+    d = np.float32(2.0 ** -7 * 1.5)
+    blk = np.concatenate([ql, qh, scales.view(np.uint8), f16(d)])
+    assert blk.size == 210
+    y = h.orc_dequant(moe.QT_Q6_K, blk, 256)
+    want = np.array([(d * np.float32(scales[v // 16])) * np.float32(q[v] - 32) for v in range(256)], dtype=np.float32)
+    assert np.array_equal(y, want)
+
+
+def test_iq4_xs_decoder():
+    """d, then scales_h (bits 2b, 2b + 1: bits 4-5 of sub-block b's scale), scales_l (byte b / 2, low nibble for even
+    b), then 16 qs bytes a sub-block (byte j: value j low, j + 16 high) (QUANT_FORMATS.md:213-232);
+    y = (d (ls - 32)) kvalues[nibble]."""
+    kv = h.orc_iq4nl().astype(np.float32)
+    ls = [0, 63, 32, 31, 1, 47, 16, 40]
+    sh = sum(((l >> 4) & 3) << (2 * b) for b, l in enumerate(ls))
+    sl = np.array([(ls[2 * i] & 15) | ((ls[2 * i + 1] & 15) << 4) for i in range(4)], dtype=np.uint8)
+    nib = (np.arange(256) * 5 + 3) % 16
+    qs = np.zeros(128, dtype=np.uint8)
+    for b in range(8):
+        for j in range(16):
+            qs[16 * b + j] = nib[32 * b + j] | (nib[32 * b + j + 16] << 4)
+    d = np.float32(-0.03125)
+    blk = np.concatenate([f16(d), np.frombuffer(np.uint16(sh).tobytes(), np.uint8), sl, qs])
+    assert blk.size == 136
+    y = h.orc_dequant(moe.QT_IQ4_XS, blk, 256)
+    want = np.array([(d * np.float32(ls[v // 32] - 32)) * kv[nib[v]] for v in range(256)], dtype=np.float32)
+    assert np.array_equal(y, want)
+
+
 # --------------------------------------------------------------------------------------------------------------
 # Activation quantisers
 
@@ -277,7 +343,8 @@ def random_blocks(qtype, n):
     b = rng.integers(0, 256, size=(n, nbytes), dtype=np.uint8)
     reach = {moe.QT_Q8_0: [(0, 128)], moe.QT_Q4_K: [(0, 63 * 15), (2, 63)], moe.QT_IQ3_S: [(0, 31 * 15)],
              moe.QT_IQ4_NL: [(0, 127)], moe.QT_Q2_0: [(0, 2)], moe.QT_IQ3_XXS: [(0, 62 * 31)],
-             moe.QT_IQ2_S: [(0, 43 * 31)]}[qtype]
+             moe.QT_IQ2_S: [(0, 43 * 31)], moe.QT_Q5_K: [(0, 63 * 31), (2, 63)], moe.QT_Q6_K: [(208, 127 * 32)],
+             moe.QT_IQ4_XS: [(0, 31 * 127)]}[qtype]
     for k in range(n):
         for off, r in reach:
             v = np.ldexp(1.0 + rng.integers(0, 1024) / 1024.0, int(rng.integers(0, 3)) - 5) / r
@@ -286,7 +353,7 @@ def random_blocks(qtype, n):
 
 
 @pytest.mark.parametrize("qtype", [moe.QT_Q8_0, moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ4_NL, moe.QT_Q2_0, moe.QT_IQ3_XXS,
-                                   moe.QT_IQ2_S])
+                                   moe.QT_IQ2_S, moe.QT_Q5_K, moe.QT_Q6_K, moe.QT_IQ4_XS])
 @pytest.mark.parametrize("n", [256, 2048])
 def test_vec_dot_against_decoded_float64(qtype, n):
     for trial in range(20):
@@ -341,10 +408,10 @@ def test_vec_dot_exact_when_every_step_is_exact():
     x = rng.integers(-20, 21, size=n).astype(np.float32)
     x[::256] = -127.0  # max = -127: iscale = 1, codes = x, d = 1
     aq = h.orc_quant_act(moe.QT_Q8_K, x)
-    for qtype in (moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ3_XXS, moe.QT_IQ2_S):
+    for qtype in (moe.QT_Q4_K, moe.QT_IQ3_S, moe.QT_IQ3_XXS, moe.QT_IQ2_S, moe.QT_Q5_K, moe.QT_Q6_K, moe.QT_IQ4_XS):
         wq = random_blocks(qtype, n // 256).reshape(n // 256, -1)
-        wq[:, :2] = f16(2.0**-4)
-        if qtype == moe.QT_Q4_K:
+        wq[:, 208 if qtype == moe.QT_Q6_K else 0:][:, :2] = f16(2.0**-4)
+        if qtype in (moe.QT_Q4_K, moe.QT_Q5_K):
             wq[:, 2:4] = f16(2.0**-5)
         wd = h.orc_dequant(qtype, wq.ravel(), n).astype(np.float64)
         assert h.orc_vec_dot(qtype, n, wq.ravel(), aq) == float(np.dot(wd, x.astype(np.float64)))
@@ -366,7 +433,8 @@ def dense_ffn(gate, up, down, gt, dt, H, F, x, limit=0.0):
 
 TYPES = [(moe.QT_Q8_0, moe.QT_Q8_0), (moe.QT_Q4_K, moe.QT_Q4_K), (moe.QT_IQ3_S, moe.QT_Q4_K), (moe.QT_IQ3_S, moe.QT_IQ3_S),
          (moe.QT_Q4_K, moe.QT_Q8_0), (moe.QT_Q4_K, moe.QT_IQ4_NL), (moe.QT_IQ4_NL, moe.QT_Q2_0),
-         (moe.QT_IQ3_XXS, moe.QT_IQ4_NL), (moe.QT_IQ2_S, moe.QT_Q2_0)]
+         (moe.QT_IQ3_XXS, moe.QT_IQ4_NL), (moe.QT_IQ2_S, moe.QT_Q2_0), (moe.QT_Q5_K, moe.QT_Q6_K),
+         (moe.QT_IQ4_XS, moe.QT_Q5_K), (moe.QT_Q6_K, moe.QT_IQ4_XS)]
 
 
 @pytest.mark.parametrize("gt,dt", TYPES)
@@ -397,6 +465,31 @@ def test_compute_many_against_dense_and_compute(gt, dt):
         assert np.array_equal(y1, y[t])
     # threads change nothing
     assert np.array_equal(y, h.orc_compute_many(gt, dt, H, F, jobs, x, nthreads=1))
+
+
+@pytest.mark.parametrize("gt,ut", [(moe.QT_Q4_K, moe.QT_IQ4_XS), (moe.QT_Q6_K, moe.QT_Q5_K), (moe.QT_IQ4_XS, moe.QT_Q6_K)])
+def test_compute_many_with_up_of_another_type(gt, ut):
+    """A shared expert whose up differs from its gate in type (the model file's blk.0: Q4_K gate, IQ4_XS up): the
+    dense FFN on the decoded weights, and the same bits as a gate/up pair of one type where the two agree."""
+    import ctypes as C
+    H, F, T, dt = 512, 256, 2, moe.QT_IQ4_NL
+    g = moe.synth_matrix(5, 1, gt, F, H)
+    u = moe.synth_matrix(5, 2, ut, F, H)
+    d = moe.synth_matrix(5, 3, dt, H, F)
+    x = h.tokens(6, T, H)
+    jobs = (h.OrcJob * T)(*[h.OrcJob(h.ptr(g), h.ptr(u), h.ptr(d), t, 1.0) for t in range(T)])
+    y = np.empty((T, H), dtype=np.float32)
+    s = h.OrcShape(gt, dt, H, F, 0.0, ut)
+    assert h.oracle.orc_compute_many(C.byref(s), jobs, T, T, h.ptr(x), H, h.ptr(y), H, 1) == 0
+    G = h.orc_dequant(gt, g, F * H).reshape(F, H).astype(np.float64)
+    U = h.orc_dequant(ut, u, F * H).reshape(F, H).astype(np.float64)
+    D = h.orc_dequant(dt, d, H * F).reshape(H, F).astype(np.float64)
+    for t in range(T):
+        a, b = G @ x[t], U @ x[t]
+        ref = D @ (a / (1 + np.exp(-a)) * b)
+        assert h.rel_l2(y[t], ref) < 3e-2
+    s_bad = h.OrcShape(gt, dt, H, F, 0.0, moe.QT_Q8_0)  # q8_0 up against a q8_K gate: refused
+    assert h.oracle.orc_compute_many(C.byref(s_bad), jobs, T, T, h.ptr(x), H, h.ptr(y), H, 1) == -1
 
 
 def test_compute_many_no_jobs_and_swiglu_limit():
