@@ -539,6 +539,7 @@ def prefill(args, cfg, key, moe, h):
     y = np.empty_like(x)
     w = np.empty((T, K), np.float32)
     wd = hip.malloc(T * K * 4)
+    blk.prefill_exact_tokens()  # clears the count: the next forward's alone is reported
     blk.forward_async(0, xd, T, yd, idsd, wd)
     hip.sync()
     hip.d2h(y, yd)
@@ -547,9 +548,12 @@ def prefill(args, cfg, key, moe, h):
     _, io, wo = L0.oracle_route(x)
     sample = np.r_[0:64, T // 2:T // 2 + 64, T - 64:T]
     yo, _, _ = L0.oracle_forward(x[sample], nthreads=min(16, os.cpu_count() or 1))
+    ma, rl = h.max_abs(y[sample], yo), h.rel_l2(y[sample], yo)
     parity = dict(sample_tokens=len(sample), ids_equal_all_tokens=bool(np.array_equal(ids, io)),
-                  w_bit_exact_all_tokens=bool(np.array_equal(w, wo)), y_bit_exact=bool(np.array_equal(y[sample], yo)),
-                  max_abs=h.max_abs(y[sample], yo), rel_l2=h.rel_l2(y[sample], yo))
+                  w_bit_exact_all_tokens=bool(np.array_equal(w, wo)), w_max_abs_all_tokens=h.max_abs(w, wo),
+                  y_bit_exact=bool(np.array_equal(y[sample], yo)), max_abs=ma, rel_l2=rl,
+                  y_within_tolerance=bool(ma <= h.TOL_ABS and rl <= h.TOL_REL),
+                  router="matrix-core, certified top-k", exact_sum_tokens=blk.prefill_exact_tokens())
     cpu = None
     if not args.no_cpu:  # a bounded sample: 192 of the chunk's tokens (all cores), 32 (one core)
         cpu = cpu_baseline(h, L0, x[sample], block_flop / T / 1e12, "TFLOP/s", check=y[sample], one_core_tokens=32)

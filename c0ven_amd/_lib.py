@@ -28,6 +28,7 @@ QGRID_IQ2S, QGRID_IQ3XXS, QGRID_IQ3S, QGRID_KVALUES, QGRID_BYTES = 0, 8192, 9216
 Q8_FAMILY = (QT_Q8_0, QT_IQ4_NL, QT_Q2_0)  # the weight types whose dot products take q8_0 activations
 
 MOE_OK, MOE_ERROR, MOE_BAD_ARGUMENT, MOE_BUSY, MOE_TIMEOUT = 0, 1, 2, 3, 4
+MOE_FLAG_EXACT_ROUTER = 1
 
 
 class MoeConfig(C.Structure):
@@ -36,7 +37,7 @@ class MoeConfig(C.Structure):
         ("n_layer", C.c_uint32), ("gate_type", C.c_uint32), ("down_type", C.c_uint32), ("has_shared", C.c_uint32),
         ("sh_gate_type", C.c_uint32), ("sh_down_type", C.c_uint32), ("max_tokens", C.c_uint32),
         ("swiglu_limit", C.c_float), ("device", C.c_int32), ("borrowed_immutable", C.c_uint32),
-        ("hc_lr", C.c_uint32), ("sh_up_type", C.c_uint32), ("reserved", C.c_uint32 * 1),
+        ("hc_lr", C.c_uint32), ("sh_up_type", C.c_uint32), ("flags", C.c_uint32),
     ]
 
 
@@ -90,6 +91,7 @@ _SIGS = {
     "moe_h_rows": (_u32, [C.POINTER(MoeConfig)]),
     "moe_check_config": (_i32, [C.POINTER(MoeConfig)]),
     "moe_prefill_dispatch": (_i32, [_P, C.POINTER(MoeTile), _u32, C.POINTER(_u32), _P]),
+    "moe_prefill_exact_tokens": (_i32, [_P, C.POINTER(_u32)]),
     "moe_sync": (_i32, [_P]),
     "moe_check": (_i32, [_P, _P]),
     "moe_stream": (_P, [_P]),
@@ -194,6 +196,11 @@ class GgufFile:
             raise MoeError(st, lib.gguf_last_error(None).decode())
         self.h = h
 
+    def bit_exact(self, ntok):
+        """Whether a forward of ntok tokens reproduces the oracle's bits (the decode kernel, or the prefill path with
+        the exact router), rather than its ids with y within the tolerance."""
+        return ntok <= 16 or self.exact_router
+
     def _check(self, st):
         if st != MOE_OK:
             raise MoeError(st, lib.gguf_last_error(self.h).decode())
@@ -291,14 +298,16 @@ class MoeBlock:
 
     def __init__(self, n_embd, n_ff, n_expert, n_used, gate_type, down_type, has_shared=True, sh_gate_type=None,
                  sh_down_type=None, n_layer=1, max_tokens=16, swiglu_limit=0.0, device=0, borrowed_immutable=0,
-                 hc_lr=0, sh_up_type=None):
+                 hc_lr=0, sh_up_type=None, exact_router=False):
         self.cfg = MoeConfig(n_embd=n_embd, n_ff=n_ff, n_expert=n_expert, n_used=n_used, n_layer=n_layer,
                              gate_type=gate_type, down_type=down_type, has_shared=1 if has_shared else 0,
                              sh_gate_type=sh_gate_type if sh_gate_type is not None else gate_type,
                              sh_down_type=sh_down_type if sh_down_type is not None else down_type,
                              max_tokens=max_tokens, swiglu_limit=swiglu_limit, device=device,
                              borrowed_immutable=borrowed_immutable, hc_lr=hc_lr,
-                             sh_up_type=0 if sh_up_type is None else sh_up_type)
+                             sh_up_type=0 if sh_up_type is None else sh_up_type,
+                             flags=MOE_FLAG_EXACT_ROUTER if exact_router else 0)
+        self.exact_router = bool(exact_router)
         h = _P()
         st = lib.moe_open(C.byref(self.cfg), C.byref(h))
         if st != MOE_OK:
@@ -395,6 +404,12 @@ class MoeBlock:
         out = np.empty((rows, cols), dtype=np.float32)
         self._check(lib.moe_dequantize(self.h, qtype, _ptr(blocks), rows, cols, _ptr(out)))
         return out
+
+    def prefill_exact_tokens(self):
+        """Tokens whose top k the prefill router summed exactly since the last call."""
+        n = _u32()
+        self._check(lib.moe_prefill_exact_tokens(self.h, C.byref(n)))
+        return n.value
 
     def load_layer_gguf(self, layer, gguf, blk):
         """Block blk's router and experts from a GgufFile into layer."""

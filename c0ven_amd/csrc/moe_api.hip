@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstddef>
 #include <cstdlib>
 #include <cstring>
@@ -43,6 +44,7 @@ struct Layer {
   uint16_t *router = nullptr;
   float *bias = nullptr;
   bool has_bias = false;
+  float rmax = 0.0f, bias_max = 0.0f;  // the largest routed row norm and |bias| (the prefill router's bound)
   uint8_t *experts = nullptr;
   uint8_t *shared = nullptr;
   // The hyper-connection module before the block (hc_lr > 0).
@@ -410,9 +412,9 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
     const moe_config &g = c->cfg;
     const Layer &L = c->layers[layer];
     PfShape S{g.n_embd, g.n_ff, g.n_expert, K, T, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type,
-              g.has_shared, g.swiglu_limit, g.sh_up_type};
+              g.has_shared, g.swiglu_limit, g.sh_up_type, (g.flags & MOE_FLAG_EXACT_ROUTER) ? 1u : 0u};
     PfLayer PL{L.router, L.has_bias ? L.bias : nullptr, L.experts, c->ex_bytes, c->ex_up, c->ex_down, L.shared,
-               c->sh_up, c->sh_down, c->codebooks};
+               c->sh_up, c->sh_down, c->codebooks, L.rmax, L.bias_max};
     PfHook hook{c->timing ? timing_hook : nullptr, c};
     check(prefill_forward(S, PL, c->pf, x, y, s, hook), "prefill launch");
     c->last_ids = c->pf.ids, c->last_w = c->pf.w, c->last_pf_T = T;
@@ -535,6 +537,10 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
                     ? c->alloc<uint8_t>((uint64_t)TM * Ug * kActBytes)
                     : b.act_r;
       b.logits = c->alloc<float>((uint64_t)TM * (E + 1));
+      b.xb = c->alloc<uint16_t>((uint64_t)TM * H);
+      b.xn = c->alloc<float>(TM);
+      b.cnt_exact = c->alloc<uint32_t>(1);
+      check(hipMemset(b.cnt_exact, 0, sizeof(uint32_t)), "hipMemset");
       b.ids = c->alloc<int32_t>(A2);
       b.w = c->alloc<float>(A2);
       b.gs = c->alloc<float>(TM);
@@ -656,6 +662,22 @@ MOE_API moe_status moe_load_router(moe_ctx *c, uint32_t layer, const uint16_t *r
     check(hipMemcpy(L.router, router, n * sizeof(uint16_t), hipMemcpyHostToDevice), "upload router");
     L.has_bias = bias != nullptr;
     if (bias) check(hipMemcpy(L.bias, bias, c->cfg.n_expert * sizeof(float), hipMemcpyHostToDevice), "upload bias");
+    // The prefill router's bound: max ||W_e||_2 over the routed rows and max |bias|, rounded up.
+    double r2 = 0.0;
+    for (uint32_t e = 0; e < c->cfg.n_expert; e++) {
+      double s2 = 0.0;
+      for (uint32_t k = 0; k < c->cfg.n_embd; k++) {
+        uint32_t u = (uint32_t)router[(uint64_t)e * c->cfg.n_embd + k] << 16;
+        float f;
+        std::memcpy(&f, &u, 4);
+        s2 += (double)f * (double)f;
+      }
+      r2 = std::max(r2, s2);
+    }
+    L.rmax = (float)(std::sqrt(r2) * (1.0 + 1e-9)) * (1.0f + 0x1p-22f);
+    L.bias_max = 0.0f;
+    if (bias)
+      for (uint32_t e = 0; e < c->cfg.n_expert; e++) L.bias_max = std::max(L.bias_max, std::fabs(bias[e]));
   });
 }
 
@@ -994,7 +1016,7 @@ MOE_API moe_status moe_compute_many(moe_ctx *c, const moe_cm_job *jobs, uint32_t
       check(hipMemcpyAsync(c->pf.w, w.data(), sizeof(float) * w.size(), hipMemcpyHostToDevice, s), "w");
       PfShape S{H, F, c->bc_slots, K, ntok, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type, 0, g.swiglu_limit,
                 g.sh_up_type};
-      PfLayer PL{nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0, c->codebooks};
+      PfLayer PL{nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0, c->codebooks, 0.0f, 0.0f};
       PfHook hook{c->timing ? timing_hook : nullptr, c};
       check(prefill_jobs(S, PL, c->pf, c->x_dev, c->y_dev, s, hook), "prefill launch");
       c->last_ids = c->pf.ids, c->last_w = c->pf.w, c->last_pf_T = ntok;
@@ -1273,6 +1295,17 @@ MOE_API moe_status moe_prefill_dispatch(moe_ctx *c, MoeTile *tiles, uint32_t cap
   });
 }
 
+MOE_API moe_status moe_prefill_exact_tokens(moe_ctx *c, uint32_t *n) {
+  return guarded(c, [&] {
+    require(n != nullptr, "null n");
+    *n = 0;
+    if (!c->pf.cnt_exact) return;
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    check(hipMemcpy(n, c->pf.cnt_exact, 4, hipMemcpyDeviceToHost), "read count");
+    check(hipMemset(c->pf.cnt_exact, 0, 4), "clear count");
+  });
+}
+
 MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap) {
   static const moe_abi_row rows[] = {
       ROW(moe_config, n_embd),       ROW(moe_config, n_ff),         ROW(moe_config, n_expert),
@@ -1280,7 +1313,7 @@ MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap) {
       ROW(moe_config, down_type),    ROW(moe_config, has_shared),   ROW(moe_config, sh_gate_type),
       ROW(moe_config, sh_down_type), ROW(moe_config, max_tokens),   ROW(moe_config, swiglu_limit),
       ROW(moe_config, device),       ROW(moe_config, borrowed_immutable), ROW(moe_config, hc_lr),
-      ROW(moe_config, sh_up_type),   ROW(moe_config, reserved),
+      ROW(moe_config, sh_up_type),   ROW(moe_config, flags),
       STRUCT(moe_config),            ROW(moe_expert_weights, gate), ROW(moe_expert_weights, up),
       ROW(moe_expert_weights, down), ROW(moe_expert_weights, down_parts), ROW(moe_expert_weights, down_blocks),
       STRUCT(moe_expert_weights),    ROW(moe_cm_job, expert),       ROW(moe_cm_job, tok),

@@ -59,6 +59,17 @@ __global__ void __launch_bounds__(kPfWG) pf_quant_rows(const float *src, uint64_
   if (o2) quant_unit<false, true, true, true>(v, l32, t2, o2 + ((uint64_t)row * U + u) * kActBytes);
 }
 
+// Work-group b (< n) of a 1-D grid runs on XCD b % 8 (the dispatcher deals work-groups to the eight XCDs in turn), as
+// the (b / 8)-th of the cnt_x = floor((n - x + 7) / 8) that XCD x receives among the first n. Its logical index puts
+// consecutive logical indices on one XCD: XCD x takes [off_x, off_x + cnt_x), off_x = x floor(n / 8) + min(x, n % 8),
+// a bijection of [0, n) for any n. With the row block fastest in the logical index, a tile's row blocks run together
+// on one XCD (its activations come from that XCD's L2), and the next tile of the same expert follows on the same XCD
+// (its weights too). The caller returns for b >= n.
+__device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
+  const uint32_t x = b % 8, q = n / 8, r = n % 8;
+  return x * q + min(x, r) + b / 8;
+}
+
 // h = silu(g) u of gate and up rows computed apart (a shared expert whose gate and up differ in type), quantised as
 // pf_quant_rows quantises h: the same SwiGLU as the fused gate/up kernels' epilogue, then the same units.
 __global__ void __launch_bounds__(kPfWG) pf_quant_swiglu(const float *g, const float *up, uint32_t ld, uint32_t rows,
@@ -218,6 +229,207 @@ __global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T
     atomicOr(&masks[(uint64_t)(t / 64) * E + my_id], 1ull << (t % 64));  // the dispatch's window mask
   }
   if (lane == 0 && gs) gs[t] = sigmoid_libm(lg[E], tab);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// The router on the bf16 matrix cores, with certified top-k. The logits come from v_mfma_f32_16x16x32_bf16 (every
+// bf16 x bf16 product exact, sums in fp32) instead of the fp64 k-order sum; each is within a bound of the exact one,
+// and where the bound leaves the top k or their order open, the experts that could be among them are summed again
+// exactly (fp64, k order, the oracle's arithmetic) before the selection. So ids are the oracle's; the weights and the
+// shared gate are computed from logits within ~1e-6 of the oracle's (the block output within its tolerance, not bit
+// for bit).
+//
+// The bound. A work-group takes 32 rows x 32 tokens; its four waves take a quarter of K each as chains of MFMAs into
+// one fp32 accumulator, then the four partials are added in order: at most n = H / 4 + 4 additions per result, each
+// with a relative rounding error of at most 2^-23 (any rounding mode), so |l~ - l| <= 1.01 n 2^-23 sum_k |w_k x_k|
+// <= gamma ||W_e|| ||bf16(x_t)|| (Cauchy-Schwarz), gamma passed by the host; rounding the sum to fp32 and adding the
+// bias add at most 2^-23 (|l~| + |bias|) more.
+
+// x to bf16 (round to nearest even) and its norm ||bf16(x_t)||_2, rounded up; the dispatch masks cleared. One wave a
+// token.
+__global__ void __launch_bounds__(kPfWG) pf_xprep(const float *x, uint32_t T, uint32_t H, uint32_t E, uint16_t *xb,
+                                                  float *xn, unsigned long long *masks) {
+  const uint32_t t = blockIdx.x * (kPfWG / 64) + wave_id(), lane = lane_id();
+  for (uint32_t i = blockIdx.x * kPfWG + threadIdx.x; i < pf_windows(T) * E; i += gridDim.x * kPfWG) masks[i] = 0ull;
+  if (t >= T) return;
+  double ss = 0.0;
+  for (uint32_t k = 8 * lane; k < H; k += 512) {
+    const float4 *p = (const float4 *)(x + (uint64_t)t * H + k);
+    const float4 a = p[0], b = p[1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float r0, r1;
+      round_bf16_2(v[2 * i], v[2 * i + 1], r0, r1);
+      ss = __builtin_fma((double)r0, (double)r0, ss);
+      ss = __builtin_fma((double)r1, (double)r1, ss);
+      o[i] = (__float_as_uint(r0) >> 16) | (__float_as_uint(r1) & 0xffff0000u);
+    }
+    *(uint4 *)(xb + (uint64_t)t * H + k) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  const double tot = wave_sum_f64(ss);
+  if (lane == 0) xn[t] = (float)(sqrt(tot) * (1.0 + 0x1p-40)) * (1.0f + 0x1p-22f);
+}
+
+typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+// Approximate logits of rows < E: a 32-row x 32-token tile a work-group (1-D grid, XCD-aware: a token block's row
+// blocks run on one XCD, so its bf16 x is fetched into that XCD's L2 once), wave w summing K range [w H / 4,
+// (w + 1) H / 4). Operands straight from memory (the router's bf16 rows and the prepared bf16 x), one step ahead.
+__global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *W, const uint16_t *xb, uint32_t T, uint32_t E,
+                                                        uint32_t H, const float *bias, float *logits) {
+  __shared__ v4f_t part[3][4][64];
+  const uint32_t nrb = (E + 31) / 32, ntb = (T + 31) / 32, n = nrb * ntb;
+  if (blockIdx.x >= n) return;
+  const uint32_t L = xcd_logical(blockIdx.x, n), e0 = 32 * (L % nrb), t0 = 32 * (L / nrb);
+  const uint32_t l = lane_id(), w = wave_id(), g = l / 16, c16 = l % 16;
+  const uint32_t kq = H / 4, k0 = w * kq;
+  // Rows past E and tokens past T read row / token 0 (valid memory); their results are never stored.
+  const uint32_t ra = e0 + c16 < E ? e0 + c16 : 0u, rb = e0 + 16 + c16 < E ? e0 + 16 + c16 : 0u;
+  const uint32_t ta = t0 + c16 < T ? t0 + c16 : 0u, tb = t0 + 16 + c16 < T ? t0 + 16 + c16 : 0u;
+  const uint16_t *pa = W + (uint64_t)ra * H + k0 + 8 * g, *pb = W + (uint64_t)rb * H + k0 + 8 * g;
+  const uint16_t *qa = xb + (uint64_t)ta * H + k0 + 8 * g, *qb = xb + (uint64_t)tb * H + k0 + 8 * g;
+  v4f_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+  v8bf_t a0 = *(const v8bf_t *)pa, a1 = *(const v8bf_t *)pb, b0 = *(const v8bf_t *)qa, b1 = *(const v8bf_t *)qb;
+  for (uint32_t k = 32; k <= kq; k += 32) {
+    v8bf_t na0 = a0, na1 = a1, nb0 = b0, nb1 = b1;
+    if (k < kq) {
+      na0 = *(const v8bf_t *)(pa + k), na1 = *(const v8bf_t *)(pb + k);
+      nb0 = *(const v8bf_t *)(qa + k), nb1 = *(const v8bf_t *)(qb + k);
+    }
+    acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[0][0], 0, 0, 0);
+    acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b1, acc[0][1], 0, 0, 0);
+    acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b0, acc[1][0], 0, 0, 0);
+    acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[1][1], 0, 0, 0);
+    a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) part[w - 1][2 * i + j][l] = acc[i][j];
+  }
+  __syncthreads();
+  if (w != 0) return;
+  // acc[i][j][q]: row e0 + 16 i + 4 g + q, token t0 + 16 j + c16.
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      v4f_t s = acc[i][j];
+#pragma unroll
+      for (int v = 0; v < 3; v++) {
+        const v4f_t o = part[v][2 * i + j][l];
+#pragma unroll
+        for (int q = 0; q < 4; q++) s[q] = __fadd_rn(s[q], o[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t t = t0 + 16 * j + c16, e = e0 + 16 * i + 4 * g + q;
+        if (t < T && e < E) logits[(uint64_t)t * (E + 1) + e] = bias ? __fadd_rn(s[q], bias[e]) : s[q];
+      }
+    }
+}
+
+// Row e's exact logit for token t: sum over k ascending of bf16(W[e][k]) bf16(x[t][k]) in fp64 (each product exact,
+// one fused step a term: the oracle's k-order sum), rounded to fp32, + bias. One lane.
+__device__ __forceinline__ float exact_logit(const uint16_t *W, const uint16_t *xb, uint32_t H, uint32_t e, uint32_t t,
+                                             const float *bias) {
+  const uint4 *wr = (const uint4 *)(W + (uint64_t)e * H), *xr = (const uint4 *)(xb + (uint64_t)t * H);
+  double acc = 0.0;
+  for (uint32_t k = 0; k < H / 8; k++) {
+    const uint4 a = wr[k], b = xr[k];
+    const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      acc = __builtin_fma((double)__uint_as_float(aw[i] << 16), (double)__uint_as_float(bw[i] << 16), acc);
+      acc = __builtin_fma((double)__uint_as_float(aw[i] & 0xffff0000u), (double)__uint_as_float(bw[i] & 0xffff0000u), acc);
+    }
+  }
+  const float lg = (float)acc;
+  return bias ? __fadd_rn(lg, bias[e]) : lg;
+}
+
+// Top-k on the approximate logits, certified: with B the token's bound, the K winners and their order stand when each
+// of the K + 1 largest keys exceeds the next by more than 2 B. Otherwise every expert whose logit may reach the K-th
+// (approximate logit >= the K-th's - 2 B) is summed again exactly and the selection runs on those exact logits (the
+// others cannot be among the K). The shared gate's row E is summed here in fp32 (it only scales the shared expert's
+// output). cnt_exact counts the tokens that needed the exact sums.
+__global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint16_t *W, const uint16_t *xb,
+                                                      const float *xn, uint32_t T, uint32_t E, uint32_t H, uint32_t K,
+                                                      const float *bias, float gamma_rmax, float bias_max,
+                                                      int32_t *ids, float *w, float *gs, unsigned long long *masks,
+                                                      uint32_t *cnt_exact) {
+  __shared__ uint64_t tab[32];
+  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
+  const uint32_t t = blockIdx.x * (kPfWG / 64) + wave_id(), lane = lane_id();
+  if (t >= T) return;
+  float *lg = logits + (uint64_t)t * (E + 1);
+  uint32_t key[kRoutePer], id[kRoutePer], my_id, my_key;
+  route_load(lg, E, lane, key, id);
+  if (gs) {  // the shared gate: row E, fp32 partials a lane, summed over the wave in a fixed order
+    const uint16_t *we = W + (uint64_t)E * H;
+    float part = 0.0f;
+    for (uint32_t k = 8 * lane; k < H; k += 512) {
+      const uint4 a = *(const uint4 *)(we + k), b = *(const uint4 *)(xb + (uint64_t)t * H + k);
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        part = __builtin_fmaf(__uint_as_float(aw[i] << 16), __uint_as_float(bw[i] << 16), part);
+        part = __builtin_fmaf(__uint_as_float(aw[i] & 0xffff0000u), __uint_as_float(bw[i] & 0xffff0000u), part);
+      }
+    }
+    const float le = (float)wave_sum_f64((double)part);
+    if (lane == 0) {
+      lg[E] = le;
+      gs[t] = sigmoid_libm(le, tab);
+    }
+  }
+  // The bound: the sum's rounding (gamma ||W||max ||x||) and the fp32 rounding of the sum and of the bias add.
+  uint32_t mk = 0;
+#pragma unroll
+  for (int i = 0; i < kRoutePer; i++) mk = max(mk, lane + 64 * i < E ? float_key(fabsf(key_float(key[i]))) : 0u);
+  const double labs = (double)key_float(wave_max_u32(mk));
+  const double B = (double)gamma_rmax * (double)xn[t] + 0x1p-22 * (labs + (double)bias_max) + 1e-30;
+  // The K + 1 largest (lane r < K + 1: rank r), on a copy of the keys.
+  const uint32_t K1 = K < E ? K + 1 : K;
+  {
+    uint32_t kc[kRoutePer], ic[kRoutePer];
+#pragma unroll
+    for (int i = 0; i < kRoutePer; i++) kc[i] = key[i], ic[i] = id[i];
+    route_select(kc, ic, K1, lane, &my_id, &my_key);
+  }
+  const double v = (double)key_float(my_key);
+  const double nxt = __shfl_down(v, 1, 64);
+  const bool open = lane + 1 < K1 && !(v - nxt > 2.0 * B);
+  if (__ballot(open) != 0ull) {
+    const double thr = __shfl(v, (int)K - 1, 64) - 2.0 * B;
+#pragma unroll
+    for (int i = 0; i < kRoutePer; i++) {
+      const uint32_t e = lane + 64 * i;
+      if (e < E && (double)key_float(key[i]) >= thr) key[i] = float_key(exact_logit(W, xb, H, e, t, bias));
+    }
+    if (lane == 0) atomicAdd(cnt_exact, 1u);
+    uint32_t kc[kRoutePer], ic[kRoutePer];
+#pragma unroll
+    for (int i = 0; i < kRoutePer; i++) kc[i] = key[i], ic[i] = id[i];
+    route_select(kc, ic, K, lane, &my_id, &my_key);
+  }
+  float mx, inv;
+  route_norm(key, E, lane, tab, &mx, &inv);
+  const float wk = route_weight(my_key, mx, inv, K, lane, tab);
+  if (lane < K) {
+    ids[(uint64_t)t * K + lane] = (int32_t)my_id;
+    w[(uint64_t)t * K + lane] = wk;
+    atomicOr(&masks[(uint64_t)(t / 64) * E + my_id], 1ull << (t % 64));
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -388,16 +600,6 @@ struct Dma {
   }
 };
 
-// Work-group b (< n) of a 1-D grid runs on XCD b % 8 (the dispatcher deals work-groups to the eight XCDs in turn), as
-// the (b / 8)-th of the cnt_x = floor((n - x + 7) / 8) that XCD x receives among the first n. Its logical index puts
-// consecutive logical indices on one XCD: XCD x takes [off_x, off_x + cnt_x), off_x = x floor(n / 8) + min(x, n % 8),
-// a bijection of [0, n) for any n. With the row block fastest in the logical index, a tile's row blocks run together
-// on one XCD (its activations come from that XCD's L2), and the next tile of the same expert follows on the same XCD
-// (its weights too). The caller returns for b >= n.
-__device__ __forceinline__ uint32_t xcd_logical(uint32_t b, uint32_t n) {
-  const uint32_t x = b % 8, q = n / 8, r = n % 8;
-  return x * q + min(x, r) + b / 8;
-}
 
 // The s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory loads are outstanding and
 // leaves the other counters alone.
@@ -1246,14 +1448,34 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     }
     if (hipEventRecord(b.join, ss) != hipSuccess) return hipGetLastError();
   }
-  {
-    HookScope k(hook, "pf_router", st);
-    pf_router<<<dim3((T + 63) / 64, (E + 63) / 64 + 1), kPfWG, 0, st>>>(x, T, L.router, L.bias, E, H, b.logits,
-                                                                       b.masks);
-  }
-  {
-    HookScope k(hook, "pf_topk", st);
-    pf_topk<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, T, E, K, b.ids, b.w, S.has_shared ? b.gs : nullptr, b.masks);
+  if (S.exact_router) {
+    {
+      HookScope k(hook, "pf_router", st);
+      pf_router<<<dim3((T + 63) / 64, (E + 63) / 64 + 1), kPfWG, 0, st>>>(x, T, L.router, L.bias, E, H, b.logits,
+                                                                         b.masks);
+    }
+    {
+      HookScope k(hook, "pf_topk", st);
+      pf_topk<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, T, E, K, b.ids, b.w, S.has_shared ? b.gs : nullptr, b.masks);
+    }
+  } else {
+    {
+      HookScope k(hook, "pf_xprep", st);
+      pf_xprep<<<(T + 3) / 4, kPfWG, 0, st>>>(x, T, H, E, b.xb, b.xn, b.masks);
+    }
+    {
+      HookScope k(hook, "pf_router", st);
+      const uint32_t n = ((E + 31) / 32) * ((T + 31) / 32);
+      pf_router_bf16<<<n, kPfWG, 0, st>>>(L.router, b.xb, T, E, H, L.bias, b.logits);
+    }
+    {
+      HookScope k(hook, "pf_topk", st);
+      // 1.01 n 2^-23 with n = H / 4 + 4 additions a result (the waves' chains, then their partials).
+      const float gamma = (float)(1.01 * (H / 4 + 4) * 0x1p-23);
+      pf_topk_cert<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, L.router, b.xb, b.xn, T, E, H, K, L.bias,
+                                                  gamma * L.rmax * 1.0001f, L.bias_max, b.ids, b.w,
+                                                  S.has_shared ? b.gs : nullptr, b.masks, b.cnt_exact);
+    }
   }
   if (S.has_shared && hipStreamWaitEvent(st, b.xq, 0) != hipSuccess) return hipGetLastError();
   const hipError_t e = routed_experts(S, L, b, st, hook, true);

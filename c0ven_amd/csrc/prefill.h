@@ -6,6 +6,8 @@
 //   pf_quant_rows  x -> the experts' activation units (q8_K or q8_0, the CPU rules)
 //   pf_router      logits = bf16(W) bf16(x) summed in fp64 in k order (each product exact), rounded once, + bias
 //   pf_topk        one wave a token: softmax, top k, weights, shared gate; each choice's bit in its window's mask
+//                  (by default instead: pf_xprep, pf_router_bf16 on the bf16 matrix cores within a stated bound, and
+//                  pf_topk_cert, which sums exactly the experts the bound leaves open: ids the same)
 //   pf_place       counting sort of the T k assignments by expert (stable: token order within an expert) into
 //                  MoeTile[] of at most MOE_TILE rows, perm (position -> assignment) and inv (assignment -> position)
 //                  (pre-routed ids: pf_masks builds the masks first)
@@ -31,6 +33,8 @@ struct PfShape {
   uint32_t gate_type, down_type, sh_gate_type, sh_down_type, has_shared;
   float swiglu_limit;
   uint32_t sh_up_type;  // the shared expert's up; when it is not sh_gate_type, gate and up run as two GEMMs
+  uint32_t exact_router;  // 1: the router's fp64 k-order sums for every logit (pf_router); 0: bf16 matrix cores and
+                          // certified top-k (pf_router_bf16, pf_topk_cert)
 };
 
 struct PfLayer {
@@ -41,12 +45,17 @@ struct PfLayer {
   const uint8_t *shared;
   uint64_t sh_up_off, sh_down_off;
   const uint8_t *codebooks;  // the caller's codebooks (QGRID layout) for IQ3_XXS and IQ2_S
+  float rmax;                // the largest ||W_e||_2 over the routed rows (bf16 values), rounded up
+  float bias_max;            // the largest |bias_e| (0 without a bias)
 };
 
 // Scratch for up to Tmax tokens (allocated at open).
 struct PfBufs {
   uint8_t *act_r, *act_s;  // Tmax x (H / 256) activation units (act_s == act_r when the types agree)
   float *logits;           // Tmax x (E + 1)
+  uint16_t *xb;            // Tmax x H: bf16(x), for the matrix-core router
+  float *xn;               // Tmax: ||bf16(x_t)||_2, rounded up
+  uint32_t *cnt_exact;     // tokens whose top-k needed exact sums (accumulates until read)
   int32_t *ids;            // Tmax x K
   float *w, *gs;           // Tmax x K, Tmax
   uint32_t *perm, *inv;    // Tmax K

@@ -70,8 +70,13 @@ typedef struct {
                           * mixes them per layer (blk.0: gate Q4_K, up IQ4_XS), as the reference runs the shared gate,
                           * up and down as three matvecs of their own types (model.cpp:828-830). Gate and up must take
                           * the same activation type, and may differ only among the types without a codebook. */
-  uint32_t reserved[1];
+  uint32_t flags;        /* MOE_FLAG_* below */
 } moe_config;
+
+/* moe_config.flags: the prefill router sums every logit exactly (fp64, k order: the oracle's bits for the weights and
+ * y too) instead of on the bf16 matrix cores within a bound, with the top k certified (the same ids; the weights and
+ * y within the block's tolerance). */
+#define MOE_FLAG_EXACT_ROUTER 1u
 
 /* The routing result of a forward, per token: k expert ids in rank order and their weights. */
 typedef struct {
@@ -168,6 +173,9 @@ MOE_API moe_status moe_check_config(const moe_config *cfg);
  * (token * n_used + rank) at each row of the expert-ordered activations. Within an expert the rows are in token
  * order (the reference's fill takes atomic order). Synchronous. */
 MOE_API moe_status moe_prefill_dispatch(moe_ctx *ctx, MoeTile *tiles, uint32_t cap, uint32_t *ntiles, uint32_t *perm);
+/* The number of tokens whose top k the prefill router had to sum exactly (the bound left the winners or their order
+ * open) since the last call, then cleared. Synchronous. */
+MOE_API moe_status moe_prefill_exact_tokens(moe_ctx *ctx, uint32_t *n);
 
 /* The hyper-connection module before a layer's block (docs/spec/MODEL_LAYER.md 1.1-1.2; the hc_ffn_* tensors of
  * blk.N): gamma 4 n_embd fp32 (hc_ffn_norm, the folded 1 + w), W_down hc_lr x 4 n_embd bf16, W_inject 4 x 4 n_embd

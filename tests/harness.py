@@ -198,10 +198,11 @@ class Layer:
         if self.shared is not None:
             blk.load_expert(layer, self.E, *self.shared)
 
-    def block(self, n_layer=1, max_tokens=16, device=0):
+    def block(self, n_layer=1, max_tokens=16, device=0, exact_router=False):
         return moe.MoeBlock(self.H, self.F, self.E, self.K, self.gate_type, self.down_type, self.has_shared,
                             self.sh_gate_type, self.sh_down_type, n_layer=n_layer, max_tokens=max_tokens,
-                            swiglu_limit=self.swiglu_limit, device=device, sh_up_type=self.sh_up_type)
+                            swiglu_limit=self.swiglu_limit, device=device, sh_up_type=self.sh_up_type,
+                            exact_router=exact_router)
 
     def oracle_forward(self, x, nthreads=8):
         """The whole block on the CPU oracle: y, ids, w."""
@@ -321,6 +322,23 @@ def rel_l2(a, b):
 
 def max_abs(a, b):
     return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+# The block's bar (north_star): top-k ids bit-exact, y within max-abs 1e-3 and rel-L2 1e-4. The prefill path's
+# default router gives the oracle's ids with logits within ~1e-6 of its own, so its weights are held to W_TOL.
+TOL_ABS, TOL_REL, W_TOL = 1e-3, 1e-4, 2e-5
+
+
+def check_block(y, ids, w, yo, io, wo, exact=True):
+    """ids equal; y within the tolerance; with exact, w and y equal bit for bit, else w within W_TOL."""
+    assert np.array_equal(ids, io), "top-k ids differ"
+    ma, rl = max_abs(y, yo), rel_l2(y, yo)
+    assert ma <= TOL_ABS and rl <= TOL_REL, (ma, rl)
+    if exact:
+        assert np.array_equal(w, wo), "routing weights not bit-exact: max %g" % max_abs(w, wo)
+        assert np.array_equal(y, yo), "y not bit-exact: max-abs %g rel-L2 %g" % (ma, rl)
+    else:
+        assert max_abs(w, wo) <= W_TOL, max_abs(w, wo)
 
 
 def tokens(seed, T, H, stream=999):

@@ -53,8 +53,7 @@ def test_load_layer_from_gguf(tmp_path, types):
     for T in (1, 8, 40):
         x = h.tokens(500 + T, T, 2560)
         y, ids, w = blk.forward(1, x)
-        yo, io, wo = L.oracle_forward(x)
-        assert np.array_equal(ids, io) and np.array_equal(w, wo) and np.array_equal(y, yo), T
+        h.check_block(y, ids, w, *L.oracle_forward(x), blk.bit_exact(T))
     with pytest.raises(moe.MoeError):  # no block 4 in the file
         blk.load_layer_gguf(0, g, 4)
     blk.close()

@@ -24,5 +24,5 @@ def test_model_file_type_mix(tup):
     for T in (8, 100):
         x = h.tokens(4800 + T, T, 2560)
         y, ids, w = blk.forward(0, x)
-        check_block(y, ids, w, *L.oracle_forward(x))
+        check_block(y, ids, w, *L.oracle_forward(x), blk.bit_exact(T))
     blk.close()

@@ -23,12 +23,7 @@ def say(*a):
 
 
 def check_block(y, ids, w, yo, io, wo, exact=True):
-    assert np.array_equal(ids, io), "top-k ids differ"
-    ma, rl = h.max_abs(y, yo), h.rel_l2(y, yo)
-    assert ma <= TOL_ABS and rl <= TOL_REL, (ma, rl)
-    if exact:
-        assert np.array_equal(w, wo), "routing weights not bit-exact: max %g" % h.max_abs(w, wo)
-        assert np.array_equal(y, yo), "y not bit-exact: max-abs %g rel-L2 %g" % (ma, rl)
+    h.check_block(y, ids, w, yo, io, wo, exact)
 
 
 def random_blocks(qtype, nblocks):
@@ -124,7 +119,9 @@ def test_routing_ties(tie):
         yo, io, wo = L.oracle_forward(x)
         if tie == "all":
             assert (io == np.arange(16)).all()
-        check_block(y, ids, w, yo, io, wo)
+        check_block(y, ids, w, yo, io, wo, blk.bit_exact(T))
+    if tie == "all":
+        assert blk.prefill_exact_tokens() == 24  # every prefill token's top k left open by the bound
     blk.close()
 
 
@@ -263,7 +260,7 @@ def test_model_shape_2560_640(types, T):
     L.upload(blk)
     x = h.tokens(640 + T, T, 2560)
     y, ids, w = blk.forward(0, x)
-    check_block(y, ids, w, *L.oracle_forward(x))
+    check_block(y, ids, w, *L.oracle_forward(x), blk.bit_exact(T))
     blk.close()
 
 

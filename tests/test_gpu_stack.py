@@ -29,7 +29,7 @@ def say(*a):
 def stack():
     say("stack: drawing", NL, "layers")
     L0 = h.Layer(2048, 512, 512, 10, I3, Q4, Q8, Q8, seed=2026, zipf=1.1, nthreads=0)
-    blk = L0.block(n_layer=NL, max_tokens=2048)
+    blk = L0.block(n_layer=NL, max_tokens=2048, exact_router=True)  # the oracle's bits through every layer
     L0.upload(blk, 0)
     layers = [L0]
     for l in range(1, NL):
