@@ -101,6 +101,10 @@ _SIGS = {
     "moe_set_trace": (_i32, [_P, C.c_int]),
     "moe_trace": (_i32, [_P, _P, _u32, C.POINTER(_u32), _P]),
     "moe_grid": (_u32, [_P]),
+    "moe_set_resident": (_i32, [_P, _u32, _P]),
+    "moe_miss_buffers": (_i32, [_P, C.POINTER(_P), C.POINTER(_u64), C.POINTER(_P), C.POINTER(_P)]),
+    "moe_last_step": (_u32, [_P]),
+    "moe_set_grid": (_i32, [_P, _u32]),
     "moe_expert_bytes": (_i32, [_P, _u32, C.POINTER(_u64)]),
     "moe_device_bytes": (_u64, [_P]),
     "moe_dequantize": (_i32, [_P, _u32, _P, _u32, _u32, _P]),
@@ -195,11 +199,6 @@ class GgufFile:
         if st != MOE_OK:
             raise MoeError(st, lib.gguf_last_error(None).decode())
         self.h = h
-
-    def bit_exact(self, ntok):
-        """Whether a forward of ntok tokens reproduces the oracle's bits (the decode kernel, or the prefill path with
-        the exact router), rather than its ids with y within the tolerance."""
-        return ntok <= 16 or self.exact_router
 
     def _check(self, st):
         if st != MOE_OK:
@@ -314,6 +313,11 @@ class MoeBlock:
             raise MoeError(st, lib.moe_last_error(None).decode())
         self.h = h
 
+    def bit_exact(self, ntok):
+        """Whether a forward of ntok tokens reproduces the oracle's bits (the decode kernel, or the prefill path with
+        the exact router), rather than its ids with y within the tolerance."""
+        return ntok <= 16 or self.exact_router
+
     def _check(self, st):
         if st != MOE_OK:
             raise MoeError(st, lib.moe_last_error(self.h).decode())
@@ -410,6 +414,21 @@ class MoeBlock:
         n = _u32()
         self._check(lib.moe_prefill_exact_tokens(self.h, C.byref(n)))
         return n.value
+
+    def set_resident(self, layer, resident=None):
+        """Which routed experts of layer the device holds (n_expert flags; None: all)."""
+        r = None if resident is None else np.ascontiguousarray(resident, dtype=np.uint8)
+        self._check(lib.moe_set_resident(self.h, layer, _ptr(r)))
+
+    def miss_buffers(self):
+        """(jobs, job_stride, ans_y, ans_seq): host addresses of the hybrid's records and answer (moe_miss_buffers)."""
+        j, a, q = _P(), _P(), _P()
+        st = _u64()
+        self._check(lib.moe_miss_buffers(self.h, C.byref(j), C.byref(st), C.byref(a), C.byref(q)))
+        return j.value, st.value, a.value, q.value
+
+    def last_step(self):
+        return int(lib.moe_last_step(self.h))
 
     def load_layer_gguf(self, layer, gguf, blk):
         """Block blk's router and experts from a GgufFile into layer."""

@@ -132,6 +132,15 @@ struct DecodeParams {
   float *hc_l;               // T x (lr + 4): the gate silu(W_down n / 4), then the inject logits
   float *hc_x;               // T x H: the mixed input (x points here)
   uint32_t *cnt_hc;          // 2 counters, kDynStride words apart: down items in, up items in
+  // Experts not on the device (core/models/qwen4exp/layout.h:64-71, layer.cl:838-884): a routed expert e with
+  // resident[e] == 0 is a miss. Its assignment joins no group; the top-k item publishes the token's misses in its
+  // record in host memory (miss_jobs, behind a system-scope release of the step number), and the token's combine items
+  // wait (bounded) for the host's answer (ans_seq == the step) and add ans_y's row after the shared expert's term.
+  const uint8_t *resident;   // E flags, or null: every expert is on the device
+  uint8_t *miss_jobs;        // a moe_miss_job record a token, miss_stride bytes apart (host memory), or null
+  uint32_t miss_stride;
+  const float *ans_y;        // T x H (host memory): the host's sum over each token's misses
+  const uint32_t *ans_seq;   // (host memory): the step whose answer ans_y holds
 };
 
 // The weight types a launch may meet, as a set (bits below): moe_decode is compiled once per set, so a context whose

@@ -45,6 +45,9 @@ struct Layer {
   float *bias = nullptr;
   bool has_bias = false;
   float rmax = 0.0f, bias_max = 0.0f;  // the largest routed row norm and |bias| (the prefill router's bound)
+  int *rlsb = nullptr;                 // per routed row: the least lsb of its bf16 values (its exact-sum condition)
+  uint8_t *resident = nullptr;         // n_expert flags: the experts on the device (when has_miss)
+  bool has_miss = false;               // some routed expert is not on the device
   uint8_t *experts = nullptr;
   uint8_t *shared = nullptr;
   // The hyper-connection module before the block (hc_lr > 0).
@@ -197,6 +200,10 @@ struct moe_ctx {
   uint32_t *err_flag = nullptr;
   uint64_t *flags = nullptr;
   uint64_t noalloc_bytes = 0;  // the no-alloc path's share of the device's scratch array for this shape
+  // The hybrid's records and answer in pinned host memory (moe_miss_buffers), and their device addresses.
+  uint8_t *miss_host = nullptr, *miss_dev = nullptr;
+  uint64_t miss_stride = 0;
+  uint32_t last_step = 0;
   // moe_compute_many's device copies of borrowed experts (routed types, ex_bytes each), keyed by gate pointer.
   uint8_t *bc_base = nullptr;
   uint32_t bc_slots = 0;
@@ -214,6 +221,7 @@ struct moe_ctx {
   const void *kernel = nullptr;  // moe_decode for the context's set of weight types
   const void *kernel_hc = nullptr;  // the same with the hyper-connection items (hc_lr > 0)
   uint32_t grid_hc = 0;
+  uint32_t grid_fit = 0, grid_hc_fit = 0;  // what the device holds at once (moe_set_grid(0) returns to them)
   size_t lds_hc = 0;
   size_t lds = 0;              // its dynamic LDS
   int timing = 0;  // 0 off, 1 every kernel, 2 the decode kernel and the prefill gate/up launches
@@ -323,6 +331,13 @@ DecodeParams base_params(moe_ctx *c, uint32_t layer, uint32_t T) {
   p.shared = L.shared, p.sh_up_off = c->sh_up, p.sh_down_off = c->sh_down;
   p.act_r = c->act_r, p.act_s = p.xact_s == p.xact_r ? c->act_r : c->act_s;
   p.codebooks = c->codebooks;
+  if (L.has_miss) {
+    require(c->miss_dev != nullptr, "the layer has experts off the device: call moe_miss_buffers first");
+    p.resident = L.resident;
+    p.miss_jobs = c->miss_dev, p.miss_stride = (uint32_t)c->miss_stride;
+    p.ans_y = (const float *)(c->miss_dev + c->miss_stride * c->tdec);
+    p.ans_seq = (const uint32_t *)(c->miss_dev + c->miss_stride * c->tdec + (uint64_t)c->tdec * g.n_embd * 4);
+  }
   p.logits = c->logits, p.ids = c->ids, p.w = c->w, p.gs = c->gs, p.ids_t = c->ids_t, p.w_t = c->w_t;
   p.groups = c->groups, p.ngroups = c->ngroups;
   p.h = c->h, p.y_asg = c->y_asg;
@@ -383,6 +398,7 @@ void launch(moe_ctx *c, const DecodeParams &p, hipStream_t s) {
     q.epoch = ++c->epoch;
   }
   q.tag = (uint32_t)q.epoch;
+  c->last_step = q.tag;
   if (c->trace) q.trace = c->trace, q.trace_cap = c->trace_cap;
   c->last_T = p.T, c->last_route = p.route, c->last_hc = p.hc_R != nullptr;
   if (c->timing) timing_hook(c, "moe_decode", 0, s);
@@ -411,10 +427,11 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
   } else {
     const moe_config &g = c->cfg;
     const Layer &L = c->layers[layer];
+    require(!L.has_miss, "the prefill path takes only layers whose experts are all on the device (moe_set_resident)");
     PfShape S{g.n_embd, g.n_ff, g.n_expert, K, T, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type,
               g.has_shared, g.swiglu_limit, g.sh_up_type, (g.flags & MOE_FLAG_EXACT_ROUTER) ? 1u : 0u};
     PfLayer PL{L.router, L.has_bias ? L.bias : nullptr, L.experts, c->ex_bytes, c->ex_up, c->ex_down, L.shared,
-               c->sh_up, c->sh_down, c->codebooks, L.rmax, L.bias_max};
+               c->sh_up, c->sh_down, c->codebooks, L.rlsb, L.rmax, L.bias_max};
     PfHook hook{c->timing ? timing_hook : nullptr, c};
     check(prefill_forward(S, PL, c->pf, x, y, s, hook), "prefill launch");
     c->last_ids = c->pf.ids, c->last_w = c->pf.w, c->last_pf_T = T;
@@ -507,9 +524,12 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     for (auto &L : c->layers) {
       L.router = c->alloc<uint16_t>((uint64_t)(E + 1) * H);
       L.bias = c->alloc<float>(E);
+      L.rlsb = c->alloc<int>(E);
+      L.resident = c->alloc<uint8_t>(E);
       L.experts = c->alloc<uint8_t>(c->ex_bytes * E);
       if (g.has_shared) L.shared = c->alloc<uint8_t>(c->sh_bytes);
       check(hipMemset(L.experts, 0, c->ex_bytes * E), "hipMemset");
+      check(hipMemset(L.resident, 1, E), "hipMemset");
       if (L.shared) check(hipMemset(L.shared, 0, c->sh_bytes), "hipMemset");
       if (g.hc_lr) {
         L.hc_gamma = c->alloc<float>((uint64_t)kHcStreams * H);
@@ -539,6 +559,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
       b.logits = c->alloc<float>((uint64_t)TM * (E + 1));
       b.xb = c->alloc<uint16_t>((uint64_t)TM * H);
       b.xn = c->alloc<float>(TM);
+      b.xlsb = c->alloc<int>(TM);
       b.cnt_exact = c->alloc<uint32_t>(1);
       check(hipMemset(b.cnt_exact, 0, sizeof(uint32_t)), "hipMemset");
       b.ids = c->alloc<int32_t>(A2);
@@ -614,14 +635,14 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     check(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, g.device), "CU count");
     require(per_cu >= 1, "moe_decode does not fit a CU");
     if (const char *e = std::getenv("C0VEN_DECODE_WG_PER_CU")) per_cu = std::max(1, std::min(per_cu, std::atoi(e)));
-    c->grid = (uint32_t)(per_cu * ncu);
+    c->grid = c->grid_fit = (uint32_t)(per_cu * ncu);
     if (g.hc_lr) {  // the variant with the hyper-connection items: its own occupancy (every work-group resident)
       c->kernel_hc = decode_kernel(types, true);
       c->lds_hc = std::max(c->lds, hc_lds);
       int hc_per_cu = 0;
       check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&hc_per_cu, c->kernel_hc, kWG, c->lds_hc), "occupancy");
       require(hc_per_cu >= 1, "moe_decode with the hyper-connection items does not fit a CU");
-      c->grid_hc = (uint32_t)(std::min(hc_per_cu, per_cu) * ncu);
+      c->grid_hc = c->grid_hc_fit = (uint32_t)(std::min(hc_per_cu, per_cu) * ncu);
     }
     require(g.device < kMaxDevices, "device ordinal too large");
     noalloc_setup(g.device);
@@ -651,6 +672,7 @@ MOE_API void moe_close(moe_ctx *c) {
   if (c->pf.xq) (void)hipEventDestroy(c->pf.xq);
   if (c->pf.side) (void)hipStreamDestroy(c->pf.side);
   if (c->stream) (void)hipStreamDestroy(c->stream);
+  if (c->miss_host) (void)hipHostFree(c->miss_host);
   delete c;
 }
 
@@ -675,6 +697,13 @@ MOE_API moe_status moe_load_router(moe_ctx *c, uint32_t layer, const uint16_t *r
       r2 = std::max(r2, s2);
     }
     L.rmax = (float)(std::sqrt(r2) * (1.0 + 1e-9)) * (1.0f + 0x1p-22f);
+    std::vector<int> lsb(c->cfg.n_expert, 1 << 20);
+    for (uint32_t e = 0; e < c->cfg.n_expert; e++)
+      for (uint32_t k = 0; k < c->cfg.n_embd; k++) {
+        const uint32_t b = router[(uint64_t)e * c->cfg.n_embd + k], ex = (b >> 7) & 0xffu;
+        if (b & 0x7fffu) lsb[e] = std::min(lsb[e], ex == 0 ? -133 : (int)ex - 134);
+      }
+    check(hipMemcpy(L.rlsb, lsb.data(), lsb.size() * sizeof(int), hipMemcpyHostToDevice), "upload row lsb");
     L.bias_max = 0.0f;
     if (bias)
       for (uint32_t e = 0; e < c->cfg.n_expert; e++) L.bias_max = std::max(L.bias_max, std::fabs(bias[e]));
@@ -1016,7 +1045,7 @@ MOE_API moe_status moe_compute_many(moe_ctx *c, const moe_cm_job *jobs, uint32_t
       check(hipMemcpyAsync(c->pf.w, w.data(), sizeof(float) * w.size(), hipMemcpyHostToDevice, s), "w");
       PfShape S{H, F, c->bc_slots, K, ntok, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type, 0, g.swiglu_limit,
                 g.sh_up_type};
-      PfLayer PL{nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0, c->codebooks, 0.0f, 0.0f};
+      PfLayer PL{nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0, c->codebooks, nullptr, 0.0f, 0.0f};
       PfHook hook{c->timing ? timing_hook : nullptr, c};
       check(prefill_jobs(S, PL, c->pf, c->x_dev, c->y_dev, s, hook), "prefill launch");
       c->last_ids = c->pf.ids, c->last_w = c->pf.w, c->last_pf_T = ntok;
@@ -1141,6 +1170,7 @@ MOE_API moe_status moe_forward_async_noalloc(moe_ctx *c, uint32_t layer, const f
       p.epoch = ++d.epoch;
     }
     p.tag = (uint32_t)p.epoch;
+    c->last_step = p.tag;
     void *args[] = {&p};
     check(hipLaunchKernel(c->kernel, dim3(c->grid), dim3(kWG), args, c->lds, s), "moe_decode launch");
     check(hipGetLastError(), "moe_decode launch");
@@ -1183,6 +1213,14 @@ MOE_API moe_status moe_kernel_times(moe_ctx *c, const char **names, float *avg_m
 }
 
 MOE_API uint32_t moe_grid(const moe_ctx *c) { return c ? c->grid : 0; }
+
+MOE_API moe_status moe_set_grid(moe_ctx *c, uint32_t grid) {
+  return guarded(c, [&] {
+    require(grid % 8 == 0 && grid <= (1u << 20), "the grid must be a multiple of 8 (the routed items' lists)");
+    c->grid = grid ? grid : c->grid_fit;
+    if (c->cfg.hc_lr) c->grid_hc = grid ? grid : c->grid_hc_fit;
+  });
+}
 
 MOE_API moe_status moe_set_trace(moe_ctx *c, int on) {
   return guarded(c, [&] {
@@ -1295,6 +1333,39 @@ MOE_API moe_status moe_prefill_dispatch(moe_ctx *c, MoeTile *tiles, uint32_t cap
   });
 }
 
+MOE_API moe_status moe_set_resident(moe_ctx *c, uint32_t layer, const uint8_t *resident) {
+  return guarded(c, [&] {
+    require(layer < c->cfg.n_layer, "layer out of range");
+    Layer &L = c->layers[layer];
+    std::vector<uint8_t> r(c->cfg.n_expert, 1);
+    if (resident)
+      for (uint32_t e = 0; e < c->cfg.n_expert; e++) r[e] = resident[e] ? 1 : 0;
+    check(hipMemcpy(L.resident, r.data(), r.size(), hipMemcpyHostToDevice), "upload resident flags");
+    L.has_miss = std::find(r.begin(), r.end(), 0) != r.end();
+  });
+}
+
+MOE_API moe_status moe_miss_buffers(moe_ctx *c, void **jobs, uint64_t *job_stride, float **ans_y, uint32_t **ans_seq) {
+  return guarded(c, [&] {
+    if (!c->miss_host) {
+      const uint64_t stride = (sizeof(moe_miss_job) + 4ull * c->cfg.n_embd + 255) / 256 * 256;
+      const uint64_t bytes = stride * c->tdec + 4ull * c->tdec * c->cfg.n_embd + 256;
+      void *h = nullptr, *d = nullptr;
+      check(hipHostMalloc(&h, bytes, hipHostMallocCoherent | hipHostMallocMapped), "hipHostMalloc");
+      std::memset(h, 0, bytes);
+      check(hipHostGetDevicePointer(&d, h, 0), "hipHostGetDevicePointer");
+      c->miss_host = (uint8_t *)h, c->miss_dev = (uint8_t *)d, c->miss_stride = stride;
+    }
+    const uint64_t ans = c->miss_stride * c->tdec;
+    if (jobs) *jobs = c->miss_host;
+    if (job_stride) *job_stride = c->miss_stride;
+    if (ans_y) *ans_y = (float *)(c->miss_host + ans);
+    if (ans_seq) *ans_seq = (uint32_t *)(c->miss_host + ans + 4ull * c->tdec * c->cfg.n_embd);
+  });
+}
+
+MOE_API uint32_t moe_last_step(const moe_ctx *c) { return c ? c->last_step : 0; }
+
 MOE_API moe_status moe_prefill_exact_tokens(moe_ctx *c, uint32_t *n) {
   return guarded(c, [&] {
     require(n != nullptr, "null n");
@@ -1314,6 +1385,8 @@ MOE_API uint32_t moe_abi_layout(moe_abi_row *table, uint32_t cap) {
       ROW(moe_config, sh_down_type), ROW(moe_config, max_tokens),   ROW(moe_config, swiglu_limit),
       ROW(moe_config, device),       ROW(moe_config, borrowed_immutable), ROW(moe_config, hc_lr),
       ROW(moe_config, sh_up_type),   ROW(moe_config, flags),
+      ROW(moe_miss_job, seq),        ROW(moe_miss_job, nmiss),      ROW(moe_miss_job, ids),
+      ROW(moe_miss_job, w),          ROW(moe_miss_job, all),        STRUCT(moe_miss_job),
       STRUCT(moe_config),            ROW(moe_expert_weights, gate), ROW(moe_expert_weights, up),
       ROW(moe_expert_weights, down), ROW(moe_expert_weights, down_parts), ROW(moe_expert_weights, down_blocks),
       STRUCT(moe_expert_weights),    ROW(moe_cm_job, expert),       ROW(moe_cm_job, tok),

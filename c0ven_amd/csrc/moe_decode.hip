@@ -3,22 +3,23 @@
 // Replaces the reference's decode kernel list for the block (model.cpp:1348-1414): the router's bf16 GEMV
 // (mv_xmx_bf16), router_group (layer.cl:984-1023), moe_gate_up_g (moe.cl:230-302), moe_down_g (moe.cl:416-471) and
 // moe_combine (layer.cl:869-884). Every work-group walks the work items b, b + grid, b + 2 grid, ... in one order
-// (decode.h): lead items (router rows; x quantised), top-k items, gate/up items, down items. An item that needs earlier
-// work waits on flags set (to this launch's epoch) by the work it needs:
-//   - each lead item sets its own flag; a top-k item waits for all of them (no counter the lead items contend on);
-//   - the last top-k item in groups the assignments into MoeGroups and sets "routed" (gate/up items wait on it);
-//   - the last gate/up item of a 256-row unit of group g quantises that unit of h for the down; the last unit sets
-//     group g's flag (its down items wait on it);
-//   - the last down item of a (token, row block) to finish combines that token's rows: sum_k w_k y_k + gs s.
-// Every item's dependencies have smaller indices, and a work-group takes its items in increasing order, so the
-// smallest unfinished item always has everything it waits for once every work-group runs: the grid is no larger than
-// what the device holds at once, so each is dispatched (behind other streams' kernels at worst, which do not wait on
-// this one). A cooperative launch would state the same guarantee but costs ~20 us more per launch on this runtime.
-// Waits are bounded anyway: past kSpinLimit polls a wait gives up and sets *err.
+// (decode.h): lead items (router rows; x quantised), top-k items, the shared expert's items; then it takes the routed
+// gate/up, down and combine items from the list of its index modulo 8 (a counter a list). An item that needs earlier
+// work waits for it (flags set to this launch's epoch, or tagged records whose tag is this launch's):
+//   - each lead item sets its own flag; a top-k item polls the logits the lead items store;
+//   - every work-group builds the routed groups from the ids the top-k items store;
+//   - a down item polls its group's h, a combine item the outputs of its token's assignments.
+// Every item's dependencies have smaller indices. Progress: lead items wait for nothing; the dispatcher deals a grid's
+// work-groups to the eight XCDs in turn (work-group b to XCD b mod 8) and each XCD starts its share in index order,
+// so a work-group never waits behind a later one of its own XCD, and list x is served by XCD x's work-groups, which
+// take its items in order. So the smallest unfinished item always progresses once its XCD admits any work-group of
+// this kernel, whatever else the device runs and however large the grid (a multiple of 8; moe_set_grid). Waits are
+// bounded anyway: past kSpinLimit polls (seconds) a wait gives up and sets *err.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
 
+#include "../../include/c0ven_moe.h"
 #include "act_quant.h"
 #include "decode.h"
 #include "route.h"
@@ -186,6 +187,7 @@ __device__ __forceinline__ void route_token(const DecodeParams &p, uint32_t t, c
     if (lane == 0) dpart[wv - 1] = part;
   }
   __syncthreads();
+  uint32_t *nm = (uint32_t *)dpart + 8;
   if (wv == 0) {
     const float inv = (float)(1.0 / __dadd_rn(__dadd_rn(dpart[0], dpart[1]), dpart[2]));
     const float w = route_weight(my_key, mx, inv, K, lane, tab);
@@ -194,6 +196,32 @@ __device__ __forceinline__ void route_token(const DecodeParams &p, uint32_t t, c
       st_tag(p.w_t + t * K + lane, __float_as_uint(w), p.tag);
       p.ids[t * K + lane] = (int32_t)my_id;  // the caller's copies, read after the launch
       p.w[t * K + lane] = w;
+    }
+    if (p.miss_jobs) {  // the token's record: the misses in rank order (layer.cl:781-804's rt_finish)
+      moe_miss_job *job = (moe_miss_job *)(p.miss_jobs + (uint64_t)t * p.miss_stride);
+      const bool miss = lane < K && !p.resident[my_id];
+      const uint64_t b = __ballot(miss);
+      if (lane < K) job->all[lane] = (int32_t)my_id;
+      if (miss) {
+        const uint32_t at = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        job->ids[at] = (int32_t)my_id;
+        job->w[at] = w;
+      }
+      if (lane == 0) *nm = (uint32_t)__popcll(b);
+    }
+  }
+  if (p.miss_jobs) {  // x, then nmiss and the step (rt_publish: the step last, behind a system-scope release)
+    __syncthreads();
+    moe_miss_job *job = (moe_miss_job *)(p.miss_jobs + (uint64_t)t * p.miss_stride);
+    float *jx = (float *)(job + 1);
+    if (*nm > 0)
+      for (uint32_t i = tid(); i < p.H; i += kWG) jx[i] = ld_co(p.x + (uint64_t)t * p.H + i);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+    __syncthreads();
+    if (tid() == 0) {
+      job->nmiss = *nm;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+      __hip_atomic_store(&job->seq, p.tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
 }
@@ -616,28 +644,32 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds,
     ids[a] = (uint32_t)ri;
   }
   __syncthreads();
+  // Assignments to experts not on the device (misses) join no group.
+  const bool live = a < n && (!p.resident || p.resident[ids[a]]);
   if (T == 1) {  // one token: every group is one assignment, in rank order (what the general numbering gives)
-    if (a < K) {
-      tab->slot[a] = (int32_t)ids[a];
-      tab->n[a] = 1u;
-      tab->asg[a][0] = (uint16_t)a;
+    const uint64_t b = __ballot(live);  // a < K < 64: wave 0 holds them all
+    if (wv == 0 && live) {
+      const uint32_t g = __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u);
+      tab->slot[g] = (int32_t)ids[a];
+      tab->n[g] = 1u;
+      tab->asg[g][0] = (uint16_t)a;
     }
-    if (a == 0) tab->ng = K;
+    if (a == 0) tab->ng = (uint32_t)__popcll(b);
     __syncthreads();
     return;
   }
   uint32_t e = 0, rank = 0, total = 0;
-  if (a < n) {
+  if (live) {
     e = ids[a];
     atomicOr(mask + e, 1u << t);
   }
   __syncthreads();
-  if (a < n) {
+  if (live) {
     const uint32_t m = mask[e];
     rank = __popc(m & ((1u << t) - 1u));
     total = __popc(m);
   }
-  const bool head = a < n && rank % MOE_GROUP_MAX == 0;
+  const bool head = live && rank % MOE_GROUP_MAX == 0;
   const uint32_t gn = head ? min((uint32_t)MOE_GROUP_MAX, total - rank) : 0u;
   uint32_t before = 0;  // heads of this size at lower assignments of this wave
 #pragma unroll
@@ -662,7 +694,7 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds,
     tab->n[g] = gn;
   }
   __syncthreads();
-  if (a < n) tab->asg[gnum[2 * e + rank / MOE_GROUP_MAX]][rank % MOE_GROUP_MAX] = (uint16_t)a;
+  if (live) tab->asg[gnum[2 * e + rank / MOE_GROUP_MAX]][rank % MOE_GROUP_MAX] = (uint16_t)a;
   if (a == 0) tab->ng = G;
   __syncthreads();
 }
@@ -981,9 +1013,10 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
   const uint32_t ns = p.has_shared ? 1u : 0u;
   {
     const uint32_t k = tid();
-    if (k < K) {  // thread k: w_k and whether assignment k is live (a pre-routed call marks a dead one id < 0)
+    if (k < K) {  // thread k: w_k and whether assignment k is live (a pre-routed call marks a dead one id < 0, a
+                  // routed one is dead when its expert is a miss)
       const float w = p.route ? __uint_as_float(poll_tag(p, p.w_t + t * K + k)) : ld_co(p.w + t * K + k);
-      const bool on = p.route || ld_co(p.ids + t * K + k) >= 0;
+      const bool on = p.route ? (!p.resident || p.resident[poll_tag(p, p.ids_t + t * K + k)]) : ld_co(p.ids + t * K + k) >= 0;
       wl[k] = w;
       wl[kMaxUsed + 1 + k] = on ? 1.0f : 0.0f;
     } else if (k == K && ns) {  // thread K: the shared expert's gate
@@ -994,8 +1027,27 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
       wl[2 * kMaxUsed + 1 + s] = __fmul_rn(2.0f, sigmoid_libm(__fmul_rn(inj, 0.25f), tab));
     }
   }
-  if (p.route) wait_tag(p, p.y_asg + ((uint64_t)t * K + K - 1) * p.H + blk * rows + rows - 1);
+  if (p.route && !p.resident) wait_tag(p, p.y_asg + ((uint64_t)t * K + K - 1) * p.H + blk * rows + rows - 1);
   else __syncthreads();
+  // The host's answer for the token's misses (cpu_wait, layer.cl:849-866): thread 0 polls the step with system-scope
+  // acquires, bounded in time (5 s on the 100 MHz clock), the work-group follows.
+  bool cpu = false;
+  if (p.route && p.resident) {
+    uint32_t miss = 0;
+    for (uint32_t k = 0; k < K; k++) miss += wl[kMaxUsed + 1 + k] == 0.0f ? 1u : 0u;
+    cpu = miss > 0 && p.ans_y;
+    if (cpu && tid() == 0) {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      while (__hip_atomic_load(p.ans_seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) != p.tag) {
+        __builtin_amdgcn_s_sleep(8);
+        if (__builtin_amdgcn_s_memrealtime() - t0 > 500000000ull) {
+          st_co(p.err, 1u);
+          break;
+        }
+      }
+    }
+    __syncthreads();
+  }
   if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
   if (tid() < rows) {
     bool on[kMaxUsed];
@@ -1033,6 +1085,7 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
     for (uint32_t k = 0; k < kMaxUsed; k++)
       if (on[k]) acc = __fadd_rn(acc, __fmul_rn(wv[k], yv[k]));
     if (ns) acc = __fadd_rn(acc, __fmul_rn(gs, ys));
+    if (cpu) acc = __fadd_rn(acc, __hip_atomic_load(p.ans_y + (uint64_t)t * p.H + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM));
     if (p.y) p.y[(uint64_t)t * p.H + row] = acc;
     if constexpr (kHc) {  // the combine (MODEL_LAYER.md 1.2): R_s += 2 sigma(inject_s / 4) y
 #pragma unroll

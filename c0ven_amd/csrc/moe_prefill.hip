@@ -22,6 +22,8 @@
 
 namespace c0ven {
 
+constexpr uint32_t kMaxRouteExperts = 512;  // routed experts a layer may have
+
 __device__ __constant__ static const uint32_t kIq3sGridPf[512] = {C0VEN_IQ3S_GRID_VALUES};
 
 namespace {
@@ -235,24 +237,38 @@ __global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T
 // The router on the bf16 matrix cores, with certified top-k. The logits come from v_mfma_f32_16x16x32_bf16 (every
 // bf16 x bf16 product exact, sums in fp32) instead of the fp64 k-order sum; each is within a bound of the exact one,
 // and where the bound leaves the top k or their order open, the experts that could be among them are summed again
-// exactly (fp64, k order, the oracle's arithmetic) before the selection. So ids are the oracle's; the weights and the
-// shared gate are computed from logits within ~1e-6 of the oracle's (the block output within its tolerance, not bit
-// for bit).
+// exactly before the selection. So ids are the oracle's; the weights and the shared gate are computed from logits
+// within ~1e-6 of the oracle's (the block output within its tolerance, not bit for bit).
 //
-// The bound. A work-group takes 32 rows x 32 tokens; its four waves take a quarter of K each as chains of MFMAs into
-// one fp32 accumulator, then the four partials are added in order: at most n = H / 4 + 4 additions per result, each
-// with a relative rounding error of at most 2^-23 (any rounding mode), so |l~ - l| <= 1.01 n 2^-23 sum_k |w_k x_k|
-// <= gamma ||W_e|| ||bf16(x_t)|| (Cauchy-Schwarz), gamma passed by the host; rounding the sum to fp32 and adding the
-// bias add at most 2^-23 (|l~| + |bias|) more.
+// The bound. A work-group takes 32 rows x 32 tokens; its four waves take a quarter of K each. Every MFMA starts from
+// zero (32 products, at most 31 roundings inside), its result is added to the wave's fp32 sum (one rounding a chunk),
+// and the four quarters are added in order (three more): at most n = 31 + H / 128 + 3 roundings touch any product,
+// each of relative size at most 2^-23 whatever the rounding mode, so |l~ - l| <= 1.01 n 2^-23 sum_k |w_k x_k| <=
+// gamma ||W_e|| ||bf16(x_t)|| (Cauchy-Schwarz); rounding the sum to fp32 and adding the bias add at most
+// 2^-23 (|l~| + |bias|) more.
+//
+// The exact sums. Every product w x of two bf16 values is a multiple of 2^(lsb(w) + lsb(x)) (lsb: the weight of the
+// value's last mantissa bit), and so is every partial sum of the row's products. When sum_k |w_k x_k| < 2^(L + 53),
+// L = min_k lsb(W_e[k]) + min_k lsb(x_t[k]), every partial sum, in any order, is exact in fp64: the oracle's k-order
+// double sum is that exact value, and so is a parallel sum. Then eight lanes sum an expert's row (a contiguous eighth
+// each, then a fixed tree); otherwise one lane runs the k-order chain.
 
-// x to bf16 (round to nearest even) and its norm ||bf16(x_t)||_2, rounded up; the dispatch masks cleared. One wave a
-// token.
+// The weight of a bf16 value's last mantissa bit as a power of two (normal: exponent - 7; subnormal: -133); zero
+// contributes nothing (a large sentinel).
+__device__ __forceinline__ int bf16_lsb(uint32_t b) {
+  const uint32_t ex = (b >> 7) & 0xffu;
+  return (b & 0x7fffu) == 0 ? 1 << 20 : ex == 0 ? -133 : (int)ex - 134;
+}
+
+// x to bf16 (round to nearest even), its norm ||bf16(x_t)||_2 rounded up and the least lsb of its values; the dispatch
+// masks cleared. One wave a token.
 __global__ void __launch_bounds__(kPfWG) pf_xprep(const float *x, uint32_t T, uint32_t H, uint32_t E, uint16_t *xb,
-                                                  float *xn, unsigned long long *masks) {
+                                                  float *xn, int *xlsb, unsigned long long *masks) {
   const uint32_t t = blockIdx.x * (kPfWG / 64) + wave_id(), lane = lane_id();
   for (uint32_t i = blockIdx.x * kPfWG + threadIdx.x; i < pf_windows(T) * E; i += gridDim.x * kPfWG) masks[i] = 0ull;
   if (t >= T) return;
   double ss = 0.0;
+  int lsb = 1 << 20;
   for (uint32_t k = 8 * lane; k < H; k += 512) {
     const float4 *p = (const float4 *)(x + (uint64_t)t * H + k);
     const float4 a = p[0], b = p[1];
@@ -265,11 +281,16 @@ __global__ void __launch_bounds__(kPfWG) pf_xprep(const float *x, uint32_t T, ui
       ss = __builtin_fma((double)r0, (double)r0, ss);
       ss = __builtin_fma((double)r1, (double)r1, ss);
       o[i] = (__float_as_uint(r0) >> 16) | (__float_as_uint(r1) & 0xffff0000u);
+      lsb = min(lsb, min(bf16_lsb(o[i] & 0xffffu), bf16_lsb(o[i] >> 16)));
     }
     *(uint4 *)(xb + (uint64_t)t * H + k) = make_uint4(o[0], o[1], o[2], o[3]);
   }
   const double tot = wave_sum_f64(ss);
-  if (lane == 0) xn[t] = (float)(sqrt(tot) * (1.0 + 0x1p-40)) * (1.0f + 0x1p-22f);
+  lsb = -(int)wave_max_u32((uint32_t)(-lsb + (1 << 21))) + (1 << 21);
+  if (lane == 0) {
+    xn[t] = (float)(sqrt(tot) * (1.0 + 0x1p-40)) * (1.0f + 0x1p-22f);
+    xlsb[t] = lsb;
+  }
 }
 
 typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
@@ -277,7 +298,8 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 // Approximate logits of rows < E: a 32-row x 32-token tile a work-group (1-D grid, XCD-aware: a token block's row
 // blocks run on one XCD, so its bf16 x is fetched into that XCD's L2 once), wave w summing K range [w H / 4,
-// (w + 1) H / 4). Operands straight from memory (the router's bf16 rows and the prepared bf16 x), one step ahead.
+// (w + 1) H / 4). Operands straight from memory (the router's bf16 rows and the prepared bf16 x), kPre steps ahead.
+constexpr uint32_t kRtPre = 4;  // steps of loads in flight; a wave's K steps (H / 128) are a multiple of it
 __global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *W, const uint16_t *xb, uint32_t T, uint32_t E,
                                                         uint32_t H, const float *bias, float *logits) {
   __shared__ v4f_t part[3][4][64];
@@ -285,7 +307,7 @@ __global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *W, const
   if (blockIdx.x >= n) return;
   const uint32_t L = xcd_logical(blockIdx.x, n), e0 = 32 * (L % nrb), t0 = 32 * (L / nrb);
   const uint32_t l = lane_id(), w = wave_id(), g = l / 16, c16 = l % 16;
-  const uint32_t kq = H / 4, k0 = w * kq;
+  const uint32_t kq = H / 4, k0 = w * kq, ns = kq / 32;
   // Rows past E and tokens past T read row / token 0 (valid memory); their results are never stored.
   const uint32_t ra = e0 + c16 < E ? e0 + c16 : 0u, rb = e0 + 16 + c16 < E ? e0 + 16 + c16 : 0u;
   const uint32_t ta = t0 + c16 < T ? t0 + c16 : 0u, tb = t0 + 16 + c16 < T ? t0 + 16 + c16 : 0u;
@@ -296,18 +318,32 @@ __global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *W, const
   for (int i = 0; i < 2; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
-  v8bf_t a0 = *(const v8bf_t *)pa, a1 = *(const v8bf_t *)pb, b0 = *(const v8bf_t *)qa, b1 = *(const v8bf_t *)qb;
-  for (uint32_t k = 32; k <= kq; k += 32) {
-    v8bf_t na0 = a0, na1 = a1, nb0 = b0, nb1 = b1;
-    if (k < kq) {
-      na0 = *(const v8bf_t *)(pa + k), na1 = *(const v8bf_t *)(pb + k);
-      nb0 = *(const v8bf_t *)(qa + k), nb1 = *(const v8bf_t *)(qb + k);
+  v8bf_t op[kRtPre][4];
+#pragma unroll
+  for (uint32_t d = 0; d < kRtPre; d++) {
+    const uint32_t k = 32 * min(d, ns - 1);
+    op[d][0] = *(const v8bf_t *)(pa + k), op[d][1] = *(const v8bf_t *)(pb + k);
+    op[d][2] = *(const v8bf_t *)(qa + k), op[d][3] = *(const v8bf_t *)(qb + k);
+  }
+  // No branch inside the unrolled steps: the compiler's waits then count the loads in flight (a branch made it wait for
+  // all of them, the prefetch lost).
+  for (uint32_t s0 = 0; s0 < ns; s0 += kRtPre) {
+#pragma unroll
+    for (uint32_t d = 0; d < kRtPre; d++) {
+      const v4f_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+      const v4f_t d00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][0], op[d][2], z, 0, 0, 0);
+      const v4f_t d01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][0], op[d][3], z, 0, 0, 0);
+      const v4f_t d10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][1], op[d][2], z, 0, 0, 0);
+      const v4f_t d11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][1], op[d][3], z, 0, 0, 0);
+      const uint32_t kn = 32 * min(s0 + d + kRtPre, ns - 1);  // the load kPre steps ahead (the last again past the end)
+      op[d][0] = *(const v8bf_t *)(pa + kn), op[d][1] = *(const v8bf_t *)(pb + kn);
+      op[d][2] = *(const v8bf_t *)(qa + kn), op[d][3] = *(const v8bf_t *)(qb + kn);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        acc[0][0][q] = __fadd_rn(acc[0][0][q], d00[q]), acc[0][1][q] = __fadd_rn(acc[0][1][q], d01[q]);
+        acc[1][0][q] = __fadd_rn(acc[1][0][q], d10[q]), acc[1][1][q] = __fadd_rn(acc[1][1][q], d11[q]);
+      }
     }
-    acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[0][0], 0, 0, 0);
-    acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b1, acc[0][1], 0, 0, 0);
-    acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b0, acc[1][0], 0, 0, 0);
-    acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[1][1], 0, 0, 0);
-    a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
   }
   if (w > 0) {
 #pragma unroll
@@ -337,10 +373,10 @@ __global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *W, const
     }
 }
 
-// Row e's exact logit for token t: sum over k ascending of bf16(W[e][k]) bf16(x[t][k]) in fp64 (each product exact,
-// one fused step a term: the oracle's k-order sum), rounded to fp32, + bias. One lane.
-__device__ __forceinline__ float exact_logit(const uint16_t *W, const uint16_t *xb, uint32_t H, uint32_t e, uint32_t t,
-                                             const float *bias) {
+// Row e's exact logit for token t by the k-order chain: sum over k ascending of bf16(W[e][k]) bf16(x[t][k]) in fp64
+// (each product exact, one fused step a term: the oracle's arithmetic), rounded to fp32. One lane.
+__device__ __forceinline__ float exact_logit_chain(const uint16_t *W, const uint16_t *xb, uint32_t H, uint32_t e,
+                                                   uint32_t t) {
   const uint4 *wr = (const uint4 *)(W + (uint64_t)e * H), *xr = (const uint4 *)(xb + (uint64_t)t * H);
   double acc = 0.0;
   for (uint32_t k = 0; k < H / 8; k++) {
@@ -352,24 +388,26 @@ __device__ __forceinline__ float exact_logit(const uint16_t *W, const uint16_t *
       acc = __builtin_fma((double)__uint_as_float(aw[i] & 0xffff0000u), (double)__uint_as_float(bw[i] & 0xffff0000u), acc);
     }
   }
-  const float lg = (float)acc;
-  return bias ? __fadd_rn(lg, bias[e]) : lg;
+  return (float)acc;
 }
 
 // Top-k on the approximate logits, certified: with B the token's bound, the K winners and their order stand when each
 // of the K + 1 largest keys exceeds the next by more than 2 B. Otherwise every expert whose logit may reach the K-th
-// (approximate logit >= the K-th's - 2 B) is summed again exactly and the selection runs on those exact logits (the
-// others cannot be among the K). The shared gate's row E is summed here in fp32 (it only scales the shared expert's
-// output). cnt_exact counts the tokens that needed the exact sums.
-__global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint16_t *W, const uint16_t *xb,
-                                                      const float *xn, uint32_t T, uint32_t E, uint32_t H, uint32_t K,
-                                                      const float *bias, float gamma_rmax, float bias_max,
-                                                      int32_t *ids, float *w, float *gs, unsigned long long *masks,
-                                                      uint32_t *cnt_exact) {
+// (approximate logit >= the K-th's - 2 B) is summed again exactly, eight lanes an expert (or one lane's k-order chain
+// where the exactness condition fails), and the selection runs on those exact logits (the others cannot be among the
+// K). The shared gate's row E is summed here in fp32 (it only scales the shared expert's output). cnt_exact counts
+// the tokens that needed the exact sums.
+__global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint16_t *W, const int *rlsb,
+                                                      const uint16_t *xb, const float *xn, const int *xlsb, uint32_t T,
+                                                      uint32_t E, uint32_t H, uint32_t K, const float *bias,
+                                                      float gamma_rmax, float bias_max, int32_t *ids, float *w,
+                                                      float *gs, unsigned long long *masks, uint32_t *cnt_exact) {
   __shared__ uint64_t tab[32];
+  __shared__ uint32_t cand[kPfWG / 64][kMaxRouteExperts];
+  __shared__ float exact[kPfWG / 64][kMaxRouteExperts];
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
-  const uint32_t t = blockIdx.x * (kPfWG / 64) + wave_id(), lane = lane_id();
+  const uint32_t t = blockIdx.x * (kPfWG / 64) + wave_id(), lane = lane_id(), wv = wave_id();
   if (t >= T) return;
   float *lg = logits + (uint64_t)t * (E + 1);
   uint32_t key[kRoutePer], id[kRoutePer], my_id, my_key;
@@ -411,10 +449,69 @@ __global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint1
   const bool open = lane + 1 < K1 && !(v - nxt > 2.0 * B);
   if (__ballot(open) != 0ull) {
     const double thr = __shfl(v, (int)K - 1, 64) - 2.0 * B;
+    // The candidates, packed in expert order.
+    uint32_t nc = 0;
 #pragma unroll
     for (int i = 0; i < kRoutePer; i++) {
       const uint32_t e = lane + 64 * i;
-      if (e < E && (double)key_float(key[i]) >= thr) key[i] = float_key(exact_logit(W, xb, H, e, t, bias));
+      const bool c = e < E && (double)key_float(key[i]) >= thr;
+      const uint64_t bal = __ballot(c);
+      if (c) cand[wv][nc + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u))] = e;
+      nc += (uint32_t)__popcll(bal);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    // Eight lanes a candidate: lane s of group j sums the row's eighth s in fp64 (and its magnitudes), the group adds
+    // its eight partials in a fixed tree; exact when the magnitudes' sum is below 2^(lsb_w + lsb_x + 53).
+    const uint32_t j = lane / 8, sl = lane % 8, H8 = H / 8;
+    for (uint32_t c0 = 0; c0 < nc; c0 += 8) {
+      const uint32_t ci = c0 + j, e = cand[wv][min(ci, nc - 1)];
+      const uint4 *wr = (const uint4 *)(W + (uint64_t)e * H + sl * H8), *xr = (const uint4 *)(xb + (uint64_t)t * H + sl * H8);
+      double acc = 0.0, mag = 0.0;
+      uint32_t emin = 0xffffffffu;  // the least sum of the two exponent fields of a product, two 16-bit halves
+      // Eight 16-byte pieces of the row and of x in flight at a time (one memory latency a chunk, not a piece).
+      for (uint32_t k0 = 0; k0 < H8 / 8; k0 += 8) {
+        uint4 a[8], b[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) a[q] = wr[k0 + q], b[q] = xr[k0 + q];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          const uint32_t aw[4] = {a[q].x, a[q].y, a[q].z, a[q].w}, bw[4] = {b[q].x, b[q].y, b[q].z, b[q].w};
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            // Each half's exponent fields (at most 255 each) added, the halves apart (no carry between them); a
+            // zero or subnormal value counts as exponent 0 (its lsb is at least that low: a safe underestimate).
+            const uint32_t es = ((aw[i] >> 7) & 0x00ff00ffu) + ((bw[i] >> 7) & 0x00ff00ffu);
+            emin = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2_t, emin),
+                                                                          __builtin_bit_cast(u16x2_t, es)));
+            const double p0 = (double)__uint_as_float(aw[i] << 16) * (double)__uint_as_float(bw[i] << 16);
+            const double p1 = (double)__uint_as_float(aw[i] & 0xffff0000u) * (double)__uint_as_float(bw[i] & 0xffff0000u);
+            acc = __dadd_rn(__dadd_rn(acc, p0), p1);
+            mag = __dadd_rn(__dadd_rn(mag, fabs(p0)), fabs(p1));
+          }
+        }
+      }
+      uint32_t em = min(emin & 0xffffu, emin >> 16);
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) {
+        acc = __dadd_rn(acc, __shfl_xor(acc, o, 64));
+        mag = __dadd_rn(mag, __shfl_xor(mag, o, 64));
+        em = min(em, (uint32_t)__shfl_xor((int)em, o, 64));
+      }
+      // Every product is a multiple of 2^(em - 268) (exponent fields less 127 each, less 7 mantissa bits each), and of
+      // 2^(rlsb + xlsb): exact when the magnitudes' sum stays below 2^53 times the larger of the two.
+      const int lsb = max((int)em - 268, rlsb[e] + xlsb[t]);
+      const bool exact_ok = mag * (1.0 + 0x1p-40) < ldexp(1.0, lsb + 53);
+      float lgv = (float)acc;
+      if (!exact_ok && sl == 0 && ci < nc) lgv = exact_logit_chain(W, xb, H, e, t);
+      if (sl == 0 && ci < nc) exact[wv][e] = bias ? __fadd_rn(lgv, bias[e]) : lgv;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < kRoutePer; i++) {
+      const uint32_t e = lane + 64 * i;
+      if (e < E && (double)key_float(key[i]) >= thr) key[i] = float_key(exact[wv][e]);
     }
     if (lane == 0) atomicAdd(cnt_exact, 1u);
     uint32_t kc[kRoutePer], ic[kRoutePer];
@@ -1461,7 +1558,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
   } else {
     {
       HookScope k(hook, "pf_xprep", st);
-      pf_xprep<<<(T + 3) / 4, kPfWG, 0, st>>>(x, T, H, E, b.xb, b.xn, b.masks);
+      pf_xprep<<<(T + 3) / 4, kPfWG, 0, st>>>(x, T, H, E, b.xb, b.xn, b.xlsb, b.masks);
     }
     {
       HookScope k(hook, "pf_router", st);
@@ -1470,9 +1567,9 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     }
     {
       HookScope k(hook, "pf_topk", st);
-      // 1.01 n 2^-23 with n = H / 4 + 4 additions a result (the waves' chains, then their partials).
-      const float gamma = (float)(1.01 * (H / 4 + 4) * 0x1p-23);
-      pf_topk_cert<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, L.router, b.xb, b.xn, T, E, H, K, L.bias,
+      // 1.01 n 2^-23, n = 31 + H / 128 + 3 roundings a product may meet (see pf_router_bf16).
+      const float gamma = (float)(1.01 * (31 + H / 128 + 3) * 0x1p-23);
+      pf_topk_cert<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, L.router, L.rlsb, b.xb, b.xn, b.xlsb, T, E, H, K, L.bias,
                                                   gamma * L.rmax * 1.0001f, L.bias_max, b.ids, b.w,
                                                   S.has_shared ? b.gs : nullptr, b.masks, b.cnt_exact);
     }

@@ -45,6 +45,7 @@ struct PfLayer {
   const uint8_t *shared;
   uint64_t sh_up_off, sh_down_off;
   const uint8_t *codebooks;  // the caller's codebooks (QGRID layout) for IQ3_XXS and IQ2_S
+  const int *rlsb;           // per routed row: the least lsb of its bf16 values (the exact-sum condition)
   float rmax;                // the largest ||W_e||_2 over the routed rows (bf16 values), rounded up
   float bias_max;            // the largest |bias_e| (0 without a bias)
 };
@@ -55,6 +56,7 @@ struct PfBufs {
   float *logits;           // Tmax x (E + 1)
   uint16_t *xb;            // Tmax x H: bf16(x), for the matrix-core router
   float *xn;               // Tmax: ||bf16(x_t)||_2, rounded up
+  int *xlsb;               // Tmax: the least lsb of bf16(x_t)'s values
   uint32_t *cnt_exact;     // tokens whose top-k needed exact sums (accumulates until read)
   int32_t *ids;            // Tmax x K
   float *w, *gs;           // Tmax x K, Tmax

@@ -193,6 +193,32 @@ MOE_API moe_status moe_forward_hc_async(moe_ctx *ctx, uint32_t layer, float *R_d
 MOE_API moe_status moe_forward_hc(moe_ctx *ctx, uint32_t layer, float *R, uint32_t ntok, float *y,
                                   moe_route_out *route);
 
+/* Experts on the CPU (the hybrid of core/models/qwen4exp: layout.h:64-71 MissJob, layer.cl:838-884, model.cpp:1597-
+ * 1627). resident (n_expert flags; null: all) says which routed experts of a layer the device holds; a decode forward
+ * (up to 16 tokens) computes only those, and for each token publishes its misses in a record in host memory: */
+typedef struct {
+  uint32_t seq;       /* the forward's step (moe_last_step), stored last, behind a system-scope release */
+  uint32_t nmiss;     /* routed experts of the token not resident */
+  int32_t ids[16];    /* the misses' ids in rank order, then their weights */
+  float w[16];
+  int32_t all[16];    /* every routed id in rank order */
+  /* followed by float x[n_embd]: the block's input for the token */
+} moe_miss_job;
+/* The host answers with ans_y[t] = its experts' sum over token t's misses, w in rank order (CpuExperts::compute_many
+ * on the misses as jobs: y overwritten, then each job's w * out added in order), for every token with nmiss > 0, then
+ * stores *ans_seq = the step (release). The forward's combine for such a token waits for that store (bounded: a
+ * forward whose answer does not come within seconds reports MOE_TIMEOUT through moe_check) and adds ans_y[t]'s row
+ * after the resident experts' terms and the shared expert's, as layer.cl:869-884 does. Tokens without misses do not
+ * wait. The prefill path refuses a layer with non-resident experts. */
+MOE_API moe_status moe_set_resident(moe_ctx *ctx, uint32_t layer, const uint8_t *resident);
+/* The records and the answer, allocated in pinned host memory on the first call and kept until moe_close: jobs (a
+ * moe_miss_job record a token, job_stride bytes apart, room for min(max_tokens, 16) tokens), ans_y (16 x n_embd
+ * floats), ans_seq. A layer with misses needs them set up before its forwards. */
+MOE_API moe_status moe_miss_buffers(moe_ctx *ctx, void **jobs, uint64_t *job_stride, float **ans_y,
+                                    uint32_t **ans_seq);
+/* The step number of the last forward enqueued on ctx (what its records' seq and the answer's seq must hold). */
+MOE_API uint32_t moe_last_step(const moe_ctx *ctx);
+
 /* Waits for the context's stream. */
 MOE_API moe_status moe_sync(moe_ctx *ctx);
 /* Waits for stream (null: the context's stream), then reports whether any forward since the last check had a wait
@@ -218,9 +244,15 @@ MOE_API moe_status moe_kernel_times(moe_ctx *ctx, const char **names, float *avg
  * computed, end) quadruples in item order, up to cap of them (a cap past n copies the rest of the 65536-quadruple
  * buffer too); n receives the number of items, bounds (8 entries, or null) where each kind begins: lead (router
  * rows; the hyper-connection mix's items, when moe_forward_hc ran, are the ones before it), top-k, the shared expert's gate/up and down (which run beside the router), the routed gate/up and down, the
- * combine, and the end. The items before the routed ones ran on work-group i mod moe_grid(ctx); the routed ones are
- * dealt out dynamically. */
+ * combine, and the end. Items are dealt to the work-groups in order from one counter, as they ask. */
 MOE_API uint32_t moe_grid(const moe_ctx *ctx);
+/* Sets the decode kernel's grid, a multiple of 8 (0: back to what the device holds at once, the default). Any such
+ * grid completes, whatever part of it the device admits at a time (another stream's kernels holding CUs, or a grid
+ * larger than the device holds): the dispatcher deals work-groups to the eight XCDs in turn and each XCD starts its
+ * share in index order, and every item's dependencies come earlier in that order, so the precondition is only that
+ * each XCD eventually admits work-groups of the kernel. No counterpart in the reference (its kernel list has no
+ * persistent kernel). */
+MOE_API moe_status moe_set_grid(moe_ctx *ctx, uint32_t grid);
 MOE_API moe_status moe_set_trace(moe_ctx *ctx, int on);
 MOE_API moe_status moe_trace(moe_ctx *ctx, uint64_t *stamps, uint32_t cap, uint32_t *n, uint32_t *bounds);
 

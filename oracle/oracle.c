@@ -891,6 +891,59 @@ done:
   return rc;
 }
 
+/* The block with some routed experts off the device (the hybrid: layer.cl:869-884): per token the resident experts'
+ * outputs summed in rank order (compute_many on those jobs), + gs s, + the misses' sum (compute_many on the misses in
+ * rank order, the CPU's answer), each sum rounded as it is added. resident: n_expert flags. */
+int orc_moe_forward_resident(const orc_layer *L, const uint8_t *resident, const float *x, uint32_t ntok,
+                             uint64_t x_stride, float *y, uint64_t y_stride, int nthreads) {
+  const uint32_t E = L->n_expert, H = L->n_embd, k = L->n_used;
+  if (ntok == 0) return 0;
+  float *lg = (float *)malloc(sizeof(float) * ntok * (E + 1));
+  int32_t *ids = (int32_t *)malloc(sizeof(int32_t) * ntok * k);
+  float *w = (float *)malloc(sizeof(float) * ntok * k);
+  orc_job *jobs = (orc_job *)malloc(sizeof(orc_job) * ntok * k);
+  float *s = (float *)malloc(sizeof(float) * ntok * H), *cpu = (float *)malloc(sizeof(float) * ntok * H);
+  orc_shape sh = {L->gate_type, L->down_type, H, L->n_ff, L->swiglu_limit, 0};
+  int rc = orc_route(L->router, L->bias, E, H, k, x, ntok, x_stride, lg, ids, w);
+  uint32_t n = 0;
+  if (rc) goto done;
+  for (int pass = 0; pass < 2; pass++) { /* 0: the resident jobs into y; 1: the misses into cpu */
+    n = 0;
+    for (uint32_t t = 0; t < ntok; t++)
+      for (uint32_t r = 0; r < k; r++) {
+        const int32_t e = ids[t * k + r];
+        if ((resident[e] != 0) != (pass == 0)) continue;
+        orc_job *j = &jobs[n++];
+        j->gate = L->gate[e], j->up = L->up[e], j->down = L->down[e];
+        j->tok = t, j->w = w[t * k + r];
+      }
+    rc = orc_compute_many(&sh, jobs, n, ntok, x, x_stride, pass ? cpu : y, pass ? H : y_stride, nthreads);
+    if (rc) goto done;
+  }
+  if (L->sh_gate) {
+    for (uint32_t t = 0; t < ntok; t++) {
+      jobs[t].gate = L->sh_gate, jobs[t].up = L->sh_up, jobs[t].down = L->sh_down;
+      jobs[t].tok = t, jobs[t].w = 1.0f;
+    }
+    orc_shape ss = {L->sh_gate_type, L->sh_down_type, H, L->n_ff, L->swiglu_limit, L->sh_up_type};
+    rc = orc_compute_many(&ss, jobs, ntok, ntok, x, x_stride, s, H, nthreads);
+    if (rc) goto done;
+  }
+  for (uint32_t t = 0; t < ntok; t++) {
+    const float gs = 1.0f / (1.0f + expf(-lg[(uint64_t)t * (E + 1) + E]));
+    uint32_t miss = 0;
+    for (uint32_t r = 0; r < k; r++) miss += resident[ids[t * k + r]] == 0;
+    float *yt = y + t * y_stride;
+    for (uint32_t i = 0; i < H; i++) {
+      if (L->sh_gate) yt[i] = yt[i] + gs * s[(uint64_t)t * H + i];
+      if (miss) yt[i] = yt[i] + cpu[(uint64_t)t * H + i];
+    }
+  }
+done:
+  free(lg), free(ids), free(w), free(jobs), free(s), free(cpu);
+  return rc;
+}
+
 /* ---------------------------------------------------------------------------------------------------------------
  * The hyper-connection mix and combine around the block (docs/spec/MODEL_LAYER.md 1.1-1.2: build_hc_mix and
  * build_hc_combine; the CPU ops ggml_compute_forward_rms_norm_f32 and the BF16 products, whose fp32 sums run in an

@@ -104,6 +104,11 @@ int orc_topk_logits(const float *logits, uint32_t n_expert, uint32_t k, int32_t 
 int orc_moe_forward(const orc_layer *L, const float *x, uint32_t ntok, uint64_t x_stride, float *y, uint64_t y_stride,
                     int32_t *ids, float *w, int nthreads);
 
+/* The block with the experts whose resident flag is 0 computed apart (the CPU's answer) and added after the shared
+ * expert's term, as the device combines them. */
+int orc_moe_forward_resident(const orc_layer *L, const uint8_t *resident, const float *x, uint32_t ntok,
+                             uint64_t x_stride, float *y, uint64_t y_stride, int nthreads);
+
 /* The CPU baseline (cpu_fast.c): the same block, the same bits as orc_moe_forward, with SIMD integer dot products
  * (AVX-512BW when the CPU has it, else AVX2), the router's rows as SIMD lanes each summed in k order, and
  * OpenMP over rows. Returns 0 or -1. orc_fast_isa names the instruction set it uses. */

@@ -43,6 +43,7 @@ def _load_oracle():
         "orc_moe_forward": (C.c_int, [_P, _P, C.c_uint32, C.c_uint64, _P, C.c_uint64, _P, _P, C.c_int]),
         "orc_fast_moe_forward": (C.c_int, [_P, _P, C.c_uint32, C.c_uint64, _P, C.c_uint64, _P, _P, C.c_int]),
         "orc_fast_isa": (C.c_char_p, []),
+        "orc_moe_forward_resident": (C.c_int, [_P, _P, _P, C.c_uint32, C.c_uint64, _P, C.c_uint64, C.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(o, name)
@@ -339,6 +340,38 @@ def check_block(y, ids, w, yo, io, wo, exact=True):
         assert np.array_equal(y, yo), "y not bit-exact: max-abs %g rel-L2 %g" % (ma, rl)
     else:
         assert max_abs(w, wo) <= W_TOL, max_abs(w, wo)
+
+
+class Dev:
+    """Device buffers through the HIP runtime (ctypes)."""
+
+    def __init__(self):
+        self.rt = C.CDLL("libamdhip64.so")
+        self.rt.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        self.rt.hipFree.argtypes = [C.c_void_p]
+        self.rt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        self.bufs = []
+
+    def alloc(self, n):
+        p = C.c_void_p()
+        assert self.rt.hipMalloc(C.byref(p), max(n, 256)) == 0
+        self.bufs.append(p)
+        return p
+
+    def put(self, a):
+        p = self.alloc(a.nbytes)
+        assert self.rt.hipMemcpy(p, a.ctypes.data_as(C.c_void_p), a.nbytes, 1) == 0
+        return p
+
+    def get(self, p, shape, dtype):
+        a = np.empty(shape, dtype)
+        assert self.rt.hipMemcpy(a.ctypes.data_as(C.c_void_p), p, a.nbytes, 2) == 0
+        return a
+
+    def free(self):
+        for p in self.bufs:
+            self.rt.hipFree(p)
+        self.bufs = []
 
 
 def tokens(seed, T, H, stream=999):

@@ -297,3 +297,4 @@ def test_codebooks_required_and_checked():
     y, ids, w = blk.forward(0, x)
     check_block(y, ids, w, *L.oracle_forward(x))
     blk.close()
+

@@ -14,36 +14,7 @@ from tests.harness import moe
 pytestmark = pytest.mark.gpu
 
 
-class Dev:
-    """Device buffers through the HIP runtime (ctypes)."""
-
-    def __init__(self):
-        self.rt = C.CDLL("libamdhip64.so")
-        self.rt.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
-        self.rt.hipFree.argtypes = [C.c_void_p]
-        self.rt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
-        self.bufs = []
-
-    def alloc(self, n):
-        p = C.c_void_p()
-        assert self.rt.hipMalloc(C.byref(p), max(n, 256)) == 0
-        self.bufs.append(p)
-        return p
-
-    def put(self, a):
-        p = self.alloc(a.nbytes)
-        assert self.rt.hipMemcpy(p, a.ctypes.data_as(C.c_void_p), a.nbytes, 1) == 0
-        return p
-
-    def get(self, p, shape, dtype):
-        a = np.empty(shape, dtype)
-        assert self.rt.hipMemcpy(a.ctypes.data_as(C.c_void_p), p, a.nbytes, 2) == 0
-        return a
-
-    def free(self):
-        for p in self.bufs:
-            self.rt.hipFree(p)
-        self.bufs = []
+Dev = h.Dev
 
 
 def run(blk, dev, fn, x, layer=0):
