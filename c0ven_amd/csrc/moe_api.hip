@@ -42,6 +42,7 @@ bool pow2(uint32_t v) { return v && !(v & (v - 1)); }
 
 struct Layer {
   uint16_t *router = nullptr;
+  uint16_t *router_t = nullptr;  // the routed rows in 16 x 32 tiles (the prefill router's operand)
   float *bias = nullptr;
   bool has_bias = false;
   float rmax = 0.0f, bias_max = 0.0f;  // the largest routed row norm and |bias| (the prefill router's bound)
@@ -430,7 +431,7 @@ void forward_dev(moe_ctx *c, uint32_t layer, const float *x, uint32_t T, float *
     require(!L.has_miss, "the prefill path takes only layers whose experts are all on the device (moe_set_resident)");
     PfShape S{g.n_embd, g.n_ff, g.n_expert, K, T, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type,
               g.has_shared, g.swiglu_limit, g.sh_up_type, (g.flags & MOE_FLAG_EXACT_ROUTER) ? 1u : 0u};
-    PfLayer PL{L.router, L.has_bias ? L.bias : nullptr, L.experts, c->ex_bytes, c->ex_up, c->ex_down, L.shared,
+    PfLayer PL{L.router, L.router_t, L.has_bias ? L.bias : nullptr, L.experts, c->ex_bytes, c->ex_up, c->ex_down, L.shared,
                c->sh_up, c->sh_down, c->codebooks, L.rlsb, L.rmax, L.bias_max};
     PfHook hook{c->timing ? timing_hook : nullptr, c};
     check(prefill_forward(S, PL, c->pf, x, y, s, hook), "prefill launch");
@@ -525,6 +526,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
       L.router = c->alloc<uint16_t>((uint64_t)(E + 1) * H);
       L.bias = c->alloc<float>(E);
       L.rlsb = c->alloc<int>(E);
+      L.router_t = c->alloc<uint16_t>((uint64_t)(E + 15) / 16 * 16 * H);
       L.resident = c->alloc<uint8_t>(E);
       L.experts = c->alloc<uint8_t>(c->ex_bytes * E);
       if (g.has_shared) L.shared = c->alloc<uint8_t>(c->sh_bytes);
@@ -558,6 +560,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
                     : b.act_r;
       b.logits = c->alloc<float>((uint64_t)TM * (E + 1));
       b.xb = c->alloc<uint16_t>((uint64_t)TM * H);
+      b.xt = c->alloc<uint16_t>((uint64_t)(TM + 15) / 16 * 16 * H);
       b.xn = c->alloc<float>(TM);
       b.xlsb = c->alloc<int>(TM);
       b.cnt_exact = c->alloc<uint32_t>(1);
@@ -704,6 +707,14 @@ MOE_API moe_status moe_load_router(moe_ctx *c, uint32_t layer, const uint16_t *r
         if (b & 0x7fffu) lsb[e] = std::min(lsb[e], ex == 0 ? -133 : (int)ex - 134);
       }
     check(hipMemcpy(L.rlsb, lsb.data(), lsb.size() * sizeof(int), hipMemcpyHostToDevice), "upload row lsb");
+    // The routed rows in 16 x 32 tiles: tile (row / 16, k / 32) at ((row / 16) (H / 32) + k / 32) 512, a row's 32
+    // values contiguous inside it.
+    const uint32_t H = c->cfg.n_embd, E = c->cfg.n_expert;
+    std::vector<uint16_t> tiled((uint64_t)(E + 15) / 16 * 16 * H, 0);
+    for (uint32_t e = 0; e < E; e++)
+      for (uint32_t k = 0; k < H; k++)
+        tiled[((uint64_t)(e / 16) * (H / 32) + k / 32) * 512 + (e % 16) * 32 + k % 32] = router[(uint64_t)e * H + k];
+    check(hipMemcpy(L.router_t, tiled.data(), tiled.size() * 2, hipMemcpyHostToDevice), "upload tiled router");
     L.bias_max = 0.0f;
     if (bias)
       for (uint32_t e = 0; e < c->cfg.n_expert; e++) L.bias_max = std::max(L.bias_max, std::fabs(bias[e]));
@@ -1045,7 +1056,7 @@ MOE_API moe_status moe_compute_many(moe_ctx *c, const moe_cm_job *jobs, uint32_t
       check(hipMemcpyAsync(c->pf.w, w.data(), sizeof(float) * w.size(), hipMemcpyHostToDevice, s), "w");
       PfShape S{H, F, c->bc_slots, K, ntok, g.gate_type, g.down_type, g.sh_gate_type, g.sh_down_type, 0, g.swiglu_limit,
                 g.sh_up_type};
-      PfLayer PL{nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0, c->codebooks, nullptr, 0.0f, 0.0f};
+      PfLayer PL{nullptr, nullptr, nullptr, c->bc_base, c->ex_bytes, c->ex_up, c->ex_down, nullptr, 0, 0, c->codebooks, nullptr, 0.0f, 0.0f};
       PfHook hook{c->timing ? timing_hook : nullptr, c};
       check(prefill_jobs(S, PL, c->pf, c->x_dev, c->y_dev, s, hook), "prefill launch");
       c->last_ids = c->pf.ids, c->last_w = c->pf.w, c->last_pf_T = ntok;

@@ -23,6 +23,7 @@
 namespace c0ven {
 
 constexpr uint32_t kMaxRouteExperts = 512;  // routed experts a layer may have
+constexpr uint32_t kRouterLdsH = 4096;       // n_embd up to which an open token's x is staged in LDS
 
 __device__ __constant__ static const uint32_t kIq3sGridPf[512] = {C0VEN_IQ3S_GRID_VALUES};
 
@@ -220,7 +221,7 @@ __global__ void __launch_bounds__(kPfWG) pf_topk(const float *logits, uint32_t T
   if (t >= T) return;
   const float *lg = logits + (uint64_t)t * (E + 1);
   uint32_t key[kRoutePer], id[kRoutePer], my_id, my_key;
-  route_load(lg, E, lane, key, id);
+  route_load<false>(lg, E, lane, key, id);
   float mx, inv;
   route_norm(key, E, lane, tab, &mx, &inv);
   route_select(key, id, K, lane, &my_id, &my_key);
@@ -262,13 +263,25 @@ __device__ __forceinline__ int bf16_lsb(uint32_t b) {
 
 // x to bf16 (round to nearest even), its norm ||bf16(x_t)||_2 rounded up and the least lsb of its values; the dispatch
 // masks cleared. One wave a token.
+// bf16 operands of the router's matrix-core products in tiles of 16 rows x 32 values (1 KB, the 32 values of a row
+// contiguous), tile (row / 16, k / 32) at ((row / 16) (H / 32) + k / 32) 512 elements: a wave's operand load of one
+// tile reads its 1 KB whole, and a row block's K walk is one contiguous run.
+__device__ __forceinline__ uint64_t tile16x32(uint32_t row, uint32_t k, uint32_t H) {
+  return ((uint64_t)(row / 16) * (H / 32) + k / 32) * 512 + (row % 16) * 32 + k % 32;
+}
+
 __global__ void __launch_bounds__(kPfWG) pf_xprep(const float *x, uint32_t T, uint32_t H, uint32_t E, uint16_t *xb,
-                                                  float *xn, int *xlsb, unsigned long long *masks) {
+                                                  uint16_t *xt, float *xn, int *xlsb, unsigned long long *masks,
+                                                  const uint16_t *wg, float *logits, float *gs) {
+  __shared__ uint64_t tab[32];
+  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
   const uint32_t t = blockIdx.x * (kPfWG / 64) + wave_id(), lane = lane_id();
   for (uint32_t i = blockIdx.x * kPfWG + threadIdx.x; i < pf_windows(T) * E; i += gridDim.x * kPfWG) masks[i] = 0ull;
   if (t >= T) return;
   double ss = 0.0;
   int lsb = 1 << 20;
+  double gpart = 0.0;  // the shared gate's row against bf16(x): exact products, fp64 partials a lane
   for (uint32_t k = 8 * lane; k < H; k += 512) {
     const float4 *p = (const float4 *)(x + (uint64_t)t * H + k);
     const float4 a = p[0], b = p[1];
@@ -283,13 +296,29 @@ __global__ void __launch_bounds__(kPfWG) pf_xprep(const float *x, uint32_t T, ui
       o[i] = (__float_as_uint(r0) >> 16) | (__float_as_uint(r1) & 0xffff0000u);
       lsb = min(lsb, min(bf16_lsb(o[i] & 0xffffu), bf16_lsb(o[i] >> 16)));
     }
+    if (gs) {
+      const uint4 a = *(const uint4 *)(wg + k);
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        gpart = __builtin_fma((double)__uint_as_float(aw[i] << 16), (double)__uint_as_float(o[i] << 16), gpart);
+        gpart = __builtin_fma((double)__uint_as_float(aw[i] & 0xffff0000u),
+                              (double)__uint_as_float(o[i] & 0xffff0000u), gpart);
+      }
+    }
     *(uint4 *)(xb + (uint64_t)t * H + k) = make_uint4(o[0], o[1], o[2], o[3]);
+    *(uint4 *)(xt + tile16x32(t, k, H)) = make_uint4(o[0], o[1], o[2], o[3]);
   }
   const double tot = wave_sum_f64(ss);
   lsb = -(int)wave_max_u32((uint32_t)(-lsb + (1 << 21))) + (1 << 21);
+  const float le = gs ? (float)wave_sum_f64(gpart) : 0.0f;
   if (lane == 0) {
     xn[t] = (float)(sqrt(tot) * (1.0 + 0x1p-40)) * (1.0f + 0x1p-22f);
     xlsb[t] = lsb;
+    if (gs) {  // the shared gate's logit (fp64 partials in another order than the oracle's chain: within the tolerance)
+      logits[(uint64_t)t * (E + 1) + E] = le;
+      gs[t] = sigmoid_libm(le, tab);
+    }
   }
 }
 
@@ -300,7 +329,7 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 // blocks run on one XCD, so its bf16 x is fetched into that XCD's L2 once), wave w summing K range [w H / 4,
 // (w + 1) H / 4). Operands straight from memory (the router's bf16 rows and the prepared bf16 x), kPre steps ahead.
 constexpr uint32_t kRtPre = 4;  // steps of loads in flight; a wave's K steps (H / 128) are a multiple of it
-__global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *W, const uint16_t *xb, uint32_t T, uint32_t E,
+__global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *Wt, const uint16_t *xt, uint32_t T, uint32_t E,
                                                         uint32_t H, const float *bias, float *logits) {
   __shared__ v4f_t part[3][4][64];
   const uint32_t nrb = (E + 31) / 32, ntb = (T + 31) / 32, n = nrb * ntb;
@@ -308,11 +337,13 @@ __global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *W, const
   const uint32_t L = xcd_logical(blockIdx.x, n), e0 = 32 * (L % nrb), t0 = 32 * (L / nrb);
   const uint32_t l = lane_id(), w = wave_id(), g = l / 16, c16 = l % 16;
   const uint32_t kq = H / 4, k0 = w * kq, ns = kq / 32;
-  // Rows past E and tokens past T read row / token 0 (valid memory); their results are never stored.
-  const uint32_t ra = e0 + c16 < E ? e0 + c16 : 0u, rb = e0 + 16 + c16 < E ? e0 + 16 + c16 : 0u;
-  const uint32_t ta = t0 + c16 < T ? t0 + c16 : 0u, tb = t0 + 16 + c16 < T ? t0 + 16 + c16 : 0u;
-  const uint16_t *pa = W + (uint64_t)ra * H + k0 + 8 * g, *pb = W + (uint64_t)rb * H + k0 + 8 * g;
-  const uint16_t *qa = xb + (uint64_t)ta * H + k0 + 8 * g, *qb = xb + (uint64_t)tb * H + k0 + 8 * g;
+  // Tiles past E rows or T tokens (the last 16-row tile's rows past them are whatever the buffers hold) read tile 0;
+  // their results are never stored. A step advances one tile: 512 elements.
+  const uint32_t ra = e0 < E ? e0 : 0u, rb = e0 + 16 < E ? e0 + 16 : 0u;
+  const uint32_t ta = t0 < T ? t0 : 0u, tb = t0 + 16 < T ? t0 + 16 : 0u;
+  const uint32_t lo = c16 * 32 + 8 * g;  // the lane's 8 values in a tile
+  const uint16_t *pa = Wt + tile16x32(ra, k0, H) + lo, *pb = Wt + tile16x32(rb, k0, H) + lo;
+  const uint16_t *qa = xt + tile16x32(ta, k0, H) + lo, *qb = xt + tile16x32(tb, k0, H) + lo;
   v4f_t acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; i++)
@@ -321,7 +352,7 @@ __global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *W, const
   v8bf_t op[kRtPre][4];
 #pragma unroll
   for (uint32_t d = 0; d < kRtPre; d++) {
-    const uint32_t k = 32 * min(d, ns - 1);
+    const uint32_t k = 512 * min(d, ns - 1);
     op[d][0] = *(const v8bf_t *)(pa + k), op[d][1] = *(const v8bf_t *)(pb + k);
     op[d][2] = *(const v8bf_t *)(qa + k), op[d][3] = *(const v8bf_t *)(qb + k);
   }
@@ -335,7 +366,7 @@ __global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *W, const
       const v4f_t d01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][0], op[d][3], z, 0, 0, 0);
       const v4f_t d10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][1], op[d][2], z, 0, 0, 0);
       const v4f_t d11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][1], op[d][3], z, 0, 0, 0);
-      const uint32_t kn = 32 * min(s0 + d + kRtPre, ns - 1);  // the load kPre steps ahead (the last again past the end)
+      const uint32_t kn = 512 * min(s0 + d + kRtPre, ns - 1);  // the load kPre steps ahead (the last again past the end)
       op[d][0] = *(const v8bf_t *)(pa + kn), op[d][1] = *(const v8bf_t *)(pb + kn);
       op[d][2] = *(const v8bf_t *)(qa + kn), op[d][3] = *(const v8bf_t *)(qb + kn);
 #pragma unroll
@@ -392,44 +423,28 @@ __device__ __forceinline__ float exact_logit_chain(const uint16_t *W, const uint
 }
 
 // Top-k on the approximate logits, certified: with B the token's bound, the K winners and their order stand when each
-// of the K + 1 largest keys exceeds the next by more than 2 B. Otherwise every expert whose logit may reach the K-th
-// (approximate logit >= the K-th's - 2 B) is summed again exactly, eight lanes an expert (or one lane's k-order chain
-// where the exactness condition fails), and the selection runs on those exact logits (the others cannot be among the
-// K). The shared gate's row E is summed here in fp32 (it only scales the shared expert's output). cnt_exact counts
-// the tokens that needed the exact sums.
+// of the K + 1 largest keys exceeds the next by more than 2 B. Otherwise only the experts whose place is open are
+// summed again exactly (sixteen lanes an expert, or one lane's k-order chain where the exactness condition fails):
+// a ranked expert whose interval meets a neighbour's, and, when the K-th place is open, every later expert whose
+// approximate logit reaches the K-th's - 2 B. The selection then runs again on the mixed keys. cnt_exact counts the
+// tokens that needed exact sums. (The shared gate's logit and gs come from pf_xprep.)
 __global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint16_t *W, const int *rlsb,
                                                       const uint16_t *xb, const float *xn, const int *xlsb, uint32_t T,
                                                       uint32_t E, uint32_t H, uint32_t K, const float *bias,
                                                       float gamma_rmax, float bias_max, int32_t *ids, float *w,
-                                                      float *gs, unsigned long long *masks, uint32_t *cnt_exact) {
+                                                      unsigned long long *masks, uint32_t *cnt_exact) {
   __shared__ uint64_t tab[32];
   __shared__ uint32_t cand[kPfWG / 64][kMaxRouteExperts];
-  __shared__ float exact[kPfWG / 64][kMaxRouteExperts];
+  __shared__ uint32_t xkey[kPfWG / 64][kMaxRouteExperts];  // 0, or an exactly summed expert's key (cleared after)
+  __shared__ __align__(16) uint16_t xrow[kPfWG / 64][kRouterLdsH];  // an open token's bf16 x, for its exact sums
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  for (uint32_t i = threadIdx.x; i < (kPfWG / 64) * kMaxRouteExperts; i += kPfWG) (&xkey[0][0])[i] = 0u;
   __syncthreads();
   const uint32_t t = blockIdx.x * (kPfWG / 64) + wave_id(), lane = lane_id(), wv = wave_id();
   if (t >= T) return;
   float *lg = logits + (uint64_t)t * (E + 1);
   uint32_t key[kRoutePer], id[kRoutePer], my_id, my_key;
-  route_load(lg, E, lane, key, id);
-  if (gs) {  // the shared gate: row E, fp32 partials a lane, summed over the wave in a fixed order
-    const uint16_t *we = W + (uint64_t)E * H;
-    float part = 0.0f;
-    for (uint32_t k = 8 * lane; k < H; k += 512) {
-      const uint4 a = *(const uint4 *)(we + k), b = *(const uint4 *)(xb + (uint64_t)t * H + k);
-      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        part = __builtin_fmaf(__uint_as_float(aw[i] << 16), __uint_as_float(bw[i] << 16), part);
-        part = __builtin_fmaf(__uint_as_float(aw[i] & 0xffff0000u), __uint_as_float(bw[i] & 0xffff0000u), part);
-      }
-    }
-    const float le = (float)wave_sum_f64((double)part);
-    if (lane == 0) {
-      lg[E] = le;
-      gs[t] = sigmoid_libm(le, tab);
-    }
-  }
+  route_load<false>(lg, E, lane, key, id);
   // The bound: the sum's rounding (gamma ||W||max ||x||) and the fp32 rounding of the sum and of the bias add.
   uint32_t mk = 0;
 #pragma unroll
@@ -445,38 +460,67 @@ __global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint1
     route_select(kc, ic, K1, lane, &my_id, &my_key);
   }
   const double v = (double)key_float(my_key);
-  const double nxt = __shfl_down(v, 1, 64);
+  const double nxt = __shfl_down(v, 1, 64), prv = __shfl_up(v, 1, 64);
+  // Rank r's order against rank r + 1 is open when their intervals (each +- B) meet.
   const bool open = lane + 1 < K1 && !(v - nxt > 2.0 * B);
+#ifdef C0VEN_EXP_NO_EXACT
+  if (false) {
+#else
   if (__ballot(open) != 0ull) {
+#endif
+    // The experts whose place is open: a ranked one whose interval meets a neighbour's, and, when the K-th place is
+    // open, every expert ranked after the K-th whose interval reaches the K-th's. The others keep their approximate
+    // logits: each is more than 2 B from every expert on one side of it, so its order against all of them stands.
+    const bool amb = lane < K1 && (open || (lane >= 1 && !(prv - v > 2.0 * B)));
+    const bool kopen = __shfl((int)open, (int)K - 1, 64) != 0 && K < E;
     const double thr = __shfl(v, (int)K - 1, 64) - 2.0 * B;
-    // The candidates, packed in expert order.
+    const uint32_t kK = __shfl(my_key, (int)K, 64), iK = __shfl(my_id, (int)K, 64);
     uint32_t nc = 0;
+    {
+      const uint64_t bal = __ballot(amb);
+      if (amb) cand[wv][__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u))] = my_id;
+      nc = (uint32_t)__popcll(bal);
+    }
 #pragma unroll
     for (int i = 0; i < kRoutePer; i++) {
       const uint32_t e = lane + 64 * i;
-      const bool c = e < E && (double)key_float(key[i]) >= thr;
+      const bool after = key[i] < kK || (key[i] == kK && e > iK);  // ranked after the (K + 1)-th
+      const bool c = kopen && e < E && after && (double)key_float(key[i]) >= thr;
       const uint64_t bal = __ballot(c);
       if (c) cand[wv][nc + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u))] = e;
       nc += (uint32_t)__popcll(bal);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
-    // Eight lanes a candidate: lane s of group j sums the row's eighth s in fp64 (and its magnitudes), the group adds
-    // its eight partials in a fixed tree; exact when the magnitudes' sum is below 2^(lsb_w + lsb_x + 53).
-    const uint32_t j = lane / 8, sl = lane % 8, H8 = H / 8;
-    for (uint32_t c0 = 0; c0 < nc; c0 += 8) {
+    // x's bf16 row into the wave's LDS, then sixteen lanes a candidate: lane s of group j sums the row's sixteenth s
+    // in fp64 (its magnitudes too, and the least exponent sum of its products), the group adds its sixteen partials
+    // in a fixed tree; exact when the magnitudes' sum is below 2^(lsb + 53).
+    const uint4 *xg = (const uint4 *)(xb + (uint64_t)t * H), *xs = xg;
+    if (H <= kRouterLdsH) {  // (a wider row is read from memory)
+      uint4 *xl = (uint4 *)&xrow[wv][0];
+      for (uint32_t k = lane; k < H / 8; k += 64) xl[k] = xg[k];
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      xs = xl;
+    }
+    const uint32_t j = lane / 16, sl = lane % 16, H16 = H / 16;  // H16 / 8 pieces of 16 B a lane
+    for (uint32_t c0 = 0; c0 < nc; c0 += 4) {
       const uint32_t ci = c0 + j, e = cand[wv][min(ci, nc - 1)];
-      const uint4 *wr = (const uint4 *)(W + (uint64_t)e * H + sl * H8), *xr = (const uint4 *)(xb + (uint64_t)t * H + sl * H8);
-      double acc = 0.0, mag = 0.0;
+      const uint4 *wr = (const uint4 *)(W + (uint64_t)e * H + sl * H16);
+      const uint4 *xr = xs + sl * H16 / 8;
+      // Four chains (piece q % 4): when the sum is exact (checked below) every order gives it, so the chains and the
+      // tree that joins them need not follow k.
+      double acc4[4] = {0.0, 0.0, 0.0, 0.0}, mag4[4] = {0.0, 0.0, 0.0, 0.0};
       uint32_t emin = 0xffffffffu;  // the least sum of the two exponent fields of a product, two 16-bit halves
-      // Eight 16-byte pieces of the row and of x in flight at a time (one memory latency a chunk, not a piece).
-      for (uint32_t k0 = 0; k0 < H8 / 8; k0 += 8) {
-        uint4 a[8], b[8];
+      for (uint32_t k0 = 0; k0 < H16 / 8; k0 += 16) {  // sixteen pieces of the row in flight at a time
+        uint4 a[16];
 #pragma unroll
-        for (int q = 0; q < 8; q++) a[q] = wr[k0 + q], b[q] = xr[k0 + q];
+        for (int q = 0; q < 16; q++) a[q] = k0 + q < H16 / 8 ? wr[k0 + q] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-          const uint32_t aw[4] = {a[q].x, a[q].y, a[q].z, a[q].w}, bw[4] = {b[q].x, b[q].y, b[q].z, b[q].w};
+        for (int q = 0; q < 16; q++) {
+          if (k0 + q >= H16 / 8) break;
+          const uint4 bq = xr[k0 + q];
+          const uint32_t aw[4] = {a[q].x, a[q].y, a[q].z, a[q].w}, bw[4] = {bq.x, bq.y, bq.z, bq.w};
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             // Each half's exponent fields (at most 255 each) added, the halves apart (no carry between them); a
@@ -486,14 +530,16 @@ __global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint1
                                                                           __builtin_bit_cast(u16x2_t, es)));
             const double p0 = (double)__uint_as_float(aw[i] << 16) * (double)__uint_as_float(bw[i] << 16);
             const double p1 = (double)__uint_as_float(aw[i] & 0xffff0000u) * (double)__uint_as_float(bw[i] & 0xffff0000u);
-            acc = __dadd_rn(__dadd_rn(acc, p0), p1);
-            mag = __dadd_rn(__dadd_rn(mag, fabs(p0)), fabs(p1));
+            acc4[q % 4] = __dadd_rn(__dadd_rn(acc4[q % 4], p0), p1);
+            mag4[q % 4] = __dadd_rn(__dadd_rn(mag4[q % 4], fabs(p0)), fabs(p1));
           }
         }
       }
+      double acc = __dadd_rn(__dadd_rn(acc4[0], acc4[1]), __dadd_rn(acc4[2], acc4[3]));
+      double mag = __dadd_rn(__dadd_rn(mag4[0], mag4[1]), __dadd_rn(mag4[2], mag4[3]));
       uint32_t em = min(emin & 0xffffu, emin >> 16);
 #pragma unroll
-      for (int o = 1; o < 8; o <<= 1) {
+      for (int o = 1; o < 16; o <<= 1) {
         acc = __dadd_rn(acc, __shfl_xor(acc, o, 64));
         mag = __dadd_rn(mag, __shfl_xor(mag, o, 64));
         em = min(em, (uint32_t)__shfl_xor((int)em, o, 64));
@@ -504,14 +550,14 @@ __global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint1
       const bool exact_ok = mag * (1.0 + 0x1p-40) < ldexp(1.0, lsb + 53);
       float lgv = (float)acc;
       if (!exact_ok && sl == 0 && ci < nc) lgv = exact_logit_chain(W, xb, H, e, t);
-      if (sl == 0 && ci < nc) exact[wv][e] = bias ? __fadd_rn(lgv, bias[e]) : lgv;
+      if (sl == 0 && ci < nc) xkey[wv][e] = float_key(bias ? __fadd_rn(lgv, bias[e]) : lgv);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int i = 0; i < kRoutePer; i++) {
       const uint32_t e = lane + 64 * i;
-      if (e < E && (double)key_float(key[i]) >= thr) key[i] = float_key(exact[wv][e]);
+      if (e < E && xkey[wv][e] != 0u) key[i] = xkey[wv][e], xkey[wv][e] = 0u;
     }
     if (lane == 0) atomicAdd(cnt_exact, 1u);
     uint32_t kc[kRoutePer], ic[kRoutePer];
@@ -1558,12 +1604,13 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
   } else {
     {
       HookScope k(hook, "pf_xprep", st);
-      pf_xprep<<<(T + 3) / 4, kPfWG, 0, st>>>(x, T, H, E, b.xb, b.xn, b.xlsb, b.masks);
+      pf_xprep<<<(T + 3) / 4, kPfWG, 0, st>>>(x, T, H, E, b.xb, b.xt, b.xn, b.xlsb, b.masks, L.router + (uint64_t)E * H,
+                                              b.logits, S.has_shared ? b.gs : nullptr);
     }
     {
       HookScope k(hook, "pf_router", st);
       const uint32_t n = ((E + 31) / 32) * ((T + 31) / 32);
-      pf_router_bf16<<<n, kPfWG, 0, st>>>(L.router, b.xb, T, E, H, L.bias, b.logits);
+      pf_router_bf16<<<n, kPfWG, 0, st>>>(L.router_t, b.xt, T, E, H, L.bias, b.logits);
     }
     {
       HookScope k(hook, "pf_topk", st);
@@ -1571,7 +1618,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
       const float gamma = (float)(1.01 * (31 + H / 128 + 3) * 0x1p-23);
       pf_topk_cert<<<(T + 3) / 4, kPfWG, 0, st>>>(b.logits, L.router, L.rlsb, b.xb, b.xn, b.xlsb, T, E, H, K, L.bias,
                                                   gamma * L.rmax * 1.0001f, L.bias_max, b.ids, b.w,
-                                                  S.has_shared ? b.gs : nullptr, b.masks, b.cnt_exact);
+                                                  b.masks, b.cnt_exact);
     }
   }
   if (S.has_shared && hipStreamWaitEvent(st, b.xq, 0) != hipSuccess) return hipGetLastError();

@@ -39,6 +39,7 @@ struct PfShape {
 
 struct PfLayer {
   const uint16_t *router;  // (E + 1) x H bf16
+  const uint16_t *router_t;  // its E routed rows again in 16 x 32 tiles (the matrix-core router's operand)
   const float *bias;       // E or null
   const uint8_t *experts;  // expert e at experts + e * ex_bytes (gate, up at ex_up_off, down at ex_down_off)
   uint64_t ex_bytes, ex_up_off, ex_down_off;
@@ -55,6 +56,7 @@ struct PfBufs {
   uint8_t *act_r, *act_s;  // Tmax x (H / 256) activation units (act_s == act_r when the types agree)
   float *logits;           // Tmax x (E + 1)
   uint16_t *xb;            // Tmax x H: bf16(x), for the matrix-core router
+  uint16_t *xt;            // the same in 16 x 32 tiles (rows rounded up to 16)
   float *xn;               // Tmax: ||bf16(x_t)||_2, rounded up
   int *xlsb;               // Tmax: the least lsb of bf16(x_t)'s values
   uint32_t *cnt_exact;     // tokens whose top-k needed exact sums (accumulates until read)

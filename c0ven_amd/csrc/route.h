@@ -13,12 +13,15 @@ namespace c0ven {
 
 constexpr int kRoutePer = 8;  // experts a lane holds (512 / 64)
 
+// kCoherent: the logits were written by other work-groups of the same launch (an L2-coherent load); otherwise by an
+// earlier kernel (a plain load).
+template <bool kCoherent = true>
 __device__ __forceinline__ void route_load(const float *lg, uint32_t E, uint32_t lane, uint32_t key[kRoutePer],
                                            uint32_t id[kRoutePer]) {
 #pragma unroll
   for (int i = 0; i < kRoutePer; i++) {
     const uint32_t e = lane + 64 * i;
-    key[i] = e < E ? float_key(ld_co(lg + e)) : 0u;
+    key[i] = e < E ? float_key(kCoherent ? ld_co(lg + e) : lg[e]) : 0u;
     id[i] = e;
   }
 }
