@@ -18,8 +18,9 @@ constexpr uint32_t kMaxUnits = 32;         // 256-value units per row: H and F u
 constexpr uint32_t max_groups(uint32_t T, uint32_t K) { return T * K + (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX; }
 
 // The work-group (four waves) and the work items of moe_decode, in the order every work-group walks them:
-//   lead items       one router row each (a 512-value chunk a wave), when routing; item t < T also
-//                    quantises x[t];
+//   lead items       when routing: items t < T quantise x[t] (to the experts' activation types), the next ones
+//                    kRouteRows router rows each (a 512-value chunk a wave); without routing, items t < T quantise
+//                    x[t];
 //   top-k items      one a token (when routing): the shared gate's row, then softmax, top-k and weights;
 //   shared items     (when routing with a shared expert) the shared expert's gate/up then down items, for each chunk
 //                    of MOE_GROUP_MAX tokens: they need no routing, so they run beside the router;
@@ -28,11 +29,16 @@ constexpr uint32_t max_groups(uint32_t T, uint32_t K) { return T * K + (T + MOE_
 //   down items       down_rows(U_down) rows of down of one routed group (lane = r * U_down + u);
 //   combine items    one a (token, down row block): the token's outputs summed in rank order (after all down items).
 constexpr uint32_t kWG = 256;
-constexpr uint32_t kRouteRows = 1;
+#ifndef C0VEN_ROUTE_ROWS
+#define C0VEN_ROUTE_ROWS 1
+#endif
+constexpr uint32_t kRouteRows = C0VEN_ROUTE_ROWS;  // router rows a lead item (x read once for all of them)
 constexpr uint32_t lead_items(uint32_t T, uint32_t E, uint32_t route) {
-  return route ? ((E + kRouteRows - 1) / kRouteRows > T ? (E + kRouteRows - 1) / kRouteRows : T) : T;
+  return route ? T + (E + kRouteRows - 1) / kRouteRows : T;
 }
-constexpr uint32_t kMaxLeadItems = kMaxExperts / kRouteRows;
+constexpr uint32_t kMaxLeadItems = kMaxDecodeTokens + kMaxExperts;
+// LDS a lead item's dot products take from the dynamic allocation: 16 partials and the total of each (row, token).
+constexpr uint32_t kRouterLds = kRouteRows * kMaxDecodeTokens * 17 * 8;
 // Chunks of the shared expert's tokens (one group's worth each) when it runs beside the router.
 constexpr uint32_t shared_chunks(uint32_t T, uint32_t route, uint32_t has_shared) {
   return route && has_shared ? (T + MOE_GROUP_MAX - 1) / MOE_GROUP_MAX : 0;

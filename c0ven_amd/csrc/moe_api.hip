@@ -629,7 +629,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
     const size_t hc_lds = g.hc_lr ? ((size_t)T * g.hc_lr + (size_t)T * kHcStreams * kHcUpValues) * 4 : 0;
     c->lds = std::max<size_t>({(size_t)MOE_GROUP_MAX * act_tok_stride(Ug) +
                                    std::max<size_t>(Ug == 8 ? kMfmaXchBytes : 0, gate_up_xch_bytes(unit_lanes(Ug))),
-                               (size_t)MOE_GROUP_MAX * act_tok_stride(Ud), kGroupingLds});
+                               (size_t)MOE_GROUP_MAX * act_tok_stride(Ud), kGroupingLds, kRouterLds});
     int per_cu = 0, ncu = 0;
     uint32_t types = type_bit(g.gate_type) | type_bit(g.down_type);
     if (g.has_shared) types |= type_bit(g.sh_gate_type) | type_bit(g.sh_up_type) | type_bit(g.sh_down_type);

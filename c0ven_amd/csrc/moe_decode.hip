@@ -3,10 +3,10 @@
 // Replaces the reference's decode kernel list for the block (model.cpp:1348-1414): the router's bf16 GEMV
 // (mv_xmx_bf16), router_group (layer.cl:984-1023), moe_gate_up_g (moe.cl:230-302), moe_down_g (moe.cl:416-471) and
 // moe_combine (layer.cl:869-884). Every work-group walks the work items b, b + grid, b + 2 grid, ... in one order
-// (decode.h): lead items (router rows; x quantised), top-k items, the shared expert's items; then it takes the routed
+// (decode.h): lead items (x quantised; router rows), top-k items, the shared expert's items; then it takes the routed
 // gate/up, down and combine items from the list of its index modulo 8 (a counter a list). An item that needs earlier
 // work waits for it (flags set to this launch's epoch, or tagged records whose tag is this launch's):
-//   - each lead item sets its own flag; a top-k item polls the logits the lead items store;
+//   - an x item sets its token's flag; a top-k item polls the logits the lead items store;
 //   - every work-group builds the routed groups from the ids the top-k items store;
 //   - a down item polls its group's h, a combine item the outputs of its token's assignments.
 // Every item's dependencies have smaller indices. Progress: lead items wait for nothing; the dispatcher deals a grid's
@@ -92,18 +92,14 @@ __device__ __forceinline__ void wait_flag(const DecodeParams &p, uint32_t i) {
   __syncthreads();
 }
 
-// Waits until flags base .. base + count - 1 (count <= kMaxLeadItems) all hold this launch's epoch (wave 0 polls,
+// Waits until flags base .. base + count - 1 (count <= 64) all hold this launch's epoch (wave 0 polls,
 // a flag a lane, all loads of a round in flight together; the work-group follows).
 __device__ __forceinline__ void wait_flags(const DecodeParams &p, uint32_t base, uint32_t count) {
   if (wave_id() == 0) {
     uint32_t n = 0;
     for (;;) {
-      bool ok = true;
-#pragma unroll
-      for (uint32_t i = 0; i < (kMaxLeadItems + 63) / 64; i++) {
-        const uint32_t f = lane_id() + 64 * i;
-        if (f < count) ok &= ld_co(p.flags + base + f) == p.epoch;
-      }
+      const uint32_t f = lane_id();
+      const bool ok = f >= count || ld_co(p.flags + base + f) == p.epoch;
       if (__all(ok)) break;
       __builtin_amdgcn_s_sleep(1);
       if (++n == kSpinLimit) {
@@ -139,11 +135,15 @@ __device__ __forceinline__ void wait_tag(const DecodeParams &p, const uint64_t *
   __syncthreads();
 }
 
-// Token t's logits as order keys, lane l holding experts l + 64 i: the wave polls the tagged records until every one
-// holds this launch's tag (the lead items' stores are the hand-off; no flag).
+// Token t's logits as order keys, lane l holding experts l + 64 i: the wave polls the tagged records (the router rows'
+// fp32 sums) until every one holds this launch's tag (the lead items' stores are the hand-off; no flag), then adds
+// the bias.
 __device__ __forceinline__ void load_logits(const DecodeParams &p, uint32_t t, uint32_t key[kRoutePer], uint32_t id[kRoutePer]) {
   const uint32_t lane = lane_id(), E = p.E;
   const uint64_t *lg = p.logits + (uint64_t)t * (E + 1);
+  float bias[kRoutePer];  // read before the polling, added to the polled sums (the router rows' own fp32 add)
+#pragma unroll
+  for (int i = 0; i < kRoutePer; i++) bias[i] = p.bias ? p.bias[min(lane + 64 * i, E - 1)] : 0.0f;
   uint64_t v[kRoutePer];
   for (uint32_t n = 0;; n++) {
     bool ok = true;
@@ -164,7 +164,8 @@ __device__ __forceinline__ void load_logits(const DecodeParams &p, uint32_t t, u
 #pragma unroll
   for (int i = 0; i < kRoutePer; i++) {
     const uint32_t e = lane + 64 * i;
-    key[i] = e < E ? float_key(__uint_as_float((uint32_t)v[i])) : 0u;
+    const float l = __uint_as_float((uint32_t)v[i]);
+    key[i] = e < E ? float_key(p.bias ? __fadd_rn(l, bias[i]) : l) : 0u;
     id[i] = e;
   }
 }
@@ -182,6 +183,8 @@ __device__ __forceinline__ void route_token(const DecodeParams &p, uint32_t t, c
   uint32_t my_id = 0, my_key = 0;
   if (wv == 0) {
     route_select_lds(key, id, K, lane, cand, &my_id, &my_key);
+    // The ids first: the groups wait for them; the weights are read only by the combine items.
+    if (lane < K) st_tag(p.ids_t + t * K + lane, my_id, p.tag);
   } else {
     const double part = route_sum_part(key, E, lane, wv - 1, mx, tab);
     if (lane == 0) dpart[wv - 1] = part;
@@ -192,7 +195,6 @@ __device__ __forceinline__ void route_token(const DecodeParams &p, uint32_t t, c
     const float inv = (float)(1.0 / __dadd_rn(__dadd_rn(dpart[0], dpart[1]), dpart[2]));
     const float w = route_weight(my_key, mx, inv, K, lane, tab);
     if (lane < K) {
-      st_tag(p.ids_t + t * K + lane, my_id, p.tag);
       st_tag(p.w_t + t * K + lane, __float_as_uint(w), p.tag);
       p.ids[t * K + lane] = (int32_t)my_id;  // the caller's copies, read after the launch
       p.w[t * K + lane] = w;
@@ -591,16 +593,78 @@ __device__ __forceinline__ void hc_up_item(const DecodeParams &p, uint32_t j, ui
   if (arrive_last(p.cnt_hc + kDynStride, H / kHcUpValues, s_flag)) set_flag(p, kFlagHcX);
 }
 
-// Lead item i: router row i for all T tokens, plus the bias.
+// Router rows row0 .. row0 + nr - 1 (nr <= kRouteRows) against every token, rounded to fp32 and stored as the
+// logits' tagged records (the top-k item adds the bias). Each row's arithmetic is bf16_dot's (the same k chains a lane, the same 16-lane tree, the same
+// chunk and partial order), so a logit does not depend on kRouteRows; x is read once for the rows (a lane holds its
+// eight values of eight tokens), which divides the device's reads of x by kRouteRows. part: kRouterLds of LDS.
 template <bool kHc>
-__device__ __forceinline__ void router_row(const DecodeParams &p, uint32_t row, double *part, double *tot) {
-  router_dot<kHc>(p, row, 0, p.T, part, tot);
-  const uint32_t t = tid();
-  if (t < p.T) {
-    float l = (float)tot[t];
-    if (p.bias) l = __fadd_rn(l, p.bias[row]);
-    st_tag(p.logits + (uint64_t)t * (p.E + 1) + row, __float_as_uint(l), p.tag);
+__device__ __forceinline__ void router_rows(const DecodeParams &p, uint32_t row0, uint32_t nr, double *part) {
+  const uint32_t lane = lane_id(), wv = wave_id(), K = p.H, nC = K / 512, T = p.T;
+  const uint32_t pslot = 4 * wv + lane / 16;
+  const uint16_t *W = p.router + (uint64_t)row0 * K;
+  for (uint32_t c = wv; c < nC; c += kWG / 64) {
+    uint4 wa[kRouteRows];
+#pragma unroll
+    for (uint32_t r = 0; r < kRouteRows; r++)
+      wa[r] = *(const uint4 *)(W + (uint64_t)min(r, nr - 1) * K + 512 * c + 8 * lane);
+    for (uint32_t tb = 0; tb < T; tb += 8) {
+      const uint32_t nb = min(8u, T - tb);
+      float xs[8][8];  // token tb + tt's eight values, rounded to bf16
+#pragma unroll
+      for (uint32_t tt = 0; tt < 8; tt++) {
+        const uint64_t e = (uint64_t)(tb + min(tt, nb - 1)) * K + 512 * c + 8 * lane;
+        float4 xa, xb;
+        if constexpr (kHc) {
+          const uint4 u = ld_co16(p.x, (uint32_t)(4 * e)), v = ld_co16(p.x, (uint32_t)(4 * e + 16));
+          xa = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+          xb = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+        } else {
+          xa = ((const float4 *)(p.x + e))[0], xb = ((const float4 *)(p.x + e))[1];
+        }
+        round_bf16_2(xa.x, xa.y, xs[tt][0], xs[tt][1]), round_bf16_2(xa.z, xa.w, xs[tt][2], xs[tt][3]);
+        round_bf16_2(xb.x, xb.y, xs[tt][4], xs[tt][5]), round_bf16_2(xb.z, xb.w, xs[tt][6], xs[tt][7]);
+      }
+#pragma unroll
+      for (uint32_t r = 0; r < kRouteRows; r++) {
+        if (r >= nr) break;
+        __builtin_amdgcn_sched_barrier(0);  // one row's chains at a time (registers)
+        double wd[8];
+        const uint32_t w0[4] = {wa[r].x, wa[r].y, wa[r].z, wa[r].w};
+#pragma unroll
+        for (int k = 0; k < 8; k++) wd[k] = (double)__uint_as_float((k & 1) ? w0[k / 2] & 0xffff0000u : w0[k / 2] << 16);
+        double v[8];
+#pragma unroll
+        for (uint32_t tt = 0; tt < 8; tt++) {
+          double a = 0.0;
+          if (tt < nb) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) a = __builtin_fma(wd[k], (double)xs[tt][k], a);
+          }
+          v[tt] = a;
+        }
+        const double s = row16_reduce8_f64(v);  // bf16_dot's tree
+        const uint32_t tt = (lane & 15u) / 2;
+        if ((lane & 1u) == 0 && tt < nb) {
+          double *q = part + ((r * kMaxDecodeTokens) + tb + tt) * 16 + pslot;
+          *q = c == wv ? s : __dadd_rn(*q, s);
+        }
+      }
+    }
   }
+  if (wv >= nC && (lane & 15u) == 0) {  // waves without a chunk (K < 2048) give zeros
+    for (uint32_t r = 0; r < nr; r++)
+      for (uint32_t t = 0; t < T; t++) part[((r * kMaxDecodeTokens) + t) * 16 + pslot] = 0.0;
+  }
+  __syncthreads();
+  const uint32_t oi = tid(), orow = oi / T;  // the thread's output: row orow, token oi % T
+  if (orow < nr) {
+    const uint32_t t = oi % T;
+    double s = 0.0;
+#pragma unroll
+    for (uint32_t i = 0; i < 16; i++) s = __dadd_rn(s, part[((orow * kMaxDecodeTokens) + t) * 16 + i]);
+    st_tag(p.logits + (uint64_t)t * (p.E + 1) + row0 + orow, __float_as_uint((float)s), p.tag);
+  }
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -627,9 +691,7 @@ __device__ __forceinline__ void make_groups(const DecodeParams &p, uint8_t *lds,
   uint32_t *cnt = gnum + 2 * kMaxExperts;  // [wave][size 1 .. MOE_GROUP_MAX]
   for (uint32_t i = a; i < E; i += kWG) mask[i] = 0u;
   const uint32_t t = a / K;
-  // The last token's last id first, then every id; for a few records (a token or so) every reader polls its own
-  // directly, one round trip less.
-  if (n > 32) wait_tag(p, p.ids_t + n - 1);
+  // Each id's reader polls its own record (at most kMaxDecodeTokens kMaxUsed a work-group, ten cache lines at T = 8).
   if (a < n) {
     uint64_t ri;
     for (uint32_t k = 0;; k++) {
@@ -1100,11 +1162,6 @@ __device__ __forceinline__ void combine_item(const DecodeParams &p, uint32_t t, 
 
 }  // namespace
 
-#ifndef C0VEN_QUANT_TOP_MIN
-#define C0VEN_QUANT_TOP_MIN 5
-#endif
-constexpr uint32_t kQuantTopMin = C0VEN_QUANT_TOP_MIN;
-
 // Grid: the work-groups of 256 the device holds at once; dynamic LDS: the larger of a group's activation units
 // (MOE_GROUP_MAX x act_tok_stride) and the grouping's tables (kGroupingLds).
 template <uint32_t kTypes, bool kHc>
@@ -1127,9 +1184,6 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
   const uint32_t nL = lead_items(T, E, p.route), nTop = p.route ? T : 0, B1 = nH + nL + nTop;
   const uint32_t nGU = p.F / gate_up_rows(Ug), nD = p.H / down_rows(Ud), nBlk = nD;  // combine items: T x nBlk
   const uint32_t ns = shared_chunks(T, p.route, p.has_shared), B2 = B1 + ns * (nGU + nD);
-  // x is quantised by the top-k items from kQuantTopMin tokens on (the router rows that would otherwise do it then
-  // finish last), by the first T lead items below that (one top-k item would do it serially).
-  const bool quant_top = p.route && T >= kQuantTopMin;
   // Items below B2 go round-robin (work-group b takes b, b + grid, ...). The routed items, whose cost varies with their
   // group's size, are handed out dynamically: item B2 + x + kDynLists k is the k-th of list x, and the work-groups with
   // blockIdx % kDynLists == x take list x's items in order from its counter (one counter a list keeps the atomics
@@ -1176,11 +1230,15 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
     } else if (it < nH + nL) {
       const uint32_t li = it - nH;
       if (kHc) wait_flag(p, kFlagHcX);
-      if (p.route) {  // a router row; x[li] too unless the token's top-k item quantises it (quant_top)
-        if (li < T && !quant_top) quantise_x<kTypes, kHc>(p, li);
-        if (li < E) router_row<kHc>(p, li, s_part, s_tot);
+      if (p.route) {  // x[li] (its flag tells the shared expert's items), or router row li - T
+        if (li < T) {
+          quantise_x<kTypes, kHc>(p, li);
+          set_flag(p, kFlagLead + li);
+        } else {
+          const uint32_t r0 = (li - T) * kRouteRows;
+          router_rows<kHc>(p, r0, min(kRouteRows, E - r0), (double *)lds);
+        }
         if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
-        if (li < T && !quant_top) set_flag(p, kFlagLead + li);
       } else {
         if (li < T) quantise_x<kTypes, kHc>(p, li);
         if (arrive_last(p.cnt_route, nL, &s_flag)) set_flag(p, kFlagRouted);
@@ -1188,18 +1246,14 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
     } else if (it < B1) {
       const uint32_t t = it - nH - nL;
       if (kHc) wait_flag(p, kFlagHcX);
-      // With quant_top, x[t] to the experts' activation types first (the shared expert's items wait for its flag),
-      // then the rest while the lead items finish the logits.
-      if (quant_top) {
-        quantise_x<kTypes, kHc>(p, t);
-        set_flag(p, kFlagLead + t);
-      }
-      // The shared gate's logit (router row E) for this token while the lead items finish: gs = sigmoid of it.
-      router_dot<kHc>(p, E, t, 1, s_part, s_tot);
-      if (tid() == 0) st_tag(p.gs + t, __float_as_uint(sigmoid_libm((float)s_tot[0], exp_tab)), p.tag);
       if (mark && tid() == 0) mark[1] = __builtin_amdgcn_s_memrealtime();
       route_token(p, t, exp_tab, s_part, (uint2 *)lds);
       if (mark && tid() == 0) mark[2] = __builtin_amdgcn_s_memrealtime();
+      // The shared gate's logit (router row E): gs = sigmoid of it, read only by the combine items. (s_part is
+      // route_token's scratch until the barrier.)
+      __syncthreads();
+      router_dot<kHc>(p, E, t, 1, s_part, s_tot);
+      if (tid() == 0) st_tag(p.gs + t, __float_as_uint(sigmoid_libm((float)s_tot[0], exp_tab)), p.tag);
     } else if (it < B2) {
       const uint32_t i = it - B1;
       if (i < ns * nGU) {

@@ -105,7 +105,8 @@ __device__ __forceinline__ void route_select(uint32_t key[kRoutePer], uint32_t i
 // largest of the lanes' maxima, is found bit by bit with ballots; at least K keys are >= tau (one a lane of those K
 // lanes), so every winner is among the keys >= tau. Those candidates (usually little more than K) are packed into
 // cand (LDS, room for 64 kRoutePer + K entries) and each is ranked against all of them: rank = the number that beat it
-// (a larger key, or an equal key with a lower id). One wave runs this; key and id are kept.
+// (a larger key, or an equal key with a lower id): with at most 64 candidates in registers (each lane reads the others
+// with readlane), otherwise in LDS. One wave runs this; key and id are kept.
 __device__ __forceinline__ void route_select_lds(const uint32_t key[kRoutePer], const uint32_t id[kRoutePer], uint32_t K,
                                                  uint32_t lane, uint2 *cand, uint32_t *my_id, uint32_t *my_key) {
   uint32_t m = key[0];
@@ -133,6 +134,21 @@ __device__ __forceinline__ void route_select_lds(const uint32_t key[kRoutePer], 
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS stores are done before it reads them back
   __builtin_amdgcn_wave_barrier();
+  if (total <= 64) {  // (the usual case) candidate j in lane j, ranked against the others read lane by lane
+    const uint2 me = lane < total ? cand[lane] : make_uint2(0u, 0u);
+    uint32_t rank = 0;
+    for (uint32_t i = 0; i < total; i++) {
+      const uint32_t ok = readlane_u32(me.x, (int)i), oi = readlane_u32(me.y, (int)i);
+      rank += (ok > me.x) | ((ok == me.x) & (oi < me.y));
+    }
+    // Ranks of the candidates are distinct and below total; the other lanes keep their own index: a permutation, so
+    // one ds_permute (lane rank receives the candidate of that rank) moves every winner to its lane.
+    const int dst = 4 * (int)(lane < total ? rank : lane);
+    *my_key = (uint32_t)__builtin_amdgcn_ds_permute(dst, (int)me.x);
+    *my_id = (uint32_t)__builtin_amdgcn_ds_permute(dst, (int)me.y);
+    if (lane >= K) *my_key = 0u, *my_id = 0u;
+    return;
+  }
   uint2 *sel = cand + 64 * kRoutePer;
   for (uint32_t j = lane; j < total; j += 64) {
     const uint2 me = cand[j];
