@@ -29,6 +29,7 @@ Q8_FAMILY = (QT_Q8_0, QT_IQ4_NL, QT_Q2_0)  # the weight types whose dot products
 
 MOE_OK, MOE_ERROR, MOE_BAD_ARGUMENT, MOE_BUSY, MOE_TIMEOUT = 0, 1, 2, 3, 4
 MOE_FLAG_EXACT_ROUTER = 1
+MOE_FLAG_HC_FIXED_ORDER = 2
 
 
 class MoeConfig(C.Structure):
@@ -297,7 +298,7 @@ class MoeBlock:
 
     def __init__(self, n_embd, n_ff, n_expert, n_used, gate_type, down_type, has_shared=True, sh_gate_type=None,
                  sh_down_type=None, n_layer=1, max_tokens=16, swiglu_limit=0.0, device=0, borrowed_immutable=0,
-                 hc_lr=0, sh_up_type=None, exact_router=False):
+                 hc_lr=0, sh_up_type=None, exact_router=False, hc_fixed_order=False):
         self.cfg = MoeConfig(n_embd=n_embd, n_ff=n_ff, n_expert=n_expert, n_used=n_used, n_layer=n_layer,
                              gate_type=gate_type, down_type=down_type, has_shared=1 if has_shared else 0,
                              sh_gate_type=sh_gate_type if sh_gate_type is not None else gate_type,
@@ -305,7 +306,8 @@ class MoeBlock:
                              max_tokens=max_tokens, swiglu_limit=swiglu_limit, device=device,
                              borrowed_immutable=borrowed_immutable, hc_lr=hc_lr,
                              sh_up_type=0 if sh_up_type is None else sh_up_type,
-                             flags=MOE_FLAG_EXACT_ROUTER if exact_router else 0)
+                             flags=(MOE_FLAG_EXACT_ROUTER if exact_router else 0)
+                             | (MOE_FLAG_HC_FIXED_ORDER if hc_fixed_order else 0))
         self.exact_router = bool(exact_router)
         h = _P()
         st = lib.moe_open(C.byref(self.cfg), C.byref(h))

@@ -20,6 +20,7 @@
 #include "iq3s_grid.h"
 #include "layout.h"
 #include "prefill.h"
+#include "prefill_hc.h"
 #include "repack.h"
 
 using namespace c0ven;
@@ -54,6 +55,7 @@ struct Layer {
   // The hyper-connection module before the block (hc_lr > 0).
   float *hc_gamma = nullptr;
   uint16_t *hc_down = nullptr, *hc_inj = nullptr, *hc_up = nullptr;
+  double *hc_rn = nullptr;  // the 2-norms of W_down's, W_inject's and W_up's rows (the prefill mix's bound)
   bool has_hc = false;
 };
 
@@ -216,7 +218,8 @@ struct moe_ctx {
   uint32_t grid = 0;           // co-resident work-groups of moe_decode
   float *hc_n = nullptr, *hc_l = nullptr, *hc_x = nullptr;  // the hyper-connection mix's scratch (hc_lr > 0)
   uint32_t *cnt_hc = nullptr;
-  float *hc_R_stage = nullptr;  // moe_forward_hc's device copy of R
+  float *hc_R_stage = nullptr;  // moe_forward_hc's device copy of R (max_tokens tokens)
+  HcBufs hcp{};                 // the prefill mix's scratch (hc_lr > 0 and max_tokens > the decode kernel's)
   uint8_t *codebooks = nullptr;  // the caller's iq2s_grid and iq3xxs_grid (QGRID layout, up to QGRID_IQ3S)
   bool have_codebooks = false;
   const void *kernel = nullptr;  // moe_decode for the context's set of weight types
@@ -538,6 +541,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
         L.hc_down = c->alloc<uint16_t>((uint64_t)g.hc_lr * kHcStreams * H);
         L.hc_inj = c->alloc<uint16_t>((uint64_t)kHcStreams * kHcStreams * H);
         L.hc_up = c->alloc<uint16_t>((uint64_t)kHcStreams * H * g.hc_lr);
+        L.hc_rn = c->alloc<double>((uint64_t)g.hc_lr + kHcStreams + (uint64_t)kHcStreams * H);
       }
     }
     // Scratch for max_tokens tokens of n_used + 1 assignments (the pre-routed path may give a token its shared
@@ -618,7 +622,22 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
       c->hc_l = c->alloc<float>((uint64_t)T * (g.hc_lr + kHcStreams));
       c->hc_x = c->alloc<float>((uint64_t)T * H);
       c->cnt_hc = c->alloc<uint32_t>(2 * kDynStride);
-      c->hc_R_stage = c->alloc<float>((uint64_t)T * kHcStreams * H);
+      c->hc_R_stage = c->alloc<float>((uint64_t)TM * kHcStreams * H);
+      if (TM > T) {
+        const uint64_t Md = g.hc_lr + kHcStreams, D = (uint64_t)kHcStreams * H;
+        HcBufs &b = c->hcp;
+        b.n = c->alloc<float>(TM * D);
+        b.nn = c->alloc<double>(TM);
+        b.part = c->alloc<double>(kHcDownSplit * TM * Md);
+        b.raw = c->alloc<float>(TM * Md);
+        b.open = c->alloc<uint32_t>(2 * TM * Md);
+        b.cnt = c->alloc<uint32_t>(1);
+        b.l = c->alloc<float>(TM * g.hc_lr);
+        b.ln = c->alloc<double>(TM);
+        b.inj = c->alloc<float>(TM * kHcStreams);
+        b.a = c->alloc<float>(TM * D);
+        b.x = c->alloc<float>(TM * H);
+      }
       check(hipMemset(c->cnt_hc, 0, 2 * kDynStride * sizeof(uint32_t)), "hipMemset");
     }
     c->tagged = {{c->logits, (uint64_t)T * (E + 1)}, {c->gs, T}, {c->ids_t, (uint64_t)T * K1}, {c->w_t, (uint64_t)T * K1},
@@ -823,6 +842,22 @@ MOE_API moe_status moe_load_hc(moe_ctx *c, uint32_t layer, const float *gamma, c
     check(hipMemcpy(L.hc_down, w_down, (uint64_t)g.hc_lr * D * 2, hipMemcpyHostToDevice), "upload hc down");
     check(hipMemcpy(L.hc_inj, w_inject, (uint64_t)kHcStreams * D * 2, hipMemcpyHostToDevice), "upload hc inject");
     check(hipMemcpy(L.hc_up, w_up, D * g.hc_lr * 2, hipMemcpyHostToDevice), "upload hc up");
+    // Row 2-norms (double, rounded up) for the prefill mix's bound: W_down's, W_inject's, then W_up's rows.
+    std::vector<double> rn((uint64_t)g.hc_lr + kHcStreams + D);
+    const auto norm = [](const uint16_t *w, uint64_t n) {
+      double ss = 0.0;
+      for (uint64_t i = 0; i < n; i++) {
+        uint32_t b = (uint32_t)w[i] << 16;
+        float f;
+        std::memcpy(&f, &b, 4);
+        ss += (double)f * (double)f;
+      }
+      return std::sqrt(ss) * (1.0 + 0x1p-30);
+    };
+    for (uint32_t j = 0; j < g.hc_lr; j++) rn[j] = norm(w_down + (uint64_t)j * D, D);
+    for (uint32_t j = 0; j < kHcStreams; j++) rn[g.hc_lr + j] = norm(w_inject + (uint64_t)j * D, D);
+    for (uint64_t j = 0; j < D; j++) rn[g.hc_lr + kHcStreams + j] = norm(w_up + j * g.hc_lr, g.hc_lr);
+    check(hipMemcpy(L.hc_rn, rn.data(), rn.size() * sizeof(double), hipMemcpyHostToDevice), "upload hc norms");
     L.has_hc = true;
   });
 }
@@ -834,11 +869,20 @@ MOE_API moe_status moe_forward_hc_async(moe_ctx *c, uint32_t layer, float *R_dev
     require(R_dev != nullptr, "null R");
     require(layer < g.n_layer && c->layers[layer].router != nullptr, "layer out of range or its router not loaded");
     require(c->layers[layer].has_hc, "the layer's hyper-connection module is not loaded (moe_load_hc)");
-    require(ntok >= 1 && ntok <= c->tdec, "moe_forward_hc_async takes 1..min(max_tokens, 16) tokens");
+    require(ntok >= 1 && ntok <= c->tmax, "moe_forward_hc_async takes 1..max_tokens tokens");
     need_codebooks(c, {g.gate_type, g.down_type, g.has_shared ? g.sh_gate_type : 0u, g.has_shared ? g.sh_up_type : 0u,
                      g.has_shared ? g.sh_down_type : 0u});
     const Layer &L = c->layers[layer];
     hipStream_t s = stream ? (hipStream_t)stream : c->stream;
+    if (ntok > c->tdec) {  // the prefill path: the mix's kernels, the block, the combine's kernel
+      const HcShape S{g.n_embd, g.hc_lr, ntok};
+      const HcLayer HL{L.hc_gamma, L.hc_down, L.hc_inj, L.hc_up, L.hc_rn};
+      check(prefill_hc_pre(S, HL, c->hcp, R_dev, (g.flags & MOE_FLAG_HC_FIXED_ORDER) != 0, s), "prefill hc mix launch");
+      float *y = y_dev ? y_dev : c->y_dev;
+      forward_dev(c, layer, c->hcp.x, ntok, y, ids_dev, w_dev, s);
+      check(prefill_hc_post(S, c->hcp, R_dev, y, s), "prefill hc combine launch");
+      return;
+    }
     DecodeParams p = base_params(c, layer, ntok);
     p.hc_R = R_dev, p.hc_gamma = L.hc_gamma, p.hc_down = L.hc_down, p.hc_inj = L.hc_inj, p.hc_up = L.hc_up;
     p.hc_lr = g.hc_lr, p.hc_n = c->hc_n, p.hc_l = c->hc_l, p.hc_x = c->hc_x, p.cnt_hc = c->cnt_hc;
@@ -855,7 +899,7 @@ MOE_API moe_status moe_forward_hc_async(moe_ctx *c, uint32_t layer, float *R_dev
 MOE_API moe_status moe_forward_hc(moe_ctx *c, uint32_t layer, float *R, uint32_t ntok, float *y, moe_route_out *route) {
   return guarded(c, [&] {
     require(R != nullptr && c->cfg.hc_lr > 0, "null R or no hyper-connection module");
-    require(ntok >= 1 && ntok <= c->tdec, "moe_forward_hc takes 1..min(max_tokens, 16) tokens");
+    require(ntok >= 1 && ntok <= c->tmax, "moe_forward_hc takes 1..max_tokens tokens");
     const uint64_t rb = (uint64_t)ntok * kHcStreams * c->cfg.n_embd * sizeof(float);
     const uint32_t K = c->cfg.n_used;
     check(hipMemcpyAsync(c->hc_R_stage, R, rb, hipMemcpyHostToDevice, c->stream), "upload R");
@@ -868,9 +912,10 @@ MOE_API moe_status moe_forward_hc(moe_ctx *c, uint32_t layer, float *R, uint32_t
                            c->stream),
             "download y");
     if (route && route->ids)
-      check(hipMemcpyAsync(route->ids, c->ids, sizeof(int32_t) * ntok * K, hipMemcpyDeviceToHost, c->stream), "ids");
+      check(hipMemcpyAsync(route->ids, c->last_ids, sizeof(int32_t) * ntok * K, hipMemcpyDeviceToHost, c->stream),
+            "ids");
     if (route && route->w)
-      check(hipMemcpyAsync(route->w, c->w, sizeof(float) * ntok * K, hipMemcpyDeviceToHost, c->stream), "w");
+      check(hipMemcpyAsync(route->w, c->last_w, sizeof(float) * ntok * K, hipMemcpyDeviceToHost, c->stream), "w");
     check(hipStreamSynchronize(c->stream), "forward_hc");
     check_err(c);
   });

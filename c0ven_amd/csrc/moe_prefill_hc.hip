@@ -1,0 +1,332 @@
+// The hyper-connection mix before the prefill block and the combine after it (docs/spec/MODEL_LAYER.md 1.1-1.2; the
+// reference's prompt path runs p_hc_mix and p_hc_combine around the block, core/models/qwen4exp/prompt.cpp:478-504).
+//
+// The results are the decode path's, bit for bit (and the oracle's, orc_hc_pre / orc_hc_post): the norms, silu,
+// sigmoid and mix steps are the same fp32 operations; the two bf16 products (W_down and W_inject against n, W_up
+// against l) are sums of exact products that the decode kernel adds in fp64 in a fixed order and rounds to fp32 once.
+// Here they run on the fp64 matrix cores (v_mfma_f64_16x16x4f64) in another order, with a bound on the difference:
+// each sum path has at most n_mine roundings here and n_ref in the fixed order, so the two fp64 values are within
+// (n_mine + n_ref) 2^-53 sum|p| <= (n_mine + n_ref) 2^-53 ||w||_2 ||x||_2 of each other (Cauchy-Schwarz on the bf16
+// values). Where the fp32 rounding of every value in that interval is the same, it is the fixed order's rounding.
+// Otherwise the sum is recomputed in the fixed order: W_up's (a k-order chain of at most 512 terms) by the thread
+// that found it open, W_down's and W_inject's (the decode kernel's 512-value-chunk tree) by one wave each, from a
+// list, in a kernel of its own.
+#include <hip/hip_runtime.h>
+
+#include "device_math.h"
+#include "prefill_hc.h"
+
+namespace c0ven {
+namespace {
+
+typedef double v4d_t __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kHcWG = 256;
+constexpr uint32_t kHcStreams4 = 4;
+constexpr uint32_t kGroupK = 128;  // values a matrix-core chain sums before its sum joins the fp64 total
+
+__device__ __forceinline__ uint32_t lane_of() { return threadIdx.x & 63u; }
+
+__device__ __forceinline__ double bf16_lo(uint32_t w) { return (double)__uint_as_float(w << 16); }
+__device__ __forceinline__ double bf16_hi(uint32_t w) { return (double)__uint_as_float(w & 0xffff0000u); }
+
+// A double summed over the work-group (256) in a fixed order: each wave by halving exchanges, then the four waves.
+__device__ __forceinline__ double wg_sum(double v, double *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = __dadd_rn(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if (lane_of() == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const double s = __dadd_rn(__dadd_rn(red[0], red[1]), __dadd_rn(red[2], red[3]));
+  __syncthreads();
+  return s;
+}
+
+// Token t (one work-group): each stream as RMSNorm(R_s) gamma_s, the decode kernel's hc_norm_item arithmetic (each
+// thread's squares in order, then wg_sum; mean rounded to fp32; 1 / sqrtf(mean + 1e-6)), and the 2-norm of bf16(n),
+// rounded up. Work-group 0 clears the open list's count.
+__global__ void __launch_bounds__(kHcWG) pf_hc_norm(const float *R, const float *gamma, uint32_t H, float *n,
+                                                    double *nn, uint32_t *cnt) {
+  __shared__ double red[4];
+  const uint32_t t = blockIdx.x;
+  if (t == 0 && threadIdx.x == 0) *cnt = 0u;
+  double sq = 0.0;
+  for (uint32_t s = 0; s < kHcStreams4; s++) {
+    const float *r = R + ((uint64_t)t * kHcStreams4 + s) * H;
+    double ss = 0.0;
+    for (uint32_t i = threadIdx.x; i < H; i += kHcWG) ss = __dadd_rn(ss, (double)__fmul_rn(r[i], r[i]));
+    ss = wg_sum(ss, red);
+    const float mean = (float)(ss / (double)H);
+    const float scale = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, 1e-6f)));
+    float *o = n + ((uint64_t)t * kHcStreams4 + s) * H;
+    for (uint32_t i = threadIdx.x; i < H; i += kHcWG) {
+      const float v = __fmul_rn(__fmul_rn(r[i], scale), gamma[s * H + i]);
+      o[i] = v;
+      const double b = (double)round_bf16(v);
+      sq = __builtin_fma(b, b, sq);
+    }
+  }
+  sq = wg_sum(sq, red);
+  if (threadIdx.x == 0) nn[t] = sqrt(sq) * (1.0 + 0x1p-30);
+}
+
+// C = bf16(A) bf16(B)^T on the fp64 matrix cores: rows of A (M of them: A0's first M0, then A1's), tokens of B (N rows
+// of K fp32, rounded to bf16 here), K values. A work-group takes 64 rows x 64 tokens over the K range of its split
+// (blockIdx.y), wave w rows 32 (w & 1) .. and tokens 32 (w >> 1) .., as 2 x 2 tiles of 16 x 16. Lane l (g = l / 16)
+// holds A[row l % 16][k + 4 g + m] and B[token l % 16][k + 4 g + m] for MFMA step m of a 16-value chunk: both operands
+// take the same k in the same place, so each step adds 64 of the row-token products (the order of a sum is free
+// here: the bound covers any). Each kGroupK values' chain starts from zero and is added to an fp64 total.
+// kUp: one split; the sums are certified here (row norms rn, token norms tn, the fixed order's k chain where open)
+// and written as fp32 to out32 (N x M). Otherwise the fp64 totals go to part (split x N x M).
+template <bool kUp>
+__global__ void __launch_bounds__(kHcWG) pf_hc_gemm(const uint16_t *A0, uint32_t M0, const uint16_t *A1, uint32_t M,
+                                                    uint32_t K, const float *B, uint32_t N, uint32_t ksplit,
+                                                    double *part, float *out32, const double *rn, const double *tn,
+                                                    double bound_k) {
+  const uint32_t nmt = (M + 63) / 64, mt = blockIdx.x % nmt, nt = blockIdx.x / nmt, split = blockIdx.y;
+  const uint32_t lane = lane_of(), w = threadIdx.x >> 6, g = lane / 16, c16 = lane % 16;
+  const uint32_t m0 = 64 * mt + 32 * (w & 1), n0 = 64 * nt + 32 * (w >> 1);
+  const uint16_t *ar[2];
+  const float *br[2];
+#pragma unroll
+  for (int f = 0; f < 2; f++) {
+    const uint32_t row = min(m0 + 16 * f + c16, M - 1), tok = min(n0 + 16 * f + c16, N - 1);
+    ar[f] = row < M0 ? A0 + (uint64_t)row * K : A1 + (uint64_t)(row - M0) * K;
+    br[f] = B + (uint64_t)tok * K;
+  }
+  const uint32_t kb = split * ksplit, ke = min(K, kb + ksplit);
+  v4d_t tot[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) tot[i][j] = v4d_t{0.0, 0.0, 0.0, 0.0};
+  for (uint32_t kg = kb; kg < ke; kg += kGroupK) {
+    v4d_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[i][j] = v4d_t{0.0, 0.0, 0.0, 0.0};
+    const uint32_t kge = min(ke, kg + kGroupK);
+#pragma unroll 2
+    for (uint32_t kc = kg; kc < kge; kc += 16) {
+      const uint32_t k = kc + 4 * g;
+      const bool ok = k < kge;  // (K is a multiple of 4: a lane's four values are all in or all out)
+      uint2 a[2];
+      float4 b[2];
+#pragma unroll
+      for (int f = 0; f < 2; f++) {
+        a[f] = ok ? *(const uint2 *)(ar[f] + k) : make_uint2(0u, 0u);
+        b[f] = ok ? *(const float4 *)(br[f] + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+      double ad[2][4], bd[2][4];
+#pragma unroll
+      for (int f = 0; f < 2; f++) {
+        ad[f][0] = bf16_lo(a[f].x), ad[f][1] = bf16_hi(a[f].x), ad[f][2] = bf16_lo(a[f].y), ad[f][3] = bf16_hi(a[f].y);
+        bd[f][0] = (double)round_bf16(b[f].x), bd[f][1] = (double)round_bf16(b[f].y);
+        bd[f][2] = (double)round_bf16(b[f].z), bd[f][3] = (double)round_bf16(b[f].w);
+      }
+#pragma unroll
+      for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+          for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad[i][m], bd[j][m], acc[i][j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) tot[i][j][q] = __dadd_rn(tot[i][j][q], acc[i][j][q]);
+  }
+  // tot[i][j][q]: row m0 + 16 i + 4 q + g, token n0 + 16 j + c16 (the f64 form's result layout: element q of lane l
+  // is row 4 q + l / 16).
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t row = m0 + 16 * i + 4 * q + g, tok = n0 + 16 * j + c16;
+        if (row >= M || tok >= N) continue;
+        const double v = tot[i][j][q];
+        if constexpr (kUp) {
+          const double bnd = bound_k * rn[row] * tn[tok];
+          const float f = (float)v;
+          float o = f;
+          if (!(__builtin_isfinite(v) && (float)(v - bnd) == f && (float)(v + bnd) == f)) {
+            // Open: the fixed order (k ascending, one fused step a term, from zero).
+            const uint16_t *wr = A0 + (uint64_t)row * K;
+            const float *xr = B + (uint64_t)tok * K;
+            double c = 0.0;
+            for (uint32_t k = 0; k < K; k++)
+              c = __builtin_fma((double)__uint_as_float((uint32_t)wr[k] << 16), (double)round_bf16(xr[k]), c);
+            o = (float)c;
+          }
+          out32[(uint64_t)tok * M + row] = o;
+        } else {
+          part[((uint64_t)split * N + tok) * M + row] = v;
+        }
+      }
+}
+
+// Token t's down sums (rows < lr of W_down, then the 4 of W_inject): the splits added in order, certified against the
+// fixed order (bound_k rn tn), rounded to fp32 into raw (T x (lr + 4)); an open one's (t, row) goes to the list (its
+// raw entry is written by pf_hc_down_fix). force_open sends all.
+__global__ void __launch_bounds__(kHcWG) pf_hc_down_fin(const double *part, uint32_t T, uint32_t M, uint32_t nsplit,
+                                                        const double *rn, const double *tn, double bound_k,
+                                                        bool force_open, float *raw, uint32_t *open, uint32_t *cnt) {
+  const uint32_t t = blockIdx.x;
+  for (uint32_t row = threadIdx.x; row < M; row += kHcWG) {
+    double v = 0.0;
+    for (uint32_t s = 0; s < nsplit; s++) v = __dadd_rn(v, part[((uint64_t)s * T + t) * M + row]);
+    const double bnd = bound_k * rn[row] * tn[t];
+    const float f = (float)v;
+    if (!force_open && __builtin_isfinite(v) && (float)(v - bnd) == f && (float)(v + bnd) == f) {
+      raw[(uint64_t)t * M + row] = f;
+    } else {
+      const uint32_t at = atomicAdd(cnt, 1u);
+      open[2 * at] = t, open[2 * at + 1] = row;
+    }
+  }
+}
+
+// The open down sums in the decode kernel's fixed order (bf16_dot for one row and one token, restated for one wave):
+// 512-value chunks c; lane l's eight values 8 l .. 8 l + 7 a fused chain from zero; a lane row r (16 lanes) as
+// ((P0 + P7) + (P3 + P4)) + ((P1 + P6) + (P2 + P5)), P_m = a_m + a_(15 - m); slot 4 (c mod 4) + r takes the chunks'
+// sums in chunk order; the 16 slots added in order from zero. One wave an entry.
+__global__ void __launch_bounds__(kHcWG) pf_hc_down_fix(const uint16_t *w_down, const uint16_t *w_inj, uint32_t lr,
+                                                        uint32_t K, const float *n, const uint32_t *open,
+                                                        const uint32_t *cnt, float *raw) {
+  const uint32_t lane = lane_of(), r = lane / 16, nw = gridDim.x * (kHcWG / 64), M = lr + kHcStreams4;
+  for (uint32_t e = blockIdx.x * (kHcWG / 64) + (threadIdx.x >> 6); e < *cnt; e += nw) {
+    const uint32_t t = open[2 * e], row = open[2 * e + 1];
+    const uint16_t *wr = row < lr ? w_down + (uint64_t)row * K : w_inj + (uint64_t)(row - lr) * K;
+    const float *xr = n + (uint64_t)t * K;
+    double slot[4] = {0.0, 0.0, 0.0, 0.0};  // slot 4 w + r, w = c mod 4 (lane 16 r holds its row's)
+    for (uint32_t c = 0; c < K / 512; c++) {
+      const uint32_t k0 = 512 * c + 8 * lane;
+      const uint4 wq = *(const uint4 *)(wr + k0);
+      const float4 x0 = *(const float4 *)(xr + k0), x1 = *(const float4 *)(xr + k0 + 4);
+      const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      double a = 0.0;
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        a = __builtin_fma((k & 1) ? bf16_hi(ww[k / 2]) : bf16_lo(ww[k / 2]), (double)round_bf16(xs[k]), a);
+      const double P = __dadd_rn(a, __shfl_xor(a, 15, 64));  // lanes m < 8 of a row: P_m
+      double p[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) p[j] = __shfl(P, (int)(16 * r + j), 64);
+      const double S = __dadd_rn(__dadd_rn(__dadd_rn(p[0], p[7]), __dadd_rn(p[3], p[4])),
+                                 __dadd_rn(__dadd_rn(p[1], p[6]), __dadd_rn(p[2], p[5])));
+#pragma unroll
+      for (uint32_t q = 0; q < 4; q++)
+        if ((c & 3u) == q) slot[q] = c < 4 ? S : __dadd_rn(slot[q], S);
+    }
+    double s = 0.0;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++)
+#pragma unroll
+      for (uint32_t rr = 0; rr < 4; rr++) s = __dadd_rn(s, __shfl(slot[q], (int)(16 * rr), 64));
+    if (lane == 0) raw[(uint64_t)t * M + row] = (float)s;
+  }
+}
+
+// Token t: l = silu(v / 4) for W_down's rows (the quarter exact; z / (1 + e^-z)), the inject logits for W_inject's,
+// and the 2-norm of bf16(l), rounded up.
+__global__ void __launch_bounds__(kHcWG) pf_hc_down_epi(const float *raw, uint32_t lr, float *l, float *inj,
+                                                        double *ln) {
+  __shared__ uint64_t tab[32];
+  __shared__ double red[4];
+  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
+  const uint32_t t = blockIdx.x, M = lr + kHcStreams4;
+  double sq = 0.0;
+  for (uint32_t j = threadIdx.x; j < M; j += kHcWG) {
+    const float v = raw[(uint64_t)t * M + j];
+    if (j < lr) {
+      const float z = __fmul_rn(v, 0.25f);
+      const float o = __fdiv_rn(z, __fadd_rn(1.0f, expf_libm(-z, tab)));
+      l[(uint64_t)t * lr + j] = o;
+      const double b = (double)round_bf16(o);
+      sq = __builtin_fma(b, b, sq);
+    } else {
+      inj[(uint64_t)t * kHcStreams4 + j - lr] = v;
+    }
+  }
+  sq = wg_sum(sq, red);
+  if (threadIdx.x == 0) ln[t] = sqrt(sq) * (1.0 + 0x1p-30);
+}
+
+// x[t][i] = (sum over s in order of n_s[i] sigma(a_s[i])) / 4, a thread a value.
+__global__ void __launch_bounds__(kHcWG) pf_hc_mix(const float *n, const float *a, uint32_t T, uint32_t H, float *x) {
+  __shared__ uint64_t tab[32];
+  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
+  const uint64_t e = (uint64_t)blockIdx.x * kHcWG + threadIdx.x;
+  if (e >= (uint64_t)T * H) return;
+  const uint32_t t = (uint32_t)(e / H), i = (uint32_t)(e % H);
+  float acc = 0.0f;
+#pragma unroll
+  for (uint32_t s = 0; s < kHcStreams4; s++) {
+    const float nv = n[((uint64_t)t * kHcStreams4 + s) * H + i];
+    const float av = a[(uint64_t)t * kHcStreams4 * H + (uint64_t)s * H + i];
+    acc = __fadd_rn(acc, __fmul_rn(nv, sigmoid_libm(av, tab)));
+  }
+  x[e] = __fmul_rn(acc, 0.25f);
+}
+
+// R_s[i] += 2 sigma(inject_s / 4) y[i], a thread a (token, value).
+__global__ void __launch_bounds__(kHcWG) pf_hc_post(float *R, const float *y, const float *inj, uint32_t T,
+                                                    uint32_t H) {
+  __shared__ uint64_t tab[32];
+  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
+  const uint64_t e = (uint64_t)blockIdx.x * kHcWG + threadIdx.x;
+  if (e >= (uint64_t)T * H) return;
+  const uint32_t t = (uint32_t)(e / H), i = (uint32_t)(e % H);
+  const float yv = y[e];
+#pragma unroll
+  for (uint32_t s = 0; s < kHcStreams4; s++) {
+    const float w = __fmul_rn(2.0f, sigmoid_libm(__fmul_rn(inj[(uint64_t)t * kHcStreams4 + s], 0.25f), tab));
+    float *r = R + ((uint64_t)t * kHcStreams4 + s) * H + i;
+    *r = __fadd_rn(*r, __fmul_rn(w, yv));
+  }
+}
+
+}  // namespace
+
+hipError_t prefill_hc_pre(const HcShape &S, const HcLayer &L, const HcBufs &b, const float *R, bool force_open,
+                          hipStream_t st) {
+  const uint32_t H = S.H, lr = S.lr, T = S.T, D = kHcStreams4 * H, Md = lr + kHcStreams4;
+  pf_hc_norm<<<T, kHcWG, 0, st>>>(R, L.gamma, H, b.n, b.nn, b.cnt);
+  // The down GEMM: K = 4H in kHcDownSplit parts. Roundings on a sum's path: here at most 4 per matrix-core step over a
+  // kGroupK chain, one per group total, one per split; in the fixed order 8 (chain) + 1 + 3 (tree) + K / 2048 (the
+  // slot's chunks) + 16 (the slots); doubled, and 2^-53 each.
+  const uint32_t ksplit = (D / kHcDownSplit + kGroupK - 1) / kGroupK * kGroupK;
+  const double nd = 2.0 * (4.0 * (kGroupK / 4) + D / kGroupK + kHcDownSplit + 28.0 + D / 2048.0);
+  const dim3 gd(((Md + 63) / 64) * ((T + 63) / 64), kHcDownSplit);
+  pf_hc_gemm<false><<<gd, kHcWG, 0, st>>>(L.w_down, lr, L.w_inj, Md, D, b.n, T, ksplit, b.part, nullptr, nullptr,
+                                          nullptr, 0.0);
+  pf_hc_down_fin<<<T, kHcWG, 0, st>>>(b.part, T, Md, kHcDownSplit, L.row_norm, b.nn, nd * 0x1p-53, force_open, b.raw,
+                                      b.open, b.cnt);
+  pf_hc_down_fix<<<256, kHcWG, 0, st>>>(L.w_down, L.w_inj, lr, D, b.n, b.open, b.cnt, b.raw);
+  pf_hc_down_epi<<<T, kHcWG, 0, st>>>(b.raw, lr, b.l, b.inj, b.ln);
+  // The up GEMM: 4H rows of W_up against bf16(l), K = lr; the fixed order is a k chain of lr terms.
+  const double nu = 2.0 * (4.0 * (kGroupK / 4) + lr / (double)kGroupK + 1.0 + lr);
+  const dim3 gu(((D + 63) / 64) * ((T + 63) / 64), 1);
+  pf_hc_gemm<true><<<gu, kHcWG, 0, st>>>(L.w_up, D, nullptr, D, lr, b.l, T, lr, nullptr, b.a, L.row_norm + Md, b.ln,
+                                         nu * 0x1p-53);
+  const uint64_t nx = (uint64_t)T * H;
+  pf_hc_mix<<<(uint32_t)((nx + kHcWG - 1) / kHcWG), kHcWG, 0, st>>>(b.n, b.a, T, H, b.x);
+  return hipGetLastError();
+}
+
+hipError_t prefill_hc_post(const HcShape &S, const HcBufs &b, float *R, const float *y, hipStream_t st) {
+  const uint64_t nx = (uint64_t)S.T * S.H;
+  pf_hc_post<<<(uint32_t)((nx + kHcWG - 1) / kHcWG), kHcWG, 0, st>>>(R, y, b.inj, S.T, S.H);
+  return hipGetLastError();
+}
+
+}  // namespace c0ven

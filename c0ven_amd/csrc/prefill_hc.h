@@ -1,0 +1,41 @@
+// The hyper-connection mix and combine around the prefill block (more tokens than the decode kernel takes): the
+// kernels of moe_prefill_hc.hip and what they take.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace c0ven {
+
+struct HcShape {
+  uint32_t H, lr, T;  // n_embd, the low rank (a multiple of 8), tokens
+};
+
+// One layer's module on the device: gamma (4 H fp32), W_down (lr x 4H bf16), W_inject (4 x 4H), W_up (4H x lr), and
+// the 2-norms of their rows (W_down's and W_inject's lr + 4, then W_up's 4H; fp64, rounded up).
+struct HcLayer {
+  const float *gamma;
+  const uint16_t *w_down, *w_inj, *w_up;
+  const double *row_norm;
+};
+
+// Scratch for T tokens: the normed streams n (T x 4 x H), their bf16 2-norms, the down GEMM's fp64 partials
+// (kHcDownSplit x T x (lr + 4)) and rounded sums (T x (lr + 4)), the list of sums whose rounding the bound left open
+// (pairs t, row; room for all) and its count, l (T x lr) and its bf16 norms, the inject logits (T x 4), the up
+// GEMM's sums a (T x 4H), and x (T x H).
+struct HcBufs {
+  float *n, *raw, *l, *inj, *a, *x;
+  double *nn, *ln, *part;
+  uint32_t *open, *cnt;
+};
+
+constexpr uint32_t kHcDownSplit = 4;
+
+// R (T x 4 x H, device) to the block's input x (bufs.x) and the inject logits; force_open (tests) sends every down
+// sum through the exact-order recomputation.
+hipError_t prefill_hc_pre(const HcShape &S, const HcLayer &L, const HcBufs &b, const float *R, bool force_open,
+                          hipStream_t st);
+// R_s += 2 sigma(inject_s / 4) y.
+hipError_t prefill_hc_post(const HcShape &S, const HcBufs &b, float *R, const float *y, hipStream_t st);
+
+}  // namespace c0ven

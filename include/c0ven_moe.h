@@ -77,6 +77,9 @@ typedef struct {
  * y too) instead of on the bf16 matrix cores within a bound, with the top k certified (the same ids; the weights and
  * y within the block's tolerance). */
 #define MOE_FLAG_EXACT_ROUTER 1u
+/* moe_config.flags: the prefill hyper-connection mix sums every W_down and W_inject product in the decode path's fixed
+ * order, not only those its bound leaves open (slow: the check of that fallback). */
+#define MOE_FLAG_HC_FIXED_ORDER 2u
 
 /* The routing result of a forward, per token: k expert ids in rank order and their weights. */
 typedef struct {
