@@ -56,6 +56,7 @@ struct Layer {
   float *hc_gamma = nullptr;
   uint16_t *hc_down = nullptr, *hc_inj = nullptr, *hc_up = nullptr;
   double *hc_rn = nullptr;  // the 2-norms of W_down's, W_inject's and W_up's rows (the prefill mix's bound)
+  int *hc_rlsb = nullptr;   // the least lsb exponent of each of those rows' nonzero bf16 values
   bool has_hc = false;
 };
 
@@ -542,6 +543,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
         L.hc_inj = c->alloc<uint16_t>((uint64_t)kHcStreams * kHcStreams * H);
         L.hc_up = c->alloc<uint16_t>((uint64_t)kHcStreams * H * g.hc_lr);
         L.hc_rn = c->alloc<double>((uint64_t)g.hc_lr + kHcStreams + (uint64_t)kHcStreams * H);
+        L.hc_rlsb = c->alloc<int>((uint64_t)g.hc_lr + kHcStreams + (uint64_t)kHcStreams * H);
       }
     }
     // Scratch for max_tokens tokens of n_used + 1 assignments (the pre-routed path may give a token its shared
@@ -628,10 +630,13 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
         HcBufs &b = c->hcp;
         b.n = c->alloc<float>(TM * D);
         b.nn = c->alloc<double>(TM);
+        b.nlsb = c->alloc<int>(TM);
+        b.llsb = c->alloc<int>(TM);
         b.part = c->alloc<double>(kHcDownSplit * TM * Md);
         b.raw = c->alloc<float>(TM * Md);
         b.open = c->alloc<uint32_t>(2 * TM * Md);
-        b.cnt = c->alloc<uint32_t>(1);
+        b.open_up = c->alloc<uint32_t>(2 * TM * D);
+        b.cnt = c->alloc<uint32_t>(2);
         b.l = c->alloc<float>(TM * g.hc_lr);
         b.ln = c->alloc<double>(TM);
         b.inj = c->alloc<float>(TM * kHcStreams);
@@ -854,10 +859,20 @@ MOE_API moe_status moe_load_hc(moe_ctx *c, uint32_t layer, const float *gamma, c
       }
       return std::sqrt(ss) * (1.0 + 0x1p-30);
     };
-    for (uint32_t j = 0; j < g.hc_lr; j++) rn[j] = norm(w_down + (uint64_t)j * D, D);
-    for (uint32_t j = 0; j < kHcStreams; j++) rn[g.hc_lr + j] = norm(w_inject + (uint64_t)j * D, D);
-    for (uint64_t j = 0; j < D; j++) rn[g.hc_lr + kHcStreams + j] = norm(w_up + j * g.hc_lr, g.hc_lr);
+    std::vector<int> rl(rn.size());
+    const auto lsb = [](const uint16_t *w, uint64_t n) {  // 2^(e - 134) for exponent field e; zeros add no bits
+      int m = 1 << 20;
+      for (uint64_t i = 0; i < n; i++)
+        if (w[i] & 0x7fffu) m = std::min(m, ((w[i] >> 7) & 0xffu) == 0u ? -133 : (int)((w[i] >> 7) & 0xffu) - 134);
+      return m;
+    };
+    for (uint32_t j = 0; j < g.hc_lr; j++) rn[j] = norm(w_down + (uint64_t)j * D, D), rl[j] = lsb(w_down + (uint64_t)j * D, D);
+    for (uint32_t j = 0; j < kHcStreams; j++)
+      rn[g.hc_lr + j] = norm(w_inject + (uint64_t)j * D, D), rl[g.hc_lr + j] = lsb(w_inject + (uint64_t)j * D, D);
+    for (uint64_t j = 0; j < D; j++)
+      rn[g.hc_lr + kHcStreams + j] = norm(w_up + j * g.hc_lr, g.hc_lr), rl[g.hc_lr + kHcStreams + j] = lsb(w_up + j * g.hc_lr, g.hc_lr);
     check(hipMemcpy(L.hc_rn, rn.data(), rn.size() * sizeof(double), hipMemcpyHostToDevice), "upload hc norms");
+    check(hipMemcpy(L.hc_rlsb, rl.data(), rl.size() * sizeof(int), hipMemcpyHostToDevice), "upload hc lsb");
     L.has_hc = true;
   });
 }
@@ -876,7 +891,7 @@ MOE_API moe_status moe_forward_hc_async(moe_ctx *c, uint32_t layer, float *R_dev
     hipStream_t s = stream ? (hipStream_t)stream : c->stream;
     if (ntok > c->tdec) {  // the prefill path: the mix's kernels, the block, the combine's kernel
       const HcShape S{g.n_embd, g.hc_lr, ntok};
-      const HcLayer HL{L.hc_gamma, L.hc_down, L.hc_inj, L.hc_up, L.hc_rn};
+      const HcLayer HL{L.hc_gamma, L.hc_down, L.hc_inj, L.hc_up, L.hc_rn, L.hc_rlsb};
       check(prefill_hc_pre(S, HL, c->hcp, R_dev, (g.flags & MOE_FLAG_HC_FIXED_ORDER) != 0, s), "prefill hc mix launch");
       float *y = y_dev ? y_dev : c->y_dev;
       forward_dev(c, layer, c->hcp.x, ntok, y, ids_dev, w_dev, s);

@@ -7,10 +7,12 @@
 // Here they run on the fp64 matrix cores (v_mfma_f64_16x16x4f64) in another order, with a bound on the difference:
 // each sum path has at most n_mine roundings here and n_ref in the fixed order, so the two fp64 values are within
 // (n_mine + n_ref) 2^-53 sum|p| <= (n_mine + n_ref) 2^-53 ||w||_2 ||x||_2 of each other (Cauchy-Schwarz on the bf16
-// values). Where the fp32 rounding of every value in that interval is the same, it is the fixed order's rounding.
-// Otherwise the sum is recomputed in the fixed order: W_up's (a k-order chain of at most 512 terms) by the thread
-// that found it open, W_down's and W_inject's (the decode kernel's 512-value-chunk tree) by one wave each, from a
-// list, in a kernel of its own.
+// values). Where the fp32 rounding of every value in that interval is the same, it is the fixed order's rounding; and
+// where the products' bits span fewer than 53 (the least lsb of the row's and of the token's values against the
+// Cauchy-Schwarz bound on sum|p|), both sums are exact, whatever their order (ties of fp32 rounding are common for
+// W_up's short sums, and this settles them).
+// Otherwise the sum is recomputed in the fixed order, one wave an open sum, from a list, in a kernel of its own:
+// W_up's a k-order chain of at most 512 terms, W_down's and W_inject's the decode kernel's 512-value-chunk tree.
 #include <hip/hip_runtime.h>
 
 #include "device_math.h"
@@ -27,6 +29,13 @@ constexpr uint32_t kGroupK = 128;  // values a matrix-core chain sums before its
 
 __device__ __forceinline__ uint32_t lane_of() { return threadIdx.x & 63u; }
 
+// The lsb exponent of a bf16 value's bits (2^(e - 134) for exponent field e, 2^-133 for a subnormal); a large value
+// for zero, which adds no bits to a sum.
+__device__ __forceinline__ int bf16_lsb_of(float v) {
+  const uint32_t u = __float_as_uint(v), e = (u >> 23) & 0xffu;
+  return (u & 0x7fff0000u) == 0u ? (1 << 20) : (e == 0u ? -133 : (int)e - 134);
+}
+
 __device__ __forceinline__ double bf16_lo(uint32_t w) { return (double)__uint_as_float(w << 16); }
 __device__ __forceinline__ double bf16_hi(uint32_t w) { return (double)__uint_as_float(w & 0xffff0000u); }
 
@@ -42,14 +51,27 @@ __device__ __forceinline__ double wg_sum(double v, double *red) {
   return s;
 }
 
+__device__ __forceinline__ int wg_min(int v, int *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if (lane_of() == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const int m = min(min(red[0], red[1]), min(red[2], red[3]));
+  __syncthreads();
+  return m;
+}
+
 // Token t (one work-group): each stream as RMSNorm(R_s) gamma_s, the decode kernel's hc_norm_item arithmetic (each
 // thread's squares in order, then wg_sum; mean rounded to fp32; 1 / sqrtf(mean + 1e-6)), and the 2-norm of bf16(n),
-// rounded up. Work-group 0 clears the open list's count.
+// rounded up. Work-group 0 clears the open lists' counts.
 __global__ void __launch_bounds__(kHcWG) pf_hc_norm(const float *R, const float *gamma, uint32_t H, float *n,
-                                                    double *nn, uint32_t *cnt) {
+                                                    double *nn, int *nlsb, uint32_t *cnt) {
   __shared__ double red[4];
+  __shared__ int redi[4];
+  int lsb = 1 << 20;
   const uint32_t t = blockIdx.x;
-  if (t == 0 && threadIdx.x == 0) *cnt = 0u;
+  if (t == 0 && threadIdx.x < 2) cnt[threadIdx.x] = 0u;
   double sq = 0.0;
   for (uint32_t s = 0; s < kHcStreams4; s++) {
     const float *r = R + ((uint64_t)t * kHcStreams4 + s) * H;
@@ -62,12 +84,28 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_norm(const float *R, const float 
     for (uint32_t i = threadIdx.x; i < H; i += kHcWG) {
       const float v = __fmul_rn(__fmul_rn(r[i], scale), gamma[s * H + i]);
       o[i] = v;
-      const double b = (double)round_bf16(v);
+      const float bv = round_bf16(v);
+      const double b = (double)bv;
       sq = __builtin_fma(b, b, sq);
+      lsb = min(lsb, bf16_lsb_of(bv));
     }
   }
   sq = wg_sum(sq, red);
-  if (threadIdx.x == 0) nn[t] = sqrt(sq) * (1.0 + 0x1p-30);
+  lsb = wg_min(lsb, redi);
+  if (threadIdx.x == 0) nn[t] = sqrt(sq) * (1.0 + 0x1p-30), nlsb[t] = lsb;
+}
+
+// Whether an fp64 sum v of a row's and a token's bf16 products rounds to fp32 as the fixed order's does. Exact: every
+// product is a multiple of 2^(lr + lt) and sum|p| <= rn tn < 2^(lr + lt + 53), so every partial sum of any order is
+// representable and both orders give the exact sum. Otherwise bounded: the two fp64 values are within bnd, and every
+// value in [v - bnd, v + bnd] rounds to the same fp32.
+__device__ __forceinline__ bool certain(double v, double rn, double tn, int lr, int lt, double bound_k) {
+  if (!__builtin_isfinite(v)) return false;
+  const double m = rn * tn;
+  if (lr + lt < 900 && m < ldexp(1.0, lr + lt + 53)) return true;
+  const double bnd = bound_k * m;
+  const float f = (float)v;
+  return (float)(v - bnd) == f && (float)(v + bnd) == f;
 }
 
 // C = bf16(A) bf16(B)^T on the fp64 matrix cores: rows of A (M of them: A0's first M0, then A1's), tokens of B (N rows
@@ -76,13 +114,15 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_norm(const float *R, const float 
 // holds A[row l % 16][k + 4 g + m] and B[token l % 16][k + 4 g + m] for MFMA step m of a 16-value chunk: both operands
 // take the same k in the same place, so each step adds 64 of the row-token products (the order of a sum is free
 // here: the bound covers any). Each kGroupK values' chain starts from zero and is added to an fp64 total.
-// kUp: one split; the sums are certified here (row norms rn, token norms tn, the fixed order's k chain where open)
-// and written as fp32 to out32 (N x M). Otherwise the fp64 totals go to part (split x N x M).
+// kUp: one split; the sums are certified here (row norms rn, token norms tn) and written as fp32 to out32 (N x M), an
+// open one's (token, row) to the list open (pf_hc_up_fix writes it). Otherwise the fp64 totals go to part
+// (split x N x M).
 template <bool kUp>
 __global__ void __launch_bounds__(kHcWG) pf_hc_gemm(const uint16_t *A0, uint32_t M0, const uint16_t *A1, uint32_t M,
                                                     uint32_t K, const float *B, uint32_t N, uint32_t ksplit,
                                                     double *part, float *out32, const double *rn, const double *tn,
-                                                    double bound_k) {
+                                                    const int *rl, const int *tl, double bound_k, uint32_t *open,
+                                                    uint32_t *cnt) {
   const uint32_t nmt = (M + 63) / 64, mt = blockIdx.x % nmt, nt = blockIdx.x / nmt, split = blockIdx.y;
   const uint32_t lane = lane_of(), w = threadIdx.x >> 6, g = lane / 16, c16 = lane % 16;
   const uint32_t m0 = 64 * mt + 32 * (w & 1), n0 = 64 * nt + 32 * (w >> 1);
@@ -151,19 +191,12 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_gemm(const uint16_t *A0, uint32_t
         if (row >= M || tok >= N) continue;
         const double v = tot[i][j][q];
         if constexpr (kUp) {
-          const double bnd = bound_k * rn[row] * tn[tok];
-          const float f = (float)v;
-          float o = f;
-          if (!(__builtin_isfinite(v) && (float)(v - bnd) == f && (float)(v + bnd) == f)) {
-            // Open: the fixed order (k ascending, one fused step a term, from zero).
-            const uint16_t *wr = A0 + (uint64_t)row * K;
-            const float *xr = B + (uint64_t)tok * K;
-            double c = 0.0;
-            for (uint32_t k = 0; k < K; k++)
-              c = __builtin_fma((double)__uint_as_float((uint32_t)wr[k] << 16), (double)round_bf16(xr[k]), c);
-            o = (float)c;
+          if (certain(v, rn[row], tn[tok], rl[row], tl[tok], bound_k)) {
+            out32[(uint64_t)tok * M + row] = (float)v;
+          } else {  // open: pf_hc_up_fix writes it
+            const uint32_t at = atomicAdd(cnt, 1u);
+            open[2 * at] = tok, open[2 * at + 1] = row;
           }
-          out32[(uint64_t)tok * M + row] = o;
         } else {
           part[((uint64_t)split * N + tok) * M + row] = v;
         }
@@ -171,19 +204,18 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_gemm(const uint16_t *A0, uint32_t
 }
 
 // Token t's down sums (rows < lr of W_down, then the 4 of W_inject): the splits added in order, certified against the
-// fixed order (bound_k rn tn), rounded to fp32 into raw (T x (lr + 4)); an open one's (t, row) goes to the list (its
+// fixed order (certain), rounded to fp32 into raw (T x (lr + 4)); an open one's (t, row) goes to the list (its
 // raw entry is written by pf_hc_down_fix). force_open sends all.
 __global__ void __launch_bounds__(kHcWG) pf_hc_down_fin(const double *part, uint32_t T, uint32_t M, uint32_t nsplit,
-                                                        const double *rn, const double *tn, double bound_k,
-                                                        bool force_open, float *raw, uint32_t *open, uint32_t *cnt) {
+                                                        const double *rn, const double *tn, const int *rl,
+                                                        const int *tl, double bound_k, bool force_open, float *raw,
+                                                        uint32_t *open, uint32_t *cnt) {
   const uint32_t t = blockIdx.x;
   for (uint32_t row = threadIdx.x; row < M; row += kHcWG) {
     double v = 0.0;
     for (uint32_t s = 0; s < nsplit; s++) v = __dadd_rn(v, part[((uint64_t)s * T + t) * M + row]);
-    const double bnd = bound_k * rn[row] * tn[t];
-    const float f = (float)v;
-    if (!force_open && __builtin_isfinite(v) && (float)(v - bnd) == f && (float)(v + bnd) == f) {
-      raw[(uint64_t)t * M + row] = f;
+    if (!force_open && certain(v, rn[row], tn[t], rl[row], tl[t], bound_k)) {
+      raw[(uint64_t)t * M + row] = (float)v;
     } else {
       const uint32_t at = atomicAdd(cnt, 1u);
       open[2 * at] = t, open[2 * at + 1] = row;
@@ -233,12 +265,46 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_down_fix(const uint16_t *w_down, 
   }
 }
 
+// The open up sums in the fixed order: a k-order chain over the lr values of W_up's row against bf16(l) of the token,
+// one fused step a term from zero. One wave an entry: the wave brings the row and l into its LDS, lane 0 runs the
+// chain from there.
+__global__ void __launch_bounds__(kHcWG) pf_hc_up_fix(const uint16_t *w_up, uint32_t lr, uint32_t M, const float *l,
+                                                      const uint32_t *open, const uint32_t *cnt, float *out32) {
+  __shared__ __align__(16) float ws[kHcWG / 64][512], xs[kHcWG / 64][512];
+  const uint32_t lane = lane_of(), wv = threadIdx.x >> 6, nw = gridDim.x * (kHcWG / 64);
+  for (uint32_t e = blockIdx.x * (kHcWG / 64) + wv; e < *cnt; e += nw) {
+    const uint32_t t = open[2 * e], row = open[2 * e + 1];
+    const uint16_t *wr = w_up + (uint64_t)row * lr;
+    const float *xr = l + (uint64_t)t * lr;
+    for (uint32_t k = lane; k < lr; k += 64) {
+      ws[wv][k] = __uint_as_float((uint32_t)wr[k] << 16);
+      xs[wv][k] = round_bf16(xr[k]);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {
+      double c = 0.0;
+      for (uint32_t k = 0; k < lr; k += 4) {
+        const float4 w4 = *(const float4 *)&ws[wv][k], x4 = *(const float4 *)&xs[wv][k];
+        c = __builtin_fma((double)w4.x, (double)x4.x, c);
+        c = __builtin_fma((double)w4.y, (double)x4.y, c);
+        c = __builtin_fma((double)w4.z, (double)x4.z, c);
+        c = __builtin_fma((double)w4.w, (double)x4.w, c);
+      }
+      out32[(uint64_t)t * M + row] = (float)c;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // Token t: l = silu(v / 4) for W_down's rows (the quarter exact; z / (1 + e^-z)), the inject logits for W_inject's,
-// and the 2-norm of bf16(l), rounded up.
+// and the 2-norm (rounded up) and least lsb exponent of bf16(l).
 __global__ void __launch_bounds__(kHcWG) pf_hc_down_epi(const float *raw, uint32_t lr, float *l, float *inj,
-                                                        double *ln) {
+                                                        double *ln, int *llsb) {
   __shared__ uint64_t tab[32];
   __shared__ double red[4];
+  __shared__ int redi[4];
+  int lsb = 1 << 20;
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
   const uint32_t t = blockIdx.x, M = lr + kHcStreams4;
@@ -249,14 +315,17 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_down_epi(const float *raw, uint32
       const float z = __fmul_rn(v, 0.25f);
       const float o = __fdiv_rn(z, __fadd_rn(1.0f, expf_libm(-z, tab)));
       l[(uint64_t)t * lr + j] = o;
-      const double b = (double)round_bf16(o);
+      const float bo = round_bf16(o);
+      const double b = (double)bo;
       sq = __builtin_fma(b, b, sq);
+      lsb = min(lsb, bf16_lsb_of(bo));
     } else {
       inj[(uint64_t)t * kHcStreams4 + j - lr] = v;
     }
   }
   sq = wg_sum(sq, red);
-  if (threadIdx.x == 0) ln[t] = sqrt(sq) * (1.0 + 0x1p-30);
+  lsb = wg_min(lsb, redi);
+  if (threadIdx.x == 0) ln[t] = sqrt(sq) * (1.0 + 0x1p-30), llsb[t] = lsb;
 }
 
 // x[t][i] = (sum over s in order of n_s[i] sigma(a_s[i])) / 4, a thread a value.
@@ -300,7 +369,7 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_post(float *R, const float *y, co
 hipError_t prefill_hc_pre(const HcShape &S, const HcLayer &L, const HcBufs &b, const float *R, bool force_open,
                           hipStream_t st) {
   const uint32_t H = S.H, lr = S.lr, T = S.T, D = kHcStreams4 * H, Md = lr + kHcStreams4;
-  pf_hc_norm<<<T, kHcWG, 0, st>>>(R, L.gamma, H, b.n, b.nn, b.cnt);
+  pf_hc_norm<<<T, kHcWG, 0, st>>>(R, L.gamma, H, b.n, b.nn, b.nlsb, b.cnt);
   // The down GEMM: K = 4H in kHcDownSplit parts. Roundings on a sum's path: here at most 4 per matrix-core step over a
   // kGroupK chain, one per group total, one per split; in the fixed order 8 (chain) + 1 + 3 (tree) + K / 2048 (the
   // slot's chunks) + 16 (the slots); doubled, and 2^-53 each.
@@ -308,16 +377,17 @@ hipError_t prefill_hc_pre(const HcShape &S, const HcLayer &L, const HcBufs &b, c
   const double nd = 2.0 * (4.0 * (kGroupK / 4) + D / kGroupK + kHcDownSplit + 28.0 + D / 2048.0);
   const dim3 gd(((Md + 63) / 64) * ((T + 63) / 64), kHcDownSplit);
   pf_hc_gemm<false><<<gd, kHcWG, 0, st>>>(L.w_down, lr, L.w_inj, Md, D, b.n, T, ksplit, b.part, nullptr, nullptr,
-                                          nullptr, 0.0);
-  pf_hc_down_fin<<<T, kHcWG, 0, st>>>(b.part, T, Md, kHcDownSplit, L.row_norm, b.nn, nd * 0x1p-53, force_open, b.raw,
-                                      b.open, b.cnt);
+                                          nullptr, nullptr, nullptr, 0.0, nullptr, nullptr);
+  pf_hc_down_fin<<<T, kHcWG, 0, st>>>(b.part, T, Md, kHcDownSplit, L.row_norm, b.nn, L.row_lsb, b.nlsb,
+                                      nd * 0x1p-53, force_open, b.raw, b.open, b.cnt);
   pf_hc_down_fix<<<256, kHcWG, 0, st>>>(L.w_down, L.w_inj, lr, D, b.n, b.open, b.cnt, b.raw);
-  pf_hc_down_epi<<<T, kHcWG, 0, st>>>(b.raw, lr, b.l, b.inj, b.ln);
+  pf_hc_down_epi<<<T, kHcWG, 0, st>>>(b.raw, lr, b.l, b.inj, b.ln, b.llsb);
   // The up GEMM: 4H rows of W_up against bf16(l), K = lr; the fixed order is a k chain of lr terms.
   const double nu = 2.0 * (4.0 * (kGroupK / 4) + lr / (double)kGroupK + 1.0 + lr);
   const dim3 gu(((D + 63) / 64) * ((T + 63) / 64), 1);
   pf_hc_gemm<true><<<gu, kHcWG, 0, st>>>(L.w_up, D, nullptr, D, lr, b.l, T, lr, nullptr, b.a, L.row_norm + Md, b.ln,
-                                         nu * 0x1p-53);
+                                         L.row_lsb + Md, b.llsb, nu * 0x1p-53, b.open_up, b.cnt + 1);
+  pf_hc_up_fix<<<256, kHcWG, 0, st>>>(L.w_up, lr, D, b.l, b.open_up, b.cnt + 1, b.a);
   const uint64_t nx = (uint64_t)T * H;
   pf_hc_mix<<<(uint32_t)((nx + kHcWG - 1) / kHcWG), kHcWG, 0, st>>>(b.n, b.a, T, H, b.x);
   return hipGetLastError();
