@@ -637,7 +637,8 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
         b.open = c->alloc<uint32_t>(2 * TM * Md);
         b.open_up = c->alloc<uint32_t>(2 * TM * D);
         b.cnt = c->alloc<uint32_t>(2);
-        b.l = c->alloc<float>(TM * g.hc_lr);
+        b.lb = c->alloc<uint16_t>(TM * g.hc_lr);
+        b.nb = c->alloc<uint16_t>(TM * D);
         b.ln = c->alloc<double>(TM);
         b.inj = c->alloc<float>(TM * kHcStreams);
         b.a = c->alloc<float>(TM * D);

@@ -63,10 +63,10 @@ __device__ __forceinline__ int wg_min(int v, int *red) {
 }
 
 // Token t (one work-group): each stream as RMSNorm(R_s) gamma_s, the decode kernel's hc_norm_item arithmetic (each
-// thread's squares in order, then wg_sum; mean rounded to fp32; 1 / sqrtf(mean + 1e-6)), and the 2-norm of bf16(n),
-// rounded up. Work-group 0 clears the open lists' counts.
+// thread's squares in order, then wg_sum; mean rounded to fp32; 1 / sqrtf(mean + 1e-6)), into n and as bf16 bits into
+// nb, and the 2-norm (rounded up) and least lsb exponent of bf16(n). Work-group 0 clears the open lists' counts.
 __global__ void __launch_bounds__(kHcWG) pf_hc_norm(const float *R, const float *gamma, uint32_t H, float *n,
-                                                    double *nn, int *nlsb, uint32_t *cnt) {
+                                                    uint16_t *nb, double *nn, int *nlsb, uint32_t *cnt) {
   __shared__ double red[4];
   __shared__ int redi[4];
   int lsb = 1 << 20;
@@ -81,10 +81,12 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_norm(const float *R, const float 
     const float mean = (float)(ss / (double)H);
     const float scale = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, 1e-6f)));
     float *o = n + ((uint64_t)t * kHcStreams4 + s) * H;
+    uint16_t *ob = nb + ((uint64_t)t * kHcStreams4 + s) * H;
     for (uint32_t i = threadIdx.x; i < H; i += kHcWG) {
       const float v = __fmul_rn(__fmul_rn(r[i], scale), gamma[s * H + i]);
       o[i] = v;
       const float bv = round_bf16(v);
+      ob[i] = (uint16_t)(__float_as_uint(bv) >> 16);
       const double b = (double)bv;
       sq = __builtin_fma(b, b, sq);
       lsb = min(lsb, bf16_lsb_of(bv));
@@ -108,8 +110,8 @@ __device__ __forceinline__ bool certain(double v, double rn, double tn, int lr, 
   return (float)(v - bnd) == f && (float)(v + bnd) == f;
 }
 
-// C = bf16(A) bf16(B)^T on the fp64 matrix cores: rows of A (M of them: A0's first M0, then A1's), tokens of B (N rows
-// of K fp32, rounded to bf16 here), K values. A work-group takes 64 rows x 64 tokens over the K range of its split
+// C = A B^T on the fp64 matrix cores, both bf16: rows of A (M of them: A0's first M0, then A1's), tokens of B (N rows
+// of K), K values. A work-group takes 64 rows x 64 tokens over the K range of its split
 // (blockIdx.y), wave w rows 32 (w & 1) .. and tokens 32 (w >> 1) .., as 2 x 2 tiles of 16 x 16. Lane l (g = l / 16)
 // holds A[row l % 16][k + 4 g + m] and B[token l % 16][k + 4 g + m] for MFMA step m of a 16-value chunk: both operands
 // take the same k in the same place, so each step adds 64 of the row-token products (the order of a sum is free
@@ -119,7 +121,7 @@ __device__ __forceinline__ bool certain(double v, double rn, double tn, int lr, 
 // (split x N x M).
 template <bool kUp>
 __global__ void __launch_bounds__(kHcWG) pf_hc_gemm(const uint16_t *A0, uint32_t M0, const uint16_t *A1, uint32_t M,
-                                                    uint32_t K, const float *B, uint32_t N, uint32_t ksplit,
+                                                    uint32_t K, const uint16_t *B, uint32_t N, uint32_t ksplit,
                                                     double *part, float *out32, const double *rn, const double *tn,
                                                     const int *rl, const int *tl, double bound_k, uint32_t *open,
                                                     uint32_t *cnt) {
@@ -127,7 +129,7 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_gemm(const uint16_t *A0, uint32_t
   const uint32_t lane = lane_of(), w = threadIdx.x >> 6, g = lane / 16, c16 = lane % 16;
   const uint32_t m0 = 64 * mt + 32 * (w & 1), n0 = 64 * nt + 32 * (w >> 1);
   const uint16_t *ar[2];
-  const float *br[2];
+  const uint16_t *br[2];
 #pragma unroll
   for (int f = 0; f < 2; f++) {
     const uint32_t row = min(m0 + 16 * f + c16, M - 1), tok = min(n0 + 16 * f + c16, N - 1);
@@ -151,19 +153,17 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_gemm(const uint16_t *A0, uint32_t
     for (uint32_t kc = kg; kc < kge; kc += 16) {
       const uint32_t k = kc + 4 * g;
       const bool ok = k < kge;  // (K is a multiple of 4: a lane's four values are all in or all out)
-      uint2 a[2];
-      float4 b[2];
+      uint2 a[2], b[2];
 #pragma unroll
       for (int f = 0; f < 2; f++) {
         a[f] = ok ? *(const uint2 *)(ar[f] + k) : make_uint2(0u, 0u);
-        b[f] = ok ? *(const float4 *)(br[f] + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        b[f] = ok ? *(const uint2 *)(br[f] + k) : make_uint2(0u, 0u);
       }
       double ad[2][4], bd[2][4];
 #pragma unroll
       for (int f = 0; f < 2; f++) {
         ad[f][0] = bf16_lo(a[f].x), ad[f][1] = bf16_hi(a[f].x), ad[f][2] = bf16_lo(a[f].y), ad[f][3] = bf16_hi(a[f].y);
-        bd[f][0] = (double)round_bf16(b[f].x), bd[f][1] = (double)round_bf16(b[f].y);
-        bd[f][2] = (double)round_bf16(b[f].z), bd[f][3] = (double)round_bf16(b[f].w);
+        bd[f][0] = bf16_lo(b[f].x), bd[f][1] = bf16_hi(b[f].x), bd[f][2] = bf16_lo(b[f].y), bd[f][3] = bf16_hi(b[f].y);
       }
 #pragma unroll
       for (int m = 0; m < 4; m++)
@@ -228,24 +228,22 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_down_fin(const double *part, uint
 // ((P0 + P7) + (P3 + P4)) + ((P1 + P6) + (P2 + P5)), P_m = a_m + a_(15 - m); slot 4 (c mod 4) + r takes the chunks'
 // sums in chunk order; the 16 slots added in order from zero. One wave an entry.
 __global__ void __launch_bounds__(kHcWG) pf_hc_down_fix(const uint16_t *w_down, const uint16_t *w_inj, uint32_t lr,
-                                                        uint32_t K, const float *n, const uint32_t *open,
+                                                        uint32_t K, const uint16_t *nb, const uint32_t *open,
                                                         const uint32_t *cnt, float *raw) {
   const uint32_t lane = lane_of(), r = lane / 16, nw = gridDim.x * (kHcWG / 64), M = lr + kHcStreams4;
   for (uint32_t e = blockIdx.x * (kHcWG / 64) + (threadIdx.x >> 6); e < *cnt; e += nw) {
     const uint32_t t = open[2 * e], row = open[2 * e + 1];
     const uint16_t *wr = row < lr ? w_down + (uint64_t)row * K : w_inj + (uint64_t)(row - lr) * K;
-    const float *xr = n + (uint64_t)t * K;
+    const uint16_t *xr = nb + (uint64_t)t * K;
     double slot[4] = {0.0, 0.0, 0.0, 0.0};  // slot 4 w + r, w = c mod 4 (lane 16 r holds its row's)
     for (uint32_t c = 0; c < K / 512; c++) {
       const uint32_t k0 = 512 * c + 8 * lane;
-      const uint4 wq = *(const uint4 *)(wr + k0);
-      const float4 x0 = *(const float4 *)(xr + k0), x1 = *(const float4 *)(xr + k0 + 4);
-      const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
-      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      const uint4 wq = *(const uint4 *)(wr + k0), xq = *(const uint4 *)(xr + k0);
+      const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w}, xw[4] = {xq.x, xq.y, xq.z, xq.w};
       double a = 0.0;
 #pragma unroll
       for (int k = 0; k < 8; k++)
-        a = __builtin_fma((k & 1) ? bf16_hi(ww[k / 2]) : bf16_lo(ww[k / 2]), (double)round_bf16(xs[k]), a);
+        a = __builtin_fma((k & 1) ? bf16_hi(ww[k / 2]) : bf16_lo(ww[k / 2]), (k & 1) ? bf16_hi(xw[k / 2]) : bf16_lo(xw[k / 2]), a);
       const double P = __dadd_rn(a, __shfl_xor(a, 15, 64));  // lanes m < 8 of a row: P_m
       double p[8];
 #pragma unroll
@@ -268,17 +266,17 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_down_fix(const uint16_t *w_down, 
 // The open up sums in the fixed order: a k-order chain over the lr values of W_up's row against bf16(l) of the token,
 // one fused step a term from zero. One wave an entry: the wave brings the row and l into its LDS, lane 0 runs the
 // chain from there.
-__global__ void __launch_bounds__(kHcWG) pf_hc_up_fix(const uint16_t *w_up, uint32_t lr, uint32_t M, const float *l,
+__global__ void __launch_bounds__(kHcWG) pf_hc_up_fix(const uint16_t *w_up, uint32_t lr, uint32_t M, const uint16_t *lb,
                                                       const uint32_t *open, const uint32_t *cnt, float *out32) {
   __shared__ __align__(16) float ws[kHcWG / 64][512], xs[kHcWG / 64][512];
   const uint32_t lane = lane_of(), wv = threadIdx.x >> 6, nw = gridDim.x * (kHcWG / 64);
   for (uint32_t e = blockIdx.x * (kHcWG / 64) + wv; e < *cnt; e += nw) {
     const uint32_t t = open[2 * e], row = open[2 * e + 1];
     const uint16_t *wr = w_up + (uint64_t)row * lr;
-    const float *xr = l + (uint64_t)t * lr;
+    const uint16_t *xr = lb + (uint64_t)t * lr;
     for (uint32_t k = lane; k < lr; k += 64) {
       ws[wv][k] = __uint_as_float((uint32_t)wr[k] << 16);
-      xs[wv][k] = round_bf16(xr[k]);
+      xs[wv][k] = __uint_as_float((uint32_t)xr[k] << 16);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
@@ -297,9 +295,9 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_up_fix(const uint16_t *w_up, uint
   }
 }
 
-// Token t: l = silu(v / 4) for W_down's rows (the quarter exact; z / (1 + e^-z)), the inject logits for W_inject's,
-// and the 2-norm (rounded up) and least lsb exponent of bf16(l).
-__global__ void __launch_bounds__(kHcWG) pf_hc_down_epi(const float *raw, uint32_t lr, float *l, float *inj,
+// Token t: l = silu(v / 4) for W_down's rows (the quarter exact; z / (1 + e^-z)) as bf16 bits (the up GEMM's operand),
+// the inject logits for W_inject's, and the 2-norm (rounded up) and least lsb exponent of bf16(l).
+__global__ void __launch_bounds__(kHcWG) pf_hc_down_epi(const float *raw, uint32_t lr, uint16_t *lb, float *inj,
                                                         double *ln, int *llsb) {
   __shared__ uint64_t tab[32];
   __shared__ double red[4];
@@ -314,8 +312,8 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_down_epi(const float *raw, uint32
     if (j < lr) {
       const float z = __fmul_rn(v, 0.25f);
       const float o = __fdiv_rn(z, __fadd_rn(1.0f, expf_libm(-z, tab)));
-      l[(uint64_t)t * lr + j] = o;
       const float bo = round_bf16(o);
+      lb[(uint64_t)t * lr + j] = (uint16_t)(__float_as_uint(bo) >> 16);
       const double b = (double)bo;
       sq = __builtin_fma(b, b, sq);
       lsb = min(lsb, bf16_lsb_of(bo));
@@ -369,25 +367,25 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_post(float *R, const float *y, co
 hipError_t prefill_hc_pre(const HcShape &S, const HcLayer &L, const HcBufs &b, const float *R, bool force_open,
                           hipStream_t st) {
   const uint32_t H = S.H, lr = S.lr, T = S.T, D = kHcStreams4 * H, Md = lr + kHcStreams4;
-  pf_hc_norm<<<T, kHcWG, 0, st>>>(R, L.gamma, H, b.n, b.nn, b.nlsb, b.cnt);
+  pf_hc_norm<<<T, kHcWG, 0, st>>>(R, L.gamma, H, b.n, b.nb, b.nn, b.nlsb, b.cnt);
   // The down GEMM: K = 4H in kHcDownSplit parts. Roundings on a sum's path: here at most 4 per matrix-core step over a
   // kGroupK chain, one per group total, one per split; in the fixed order 8 (chain) + 1 + 3 (tree) + K / 2048 (the
   // slot's chunks) + 16 (the slots); doubled, and 2^-53 each.
   const uint32_t ksplit = (D / kHcDownSplit + kGroupK - 1) / kGroupK * kGroupK;
   const double nd = 2.0 * (4.0 * (kGroupK / 4) + D / kGroupK + kHcDownSplit + 28.0 + D / 2048.0);
   const dim3 gd(((Md + 63) / 64) * ((T + 63) / 64), kHcDownSplit);
-  pf_hc_gemm<false><<<gd, kHcWG, 0, st>>>(L.w_down, lr, L.w_inj, Md, D, b.n, T, ksplit, b.part, nullptr, nullptr,
+  pf_hc_gemm<false><<<gd, kHcWG, 0, st>>>(L.w_down, lr, L.w_inj, Md, D, b.nb, T, ksplit, b.part, nullptr, nullptr,
                                           nullptr, nullptr, nullptr, 0.0, nullptr, nullptr);
   pf_hc_down_fin<<<T, kHcWG, 0, st>>>(b.part, T, Md, kHcDownSplit, L.row_norm, b.nn, L.row_lsb, b.nlsb,
                                       nd * 0x1p-53, force_open, b.raw, b.open, b.cnt);
-  pf_hc_down_fix<<<256, kHcWG, 0, st>>>(L.w_down, L.w_inj, lr, D, b.n, b.open, b.cnt, b.raw);
-  pf_hc_down_epi<<<T, kHcWG, 0, st>>>(b.raw, lr, b.l, b.inj, b.ln, b.llsb);
+  pf_hc_down_fix<<<256, kHcWG, 0, st>>>(L.w_down, L.w_inj, lr, D, b.nb, b.open, b.cnt, b.raw);
+  pf_hc_down_epi<<<T, kHcWG, 0, st>>>(b.raw, lr, b.lb, b.inj, b.ln, b.llsb);
   // The up GEMM: 4H rows of W_up against bf16(l), K = lr; the fixed order is a k chain of lr terms.
   const double nu = 2.0 * (4.0 * (kGroupK / 4) + lr / (double)kGroupK + 1.0 + lr);
   const dim3 gu(((D + 63) / 64) * ((T + 63) / 64), 1);
-  pf_hc_gemm<true><<<gu, kHcWG, 0, st>>>(L.w_up, D, nullptr, D, lr, b.l, T, lr, nullptr, b.a, L.row_norm + Md, b.ln,
+  pf_hc_gemm<true><<<gu, kHcWG, 0, st>>>(L.w_up, D, nullptr, D, lr, b.lb, T, lr, nullptr, b.a, L.row_norm + Md, b.ln,
                                          L.row_lsb + Md, b.llsb, nu * 0x1p-53, b.open_up, b.cnt + 1);
-  pf_hc_up_fix<<<256, kHcWG, 0, st>>>(L.w_up, lr, D, b.l, b.open_up, b.cnt + 1, b.a);
+  pf_hc_up_fix<<<256, kHcWG, 0, st>>>(L.w_up, lr, D, b.lb, b.open_up, b.cnt + 1, b.a);
   const uint64_t nx = (uint64_t)T * H;
   pf_hc_mix<<<(uint32_t)((nx + kHcWG - 1) / kHcWG), kHcWG, 0, st>>>(b.n, b.a, T, H, b.x);
   return hipGetLastError();

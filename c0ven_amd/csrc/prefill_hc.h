@@ -21,12 +21,13 @@ struct HcLayer {
   const int *row_lsb;
 };
 
-// Scratch for T tokens: the normed streams n (T x 4 x H), their bf16 2-norms, the down GEMM's fp64 partials
+// Scratch for T tokens: the normed streams n (T x 4 x H) and their bf16 bits, their bf16 2-norms, the down GEMM's fp64 partials
 // (kHcDownSplit x T x (lr + 4)) and rounded sums (T x (lr + 4)), the list of sums whose rounding the bound left open
-// (pairs t, row; room for all) and the up GEMM's, their counts, l (T x lr) and its bf16 norms, the inject logits
+// (pairs t, row; room for all) and the up GEMM's, their counts, bf16(l) (T x lr) and its norms, the inject logits
 // (T x 4), the up GEMM's sums a (T x 4H), and x (T x H).
 struct HcBufs {
-  float *n, *raw, *l, *inj, *a, *x;
+  float *n, *raw, *inj, *a, *x;
+  uint16_t *nb, *lb;  // bf16(n), bf16(l): the GEMMs' operands
   double *nn, *ln, *part;
   int *nlsb, *llsb;  // the least lsb exponent of each token's bf16(n), bf16(l)
   uint32_t *open, *open_up, *cnt;  // cnt[0]: open's entries (down), cnt[1]: open_up's (up; room for T x 4H)
