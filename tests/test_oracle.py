@@ -595,3 +595,28 @@ def test_hc_mix_against_float64_and_closed_forms():
         assert np.array_equal(x0[t], acc * np.float32(0.25))
     y = rng.standard_normal((T, H)).astype(np.float32)
     assert np.array_equal(h.HcModule.post(R, np.zeros((T, 4), np.float32), y), R + y[:, None, :])
+
+
+def test_forward_resident_reduces_to_its_parts():
+    """The hybrid oracle (experts off the device summed apart, after gs s): with every expert resident it is the plain
+    block bit for bit; with none resident and no shared expert it is compute_many over the token's jobs in rank order
+    (CpuExperts::compute_many's sum, core/cpu/experts.h:32-60)."""
+    import ctypes as C
+
+    def resident_forward(L, resident, x):
+        Lo, keep = L._orc_layer()
+        y = np.empty((x.shape[0], L.H), dtype=np.float32)
+        r = np.ascontiguousarray(resident, dtype=np.uint8)
+        assert h.oracle.orc_moe_forward_resident(C.byref(Lo), h.ptr(r), h.ptr(x), x.shape[0], L.H, h.ptr(y), L.H,
+                                                 4) == 0
+        del keep
+        return y
+
+    L = h.Layer(512, 256, 16, 4, moe.QT_Q4_K, moe.QT_Q8_0, seed=17, zipf=1.1)
+    x = h.tokens(5, 6, 512)
+    assert np.array_equal(resident_forward(L, np.ones(16, np.uint8), x), L.oracle_forward(x)[0])
+    L0 = h.Layer(512, 256, 16, 4, moe.QT_Q4_K, moe.QT_Q8_0, seed=18, zipf=1.1, has_shared=False)
+    y = resident_forward(L0, np.zeros(16, np.uint8), x)
+    _, ids, w = L0.oracle_route(x)
+    jobs = [(L0.experts[int(ids[t, k])], t, float(w[t, k])) for t in range(6) for k in range(4)]
+    assert np.array_equal(y, h.orc_compute_many(L0.gate_type, L0.down_type, 512, 256, jobs, x))
