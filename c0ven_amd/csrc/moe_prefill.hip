@@ -463,11 +463,7 @@ __global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint1
   const double nxt = __shfl_down(v, 1, 64), prv = __shfl_up(v, 1, 64);
   // Rank r's order against rank r + 1 is open when their intervals (each +- B) meet.
   const bool open = lane + 1 < K1 && !(v - nxt > 2.0 * B);
-#ifdef C0VEN_EXP_NO_EXACT
-  if (false) {
-#else
   if (__ballot(open) != 0ull) {
-#endif
     // The experts whose place is open: a ranked one whose interval meets a neighbour's, and, when the K-th place is
     // open, every expert ranked after the K-th whose interval reaches the K-th's. The others keep their approximate
     // logits: each is more than 2 B from every expert on one side of it, so its order against all of them stands.
