@@ -68,7 +68,8 @@ __host__ __device__ __forceinline__ constexpr uint32_t mfma_code_off(uint32_t j)
 
 // One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
 // with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0). out is in global
-// memory, or in LDS when kLds. kMfma: the codes in the prefill order (mfma_code_off) instead of value order. kPlain:
+// memory, or in LDS when kLds. kSplitG: q8_K's block sums as the f16 split at kActSplitH in place of the int32
+// sums. kMfma: the codes in the prefill order (mfma_code_off) instead of value order. kPlain:
 // plain global stores (the unit is read by later launches only).
 template <bool kLds = false, bool kSplitG = false, bool kMfma = false, bool kPlain = false>
 __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
@@ -105,15 +106,17 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
     part += __shfl_xor(part, 1, 32);
     part += __shfl_xor(part, 2, 32);
     put_word<kLds, uint64_t, kPlain>(out, coff, ((uint64_t)code[1] << 32) | code[0]);
-    if ((l32 & 3u) == 0) put_word<kLds, int, kPlain>(out, kActSums + l32, part);
-    if (l32 == 0) put_word<kLds, float, kPlain>(out, kActScales, d);
     if constexpr (kSplitG) {
-      // Block sum j = l32 / 4 split as 64 hi + lo (hi in [-64, 63], lo in [0, 63]) into the padding at kActSplitG.
+      // Block sum j = l32 / 4 split as 64 hi + lo (hi in [-64, 63], lo in [0, 63]), both as f16, at kActSplitH.
       if ((l32 & 3u) == 0) {
-        out[kActSplitG + l32 / 4] = (uint8_t)((uint32_t)(part >> 6) & 0xffu);
-        out[kActSplitG + 8 + l32 / 4] = (uint8_t)((uint32_t)part & 63u);
+        const int lo = part & 63;
+        put_word<kLds, uint16_t, kPlain>(out, kActSplitH + l32 / 2, f2h((float)lo));
+        put_word<kLds, uint16_t, kPlain>(out, kActSplitH + 16 + l32 / 2, f2h((float)(part - lo)));
       }
+    } else {
+      if ((l32 & 3u) == 0) put_word<kLds, int, kPlain>(out, kActSums + l32, part);
     }
+    if (l32 == 0) put_word<kLds, float, kPlain>(out, kActScales, d);
   } else {  // q8_0: blocks of 32, four lanes each
     float amax = 0.0f;
 #pragma unroll

@@ -107,13 +107,15 @@ C0VEN_HD uint64_t matrix_bytes(uint32_t type, uint32_t rows, uint32_t k) {
 // A quantised activation unit (one token's or one assignment's 256 values), 320 B in global memory:
 //   [0, 256)   the int8 codes;
 //   [256, 288) the scales as f32: q8_K's d at 256; q8_0's eight block d (their f16 values widened) at 256 + 4 b;
-//   [288, 320) q8_K only: the sums of each 32 codes as int32 (bsums[2j] + bsums[2j + 1]).
+//   [288, 320) q8_K only: the sums of each 32 codes as int32 (bsums[2j] + bsums[2j + 1]), or, in units written by
+//              the prefill quantiser, the same sums split for the Q4_K minimum MFMA (kActSplitH).
 // In LDS the kernels keep them kActLds apart, so the eight units a wave reads at once fall in distinct banks.
 constexpr uint32_t kActBytes = 320, kActScales = 256, kActSums = 288, kActLds = 336;
 // In LDS the 16 bytes of padding after a unit may hold its sums split for the Q4_K minimum MFMA (hi bytes, lo bytes).
 constexpr uint32_t kActSplit = 320;
-// In a q8_K unit in global memory written by the prefill quantiser, bytes 272-287 of the padding hold the same split
-// of the block sums (hi bytes of sums 0-7, then lo bytes), so that a unit can be copied to LDS verbatim.
-constexpr uint32_t kActSplitG = 272;
+// In a q8_K unit in global memory written by the prefill quantiser, bytes 288-319 hold each block sum s_j split as
+// 64 hi_j + lo_j (hi in [-64, 63], lo in [0, 63]) as f16 values: lo_0 .. lo_7, then 64 hi_0 .. 64 hi_7 (all exact in
+// f16), the B operand of one v_mfma_f32_16x16x16_f16 per position tile, so that a unit can be copied to LDS verbatim.
+constexpr uint32_t kActSplitH = 288;
 
 }  // namespace c0ven

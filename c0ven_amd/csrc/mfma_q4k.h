@@ -72,6 +72,8 @@ struct Q4kA {
   v4i_t lo[4], hi[4];  // chain step c: blocks 2 c (elements 0-1) and 2 c + 1 (elements 2-3), as join2 packs them
   long mn;
   float d[4], dmin[4];
+  // kHalfMin: mn as the f16 operand of the prefill form (q4k_terms_p) rather than the int8 one (q4k_terms_v).
+  template <bool kHalfMin = false>
   __device__ __forceinline__ void decode(const Q4kRaw &r, uint32_t lane) {
     const uint32_t w0 = r.sc[0], w1 = r.sc[1], w2 = r.sc[2];
     const uint32_t sc03 = w0 & 0x3f3f3f3fu, sc47 = (w2 & 0x0f0f0f0fu) | ((w0 >> 2) & 0x30303030u);
@@ -90,7 +92,16 @@ struct Q4kA {
       lo[c] = v4i_t{(int)mul_bytes(l0, kl_lo), (int)mul_bytes(l1, kl_lo), (int)mul_bytes(h0, kh_lo), (int)mul_bytes(h1, kh_lo)};
       hi[c] = v4i_t{(int)mul_bytes(l0, kl_hi), (int)mul_bytes(l1, kl_hi), (int)mul_bytes(h0, kh_hi), (int)mul_bytes(h1, kh_hi)};
     }
-    mn = lane < 16 ? pack2(m03, m47) : 0;
+    if constexpr (kHalfMin) {
+      // The A operand of v_mfma_f32_16x16x16_f16 against kActSplitH's split sums: k = 0-7 and 8-15 both the minima
+      // 0-7, so lane group g takes minima 4 (g % 2) .. + 3 as f16 (exact: at most 63).
+      const uint32_t m = (lane / 16) % 2 ? m47 : m03;
+      const auto h01 = __builtin_amdgcn_cvt_pkrtz((float)(m & 0xffu), (float)((m >> 8) & 0xffu));
+      const auto h23 = __builtin_amdgcn_cvt_pkrtz((float)((m >> 16) & 0xffu), (float)(m >> 24));
+      mn = pack2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+    } else {
+      mn = lane < 16 ? pack2(m03, m47) : 0;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) d[i] = h2f((uint16_t)r.dm[i]), dmin[i] = h2f((uint16_t)(r.dm[i] >> 16));
   }
@@ -108,13 +119,12 @@ struct ActB {
     split_sums(unit, g);
     ad = *(const float *)(unit + kActScales);
   }
-  // The same, with the sums' split already in the unit's padding (at split: kActSplit, written by put_split, or
-  // kActSplitG, written by the prefill quantiser).
-  __device__ __forceinline__ void load_presplit(const uint8_t *unit, uint32_t lane, uint32_t split = kActSplit) {
+  // The same, with the sums' split already in the unit's padding (at kActSplit, written by put_split).
+  __device__ __forceinline__ void load_presplit(const uint8_t *unit, uint32_t lane) {
     const uint32_t g = lane / 16;
 #pragma unroll
     for (int s = 0; s < 8; s++) q[s] = *(const long *)(unit + 32 * s + 8 * g);
-    const uint4 v = *(const uint4 *)(unit + split);
+    const uint4 v = *(const uint4 *)(unit + kActSplit);
     bh = g == 0 ? pack2(v.x, v.y) : 0;
     bl = g == 0 ? pack2(v.z, v.w) : 0;
     ad = *(const float *)(unit + kActScales);
@@ -177,21 +187,43 @@ __device__ __forceinline__ void q4k_terms(const Q4kA &a, const ActB &b, float t[
   q4k_terms_v(a, bq, b.bh, b.bl, b.ad, t);
 }
 
-// A prefill activation unit's B operands (codes in the mfma_code_off order, split sums at kActSplitG): four 16-byte
-// reads for the code chains.
+// A prefill activation unit's B operands (codes in the mfma_code_off order, split sums as f16 at kActSplitH): four
+// 16-byte reads for the code chains, one 8-byte read for the minimum part.
 struct ActBP {
   v4i_t q[4];
-  long bh, bl;
+  long bm;
   float ad;
   __device__ __forceinline__ void load(const uint8_t *unit, uint32_t lane) {
     const uint32_t g = lane / 16;
 #pragma unroll
     for (int c = 0; c < 4; c++) q[c] = *(const v4i_t *)(unit + 64 * c + 16 * g);
-    const uint4 v = *(const uint4 *)(unit + kActSplitG);
-    bh = g == 0 ? pack2(v.x, v.y) : 0;
-    bl = g == 0 ? pack2(v.z, v.w) : 0;
+    bm = *(const long *)(unit + kActSplitH + 8 * g);
     ad = *(const float *)(unit + kActScales);
   }
 };
+
+typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+// q4k_terms_v for the prefill units (a decoded with kHalfMin): imin = sum_j mn_j (lo_j + 64 hi_j) from one
+// v_mfma_f32_16x16x16_f16, whose products and partial sums are integers below 2^24 (|imin| <= 8 * 63 * 4064), so
+// exact in f32: the same float the integer path converts.
+__device__ __forceinline__ void q4k_terms_p(const Q4kA &a, const ActBP &b, float t[4]) {
+  v4i_t dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    dlo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.lo[c], b.q[c], dlo, 0, 0, 0);
+    dhi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.hi[c], b.q[c], dhi, 0, 0, 0);
+  }
+  const v4f_t mf = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h_t, a.mn), __builtin_bit_cast(v4h_t, b.bm),
+                                                         v4f_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int isum = 8 * dhi[i] + dlo[i];
+    const float dd = __fmul_rn(a.d[i], b.ad), dm = __fmul_rn(a.dmin[i], b.ad);
+    const float pm = __fmul_rn(dm, mf[i]);
+    t[i] = __builtin_fmaf(dd, (float)isum, -pm);
+  }
+}
 
 }  // namespace c0ven

@@ -693,7 +693,7 @@ constexpr uint32_t gemm_rows() { return kGU ? 64 : 128; }
 
 // A work-group's kPos positions' activation units go into LDS by direct global-to-LDS loads: LDS holds 21 pieces of
 // 16 B a position (kActLds = 336), so load i fills pieces 64 i .. 64 i + 63 contiguously, lane l piece 64 i + l, of
-// position (64 i + l) / 21. Pieces 0-19 are the 320-byte global unit verbatim (with the split block sums at kActSplitG
+// position (64 i + l) / 21. Pieces 0-19 are the 320-byte global unit verbatim (with the split block sums at kActSplitH
 // for q8_K). The loads are dealt to the waves (load i to wave i % kWaves); a wave's global offsets are the same for
 // every unit but for + u kActBytes, so they are worked out once (plan). Piece 20 (padding) and positions without a
 // row load the first unit instead: the bytes land where no operand is read (padding, or MFMA columns never stored),
@@ -998,7 +998,9 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
           if constexpr (Raw::kMin) {
             int bs[8];
 #pragma unroll
-            for (uint32_t j = 0; j < 8; j++) bs[j] = *(const int *)(unit + kActSums + 4 * j);
+            for (uint32_t j = 0; j < 8; j++)  // lo_j + 64 hi_j from the f16 split (exact integers)
+              bs[j] = (int)h2f(*(const uint16_t *)(unit + kActSplitH + 2 * j)) +
+                      (int)h2f(*(const uint16_t *)(unit + kActSplitH + 16 + 2 * j));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
               int imin = 0;
@@ -1063,7 +1065,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
     } else {
       Q4kA a;
       pin(raw);  // the decode starts after the previous unit's barrier ...
-      a.decode(raw, lane_id());
+      a.decode<true>(raw, lane_id());
       pin(a);  // ... and ends before the next unit's loads into the raw registers
       if (u + 1 < U) load_w(raw, u + 1);
 #pragma unroll
@@ -1072,7 +1074,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
           ActBP b;
           b.load(buf + (16 * pt + lane_id() % 16) * kActLds, lane_id());
           float t[4];
-          q4k_terms_v(a, b.q, b.bh, b.bl, b.ad, t);
+          q4k_terms_p(a, b, t);
 #pragma unroll
           for (int i = 0; i < 4; i++) acc[pt][i] = __fadd_rn(acc[pt][i], t[i]);
         }
@@ -1191,7 +1193,7 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3
       const auto pass = [&](Q4kRaw &raw, uint32_t m, float (&acc)[kPt][4]) {
         Q4kA a;
         pin(raw);  // the decode starts after the previous barrier ...
-        a.decode(raw, lane);
+        a.decode<true>(raw, lane);
         pin(a);  // ... and ends before the next unit's loads into the raw registers
         if constexpr (next) load_w(raw, m, u + 1);
 #pragma unroll
@@ -1200,7 +1202,7 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3
             ActBP b;
             b.load(buf + (16 * pt + lane % 16) * kActLds, lane);
             float t[4];
-            q4k_terms_v(a, b.q, b.bh, b.bl, b.ad, t);
+            q4k_terms_p(a, b, t);
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[pt][i] = __fadd_rn(acc[pt][i], t[i]);
           }
