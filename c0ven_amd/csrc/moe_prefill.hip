@@ -282,32 +282,47 @@ __global__ void __launch_bounds__(kPfWG) pf_xprep(const float *x, uint32_t T, ui
   double ss = 0.0;
   int lsb = 1 << 20;
   double gpart = 0.0;  // the shared gate's row against bf16(x): exact products, fp64 partials a lane
-  for (uint32_t k = 8 * lane; k < H; k += 512) {
-    const float4 *p = (const float4 *)(x + (uint64_t)t * H + k);
-    const float4 a = p[0], b = p[1];
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint32_t o[4];
+  // x's loads four chunks at a time, all issued before the first is used (one wave a token leaves few waves a CU, so
+  // each dependent round trip would cost the whole latency).
+  constexpr uint32_t kBatch = 4;
+  for (uint32_t k0 = 8 * lane; k0 < H; k0 += 512 * kBatch) {
+    float4 xa[kBatch], xb4[kBatch];
+    uint4 wa[kBatch];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float r0, r1;
-      round_bf16_2(v[2 * i], v[2 * i + 1], r0, r1);
-      ss = __builtin_fma((double)r0, (double)r0, ss);
-      ss = __builtin_fma((double)r1, (double)r1, ss);
-      o[i] = (__float_as_uint(r0) >> 16) | (__float_as_uint(r1) & 0xffff0000u);
-      lsb = min(lsb, min(bf16_lsb(o[i] & 0xffffu), bf16_lsb(o[i] >> 16)));
+    for (uint32_t j = 0; j < kBatch; j++) {
+      const uint32_t k = k0 + 512 * j < H ? k0 + 512 * j : k0;
+      const float4 *p = (const float4 *)(x + (uint64_t)t * H + k);
+      xa[j] = p[0], xb4[j] = p[1];
+      if (gs) wa[j] = *(const uint4 *)(wg + k);
     }
-    if (gs) {
-      const uint4 a = *(const uint4 *)(wg + k);
-      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (uint32_t j = 0; j < kBatch; j++) {
+      const uint32_t k = k0 + 512 * j;
+      if (k >= H) break;
+      const float4 a = xa[j], b = xb4[j];
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      uint32_t o[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        gpart = __builtin_fma((double)__uint_as_float(aw[i] << 16), (double)__uint_as_float(o[i] << 16), gpart);
-        gpart = __builtin_fma((double)__uint_as_float(aw[i] & 0xffff0000u),
-                              (double)__uint_as_float(o[i] & 0xffff0000u), gpart);
+        float r0, r1;
+        round_bf16_2(v[2 * i], v[2 * i + 1], r0, r1);
+        ss = __builtin_fma((double)r0, (double)r0, ss);
+        ss = __builtin_fma((double)r1, (double)r1, ss);
+        o[i] = (__float_as_uint(r0) >> 16) | (__float_as_uint(r1) & 0xffff0000u);
+        lsb = min(lsb, min(bf16_lsb(o[i] & 0xffffu), bf16_lsb(o[i] >> 16)));
       }
+      if (gs) {
+        const uint32_t aw[4] = {wa[j].x, wa[j].y, wa[j].z, wa[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          gpart = __builtin_fma((double)__uint_as_float(aw[i] << 16), (double)__uint_as_float(o[i] << 16), gpart);
+          gpart = __builtin_fma((double)__uint_as_float(aw[i] & 0xffff0000u),
+                                (double)__uint_as_float(o[i] & 0xffff0000u), gpart);
+        }
+      }
+      *(uint4 *)(xb + (uint64_t)t * H + k) = make_uint4(o[0], o[1], o[2], o[3]);
+      *(uint4 *)(xt + tile16x32(t, k, H)) = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    *(uint4 *)(xb + (uint64_t)t * H + k) = make_uint4(o[0], o[1], o[2], o[3]);
-    *(uint4 *)(xt + tile16x32(t, k, H)) = make_uint4(o[0], o[1], o[2], o[3]);
   }
   const double tot = wave_sum_f64(ss);
   lsb = -(int)wave_max_u32((uint32_t)(-lsb + (1 << 21))) + (1 << 21);
@@ -325,74 +340,82 @@ __global__ void __launch_bounds__(kPfWG) pf_xprep(const float *x, uint32_t T, ui
 typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 
-// Approximate logits of rows < E: a 32-row x 32-token tile a work-group (1-D grid, XCD-aware: a token block's row
-// blocks run on one XCD, so its bf16 x is fetched into that XCD's L2 once), wave w summing K range [w H / 4,
+// Approximate logits of rows < E: a 16 kS-row x 16 kS-token tile a work-group (1-D grid, XCD-aware: a token block's
+// row blocks run on one XCD, so its bf16 x is fetched into that XCD's L2 once), wave w summing K range [w H / 4,
 // (w + 1) H / 4). Operands straight from memory (the router's bf16 rows and the prepared bf16 x), kPre steps ahead.
+// kS = 2: 64 x 64 tiles (kS = 4, one work-group a CU, half the bytes into each CU) measured 30 against 26 us.
 constexpr uint32_t kRtPre = 4;  // steps of loads in flight; a wave's K steps (H / 128) are a multiple of it
+template <uint32_t kS>
 __global__ void __launch_bounds__(kPfWG) pf_router_bf16(const uint16_t *Wt, const uint16_t *xt, uint32_t T, uint32_t E,
                                                         uint32_t H, const float *bias, float *logits) {
-  __shared__ v4f_t part[3][4][64];
-  const uint32_t nrb = (E + 31) / 32, ntb = (T + 31) / 32, n = nrb * ntb;
+  constexpr uint32_t kTile = 16 * kS;
+  __shared__ v4f_t part[3][kS * kS][64];
+  const uint32_t nrb = (E + kTile - 1) / kTile, ntb = (T + kTile - 1) / kTile, n = nrb * ntb;
   if (blockIdx.x >= n) return;
-  const uint32_t L = xcd_logical(blockIdx.x, n), e0 = 32 * (L % nrb), t0 = 32 * (L / nrb);
+  const uint32_t L = xcd_logical(blockIdx.x, n), e0 = kTile * (L % nrb), t0 = kTile * (L / nrb);
   const uint32_t l = lane_id(), w = wave_id(), g = l / 16, c16 = l % 16;
   const uint32_t kq = H / 4, k0 = w * kq, ns = kq / 32;
   // Tiles past E rows or T tokens (the last 16-row tile's rows past them are whatever the buffers hold) read tile 0;
   // their results are never stored. A step advances one tile: 512 elements.
-  const uint32_t ra = e0 < E ? e0 : 0u, rb = e0 + 16 < E ? e0 + 16 : 0u;
-  const uint32_t ta = t0 < T ? t0 : 0u, tb = t0 + 16 < T ? t0 + 16 : 0u;
   const uint32_t lo = c16 * 32 + 8 * g;  // the lane's 8 values in a tile
-  const uint16_t *pa = Wt + tile16x32(ra, k0, H) + lo, *pb = Wt + tile16x32(rb, k0, H) + lo;
-  const uint16_t *qa = xt + tile16x32(ta, k0, H) + lo, *qb = xt + tile16x32(tb, k0, H) + lo;
-  v4f_t acc[2][2];
+  const uint16_t *pr[kS], *pt[kS];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (uint32_t i = 0; i < kS; i++) {
+    const uint32_t r = e0 + 16 * i < E ? e0 + 16 * i : 0u, t = t0 + 16 * i < T ? t0 + 16 * i : 0u;
+    pr[i] = Wt + tile16x32(r, k0, H) + lo, pt[i] = xt + tile16x32(t, k0, H) + lo;
+  }
+  v4f_t acc[kS][kS];
 #pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
-  v8bf_t op[kRtPre][4];
+  for (uint32_t i = 0; i < kS; i++)
+#pragma unroll
+    for (uint32_t j = 0; j < kS; j++) acc[i][j] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+  v8bf_t op[kRtPre][2 * kS];  // rows 0 .. kS - 1, then tokens
 #pragma unroll
   for (uint32_t d = 0; d < kRtPre; d++) {
     const uint32_t k = 512 * min(d, ns - 1);
-    op[d][0] = *(const v8bf_t *)(pa + k), op[d][1] = *(const v8bf_t *)(pb + k);
-    op[d][2] = *(const v8bf_t *)(qa + k), op[d][3] = *(const v8bf_t *)(qb + k);
+#pragma unroll
+    for (uint32_t i = 0; i < kS; i++) op[d][i] = *(const v8bf_t *)(pr[i] + k), op[d][kS + i] = *(const v8bf_t *)(pt[i] + k);
   }
   // No branch inside the unrolled steps: the compiler's waits then count the loads in flight (a branch made it wait for
-  // all of them, the prefetch lost).
+  // all of them, the prefetch lost). Each product tile's chain starts from zero and is added to the fp32 total.
   for (uint32_t s0 = 0; s0 < ns; s0 += kRtPre) {
 #pragma unroll
     for (uint32_t d = 0; d < kRtPre; d++) {
-      const v4f_t z = {0.0f, 0.0f, 0.0f, 0.0f};
-      const v4f_t d00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][0], op[d][2], z, 0, 0, 0);
-      const v4f_t d01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][0], op[d][3], z, 0, 0, 0);
-      const v4f_t d10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][1], op[d][2], z, 0, 0, 0);
-      const v4f_t d11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][1], op[d][3], z, 0, 0, 0);
-      const uint32_t kn = 512 * min(s0 + d + kRtPre, ns - 1);  // the load kPre steps ahead (the last again past the end)
-      op[d][0] = *(const v8bf_t *)(pa + kn), op[d][1] = *(const v8bf_t *)(pb + kn);
-      op[d][2] = *(const v8bf_t *)(qa + kn), op[d][3] = *(const v8bf_t *)(qb + kn);
+      v4f_t dv[kS][kS];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        acc[0][0][q] = __fadd_rn(acc[0][0][q], d00[q]), acc[0][1][q] = __fadd_rn(acc[0][1][q], d01[q]);
-        acc[1][0][q] = __fadd_rn(acc[1][0][q], d10[q]), acc[1][1][q] = __fadd_rn(acc[1][1][q], d11[q]);
-      }
+      for (uint32_t i = 0; i < kS; i++)
+#pragma unroll
+        for (uint32_t j = 0; j < kS; j++)
+          dv[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op[d][i], op[d][kS + j], v4f_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      const uint32_t kn = 512 * min(s0 + d + kRtPre, ns - 1);  // the load kPre steps ahead (the last again past the end)
+#pragma unroll
+      for (uint32_t i = 0; i < kS; i++)
+        op[d][i] = *(const v8bf_t *)(pr[i] + kn), op[d][kS + i] = *(const v8bf_t *)(pt[i] + kn);
+#pragma unroll
+      for (uint32_t i = 0; i < kS; i++)
+#pragma unroll
+        for (uint32_t j = 0; j < kS; j++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) acc[i][j][q] = __fadd_rn(acc[i][j][q], dv[i][j][q]);
     }
   }
   if (w > 0) {
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (uint32_t i = 0; i < kS; i++)
 #pragma unroll
-      for (int j = 0; j < 2; j++) part[w - 1][2 * i + j][l] = acc[i][j];
+      for (uint32_t j = 0; j < kS; j++) part[w - 1][kS * i + j][l] = acc[i][j];
   }
   __syncthreads();
   if (w != 0) return;
   // acc[i][j][q]: row e0 + 16 i + 4 g + q, token t0 + 16 j + c16.
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (uint32_t i = 0; i < kS; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (uint32_t j = 0; j < kS; j++) {
       v4f_t s = acc[i][j];
 #pragma unroll
       for (int v = 0; v < 3; v++) {
-        const v4f_t o = part[v][2 * i + j][l];
+        const v4f_t o = part[v][kS * i + j][l];
 #pragma unroll
         for (int q = 0; q < 4; q++) s[q] = __fadd_rn(s[q], o[q]);
       }
@@ -1366,7 +1389,7 @@ constexpr bool gu_fused(uint32_t type) { return type == QT_Q4_K || type == QT_IQ
 // + gs[t] y_sh[t][r]; four rows a thread. The ranks go in batches of eight whose row loads are all issued before the
 // first is added (rows of skipped ranks are not loaded and add nothing).
 
-constexpr uint32_t kCombBatch = 8;
+constexpr uint32_t kCombBatch = 8;  // 12 and 16 (one batch for K = 10) measured 44 and 51 against 38 us
 
 __global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const uint32_t *inv, const int32_t *ids,
                                                     const float *w, uint32_t K, const float *y_sh, const float *gs,
@@ -1607,8 +1630,9 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
     }
     {
       HookScope k(hook, "pf_router", st);
-      const uint32_t n = ((E + 31) / 32) * ((T + 31) / 32);
-      pf_router_bf16<<<n, kPfWG, 0, st>>>(L.router_t, b.xt, T, E, H, L.bias, b.logits);
+      constexpr uint32_t kS = 2, kTile = 16 * kS;
+      const uint32_t n = ((E + kTile - 1) / kTile) * ((T + kTile - 1) / kTile);
+      pf_router_bf16<kS><<<n, kPfWG, 0, st>>>(L.router_t, b.xt, T, E, H, L.bias, b.logits);
     }
     {
       HookScope k(hook, "pf_topk", st);
