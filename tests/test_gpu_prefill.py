@@ -88,6 +88,27 @@ def test_prefill_unit_counts(H, F, types):
     blk.close()
 
 
+@pytest.mark.parametrize("exact", ROUTERS)
+def test_prefill_extreme_block_sums(exact):
+    """Tokens whose q8_K codes are all +-127 (constant rows of either sign, and rows whose 32-value blocks alternate
+    in sign) give block sums of +-4064, the ends of the split 64 hi + lo the Q4_K minimum term's f16 operand holds
+    (hi -64 and 63); with random rows between them. Q4_K everywhere, so every GEMM takes that path."""
+    say("prefill extreme block sums, exact router", exact)
+    H = 1024
+    L = h.Layer(H, 256, 64, 6, Q4, Q4, Q4, Q4, seed=404)
+    blk = L.block(max_tokens=128, exact_router=exact)
+    L.upload(blk)
+    x = h.tokens(41, 96, H).copy()
+    sign = np.where((np.arange(H) // 32) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    for t in range(0, 96, 4):
+        x[t] = 0.75 + 0.01 * t
+        x[t + 1] = -(0.5 + 0.01 * t)
+        x[t + 2] = sign * (0.25 + 0.01 * t)
+    y, ids, w = blk.forward(0, x)
+    check_exact(y, ids, w, *L.oracle_forward(x), exact)
+    blk.close()
+
+
 def test_prefill_then_decode_share_a_context():
     """Both paths on one context, alternating: each call's result stands alone."""
     say("prefill and decode alternate")
