@@ -832,6 +832,7 @@ MOE_API moe_status moe_forward_async(moe_ctx *c, uint32_t layer, const float *x_
                                      int32_t *ids_dev, float *w_dev, void *stream) {
   return guarded(c, [&] {
     require(x_dev && y_dev, "null x or y");
+    require((((uintptr_t)x_dev | (uintptr_t)y_dev) & 15u) == 0, "x and y must be 16-byte aligned");
     forward_dev(c, layer, x_dev, ntok, y_dev, ids_dev, w_dev, stream ? (hipStream_t)stream : c->stream);
   });
 }
@@ -883,6 +884,7 @@ MOE_API moe_status moe_forward_hc_async(moe_ctx *c, uint32_t layer, float *R_dev
   return guarded(c, [&] {
     const moe_config &g = c->cfg;
     require(R_dev != nullptr, "null R");
+    require((((uintptr_t)R_dev | (uintptr_t)y_dev) & 15u) == 0, "R and y must be 16-byte aligned");
     require(layer < g.n_layer && c->layers[layer].router != nullptr, "layer out of range or its router not loaded");
     require(c->layers[layer].has_hc, "the layer's hyper-connection module is not loaded (moe_load_hc)");
     require(ntok >= 1 && ntok <= c->tmax, "moe_forward_hc_async takes 1..max_tokens tokens");
@@ -1220,6 +1222,7 @@ MOE_API moe_status moe_forward_async_noalloc(moe_ctx *c, uint32_t layer, const f
                                              float *y_dev, int32_t *ids_dev, float *w_dev, void *stream) {
   return guarded(c, [&] {
     require(x_dev && y_dev, "null x or y");
+    require((((uintptr_t)x_dev | (uintptr_t)y_dev) & 15u) == 0, "x and y must be 16-byte aligned");
     require(layer < c->cfg.n_layer, "layer out of range");
     require(ntok >= 1 && ntok <= c->tdec, "moe_forward_async_noalloc takes 1..min(max_tokens, 16) tokens (the decode kernel)");
     require(c->layers[layer].router != nullptr, "the layer's router is not loaded");

@@ -326,39 +326,53 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_down_epi(const float *raw, uint32
   if (threadIdx.x == 0) ln[t] = sqrt(sq) * (1.0 + 0x1p-30), llsb[t] = lsb;
 }
 
-// x[t][i] = (sum over s in order of n_s[i] sigma(a_s[i])) / 4, a thread a value.
+// x[t][i] = (sum over s in order of n_s[i] sigma(a_s[i])) / 4, a thread two consecutive values (H is a multiple of
+// 512, so a work-group's 512 values are one token's); every load issued before the first is used.
 __global__ void __launch_bounds__(kHcWG) pf_hc_mix(const float *n, const float *a, uint32_t T, uint32_t H, float *x) {
   __shared__ uint64_t tab[32];
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
-  const uint64_t e = (uint64_t)blockIdx.x * kHcWG + threadIdx.x;
+  const uint64_t e = ((uint64_t)blockIdx.x * kHcWG + threadIdx.x) * 2;
   if (e >= (uint64_t)T * H) return;
   const uint32_t t = (uint32_t)(e / H), i = (uint32_t)(e % H);
-  float acc = 0.0f;
+  float2 nv[kHcStreams4], av[kHcStreams4];
 #pragma unroll
   for (uint32_t s = 0; s < kHcStreams4; s++) {
-    const float nv = n[((uint64_t)t * kHcStreams4 + s) * H + i];
-    const float av = a[(uint64_t)t * kHcStreams4 * H + (uint64_t)s * H + i];
-    acc = __fadd_rn(acc, __fmul_rn(nv, sigmoid_libm(av, tab)));
+    const uint64_t o = ((uint64_t)t * kHcStreams4 + s) * H + i;
+    nv[s] = *(const float2 *)(n + o), av[s] = *(const float2 *)(a + o);
   }
-  x[e] = __fmul_rn(acc, 0.25f);
+  float2 acc = make_float2(0.0f, 0.0f);
+#pragma unroll
+  for (uint32_t s = 0; s < kHcStreams4; s++) {
+    acc.x = __fadd_rn(acc.x, __fmul_rn(nv[s].x, sigmoid_libm(av[s].x, tab)));
+    acc.y = __fadd_rn(acc.y, __fmul_rn(nv[s].y, sigmoid_libm(av[s].y, tab)));
+  }
+  *(float2 *)(x + e) = make_float2(__fmul_rn(acc.x, 0.25f), __fmul_rn(acc.y, 0.25f));
 }
 
-// R_s[i] += 2 sigma(inject_s / 4) y[i], a thread a (token, value).
+// R_s[i] += 2 sigma(inject_s / 4) y[i], a thread two consecutive values of a token (a work-group's 512 values are one
+// token's: H is a multiple of 512), the four stream weights worked out once a work-group.
 __global__ void __launch_bounds__(kHcWG) pf_hc_post(float *R, const float *y, const float *inj, uint32_t T,
                                                     uint32_t H) {
   __shared__ uint64_t tab[32];
+  __shared__ float ws[kHcStreams4];
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
-  const uint64_t e = (uint64_t)blockIdx.x * kHcWG + threadIdx.x;
-  if (e >= (uint64_t)T * H) return;
-  const uint32_t t = (uint32_t)(e / H), i = (uint32_t)(e % H);
-  const float yv = y[e];
+  const uint64_t e0 = (uint64_t)blockIdx.x * kHcWG * 2, e = e0 + 2 * threadIdx.x;
+  if (e0 >= (uint64_t)T * H) return;
+  const uint32_t t = (uint32_t)(e0 / H), i = (uint32_t)(e % H);
+  if (threadIdx.x < kHcStreams4)
+    ws[threadIdx.x] = __fmul_rn(2.0f, sigmoid_libm(__fmul_rn(inj[(uint64_t)t * kHcStreams4 + threadIdx.x], 0.25f), tab));
+  const float2 yv = *(const float2 *)(y + e);
+  float2 rv[kHcStreams4];
+#pragma unroll
+  for (uint32_t s = 0; s < kHcStreams4; s++) rv[s] = *(const float2 *)(R + ((uint64_t)t * kHcStreams4 + s) * H + i);
+  __syncthreads();
 #pragma unroll
   for (uint32_t s = 0; s < kHcStreams4; s++) {
-    const float w = __fmul_rn(2.0f, sigmoid_libm(__fmul_rn(inj[(uint64_t)t * kHcStreams4 + s], 0.25f), tab));
-    float *r = R + ((uint64_t)t * kHcStreams4 + s) * H + i;
-    *r = __fadd_rn(*r, __fmul_rn(w, yv));
+    const float w = ws[s];
+    *(float2 *)(R + ((uint64_t)t * kHcStreams4 + s) * H + i) =
+        make_float2(__fadd_rn(rv[s].x, __fmul_rn(w, yv.x)), __fadd_rn(rv[s].y, __fmul_rn(w, yv.y)));
   }
 }
 
@@ -387,13 +401,13 @@ hipError_t prefill_hc_pre(const HcShape &S, const HcLayer &L, const HcBufs &b, c
                                          L.row_lsb + Md, b.llsb, nu * 0x1p-53, b.open_up, b.cnt + 1);
   pf_hc_up_fix<<<256, kHcWG, 0, st>>>(L.w_up, lr, D, b.lb, b.open_up, b.cnt + 1, b.a);
   const uint64_t nx = (uint64_t)T * H;
-  pf_hc_mix<<<(uint32_t)((nx + kHcWG - 1) / kHcWG), kHcWG, 0, st>>>(b.n, b.a, T, H, b.x);
+  pf_hc_mix<<<(uint32_t)((nx + 2 * kHcWG - 1) / (2 * kHcWG)), kHcWG, 0, st>>>(b.n, b.a, T, H, b.x);
   return hipGetLastError();
 }
 
 hipError_t prefill_hc_post(const HcShape &S, const HcBufs &b, float *R, const float *y, hipStream_t st) {
   const uint64_t nx = (uint64_t)S.T * S.H;
-  pf_hc_post<<<(uint32_t)((nx + kHcWG - 1) / kHcWG), kHcWG, 0, st>>>(R, y, b.inj, S.T, S.H);
+  pf_hc_post<<<(uint32_t)((nx + 2 * kHcWG - 1) / (2 * kHcWG)), kHcWG, 0, st>>>(R, y, b.inj, S.T, S.H);
   return hipGetLastError();
 }
 

@@ -118,7 +118,8 @@ MOE_API moe_status moe_load_expert(moe_ctx *ctx, uint32_t layer, uint32_t expert
  * combine), up to max_tokens. */
 MOE_API moe_status moe_forward(moe_ctx *ctx, uint32_t layer, const float *x, uint32_t ntok, uint64_t x_stride,
                                float *y, uint64_t y_stride, moe_route_out *route);
-/* The same on device memory (x and y ntok x n_embd fp32, contiguous; ids and w ntok x n_used or null), enqueued on
+/* The same on device memory (x and y ntok x n_embd fp32, contiguous, 16-byte aligned; ids and w ntok x n_used or
+ * null), enqueued on
  * stream (a hipStream_t; null: the context's stream). Nothing is copied and nothing waits. A context's forwards share
  * its scratch (work counters, hand-off records, intermediate buffers), so they must be ordered: enqueue them on one
  * stream, or make each stream wait for the previous forward's (an event) before enqueueing the next. moe_check
@@ -186,10 +187,12 @@ MOE_API moe_status moe_prefill_exact_tokens(moe_ctx *ctx, uint32_t *n);
 MOE_API moe_status moe_load_hc(moe_ctx *ctx, uint32_t layer, const float *gamma, const uint16_t *w_down,
                                const uint16_t *w_inject, const uint16_t *w_up);
 /* The block with its hyper-connection mix and combine fused into the decode launch (model.cpp:1350-1416: hc_mix, the
- * block, hc_combine): R_dev (device, ntok x 4 x n_embd fp32, the residual streams) gives the block's input
- * x = (1/4) sum_s n_s sigma(a_s) and receives R_s += 2 sigma(inject_s / 4) y. y_dev (ntok x n_embd, may be null),
- * ids_dev and w_dev (may be null) receive y and the routing. 1 <= ntok <= min(max_tokens, 16). No counterpart entry
- * point in the reference, whose kernel list runs the same steps as separate launches. */
+ * block, hc_combine): R_dev (device, ntok x 4 x n_embd fp32, the residual streams, 16-byte aligned) gives the
+ * block's input x = (1/4) sum_s n_s sigma(a_s) and receives R_s += 2 sigma(inject_s / 4) y. y_dev (ntok x n_embd,
+ * 16-byte aligned, may be null), ids_dev and w_dev (may be null) receive y and the routing. 1 <= ntok <= max_tokens:
+ * up to 16 tokens the mix and combine are items of the decode launch, above that kernels around the prefill block
+ * (prompt.cpp:478-504). No counterpart entry point in the reference, whose kernel list runs the same steps as
+ * separate launches. */
 MOE_API moe_status moe_forward_hc_async(moe_ctx *ctx, uint32_t layer, float *R_dev, uint32_t ntok, float *y_dev,
                                         int32_t *ids_dev, float *w_dev, void *stream);
 /* The same with R (ntok x 4 x n_embd) and y (ntok x n_embd, may be null) in host memory; synchronous. */

@@ -191,6 +191,19 @@ def test_bad_arguments_do_not_crash(tiny_block):
     assert e.value.status == 2
     with pytest.raises(moe.MoeError):
         moe.MoeBlock(500, 256, 8, 2, moe.QT_Q8_0, moe.QT_Q8_0)
+    # Device buffers must be 16-byte aligned (the kernels read and write them in 8- and 16-byte pieces): refused
+    # before anything is enqueued.
+    import ctypes
+    import bench
+    hip = bench.Hip()
+    buf = hip.malloc(2 * 512 * 4 + 64)
+    base = buf.value
+    for xo, yo in ((4, 0), (0, 8)):
+        with pytest.raises(moe.MoeError) as e:
+            tiny_block.forward_async(0, ctypes.c_void_p(base + xo), 1, ctypes.c_void_p(base + 2048 + 16 + yo))
+        assert e.value.status == 2
+    hip.sync()
+    hip.rt.hipFree(buf)
 
 
 def _cm_jobs(L, T, K, rng_seed, parts=False):
