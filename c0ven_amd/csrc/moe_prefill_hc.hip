@@ -128,6 +128,10 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_gemm(const uint16_t *A0, uint32_t
   const uint32_t nmt = (M + 63) / 64, mt = blockIdx.x % nmt, nt = blockIdx.x / nmt, split = blockIdx.y;
   const uint32_t lane = lane_of(), w = threadIdx.x >> 6, g = lane / 16, c16 = lane % 16;
   const uint32_t m0 = 64 * mt + 32 * (w & 1), n0 = 64 * nt + 32 * (w >> 1);
+  // 16 x 16 tiles wholly past the rows or the tokens (the down GEMM's last row tile holds 4 of W_inject's rows) are
+  // skipped: a wave with none returns (the kernel has no barrier), the others skip the MFMAs of theirs.
+  if (m0 >= M || n0 >= N) return;
+  const bool live_i1 = m0 + 16 < M, live_j1 = n0 + 16 < N;
   const uint16_t *ar[2];
   const uint16_t *br[2];
 #pragma unroll
@@ -170,7 +174,9 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_gemm(const uint16_t *A0, uint32_t
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-          for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad[i][m], bd[j][m], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < 2; j++)
+          if ((i == 0 || live_i1) && (j == 0 || live_j1))
+            acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad[i][m], bd[j][m], acc[i][j], 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 2; i++)
