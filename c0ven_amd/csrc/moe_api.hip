@@ -628,7 +628,7 @@ MOE_API moe_status moe_open(const moe_config *cfg, moe_ctx **out) {
       if (TM > T) {
         const uint64_t Md = g.hc_lr + kHcStreams, D = (uint64_t)kHcStreams * H;
         HcBufs &b = c->hcp;
-        b.n = c->alloc<float>(TM * D);
+        b.sc = c->alloc<float>(TM * kHcStreams);
         b.nn = c->alloc<double>(TM);
         b.nlsb = c->alloc<int>(TM);
         b.llsb = c->alloc<int>(TM);

@@ -63,9 +63,10 @@ __device__ __forceinline__ int wg_min(int v, int *red) {
 }
 
 // Token t (one work-group): each stream as RMSNorm(R_s) gamma_s, the decode kernel's hc_norm_item arithmetic (each
-// thread's squares in order, then wg_sum; mean rounded to fp32; 1 / sqrtf(mean + 1e-6)), into n and as bf16 bits into
-// nb, and the 2-norm (rounded up) and least lsb exponent of bf16(n). Work-group 0 clears the open lists' counts.
-__global__ void __launch_bounds__(kHcWG) pf_hc_norm(const float *R, const float *gamma, uint32_t H, float *n,
+// thread's squares in order, then wg_sum; mean rounded to fp32; 1 / sqrtf(mean + 1e-6)): the stream's scale into sc
+// (pf_hc_mix forms n again from R, the scale and gamma), bf16(n) into nb, and the 2-norm (rounded up) and least lsb
+// exponent of bf16(n). Work-group 0 clears the open lists' counts.
+__global__ void __launch_bounds__(kHcWG) pf_hc_norm(const float *R, const float *gamma, uint32_t H, float *sc,
                                                     uint16_t *nb, double *nn, int *nlsb, uint32_t *cnt) {
   __shared__ double red[4];
   __shared__ int redi[4];
@@ -80,11 +81,10 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_norm(const float *R, const float 
     ss = wg_sum(ss, red);
     const float mean = (float)(ss / (double)H);
     const float scale = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, 1e-6f)));
-    float *o = n + ((uint64_t)t * kHcStreams4 + s) * H;
+    if (threadIdx.x == 0) sc[t * kHcStreams4 + s] = scale;
     uint16_t *ob = nb + ((uint64_t)t * kHcStreams4 + s) * H;
     for (uint32_t i = threadIdx.x; i < H; i += kHcWG) {
       const float v = __fmul_rn(__fmul_rn(r[i], scale), gamma[s * H + i]);
-      o[i] = v;
       const float bv = round_bf16(v);
       ob[i] = (uint16_t)(__float_as_uint(bv) >> 16);
       const double b = (double)bv;
@@ -332,24 +332,30 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_down_epi(const float *raw, uint32
   if (threadIdx.x == 0) ln[t] = sqrt(sq) * (1.0 + 0x1p-30), llsb[t] = lsb;
 }
 
-// x[t][i] = (sum over s in order of n_s[i] sigma(a_s[i])) / 4, a thread two consecutive values (H is a multiple of
-// 512, so a work-group's 512 values are one token's); every load issued before the first is used.
-__global__ void __launch_bounds__(kHcWG) pf_hc_mix(const float *n, const float *a, uint32_t T, uint32_t H, float *x) {
+// x[t][i] = (sum over s in order of n_s[i] sigma(a_s[i])) / 4 with n_s[i] = (R_s[i] sc_s) gamma_s[i] (pf_hc_norm's
+// product), a thread two consecutive values (H is a multiple of 512, so a work-group's 512 values are one token's);
+// every load issued before the first is used.
+__global__ void __launch_bounds__(kHcWG) pf_hc_mix(const float *R, const float *gamma, const float *sc, const float *a,
+                                                   uint32_t T, uint32_t H, float *x) {
   __shared__ uint64_t tab[32];
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
   const uint64_t e = ((uint64_t)blockIdx.x * kHcWG + threadIdx.x) * 2;
   if (e >= (uint64_t)T * H) return;
   const uint32_t t = (uint32_t)(e / H), i = (uint32_t)(e % H);
-  float2 nv[kHcStreams4], av[kHcStreams4];
+  float2 nv[kHcStreams4], av[kHcStreams4], gv[kHcStreams4];
+  float scale[kHcStreams4];
 #pragma unroll
   for (uint32_t s = 0; s < kHcStreams4; s++) {
     const uint64_t o = ((uint64_t)t * kHcStreams4 + s) * H + i;
-    nv[s] = *(const float2 *)(n + o), av[s] = *(const float2 *)(a + o);
+    nv[s] = *(const float2 *)(R + o), av[s] = *(const float2 *)(a + o), gv[s] = *(const float2 *)(gamma + s * H + i);
+    scale[s] = sc[t * kHcStreams4 + s];
   }
   float2 acc = make_float2(0.0f, 0.0f);
 #pragma unroll
   for (uint32_t s = 0; s < kHcStreams4; s++) {
+    nv[s].x = __fmul_rn(__fmul_rn(nv[s].x, scale[s]), gv[s].x);
+    nv[s].y = __fmul_rn(__fmul_rn(nv[s].y, scale[s]), gv[s].y);
     acc.x = __fadd_rn(acc.x, __fmul_rn(nv[s].x, sigmoid_libm(av[s].x, tab)));
     acc.y = __fadd_rn(acc.y, __fmul_rn(nv[s].y, sigmoid_libm(av[s].y, tab)));
   }
@@ -387,7 +393,7 @@ __global__ void __launch_bounds__(kHcWG) pf_hc_post(float *R, const float *y, co
 hipError_t prefill_hc_pre(const HcShape &S, const HcLayer &L, const HcBufs &b, const float *R, bool force_open,
                           hipStream_t st) {
   const uint32_t H = S.H, lr = S.lr, T = S.T, D = kHcStreams4 * H, Md = lr + kHcStreams4;
-  pf_hc_norm<<<T, kHcWG, 0, st>>>(R, L.gamma, H, b.n, b.nb, b.nn, b.nlsb, b.cnt);
+  pf_hc_norm<<<T, kHcWG, 0, st>>>(R, L.gamma, H, b.sc, b.nb, b.nn, b.nlsb, b.cnt);
   // The down GEMM: K = 4H in kHcDownSplit parts. Roundings on a sum's path: here at most 4 per matrix-core step over a
   // kGroupK chain, one per group total, one per split; in the fixed order 8 (chain) + 1 + 3 (tree) + K / 2048 (the
   // slot's chunks) + 16 (the slots); doubled, and 2^-53 each.
@@ -407,7 +413,7 @@ hipError_t prefill_hc_pre(const HcShape &S, const HcLayer &L, const HcBufs &b, c
                                          L.row_lsb + Md, b.llsb, nu * 0x1p-53, b.open_up, b.cnt + 1);
   pf_hc_up_fix<<<256, kHcWG, 0, st>>>(L.w_up, lr, D, b.lb, b.open_up, b.cnt + 1, b.a);
   const uint64_t nx = (uint64_t)T * H;
-  pf_hc_mix<<<(uint32_t)((nx + 2 * kHcWG - 1) / (2 * kHcWG)), kHcWG, 0, st>>>(b.n, b.a, T, H, b.x);
+  pf_hc_mix<<<(uint32_t)((nx + 2 * kHcWG - 1) / (2 * kHcWG)), kHcWG, 0, st>>>(R, L.gamma, b.sc, b.a, T, H, b.x);
   return hipGetLastError();
 }
 

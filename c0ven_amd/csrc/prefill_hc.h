@@ -21,12 +21,12 @@ struct HcLayer {
   const int *row_lsb;
 };
 
-// Scratch for T tokens: the normed streams n (T x 4 x H) and their bf16 bits, their bf16 2-norms, the down GEMM's fp64 partials
-// (kHcDownSplit x T x (lr + 4)) and rounded sums (T x (lr + 4)), the list of sums whose rounding the bound left open
-// (pairs t, row; room for all) and the up GEMM's, their counts, bf16(l) (T x lr) and its norms, the inject logits
-// (T x 4), the up GEMM's sums a (T x 4H), and x (T x H).
+// Scratch for T tokens: the norm's scales (T x 4) and the normed streams' bf16 bits (T x 4 x H), their bf16 2-norms,
+// the down GEMM's fp64 partials (kHcDownSplit x T x (lr + 4)) and rounded sums (T x (lr + 4)), the list of sums whose
+// rounding the bound left open (pairs t, row; room for all) and the up GEMM's, their counts, bf16(l) (T x lr) and its
+// norms, the inject logits (T x 4), the up GEMM's sums a (T x 4H), and x (T x H).
 struct HcBufs {
-  float *n, *raw, *inj, *a, *x;
+  float *sc, *raw, *inj, *a, *x;
   uint16_t *nb, *lb;  // bf16(n), bf16(l): the GEMMs' operands
   double *nn, *ln, *part;
   int *nlsb, *llsb;  // the least lsb exponent of each token's bf16(n), bf16(l)
