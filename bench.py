@@ -38,7 +38,12 @@ CONFIGS = {
               types=(21, 12, 8, 8), T=1, zipf=1.1, layers=48),
     "5p": dict(name="config5: 48-layer stack, prefill 4096 tokens in 2 chunks of 2048, gate/up IQ3_S, down Q4_K, "
                     "shared Q8_0, Zipf(1.1) per layer", types=(21, 12, 8, 8), T=4096, chunk=2048, zipf=1.1, layers=48),
+    # Not a BASELINE config: config 4's block with the hyper-connection mix and combine around it (moe_forward_hc), a
+    # low rank of 256 at this n_embd (the model's 320 at 2560 scaled); its own JSON line, never the headline.
+    "hc": dict(name="config4 + hyper-connection mix and combine (hc_lr 256): prefill T=2048, Q4_K, Zipf(1.1)",
+               types=(12, 12, 12, 12), T=2048, zipf=1.1, hc_lr=256),
 }
+FP64_PEAK_TFLOPS = 78.6  # dense fp64 MFMA, MI355X
 H, F, E, K = 2048, 512, 512, 10
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
@@ -249,6 +254,8 @@ def main():
     cfg = CONFIGS[args.config]
     if "layers" in cfg:
         return stack(args, cfg, moe, h)
+    if "hc_lr" in cfg:
+        return hc(args, cfg, moe, h)
     out = (prefill if cfg["T"] > 16 else decode)(args, cfg, args.config, moe, h)
     print(json.dumps(out), flush=True)
 
@@ -349,6 +356,77 @@ def decode(args, cfg, key, moe, h):
     }
     blk.close()
     return out
+
+
+def hc(args, cfg, moe, h):
+    """The block with its hyper-connection mix and combine (moe_forward_hc_async on the residual streams R, T x 4 x H)
+    against the block alone (moe_forward_async) on the same weights: the difference is the mix's and combine's
+    kernels. Their roofline is the fp64 matrix cores' (the down GEMM, (lr + 4) x 4H against bf16(n), and the up
+    GEMM, 4H x lr against bf16(l), summed exactly in fp64 and certified): the two GEMMs' flops over the whole
+    difference, so a lower bound of their rate. Parity: R, y and the ids of a 64-token sample against the oracle's
+    mix, block and combine."""
+    gt, dt, sgt, sdt = cfg["types"]
+    T, lr = cfg["T"], cfg["hc_lr"]
+    steps = 50 if args.steps is None else args.steps
+    warmup = 5 if args.warmup is None else args.warmup
+    hip = Hip()
+    t_setup = time.time()
+    L = h.Layer(H, F, E, K, gt, dt, sgt, sdt, seed=2026, layer=0, zipf=cfg["zipf"])
+    hm = h.HcModule(H, lr, seed=3)
+    blk = moe.MoeBlock(H, F, E, K, gt, dt, True, sgt, sdt, max_tokens=T, hc_lr=lr)
+    L.upload(blk, 0)
+    hm.load(blk, 0)
+    R = moe.synth_normal(2026, 4242, T * 4 * H, 1.0).reshape(T, 4, H).astype(np.float32)
+    x = h.tokens(2026, T, H)
+    Rd, xd, yd = hip.malloc(R.nbytes), hip.malloc(x.nbytes), hip.malloc(x.nbytes)
+    hip.h2d(Rd, R)
+    hip.h2d(xd, x)
+    setup_s = time.time() - t_setup
+
+    def run(fn):
+        for _ in range(warmup):
+            fn()
+        hip.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        hip.sync()
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    blk.check()
+    hc_ms = run(lambda: blk.forward_hc_async(0, Rd, T, yd))  # R accumulates its combine step after step
+    plain_ms = run(lambda: blk.forward_async(0, xd, T, yd))
+    blk.check()
+    D = 4 * H
+    flop = 2.0 * T * (lr + 4) * D + 2.0 * T * D * lr
+    mix_ms = hc_ms - plain_ms
+    n = 64
+    Rs = R[:n]
+    Rg, yg, ig, _ = blk.forward_hc(0, Rs)
+    xo, inj = hm.pre(Rs)
+    yo, io, _ = L.oracle_forward(xo, nthreads=16)
+    Ro = hm.post(Rs, inj, yo)
+    parity = dict(sample_tokens=n, ids_equal=bool(np.array_equal(ig, io)), R_bit_exact=bool(np.array_equal(Rg, Ro)),
+                  R_max_abs=h.max_abs(Rg, Ro), R_rel_l2=h.rel_l2(Rg, Ro), y_max_abs=h.max_abs(yg, yo),
+                  y_rel_l2=h.rel_l2(yg, yo))
+    out = {
+        "metric": "MoE block with hyper-connection mix and combine, tokens/s (prefill; not a BASELINE metric)",
+        "value": round(T / (hc_ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(hc_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f64", "data": "synthetic",
+        "config": {"workload": cfg["name"], "n_embd": H, "n_ff": F, "n_expert": E, "n_used": K, "shared": True,
+                   "tokens": T, "hc_lr": lr, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]]},
+        "roofline": {"bound": "mfma", "kernel": "pf_hc_gemm (down and up) and the mix's other kernels",
+                     "achieved": round(flop / (mix_ms * 1e-3) / 1e12, 2), "peak": FP64_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flop / (mix_ms * 1e-3) / 1e12 / FP64_PEAK_TFLOPS, 4),
+                     "traffic": None, "algorithmic_flop_per_launch": flop, "avg_launch_ms": round(mix_ms, 4)},
+        "block": {"block_alone_ms": round(plain_ms, 4), "mix_and_combine_ms": round(mix_ms, 4)},
+        "parity": parity,
+        "cpu_baseline": None,
+        "setup_s": round(setup_s, 1),
+    }
+    blk.close()
+    print(json.dumps(out), flush=True)
 
 
 def stack(args, cfg, moe, h):
