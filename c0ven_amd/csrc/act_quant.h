@@ -48,6 +48,20 @@ __device__ __forceinline__ uint4 ld_co16(const void *base, uint32_t off) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16 bytes to base + off (base uniform over the wave), written through to the agent's coherence point (SC1) in one
+// request: the store counterpart of ld_co16.
+__device__ __forceinline__ void st_co16(void *base, uint32_t off, uint4 v) {
+  typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+  constexpr int kSc1 = 16;
+  constexpr uint32_t kRsrcWord3 = 0x00020000u;
+  const uint64_t b = (uint64_t)base;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint64_t bu = ((uint64_t)hi << 32) | lo;
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)bu, 0, 0xffffffffu, kRsrcWord3);
+  __builtin_amdgcn_raw_buffer_store_b128(v4u_t{v.x, v.y, v.z, v.w}, r, off, 0, kSc1);
+}
+
 // A word of a quantised unit: to global memory (coherent, for other work-groups of the launch) or to LDS (for this
 // one), or with kPlain a plain store (read by later launches only).
 template <bool kLds, typename T, bool kPlain = false>

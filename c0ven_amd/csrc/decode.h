@@ -69,22 +69,22 @@ constexpr uint32_t down_rows(uint32_t Ud) { return (kWG / 64) * (64 / Ud); }
 // the shared expert's items), [kFlagRouted] a pre-routed call's x is quantised. Data handed from one work item to the
 // next inside a launch (logits, ids, weights, the shared gate, h) travels as tagged records instead: 64-bit words
 // whose high half is the launch's tag, so the reader polls the data itself and needs no flag.
-// With the hyper-connection mix (hc_R not null): [kFlagHcNorm + t] token t's streams are normed, [kFlagHcDown] the
+// With the hyper-connection mix (hc_R not null): [kFlagHcNorm + 4 t + s] token t's stream s is normed, [kFlagHcDown] the
 // low-rank gate and the inject logits are in, [kFlagHcX] the mixed input x is in.
 constexpr uint32_t kFlagLead = 0, kFlagRouted = kMaxLeadItems, kFlagHcNorm = kMaxLeadItems + 1,
-                   kFlagHcDown = kFlagHcNorm + kMaxDecodeTokens, kFlagHcX = kFlagHcDown + 1,
+                   kFlagHcDown = kFlagHcNorm + 4 * kMaxDecodeTokens, kFlagHcX = kFlagHcDown + 1,
                    kFlagCount = kFlagHcX + 1;
 
 // The hyper-connection mix before the block and the combine after it (docs/spec/MODEL_LAYER.md 1.1, 1.2): 4 streams
 // of H values a token, a low rank of at most kHcMaxLr. Its items come first in a launch:
-//   norm items      one a token: the four streams' RMS norms (x gamma);
+//   norm items      one a token's stream: its RMS norm (x gamma);
 //   down items      one a row of W_down (lr rows) and of W_inject (4 rows), for all tokens: silu(W_down n / 4), and
 //                   the inject logits W_inject n;
 //   up items        kHcUpValues values of x, for all tokens: the 4 kHcUpValues rows of W_up they take, then the mix.
 // The lead items wait for x; the combine items add the block's output into the streams.
 constexpr uint32_t kHcStreams = 4, kHcMaxLr = 512, kHcUpValues = 16;
 constexpr uint32_t hc_items(uint32_t T, uint32_t H, uint32_t lr) {
-  return lr ? T + lr + kHcStreams + H / kHcUpValues : 0;
+  return lr ? kHcStreams * T + lr + kHcStreams + H / kHcUpValues : 0;
 }
 
 struct DecodeParams {
@@ -132,7 +132,8 @@ struct DecodeParams {
   const float *hc_gamma;     // 4 H: the streams' norm weights
   const uint16_t *hc_down;   // lr x 4 H bf16
   const uint16_t *hc_inj;    // 4 x 4 H bf16
-  const uint16_t *hc_up;     // 4 H x lr bf16 (row s H + i)
+  const uint16_t *hc_up;     // 4 H x lr bf16 (row s H + i), then its rows' 2-norms (4 H fp64, rounded up) and least
+                             // lsb exponents (4 H int)
   uint32_t hc_lr;
   float *hc_n;               // T x 4 H: the normed streams
   float *hc_l;               // T x (lr + 4): the gate silu(W_down n / 4), then the inject logits

@@ -503,26 +503,31 @@ __device__ __forceinline__ double wg_sum_f64(double v, double *red) {
   return __dadd_rn(__dadd_rn(red[0], red[1]), __dadd_rn(red[2], red[3]));
 }
 
-// Norm item t: each stream s of token t as RMSNorm(R_s) gamma_s (MODEL_LAYER.md 1.1 step 1; ggml_compute_forward_
+// Norm item (t, s): stream s of token t as RMSNorm(R_s) gamma_s (MODEL_LAYER.md 1.1 step 1; ggml_compute_forward_
 // rms_norm_f32: the squares summed in double, mean = sum / H rounded to fp32, scale = 1 / sqrtf(mean + 1e-6), then
 // (R scale) gamma), stored for the down and up items.
-__device__ __forceinline__ void hc_norm_item(const DecodeParams &p, uint32_t t, double *red) {
+__device__ __forceinline__ void hc_norm_item(const DecodeParams &p, uint32_t t, uint32_t s, double *red) {
   const uint32_t H = p.H;
-  for (uint32_t s = 0; s < kHcStreams; s++) {
-    const float *R = p.hc_R + ((uint64_t)t * kHcStreams + s) * H;
-    double ss = 0.0;
-    for (uint32_t i = tid(); i < H; i += kWG) {
-      const float v = R[i];
-      ss = __dadd_rn(ss, (double)__fmul_rn(v, v));
-    }
-    ss = wg_sum_f64(ss, red);
-    const float mean = (float)(ss / (double)H);
-    // sqrtf is the correctly rounded square root here (__fsqrt_rn is the hardware approximation in this build).
-    const float scale = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, 1e-6f)));
-    float *n = p.hc_n + ((uint64_t)t * kHcStreams + s) * H;
-    for (uint32_t i = tid(); i < H; i += kWG) st_co(n + i, __fmul_rn(__fmul_rn(R[i], scale), p.hc_gamma[s * H + i]));
+  const float *R = p.hc_R + ((uint64_t)t * kHcStreams + s) * H;
+  double ss = 0.0;
+  for (uint32_t i = tid(); i < H; i += kWG) {
+    const float v = R[i];
+    ss = __dadd_rn(ss, (double)__fmul_rn(v, v));
   }
-  set_flag(p, kFlagHcNorm + t);
+  ss = wg_sum_f64(ss, red);
+  const float mean = (float)(ss / (double)H);
+  // sqrtf is the correctly rounded square root here (__fsqrt_rn is the hardware approximation in this build).
+  const float scale = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, 1e-6f)));
+  // Four values a thread, each 16-byte piece written through to the coherence point in one request.
+  float *n = p.hc_n + (uint64_t)t * kHcStreams * H;
+  for (uint32_t i = 4 * tid(); i < H; i += 4 * kWG) {
+    const float4 r = *(const float4 *)(R + i), g = *(const float4 *)(p.hc_gamma + s * H + i);
+    const float4 v = make_float4(__fmul_rn(__fmul_rn(r.x, scale), g.x), __fmul_rn(__fmul_rn(r.y, scale), g.y),
+                                 __fmul_rn(__fmul_rn(r.z, scale), g.z), __fmul_rn(__fmul_rn(r.w, scale), g.w));
+    st_co16(n, (s * H + i) * 4, make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                                           __float_as_uint(v.w)));
+  }
+  set_flag(p, kFlagHcNorm + kHcStreams * t + s);
 }
 
 // Down item r (after every norm item): row r of W_down (r < lr) or of W_inject (r - lr) against bf16(n) of every
@@ -531,7 +536,7 @@ __device__ __forceinline__ void hc_norm_item(const DecodeParams &p, uint32_t t, 
 __device__ __forceinline__ void hc_down_item(const DecodeParams &p, uint32_t r, double *part, double *tot,
                                              const uint64_t *tab, uint32_t *s_flag) {
   const uint32_t K = kHcStreams * p.H, lr = p.hc_lr;
-  wait_flags(p, kFlagHcNorm, p.T);
+  wait_flags(p, kFlagHcNorm, kHcStreams * p.T);
   const uint16_t *W = r < lr ? p.hc_down + (uint64_t)r * K : p.hc_inj + (uint64_t)(r - lr) * K;
   bf16_dot<true>(W, p.hc_n, K, K, 0, p.T, part, tot);
   const uint32_t t = tid();
@@ -1221,12 +1226,12 @@ __global__ void __launch_bounds__(kWG) __attribute__((amdgpu_waves_per_eu(3))) m
     if (mark && tid() == 0) mark[0] = mark[1] = mark[2] = __builtin_amdgcn_s_memrealtime();
     if (kHc && it < nH) {
       const uint32_t lw = p.hc_lr + kHcStreams;
-      if (it < T)
-        hc_norm_item(p, it, s_part);
-      else if (it < T + lw)
-        hc_down_item(p, it - T, s_part, s_tot, exp_tab, &s_flag);
+      if (it < kHcStreams * T)
+        hc_norm_item(p, it / kHcStreams, it % kHcStreams, s_part);
+      else if (it < kHcStreams * T + lw)
+        hc_down_item(p, it - kHcStreams * T, s_part, s_tot, exp_tab, &s_flag);
       else
-        hc_up_item(p, it - T - lw, lds, exp_tab, &s_flag);
+        hc_up_item(p, it - kHcStreams * T - lw, lds, exp_tab, &s_flag);
     } else if (it < nH + nL) {
       const uint32_t li = it - nH;
       if (kHc) wait_flag(p, kFlagHcX);
