@@ -135,7 +135,7 @@ struct DecodeParams {
   const uint16_t *hc_up;     // 4 H x lr bf16 (row s H + i), then its rows' 2-norms (4 H fp64, rounded up) and least
                              // lsb exponents (4 H int)
   uint32_t hc_lr;
-  float *hc_n;               // T x 4 H: the normed streams
+  float *hc_n;               // the normed streams as bf16 (T x 4 H), then the norms' scales (T x 4 fp32)
   float *hc_l;               // T x (lr + 4): the gate silu(W_down n / 4), then the inject logits
   float *hc_x;               // T x H: the mixed input (x points here)
   uint32_t *cnt_hc;          // 2 counters, kDynStride words apart: down items in, up items in

@@ -411,15 +411,21 @@ __device__ __forceinline__ double row16_reduce8_f64(double v[8]) {
 // while four are used), each chunk's eight sums are reduced over the 16 lanes of a row (one value a lane pair left) and
 // added to that row of lanes' partial in LDS; the sixteen partials of an output (four rows of lanes, four waves) are
 // then added in a fixed order.
-template <bool kCo>
+template <bool kCo, bool kXb = false>
 __device__ __forceinline__ void bf16_dot(const uint16_t *W, const float *x, uint32_t K, uint32_t ldx, uint32_t t0,
                                          uint32_t nt, double *part, double *tot) {
   const uint32_t lane = lane_id(), wv = wave_id(), nC = K / 512;
   const uint32_t pslot = 4 * wv + lane / 16;
-  // Values 8 lane .. + 7 of chunk c of token t, as two float4.
+  // Values 8 lane .. + 7 of chunk c of token t, as two float4 (kXb: x holds bf16 bits, 16 bytes the eight).
   const auto ldx8 = [&](uint32_t t, uint32_t c, float4 &a, float4 &b) {
     const uint64_t e = (uint64_t)t * ldx + 512 * c + 8 * lane;
-    if constexpr (kCo) {
+    if constexpr (kXb) {
+      const uint4 u = ld_co16(x, (uint32_t)(2 * e));
+      a = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                      __uint_as_float(u.y & 0xffff0000u));
+      b = make_float4(__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u), __uint_as_float(u.w << 16),
+                      __uint_as_float(u.w & 0xffff0000u));
+    } else if constexpr (kCo) {
       const uint4 u = ld_co16(x, (uint32_t)(4 * e)), v = ld_co16(x, (uint32_t)(4 * e + 16));
       a = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
       b = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
@@ -503,6 +509,11 @@ __device__ __forceinline__ double wg_sum_f64(double v, double *red) {
   return __dadd_rn(__dadd_rn(red[0], red[1]), __dadd_rn(red[2], red[3]));
 }
 
+// The norm items' scales (T x 4 fp32), in the hc_n buffer after bf16(n) (T x 4 H bf16).
+__device__ __forceinline__ float *hc_scale(const DecodeParams &p) {
+  return (float *)((uint16_t *)p.hc_n + (uint64_t)p.T * kHcStreams * p.H);
+}
+
 // Norm item (t, s): stream s of token t as RMSNorm(R_s) gamma_s (MODEL_LAYER.md 1.1 step 1; ggml_compute_forward_
 // rms_norm_f32: the squares summed in double, mean = sum / H rounded to fp32, scale = 1 / sqrtf(mean + 1e-6), then
 // (R scale) gamma), stored for the down and up items.
@@ -518,15 +529,23 @@ __device__ __forceinline__ void hc_norm_item(const DecodeParams &p, uint32_t t, 
   const float mean = (float)(ss / (double)H);
   // sqrtf is the correctly rounded square root here (__fsqrt_rn is the hardware approximation in this build).
   const float scale = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, 1e-6f)));
-  // Four values a thread, each 16-byte piece written through to the coherence point in one request.
-  float *n = p.hc_n + (uint64_t)t * kHcStreams * H;
-  for (uint32_t i = 4 * tid(); i < H; i += 4 * kWG) {
-    const float4 r = *(const float4 *)(R + i), g = *(const float4 *)(p.hc_gamma + s * H + i);
-    const float4 v = make_float4(__fmul_rn(__fmul_rn(r.x, scale), g.x), __fmul_rn(__fmul_rn(r.y, scale), g.y),
-                                 __fmul_rn(__fmul_rn(r.z, scale), g.z), __fmul_rn(__fmul_rn(r.w, scale), g.w));
-    st_co16(n, (s * H + i) * 4, make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
-                                           __float_as_uint(v.w)));
+  // bf16(n), eight values a thread and 16-byte piece written through to the coherence point in one request (the
+  // down items' operand); the scale (the up items form n in fp32 again from R, the scale and gamma).
+  uint16_t *nb = (uint16_t *)p.hc_n + (uint64_t)t * kHcStreams * H;
+  for (uint32_t i = 8 * tid(); i < H; i += 8 * kWG) {
+    uint32_t o[4];
+#pragma unroll
+    for (uint32_t h = 0; h < 2; h++) {
+      const float4 r = *(const float4 *)(R + i + 4 * h), g = *(const float4 *)(p.hc_gamma + s * H + i + 4 * h);
+      float b0, b1, b2, b3;
+      round_bf16_2(__fmul_rn(__fmul_rn(r.x, scale), g.x), __fmul_rn(__fmul_rn(r.y, scale), g.y), b0, b1);
+      round_bf16_2(__fmul_rn(__fmul_rn(r.z, scale), g.z), __fmul_rn(__fmul_rn(r.w, scale), g.w), b2, b3);
+      o[2 * h] = (__float_as_uint(b0) >> 16) | (__float_as_uint(b1) & 0xffff0000u);
+      o[2 * h + 1] = (__float_as_uint(b2) >> 16) | (__float_as_uint(b3) & 0xffff0000u);
+    }
+    st_co16(nb, (s * H + i) * 2, make_uint4(o[0], o[1], o[2], o[3]));
   }
+  if (tid() == 0) st_co(hc_scale(p) + kHcStreams * t + s, scale);
   set_flag(p, kFlagHcNorm + kHcStreams * t + s);
 }
 
@@ -538,7 +557,7 @@ __device__ __forceinline__ void hc_down_item(const DecodeParams &p, uint32_t r, 
   const uint32_t K = kHcStreams * p.H, lr = p.hc_lr;
   wait_flags(p, kFlagHcNorm, kHcStreams * p.T);
   const uint16_t *W = r < lr ? p.hc_down + (uint64_t)r * K : p.hc_inj + (uint64_t)(r - lr) * K;
-  bf16_dot<true>(W, p.hc_n, K, K, 0, p.T, part, tot);
+  bf16_dot<true, true>(W, p.hc_n, K, K, 0, p.T, part, tot);
   const uint32_t t = tid();
   if (t < p.T) {
     const float v = (float)tot[t];
@@ -589,7 +608,8 @@ __device__ __forceinline__ void hc_up_item(const DecodeParams &p, uint32_t j, ui
       float acc = 0.0f;
 #pragma unroll
       for (uint32_t s = 0; s < kHcStreams; s++) {
-        const float n = ld_co(p.hc_n + ((uint64_t)t * kHcStreams + s) * H + i);
+        const float n = __fmul_rn(__fmul_rn(p.hc_R[((uint64_t)t * kHcStreams + s) * H + i],
+                                            ld_co(hc_scale(p) + kHcStreams * t + s)), p.hc_gamma[s * H + i]);
         acc = __fadd_rn(acc, __fmul_rn(n, sigmoid_libm(a[(t * kHcStreams + s) * kHcUpValues + di], tab)));
       }
       st_co(p.hc_x + (uint64_t)t * H + i, __fmul_rn(acc, 0.25f));
