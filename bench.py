@@ -402,6 +402,17 @@ def hc(args, cfg, moe, h):
     D = 4 * H
     flop = 2.0 * T * (lr + 4) * D + 2.0 * T * D * lr
     mix_ms = hc_ms - plain_ms
+    if T > 16:  # the prefill kernels: fp64 matrix cores
+        roof = {"bound": "mfma", "kernel": "pf_hc_gemm (down and up) and the mix's other kernels",
+                "achieved": round(flop / (mix_ms * 1e-3) / 1e12, 2), "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(flop / (mix_ms * 1e-3) / 1e12 / FP64_PEAK_TFLOPS, 4), "traffic": None,
+                "algorithmic_flop_per_launch": flop, "avg_launch_ms": round(mix_ms, 4)}
+    else:  # the decode launch's items: the module's weights read once (bf16 W_down, W_inject, W_up)
+        wbytes = 2.0 * ((lr + 4) * D + D * lr)
+        roof = {"bound": "hbm", "kernel": "moe_decode's hyper-connection items",
+                "achieved": round(wbytes / (mix_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(wbytes / (mix_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                "algorithmic_bytes_per_launch": int(wbytes), "avg_launch_ms": round(mix_ms, 4)}
     n = min(64, T)
     Rs = R[:n]
     Rg, yg, ig, _ = blk.forward_hc(0, Rs)
@@ -418,10 +429,7 @@ def hc(args, cfg, moe, h):
         "dtype": "f64", "data": "synthetic",
         "config": {"workload": cfg["name"], "n_embd": H, "n_ff": F, "n_expert": E, "n_used": K, "shared": True,
                    "tokens": T, "hc_lr": lr, "types": [moe.TYPE_NAMES[t] for t in cfg["types"]]},
-        "roofline": {"bound": "mfma", "kernel": "pf_hc_gemm (down and up) and the mix's other kernels",
-                     "achieved": round(flop / (mix_ms * 1e-3) / 1e12, 2), "peak": FP64_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(flop / (mix_ms * 1e-3) / 1e12 / FP64_PEAK_TFLOPS, 4),
-                     "traffic": None, "algorithmic_flop_per_launch": flop, "avg_launch_ms": round(mix_ms, 4)},
+        "roofline": roof,
         "block": {"block_alone_ms": round(plain_ms, 4), "mix_and_combine_ms": round(mix_ms, 4)},
         "parity": parity,
         "cpu_baseline": None,
