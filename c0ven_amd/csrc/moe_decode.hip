@@ -587,18 +587,33 @@ __device__ __forceinline__ void hc_up_item(const DecodeParams &p, uint32_t j, ui
     const uint32_t rr = tid() / 4, q = tid() % 4;  // row rr of the item's 4 kHcUpValues (64), token group q
     const uint32_t s = rr / kHcUpValues, i = i0 + rr % kHcUpValues;
     const uint16_t *W = p.hc_up + ((uint64_t)s * H + i) * lr;
-    for (uint32_t t = q; t < T; t += 4) {
-      double acc = 0.0;
-      for (uint32_t k = 0; k < lr; k += 8) {
-        const uint4 w = *(const uint4 *)(W + k);
-        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    // The row's weights 32 values at a time (four loads issued together, shared by the thread's tokens), each token's
+    // chain continuing through them in k order.
+    double acc[kMaxDecodeTokens / 4] = {};
+    for (uint32_t k0 = 0; k0 < lr; k0 += 32) {
+      uint4 w[4];
 #pragma unroll
-        for (int m = 0; m < 8; m++) {
-          const float wf = __uint_as_float((m & 1) ? wv[m / 2] & 0xffff0000u : wv[m / 2] << 16);
-          acc = __builtin_fma((double)wf, (double)lb[t * lr + k + m], acc);
+      for (uint32_t j = 0; j < 4; j++) w[j] = k0 + 8 * j < lr ? *(const uint4 *)(W + k0 + 8 * j) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (uint32_t tt = 0; tt < kMaxDecodeTokens / 4; tt++) {
+        const uint32_t t = q + 4 * tt;
+        if (t >= T) break;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) {
+          if (k0 + 8 * j >= lr) break;
+          const uint32_t wv[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+#pragma unroll
+          for (int m = 0; m < 8; m++) {
+            const float wf = __uint_as_float((m & 1) ? wv[m / 2] & 0xffff0000u : wv[m / 2] << 16);
+            acc[tt] = __builtin_fma((double)wf, (double)lb[t * lr + k0 + 8 * j + m], acc[tt]);
+          }
         }
       }
-      a[(t * kHcStreams + s) * kHcUpValues + rr % kHcUpValues] = (float)acc;
+    }
+#pragma unroll
+    for (uint32_t tt = 0; tt < kMaxDecodeTokens / 4; tt++) {
+      const uint32_t t = q + 4 * tt;
+      if (t < T) a[(t * kHcStreams + s) * kHcUpValues + rr % kHcUpValues] = (float)acc[tt];
     }
   }
   __syncthreads();
