@@ -705,6 +705,7 @@ struct PfGemm {
   uint32_t out_ld;
   float limit;
   uint32_t row_blocks;     // row blocks a tile (the 1-D grid is tiles x row_blocks)
+  uint32_t rb_span;        // pf_gemm16 Q4_K down: consecutive 64-row blocks a work-group (> 1 only when U <= 2)
   uint32_t U;              // 256-value units of K (a partial last one padded with zeros)
   const uint8_t *codebooks;  // the caller's codebooks (QGRID layout) for IQ3_XXS and IQ2_S
 };
@@ -803,6 +804,10 @@ struct Q4kBuf {
     lq = (g / 2) * nl * 16 + (rr + lane % 16) * 16 + 8 * (g % 2);
     ls = (rr + lane % 16) * 4;
     ld = (rr + 4 * g) * 4;
+  }
+  // The same rows of the next 64-row tile.
+  __device__ __forceinline__ void next_block(uint32_t U) {
+    base[0] += tile_bytes(QT_Q4_K, U), base[1] += tile_bytes(QT_Q4_K, U);
   }
   __device__ __forceinline__ void load_qs(uint32_t m, Q4kRaw &w, uint32_t u) const {
 #pragma unroll
@@ -907,6 +912,10 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   const uint32_t L = xcd_logical(blockIdx.x, n);
   if (L >= n) return;
   const uint32_t tile_i = L / nrb, rb = L % nrb;
+  // Down: R consecutive row blocks, one after another on the same positions. With U <= 2 (the host's condition for
+  // R > 1) every unit's activations stay in their LDS buffer after the first row block, so only its weights load.
+  // Q4_K only: the other types' forms spill with the row-block loop.
+  const uint32_t R = kGU || kType != QT_Q4_K ? 1u : g.rb_span;
   uint32_t start, count, e;
   if (g.shared_T) {
     start = MOE_TILE * tile_i;
@@ -931,7 +940,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   }
   __syncthreads();
   const uint32_t mat = kGU ? (w >> 1) : 0u;
-  const uint32_t row0 = rb * kRows + (kGU ? 16 * (w & 1) : 16 * w);
+  uint32_t row0 = rb * R * kRows + (kGU ? 16 * (w & 1) : 16 * w);
   const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
   const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
   Dma<64, 4> dma;
@@ -939,14 +948,15 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   const __amdgpu_buffer_rsrc_t act_r = uniform_rsrc(g.act);
   Q4kBuf wb;  // Q4_K's weight loads as buffer loads (the other types through their Raw::load)
   if constexpr (kType == QT_Q4_K) wb.init(M, M, U, row0, lane_id());
-  const auto load_w = [&](Raw &r, uint32_t u) {
+  // Unit u of the wave's rows from row rows0 (Q4_K: from wb's tile, which next_block moves on a row block).
+  const auto load_w = [&](Raw &r, uint32_t u, uint32_t rows0) {
     if constexpr (kType == QT_Q4_K)
       wb.load_qs(0, r, u), wb.load_meta(0, r, u);
     else
-      r.load(M, U, row0, u, lane_id());
+      r.load(M, U, rows0, u, lane_id());
   };
   Raw raw;
-  load_w(raw, 0);
+  load_w(raw, 0, row0);
   dma.load_all(act_r, 0, &abuf[0][0], dump);
   __builtin_amdgcn_s_waitcnt(vm_wait(0));
   unit_barrier();
@@ -957,15 +967,19 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
     for (int i = 0; i < 4; i++) acc[pt][i] = 0.0f;
   // buf (read) and nbuf (filled) as restrict pointers: the compiler then knows the reads of buf need not wait for the
   // global-to-LDS loads into nbuf (without it, each position tile's first LDS read waited for every load in flight).
-  const auto body = [&](uint32_t u, const uint8_t *__restrict__ buf, uint8_t *__restrict__ nbuf) {
+  // Step (r, u): unit u of row block r. The next step's weights are unit u + 1's, or the next row block's unit 0.
+  const auto body = [&](uint32_t r, uint32_t u, const uint8_t *__restrict__ buf, uint8_t *__restrict__ nbuf) {
     // Q4_K decodes the unit's raw words first and loads the next unit's into the same registers; the other types read
     // theirs in the MFMAs and load the next unit's into a second set.
     constexpr bool kInPlace = kType == QT_Q4_K || kType == QT_Q5_K;  // Q5_K: registers for one unit's words only
+    const bool more = u + 1 < U || r + 1 < R;
+    const uint32_t nu = u + 1 < U ? u + 1 : 0u, nrow = u + 1 < U ? row0 : row0 + kRows;
+    if constexpr (kType == QT_Q4_K)
+      if (u + 1 == U && r + 1 < R) wb.next_block(U);  // the raw words of (r, u) are loaded: move to block r + 1
     Raw next;
-    if (u + 1 < U) {
-      dma.load_all(act_r, u + 1, nbuf, dump);
-      if constexpr (!kInPlace) load_w(next, u + 1);
-    }
+    if (r == 0 && u + 1 < U) dma.load_all(act_r, u + 1, nbuf, dump);
+    if constexpr (!kInPlace)
+      if (more) load_w(next, nu, nrow);
     if constexpr (block_scaled(kType)) {
       // Block by block: one MFMA a position tile (IQ2_S, Q6_K: one a half block, the other half's A lanes zero), its
       // D times the row's block scale added to the unit's integer sum in block order; then kFactor ((d ad) isum) as
@@ -1044,7 +1058,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
         }
       }
       if constexpr (kInPlace)
-        if (u + 1 < U) load_w(raw, u + 1);
+        if (more) load_w(raw, nu, nrow);
     } else if constexpr (q8_family(kType)) {
       // Block by block: one MFMA a position tile, the block's term (d_w d_a) dot; the eight terms of the unit as the
       // pairwise tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then added to the row's sum.
@@ -1090,7 +1104,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
       pin(raw);  // the decode starts after the previous unit's barrier ...
       a.decode<true>(raw, lane_id());
       pin(a);  // ... and ends before the next unit's loads into the raw registers
-      if (u + 1 < U) load_w(raw, u + 1);
+      if (more) load_w(raw, nu, nrow);
 #pragma unroll
       for (uint32_t pt = 0; pt < 4; pt++) {
         if (pt < npt) {
@@ -1104,15 +1118,31 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
       }
     }
     if constexpr (!kInPlace)
-      if (u + 1 < U) raw = next;
+      if (more) raw = next;
     __builtin_amdgcn_s_waitcnt(vm_wait(0));  // this wave's loads of unit u + 1 have landed ...
     unit_barrier();                          // ... and every wave's
   };
-#pragma unroll 1
-  for (uint32_t u = 0; u < U; u++) body(u, abuf[u & 1], abuf[(u + 1) & 1]);
   // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16.
   const uint32_t l = lane_id(), r4 = 4 * (l / 16), c16 = l % 16;
-  if constexpr (kGU) {
+  if constexpr (!kGU) {
+#pragma unroll 1
+    for (uint32_t r = 0; r < R; r++) {
+#pragma unroll 1
+      for (uint32_t u = 0; u < U; u++) body(r, u, abuf[u & 1], abuf[(u + 1) & 1]);
+#pragma unroll
+      for (uint32_t pt = 0; pt < 4; pt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const uint32_t m = 16 * pt + c16;
+          if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = acc[pt][i];
+          acc[pt][i] = 0.0f;
+        }
+      row0 += kRows;
+    }
+  } else {
+#pragma unroll 1
+    for (uint32_t u = 0; u < U; u++) body(0, u, abuf[u & 1], abuf[(u + 1) & 1]);
+
     if (mat == 1) {
 #pragma unroll
       for (uint32_t pt = 0; pt < 4; pt++)
@@ -1131,14 +1161,6 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
                 swiglu_one(acc[pt][i], ub[16 * (w & 1) + r4 + i][m], g.limit, tab);
         }
     }
-  } else {
-#pragma unroll
-    for (uint32_t pt = 0; pt < 4; pt++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t m = 16 * pt + c16;
-        if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = acc[pt][i];
-      }
   }
 }
 
@@ -1430,6 +1452,11 @@ __global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const ui
 // ---------------------------------------------------------------------------------------------------------------
 // Host side.
 
+#ifndef C0VEN_DOWN_SPAN
+#define C0VEN_DOWN_SPAN 4
+#endif
+constexpr uint32_t kDownSpan = C0VEN_DOWN_SPAN;  // row blocks a down work-group, a power of two
+
 template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
   PfGemm q = g;
@@ -1445,6 +1472,12 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
   }
   // The 16 x 16 MFMA kernel: 32 gate + 32 up rows, or 64 down rows, a work-group; a 1-D XCD-aware grid.
   q.row_blocks = grid.y * gemm_rows<kGU>() / (kGU ? 32 : 64);
+  q.rb_span = 1;
+  if (!kGU && type == QT_Q4_K && U <= 2) {  // down: the activations of both units stay in LDS while the work-group walks row blocks
+    q.rb_span = kDownSpan;
+    while (q.row_blocks % q.rb_span) q.rb_span /= 2;
+    q.row_blocks /= q.rb_span;
+  }
   const dim3 g2(grid.x * q.row_blocks);
   if (type == QT_Q4_K)
     pf_gemm16<QT_Q4_K, kGU><<<g2, kPfWG, 0, s>>>(q);
