@@ -915,7 +915,8 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   // Down: R consecutive row blocks, one after another on the same positions. With U <= 2 (the host's condition for
   // R > 1) every unit's activations stay in their LDS buffer after the first row block, so only its weights load.
   // Q4_K only: the other types' forms spill with the row-block loop.
-  const uint32_t R = kGU || kType != QT_Q4_K ? 1u : g.rb_span;
+  constexpr bool kWalk = !kGU && kType == QT_Q4_K;
+  const uint32_t R = kWalk ? g.rb_span : 1u;
   uint32_t start, count, e;
   if (g.shared_T) {
     start = MOE_TILE * tile_i;
@@ -940,7 +941,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   }
   __syncthreads();
   const uint32_t mat = kGU ? (w >> 1) : 0u;
-  uint32_t row0 = rb * R * kRows + (kGU ? 16 * (w & 1) : 16 * w);
+  const uint32_t row0 = rb * R * kRows + (kGU ? 16 * (w & 1) : 16 * w);
   const uint8_t *M = g.mat + (uint64_t)e * g.stride + (mat ? g.up_off : 0);
   const uint32_t npt = (count + 15) / 16;  // 16-position tiles with positions
   Dma<64, 4> dma;
@@ -972,8 +973,8 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
     // Q4_K decodes the unit's raw words first and loads the next unit's into the same registers; the other types read
     // theirs in the MFMAs and load the next unit's into a second set.
     constexpr bool kInPlace = kType == QT_Q4_K || kType == QT_Q5_K;  // Q5_K: registers for one unit's words only
-    const bool more = u + 1 < U || r + 1 < R;
-    const uint32_t nu = u + 1 < U ? u + 1 : 0u, nrow = u + 1 < U ? row0 : row0 + kRows;
+    const bool more = kWalk ? u + 1 < U || r + 1 < R : u + 1 < U;
+    const uint32_t nu = !kWalk || u + 1 < U ? u + 1 : 0u, nrow = row0 + (!kWalk || u + 1 < U ? r : r + 1) * kRows;
     if constexpr (kType == QT_Q4_K)
       if (u + 1 == U && r + 1 < R) wb.next_block(U);  // the raw words of (r, u) are loaded: move to block r + 1
     Raw next;
@@ -1122,26 +1123,27 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
     __builtin_amdgcn_s_waitcnt(vm_wait(0));  // this wave's loads of unit u + 1 have landed ...
     unit_barrier();                          // ... and every wave's
   };
-  // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16.
-  const uint32_t l = lane_id(), r4 = 4 * (l / 16), c16 = l % 16;
   if constexpr (!kGU) {
 #pragma unroll 1
     for (uint32_t r = 0; r < R; r++) {
 #pragma unroll 1
       for (uint32_t u = 0; u < U; u++) body(r, u, abuf[u & 1], abuf[(u + 1) & 1]);
+      // Lane l holds rows row0 + r kRows + 4 (l / 16) + i of positions 16 pt + l % 16.
+      const uint32_t l = lane_id(), r4 = 4 * (l / 16), c16 = l % 16;
 #pragma unroll
       for (uint32_t pt = 0; pt < 4; pt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const uint32_t m = 16 * pt + c16;
-          if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r4 + i] = acc[pt][i];
+          if (m < count) g.out[(uint64_t)(start + m) * g.out_ld + row0 + r * kRows + r4 + i] = acc[pt][i];
           acc[pt][i] = 0.0f;
         }
-      row0 += kRows;
     }
   } else {
 #pragma unroll 1
     for (uint32_t u = 0; u < U; u++) body(0, u, abuf[u & 1], abuf[(u + 1) & 1]);
+    // Lane l holds rows row0 + 4 (l / 16) + i of positions 16 pt + l % 16.
+    const uint32_t l = lane_id(), r4 = 4 * (l / 16), c16 = l % 16;
 
     if (mat == 1) {
 #pragma unroll
