@@ -1413,15 +1413,17 @@ constexpr bool gu_fused(uint32_t type) { return type == QT_Q4_K || type == QT_IQ
 // + gs[t] y_sh[t][r]; four rows a thread. The ranks go in batches of eight whose row loads are all issued before the
 // first is added (rows of skipped ranks are not loaded and add nothing).
 
-constexpr uint32_t kCombBatch = 8;  // 12 and 16 (one batch for K = 10) measured 44 and 51 against 38 us
+// With the token uniform a work-group, batches of 4, 8, 10 and 16 measured the same (34.2-34.5 us at config 4); with
+// the token per thread, 12 and 16 measured 44 and 51 against 8's 38 us.
+constexpr uint32_t kCombBatch = 8;
 
 __global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const uint32_t *inv, const int32_t *ids,
                                                     const float *w, uint32_t K, const float *y_sh, const float *gs,
                                                     uint32_t T, uint32_t H, float *y) {
-  const uint64_t i = (uint64_t)blockIdx.x * kPfWG + threadIdx.x;
-  const uint32_t H4 = H / 4;
-  if (i >= (uint64_t)T * H4) return;
-  const uint32_t t = (uint32_t)(i / H4), r4 = (uint32_t)(i % H4);
+  // Token blockIdx.y, uniform a work-group, so its ids, weights and positions are scalar loads (a token a thread,
+  // with them as vector loads, measured 38 against 34 us at config 4); float4 column blockIdx.x kPfWG + tid.
+  const uint32_t H4 = H / 4, t = blockIdx.y, r4 = blockIdx.x * kPfWG + threadIdx.x;
+  if (t >= T || r4 >= H4) return;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (uint32_t k0 = 0; k0 < K; k0 += kCombBatch) {
     float wk[kCombBatch];
@@ -1453,6 +1455,9 @@ __global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const ui
 
 // ---------------------------------------------------------------------------------------------------------------
 // Host side.
+
+// pf_combine's grid: (H / 4 columns in work-groups of kPfWG) x T tokens.
+inline dim3 comb_grid(uint32_t T, uint32_t H) { return dim3((H / 4 + kPfWG - 1) / kPfWG, T); }
 
 #ifndef C0VEN_DOWN_SPAN
 #define C0VEN_DOWN_SPAN 4
@@ -1684,8 +1689,7 @@ hipError_t prefill_forward(const PfShape &S, const PfLayer &L, const PfBufs &b, 
   if (S.has_shared && hipStreamWaitEvent(st, b.join, 0) != hipSuccess) return hipGetLastError();
   {
     HookScope k(hook, "pf_combine", st);
-    const uint64_t n = (uint64_t)T * (H / 4);
-    pf_combine<<<(uint32_t)((n + kPfWG - 1) / kPfWG), kPfWG, 0, st>>>(b.y_asg, b.inv, b.ids, b.w, K,
+    pf_combine<<<comb_grid(T, H), kPfWG, 0, st>>>(b.y_asg, b.inv, b.ids, b.w, K,
                                                                         S.has_shared ? b.y_sh : nullptr, b.gs, T, H, y);
   }
   return hipGetLastError();
@@ -1704,8 +1708,7 @@ hipError_t prefill_jobs(const PfShape &S, const PfLayer &L, const PfBufs &b, con
   if (e != hipSuccess) return e;
   {
     HookScope k(hook, "pf_combine", st);
-    const uint64_t n = (uint64_t)T * (H / 4);
-    pf_combine<<<(uint32_t)((n + kPfWG - 1) / kPfWG), kPfWG, 0, st>>>(b.y_asg, b.inv, b.ids, b.w, K, nullptr, nullptr,
+    pf_combine<<<comb_grid(T, H), kPfWG, 0, st>>>(b.y_asg, b.inv, b.ids, b.w, K, nullptr, nullptr,
                                                                         T, H, y);
   }
   return hipGetLastError();
