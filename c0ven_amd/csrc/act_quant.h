@@ -80,12 +80,19 @@ __host__ __device__ __forceinline__ constexpr uint32_t mfma_code_off(uint32_t j)
   return 64 * (j / 8) + 16 * (j % 4) + 8 * ((j / 4) % 2);
 }
 
+// A float through dpp_u32 (device_math.h's DPP exchanges inside a 16-lane row).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<kCtrl>(__float_as_uint(v)));
+}
+
 // One activation unit (256 values) quantised by a half-wave, eight values a lane (lane l32 holds values 8 l32..+7),
 // with the CPU path's rules: q8_K (quantize_row_q8_K_ref) or q8_0 (the x86 quantize_row_q8_0). out is in global
 // memory, or in LDS when kLds. kSplitG: q8_K's block sums as the f16 split at kActSplitH in place of the int32
 // sums. kMfma: the codes in the prefill order (mfma_code_off) instead of value order. kPlain:
-// plain global stores (the unit is read by later launches only).
-template <bool kLds = false, bool kSplitG = false, bool kMfma = false, bool kPlain = false>
+// plain global stores (the unit is read by later launches only). kDpp: the exchanges inside 16-lane rows as DPP
+// moves (the same results: the combines are exact and order-free); all 32 lanes of the half-wave take part.
+template <bool kLds = false, bool kSplitG = false, bool kMfma = false, bool kPlain = false, bool kDpp = false>
 __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint32_t act_type, uint8_t *out) {
   const uint32_t coff = kMfma ? mfma_code_off(l32) : 8 * l32;
   uint32_t code[2] = {0u, 0u};
@@ -98,11 +105,19 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
       const float a = fabsf(v[i]);
       if (a > amax) amax = a, mx = v[i], at = 8 * l32 + i;
     }
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-      const float oa = __shfl_xor(amax, o, 32), om = __shfl_xor(mx, o, 32);
-      const uint32_t oi = __shfl_xor(at, o, 32);
+    // The largest |v|, the first of equals: a commutative and associative combine, so any pairing order gives it.
+    const auto take = [&](float oa, float om, uint32_t oi) {
       if (oa > amax || (oa == amax && oi < at)) amax = oa, mx = om, at = oi;
+    };
+    if constexpr (kDpp) {
+      take(dpp_f32<kDppXor1>(amax), dpp_f32<kDppXor1>(mx), dpp_u32<kDppXor1>(at));
+      take(dpp_f32<kDppXor2>(amax), dpp_f32<kDppXor2>(mx), dpp_u32<kDppXor2>(at));
+      take(dpp_f32<kDppHalfMirror>(amax), dpp_f32<kDppHalfMirror>(mx), dpp_u32<kDppHalfMirror>(at));
+      take(dpp_f32<kDppMirror>(amax), dpp_f32<kDppMirror>(mx), dpp_u32<kDppMirror>(at));
+      take(__shfl_xor(amax, 16, 32), __shfl_xor(mx, 16, 32), (uint32_t)__shfl_xor((int)at, 16, 32));
+    } else {
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) take(__shfl_xor(amax, o, 32), __shfl_xor(mx, o, 32), (uint32_t)__shfl_xor((int)at, o, 32));
     }
     float d = 0.0f;
     int part = 0;
@@ -117,8 +132,13 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
       }
       d = __fdiv_rn(1.0f, iscale);
     }
-    part += __shfl_xor(part, 1, 32);
-    part += __shfl_xor(part, 2, 32);
+    if constexpr (kDpp) {
+      part += (int)dpp_u32<kDppXor1>((uint32_t)part);
+      part += (int)dpp_u32<kDppXor2>((uint32_t)part);
+    } else {
+      part += __shfl_xor(part, 1, 32);
+      part += __shfl_xor(part, 2, 32);
+    }
     put_word<kLds, uint64_t, kPlain>(out, coff, ((uint64_t)code[1] << 32) | code[0]);
     if constexpr (kSplitG) {
       // Block sum j = l32 / 4 split as 64 hi + lo (hi in [-64, 63], lo in [0, 63]), both as f16, at kActSplitH.
@@ -135,8 +155,13 @@ __device__ __forceinline__ void quant_unit(const float v[8], uint32_t l32, uint3
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 32));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 32));
+    if constexpr (kDpp) {
+      amax = fmaxf(amax, dpp_f32<kDppXor1>(amax));
+      amax = fmaxf(amax, dpp_f32<kDppXor2>(amax));
+    } else {
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 32));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 32));
+    }
     const float d = __fdiv_rn(amax, 127.0f), id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
