@@ -1263,8 +1263,10 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3
       };
       pass(rg, 0, accg);
       pass(ru, 1, accu);
-      __builtin_amdgcn_s_waitcnt(vm_wait(0));  // unit u + 1's loads (this wave's) ...
-      unit_barrier();                          // ... and every wave's; buffer u % 2 is free for unit u + 2
+      if constexpr (next) {  // (after the last unit only the epilogue follows, which reads no activations)
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));  // unit u + 1's loads (this wave's) ...
+        unit_barrier();                          // ... and every wave's; buffer u % 2 is free for unit u + 2
+      }
     };
     body(abuf[u & 1], abuf[(u + 1) & 1]);
   };
@@ -1389,8 +1391,10 @@ __global__ void __launch_bounds__(4 * kPos) __attribute__((amdgpu_waves_per_eu(3
       };
       pass(rg, 0, accg);
       pass(ru, 1, accu);
-      __builtin_amdgcn_s_waitcnt(vm_wait(0));  // unit u + 1's loads (this wave's) ...
-      unit_barrier();                          // ... and every wave's; buffer u % 2 is free for unit u + 2
+      if constexpr (next) {  // (after the last unit only the epilogue follows, which reads no activations)
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));  // unit u + 1's loads (this wave's) ...
+        unit_barrier();                          // ... and every wave's; buffer u % 2 is free for unit u + 2
+      }
     };
     body(abuf[u & 1], abuf[(u + 1) & 1]);
   };
