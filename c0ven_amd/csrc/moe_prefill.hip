@@ -23,7 +23,6 @@
 namespace c0ven {
 
 constexpr uint32_t kMaxRouteExperts = 512;  // routed experts a layer may have
-constexpr uint32_t kRouterLdsH = 4096;       // n_embd up to which an open token's x is staged in LDS
 
 __device__ __constant__ static const uint32_t kIq3sGridPf[512] = {C0VEN_IQ3S_GRID_VALUES};
 
@@ -462,7 +461,6 @@ __global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint1
   __shared__ uint64_t tab[32];
   __shared__ uint32_t cand[kPfWG / 64][kMaxRouteExperts];
   __shared__ uint32_t xkey[kPfWG / 64][kMaxRouteExperts];  // 0, or an exactly summed expert's key (cleared after)
-  __shared__ __align__(16) uint16_t xrow[kPfWG / 64][kRouterLdsH];  // an open token's bf16 x, for its exact sums
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   for (uint32_t i = threadIdx.x; i < (kPfWG / 64) * kMaxRouteExperts; i += kPfWG) (&xkey[0][0])[i] = 0u;
   __syncthreads();
@@ -514,17 +512,12 @@ __global__ void __launch_bounds__(kPfWG) pf_topk_cert(float *logits, const uint1
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
-    // x's bf16 row into the wave's LDS, then sixteen lanes a candidate: lane s of group j sums the row's sixteenth s
-    // in fp64 (its magnitudes too, and the least exponent sum of its products), the group adds its sixteen partials
-    // in a fixed tree; exact when the magnitudes' sum is below 2^(lsb + 53).
-    const uint4 *xg = (const uint4 *)(xb + (uint64_t)t * H), *xs = xg;
-    if (H <= kRouterLdsH) {  // (a wider row is read from memory)
-      uint4 *xl = (uint4 *)&xrow[wv][0];
-      for (uint32_t k = lane; k < H / 8; k += 64) xl[k] = xg[k];
-      __builtin_amdgcn_s_waitcnt(0xc07f);
-      __builtin_amdgcn_wave_barrier();
-      xs = xl;
-    }
+    // Sixteen lanes a candidate: lane s of group j sums the row's sixteenth s in fp64 (its magnitudes too, and the
+    // least exponent sum of its products), the group adds its sixteen partials in a fixed tree; exact when the
+    // magnitudes' sum is below 2^(lsb + 53). x's bf16 row is read from memory (L2) by each candidate's group: staged
+    // in LDS (32 KB a work-group) it measured ~1 us slower at config 4, and kept the kernel off CUs whose LDS the
+    // shared expert's launches beside it hold.
+    const uint4 *xs = (const uint4 *)(xb + (uint64_t)t * H);
     const uint32_t j = lane / 16, sl = lane % 16, H16 = H / 16;  // H16 / 8 pieces of 16 B a lane
     for (uint32_t c0 = 0; c0 < nc; c0 += 4) {
       const uint32_t ci = c0 + j, e = cand[wv][min(ci, nc - 1)];
