@@ -1464,6 +1464,7 @@ inline dim3 comb_grid(uint32_t T, uint32_t H) { return dim3((H / 4 + kPfWG - 1) 
 
 // Row blocks a Q4_K down work-group walks, a power of two (config 4's routed down: 1 120, 2 107, 4 103, 8 105 us).
 constexpr uint32_t kDownSpan = 4;
+constexpr uint32_t kDownMinGroups = 512;  // work-groups a walking down grid keeps (two a CU)
 
 template <bool kGU>
 void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStream_t s) {
@@ -1482,8 +1483,11 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
   q.row_blocks = grid.y * gemm_rows<kGU>() / (kGU ? 32 : 64);
   q.rb_span = 1;
   if (!kGU && type == QT_Q4_K && U <= 2) {  // down: the activations of both units stay in LDS while the work-group walks row blocks
+    // Fewer row blocks a work-group where the grid would leave fewer than two work-groups a CU (the shared
+    // expert's 32 tiles at 2048 tokens: span 2 15.7 against span 4 18.0 us).
     q.rb_span = kDownSpan;
-    while (q.row_blocks % q.rb_span) q.rb_span /= 2;
+    while (q.rb_span > 1 && (q.row_blocks % q.rb_span || grid.x * (q.row_blocks / q.rb_span) < kDownMinGroups))
+      q.rb_span /= 2;
     q.row_blocks /= q.rb_span;
   }
   const dim3 g2(grid.x * q.row_blocks);
