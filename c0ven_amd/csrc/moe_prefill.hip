@@ -912,7 +912,7 @@ __global__ void __launch_bounds__(kPfWG) __attribute__((amdgpu_waves_per_eu(3)))
   // R > 1) every unit's activations stay in their LDS buffer after the first row block, so only its weights load.
   // Q4_K only: the other types' forms spill with the row-block loop.
   constexpr bool kWalk = !kGU && kType == QT_Q4_K;
-  const uint32_t R = kWalk ? g.rb_span : 1u;
+  const uint32_t R = kWalk && U <= 2 ? g.rb_span : 1u;  // (the host sets rb_span 1 for U > 2 too)
   uint32_t start, count, e;
   if (g.shared_T) {
     start = MOE_TILE * tile_i;
