@@ -1463,6 +1463,7 @@ __global__ void __launch_bounds__(kPfWG) pf_combine(const float *y_asg, const ui
 inline dim3 comb_grid(uint32_t T, uint32_t H) { return dim3((H / 4 + kPfWG - 1) / kPfWG, T); }
 
 // Row blocks a Q4_K down work-group walks, a power of two (config 4's routed down: 1 120, 2 107, 4 103, 8 105 us).
+constexpr uint32_t kSharedGuLds = 16384;  // dynamic LDS reserved by the shared Q8_0 gate/up launch (not used)
 constexpr uint32_t kDownSpan = 4;
 constexpr uint32_t kDownMinGroups = 512;  // work-groups a walking down grid keeps (two a CU)
 
@@ -1491,6 +1492,13 @@ void launch_gemm(uint32_t type, uint32_t U, dim3 grid, const PfGemm &g, hipStrea
     q.row_blocks /= q.rb_span;
   }
   const dim3 g2(grid.x * q.row_blocks);
+  if (kGU && q.shared_T && type == QT_Q8_0) {
+    // The shared expert's Q8_0 gate/up runs beside the router and top-k on the side stream; at three work-groups a
+    // CU it takes every register of the CUs it holds. kSharedGuLds of LDS it does not use caps it at two, leaving a
+    // wave a SIMD to the top-k (config 5p: top-k 46 -> 33 us, this launch 51 -> 71, a step 52.8 -> 52.5 ms).
+    pf_gemm16<QT_Q8_0, kGU><<<g2, kPfWG, kSharedGuLds, s>>>(q);
+    return;
+  }
   if (type == QT_Q4_K)
     pf_gemm16<QT_Q4_K, kGU><<<g2, kPfWG, 0, s>>>(q);
   else if (type == QT_IQ3_S)
